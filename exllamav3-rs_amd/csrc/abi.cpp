@@ -1,0 +1,68 @@
+// Thread-local error reporting and the version/tuning entry points of the C ABI.
+#include "abi.hpp"
+#include "tuning.h"
+
+#include <cstdarg>
+#include <cstdio>
+
+namespace exl3r {
+
+static thread_local char g_last_error[512] = "";
+
+int set_error(int code, const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int launch_status(const char* op)
+{
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error((int)e, "%s: kernel launch failed: %s", op, hipGetErrorString(e));
+    return EXL3R_OK;
+}
+
+const char* dtype_name(int dt)
+{
+    switch (dt)
+    {
+        case EXL3R_F32: return "f32";
+        case EXL3R_F16: return "f16";
+        case EXL3R_BF16: return "bf16";
+        case EXL3R_I32: return "i32";
+        case EXL3R_I64: return "i64";
+        default: return "?";
+    }
+}
+
+Tuning& tuning()
+{
+    static Tuning t;
+    return t;
+}
+
+}  // namespace exl3r
+
+extern "C" int exl3r_version(void) { return 10000; }
+
+extern "C" const char* exl3r_last_error(void) { return exl3r::g_last_error; }
+
+extern "C" void exl3r_tune_rms(int maxv, int threads)
+{
+    exl3r::tuning().rms_maxv = maxv;
+    exl3r::tuning().rms_threads = threads;
+}
+
+extern "C" void exl3r_tune_act(int unroll, int threads, int blocks_per_cu)
+{
+    exl3r::tuning().act_unroll = unroll;
+    exl3r::tuning().act_threads = threads;
+    exl3r::tuning().act_blocks_per_cu = blocks_per_cu;
+}
+
+extern "C" void exl3r_tune_rope(int threads) { exl3r::tuning().rope_threads = threads; }
+
+extern "C" void exl3r_tune_embed(int threads) { exl3r::tuning().embed_threads = threads; }

@@ -1,0 +1,45 @@
+// Host-side helpers shared by the C ABI entry points: thread-local error message, argument
+// validation, launch-status check.  Nothing here allocates or synchronises.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/exl3r/rowops.h"
+
+namespace exl3r {
+
+// Records a printf-style message for exl3r_last_error() and returns `code`.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Status of the kernel launch just issued (hipGetLastError); sets the message on failure.
+int launch_status(const char* op);
+
+inline bool is_float_dtype(int dt) { return dt == EXL3R_F32 || dt == EXL3R_F16 || dt == EXL3R_BF16; }
+inline int dtype_bytes(int dt)
+{
+    switch (dt)
+    {
+        case EXL3R_F32: case EXL3R_I32: return 4;
+        case EXL3R_F16: case EXL3R_BF16: return 2;
+        case EXL3R_I64: return 8;
+        default: return 0;
+    }
+}
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+const char* dtype_name(int dt);
+
+// Grid rows are walked with a stride loop beyond this many workgroups.
+constexpr int64_t kMaxGridX = 1 << 20;
+
+// Tuning overrides (0 = automatic); set only by exl3r_tune_* for sweeps.
+struct Tuning
+{
+    int rms_maxv = 0, rms_threads = 0;
+    int act_unroll = 0, act_threads = 0, act_blocks_per_cu = 0;
+    int rope_threads = 0;
+    int embed_threads = 0;
+};
+Tuning& tuning();
+
+}  // namespace exl3r

@@ -1,0 +1,233 @@
+// Gated activations z = act(x) * y for gfx950: exl3r_silu_mul / exl3r_gelu_mul (replace
+// exl3_shim_silu_mul / exl3_shim_gelu_mul, reference csrc/exl3_shim.cpp:151-152 ->
+// kernels/activation.cu:24-98, 181-255).
+//
+// Semantics are the reference's fp32 path (act_mul_kernel_f, kernels/activation_kernels.cuh:189-252)
+// applied to upcast inputs: act in fp32, optional act_limit clamps (237-245), product in fp32, one
+// round-to-nearest-even to z's dtype, f16 z clamped to +-65504 (2-7, 249-251).
+//   silu(x) = x / (1 + exp(-x))                                   (activation_kernels.cuh:34-39)
+//   gelu(x) = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))      (activation_kernels.cuh:52-58)
+// evaluated as x * rcp(1 + exp2(...)) via 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)), so both are one
+// v_exp_f32 and one v_rcp_f32 per element and GELU has no 1 + tanh cancellation for x << 0.
+//
+// Streaming layout: 8-element chunks (16 bytes per 16-bit tensor) per lane, UNROLL chunks in flight
+// per thread, strided by blockDim so each wave-wide access is 1 KiB contiguous.  Contiguous
+// operands are flattened to one row; strided rows use gridDim.y over rows.
+#include "abi.hpp"
+#include "common.cuh"
+
+namespace exl3r {
+
+enum { ACT_SILU = 0, ACT_GELU = 1 };
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kGeluK1 = (float)(-2.0 * 0.79788456080286535588 * 1.4426950408889634074);
+constexpr float kGeluK2 = (float)(-2.0 * 0.79788456080286535588 * 0.044715 * 1.4426950408889634074);
+
+template <int ACT>
+__device__ __forceinline__ float act_f(float x)
+{
+    float t;
+    if constexpr (ACT == ACT_SILU) t = x * -kLog2e;
+    else t = x * fmaf(kGeluK2, x * x, kGeluK1);
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
+}
+
+struct ActArgs
+{
+    const void* x;
+    const void* y;
+    void* z;
+    int64_t ldx, ldy, ldz;   // row strides (elements)
+    int64_t rows;
+    int64_t cols;            // elements per row
+    float limit;
+};
+
+template <int ACT, class OT>
+__device__ __forceinline__ void act_chunk(const float (&g)[8], float (&u)[8], float limit, float (&o)[8])
+{
+    #pragma unroll
+    for (int j = 0; j < 8; ++j)
+    {
+        float a = act_f<ACT>(g[j]);
+        float v = u[j];
+        if (limit != 0.0f)
+        {
+            if (v < -limit) v = -limit;
+            if (v > limit) v = limit;
+            if (a > limit) a = limit;
+        }
+        float p = a * v;
+        if constexpr (OT::code == DT_F16) p = clamp_f16(p);
+        o[j] = p;
+    }
+}
+
+template <int ACT, class IT, class OT, int UNROLL>
+__global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
+{
+    const int64_t cpr = a.cols >> 3;   // chunks per row
+    const int nt = blockDim.x;
+    for (int64_t row = blockIdx.y; row < a.rows; row += gridDim.y)
+    {
+        const char* xr = (const char*)a.x + row * a.ldx * IT::bytes;
+        const char* yr = (const char*)a.y + row * a.ldy * IT::bytes;
+        char* zr = (char*)a.z + row * a.ldz * OT::bytes;
+        for (int64_t base = (int64_t)blockIdx.x * nt * UNROLL + threadIdx.x; base < cpr;
+             base += (int64_t)gridDim.x * nt * UNROLL)
+        {
+            typename IT::Vec xv[UNROLL], yv[UNROLL];
+            #pragma unroll
+            for (int u = 0; u < UNROLL; ++u)
+            {
+                const int64_t c = base + (int64_t)u * nt;
+                if (c < cpr)
+                {
+                    xv[u] = load8<IT>(xr, c * 8);
+                    yv[u] = load8<IT>(yr, c * 8);
+                }
+            }
+            #pragma unroll
+            for (int u = 0; u < UNROLL; ++u)
+            {
+                const int64_t c = base + (int64_t)u * nt;
+                if (c < cpr)
+                {
+                    float g[8], v[8], o[8];
+                    unpack8<IT>(xv[u], g);
+                    unpack8<IT>(yv[u], v);
+                    act_chunk<ACT, OT>(g, v, a.limit, o);
+                    store8<OT>(zr, c * 8, pack8<OT>(o));
+                }
+            }
+        }
+    }
+}
+
+// Generic fallback: any shape, stride and alignment, one element per thread.
+template <int ACT>
+__global__ __launch_bounds__(256) void k_act_mul_generic(ActArgs a, int it, int ot)
+{
+    const int64_t n = a.rows * a.cols;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    {
+        const int64_t r = i / a.cols, c = i - r * a.cols;
+        float g[8] = { load1(a.x, it, r * a.ldx + c) };
+        float v[8] = { load1(a.y, it, r * a.ldy + c) };
+        float o[8];
+        if (ot == DT_F16) act_chunk<ACT, TF16>(g, v, a.limit, o);
+        else act_chunk<ACT, TF32>(g, v, a.limit, o);
+        store1(a.z, ot, r * a.ldz + c, o[0]);
+    }
+}
+
+static int num_cus()
+{
+    static int n = 0;
+    if (n == 0)
+    {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+    }
+    return n;
+}
+
+template <int ACT, class IT, class OT>
+static void launch_act_vec(const ActArgs& a, hipStream_t s)
+{
+    const Tuning& tu = tuning();
+    const int unroll = (tu.act_unroll == 1 || tu.act_unroll == 2 || tu.act_unroll == 4 || tu.act_unroll == 8) ? tu.act_unroll : 4;
+    const int threads = (tu.act_threads > 0 && tu.act_threads % 64 == 0 && tu.act_threads <= 256) ? tu.act_threads : 256;
+    const int64_t cpr = a.cols >> 3;
+    int64_t bx = (cpr + (int64_t)threads * unroll - 1) / ((int64_t)threads * unroll);
+    if (tu.act_blocks_per_cu > 0)
+    {
+        const int64_t cap = (int64_t)tu.act_blocks_per_cu * num_cus() / (a.rows < 65535 ? (a.rows > 0 ? a.rows : 1) : 65535);
+        if (bx > cap) bx = cap > 0 ? cap : 1;
+    }
+    if (bx > kMaxGridX) bx = kMaxGridX;
+    const dim3 grid((unsigned)bx, (unsigned)(a.rows < 65535 ? a.rows : 65535));
+    switch (unroll)
+    {
+        case 1: k_act_mul<ACT, IT, OT, 1><<<grid, threads, 0, s>>>(a); break;
+        case 2: k_act_mul<ACT, IT, OT, 2><<<grid, threads, 0, s>>>(a); break;
+        case 8: k_act_mul<ACT, IT, OT, 8><<<grid, threads, 0, s>>>(a); break;
+        default: k_act_mul<ACT, IT, OT, 4><<<grid, threads, 0, s>>>(a); break;
+    }
+}
+
+template <int ACT>
+static int act_mul_entry(const char* op, const void* x, const void* y, int it, void* z, int ot,
+                         int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz,
+                         float limit, void* stream)
+{
+    if (!x || !y || !z) return set_error(EXL3R_EINVAL, "%s: x, y and z must be non-null", op);
+    if (rows < 0 || cols < 0) return set_error(EXL3R_EINVAL, "%s: invalid shape rows=%lld cols=%lld", op, (long long)rows, (long long)cols);
+    if (rows > 1 && (ldx < cols || ldy < cols || ldz < cols))
+        return set_error(EXL3R_EINVAL, "%s: row strides must be >= cols", op);
+    if (!is_float_dtype(it) || !is_float_dtype(ot))
+        return set_error(EXL3R_EDTYPE, "%s: unsupported dtypes in=%s z=%s", op, dtype_name(it), dtype_name(ot));
+    if ((z == x && (ot != it || ldz != ldx)) || (z == y && (ot != it || ldz != ldy)))
+        return set_error(EXL3R_EINVAL, "%s: in-place z needs the aliased operand's dtype and stride", op);
+    if (rows == 0 || cols == 0) return EXL3R_OK;
+
+    ActArgs a{ x, y, z, ldx, ldy, ldz, rows, cols, limit };
+    if (rows == 1 || (ldx == cols && ldy == cols && ldz == cols))
+    {
+        a.cols = rows * cols;
+        a.rows = 1;
+        a.ldx = a.ldy = a.ldz = a.cols;
+    }
+    hipStream_t s = (hipStream_t)stream;
+
+    const bool rows_ok = a.rows == 1 || ((a.ldx * dtype_bytes(it)) % 16 == 0 && (a.ldy * dtype_bytes(it)) % 16 == 0 &&
+                                         (a.ldz * dtype_bytes(ot)) % 16 == 0 && a.cols % 8 == 0);
+    const bool vec = rows_ok && aligned16(x) && aligned16(y) && aligned16(z) && a.cols >= 8;
+    if (vec)
+    {
+        const int64_t body = a.cols & ~(int64_t)7;
+        ActArgs b = a;
+        b.cols = body;
+        with_float_type(it, [&](auto I) {
+            with_float_type(ot, [&](auto O) { launch_act_vec<ACT, decltype(I), decltype(O)>(b, s); });
+        });
+        if (body != a.cols)   // flat tail of < 8 elements
+        {
+            ActArgs t = a;
+            t.x = (const char*)a.x + body * dtype_bytes(it);
+            t.y = (const char*)a.y + body * dtype_bytes(it);
+            t.z = (char*)a.z + body * dtype_bytes(ot);
+            t.cols = a.cols - body;
+            t.ldx = t.ldy = t.ldz = t.cols;
+            k_act_mul_generic<ACT><<<1, 64, 0, s>>>(t, it, ot);
+        }
+    }
+    else
+    {
+        const int64_t n = a.rows * a.cols;
+        int64_t blocks = (n + 255) / 256;
+        if (blocks > kMaxGridX) blocks = kMaxGridX;
+        k_act_mul_generic<ACT><<<(unsigned)blocks, 256, 0, s>>>(a, it, ot);
+    }
+    return launch_status(op);
+}
+
+}  // namespace exl3r
+
+using namespace exl3r;
+
+extern "C" int exl3r_silu_mul(const void* x, const void* y, int in_dtype, void* z, int z_dtype,
+                              int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz,
+                              float act_limit, void* stream)
+{
+    return act_mul_entry<ACT_SILU>("exl3r_silu_mul", x, y, in_dtype, z, z_dtype, rows, cols, ldx, ldy, ldz, act_limit, stream);
+}
+
+extern "C" int exl3r_gelu_mul(const void* x, const void* y, int in_dtype, void* z, int z_dtype,
+                              int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz,
+                              float act_limit, void* stream)
+{
+    return act_mul_entry<ACT_GELU>("exl3r_gelu_mul", x, y, in_dtype, z, z_dtype, rows, cols, ldx, ldy, ldz, act_limit, stream);
+}

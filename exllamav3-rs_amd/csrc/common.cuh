@@ -1,0 +1,297 @@
+// Device-side building blocks shared by the gfx950 row kernels:
+//   - dtype tags with 8-element (16-byte per 16-bit tensor) vector load/store and exact
+//     conversions (f16/bf16 -> f32 exact, f32 -> f16/bf16 round-to-nearest-even in hardware:
+//     v_cvt_f16_f32 and gfx950's v_cvt_pk_bf16_f32);
+//   - wave64 reductions built from DPP row ops (quad_perm / row_half_mirror / row_mirror) with
+//     one readlane hop across the four 16-lane rows, and a single LDS hop across waves.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace exl3r {
+
+enum : int { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2, DT_I32 = 3, DT_I64 = 4 };
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------------------------
+// dtype tags.  Each tag loads/stores chunks of 8 consecutive elements; F16/BF16 chunks are one
+// 16-byte access, F32 chunks two.
+
+struct TNone
+{
+    static constexpr int code = -1;
+    static constexpr int bytes = 0;
+    struct Vec {};
+};
+
+struct TF32
+{
+    static constexpr int code = DT_F32;
+    static constexpr int bytes = 4;
+    struct Vec { u32x4 a, b; };
+};
+struct TF16
+{
+    static constexpr int code = DT_F16;
+    static constexpr int bytes = 2;
+    struct Vec { u32x4 a; };
+};
+struct TBF16
+{
+    static constexpr int code = DT_BF16;
+    static constexpr int bytes = 2;
+    struct Vec { u32x4 a; };
+};
+
+__device__ __forceinline__ float f16lo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu)); }
+__device__ __forceinline__ float f16hi(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)); }
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t pack_f16(float lo, float hi)
+{
+    f16x2 h = { (_Float16)lo, (_Float16)hi };
+    return __builtin_bit_cast(uint32_t, h);
+}
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi)
+{
+    f32x2 f = { lo, hi };
+    bf16x2 h = __builtin_convertvector(f, bf16x2);
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// Round an fp32 value to a 16-bit format and back (exact re-expansion).
+__device__ __forceinline__ float round_f16(float v) { return (float)(_Float16)v; }
+__device__ __forceinline__ float round_bf16(float v) { return bf16lo(pack_bf16(v, 0.0f)); }
+
+template <class T> __device__ __forceinline__ typename T::Vec load8(const void* base, int64_t elem);
+template <class T> __device__ __forceinline__ void store8(void* base, int64_t elem, const typename T::Vec& v);
+template <class T> __device__ __forceinline__ void unpack8(const typename T::Vec& v, float (&f)[8]);
+template <class T> __device__ __forceinline__ typename T::Vec pack8(const float (&f)[8]);
+template <class T> __device__ __forceinline__ float round_to(float v);
+
+template <> __device__ __forceinline__ TF16::Vec load8<TF16>(const void* base, int64_t e)
+{
+    return { *(const u32x4*)((const uint16_t*)base + e) };
+}
+template <> __device__ __forceinline__ TBF16::Vec load8<TBF16>(const void* base, int64_t e)
+{
+    return { *(const u32x4*)((const uint16_t*)base + e) };
+}
+template <> __device__ __forceinline__ TF32::Vec load8<TF32>(const void* base, int64_t e)
+{
+    const u32x4* p = (const u32x4*)((const float*)base + e);
+    return { p[0], p[1] };
+}
+
+template <> __device__ __forceinline__ void store8<TF16>(void* base, int64_t e, const TF16::Vec& v)
+{
+    *(u32x4*)((uint16_t*)base + e) = v.a;
+}
+template <> __device__ __forceinline__ void store8<TBF16>(void* base, int64_t e, const TBF16::Vec& v)
+{
+    *(u32x4*)((uint16_t*)base + e) = v.a;
+}
+template <> __device__ __forceinline__ void store8<TF32>(void* base, int64_t e, const TF32::Vec& v)
+{
+    u32x4* p = (u32x4*)((float*)base + e);
+    p[0] = v.a;
+    p[1] = v.b;
+}
+
+template <> __device__ __forceinline__ void unpack8<TF16>(const TF16::Vec& v, float (&f)[8])
+{
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) { f[2 * i] = f16lo(v.a[i]); f[2 * i + 1] = f16hi(v.a[i]); }
+}
+template <> __device__ __forceinline__ void unpack8<TBF16>(const TBF16::Vec& v, float (&f)[8])
+{
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) { f[2 * i] = bf16lo(v.a[i]); f[2 * i + 1] = bf16hi(v.a[i]); }
+}
+template <> __device__ __forceinline__ void unpack8<TF32>(const TF32::Vec& v, float (&f)[8])
+{
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) { f[i] = __builtin_bit_cast(float, v.a[i]); f[4 + i] = __builtin_bit_cast(float, v.b[i]); }
+}
+
+template <> __device__ __forceinline__ TF16::Vec pack8<TF16>(const float (&f)[8])
+{
+    TF16::Vec v;
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) v.a[i] = pack_f16(f[2 * i], f[2 * i + 1]);
+    return v;
+}
+template <> __device__ __forceinline__ TBF16::Vec pack8<TBF16>(const float (&f)[8])
+{
+    TBF16::Vec v;
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) v.a[i] = pack_bf16(f[2 * i], f[2 * i + 1]);
+    return v;
+}
+template <> __device__ __forceinline__ TF32::Vec pack8<TF32>(const float (&f)[8])
+{
+    TF32::Vec v;
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) { v.a[i] = __builtin_bit_cast(uint32_t, f[i]); v.b[i] = __builtin_bit_cast(uint32_t, f[4 + i]); }
+    return v;
+}
+
+template <> __device__ __forceinline__ float round_to<TF32>(float v) { return v; }
+template <> __device__ __forceinline__ float round_to<TF16>(float v) { return round_f16(v); }
+template <> __device__ __forceinline__ float round_to<TBF16>(float v) { return round_bf16(v); }
+
+// Scalar element access (generic fallback kernels).
+__device__ __forceinline__ float load1(const void* p, int dt, int64_t i)
+{
+    if (dt == DT_F16) return (float)((const _Float16*)p)[i];
+    if (dt == DT_BF16) return __builtin_bit_cast(float, (uint32_t)((const uint16_t*)p)[i] << 16);
+    return ((const float*)p)[i];
+}
+__device__ __forceinline__ void store1(void* p, int dt, int64_t i, float v)
+{
+    if (dt == DT_F16) ((_Float16*)p)[i] = (_Float16)v;
+    else if (dt == DT_BF16) ((uint16_t*)p)[i] = (uint16_t)(pack_bf16(v, 0.0f) & 0xffffu);
+    else ((float*)p)[i] = v;
+}
+__device__ __forceinline__ float round1(float v, int dt)
+{
+    if (dt == DT_F16) return round_f16(v);
+    if (dt == DT_BF16) return round_bf16(v);
+    return v;
+}
+
+// 8 elements of a runtime-typed vector (norm weights: tiny, L2-resident, uniform branch).
+__device__ __forceinline__ void load8_dyn(const void* base, int dt, int64_t e, float (&f)[8])
+{
+    if (dt == DT_F16) unpack8<TF16>(load8<TF16>(base, e), f);
+    else if (dt == DT_BF16) unpack8<TBF16>(load8<TBF16>(base, e), f);
+    else unpack8<TF32>(load8<TF32>(base, e), f);
+}
+
+// CLAMP_FP16: +-inf -> +-65504, NaN -> 65504 (v_min/v_max return the non-NaN operand).
+__device__ __forceinline__ float clamp_f16(float v) { return fmaxf(-65504.0f, fminf(v, 65504.0f)); }
+
+// ---------------------------------------------------------------------------------------------
+// Reductions.
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+constexpr int DPP_QUAD_XOR1 = 0xb1;       // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4e;       // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;
+constexpr int DPP_ROW_ROR8 = 0x128;
+
+// Sum over aligned groups of W lanes (W = 1, 2, 4, ..., 64); every lane of a group gets the sum.
+// Must be called with the whole wave active.
+template <int W>
+__device__ __forceinline__ float group_sum(float v)
+{
+    if constexpr (W >= 2) v += dpp<DPP_QUAD_XOR1>(v);
+    if constexpr (W >= 4) v += dpp<DPP_QUAD_XOR2>(v);
+    if constexpr (W >= 8) v += dpp<DPP_ROW_HALF_MIRROR>(v);
+    if constexpr (W >= 16) v += dpp<DPP_ROW_MIRROR>(v);
+    if constexpr (W >= 32)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401f)); // xor 16
+    if constexpr (W >= 64)
+        v += __shfl_xor(v, 32);
+    return v;
+}
+
+template <int CTRL>
+__device__ __forceinline__ double dpp64(double v)
+{
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xf, 0xf, false);
+    return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+// fp64 group sum (as group_sum): used where the statistic must match a double-precision oracle
+// bit-for-bit after rounding to fp32.
+template <int W>
+__device__ __forceinline__ double group_sum64(double v)
+{
+    if constexpr (W >= 2) v += dpp64<DPP_QUAD_XOR1>(v);
+    if constexpr (W >= 4) v += dpp64<DPP_QUAD_XOR2>(v);
+    if constexpr (W >= 8) v += dpp64<DPP_ROW_HALF_MIRROR>(v);
+    if constexpr (W >= 16) v += dpp64<DPP_ROW_MIRROR>(v);
+    if constexpr (W >= 32) v += __shfl_xor(v, 16);
+    if constexpr (W >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
+// Full-wave sum, uniform result: row sums by DPP, then the four rows combined through readlane.
+__device__ __forceinline__ float wave_sum(float v)
+{
+    v = group_sum<16>(v);
+    int iv = __builtin_bit_cast(int, v);
+    float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
+    float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16));
+    float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32));
+    float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+// Workgroup sum (blockDim.x a multiple of 64, at most 1024): one LDS hop across waves.  Every
+// thread gets the same value (all waves add the partials in the same order).
+__device__ __forceinline__ float block_sum(float v, float* lds16)
+{
+    v = wave_sum(v);
+    const int nw = blockDim.x >> 6;
+    if (nw == 1) return v;
+    if ((threadIdx.x & 63) == 0) lds16[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < nw; ++i) t += lds16[i];
+    return t;
+}
+
+// fp64 workgroup sum through LDS (lds must hold one double per wave).
+__device__ __forceinline__ double block_sum64(double v, double* lds16)
+{
+    v = group_sum64<64>(v);
+    const int nw = blockDim.x >> 6;
+    if (nw == 1) return v;
+    if ((threadIdx.x & 63) == 0) lds16[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int i = 0; i < nw; ++i) t += lds16[i];
+    __syncthreads();
+    return t;
+}
+
+// rsqrt(sum / n + eps) with the sum carried in fp64 and rounded once to fp32, the division and add
+// in fp32, and the reciprocal square root in fp64 rounded once: the exact statistic of the CPU oracle.
+__device__ __forceinline__ float rms_factor_f64(double sum, int n, float eps)
+{
+    const float mean = (float)sum / (float)n;
+    return (float)(1.0 / sqrt((double)(mean + eps)));
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host-side runtime dtype -> tag dispatch.
+
+template <class F>
+inline bool with_float_type(int dt, F&& f)
+{
+    switch (dt)
+    {
+        case DT_F32: f(TF32{}); return true;
+        case DT_F16: f(TF16{}); return true;
+        case DT_BF16: f(TBF16{}); return true;
+        default: return false;
+    }
+}
+
+}  // namespace exl3r

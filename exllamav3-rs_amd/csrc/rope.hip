@@ -1,0 +1,414 @@
+// Fused per-head RMSNorm + rotary embedding for gfx950: exl3r_rope (replaces exl3_shim_rope,
+// reference csrc/exl3_shim.cpp:87-98 -> rope / rope_gr, kernels/rope.cu:279-467).
+//
+// Semantics follow rope_kernel (kernels/rope.cu:16-255):
+//   position of token s of sequence b: position + s | positions[b] + s | position_ids[b*seq + s]
+//   (rope.cu:55-67); head RMSNorm iff q_norm is given (rope.cu:250): sum of squares over the head
+//   (carried in fp64), rmf = rsqrt(sum / head_dim + eps); f16 weights with f16 heads round twice in half precision,
+//   out = h(h(w + cb) * h(v * rmf)) (rope.cu:222-229); other weights out = io((v * rmf) * (w + cb))
+//   (rope.cu:212-221); the rotation reads the io-rounded normed head: angle = inv_freq[t] * (float)pos,
+//   cos/sin * attn_factor (rope.cu:69-85), NeoX pairs (t, t + R/2), GPT-J pairs (2t, 2t+1), each
+//   result rounded once (rope.cu:152-185); dims >= R pass through.
+//   sin/cos use the accurately range-reduced sincosf (positions reach 3e4 and beyond), not the
+//   reference's __sinf/__cosf; the head sum is a full xor-butterfly sum in every lane (the reference's
+//   shfl_down sum stored from all lanes, rope.cu:190-204, is only correct in lane 0).
+//
+// Layout: one workgroup per token (decode: several per token, splitting the heads).  A head of
+// head_dim elements is held by LPH = head_dim / 8 lanes, 8 elements (16 bytes) per lane, so a wave
+// holds 64 / LPH heads (4 heads of 128).  The head sum is a DPP butterfly inside the LPH-lane group;
+// NeoX partners live R/16 lanes apart in the same group and are exchanged with ds_bpermute, GPT-J
+// partners sit in the same lane.  sin/cos are computed once per (token, frequency) into LDS and
+// shared by every head of the token.
+#include "abi.hpp"
+#include "common.cuh"
+
+namespace exl3r {
+
+struct RopeArgs
+{
+    const void* q;
+    void* oq;
+    const void* k;
+    void* ok;
+    int64_t q_ts, q_hs, k_ts, k_hs;   // token / head strides (elements)
+    int hq, hk, hd, R;
+    int64_t seq_len, tokens;
+    const float* inv_freq;
+    int32_t position;
+    const int32_t* positions;
+    const int32_t* position_ids;
+    const void* qw;
+    const void* kw;
+    int wt;
+    float eps, cb, attn;
+    int heads_per_wg;
+};
+
+enum { NORM_NONE = 0, NORM_HALF = 1, NORM_F32 = 2 };
+
+__device__ __forceinline__ int token_position(const RopeArgs& a, int64_t tok)
+{
+    const int64_t b = tok / a.seq_len;
+    const int s = (int)(tok - b * a.seq_len);
+    if (a.positions) return a.positions[b] + s;
+    if (a.position_ids) return a.position_ids[tok];
+    return a.position + s;
+}
+
+// sin/cos of every rotary frequency of this token into LDS (float2 {cos, sin} * attn_factor).
+__device__ __forceinline__ void fill_sincos(const RopeArgs& a, int pos, float2* cs)
+{
+    const float pf = (float)pos;
+    for (int t = threadIdx.x; t < a.R / 2; t += blockDim.x)
+    {
+        const float ang = __fmul_rn(a.inv_freq[t], pf);
+        float sn, c;
+        sincosf(ang, &sn, &c);
+        cs[t] = make_float2(c * a.attn, sn * a.attn);
+    }
+}
+
+template <class IO, int MODE, int LPH, int ITERS, int NORM>
+__global__ __launch_bounds__(1024) void k_rope(RopeArgs a)
+{
+    extern __shared__ float2 cs[];
+    for (int64_t tok = blockIdx.x; tok < a.tokens; tok += gridDim.x)
+    {
+        const int tid = threadIdx.x;
+        const int slot = tid / LPH;
+        const int lane = tid % LPH;
+        const int slots = blockDim.x / LPH;
+        const int nheads = a.hq + a.hk;
+        const int h0 = blockIdx.y * a.heads_per_wg;
+        const int h1 = min(nheads, h0 + a.heads_per_wg);
+        const bool lane_ok = lane * 8 < a.hd;
+
+        // Head loads first, so HBM latency overlaps the sin/cos evaluation.
+        typename IO::Vec v[ITERS];
+        char* optr[ITERS];
+        bool act[ITERS];
+        #pragma unroll
+        for (int it = 0; it < ITERS; ++it)
+        {
+            const int head = h0 + slot + it * slots;
+            act[it] = head < h1 && lane_ok;
+            optr[it] = nullptr;
+            if (act[it])
+            {
+                const char* ip;
+                if (head < a.hq)
+                {
+                    ip = (const char*)a.q + (tok * a.q_ts + (int64_t)head * a.q_hs) * IO::bytes;
+                    optr[it] = (char*)a.oq + (tok * a.q_ts + (int64_t)head * a.q_hs) * IO::bytes;
+                }
+                else
+                {
+                    ip = (const char*)a.k + (tok * a.k_ts + (int64_t)(head - a.hq) * a.k_hs) * IO::bytes;
+                    optr[it] = (char*)a.ok + (tok * a.k_ts + (int64_t)(head - a.hq) * a.k_hs) * IO::bytes;
+                }
+                v[it] = load8<IO>(ip, (int64_t)lane * 8);
+            }
+        }
+
+        const int pos = token_position(a, tok);
+        fill_sincos(a, pos, cs);
+        __syncthreads();
+
+        const int e0 = lane * 8;            // first head element held by this lane
+        const int half = a.R / 2;
+        #pragma unroll
+        for (int it = 0; it < ITERS; ++it)
+        {
+            const int head = h0 + slot + it * slots;
+            float f[8];
+            if (act[it]) unpack8<IO>(v[it], f);
+            else
+            {
+                #pragma unroll
+                for (int j = 0; j < 8; ++j) f[j] = 0.0f;
+            }
+
+            if constexpr (NORM != NORM_NONE)
+            {
+                // Sum of squares in fp64 (squares of 16-bit values are exact), one rounding to fp32:
+                // the normed head is then bit-identical to a double-precision evaluation, so the
+                // rotation that follows cannot amplify a last-bit difference through cancellation.
+                double ss = 0.0;
+                #pragma unroll
+                for (int j = 0; j < 8; ++j) ss = fma((double)f[j], (double)f[j], ss);
+                ss = group_sum64<LPH>(ss);
+                const float rmf = rms_factor_f64(ss, a.hd, a.eps);
+                if (act[it])
+                {
+                    const void* w = head < a.hq ? a.qw : a.kw;
+                    if constexpr (NORM == NORM_HALF)
+                    {
+                        const TF16::Vec wv = load8<TF16>(w, e0);
+                        const _Float16 cbh = (_Float16)a.cb;
+                        #pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                        {
+                            const uint32_t word = wv.a[j >> 1];
+                            const _Float16 wh = __builtin_bit_cast(_Float16, (uint16_t)((j & 1) ? word >> 16 : word & 0xffffu)) + cbh;
+                            const _Float16 nh = (_Float16)(f[j] * rmf);
+                            f[j] = (float)(wh * nh);
+                        }
+                    }
+                    else
+                    {
+                        float wf[8];
+                        load8_dyn(w, a.wt, e0, wf);
+                        #pragma unroll
+                        for (int j = 0; j < 8; ++j) f[j] = round_to<IO>((f[j] * rmf) * (wf[j] + a.cb));
+                    }
+                }
+            }
+
+            if constexpr (MODE == EXL3R_ROPE_GPTJ)
+            {
+                #pragma unroll
+                for (int p = 0; p < 4; ++p)
+                {
+                    const int e = e0 + 2 * p;
+                    if (e < a.R)
+                    {
+                        const float2 c = cs[e >> 1];
+                        const float v1 = f[2 * p], v2 = f[2 * p + 1];
+                        f[2 * p] = v1 * c.x - v2 * c.y;
+                        f[2 * p + 1] = v2 * c.x + v1 * c.y;
+                    }
+                }
+            }
+            else
+            {
+                // Partner lane half / 8 lanes away inside the head's lane group; values are exchanged as
+                // packed io words (exact: they are io-rounded already).
+                const int dl = half >> 3;
+                const bool rot = e0 < a.R;
+                const bool lower = e0 < half;
+                const int src_lane = rot ? (lower ? tid + dl : tid - dl) : tid;
+                uint32_t mine[4], other[4];
+                const typename IO::Vec pk = pack8<IO>(f);
+                #pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    mine[i] = pk.a[i];
+                    other[i] = (uint32_t)__builtin_amdgcn_ds_bpermute((src_lane & 63) << 2, (int)mine[i]);
+                }
+                if (rot)
+                {
+                    typename IO::Vec po;
+                    #pragma unroll
+                    for (int i = 0; i < 4; ++i) po.a[i] = other[i];
+                    float g[8];
+                    unpack8<IO>(po, g);
+                    const int t0 = lower ? e0 : e0 - half;
+                    #pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                    {
+                        const float2 c = cs[t0 + j];
+                        f[j] = lower ? f[j] * c.x - g[j] * c.y : f[j] * c.x + g[j] * c.y;
+                    }
+                }
+            }
+
+            if (act[it]) store8<IO>(optr[it], (int64_t)e0, pack8<IO>(f));
+        }
+        __syncthreads();   // cs[] is refilled for the next token
+    }
+}
+
+// Generic fallback (any even head_dim / rotary_dim, any alignment): one workgroup per token, heads
+// walked serially through an LDS copy.
+__global__ __launch_bounds__(256) void k_rope_generic(RopeArgs a, int dt, int mode, int norm)
+{
+    extern __shared__ float2 cs[];
+    __shared__ double red[16];
+    float* hv = (float*)(cs + a.R / 2);
+    const int tid = threadIdx.x;
+    const int half = a.R / 2;
+    for (int64_t tok = blockIdx.x; tok < a.tokens; tok += gridDim.x)
+    {
+    fill_sincos(a, token_position(a, tok), cs);
+    __syncthreads();
+    for (int head = 0; head < a.hq + a.hk; ++head)
+    {
+        const bool isq = head < a.hq;
+        const void* ip = isq ? a.q : a.k;
+        void* op = isq ? a.oq : a.ok;
+        const int64_t off = isq ? tok * a.q_ts + (int64_t)head * a.q_hs : tok * a.k_ts + (int64_t)(head - a.hq) * a.k_hs;
+        double ss = 0.0;
+        for (int d = tid; d < a.hd; d += blockDim.x)
+        {
+            const float x = load1(ip, dt, off + d);
+            hv[d] = x;
+            ss = fma((double)x, (double)x, ss);
+        }
+        ss = block_sum64(ss, red);
+        if (norm != NORM_NONE)
+        {
+            const float rmf = rms_factor_f64(ss, a.hd, a.eps);
+            const void* w = isq ? a.qw : a.kw;
+            for (int d = tid; d < a.hd; d += blockDim.x)
+            {
+                if (norm == NORM_HALF)
+                {
+                    const _Float16 wh = ((const _Float16*)w)[d] + (_Float16)a.cb;
+                    hv[d] = (float)(wh * (_Float16)(hv[d] * rmf));
+                }
+                else
+                    hv[d] = round1((hv[d] * rmf) * (load1(w, a.wt, d) + a.cb), dt);
+            }
+        }
+        __syncthreads();
+        for (int t = tid; t < half; t += blockDim.x)
+        {
+            const int i1 = mode == EXL3R_ROPE_NEOX ? t : 2 * t;
+            const int i2 = mode == EXL3R_ROPE_NEOX ? t + half : 2 * t + 1;
+            const float v1 = hv[i1], v2 = hv[i2];
+            hv[i1] = v1 * cs[t].x - v2 * cs[t].y;
+            hv[i2] = v2 * cs[t].x + v1 * cs[t].y;
+        }
+        __syncthreads();
+        for (int d = tid; d < a.hd; d += blockDim.x) store1(op, dt, off + d, hv[d]);
+        __syncthreads();
+    }
+    }
+}
+
+template <class IO, int MODE, int LPH, int NORM>
+static void launch_rope_lph(const RopeArgs& a, dim3 grid, int threads, int iters, hipStream_t s)
+{
+    const size_t lds = (size_t)(a.R / 2) * sizeof(float2);
+    switch (iters)
+    {
+        case 1: k_rope<IO, MODE, LPH, 1, NORM><<<grid, threads, lds, s>>>(a); break;
+        case 2: k_rope<IO, MODE, LPH, 2, NORM><<<grid, threads, lds, s>>>(a); break;
+        default: k_rope<IO, MODE, LPH, 4, NORM><<<grid, threads, lds, s>>>(a); break;
+    }
+}
+
+template <class IO, int MODE, int NORM>
+static void launch_rope_vec(RopeArgs a, int lph, hipStream_t s)
+{
+    // Heads per workgroup: a whole token per workgroup when there are enough tokens to fill the
+    // GPU, otherwise split the heads of a token over 256-thread workgroups.
+    const int nheads = a.hq + a.hk;
+    const int lanes = nheads * lph;
+    int threads, iters;
+    const Tuning& tu = tuning();
+    if (tu.rope_threads > 0 && tu.rope_threads % 64 == 0 && tu.rope_threads <= 1024 && tu.rope_threads >= lph)
+    {
+        threads = tu.rope_threads;
+        iters = 1;
+    }
+    else if (a.tokens >= 512)
+    {
+        iters = (lanes + 1023) / 1024;
+        if (iters > 4) iters = 4;
+        int per = (lanes + iters - 1) / iters;
+        threads = ((per + 63) / 64) * 64;
+        if (threads > 1024) threads = 1024;
+    }
+    else
+    {
+        iters = 1;
+        threads = lanes < 256 ? ((lanes + 63) / 64) * 64 : 256;
+    }
+    if (iters == 3) iters = 4;
+    a.heads_per_wg = (threads / lph) * iters;
+    const int groups = (nheads + a.heads_per_wg - 1) / a.heads_per_wg;
+    const dim3 grid((unsigned)(a.tokens < kMaxGridX ? a.tokens : kMaxGridX), (unsigned)groups);
+    switch (lph)
+    {
+        case 1: launch_rope_lph<IO, MODE, 1, NORM>(a, grid, threads, iters, s); break;
+        case 2: launch_rope_lph<IO, MODE, 2, NORM>(a, grid, threads, iters, s); break;
+        case 4: launch_rope_lph<IO, MODE, 4, NORM>(a, grid, threads, iters, s); break;
+        case 8: launch_rope_lph<IO, MODE, 8, NORM>(a, grid, threads, iters, s); break;
+        case 16: launch_rope_lph<IO, MODE, 16, NORM>(a, grid, threads, iters, s); break;
+        case 32: launch_rope_lph<IO, MODE, 32, NORM>(a, grid, threads, iters, s); break;
+        default: launch_rope_lph<IO, MODE, 64, NORM>(a, grid, threads, iters, s); break;
+    }
+}
+
+template <class IO>
+static void launch_rope_io(const RopeArgs& a, int mode, int norm, int lph, hipStream_t s)
+{
+    auto go = [&](auto M) {
+        constexpr int MODE = decltype(M)::value;
+        if (norm == NORM_NONE) launch_rope_vec<IO, MODE, NORM_NONE>(a, lph, s);
+        else if (norm == NORM_HALF) launch_rope_vec<IO, MODE, NORM_HALF>(a, lph, s);
+        else launch_rope_vec<IO, MODE, NORM_F32>(a, lph, s);
+    };
+    if (mode == EXL3R_ROPE_GPTJ) go(std::integral_constant<int, EXL3R_ROPE_GPTJ>{});
+    else go(std::integral_constant<int, EXL3R_ROPE_NEOX>{});
+}
+
+}  // namespace exl3r
+
+using namespace exl3r;
+
+extern "C" int exl3r_rope(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int num_heads_q,
+                          const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int num_heads_k,
+                          int dtype, int64_t bsz, int64_t seq_len, int head_dim,
+                          const float* inv_freq, int rotary_dim,
+                          int32_t position, const int32_t* positions, const int32_t* position_ids,
+                          const void* q_norm, const void* k_norm, int norm_dtype,
+                          float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
+                          void* stream)
+{
+    const char* op = "exl3r_rope";
+    if (!q || !out_q || !inv_freq) return set_error(EXL3R_EINVAL, "%s: q, out_q and inv_freq must be non-null", op);
+    if (dtype != EXL3R_F16 && dtype != EXL3R_BF16)
+        return set_error(EXL3R_EDTYPE, "%s: q/k dtype must be f16 or bf16, got %s", op, dtype_name(dtype));
+    if (rope_mode != EXL3R_ROPE_GPTJ && rope_mode != EXL3R_ROPE_NEOX)
+        return set_error(EXL3R_EINVAL, "%s: rope_mode must be GPTJ (1) or NEOX (2), got %d", op, rope_mode);
+    if (bsz < 0 || seq_len < 0 || num_heads_q <= 0 || (k && num_heads_k <= 0))
+        return set_error(EXL3R_EINVAL, "%s: invalid shape bsz=%lld seq_len=%lld heads=(%d,%d)", op, (long long)bsz,
+                         (long long)seq_len, num_heads_q, num_heads_k);
+    if (head_dim <= 0 || head_dim % 2 || head_dim > 4096)
+        return set_error(EXL3R_EINVAL, "%s: head_dim %d must be even and in [2, 4096]", op, head_dim);
+    if (rotary_dim < 2 || rotary_dim % 2 || rotary_dim > head_dim)
+        return set_error(EXL3R_EINVAL, "%s: rotary_dim %d must be even and in [2, head_dim]", op, rotary_dim);
+    if (q_head_stride < head_dim || q_tok_stride < (int64_t)num_heads_q * q_head_stride)
+        return set_error(EXL3R_EINVAL, "%s: q strides (%lld, %lld) overlap heads", op, (long long)q_tok_stride, (long long)q_head_stride);
+    if (k && (!out_k || k_head_stride < head_dim || k_tok_stride < (int64_t)num_heads_k * k_head_stride))
+        return set_error(EXL3R_EINVAL, "%s: k needs out_k and non-overlapping strides", op);
+    if (positions && position_ids) return set_error(EXL3R_EINVAL, "%s: at most one of positions / position_ids", op);
+    if (q_norm && k && !k_norm) return set_error(EXL3R_EINVAL, "%s: q_norm given without k_norm", op);
+    if (!q_norm && k_norm) return set_error(EXL3R_EINVAL, "%s: k_norm given without q_norm", op);
+    if (q_norm && !is_float_dtype(norm_dtype))
+        return set_error(EXL3R_EDTYPE, "%s: unsupported norm weight dtype %s", op, dtype_name(norm_dtype));
+    const int64_t tokens = bsz * seq_len;
+    if (tokens == 0) return EXL3R_OK;
+    if (tokens > 0x7fffffff) return set_error(EXL3R_EINVAL, "%s: too many tokens", op);
+
+    RopeArgs a{};
+    a.q = q; a.oq = out_q; a.k = k; a.ok = out_k;
+    a.q_ts = q_tok_stride; a.q_hs = q_head_stride; a.k_ts = k_tok_stride; a.k_hs = k_head_stride;
+    a.hq = num_heads_q; a.hk = k ? num_heads_k : 0; a.hd = head_dim; a.R = rotary_dim;
+    a.seq_len = seq_len; a.tokens = tokens; a.inv_freq = inv_freq;
+    a.position = position; a.positions = positions; a.position_ids = position_ids;
+    a.qw = q_norm; a.kw = k_norm; a.wt = norm_dtype;
+    a.eps = norm_eps; a.cb = norm_constant_bias; a.attn = attn_factor;
+    const int norm = !q_norm ? NORM_NONE : (norm_dtype == EXL3R_F16 && dtype == EXL3R_F16) ? NORM_HALF : NORM_F32;
+    hipStream_t s = (hipStream_t)stream;
+
+    int lph = 1;
+    while (lph * 8 < head_dim) lph *= 2;
+    bool vec = head_dim % 8 == 0 && lph <= 64 && rotary_dim % (rope_mode == EXL3R_ROPE_NEOX ? 16 : 2) == 0;
+    vec = vec && aligned16(q) && aligned16(out_q) && q_tok_stride % 8 == 0 && q_head_stride % 8 == 0;
+    vec = vec && (!k || (aligned16(k) && aligned16(out_k) && k_tok_stride % 8 == 0 && k_head_stride % 8 == 0));
+    vec = vec && (!q_norm || (aligned16(q_norm) && (!k_norm || aligned16(k_norm))));
+    if (vec)
+    {
+        if (dtype == EXL3R_F16) launch_rope_io<TF16>(a, rope_mode, norm, lph, s);
+        else launch_rope_io<TBF16>(a, rope_mode, norm, lph, s);
+    }
+    else
+    {
+        const size_t lds = (size_t)(rotary_dim / 2) * sizeof(float2) + (size_t)head_dim * sizeof(float);
+        k_rope_generic<<<(unsigned)(tokens < kMaxGridX ? tokens : kMaxGridX), 256, lds, s>>>(a, dtype, rope_mode, norm);
+    }
+    return launch_status(op);
+}

@@ -1,0 +1,16 @@
+/* Launch-shape overrides for benchmarking sweeps (not part of the drop-in ABI).  0 restores the
+ * automatic choice.  Process-global, not thread-safe: set them before launching. */
+#ifndef EXL3R_TUNING_H
+#define EXL3R_TUNING_H
+#include "../../include/exl3r/rowops.h"
+#ifdef __cplusplus
+extern "C" {
+#endif
+EXL3R_API void exl3r_tune_rms(int maxv, int threads);
+EXL3R_API void exl3r_tune_act(int unroll, int threads, int blocks_per_cu);
+EXL3R_API void exl3r_tune_rope(int threads);
+EXL3R_API void exl3r_tune_embed(int threads);
+#ifdef __cplusplus
+}
+#endif
+#endif

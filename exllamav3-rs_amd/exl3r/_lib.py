@@ -1,0 +1,95 @@
+"""ctypes loading of the gfx950 row-op library (lib/libexl3rowops.so) and its prototypes.
+
+The library is the product; this module is plumbing.  `load()` raises when the shared object is
+missing -- there is no fallback implementation of any op."""
+import ctypes
+import os
+
+_PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_DIR = os.path.join(_PKG_ROOT, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libexl3rowops.so")
+NAIVE_PATH = os.path.join(LIB_DIR, "libexl3r_naive.so")
+HEADER_PATH = os.path.join(os.path.dirname(_PKG_ROOT), "include", "exl3r", "rowops.h")
+
+F32, F16, BF16, I32, I64 = 0, 1, 2, 3, 4
+OK, EINVAL, EDTYPE = 0, -1, -2
+ROPE_NONE, ROPE_GPTJ, ROPE_NEOX = 0, 1, 2
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_f = ctypes.c_float
+_i32 = ctypes.c_int32
+
+PROTOTYPES = {
+    "exl3r_version": (_i, []),
+    "exl3r_last_error": (ctypes.c_char_p, []),
+    "exl3r_rms_norm": (_i, [_vp, _i, _i64, _vp, _i, _vp, _i, _i64, _i64, _i64, _f, _f, _f, _vp]),
+    "exl3r_rms_norm_res_in": (_i, [_vp, _i, _i64, _vp, _i, _vp, _i, _i64, _vp, _i, _i64, _i64, _i64, _f, _f, _f, _vp]),
+    "exl3r_silu_mul": (_i, [_vp, _vp, _i, _vp, _i, _i64, _i64, _i64, _i64, _i64, _f, _vp]),
+    "exl3r_gelu_mul": (_i, [_vp, _vp, _i, _vp, _i, _i64, _i64, _i64, _i64, _i64, _f, _vp]),
+    "exl3r_rope": (_i, [_vp, _vp, _i64, _i64, _i, _vp, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _i,
+                        _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _vp]),
+    "exl3r_embedding": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _i64, _vp, _vp]),
+    "exl3r_embedding_rms_norm": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _i64, _vp, _i,
+                                      _vp, _i, _i64, _f, _f, _f, _vp, _vp]),
+    "exl3r_tune_rms": (None, [_i, _i]),
+    "exl3r_tune_act": (None, [_i, _i, _i]),
+    "exl3r_tune_rope": (None, [_i]),
+    "exl3r_tune_embed": (None, [_i]),
+}
+
+NAIVE_PROTOTYPES = {
+    "naive_add_f16": (_i, [_vp, _vp, _vp, _i64, _vp]),
+    "naive_rms_norm_f16": (_i, [_vp, _vp, _vp, _i64, _i, _f, _vp]),
+    "naive_head_norm_f16": (_i, [_vp, _vp, _i64, _i, _i, _f, _vp]),
+    "naive_rope_neox_f16": (_i, [_vp, _vp, _vp, _i64, _i64, _i, _i, _vp]),
+    "naive_silu_f16": (_i, [_vp, _vp, _i64, _vp]),
+    "naive_mul_f16": (_i, [_vp, _vp, _vp, _i64, _vp]),
+    "calib_copy": (_i, [_vp, _vp, _i64, _vp]),
+}
+
+_lib = None
+_naive = None
+
+
+def _bind(path, protos):
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built: run __graft_entry__.build() (make -C exllamav3-rs_amd)")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in protos.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def load():
+    """The row-op library (ctypes.CDLL with prototypes set)."""
+    global _lib
+    if _lib is None:
+        _lib = _bind(LIB_PATH, PROTOTYPES)
+    return _lib
+
+
+def load_naive():
+    """The naive unfused baseline library (bench only)."""
+    global _naive
+    if _naive is None:
+        _naive = _bind(NAIVE_PATH, NAIVE_PROTOTYPES)
+    return _naive
+
+
+class Exl3rError(RuntimeError):
+    """A non-zero status from a C-ABI entry point (message from exl3r_last_error())."""
+
+    def __init__(self, code, message):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+        self.message = message
+
+
+def check(rc):
+    if rc != OK:
+        raise Exl3rError(rc, load().exl3r_last_error().decode(errors="replace"))
+    return rc

@@ -1,0 +1,156 @@
+"""Torch-tensor wrappers over the C ABI, with the names and argument meaning of the reference's
+`src/ffi.rs` wrappers (rms_norm ffi.rs:293-296, rms_norm_res_in 464-468, silu_mul 492-495,
+gelu_mul 496-499, rope 298-333) plus the embedding gather that replaces Embedding::forward's
+index_select (src/modules.rs:430-436).
+
+Tensors must live on the GPU; every wrapper launches on the current torch stream (the reference's
+kernels use the current torch stream too, kernels/norm.cu:328) unless `stream` is given, and raises
+Exl3rError on a non-zero status (the reference's TORCH_CHECK raises)."""
+import torch
+
+from ._lib import BF16, F16, F32, I32, I64, check, load
+
+_DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.int32: I32, torch.int64: I64}
+
+
+def dtype_code(t):
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}") from None
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t, stream):
+    if stream is not None:
+        return stream.cuda_stream if hasattr(stream, "cuda_stream") else stream
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _rows(t):
+    """[..., dim] tensor as (rows, dim, row_stride); the last dim must be dense and the leading dims
+    must collapse into one stride."""
+    if t.dim() == 0:
+        raise ValueError("expected at least 1-D tensor")
+    dim = t.shape[-1]
+    if t.dim() == 1:
+        return 1, dim, dim
+    if dim > 1 and t.stride(-1) != 1:
+        raise ValueError("last dimension must be contiguous")
+    try:
+        v = t.view(-1, dim)
+    except RuntimeError as e:
+        raise ValueError("leading dimensions must collapse to one row stride") from e
+    rows = v.shape[0]
+    return rows, dim, max(dim, v.stride(0)) if rows > 1 else dim
+
+
+def rms_norm(x, w, y, eps, constant_bias=0.0, constant_scale=1.0, stream=None):
+    """y = RMSNorm(x) * (w + constant_bias) * constant_scale over the last dim (w may be None)."""
+    rows, dim, ldx = _rows(x)
+    ry, dy, ldy = _rows(y)
+    if (ry, dy) != (rows, dim):
+        raise ValueError("x and y shapes differ")
+    check(load().exl3r_rms_norm(_ptr(x), dtype_code(x), ldx, _ptr(w), dtype_code(w) if w is not None else F16,
+                                _ptr(y), dtype_code(y), ldy, rows, dim, eps, constant_bias, constant_scale,
+                                _stream(x, stream)))
+
+
+def rms_norm_res_in(x, w, y, r, eps, constant_bias=0.0, constant_scale=1.0, stream=None):
+    """r += x (in place, rounded to r's dtype), y = RMSNorm(r) * (w + constant_bias) * constant_scale."""
+    rows, dim, ldx = _rows(x)
+    ry, dy, ldy = _rows(y)
+    rr, dr, ldr = _rows(r)
+    if (ry, dy) != (rows, dim) or (rr, dr) != (rows, dim):
+        raise ValueError("x, y and r shapes differ")
+    check(load().exl3r_rms_norm_res_in(_ptr(x), dtype_code(x), ldx, _ptr(w), dtype_code(w) if w is not None else F16,
+                                       _ptr(y), dtype_code(y), ldy, _ptr(r), dtype_code(r), ldr, rows, dim,
+                                       eps, constant_bias, constant_scale, _stream(x, stream)))
+
+
+def _act(fn, x, y, z, act_limit, stream):
+    rows, cols, ldx = _rows(x)
+    ry, cy, ldy = _rows(y)
+    rz, cz, ldz = _rows(z)
+    if (ry, cy) != (rows, cols) or (rz, cz) != (rows, cols):
+        raise ValueError("x, y and z shapes differ")
+    if x.dtype != y.dtype:
+        raise TypeError("x and y must share a dtype")
+    check(fn(_ptr(x), _ptr(y), dtype_code(x), _ptr(z), dtype_code(z), rows, cols, ldx, ldy, ldz, act_limit,
+             _stream(x, stream)))
+
+
+def silu_mul(x, y, z, act_limit=0.0, stream=None):
+    """z = silu(x) * y (SwiGLU); act_limit 0 disables clamping."""
+    _act(load().exl3r_silu_mul, x, y, z, act_limit, stream)
+
+
+def gelu_mul(x, y, z, act_limit=0.0, stream=None):
+    """z = gelu_tanh(x) * y."""
+    _act(load().exl3r_gelu_mul, x, y, z, act_limit, stream)
+
+
+def rope(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias,
+         rope_mode, attn_factor, position_ids=None, stream=None):
+    """Fused (optional) q/k head RMSNorm + RoPE.  q, k: (bsz, seq_len, heads, head_dim); `positions`
+    (int32 [bsz], device) or `position_ids` (int32 [bsz, seq_len], device) override `position`."""
+    if q.dim() != 4:
+        raise ValueError("q must be (bsz, seq_len, heads, head_dim)")
+    bsz, seq, hq, hd = q.shape
+    if q.stride(3) != 1 or out_q.stride() != q.stride() or out_q.shape != q.shape:
+        raise ValueError("q innermost dim must be dense and out_q must share q's layout")
+    if seq > 1 and q.stride(0) != seq * q.stride(1) and bsz > 1:
+        raise ValueError("q batch stride must be seq_len * token stride")
+    hk, k_ts, k_hs = 0, 0, 0
+    if k is not None:
+        if k.dim() != 4 or k.shape[0] != bsz or k.shape[1] != seq or k.shape[3] != hd:
+            raise ValueError("k is incorrect shape")
+        if k.stride(3) != 1 or out_k is None or out_k.stride() != k.stride():
+            raise ValueError("k innermost dim must be dense and out_k must share k's layout")
+        hk, k_ts, k_hs = k.shape[2], k.stride(1), k.stride(2)
+    for t in (positions, position_ids):
+        if t is not None and t.dtype != torch.int32:
+            raise TypeError("positions / position_ids must be int32")
+    nw = q_norm if q_norm is not None else k_norm
+    check(load().exl3r_rope(_ptr(q), _ptr(out_q), q.stride(1), q.stride(2), hq,
+                            _ptr(k), _ptr(out_k), k_ts, k_hs, hk,
+                            dtype_code(q), bsz, seq, hd, _ptr(inv_freq), inv_freq.shape[-1] * 2,
+                            int(position), _ptr(positions), _ptr(position_ids),
+                            _ptr(q_norm), _ptr(k_norm), dtype_code(nw) if nw is not None else F16,
+                            norm_eps, norm_constant_bias, rope_mode, attn_factor, _stream(q, stream)))
+
+
+def embedding(table, ids, out, err_flag=None, stream=None):
+    """out[i] = table[ids[i]] (bit-exact, or exact upcast to f32)."""
+    vocab, hidden = table.shape
+    n = ids.numel()
+    ro, ho, ldo = _rows(out)
+    if (ro, ho) != (n, hidden):
+        raise ValueError("out must be [ids.numel(), hidden]")
+    check(load().exl3r_embedding(_ptr(table), dtype_code(table), vocab, hidden, table.stride(0),
+                                 _ptr(ids), dtype_code(ids), n, _ptr(out), dtype_code(out), ldo,
+                                 _ptr(err_flag), _stream(table, stream)))
+
+
+def embedding_rms_norm(table, ids, h, w, y, eps, constant_bias=0.0, constant_scale=1.0, err_flag=None,
+                       stream=None):
+    """h[i] = table[ids[i]] (h may be None), y = RMSNorm(h) * (w + constant_bias) * constant_scale."""
+    vocab, hidden = table.shape
+    n = ids.numel()
+    ry, hy, ldy = _rows(y)
+    if (ry, hy) != (n, hidden):
+        raise ValueError("y must be [ids.numel(), hidden]")
+    ldh, ht = hidden, F32
+    if h is not None:
+        rh, hh, ldh = _rows(h)
+        if (rh, hh) != (n, hidden):
+            raise ValueError("h must be [ids.numel(), hidden]")
+        ht = dtype_code(h)
+    check(load().exl3r_embedding_rms_norm(_ptr(table), dtype_code(table), vocab, hidden, table.stride(0),
+                                          _ptr(ids), dtype_code(ids), n, _ptr(h), ht, ldh,
+                                          _ptr(w), dtype_code(w) if w is not None else F16,
+                                          _ptr(y), dtype_code(y), ldy, eps, constant_bias, constant_scale,
+                                          _ptr(err_flag), _stream(table, stream)))

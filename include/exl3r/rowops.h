@@ -1,0 +1,175 @@
+/*
+ * exl3r rowops — C ABI of the MI355X (gfx950) fused per-layer row kernels.
+ *
+ * Drop-in replacement for the `at::Tensor*` shim entry points of exllamav3-rs that cover
+ * RMSNorm, residual-fused RMSNorm, SiLU/GELU-gated multiply, q/k head-norm + rotary, and the
+ * token-embedding gather.  Every entry point takes raw device pointers, element counts and row
+ * strides (in ELEMENTS, not bytes), dtype codes and an explicit HIP stream (`hipStream_t`
+ * passed as `void*`; NULL = the null stream).
+ *
+ * Common contract of every `int exl3r_*` entry point:
+ *   - returns EXL3R_OK (0) on success, a negative EXL3R_E* code for an invalid argument (nothing is
+ *     launched), or a positive hipError_t when the launch itself failed;
+ *   - on failure exl3r_last_error() returns a message for the calling thread;
+ *   - never allocates, never synchronises the host, never throws or exits;
+ *   - is stateless and thread-safe; work is enqueued on `stream` only (capture-safe: the
+ *     device-resident position/id buffers are read by the kernels, so a captured graph can be
+ *     replayed after their contents change);
+ *   - arguments are validated before any HIP call, so validation errors are reported even on a
+ *     machine without a GPU.
+ *
+ * Reference entry points replaced (apiplant/exllamav3-rs, cited file:line):
+ *   exl3r_rms_norm          <- exl3_shim_rms_norm         csrc/exl3_shim.cpp:76-80   (ffi.rs:43-50, 293-296)
+ *   exl3r_rms_norm_res_in   <- exl3_shim_rms_norm_res_in  csrc/exl3_shim.cpp:139-142 (ffi.rs:114-117, 464-468)
+ *   exl3r_silu_mul          <- exl3_shim_silu_mul         csrc/exl3_shim.cpp:151     (ffi.rs:125, 492-495)
+ *   exl3r_gelu_mul          <- exl3_shim_gelu_mul         csrc/exl3_shim.cpp:152     (ffi.rs:126, 496-499)
+ *   exl3r_rope              <- exl3_shim_rope             csrc/exl3_shim.cpp:87-98   (ffi.rs:51-65, 298-333)
+ *   exl3r_embedding         <- Embedding::forward's tch index_select + to_kind   src/modules.rs:430-436
+ *   exl3r_embedding_rms_norm<- embed followed by RmsNorm::forward (MTP head)    src/mtp.rs:189-190
+ */
+#ifndef EXL3R_ROWOPS_H
+#define EXL3R_ROWOPS_H
+
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define EXL3R_API __attribute__((visibility("default")))
+#else
+#define EXL3R_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+#define EXL3R_F32  0
+#define EXL3R_F16  1
+#define EXL3R_BF16 2
+#define EXL3R_I32  3
+#define EXL3R_I64  4
+
+/* status codes (positive values are hipError_t) */
+#define EXL3R_OK            0
+#define EXL3R_EINVAL      (-1) /* null pointer, bad shape, stride or scalar argument */
+#define EXL3R_EDTYPE      (-2) /* unsupported dtype or dtype combination */
+
+/* rotary styles: same values as ROPESTYLE_* (kernels/rope.cuh:6-8) and ffi::ROPE_* (src/ffi.rs:217-219) */
+#define EXL3R_ROPE_NONE 0
+#define EXL3R_ROPE_GPTJ 1
+#define EXL3R_ROPE_NEOX 2
+
+/* ABI version: major * 10000 + minor * 100 + patch */
+EXL3R_API int exl3r_version(void);
+
+/* Message describing the last failing call on this thread ("" if none). */
+EXL3R_API const char* exl3r_last_error(void);
+
+/*
+ * RMSNorm over the last dimension:
+ *   y[i, :] = (x[i, :] * (w + constant_bias)) * (constant_scale / sqrt(mean(x[i, :]^2) + eps))
+ * Replaces exl3_shim_rms_norm (csrc/exl3_shim.cpp:76-80) -> rms_norm RES_NONE (kernels/norm.cu:434-448).
+ *   x: [rows, dim] with row stride ldx; dtype F16 (clamped to +-65504 on read), BF16 or F32.
+ *   w: [dim] contiguous, F16/BF16/F32, or NULL for no weight.
+ *   y: [rows, dim] with row stride ldy; F16/BF16/F32.  y == x (in place) is allowed when the
+ *      element sizes and strides agree.
+ */
+EXL3R_API int exl3r_rms_norm(const void* x, int x_dtype, int64_t ldx,
+                   const void* w, int w_dtype,
+                   void* y, int y_dtype, int64_t ldy,
+                   int64_t rows, int64_t dim,
+                   float eps, float constant_bias, float constant_scale,
+                   void* stream);
+
+/*
+ * Pre-norm residual add fused with RMSNorm:
+ *   r[i, :] <- round_r(x[i, :] + r[i, :])   (in place, rounded to r's dtype like an unfused add)
+ *   y[i, :]  = RMSNorm(r[i, :])             (as exl3r_rms_norm, no clamp on the sum)
+ * Replaces exl3_shim_rms_norm_res_in (csrc/exl3_shim.cpp:139-142) -> rms_norm RES_IN
+ * (kernels/norm.cu:467-479, kernel 198-223).  r: [rows, dim], row stride ldr, F16/BF16/F32.
+ */
+EXL3R_API int exl3r_rms_norm_res_in(const void* x, int x_dtype, int64_t ldx,
+                          const void* w, int w_dtype,
+                          void* y, int y_dtype, int64_t ldy,
+                          void* r, int r_dtype, int64_t ldr,
+                          int64_t rows, int64_t dim,
+                          float eps, float constant_bias, float constant_scale,
+                          void* stream);
+
+/*
+ * Gated activations, z = act(x) * y, computed in fp32 and rounded once to z's dtype:
+ *   silu(x) = x / (1 + exp(-x));   gelu(x) = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
+ * With act_limit != 0: act(x) is clamped from above and y to [-act_limit, act_limit] first.
+ * An F16 z is clamped to +-65504 (NaN -> 65504), as the reference's fp32 path does.
+ * Replaces exl3_shim_silu_mul / exl3_shim_gelu_mul (csrc/exl3_shim.cpp:151-152 ->
+ * kernels/activation.cu:24-98, 181-255).
+ *   x, y: [rows, cols], row strides ldx, ldy; both of in_dtype (F16/BF16/F32).
+ *   z:    [rows, cols], row stride ldz; F16/BF16/F32.  z may alias x or y exactly.
+ */
+EXL3R_API int exl3r_silu_mul(const void* x, const void* y, int in_dtype, void* z, int z_dtype,
+                   int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz,
+                   float act_limit, void* stream);
+EXL3R_API int exl3r_gelu_mul(const void* x, const void* y, int in_dtype, void* z, int z_dtype,
+                   int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz,
+                   float act_limit, void* stream);
+
+/*
+ * Fused per-head RMSNorm (optional) + rotary embedding on q and (optional) k.
+ * Replaces exl3_shim_rope (csrc/exl3_shim.cpp:87-98) -> rope (kernels/rope.cu:279-467).
+ *   q, out_q: [bsz, seq_len, num_heads_q, head_dim] of dtype (F16/BF16); element (b, s, h, d) at
+ *             (b*seq_len + s)*q_tok_stride + h*q_head_stride + d.  out_q may equal q (in place);
+ *             out_q uses q's strides.
+ *   k, out_k: same for num_heads_k key heads (k == NULL: q only, as RoPE::apply_one).
+ *   inv_freq: [rotary_dim / 2] float32; rotary_dim even, 2 <= rotary_dim <= head_dim.  Dimensions
+ *             >= rotary_dim pass through (normed if a norm is applied).
+ *   position / positions / position_ids: rotary position of token s of sequence b is
+ *             position + s, or positions[b] + s (int32 [bsz], device), or position_ids[b*seq_len + s]
+ *             (int32 [bsz*seq_len], device).  At most one of positions/position_ids is non-NULL.
+ *   q_norm, k_norm: [head_dim] contiguous norm weights of norm_dtype (F16/BF16/F32) or NULL.  A
+ *             norm is applied iff q_norm != NULL; then k_norm is required when k != NULL.
+ *   rope_mode: EXL3R_ROPE_GPTJ (pairs 2t, 2t+1) or EXL3R_ROPE_NEOX (pairs t, t + rotary_dim/2).
+ *   sin and cos are computed in fp32 from angle = inv_freq[t] * (float)pos and scaled by attn_factor.
+ */
+EXL3R_API int exl3r_rope(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int num_heads_q,
+               const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int num_heads_k,
+               int dtype, int64_t bsz, int64_t seq_len, int head_dim,
+               const float* inv_freq, int rotary_dim,
+               int32_t position, const int32_t* positions, const int32_t* position_ids,
+               const void* q_norm, const void* k_norm, int norm_dtype,
+               float norm_eps, float norm_constant_bias,
+               int rope_mode, float attn_factor,
+               void* stream);
+
+/*
+ * Token-embedding gather: out[i, :] = table[ids[i], :], bit-exact (same dtype) or exactly upcast to
+ * F32.  Replaces Embedding::forward's index_select + to_kind(Float) (src/modules.rs:430-436).
+ *   table: [vocab, hidden], row stride ldt, F16/BF16/F32.
+ *   ids:   [n] I32 or I64, device.
+ *   out:   [n, hidden], row stride ldo; dtype == table dtype, or F32.
+ *   err_flag: NULL or an int32 in device memory; a row whose id is outside [0, vocab) is written as
+ *             zeros and 1 is stored to *err_flag (never cleared by the kernel).
+ */
+EXL3R_API int exl3r_embedding(const void* table, int table_dtype, int64_t vocab, int64_t hidden, int64_t ldt,
+                    const void* ids, int ids_dtype, int64_t n,
+                    void* out, int out_dtype, int64_t ldo,
+                    int32_t* err_flag, void* stream);
+
+/*
+ * Embedding gather fused with the RMSNorm that follows it (src/mtp.rs:189-190 applies
+ * pre_fc_norm_embedding to embed(t)):
+ *   h[i, :] = table[ids[i], :]   (optional output, exact as exl3r_embedding; h == NULL skips it)
+ *   y[i, :] = RMSNorm(h[i, :]) with weight w (NULL: none), eps, constant_bias, constant_scale.
+ */
+EXL3R_API int exl3r_embedding_rms_norm(const void* table, int table_dtype, int64_t vocab, int64_t hidden, int64_t ldt,
+                             const void* ids, int ids_dtype, int64_t n,
+                             void* h, int h_dtype, int64_t ldh,
+                             const void* w, int w_dtype,
+                             void* y, int y_dtype, int64_t ldy,
+                             float eps, float constant_bias, float constant_scale,
+                             int32_t* err_flag, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXL3R_ROWOPS_H */

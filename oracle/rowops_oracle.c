@@ -1,0 +1,497 @@
+/*
+ * CPU oracle for the fused row ops — TEST INFRASTRUCTURE ONLY (see rowops_oracle.h).
+ *
+ * Built with -ffp-contract=off so every fp32 expression is rounded exactly as written: the
+ * reference's rounding points are restated operation by operation, while reductions and
+ * transcendentals are evaluated more accurately (double) than the GPU does, so the oracle is the
+ * "reference semantics with exact arithmetic" the tolerances are measured from.
+ */
+#include "rowops_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+int oracle_mutation = ORM_NONE;
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ------------------------------------------------------------------------------------------ */
+/* Conversions.  f32 -> f16 follows IEEE 754 binary16 RNE (the semantics of __float2half_rn used
+ * at kernels/norm.cu:75-83 and kernels/rope.cu:168-169); f32 -> bf16 is RNE as torch rounds it. */
+
+uint16_t oracle_f32_to_f16(float f)
+{
+    uint32_t x = f2u(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (uint16_t)(sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u));
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);          /* >= 65520 rounds to inf */
+    if (ax < 0x38800000u)                                               /* below 2^-14: subnormal */
+    {
+        if (ax <= 0x33000000u) return (uint16_t)sign;                   /* <= 2^-25 rounds to 0 */
+        uint32_t e = ax >> 23;
+        uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        uint32_t shift = 126u - e;                                      /* 14 .. 24 */
+        uint32_t r = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (r & 1u))) r++;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = (ax - 0x38000000u) >> 13;
+    uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r++;
+    return (uint16_t)(sign | r);
+}
+
+float oracle_f16_to_f32(uint16_t h)
+{
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = ((uint32_t)h >> 10) & 0x1fu;
+    uint32_t m = (uint32_t)h & 0x3ffu;
+    if (e == 0)
+    {
+        float v = (float)m * 0x1p-24f;
+        return u2f(f2u(v) | sign);
+    }
+    if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+uint16_t oracle_f32_to_bf16(float f)
+{
+    uint32_t x = f2u(f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x0040u);
+    uint32_t lsb = (x >> 16) & 1u;
+    x += 0x7fffu + lsb;
+    return (uint16_t)(x >> 16);
+}
+
+float oracle_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+static double round_fmt(double v, int mant_bits, int emin, double maxv)
+{
+    if (v != v || isinf(v) || v == 0.0) return v;
+    int e;
+    frexp(v, &e);
+    int lead = e - 1;
+    if (lead < emin) lead = emin;
+    double q = ldexp(1.0, lead - (mant_bits - 1));
+    double r = nearbyint(v / q) * q;
+    if (fabs(r) > maxv) r = copysign(INFINITY, v);
+    return r;
+}
+
+double oracle_round(double v, int dtype)
+{
+    switch (dtype)
+    {
+        case OR_F16:  return round_fmt(v, 11, -14, 65504.0);
+        case OR_BF16: return round_fmt(v, 8, -126, 0x1.fep127);
+        default:      return (double)(float)v;
+    }
+}
+
+void oracle_f32_to_f16_array(const float* in, uint16_t* out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) out[i] = oracle_f32_to_f16(in[i]);
+}
+
+void oracle_f32_to_bf16_array(const float* in, uint16_t* out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) out[i] = oracle_f32_to_bf16(in[i]);
+}
+
+static inline float ld(const void* p, int dt, int64_t i)
+{
+    switch (dt)
+    {
+        case OR_F16:  return oracle_f16_to_f32(((const uint16_t*)p)[i]);
+        case OR_BF16: return oracle_bf16_to_f32(((const uint16_t*)p)[i]);
+        default:      return ((const float*)p)[i];
+    }
+}
+
+/* Store an fp32 value, rounded once (RNE) to dt. */
+static inline void st(void* p, int dt, int64_t i, float v)
+{
+    switch (dt)
+    {
+        case OR_F16:  ((uint16_t*)p)[i] = oracle_f32_to_f16(v); break;
+        case OR_BF16: ((uint16_t*)p)[i] = oracle_f32_to_bf16(v); break;
+        default:      ((float*)p)[i] = v; break;
+    }
+}
+
+/* Value of v after rounding to dt (what st() followed by ld() yields). */
+static inline float rnd(float v, int dt)
+{
+    switch (dt)
+    {
+        case OR_F16:  return oracle_f16_to_f32(oracle_f32_to_f16(v));
+        case OR_BF16: return oracle_bf16_to_f32(oracle_f32_to_bf16(v));
+        default:      return v;
+    }
+}
+
+/* CLAMP_FP16 = fmaxf(-65504, fminf(x, 65504)) (kernels/util.cuh:69-70): +-inf -> +-65504, NaN -> 65504 */
+static inline float clamp_f16(float v) { return fmaxf(-65504.0f, fminf(v, 65504.0f)); }
+
+static int nthr(int n) { return n > 0 ? n : 1; }
+
+static int fdtype(int dt) { return dt == OR_F32 || dt == OR_F16 || dt == OR_BF16; }
+
+/* ------------------------------------------------------------------------------------------ */
+/* RMSNorm, plain and residual-fused.
+ * Follows rms_norm_kernel (kernels/norm.cu:160-304):
+ *   - f16 x clamped on read (read_half4<true>, norm.cu:42-58, used by read_in at 192-196);
+ *   - RES_IN: r <- round_r(x + r) in place, then the norm reads the rounded sum (add_resid_in,
+ *     norm.cu:198-223);
+ *   - sum of squares (norm.cu:101-108, reduced 140-151; here exactly in double, rounded to fp32);
+ *   - rmf = rsqrt(sum / dim + eps) * constant_scale (norm.cu:273, 288);
+ *   - y = (x * (w + constant_bias)) * rmf in fp32 (apply4, norm.cu:110-116, bias 232-239), or
+ *     x * rmf without a weight (apply4_nw, 118-124), rounded once to y's dtype (write_half4, 75-83). */
+static void rms_row(const float* h, const float* wf, void* y, int yt, int64_t yoff, int64_t dim,
+                    float eps, float cs)
+{
+    double s = 0.0;
+    for (int64_t j = 0; j < dim; ++j) s += (double)h[j] * (double)h[j];
+    float sf = (float)s;
+    int64_t d = oracle_mutation == ORM_RMS_DIM_OFF ? dim - 1 : dim;
+    float mean = sf / (float)d;
+    float t = oracle_mutation == ORM_RMS_NO_EPS ? mean : mean + eps;
+    float rmf = (float)(1.0 / sqrt((double)t));
+    rmf = rmf * cs;
+    for (int64_t j = 0; j < dim; ++j)
+    {
+        float v = wf ? (h[j] * wf[j]) * rmf : h[j] * rmf;
+        st(y, yt, yoff + j, v);
+    }
+}
+
+static float* weight_f32(const void* w, int wt, int64_t dim, float cb)
+{
+    if (!w) return NULL;
+    float* wf = (float*)malloc((size_t)dim * sizeof(float));
+    for (int64_t j = 0; j < dim; ++j)
+    {
+        float v = ld(w, wt, j);
+        if (cb != 0.0f && oracle_mutation != ORM_RMS_NO_BIAS) v = v + cb;
+        wf[j] = v;
+    }
+    return wf;
+}
+
+int oracle_rms_norm(const void* x, int xt, int64_t ldx, const void* w, int wt, void* y, int yt, int64_t ldy,
+                    void* r, int rt, int64_t ldr, int64_t rows, int64_t dim,
+                    float eps, float cb, float cs, int nthreads)
+{
+    if (!x || !y || dim <= 0 || rows < 0) return -1;
+    if (!fdtype(xt) || !fdtype(yt) || (w && !fdtype(wt)) || (r && !fdtype(rt))) return -2;
+    float* wf = weight_f32(w, wt, dim, cb);
+
+    #pragma omp parallel num_threads(nthr(nthreads))
+    {
+        float* h = (float*)malloc((size_t)dim * sizeof(float));
+        #pragma omp for schedule(static)
+        for (int64_t i = 0; i < rows; ++i)
+        {
+            for (int64_t j = 0; j < dim; ++j)
+            {
+                float xv = ld(x, xt, i * ldx + j);
+                if (xt == OR_F16 && oracle_mutation != ORM_RMS_NO_CLAMP) xv = clamp_f16(xv);
+                if (r)
+                {
+                    float hv = xv + ld(r, rt, i * ldr + j);
+                    st(r, rt, i * ldr + j, hv);
+                    if (oracle_mutation != ORM_RES_NO_ROUND) hv = rnd(hv, rt);
+                    xv = hv;
+                }
+                h[j] = xv;
+            }
+            rms_row(h, wf, y, yt, i * ldy, dim, eps, cs);
+        }
+        free(h);
+    }
+    free(wf);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Gated activations, the reference's fp32 path (act_mul_kernel_f, kernels/activation_kernels.cuh:
+ * 189-252) applied to upcast inputs:
+ *   silu(x) = x / (1 + exp(-x))                    (activation_kernels.cuh:34-39)
+ *   gelu(x) = 0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3)))   (activation_kernels.cuh:52-58,
+ *             tanh-form GELU of Hendrycks & Gimpel); evaluated in double through the identity
+ *             0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)), which has no cancellation for x << 0;
+ *   act_limit: y clamped to [-L, L], act clamped from above (activation_kernels.cuh:237-245);
+ *   product in fp32, one RNE to z's dtype, f16 z clamped to +-65504 (clamp_half2_to_finite,
+ *   activation_kernels.cuh:2-7, 249-251; __hmin2/__hmax2 return the non-NaN operand). */
+static double act_d(int act, double x)
+{
+    if (act == OR_ACT_SILU)
+    {
+        double e = oracle_mutation == ORM_SILU_SIGN ? exp(x) : exp(-x);
+        return x / (1.0 + e);
+    }
+    const double c = 0.79788456080286535588;   /* sqrt(2/pi) */
+    double cubic = oracle_mutation == ORM_GELU_NO_CUBIC ? 0.0 : 0.044715 * x * x * x;
+    double u = c * (x + cubic);
+    return x / (1.0 + exp(-2.0 * u));
+}
+
+int oracle_act_mul(int act, const void* x, const void* y, int it, void* z, int zt,
+                   int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz,
+                   float limit, int nthreads)
+{
+    if (!x || !y || !z || rows < 0 || cols < 0) return -1;
+    if (!fdtype(it) || !fdtype(zt)) return -2;
+    if (act != OR_ACT_SILU && act != OR_ACT_GELU) return -1;
+
+    #pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t i = 0; i < rows; ++i)
+    {
+        for (int64_t j = 0; j < cols; ++j)
+        {
+            float a = (float)act_d(act, (double)ld(x, it, i * ldx + j));
+            float u = ld(y, it, i * ldy + j);
+            if (limit != 0.0f)
+            {
+                if (oracle_mutation != ORM_ACT_NO_LIMIT_Y)
+                {
+                    if (u < -limit) u = -limit;
+                    if (u > limit) u = limit;
+                }
+                if (a > limit) a = limit;
+            }
+            float p = a * u;
+            if (zt == OR_F16) p = clamp_f16(p);
+            st(z, zt, i * ldz + j, p);
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Head RMSNorm + rotary embedding, following rope_kernel (kernels/rope.cu:16-255):
+ *   pos = position + s | positions[b] + s | position_ids[b*seq + s]             (rope.cu:55-67)
+ *   head norm (rope.cu:188-233), applied iff q_norm is given (rope.cu:250):
+ *     sum of squares over the head (exact here; the reference's reduction at rope.cu:196-204
+ *     races on a shared slot, the intended full sum is used), rmf = rsqrt(sum/hd + eps),
+ *     f16 weight with f16 I/O: out = h(h(w + h(cb)) * h(v * rmf)), two half roundings
+ *       (rope.cu:222-229; half add/mul are correctly rounded);
+ *     otherwise: out = io(fl32(fl32(v * rmf) * fl32(w + cb)))           (rope.cu:212-221);
+ *   rotary (rope.cu:69-85, 152-185) on the io-rounded normed head:
+ *     angle = fl32(inv_freq[t] * fl32(pos)); c = fl32(cos(angle)) * attn_factor, s likewise;
+ *     NeoX pairs (t, t + R/2), GPT-J pairs (2t, 2t + 1), t < R/2;
+ *     r1 = io(v1 c - v2 s), r2 = io(v2 c + v1 s) in fp32; dims >= R pass through. */
+static void head_norm(float* v, int dt, int hd, const float* wf, const uint16_t* wh16, float eps)
+{
+    if (!wf && !wh16) return;
+    double s = 0.0;
+    for (int d = 0; d < hd; ++d) s += (double)v[d] * (double)v[d];
+    float sf = (float)s;
+    float rmf = (float)(1.0 / sqrt((double)(sf / (float)hd + eps)));
+    for (int d = 0; d < hd; ++d)
+    {
+        float n = v[d] * rmf;
+        if (wh16)
+        {
+            float wv = oracle_f16_to_f32(wh16[d]);
+            if (oracle_mutation == ORM_HEADNORM_1ROUND)
+                v[d] = rnd(n * wv, dt);
+            else
+                v[d] = rnd(rnd(n, OR_F16) * wv, OR_F16);   /* exact product of two halves */
+        }
+        else
+            v[d] = rnd(n * wf[d], dt);
+    }
+}
+
+static void rotate_head(float* v, int dt, int R, const float* cosv, const float* sinv, int mode)
+{
+    for (int t = 0; t < R / 2; ++t)
+    {
+        int i1, i2;
+        if (mode == OR_ROPE_NEOX && oracle_mutation != ORM_ROPE_NEOX_PAIR) { i1 = t; i2 = t + R / 2; }
+        else { i1 = 2 * t; i2 = 2 * t + 1; }
+        float c = cosv[t], s = sinv[t];
+        float v1 = v[i1], v2 = v[i2];
+        float r1 = oracle_mutation == ORM_ROPE_SIGN ? v1 * c + v2 * s : v1 * c - v2 * s;
+        float r2 = v2 * c + v1 * s;
+        v[i1] = rnd(r1, dt);
+        v[i2] = rnd(r2, dt);
+    }
+}
+
+static void rope_head(const void* in, void* out, int64_t off, int dt, int hd, int R,
+                      const float* cosv, const float* sinv, const float* wf, const uint16_t* wh16,
+                      float eps, int mode, float* v)
+{
+    for (int d = 0; d < hd; ++d) v[d] = ld(in, dt, off + d);
+    int norm_after = oracle_mutation == ORM_ROPE_NORM_AFTER;
+    if (!norm_after) head_norm(v, dt, hd, wf, wh16, eps);
+    rotate_head(v, dt, R, cosv, sinv, mode);
+    if (norm_after) head_norm(v, dt, hd, wf, wh16, eps);
+    for (int d = 0; d < hd; ++d) st(out, dt, off + d, v[d]);
+}
+
+int oracle_rope(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int hq,
+                const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int hk,
+                int dt, int64_t bsz, int64_t seq_len, int hd,
+                const float* inv_freq, int R,
+                int32_t position, const int32_t* positions, const int32_t* position_ids,
+                const void* q_norm, const void* k_norm, int nwt,
+                float eps, float cb, int mode, float attn_factor, int nthreads)
+{
+    if (!q || !out_q || !inv_freq || hd <= 0 || (hd & 1) || R < 2 || (R & 1) || R > hd) return -1;
+    if (dt != OR_F16 && dt != OR_BF16) return -2;
+    if (mode != OR_ROPE_GPTJ && mode != OR_ROPE_NEOX) return -1;
+    if (k && !out_k) return -1;
+    if (!k) hk = 0;
+    if (positions && position_ids) return -1;
+    int norm = q_norm != NULL;
+    if (norm && k && !k_norm) return -1;
+    if (norm && !fdtype(nwt)) return -2;
+
+    /* norm weights: f16 weight + f16 io -> half path (weights pre-added in half) */
+    int half_path = norm && nwt == OR_F16 && dt == OR_F16;
+    float* wfq = NULL; float* wfk = NULL; uint16_t* whq = NULL; uint16_t* whk = NULL;
+    if (norm)
+    {
+        const void* ws[2] = { q_norm, k_norm };
+        for (int which = 0; which < 2; ++which)
+        {
+            if (!ws[which]) continue;
+            if (half_path)
+            {
+                uint16_t* wh = (uint16_t*)malloc((size_t)hd * 2);
+                double cbh = (double)oracle_f16_to_f32(oracle_f32_to_f16(cb));
+                for (int d = 0; d < hd; ++d)
+                {
+                    double sum = (double)ld(ws[which], nwt, d) + cbh;      /* __hadd2 (rope.cu:226) */
+                    wh[d] = oracle_f32_to_f16((float)oracle_round(sum, OR_F16));
+                }
+                if (which == 0) whq = wh; else whk = wh;
+            }
+            else
+            {
+                float* wf = (float*)malloc((size_t)hd * sizeof(float));
+                for (int d = 0; d < hd; ++d) wf[d] = ld(ws[which], nwt, d) + cb;
+                if (which == 0) wfq = wf; else wfk = wf;
+            }
+        }
+    }
+
+    int64_t tokens = bsz * seq_len;
+    #pragma omp parallel num_threads(nthr(nthreads))
+    {
+        float* v = (float*)malloc((size_t)hd * sizeof(float));
+        float* cosv = (float*)malloc((size_t)(R / 2) * sizeof(float));
+        float* sinv = (float*)malloc((size_t)(R / 2) * sizeof(float));
+        #pragma omp for schedule(static)
+        for (int64_t tok = 0; tok < tokens; ++tok)
+        {
+            int64_t b = tok / seq_len, s = tok % seq_len;
+            int32_t pos = (int32_t)(position + s);
+            if (positions) pos = (int32_t)(positions[b] + s);
+            else if (position_ids) pos = position_ids[tok];
+            if (oracle_mutation == ORM_ROPE_POS_OFF) pos += 1;
+            float pf = (float)pos;
+            for (int t = 0; t < R / 2; ++t)
+            {
+                float a = inv_freq[t] * pf;
+                float c = (float)cos((double)a) * attn_factor;
+                float sn = (float)sin((double)a) * attn_factor;
+                if (oracle_mutation == ORM_ROPE_SWAP_SINCOS) { float tmp = c; c = sn; sn = tmp; }
+                cosv[t] = c;
+                sinv[t] = sn;
+            }
+            for (int h = 0; h < hq; ++h)
+                rope_head(q, out_q, tok * q_tok_stride + h * q_head_stride, dt, hd, R, cosv, sinv,
+                          wfq, whq, eps, mode, v);
+            for (int h = 0; h < hk; ++h)
+                rope_head(k, out_k, tok * k_tok_stride + h * k_head_stride, dt, hd, R, cosv, sinv,
+                          wfk, whk, eps, mode, v);
+        }
+        free(v); free(cosv); free(sinv);
+    }
+    free(wfq); free(wfk); free(whq); free(whk);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Embedding gather: out[i] = table[ids[i]] (src/modules.rs:430-436: index_select, then an exact
+ * to_kind(Float) upcast).  Out-of-range ids: zero row, *err_flag = 1. */
+static inline int64_t load_id(const void* ids, int idt, int64_t i)
+{
+    return idt == OR_I64 ? ((const int64_t*)ids)[i] : (int64_t)((const int32_t*)ids)[i];
+}
+
+static size_t dsize(int dt) { return dt == OR_F32 ? 4 : 2; }
+
+static int exact_conv(int from, int to) { return from == to || to == OR_F32; }
+
+int oracle_embedding(const void* table, int tt, int64_t vocab, int64_t hidden, int64_t ldt,
+                     const void* ids, int idt, int64_t n, void* out, int ot, int64_t ldo,
+                     int32_t* err_flag, int nthreads)
+{
+    if (!table || !ids || !out || vocab <= 0 || hidden <= 0 || n < 0) return -1;
+    if (!fdtype(tt) || !fdtype(ot) || (idt != OR_I32 && idt != OR_I64) || !exact_conv(tt, ot)) return -2;
+    int bad = 0;
+    #pragma omp parallel for num_threads(nthr(nthreads)) schedule(static) reduction(|:bad)
+    for (int64_t i = 0; i < n; ++i)
+    {
+        int64_t id = load_id(ids, idt, i);
+        if (oracle_mutation == ORM_EMBED_OFF) id += 1;
+        if (id < 0 || id >= vocab)
+        {
+            bad = 1;
+            for (int64_t j = 0; j < hidden; ++j) st(out, ot, i * ldo + j, 0.0f);
+            continue;
+        }
+        if (ot == tt)   /* index_select is a bit copy (NaN payloads included) */
+            memcpy((char*)out + i * ldo * dsize(ot), (const char*)table + id * ldt * dsize(tt), (size_t)hidden * dsize(tt));
+        else
+            for (int64_t j = 0; j < hidden; ++j) st(out, ot, i * ldo + j, ld(table, tt, id * ldt + j));
+    }
+    if (bad && err_flag) *err_flag = 1;
+    return 0;
+}
+
+int oracle_embedding_rms_norm(const void* table, int tt, int64_t vocab, int64_t hidden, int64_t ldt,
+                              const void* ids, int idt, int64_t n,
+                              void* h, int ht, int64_t ldh,
+                              const void* w, int wt, void* y, int yt, int64_t ldy,
+                              float eps, float cb, float cs, int32_t* err_flag, int nthreads)
+{
+    if (!table || !ids || !y || vocab <= 0 || hidden <= 0 || n < 0) return -1;
+    if (!fdtype(tt) || !fdtype(yt) || (w && !fdtype(wt)) || (idt != OR_I32 && idt != OR_I64)) return -2;
+    if (h && (!fdtype(ht) || !exact_conv(tt, ht))) return -2;
+    float* wf = weight_f32(w, wt, hidden, cb);
+    int bad = 0;
+    #pragma omp parallel num_threads(nthr(nthreads)) reduction(|:bad)
+    {
+        float* row = (float*)malloc((size_t)hidden * sizeof(float));
+        #pragma omp for schedule(static)
+        for (int64_t i = 0; i < n; ++i)
+        {
+            int64_t id = load_id(ids, idt, i);
+            if (oracle_mutation == ORM_EMBED_OFF) id += 1;
+            int ok = id >= 0 && id < vocab;
+            if (!ok) bad = 1;
+            for (int64_t j = 0; j < hidden; ++j) row[j] = ok ? ld(table, tt, id * ldt + j) : 0.0f;
+            if (h && ht == tt && ok)
+                memcpy((char*)h + i * ldh * dsize(ht), (const char*)table + id * ldt * dsize(tt), (size_t)hidden * dsize(tt));
+            else if (h)
+                for (int64_t j = 0; j < hidden; ++j) st(h, ht, i * ldh + j, row[j]);
+            rms_row(row, wf, y, yt, i * ldy, hidden, eps, cs);
+        }
+        free(row);
+    }
+    free(wf);
+    if (bad && err_flag) *err_flag = 1;
+    return 0;
+}

@@ -1,0 +1,105 @@
+/*
+ * CPU oracle for the fused row ops — TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference semantics of exllamav3-rs's RMSNorm, SiLU/GELU-gated
+ * multiply, q/k head-norm + rotary embedding and embedding gather (each function cites the
+ * reference file:line it follows).  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it, and only as the checker or the timed CPU baseline; the product path
+ * (the HIP library) never calls it.
+ *
+ * Arguments mirror include/exl3r/rowops.h, but pointers are HOST pointers and every function takes
+ * an OpenMP thread count (<= 0 means 1).  Dtype codes are the EXL3R_* codes of that header.
+ *
+ * Parity pins (tests/test_oracle_*.py): exhaustive/ random conversion checks against numpy/torch,
+ * fp64 closed forms and torch-CPU library routines (committed fixtures under tests/golden/),
+ * invariants and special cases; `oracle_mutation` plants known mistakes so the tests can show that
+ * each pin catches them.
+ */
+#ifndef EXL3R_ROWOPS_ORACLE_H
+#define EXL3R_ROWOPS_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OR_F32  0
+#define OR_F16  1
+#define OR_BF16 2
+#define OR_I32  3
+#define OR_I64  4
+
+#define OR_ROPE_GPTJ 1
+#define OR_ROPE_NEOX 2
+
+#define OR_ACT_SILU 0
+#define OR_ACT_GELU 1
+
+/* Planted-mistake switch for the oracle's own tests (0 = faithful). */
+extern int oracle_mutation;
+#define ORM_NONE              0
+#define ORM_RMS_NO_EPS        1  /* eps dropped from the mean square */
+#define ORM_RMS_NO_CLAMP      2  /* f16 x not clamped to +-65504 on read */
+#define ORM_RES_NO_ROUND      3  /* residual sum not rounded to r's dtype before the norm */
+#define ORM_RMS_NO_BIAS       4  /* constant_bias ignored */
+#define ORM_RMS_DIM_OFF       5  /* mean taken over dim - 1 */
+#define ORM_SILU_SIGN         6  /* silu uses exp(+x) */
+#define ORM_GELU_NO_CUBIC     7  /* gelu drops the 0.044715 x^3 term */
+#define ORM_ACT_NO_LIMIT_Y    8  /* act_limit does not clamp y */
+#define ORM_ROPE_SIGN         9  /* r1 = v1 cos + v2 sin */
+#define ORM_ROPE_SWAP_SINCOS 10  /* sin and cos exchanged */
+#define ORM_ROPE_POS_OFF     11  /* position off by one */
+#define ORM_ROPE_NEOX_PAIR   12  /* NeoX pairs (2t, 2t+1) like GPT-J */
+#define ORM_HEADNORM_1ROUND  13  /* f16-weight head norm rounded once instead of twice */
+#define ORM_EMBED_OFF        14  /* gathers row ids[i] + 1 */
+#define ORM_ROPE_NORM_AFTER  15  /* head norm applied after the rotation */
+
+/* Conversions (round to nearest even; NaN -> canonical quiet NaN). */
+uint16_t oracle_f32_to_f16(float f);
+float    oracle_f16_to_f32(uint16_t h);
+uint16_t oracle_f32_to_bf16(float f);
+float    oracle_bf16_to_f32(uint16_t h);
+/* Round a double to the value set of dtype (F32/F16/BF16), RNE, overflow -> inf. */
+double   oracle_round(double v, int dtype);
+void     oracle_f32_to_f16_array(const float* in, uint16_t* out, int64_t n);
+void     oracle_f32_to_bf16_array(const float* in, uint16_t* out, int64_t n);
+
+int oracle_rms_norm(const void* x, int x_dtype, int64_t ldx,
+                    const void* w, int w_dtype,
+                    void* y, int y_dtype, int64_t ldy,
+                    void* r /* NULL: plain RMSNorm */, int r_dtype, int64_t ldr,
+                    int64_t rows, int64_t dim,
+                    float eps, float constant_bias, float constant_scale, int nthreads);
+
+int oracle_act_mul(int act, const void* x, const void* y, int in_dtype, void* z, int z_dtype,
+                   int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz,
+                   float act_limit, int nthreads);
+
+int oracle_rope(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int num_heads_q,
+                const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int num_heads_k,
+                int dtype, int64_t bsz, int64_t seq_len, int head_dim,
+                const float* inv_freq, int rotary_dim,
+                int32_t position, const int32_t* positions, const int32_t* position_ids,
+                const void* q_norm, const void* k_norm, int norm_dtype,
+                float norm_eps, float norm_constant_bias,
+                int rope_mode, float attn_factor, int nthreads);
+
+int oracle_embedding(const void* table, int table_dtype, int64_t vocab, int64_t hidden, int64_t ldt,
+                     const void* ids, int ids_dtype, int64_t n,
+                     void* out, int out_dtype, int64_t ldo,
+                     int32_t* err_flag, int nthreads);
+
+int oracle_embedding_rms_norm(const void* table, int table_dtype, int64_t vocab, int64_t hidden, int64_t ldt,
+                              const void* ids, int ids_dtype, int64_t n,
+                              void* h, int h_dtype, int64_t ldh,
+                              const void* w, int w_dtype,
+                              void* y, int y_dtype, int64_t ldy,
+                              float eps, float constant_bias, float constant_scale,
+                              int32_t* err_flag, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,53 @@
+"""GPU-side test helpers: move storage arrays (fp32 / raw 16-bit bits) to and from torch tensors,
+seeded device-side input generation, and the parity assertions of the north-star tolerances."""
+import numpy as np
+import torch
+
+from _util import max_rel_err, ulp_dist
+from oracle import oracle as orc
+
+TORCH_DT = {orc.F32: torch.float32, orc.F16: torch.float16, orc.BF16: torch.bfloat16, orc.I32: torch.int32,
+            orc.I64: torch.int64}
+NTHREADS = 8
+
+
+def to_dev(a, code, device="cuda"):
+    a = np.ascontiguousarray(a)
+    if code in (orc.F16, orc.BF16):
+        return torch.from_numpy(a.view(np.int16)).view(TORCH_DT[code]).to(device)
+    return torch.from_numpy(a).to(device)
+
+
+def from_dev(t):
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.float16, torch.bfloat16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def code_of(t):
+    return {v: k for k, v in TORCH_DT.items()}[t.dtype]
+
+
+def dev_normal(shape, mean, std, code, seed, device="cuda"):
+    """Seeded N(mean, std) generated in fp32 on the GPU and rounded RNE to `code`."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    v = torch.randn(shape, generator=g, device=device, dtype=torch.float32) * std + mean
+    return v.to(TORCH_DT[code])
+
+
+def assert_close_ulp(got, exp, code, max_ulp, rel=2e-3, what=""):
+    """GPU vs oracle: elementwise ulp distance <= max_ulp and max abs err <= rel * output scale."""
+    d = ulp_dist(got, exp, code)
+    mre = max_rel_err(got, exp, code)
+    stats = f"{what}: max_ulp={int(d.max()) if d.size else 0} exact={np.mean(d == 0) if d.size else 1:.6f} max_rel_err={mre:.3e}"
+    print(stats)
+    assert d.size == 0 or d.max() <= max_ulp, stats
+    assert mre <= rel, stats
+    return d
+
+
+def assert_bitwise(got, exp, what=""):
+    same = np.array_equal(np.ascontiguousarray(got).view(np.uint8), np.ascontiguousarray(exp).view(np.uint8))
+    print(f"{what}: bitwise={'yes' if same else 'NO'}")
+    assert same, what

@@ -1,0 +1,126 @@
+"""GPU parity of exl3r_rms_norm / exl3r_rms_norm_res_in against the CPU oracle on the same bits:
+<= 1 ulp for 16-bit outputs (<= 3 for f32), max abs err <= 2e-3 of the output scale, and the
+residual written back by RES_IN bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+import exl3r.ffi as ffi
+from _gpu import NTHREADS, assert_bitwise, assert_close_ulp, code_of, dev_normal, from_dev
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+F16, BF16, F32 = orc.F16, orc.BF16, orc.F32
+
+
+def ulp_for(code):
+    return 3 if code == F32 else 1
+
+
+def run_plain(rows, dim, xt, wt, yt, eps=1e-6, cb=0.0, cs=1.0, seed=0, ldx=None, ldy=None, weight=True):
+    ldx = ldx or dim
+    ldy = ldy or dim
+    xs = dev_normal((rows, ldx), 0.0, 1.0, xt, seed)
+    w = dev_normal((dim,), 1.0, 0.1, wt, seed + 1) if weight else None
+    ys = torch.full((rows, ldy), float("nan"), device="cuda", dtype=orc_t(yt))
+    x, y = xs[:, :dim], ys[:, :dim]
+    ffi.rms_norm(x, w, y, eps, cb, cs)
+    torch.cuda.synchronize()
+    xh = np.ascontiguousarray(from_dev(x))
+    exp = orc.rms_norm(xh, xt, from_dev(w) if weight else None, wt, yt, eps, cb, cs, nthreads=NTHREADS)
+    assert_close_ulp(from_dev(y), exp, yt, ulp_for(yt), what=f"rms_norm {rows}x{dim} x={xt} w={wt} y={yt}")
+    if ldy > dim:   # padding untouched
+        assert torch.isnan(ys[:, dim:].float()).all()
+
+
+def orc_t(code):
+    return {F32: torch.float32, F16: torch.float16, BF16: torch.bfloat16}[code]
+
+
+def test_c1_rmsnorm_f16():
+    """Config 1(1): [512, 1024] f16, eps 1e-6, x ~ N(0,1), w ~ N(1, 0.1)."""
+    run_plain(512, 1024, F16, F16, F16)
+
+
+@pytest.mark.parametrize("xt", [F16, BF16, F32])
+@pytest.mark.parametrize("yt", [F16, BF16, F32])
+@pytest.mark.parametrize("wt", [F16, BF16, F32])
+def test_dtype_matrix(xt, yt, wt):
+    run_plain(37, 512, xt, wt, yt, seed=xt * 9 + yt * 3 + wt)
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 5120), (3, 64), (64, 5120), (700, 5120), (5, 2048), (9, 16384),
+                                      (4, 65536), (7, 1000), (2, 12), (1100, 8)])
+def test_shapes(rows, dim):
+    run_plain(rows, dim, BF16, BF16, BF16, seed=rows + dim)
+
+
+def test_no_weight_bias_scale_strides():
+    run_plain(33, 768, F16, F16, F16, weight=False)
+    run_plain(33, 768, F16, BF16, F16, cb=1.0, cs=0.5, eps=1e-5)
+    run_plain(33, 768, BF16, BF16, F32, ldx=1024, ldy=800)
+    run_plain(9, 768, F16, F16, F16, ldx=772)           # misaligned stride -> generic kernel
+
+
+def test_f16_clamp_on_read():
+    x = torch.randn(4, 256, device="cuda").half()
+    x[0, 3], x[1, 5], x[2, 7] = float("inf"), float("-inf"), float("nan")
+    w = torch.ones(256, device="cuda", dtype=torch.float16)
+    y = torch.empty_like(x)
+    ffi.rms_norm(x, w, y, 1e-6)
+    exp = orc.rms_norm(from_dev(x), F16, from_dev(w), F16, F16, 1e-6)
+    assert_close_ulp(from_dev(y), exp, F16, 1, what="clamp")
+    assert torch.isfinite(y).all()
+
+
+def test_in_place():
+    x = dev_normal((16, 4096), 0.0, 1.0, F16, 3)
+    w = dev_normal((4096,), 1.0, 0.1, F16, 4)
+    exp = orc.rms_norm(from_dev(x), F16, from_dev(w), F16, F16, 1e-6)
+    ffi.rms_norm(x, w, x, 1e-6)
+    assert_close_ulp(from_dev(x), exp, F16, 1, what="in place")
+
+
+def run_res(rows, dim, xt, rt, yt, wt, seed=0, cb=0.0, cs=1.0):
+    x = dev_normal((rows, dim), 0.0, 1.0, xt, seed)
+    r = dev_normal((rows, dim), 0.0, 4.0, rt, seed + 1)
+    w = dev_normal((dim,), 1.0, 0.1, wt, seed + 2)
+    y = torch.empty((rows, dim), device="cuda", dtype=orc_t(yt))
+    xh, rh, wh = from_dev(x), from_dev(r).copy(), from_dev(w)
+    ffi.rms_norm_res_in(x, w, y, r, 1e-6, cb, cs)
+    torch.cuda.synchronize()
+    exp = orc.rms_norm(xh, xt, wh, wt, yt, 1e-6, cb, cs, r=rh, rt=rt, nthreads=NTHREADS)
+    assert_bitwise(from_dev(r), rh, what=f"res_in residual {rows}x{dim}")
+    assert_close_ulp(from_dev(y), exp, yt, ulp_for(yt), what=f"res_in y {rows}x{dim} x={xt} r={rt} y={yt}")
+
+
+@pytest.mark.parametrize("tokens", [1, 8, 32, 64])
+def test_c2_decode_residual_norm(tokens):
+    """Config 2: residual RMSNorm f16, hidden 5120, x ~ N(0,1), r ~ N(0,4), w ~ N(1,0.1)."""
+    run_res(tokens, 5120, F16, F16, F16, F16, seed=tokens)
+
+
+def test_c3_prefill_residual_norm_bf16():
+    """Config 3(1): residual RMSNorm bf16, 8192 tokens, hidden 5120 (full size)."""
+    run_res(8192, 5120, BF16, BF16, BF16, BF16, seed=31)
+
+
+@pytest.mark.parametrize("xt,rt,yt,wt", [(F16, F32, F16, F16), (F16, F32, F16, BF16), (BF16, F32, BF16, BF16),
+                                         (F32, F16, F16, F16), (F16, F16, F32, F16), (F32, F32, BF16, F32)])
+def test_res_in_dtype_mixes(xt, rt, yt, wt):
+    """The real Qwen3 path is x f16 (sublayer output), r f32 (residual stream), y f16 (norm.cu:403)."""
+    run_res(50, 2560, xt, rt, yt, wt, seed=xt + 4 * rt + 16 * yt)
+
+
+def test_res_in_generic_and_bias():
+    run_res(5, 1001, F16, F32, F16, F16, seed=5, cb=1.0, cs=2.0)
+
+
+def test_deterministic():
+    x = dev_normal((300, 5120), 0.0, 1.0, BF16, 7)
+    w = dev_normal((5120,), 1.0, 0.1, BF16, 8)
+    y1, y2 = torch.empty_like(x), torch.empty_like(x)
+    ffi.rms_norm(x, w, y1, 1e-6)
+    ffi.rms_norm(x, w, y2, 1e-6)
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
