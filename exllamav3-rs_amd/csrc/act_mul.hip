@@ -7,8 +7,10 @@
 // round-to-nearest-even to z's dtype, f16 z clamped to +-65504 (2-7, 249-251).
 //   silu(x) = x / (1 + exp(-x))                                   (activation_kernels.cuh:34-39)
 //   gelu(x) = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))      (activation_kernels.cuh:52-58)
-// evaluated as x * rcp(1 + exp2(...)) via 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)), so both are one
-// v_exp_f32 and one v_rcp_f32 per element and GELU has no 1 + tanh cancellation for x << 0.
+// both evaluated as x * sigmoid(z) (GELU through 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)), which has
+// no 1 + tanh cancellation for x << 0): with e^-z = 2^t, sigmoid = q for t <= 0 and p * q for t > 0,
+// where p = 2^-|t| in (0, 1] and q = 1 / (1 + p), so results far in the tail (down to fp32
+// denormals) keep full relative precision instead of flushing through 1 / (1 + huge).
 //
 // Streaming layout: 8-element chunks (16 bytes per 16-bit tensor) per lane, UNROLL chunks in flight
 // per thread, strided by blockDim so each wave-wide access is 1 KiB contiguous.  Contiguous
@@ -27,10 +29,12 @@ constexpr float kGeluK2 = (float)(-2.0 * 0.79788456080286535588 * 0.044715 * 1.4
 template <int ACT>
 __device__ __forceinline__ float act_f(float x)
 {
-    float t;
+    float t;   // e^-z = 2^t
     if constexpr (ACT == ACT_SILU) t = x * -kLog2e;
     else t = x * fmaf(kGeluK2, x * x, kGeluK1);
-    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
+    const float p = exp2f(-fabsf(t));                     // denormal-correct exp2
+    const float q = __builtin_amdgcn_rcpf(1.0f + p);      // argument in [1, 2]
+    return x * (t <= 0.0f ? q : p * q);
 }
 
 struct ActArgs
@@ -44,7 +48,7 @@ struct ActArgs
     float limit;
 };
 
-template <int ACT, class OT>
+template <int ACT, class OT, bool LIMIT>
 __device__ __forceinline__ void act_chunk(const float (&g)[8], float (&u)[8], float limit, float (&o)[8])
 {
     #pragma unroll
@@ -52,7 +56,7 @@ __device__ __forceinline__ void act_chunk(const float (&g)[8], float (&u)[8], fl
     {
         float a = act_f<ACT>(g[j]);
         float v = u[j];
-        if (limit != 0.0f)
+        if constexpr (LIMIT)
         {
             if (v < -limit) v = -limit;
             if (v > limit) v = limit;
@@ -64,7 +68,7 @@ __device__ __forceinline__ void act_chunk(const float (&g)[8], float (&u)[8], fl
     }
 }
 
-template <int ACT, class IT, class OT, int UNROLL>
+template <int ACT, class IT, class OT, int UNROLL, bool LIMIT>
 __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
 {
     const int64_t cpr = a.cols >> 3;   // chunks per row
@@ -97,7 +101,7 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
                     float g[8], v[8], o[8];
                     unpack8<IT>(xv[u], g);
                     unpack8<IT>(yv[u], v);
-                    act_chunk<ACT, OT>(g, v, a.limit, o);
+                    act_chunk<ACT, OT, LIMIT>(g, v, a.limit, o);
                     store8<OT>(zr, c * 8, pack8<OT>(o));
                 }
             }
@@ -116,8 +120,8 @@ __global__ __launch_bounds__(256) void k_act_mul_generic(ActArgs a, int it, int 
         float g[8] = { load1(a.x, it, r * a.ldx + c) };
         float v[8] = { load1(a.y, it, r * a.ldy + c) };
         float o[8];
-        if (ot == DT_F16) act_chunk<ACT, TF16>(g, v, a.limit, o);
-        else act_chunk<ACT, TF32>(g, v, a.limit, o);
+        if (ot == DT_F16) act_chunk<ACT, TF16, true>(g, v, a.limit, o);
+        else act_chunk<ACT, TF32, true>(g, v, a.limit, o);
         store1(a.z, ot, r * a.ldz + c, o[0]);
     }
 }
@@ -141,7 +145,8 @@ static void launch_act_vec(const ActArgs& a, hipStream_t s)
     const int unroll = (tu.act_unroll == 1 || tu.act_unroll == 2 || tu.act_unroll == 4 || tu.act_unroll == 8) ? tu.act_unroll : 4;
     const int threads = (tu.act_threads > 0 && tu.act_threads % 64 == 0 && tu.act_threads <= 256) ? tu.act_threads : 256;
     const int64_t cpr = a.cols >> 3;
-    int64_t bx = (cpr + (int64_t)threads * unroll - 1) / ((int64_t)threads * unroll);
+    const int per = a.limit != 0.0f ? 4 : unroll;
+    int64_t bx = (cpr + (int64_t)threads * per - 1) / ((int64_t)threads * per);
     if (tu.act_blocks_per_cu > 0)
     {
         const int64_t cap = (int64_t)tu.act_blocks_per_cu * num_cus() / (a.rows < 65535 ? (a.rows > 0 ? a.rows : 1) : 65535);
@@ -149,12 +154,17 @@ static void launch_act_vec(const ActArgs& a, hipStream_t s)
     }
     if (bx > kMaxGridX) bx = kMaxGridX;
     const dim3 grid((unsigned)bx, (unsigned)(a.rows < 65535 ? a.rows : 65535));
-    switch (unroll)
+    if (a.limit != 0.0f)
+        k_act_mul<ACT, IT, OT, 4, true><<<grid, threads, 0, s>>>(a);
+    else
     {
-        case 1: k_act_mul<ACT, IT, OT, 1><<<grid, threads, 0, s>>>(a); break;
-        case 2: k_act_mul<ACT, IT, OT, 2><<<grid, threads, 0, s>>>(a); break;
-        case 8: k_act_mul<ACT, IT, OT, 8><<<grid, threads, 0, s>>>(a); break;
-        default: k_act_mul<ACT, IT, OT, 4><<<grid, threads, 0, s>>>(a); break;
+        switch (unroll)
+        {
+            case 1: k_act_mul<ACT, IT, OT, 1, false><<<grid, threads, 0, s>>>(a); break;
+            case 2: k_act_mul<ACT, IT, OT, 2, false><<<grid, threads, 0, s>>>(a); break;
+            case 8: k_act_mul<ACT, IT, OT, 8, false><<<grid, threads, 0, s>>>(a); break;
+            default: k_act_mul<ACT, IT, OT, 4, false><<<grid, threads, 0, s>>>(a); break;
+        }
     }
 }
 

@@ -85,8 +85,13 @@ template <> __device__ __forceinline__ TBF16::Vec load8<TBF16>(const void* base,
 }
 template <> __device__ __forceinline__ TF32::Vec load8<TF32>(const void* base, int64_t e)
 {
+    // Members are assigned one by one: a braced {p[0], p[1]} would be brace-elided into the
+    // elements of the first vector member.
     const u32x4* p = (const u32x4*)((const float*)base + e);
-    return { p[0], p[1] };
+    TF32::Vec v;
+    v.a = p[0];
+    v.b = p[1];
+    return v;
 }
 
 template <> __device__ __forceinline__ void store8<TF16>(void* base, int64_t e, const TF16::Vec& v)
@@ -172,6 +177,15 @@ __device__ __forceinline__ void load8_dyn(const void* base, int dt, int64_t e, f
     if (dt == DT_F16) unpack8<TF16>(load8<TF16>(base, e), f);
     else if (dt == DT_BF16) unpack8<TBF16>(load8<TBF16>(base, e), f);
     else unpack8<TF32>(load8<TF32>(base, e), f);
+}
+
+// Reciprocal RMS factor from an fp64 sum of squares: the sum is rounded once to fp32, then
+// mean = sum / n, and 1 / sqrt(mean + eps) with IEEE-correct fp32 sqrt and division (hipcc's
+// default), so the CPU oracle reproduces it bit-for-bit.
+__device__ __forceinline__ float rms_factor(double sum, int n, float eps)
+{
+    const float mean = (float)sum / (float)n;
+    return 1.0f / sqrtf(mean + eps);
 }
 
 // CLAMP_FP16: +-inf -> +-65504, NaN -> 65504 (v_min/v_max return the non-NaN operand).
@@ -269,14 +283,6 @@ __device__ __forceinline__ double block_sum64(double v, double* lds16)
     for (int i = 0; i < nw; ++i) t += lds16[i];
     __syncthreads();
     return t;
-}
-
-// rsqrt(sum / n + eps) with the sum carried in fp64 and rounded once to fp32, the division and add
-// in fp32, and the reciprocal square root in fp64 rounded once: the exact statistic of the CPU oracle.
-__device__ __forceinline__ float rms_factor_f64(double sum, int n, float eps)
-{
-    const float mean = (float)sum / (float)n;
-    return (float)(1.0 / sqrt((double)(mean + eps)));
 }
 
 // ---------------------------------------------------------------------------------------------

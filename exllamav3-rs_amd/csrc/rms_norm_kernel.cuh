@@ -3,14 +3,15 @@
 // Semantics follow rms_norm_kernel (reference kernels/norm.cu:160-304):
 //   f16 x is clamped to +-65504 on read (norm.cu:42-58, 192-196); RES_IN rounds x + r to r's dtype,
 //   writes it back to r and normalises the rounded sum (norm.cu:198-223); the sum of squares is an
-//   fp32 FMA chain (norm.cu:101-108); rmf = rsqrt(sum / dim + eps) * constant_scale (norm.cu:273);
+//   FMA chain (norm.cu:101-108; carried in fp64 here); rmf = rsqrt(sum / dim + eps) * constant_scale
+//   (norm.cu:273; IEEE fp32 sqrt and divide here);
 //   y = (x * (w + constant_bias)) * rmf in fp32, rounded once (norm.cu:110-124, 232-239, 75-83).
 //
 // Layout: one row per workgroup.  A row is split into chunks of 8 elements; thread t owns chunks
 // t, t + blockDim, ... (at most MAXV), so every wave-wide access is 64 lanes x 16 bytes contiguous.
 // The whole row stays in VGPRs between the reduction and the output pass: one HBM read of x (and r),
 // one write of y (and r) per row -- the 4-pass minimum for RES_IN, where the reference re-reads r
-// at dim > 4096.  The row reduction is DPP + readlane inside each wave and one LDS hop across waves.
+// at dim > 4096.  The row reduction is a DPP butterfly inside each wave and one LDS hop across waves.
 #pragma once
 
 #include "abi.hpp"
@@ -56,9 +57,15 @@ __device__ __forceinline__ u32x4 prefetch_w8(const void* w, int wt, int64_t e)
 
 __device__ __forceinline__ void unpack_w8(u32x4 pre, const void* w, int wt, int64_t e, float (&f)[8])
 {
-    if (wt == DT_F16) unpack8<TF16>(TF16::Vec{ pre }, f);
-    else if (wt == DT_BF16) unpack8<TBF16>(TBF16::Vec{ pre }, f);
-    else unpack8<TF32>(TF32::Vec{ pre, *(const u32x4*)((const float*)w + e + 4) }, f);
+    if (wt == DT_F16) { TF16::Vec v; v.a = pre; unpack8<TF16>(v, f); }
+    else if (wt == DT_BF16) { TBF16::Vec v; v.a = pre; unpack8<TBF16>(v, f); }
+    else
+    {
+        TF32::Vec v;
+        v.a = pre;
+        v.b = *(const u32x4*)((const float*)w + e + 4);
+        unpack8<TF32>(v, f);
+    }
 }
 
 // Register budget: MAXV chunks of x, r and w stay live across the loads, so wide rows per lane get
@@ -68,7 +75,7 @@ template <int MAXV> constexpr int rms_max_threads() { return 1024; }
 template <class XT, class YT, class RT, int MAXV, int MODE>
 __global__ __launch_bounds__(rms_max_threads<MAXV>()) void k_rms_norm(RmsArgs a)
 {
-    __shared__ float red[16];
+    __shared__ double red[16];
     const int tid = threadIdx.x;
     const int nt = blockDim.x;
     const int nc = a.dim >> 3;
@@ -115,7 +122,7 @@ __global__ __launch_bounds__(rms_max_threads<MAXV>()) void k_rms_norm(RmsArgs a)
         // and re-expanded in pass 2.
         using CT = std::conditional_t<MODE == RMS_RES_IN, RT, XT>;
         typename CT::Vec cache[MAXV];
-        float ss = 0.0f;
+        double ss = 0.0;
         #pragma unroll
         for (int k = 0; k < MAXV; ++k)
         {
@@ -159,12 +166,13 @@ __global__ __launch_bounds__(rms_max_threads<MAXV>()) void k_rms_norm(RmsArgs a)
                     }
                 }
                 #pragma unroll
-                for (int j = 0; j < 8; ++j) ss = fmaf(h[j], h[j], ss);
+                for (int j = 0; j < 8; ++j) ss = fma((double)h[j], (double)h[j], ss);
             }
         }
 
-        ss = block_sum(ss, red);
-        const float rmf = rsqrtf(ss / (float)a.dim + a.eps) * a.cs;
+        // fp64 row sum (exact for 16-bit data), one rounding, IEEE fp32 sqrt and divide.
+        ss = block_sum64(ss, red);
+        const float rmf = rms_factor(ss, a.dim, a.eps) * a.cs;
 
         // Pass 2: scale, weight, round once, store.
         #pragma unroll
@@ -201,7 +209,7 @@ __global__ __launch_bounds__(rms_max_threads<MAXV>()) void k_rms_norm(RmsArgs a)
                 store8<YT>(yrow, (int64_t)c * 8, pack8<YT>(o));
             }
         }
-        if (nt > 64) __syncthreads();   // red[] is reused by the next row
+
     }
 }
 
@@ -209,7 +217,7 @@ __global__ __launch_bounds__(rms_max_threads<MAXV>()) void k_rms_norm(RmsArgs a)
 template <int MODE>
 __global__ __launch_bounds__(256) void k_rms_norm_generic(RmsArgs a, int xt, int yt, int rt)
 {
-    __shared__ float red[16];
+    __shared__ double red[16];
     const int tid = threadIdx.x;
     for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x)
     {
@@ -222,7 +230,7 @@ __global__ __launch_bounds__(256) void k_rms_norm_generic(RmsArgs a, int xt, int
             if (!valid && tid == 0 && a.err) atomicOr(a.err, 1);
             xoff = valid ? id * a.ldx : 0;
         }
-        float ss = 0.0f;
+        double ss = 0.0;
         for (int j = tid; j < a.dim; j += blockDim.x)
         {
             float v = valid ? load1(a.x, xt, xoff + j) : 0.0f;
@@ -239,10 +247,10 @@ __global__ __launch_bounds__(256) void k_rms_norm_generic(RmsArgs a, int xt, int
                 else
                     store1(a.r, rt, row * a.ldr + j, v);
             }
-            ss = fmaf(v, v, ss);
+            ss = fma((double)v, (double)v, ss);
         }
-        ss = block_sum(ss, red);
-        const float rmf = rsqrtf(ss / (float)a.dim + a.eps) * a.cs;
+        ss = block_sum64(ss, red);
+        const float rmf = rms_factor(ss, a.dim, a.eps) * a.cs;
         for (int j = tid; j < a.dim; j += blockDim.x)
         {
             float v;

@@ -4,13 +4,13 @@
 // Semantics follow rope_kernel (kernels/rope.cu:16-255):
 //   position of token s of sequence b: position + s | positions[b] + s | position_ids[b*seq + s]
 //   (rope.cu:55-67); head RMSNorm iff q_norm is given (rope.cu:250): sum of squares over the head
-//   (carried in fp64), rmf = rsqrt(sum / head_dim + eps); f16 weights with f16 heads round twice in half precision,
+//   (carried in fp64), rmf = 1 / sqrt(sum / head_dim + eps) (IEEE fp32); f16 weights with f16 heads round twice in half precision,
 //   out = h(h(w + cb) * h(v * rmf)) (rope.cu:222-229); other weights out = io((v * rmf) * (w + cb))
 //   (rope.cu:212-221); the rotation reads the io-rounded normed head: angle = inv_freq[t] * (float)pos,
 //   cos/sin * attn_factor (rope.cu:69-85), NeoX pairs (t, t + R/2), GPT-J pairs (2t, 2t+1), each
 //   result rounded once (rope.cu:152-185); dims >= R pass through.
-//   sin/cos use the accurately range-reduced sincosf (positions reach 3e4 and beyond), not the
-//   reference's __sinf/__cosf; the head sum is a full xor-butterfly sum in every lane (the reference's
+//   sin/cos are fp64 evaluations of the fp32 angle rounded once (positions reach 3e4 and beyond),
+//   not the reference's __sinf/__cosf; the head sum is a full xor-butterfly sum in every lane (the reference's
 //   shfl_down sum stored from all lanes, rope.cu:190-204, is only correct in lane 0).
 //
 // Layout: one workgroup per token (decode: several per token, splitting the heads).  A head of
@@ -58,13 +58,15 @@ __device__ __forceinline__ int token_position(const RopeArgs& a, int64_t tok)
 // sin/cos of every rotary frequency of this token into LDS (float2 {cos, sin} * attn_factor).
 __device__ __forceinline__ void fill_sincos(const RopeArgs& a, int pos, float2* cs)
 {
+    // sin/cos of the fp32 angle evaluated in fp64 and rounded once: correctly rounded fp32 values
+    // (R/2 evaluations per token, shared by all heads, so the fp64 cost is negligible).
     const float pf = (float)pos;
     for (int t = threadIdx.x; t < a.R / 2; t += blockDim.x)
     {
         const float ang = __fmul_rn(a.inv_freq[t], pf);
-        float sn, c;
-        sincosf(ang, &sn, &c);
-        cs[t] = make_float2(c * a.attn, sn * a.attn);
+        double sd, cd;
+        sincos((double)ang, &sd, &cd);
+        cs[t] = make_float2((float)cd * a.attn, (float)sd * a.attn);
     }
 }
 
@@ -137,7 +139,7 @@ __global__ __launch_bounds__(1024) void k_rope(RopeArgs a)
                 #pragma unroll
                 for (int j = 0; j < 8; ++j) ss = fma((double)f[j], (double)f[j], ss);
                 ss = group_sum64<LPH>(ss);
-                const float rmf = rms_factor_f64(ss, a.hd, a.eps);
+                const float rmf = rms_factor(ss, a.hd, a.eps);
                 if (act[it])
                 {
                     const void* w = head < a.hq ? a.qw : a.kw;
@@ -164,8 +166,11 @@ __global__ __launch_bounds__(1024) void k_rope(RopeArgs a)
                 }
             }
 
+            // Rotation products rounded separately (no FMA contraction), as the reference semantics
+            // state them: r1 = fl(fl(v1 c) - fl(v2 s)).
             if constexpr (MODE == EXL3R_ROPE_GPTJ)
             {
+                #pragma clang fp contract(off)
                 #pragma unroll
                 for (int p = 0; p < 4; ++p)
                 {
@@ -197,6 +202,7 @@ __global__ __launch_bounds__(1024) void k_rope(RopeArgs a)
                 }
                 if (rot)
                 {
+                    #pragma clang fp contract(off)
                     typename IO::Vec po;
                     #pragma unroll
                     for (int i = 0; i < 4; ++i) po.a[i] = other[i];
@@ -247,7 +253,7 @@ __global__ __launch_bounds__(256) void k_rope_generic(RopeArgs a, int dt, int mo
         ss = block_sum64(ss, red);
         if (norm != NORM_NONE)
         {
-            const float rmf = rms_factor_f64(ss, a.hd, a.eps);
+            const float rmf = rms_factor(ss, a.hd, a.eps);
             const void* w = isq ? a.qw : a.kw;
             for (int d = tid; d < a.hd; d += blockDim.x)
             {
@@ -263,6 +269,7 @@ __global__ __launch_bounds__(256) void k_rope_generic(RopeArgs a, int dt, int mo
         __syncthreads();
         for (int t = tid; t < half; t += blockDim.x)
         {
+            #pragma clang fp contract(off)
             const int i1 = mode == EXL3R_ROPE_NEOX ? t : 2 * t;
             const int i2 = mode == EXL3R_ROPE_NEOX ? t + half : 2 * t + 1;
             const float v1 = hv[i1], v2 = hv[i2];

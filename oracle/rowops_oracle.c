@@ -149,8 +149,9 @@ static int fdtype(int dt) { return dt == OR_F32 || dt == OR_F16 || dt == OR_BF16
  *   - f16 x clamped on read (read_half4<true>, norm.cu:42-58, used by read_in at 192-196);
  *   - RES_IN: r <- round_r(x + r) in place, then the norm reads the rounded sum (add_resid_in,
  *     norm.cu:198-223);
- *   - sum of squares (norm.cu:101-108, reduced 140-151; here exactly in double, rounded to fp32);
- *   - rmf = rsqrt(sum / dim + eps) * constant_scale (norm.cu:273, 288);
+ *   - sum of squares (norm.cu:101-108, reduced 140-151; here in double, rounded once to fp32);
+ *   - rmf = rsqrt(sum / dim + eps) * constant_scale (norm.cu:273, 288), evaluated as an IEEE fp32
+ *     sqrt and an IEEE fp32 division (the reference's rsqrtf is an approximation of the same);
  *   - y = (x * (w + constant_bias)) * rmf in fp32 (apply4, norm.cu:110-116, bias 232-239), or
  *     x * rmf without a weight (apply4_nw, 118-124), rounded once to y's dtype (write_half4, 75-83). */
 static void rms_row(const float* h, const float* wf, void* y, int yt, int64_t yoff, int64_t dim,
@@ -162,7 +163,7 @@ static void rms_row(const float* h, const float* wf, void* y, int yt, int64_t yo
     int64_t d = oracle_mutation == ORM_RMS_DIM_OFF ? dim - 1 : dim;
     float mean = sf / (float)d;
     float t = oracle_mutation == ORM_RMS_NO_EPS ? mean : mean + eps;
-    float rmf = (float)(1.0 / sqrt((double)t));
+    float rmf = 1.0f / sqrtf(t);
     rmf = rmf * cs;
     for (int64_t j = 0; j < dim; ++j)
     {
@@ -278,8 +279,8 @@ int oracle_act_mul(int act, const void* x, const void* y, int it, void* z, int z
 /* Head RMSNorm + rotary embedding, following rope_kernel (kernels/rope.cu:16-255):
  *   pos = position + s | positions[b] + s | position_ids[b*seq + s]             (rope.cu:55-67)
  *   head norm (rope.cu:188-233), applied iff q_norm is given (rope.cu:250):
- *     sum of squares over the head (exact here; the reference's reduction at rope.cu:196-204
- *     races on a shared slot, the intended full sum is used), rmf = rsqrt(sum/hd + eps),
+ *     sum of squares over the head (double here; the reference's reduction at rope.cu:196-204
+ *     races on a shared slot, the intended full sum is used), rmf = 1 / sqrtf(sum/hd + eps),
  *     f16 weight with f16 I/O: out = h(h(w + h(cb)) * h(v * rmf)), two half roundings
  *       (rope.cu:222-229; half add/mul are correctly rounded);
  *     otherwise: out = io(fl32(fl32(v * rmf) * fl32(w + cb)))           (rope.cu:212-221);
@@ -293,7 +294,7 @@ static void head_norm(float* v, int dt, int hd, const float* wf, const uint16_t*
     double s = 0.0;
     for (int d = 0; d < hd; ++d) s += (double)v[d] * (double)v[d];
     float sf = (float)s;
-    float rmf = (float)(1.0 / sqrt((double)(sf / (float)hd + eps)));
+    float rmf = 1.0f / sqrtf(sf / (float)hd + eps);
     for (int d = 0; d < hd; ++d)
     {
         float n = v[d] * rmf;

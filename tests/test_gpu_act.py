@@ -1,5 +1,7 @@
-"""GPU parity of exl3r_silu_mul / exl3r_gelu_mul against the CPU oracle: <= 1 ulp for 16-bit z
-(<= 4 for f32 z), max abs err <= 2e-3 of the output scale."""
+"""GPU parity of exl3r_silu_mul / exl3r_gelu_mul against the CPU oracle: <= 1 ulp for 16-bit z,
+max abs err <= 2e-3 of the output scale (one ulp for bf16).  An f32 z carries the GPU's fp32
+evaluation error (v_exp_f32 / v_rcp_f32 are 1-ulp approximations; the oracle evaluates in fp64):
+<= 8 fp32 ulps."""
 import numpy as np
 import pytest
 import torch
@@ -25,7 +27,7 @@ def run(act, rows, cols, it, zt, limit=0.0, seed=0, ld=None, std=1.0):
     torch.cuda.synchronize()
     exp = orc.act_mul(code, np.ascontiguousarray(from_dev(x)), np.ascontiguousarray(from_dev(y)), it, zt, limit,
                       nthreads=NTHREADS)
-    assert_close_ulp(from_dev(z), exp, zt, 4 if zt == F32 else 1, what=f"{act} {rows}x{cols} in={it} z={zt} L={limit}")
+    assert_close_ulp(from_dev(z), exp, zt, 8 if zt == F32 else 1, what=f"{act} {rows}x{cols} in={it} z={zt} L={limit}")
 
 
 @pytest.mark.parametrize("act", ["silu", "gelu"])
