@@ -1,0 +1,464 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X fused row ops (the exl3r C ABI), one JSON line on stdout.
+
+Metric: fused norm/act/RoPE/embed HBM GB/s + % of MI355X peak; decode-step us.
+
+A step is one pass of the config-3 prefill row ops (residual RMSNorm [8192, 5120] + SiLU-gated mul
++ GELU-gated mul [8192, 17408], bf16 I/O, fp32 arithmetic) over inputs resident in HBM; `value` is
+the step's algorithmic bytes / step time.  The line also carries every other config's per-op
+figures (C1 Qwen3-0.6B ops, C2 decode residual norm, C4 paged q/k-norm + RoPE, C5 embedding gather
+and gather + norm), the 64-row decode-step composite fused vs the naive unfused HIP baseline, the
+roofline of the dominant kernel (SiLU-mul), and the CPU oracle timed on this host as a baseline.
+
+  python bench.py [--steps K] [--warmup W]            full run (N = 1)
+  python bench.py --op silu_c3 [--steps K]            one kernel only (for rocprofv3 --pmc runs)
+  python bench.py --op calib_copy                     plain 1 GiB copy (counter calibration)
+
+Inputs are seeded synthetic data of the configs' shapes (the reference ships no datasets); each
+timed loop rotates over enough buffer sets that a launch never finds its operands in the 256 MB
+Infinity Cache from the previous launch.
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "exllamav3-rs_amd"))
+
+PEAK_GBS = 8000.0            # MI355X HBM3E
+METRIC = "fused norm/act/RoPE/embed HBM GB/s + % of MI355X peak; decode-step us"
+OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "gather_norm_c5", "rms_c1",
+       "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "calib_copy"]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--op", choices=OPS, default=None, help="time one kernel only")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    return p.parse_args()
+
+
+# ------------------------------------------------------------------------------------------------
+# Workloads: each builds its buffers once and returns (launch(i), bytes_per_launch, description).
+
+class Work:
+    def __init__(self, name, nbytes, launch, desc, sets=1):
+        self.name, self.nbytes, self.launch, self.desc, self.sets = name, nbytes, launch, desc, sets
+
+
+def gen(shape, mean, std, dtype, seed):
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return (torch.randn(shape, generator=g, device="cuda", dtype=torch.float32) * std + mean).to(dtype)
+
+
+def sets_for(nbytes, span=600 << 20):
+    """Buffer sets so that the bytes touched between two uses of one set exceed the MALL."""
+    return max(2, -(-span // max(nbytes, 1)) + 1)
+
+
+def zipf_ids(n, vocab, seed, s=1.1, repeat=0.05):
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    p = np.arange(1, vocab + 1, dtype=np.float64) ** -s
+    p /= p.sum()
+    ids = rng.choice(vocab, size=n, p=p)
+    rep = np.nonzero(rng.random(n) < repeat)[0]
+    for i in rep[rep > 0]:
+        ids[i] = ids[i - 1]
+    return ids.astype(np.int64)
+
+
+def ragged_positions(seed):
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(64, 513, 16)
+    starts = rng.integers(0, 32768, 16)
+    return np.concatenate([s + np.arange(n) for s, n in zip(starts, lens)]).astype(np.int32)
+
+
+def make_rms(name, rows, dim, dt, res, seed):
+    import torch
+    import exl3r.ffi as ffi
+    es = 2
+    nbytes = (4 if res else 2) * rows * dim * es + dim * es
+    sets = sets_for(nbytes)
+    bufs = []
+    for k in range(sets):
+        x = gen((rows, dim), 0.0, 1.0, dt, seed + 3 * k)
+        r = gen((rows, dim), 0.0, 4.0, dt, seed + 3 * k + 1) if res else None
+        bufs.append((x, r, torch.empty_like(x)))
+    w = gen((dim,), 1.0, 0.1, dt, seed + 99)
+
+    def launch(i):
+        x, r, y = bufs[i % sets]
+        if res:
+            ffi.rms_norm_res_in(x, w, y, r, 1e-6)
+        else:
+            ffi.rms_norm(x, w, y, 1e-6)
+    kind = "residual RMSNorm" if res else "RMSNorm"
+    return Work(name, nbytes, launch, f"{kind} [{rows},{dim}] {str(dt).split('.')[-1]}", sets)
+
+
+def make_act(name, rows, cols, dt, act, seed):
+    import torch
+    import exl3r.ffi as ffi
+    nbytes = 3 * rows * cols * 2
+    sets = sets_for(nbytes)
+    bufs = [(gen((rows, cols), 0.0, 1.0, dt, seed + 2 * k), gen((rows, cols), 0.0, 1.0, dt, seed + 2 * k + 1),
+             torch.empty((rows, cols), device="cuda", dtype=dt)) for k in range(sets)]
+    fn = ffi.silu_mul if act == "silu" else ffi.gelu_mul
+
+    def launch(i):
+        g, u, z = bufs[i % sets]
+        fn(g, u, z)
+    return Work(name, nbytes, launch, f"{act.upper()}(gate)*up [{rows},{cols}] {str(dt).split('.')[-1]}", sets)
+
+
+def make_rope(name, pos, hq, hk, hd, R, mode, dt, seed, bsz=1, per_seq=False):
+    import numpy as np
+    import torch
+    import exl3r
+    import exl3r.ffi as ffi
+    T = pos.size if not per_seq else bsz
+    seq = T if not per_seq else 1
+    b = 1 if not per_seq else bsz
+    nbytes = 2 * T * (hq + hk) * hd * 2 + 4 * T + 2 * hd * 2
+    sets = sets_for(nbytes)
+    inv = torch.from_numpy((1.0 / 1e6 ** (np.arange(0, R, 2, dtype=np.float64) / R)).astype(np.float32)).cuda()
+    qn, kn = gen((hd,), 1.0, 0.1, dt, seed + 50), gen((hd,), 1.0, 0.1, dt, seed + 51)
+    pos_d = torch.from_numpy(pos).cuda()
+    bufs = [(gen((b, seq, hq, hd), 0.0, 1.0, dt, seed + 2 * k), gen((b, seq, hk, hd), 0.0, 1.0, dt, seed + 2 * k + 1))
+            for k in range(sets)]
+    m = exl3r.ROPE_NEOX if mode == "neox" else exl3r.ROPE_GPTJ
+
+    def launch(i):
+        q, k = bufs[i % sets]
+        if per_seq:
+            ffi.rope(q, q, k, k, inv, 0, pos_d, qn, kn, 1e-6, 0.0, m, 1.0)
+        else:
+            ffi.rope(q, q, k, k, inv, 0, None, qn, kn, 1e-6, 0.0, m, 1.0, position_ids=pos_d.view(1, -1))
+    return Work(name, nbytes, launch, f"q/k head-norm + {mode} RoPE T={T} heads {hq}/{hk} hd {hd} rotary {R}", sets)
+
+
+def make_gather(name, vocab, hidden, n, dt, out_dt, ids, seed, norm=False):
+    import torch
+    import exl3r.ffi as ffi
+    table = gen((vocab, hidden), 0.0, 0.02, dt, seed)
+    ids_d = torch.from_numpy(ids).cuda()
+    es_o = torch.empty((), dtype=out_dt).element_size()
+    if not norm:
+        nbytes = n * hidden * (2 + es_o) + n * 8
+        sets = sets_for(n * hidden * es_o)
+        outs = [torch.empty((n, hidden), device="cuda", dtype=out_dt) for _ in range(sets)]
+
+        def launch(i):
+            ffi.embedding(table, ids_d, outs[i % sets])
+        desc = f"embedding gather [{vocab},{hidden}] n={n}"
+    else:
+        w = gen((hidden,), 1.0, 0.1, dt, seed + 1)
+        nbytes = n * hidden * 2 * 3 + n * 8 + hidden * 2
+        sets = sets_for(2 * n * hidden * 2)
+        outs = [(torch.empty((n, hidden), device="cuda", dtype=dt), torch.empty((n, hidden), device="cuda", dtype=dt))
+                for _ in range(sets)]
+
+        def launch(i):
+            h, y = outs[i % sets]
+            ffi.embedding_rms_norm(table, ids_d, h, w, y, 1e-6)
+        desc = f"embedding gather + RMSNorm [{vocab},{hidden}] n={n} (h and y written)"
+    return Work(name, nbytes, launch, desc, sets)
+
+
+def make_copy(name):
+    import torch
+    import exl3r
+    nb = 1 << 30
+    src = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    dst = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    naive = exl3r.load_naive()
+
+    def launch(i):
+        rc = naive.calib_copy(src.data_ptr(), dst.data_ptr(), nb, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+    return Work(name, 2 * nb, launch, "plain copy 1 GiB (counter calibration)")
+
+
+def make_decode(fused, seed=7):
+    """One layer of a 64-row decode step, fp16: attn-norm (residual) + q/k head-norm + RoPE +
+    mlp-norm (residual) + SiLU-mul, fused (4 launches) or naive unfused (10 launches)."""
+    import numpy as np
+    import torch
+    import exl3r
+    import exl3r.ffi as ffi
+    T, H, I, hq, hk, hd = 64, 5120, 17408, 64, 8, 128
+    f16 = torch.float16
+    resid = gen((T, H), 0.0, 4.0, f16, seed)
+    a_out = gen((T, H), 0.0, 1.0, f16, seed + 1)
+    m_out = gen((T, H), 0.0, 1.0, f16, seed + 2)
+    w1, w2 = gen((H,), 1.0, 0.1, f16, seed + 3), gen((H,), 1.0, 0.1, f16, seed + 4)
+    y = torch.empty((T, H), device="cuda", dtype=f16)
+    q = gen((T, 1, hq, hd), 0.0, 1.0, f16, seed + 5)
+    k = gen((T, 1, hk, hd), 0.0, 1.0, f16, seed + 6)
+    qn, kn = gen((hd,), 1.0, 0.1, f16, seed + 7), gen((hd,), 1.0, 0.1, f16, seed + 8)
+    pos = torch.from_numpy(np.random.default_rng(seed).integers(0, 32768, T).astype(np.int32)).cuda()
+    inv = torch.from_numpy((1.0 / 1e6 ** (np.arange(0, hd, 2, dtype=np.float64) / hd)).astype(np.float32)).cuda()
+    gate, up = gen((T, I), 0.0, 1.0, f16, seed + 9), gen((T, I), 0.0, 1.0, f16, seed + 10)
+    act = torch.empty((T, I), device="cuda", dtype=f16)
+    nbytes = 2 * (4 * T * H * 2 + H * 2) + (2 * T * (hq + hk) * hd * 2 + 4 * T) + 3 * T * I * 2
+    if fused:
+        def launch(i):
+            ffi.rms_norm_res_in(a_out, w1, y, resid, 1e-6)
+            ffi.rope(q, q, k, k, inv, 0, pos, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0)
+            ffi.rms_norm_res_in(m_out, w2, y, resid, 1e-6)
+            ffi.silu_mul(gate, up, act)
+        return Work("decode_fused", nbytes, launch, "decode layer T=64 fused (4 launches)")
+    naive = exl3r.load_naive()
+    tmp = torch.empty((T, I), device="cuda", dtype=f16)
+    P = lambda t: t.data_ptr()
+
+    def launch(i):
+        s = torch.cuda.current_stream().cuda_stream
+        rc = naive.naive_add_f16(P(a_out), P(resid), P(resid), T * H, s)
+        rc |= naive.naive_rms_norm_f16(P(resid), P(w1), P(y), T, H, 1e-6, s)
+        rc |= naive.naive_head_norm_f16(P(q), P(qn), T, hq, hd, 1e-6, s)
+        rc |= naive.naive_head_norm_f16(P(k), P(kn), T, hk, hd, 1e-6, s)
+        rc |= naive.naive_rope_neox_f16(P(q), P(inv), P(pos), T, 1, hq, hd, s)
+        rc |= naive.naive_rope_neox_f16(P(k), P(inv), P(pos), T, 1, hk, hd, s)
+        rc |= naive.naive_add_f16(P(m_out), P(resid), P(resid), T * H, s)
+        rc |= naive.naive_rms_norm_f16(P(resid), P(w2), P(y), T, H, 1e-6, s)
+        rc |= naive.naive_silu_f16(P(gate), P(tmp), T * I, s)
+        rc |= naive.naive_mul_f16(P(tmp), P(up), P(act), T * I, s)
+        assert rc == 0
+    return Work("decode_naive", nbytes, launch, "decode layer T=64 naive unfused (10 launches)")
+
+
+def make_all(only=None):
+    import torch
+    bf16, f16 = torch.bfloat16, torch.float16
+    ragged = ragged_positions(0)
+    builders = {
+        "rms_c3": lambda: make_rms("rms_c3", 8192, 5120, bf16, True, 100),
+        "silu_c3": lambda: make_act("silu_c3", 8192, 17408, bf16, "silu", 200),
+        "gelu_c3": lambda: make_act("gelu_c3", 8192, 17408, bf16, "gelu", 200),
+        "rope_c4": lambda: make_rope("rope_c4", ragged, 64, 8, 128, 128, "neox", f16, 300),
+        "rope_c4_gptj": lambda: make_rope("rope_c4_gptj", ragged, 64, 8, 128, 64, "gptj", f16, 310),
+        "gather_c5": lambda: make_gather("gather_c5", 151936, 5120, 16384, bf16, bf16, zipf_ids(16384, 151936, 1), 400),
+        "gather_norm_c5": lambda: make_gather("gather_norm_c5", 151936, 5120, 16384, bf16, bf16,
+                                              zipf_ids(16384, 151936, 1), 400, norm=True),
+        "rms_c1": lambda: make_rms("rms_c1", 512, 1024, f16, False, 500),
+        "silu_c1": lambda: make_act("silu_c1", 512, 3072, f16, "silu", 510),
+        "rope_c1": lambda: make_rope("rope_c1", __import__("numpy").arange(512, dtype="int32"), 16, 8, 128, 128, "neox",
+                                     f16, 520),
+        "gather_c1": lambda: make_gather("gather_c1", 151936, 1024, 512, f16, f16,
+                                         __import__("numpy").random.default_rng(0).integers(0, 151936, 512), 530),
+        "decode_fused": lambda: make_decode(True),
+        "decode_naive": lambda: make_decode(False),
+        "calib_copy": lambda: make_copy("calib_copy"),
+    }
+    names = [only] if only else [n for n in OPS if n not in ("calib_copy", "rms_c2")]
+    return {n: builders[n]() for n in names}
+
+
+# ------------------------------------------------------------------------------------------------
+# Timing
+
+def time_launches(work, steps, warmup):
+    """Average duration of one launch (ms): HIP events on the launch stream around `steps`
+    back-to-back launches."""
+    import torch
+    for i in range(warmup):
+        work.launch(i)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(steps):
+        work.launch(warmup + i)
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def time_graph(work, per_graph=20, replays=10):
+    """Per-launch time with the launches captured in a HIP graph (no host launch overhead)."""
+    import torch
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(per_graph):
+            work.launch(i)
+    g.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(replays):
+        g.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / (per_graph * replays)
+
+
+def rms_c2_latencies():
+    """Config 2: decode-batch residual RMSNorm, f16, hidden 5120, T in {1, 8, 32, 64}: us per call,
+    eager (back-to-back launches) and inside a HIP graph."""
+    import torch
+    out = {}
+    for T in (1, 8, 32, 64):
+        w = make_rms(f"rms_c2_t{T}", T, 5120, torch.float16, True, 600 + T)
+        eager = time_launches(w, 200, 20) * 1000
+        graph = time_graph(w, 50, 10) * 1000
+        out[str(T)] = {"us_eager": round(eager, 3), "us_graph": round(graph, 3), "bytes": w.nbytes,
+                       "gbs_graph": round(w.nbytes / (graph * 1e-6) / 1e9, 1)}
+    return out
+
+
+# ------------------------------------------------------------------------------------------------
+# CPU baseline (the oracle, timed on this host)
+
+def cpu_baseline(seconds):
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as orc
+    cores = min(16, len(os.sched_getaffinity(0)))
+    rng = np.random.default_rng(0)
+    rows_n, rows_a = 256, 64
+    x = orc.to_bits(rng.standard_normal((rows_n, 5120), dtype=np.float32), orc.BF16)
+    r0 = orc.to_bits(rng.standard_normal((rows_n, 5120), dtype=np.float32) * 4, orc.BF16)
+    w = orc.to_bits(rng.standard_normal(5120, dtype=np.float32) * 0.1 + 1, orc.BF16)
+    g = orc.to_bits(rng.standard_normal((rows_a, 17408), dtype=np.float32), orc.BF16)
+    u = orc.to_bits(rng.standard_normal((rows_a, 17408), dtype=np.float32), orc.BF16)
+    nbytes = (4 * rows_n * 5120 + 5120) * 2 + 2 * 3 * rows_a * 17408 * 2
+
+    def step():
+        r = r0.copy()
+        orc.rms_norm(x, orc.BF16, w, orc.BF16, orc.BF16, 1e-6, r=r, rt=orc.BF16, nthreads=cores)
+        orc.act_mul(orc.ACT_SILU, g, u, orc.BF16, orc.BF16, nthreads=cores)
+        orc.act_mul(orc.ACT_GELU, g, u, orc.BF16, orc.BF16, nthreads=cores)
+
+    step()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 5:
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": (f"C3 step on a row sample: residual RMSNorm [{rows_n},5120] + SiLU-mul and GELU-mul "
+                       f"[{rows_a},17408] bf16, CPU oracle (C, OpenMP, {cores} threads), median of {len(times)} "
+                       f"reps over ~{seconds:.0f} s")}
+
+
+def traffic_from_profiles(op):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, or None."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        parts = line.split()
+        if len(parts) >= 2 and parts[0] == op + ":":
+            kv = dict(p.split("=", 1) for p in parts[1:] if "=" in p)
+            if "traffic_bytes" in kv:
+                return int(float(kv["traffic_bytes"]))
+    return None
+
+
+# ------------------------------------------------------------------------------------------------
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the row ops are "
+              "token-independent and would shard over tokens with no exchange -- run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import exl3r
+    exl3r.load()
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        if args.op:
+            work = make_all(args.op)[args.op] if args.op != "rms_c2" else None
+            if work is None:
+                log(json.dumps(rms_c2_latencies()))
+                return
+            ms = time_launches(work, args.steps, args.warmup)
+            log(f"{work.name}: {work.desc}: {ms * 1000:.2f} us/launch, {work.nbytes / (ms * 1e-3) / 1e9:.1f} GB/s")
+            return
+
+        works = make_all()
+        torch.cuda.synchronize()
+        ops = {}
+        for name, w in works.items():
+            steps = max(args.steps, 50) if name.endswith("_c1") or name.startswith("decode") else args.steps
+            ms = time_launches(w, steps, args.warmup)
+            gbs = w.nbytes / (ms * 1e-3) / 1e9
+            ops[name] = {"desc": w.desc, "us": round(ms * 1000, 3), "bytes": w.nbytes, "gbs": round(gbs, 1),
+                         "frac_peak": round(gbs / PEAK_GBS, 4)}
+            log(f"{name:15s} {ms * 1000:10.2f} us  {gbs:8.1f} GB/s  {gbs / PEAK_GBS * 100:5.1f}%  {w.desc}")
+
+        dec = {}
+        for name in ("decode_fused", "decode_naive"):
+            dec[name] = {"us_eager": ops[name]["us"], "us_graph": round(time_graph(works[name], 20, 10) * 1000, 3)}
+        decode = {"fused_us": dec["decode_fused"]["us_graph"], "naive_us": dec["decode_naive"]["us_graph"],
+                  "speedup": round(dec["decode_naive"]["us_graph"] / dec["decode_fused"]["us_graph"], 3),
+                  "eager": {"fused_us": dec["decode_fused"]["us_eager"], "naive_us": dec["decode_naive"]["us_eager"],
+                            "speedup": round(dec["decode_naive"]["us_eager"] / dec["decode_fused"]["us_eager"], 3)},
+                  "timing": "HIP graph replay of 20 layers x 10 replays (eager: back-to-back launches)"}
+        log(f"decode layer T=64: fused {decode['fused_us']:.2f} us vs naive {decode['naive_us']:.2f} us "
+            f"(x{decode['speedup']:.2f}, graph); eager x{decode['eager']['speedup']:.2f}")
+        c2 = rms_c2_latencies()
+        log(f"C2 residual RMSNorm us (graph): {[c2[t]['us_graph'] for t in c2]}")
+
+        # The timed step: config-3 prefill row ops back to back.
+        step_works = [works["rms_c3"], works["silu_c3"], works["gelu_c3"]]
+        step_bytes = sum(w.nbytes for w in step_works)
+        for i in range(args.warmup):
+            for w in step_works:
+                w.launch(i)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for i in range(args.steps):
+            for w in step_works:
+                w.launch(args.warmup + i)
+        e.record()
+        torch.cuda.synchronize()
+        ms_step = s.elapsed_time(e) / args.steps
+
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    dom = ops["silu_c3"]
+    roof = {"bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_GBS, "unit": "GB/s",
+            "frac": round(dom["gbs"] / PEAK_GBS, 4), "traffic": traffic_from_profiles("silu_c3"),
+            "kernel": "k_act_mul<SILU, bf16, bf16> (silu_c3)", "bytes_per_launch": dom["bytes"]}
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(args.cpu_seconds)
+        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: seeded N(0,1) activations, N(0,4) residual, N(1,0.1) weights, N(0,0.02) table, "
+                "Zipf(1.1) ids, ragged positions",
+        "config": {"workload": "C3 prefill row ops (BASELINE configs[2]): residual RMSNorm [8192,5120] + "
+                               "SiLU-mul + GELU-mul [8192,17408], bf16 I/O, fp32 arithmetic",
+                   "io_dtype": "bf16", "tokens": 8192, "hidden": 5120, "intermediate": 17408,
+                   "frac_peak": round(value / PEAK_GBS, 4)},
+        "roofline": roof, "cpu_baseline": cpu, "ops": ops, "decode_step": decode, "c2_decode_rms_norm": c2,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -9,8 +9,9 @@
 //   gelu(x) = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))      (activation_kernels.cuh:52-58)
 // both evaluated as x * sigmoid(z) (GELU through 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)), which has
 // no 1 + tanh cancellation for x << 0): with e^-z = 2^t, sigmoid = q for t <= 0 and p * q for t > 0,
-// where p = 2^-|t| in (0, 1] and q = 1 / (1 + p), so results far in the tail (down to fp32
-// denormals) keep full relative precision instead of flushing through 1 / (1 + huge).
+// where p = 2^-|t| in (0, 1] and q = 1 / (1 + p).  For |t| > 64 (where 1 + p == 1) p is evaluated
+// as 2^(64 - |t|) and the 2^-64 is applied to the final product, so tail results keep full precision
+// down into the fp32 denormals instead of flushing inside v_exp_f32.
 //
 // Streaming layout: 8-element chunks (16 bytes per 16-bit tensor) per lane, UNROLL chunks in flight
 // per thread, strided by blockDim so each wave-wide access is 1 KiB contiguous.  Contiguous
@@ -32,9 +33,12 @@ __device__ __forceinline__ float act_f(float x)
     float t;   // e^-z = 2^t
     if constexpr (ACT == ACT_SILU) t = x * -kLog2e;
     else t = x * fmaf(kGeluK2, x * x, kGeluK1);
-    const float p = exp2f(-fabsf(t));                     // denormal-correct exp2
-    const float q = __builtin_amdgcn_rcpf(1.0f + p);      // argument in [1, 2]
-    return x * (t <= 0.0f ? q : p * q);
+    const float n = -fabsf(t);
+    const bool tail = n < -64.0f;
+    const float p = __builtin_amdgcn_exp2f(tail ? n + 64.0f : n);   // normal for n >= -190
+    const float q = __builtin_amdgcn_rcpf(1.0f + (tail ? 0.0f : p)); // argument in [1, 2]
+    const float r = x * (t <= 0.0f ? q : p * q);
+    return (tail && t > 0.0f) ? r * 0x1p-64f : r;
 }
 
 struct ActArgs
@@ -48,21 +52,26 @@ struct ActArgs
     float limit;
 };
 
+template <int ACT, bool LIMIT>
+__device__ __forceinline__ float act_mul1(float g, float u, float limit)
+{
+    float a = act_f<ACT>(g);
+    if constexpr (LIMIT)
+    {
+        if (u < -limit) u = -limit;
+        if (u > limit) u = limit;
+        if (a > limit) a = limit;
+    }
+    return a * u;
+}
+
 template <int ACT, class OT, bool LIMIT>
-__device__ __forceinline__ void act_chunk(const float (&g)[8], float (&u)[8], float limit, float (&o)[8])
+__device__ __forceinline__ void act_chunk(const float (&g)[8], const float (&u)[8], float limit, float (&o)[8])
 {
     #pragma unroll
     for (int j = 0; j < 8; ++j)
     {
-        float a = act_f<ACT>(g[j]);
-        float v = u[j];
-        if constexpr (LIMIT)
-        {
-            if (v < -limit) v = -limit;
-            if (v > limit) v = limit;
-            if (a > limit) a = limit;
-        }
-        float p = a * v;
+        float p = act_mul1<ACT, LIMIT>(g[j], u[j], limit);
         if constexpr (OT::code == DT_F16) p = clamp_f16(p);
         o[j] = p;
     }
@@ -117,12 +126,11 @@ __global__ __launch_bounds__(256) void k_act_mul_generic(ActArgs a, int it, int 
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     {
         const int64_t r = i / a.cols, c = i - r * a.cols;
-        float g[8] = { load1(a.x, it, r * a.ldx + c) };
-        float v[8] = { load1(a.y, it, r * a.ldy + c) };
-        float o[8];
-        if (ot == DT_F16) act_chunk<ACT, TF16, true>(g, v, a.limit, o);
-        else act_chunk<ACT, TF32, true>(g, v, a.limit, o);
-        store1(a.z, ot, r * a.ldz + c, o[0]);
+        const float g = load1(a.x, it, r * a.ldx + c);
+        const float u = load1(a.y, it, r * a.ldy + c);
+        float p = a.limit != 0.0f ? act_mul1<ACT, true>(g, u, a.limit) : act_mul1<ACT, false>(g, u, a.limit);
+        if (ot == DT_F16) p = clamp_f16(p);
+        store1(a.z, ot, r * a.ldz + c, p);
     }
 }
 

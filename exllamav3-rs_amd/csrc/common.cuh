@@ -14,6 +14,7 @@ namespace exl3r {
 enum : int { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2, DT_I32 = 3, DT_I64 = 4 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -65,8 +66,17 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi)
     return __builtin_bit_cast(uint32_t, h);
 }
 
-// Round an fp32 value to a 16-bit format and back (exact re-expansion).
-__device__ __forceinline__ float round_f16(float v) { return (float)(_Float16)v; }
+// Round an fp32 value to a 16-bit format and back (exact re-expansion).  A scalar
+// (_Float16)(a * b) is selected as v_fma_mixlo_f16, which rounds the exact product once instead of
+// the fp32 product (a different result when the fp32 product lands on an f16 tie).
+// An empty asm statement hides the producing multiply from that pattern (it emits no instruction).
+__device__ __forceinline__ float opaque(float v)
+{
+    asm volatile("" : "+v"(v));
+    return v;
+}
+__device__ __forceinline__ _Float16 to_f16(float v) { return (_Float16)opaque(v); }
+__device__ __forceinline__ float round_f16(float v) { return (float)to_f16(v); }
 __device__ __forceinline__ float round_bf16(float v) { return bf16lo(pack_bf16(v, 0.0f)); }
 
 template <class T> __device__ __forceinline__ typename T::Vec load8(const void* base, int64_t elem);
@@ -119,10 +129,15 @@ template <> __device__ __forceinline__ void unpack8<TBF16>(const TBF16::Vec& v, 
     #pragma unroll
     for (int i = 0; i < 4; ++i) { f[2 * i] = bf16lo(v.a[i]); f[2 * i + 1] = bf16hi(v.a[i]); }
 }
+// F32 chunks are reinterpreted as whole float vectors before element access: with the packed-fp32
+// VALU forms disabled, hipcc (ROCm 7.2) lowers a bit_cast of a single u32x4 element to a broadcast of
+// element 0, while a whole-vector bit_cast is lowered correctly.
 template <> __device__ __forceinline__ void unpack8<TF32>(const TF32::Vec& v, float (&f)[8])
 {
+    const f32x4 a = __builtin_bit_cast(f32x4, v.a);
+    const f32x4 b = __builtin_bit_cast(f32x4, v.b);
     #pragma unroll
-    for (int i = 0; i < 4; ++i) { f[i] = __builtin_bit_cast(float, v.a[i]); f[4 + i] = __builtin_bit_cast(float, v.b[i]); }
+    for (int i = 0; i < 4; ++i) { f[i] = a[i]; f[4 + i] = b[i]; }
 }
 
 template <> __device__ __forceinline__ TF16::Vec pack8<TF16>(const float (&f)[8])
@@ -141,9 +156,12 @@ template <> __device__ __forceinline__ TBF16::Vec pack8<TBF16>(const float (&f)[
 }
 template <> __device__ __forceinline__ TF32::Vec pack8<TF32>(const float (&f)[8])
 {
-    TF32::Vec v;
+    f32x4 a, b;
     #pragma unroll
-    for (int i = 0; i < 4; ++i) { v.a[i] = __builtin_bit_cast(uint32_t, f[i]); v.b[i] = __builtin_bit_cast(uint32_t, f[4 + i]); }
+    for (int i = 0; i < 4; ++i) { a[i] = f[i]; b[i] = f[4 + i]; }
+    TF32::Vec v;
+    v.a = __builtin_bit_cast(u32x4, a);
+    v.b = __builtin_bit_cast(u32x4, b);
     return v;
 }
 
@@ -160,7 +178,7 @@ __device__ __forceinline__ float load1(const void* p, int dt, int64_t i)
 }
 __device__ __forceinline__ void store1(void* p, int dt, int64_t i, float v)
 {
-    if (dt == DT_F16) ((_Float16*)p)[i] = (_Float16)v;
+    if (dt == DT_F16) ((_Float16*)p)[i] = to_f16(v);
     else if (dt == DT_BF16) ((uint16_t*)p)[i] = (uint16_t)(pack_bf16(v, 0.0f) & 0xffffu);
     else ((float*)p)[i] = v;
 }

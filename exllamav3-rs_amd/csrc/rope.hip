@@ -146,13 +146,13 @@ __global__ __launch_bounds__(1024) void k_rope(RopeArgs a)
                     if constexpr (NORM == NORM_HALF)
                     {
                         const TF16::Vec wv = load8<TF16>(w, e0);
-                        const _Float16 cbh = (_Float16)a.cb;
+                        const _Float16 cbh = to_f16(a.cb);
                         #pragma unroll
                         for (int j = 0; j < 8; ++j)
                         {
                             const uint32_t word = wv.a[j >> 1];
                             const _Float16 wh = __builtin_bit_cast(_Float16, (uint16_t)((j & 1) ? word >> 16 : word & 0xffffu)) + cbh;
-                            const _Float16 nh = (_Float16)(f[j] * rmf);
+                            const _Float16 nh = to_f16(f[j] * rmf);
                             f[j] = (float)(wh * nh);
                         }
                     }
@@ -259,8 +259,8 @@ __global__ __launch_bounds__(256) void k_rope_generic(RopeArgs a, int dt, int mo
             {
                 if (norm == NORM_HALF)
                 {
-                    const _Float16 wh = ((const _Float16*)w)[d] + (_Float16)a.cb;
-                    hv[d] = (float)(wh * (_Float16)(hv[d] * rmf));
+                    const _Float16 wh = ((const _Float16*)w)[d] + to_f16(a.cb);
+                    hv[d] = (float)(wh * to_f16(hv[d] * rmf));
                 }
                 else
                     hv[d] = round1((hv[d] * rmf) * (load1(w, a.wt, d) + a.cb), dt);

@@ -56,6 +56,22 @@ def assert_close_ulp(got, exp, code, max_ulp, rel=None, what=""):
     return d
 
 
+def assert_close_rel(got, exp, rel, what=""):
+    """f32 outputs: elementwise |got - exp| <= rel * |exp| + 2^-146 (a few fp32 denormal ulps;
+    NaN must match NaN)."""
+    g = np.asarray(got, np.float64)
+    e = np.asarray(exp, np.float64)
+    nan_ok = np.array_equal(np.isnan(g), np.isnan(e))
+    m = ~np.isnan(e)
+    inf_ok = np.array_equal(g[m & np.isinf(e)], e[m & np.isinf(e)])
+    f = m & np.isfinite(e)
+    err = np.maximum(np.abs(g[f] - e[f]) - 2.0 ** -146, 0.0) / np.maximum(np.abs(e[f]), 2.0 ** -149)
+    worst = float(err.max()) if err.size else 0.0
+    stats = f"{what}: max_elem_rel_err={worst:.3e} nan_ok={nan_ok} inf_ok={inf_ok}"
+    print(stats)
+    assert nan_ok and inf_ok and worst <= rel, stats
+
+
 def assert_bitwise(got, exp, what=""):
     same = np.array_equal(np.ascontiguousarray(got).view(np.uint8), np.ascontiguousarray(exp).view(np.uint8))
     print(f"{what}: bitwise={'yes' if same else 'NO'}")

@@ -1,13 +1,15 @@
 """GPU parity of exl3r_silu_mul / exl3r_gelu_mul against the CPU oracle: <= 1 ulp for 16-bit z,
-max abs err <= 2e-3 of the output scale (one ulp for bf16).  An f32 z carries the GPU's fp32
-evaluation error (v_exp_f32 / v_rcp_f32 are 1-ulp approximations; the oracle evaluates in fp64):
-<= 8 fp32 ulps."""
+max abs err <= 2e-3 of the output scale (one ulp for bf16).  An f32 z (an extension: the
+reference writes f16) carries the fp32 evaluation error of the GPU (v_exp_f32 / v_rcp_f32 are
+1-ulp approximations, and the fp32 rounding of the exponent argument t = x (K1 + K2 x^2) shifts
+exp2(t) by ~|t| 2^-23 ln 2 relative, with |t| <= ~150 before the result underflows; the oracle
+evaluates in fp64): elementwise relative error <= 2^-15 (plus a few denormal ulps)."""
 import numpy as np
 import pytest
 import torch
 
 import exl3r.ffi as ffi
-from _gpu import NTHREADS, TORCH_DT, assert_close_ulp, dev_normal, from_dev
+from _gpu import NTHREADS, TORCH_DT, assert_close_rel, assert_close_ulp, dev_normal, from_dev
 from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -27,7 +29,11 @@ def run(act, rows, cols, it, zt, limit=0.0, seed=0, ld=None, std=1.0):
     torch.cuda.synchronize()
     exp = orc.act_mul(code, np.ascontiguousarray(from_dev(x)), np.ascontiguousarray(from_dev(y)), it, zt, limit,
                       nthreads=NTHREADS)
-    assert_close_ulp(from_dev(z), exp, zt, 8 if zt == F32 else 1, what=f"{act} {rows}x{cols} in={it} z={zt} L={limit}")
+    what = f"{act} {rows}x{cols} in={it} z={zt} L={limit}"
+    if zt == F32:
+        assert_close_rel(from_dev(z), exp, 2.0 ** -15, what=what)
+    else:
+        assert_close_ulp(from_dev(z), exp, zt, 1, what=what)
 
 
 @pytest.mark.parametrize("act", ["silu", "gelu"])
