@@ -56,6 +56,8 @@ extern "C" void exl3r_tune_rms(int maxv, int threads)
     exl3r::tuning().rms_threads = threads;
 }
 
+extern "C" void exl3r_tune_rms_mode(int mode) { exl3r::tuning().rms_mode = mode; }
+
 extern "C" void exl3r_tune_act(int unroll, int threads, int blocks_per_cu)
 {
     exl3r::tuning().act_unroll = unroll;
@@ -63,6 +65,8 @@ extern "C" void exl3r_tune_act(int unroll, int threads, int blocks_per_cu)
     exl3r::tuning().act_blocks_per_cu = blocks_per_cu;
 }
 
-extern "C" void exl3r_tune_rope(int threads) { exl3r::tuning().rope_threads = threads; }
+extern "C" void exl3r_tune_rope(int iters) { exl3r::tuning().rope_iters = iters; }
 
 extern "C" void exl3r_tune_embed(int threads) { exl3r::tuning().embed_threads = threads; }
+
+extern "C" void exl3r_tune_xcd(int on) { exl3r::tuning().xcd = on; }

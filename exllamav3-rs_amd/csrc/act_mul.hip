@@ -50,6 +50,7 @@ struct ActArgs
     int64_t rows;
     int64_t cols;            // elements per row
     float limit;
+    int xcd;                 // XCD-sliced block order (single-pass flat grids)
 };
 
 template <int ACT, bool LIMIT>
@@ -82,12 +83,14 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
 {
     const int64_t cpr = a.cols >> 3;   // chunks per row
     const int nt = blockDim.x;
+    const int64_t bx = (a.xcd && gridDim.y == 1 && (int64_t)gridDim.x * nt * UNROLL >= cpr)
+                           ? xcd_slice(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
     for (int64_t row = blockIdx.y; row < a.rows; row += gridDim.y)
     {
         const char* xr = (const char*)a.x + row * a.ldx * IT::bytes;
         const char* yr = (const char*)a.y + row * a.ldy * IT::bytes;
         char* zr = (char*)a.z + row * a.ldz * OT::bytes;
-        for (int64_t base = (int64_t)blockIdx.x * nt * UNROLL + threadIdx.x; base < cpr;
+        for (int64_t base = bx * nt * UNROLL + threadIdx.x; base < cpr;
              base += (int64_t)gridDim.x * nt * UNROLL)
         {
             typename IT::Vec xv[UNROLL], yv[UNROLL];
@@ -97,8 +100,8 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
                 const int64_t c = base + (int64_t)u * nt;
                 if (c < cpr)
                 {
-                    xv[u] = load8<IT>(xr, c * 8);
-                    yv[u] = load8<IT>(yr, c * 8);
+                    xv[u] = load8s<IT>(xr, c * 8);
+                    yv[u] = load8s<IT>(yr, c * 8);
                 }
             }
             #pragma unroll
@@ -150,10 +153,11 @@ template <int ACT, class IT, class OT>
 static void launch_act_vec(const ActArgs& a, hipStream_t s)
 {
     const Tuning& tu = tuning();
-    const int unroll = (tu.act_unroll == 1 || tu.act_unroll == 2 || tu.act_unroll == 4 || tu.act_unroll == 8) ? tu.act_unroll : 4;
-    const int threads = (tu.act_threads > 0 && tu.act_threads % 64 == 0 && tu.act_threads <= 256) ? tu.act_threads : 256;
+    // Two chunks per thread in 128-thread workgroups measured best on MI355X (C3: 136 us, 6.3 TB/s).
+    const int unroll = (tu.act_unroll == 1 || tu.act_unroll == 2 || tu.act_unroll == 4 || tu.act_unroll == 8) ? tu.act_unroll : 2;
+    const int threads = (tu.act_threads > 0 && tu.act_threads % 64 == 0 && tu.act_threads <= 256) ? tu.act_threads : 128;
     const int64_t cpr = a.cols >> 3;
-    const int per = a.limit != 0.0f ? 4 : unroll;
+    const int per = a.limit != 0.0f ? 2 : unroll;
     int64_t bx = (cpr + (int64_t)threads * per - 1) / ((int64_t)threads * per);
     if (tu.act_blocks_per_cu > 0)
     {
@@ -163,7 +167,7 @@ static void launch_act_vec(const ActArgs& a, hipStream_t s)
     if (bx > kMaxGridX) bx = kMaxGridX;
     const dim3 grid((unsigned)bx, (unsigned)(a.rows < 65535 ? a.rows : 65535));
     if (a.limit != 0.0f)
-        k_act_mul<ACT, IT, OT, 4, true><<<grid, threads, 0, s>>>(a);
+        k_act_mul<ACT, IT, OT, 2, true><<<grid, threads, 0, s>>>(a);
     else
     {
         switch (unroll)
@@ -191,7 +195,7 @@ static int act_mul_entry(const char* op, const void* x, const void* y, int it, v
         return set_error(EXL3R_EINVAL, "%s: in-place z needs the aliased operand's dtype and stride", op);
     if (rows == 0 || cols == 0) return EXL3R_OK;
 
-    ActArgs a{ x, y, z, ldx, ldy, ldz, rows, cols, limit };
+    ActArgs a{ x, y, z, ldx, ldy, ldz, rows, cols, limit, tuning().xcd };
     if (rows == 1 || (ldx == cols && ldy == cols && ldz == cols))
     {
         a.cols = rows * cols;

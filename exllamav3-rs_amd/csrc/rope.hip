@@ -41,87 +41,106 @@ struct RopeArgs
     const void* kw;
     int wt;
     float eps, cb, attn;
-    int heads_per_wg;
+    int tok_span;       // tokens spanned by one workgroup's item range (k_rope)
 };
 
 enum { NORM_NONE = 0, NORM_HALF = 1, NORM_F32 = 2 };
 
-__device__ __forceinline__ int token_position(const RopeArgs& a, int64_t tok)
+__device__ __forceinline__ int token_position(const RopeArgs& a, int tok)
 {
-    const int64_t b = tok / a.seq_len;
-    const int s = (int)(tok - b * a.seq_len);
+    const int seq = (int)a.seq_len;
+    const int b = tok / seq;
+    const int s = tok - b * seq;
     if (a.positions) return a.positions[b] + s;
     if (a.position_ids) return a.position_ids[tok];
     return a.position + s;
 }
 
-// sin/cos of every rotary frequency of this token into LDS (float2 {cos, sin} * attn_factor).
-__device__ __forceinline__ void fill_sincos(const RopeArgs& a, int pos, float2* cs)
+// {cos, sin} * attn_factor of rotary frequency t at position pos: fp64 evaluation of the fp32
+// angle, rounded once (correctly rounded fp32 values).
+__device__ __forceinline__ float2 rope_cs(const RopeArgs& a, int t, int pos)
 {
-    // sin/cos of the fp32 angle evaluated in fp64 and rounded once: correctly rounded fp32 values
-    // (R/2 evaluations per token, shared by all heads, so the fp64 cost is negligible).
-    const float pf = (float)pos;
-    for (int t = threadIdx.x; t < a.R / 2; t += blockDim.x)
-    {
-        const float ang = __fmul_rn(a.inv_freq[t], pf);
-        double sd, cd;
-        sincos((double)ang, &sd, &cd);
-        cs[t] = make_float2((float)cd * a.attn, (float)sd * a.attn);
-    }
+    const float ang = __fmul_rn(a.inv_freq[t], (float)pos);
+    double sd, cd;
+    sincos((double)ang, &sd, &cd);
+    return make_float2((float)cd * a.attn, (float)sd * a.attn);
 }
 
-template <class IO, int MODE, int LPH, int ITERS, int NORM>
-__global__ __launch_bounds__(1024) void k_rope(RopeArgs a)
+// sin/cos of every rotary frequency of one token into LDS (generic kernel).
+__device__ __forceinline__ void fill_sincos(const RopeArgs& a, int pos, float2* cs)
 {
-    extern __shared__ float2 cs[];
-    for (int64_t tok = blockIdx.x; tok < a.tokens; tok += gridDim.x)
-    {
-        const int tid = threadIdx.x;
-        const int slot = tid / LPH;
-        const int lane = tid % LPH;
-        const int slots = blockDim.x / LPH;
-        const int nheads = a.hq + a.hk;
-        const int h0 = blockIdx.y * a.heads_per_wg;
-        const int h1 = min(nheads, h0 + a.heads_per_wg);
-        const bool lane_ok = lane * 8 < a.hd;
+    for (int t = threadIdx.x; t < a.R / 2; t += blockDim.x) cs[t] = rope_cs(a, t, pos);
+}
 
-        // Head loads first, so HBM latency overlaps the sin/cos evaluation.
+// Work item = one (token, head) pair; a workgroup takes a contiguous range of slots * ITERS items,
+// which spans at most a.tok_span tokens.  Every head chunk is loaded first; the sin/cos of the
+// spanned tokens are evaluated into LDS while those loads are in flight.
+template <class IO, int MODE, int LPH, int ITERS, int NORM>
+__global__ __launch_bounds__(256) void k_rope(RopeArgs a)
+{
+    extern __shared__ float2 cs[];            // [tok_span][R / 2]
+    const int tid = threadIdx.x;
+    const int slot = tid / LPH;
+    const int lane = tid % LPH;
+    const int slots = blockDim.x / LPH;
+    const int nheads = a.hq + a.hk;
+    const int R2 = a.R / 2;
+    const int64_t items = a.tokens * nheads;
+    const int64_t per_wg = (int64_t)slots * ITERS;
+    const bool lane_ok = lane * 8 < a.hd;
+    const int e0 = lane * 8;                  // first head element held by this lane
+
+    for (int64_t i0 = (int64_t)blockIdx.x * per_wg; i0 < items; i0 += (int64_t)gridDim.x * per_wg)
+    {
+        const int tok0 = (int)(i0 / nheads);
+        const int hfirst = (int)(i0 - (int64_t)tok0 * nheads);
+
         typename IO::Vec v[ITERS];
         char* optr[ITERS];
+        int trel[ITERS], head[ITERS];
         bool act[ITERS];
         #pragma unroll
         for (int it = 0; it < ITERS; ++it)
         {
-            const int head = h0 + slot + it * slots;
-            act[it] = head < h1 && lane_ok;
+            int rel = hfirst + it * slots + slot;
+            int tr = 0;
+            while (rel >= nheads) { rel -= nheads; ++tr; }
+            trel[it] = tr;
+            head[it] = rel;
+            const int tok = tok0 + tr;
+            act[it] = tok < a.tokens && lane_ok;
             optr[it] = nullptr;
             if (act[it])
             {
                 const char* ip;
-                if (head < a.hq)
+                if (rel < a.hq)
                 {
-                    ip = (const char*)a.q + (tok * a.q_ts + (int64_t)head * a.q_hs) * IO::bytes;
-                    optr[it] = (char*)a.oq + (tok * a.q_ts + (int64_t)head * a.q_hs) * IO::bytes;
+                    const int64_t off = ((int64_t)tok * a.q_ts + (int64_t)rel * a.q_hs) * IO::bytes;
+                    ip = (const char*)a.q + off;
+                    optr[it] = (char*)a.oq + off;
                 }
                 else
                 {
-                    ip = (const char*)a.k + (tok * a.k_ts + (int64_t)(head - a.hq) * a.k_hs) * IO::bytes;
-                    optr[it] = (char*)a.ok + (tok * a.k_ts + (int64_t)(head - a.hq) * a.k_hs) * IO::bytes;
+                    const int64_t off = ((int64_t)tok * a.k_ts + (int64_t)(rel - a.hq) * a.k_hs) * IO::bytes;
+                    ip = (const char*)a.k + off;
+                    optr[it] = (char*)a.ok + off;
                 }
-                v[it] = load8<IO>(ip, (int64_t)lane * 8);
+                v[it] = load8s<IO>(ip, e0);
             }
         }
 
-        const int pos = token_position(a, tok);
-        fill_sincos(a, pos, cs);
+        for (int i = tid; i < a.tok_span * R2; i += blockDim.x)
+        {
+            const int tr = i / R2;
+            const int tok = tok0 + tr;
+            if (tok < a.tokens) cs[i] = rope_cs(a, i - tr * R2, token_position(a, tok));
+        }
         __syncthreads();
 
-        const int e0 = lane * 8;            // first head element held by this lane
-        const int half = a.R / 2;
         #pragma unroll
         for (int it = 0; it < ITERS; ++it)
         {
-            const int head = h0 + slot + it * slots;
+            const float2* csr = cs + trel[it] * R2;
             float f[8];
             if (act[it]) unpack8<IO>(v[it], f);
             else
@@ -142,7 +161,7 @@ __global__ __launch_bounds__(1024) void k_rope(RopeArgs a)
                 const float rmf = rms_factor(ss, a.hd, a.eps);
                 if (act[it])
                 {
-                    const void* w = head < a.hq ? a.qw : a.kw;
+                    const void* w = head[it] < a.hq ? a.qw : a.kw;
                     if constexpr (NORM == NORM_HALF)
                     {
                         const TF16::Vec wv = load8<TF16>(w, e0);
@@ -177,7 +196,7 @@ __global__ __launch_bounds__(1024) void k_rope(RopeArgs a)
                     const int e = e0 + 2 * p;
                     if (e < a.R)
                     {
-                        const float2 c = cs[e >> 1];
+                        const float2 c = csr[e >> 1];
                         const float v1 = f[2 * p], v2 = f[2 * p + 1];
                         f[2 * p] = v1 * c.x - v2 * c.y;
                         f[2 * p + 1] = v2 * c.x + v1 * c.y;
@@ -186,20 +205,18 @@ __global__ __launch_bounds__(1024) void k_rope(RopeArgs a)
             }
             else
             {
-                // Partner lane half / 8 lanes away inside the head's lane group; values are exchanged as
+                // Partner lane R/16 lanes away inside the head's lane group; values are exchanged as
                 // packed io words (exact: they are io-rounded already).
+                const int half = R2;
                 const int dl = half >> 3;
                 const bool rot = e0 < a.R;
                 const bool lower = e0 < half;
                 const int src_lane = rot ? (lower ? tid + dl : tid - dl) : tid;
-                uint32_t mine[4], other[4];
+                uint32_t other[4];
                 const typename IO::Vec pk = pack8<IO>(f);
                 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                {
-                    mine[i] = pk.a[i];
-                    other[i] = (uint32_t)__builtin_amdgcn_ds_bpermute((src_lane & 63) << 2, (int)mine[i]);
-                }
+                    other[i] = (uint32_t)__builtin_amdgcn_ds_bpermute((src_lane & 63) << 2, (int)(uint32_t)pk.a[i]);
                 if (rot)
                 {
                     #pragma clang fp contract(off)
@@ -212,7 +229,7 @@ __global__ __launch_bounds__(1024) void k_rope(RopeArgs a)
                     #pragma unroll
                     for (int j = 0; j < 8; ++j)
                     {
-                        const float2 c = cs[t0 + j];
+                        const float2 c = csr[t0 + j];
                         f[j] = lower ? f[j] * c.x - g[j] * c.y : f[j] * c.x + g[j] * c.y;
                     }
                 }
@@ -220,7 +237,7 @@ __global__ __launch_bounds__(1024) void k_rope(RopeArgs a)
 
             if (act[it]) store8<IO>(optr[it], (int64_t)e0, pack8<IO>(f));
         }
-        __syncthreads();   // cs[] is refilled for the next token
+        __syncthreads();   // cs[] is refilled for the next range
     }
 }
 
@@ -235,7 +252,7 @@ __global__ __launch_bounds__(256) void k_rope_generic(RopeArgs a, int dt, int mo
     const int half = a.R / 2;
     for (int64_t tok = blockIdx.x; tok < a.tokens; tok += gridDim.x)
     {
-    fill_sincos(a, token_position(a, tok), cs);
+    fill_sincos(a, token_position(a, (int)tok), cs);
     __syncthreads();
     for (int head = 0; head < a.hq + a.hk; ++head)
     {
@@ -284,57 +301,45 @@ __global__ __launch_bounds__(256) void k_rope_generic(RopeArgs a, int dt, int mo
 }
 
 template <class IO, int MODE, int LPH, int NORM>
-static void launch_rope_lph(const RopeArgs& a, dim3 grid, int threads, int iters, hipStream_t s)
+static void launch_rope_lph(RopeArgs a, int iters, hipStream_t s)
 {
-    const size_t lds = (size_t)(a.R / 2) * sizeof(float2);
+    const int threads = 256;
+    const int64_t per_wg = (int64_t)(threads / LPH) * iters;
+    const int nheads = a.hq + a.hk;
+    a.tok_span = (int)((nheads + per_wg - 2) / nheads) + 1;
+    const int64_t items = a.tokens * nheads;
+    int64_t blocks = (items + per_wg - 1) / per_wg;
+    if (blocks > kMaxGridX) blocks = kMaxGridX;
+    const size_t lds = (size_t)a.tok_span * (a.R / 2) * sizeof(float2);
     switch (iters)
     {
-        case 1: k_rope<IO, MODE, LPH, 1, NORM><<<grid, threads, lds, s>>>(a); break;
-        case 2: k_rope<IO, MODE, LPH, 2, NORM><<<grid, threads, lds, s>>>(a); break;
-        default: k_rope<IO, MODE, LPH, 4, NORM><<<grid, threads, lds, s>>>(a); break;
+        case 1: k_rope<IO, MODE, LPH, 1, NORM><<<(unsigned)blocks, threads, lds, s>>>(a); break;
+        case 2: k_rope<IO, MODE, LPH, 2, NORM><<<(unsigned)blocks, threads, lds, s>>>(a); break;
+        default: k_rope<IO, MODE, LPH, 4, NORM><<<(unsigned)blocks, threads, lds, s>>>(a); break;
     }
 }
 
+// Items per lane: enough workgroups to fill 256 CUs several times over, then up to four heads per
+// lane so each wave keeps 4 KiB of loads in flight.
 template <class IO, int MODE, int NORM>
-static void launch_rope_vec(RopeArgs a, int lph, hipStream_t s)
+static void launch_rope_vec(const RopeArgs& a, int lph, hipStream_t s)
 {
-    // Heads per workgroup: a whole token per workgroup when there are enough tokens to fill the
-    // GPU, otherwise split the heads of a token over 256-thread workgroups.
-    const int nheads = a.hq + a.hk;
-    const int lanes = nheads * lph;
-    int threads, iters;
+    const int64_t items = a.tokens * (a.hq + a.hk);
+    const int64_t slots = 256 / lph;
     const Tuning& tu = tuning();
-    if (tu.rope_threads > 0 && tu.rope_threads % 64 == 0 && tu.rope_threads <= 1024 && tu.rope_threads >= lph)
-    {
-        threads = tu.rope_threads;
-        iters = 1;
-    }
-    else if (a.tokens >= 512)
-    {
-        iters = (lanes + 1023) / 1024;
-        if (iters > 4) iters = 4;
-        int per = (lanes + iters - 1) / iters;
-        threads = ((per + 63) / 64) * 64;
-        if (threads > 1024) threads = 1024;
-    }
-    else
-    {
-        iters = 1;
-        threads = lanes < 256 ? ((lanes + 63) / 64) * 64 : 256;
-    }
-    if (iters == 3) iters = 4;
-    a.heads_per_wg = (threads / lph) * iters;
-    const int groups = (nheads + a.heads_per_wg - 1) / a.heads_per_wg;
-    const dim3 grid((unsigned)(a.tokens < kMaxGridX ? a.tokens : kMaxGridX), (unsigned)groups);
+    int iters = 1;
+    if (tu.rope_iters == 1 || tu.rope_iters == 2 || tu.rope_iters == 4) iters = tu.rope_iters;
+    else if (items >= slots * 4 * 2048) iters = 4;
+    else if (items >= slots * 2 * 2048) iters = 2;
     switch (lph)
     {
-        case 1: launch_rope_lph<IO, MODE, 1, NORM>(a, grid, threads, iters, s); break;
-        case 2: launch_rope_lph<IO, MODE, 2, NORM>(a, grid, threads, iters, s); break;
-        case 4: launch_rope_lph<IO, MODE, 4, NORM>(a, grid, threads, iters, s); break;
-        case 8: launch_rope_lph<IO, MODE, 8, NORM>(a, grid, threads, iters, s); break;
-        case 16: launch_rope_lph<IO, MODE, 16, NORM>(a, grid, threads, iters, s); break;
-        case 32: launch_rope_lph<IO, MODE, 32, NORM>(a, grid, threads, iters, s); break;
-        default: launch_rope_lph<IO, MODE, 64, NORM>(a, grid, threads, iters, s); break;
+        case 1: launch_rope_lph<IO, MODE, 1, NORM>(a, iters, s); break;
+        case 2: launch_rope_lph<IO, MODE, 2, NORM>(a, iters, s); break;
+        case 4: launch_rope_lph<IO, MODE, 4, NORM>(a, iters, s); break;
+        case 8: launch_rope_lph<IO, MODE, 8, NORM>(a, iters, s); break;
+        case 16: launch_rope_lph<IO, MODE, 16, NORM>(a, iters, s); break;
+        case 32: launch_rope_lph<IO, MODE, 32, NORM>(a, iters, s); break;
+        default: launch_rope_lph<IO, MODE, 64, NORM>(a, iters, s); break;
     }
 }
 
