@@ -44,6 +44,20 @@ Tuning& tuning()
     return t;
 }
 
+int device_cus()
+{
+    static int n = 0;
+    if (n == 0)
+    {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            n = v;
+        else
+            n = 256;
+    }
+    return n;
+}
+
 }  // namespace exl3r
 
 extern "C" int exl3r_version(void) { return 10000; }
@@ -56,8 +70,6 @@ extern "C" void exl3r_tune_rms(int maxv, int threads)
     exl3r::tuning().rms_threads = threads;
 }
 
-extern "C" void exl3r_tune_rms_mode(int mode) { exl3r::tuning().rms_mode = mode; }
-
 extern "C" void exl3r_tune_act(int unroll, int threads, int blocks_per_cu)
 {
     exl3r::tuning().act_unroll = unroll;
@@ -68,5 +80,3 @@ extern "C" void exl3r_tune_act(int unroll, int threads, int blocks_per_cu)
 extern "C" void exl3r_tune_rope(int iters) { exl3r::tuning().rope_iters = iters; }
 
 extern "C" void exl3r_tune_embed(int threads) { exl3r::tuning().embed_threads = threads; }
-
-extern "C" void exl3r_tune_xcd(int on) { exl3r::tuning().xcd = on; }

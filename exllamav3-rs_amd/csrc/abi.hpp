@@ -35,12 +35,14 @@ constexpr int64_t kMaxGridX = 1 << 20;
 // Tuning overrides (0 = automatic); set only by exl3r_tune_* for sweeps.
 struct Tuning
 {
-    int rms_maxv = 0, rms_threads = 0, rms_mode = 0;
+    int rms_maxv = 0, rms_threads = 0;
     int act_unroll = 0, act_threads = 0, act_blocks_per_cu = 0;
     int rope_iters = 0;
     int embed_threads = 0;
-    int xcd = 0;
 };
 Tuning& tuning();
+
+// Compute units of the current device (cached after the first call).
+int device_cus();
 
 }  // namespace exl3r

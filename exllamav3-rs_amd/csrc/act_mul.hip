@@ -50,7 +50,6 @@ struct ActArgs
     int64_t rows;
     int64_t cols;            // elements per row
     float limit;
-    int xcd;                 // XCD-sliced block order (single-pass flat grids)
 };
 
 template <int ACT, bool LIMIT>
@@ -83,14 +82,12 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
 {
     const int64_t cpr = a.cols >> 3;   // chunks per row
     const int nt = blockDim.x;
-    const int64_t bx = (a.xcd && gridDim.y == 1 && (int64_t)gridDim.x * nt * UNROLL >= cpr)
-                           ? xcd_slice(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
     for (int64_t row = blockIdx.y; row < a.rows; row += gridDim.y)
     {
         const char* xr = (const char*)a.x + row * a.ldx * IT::bytes;
         const char* yr = (const char*)a.y + row * a.ldy * IT::bytes;
         char* zr = (char*)a.z + row * a.ldz * OT::bytes;
-        for (int64_t base = bx * nt * UNROLL + threadIdx.x; base < cpr;
+        for (int64_t base = (int64_t)blockIdx.x * nt * UNROLL + threadIdx.x; base < cpr;
              base += (int64_t)gridDim.x * nt * UNROLL)
         {
             typename IT::Vec xv[UNROLL], yv[UNROLL];
@@ -137,18 +134,6 @@ __global__ __launch_bounds__(256) void k_act_mul_generic(ActArgs a, int it, int 
     }
 }
 
-static int num_cus()
-{
-    static int n = 0;
-    if (n == 0)
-    {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-            n = 256;
-    }
-    return n;
-}
-
 template <int ACT, class IT, class OT>
 static void launch_act_vec(const ActArgs& a, hipStream_t s)
 {
@@ -161,7 +146,7 @@ static void launch_act_vec(const ActArgs& a, hipStream_t s)
     int64_t bx = (cpr + (int64_t)threads * per - 1) / ((int64_t)threads * per);
     if (tu.act_blocks_per_cu > 0)
     {
-        const int64_t cap = (int64_t)tu.act_blocks_per_cu * num_cus() / (a.rows < 65535 ? (a.rows > 0 ? a.rows : 1) : 65535);
+        const int64_t cap = (int64_t)tu.act_blocks_per_cu * device_cus() / (a.rows < 65535 ? (a.rows > 0 ? a.rows : 1) : 65535);
         if (bx > cap) bx = cap > 0 ? cap : 1;
     }
     if (bx > kMaxGridX) bx = kMaxGridX;
@@ -195,7 +180,7 @@ static int act_mul_entry(const char* op, const void* x, const void* y, int it, v
         return set_error(EXL3R_EINVAL, "%s: in-place z needs the aliased operand's dtype and stride", op);
     if (rows == 0 || cols == 0) return EXL3R_OK;
 
-    ActArgs a{ x, y, z, ldx, ldy, ldz, rows, cols, limit, tuning().xcd };
+    ActArgs a{ x, y, z, ldx, ldy, ldz, rows, cols, limit };
     if (rows == 1 || (ldx == cols && ldy == cols && ldz == cols))
     {
         a.cols = rows * cols;

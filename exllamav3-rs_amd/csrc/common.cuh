@@ -232,17 +232,6 @@ __device__ __forceinline__ float rms_factor(double sum, int n, float eps)
 __device__ __forceinline__ float clamp_f16(float v) { return fmaxf(-65504.0f, fminf(v, 65504.0f)); }
 
 // ---------------------------------------------------------------------------------------------
-// XCD-aware block order.  MI355X dispatches consecutive workgroups round-robin over its 8 XCDs
-// (each with its own L2); this bijection on [0, n) gives XCD k a contiguous k-th slice of the
-// work, so each XCD streams its own address range.
-__device__ __forceinline__ int64_t xcd_slice(int64_t bid, int64_t n)
-{
-    const int64_t q = n >> 3, r = n & 7;
-    const int64_t k = bid & 7;
-    return k * q + (k < r ? k : r) + (bid >> 3);
-}
-
-// ---------------------------------------------------------------------------------------------
 // Reductions.
 
 template <int CTRL>

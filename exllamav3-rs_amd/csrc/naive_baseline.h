@@ -21,7 +21,8 @@ EXL3R_API int naive_rope_neox_f16(void* x, const float* inv_freq, const int32_t*
 EXL3R_API int naive_silu_f16(const void* g, void* z, int64_t n, void* stream);
 /* z = a * b */
 EXL3R_API int naive_mul_f16(const void* a, const void* b, void* z, int64_t n, void* stream);
-/* Plain 16-byte-per-lane copy of nbytes (multiple of 16), for rocprof counter calibration. */
+/* Non-temporal 16-byte-per-lane copy of nbytes (multiple of 16): bandwidth reference and rocprof
+ * counter calibration. */
 EXL3R_API int calib_copy(const void* src, void* dst, int64_t nbytes, void* stream);
 #ifdef __cplusplus
 }

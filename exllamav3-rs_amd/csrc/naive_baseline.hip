@@ -79,10 +79,12 @@ __global__ void k_naive_mul(const half_t* a, const half_t* b, half_t* z, int64_t
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(256) void k_calib_copy(const u32x4* src, u32x4* dst, int64_t n16)
+// One 16-byte chunk per thread, non-temporal load and store: the fastest copy measured on MI355X
+// (6.6 TB/s for 1 GiB), used both as the practical bandwidth reference and to calibrate counters.
+__global__ __launch_bounds__(128) void k_calib_copy(const u32x4* src, u32x4* dst, int64_t n16)
 {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x)
-        dst[i] = src[i];
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n16) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
 static unsigned blocks_for(int64_t n, int threads)
@@ -135,8 +137,7 @@ extern "C" int calib_copy(const void* src, void* dst, int64_t nbytes, void* stre
 {
     if (nbytes % 16) return -1;
     const int64_t n16 = nbytes / 16;
-    int64_t b = (n16 + 255) / 256;
-    if (b > 8192) b = 8192;
-    k_calib_copy<<<(unsigned)b, 256, 0, (hipStream_t)stream>>>((const u32x4*)src, (u32x4*)dst, n16);
+    if (n16 > ((int64_t)1 << 37)) return -1;
+    k_calib_copy<<<(unsigned)((n16 + 127) / 128), 128, 0, (hipStream_t)stream>>>((const u32x4*)src, (u32x4*)dst, n16);
     return (int)hipGetLastError();
 }

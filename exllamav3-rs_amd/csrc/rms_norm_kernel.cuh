@@ -7,13 +7,11 @@
 //   (norm.cu:273; IEEE fp32 sqrt and divide here);
 //   y = (x * (w + constant_bias)) * rmf in fp32, rounded once (norm.cu:110-124, 232-239, 75-83).
 //
-// Layout: one row per wave (rows up to 8192 elements) or per workgroup (longer rows).  A row is split
-// into chunks of 8 elements; lane t owns chunks t, t + nt, ... (at most MAXV), so every wave-wide
-// access is 64 lanes x 16 bytes contiguous.
+// Layout: one row per workgroup.  A row is split into chunks of 8 elements; thread t owns chunks
+// t, t + nt, ... (at most MAXV), so every wave-wide access is 64 lanes x 16 bytes contiguous.
 // The whole row stays in VGPRs between the reduction and the output pass: one HBM read of x (and r),
 // one write of y (and r) per row -- the 4-pass minimum for RES_IN, where the reference re-reads r
-// at dim > 4096.  The row reduction is a DPP butterfly inside the wave (plus one LDS hop across waves
-// for workgroup-per-row).
+// at dim > 4096.  The row reduction is a DPP butterfly inside each wave and one LDS hop across waves.
 #pragma once
 
 #include "abi.hpp"
@@ -42,7 +40,6 @@ struct RmsArgs
     int64_t rows;
     int dim;
     float eps, cb, cs;
-    int xcd;            // XCD-sliced row order (single-pass grids)
 };
 
 __device__ __forceinline__ int64_t load_id(const void* ids, int idt, int64_t i)
@@ -71,21 +68,30 @@ __device__ __forceinline__ void unpack_w8(u32x4 pre, const void* w, int wt, int6
     }
 }
 
-// One row: x (and r) loaded in chunks c = tid, tid + nt, ... (at most MAXV per lane), every load
-// issued before any arithmetic; the row is reduced either inside one wave (WAVE: nt == 64, DPP +
-// swizzle butterfly, no LDS) or across the workgroup (one LDS hop).
-template <class XT, class YT, class RT, int MAXV, int MODE, bool WAVE>
-__device__ __forceinline__ void rms_row(const RmsArgs& a, int64_t row, int tid, int nt, double* red)
+// Registers of one row between its loads and its arithmetic.
+template <class XT, class RT, int MAXV>
+struct RowRegs
+{
+    typename XT::Vec xv[MAXV];
+    typename RT::Vec rv[MAXV];
+    u32x4 wv[MAXV];
+    bool valid;
+};
+
+// Issues every HBM load of one row -- x (and r) in chunks c = tid, tid + nt, ... (at most MAXV per
+// lane), plus the weight chunks when load_w -- before any arithmetic.
+template <class XT, class RT, int MAXV, int MODE>
+__device__ __forceinline__ void rms_load(const RmsArgs& a, int64_t row, int tid, int nt, bool load_w,
+                                         RowRegs<XT, RT, MAXV>& L)
 {
     const int nc = a.dim >> 3;
-    const bool has_w = a.w != nullptr;
     const char* xrow;
-    bool valid = true;
+    L.valid = true;
     if constexpr (MODE == RMS_GATHER)
     {
         int64_t id = load_id(a.ids, a.idt, row);
-        valid = id >= 0 && id < a.vocab;
-        if (!valid)
+        L.valid = id >= 0 && id < a.vocab;
+        if (!L.valid)
         {
             if (tid == 0 && a.err) atomicOr(a.err, 1);
             id = 0;
@@ -94,29 +100,38 @@ __device__ __forceinline__ void rms_row(const RmsArgs& a, int64_t row, int tid, 
     }
     else
         xrow = (const char*)a.x + row * a.ldx * XT::bytes;
-    char* rrow = (char*)a.r + row * a.ldr * RT::bytes;
-    char* yrow = (char*)a.y + row * a.ldy * YT::bytes;
-
-    // Issue every HBM load of the row (x, r) and the weight fetch before any arithmetic.
-    typename XT::Vec xv[MAXV];
-    [[maybe_unused]] typename RT::Vec rv[MAXV];
-    u32x4 wv[MAXV];
+    const char* rrow = (const char*)a.r + row * a.ldr * RT::bytes;
     #pragma unroll
     for (int k = 0; k < MAXV; ++k)
     {
         const int c = tid + k * nt;
         if (c < nc)
         {
-            if (valid)
+            if (L.valid)
             {
-                if constexpr (MODE == RMS_GATHER) xv[k] = load8<XT>(xrow, (int64_t)c * 8);   // hot table rows
-                else xv[k] = load8s<XT>(xrow, (int64_t)c * 8);
+                if constexpr (MODE == RMS_GATHER) L.xv[k] = load8<XT>(xrow, (int64_t)c * 8);   // hot table rows
+                else L.xv[k] = load8s<XT>(xrow, (int64_t)c * 8);
             }
-            if constexpr (MODE == RMS_RES_IN) rv[k] = load8s<RT>(rrow, (int64_t)c * 8);
-            if (has_w) wv[k] = prefetch_w8(a.w, a.wt, (int64_t)c * 8);
+            if constexpr (MODE == RMS_RES_IN) L.rv[k] = load8s<RT>(rrow, (int64_t)c * 8);
+            if (load_w && a.w) L.wv[k] = prefetch_w8(a.w, a.wt, (int64_t)c * 8);
         }
     }
+}
 
+// Arithmetic and stores of one loaded row; the row sum is reduced across the workgroup (DPP butterfly
+// inside each wave, one LDS hop across waves).
+template <class XT, class YT, class RT, int MAXV, int MODE>
+__device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int tid, int nt, RowRegs<XT, RT, MAXV>& L,
+                                           double* red)
+{
+    const int nc = a.dim >> 3;
+    const bool has_w = a.w != nullptr;
+    const bool valid = L.valid;
+    char* rrow = (char*)a.r + row * a.ldr * RT::bytes;
+    char* yrow = (char*)a.y + row * a.ldy * YT::bytes;
+    auto& xv = L.xv;
+    auto& rv = L.rv;
+    auto& wv = L.wv;
     // Pass 1: residual update and sum of squares.  The row is then cached in its narrowest
     // exact form (x as loaded, or the rounded residual), 4 VGPRs per chunk for 16-bit data,
     // and re-expanded in pass 2.
@@ -171,8 +186,7 @@ __device__ __forceinline__ void rms_row(const RmsArgs& a, int64_t row, int tid, 
     }
 
     // fp64 row sum (exact for 16-bit data), one rounding, IEEE fp32 sqrt and divide.
-    if constexpr (WAVE) ss = group_sum64<64>(ss);
-    else ss = block_sum64(ss, red);
+    ss = block_sum64(ss, red);
     const float rmf = rms_factor(ss, a.dim, a.eps) * a.cs;
 
     // Pass 2: scale, weight, round once, store.
@@ -214,27 +228,19 @@ __device__ __forceinline__ void rms_row(const RmsArgs& a, int64_t row, int tid, 
 }
 
 template <class XT, class YT, class RT, int MAXV, int MODE>
+__device__ __forceinline__ void rms_row(const RmsArgs& a, int64_t row, int tid, int nt, double* red)
+{
+    RowRegs<XT, RT, MAXV> L;
+    rms_load<XT, RT, MAXV, MODE>(a, row, tid, nt, true, L);
+    rms_finish<XT, YT, RT, MAXV, MODE>(a, row, tid, nt, L, red);
+}
+
+template <class XT, class YT, class RT, int MAXV, int MODE>
 __global__ __launch_bounds__(1024) void k_rms_norm(RmsArgs a)
 {
     __shared__ double red[16];
-    if (a.xcd && gridDim.x == a.rows)
-    {
-        rms_row<XT, YT, RT, MAXV, MODE, false>(a, xcd_slice(blockIdx.x, a.rows), threadIdx.x, blockDim.x, red);
-        return;
-    }
     for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x)
-        rms_row<XT, YT, RT, MAXV, MODE, false>(a, row, threadIdx.x, blockDim.x, red);
-}
-
-// Wave-per-row: each wave of a 256-thread workgroup owns one row (dim <= 8192 at MAXV <= 16), so a
-// wave keeps up to 16 chunks of x and r (~20 KiB at hidden 5120) in flight and never waits on a
-// barrier.
-template <class XT, class YT, class RT, int MAXV, int MODE>
-__global__ __launch_bounds__(256) void k_rms_norm_wave(RmsArgs a)
-{
-    const int wpb = blockDim.x >> 6;
-    for (int64_t row = (int64_t)blockIdx.x * wpb + (threadIdx.x >> 6); row < a.rows; row += (int64_t)gridDim.x * wpb)
-        rms_row<XT, YT, RT, MAXV, MODE, true>(a, row, threadIdx.x & 63, 64, nullptr);
+        rms_row<XT, YT, RT, MAXV, MODE>(a, row, threadIdx.x, blockDim.x, red);
 }
 
 // Generic fallback: any dim, any alignment, element-granular, two passes over global memory.
@@ -302,66 +308,36 @@ __global__ __launch_bounds__(256) void k_rms_norm_generic(RmsArgs a, int xt, int
 // ---------------------------------------------------------------------------------------------
 // Host-side launch.
 
-// Launch shape.  Rows of up to 8192 elements (1024 chunks) go wave-per-row with MAXV = chunks / 64
-// rounded up to a compiled size; longer rows use a workgroup per row (MAXV chunks per thread).
+// Launch shape: a workgroup per row, MAXV chunks per thread.  Latency-bound launches (few rows)
+// spread a row over up to 1024 lanes; bandwidth-bound launches use <= 384 lanes per row so several
+// rows share a CU (C3 on MI355X: 2 chunks x 320 threads 58 us, 4 x 192 66 us, 1 x 640 70 us; one
+// wave per row 74 us; persistent workgroups prefetching the next row 58 us).
 struct RmsShape
 {
-    bool wave;
     int maxv;
     int threads;
 };
-
-inline int rms_wave_maxv(int nc)
-{
-    static const int opts[8] = { 1, 2, 4, 6, 8, 10, 12, 16 };
-    const int need = (nc + 63) / 64;
-    for (int m : opts)
-        if (m >= need) return m;
-    return 0;
-}
 
 inline RmsShape rms_shape(int nc, int64_t rows)
 {
     auto thr = [&](int m) { int t = (nc + m - 1) / m; return ((t + 63) / 64) * 64; };
     const Tuning& tu = tuning();
-    // Wave-per-row measured slower than a workgroup per row on MI355X (C3: 74 vs 64 us, decode rows
-    // 6-7 vs 3 us); it is kept as a tuning option.
-    if (tu.rms_mode == 2 && rms_wave_maxv(nc) > 0)
-        return { true, rms_wave_maxv(nc), 256 };
     if (((tu.rms_maxv >= 1 && tu.rms_maxv <= 5) || tu.rms_maxv == 8) &&
         (tu.rms_threads == 0 || (tu.rms_threads % 64 == 0 && tu.rms_threads <= 1024)))
-        return { false, tu.rms_maxv, tu.rms_threads > 0 ? tu.rms_threads : thr(tu.rms_maxv) };
+        return { tu.rms_maxv, tu.rms_threads > 0 ? tu.rms_threads : thr(tu.rms_maxv) };
     // MAXV = 8 does not fit the VGPR budget of a 1024-thread bound; it is the last resort.
     static const int opts[3] = { 1, 2, 4 };
     const int target = rows <= 1024 ? 1024 : 384;
     for (int m : opts)
-        if (thr(m) <= target) return { false, m, thr(m) };
-    if (thr(4) <= 1024) return { false, 4, thr(4) };
-    return { false, 8, thr(8) };   // <= 1024 (rms_vec_ok bounds the row at 8192 chunks)
+        if (thr(m) <= target) return { m, thr(m) };
+    if (thr(4) <= 1024) return { 4, thr(4) };
+    return { 8, thr(8) };   // <= 1024 (rms_vec_ok bounds the row at 8192 chunks)
 }
 
 template <class XT, class YT, class RT, int MODE>
-int launch_rms_vec(RmsArgs a, hipStream_t s)
+int launch_rms_vec(const RmsArgs& a, hipStream_t s)
 {
     const RmsShape sh = rms_shape(a.dim / 8, a.rows);
-    a.xcd = tuning().xcd;
-    if (sh.wave)
-    {
-        int64_t blocks = (a.rows + 3) / 4;
-        const dim3 grid((unsigned)(blocks < kMaxGridX ? blocks : kMaxGridX));
-        switch (sh.maxv)
-        {
-            case 1: k_rms_norm_wave<XT, YT, RT, 1, MODE><<<grid, 256, 0, s>>>(a); break;
-            case 2: k_rms_norm_wave<XT, YT, RT, 2, MODE><<<grid, 256, 0, s>>>(a); break;
-            case 4: k_rms_norm_wave<XT, YT, RT, 4, MODE><<<grid, 256, 0, s>>>(a); break;
-            case 6: k_rms_norm_wave<XT, YT, RT, 6, MODE><<<grid, 256, 0, s>>>(a); break;
-            case 8: k_rms_norm_wave<XT, YT, RT, 8, MODE><<<grid, 256, 0, s>>>(a); break;
-            case 10: k_rms_norm_wave<XT, YT, RT, 10, MODE><<<grid, 256, 0, s>>>(a); break;
-            case 12: k_rms_norm_wave<XT, YT, RT, 12, MODE><<<grid, 256, 0, s>>>(a); break;
-            default: k_rms_norm_wave<XT, YT, RT, 16, MODE><<<grid, 256, 0, s>>>(a); break;
-        }
-        return 0;
-    }
     const dim3 grid((unsigned)(a.rows < kMaxGridX ? a.rows : kMaxGridX));
     switch (sh.maxv)
     {
@@ -386,7 +362,7 @@ inline bool rms_vec_ok(const RmsArgs& a, int xt, int yt, int rt, bool has_r)
     if (has_r && !ok(a.r, a.ldr, rt)) return false;
     if (a.w && !aligned16(a.w)) return false;
     const RmsShape sh = rms_shape(a.dim / 8, a.rows);
-    return sh.wave || ((int64_t)sh.maxv * sh.threads >= a.dim / 8 && sh.threads <= 1024);
+    return (int64_t)sh.maxv * sh.threads >= a.dim / 8 && sh.threads <= 1024;
 }
 
 }  // namespace exl3r

@@ -7,14 +7,10 @@
 extern "C" {
 #endif
 EXL3R_API void exl3r_tune_rms(int maxv, int threads);
-/* 0 automatic, 1 workgroup per row, 2 wave per row */
-EXL3R_API void exl3r_tune_rms_mode(int mode);
 EXL3R_API void exl3r_tune_act(int unroll, int threads, int blocks_per_cu);
 /* heads per lane: 1, 2 or 4 */
 EXL3R_API void exl3r_tune_rope(int iters);
 EXL3R_API void exl3r_tune_embed(int threads);
-/* 1: XCD-sliced workgroup order for single-pass grids */
-EXL3R_API void exl3r_tune_xcd(int on);
 #ifdef __cplusplus
 }
 #endif

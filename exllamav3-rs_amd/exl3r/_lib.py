@@ -37,8 +37,6 @@ PROTOTYPES = {
     "exl3r_tune_act": (None, [_i, _i, _i]),
     "exl3r_tune_rope": (None, [_i]),
     "exl3r_tune_embed": (None, [_i]),
-    "exl3r_tune_rms_mode": (None, [_i]),
-    "exl3r_tune_xcd": (None, [_i]),
 }
 
 NAIVE_PROTOTYPES = {
