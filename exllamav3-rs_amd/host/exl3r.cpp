@@ -1,0 +1,363 @@
+// exl3r host layer implementation (see exl3r.hpp).
+#include "exl3r.hpp"
+
+#include <cmath>
+#include <utility>
+
+namespace exl3r {
+
+namespace {
+
+void check_abi(int rc)
+{
+    if (rc != EXL3R_OK) throw Error(rc, exl3r_last_error());
+}
+
+void check_hip(hipError_t e, const char* what)
+{
+    if (e != hipSuccess) throw Error((int)e, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void require(bool ok, const std::string& msg)
+{
+    if (!ok) throw Error(EXL3R_EINVAL, msg);
+}
+
+int code(DType t) { return (int)t; }
+int code_or(const Tensor* t, DType dflt) { return t ? (int)t->dtype : (int)dflt; }
+const void* ptr(const Tensor* t) { return t ? t->data : nullptr; }
+
+std::vector<int64_t> contiguous_strides(const std::vector<int64_t>& shape)
+{
+    std::vector<int64_t> st(shape.size());
+    int64_t acc = 1;
+    for (int i = (int)shape.size() - 1; i >= 0; --i)
+    {
+        st[i] = acc;
+        acc *= shape[i];
+    }
+    return st;
+}
+
+}  // namespace
+
+size_t dtype_size(DType dt)
+{
+    switch (dt)
+    {
+        case DType::F32: case DType::I32: return 4;
+        case DType::F16: case DType::BF16: return 2;
+        case DType::I64: return 8;
+    }
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Stream / DeviceBuffer
+
+Stream Stream::create()
+{
+    Stream s;
+    check_hip(hipStreamCreate(&s.s_), "hipStreamCreate");
+    s.owned_ = true;
+    return s;
+}
+
+Stream::~Stream()
+{
+    if (owned_ && s_) (void)hipStreamDestroy(s_);
+}
+
+Stream::Stream(Stream&& o) noexcept : s_(o.s_), owned_(o.owned_)
+{
+    o.s_ = nullptr;
+    o.owned_ = false;
+}
+
+Stream& Stream::operator=(Stream&& o) noexcept
+{
+    if (this != &o)
+    {
+        if (owned_ && s_) (void)hipStreamDestroy(s_);
+        s_ = o.s_;
+        owned_ = o.owned_;
+        o.s_ = nullptr;
+        o.owned_ = false;
+    }
+    return *this;
+}
+
+void Stream::synchronize() const { check_hip(hipStreamSynchronize(s_), "hipStreamSynchronize"); }
+
+DeviceBuffer::DeviceBuffer(size_t bytes) : n_(bytes)
+{
+    if (bytes) check_hip(hipMalloc(&p_, bytes), "hipMalloc");
+}
+
+DeviceBuffer::~DeviceBuffer()
+{
+    if (p_) (void)hipFree(p_);
+}
+
+DeviceBuffer::DeviceBuffer(DeviceBuffer&& o) noexcept : p_(o.p_), n_(o.n_)
+{
+    o.p_ = nullptr;
+    o.n_ = 0;
+}
+
+DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept
+{
+    if (this != &o)
+    {
+        if (p_) (void)hipFree(p_);
+        p_ = o.p_;
+        n_ = o.n_;
+        o.p_ = nullptr;
+        o.n_ = 0;
+    }
+    return *this;
+}
+
+void DeviceBuffer::upload(const void* host, size_t bytes, const Stream& s)
+{
+    require(bytes <= n_, "DeviceBuffer::upload: too many bytes");
+    check_hip(hipMemcpyAsync(p_, host, bytes, hipMemcpyHostToDevice, s.get()), "hipMemcpyAsync H2D");
+    s.synchronize();
+}
+
+void DeviceBuffer::download(void* host, size_t bytes, const Stream& s) const
+{
+    require(bytes <= n_, "DeviceBuffer::download: too many bytes");
+    check_hip(hipMemcpyAsync(host, p_, bytes, hipMemcpyDeviceToHost, s.get()), "hipMemcpyAsync D2H");
+    s.synchronize();
+}
+
+// ------------------------------------------------------------------------------------------------
+// Tensor
+
+Tensor::Tensor(void* d, DType t, std::vector<int64_t> shp) : data(d), dtype(t), shape(std::move(shp))
+{
+    strides = contiguous_strides(shape);
+}
+
+Tensor::Tensor(void* d, DType t, std::vector<int64_t> shp, std::vector<int64_t> str)
+    : data(d), dtype(t), shape(std::move(shp)), strides(std::move(str))
+{
+    require(shape.size() == strides.size(), "Tensor: shape and strides differ in rank");
+}
+
+int64_t Tensor::numel() const
+{
+    int64_t n = 1;
+    for (int64_t s : shape) n *= s;
+    return n;
+}
+
+bool Tensor::is_contiguous() const { return strides == contiguous_strides(shape); }
+
+void Tensor::rows_view(int64_t& rows, int64_t& cols, int64_t& ld) const
+{
+    require(dim() >= 1, "expected at least a 1-D tensor");
+    cols = shape.back();
+    require(cols <= 1 || strides.back() == 1, "last dimension must be contiguous");
+    rows = 1;
+    for (int i = 0; i < dim() - 1; ++i) rows *= shape[i];
+    ld = dim() >= 2 ? strides[dim() - 2] : cols;
+    // leading dims must collapse into one stride: stride[i] == stride[i+1] * shape[i+1]
+    for (int i = 0; i + 2 < dim(); ++i)
+        if (shape[i] > 1) require(strides[i] == strides[i + 1] * shape[i + 1], "leading dimensions must collapse to one row stride");
+    if (rows <= 1) ld = cols;
+}
+
+OwnedTensor OwnedTensor::empty(DType dt, std::vector<int64_t> shape)
+{
+    OwnedTensor o;
+    int64_t n = 1;
+    for (int64_t s : shape) n *= s;
+    o.buf = DeviceBuffer((size_t)n * dtype_size(dt));
+    o.t = Tensor(o.buf.data(), dt, std::move(shape));
+    return o;
+}
+
+// ------------------------------------------------------------------------------------------------
+// ffi
+
+namespace ffi {
+
+void rms_norm(const Tensor& x, const Tensor* w, const Tensor& y, float eps, float constant_bias, float constant_scale,
+              const Stream& s)
+{
+    int64_t rows, dim, ldx, ry, dy, ldy;
+    x.rows_view(rows, dim, ldx);
+    y.rows_view(ry, dy, ldy);
+    require(ry == rows && dy == dim, "rms_norm: x and y shapes differ");
+    check_abi(exl3r_rms_norm(x.data, code(x.dtype), ldx, ptr(w), code_or(w, DType::F16), y.data, code(y.dtype), ldy,
+                             rows, dim, eps, constant_bias, constant_scale, s.get()));
+}
+
+void rms_norm_res_in(const Tensor& x, const Tensor* w, const Tensor& y, const Tensor& r, float eps, float bias,
+                     float scale, const Stream& s)
+{
+    int64_t rows, dim, ldx, ry, dy, ldy, rr, dr, ldr;
+    x.rows_view(rows, dim, ldx);
+    y.rows_view(ry, dy, ldy);
+    r.rows_view(rr, dr, ldr);
+    require(ry == rows && dy == dim && rr == rows && dr == dim, "rms_norm_res_in: x, y and r shapes differ");
+    check_abi(exl3r_rms_norm_res_in(x.data, code(x.dtype), ldx, ptr(w), code_or(w, DType::F16), y.data,
+                                    code(y.dtype), ldy, r.data, code(r.dtype), ldr, rows, dim, eps, bias, scale,
+                                    s.get()));
+}
+
+static void act(int which, const Tensor& x, const Tensor& y, const Tensor& z, float act_limit, const Stream& s)
+{
+    int64_t rows, cols, ldx, ry, cy, ldy, rz, cz, ldz;
+    x.rows_view(rows, cols, ldx);
+    y.rows_view(ry, cy, ldy);
+    z.rows_view(rz, cz, ldz);
+    require(ry == rows && cy == cols && rz == rows && cz == cols, "act_mul: x, y and z shapes differ");
+    require(x.dtype == y.dtype, "act_mul: x and y must share a dtype");
+    auto fn = which == 0 ? exl3r_silu_mul : exl3r_gelu_mul;
+    check_abi(fn(x.data, y.data, code(x.dtype), z.data, code(z.dtype), rows, cols, ldx, ldy, ldz, act_limit, s.get()));
+}
+
+void silu_mul(const Tensor& x, const Tensor& y, const Tensor& z, float act_limit, const Stream& s) { act(0, x, y, z, act_limit, s); }
+void gelu_mul(const Tensor& x, const Tensor& y, const Tensor& z, float act_limit, const Stream& s) { act(1, x, y, z, act_limit, s); }
+
+void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
+          int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
+          float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s, const Tensor* position_ids)
+{
+    require(q.dim() == 4, "rope: q must be (bsz, seq_len, heads, head_dim)");
+    require(q.stride(3) == 1 && out_q.strides == q.strides && out_q.shape == q.shape,
+            "rope: q innermost dim must be dense and out_q must share q's layout");
+    const int64_t bsz = q.size(0), seq = q.size(1), hd = q.size(3);
+    require(bsz <= 1 || seq <= 1 || q.stride(0) == seq * q.stride(1), "rope: q batch stride must be seq_len * token stride");
+    int64_t hk = 0, kts = 0, khs = 0;
+    if (k)
+    {
+        require(out_k && k->dim() == 4 && k->size(0) == bsz && k->size(1) == seq && k->size(3) == hd,
+                "rope: k is incorrect shape");
+        require(k->stride(3) == 1 && out_k->strides == k->strides, "rope: out_k must share k's layout");
+        hk = k->size(2);
+        kts = k->stride(1);
+        khs = k->stride(2);
+    }
+    require(inv_freq.dtype == DType::F32, "rope: inv_freq must be float32");
+    require(!positions || positions->dtype == DType::I32, "rope: positions must be int32");
+    require(!position_ids || position_ids->dtype == DType::I32, "rope: position_ids must be int32");
+    const Tensor* nw = q_norm ? q_norm : k_norm;
+    check_abi(exl3r_rope(q.data, out_q.data, q.stride(1), q.stride(2), (int)q.size(2), k ? k->data : nullptr,
+                         out_k ? out_k->data : nullptr, kts, khs, (int)hk, code(q.dtype), bsz, seq, (int)hd,
+                         (const float*)inv_freq.data, (int)(inv_freq.numel() * 2), (int32_t)position,
+                         (const int32_t*)ptr(positions), (const int32_t*)ptr(position_ids), ptr(q_norm), ptr(k_norm),
+                         code_or(nw, DType::F16), norm_eps, norm_constant_bias, (int)rope_mode, attn_factor, s.get()));
+}
+
+void embedding(const Tensor& table, const Tensor& ids, const Tensor& out, int32_t* err_flag, const Stream& s)
+{
+    require(table.dim() == 2 && table.stride(1) == 1, "embedding: table must be [vocab, hidden] with dense rows");
+    int64_t rows, hidden, ldo;
+    out.rows_view(rows, hidden, ldo);
+    require(rows == ids.numel() && hidden == table.size(1), "embedding: out must be [ids.numel(), hidden]");
+    require(ids.is_contiguous(), "embedding: ids must be contiguous");
+    check_abi(exl3r_embedding(table.data, code(table.dtype), table.size(0), table.size(1), table.stride(0), ids.data,
+                              code(ids.dtype), ids.numel(), out.data, code(out.dtype), ldo, err_flag, s.get()));
+}
+
+void embedding_rms_norm(const Tensor& table, const Tensor& ids, const Tensor* h, const Tensor* w, const Tensor& y,
+                        float eps, float constant_bias, float constant_scale, int32_t* err_flag, const Stream& s)
+{
+    require(table.dim() == 2 && table.stride(1) == 1, "embedding_rms_norm: table must be [vocab, hidden]");
+    require(ids.is_contiguous(), "embedding_rms_norm: ids must be contiguous");
+    int64_t rows, hidden, ldy, rh = 0, hh = 0, ldh = table.size(1);
+    y.rows_view(rows, hidden, ldy);
+    require(rows == ids.numel() && hidden == table.size(1), "embedding_rms_norm: y must be [ids.numel(), hidden]");
+    if (h)
+    {
+        h->rows_view(rh, hh, ldh);
+        require(rh == rows && hh == hidden, "embedding_rms_norm: h must be [ids.numel(), hidden]");
+    }
+    check_abi(exl3r_embedding_rms_norm(table.data, code(table.dtype), table.size(0), table.size(1), table.stride(0),
+                                       ids.data, code(ids.dtype), ids.numel(), h ? h->data : nullptr,
+                                       code_or(h, DType::F32), ldh, ptr(w), code_or(w, DType::F16), y.data,
+                                       code(y.dtype), ldy, eps, constant_bias, constant_scale, err_flag, s.get()));
+}
+
+}  // namespace ffi
+
+// ------------------------------------------------------------------------------------------------
+// Modules
+
+OwnedTensor RmsNorm::forward(const Tensor& x, const Stream& s) const
+{
+    OwnedTensor y = OwnedTensor::empty(DType::F16, x.shape);
+    ffi::rms_norm(x, &weight_, y.t, eps_, constant_bias_, constant_scale_, s);
+    return y;
+}
+
+OwnedTensor RmsNorm::forward_res(const Tensor& r, const Tensor* add, const Stream& s) const
+{
+    if (!add) return forward(r, s);
+    require(add->shape == r.shape, "RmsNorm::forward_res: add and residual shapes differ");
+    OwnedTensor y = OwnedTensor::empty(DType::F16, r.shape);
+    ffi::rms_norm_res_in(*add, &weight_, y.t, r, eps_, constant_bias_, constant_scale_, s);
+    return y;
+}
+
+OwnedTensor Embedding::forward(const Tensor& ids, const Stream& s) const
+{
+    std::vector<int64_t> shape = ids.shape;
+    shape.push_back(weight_.size(1));
+    OwnedTensor out = OwnedTensor::empty(out_kind_, shape);
+    ffi::embedding(weight_, ids, out.t, nullptr, s);
+    return out;
+}
+
+OwnedTensor GatedMlp::activate(const Tensor& g, const Tensor& u, Act act, float act_limit, const Stream& s)
+{
+    OwnedTensor a = OwnedTensor::empty(g.dtype, g.shape);
+    if (act == Act::Silu) ffi::silu_mul(g, u, a.t, act_limit, s);
+    else ffi::gelu_mul(g, u, a.t, act_limit, s);
+    return a;
+}
+
+RoPE::RoPE(double theta, int rotary_dim, RopeStyle style, double attn_factor, double linear_factor)
+    : rotary_dim_(rotary_dim), style_(style), attn_factor_((float)attn_factor)
+{
+    inv_freq_host_ = default_inv_freq(theta, rotary_dim, linear_factor);
+    inv_freq_ = DeviceBuffer(inv_freq_host_.size() * sizeof(float));
+    check_hip(hipMemcpy(inv_freq_.data(), inv_freq_host_.data(), inv_freq_.bytes(), hipMemcpyHostToDevice), "hipMemcpy inv_freq");
+    inv_freq_t_ = Tensor(inv_freq_.data(), DType::F32, { (int64_t)inv_freq_host_.size() });
+}
+
+std::vector<float> RoPE::default_inv_freq(double theta, int rotary_dim, double linear_factor)
+{
+    require(rotary_dim >= 2 && rotary_dim % 2 == 0, "RoPE: rotary_dim must be even and >= 2");
+    require(theta > 0.0 && linear_factor > 0.0, "RoPE: theta and the scaling factor must be positive");
+    const float ln_theta = (float)std::log(theta);
+    std::vector<float> inv(rotary_dim / 2);
+    for (int i = 0; i < rotary_dim / 2; ++i)
+    {
+        const float t = (float)(2 * i) / (float)rotary_dim;     // arange(0, d, 2) / d
+        float f = 1.0f / std::exp(t * ln_theta);                 // 1 / exp(t * ln theta)
+        if (linear_factor != 1.0) f = f / (float)linear_factor;
+        inv[i] = f;
+    }
+    return inv;
+}
+
+void RoPE::apply(const Tensor& q, const Tensor& k, int64_t position, const Tensor* positions, const Tensor* q_norm,
+                 const Tensor* k_norm, float norm_eps, float norm_constant_bias, const Stream& s) const
+{
+    ffi::rope(q, q, &k, &k, inv_freq_t_, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias, style_,
+              attn_factor_, s);
+}
+
+void RoPE::apply_one(const Tensor& x, int64_t position, const Tensor* positions, const Tensor* norm, float norm_eps,
+                     float norm_constant_bias, const Stream& s) const
+{
+    ffi::rope(x, x, nullptr, nullptr, inv_freq_t_, position, positions, norm, nullptr, norm_eps, norm_constant_bias,
+              style_, attn_factor_, s);
+}
+
+}  // namespace exl3r

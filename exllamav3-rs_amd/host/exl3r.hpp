@@ -1,0 +1,205 @@
+// exl3r host layer: the C++ counterpart of the reference's Rust side for the fused row ops.
+//
+// The reference binds its kernels through `src/ffi.rs` (safe wrappers over `extern "C"` shim
+// functions taking tch tensors) and calls them from `src/modules.rs` / `src/rope.rs`.  This layer
+// keeps those names and argument meanings over the pointer/shape/stride C ABI of
+// include/exl3r/rowops.h, with a small HIP device-buffer/stream type in place of tch:
+//
+//   exl3r::ffi::rms_norm / rms_norm_res_in / silu_mul / gelu_mul / rope  <- src/ffi.rs:293-333, 464-503
+//   exl3r::ffi::embedding                                                <- index_select, src/modules.rs:430-436
+//   exl3r::RmsNorm::forward / forward_res                                <- src/modules.rs:342-412
+//   exl3r::Embedding::forward                                            <- src/modules.rs:418-437
+//   exl3r::GatedMlp::activate                                            <- src/modules.rs:932-940 (silu_mul step)
+//   exl3r::RoPE (default / linear inv_freq, apply, apply_one)            <- src/rope.rs:33-86, 233-292, 309-317
+//
+// Error behaviour: the reference panics / throws (TORCH_CHECK) on invalid input; here every failure
+// throws exl3r::Error carrying the C ABI status and message.  Kernels are enqueued on the given
+// Stream; nothing here synchronises except the explicit host copies.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/exl3r/rowops.h"
+
+namespace exl3r {
+
+enum class DType : int { F32 = EXL3R_F32, F16 = EXL3R_F16, BF16 = EXL3R_BF16, I32 = EXL3R_I32, I64 = EXL3R_I64 };
+enum class RopeStyle : int { None = EXL3R_ROPE_NONE, GptJ = EXL3R_ROPE_GPTJ, NeoX = EXL3R_ROPE_NEOX };
+
+size_t dtype_size(DType dt);
+
+class Error : public std::runtime_error
+{
+public:
+    Error(int code, const std::string& what) : std::runtime_error(what), code_(code) {}
+    int code() const { return code_; }
+
+private:
+    int code_;
+};
+
+// Owning HIP stream (default priority).  Stream() wraps the null stream.
+class Stream
+{
+public:
+    Stream() = default;
+    static Stream create();
+    ~Stream();
+    Stream(Stream&& o) noexcept;
+    Stream& operator=(Stream&& o) noexcept;
+    Stream(const Stream&) = delete;
+    Stream& operator=(const Stream&) = delete;
+    hipStream_t get() const { return s_; }
+    void synchronize() const;
+
+private:
+    hipStream_t s_ = nullptr;
+    bool owned_ = false;
+};
+
+// Owning device allocation (hipMalloc / hipFree).
+class DeviceBuffer
+{
+public:
+    DeviceBuffer() = default;
+    explicit DeviceBuffer(size_t bytes);
+    ~DeviceBuffer();
+    DeviceBuffer(DeviceBuffer&& o) noexcept;
+    DeviceBuffer& operator=(DeviceBuffer&& o) noexcept;
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    void* data() const { return p_; }
+    size_t bytes() const { return n_; }
+    void upload(const void* host, size_t bytes, const Stream& s);     // async H2D, then stream sync
+    void download(void* host, size_t bytes, const Stream& s) const;   // async D2H, then stream sync
+
+private:
+    void* p_ = nullptr;
+    size_t n_ = 0;
+};
+
+// Non-owning strided view of device memory (the role tch::Tensor plays at the reference's FFI).
+// Strides are in elements; the innermost dimension must be dense for every op here.
+struct Tensor
+{
+    void* data = nullptr;
+    DType dtype = DType::F16;
+    std::vector<int64_t> shape;
+    std::vector<int64_t> strides;
+
+    Tensor() = default;
+    Tensor(void* d, DType t, std::vector<int64_t> shp);                              // contiguous
+    Tensor(void* d, DType t, std::vector<int64_t> shp, std::vector<int64_t> str);    // strided
+    int64_t numel() const;
+    int dim() const { return (int)shape.size(); }
+    int64_t size(int i) const { return shape[i < 0 ? i + dim() : i]; }
+    int64_t stride(int i) const { return strides[i < 0 ? i + dim() : i]; }
+    bool is_contiguous() const;
+    // View as [rows, last] with one row stride (throws if the leading dims do not collapse).
+    void rows_view(int64_t& rows, int64_t& cols, int64_t& ld) const;
+};
+
+// Tensor with its own storage.
+struct OwnedTensor
+{
+    DeviceBuffer buf;
+    Tensor t;
+    static OwnedTensor empty(DType dt, std::vector<int64_t> shape);
+};
+
+namespace ffi {
+
+// src/ffi.rs:293-296: y = RMSNorm(x) over the last dim; w may be null.
+void rms_norm(const Tensor& x, const Tensor* w, const Tensor& y, float eps, float constant_bias,
+              float constant_scale, const Stream& s);
+// src/ffi.rs:464-468: r += x (in place, rounded to r's dtype), y = RMSNorm(r).
+void rms_norm_res_in(const Tensor& x, const Tensor* w, const Tensor& y, const Tensor& r, float eps, float bias,
+                     float scale, const Stream& s);
+// src/ffi.rs:492-499: z = act(x) * y; act_limit 0 disables clamping.
+void silu_mul(const Tensor& x, const Tensor& y, const Tensor& z, float act_limit, const Stream& s);
+void gelu_mul(const Tensor& x, const Tensor& y, const Tensor& z, float act_limit, const Stream& s);
+// src/ffi.rs:298-333: fused (optional) q/k head RMSNorm + RoPE on (bsz, seq, heads, head_dim)
+// tensors; positions (int32 [bsz]) or position_ids (int32 [bsz, seq]) override position.
+void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
+          int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
+          float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s,
+          const Tensor* position_ids = nullptr);
+// Embedding gather: out[i] = table[ids[i]] (bit-exact, or exact upcast to f32); err_flag optional.
+void embedding(const Tensor& table, const Tensor& ids, const Tensor& out, int32_t* err_flag, const Stream& s);
+// Gather fused with the following RMSNorm; h optional.
+void embedding_rms_norm(const Tensor& table, const Tensor& ids, const Tensor* h, const Tensor* w, const Tensor& y,
+                        float eps, float constant_bias, float constant_scale, int32_t* err_flag, const Stream& s);
+
+}  // namespace ffi
+
+// src/modules.rs:342-412.
+class RmsNorm
+{
+public:
+    RmsNorm(Tensor weight, float eps, float constant_bias = 0.0f, float constant_scale = 1.0f)
+        : weight_(std::move(weight)), eps_(eps), constant_bias_(constant_bias), constant_scale_(constant_scale) {}
+    // y = norm(x) in f16 (every call site in the Qwen3 tree), same shape as x.
+    OwnedTensor forward(const Tensor& x, const Stream& s) const;
+    // Pre-norm residual add fused with the norm: r += add (in place), returns norm(r) in f16.
+    // add == nullptr: plain forward(r).
+    OwnedTensor forward_res(const Tensor& r, const Tensor* add, const Stream& s) const;
+    const Tensor& weight() const { return weight_; }
+
+private:
+    Tensor weight_;
+    float eps_, constant_bias_, constant_scale_;
+};
+
+// src/modules.rs:418-437: f32 rows out of an f16/bf16 table (the residual stream is f32).
+class Embedding
+{
+public:
+    explicit Embedding(Tensor weight, DType out_kind = DType::F32) : weight_(std::move(weight)), out_kind_(out_kind) {}
+    // ids: [b, s] int64 -> [b, s, hidden] of out_kind.
+    OwnedTensor forward(const Tensor& ids, const Stream& s) const;
+
+private:
+    Tensor weight_;
+    DType out_kind_;
+};
+
+// The activation step of src/modules.rs:932-940 (gate/up/down Linear layers are outside this path).
+struct GatedMlp
+{
+    enum class Act { Silu, Gelu };
+    // a = act(g) * u, same shape and dtype as g.
+    static OwnedTensor activate(const Tensor& g, const Tensor& u, Act act, float act_limit, const Stream& s);
+};
+
+// src/rope.rs:33-86, 233-292, 309-317: inv_freq producer (default and linear scaling) and the
+// in-place apply / apply_one.
+class RoPE
+{
+public:
+    // inv_freq[i] = 1 / exp((2i / rotary_dim) * ln(theta)) in fp32 (rope.rs:39-42, 82-86, 309-317),
+    // divided by `linear_factor` for rope_type "linear" (rope.rs:55-59).
+    RoPE(double theta, int rotary_dim, RopeStyle style, double attn_factor = 1.0, double linear_factor = 1.0);
+    static std::vector<float> default_inv_freq(double theta, int rotary_dim, double linear_factor = 1.0);
+    void apply(const Tensor& q, const Tensor& k, int64_t position, const Tensor* positions, const Tensor* q_norm,
+               const Tensor* k_norm, float norm_eps, float norm_constant_bias, const Stream& s) const;
+    void apply_one(const Tensor& x, int64_t position, const Tensor* positions, const Tensor* norm, float norm_eps,
+                   float norm_constant_bias, const Stream& s) const;
+    const std::vector<float>& inv_freq_host() const { return inv_freq_host_; }
+    int rotary_dim() const { return rotary_dim_; }
+
+private:
+    std::vector<float> inv_freq_host_;
+    DeviceBuffer inv_freq_;
+    Tensor inv_freq_t_;
+    int rotary_dim_;
+    RopeStyle style_;
+    float attn_factor_;
+};
+
+}  // namespace exl3r

@@ -1,0 +1,195 @@
+// GPU checks of the C++ host layer: each module (RmsNorm, Embedding, GatedMlp, RoPE) runs through
+// the C ABI on a HIP stream and is compared with the CPU oracle on the same bits.
+#include "exl3r.hpp"
+#include "rowops_oracle.h"
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+using namespace exl3r;
+
+static int failures = 0;
+static uint64_t rng_state = 0x9e3779b97f4a7c15ull;
+
+static uint64_t splitmix()
+{
+    uint64_t z = (rng_state += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+static float normal(float mean, float std)
+{
+    const double u1 = ((splitmix() >> 11) + 1) * 0x1.0p-53, u2 = (splitmix() >> 11) * 0x1.0p-53;
+    return (float)(mean + std * std::sqrt(-2.0 * std::log(u1)) * std::cos(2.0 * M_PI * u2));
+}
+
+// Host storage of n elements of dtype dt with N(mean, std) values rounded to dt.
+static std::vector<uint8_t> host_normal(DType dt, size_t n, float mean, float std)
+{
+    std::vector<uint8_t> b(n * dtype_size(dt));
+    for (size_t i = 0; i < n; ++i)
+    {
+        const float v = normal(mean, std);
+        if (dt == DType::F32) std::memcpy(&b[i * 4], &v, 4);
+        else
+        {
+            const uint16_t h = dt == DType::F16 ? oracle_f32_to_f16(v) : oracle_f32_to_bf16(v);
+            std::memcpy(&b[i * 2], &h, 2);
+        }
+    }
+    return b;
+}
+
+static OwnedTensor upload(const std::vector<uint8_t>& h, DType dt, std::vector<int64_t> shape, const Stream& s)
+{
+    OwnedTensor t = OwnedTensor::empty(dt, shape);
+    t.buf.upload(h.data(), h.size(), s);
+    return t;
+}
+
+static std::vector<uint8_t> download(const OwnedTensor& t, const Stream& s)
+{
+    std::vector<uint8_t> h(t.buf.bytes());
+    t.buf.download(h.data(), h.size(), s);
+    return h;
+}
+
+static int64_t ordered16(uint16_t b) { return (b & 0x8000) ? -(int64_t)(b & 0x7fff) : (int64_t)b; }
+
+// Max ulp distance of two 16-bit storage arrays.
+static int64_t max_ulp16(const std::vector<uint8_t>& a, const std::vector<uint8_t>& b)
+{
+    int64_t worst = 0;
+    for (size_t i = 0; i + 1 < a.size(); i += 2)
+    {
+        uint16_t x, y;
+        std::memcpy(&x, &a[i], 2);
+        std::memcpy(&y, &b[i], 2);
+        const int64_t d = std::llabs(ordered16(x) - ordered16(y));
+        worst = d > worst ? d : worst;
+    }
+    return worst;
+}
+
+static void report(const char* what, bool ok, const char* detail)
+{
+    std::printf("%s %s: %s\n", ok ? "ok  " : "FAIL", what, detail);
+    if (!ok) ++failures;
+}
+
+int main()
+{
+    Stream s = Stream::create();
+    char msg[256];
+
+    // RmsNorm::forward on a 3-D f16 tensor (rows collapse to 21 x 512), f16 weight.
+    {
+        auto xh = host_normal(DType::F16, 3 * 7 * 512, 0.f, 1.f);
+        auto wh = host_normal(DType::F16, 512, 1.f, 0.1f);
+        auto x = upload(xh, DType::F16, { 3, 7, 512 }, s);
+        auto w = upload(wh, DType::F16, { 512 }, s);
+        RmsNorm norm(w.t, 1e-6f);
+        auto y = norm.forward(x.t, s);
+        auto yh = download(y, s);
+        std::vector<uint8_t> ey(yh.size());
+        oracle_rms_norm(xh.data(), OR_F16, 512, wh.data(), OR_F16, ey.data(), OR_F16, 512, nullptr, OR_F32, 512, 21, 512,
+                        1e-6f, 0.f, 1.f, 1);
+        const int64_t u = max_ulp16(yh, ey);
+        std::snprintf(msg, sizeof msg, "max ulp %lld", (long long)u);
+        report("RmsNorm::forward f16 [3,7,512]", u <= 1, msg);
+    }
+    // RmsNorm::forward_res: f32 residual stream + f16 sublayer output (the Qwen3 path, norm.cu:403).
+    {
+        auto rh = host_normal(DType::F32, 8 * 1024, 0.f, 4.f);
+        auto ah = host_normal(DType::F16, 8 * 1024, 0.f, 1.f);
+        auto wh = host_normal(DType::F16, 1024, 1.f, 0.1f);
+        auto r = upload(rh, DType::F32, { 1, 8, 1024 }, s);
+        auto add = upload(ah, DType::F16, { 1, 8, 1024 }, s);
+        auto w = upload(wh, DType::F16, { 1024 }, s);
+        RmsNorm norm(w.t, 1e-6f, 1.0f);
+        auto y = norm.forward_res(r.t, &add.t, s);
+        auto yh = download(y, s), rh2 = download(r, s);
+        std::vector<uint8_t> ey(yh.size()), er = rh;
+        oracle_rms_norm(ah.data(), OR_F16, 1024, wh.data(), OR_F16, ey.data(), OR_F16, 1024, er.data(), OR_F32, 1024, 8,
+                        1024, 1e-6f, 1.0f, 1.f, 1);
+        const int64_t u = max_ulp16(yh, ey);
+        const bool r_ok = std::memcmp(rh2.data(), er.data(), er.size()) == 0;
+        std::snprintf(msg, sizeof msg, "y max ulp %lld, residual bit-exact %s", (long long)u, r_ok ? "yes" : "no");
+        report("RmsNorm::forward_res f32 residual", u <= 1 && r_ok, msg);
+    }
+    // Embedding::forward: bf16 table -> f32 rows (exact upcast), ids [2, 5] int64.
+    {
+        auto th = host_normal(DType::BF16, 100 * 64, 0.f, 0.02f);
+        std::vector<int64_t> ids = { 3, 99, 0, 3, 50, 1, 2, 97, 42, 7 };
+        auto table = upload(th, DType::BF16, { 100, 64 }, s);
+        OwnedTensor idt = OwnedTensor::empty(DType::I64, { 2, 5 });
+        idt.buf.upload(ids.data(), ids.size() * 8, s);
+        Embedding emb(table.t);
+        auto out = emb.forward(idt.t, s);
+        auto oh = download(out, s);
+        std::vector<uint8_t> eo(oh.size());
+        int32_t err = 0;
+        oracle_embedding(th.data(), OR_BF16, 100, 64, 64, ids.data(), OR_I64, 10, eo.data(), OR_F32, 64, &err, 1);
+        const bool ok = out.t.shape == std::vector<int64_t>({ 2, 5, 64 }) && std::memcmp(oh.data(), eo.data(), eo.size()) == 0;
+        report("Embedding::forward bf16 -> f32", ok, ok ? "bit-exact" : "mismatch");
+    }
+    // GatedMlp::activate (SiLU and GELU), bf16 [16, 256].
+    for (int act = 0; act < 2; ++act)
+    {
+        auto gh = host_normal(DType::BF16, 16 * 256, 0.f, 2.f);
+        auto uh = host_normal(DType::BF16, 16 * 256, 0.f, 1.f);
+        auto g = upload(gh, DType::BF16, { 16, 256 }, s);
+        auto u = upload(uh, DType::BF16, { 16, 256 }, s);
+        auto a = GatedMlp::activate(g.t, u.t, act ? GatedMlp::Act::Gelu : GatedMlp::Act::Silu, 0.f, s);
+        auto ah = download(a, s);
+        std::vector<uint8_t> ea(ah.size());
+        oracle_act_mul(act ? OR_ACT_GELU : OR_ACT_SILU, gh.data(), uh.data(), OR_BF16, ea.data(), OR_BF16, 16, 256, 256,
+                       256, 256, 0.f, 1);
+        const int64_t d = max_ulp16(ah, ea);
+        std::snprintf(msg, sizeof msg, "max ulp %lld", (long long)d);
+        report(act ? "GatedMlp::activate gelu" : "GatedMlp::activate silu", d <= 1, msg);
+    }
+    // RoPE::apply (NeoX, f16 heads, f16 head-norm weights, per-sequence positions) and apply_one.
+    {
+        const int bsz = 2, seq = 3, hq = 4, hk = 2, hd = 64;
+        auto qh = host_normal(DType::F16, bsz * seq * hq * hd, 0.f, 1.f);
+        auto kh = host_normal(DType::F16, bsz * seq * hk * hd, 0.f, 1.f);
+        auto qnh = host_normal(DType::F16, hd, 1.f, 0.1f), knh = host_normal(DType::F16, hd, 1.f, 0.1f);
+        std::vector<int32_t> pos = { 17, 30000 };
+        auto q = upload(qh, DType::F16, { bsz, seq, hq, hd }, s);
+        auto k = upload(kh, DType::F16, { bsz, seq, hk, hd }, s);
+        auto qn = upload(qnh, DType::F16, { hd }, s), kn = upload(knh, DType::F16, { hd }, s);
+        OwnedTensor pd = OwnedTensor::empty(DType::I32, { bsz });
+        pd.buf.upload(pos.data(), pos.size() * 4, s);
+        RoPE rope(1e6, hd, RopeStyle::NeoX);
+        rope.apply(q.t, k.t, 0, &pd.t, &qn.t, &kn.t, 1e-6f, 0.f, s);
+        auto qo = download(q, s), ko = download(k, s);
+        std::vector<uint8_t> eq(qh.size()), ek(kh.size());
+        oracle_rope(qh.data(), eq.data(), hq * hd, hd, hq, kh.data(), ek.data(), hk * hd, hd, hk, OR_F16, bsz, seq, hd,
+                    rope.inv_freq_host().data(), hd, 0, pos.data(), nullptr, qnh.data(), knh.data(), OR_F16, 1e-6f, 0.f,
+                    OR_ROPE_NEOX, 1.f, 1);
+        const int64_t dq = max_ulp16(qo, eq), dk = max_ulp16(ko, ek);
+        std::snprintf(msg, sizeof msg, "q max ulp %lld, k max ulp %lld", (long long)dq, (long long)dk);
+        report("RoPE::apply neox f16 + head norm", dq <= 2 && dk <= 2, msg);
+
+        auto xh = host_normal(DType::F16, seq * hq * hd, 0.f, 1.f);
+        auto x = upload(xh, DType::F16, { 1, seq, hq, hd }, s);
+        RoPE gptj(1e4, 32, RopeStyle::GptJ);
+        gptj.apply_one(x.t, 5, nullptr, nullptr, 1e-6f, 0.f, s);
+        auto xo = download(x, s);
+        std::vector<uint8_t> ex(xh.size());
+        oracle_rope(xh.data(), ex.data(), hq * hd, hd, hq, nullptr, nullptr, 0, 0, 0, OR_F16, 1, seq, hd,
+                    gptj.inv_freq_host().data(), 32, 5, nullptr, nullptr, nullptr, nullptr, OR_F16, 1e-6f, 0.f,
+                    OR_ROPE_GPTJ, 1.f, 1);
+        const int64_t dx = max_ulp16(xo, ex);
+        std::snprintf(msg, sizeof msg, "max ulp %lld", (long long)dx);
+        report("RoPE::apply_one gptj partial rotary", dx <= 2, msg);
+    }
+    std::printf(failures ? "test_host_gpu: %d failures\n" : "test_host_gpu: all passed\n", failures);
+    return failures ? 1 : 0;
+}
