@@ -31,7 +31,7 @@ sys.path.insert(0, os.path.join(ROOT, "exllamav3-rs_amd"))
 PEAK_GBS = 8000.0            # MI355X HBM3E
 METRIC = "fused norm/act/RoPE/embed HBM GB/s + % of MI355X peak; decode-step us"
 OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "gather_norm_c5", "rms_c1",
-       "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "calib_copy"]
+       "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "calib_copy", "calib_copy_cached"]
 
 
 def log(*a):
@@ -138,7 +138,8 @@ def make_rope(name, pos, hq, hk, hd, R, mode, dt, seed, bsz=1, per_seq=False):
     T = pos.size if not per_seq else bsz
     seq = T if not per_seq else 1
     b = 1 if not per_seq else bsz
-    nbytes = 2 * T * (hq + hk) * hd * 2 + 4 * T + 2 * hd * 2
+    # q/k read + written, one int32 position per token, both norm weights, inv_freq.
+    nbytes = 2 * T * (hq + hk) * hd * 2 + 4 * T + 2 * hd * 2 + (R // 2) * 4
     sets = sets_for(nbytes)
     inv = torch.from_numpy((1.0 / 1e6 ** (np.arange(0, R, 2, dtype=np.float64) / R)).astype(np.float32)).cuda()
     qn, kn = gen((hd,), 1.0, 0.1, dt, seed + 50), gen((hd,), 1.0, 0.1, dt, seed + 51)
@@ -184,18 +185,19 @@ def make_gather(name, vocab, hidden, n, dt, out_dt, ids, seed, norm=False):
     return Work(name, nbytes, launch, desc, sets)
 
 
-def make_copy(name):
+def make_copy(name, cached=False):
     import torch
     import exl3r
     nb = 1 << 30
     src = torch.empty(nb, dtype=torch.uint8, device="cuda")
     dst = torch.empty(nb, dtype=torch.uint8, device="cuda")
     naive = exl3r.load_naive()
+    fn = naive.calib_copy_cached if cached else naive.calib_copy
 
     def launch(i):
-        rc = naive.calib_copy(src.data_ptr(), dst.data_ptr(), nb, torch.cuda.current_stream().cuda_stream)
+        rc = fn(src.data_ptr(), dst.data_ptr(), nb, torch.cuda.current_stream().cuda_stream)
         assert rc == 0
-    return Work(name, 2 * nb, launch, "plain copy 1 GiB (counter calibration)")
+    return Work(name, 2 * nb, launch, f"{'cached' if cached else 'non-temporal'} copy 1 GiB (counter calibration)")
 
 
 def make_decode(fused, seed=7):
@@ -204,7 +206,6 @@ def make_decode(fused, seed=7):
     import numpy as np
     import torch
     import exl3r
-    import exl3r.ffi as ffi
     T, H, I, hq, hk, hd = 64, 5120, 17408, 64, 8, 128
     f16 = torch.float16
     resid = gen((T, H), 0.0, 4.0, f16, seed)
@@ -219,17 +220,28 @@ def make_decode(fused, seed=7):
     inv = torch.from_numpy((1.0 / 1e6 ** (np.arange(0, hd, 2, dtype=np.float64) / hd)).astype(np.float32)).cuda()
     gate, up = gen((T, I), 0.0, 1.0, f16, seed + 9), gen((T, I), 0.0, 1.0, f16, seed + 10)
     act = torch.empty((T, I), device="cuda", dtype=f16)
-    nbytes = 2 * (4 * T * H * 2 + H * 2) + (2 * T * (hq + hk) * hd * 2 + 4 * T) + 3 * T * I * 2
+    nbytes = 2 * (4 * T * H * 2 + H * 2) + (2 * T * (hq + hk) * hd * 2 + 4 * T + 2 * hd * 2 + hd * 2) + 3 * T * I * 2
+    P = lambda t: t.data_ptr()
     if fused:
+        # Both variants call their C ABI directly with pre-bound arguments (as a compiled caller
+        # would), so the eager timing compares launches, not Python wrapper overhead.
+        lib = exl3r.load()
+        F16 = exl3r.F16
+
         def launch(i):
-            ffi.rms_norm_res_in(a_out, w1, y, resid, 1e-6)
-            ffi.rope(q, q, k, k, inv, 0, pos, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0)
-            ffi.rms_norm_res_in(m_out, w2, y, resid, 1e-6)
-            ffi.silu_mul(gate, up, act)
+            s = torch.cuda.current_stream().cuda_stream
+            rc = lib.exl3r_rms_norm_res_in(P(a_out), F16, H, P(w1), F16, P(y), F16, H, P(resid), F16, H,
+                                           T, H, 1e-6, 0.0, 1.0, s)
+            rc |= lib.exl3r_rope(P(q), P(q), hq * hd, hd, hq, P(k), P(k), hk * hd, hd, hk, F16, T, 1, hd,
+                                 P(inv), hd, 0, P(pos), None, P(qn), P(kn), F16, 1e-6, 0.0,
+                                 exl3r.ROPE_NEOX, 1.0, s)
+            rc |= lib.exl3r_rms_norm_res_in(P(m_out), F16, H, P(w2), F16, P(y), F16, H, P(resid), F16, H,
+                                            T, H, 1e-6, 0.0, 1.0, s)
+            rc |= lib.exl3r_silu_mul(P(gate), P(up), F16, P(act), F16, T, I, I, I, I, 0.0, s)
+            assert rc == 0
         return Work("decode_fused", nbytes, launch, "decode layer T=64 fused (4 launches)")
     naive = exl3r.load_naive()
     tmp = torch.empty((T, I), device="cuda", dtype=f16)
-    P = lambda t: t.data_ptr()
 
     def launch(i):
         s = torch.cuda.current_stream().cuda_stream
@@ -269,8 +281,9 @@ def make_all(only=None):
         "decode_fused": lambda: make_decode(True),
         "decode_naive": lambda: make_decode(False),
         "calib_copy": lambda: make_copy("calib_copy"),
+        "calib_copy_cached": lambda: make_copy("calib_copy_cached", cached=True),
     }
-    names = [only] if only else [n for n in OPS if n != "rms_c2"]
+    names = [only] if only else [n for n in OPS if n not in ("rms_c2", "calib_copy_cached")]
     return {n: builders[n]() for n in names}
 
 

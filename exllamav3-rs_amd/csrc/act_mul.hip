@@ -170,15 +170,15 @@ static int act_mul_entry(const char* op, const void* x, const void* y, int it, v
                          int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz,
                          float limit, void* stream)
 {
-    if (!x || !y || !z) return set_error(EXL3R_EINVAL, "%s: x, y and z must be non-null", op);
     if (rows < 0 || cols < 0) return set_error(EXL3R_EINVAL, "%s: invalid shape rows=%lld cols=%lld", op, (long long)rows, (long long)cols);
     if (rows > 1 && (ldx < cols || ldy < cols || ldz < cols))
         return set_error(EXL3R_EINVAL, "%s: row strides must be >= cols", op);
     if (!is_float_dtype(it) || !is_float_dtype(ot))
         return set_error(EXL3R_EDTYPE, "%s: unsupported dtypes in=%s z=%s", op, dtype_name(it), dtype_name(ot));
+    if (rows == 0 || cols == 0) return EXL3R_OK;
+    if (!x || !y || !z) return set_error(EXL3R_EINVAL, "%s: x, y and z must be non-null", op);
     if ((z == x && (ot != it || ldz != ldx)) || (z == y && (ot != it || ldz != ldy)))
         return set_error(EXL3R_EINVAL, "%s: in-place z needs the aliased operand's dtype and stride", op);
-    if (rows == 0 || cols == 0) return EXL3R_OK;
 
     ActArgs a{ x, y, z, ldx, ldy, ldz, rows, cols, limit };
     if (rows == 1 || (ldx == cols && ldy == cols && ldz == cols))

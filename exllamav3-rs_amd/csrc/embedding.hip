@@ -100,7 +100,7 @@ static bool exact_conversion(int from, int to) { return from == to || to == EXL3
 static int check_gather(const char* op, const void* table, int tt, int64_t vocab, int64_t hidden, int64_t ldt,
                         const void* ids, int idt, int64_t n)
 {
-    if (!table || !ids) return set_error(EXL3R_EINVAL, "%s: table and ids must be non-null", op);
+    if (!table || (n > 0 && !ids)) return set_error(EXL3R_EINVAL, "%s: table and ids must be non-null", op);
     if (vocab <= 0 || hidden <= 0 || hidden > (int64_t)1 << 30 || n < 0 || ldt < hidden)
         return set_error(EXL3R_EINVAL, "%s: invalid shape vocab=%lld hidden=%lld n=%lld ldt=%lld", op, (long long)vocab,
                          (long long)hidden, (long long)n, (long long)ldt);
@@ -120,7 +120,7 @@ extern "C" int exl3r_embedding(const void* table, int tt, int64_t vocab, int64_t
     const char* op = "exl3r_embedding";
     int rc = check_gather(op, table, tt, vocab, hidden, ldt, ids, idt, n);
     if (rc) return rc;
-    if (!out) return set_error(EXL3R_EINVAL, "%s: out must be non-null", op);
+    if (n > 0 && !out) return set_error(EXL3R_EINVAL, "%s: out must be non-null", op);
     if (ldo < hidden) return set_error(EXL3R_EINVAL, "%s: out row stride %lld < hidden %lld", op, (long long)ldo, (long long)hidden);
     if (!is_float_dtype(ot) || !exact_conversion(tt, ot))
         return set_error(EXL3R_EDTYPE, "%s: out dtype %s is not an exact copy of table dtype %s", op, dtype_name(ot), dtype_name(tt));
@@ -166,7 +166,7 @@ extern "C" int exl3r_embedding_rms_norm(const void* table, int tt, int64_t vocab
     if (rc) return rc;
     if (h && (ldh < hidden || !is_float_dtype(ht) || !exact_conversion(tt, ht)))
         return set_error(EXL3R_EINVAL, "%s: h must be an exact copy of the table dtype (or f32) with stride >= hidden", op);
-    if (h && h == y) return set_error(EXL3R_EINVAL, "%s: h must not alias y", op);
+    if (n > 0 && h && h == y) return set_error(EXL3R_EINVAL, "%s: h must not alias y", op);
     if (n == 0) return EXL3R_OK;
 
     RmsArgs a{};

@@ -24,6 +24,8 @@ EXL3R_API int naive_mul_f16(const void* a, const void* b, void* z, int64_t n, vo
 /* Non-temporal 16-byte-per-lane copy of nbytes (multiple of 16): bandwidth reference and rocprof
  * counter calibration. */
 EXL3R_API int calib_copy(const void* src, void* dst, int64_t nbytes, void* stream);
+/* The same copy with ordinary (cached) loads and stores. */
+EXL3R_API int calib_copy_cached(const void* src, void* dst, int64_t nbytes, void* stream);
 #ifdef __cplusplus
 }
 #endif

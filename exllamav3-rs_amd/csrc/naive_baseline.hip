@@ -87,6 +87,14 @@ __global__ __launch_bounds__(128) void k_calib_copy(const u32x4* src, u32x4* dst
     if (i < n16) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
+// Same copy with ordinary (cached) loads and stores: calibrates counters for kernels whose loads are
+// cached (the embedding table rows).
+__global__ __launch_bounds__(128) void k_calib_copy_cached(const u32x4* src, u32x4* dst, int64_t n16)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n16) dst[i] = src[i];
+}
+
 static unsigned blocks_for(int64_t n, int threads)
 {
     int64_t b = (n + threads - 1) / threads;
@@ -139,5 +147,14 @@ extern "C" int calib_copy(const void* src, void* dst, int64_t nbytes, void* stre
     const int64_t n16 = nbytes / 16;
     if (n16 > ((int64_t)1 << 37)) return -1;
     k_calib_copy<<<(unsigned)((n16 + 127) / 128), 128, 0, (hipStream_t)stream>>>((const u32x4*)src, (u32x4*)dst, n16);
+    return (int)hipGetLastError();
+}
+
+extern "C" int calib_copy_cached(const void* src, void* dst, int64_t nbytes, void* stream)
+{
+    if (nbytes % 16) return -1;
+    const int64_t n16 = nbytes / 16;
+    if (n16 > ((int64_t)1 << 37)) return -1;
+    k_calib_copy_cached<<<(unsigned)((n16 + 127) / 128), 128, 0, (hipStream_t)stream>>>((const u32x4*)src, (u32x4*)dst, n16);
     return (int)hipGetLastError();
 }

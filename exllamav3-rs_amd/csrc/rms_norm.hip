@@ -8,7 +8,7 @@ namespace exl3r {
 int check_rms_common(const char* op, const void* x, int xt, int64_t ldx, const void* w, int wt,
                      const void* y, int yt, int64_t ldy, int64_t rows, int64_t dim)
 {
-    if (!x || !y) return set_error(EXL3R_EINVAL, "%s: x and y must be non-null", op);
+    if (rows > 0 && (!x || !y)) return set_error(EXL3R_EINVAL, "%s: x and y must be non-null", op);
     if (rows < 0 || dim <= 0 || dim > (int64_t)1 << 30)
         return set_error(EXL3R_EINVAL, "%s: invalid shape rows=%lld dim=%lld", op, (long long)rows, (long long)dim);
     if (ldx < dim || ldy < dim)
@@ -17,7 +17,7 @@ int check_rms_common(const char* op, const void* x, int xt, int64_t ldx, const v
     if (!is_float_dtype(xt) || !is_float_dtype(yt) || (w && !is_float_dtype(wt)))
         return set_error(EXL3R_EDTYPE, "%s: unsupported dtypes x=%s y=%s w=%s", op, dtype_name(xt),
                          dtype_name(yt), w ? dtype_name(wt) : "none");
-    if (x == y && (xt != yt || ldx != ldy))
+    if (rows > 0 && x == y && (xt != yt || ldx != ldy))
         return set_error(EXL3R_EINVAL, "%s: in-place y == x needs equal dtypes and strides", op);
     return EXL3R_OK;
 }

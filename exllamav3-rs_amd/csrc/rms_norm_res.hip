@@ -13,12 +13,12 @@ extern "C" int exl3r_rms_norm_res_in(const void* x, int xt, int64_t ldx, const v
     const char* op = "exl3r_rms_norm_res_in";
     int rc = check_rms_common(op, x, xt, ldx, w, wt, y, yt, ldy, rows, dim);
     if (rc) return rc;
-    if (!r) return set_error(EXL3R_EINVAL, "%s: residual r must be non-null", op);
     if (!is_float_dtype(rt)) return set_error(EXL3R_EDTYPE, "%s: unsupported residual dtype %s", op, dtype_name(rt));
     if (ldr < dim) return set_error(EXL3R_EINVAL, "%s: residual row stride %lld < dim %lld", op, (long long)ldr, (long long)dim);
+    if (rows == 0) return EXL3R_OK;
+    if (!r) return set_error(EXL3R_EINVAL, "%s: residual r must be non-null", op);
     if (r == y) return set_error(EXL3R_EINVAL, "%s: y must not alias the residual", op);
     if (x == r && (xt != rt || ldx != ldr)) return set_error(EXL3R_EINVAL, "%s: x == r needs equal dtypes and strides", op);
-    if (rows == 0) return EXL3R_OK;
 
     RmsArgs a{};
     a.x = x; a.ldx = ldx; a.w = w; a.wt = wt; a.y = y; a.ldy = ldy; a.r = r; a.ldr = ldr;

@@ -370,7 +370,7 @@ extern "C" int exl3r_rope(const void* q, void* out_q, int64_t q_tok_stride, int6
                           void* stream)
 {
     const char* op = "exl3r_rope";
-    if (!q || !out_q || !inv_freq) return set_error(EXL3R_EINVAL, "%s: q, out_q and inv_freq must be non-null", op);
+    if (!inv_freq) return set_error(EXL3R_EINVAL, "%s: inv_freq must be non-null", op);
     if (dtype != EXL3R_F16 && dtype != EXL3R_BF16)
         return set_error(EXL3R_EDTYPE, "%s: q/k dtype must be f16 or bf16, got %s", op, dtype_name(dtype));
     if (rope_mode != EXL3R_ROPE_GPTJ && rope_mode != EXL3R_ROPE_NEOX)
@@ -384,7 +384,7 @@ extern "C" int exl3r_rope(const void* q, void* out_q, int64_t q_tok_stride, int6
         return set_error(EXL3R_EINVAL, "%s: rotary_dim %d must be even and in [2, head_dim]", op, rotary_dim);
     if (q_head_stride < head_dim || q_tok_stride < (int64_t)num_heads_q * q_head_stride)
         return set_error(EXL3R_EINVAL, "%s: q strides (%lld, %lld) overlap heads", op, (long long)q_tok_stride, (long long)q_head_stride);
-    if (k && (!out_k || k_head_stride < head_dim || k_tok_stride < (int64_t)num_heads_k * k_head_stride))
+    if (k && ((bsz * seq_len > 0 && !out_k) || k_head_stride < head_dim || k_tok_stride < (int64_t)num_heads_k * k_head_stride))
         return set_error(EXL3R_EINVAL, "%s: k needs out_k and non-overlapping strides", op);
     if (positions && position_ids) return set_error(EXL3R_EINVAL, "%s: at most one of positions / position_ids", op);
     if (q_norm && k && !k_norm) return set_error(EXL3R_EINVAL, "%s: q_norm given without k_norm", op);
@@ -393,6 +393,7 @@ extern "C" int exl3r_rope(const void* q, void* out_q, int64_t q_tok_stride, int6
         return set_error(EXL3R_EDTYPE, "%s: unsupported norm weight dtype %s", op, dtype_name(norm_dtype));
     const int64_t tokens = bsz * seq_len;
     if (tokens == 0) return EXL3R_OK;
+    if (!q || !out_q) return set_error(EXL3R_EINVAL, "%s: q and out_q must be non-null", op);
     if (tokens > 0x7fffffff) return set_error(EXL3R_EINVAL, "%s: too many tokens", op);
 
     RopeArgs a{};

@@ -47,6 +47,7 @@ NAIVE_PROTOTYPES = {
     "naive_silu_f16": (_i, [_vp, _vp, _i64, _vp]),
     "naive_mul_f16": (_i, [_vp, _vp, _vp, _i64, _vp]),
     "calib_copy": (_i, [_vp, _vp, _i64, _vp]),
+    "calib_copy_cached": (_i, [_vp, _vp, _i64, _vp]),
 }
 
 _lib = None

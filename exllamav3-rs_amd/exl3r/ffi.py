@@ -110,6 +110,8 @@ def rope(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm
             raise ValueError("k is incorrect shape")
         if k.stride(3) != 1 or out_k is None or out_k.stride() != k.stride():
             raise ValueError("k innermost dim must be dense and out_k must share k's layout")
+        if seq > 1 and k.stride(0) != seq * k.stride(1) and bsz > 1:
+            raise ValueError("k batch stride must be seq_len * token stride")
         hk, k_ts, k_hs = k.shape[2], k.stride(1), k.stride(2)
     for t in (positions, position_ids):
         if t is not None and t.dtype != torch.int32:

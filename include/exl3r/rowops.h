@@ -16,7 +16,9 @@
  *     device-resident position/id buffers are read by the kernels, so a captured graph can be
  *     replayed after their contents change);
  *   - arguments are validated before any HIP call, so validation errors are reported even on a
- *     machine without a GPU.
+ *     machine without a GPU;
+ *   - a call with no rows / tokens / ids validates its shapes and dtypes and returns EXL3R_OK
+ *     without launching; its data pointers may then be NULL (empty tensors carry none).
  *
  * Reference entry points replaced (apiplant/exllamav3-rs, cited file:line):
  *   exl3r_rms_norm          <- exl3_shim_rms_norm         csrc/exl3_shim.cpp:76-80   (ffi.rs:43-50, 293-296)

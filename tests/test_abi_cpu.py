@@ -122,3 +122,21 @@ def test_errors_are_thread_local():
     t.start()
     t.join()
     assert seen == [""] and "non-null" in _err()
+
+
+def test_zero_size_calls_accept_null_data():
+    """Empty tensors carry null data pointers: a call with no rows / tokens / ids validates its
+    shapes and dtypes, launches nothing and succeeds (no GPU needed)."""
+    lib = exl3r.load()
+    assert lib.exl3r_rms_norm(None, F16, 64, None, F16, None, F16, 64, 0, 64, 1e-6, 0.0, 1.0, None) == exl3r.OK
+    assert lib.exl3r_rms_norm(None, 9, 64, None, F16, None, F16, 64, 0, 64, 1e-6, 0.0, 1.0, None) == exl3r.EDTYPE
+    assert lib.exl3r_rms_norm_res_in(None, F16, 64, None, F16, None, F16, 64, None, F32, 64, 0, 64,
+                                     1e-6, 0.0, 1.0, None) == exl3r.OK
+    for fn in (lib.exl3r_silu_mul, lib.exl3r_gelu_mul):
+        assert fn(None, None, BF16, None, BF16, 0, 17408, 17408, 17408, 17408, 0.0, None) == exl3r.OK
+        assert fn(None, None, I32, None, BF16, 0, 8, 8, 8, 8, 0.0, None) == exl3r.EDTYPE
+    assert _rope(q=None, oq=None, k=None, ok=None, seq=0) == exl3r.OK
+    assert _rope(q=None, oq=None, k=None, ok=None, seq=0, mode=0) == exl3r.EINVAL
+    assert lib.exl3r_embedding(FAKE, BF16, 10, 16, 16, None, I64, 0, None, F32, 16, None, None) == exl3r.OK
+    assert lib.exl3r_embedding_rms_norm(FAKE, BF16, 10, 16, 16, None, I64, 0, None, BF16, 16, None, BF16,
+                                        None, BF16, 16, 1e-6, 0.0, 1.0, None, None) == exl3r.OK

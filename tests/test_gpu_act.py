@@ -83,3 +83,10 @@ def test_in_place_and_specials():
         exp2 = orc.act_mul(code, from_dev(xh), from_dev(y.half()), F16, F16)
         fn(xh, y.half(), xh)                                # z == x in place
         assert_close_ulp(from_dev(xh), exp2, F16, 0, rel=0.0, what=f"{act} in place")
+
+
+def test_zero_rows():
+    x = torch.empty((0, 17408), device="cuda", dtype=torch.bfloat16)
+    ffi.silu_mul(x, x, torch.empty_like(x))
+    ffi.gelu_mul(x, x, torch.empty_like(x))
+    torch.cuda.synchronize()

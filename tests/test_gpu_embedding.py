@@ -106,3 +106,12 @@ def test_fused_variants(tt, ht, yt, wt):
 def test_fused_bad_ids_and_generic():
     run_fused(4, 64, 256, BF16, BF16, BF16, BF16, seed=9, ids=np.array([1, -5, 64, 2], np.int64))
     run_fused(6, 64, 100, F16, F16, F16, F16, seed=10)
+
+
+def test_zero_ids():
+    table = torch.zeros((16, 64), device="cuda", dtype=torch.bfloat16)
+    ids = torch.empty(0, device="cuda", dtype=torch.int64)
+    ffi.embedding(table, ids, torch.empty((0, 64), device="cuda", dtype=torch.float32))
+    y = torch.empty((0, 64), device="cuda", dtype=torch.bfloat16)
+    ffi.embedding_rms_norm(table, ids, None, None, y, 1e-6)
+    torch.cuda.synchronize()

@@ -124,3 +124,11 @@ def test_deterministic():
     ffi.rms_norm(x, w, y1, 1e-6)
     ffi.rms_norm(x, w, y2, 1e-6)
     assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+
+
+def test_zero_rows():
+    x = torch.empty((0, 5120), device="cuda", dtype=torch.float16)
+    w = torch.ones(5120, device="cuda", dtype=torch.float16)
+    ffi.rms_norm(x, w, torch.empty_like(x), 1e-6)
+    ffi.rms_norm_res_in(x, w, torch.empty_like(x), torch.empty_like(x), 1e-6)
+    torch.cuda.synchronize()

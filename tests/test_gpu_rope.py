@@ -94,3 +94,33 @@ def test_no_norm_q_only_out_of_place_attn():
 
 def test_large_positions():
     run(1, 64, 4, 2, 128, 128, exl3r.ROPE_NEOX, F16, position=1_000_000, seed=9)
+
+
+def test_packed_qkv_views():
+    """q and k as views into one [bsz, seq, hq + 2 hk, hd] QKV projection output (token stride
+    (hq + 2 hk) hd), rotated in place; the V heads between and after them stay bit-identical."""
+    bsz, seq, hq, hk, hd = 2, 37, 16, 4, 128
+    qkv = dev_normal((bsz, seq, hq + 2 * hk, hd), 0.0, 1.0, F16, 21)
+    qn, kn = dev_normal((hd,), 1.0, 0.1, F16, 22), dev_normal((hd,), 1.0, 0.1, F16, 23)
+    before = from_dev(qkv)
+    q, k = qkv[:, :, :hq], qkv[:, :, hq:hq + hk]
+    f = inv_freq(128)
+    pos = np.array([3, 20000], np.int32)
+    ffi.rope(q, q, k, k, torch.from_numpy(f).cuda(), 0, torch.from_numpy(pos).cuda(), qn, kn, 1e-6, 0.0,
+             exl3r.ROPE_NEOX, 1.0)
+    torch.cuda.synchronize()
+    eq, ek = orc.rope(np.ascontiguousarray(before[:, :, :hq]), np.ascontiguousarray(before[:, :, hq:hq + hk]), F16, f,
+                      exl3r.ROPE_NEOX, positions=pos, q_norm=from_dev(qn), k_norm=from_dev(kn), nwt=F16, eps=1e-6,
+                      nthreads=NTHREADS)
+    after = from_dev(qkv)
+    assert_close_ulp(after[:, :, :hq], eq, F16, 2, what="packed q")
+    assert_close_ulp(after[:, :, hq:hq + hk], ek, F16, 2, what="packed k")
+    assert np.array_equal(after[:, :, hq + hk:], before[:, :, hq + hk:]), "v heads modified"
+
+
+def test_zero_tokens():
+    q = torch.empty((1, 0, 8, 128), device="cuda", dtype=torch.float16)
+    k = torch.empty((1, 0, 2, 128), device="cuda", dtype=torch.float16)
+    ffi.rope(q, q, k, k, torch.from_numpy(inv_freq(128)).cuda(), 0, None, None, None, 1e-6, 0.0,
+             exl3r.ROPE_NEOX, 1.0)
+    torch.cuda.synchronize()
