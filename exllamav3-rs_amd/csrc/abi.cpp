@@ -78,5 +78,11 @@ extern "C" void exl3r_tune_act(int unroll, int threads, int blocks_per_cu)
 }
 
 extern "C" void exl3r_tune_rope(int iters) { exl3r::tuning().rope_iters = iters; }
+extern "C" void exl3r_tune_rope_tok(int use, int hpl, int wgs_per_cu)
+{
+    exl3r::tuning().rope_tok = use;
+    exl3r::tuning().rope_hpl = hpl;
+    exl3r::tuning().rope_wgs_per_cu = wgs_per_cu;
+}
 
 extern "C" void exl3r_tune_embed(int threads) { exl3r::tuning().embed_threads = threads; }

@@ -38,6 +38,9 @@ struct Tuning
     int rms_maxv = 0, rms_threads = 0;
     int act_unroll = 0, act_threads = 0, act_blocks_per_cu = 0;
     int rope_iters = 0;
+    int rope_tok = 0;       // 0 auto, 1 never the wave-per-token kernel, 2 always (where it applies)
+    int rope_hpl = 0;       // heads per lane in flight of the wave-per-token kernel (2, 4, 6, 8)
+    int rope_wgs_per_cu = 0; // wave-per-token kernel: persistent grid of this many workgroups per CU (0: one token per wave)
     int embed_threads = 0;
 };
 Tuning& tuning();

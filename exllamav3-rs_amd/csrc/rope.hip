@@ -9,16 +9,18 @@
 //   (rope.cu:212-221); the rotation reads the io-rounded normed head: angle = inv_freq[t] * (float)pos,
 //   cos/sin * attn_factor (rope.cu:69-85), NeoX pairs (t, t + R/2), GPT-J pairs (2t, 2t+1), each
 //   result rounded once (rope.cu:152-185); dims >= R pass through.
-//   sin/cos are fp64 evaluations of the fp32 angle rounded once (positions reach 3e4 and beyond),
-//   not the reference's __sinf/__cosf; the head sum is a full xor-butterfly sum in every lane (the reference's
+//   sin/cos are double-precision evaluations of the fp32 angle rounded once (positions reach 3e4 and
+//   beyond), not the reference's __sinf/__cosf; the head sum is a full xor-butterfly sum in every lane (the reference's
 //   shfl_down sum stored from all lanes, rope.cu:190-204, is only correct in lane 0).
 //
-// Layout: one workgroup per token (decode: several per token, splitting the heads).  A head of
-// head_dim elements is held by LPH = head_dim / 8 lanes, 8 elements (16 bytes) per lane, so a wave
-// holds 64 / LPH heads (4 heads of 128).  The head sum is a DPP butterfly inside the LPH-lane group;
-// NeoX partners live R/16 lanes apart in the same group and are exchanged with ds_bpermute, GPT-J
-// partners sit in the same lane.  sin/cos are computed once per (token, frequency) into LDS and
-// shared by every head of the token.
+// Layout: a head of head_dim elements is held by LPH = head_dim / 8 lanes, 8 elements (16 bytes) per
+// lane, so a wave holds 64 / LPH heads (4 heads of 128).  The head sum is a DPP butterfly inside the
+// LPH-lane group; NeoX partners live R/16 lanes apart in the same group and are exchanged by DPP
+// (a rotation by 8 lanes for R = 128) or ds_bpermute, GPT-J partners sit in the same lane.  Two
+// kernels: k_rope_tok (prefill NeoX) gives each wave whole tokens -- the token's sin/cos evaluated
+// once, one per lane, and its heads walked in software-pipelined batches; k_rope (decode, GPT-J)
+// flattens (token, head) items over workgroups that share the sin/cos of the tokens they span
+// through LDS.
 #include "abi.hpp"
 #include "common.cuh"
 
@@ -41,6 +43,7 @@ struct RopeArgs
     const void* kw;
     int wt;
     float eps, cb, attn;
+    float inv_hd;       // 1 / head_dim when head_dim is a power of two, else 0
     int tok_span;       // tokens spanned by one workgroup's item range (k_rope)
 };
 
@@ -56,13 +59,52 @@ __device__ __forceinline__ int token_position(const RopeArgs& a, int tok)
     return a.position + s;
 }
 
+// sin and cos of an fp32 angle |a| < 2^52 in double precision (an int32 position times any
+// inv_freq below 2^21), without the large-argument machinery of a general double sincos, which
+// would cost ~30 VGPRs here.  Cody-Waite reduction a = k pi/2 + r with pi/2 split into three
+// doubles: each FMA step is exact before its one rounding, so |r| <= pi/4 comes out with an
+// absolute error near 2^-53 |r| for every k < 2^52.  Then the Taylor series of sin through r^15 and
+// of cos through r^16 (truncation below 2^-54 on |r| <= pi/4).  Rounded to fp32 these agree with a
+// libm double sin / cos of the same angle (checked on 4e7 angles: wide exponent range, inv_freq *
+// position products, angles next to multiples of pi/2).  Larger angles give finite values with the
+// wrong quadrant; no rotary table reaches them.
+__device__ __forceinline__ void sincos_angle(float a, double& sd, double& cd)
+{
+    const double x = (double)a;
+    const double k = rint(x * 0x1.45f306dc9c883p-1);            // 2 / pi
+    double r = fma(-k, 0x1.921fb54442d18p+0, x);                // pi/2 = P1 + P2 + P3
+    r = fma(-k, 0x1.1a62633145c07p-54, r);
+    r = fma(-k, -0x1.f1976b7ed8fbcp-110, r);
+    const double r2 = r * r;
+    double ps = -0x1.ae7f3e733b81fp-41;                         // -1/15!
+    ps = fma(ps, r2, 0x1.6124613a86d09p-33);                    //  1/13!
+    ps = fma(ps, r2, -0x1.ae64567f544e4p-26);                   // -1/11!
+    ps = fma(ps, r2, 0x1.71de3a556c734p-19);                    //  1/9!
+    ps = fma(ps, r2, -0x1.a01a01a01a01ap-13);                   // -1/7!
+    ps = fma(ps, r2, 0x1.1111111111111p-7);                     //  1/5!
+    ps = fma(ps, r2, -0x1.5555555555555p-3);                    // -1/3!
+    const double s = fma(r * r2, ps, r);
+    double pc = 0x1.ae7f3e733b81fp-45;                          //  1/16!
+    pc = fma(pc, r2, -0x1.93974a8c07c9dp-37);                   // -1/14!
+    pc = fma(pc, r2, 0x1.1eed8eff8d898p-29);                    //  1/12!
+    pc = fma(pc, r2, -0x1.27e4fb7789f5cp-22);                   // -1/10!
+    pc = fma(pc, r2, 0x1.a01a01a01a01ap-16);                    //  1/8!
+    pc = fma(pc, r2, -0x1.6c16c16c16c17p-10);                   // -1/6!
+    pc = fma(pc, r2, 0x1.5555555555555p-5);                     //  1/4!
+    pc = fma(pc, r2, -0.5);                                     // -1/2!
+    const double c = fma(r2, pc, 1.0);
+    const int q = (int)(k - 4.0 * floor(k * 0.25));             // k mod 4, exact for |k| < 2^53
+    sd = q == 0 ? s : q == 1 ? c : q == 2 ? -s : -c;
+    cd = q == 0 ? c : q == 1 ? -s : q == 2 ? -c : s;
+}
+
 // {cos, sin} * attn_factor of rotary frequency t at position pos: fp64 evaluation of the fp32
 // angle, rounded once (correctly rounded fp32 values).
 __device__ __forceinline__ float2 rope_cs(const RopeArgs& a, int t, int pos)
 {
     const float ang = __fmul_rn(a.inv_freq[t], (float)pos);
     double sd, cd;
-    sincos((double)ang, &sd, &cd);
+    sincos_angle(ang, sd, cd);
     return make_float2((float)cd * a.attn, (float)sd * a.attn);
 }
 
@@ -72,9 +114,177 @@ __device__ __forceinline__ void fill_sincos(const RopeArgs& a, int pos, float2* 
     for (int t = threadIdx.x; t < a.R / 2; t += blockDim.x) cs[t] = rope_cs(a, t, pos);
 }
 
-// Work item = one (token, head) pair; a workgroup takes a contiguous range of slots * ITERS items,
-// which spans at most a.tok_span tokens.  Every head chunk is loaded first; the sin/cos of the
-// spanned tokens are evaluated into LDS while those loads are in flight.
+// Norm weights of one lane's 8-element chunk with the constant bias folded in, loaded once per
+// kernel: the packed half sums h(w + h(cb)) (NORM_HALF), or fp32 w + cb (NORM_F32).
+template <int NORM> struct LaneW { };
+template <> struct LaneW<NORM_HALF> { uint32_t a[4]; };
+template <> struct LaneW<NORM_F32> { float f[8]; };
+
+template <int NORM>
+__device__ __forceinline__ LaneW<NORM> lane_weights(const RopeArgs& a, const void* w, int e0, bool ok)
+{
+    LaneW<NORM> r;
+    if constexpr (NORM == NORM_HALF)
+    {
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) r.a[i] = 0;
+        if (!ok || !w) return r;
+        const TF16::Vec wv = load8<TF16>(w, e0);
+        const _Float16 cbh = to_f16(a.cb);
+        const f16x2 cb2 = { cbh, cbh };
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) r.a[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, (uint32_t)wv.a[i]) + cb2);
+    }
+    else if constexpr (NORM == NORM_F32)
+    {
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) r.f[j] = 0.0f;
+        if (!ok || !w) return r;
+        load8_dyn(w, a.wt, e0, r.f);
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) r.f[j] = r.f[j] + a.cb;
+    }
+    return r;
+}
+
+template <int NORM>
+__device__ __forceinline__ LaneW<NORM> select_w(bool q, const LaneW<NORM>& wq, const LaneW<NORM>& wk)
+{
+    LaneW<NORM> r;
+    if constexpr (NORM == NORM_HALF)
+    {
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) r.a[i] = q ? wq.a[i] : wk.a[i];
+    }
+    else if constexpr (NORM == NORM_F32)
+    {
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) r.f[j] = q ? wq.f[j] : wk.f[j];
+    }
+    return r;
+}
+
+// Head norm + rotation of the 8 elements e0 .. e0 + 7 one lane holds of a head spread over LPH
+// lanes, in place on the lane's packed io chunk.  Must be called by the whole wave (the head sum
+// and the NeoX exchange are cross-lane).
+//   w:    the lane's weights (lane_weights) of this head's tensor;
+//   c, s: cos / sin (times attn_factor) of the lane's frequencies: NeoX t0 .. t0 + 7 with
+//         t0 = e0 mod R/2, GPT-J pairs (e0 + 2p, e0 + 2p + 1) in c[p], s[p] for p < 4;
+//   l64:  lane index in the wave.
+template <class IO, int MODE, int LPH, int NORM>
+__device__ __forceinline__ void rope_head(const RopeArgs& a, typename IO::Vec& v, const LaneW<NORM>& w,
+                                          const float (&c)[8], const float (&s)[8], int e0, int l64)
+{
+    if constexpr (NORM != NORM_NONE)
+    {
+        float f[8];
+        unpack8<IO>(v, f);
+        // Sum of squares in fp64 (squares of 16-bit values are exact), one rounding to fp32: the
+        // normed head is then bit-identical to a double-precision evaluation, so the rotation that
+        // follows cannot amplify a last-bit difference through cancellation.  sum / head_dim is a
+        // multiply by the exact reciprocal when head_dim is a power of two (the same rounding).
+        double ss = 0.0;
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fma((double)f[j], (double)f[j], ss);
+        ss = group_sum64<LPH>(ss);
+        const float mean = a.inv_hd != 0.0f ? (float)ss * a.inv_hd : (float)ss / (float)a.hd;
+        const float rmf = 1.0f / sqrtf(mean + a.eps);
+        if constexpr (NORM == NORM_HALF)
+        {
+            // Two half roundings: h(w + h(cb)) * h(v * rmf), multiplied as packed halves.
+            #pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                const f16x2 n2 = { to_f16(f[2 * i] * rmf), to_f16(f[2 * i + 1] * rmf) };
+                v.a[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, w.a[i]) * n2);
+            }
+        }
+        else
+        {
+            #pragma unroll
+            for (int j = 0; j < 8; ++j) f[j] = (f[j] * rmf) * w.f[j];
+            v = pack8<IO>(f);
+        }
+    }
+
+    // Rotation products rounded separately (no FMA contraction), as the reference semantics state
+    // them: r1 = fl(fl(v1 c) - fl(v2 s)).
+    if constexpr (MODE == EXL3R_ROPE_GPTJ)
+    {
+        if (e0 < a.R)
+        {
+            #pragma clang fp contract(off)
+            float f[8];
+            unpack8<IO>(v, f);
+            #pragma unroll
+            for (int p = 0; p < 4; ++p)
+            {
+                if (e0 + 2 * p < a.R)
+                {
+                    const float v1 = f[2 * p], v2 = f[2 * p + 1];
+                    f[2 * p] = v1 * c[p] - v2 * s[p];
+                    f[2 * p + 1] = v2 * c[p] + v1 * s[p];
+                }
+            }
+            v = pack8<IO>(f);
+        }
+    }
+    else
+    {
+        // The partner lane is dl = R/16 lanes away inside the head's lane group; the packed io words
+        // are exchanged as they are.  R = 128 at 16 lanes per head is a rotation by 8 inside a DPP row.
+        const int R2 = a.R >> 1;
+        const int dl = R2 >> 3;
+        const bool rot = e0 < a.R;
+        const bool lower = e0 < R2;
+        typename IO::Vec po;
+        if (LPH == 16 && dl == 8)
+        {
+            #pragma unroll
+            for (int i = 0; i < 4; ++i)
+                po.a[i] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v.a[i], DPP_ROW_ROR8, 0xf, 0xf, false);
+        }
+        else
+        {
+            const int src = rot ? (lower ? l64 + dl : l64 - dl) : l64;
+            #pragma unroll
+            for (int i = 0; i < 4; ++i)
+                po.a[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)v.a[i]);
+        }
+        if (rot)
+        {
+            #pragma clang fp contract(off)
+            float f[8], g[8];
+            unpack8<IO>(v, f);
+            unpack8<IO>(po, g);
+            #pragma unroll
+            for (int j = 0; j < 8; ++j) f[j] = lower ? f[j] * c[j] - g[j] * s[j] : f[j] * c[j] + g[j] * s[j];
+            v = pack8<IO>(f);
+        }
+    }
+}
+
+// cos / sin of the lane's frequencies (rope_head's c, s) out of a row of R/2 {cos, sin} pairs.
+template <int MODE>
+__device__ __forceinline__ void lane_sincos(const float2* row, int e0, int R, float (&c)[8], float (&s)[8])
+{
+    const int t0 = MODE == EXL3R_ROPE_GPTJ ? (e0 >> 1) : (e0 < (R >> 1) ? e0 : e0 - (R >> 1));
+    #pragma unroll
+    for (int j = 0; j < 8; ++j)
+    {
+        c[j] = s[j] = 0.0f;
+        if (MODE == EXL3R_ROPE_NEOX ? e0 < R : (j < 4 && e0 + 2 * j < R))
+        {
+            const float2 x = row[t0 + j];
+            c[j] = x.x;
+            s[j] = x.y;
+        }
+    }
+}
+
+// Decode / small launches.  Work item = one (token, head) pair; a workgroup takes a contiguous range
+// of slots * ITERS items, which spans at most a.tok_span tokens.  Every head chunk is loaded first;
+// the sin/cos of the spanned tokens are evaluated into LDS while those loads are in flight.
 template <class IO, int MODE, int LPH, int ITERS, int NORM>
 __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
 {
@@ -89,6 +299,8 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
     const int64_t per_wg = (int64_t)slots * ITERS;
     const bool lane_ok = lane * 8 < a.hd;
     const int e0 = lane * 8;                  // first head element held by this lane
+    const LaneW<NORM> wq = lane_weights<NORM>(a, a.qw, e0, lane_ok);
+    const LaneW<NORM> wk = lane_weights<NORM>(a, a.kw, e0, lane_ok);
 
     for (int64_t i0 = (int64_t)blockIdx.x * per_wg; i0 < items; i0 += (int64_t)gridDim.x * per_wg)
     {
@@ -97,8 +309,8 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
 
         typename IO::Vec v[ITERS];
         char* optr[ITERS];
-        int trel[ITERS], head[ITERS];
-        bool act[ITERS];
+        int trel[ITERS];
+        bool act[ITERS], isq[ITERS];
         #pragma unroll
         for (int it = 0; it < ITERS; ++it)
         {
@@ -106,14 +318,14 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
             int tr = 0;
             while (rel >= nheads) { rel -= nheads; ++tr; }
             trel[it] = tr;
-            head[it] = rel;
+            isq[it] = rel < a.hq;
             const int tok = tok0 + tr;
             act[it] = tok < a.tokens && lane_ok;
             optr[it] = nullptr;
             if (act[it])
             {
                 const char* ip;
-                if (rel < a.hq)
+                if (isq[it])
                 {
                     const int64_t off = ((int64_t)tok * a.q_ts + (int64_t)rel * a.q_hs) * IO::bytes;
                     ip = (const char*)a.q + off;
@@ -140,105 +352,125 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
         #pragma unroll
         for (int it = 0; it < ITERS; ++it)
         {
-            const float2* csr = cs + trel[it] * R2;
-            float f[8];
-            if (act[it]) unpack8<IO>(v[it], f);
-            else
+            float c[8], s[8];
+            if (!act[it])
             {
                 #pragma unroll
-                for (int j = 0; j < 8; ++j) f[j] = 0.0f;
+                for (int i = 0; i < 4; ++i) v[it].a[i] = 0;
             }
-
-            if constexpr (NORM != NORM_NONE)
-            {
-                // Sum of squares in fp64 (squares of 16-bit values are exact), one rounding to fp32:
-                // the normed head is then bit-identical to a double-precision evaluation, so the
-                // rotation that follows cannot amplify a last-bit difference through cancellation.
-                double ss = 0.0;
-                #pragma unroll
-                for (int j = 0; j < 8; ++j) ss = fma((double)f[j], (double)f[j], ss);
-                ss = group_sum64<LPH>(ss);
-                const float rmf = rms_factor(ss, a.hd, a.eps);
-                if (act[it])
-                {
-                    const void* w = head[it] < a.hq ? a.qw : a.kw;
-                    if constexpr (NORM == NORM_HALF)
-                    {
-                        const TF16::Vec wv = load8<TF16>(w, e0);
-                        const _Float16 cbh = to_f16(a.cb);
-                        #pragma unroll
-                        for (int j = 0; j < 8; ++j)
-                        {
-                            const uint32_t word = wv.a[j >> 1];
-                            const _Float16 wh = __builtin_bit_cast(_Float16, (uint16_t)((j & 1) ? word >> 16 : word & 0xffffu)) + cbh;
-                            const _Float16 nh = to_f16(f[j] * rmf);
-                            f[j] = (float)(wh * nh);
-                        }
-                    }
-                    else
-                    {
-                        float wf[8];
-                        load8_dyn(w, a.wt, e0, wf);
-                        #pragma unroll
-                        for (int j = 0; j < 8; ++j) f[j] = round_to<IO>((f[j] * rmf) * (wf[j] + a.cb));
-                    }
-                }
-            }
-
-            // Rotation products rounded separately (no FMA contraction), as the reference semantics
-            // state them: r1 = fl(fl(v1 c) - fl(v2 s)).
-            if constexpr (MODE == EXL3R_ROPE_GPTJ)
-            {
-                #pragma clang fp contract(off)
-                #pragma unroll
-                for (int p = 0; p < 4; ++p)
-                {
-                    const int e = e0 + 2 * p;
-                    if (e < a.R)
-                    {
-                        const float2 c = csr[e >> 1];
-                        const float v1 = f[2 * p], v2 = f[2 * p + 1];
-                        f[2 * p] = v1 * c.x - v2 * c.y;
-                        f[2 * p + 1] = v2 * c.x + v1 * c.y;
-                    }
-                }
-            }
-            else
-            {
-                // Partner lane R/16 lanes away inside the head's lane group; values are exchanged as
-                // packed io words (exact: they are io-rounded already).
-                const int half = R2;
-                const int dl = half >> 3;
-                const bool rot = e0 < a.R;
-                const bool lower = e0 < half;
-                const int src_lane = rot ? (lower ? tid + dl : tid - dl) : tid;
-                uint32_t other[4];
-                const typename IO::Vec pk = pack8<IO>(f);
-                #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    other[i] = (uint32_t)__builtin_amdgcn_ds_bpermute((src_lane & 63) << 2, (int)(uint32_t)pk.a[i]);
-                if (rot)
-                {
-                    #pragma clang fp contract(off)
-                    typename IO::Vec po;
-                    #pragma unroll
-                    for (int i = 0; i < 4; ++i) po.a[i] = other[i];
-                    float g[8];
-                    unpack8<IO>(po, g);
-                    const int t0 = lower ? e0 : e0 - half;
-                    #pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                    {
-                        const float2 c = csr[t0 + j];
-                        f[j] = lower ? f[j] * c.x - g[j] * c.y : f[j] * c.x + g[j] * c.y;
-                    }
-                }
-            }
-
-            if (act[it]) store8<IO>(optr[it], (int64_t)e0, pack8<IO>(f));
+            lane_sincos<MODE>(cs + trel[it] * R2, e0, a.R, c, s);
+            rope_head<IO, MODE, LPH, NORM>(a, v[it], select_w<NORM>(isq[it], wq, wk), c, s, e0, tid & 63);
+            if (act[it]) store8<IO>(optr[it], (int64_t)e0, v[it]);
         }
         __syncthreads();   // cs[] is refilled for the next range
     }
+}
+
+// Orders one wave's LDS writes before its following LDS reads (and the reads before later writes)
+// without a workgroup barrier.
+__device__ __forceinline__ void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Prefill launches: one wave per token at a time.  The wave evaluates a token's R/2 {cos, sin}
+// pairs once, one per lane, into its LDS row; each lane keeps the pairs its elements need in
+// registers, and the wave walks the token's heads in batches of HPL passes (64/LPH heads per pass).
+// The loads of the next batch are issued before the current batch is computed, and a new token's
+// sin/cos are evaluated while its first batch is in flight, so every wave keeps loads in flight
+// while it computes.  The four waves of a workgroup take different tokens and never wait for each
+// other.
+template <class IO, int HPL>
+struct RopeBatch
+{
+    typename IO::Vec v[HPL];
+    int32_t off[HPL];            // element offset of the lane's chunk inside its token
+    bool act[HPL], isq[HPL];
+    int64_t tok;
+    int b;
+};
+
+template <class IO, int MODE, int LPH, int HPL, int NORM>
+__global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
+{
+    extern __shared__ float2 cs[];            // [4 waves][R / 2]
+    constexpr int HPP = 64 / LPH;             // heads per pass
+    const int l64 = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int sub = l64 / LPH;
+    const int e0 = (l64 % LPH) * 8;
+    const bool lane_ok = e0 < a.hd;
+    const int R2 = a.R >> 1;
+    const int nheads = a.hq + a.hk;
+    const int nb = ((nheads + HPP - 1) / HPP + HPL - 1) / HPL;    // batches per token
+    const int64_t nwaves = (int64_t)gridDim.x * 4;
+    float2* row = cs + wave * R2;
+    const LaneW<NORM> wq = lane_weights<NORM>(a, a.qw, e0, lane_ok);
+    const LaneW<NORM> wk = lane_weights<NORM>(a, a.kw, e0, lane_ok);
+
+    auto issue = [&](RopeBatch<IO, HPL>& t) {
+        const char* qb = (const char*)a.q + t.tok * a.q_ts * IO::bytes;
+        const char* kb = (const char*)a.k + t.tok * a.k_ts * IO::bytes;
+        #pragma unroll
+        for (int i = 0; i < HPL; ++i)
+        {
+            const int h = (t.b * HPL + i) * HPP + sub;
+            t.act[i] = lane_ok && h < nheads;
+            t.isq[i] = h < a.hq;
+            t.off[i] = (int32_t)(t.isq[i] ? (int64_t)h * a.q_hs : (int64_t)(h - a.hq) * a.k_hs) + e0;
+            if (t.act[i]) t.v[i] = load8s<IO>(t.isq[i] ? qb : kb, t.off[i]);
+        }
+    };
+    float c[8], s[8];
+    auto fill = [&](int64_t tok) {
+        const int pos = token_position(a, (int)tok);
+        wave_lds_sync();
+        for (int t = l64; t < R2; t += 64) row[t] = rope_cs(a, t, pos);
+        wave_lds_sync();
+        lane_sincos<MODE>(row, e0, a.R, c, s);
+    };
+    auto compute = [&](RopeBatch<IO, HPL>& t, const float (&c)[8], const float (&s)[8]) {
+        char* qo = (char*)a.oq + t.tok * a.q_ts * IO::bytes;
+        char* ko = (char*)a.ok + t.tok * a.k_ts * IO::bytes;
+        #pragma unroll
+        for (int i = 0; i < HPL; ++i)
+        {
+            if (!t.act[i])
+            {
+                #pragma unroll
+                for (int j = 0; j < 4; ++j) t.v[i].a[j] = 0;
+            }
+            rope_head<IO, MODE, LPH, NORM>(a, t.v[i], select_w<NORM>(t.isq[i], wq, wk), c, s, e0, l64);
+            if (t.act[i]) store8<IO>(t.isq[i] ? qo : ko, t.off[i], t.v[i]);
+        }
+    };
+
+    RopeBatch<IO, HPL> A, B;
+    A.tok = (int64_t)blockIdx.x * 4 + wave;
+    A.b = 0;
+    if (A.tok >= a.tokens) return;
+    issue(A);
+    fill(A.tok);
+
+    // One pipeline step: start `nxt` (the batch after `cur`), then finish `cur`.  Returns false
+    // when `cur` was the wave's last batch.
+    auto step = [&](RopeBatch<IO, HPL>& cur, RopeBatch<IO, HPL>& nxt) -> bool {
+        nxt.tok = cur.tok;
+        nxt.b = cur.b + 1;
+        if (nxt.b == nb)
+        {
+            nxt.b = 0;
+            nxt.tok += nwaves;
+        }
+        const bool more = nxt.tok < a.tokens;
+        if (more) issue(nxt);
+        compute(cur, c, s);
+        if (more && nxt.b == 0) fill(nxt.tok);
+        return more;
+    };
+    while (step(A, B) && step(B, A)) {}
 }
 
 // Generic fallback (any even head_dim / rotary_dim, any alignment): one workgroup per token, heads
@@ -319,14 +551,51 @@ static void launch_rope_lph(RopeArgs a, int iters, hipStream_t s)
     }
 }
 
-// Items per lane: enough workgroups to fill 256 CUs several times over, then up to four heads per
-// lane so each wave keeps 4 KiB of loads in flight.
+// Wave-per-token launch.  Measured on MI355X at C4 (4639 tokens, 64 + 8 heads of 128, NeoX, in
+// place): f16 heads (packed-half norm, 96 VGPRs) run best with 2 heads per lane in flight and one
+// token per wave (38.5 us; 3 per lane 42 us); bf16 heads (fp32 norm) with 3 per lane on a
+// persistent grid of 4 workgroups per CU (37.0 us; 2 per lane 42 us).
+template <class IO, int MODE, int LPH, int NORM>
+static void launch_rope_tok(RopeArgs a, hipStream_t s)
+{
+    const Tuning& tu = tuning();
+    int hpl = IO::code == DT_F16 ? 2 : 3;
+    int wgs_per_cu = IO::code == DT_F16 ? 0 : 4;
+    if (tu.rope_hpl > 0) hpl = tu.rope_hpl;
+    if (tu.rope_wgs_per_cu > 0) wgs_per_cu = tu.rope_wgs_per_cu;
+    hpl = hpl <= 2 ? 2 : hpl <= 3 ? 3 : hpl <= 4 ? 4 : hpl <= 6 ? 6 : 8;
+    int64_t blocks = (a.tokens + 3) / 4;
+    if (wgs_per_cu > 0 && blocks > (int64_t)wgs_per_cu * device_cus()) blocks = (int64_t)wgs_per_cu * device_cus();
+    if (blocks > kMaxGridX) blocks = kMaxGridX;
+    const size_t lds = 4 * (size_t)(a.R / 2) * sizeof(float2);
+    switch (hpl)
+    {
+        case 2: k_rope_tok<IO, MODE, LPH, 2, NORM><<<(unsigned)blocks, 256, lds, s>>>(a); break;
+        case 3: k_rope_tok<IO, MODE, LPH, 3, NORM><<<(unsigned)blocks, 256, lds, s>>>(a); break;
+        case 4: k_rope_tok<IO, MODE, LPH, 4, NORM><<<(unsigned)blocks, 256, lds, s>>>(a); break;
+        case 6: k_rope_tok<IO, MODE, LPH, 6, NORM><<<(unsigned)blocks, 256, lds, s>>>(a); break;
+        default: k_rope_tok<IO, MODE, LPH, 8, NORM><<<(unsigned)blocks, 256, lds, s>>>(a); break;
+    }
+}
+
+// Prefill-sized NeoX launches (a wave per token still gives every CU several waves) take the
+// wave-per-token kernel.  GPT-J (C4 at rotary 64: 35.2 us flattened vs 37.5 us per token) and
+// decode-sized launches take the flattened kernel: items per lane enough workgroups to fill 256 CUs
+// several times over, then up to four heads per lane so each wave keeps 4 KiB of loads in flight.
 template <class IO, int MODE, int NORM>
 static void launch_rope_vec(const RopeArgs& a, int lph, hipStream_t s)
 {
+    const Tuning& tu = tuning();
+    const bool tok_ok = lph == 8 || lph == 16 || lph == 32;
+    if (tok_ok && (tu.rope_tok == 2 || (tu.rope_tok == 0 && MODE == EXL3R_ROPE_NEOX && a.tokens >= 1024)))
+    {
+        if (lph == 8) launch_rope_tok<IO, MODE, 8, NORM>(a, s);
+        else if (lph == 16) launch_rope_tok<IO, MODE, 16, NORM>(a, s);
+        else launch_rope_tok<IO, MODE, 32, NORM>(a, s);
+        return;
+    }
     const int64_t items = a.tokens * (a.hq + a.hk);
     const int64_t slots = 256 / lph;
-    const Tuning& tu = tuning();
     int iters = 1;
     if (tu.rope_iters == 1 || tu.rope_iters == 2 || tu.rope_iters == 4) iters = tu.rope_iters;
     else if (items >= slots * 4 * 2048) iters = 4;
@@ -404,6 +673,7 @@ extern "C" int exl3r_rope(const void* q, void* out_q, int64_t q_tok_stride, int6
     a.position = position; a.positions = positions; a.position_ids = position_ids;
     a.qw = q_norm; a.kw = k_norm; a.wt = norm_dtype;
     a.eps = norm_eps; a.cb = norm_constant_bias; a.attn = attn_factor;
+    a.inv_hd = (head_dim & (head_dim - 1)) == 0 ? 1.0f / (float)head_dim : 0.0f;
     const int norm = !q_norm ? NORM_NONE : (norm_dtype == EXL3R_F16 && dtype == EXL3R_F16) ? NORM_HALF : NORM_F32;
     hipStream_t s = (hipStream_t)stream;
 
