@@ -45,7 +45,41 @@ struct RopeArgs
     float eps, cb, attn;
     float inv_hd;       // 1 / head_dim when head_dim is a power of two, else 0
     int tok_span;       // tokens spanned by one workgroup's item range (k_rope)
+    // Paged KV-cache append (exl3r_rope_paged_kv): v heads are copied and the roped k heads written
+    // to caches [pages, 1 << page_log2, hk, hd]; kc == nullptr means no append.
+    const void* v;
+    int64_t v_ts, v_hs;
+    int hv;             // v heads (hk with an append, else 0)
+    void* kc;
+    void* vc;
+    int page_log2;
+    int64_t pages, max_blocks;
+    const int32_t* block_table;
+    const int32_t* cache_seqlens;
+    int32_t* err;
 };
+
+// Head kinds of the item space [0, hq) q, [hq, hq + hk) k, [hq + hk, hq + hk + hv) v.
+enum { KIND_Q = 0, KIND_K = 1, KIND_V = 2 };
+
+__device__ __forceinline__ int head_kind(const RopeArgs& a, int h) { return h < a.hq ? KIND_Q : h < a.hq + a.hk ? KIND_K : KIND_V; }
+
+// Element offset of token tok's row in the caches (cache_seqlens[b] + s through the block table,
+// reference kernels/generator/cache.cu:173-179), or -1 after flagging a position outside the block
+// table or a page outside the pool.
+__device__ __forceinline__ int64_t cache_row(const RopeArgs& a, int64_t tok)
+{
+    const int64_t b = tok / a.seq_len;
+    const int64_t pos = (int64_t)a.cache_seqlens[b] + (tok - b * a.seq_len);
+    const int64_t lb = pos >> a.page_log2;
+    const int64_t page = (pos >= 0 && lb < a.max_blocks) ? (int64_t)a.block_table[b * a.max_blocks + lb] : -1;
+    if (page < 0 || page >= a.pages)
+    {
+        if (a.err) atomicOr(a.err, 1);
+        return -1;
+    }
+    return ((page << a.page_log2) + (pos & (((int64_t)1 << a.page_log2) - 1))) * a.hk * a.hd;
+}
 
 enum { NORM_NONE = 0, NORM_HALF = 1, NORM_F32 = 2 };
 
@@ -170,9 +204,10 @@ __device__ __forceinline__ LaneW<NORM> select_w(bool q, const LaneW<NORM>& wq, c
 //   w:    the lane's weights (lane_weights) of this head's tensor;
 //   c, s: cos / sin (times attn_factor) of the lane's frequencies: NeoX t0 .. t0 + 7 with
 //         t0 = e0 mod R/2, GPT-J pairs (e0 + 2p, e0 + 2p + 1) in c[p], s[p] for p < 4;
-//   l64:  lane index in the wave.
+//   l64:  lane index in the wave;
+//   math: false leaves the chunk as loaded (v heads of a paged append; the cross-lane steps still run).
 template <class IO, int MODE, int LPH, int NORM>
-__device__ __forceinline__ void rope_head(const RopeArgs& a, typename IO::Vec& v, const LaneW<NORM>& w,
+__device__ __forceinline__ void rope_head(const RopeArgs& a, typename IO::Vec& v, bool math, const LaneW<NORM>& w,
                                           const float (&c)[8], const float (&s)[8], int e0, int l64)
 {
     if constexpr (NORM != NORM_NONE)
@@ -189,7 +224,8 @@ __device__ __forceinline__ void rope_head(const RopeArgs& a, typename IO::Vec& v
         ss = group_sum64<LPH>(ss);
         const float mean = a.inv_hd != 0.0f ? (float)ss * a.inv_hd : (float)ss / (float)a.hd;
         const float rmf = 1.0f / sqrtf(mean + a.eps);
-        if constexpr (NORM == NORM_HALF)
+        if (!math) {}
+        else if constexpr (NORM == NORM_HALF)
         {
             // Two half roundings: h(w + h(cb)) * h(v * rmf), multiplied as packed halves.
             #pragma unroll
@@ -211,7 +247,7 @@ __device__ __forceinline__ void rope_head(const RopeArgs& a, typename IO::Vec& v
     // them: r1 = fl(fl(v1 c) - fl(v2 s)).
     if constexpr (MODE == EXL3R_ROPE_GPTJ)
     {
-        if (e0 < a.R)
+        if (math && e0 < a.R)
         {
             #pragma clang fp contract(off)
             float f[8];
@@ -251,7 +287,7 @@ __device__ __forceinline__ void rope_head(const RopeArgs& a, typename IO::Vec& v
             for (int i = 0; i < 4; ++i)
                 po.a[i] = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)(uint32_t)v.a[i]);
         }
-        if (rot)
+        if (math && rot)
         {
             #pragma clang fp contract(off)
             float f[8], g[8];
@@ -285,7 +321,7 @@ __device__ __forceinline__ void lane_sincos(const float2* row, int e0, int R, fl
 // Decode / small launches.  Work item = one (token, head) pair; a workgroup takes a contiguous range
 // of slots * ITERS items, which spans at most a.tok_span tokens.  Every head chunk is loaded first;
 // the sin/cos of the spanned tokens are evaluated into LDS while those loads are in flight.
-template <class IO, int MODE, int LPH, int ITERS, int NORM>
+template <class IO, int MODE, int LPH, int ITERS, int NORM, bool APPEND>
 __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
 {
     extern __shared__ float2 cs[];            // [tok_span][R / 2]
@@ -293,7 +329,7 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
     const int slot = tid / LPH;
     const int lane = tid % LPH;
     const int slots = blockDim.x / LPH;
-    const int nheads = a.hq + a.hk;
+    const int nheads = a.hq + a.hk + (APPEND ? a.hv : 0);
     const int R2 = a.R / 2;
     const int64_t items = a.tokens * nheads;
     const int64_t per_wg = (int64_t)slots * ITERS;
@@ -308,9 +344,10 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
         const int hfirst = (int)(i0 - (int64_t)tok0 * nheads);
 
         typename IO::Vec v[ITERS];
-        char* optr[ITERS];
-        int trel[ITERS];
-        bool act[ITERS], isq[ITERS];
+        char* optr[ITERS];      // io output (nullptr: none)
+        char* cptr[ITERS];      // cache output (nullptr: none)
+        int trel[ITERS], kind[ITERS];
+        bool act[ITERS];
         #pragma unroll
         for (int it = 0; it < ITERS; ++it)
         {
@@ -318,14 +355,14 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
             int tr = 0;
             while (rel >= nheads) { rel -= nheads; ++tr; }
             trel[it] = tr;
-            isq[it] = rel < a.hq;
+            kind[it] = APPEND ? head_kind(a, rel) : rel < a.hq ? KIND_Q : KIND_K;
             const int tok = tok0 + tr;
             act[it] = tok < a.tokens && lane_ok;
-            optr[it] = nullptr;
+            optr[it] = cptr[it] = nullptr;
             if (act[it])
             {
                 const char* ip;
-                if (isq[it])
+                if (kind[it] == KIND_Q)
                 {
                     const int64_t off = ((int64_t)tok * a.q_ts + (int64_t)rel * a.q_hs) * IO::bytes;
                     ip = (const char*)a.q + off;
@@ -333,9 +370,21 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
                 }
                 else
                 {
-                    const int64_t off = ((int64_t)tok * a.k_ts + (int64_t)(rel - a.hq) * a.k_hs) * IO::bytes;
-                    ip = (const char*)a.k + off;
-                    optr[it] = (char*)a.ok + off;
+                    const int hkv = rel - a.hq - (kind[it] == KIND_V ? a.hk : 0);
+                    if (kind[it] == KIND_K)
+                    {
+                        const int64_t off = ((int64_t)tok * a.k_ts + (int64_t)hkv * a.k_hs) * IO::bytes;
+                        ip = (const char*)a.k + off;
+                        if (a.ok) optr[it] = (char*)a.ok + off;
+                    }
+                    else
+                        ip = (const char*)a.v + ((int64_t)tok * a.v_ts + (int64_t)hkv * a.v_hs) * IO::bytes;
+                    if (APPEND)
+                    {
+                        const int64_t row = cache_row(a, tok);
+                        if (row >= 0)
+                            cptr[it] = (char*)(kind[it] == KIND_K ? a.kc : a.vc) + (row + (int64_t)hkv * a.hd) * IO::bytes;
+                    }
                 }
                 v[it] = load8s<IO>(ip, e0);
             }
@@ -359,8 +408,10 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
                 for (int i = 0; i < 4; ++i) v[it].a[i] = 0;
             }
             lane_sincos<MODE>(cs + trel[it] * R2, e0, a.R, c, s);
-            rope_head<IO, MODE, LPH, NORM>(a, v[it], select_w<NORM>(isq[it], wq, wk), c, s, e0, tid & 63);
-            if (act[it]) store8<IO>(optr[it], (int64_t)e0, v[it]);
+            rope_head<IO, MODE, LPH, NORM>(a, v[it], kind[it] != KIND_V, select_w<NORM>(kind[it] == KIND_Q, wq, wk), c, s,
+                                           e0, tid & 63);
+            if (act[it] && optr[it]) store8<IO>(optr[it], (int64_t)e0, v[it]);
+            if (APPEND && act[it] && cptr[it]) store8<IO>(cptr[it], (int64_t)e0, v[it]);
         }
         __syncthreads();   // cs[] is refilled for the next range
     }
@@ -386,13 +437,15 @@ template <class IO, int HPL>
 struct RopeBatch
 {
     typename IO::Vec v[HPL];
-    int32_t off[HPL];            // element offset of the lane's chunk inside its token
-    bool act[HPL], isq[HPL];
+    int32_t hidx[HPL];           // head index inside q, k or v
+    bool isq[HPL], isv[HPL];
+    bool act[HPL];
     int64_t tok;
+    int64_t crow;                // the token's cache row (cache_row), -1: no append
     int b;
 };
 
-template <class IO, int MODE, int LPH, int HPL, int NORM>
+template <class IO, int MODE, int LPH, int HPL, int NORM, bool APPEND>
 __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
 {
     extern __shared__ float2 cs[];            // [4 waves][R / 2]
@@ -403,25 +456,31 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
     const int e0 = (l64 % LPH) * 8;
     const bool lane_ok = e0 < a.hd;
     const int R2 = a.R >> 1;
-    const int nheads = a.hq + a.hk;
+    const int nheads = a.hq + a.hk + (APPEND ? a.hv : 0);
     const int nb = ((nheads + HPP - 1) / HPP + HPL - 1) / HPL;    // batches per token
     const int64_t nwaves = (int64_t)gridDim.x * 4;
     float2* row = cs + wave * R2;
     const LaneW<NORM> wq = lane_weights<NORM>(a, a.qw, e0, lane_ok);
     const LaneW<NORM> wk = lane_weights<NORM>(a, a.kw, e0, lane_ok);
+    auto head_stride = [&](int kind) { return kind == KIND_Q ? a.q_hs : kind == KIND_K ? a.k_hs : a.v_hs; };
 
     auto issue = [&](RopeBatch<IO, HPL>& t) {
         const char* qb = (const char*)a.q + t.tok * a.q_ts * IO::bytes;
         const char* kb = (const char*)a.k + t.tok * a.k_ts * IO::bytes;
+        const char* vb = (const char*)a.v + t.tok * a.v_ts * IO::bytes;
         #pragma unroll
         for (int i = 0; i < HPL; ++i)
         {
             const int h = (t.b * HPL + i) * HPP + sub;
             t.act[i] = lane_ok && h < nheads;
             t.isq[i] = h < a.hq;
-            t.off[i] = (int32_t)(t.isq[i] ? (int64_t)h * a.q_hs : (int64_t)(h - a.hq) * a.k_hs) + e0;
-            if (t.act[i]) t.v[i] = load8s<IO>(t.isq[i] ? qb : kb, t.off[i]);
+            t.isv[i] = APPEND && h >= a.hq + a.hk;
+            const int kd = t.isq[i] ? KIND_Q : t.isv[i] ? KIND_V : KIND_K;
+            t.hidx[i] = h - (kd == KIND_Q ? 0 : kd == KIND_K ? a.hq : a.hq + a.hk);
+            if (t.act[i])
+                t.v[i] = load8s<IO>(kd == KIND_Q ? qb : kd == KIND_K ? kb : vb, (int64_t)t.hidx[i] * head_stride(kd) + e0);
         }
+        t.crow = APPEND ? cache_row(a, t.tok) : -1;
     };
     float c[8], s[8];
     auto fill = [&](int64_t tok) {
@@ -442,8 +501,17 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
                 #pragma unroll
                 for (int j = 0; j < 4; ++j) t.v[i].a[j] = 0;
             }
-            rope_head<IO, MODE, LPH, NORM>(a, t.v[i], select_w<NORM>(t.isq[i], wq, wk), c, s, e0, l64);
-            if (t.act[i]) store8<IO>(t.isq[i] ? qo : ko, t.off[i], t.v[i]);
+            const int kd = t.isq[i] ? KIND_Q : t.isv[i] ? KIND_V : KIND_K;
+            rope_head<IO, MODE, LPH, NORM>(a, t.v[i], kd != KIND_V, select_w<NORM>(kd == KIND_Q, wq, wk), c, s, e0, l64);
+            if (!t.act[i]) continue;
+            const int64_t off = (int64_t)t.hidx[i] * head_stride(kd) + e0;
+            if (kd == KIND_Q) store8<IO>(qo, off, t.v[i]);
+            else
+            {
+                if (kd == KIND_K && a.ok) store8<IO>(ko, off, t.v[i]);
+                if (APPEND && t.crow >= 0)
+                    store8<IO>(kd == KIND_K ? a.kc : a.vc, t.crow + (int64_t)t.hidx[i] * a.hd + e0, t.v[i]);
+            }
         }
     };
 
@@ -485,13 +553,25 @@ __global__ __launch_bounds__(256) void k_rope_generic(RopeArgs a, int dt, int mo
     for (int64_t tok = blockIdx.x; tok < a.tokens; tok += gridDim.x)
     {
     fill_sincos(a, token_position(a, (int)tok), cs);
+    const int64_t crow = a.kc ? cache_row(a, tok) : -1;
     __syncthreads();
-    for (int head = 0; head < a.hq + a.hk; ++head)
+    for (int head = 0; head < a.hq + a.hk + a.hv; ++head)
     {
-        const bool isq = head < a.hq;
-        const void* ip = isq ? a.q : a.k;
-        void* op = isq ? a.oq : a.ok;
-        const int64_t off = isq ? tok * a.q_ts + (int64_t)head * a.q_hs : tok * a.k_ts + (int64_t)(head - a.hq) * a.k_hs;
+        const int kind = head_kind(a, head);
+        const bool isq = kind == KIND_Q;
+        const int hkv = head - a.hq - (kind == KIND_V ? a.hk : 0);
+        const void* ip = isq ? a.q : kind == KIND_K ? a.k : a.v;
+        void* op = isq ? a.oq : kind == KIND_K ? a.ok : nullptr;
+        const int64_t off = isq ? tok * a.q_ts + (int64_t)head * a.q_hs
+                                : kind == KIND_K ? tok * a.k_ts + (int64_t)hkv * a.k_hs : tok * a.v_ts + (int64_t)hkv * a.v_hs;
+        void* cp = crow >= 0 && kind != KIND_Q ? (kind == KIND_K ? a.kc : a.vc) : nullptr;
+        const int64_t coff = crow + (int64_t)hkv * a.hd;
+        if (kind == KIND_V)
+        {
+            for (int d = tid; d < a.hd; d += blockDim.x)
+                if (cp) store1(cp, dt, coff + d, load1(ip, dt, off + d));
+            continue;
+        }
         double ss = 0.0;
         for (int d = tid; d < a.hd; d += blockDim.x)
         {
@@ -526,7 +606,11 @@ __global__ __launch_bounds__(256) void k_rope_generic(RopeArgs a, int dt, int mo
             hv[i2] = v2 * cs[t].x + v1 * cs[t].y;
         }
         __syncthreads();
-        for (int d = tid; d < a.hd; d += blockDim.x) store1(op, dt, off + d, hv[d]);
+        for (int d = tid; d < a.hd; d += blockDim.x)
+        {
+            if (op) store1(op, dt, off + d, hv[d]);
+            if (cp) store1(cp, dt, coff + d, hv[d]);
+        }
         __syncthreads();
     }
     }
@@ -537,17 +621,22 @@ static void launch_rope_lph(RopeArgs a, int iters, hipStream_t s)
 {
     const int threads = 256;
     const int64_t per_wg = (int64_t)(threads / LPH) * iters;
-    const int nheads = a.hq + a.hk;
+    const int nheads = a.hq + a.hk + a.hv;
     a.tok_span = (int)((nheads + per_wg - 2) / nheads) + 1;
     const int64_t items = a.tokens * nheads;
     int64_t blocks = (items + per_wg - 1) / per_wg;
     if (blocks > kMaxGridX) blocks = kMaxGridX;
     const size_t lds = (size_t)a.tok_span * (a.R / 2) * sizeof(float2);
+    auto go = [&](auto I) {
+        constexpr int IT = decltype(I)::value;
+        if (a.kc) k_rope<IO, MODE, LPH, IT, NORM, true><<<(unsigned)blocks, threads, lds, s>>>(a);
+        else k_rope<IO, MODE, LPH, IT, NORM, false><<<(unsigned)blocks, threads, lds, s>>>(a);
+    };
     switch (iters)
     {
-        case 1: k_rope<IO, MODE, LPH, 1, NORM><<<(unsigned)blocks, threads, lds, s>>>(a); break;
-        case 2: k_rope<IO, MODE, LPH, 2, NORM><<<(unsigned)blocks, threads, lds, s>>>(a); break;
-        default: k_rope<IO, MODE, LPH, 4, NORM><<<(unsigned)blocks, threads, lds, s>>>(a); break;
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        default: go(std::integral_constant<int, 4>{}); break;
     }
 }
 
@@ -563,19 +652,18 @@ static void launch_rope_tok(RopeArgs a, hipStream_t s)
     int wgs_per_cu = IO::code == DT_F16 ? 0 : 4;
     if (tu.rope_hpl > 0) hpl = tu.rope_hpl;
     if (tu.rope_wgs_per_cu > 0) wgs_per_cu = tu.rope_wgs_per_cu;
-    hpl = hpl <= 2 ? 2 : hpl <= 3 ? 3 : hpl <= 4 ? 4 : hpl <= 6 ? 6 : 8;
+    hpl = hpl <= 2 ? 2 : 3;
     int64_t blocks = (a.tokens + 3) / 4;
     if (wgs_per_cu > 0 && blocks > (int64_t)wgs_per_cu * device_cus()) blocks = (int64_t)wgs_per_cu * device_cus();
     if (blocks > kMaxGridX) blocks = kMaxGridX;
     const size_t lds = 4 * (size_t)(a.R / 2) * sizeof(float2);
-    switch (hpl)
-    {
-        case 2: k_rope_tok<IO, MODE, LPH, 2, NORM><<<(unsigned)blocks, 256, lds, s>>>(a); break;
-        case 3: k_rope_tok<IO, MODE, LPH, 3, NORM><<<(unsigned)blocks, 256, lds, s>>>(a); break;
-        case 4: k_rope_tok<IO, MODE, LPH, 4, NORM><<<(unsigned)blocks, 256, lds, s>>>(a); break;
-        case 6: k_rope_tok<IO, MODE, LPH, 6, NORM><<<(unsigned)blocks, 256, lds, s>>>(a); break;
-        default: k_rope_tok<IO, MODE, LPH, 8, NORM><<<(unsigned)blocks, 256, lds, s>>>(a); break;
-    }
+    auto go = [&](auto H) {
+        constexpr int HP = decltype(H)::value;
+        if (a.kc) k_rope_tok<IO, MODE, LPH, HP, NORM, true><<<(unsigned)blocks, 256, lds, s>>>(a);
+        else k_rope_tok<IO, MODE, LPH, HP, NORM, false><<<(unsigned)blocks, 256, lds, s>>>(a);
+    };
+    if (hpl == 2) go(std::integral_constant<int, 2>{});
+    else go(std::integral_constant<int, 3>{});
 }
 
 // Prefill-sized NeoX launches (a wave per token still gives every CU several waves) take the
@@ -586,30 +674,25 @@ template <class IO, int MODE, int NORM>
 static void launch_rope_vec(const RopeArgs& a, int lph, hipStream_t s)
 {
     const Tuning& tu = tuning();
-    const bool tok_ok = lph == 8 || lph == 16 || lph == 32;
-    if (tok_ok && (tu.rope_tok == 2 || (tu.rope_tok == 0 && MODE == EXL3R_ROPE_NEOX && a.tokens >= 1024)))
+    if constexpr (MODE == EXL3R_ROPE_NEOX)
     {
-        if (lph == 8) launch_rope_tok<IO, MODE, 8, NORM>(a, s);
-        else if (lph == 16) launch_rope_tok<IO, MODE, 16, NORM>(a, s);
-        else launch_rope_tok<IO, MODE, 32, NORM>(a, s);
-        return;
+        if (tu.rope_tok == 2 || (tu.rope_tok == 0 && a.tokens >= 1024))
+        {
+            if (lph == 8) launch_rope_tok<IO, MODE, 8, NORM>(a, s);
+            else if (lph == 16) launch_rope_tok<IO, MODE, 16, NORM>(a, s);
+            else launch_rope_tok<IO, MODE, 32, NORM>(a, s);
+            return;
+        }
     }
-    const int64_t items = a.tokens * (a.hq + a.hk);
+    const int64_t items = a.tokens * (a.hq + a.hk + a.hv);
     const int64_t slots = 256 / lph;
     int iters = 1;
     if (tu.rope_iters == 1 || tu.rope_iters == 2 || tu.rope_iters == 4) iters = tu.rope_iters;
     else if (items >= slots * 4 * 2048) iters = 4;
     else if (items >= slots * 2 * 2048) iters = 2;
-    switch (lph)
-    {
-        case 1: launch_rope_lph<IO, MODE, 1, NORM>(a, iters, s); break;
-        case 2: launch_rope_lph<IO, MODE, 2, NORM>(a, iters, s); break;
-        case 4: launch_rope_lph<IO, MODE, 4, NORM>(a, iters, s); break;
-        case 8: launch_rope_lph<IO, MODE, 8, NORM>(a, iters, s); break;
-        case 16: launch_rope_lph<IO, MODE, 16, NORM>(a, iters, s); break;
-        case 32: launch_rope_lph<IO, MODE, 32, NORM>(a, iters, s); break;
-        default: launch_rope_lph<IO, MODE, 64, NORM>(a, iters, s); break;
-    }
+    if (lph == 8) launch_rope_lph<IO, MODE, 8, NORM>(a, iters, s);
+    else if (lph == 16) launch_rope_lph<IO, MODE, 16, NORM>(a, iters, s);
+    else launch_rope_lph<IO, MODE, 32, NORM>(a, iters, s);
 }
 
 template <class IO>
@@ -623,6 +706,80 @@ static void launch_rope_io(const RopeArgs& a, int mode, int norm, int lph, hipSt
     };
     if (mode == EXL3R_ROPE_GPTJ) go(std::integral_constant<int, EXL3R_ROPE_GPTJ>{});
     else go(std::integral_constant<int, EXL3R_ROPE_NEOX>{});
+}
+
+// Argument checks and RopeArgs of the rotary part, shared by exl3r_rope and exl3r_rope_paged_kv.
+// Returns EXL3R_OK with a.tokens == 0 when there is nothing to launch.
+static int rope_prepare(const char* op, RopeArgs& a, const void* q, void* out_q, int64_t q_tok_stride,
+                        int64_t q_head_stride, int num_heads_q, const void* k, void* out_k, bool out_k_optional,
+                        int64_t k_tok_stride, int64_t k_head_stride, int num_heads_k, int dtype, int64_t bsz,
+                        int64_t seq_len, int head_dim, const float* inv_freq, int rotary_dim, int32_t position,
+                        const int32_t* positions, const int32_t* position_ids, const void* q_norm, const void* k_norm,
+                        int norm_dtype, float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor)
+{
+    if (!inv_freq) return set_error(EXL3R_EINVAL, "%s: inv_freq must be non-null", op);
+    if (dtype != EXL3R_F16 && dtype != EXL3R_BF16)
+        return set_error(EXL3R_EDTYPE, "%s: q/k dtype must be f16 or bf16, got %s", op, dtype_name(dtype));
+    if (rope_mode != EXL3R_ROPE_GPTJ && rope_mode != EXL3R_ROPE_NEOX)
+        return set_error(EXL3R_EINVAL, "%s: rope_mode must be GPTJ (1) or NEOX (2), got %d", op, rope_mode);
+    if (bsz < 0 || seq_len < 0 || num_heads_q <= 0 || (k && num_heads_k <= 0))
+        return set_error(EXL3R_EINVAL, "%s: invalid shape bsz=%lld seq_len=%lld heads=(%d,%d)", op, (long long)bsz,
+                         (long long)seq_len, num_heads_q, num_heads_k);
+    if (head_dim <= 0 || head_dim % 2 || head_dim > 4096)
+        return set_error(EXL3R_EINVAL, "%s: head_dim %d must be even and in [2, 4096]", op, head_dim);
+    if (rotary_dim < 2 || rotary_dim % 2 || rotary_dim > head_dim)
+        return set_error(EXL3R_EINVAL, "%s: rotary_dim %d must be even and in [2, head_dim]", op, rotary_dim);
+    if (q_head_stride < head_dim || q_tok_stride < (int64_t)num_heads_q * q_head_stride)
+        return set_error(EXL3R_EINVAL, "%s: q strides (%lld, %lld) overlap heads", op, (long long)q_tok_stride, (long long)q_head_stride);
+    if (k && ((bsz * seq_len > 0 && !out_k && !out_k_optional) || k_head_stride < head_dim ||
+              k_tok_stride < (int64_t)num_heads_k * k_head_stride))
+        return set_error(EXL3R_EINVAL, "%s: k needs out_k and non-overlapping strides", op);
+    if (positions && position_ids) return set_error(EXL3R_EINVAL, "%s: at most one of positions / position_ids", op);
+    if (q_norm && k && !k_norm) return set_error(EXL3R_EINVAL, "%s: q_norm given without k_norm", op);
+    if (!q_norm && k_norm) return set_error(EXL3R_EINVAL, "%s: k_norm given without q_norm", op);
+    if (q_norm && !is_float_dtype(norm_dtype))
+        return set_error(EXL3R_EDTYPE, "%s: unsupported norm weight dtype %s", op, dtype_name(norm_dtype));
+    const int64_t tokens = bsz * seq_len;
+    a = RopeArgs{};
+    if (tokens == 0) return EXL3R_OK;
+    if (!q || !out_q) return set_error(EXL3R_EINVAL, "%s: q and out_q must be non-null", op);
+    if (tokens > 0x7fffffff) return set_error(EXL3R_EINVAL, "%s: too many tokens", op);
+
+    a.q = q; a.oq = out_q; a.k = k; a.ok = out_k;
+    a.q_ts = q_tok_stride; a.q_hs = q_head_stride; a.k_ts = k_tok_stride; a.k_hs = k_head_stride;
+    a.hq = num_heads_q; a.hk = k ? num_heads_k : 0; a.hd = head_dim; a.R = rotary_dim;
+    a.seq_len = seq_len; a.tokens = tokens; a.inv_freq = inv_freq;
+    a.position = position; a.positions = positions; a.position_ids = position_ids;
+    a.qw = q_norm; a.kw = k_norm; a.wt = norm_dtype;
+    a.eps = norm_eps; a.cb = norm_constant_bias; a.attn = attn_factor;
+    a.inv_hd = (head_dim & (head_dim - 1)) == 0 ? 1.0f / (float)head_dim : 0.0f;
+    return EXL3R_OK;
+}
+
+static int rope_dispatch(const char* op, const RopeArgs& a, int dtype, int rope_mode, void* stream)
+{
+    const int norm = !a.qw ? NORM_NONE : (a.wt == EXL3R_F16 && dtype == EXL3R_F16) ? NORM_HALF : NORM_F32;
+    hipStream_t s = (hipStream_t)stream;
+    auto a16 = [](const void* p) { return p == nullptr || aligned16(p); };
+    int lph = 1;
+    while (lph * 8 < a.hd) lph *= 2;
+    // Vector kernels: 8-element lane chunks, 8 to 32 lanes per head (head_dim 64 .. 256).
+    bool vec = a.hd % 8 == 0 && lph >= 8 && lph <= 32 && a.R % (rope_mode == EXL3R_ROPE_NEOX ? 16 : 2) == 0;
+    vec = vec && aligned16(a.q) && aligned16(a.oq) && a.q_ts % 8 == 0 && a.q_hs % 8 == 0;
+    vec = vec && (!a.k || (aligned16(a.k) && a16(a.ok) && a.k_ts % 8 == 0 && a.k_hs % 8 == 0));
+    vec = vec && (!a.v || (aligned16(a.v) && a.v_ts % 8 == 0 && a.v_hs % 8 == 0 && a16(a.kc) && a16(a.vc)));
+    vec = vec && (!a.qw || (aligned16(a.qw) && a16(a.kw)));
+    if (vec)
+    {
+        if (dtype == EXL3R_F16) launch_rope_io<TF16>(a, rope_mode, norm, lph, s);
+        else launch_rope_io<TBF16>(a, rope_mode, norm, lph, s);
+    }
+    else
+    {
+        const size_t lds = (size_t)(a.R / 2) * sizeof(float2) + (size_t)a.hd * sizeof(float);
+        k_rope_generic<<<(unsigned)(a.tokens < kMaxGridX ? a.tokens : kMaxGridX), 256, lds, s>>>(a, dtype, rope_mode, norm);
+    }
+    return launch_status(op);
 }
 
 }  // namespace exl3r
@@ -639,59 +796,51 @@ extern "C" int exl3r_rope(const void* q, void* out_q, int64_t q_tok_stride, int6
                           void* stream)
 {
     const char* op = "exl3r_rope";
-    if (!inv_freq) return set_error(EXL3R_EINVAL, "%s: inv_freq must be non-null", op);
-    if (dtype != EXL3R_F16 && dtype != EXL3R_BF16)
-        return set_error(EXL3R_EDTYPE, "%s: q/k dtype must be f16 or bf16, got %s", op, dtype_name(dtype));
-    if (rope_mode != EXL3R_ROPE_GPTJ && rope_mode != EXL3R_ROPE_NEOX)
-        return set_error(EXL3R_EINVAL, "%s: rope_mode must be GPTJ (1) or NEOX (2), got %d", op, rope_mode);
-    if (bsz < 0 || seq_len < 0 || num_heads_q <= 0 || (k && num_heads_k <= 0))
-        return set_error(EXL3R_EINVAL, "%s: invalid shape bsz=%lld seq_len=%lld heads=(%d,%d)", op, (long long)bsz,
-                         (long long)seq_len, num_heads_q, num_heads_k);
-    if (head_dim <= 0 || head_dim % 2 || head_dim > 4096)
-        return set_error(EXL3R_EINVAL, "%s: head_dim %d must be even and in [2, 4096]", op, head_dim);
-    if (rotary_dim < 2 || rotary_dim % 2 || rotary_dim > head_dim)
-        return set_error(EXL3R_EINVAL, "%s: rotary_dim %d must be even and in [2, head_dim]", op, rotary_dim);
-    if (q_head_stride < head_dim || q_tok_stride < (int64_t)num_heads_q * q_head_stride)
-        return set_error(EXL3R_EINVAL, "%s: q strides (%lld, %lld) overlap heads", op, (long long)q_tok_stride, (long long)q_head_stride);
-    if (k && ((bsz * seq_len > 0 && !out_k) || k_head_stride < head_dim || k_tok_stride < (int64_t)num_heads_k * k_head_stride))
-        return set_error(EXL3R_EINVAL, "%s: k needs out_k and non-overlapping strides", op);
-    if (positions && position_ids) return set_error(EXL3R_EINVAL, "%s: at most one of positions / position_ids", op);
-    if (q_norm && k && !k_norm) return set_error(EXL3R_EINVAL, "%s: q_norm given without k_norm", op);
-    if (!q_norm && k_norm) return set_error(EXL3R_EINVAL, "%s: k_norm given without q_norm", op);
-    if (q_norm && !is_float_dtype(norm_dtype))
-        return set_error(EXL3R_EDTYPE, "%s: unsupported norm weight dtype %s", op, dtype_name(norm_dtype));
-    const int64_t tokens = bsz * seq_len;
-    if (tokens == 0) return EXL3R_OK;
-    if (!q || !out_q) return set_error(EXL3R_EINVAL, "%s: q and out_q must be non-null", op);
-    if (tokens > 0x7fffffff) return set_error(EXL3R_EINVAL, "%s: too many tokens", op);
+    RopeArgs a;
+    const int rc = rope_prepare(op, a, q, out_q, q_tok_stride, q_head_stride, num_heads_q, k, out_k, false, k_tok_stride,
+                                k_head_stride, num_heads_k, dtype, bsz, seq_len, head_dim, inv_freq, rotary_dim, position,
+                                positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias,
+                                rope_mode, attn_factor);
+    if (rc || a.tokens == 0) return rc;
+    return rope_dispatch(op, a, dtype, rope_mode, stream);
+}
 
-    RopeArgs a{};
-    a.q = q; a.oq = out_q; a.k = k; a.ok = out_k;
-    a.q_ts = q_tok_stride; a.q_hs = q_head_stride; a.k_ts = k_tok_stride; a.k_hs = k_head_stride;
-    a.hq = num_heads_q; a.hk = k ? num_heads_k : 0; a.hd = head_dim; a.R = rotary_dim;
-    a.seq_len = seq_len; a.tokens = tokens; a.inv_freq = inv_freq;
-    a.position = position; a.positions = positions; a.position_ids = position_ids;
-    a.qw = q_norm; a.kw = k_norm; a.wt = norm_dtype;
-    a.eps = norm_eps; a.cb = norm_constant_bias; a.attn = attn_factor;
-    a.inv_hd = (head_dim & (head_dim - 1)) == 0 ? 1.0f / (float)head_dim : 0.0f;
-    const int norm = !q_norm ? NORM_NONE : (norm_dtype == EXL3R_F16 && dtype == EXL3R_F16) ? NORM_HALF : NORM_F32;
-    hipStream_t s = (hipStream_t)stream;
-
-    int lph = 1;
-    while (lph * 8 < head_dim) lph *= 2;
-    bool vec = head_dim % 8 == 0 && lph <= 64 && rotary_dim % (rope_mode == EXL3R_ROPE_NEOX ? 16 : 2) == 0;
-    vec = vec && aligned16(q) && aligned16(out_q) && q_tok_stride % 8 == 0 && q_head_stride % 8 == 0;
-    vec = vec && (!k || (aligned16(k) && aligned16(out_k) && k_tok_stride % 8 == 0 && k_head_stride % 8 == 0));
-    vec = vec && (!q_norm || (aligned16(q_norm) && (!k_norm || aligned16(k_norm))));
-    if (vec)
-    {
-        if (dtype == EXL3R_F16) launch_rope_io<TF16>(a, rope_mode, norm, lph, s);
-        else launch_rope_io<TBF16>(a, rope_mode, norm, lph, s);
-    }
-    else
-    {
-        const size_t lds = (size_t)(rotary_dim / 2) * sizeof(float2) + (size_t)head_dim * sizeof(float);
-        k_rope_generic<<<(unsigned)(tokens < kMaxGridX ? tokens : kMaxGridX), 256, lds, s>>>(a, dtype, rope_mode, norm);
-    }
-    return launch_status(op);
+extern "C" int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride,
+                                   int num_heads_q, const void* k, void* out_k, int64_t k_tok_stride,
+                                   int64_t k_head_stride, const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                                   int num_heads_kv, int dtype, int64_t bsz, int64_t seq_len, int head_dim,
+                                   const float* inv_freq, int rotary_dim,
+                                   int32_t position, const int32_t* positions, const int32_t* position_ids,
+                                   const void* q_norm, const void* k_norm, int norm_dtype,
+                                   float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
+                                   void* k_cache, void* v_cache, int page_size, int64_t num_pages,
+                                   const int32_t* block_table, int64_t max_blocks_per_seq,
+                                   const int32_t* cache_seqlens, int32_t* err_flag, void* stream)
+{
+    const char* op = "exl3r_rope_paged_kv";
+    if (num_heads_kv <= 0) return set_error(EXL3R_EINVAL, "%s: num_heads_kv must be positive", op);
+    if (page_size <= 0 || (page_size & (page_size - 1)) || num_pages <= 0 || max_blocks_per_seq <= 0)
+        return set_error(EXL3R_EINVAL, "%s: page_size %d must be a power of two, num_pages and max_blocks_per_seq positive",
+                         op, page_size);
+    if (v_head_stride < head_dim || v_tok_stride < (int64_t)num_heads_kv * v_head_stride)
+        return set_error(EXL3R_EINVAL, "%s: v strides (%lld, %lld) overlap heads", op, (long long)v_tok_stride,
+                         (long long)v_head_stride);
+    if (num_pages > ((int64_t)1 << 62) / ((int64_t)page_size * num_heads_kv * (head_dim > 0 ? head_dim : 1)))
+        return set_error(EXL3R_EINVAL, "%s: cache too large", op);
+    if (bsz > 0 && seq_len > 0 && (!k || !v || !k_cache || !v_cache || !block_table || !cache_seqlens))
+        return set_error(EXL3R_EINVAL, "%s: k, v, k_cache, v_cache, block_table and cache_seqlens must be non-null", op);
+    RopeArgs a;
+    const int rc = rope_prepare(op, a, q, out_q, q_tok_stride, q_head_stride, num_heads_q, k, out_k, true, k_tok_stride,
+                                k_head_stride, num_heads_kv, dtype, bsz, seq_len, head_dim, inv_freq, rotary_dim, position,
+                                positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias,
+                                rope_mode, attn_factor);
+    if (rc || a.tokens == 0) return rc;
+    a.v = v; a.v_ts = v_tok_stride; a.v_hs = v_head_stride; a.hv = num_heads_kv;
+    a.kc = k_cache; a.vc = v_cache;
+    int lg = 0;
+    while ((1 << lg) < page_size) ++lg;
+    a.page_log2 = lg;
+    a.pages = num_pages; a.max_blocks = max_blocks_per_seq;
+    a.block_table = block_table; a.cache_seqlens = cache_seqlens; a.err = err_flag;
+    return rope_dispatch(op, a, dtype, rope_mode, stream);
 }

@@ -125,6 +125,49 @@ def rope(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm
                             norm_eps, norm_constant_bias, rope_mode, attn_factor, _stream(q, stream)))
 
 
+def rope_paged_kv(q, out_q, k, out_k, v, inv_freq, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias,
+                  rope_mode, attn_factor, k_cache, v_cache, block_table, cache_seqlens, position_ids=None,
+                  err_flag=None, stream=None):
+    """rope() on q and k fused with the paged KV-cache append that follows it (paged_kv_cache_update):
+    the roped k (also written to out_k unless it is None) and v go to k_cache / v_cache
+    [pages, page_size, kv_heads, head_dim] at cache_seqlens[b] + s through block_table
+    (int32 [bsz, max_blocks])."""
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be (bsz, seq_len, heads, head_dim)")
+    bsz, seq, hq, hd = q.shape
+    hk = k.shape[2]
+    if k.shape != v.shape or k.shape[0] != bsz or k.shape[1] != seq or k.shape[3] != hd:
+        raise ValueError("k and v must be (bsz, seq_len, kv_heads, head_dim) like q")
+    if q.stride(3) != 1 or out_q.stride() != q.stride() or out_q.shape != q.shape:
+        raise ValueError("q innermost dim must be dense and out_q must share q's layout")
+    for t in (k, v) + ((out_k,) if out_k is not None else ()):
+        if t.stride(3) != 1 or (seq > 1 and bsz > 1 and t.stride(0) != seq * t.stride(1)):
+            raise ValueError("k / v / out_k: dense innermost dim and batch stride seq_len * token stride")
+    if out_k is not None and out_k.stride() != k.stride():
+        raise ValueError("out_k must share k's layout")
+    if seq > 1 and bsz > 1 and q.stride(0) != seq * q.stride(1):
+        raise ValueError("q batch stride must be seq_len * token stride")
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or k_cache.shape[2:] != (hk, hd) or not k_cache.is_contiguous() \
+            or not v_cache.is_contiguous():
+        raise ValueError("caches must be contiguous (pages, page_size, kv_heads, head_dim)")
+    if block_table.dim() != 2 or block_table.dtype != torch.int32 or cache_seqlens.dtype != torch.int32:
+        raise TypeError("block_table (bsz, max_blocks) and cache_seqlens (bsz) must be int32")
+    for t in (positions, position_ids):
+        if t is not None and t.dtype != torch.int32:
+            raise TypeError("positions / position_ids must be int32")
+    nw = q_norm if q_norm is not None else k_norm
+    check(load().exl3r_rope_paged_kv(_ptr(q), _ptr(out_q), q.stride(1), q.stride(2), hq,
+                                     _ptr(k), _ptr(out_k), k.stride(1), k.stride(2),
+                                     _ptr(v), v.stride(1), v.stride(2), hk,
+                                     dtype_code(q), bsz, seq, hd, _ptr(inv_freq), inv_freq.shape[-1] * 2,
+                                     int(position), _ptr(positions), _ptr(position_ids),
+                                     _ptr(q_norm), _ptr(k_norm), dtype_code(nw) if nw is not None else F16,
+                                     norm_eps, norm_constant_bias, rope_mode, attn_factor,
+                                     _ptr(k_cache), _ptr(v_cache), k_cache.shape[1], k_cache.shape[0],
+                                     _ptr(block_table), block_table.shape[1], _ptr(cache_seqlens),
+                                     _ptr(err_flag), _stream(q, stream)))
+
+
 def embedding(table, ids, out, err_flag=None, stream=None):
     """out[i] = table[ids[i]] (bit-exact, or exact upcast to f32)."""
     vocab, hidden = table.shape

@@ -26,6 +26,8 @@
  *   exl3r_silu_mul          <- exl3_shim_silu_mul         csrc/exl3_shim.cpp:151     (ffi.rs:125, 492-495)
  *   exl3r_gelu_mul          <- exl3_shim_gelu_mul         csrc/exl3_shim.cpp:152     (ffi.rs:126, 496-499)
  *   exl3r_rope              <- exl3_shim_rope             csrc/exl3_shim.cpp:87-98   (ffi.rs:51-65, 298-333)
+ *   exl3r_rope_paged_kv     <- exl3_shim_rope followed by exl3_shim_paged_kv_cache_update
+ *                              csrc/exl3_shim.cpp:87-98, 109-112 (ffi.rs:298-350; call sites modules.rs:666-704)
  *   exl3r_embedding         <- Embedding::forward's tch index_select + to_kind   src/modules.rs:430-436
  *   exl3r_embedding_rms_norm<- embed followed by RmsNorm::forward (MTP head)    src/mtp.rs:189-190
  */
@@ -130,7 +132,8 @@ EXL3R_API int exl3r_gelu_mul(const void* x, const void* y, int in_dtype, void* z
  *   q_norm, k_norm: [head_dim] contiguous norm weights of norm_dtype (F16/BF16/F32) or NULL.  A
  *             norm is applied iff q_norm != NULL; then k_norm is required when k != NULL.
  *   rope_mode: EXL3R_ROPE_GPTJ (pairs 2t, 2t+1) or EXL3R_ROPE_NEOX (pairs t, t + rotary_dim/2).
- *   sin and cos are computed in fp32 from angle = inv_freq[t] * (float)pos and scaled by attn_factor.
+ *   sin and cos of angle = fl32(inv_freq[t] * (float)pos) are evaluated in double precision, rounded
+ *   once to fp32 and scaled by attn_factor (supported for |angle| < 2^52).
  */
 EXL3R_API int exl3r_rope(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int num_heads_q,
                const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int num_heads_k,
@@ -141,6 +144,36 @@ EXL3R_API int exl3r_rope(const void* q, void* out_q, int64_t q_tok_stride, int64
                float norm_eps, float norm_constant_bias,
                int rope_mode, float attn_factor,
                void* stream);
+
+/*
+ * exl3r_rope fused with the paged KV-cache append that follows it in paged attention
+ * (Attention::forward, src/modules.rs:666-704: rope in place, then paged_kv_cache_update,
+ * kernels/generator/cache.cu:143-243):
+ *   q, k: as exl3r_rope (q -> out_q); the roped k heads are written to out_k when out_k != NULL
+ *         (may equal k) and, for each token, to k_cache;
+ *   v:    [bsz, seq_len, num_heads_kv, head_dim] of dtype, row (b*seq_len + s)*v_tok_stride +
+ *         h*v_head_stride, copied unchanged to v_cache;
+ *   k_cache, v_cache: contiguous [num_pages, page_size, num_heads_kv, head_dim] of dtype; token s of
+ *         sequence b goes to page block_table[b*max_blocks_per_seq + pos / page_size], row
+ *         pos % page_size, with pos = cache_seqlens[b] + s (int32 device arrays).  page_size is a
+ *         power of two (the reference's pages hold 256 tokens).
+ *   err_flag: NULL or a device int32; a token whose pos is negative or past the block table, or whose
+ *         page is outside [0, num_pages), is not appended and 1 is stored to *err_flag (the
+ *         reference does not check).  k heads are still written to out_k.
+ * The rotary position arguments are independent of cache_seqlens (the paged path passes the same
+ * per-sequence lengths to both: positions = cache_seqlens).
+ */
+EXL3R_API int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int num_heads_q,
+                        const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride,
+                        const void* v, int64_t v_tok_stride, int64_t v_head_stride, int num_heads_kv,
+                        int dtype, int64_t bsz, int64_t seq_len, int head_dim,
+                        const float* inv_freq, int rotary_dim,
+                        int32_t position, const int32_t* positions, const int32_t* position_ids,
+                        const void* q_norm, const void* k_norm, int norm_dtype,
+                        float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
+                        void* k_cache, void* v_cache, int page_size, int64_t num_pages,
+                        const int32_t* block_table, int64_t max_blocks_per_seq, const int32_t* cache_seqlens,
+                        int32_t* err_flag, void* stream);
 
 /*
  * Token-embedding gather: out[i, :] = table[ids[i], :], bit-exact (same dtype) or exactly upcast to

@@ -28,6 +28,8 @@ _PROTOS = {
     "oracle_rope": (_i, [_vp, _vp, _i64, _i64, _i, _vp, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _i,
                          _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _i]),
     "oracle_embedding": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _i64, _vp, _i]),
+    "oracle_paged_kv_append": (_i, [_vp, _i64, _i64, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _vp, _i, _i64,
+                                    _vp, _i64, _vp, _vp, _i]),
     "oracle_embedding_rms_norm": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _i64, _vp, _i,
                                        _vp, _i, _i64, _f, _f, _f, _vp, _i]),
 }
@@ -144,6 +146,24 @@ def embedding(table, tt, ids, idt, ot, nthreads=1):
     _check(load().oracle_embedding(_p(table), tt, vocab, hidden, hidden, _p(ids), idt, n, _p(out), ot, hidden,
                                    _p(err), nthreads), "oracle_embedding")
     return out, int(err[0])
+
+
+def paged_kv_append(k, v, dt, k_cache, v_cache, block_table, cache_seqlens, nthreads=1):
+    """k, v: [bsz, seq, hk, hd] storage arrays (either may be None); k_cache / v_cache:
+    [pages, page_size, hk, hd], updated in place; block_table int32 [bsz, max_blocks];
+    cache_seqlens int32 [bsz].  Returns the error flag."""
+    src = k if k is not None else v
+    bsz, seq, hk, hd = src.shape
+    pages, page_size = (k_cache if k_cache is not None else v_cache).shape[:2]
+    bt = np.ascontiguousarray(block_table, np.int32)
+    cl = np.ascontiguousarray(cache_seqlens, np.int32)
+    err = np.zeros(1, np.int32)
+    k = None if k is None else np.ascontiguousarray(k)
+    v = None if v is None else np.ascontiguousarray(v)
+    _check(load().oracle_paged_kv_append(_p(k), hk * hd, hd, _p(v), hk * hd, hd, hk, dt, bsz, seq, hd,
+                                         _p(k_cache), _p(v_cache), page_size, pages, _p(bt), bt.shape[1], _p(cl),
+                                         _p(err), nthreads), "oracle_paged_kv_append")
+    return int(err[0])
 
 
 def embedding_rms_norm(table, tt, ids, idt, w, wt, yt, ht=None, eps=1e-6, cb=0.0, cs=1.0, nthreads=1):

@@ -435,6 +435,40 @@ static size_t dsize(int dt) { return dt == OR_F32 ? 4 : 2; }
 
 static int exact_conv(int from, int to) { return from == to || to == OR_F32; }
 
+/* kernels/generator/cache.cu:159-183 (index arithmetic), 186-243 (shape rules) */
+int oracle_paged_kv_append(const void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                           const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                           int hk, int dt, int64_t bsz, int64_t seq_len, int hd,
+                           void* k_cache, void* v_cache, int page_size, int64_t num_pages,
+                           const int32_t* block_table, int64_t max_blocks, const int32_t* cache_seqlens,
+                           int32_t* err_flag, int nthreads)
+{
+    if (dt != OR_F16 && dt != OR_BF16) return -2;
+    if (hk <= 0 || hd <= 0 || page_size <= 0 || num_pages <= 0 || max_blocks <= 0 || bsz < 0 || seq_len < 0) return -1;
+    if (!block_table || !cache_seqlens || (k && !k_cache) || (v && !v_cache)) return -1;
+    const size_t row = (size_t)hd * 2;
+    int bad = 0;
+    #pragma omp parallel for num_threads(nthr(nthreads)) reduction(|:bad) schedule(static)
+    for (int64_t tok = 0; tok < bsz * seq_len; ++tok)
+    {
+        const int64_t b = tok / seq_len, s = tok % seq_len;
+        int64_t pos = (int64_t)cache_seqlens[b] + s;
+        if (oracle_mutation == ORM_PAGE_OFF) pos += 1;
+        const int64_t lb = pos >= 0 ? pos / page_size : -1;
+        const int64_t page = (lb >= 0 && lb < max_blocks) ? (int64_t)block_table[b * max_blocks + lb] : -1;
+        if (page < 0 || page >= num_pages) { bad = 1; continue; }
+        const int64_t dst_tok = page * page_size + pos % page_size;
+        for (int h = 0; h < hk; ++h)
+        {
+            const int64_t dst = (dst_tok * hk + h) * hd;
+            if (k) memcpy((char*)k_cache + dst * 2, (const char*)k + (tok * k_tok_stride + h * k_head_stride) * 2, row);
+            if (v) memcpy((char*)v_cache + dst * 2, (const char*)v + (tok * v_tok_stride + h * v_head_stride) * 2, row);
+        }
+    }
+    if (bad && err_flag) *err_flag = 1;
+    return 0;
+}
+
 int oracle_embedding(const void* table, int tt, int64_t vocab, int64_t hidden, int64_t ldt,
                      const void* ids, int idt, int64_t n, void* out, int ot, int64_t ldo,
                      int32_t* err_flag, int nthreads)

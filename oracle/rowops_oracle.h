@@ -54,6 +54,7 @@ extern int oracle_mutation;
 #define ORM_HEADNORM_1ROUND  13  /* f16-weight head norm rounded once instead of twice */
 #define ORM_EMBED_OFF        14  /* gathers row ids[i] + 1 */
 #define ORM_ROPE_NORM_AFTER  15  /* head norm applied after the rotation */
+#define ORM_PAGE_OFF         16  /* paged append writes one row past the cache position */
 
 /* Conversions (round to nearest even; NaN -> canonical quiet NaN). */
 uint16_t oracle_f32_to_f16(float f);
@@ -84,6 +85,22 @@ int oracle_rope(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head
                 const void* q_norm, const void* k_norm, int norm_dtype,
                 float norm_eps, float norm_constant_bias,
                 int rope_mode, float attn_factor, int nthreads);
+
+/*
+ * Paged KV-cache append (paged_kv_update_vec8_kernel, reference kernels/generator/cache.cu:143-243):
+ * for each sequence b, token s and kv head h, with pos = cache_seqlens[b] + s,
+ *   k_cache[page, pos % page_size, h, :] = k[b, s, h, :]   (v likewise),
+ *   page = block_table[b * max_blocks + pos / page_size].
+ * Caches are contiguous [num_pages, page_size, num_heads_kv, head_dim] of k's dtype (F16 / BF16).
+ * A position outside the block table or a page outside the pool is skipped and sets *err_flag
+ * (the reference does not check them).  k or v may be NULL (that cache is not written).
+ */
+int oracle_paged_kv_append(const void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                           const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                           int num_heads_kv, int dtype, int64_t bsz, int64_t seq_len, int head_dim,
+                           void* k_cache, void* v_cache, int page_size, int64_t num_pages,
+                           const int32_t* block_table, int64_t max_blocks, const int32_t* cache_seqlens,
+                           int32_t* err_flag, int nthreads);
 
 int oracle_embedding(const void* table, int table_dtype, int64_t vocab, int64_t hidden, int64_t ldt,
                      const void* ids, int ids_dtype, int64_t n,

@@ -140,3 +140,25 @@ def test_zero_size_calls_accept_null_data():
     assert lib.exl3r_embedding(FAKE, BF16, 10, 16, 16, None, I64, 0, None, F32, 16, None, None) == exl3r.OK
     assert lib.exl3r_embedding_rms_norm(FAKE, BF16, 10, 16, 16, None, I64, 0, None, BF16, 16, None, BF16,
                                         None, BF16, 16, 1e-6, 0.0, 1.0, None, None) == exl3r.OK
+
+
+def test_rope_paged_kv_validation():
+    lib = exl3r.load()
+    inv, kc, vc, bt, sl = FAKE + 131072, FAKE + 262144, FAKE + 393216, FAKE + 524288, FAKE + 528384
+
+    def call(**kw):
+        a = dict(q=FAKE, oq=FAKE, qts=4 * 64, qhs=64, hq=4, k=FAKE + 65536, ok=None, kts=2 * 64, khs=64,
+                 v=FAKE + 98304, vts=2 * 64, vhs=64, hkv=2, dt=F16, bsz=1, seq=3, hd=64, inv=inv, R=64, pos=0,
+                 positions=None, ids=None, qn=None, kn=None, nwt=F16, eps=1e-6, cb=0.0, mode=exl3r.ROPE_NEOX, attn=1.0,
+                 kc=kc, vc=vc, page=256, pages=4, bt=bt, mb=2, sl=sl, err=None)
+        a.update(kw)
+        return lib.exl3r_rope_paged_kv(*a.values(), None)
+    assert call(page=100) == exl3r.EINVAL
+    assert call(pages=0) == exl3r.EINVAL
+    assert call(v=None) == exl3r.EINVAL
+    assert call(kc=None) == exl3r.EINVAL
+    assert call(bt=None) == exl3r.EINVAL
+    assert call(vhs=32) == exl3r.EINVAL
+    assert call(dt=F32) == exl3r.EDTYPE
+    assert call(hkv=0) == exl3r.EINVAL
+    assert call(q=None, oq=None, k=None, v=None, kc=None, vc=None, bt=None, sl=None, seq=0) == exl3r.OK

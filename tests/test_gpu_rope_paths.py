@@ -1,8 +1,8 @@
-"""Both vector RoPE kernels (the wave-per-token prefill kernel and the flattened kernel) forced
-through the launch-shape hook on the same cases, each checked against the CPU oracle: every batch
-width and grid shape of the prefill kernel, head dims 64 / 128 / 256, partial rotary, q only,
-packed strides and every position source, so parity does not depend on which kernel the size
-heuristic picks."""
+"""Both vector RoPE kernels (the wave-per-token NeoX prefill kernel and the flattened kernel)
+forced through the launch-shape hook on the same cases, each checked against the CPU oracle: every
+batch width and grid shape of the prefill kernel, head dims 64 / 128 / 256, partial rotary, q only,
+strided rows and every position source, so parity does not depend on which kernel the size
+heuristic picks (GPT-J always takes the flattened kernel)."""
 import ctypes
 
 import numpy as np
@@ -28,7 +28,7 @@ def tune():
     lib.exl3r_tune_rope_tok(0, 0, 0)
 
 
-@pytest.mark.parametrize("hpl,wpc", [(2, 0), (3, 0), (4, 0), (6, 0), (8, 0), (2, 1), (3, 4)])
+@pytest.mark.parametrize("hpl,wpc", [(2, 0), (3, 0), (2, 1), (3, 1), (2, 4), (3, 4)])
 def test_prefill_kernel_batches_and_grids(tune, hpl, wpc):
     tune(2, hpl, wpc)
     rng = np.random.default_rng(hpl * 10 + wpc)
