@@ -31,7 +31,8 @@ sys.path.insert(0, os.path.join(ROOT, "exllamav3-rs_amd"))
 PEAK_GBS = 8000.0            # MI355X HBM3E
 METRIC = "fused norm/act/RoPE/embed HBM GB/s + % of MI355X peak; decode-step us"
 OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "gather_norm_c5", "rms_c1",
-       "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "calib_copy", "calib_copy_cached"]
+       "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "rope_kv_prefill",
+       "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "calib_copy", "calib_copy_cached"]
 
 
 def log(*a):
@@ -185,6 +186,45 @@ def make_gather(name, vocab, hidden, n, dt, out_dt, ids, seed, norm=False):
     return Work(name, nbytes, launch, desc, sets)
 
 
+def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64):
+    """q/k head-norm + NeoX RoPE followed by the paged KV-cache append (64 q / 8 kv heads of 128, f16,
+    256-token pages, positions = cache lengths): one fused exl3r_rope_paged_kv launch, or exl3r_rope
+    then a separate append kernel (the reference's two launches)."""
+    import numpy as np
+    import torch
+    import exl3r
+    import exl3r.ffi as ffi
+    hq, hk, hd, page = 64, 8, 128, 256
+    T = bsz * seq
+    # fused-op bytes: q, k read + written in place, v read, both cache rows written, positions
+    nbytes = 2 * T * hq * hd * 2 + 2 * T * hk * hd * 2 + T * hk * hd * 2 + 2 * T * hk * hd * 2 + 4 * bsz + 2 * hd * 2
+    sets = sets_for(nbytes)
+    rng = np.random.default_rng(seed)
+    pages = bsz * max_blocks + 4
+    bt = torch.from_numpy(rng.permutation(pages)[: bsz * max_blocks].reshape(bsz, max_blocks).astype(np.int32)).cuda()
+    sl = torch.from_numpy(rng.integers(0, max_blocks * page - seq, bsz).astype(np.int32)).cuda()
+    kc = torch.empty((pages, page, hk, hd), device="cuda", dtype=torch.float16)
+    vc = torch.empty_like(kc)
+    inv = torch.from_numpy((1.0 / 1e6 ** (np.arange(0, hd, 2, dtype=np.float64) / hd)).astype(np.float32)).cuda()
+    qn, kn = gen((hd,), 1.0, 0.1, torch.float16, seed + 1), gen((hd,), 1.0, 0.1, torch.float16, seed + 2)
+    bufs = [tuple(gen((bsz, seq, h, hd), 0.0, 1.0, torch.float16, seed + 10 * j + i) for i, h in enumerate((hq, hk, hk)))
+            for j in range(sets)]
+    naive = exl3r.load_naive()
+
+    def launch(i):
+        q, k, v = bufs[i % sets]
+        if fused:
+            ffi.rope_paged_kv(q, q, k, k, v, inv, 0, sl, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, kc, vc, bt, sl)
+        else:
+            ffi.rope(q, q, k, k, inv, 0, sl, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0)
+            rc = naive.naive_paged_kv_update_f16(k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(),
+                                                 sl.data_ptr(), bsz, seq, hk, hd, max_blocks, page,
+                                                 torch.cuda.current_stream().cuda_stream)
+            assert rc == 0
+    kind = "fused (1 launch)" if fused else "rope + separate append (2 launches)"
+    return Work(name, nbytes, launch, f"q/k norm + RoPE + paged KV append bsz {bsz} x {seq} tokens, {kind}", sets)
+
+
 def make_copy(name, cached=False):
     import torch
     import exl3r
@@ -280,6 +320,10 @@ def make_all(only=None):
                                          __import__("numpy").random.default_rng(0).integers(0, 151936, 512), 530),
         "decode_fused": lambda: make_decode(True),
         "decode_naive": lambda: make_decode(False),
+        "rope_kv_prefill": lambda: make_rope_kv("rope_kv_prefill", 1, 4096, True),
+        "rope_kv_prefill_unfused": lambda: make_rope_kv("rope_kv_prefill_unfused", 1, 4096, False),
+        "rope_kv_dec": lambda: make_rope_kv("rope_kv_dec", 64, 1, True, max_blocks=16),
+        "rope_kv_dec_unfused": lambda: make_rope_kv("rope_kv_dec_unfused", 64, 1, False, max_blocks=16),
         "calib_copy": lambda: make_copy("calib_copy"),
         "calib_copy_cached": lambda: make_copy("calib_copy_cached", cached=True),
     }
@@ -425,7 +469,7 @@ def main():
             ops[name] = {"desc": w.desc, "us": round(ms * 1000, 3), "bytes": w.nbytes, "gbs": round(gbs, 1),
                          "frac_peak": round(gbs / PEAK_GBS, 4)}
             extra = ""
-            if name.endswith("_c1"):
+            if name.endswith("_c1") or name.startswith("rope_kv_dec"):
                 # Launch-latency-bound: eager timing is the host's launch rate; the graph replay is
                 # the device time per launch.
                 us_g = time_graph(w, 20, 10) * 1000
@@ -447,6 +491,14 @@ def main():
                   "timing": "HIP graph replay of 20 layers x 10 replays (eager: back-to-back launches)"}
         log(f"decode layer T=64: fused {decode['fused_us']:.2f} us vs naive {decode['naive_us']:.2f} us "
             f"(x{decode['speedup']:.2f}, graph); eager x{decode['eager']['speedup']:.2f}")
+        pf, pu = ops["rope_kv_prefill"]["us"], ops["rope_kv_prefill_unfused"]["us"]
+        df, du = ops["rope_kv_dec"]["us_graph"], ops["rope_kv_dec_unfused"]["us_graph"]
+        rope_kv = {"prefill_4096": {"fused_us": pf, "unfused_us": pu, "speedup": round(pu / pf, 3)},
+                   "decode_64x1_graph": {"fused_us": df, "unfused_us": du, "speedup": round(du / df, 3)},
+                   "desc": "q/k norm + RoPE + paged KV append: one exl3r_rope_paged_kv launch vs exl3r_rope "
+                           "followed by a separate append kernel"}
+        log(f"rope + paged KV append: prefill fused {pf:.2f} us vs {pu:.2f} us (x{pu / pf:.2f}); "
+            f"decode graph {df:.2f} us vs {du:.2f} us (x{du / df:.2f})")
         c2 = rms_c2_latencies()
         log(f"C2 residual RMSNorm us (graph): {[c2[t]['us_graph'] for t in c2]}")
 
@@ -486,6 +538,7 @@ def main():
                    "io_dtype": "bf16", "tokens": 8192, "hidden": 5120, "intermediate": 17408,
                    "frac_peak": round(value / PEAK_GBS, 4)},
         "roofline": roof, "cpu_baseline": cpu, "ops": ops, "decode_step": decode, "c2_decode_rms_norm": c2,
+        "rope_paged_kv": rope_kv,
         "copy_reference": {"gbs": round(copy_gbs, 1), "frac_peak": round(copy_gbs / PEAK_GBS, 4),
                            "desc": "non-temporal 16 B/lane device copy of 1 GiB (read + write), the practical HBM ceiling reference"},
     }

@@ -21,6 +21,12 @@ EXL3R_API int naive_rope_neox_f16(void* x, const float* inv_freq, const int32_t*
 EXL3R_API int naive_silu_f16(const void* g, void* z, int64_t n, void* stream);
 /* z = a * b */
 EXL3R_API int naive_mul_f16(const void* a, const void* b, void* z, int64_t n, void* stream);
+/* Paged KV-cache append as a separate launch: k, v [bsz, seq_len, heads, hd] into caches
+ * [pages, page_size, heads, hd] at cache_seqlens[b] + s through block_table [bsz, max_blocks]. */
+EXL3R_API int naive_paged_kv_update_f16(const void* k, const void* v, void* k_cache, void* v_cache,
+                                        const int32_t* block_table, const int32_t* cache_seqlens, int64_t bsz,
+                                        int64_t seq_len, int heads, int hd, int64_t max_blocks, int page_size,
+                                        void* stream);
 /* Non-temporal 16-byte-per-lane copy of nbytes (multiple of 16): bandwidth reference and rocprof
  * counter calibration. */
 EXL3R_API int calib_copy(const void* src, void* dst, int64_t nbytes, void* stream);

@@ -95,6 +95,26 @@ __global__ __launch_bounds__(128) void k_calib_copy_cached(const u32x4* src, u32
     if (i < n16) dst[i] = src[i];
 }
 
+// Unfused paged KV-cache append (the separate launch that follows RoPE in paged attention): one
+// 16-byte vector of k and of v per thread, pages of page_size tokens through the block table.
+// Positions are assumed valid (as the reference's kernel assumes them).
+__global__ void k_naive_paged_kv(const u32x4* k, const u32x4* v, u32x4* kc, u32x4* vc, const int32_t* block_table,
+                                 const int32_t* seqlens, int64_t seq_len, int heads, int vecs, int64_t max_blocks,
+                                 int page_size, int64_t total)
+{
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x)
+    {
+        const int64_t row = i / vecs;                   // (token, head)
+        const int64_t tok = row / heads;
+        const int64_t b = tok / seq_len;
+        const int64_t pos = (int64_t)seqlens[b] + (tok - b * seq_len);
+        const int64_t page = block_table[b * max_blocks + pos / page_size];
+        const int64_t dst = ((page * page_size + pos % page_size) * heads + (row - tok * heads)) * vecs + (i - row * vecs);
+        kc[dst] = k[i];
+        vc[dst] = v[i];
+    }
+}
+
 static unsigned blocks_for(int64_t n, int threads)
 {
     int64_t b = (n + threads - 1) / threads;
@@ -156,5 +176,19 @@ extern "C" int calib_copy_cached(const void* src, void* dst, int64_t nbytes, voi
     const int64_t n16 = nbytes / 16;
     if (n16 > ((int64_t)1 << 37)) return -1;
     k_calib_copy_cached<<<(unsigned)((n16 + 127) / 128), 128, 0, (hipStream_t)stream>>>((const u32x4*)src, (u32x4*)dst, n16);
+    return (int)hipGetLastError();
+}
+
+extern "C" int naive_paged_kv_update_f16(const void* k, const void* v, void* k_cache, void* v_cache,
+                                         const int32_t* block_table, const int32_t* cache_seqlens, int64_t bsz,
+                                         int64_t seq_len, int heads, int hd, int64_t max_blocks, int page_size,
+                                         void* stream)
+{
+    if (hd % 8 || bsz <= 0 || seq_len <= 0) return -1;
+    const int64_t total = bsz * seq_len * heads * (hd / 8);
+    const unsigned grid = (unsigned)((total + 255) / 256 < 65535 ? (total + 255) / 256 : 65535);
+    k_naive_paged_kv<<<grid, 256, 0, (hipStream_t)stream>>>((const u32x4*)k, (const u32x4*)v, (u32x4*)k_cache,
+                                                           (u32x4*)v_cache, block_table, cache_seqlens, seq_len, heads,
+                                                           hd / 8, max_blocks, page_size, total);
     return (int)hipGetLastError();
 }

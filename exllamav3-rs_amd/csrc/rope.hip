@@ -368,6 +368,12 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
                     ip = (const char*)a.q + off;
                     optr[it] = (char*)a.oq + off;
                 }
+                else if constexpr (!APPEND)
+                {
+                    const int64_t off = ((int64_t)tok * a.k_ts + (int64_t)(rel - a.hq) * a.k_hs) * IO::bytes;
+                    ip = (const char*)a.k + off;
+                    optr[it] = (char*)a.ok + off;
+                }
                 else
                 {
                     const int hkv = rel - a.hq - (kind[it] == KIND_V ? a.hk : 0);
@@ -410,7 +416,7 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
             lane_sincos<MODE>(cs + trel[it] * R2, e0, a.R, c, s);
             rope_head<IO, MODE, LPH, NORM>(a, v[it], kind[it] != KIND_V, select_w<NORM>(kind[it] == KIND_Q, wq, wk), c, s,
                                            e0, tid & 63);
-            if (act[it] && optr[it]) store8<IO>(optr[it], (int64_t)e0, v[it]);
+            if (act[it] && (!APPEND || optr[it])) store8<IO>(optr[it], (int64_t)e0, v[it]);
             if (APPEND && act[it] && cptr[it]) store8<IO>(cptr[it], (int64_t)e0, v[it]);
         }
         __syncthreads();   // cs[] is refilled for the next range
@@ -437,7 +443,8 @@ template <class IO, int HPL>
 struct RopeBatch
 {
     typename IO::Vec v[HPL];
-    int32_t hidx[HPL];           // head index inside q, k or v
+    int32_t off[HPL];            // element offset of the lane's chunk inside its token's q, k or v row
+    int32_t hidx[HPL];           // head index inside k or v (the cache row offset of an append)
     bool isq[HPL], isv[HPL];
     bool act[HPL];
     int64_t tok;
@@ -462,7 +469,10 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
     float2* row = cs + wave * R2;
     const LaneW<NORM> wq = lane_weights<NORM>(a, a.qw, e0, lane_ok);
     const LaneW<NORM> wk = lane_weights<NORM>(a, a.kw, e0, lane_ok);
-    auto head_stride = [&](int kind) { return kind == KIND_Q ? a.q_hs : kind == KIND_K ? a.k_hs : a.v_hs; };
+    // Per-lane choices between argument fields select values, not addresses: a selected field
+    // address is read with a vector load from the argument segment on every use.
+    const int64_t q_hs = a.q_hs, k_hs = a.k_hs, v_hs = APPEND ? a.v_hs : 0;
+    auto head_stride = [&](int kind) { return kind == KIND_Q ? q_hs : kind == KIND_K ? k_hs : v_hs; };
 
     auto issue = [&](RopeBatch<IO, HPL>& t) {
         const char* qb = (const char*)a.q + t.tok * a.q_ts * IO::bytes;
@@ -477,10 +487,9 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
             t.isv[i] = APPEND && h >= a.hq + a.hk;
             const int kd = t.isq[i] ? KIND_Q : t.isv[i] ? KIND_V : KIND_K;
             t.hidx[i] = h - (kd == KIND_Q ? 0 : kd == KIND_K ? a.hq : a.hq + a.hk);
-            if (t.act[i])
-                t.v[i] = load8s<IO>(kd == KIND_Q ? qb : kd == KIND_K ? kb : vb, (int64_t)t.hidx[i] * head_stride(kd) + e0);
+            t.off[i] = (int32_t)((int64_t)t.hidx[i] * head_stride(kd)) + e0;
+            if (t.act[i]) t.v[i] = load8s<IO>(kd == KIND_Q ? qb : kd == KIND_K ? kb : vb, t.off[i]);
         }
-        t.crow = APPEND ? cache_row(a, t.tok) : -1;
     };
     float c[8], s[8];
     auto fill = [&](int64_t tok) {
@@ -504,11 +513,15 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
             const int kd = t.isq[i] ? KIND_Q : t.isv[i] ? KIND_V : KIND_K;
             rope_head<IO, MODE, LPH, NORM>(a, t.v[i], kd != KIND_V, select_w<NORM>(kd == KIND_Q, wq, wk), c, s, e0, l64);
             if (!t.act[i]) continue;
-            const int64_t off = (int64_t)t.hidx[i] * head_stride(kd) + e0;
-            if (kd == KIND_Q) store8<IO>(qo, off, t.v[i]);
+            if (!APPEND)
+            {
+                store8<IO>(kd == KIND_Q ? qo : ko, t.off[i], t.v[i]);
+                continue;
+            }
+            if (kd == KIND_Q) store8<IO>(qo, t.off[i], t.v[i]);
             else
             {
-                if (kd == KIND_K && a.ok) store8<IO>(ko, off, t.v[i]);
+                if (kd == KIND_K && a.ok) store8<IO>(ko, t.off[i], t.v[i]);
                 if (APPEND && t.crow >= 0)
                     store8<IO>(kd == KIND_K ? a.kc : a.vc, t.crow + (int64_t)t.hidx[i] * a.hd + e0, t.v[i]);
             }
@@ -519,6 +532,7 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
     A.tok = (int64_t)blockIdx.x * 4 + wave;
     A.b = 0;
     if (A.tok >= a.tokens) return;
+    A.crow = APPEND ? cache_row(a, A.tok) : -1;
     issue(A);
     fill(A.tok);
 
@@ -533,6 +547,7 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
             nxt.tok += nwaves;
         }
         const bool more = nxt.tok < a.tokens;
+        if (APPEND && more) nxt.crow = nxt.b == 0 ? cache_row(a, nxt.tok) : cur.crow;
         if (more) issue(nxt);
         compute(cur, c, s);
         if (more && nxt.b == 0) fill(nxt.tok);
@@ -641,14 +656,15 @@ static void launch_rope_lph(RopeArgs a, int iters, hipStream_t s)
 }
 
 // Wave-per-token launch.  Measured on MI355X at C4 (4639 tokens, 64 + 8 heads of 128, NeoX, in
-// place): f16 heads (packed-half norm, 96 VGPRs) run best with 2 heads per lane in flight and one
+// place): f16 heads (packed-half norm, 94 VGPRs) run best with 2 heads per lane in flight and one
 // token per wave (38.5 us; 3 per lane 42 us); bf16 heads (fp32 norm) with 3 per lane on a
-// persistent grid of 4 workgroups per CU (37.0 us; 2 per lane 42 us).
+// persistent grid of 4 workgroups per CU (37.0 us; 2 per lane 42 us).  With the paged append
+// (4096 tokens, + 8 v heads) 3 per lane: 40.0 us, 2 per lane 41-43 us.
 template <class IO, int MODE, int LPH, int NORM>
 static void launch_rope_tok(RopeArgs a, hipStream_t s)
 {
     const Tuning& tu = tuning();
-    int hpl = IO::code == DT_F16 ? 2 : 3;
+    int hpl = IO::code == DT_F16 && !a.kc ? 2 : 3;
     int wgs_per_cu = IO::code == DT_F16 ? 0 : 4;
     if (tu.rope_hpl > 0) hpl = tu.rope_hpl;
     if (tu.rope_wgs_per_cu > 0) wgs_per_cu = tu.rope_wgs_per_cu;

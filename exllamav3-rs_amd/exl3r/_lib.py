@@ -50,6 +50,7 @@ NAIVE_PROTOTYPES = {
     "naive_rope_neox_f16": (_i, [_vp, _vp, _vp, _i64, _i64, _i, _i, _vp]),
     "naive_silu_f16": (_i, [_vp, _vp, _i64, _vp]),
     "naive_mul_f16": (_i, [_vp, _vp, _vp, _i64, _vp]),
+    "naive_paged_kv_update_f16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i, _i, _i64, _i, _vp]),
     "calib_copy": (_i, [_vp, _vp, _i64, _vp]),
     "calib_copy_cached": (_i, [_vp, _vp, _i64, _vp]),
 }

@@ -130,6 +130,14 @@ void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* o
           int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
           float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s,
           const Tensor* position_ids = nullptr);
+// rope() fused with the paged KV-cache append that follows it in paged attention (src/modules.rs:666-704,
+// ffi.rs:337-350): the roped k (also written to out_k when given) and v go to k_cache / v_cache
+// [pages, page_size, kv_heads, head_dim] at cache_seqlens[b] + s through block_table [bsz, max_blocks].
+void rope_paged_kv(const Tensor& q, const Tensor& out_q, const Tensor& k, const Tensor* out_k, const Tensor& v,
+                   const Tensor& inv_freq, int64_t position, const Tensor* positions, const Tensor* q_norm,
+                   const Tensor* k_norm, float norm_eps, float norm_constant_bias, RopeStyle rope_mode, float attn_factor,
+                   const Tensor& k_cache, const Tensor& v_cache, const Tensor& block_table, const Tensor& cache_seqlens,
+                   int32_t* err_flag, const Stream& s);
 // Embedding gather: out[i] = table[ids[i]] (bit-exact, or exact upcast to f32); err_flag optional.
 void embedding(const Tensor& table, const Tensor& ids, const Tensor& out, int32_t* err_flag, const Stream& s);
 // Gather fused with the following RMSNorm; h optional.
@@ -190,6 +198,11 @@ public:
                const Tensor* k_norm, float norm_eps, float norm_constant_bias, const Stream& s) const;
     void apply_one(const Tensor& x, int64_t position, const Tensor* positions, const Tensor* norm, float norm_eps,
                    float norm_constant_bias, const Stream& s) const;
+    // apply() on q and k in place, then k and v appended to the paged caches (one launch); the rotary
+    // positions are the cache lengths, as in the paged attention path (src/modules.rs:666-681).
+    void apply_paged(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& k_cache, const Tensor& v_cache,
+                     const Tensor& block_table, const Tensor& cache_seqlens, const Tensor* q_norm, const Tensor* k_norm,
+                     float norm_eps, float norm_constant_bias, int32_t* err_flag, const Stream& s) const;
     const std::vector<float>& inv_freq_host() const { return inv_freq_host_; }
     int rotary_dim() const { return rotary_dim_; }
 

@@ -190,6 +190,40 @@ int main()
         std::snprintf(msg, sizeof msg, "max ulp %lld", (long long)dx);
         report("RoPE::apply_one gptj partial rotary", dx <= 2, msg);
     }
+    // RoPE::apply_paged: rope + paged KV append (16-token pages, positions = cache lengths).
+    {
+        const int bsz = 2, seq = 5, hq = 4, hk = 2, hd = 64, page = 16, pages = 9, max_blocks = 4;
+        auto qh = host_normal(DType::F16, bsz * seq * hq * hd, 0.f, 1.f);
+        auto kh = host_normal(DType::F16, bsz * seq * hk * hd, 0.f, 1.f);
+        auto vh = host_normal(DType::F16, bsz * seq * hk * hd, 0.f, 1.f);
+        auto kch = host_normal(DType::F16, (size_t)pages * page * hk * hd, 0.f, 1.f);
+        auto vch = host_normal(DType::F16, (size_t)pages * page * hk * hd, 0.f, 1.f);
+        auto qnh = host_normal(DType::F16, hd, 1.f, 0.1f), knh = host_normal(DType::F16, hd, 1.f, 0.1f);
+        std::vector<int32_t> lens = { 14, 40 }, table = { 3, 0, 7, 5, 1, 8, 2, 6 };
+        auto q = upload(qh, DType::F16, { bsz, seq, hq, hd }, s);
+        auto k = upload(kh, DType::F16, { bsz, seq, hk, hd }, s);
+        auto v = upload(vh, DType::F16, { bsz, seq, hk, hd }, s);
+        auto kc = upload(kch, DType::F16, { pages, page, hk, hd }, s);
+        auto vc = upload(vch, DType::F16, { pages, page, hk, hd }, s);
+        auto qn = upload(qnh, DType::F16, { hd }, s), kn = upload(knh, DType::F16, { hd }, s);
+        OwnedTensor ld = OwnedTensor::empty(DType::I32, { bsz }), bt = OwnedTensor::empty(DType::I32, { bsz, max_blocks });
+        ld.buf.upload(lens.data(), lens.size() * 4, s);
+        bt.buf.upload(table.data(), table.size() * 4, s);
+        RoPE rope(1e6, hd, RopeStyle::NeoX);
+        rope.apply_paged(q.t, k.t, v.t, kc.t, vc.t, bt.t, ld.t, &qn.t, &kn.t, 1e-6f, 0.f, nullptr, s);
+        auto qo = download(q, s), ko = download(k, s), kco = download(kc, s), vco = download(vc, s);
+        std::vector<uint8_t> eq(qh.size()), ek(kh.size());
+        oracle_rope(qh.data(), eq.data(), hq * hd, hd, hq, kh.data(), ek.data(), hk * hd, hd, hk, OR_F16, bsz, seq, hd,
+                    rope.inv_freq_host().data(), hd, 0, lens.data(), nullptr, qnh.data(), knh.data(), OR_F16, 1e-6f, 0.f,
+                    OR_ROPE_NEOX, 1.f, 1);
+        oracle_paged_kv_append(ek.data(), hk * hd, hd, vh.data(), hk * hd, hd, hk, OR_F16, bsz, seq, hd, kch.data(),
+                               vch.data(), page, pages, table.data(), max_blocks, lens.data(), nullptr, 1);
+        const int64_t dq = max_ulp16(qo, eq), dk = max_ulp16(ko, ek);
+        const bool caches = kco == kch && vco == vch;
+        std::snprintf(msg, sizeof msg, "q max ulp %lld, k max ulp %lld, caches %s", (long long)dq, (long long)dk,
+                      caches ? "bitwise" : "DIFFER");
+        report("RoPE::apply_paged neox f16 + paged append", dq == 0 && dk == 0 && caches, msg);
+    }
     std::printf(failures ? "test_host_gpu: %d failures\n" : "test_host_gpu: all passed\n", failures);
     return failures ? 1 : 0;
 }
