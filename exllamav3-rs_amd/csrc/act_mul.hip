@@ -7,11 +7,7 @@
 // round-to-nearest-even to z's dtype, f16 z clamped to +-65504 (2-7, 249-251).
 //   silu(x) = x / (1 + exp(-x))                                   (activation_kernels.cuh:34-39)
 //   gelu(x) = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))      (activation_kernels.cuh:52-58)
-// both evaluated as x * sigmoid(z) (GELU through 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)), which has
-// no 1 + tanh cancellation for x << 0): with e^-z = 2^t, sigmoid = q for t <= 0 and p * q for t > 0,
-// where p = 2^-|t| in (0, 1] and q = 1 / (1 + p).  For |t| > 64 (where 1 + p == 1) p is evaluated
-// as 2^(64 - |t|) and the 2^-64 is applied to the final product, so tail results keep full precision
-// down into the fp32 denormals instead of flushing inside v_exp_f32.
+// both evaluated as x * sigmoid(z) by act_f (common.cuh).
 //
 // Streaming layout: 8-element chunks (16 bytes per 16-bit tensor) per lane, UNROLL chunks in flight
 // per thread, strided by blockDim so each wave-wide access is 1 KiB contiguous.  Contiguous
@@ -20,26 +16,6 @@
 #include "common.cuh"
 
 namespace exl3r {
-
-enum { ACT_SILU = 0, ACT_GELU = 1 };
-
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kGeluK1 = (float)(-2.0 * 0.79788456080286535588 * 1.4426950408889634074);
-constexpr float kGeluK2 = (float)(-2.0 * 0.79788456080286535588 * 0.044715 * 1.4426950408889634074);
-
-template <int ACT>
-__device__ __forceinline__ float act_f(float x)
-{
-    float t;   // e^-z = 2^t
-    if constexpr (ACT == ACT_SILU) t = x * -kLog2e;
-    else t = x * fmaf(kGeluK2, x * x, kGeluK1);
-    const float n = -fabsf(t);
-    const bool tail = n < -64.0f;
-    const float p = __builtin_amdgcn_exp2f(tail ? n + 64.0f : n);   // normal for n >= -190
-    const float q = __builtin_amdgcn_rcpf(1.0f + (tail ? 0.0f : p)); // argument in [1, 2]
-    const float r = x * (t <= 0.0f ? q : p * q);
-    return (tail && t > 0.0f) ? r * 0x1p-64f : r;
-}
 
 struct ActArgs
 {
@@ -237,4 +213,12 @@ extern "C" int exl3r_gelu_mul(const void* x, const void* y, int in_dtype, void* 
                               float act_limit, void* stream)
 {
     return act_mul_entry<ACT_GELU>("exl3r_gelu_mul", x, y, in_dtype, z, z_dtype, rows, cols, ldx, ldy, ldz, act_limit, stream);
+}
+
+// z = x * sigmoid(y): the act-mul kernels with the gate and value operands exchanged.
+extern "C" int exl3r_mul_sigmoid(const void* x, const void* y, int in_dtype, void* z, int z_dtype,
+                                 int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz, void* stream)
+{
+    return act_mul_entry<ACT_SIGMOID>("exl3r_mul_sigmoid", y, x, in_dtype, z, z_dtype, rows, cols, ldy, ldx, ldz, 0.0f,
+                                      stream);
 }

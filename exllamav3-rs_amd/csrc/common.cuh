@@ -228,6 +228,34 @@ __device__ __forceinline__ float rms_factor(double sum, int n, float eps)
     return 1.0f / sqrtf(mean + eps);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Activations in fp32, each a product m * sigmoid(z): SiLU m = x, z = x; GELU(tanh) m = x,
+// z = 2 sqrt(2/pi) (x + 0.044715 x^3) (0.5 (1 + tanh(u)) = sigmoid(2u), no 1 + tanh cancellation for
+// x << 0); SIGMOID m = 1, z = x.  With e^-z = 2^t, sigmoid = q for t <= 0 and p * q for t > 0, where
+// p = 2^-|t| in (0, 1] and q = 1 / (1 + p).  For |t| > 64 (where 1 + p == 1) p is evaluated as
+// 2^(64 - |t|) and the 2^-64 is applied to the final product, so tail results keep full precision
+// down into the fp32 denormals instead of flushing inside v_exp_f32.
+enum { ACT_SILU = 0, ACT_GELU = 1, ACT_SIGMOID = 2 };
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kGeluK1 = (float)(-2.0 * 0.79788456080286535588 * 1.4426950408889634074);
+constexpr float kGeluK2 = (float)(-2.0 * 0.79788456080286535588 * 0.044715 * 1.4426950408889634074);
+
+template <int ACT>
+__device__ __forceinline__ float act_f(float x)
+{
+    float t;   // e^-z = 2^t
+    if constexpr (ACT == ACT_GELU) t = x * fmaf(kGeluK2, x * x, kGeluK1);
+    else t = x * -kLog2e;
+    const float n = -fabsf(t);
+    const bool tail = n < -64.0f;
+    const float p = __builtin_amdgcn_exp2f(tail ? n + 64.0f : n);   // normal for n >= -190
+    const float q = __builtin_amdgcn_rcpf(1.0f + (tail ? 0.0f : p)); // argument in [1, 2]
+    const float s = t <= 0.0f ? q : p * q;
+    const float r = ACT == ACT_SIGMOID ? s : x * s;
+    return (tail && t > 0.0f) ? r * 0x1p-64f : r;
+}
+
 // CLAMP_FP16: +-inf -> +-65504, NaN -> 65504 (v_min/v_max return the non-NaN operand).
 __device__ __forceinline__ float clamp_f16(float v) { return fmaxf(-65504.0f, fminf(v, 65504.0f)); }
 

@@ -1,0 +1,52 @@
+// C ABI: exl3r_gated_rms_norm (replaces exl3_shim_gated_rms_norm, reference csrc/exl3_shim.cpp:143-147 ->
+// gated_rms_norm, kernels/norm.cu:482-668; the Qwen3.5 gated-delta-net output norm, src/qwen3_5.rs:212).
+//
+// y = RMSNorm(x) * w * act(g) with act = silu or sigmoid, or RMSNorm(x * act(g)) * w with gate_first,
+// the weight cycling over w_groups rows (Mamba2 group norm).  The RMSNorm kernel family's register-
+// resident row (rms_norm_kernel.cuh, mode RMS_GATED) carries the gate through its second operand.
+#include "rms_norm_kernel.cuh"
+#include "rms_norm_launch.hpp"
+
+using namespace exl3r;
+
+extern "C" int exl3r_gated_rms_norm(const void* x, int xt, int64_t ldx, const void* w, int wt, int w_groups,
+                                    void* y, int yt, int64_t ldy, const void* g, int gt, int64_t ldg,
+                                    int64_t rows, int64_t dim, float eps, float constant_bias,
+                                    int gate_first, int gate_act, void* stream)
+{
+    const char* op = "exl3r_gated_rms_norm";
+    int rc = check_rms_common(op, x, xt, ldx, w, wt, y, yt, ldy, rows, dim);
+    if (rc) return rc;
+    if (!is_float_dtype(gt)) return set_error(EXL3R_EDTYPE, "%s: unsupported gate dtype %s", op, dtype_name(gt));
+    if (ldg < dim) return set_error(EXL3R_EINVAL, "%s: gate row stride %lld < dim %lld", op, (long long)ldg, (long long)dim);
+    if (w_groups < 1) return set_error(EXL3R_EINVAL, "%s: w_groups must be >= 1", op);
+    if (gate_act != 0 && gate_act != 1) return set_error(EXL3R_EINVAL, "%s: gate_act must be 0 (silu) or 1 (sigmoid)", op);
+    if (rows == 0) return EXL3R_OK;
+    if (!g) return set_error(EXL3R_EINVAL, "%s: gate g must be non-null", op);
+    if (g == y) return set_error(EXL3R_EINVAL, "%s: y must not alias the gate", op);
+
+    RmsArgs a{};
+    a.x = x; a.ldx = ldx; a.w = w; a.wt = wt; a.y = y; a.ldy = ldy; a.r = const_cast<void*>(g); a.ldr = ldg;
+    a.rows = rows; a.dim = (int)dim; a.eps = eps; a.cb = constant_bias; a.cs = 1.0f;
+    a.gact = gate_act; a.gfirst = gate_first != 0; a.w_groups = w_groups;
+    hipStream_t s = (hipStream_t)stream;
+
+    if (xt != EXL3R_F32 && rms_vec_ok(a, xt, yt, gt, true))
+    {
+        auto go_x = [&](auto X) {
+            with_float_type(yt, [&](auto Y) {
+                with_float_type(gt, [&](auto G) {
+                    launch_rms_vec<decltype(X), decltype(Y), decltype(G), RMS_GATED>(a, s);
+                });
+            });
+        };
+        if (xt == EXL3R_F16) go_x(TF16{});
+        else go_x(TBF16{});
+    }
+    else
+    {
+        const unsigned grid = (unsigned)(rows < kMaxGridX ? rows : kMaxGridX);
+        k_rms_norm_generic<RMS_GATED><<<grid, 256, 0, s>>>(a, xt, yt, gt);
+    }
+    return launch_status(op);
+}

@@ -21,7 +21,7 @@
 
 namespace exl3r {
 
-enum { RMS_PLAIN = 0, RMS_RES_IN = 1, RMS_GATHER = 2 };
+enum { RMS_PLAIN = 0, RMS_RES_IN = 1, RMS_GATHER = 2, RMS_GATED = 3 };
 
 struct RmsArgs
 {
@@ -31,7 +31,8 @@ struct RmsArgs
     int wt;
     void* y;
     int64_t ldy;
-    void* r;            // RMS_RES_IN: residual (in/out); RMS_GATHER: optional gathered-row output h
+    void* r;            // RMS_RES_IN: residual (in/out); RMS_GATHER: optional gathered-row output h;
+                        // RMS_GATED: the gate g (read only)
     int64_t ldr;
     const void* ids;    // RMS_GATHER: [rows] token ids (I32 or I64, see idt)
     int idt;
@@ -40,7 +41,21 @@ struct RmsArgs
     int64_t rows;
     int dim;
     float eps, cb, cs;
+    int gact;           // RMS_GATED: 0 silu, 1 sigmoid
+    int gfirst;         // RMS_GATED: gate applied before the norm
+    int w_groups;       // RMS_GATED: the weight holds w_groups rows of dim, row r uses r % w_groups
 };
+
+// RMS_GATED gate activation in fp32.
+__device__ __forceinline__ float gate_act(int gact, float g) { return gact ? act_f<ACT_SIGMOID>(g) : act_f<ACT_SILU>(g); }
+
+// Element offset of the weight row a row uses.
+template <int MODE>
+__device__ __forceinline__ int64_t weight_row(const RmsArgs& a, int64_t row)
+{
+    if constexpr (MODE == RMS_GATED) return (row % a.w_groups) * a.dim;
+    else return 0;
+}
 
 __device__ __forceinline__ int64_t load_id(const void* ids, int idt, int64_t i)
 {
@@ -112,8 +127,8 @@ __device__ __forceinline__ void rms_load(const RmsArgs& a, int64_t row, int tid,
                 if constexpr (MODE == RMS_GATHER) L.xv[k] = load8<XT>(xrow, (int64_t)c * 8);   // hot table rows
                 else L.xv[k] = load8s<XT>(xrow, (int64_t)c * 8);
             }
-            if constexpr (MODE == RMS_RES_IN) L.rv[k] = load8s<RT>(rrow, (int64_t)c * 8);
-            if (load_w && a.w) L.wv[k] = prefetch_w8(a.w, a.wt, (int64_t)c * 8);
+            if constexpr (MODE == RMS_RES_IN || MODE == RMS_GATED) L.rv[k] = load8s<RT>(rrow, (int64_t)c * 8);
+            if (load_w && a.w) L.wv[k] = prefetch_w8(a.w, a.wt, weight_row<MODE>(a, row) + (int64_t)c * 8);
         }
     }
 }
@@ -153,10 +168,20 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
                 for (int j = 0; j < 8; ++j) h[j] = 0.0f;
                 xv[k] = pack8<XT>(h);
             }
-            if constexpr (MODE != RMS_GATHER && XT::code == DT_F16)
+            if constexpr (MODE != RMS_GATHER && MODE != RMS_GATED && XT::code == DT_F16)
             {
                 #pragma unroll
                 for (int j = 0; j < 8; ++j) h[j] = clamp_f16(h[j]);
+            }
+            if constexpr (MODE == RMS_GATED)
+            {
+                if (a.gfirst)
+                {
+                    float gf[8];
+                    unpack8<RT>(rv[k], gf);
+                    #pragma unroll
+                    for (int j = 0; j < 8; ++j) h[j] = h[j] * gate_act(a.gact, gf[j]);
+                }
             }
             if constexpr (MODE == RMS_RES_IN)
             {
@@ -203,11 +228,23 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
                 #pragma unroll
                 for (int j = 0; j < 8; ++j) h[j] = clamp_f16(h[j]);
             }
+            float ga[8];
+            if constexpr (MODE == RMS_GATED)
+            {
+                float gf[8];
+                unpack8<RT>(rv[k], gf);
+                #pragma unroll
+                for (int j = 0; j < 8; ++j)
+                {
+                    ga[j] = gate_act(a.gact, gf[j]);
+                    if (a.gfirst) h[j] = h[j] * ga[j];
+                }
+            }
             float o[8];
             if (has_w)
             {
                 float wf[8];
-                unpack_w8(wv[k], a.w, a.wt, (int64_t)c * 8, wf);
+                unpack_w8(wv[k], a.w, a.wt, weight_row<MODE>(a, row) + (int64_t)c * 8, wf);
                 if (a.cb != 0.0f)
                 {
                     #pragma unroll
@@ -220,6 +257,14 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
             {
                 #pragma unroll
                 for (int j = 0; j < 8; ++j) o[j] = h[j] * rmf;
+            }
+            if constexpr (MODE == RMS_GATED)
+            {
+                if (!a.gfirst)
+                {
+                    #pragma unroll
+                    for (int j = 0; j < 8; ++j) o[j] = o[j] * ga[j];
+                }
             }
             store8<YT>(yrow, (int64_t)c * 8, pack8<YT>(o));
         }
@@ -264,7 +309,8 @@ __global__ __launch_bounds__(256) void k_rms_norm_generic(RmsArgs a, int xt, int
         for (int j = tid; j < a.dim; j += blockDim.x)
         {
             float v = valid ? load1(a.x, xt, xoff + j) : 0.0f;
-            if (MODE != RMS_GATHER && xt == DT_F16) v = clamp_f16(v);
+            if (MODE != RMS_GATHER && MODE != RMS_GATED && xt == DT_F16) v = clamp_f16(v);
+            if (MODE == RMS_GATED && a.gfirst) v = v * gate_act(a.gact, load1(a.r, rt, row * a.ldr + j));
             if (MODE == RMS_RES_IN)
             {
                 v = round1(v + load1(a.r, rt, row * a.ldr + j), rt);
@@ -288,17 +334,20 @@ __global__ __launch_bounds__(256) void k_rms_norm_generic(RmsArgs a, int xt, int
             else
             {
                 v = valid ? load1(a.x, xt, xoff + j) : 0.0f;
-                if (MODE != RMS_GATHER && xt == DT_F16) v = clamp_f16(v);
+                if (MODE != RMS_GATHER && MODE != RMS_GATED && xt == DT_F16) v = clamp_f16(v);
             }
+            const float ga = MODE == RMS_GATED ? gate_act(a.gact, load1(a.r, rt, row * a.ldr + j)) : 1.0f;
+            if (MODE == RMS_GATED && a.gfirst) v = v * ga;
             float o;
             if (a.w)
             {
-                float wf = load1(a.w, a.wt, j);
+                float wf = load1(a.w, a.wt, weight_row<MODE>(a, row) + j);
                 if (a.cb != 0.0f) wf = wf + a.cb;
                 o = (v * wf) * rmf;
             }
             else
                 o = v * rmf;
+            if (MODE == RMS_GATED && !a.gfirst) o = o * ga;
             store1(a.y, yt, row * a.ldy + j, o);
         }
         __syncthreads();
@@ -339,6 +388,15 @@ int launch_rms_vec(const RmsArgs& a, hipStream_t s)
 {
     const RmsShape sh = rms_shape(a.dim / 8, a.rows);
     const dim3 grid((unsigned)(a.rows < kMaxGridX ? a.rows : kMaxGridX));
+    if constexpr (MODE == RMS_GATED)
+    {
+        // Chunks per lane 1, 2, 4 or 8 (a tuned 3 or 5 rounds up; the grid still covers the row).
+        if (sh.maxv == 1) k_rms_norm<XT, YT, RT, 1, MODE><<<grid, sh.threads, 0, s>>>(a);
+        else if (sh.maxv == 2) k_rms_norm<XT, YT, RT, 2, MODE><<<grid, sh.threads, 0, s>>>(a);
+        else if (sh.maxv <= 4) k_rms_norm<XT, YT, RT, 4, MODE><<<grid, sh.threads, 0, s>>>(a);
+        else k_rms_norm<XT, YT, RT, 8, MODE><<<grid, sh.threads, 0, s>>>(a);
+        return 0;
+    }
     switch (sh.maxv)
     {
         case 1: k_rms_norm<XT, YT, RT, 1, MODE><<<grid, sh.threads, 0, s>>>(a); break;

@@ -93,6 +93,59 @@ def gelu_mul(x, y, z, act_limit=0.0, stream=None):
     _act(load().exl3r_gelu_mul, x, y, z, act_limit, stream)
 
 
+def gated_rms_norm(x, w, y, g, eps, constant_bias=0.0, w_groups=1, gate_first=False, gate_act=0, stream=None):
+    """y = RMSNorm(x) * (w + constant_bias) * act(g), or RMSNorm(x * act(g)) * (w + constant_bias) with
+    gate_first; act = silu (gate_act 0) or sigmoid (1); w may be None or hold w_groups rows of dim
+    (src/ffi.rs:479-483)."""
+    rows, dim, ldx = _rows(x)
+    ry, dy, ldy = _rows(y)
+    rg, dg, ldg = _rows(g)
+    if (ry, dy) != (rows, dim) or (rg, dg) != (rows, dim):
+        raise ValueError("x, y and g shapes differ")
+    if w is not None and w.numel() != w_groups * dim:
+        raise ValueError("w must hold w_groups * dim values")
+    check(load().exl3r_gated_rms_norm(_ptr(x), dtype_code(x), ldx, _ptr(w), dtype_code(w) if w is not None else F32,
+                                      w_groups, _ptr(y), dtype_code(y), ldy, _ptr(g), dtype_code(g), ldg, rows, dim, eps,
+                                      constant_bias, int(bool(gate_first)), int(gate_act), _stream(x, stream)))
+
+
+def mul_sigmoid(x, y, z, stream=None):
+    """z = x * sigmoid(y) (fp32, one rounding); z may be x."""
+    rows, cols, ldx = _rows(x)
+    ry, cy, ldy = _rows(y)
+    rz, cz, ldz = _rows(z)
+    if (ry, cy) != (rows, cols) or (rz, cz) != (rows, cols):
+        raise ValueError("x, y and z shapes differ")
+    if x.dtype != y.dtype:
+        raise TypeError("x and y must share a dtype")
+    check(load().exl3r_mul_sigmoid(_ptr(x), _ptr(y), dtype_code(x), _ptr(z), dtype_code(z), rows, cols, ldx, ldy, ldz,
+                                   _stream(x, stream)))
+
+
+def mul_sigmoid_(x, y, stream=None):
+    """x *= sigmoid(y) in place (src/ffi.rs:616-618)."""
+    mul_sigmoid(x, y, x, stream)
+
+
+def deinterleave_qg(qg, q, g, head_dim, stream=None):
+    """Split [.., heads * 2 * head_dim] per-head interleaved (q | g) rows into q [.., heads, head_dim] and
+    g [.., heads * head_dim] (src/ffi.rs:622-624)."""
+    width = qg.shape[-1]
+    if width % (2 * head_dim):
+        raise ValueError("qg's last dim must be heads * 2 * head_dim")
+    heads = width // (2 * head_dim)
+    rows, _, ldqg = _rows(qg)
+    q2 = q.reshape(rows, heads * head_dim) if q.is_contiguous() else q.view(rows, heads * head_dim)
+    rq, cq, ldq = _rows(q2)
+    rg, cg, ldg = _rows(g.reshape(rows, heads * head_dim) if g.is_contiguous() else g)
+    if (rq, cq) != (rows, heads * head_dim) or (rg, cg) != (rows, heads * head_dim):
+        raise ValueError("q and g must hold heads * head_dim values per row")
+    if q.dtype != qg.dtype or g.dtype != qg.dtype:
+        raise TypeError("qg, q and g must share a dtype")
+    check(load().exl3r_deinterleave_qg(_ptr(qg), ldqg, _ptr(q), ldq, _ptr(g), ldg, dtype_code(qg), rows, heads, head_dim,
+                                       _stream(qg, stream)))
+
+
 def rope(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias,
          rope_mode, attn_factor, position_ids=None, stream=None):
     """Fused (optional) q/k head RMSNorm + RoPE.  q, k: (bsz, seq_len, heads, head_dim); `positions`

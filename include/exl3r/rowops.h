@@ -28,6 +28,9 @@
  *   exl3r_rope              <- exl3_shim_rope             csrc/exl3_shim.cpp:87-98   (ffi.rs:51-65, 298-333)
  *   exl3r_rope_paged_kv     <- exl3_shim_rope followed by exl3_shim_paged_kv_cache_update
  *                              csrc/exl3_shim.cpp:87-98, 109-112 (ffi.rs:298-350; call sites modules.rs:666-704)
+ *   exl3r_gated_rms_norm    <- exl3_shim_gated_rms_norm   csrc/exl3_shim.cpp:143-147 (ffi.rs:118-124, 479-483)
+ *   exl3r_mul_sigmoid       <- exl3_shim_mul_sigmoid_     csrc/exl3_shim.cpp:167     (ffi.rs:166, 616-618)
+ *   exl3r_deinterleave_qg   <- exl3_shim_deinterleave_qg  csrc/exl3_shim.cpp:168-171 (ffi.rs:167, 622-624)
  *   exl3r_embedding         <- Embedding::forward's tch index_select + to_kind   src/modules.rs:430-436
  *   exl3r_embedding_rms_norm<- embed followed by RmsNorm::forward (MTP head)    src/mtp.rs:189-190
  */
@@ -116,6 +119,42 @@ EXL3R_API int exl3r_silu_mul(const void* x, const void* y, int in_dtype, void* z
 EXL3R_API int exl3r_gelu_mul(const void* x, const void* y, int in_dtype, void* z, int z_dtype,
                    int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz,
                    float act_limit, void* stream);
+
+/*
+ * Gated RMSNorm (the Qwen3.5 gated-delta-net output norm, src/qwen3_5.rs:212; Mamba2 group norm):
+ *   a = act(g) with act = silu (gate_act 0) or sigmoid (gate_act 1), in fp32;
+ *   gate_first == 0: y = ((x * w') * rmf) * a,   rmf = 1 / sqrt(mean(x^2) + eps);
+ *   gate_first != 0: y = (v * w') * rmf with v = x * a and rmf over v;
+ *   w' = w + constant_bias, row i using weight row i % w_groups (w holds w_groups * dim values;
+ *   w == NULL: no weight); one rounding to y's dtype; x is not clamped.
+ * Replaces exl3_shim_gated_rms_norm (csrc/exl3_shim.cpp:143-147) -> gated_rms_norm
+ * (kernels/norm.cu:482-668), which takes bf16 x, f32/bf16 w, bf16/f32 g and f16/f32 y.
+ *   x: [rows, dim] F16/BF16/F32, row stride ldx;  g: [rows, dim] F16/BF16/F32, row stride ldg;
+ *   y: [rows, dim] F16/BF16/F32, row stride ldy (y may equal x, not g).
+ */
+EXL3R_API int exl3r_gated_rms_norm(const void* x, int x_dtype, int64_t ldx, const void* w, int w_dtype, int w_groups,
+                         void* y, int y_dtype, int64_t ldy, const void* g, int g_dtype, int64_t ldg,
+                         int64_t rows, int64_t dim, float eps, float constant_bias,
+                         int gate_first, int gate_act, void* stream);
+
+/*
+ * Sigmoid gate: z = x * sigmoid(y), in fp32, rounded once to z's dtype (the gated-attention
+ * output gate, src/modules.rs:785-787).  Replaces exl3_shim_mul_sigmoid_ (csrc/exl3_shim.cpp:167 ->
+ * mul_sigmoid_, kernels/activation.cu:532-568, in place on f16 with half arithmetic).
+ *   x, y: [rows, cols] of in_dtype (F16/BF16/F32), row strides ldx, ldy; z of z_dtype, row stride
+ *   ldz; z may equal x (the reference's in-place form) or y.
+ */
+EXL3R_API int exl3r_mul_sigmoid(const void* x, const void* y, int in_dtype, void* z, int z_dtype,
+                      int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz, void* stream);
+
+/*
+ * Split a per-head interleaved projection (rows of [heads, q | g], 2 * head_dim per head) into
+ * q [rows, heads, head_dim] and g [rows, heads * head_dim], bit for bit.  Replaces
+ * exl3_shim_deinterleave_qg (csrc/exl3_shim.cpp:168-171 -> deinterleave_qg,
+ * kernels/activation.cu:721-779).  Row strides in elements; dtype F16/BF16/F32 (copied as bits).
+ */
+EXL3R_API int exl3r_deinterleave_qg(const void* qg, int64_t ld_qg, void* q, int64_t ld_q, void* g, int64_t ld_g,
+                          int dtype, int64_t rows, int heads, int head_dim, void* stream);
 
 /*
  * Fused per-head RMSNorm (optional) + rotary embedding on q and (optional) k.

@@ -12,7 +12,7 @@ LIB_PATH = os.path.join(HERE, "lib", "liboracle_rowops.so")
 
 F32, F16, BF16, I32, I64 = 0, 1, 2, 3, 4
 ROPE_GPTJ, ROPE_NEOX = 1, 2
-ACT_SILU, ACT_GELU = 0, 1
+ACT_SILU, ACT_GELU, ACT_SIGMOID = 0, 1, 2
 
 _vp, _i, _i64, _f, _i32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_int32
 _PROTOS = {
@@ -28,6 +28,9 @@ _PROTOS = {
     "oracle_rope": (_i, [_vp, _vp, _i64, _i64, _i, _vp, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _i,
                          _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _i]),
     "oracle_embedding": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _i64, _vp, _i]),
+    "oracle_gated_rms_norm": (_i, [_vp, _i, _i64, _vp, _i, _i, _vp, _i, _i64, _vp, _i, _i64, _i64, _i64, _f, _f, _i,
+                                   _i, _i]),
+    "oracle_deinterleave_qg": (_i, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i, _i, _i]),
     "oracle_paged_kv_append": (_i, [_vp, _i64, _i64, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _vp, _i, _i64,
                                     _vp, _i64, _vp, _vp, _i]),
     "oracle_embedding_rms_norm": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _i64, _vp, _i,
@@ -120,6 +123,31 @@ def act_mul(act, x, y, it, zt, limit=0.0, nthreads=1):
     _check(load().oracle_act_mul(act, _p(x), _p(y), it, _p(z), zt, rows, cols, cols, cols, cols, limit, nthreads),
            "oracle_act_mul")
     return z
+
+
+def mul_sigmoid(x, y, it, zt, nthreads=1):
+    """z = x * sigmoid(y) (fp32 product, one rounding): act_mul with the operands' roles swapped."""
+    return act_mul(ACT_SIGMOID, y, x, it, zt, nthreads=nthreads)
+
+
+def gated_rms_norm(x, xt, g, gt, yt, w=None, wt=F32, w_groups=1, eps=1e-6, cb=0.0, gate_first=False, gate_act=0,
+                   nthreads=1):
+    """x, g: [rows, dim] storage arrays; w: [w_groups * dim] or None.  Returns y."""
+    rows, dim = x.shape
+    y = np.zeros((rows, dim), storage_dtype(yt))
+    _check(load().oracle_gated_rms_norm(_p(x), xt, dim, _p(w), wt, w_groups, _p(y), yt, dim, _p(g), gt, dim, rows,
+                                        dim, eps, cb, int(gate_first), gate_act, nthreads), "oracle_gated_rms_norm")
+    return y
+
+
+def deinterleave_qg(qg, heads, hd, nthreads=1):
+    """qg: [rows, heads * 2 * hd] 16-bit storage.  Returns (q [rows, heads * hd], g [rows, heads * hd])."""
+    rows = qg.shape[0]
+    q = np.zeros((rows, heads * hd), qg.dtype)
+    g = np.zeros((rows, heads * hd), qg.dtype)
+    _check(load().oracle_deinterleave_qg(_p(qg), heads * 2 * hd, _p(q), heads * hd, _p(g), heads * hd, rows, heads, hd,
+                                         nthreads), "oracle_deinterleave_qg")
+    return q, g
 
 
 def rope(q, k, dt, inv_freq, mode, position=0, positions=None, position_ids=None, q_norm=None, k_norm=None,

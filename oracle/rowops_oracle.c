@@ -237,6 +237,8 @@ static double act_d(int act, double x)
         double e = oracle_mutation == ORM_SILU_SIGN ? exp(x) : exp(-x);
         return x / (1.0 + e);
     }
+    if (act == OR_ACT_SIGMOID)   /* mul_sigmoid_ (activation.cu:532-568), _sigmoid_f (norm.cu:133-136) */
+        return 1.0 / (1.0 + (oracle_mutation == ORM_SIGMOID_SIGN ? exp(x) : exp(-x)));
     const double c = 0.79788456080286535588;   /* sqrt(2/pi) */
     double cubic = oracle_mutation == ORM_GELU_NO_CUBIC ? 0.0 : 0.044715 * x * x * x;
     double u = c * (x + cubic);
@@ -249,7 +251,7 @@ int oracle_act_mul(int act, const void* x, const void* y, int it, void* z, int z
 {
     if (!x || !y || !z || rows < 0 || cols < 0) return -1;
     if (!fdtype(it) || !fdtype(zt)) return -2;
-    if (act != OR_ACT_SILU && act != OR_ACT_GELU) return -1;
+    if (act != OR_ACT_SILU && act != OR_ACT_GELU && act != OR_ACT_SIGMOID) return -1;
 
     #pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
     for (int64_t i = 0; i < rows; ++i)
@@ -434,6 +436,71 @@ static inline int64_t load_id(const void* ids, int idt, int64_t i)
 static size_t dsize(int dt) { return dt == OR_F32 ? 4 : 2; }
 
 static int exact_conv(int from, int to) { return from == to || to == OR_F32; }
+
+/* kernels/norm.cu:482-581 (kernel), 591-668 (host rules) */
+int oracle_gated_rms_norm(const void* x, int xt, int64_t ldx, const void* w, int wt, int w_groups,
+                          void* y, int yt, int64_t ldy, const void* g, int gt, int64_t ldg,
+                          int64_t rows, int64_t dim, float eps, float cb, int gate_first, int gate_act,
+                          int nthreads)
+{
+    if (!x || !y || !g || dim <= 0 || rows < 0 || w_groups < 1) return -1;
+    if (!fdtype(xt) || !fdtype(yt) || !fdtype(gt) || (w && !fdtype(wt))) return -2;
+    if (gate_act != 0 && gate_act != 1) return -1;
+    if (oracle_mutation == ORM_GATED_ORDER) gate_first = 0;
+    const int act = gate_act ? OR_ACT_SIGMOID : OR_ACT_SILU;
+    #pragma omp parallel num_threads(nthr(nthreads))
+    {
+        float* v = (float*)malloc((size_t)dim * sizeof(float));
+        float* a = (float*)malloc((size_t)dim * sizeof(float));
+        #pragma omp for schedule(static)
+        for (int64_t i = 0; i < rows; ++i)
+        {
+            const int64_t wrow = oracle_mutation == ORM_GATED_WGROUP ? 0 : (i % w_groups) * dim;
+            double s = 0.0;
+            for (int64_t j = 0; j < dim; ++j)
+            {
+                a[j] = (float)act_d(act, (double)ld(g, gt, i * ldg + j));
+                const float xv = ld(x, xt, i * ldx + j);
+                v[j] = gate_first ? xv * a[j] : xv;
+                s += (double)v[j] * (double)v[j];
+            }
+            const float rmf = 1.0f / sqrtf((float)s / (float)dim + eps);
+            for (int64_t j = 0; j < dim; ++j)
+            {
+                float wv = 1.0f;
+                if (w)
+                {
+                    wv = ld(w, wt, wrow + j);
+                    if (cb != 0.0f) wv = wv + cb;
+                }
+                float o = w ? (v[j] * wv) * rmf : v[j] * rmf;
+                if (!gate_first) o = o * a[j];
+                st(y, yt, i * ldy + j, o);
+            }
+        }
+        free(v);
+        free(a);
+    }
+    return 0;
+}
+
+/* kernels/activation.cu:721-779 */
+int oracle_deinterleave_qg(const void* qg, int64_t ldqg, void* q, int64_t ldq, void* g, int64_t ldg,
+                           int64_t rows, int heads, int hd, int nthreads)
+{
+    if (!qg || !q || !g || rows < 0 || heads <= 0 || hd <= 0) return -1;
+    void* dq = oracle_mutation == ORM_QG_SWAP ? g : q;
+    void* dg = oracle_mutation == ORM_QG_SWAP ? q : g;
+    #pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t i = 0; i < rows; ++i)
+        for (int h = 0; h < heads; ++h)
+        {
+            const char* src = (const char*)qg + (i * ldqg + (int64_t)h * 2 * hd) * 2;
+            memcpy((char*)dq + (i * ldq + (int64_t)h * hd) * 2, src, (size_t)hd * 2);
+            memcpy((char*)dg + (i * ldg + (int64_t)h * hd) * 2, src + (size_t)hd * 2, (size_t)hd * 2);
+        }
+    return 0;
+}
 
 /* kernels/generator/cache.cu:159-183 (index arithmetic), 186-243 (shape rules) */
 int oracle_paged_kv_append(const void* k, int64_t k_tok_stride, int64_t k_head_stride,

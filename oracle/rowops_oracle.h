@@ -35,6 +35,7 @@ extern "C" {
 
 #define OR_ACT_SILU 0
 #define OR_ACT_GELU 1
+#define OR_ACT_SIGMOID 2
 
 /* Planted-mistake switch for the oracle's own tests (0 = faithful). */
 extern int oracle_mutation;
@@ -55,6 +56,10 @@ extern int oracle_mutation;
 #define ORM_EMBED_OFF        14  /* gathers row ids[i] + 1 */
 #define ORM_ROPE_NORM_AFTER  15  /* head norm applied after the rotation */
 #define ORM_PAGE_OFF         16  /* paged append writes one row past the cache position */
+#define ORM_GATED_WGROUP     17  /* gated norm ignores w_groups (always weight row 0) */
+#define ORM_GATED_ORDER      18  /* gate_first handled as gate-after */
+#define ORM_SIGMOID_SIGN     19  /* sigmoid uses exp(+x) */
+#define ORM_QG_SWAP          20  /* deinterleave returns q and g exchanged */
 
 /* Conversions (round to nearest even; NaN -> canonical quiet NaN). */
 uint16_t oracle_f32_to_f16(float f);
@@ -85,6 +90,27 @@ int oracle_rope(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head
                 const void* q_norm, const void* k_norm, int norm_dtype,
                 float norm_eps, float norm_constant_bias,
                 int rope_mode, float attn_factor, int nthreads);
+
+/*
+ * Gated RMSNorm (gated_rms_norm_kernel, reference kernels/norm.cu:482-581; host checks 591-668):
+ *   a = act(g) in fp32 (gate_act 0 silu, 1 sigmoid);
+ *   gate_first: v = fl32(x * a) and the row sum is over v; otherwise v = x;
+ *   rmf = 1 / sqrtf(sum(v^2) / dim + eps);  w row = row % w_groups, plus constant_bias when it is != 0;
+ *   y = (v * w) * rmf (gate_first) or ((x * w) * rmf) * a, rounded once to y's dtype.
+ * x, w, g, y: F16 / BF16 / F32 (w may be NULL: no weight); x is not clamped.
+ */
+int oracle_gated_rms_norm(const void* x, int x_dtype, int64_t ldx, const void* w, int w_dtype, int w_groups,
+                          void* y, int y_dtype, int64_t ldy, const void* g, int g_dtype, int64_t ldg,
+                          int64_t rows, int64_t dim, float eps, float constant_bias, int gate_first, int gate_act,
+                          int nthreads);
+
+/*
+ * Split per-head interleaved rows [rows, heads, 2 * head_dim] into q [rows, heads, head_dim] and
+ * g [rows, heads * head_dim] (deinterleave_qg, reference kernels/activation.cu:721-779); row strides in
+ * elements.  A bit copy of 16-bit elements.
+ */
+int oracle_deinterleave_qg(const void* qg, int64_t ldqg, void* q, int64_t ldq, void* g, int64_t ldg,
+                           int64_t rows, int heads, int head_dim, int nthreads);
 
 /*
  * Paged KV-cache append (paged_kv_update_vec8_kernel, reference kernels/generator/cache.cu:143-243):
