@@ -32,7 +32,8 @@ PEAK_GBS = 8000.0            # MI355X HBM3E
 METRIC = "fused norm/act/RoPE/embed HBM GB/s + % of MI355X peak; decode-step us"
 OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "gather_norm_c5", "rms_c1",
        "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "rope_kv_prefill",
-       "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "calib_copy", "calib_copy_cached"]
+       "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
+       "deinterleave_q35", "calib_copy", "calib_copy_cached"]
 
 
 def log(*a):
@@ -225,6 +226,49 @@ def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64):
     return Work(name, nbytes, launch, f"q/k norm + RoPE + paged KV append bsz {bsz} x {seq} tokens, {kind}", sets)
 
 
+def make_gated(name, kind, tokens=4096, heads=32, hd=128, seed=600):
+    """Qwen3.5-style gated ops over a prefill of `tokens`: the gated-delta-net output norm (bf16 core,
+    f32 gate, f32 weight, f16 out, rows = tokens x heads of hd), the attention output gate
+    x *= sigmoid(g) in place (f16 [tokens, heads * hd]), and the q | g split of the q projection."""
+    import torch
+    import exl3r.ffi as ffi
+    n = tokens * heads * hd
+    if kind == "norm":
+        nbytes = n * (2 + 4 + 2) + hd * 4
+        sets = sets_for(nbytes)
+        bufs = [(gen((tokens * heads, hd), 0.0, 1.0, torch.bfloat16, seed + 3 * k),
+                 gen((tokens * heads, hd), 0.0, 2.0, torch.float32, seed + 3 * k + 1),
+                 torch.empty((tokens * heads, hd), device="cuda", dtype=torch.float16)) for k in range(sets)]
+        w = gen((hd,), 1.0, 0.1, torch.float32, seed + 99)
+
+        def launch(i):
+            x, g, y = bufs[i % sets]
+            ffi.gated_rms_norm(x, w, y, g, 1e-6, 0.0, 1, False, 0)
+        desc = f"gated RMSNorm (silu gate) [{tokens * heads},{hd}] bf16 x, f32 g, f16 y"
+    elif kind == "sigmoid":
+        nbytes = 3 * n * 2
+        sets = sets_for(nbytes)
+        bufs = [(gen((tokens, heads * hd), 0.0, 1.0, torch.float16, seed + 2 * k),
+                 gen((tokens, heads * hd), 0.0, 2.0, torch.float16, seed + 2 * k + 1)) for k in range(sets)]
+
+        def launch(i):
+            x, g = bufs[i % sets]
+            ffi.mul_sigmoid_(x, g)
+        desc = f"x *= sigmoid(g) in place [{tokens},{heads * hd}] f16"
+    else:
+        nbytes = 4 * n * 2
+        sets = sets_for(nbytes)
+        bufs = [(gen((tokens, heads * 2 * hd), 0.0, 1.0, torch.float16, seed + k),
+                 torch.empty((tokens, heads, hd), device="cuda", dtype=torch.float16),
+                 torch.empty((tokens, heads * hd), device="cuda", dtype=torch.float16)) for k in range(sets)]
+
+        def launch(i):
+            qg, q, g = bufs[i % sets]
+            ffi.deinterleave_qg(qg, q, g, hd)
+        desc = f"q | g deinterleave [{tokens},{heads},2x{hd}] f16"
+    return Work(name, nbytes, launch, desc, sets)
+
+
 def make_copy(name, cached=False):
     import torch
     import exl3r
@@ -324,6 +368,9 @@ def make_all(only=None):
         "rope_kv_prefill_unfused": lambda: make_rope_kv("rope_kv_prefill_unfused", 1, 4096, False),
         "rope_kv_dec": lambda: make_rope_kv("rope_kv_dec", 64, 1, True, max_blocks=16),
         "rope_kv_dec_unfused": lambda: make_rope_kv("rope_kv_dec_unfused", 64, 1, False, max_blocks=16),
+        "gated_norm_q35": lambda: make_gated("gated_norm_q35", "norm"),
+        "mul_sigmoid_q35": lambda: make_gated("mul_sigmoid_q35", "sigmoid"),
+        "deinterleave_q35": lambda: make_gated("deinterleave_q35", "deinterleave"),
         "calib_copy": lambda: make_copy("calib_copy"),
         "calib_copy_cached": lambda: make_copy("calib_copy_cached", cached=True),
     }

@@ -36,6 +36,7 @@ constexpr int64_t kMaxGridX = 1 << 20;
 struct Tuning
 {
     int rms_maxv = 0, rms_threads = 0;
+    int rms_rows_rpl = 0;    // short-row RMSNorm kernel: rows per lane in flight (1, 2, 4; 0 auto)
     int act_unroll = 0, act_threads = 0, act_blocks_per_cu = 0;
     int rope_iters = 0;
     int rope_tok = 0;       // 0 auto, 1 never the wave-per-token kernel, 2 always (where it applies)

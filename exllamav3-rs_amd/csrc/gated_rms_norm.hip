@@ -31,13 +31,22 @@ extern "C" int exl3r_gated_rms_norm(const void* x, int xt, int64_t ldx, const vo
     a.gact = gate_act; a.gfirst = gate_first != 0; a.w_groups = w_groups;
     hipStream_t s = (hipStream_t)stream;
 
+    // Short rows (head-dim rows of the gated-delta-net output) take the lanes-per-row kernel for the
+    // reference's gate types (bf16 / f32); everything else the workgroup-per-row kernel.
+    const bool short_rows = dim <= 512 && (gt == EXL3R_F32 || gt == EXL3R_BF16);
     if (xt != EXL3R_F32 && rms_vec_ok(a, xt, yt, gt, true))
     {
         auto go_x = [&](auto X) {
             with_float_type(yt, [&](auto Y) {
-                with_float_type(gt, [&](auto G) {
-                    launch_rms_vec<decltype(X), decltype(Y), decltype(G), RMS_GATED>(a, s);
-                });
+                using XTy = decltype(X);
+                using YTy = decltype(Y);
+                if (short_rows)
+                {
+                    if (gt == EXL3R_F32) launch_rms_rows<XTy, YTy, TF32, RMS_GATED>(a, s);
+                    else launch_rms_rows<XTy, YTy, TBF16, RMS_GATED>(a, s);
+                    return;
+                }
+                with_float_type(gt, [&](auto G) { launch_rms_vec<XTy, YTy, decltype(G), RMS_GATED>(a, s); });
             });
         };
         if (xt == EXL3R_F16) go_x(TF16{});

@@ -135,79 +135,143 @@ __device__ __forceinline__ void rms_load(const RmsArgs& a, int64_t row, int tid,
 
 // Arithmetic and stores of one loaded row; the row sum is reduced across the workgroup (DPP butterfly
 // inside each wave, one LDS hop across waves).
+// The cached form of a row between the passes: x as loaded, or the rounded residual.
+template <class XT, class RT, int MODE>
+using RmsCache = std::conditional_t<MODE == RMS_RES_IN, RT, XT>;
+
+// Pass 1 of the 8-element chunk at element e of a row: clamp (f16 x), residual update (RES_IN),
+// gathered-row copy (GATHER), gate before the norm (GATED), and the chunk's squares added to ss
+// (fp64: squares and sums of 16-bit data are exact).  Returns the chunk's cached form.
+template <class XT, class RT, int MODE>
+__device__ __forceinline__ typename RmsCache<XT, RT, MODE>::Vec rms_chunk1(const RmsArgs& a, char* rrow, int64_t e,
+                                                                          bool valid, typename XT::Vec& xv,
+                                                                          const typename RT::Vec& rv, double& ss)
+{
+    using CT = RmsCache<XT, RT, MODE>;
+    typename CT::Vec cv;
+    float h[8];
+    if (valid)
+        unpack8<XT>(xv, h);
+    else
+    {
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = 0.0f;
+        xv = pack8<XT>(h);
+    }
+    if constexpr (MODE != RMS_GATHER && MODE != RMS_GATED && XT::code == DT_F16)
+    {
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = clamp_f16(h[j]);
+    }
+    if constexpr (MODE == RMS_GATED)
+    {
+        if (a.gfirst)
+        {
+            float gf[8];
+            unpack8<RT>(rv, gf);
+            #pragma unroll
+            for (int j = 0; j < 8; ++j) h[j] = h[j] * gate_act(a.gact, gf[j]);
+        }
+    }
+    if constexpr (MODE == RMS_RES_IN)
+    {
+        float rf[8];
+        unpack8<RT>(rv, rf);
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = h[j] + rf[j];
+        cv = pack8<RT>(h);
+        store8<RT>(rrow, e, cv);
+        unpack8<RT>(cv, h);   // the norm sees the rounded residual
+    }
+    else
+        cv = xv;
+    if constexpr (MODE == RMS_GATHER && RT::code >= 0)
+    {
+        if (a.r)
+        {
+            if constexpr (RT::code == XT::code)
+                store8<XT>(rrow, e, xv);        // bit-exact copy
+            else
+                store8<RT>(rrow, e, pack8<RT>(h)); // exact upcast
+        }
+    }
+    #pragma unroll
+    for (int j = 0; j < 8; ++j) ss = fma((double)h[j], (double)h[j], ss);
+    return cv;
+}
+
+// Pass 2 of the chunk at element e: gate (GATED), weight (row offset wofs), scale, gate after the
+// norm (GATED), one rounding, store.
+template <class XT, class YT, class RT, int MODE>
+__device__ __forceinline__ void rms_chunk2(const RmsArgs& a, char* yrow, int64_t e, int64_t wofs,
+                                           const typename RmsCache<XT, RT, MODE>::Vec& cv,
+                                           const typename RT::Vec& rv, u32x4 wv, float rmf)
+{
+    float h[8];
+    unpack8<RmsCache<XT, RT, MODE>>(cv, h);
+    if constexpr (MODE == RMS_PLAIN && XT::code == DT_F16)
+    {
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = clamp_f16(h[j]);
+    }
+    float ga[8];
+    if constexpr (MODE == RMS_GATED)
+    {
+        float gf[8];
+        unpack8<RT>(rv, gf);
+        #pragma unroll
+        for (int j = 0; j < 8; ++j)
+        {
+            ga[j] = gate_act(a.gact, gf[j]);
+            if (a.gfirst) h[j] = h[j] * ga[j];
+        }
+    }
+    float o[8];
+    if (a.w)
+    {
+        float wf[8];
+        unpack_w8(wv, a.w, a.wt, wofs + e, wf);
+        if (a.cb != 0.0f)
+        {
+            #pragma unroll
+            for (int j = 0; j < 8; ++j) wf[j] = wf[j] + a.cb;
+        }
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = (h[j] * wf[j]) * rmf;
+    }
+    else
+    {
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = h[j] * rmf;
+    }
+    if constexpr (MODE == RMS_GATED)
+    {
+        if (!a.gfirst)
+        {
+            #pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = o[j] * ga[j];
+        }
+    }
+    store8<YT>(yrow, e, pack8<YT>(o));
+}
+
 template <class XT, class YT, class RT, int MAXV, int MODE>
 __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int tid, int nt, RowRegs<XT, RT, MAXV>& L,
                                            double* red)
 {
     const int nc = a.dim >> 3;
-    const bool has_w = a.w != nullptr;
-    const bool valid = L.valid;
     char* rrow = (char*)a.r + row * a.ldr * RT::bytes;
     char* yrow = (char*)a.y + row * a.ldy * YT::bytes;
-    auto& xv = L.xv;
-    auto& rv = L.rv;
-    auto& wv = L.wv;
-    // Pass 1: residual update and sum of squares.  The row is then cached in its narrowest
-    // exact form (x as loaded, or the rounded residual), 4 VGPRs per chunk for 16-bit data,
-    // and re-expanded in pass 2.
-    using CT = std::conditional_t<MODE == RMS_RES_IN, RT, XT>;
-    typename CT::Vec cache[MAXV];
+    // Pass 1: residual update and sum of squares.  The row is then cached in its narrowest exact
+    // form (x as loaded, or the rounded residual), 4 VGPRs per chunk for 16-bit data, and
+    // re-expanded in pass 2.
+    typename RmsCache<XT, RT, MODE>::Vec cache[MAXV];
     double ss = 0.0;
     #pragma unroll
     for (int k = 0; k < MAXV; ++k)
     {
         const int c = tid + k * nt;
-        if (c < nc)
-        {
-            float h[8];
-            if (valid)
-                unpack8<XT>(xv[k], h);
-            else
-            {
-                #pragma unroll
-                for (int j = 0; j < 8; ++j) h[j] = 0.0f;
-                xv[k] = pack8<XT>(h);
-            }
-            if constexpr (MODE != RMS_GATHER && MODE != RMS_GATED && XT::code == DT_F16)
-            {
-                #pragma unroll
-                for (int j = 0; j < 8; ++j) h[j] = clamp_f16(h[j]);
-            }
-            if constexpr (MODE == RMS_GATED)
-            {
-                if (a.gfirst)
-                {
-                    float gf[8];
-                    unpack8<RT>(rv[k], gf);
-                    #pragma unroll
-                    for (int j = 0; j < 8; ++j) h[j] = h[j] * gate_act(a.gact, gf[j]);
-                }
-            }
-            if constexpr (MODE == RMS_RES_IN)
-            {
-                float rf[8];
-                unpack8<RT>(rv[k], rf);
-                #pragma unroll
-                for (int j = 0; j < 8; ++j) h[j] = h[j] + rf[j];
-                cache[k] = pack8<RT>(h);
-                store8<RT>(rrow, (int64_t)c * 8, cache[k]);
-                unpack8<RT>(cache[k], h);   // the norm sees the rounded residual
-            }
-            else
-                cache[k] = xv[k];
-            if constexpr (MODE == RMS_GATHER && RT::code >= 0)
-            {
-                if (a.r)
-                {
-                    if constexpr (RT::code == XT::code)
-                        store8<XT>(rrow, (int64_t)c * 8, xv[k]);        // bit-exact copy
-                    else
-                        store8<RT>(rrow, (int64_t)c * 8, pack8<RT>(h)); // exact upcast
-                }
-            }
-            #pragma unroll
-            for (int j = 0; j < 8; ++j) ss = fma((double)h[j], (double)h[j], ss);
-        }
+        if (c < nc) cache[k] = rms_chunk1<XT, RT, MODE>(a, rrow, (int64_t)c * 8, L.valid, L.xv[k], L.rv[k], ss);
     }
 
     // fp64 row sum (exact for 16-bit data), one rounding, IEEE fp32 sqrt and divide.
@@ -215,61 +279,13 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
     const float rmf = rms_factor(ss, a.dim, a.eps) * a.cs;
 
     // Pass 2: scale, weight, round once, store.
+    const int64_t wofs = weight_row<MODE>(a, row);
     #pragma unroll
     for (int k = 0; k < MAXV; ++k)
     {
         const int c = tid + k * nt;
-        if (c < nc)
-        {
-            float h[8];
-            unpack8<CT>(cache[k], h);
-            if constexpr (MODE == RMS_PLAIN && XT::code == DT_F16)
-            {
-                #pragma unroll
-                for (int j = 0; j < 8; ++j) h[j] = clamp_f16(h[j]);
-            }
-            float ga[8];
-            if constexpr (MODE == RMS_GATED)
-            {
-                float gf[8];
-                unpack8<RT>(rv[k], gf);
-                #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                {
-                    ga[j] = gate_act(a.gact, gf[j]);
-                    if (a.gfirst) h[j] = h[j] * ga[j];
-                }
-            }
-            float o[8];
-            if (has_w)
-            {
-                float wf[8];
-                unpack_w8(wv[k], a.w, a.wt, weight_row<MODE>(a, row) + (int64_t)c * 8, wf);
-                if (a.cb != 0.0f)
-                {
-                    #pragma unroll
-                    for (int j = 0; j < 8; ++j) wf[j] = wf[j] + a.cb;
-                }
-                #pragma unroll
-                for (int j = 0; j < 8; ++j) o[j] = (h[j] * wf[j]) * rmf;
-            }
-            else
-            {
-                #pragma unroll
-                for (int j = 0; j < 8; ++j) o[j] = h[j] * rmf;
-            }
-            if constexpr (MODE == RMS_GATED)
-            {
-                if (!a.gfirst)
-                {
-                    #pragma unroll
-                    for (int j = 0; j < 8; ++j) o[j] = o[j] * ga[j];
-                }
-            }
-            store8<YT>(yrow, (int64_t)c * 8, pack8<YT>(o));
-        }
+        if (c < nc) rms_chunk2<XT, YT, RT, MODE>(a, yrow, (int64_t)c * 8, wofs, cache[k], L.rv[k], L.wv[k], rmf);
     }
-
 }
 
 template <class XT, class YT, class RT, int MAXV, int MODE>
@@ -286,6 +302,78 @@ __global__ __launch_bounds__(1024) void k_rms_norm(RmsArgs a)
     __shared__ double red[16];
     for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x)
         rms_row<XT, YT, RT, MAXV, MODE>(a, row, threadIdx.x, blockDim.x, red);
+}
+
+// Short rows (at most 64 chunks of 8): LPR lanes per row (a power of two covering dim / 8), one
+// chunk per lane, 256 / LPR rows per workgroup and RPL rows per lane in flight.  The row sum is a
+// DPP butterfly inside the LPR-lane group -- no LDS, no barrier -- so a 128-element head row costs
+// 16 lanes instead of a workgroup.
+template <class XT, class YT, class RT, int LPR, int RPL, int MODE>
+__global__ __launch_bounds__(256) void k_rms_rows(RmsArgs a)
+{
+    static_assert(MODE != RMS_GATHER, "gathered rows take the workgroup kernel");
+    constexpr int SLOTS = 256 / LPR;
+    const int lane = threadIdx.x % LPR;
+    const int slot = threadIdx.x / LPR;
+    const bool lane_ok = lane < (a.dim >> 3);
+    const int64_t e = (int64_t)lane * 8;
+    for (int64_t r0 = (int64_t)blockIdx.x * SLOTS * RPL; r0 < a.rows; r0 += (int64_t)gridDim.x * SLOTS * RPL)
+    {
+        typename XT::Vec xv[RPL];
+        typename RT::Vec rv[RPL];
+        u32x4 wv[RPL];
+        bool act[RPL];
+        #pragma unroll
+        for (int i = 0; i < RPL; ++i)
+        {
+            const int64_t row = r0 + (int64_t)i * SLOTS + slot;
+            act[i] = lane_ok && row < a.rows;
+            if (act[i])
+            {
+                xv[i] = load8s<XT>((const char*)a.x + row * a.ldx * XT::bytes, e);
+                if constexpr (MODE == RMS_RES_IN || MODE == RMS_GATED)
+                    rv[i] = load8s<RT>((const char*)a.r + row * a.ldr * RT::bytes, e);
+                if (a.w) wv[i] = prefetch_w8(a.w, a.wt, weight_row<MODE>(a, row) + e);
+            }
+        }
+        #pragma unroll
+        for (int i = 0; i < RPL; ++i)
+        {
+            const int64_t row = r0 + (int64_t)i * SLOTS + slot;
+            double ss = 0.0;
+            typename RmsCache<XT, RT, MODE>::Vec cv;
+            if (act[i]) cv = rms_chunk1<XT, RT, MODE>(a, (char*)a.r + row * a.ldr * RT::bytes, e, true, xv[i], rv[i], ss);
+            ss = group_sum64<LPR>(ss);
+            const float rmf = rms_factor(ss, a.dim, a.eps) * a.cs;
+            if (act[i])
+                rms_chunk2<XT, YT, RT, MODE>(a, (char*)a.y + row * a.ldy * YT::bytes, e, weight_row<MODE>(a, row), cv,
+                                             rv[i], wv[i], rmf);
+        }
+    }
+}
+
+template <class XT, class YT, class RT, int MODE>
+void launch_rms_rows(const RmsArgs& a, hipStream_t s)
+{
+    const int nc = a.dim >> 3;
+    auto go = [&](auto L) {
+        constexpr int LPR = decltype(L)::value;
+        constexpr int SLOTS = 256 / LPR;
+        const int tuned = tuning().rms_rows_rpl;
+        // One row per lane: at 62 VGPRs (f32 gate) 8 waves per SIMD keep the loads in flight.  Measured
+        // on MI355X, gated norm [131072, 128] bf16 x / f32 g / f16 y: 1 row per lane 25.2 us, 2 rows
+        // 30.6 us, 4 rows (156 VGPRs) 33.4 us; a workgroup per row 63 us.
+        const int rpl = (tuned == 1 || tuned == 2 || tuned == 4) ? tuned : 1;
+        int64_t blocks = (a.rows + (int64_t)SLOTS * rpl - 1) / ((int64_t)SLOTS * rpl);
+        if (blocks > kMaxGridX) blocks = kMaxGridX;
+        if (rpl == 4) k_rms_rows<XT, YT, RT, LPR, 4, MODE><<<(unsigned)blocks, 256, 0, s>>>(a);
+        else if (rpl == 2) k_rms_rows<XT, YT, RT, LPR, 2, MODE><<<(unsigned)blocks, 256, 0, s>>>(a);
+        else k_rms_rows<XT, YT, RT, LPR, 1, MODE><<<(unsigned)blocks, 256, 0, s>>>(a);
+    };
+    if (nc <= 8) go(std::integral_constant<int, 8>{});
+    else if (nc <= 16) go(std::integral_constant<int, 16>{});
+    else if (nc <= 32) go(std::integral_constant<int, 32>{});
+    else go(std::integral_constant<int, 64>{});
 }
 
 // Generic fallback: any dim, any alignment, element-granular, two passes over global memory.

@@ -7,6 +7,8 @@
 extern "C" {
 #endif
 EXL3R_API void exl3r_tune_rms(int maxv, int threads);
+/* short-row RMSNorm kernel: rows per lane in flight (1, 2, 4; 0 auto) */
+EXL3R_API void exl3r_tune_rms_rows(int rows_per_lane);
 EXL3R_API void exl3r_tune_act(int unroll, int threads, int blocks_per_cu);
 /* heads per lane: 1, 2 or 4 */
 EXL3R_API void exl3r_tune_rope(int iters);

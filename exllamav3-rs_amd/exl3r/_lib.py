@@ -43,6 +43,7 @@ PROTOTYPES = {
     "exl3r_tune_rms": (None, [_i, _i]),
     "exl3r_tune_act": (None, [_i, _i, _i]),
     "exl3r_tune_rope": (None, [_i]),
+    "exl3r_tune_rms_rows": (None, [_i]),
     "exl3r_tune_rope_tok": (None, [_i, _i, _i]),
     "exl3r_tune_embed": (None, [_i]),
 }
