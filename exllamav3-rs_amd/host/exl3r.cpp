@@ -223,6 +223,40 @@ static void act(int which, const Tensor& x, const Tensor& y, const Tensor& z, fl
 void silu_mul(const Tensor& x, const Tensor& y, const Tensor& z, float act_limit, const Stream& s) { act(0, x, y, z, act_limit, s); }
 void gelu_mul(const Tensor& x, const Tensor& y, const Tensor& z, float act_limit, const Stream& s) { act(1, x, y, z, act_limit, s); }
 
+void gated_rms_norm(const Tensor& x, const Tensor* w, const Tensor& y, const Tensor& g, float eps, float bias,
+                    int w_groups, bool gate_first, int gate_act, const Stream& s)
+{
+    int64_t rows, dim, ldx, ry, dy, ldy, rg, dg, ldg;
+    x.rows_view(rows, dim, ldx);
+    y.rows_view(ry, dy, ldy);
+    g.rows_view(rg, dg, ldg);
+    require(ry == rows && dy == dim && rg == rows && dg == dim, "gated_rms_norm: x, y and g shapes differ");
+    require(!w || w->numel() == (int64_t)w_groups * dim, "gated_rms_norm: w must hold w_groups * dim values");
+    check_abi(exl3r_gated_rms_norm(x.data, code(x.dtype), ldx, ptr(w), code_or(w, DType::F32), w_groups, y.data,
+                                   code(y.dtype), ldy, g.data, code(g.dtype), ldg, rows, dim, eps, bias, gate_first ? 1 : 0,
+                                   gate_act, s.get()));
+}
+
+void mul_sigmoid_(const Tensor& x, const Tensor& y, const Stream& s)
+{
+    int64_t rows, cols, ldx, ry, cy, ldy;
+    x.rows_view(rows, cols, ldx);
+    y.rows_view(ry, cy, ldy);
+    require(ry == rows && cy == cols && x.dtype == y.dtype, "mul_sigmoid_: x and y must share shape and dtype");
+    check_abi(exl3r_mul_sigmoid(x.data, y.data, code(x.dtype), x.data, code(x.dtype), rows, cols, ldx, ldy, ldx, s.get()));
+}
+
+void deinterleave_qg(const Tensor& qg, const Tensor& q, const Tensor& g, int64_t head_dim, const Stream& s)
+{
+    require(head_dim > 0 && qg.size(-1) % (2 * head_dim) == 0, "deinterleave_qg: qg's last dim must be heads * 2 * head_dim");
+    require(qg.is_contiguous() && q.is_contiguous() && g.is_contiguous(), "deinterleave_qg: tensors must be contiguous");
+    const int64_t heads = qg.size(-1) / (2 * head_dim), rows = qg.numel() / qg.size(-1);
+    require(q.numel() == rows * heads * head_dim && g.numel() == q.numel(), "deinterleave_qg: size mismatch");
+    require(q.dtype == qg.dtype && g.dtype == qg.dtype, "deinterleave_qg: qg, q and g must share a dtype");
+    check_abi(exl3r_deinterleave_qg(qg.data, 2 * heads * head_dim, q.data, heads * head_dim, g.data, heads * head_dim,
+                                    code(qg.dtype), rows, (int)heads, (int)head_dim, s.get()));
+}
+
 void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
           int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
           float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s, const Tensor* position_ids)

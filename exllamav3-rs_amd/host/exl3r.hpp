@@ -124,6 +124,15 @@ void rms_norm_res_in(const Tensor& x, const Tensor* w, const Tensor& y, const Te
 // src/ffi.rs:492-499: z = act(x) * y; act_limit 0 disables clamping.
 void silu_mul(const Tensor& x, const Tensor& y, const Tensor& z, float act_limit, const Stream& s);
 void gelu_mul(const Tensor& x, const Tensor& y, const Tensor& z, float act_limit, const Stream& s);
+// src/ffi.rs:479-483: y = RMSNorm(x) * (w + bias) * act(g), or RMSNorm(x * act(g)) * (w + bias) with
+// gate_first; act = silu (gate_act 0) or sigmoid (1); w may be null or hold w_groups rows of dim.
+void gated_rms_norm(const Tensor& x, const Tensor* w, const Tensor& y, const Tensor& g, float eps, float bias,
+                    int w_groups, bool gate_first, int gate_act, const Stream& s);
+// src/ffi.rs:616-618: x *= sigmoid(y), in place.
+void mul_sigmoid_(const Tensor& x, const Tensor& y, const Stream& s);
+// src/ffi.rs:622-624: split [.., heads * 2 * head_dim] interleaved (q | g) rows into q [.., heads, head_dim] and
+// g [.., heads * head_dim].
+void deinterleave_qg(const Tensor& qg, const Tensor& q, const Tensor& g, int64_t head_dim, const Stream& s);
 // src/ffi.rs:298-333: fused (optional) q/k head RMSNorm + RoPE on (bsz, seq, heads, head_dim)
 // tensors; positions (int32 [bsz]) or position_ids (int32 [bsz, seq]) override position.
 void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,

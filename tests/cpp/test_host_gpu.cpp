@@ -224,6 +224,43 @@ int main()
                       caches ? "bitwise" : "DIFFER");
         report("RoPE::apply_paged neox f16 + paged append", dq == 0 && dk == 0 && caches, msg);
     }
+    // Gated ops: gated_rms_norm (bf16 x, f32 gate and weight, f16 y), mul_sigmoid_, deinterleave_qg.
+    {
+        const int rows = 40, dim = 128, heads = 4, hd = 32;
+        auto xh = host_normal(DType::BF16, rows * dim, 0.f, 1.f);
+        auto gh = host_normal(DType::F32, rows * dim, 0.f, 2.f);
+        auto wh = host_normal(DType::F32, dim, 1.f, 0.1f);
+        auto x = upload(xh, DType::BF16, { rows, dim }, s), g = upload(gh, DType::F32, { rows, dim }, s);
+        auto w = upload(wh, DType::F32, { dim }, s);
+        OwnedTensor y = OwnedTensor::empty(DType::F16, { rows, dim });
+        ffi::gated_rms_norm(x.t, &w.t, y.t, g.t, 1e-6f, 0.f, 1, false, 0, s);
+        auto yo = download(y, s);
+        std::vector<uint8_t> ey(yo.size());
+        oracle_gated_rms_norm(xh.data(), OR_BF16, dim, wh.data(), OR_F32, 1, ey.data(), OR_F16, dim, gh.data(), OR_F32,
+                              dim, rows, dim, 1e-6f, 0.f, 0, 0, 1);
+        const int64_t dy = max_ulp16(yo, ey);
+        std::snprintf(msg, sizeof msg, "max ulp %lld", (long long)dy);
+        report("ffi::gated_rms_norm silu gate", dy <= 1, msg);
+
+        auto ah = host_normal(DType::F16, rows * dim, 0.f, 2.f), bh = host_normal(DType::F16, rows * dim, 0.f, 3.f);
+        auto av = upload(ah, DType::F16, { rows, dim }, s), bv = upload(bh, DType::F16, { rows, dim }, s);
+        ffi::mul_sigmoid_(av.t, bv.t, s);
+        auto ao = download(av, s);
+        std::vector<uint8_t> ea(ao.size());
+        oracle_act_mul(OR_ACT_SIGMOID, bh.data(), ah.data(), OR_F16, ea.data(), OR_F16, rows, dim, dim, dim, dim, 0.f, 1);
+        const int64_t da = max_ulp16(ao, ea);
+        std::snprintf(msg, sizeof msg, "max ulp %lld", (long long)da);
+        report("ffi::mul_sigmoid_", da <= 1, msg);
+
+        auto qgh = host_normal(DType::F16, rows * heads * 2 * hd, 0.f, 1.f);
+        auto qg = upload(qgh, DType::F16, { rows, heads * 2 * hd }, s);
+        OwnedTensor q = OwnedTensor::empty(DType::F16, { rows, heads, hd }), gg = OwnedTensor::empty(DType::F16, { rows, heads * hd });
+        ffi::deinterleave_qg(qg.t, q.t, gg.t, hd, s);
+        auto qo = download(q, s), go = download(gg, s);
+        std::vector<uint8_t> eq(qo.size()), eg(go.size());
+        oracle_deinterleave_qg(qgh.data(), heads * 2 * hd, eq.data(), heads * hd, eg.data(), heads * hd, rows, heads, hd, 1);
+        report("ffi::deinterleave_qg", qo == eq && go == eg, qo == eq && go == eg ? "bitwise" : "DIFFER");
+    }
     std::printf(failures ? "test_host_gpu: %d failures\n" : "test_host_gpu: all passed\n", failures);
     return failures ? 1 : 0;
 }
