@@ -221,6 +221,16 @@ def rope_paged_kv(q, out_q, k, out_k, v, inv_freq, position, positions, q_norm, 
                                      _ptr(err_flag), _stream(q, stream)))
 
 
+def argmax_sample(logits, ids, max_logit=0, stream=None):
+    """ids[i] = first index of the maximum of logits[i, :max_logit] (NaN maximal), int64
+    (src/ffi.rs:521-525; the generator's batched argmax)."""
+    rows, vocab, ld = _rows(logits)
+    if ids.dtype != torch.int64 or ids.numel() != rows:
+        raise ValueError("ids must be int64 with one entry per row")
+    check(load().exl3r_argmax_sample(_ptr(logits), dtype_code(logits), rows, vocab, ld, int(max_logit), _ptr(ids),
+                                     _stream(logits, stream)))
+
+
 def embedding(table, ids, out, err_flag=None, stream=None):
     """out[i] = table[ids[i]] (bit-exact, or exact upcast to f32)."""
     vocab, hidden = table.shape

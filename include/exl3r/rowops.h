@@ -31,6 +31,8 @@
  *   exl3r_gated_rms_norm    <- exl3_shim_gated_rms_norm   csrc/exl3_shim.cpp:143-147 (ffi.rs:118-124, 479-483)
  *   exl3r_mul_sigmoid       <- exl3_shim_mul_sigmoid_     csrc/exl3_shim.cpp:167     (ffi.rs:166, 616-618)
  *   exl3r_deinterleave_qg   <- exl3_shim_deinterleave_qg  csrc/exl3_shim.cpp:168-171 (ffi.rs:167, 622-624)
+ *   exl3r_argmax_sample     <- exl3_shim_argmax_sample    csrc/exl3_shim.cpp:229-231 (ffi.rs:136, 521-525) and the
+ *                              generator's batched tch argmax over [bsz, vocab] logits  src/generator.rs:1596
  *   exl3r_embedding         <- Embedding::forward's tch index_select + to_kind   src/modules.rs:430-436
  *   exl3r_embedding_rms_norm<- embed followed by RmsNorm::forward (MTP head)    src/mtp.rs:189-190
  */
@@ -213,6 +215,18 @@ EXL3R_API int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_stri
                         void* k_cache, void* v_cache, int page_size, int64_t num_pages,
                         const int32_t* block_table, int64_t max_blocks_per_seq, const int32_t* cache_seqlens,
                         int32_t* err_flag, void* stream);
+
+/*
+ * Row argmax of logits [rows, vocab] (row stride ld elements; F16/BF16/F32) into int64 ids[rows]:
+ * the first index of the row maximum among indices < max_logit (max_logit <= 0 or > vocab: the whole
+ * row), NaN counting as the maximum (the first NaN wins), -0 equal to +0 (torch.argmax's rule).
+ * Replaces exl3_shim_argmax_sample (csrc/exl3_shim.cpp:229-231 -> kernels/generator/sampling_basic.cu:
+ * 65-92, 151-172; its mask swaps the two boundary elements when max_logit is odd, here it is exact)
+ * and the generator's batched tch argmax (src/generator.rs:1596).  ids must be 8-byte aligned; it is
+ * used as the reduction slot during the call (three launches on `stream`).
+ */
+EXL3R_API int exl3r_argmax_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                        int max_logit, int64_t* ids, void* stream);
 
 /*
  * Token-embedding gather: out[i, :] = table[ids[i], :], bit-exact (same dtype) or exactly upcast to

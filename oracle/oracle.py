@@ -31,6 +31,7 @@ _PROTOS = {
     "oracle_gated_rms_norm": (_i, [_vp, _i, _i64, _vp, _i, _i, _vp, _i, _i64, _vp, _i, _i64, _i64, _i64, _f, _f, _i,
                                    _i, _i]),
     "oracle_deinterleave_qg": (_i, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i, _i, _i]),
+    "oracle_argmax": (_i, [_vp, _i, _i64, _i64, _i64, _i, _vp, _i]),
     "oracle_paged_kv_append": (_i, [_vp, _i64, _i64, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _vp, _i, _i64,
                                     _vp, _i64, _vp, _vp, _i]),
     "oracle_embedding_rms_norm": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _i64, _vp, _i,
@@ -138,6 +139,14 @@ def gated_rms_norm(x, xt, g, gt, yt, w=None, wt=F32, w_groups=1, eps=1e-6, cb=0.
     _check(load().oracle_gated_rms_norm(_p(x), xt, dim, _p(w), wt, w_groups, _p(y), yt, dim, _p(g), gt, dim, rows,
                                         dim, eps, cb, int(gate_first), gate_act, nthreads), "oracle_gated_rms_norm")
     return y
+
+
+def argmax(logits, dt, max_logit=0, nthreads=1):
+    """logits: [rows, vocab] storage array.  Returns int64 [rows]: first maximal index below max_logit."""
+    rows, vocab = logits.shape
+    ids = np.zeros(rows, np.int64)
+    _check(load().oracle_argmax(_p(logits), dt, rows, vocab, vocab, max_logit, _p(ids), nthreads), "oracle_argmax")
+    return ids
 
 
 def deinterleave_qg(qg, heads, hd, nthreads=1):

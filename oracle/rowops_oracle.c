@@ -437,6 +437,30 @@ static size_t dsize(int dt) { return dt == OR_F32 ? 4 : 2; }
 
 static int exact_conv(int from, int to) { return from == to || to == OR_F32; }
 
+/* torch.argmax over each row (first maximal index, NaN maximal); kernels/generator/sampling_basic.cu:65-92 */
+int oracle_argmax(const void* logits, int dt, int64_t rows, int64_t vocab, int64_t ldl, int max_logit, int64_t* ids,
+                  int nthreads)
+{
+    if (!logits || !ids || rows < 0 || vocab <= 0 || ldl < vocab) return -1;
+    if (!fdtype(dt)) return -2;
+    int64_t n = (max_logit <= 0 || max_logit > vocab || oracle_mutation == ORM_ARGMAX_NO_MASK) ? vocab : max_logit;
+    #pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t i = 0; i < rows; ++i)
+    {
+        int64_t best = 0;
+        float bv = ld(logits, dt, i * ldl + 0);
+        for (int64_t j = 1; j < n; ++j)
+        {
+            const float v = ld(logits, dt, i * ldl + j);
+            if (isnan(bv)) break;                                   /* the first NaN is final */
+            const int better = isnan(v) || v > bv || (oracle_mutation == ORM_ARGMAX_LAST_TIE && v == bv);
+            if (better) { bv = v; best = j; }
+        }
+        ids[i] = best;
+    }
+    return 0;
+}
+
 /* kernels/norm.cu:482-581 (kernel), 591-668 (host rules) */
 int oracle_gated_rms_norm(const void* x, int xt, int64_t ldx, const void* w, int wt, int w_groups,
                           void* y, int yt, int64_t ldy, const void* g, int gt, int64_t ldg,

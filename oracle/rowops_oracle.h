@@ -60,6 +60,8 @@ extern int oracle_mutation;
 #define ORM_GATED_ORDER      18  /* gate_first handled as gate-after */
 #define ORM_SIGMOID_SIGN     19  /* sigmoid uses exp(+x) */
 #define ORM_QG_SWAP          20  /* deinterleave returns q and g exchanged */
+#define ORM_ARGMAX_LAST_TIE  21  /* argmax ties go to the last index */
+#define ORM_ARGMAX_NO_MASK   22  /* argmax ignores max_logit */
 
 /* Conversions (round to nearest even; NaN -> canonical quiet NaN). */
 uint16_t oracle_f32_to_f16(float f);
@@ -111,6 +113,16 @@ int oracle_gated_rms_norm(const void* x, int x_dtype, int64_t ldx, const void* w
  */
 int oracle_deinterleave_qg(const void* qg, int64_t ldqg, void* q, int64_t ldq, void* g, int64_t ldg,
                            int64_t rows, int heads, int head_dim, int nthreads);
+
+/*
+ * Row argmax of logits [rows, vocab] (row stride ld; F16 / BF16 / F32) into int64 ids[rows]: the
+ * first index of the maximum among indices < max_logit (max_logit <= 0 or > vocab: the whole row),
+ * NaN counting as the maximum (the first NaN wins), -0 equal to +0 -- torch.argmax's rule, the batched
+ * argmax of the generator (src/generator.rs:1596) that exl3_shim_argmax_sample
+ * (kernels/generator/sampling_basic.cu:65-92, 151-172) also serves.
+ */
+int oracle_argmax(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld, int max_logit,
+                  int64_t* ids, int nthreads);
 
 /*
  * Paged KV-cache append (paged_kv_update_vec8_kernel, reference kernels/generator/cache.cu:143-243):
