@@ -257,6 +257,16 @@ void deinterleave_qg(const Tensor& qg, const Tensor& q, const Tensor& g, int64_t
                                     code(qg.dtype), rows, (int)heads, (int)head_dim, s.get()));
 }
 
+void argmax_sample(const Tensor& logits, const Tensor& ids, int max_logit, const Stream& s)
+{
+    int64_t rows, vocab, ld;
+    logits.rows_view(rows, vocab, ld);
+    require(ids.dtype == DType::I64 && ids.numel() == rows && ids.is_contiguous(),
+            "argmax_sample: ids must be contiguous int64 with one entry per logits row");
+    check_abi(exl3r_argmax_sample(logits.data, code(logits.dtype), rows, vocab, ld, max_logit,
+                                  static_cast<int64_t*>(ids.data), s.get()));
+}
+
 void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
           int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
           float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s, const Tensor* position_ids)

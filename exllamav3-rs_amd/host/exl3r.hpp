@@ -6,6 +6,9 @@
 // include/exl3r/rowops.h, with a small HIP device-buffer/stream type in place of tch:
 //
 //   exl3r::ffi::rms_norm / rms_norm_res_in / silu_mul / gelu_mul / rope  <- src/ffi.rs:293-333, 464-503
+//   exl3r::ffi::gated_rms_norm / mul_sigmoid_ / deinterleave_qg          <- src/ffi.rs:479-483, 616-624
+//   exl3r::ffi::rope_paged_kv                                            <- rope + paged append, src/modules.rs:666-704
+//   exl3r::ffi::argmax_sample                                            <- src/ffi.rs:521-525, src/generator.rs:1596
 //   exl3r::ffi::embedding                                                <- index_select, src/modules.rs:430-436
 //   exl3r::RmsNorm::forward / forward_res                                <- src/modules.rs:342-412
 //   exl3r::Embedding::forward                                            <- src/modules.rs:418-437
@@ -147,6 +150,9 @@ void rope_paged_kv(const Tensor& q, const Tensor& out_q, const Tensor& k, const 
                    const Tensor* k_norm, float norm_eps, float norm_constant_bias, RopeStyle rope_mode, float attn_factor,
                    const Tensor& k_cache, const Tensor& v_cache, const Tensor& block_table, const Tensor& cache_seqlens,
                    int32_t* err_flag, const Stream& s);
+// src/ffi.rs:521-525 (and the generator's batched argmax, src/generator.rs:1596): ids[i] = first index of the
+// maximum of logits[i, :max_logit] (whole row when max_logit <= 0), NaN maximal; ids int64 [rows].
+void argmax_sample(const Tensor& logits, const Tensor& ids, int max_logit, const Stream& s);
 // Embedding gather: out[i] = table[ids[i]] (bit-exact, or exact upcast to f32); err_flag optional.
 void embedding(const Tensor& table, const Tensor& ids, const Tensor& out, int32_t* err_flag, const Stream& s);
 // Gather fused with the following RMSNorm; h optional.

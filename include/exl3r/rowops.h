@@ -221,9 +221,11 @@ EXL3R_API int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_stri
  * the first index of the row maximum among indices < max_logit (max_logit <= 0 or > vocab: the whole
  * row), NaN counting as the maximum (the first NaN wins), -0 equal to +0 (torch.argmax's rule).
  * Replaces exl3_shim_argmax_sample (csrc/exl3_shim.cpp:229-231 -> kernels/generator/sampling_basic.cu:
- * 65-92, 151-172; its mask swaps the two boundary elements when max_logit is odd, here it is exact)
- * and the generator's batched tch argmax (src/generator.rs:1596).  ids must be 8-byte aligned; it is
- * used as the reduction slot during the call (three launches on `stream`).
+ * 65-92, 151-172; for an odd max_logit its pairwise mask, 57-60, also drops index max_logit - 1;
+ * here the mask is exact)
+ * and the generator's batched tch argmax (src/generator.rs:1596).  ids must be 8-byte aligned.  Below
+ * 512 rows ids is the reduction slot during the call (three launches on `stream`); from 512 rows a
+ * single launch writes it directly.
  */
 EXL3R_API int exl3r_argmax_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
                         int max_logit, int64_t* ids, void* stream);

@@ -261,6 +261,26 @@ int main()
         oracle_deinterleave_qg(qgh.data(), heads * 2 * hd, eq.data(), heads * hd, eg.data(), heads * hd, rows, heads, hd, 1);
         report("ffi::deinterleave_qg", qo == eq && go == eg, qo == eq && go == eg ? "bitwise" : "DIFFER");
     }
+    // argmax_sample: bf16 logits [6, 9000] with planted ties, masked to the first 8001 columns.
+    {
+        const int rows = 6, vocab = 9000, mask = 8001;
+        auto lh = host_normal(DType::BF16, rows * vocab, 0.f, 2.f);
+        const uint16_t big = oracle_f32_to_bf16(40.f);
+        for (int r = 0; r < rows; ++r)
+        {
+            std::memcpy(&lh[(r * vocab + 100 * r + 7) * 2], &big, 2);
+            std::memcpy(&lh[(r * vocab + 7900) * 2], &big, 2);
+            std::memcpy(&lh[(r * vocab + 8500) * 2], &big, 2);
+        }
+        auto l = upload(lh, DType::BF16, { rows, vocab }, s);
+        auto ids = OwnedTensor::empty(DType::I64, { rows });
+        ffi::argmax_sample(l.t, ids.t, mask, s);
+        auto got = download(ids, s);
+        std::vector<int64_t> want(rows);
+        oracle_argmax(lh.data(), OR_BF16, rows, vocab, vocab, mask, want.data(), 1);
+        const bool ok = std::memcmp(got.data(), want.data(), rows * 8) == 0 && want[3] == 307;
+        report("ffi::argmax_sample bf16 masked", ok, ok ? "exact" : "DIFFER");
+    }
     std::printf(failures ? "test_host_gpu: %d failures\n" : "test_host_gpu: all passed\n", failures);
     return failures ? 1 : 0;
 }
