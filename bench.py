@@ -33,7 +33,8 @@ METRIC = "fused norm/act/RoPE/embed HBM GB/s + % of MI355X peak; decode-step us"
 OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "gather_norm_c5", "rms_c1",
        "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "rope_kv_prefill",
        "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
-       "deinterleave_q35", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch", "calib_copy",
+       "deinterleave_q35", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
+       "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "calib_copy",
        "calib_copy_cached"]
 
 
@@ -290,6 +291,27 @@ def make_argmax(name, rows, use_torch, vocab=151936, seed=700):
                 sets)
 
 
+def make_gumbel(name, rows, use_torch, vocab=151936, seed=720):
+    """Categorical draw from softmax(f16 logits [rows, vocab]): exl3r_gumbel_sample (Gumbel-max, one
+    launch chain), or the reference sampler's tch path (src/sampler.rs:114: softmax, then
+    multinomial(1, replacement)) on the same tensor."""
+    import torch
+    import exl3r.ffi as ffi
+    nbytes = rows * vocab * 2 + rows * 8
+    sets = sets_for(nbytes)
+    bufs = [gen((rows, vocab), 0.0, 3.0, torch.float16, seed + k) for k in range(sets)]
+    ids = torch.empty(rows, dtype=torch.int64, device="cuda")
+
+    def launch(i):
+        x = bufs[i % sets]
+        if use_torch:
+            torch.multinomial(torch.softmax(x.float(), dim=-1), 1, True)
+        else:
+            ffi.gumbel_sample(x, ids, 0, i)
+    what = "torch softmax + multinomial" if use_torch else "exl3r Gumbel-max"
+    return Work(name, nbytes, launch, f"categorical draw over f16 logits [{rows},{vocab}] ({what})", sets)
+
+
 def make_copy(name, cached=False):
     import torch
     import exl3r
@@ -396,6 +418,9 @@ def make_all(only=None):
         "argmax_dec_torch": lambda: make_argmax("argmax_dec_torch", 64, True),
         "argmax_prefill": lambda: make_argmax("argmax_prefill", 1024, False),
         "argmax_prefill_torch": lambda: make_argmax("argmax_prefill_torch", 1024, True),
+        "gumbel_dec": lambda: make_gumbel("gumbel_dec", 64, False),
+        "gumbel_dec_torch": lambda: make_gumbel("gumbel_dec_torch", 64, True),
+        "gumbel_prefill": lambda: make_gumbel("gumbel_prefill", 1024, False),
         "calib_copy": lambda: make_copy("calib_copy"),
         "calib_copy_cached": lambda: make_copy("calib_copy_cached", cached=True),
     }
@@ -541,7 +566,8 @@ def main():
             ops[name] = {"desc": w.desc, "us": round(ms * 1000, 3), "bytes": w.nbytes, "gbs": round(gbs, 1),
                          "frac_peak": round(gbs / PEAK_GBS, 4)}
             extra = ""
-            if name.endswith("_c1") or name.startswith("rope_kv_dec") or name.startswith("argmax_dec"):
+            if name.endswith("_c1") or name.startswith("rope_kv_dec") or name.startswith("argmax_dec") or \
+                    name == "gumbel_dec":
                 # Launch-latency-bound: eager timing is the host's launch rate; the graph replay is
                 # the device time per launch.
                 us_g = time_graph(w, 20, 10) * 1000

@@ -1,18 +1,29 @@
-// Row argmax for gfx950: exl3r_argmax_sample (replaces exl3_shim_argmax_sample, reference
-// csrc/exl3_shim.cpp:229-231 -> argmax_sample, kernels/generator/sampling_basic.cu:65-92, 151-172, and
-// the generator's batched tch argmax over [bsz, vocab] logits, src/generator.rs:1596, draft.rs:121).
+// Row sampling for gfx950.
 //
-// Rule (torch.argmax's): the first index of the row maximum among indices < max_logit, NaN counting
-// as the maximum (the first NaN wins) and -0 equal to +0.
+// exl3r_argmax_sample replaces exl3_shim_argmax_sample (reference csrc/exl3_shim.cpp:229-231 ->
+// argmax_sample, kernels/generator/sampling_basic.cu:65-92, 151-172) and the generator's batched tch
+// argmax over [bsz, vocab] logits (src/generator.rs:1596, draft.rs:121).  Rule (torch.argmax's): the
+// first index of the row maximum among indices < max_logit, NaN counting as the maximum (the first
+// NaN wins) and -0 equal to +0.
+//
+// exl3r_gumbel_sample / exl3r_gumbel_noise take the role of exl3_shim_gumbel_sample and
+// exl3_shim_gumbel_noise_f32 (exl3_shim.cpp:232-237; sampling_basic.cu:94-128, gumbel.cu:45-62): a
+// Gumbel-max draw, the argmax of logits + Gumbel(0, 1) noise, which picks index i with probability
+// softmax(logits)_i.  The noise stream is this library's own, a function of (seed, row, column) only:
+//   bits = Philox4x32-10(counter {column >> 2, row low, row high, 0}, key {seed, 0}), word column & 3
+//   u    = ((bits >> 9) + 0.5) * 2^-23          exact, in [2^-24, 1 - 2^-24]
+//   g    = -log(-log(u))                         log_f32 below, correctly ordered fp32 operations
+// Philox4x32-10 is the published generator of Salmon, Moraes, Dror and Shaw ("Parallel random
+// numbers: as easy as 1, 2, 3", SC 2011).
 //
 // Layout, fewer than 512 rows (decode): a row is cut into slices of 2048 or 8192 elements, a 256-lane
 // workgroup per slice (grid (slices, rows)), so a single decode row of 152k logits still spreads over
-// ~75 CUs.  512 rows and more: a workgroup per row, the index written directly.  Each lane keeps its best candidate
-// as one 64-bit key -- an order-preserving image of the value in the high word, the complement of
-// the index in the low word -- so "larger key" is exactly "larger value, then lower index".  The
-// workgroup's maximum key (DPP butterfly, one LDS hop) goes to the row's int64 output with one
-// atomicMax; a clear
-// kernel before and a convert kernel after turn that slot into the index.  Capture-safe: no memset.
+// ~75 CUs.  512 rows and more: a workgroup per row, the index written directly.  Each lane keeps its
+// best candidate as one 64-bit key -- an order-preserving image of the value in the high word, the
+// complement of the index in the low word -- so "larger key" is exactly "larger value, then lower
+// index".  With slices, the workgroup's maximum key (DPP butterfly, one LDS hop) goes to the row's
+// int64 output with one atomicMax; a clear kernel before and a convert kernel after turn that slot
+// into the index.  Capture-safe: no memset.
 #include "abi.hpp"
 #include "common.cuh"
 
@@ -25,7 +36,109 @@ struct ArgArgs
     int64_t n;           // candidates per row (masked length)
     int64_t rows;
     uint64_t* ids;
+    uint32_t seed;       // Gumbel noise key
 };
+
+// Philox4x32-10: ten rounds of two 32 x 32 -> 64-bit products with the published multipliers,
+// the key advanced by the published Weyl increments between rounds.
+__device__ __forceinline__ void philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
+                                              uint32_t k1, uint32_t (&out)[4])
+{
+    #pragma unroll
+    for (int round = 0; round < 10; ++round)
+    {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+        // three-way xor in one gfx950 bitop3 (truth table 0x96 = a ^ b ^ c)
+        const uint32_t n0 = __builtin_amdgcn_bitop3_b32((uint32_t)(p1 >> 32), c1, k0, 0x96);
+        const uint32_t n2 = __builtin_amdgcn_bitop3_b32((uint32_t)(p0 >> 32), c3, k1, 0x96);
+        c1 = (uint32_t)p1;
+        c3 = (uint32_t)p0;
+        c0 = n0;
+        c2 = n2;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+// Natural log of a positive normal float in plain fp32 operations and explicit fmas, so that any
+// IEEE implementation of the same steps gives the same bits.  x = 2^e m, m in [sqrt(1/2), sqrt(2))
+// (0x3f3504f3 is sqrt(1/2)); f = m - 1 exactly; log(1 + f) = 2 atanh(s), s = f / (2 + f), arranged as
+// f - (f^2/2 - s (f^2/2 + R)) with R = sum_k 2 s^2k / (2k + 1) through k = 5.  s enters only the
+// correction term, so 1/(2 + f) comes from the linear minimax seed on [2 - 0.2929, 2 + 0.4143]
+// (relative error 1.49e-2) and two Newton steps (5.0e-8) instead of an IEEE divide.  e ln2 is split
+// so that e * ln2_hi is exact (15-bit ln2_hi, |e| < 2^9); ln2_lo is the float nearest ln2 - ln2_hi.
+// Error: under 0.72 ulp on a sweep of normal floats.
+__device__ __forceinline__ float log_f32(float x)
+{
+    #pragma clang fp contract(off)
+    const uint32_t ix = __builtin_bit_cast(uint32_t, x);
+    const int32_t e = ((int32_t)(ix - 0x3f3504f3u)) >> 23;
+    const float m = __builtin_bit_cast(float, ix - ((uint32_t)e << 23));
+    const float f = m - 1.0f;
+    const float d = 2.0f + f;
+    float y = __builtin_fmaf(d, -0x1.e9813ap-3f, 0x1.f859fcp-1f);
+    y = __builtin_fmaf(y, __builtin_fmaf(-d, y, 1.0f), y);
+    y = __builtin_fmaf(y, __builtin_fmaf(-d, y, 1.0f), y);
+    const float s = f * y;
+    const float z = s * s;
+    const float R = z * __builtin_fmaf(z, __builtin_fmaf(z, __builtin_fmaf(z, __builtin_fmaf(z, 0x1.745d18p-3f,
+                    0x1.c71c72p-3f), 0x1.24924ap-2f), 0x1.99999ap-2f), 0x1.555556p-1f);
+    const float hfsq = 0.5f * f * f;
+    const float ef = (float)e;
+    return __builtin_fmaf(ef, 0x1.62e4p-1f, -((hfsq - __builtin_fmaf(s, hfsq + R, ef * 0x1.7f7d1cp-20f)) - f));
+}
+
+__device__ __forceinline__ float gumbel_of_bits(uint32_t b)
+{
+    #pragma clang fp contract(off)
+    const float u = ((float)(b >> 9) + 0.5f) * 1.1920928955078125e-07f;    // 2^-23
+    return -log_f32(-log_f32(u));
+}
+
+// Noise for columns c .. c+7 of `row`, c a multiple of 4.
+__device__ __forceinline__ void gumbel8(uint32_t seed, int64_t row, int64_t c, float (&g)[8])
+{
+    uint32_t w[4];
+    #pragma unroll
+    for (int h = 0; h < 2; ++h)
+    {
+        philox4x32_10((uint32_t)(c >> 2) + h, (uint32_t)row, (uint32_t)((uint64_t)row >> 32), 0u, seed, 0u, w);
+        #pragma unroll
+        for (int j = 0; j < 4; ++j) g[4 * h + j] = gumbel_of_bits(w[j]);
+    }
+}
+
+__device__ __forceinline__ float gumbel1(uint32_t seed, int64_t row, int64_t c)
+{
+    uint32_t w[4];
+    philox4x32_10((uint32_t)(c >> 2), (uint32_t)row, (uint32_t)((uint64_t)row >> 32), 0u, seed, 0u, w);
+    const int j = (int)(c & 3);
+    return gumbel_of_bits(j == 0 ? w[0] : j == 1 ? w[1] : j == 2 ? w[2] : w[3]);
+}
+
+// Candidate value: the logit, plus its noise for a Gumbel draw.
+template <bool GUMBEL>
+__device__ __forceinline__ void candidates8(float (&f)[8], const ArgArgs& a, int64_t row, int64_t c)
+{
+    #pragma clang fp contract(off)
+    if constexpr (GUMBEL)
+    {
+        float g[8];
+        gumbel8(a.seed, row, c, g);
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = f[j] + g[j];
+    }
+}
+
+template <bool GUMBEL>
+__device__ __forceinline__ float candidate1(const char* base, int dt, const ArgArgs& a, int64_t row, int64_t c)
+{
+    #pragma clang fp contract(off)
+    const float x = load1(base, dt, c);
+    if constexpr (GUMBEL) return x + gumbel1(a.seed, row, c);
+    else return x;
+}
 
 // Order-preserving 32-bit image of a float (larger float -> larger key); -0 maps with +0 and every
 // NaN to the top key.
@@ -42,6 +155,25 @@ __device__ __forceinline__ uint64_t cand_key(float v, int64_t idx)
 }
 
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// A lane's running best over candidates seen in increasing index order: a candidate replaces the
+// best when none is held yet, when it is larger, or when it is the first NaN (a NaN best is final);
+// ties keep the earlier index.  Float compares per element; the 64-bit key is formed once.
+struct LaneBest
+{
+    float v = 0.0f;
+    uint32_t i = 0;
+    bool has = false;
+
+    __device__ __forceinline__ void consider(float x, int64_t idx)
+    {
+        const bool take = (!has) | (x > v) | ((x != x) & (v == v));    // no short circuit: selects, no branches
+        v = take ? x : v;
+        i = take ? (uint32_t)idx : i;
+        has = true;
+    }
+    __device__ __forceinline__ uint64_t key() const { return has ? cand_key(v, i) : 0; }
+};
 
 template <int CTRL>
 __device__ __forceinline__ uint64_t dpp_u64(uint64_t v)
@@ -83,7 +215,7 @@ __global__ __launch_bounds__(256) void k_argmax_convert(uint64_t* ids, int64_t r
 // flight) to one key, so a row takes only vocab / slice atomics: same-address atomics from many
 // workgroups (and XCDs) serialize.  VEC: 16-byte aligned rows, whole chunks loaded as vectors (a
 // chunk crossing n is read element by element); otherwise every element is read on its own.
-template <class IT, bool VEC, int UNROLL>
+template <class IT, bool VEC, int UNROLL, bool GUMBEL>
 __global__ __launch_bounds__(256) void k_argmax(ArgArgs a)
 {
     __shared__ uint64_t part[4];
@@ -92,7 +224,7 @@ __global__ __launch_bounds__(256) void k_argmax(ArgArgs a)
     for (int64_t row = blockIdx.y; row < a.rows; row += gridDim.y)
     {
         const char* base = a.x + row * a.ld;
-        uint64_t best = 0;
+        LaneBest lb;
         typename IT::Vec v[UNROLL];
         #pragma unroll
         for (int u = 0; u < UNROLL; ++u)
@@ -108,16 +240,17 @@ __global__ __launch_bounds__(256) void k_argmax(ArgArgs a)
             {
                 float f[8];
                 unpack8<IT>(v[u], f);
+                candidates8<GUMBEL>(f, a, row, c);
                 #pragma unroll
-                for (int j = 0; j < 8; ++j) best = max_u64(best, cand_key(f[j], c + j));
+                for (int j = 0; j < 8; ++j) lb.consider(f[j], c + j);
             }
             else
             {
                 for (int j = 0; j < 8 && c + j < a.n; ++j)
-                    best = max_u64(best, cand_key(load1(base, IT::code, c + j), c + j));
+                    lb.consider(candidate1<GUMBEL>(base, IT::code, a, row, c + j), c + j);
             }
         }
-        best = wave_max_u64(best);
+        uint64_t best = wave_max_u64(lb.key());
         if ((tid & 63) == 0) part[tid >> 6] = best;
         __syncthreads();
         if (tid == 0)
@@ -131,7 +264,7 @@ __global__ __launch_bounds__(256) void k_argmax(ArgArgs a)
 
 // Many rows: a workgroup owns a row, walks it 2048 elements per step with 4 chunks per lane in
 // flight, and writes the index itself (no atomics, no clear / convert launches).
-template <class IT, bool VEC>
+template <class IT, bool VEC, bool GUMBEL>
 __global__ __launch_bounds__(256) void k_argmax_rows(ArgArgs a)
 {
     __shared__ uint64_t part[4];
@@ -139,7 +272,7 @@ __global__ __launch_bounds__(256) void k_argmax_rows(ArgArgs a)
     for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x)
     {
         const char* base = a.x + row * a.ld;
-        uint64_t best = 0;
+        LaneBest lb;
         for (int64_t s0 = 0; s0 < a.n; s0 += 4 * 2048)
         {
             typename IT::Vec v[4];
@@ -157,17 +290,18 @@ __global__ __launch_bounds__(256) void k_argmax_rows(ArgArgs a)
                 {
                     float f[8];
                     unpack8<IT>(v[u], f);
+                    candidates8<GUMBEL>(f, a, row, c);
                     #pragma unroll
-                    for (int j = 0; j < 8; ++j) best = max_u64(best, cand_key(f[j], c + j));
+                    for (int j = 0; j < 8; ++j) lb.consider(f[j], c + j);
                 }
                 else
                 {
                     for (int j = 0; j < 8 && c + j < a.n; ++j)
-                        best = max_u64(best, cand_key(load1(base, IT::code, c + j), c + j));
+                        lb.consider(candidate1<GUMBEL>(base, IT::code, a, row, c + j), c + j);
                 }
             }
         }
-        best = wave_max_u64(best);
+        uint64_t best = wave_max_u64(lb.key());
         if ((tid & 63) == 0) part[tid >> 6] = best;
         __syncthreads();
         if (tid == 0)
@@ -179,14 +313,56 @@ __global__ __launch_bounds__(256) void k_argmax_rows(ArgArgs a)
     }
 }
 
+// out[r, c] = x[r, c] + g(seed, r, c): a lane per 8 columns (grid (column chunks, rows)).  VEC: 16-byte
+// aligned rows of x and out; otherwise element by element.
+struct NoiseArgs
+{
+    const char* x;
+    char* out;
+    int64_t ldx, ldo;    // bytes
+    int64_t rows, cols;
+    uint32_t seed;
+};
+
+template <class IT, class OT, bool VEC>
+__global__ __launch_bounds__(256) void k_gumbel_noise(NoiseArgs a)
+{
+    #pragma clang fp contract(off)
+    const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (c >= a.cols) return;
+    for (int64_t row = blockIdx.y; row < a.rows; row += gridDim.y)
+    {
+        const char* xr = a.x + row * a.ldx;
+        char* orow = a.out + row * a.ldo;
+        if (VEC && c + 8 <= a.cols)
+        {
+            float f[8], g[8];
+            unpack8<IT>(load8s<IT>(xr, c), f);
+            gumbel8(a.seed, row, c, g);
+            #pragma unroll
+            for (int j = 0; j < 8; ++j) f[j] = f[j] + g[j];
+            store8<OT>(orow, c, pack8<OT>(f));
+        }
+        else
+        {
+            for (int64_t j = c; j < c + 8 && j < a.cols; ++j)
+                store1(orow, OT::code, j, load1(xr, IT::code, j) + gumbel1(a.seed, row, j));
+        }
+    }
+}
+
 }  // namespace exl3r
 
 using namespace exl3r;
 
-extern "C" int exl3r_argmax_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
-                                   int max_logit, int64_t* ids, void* stream)
+namespace {
+
+// Shared by the argmax and the Gumbel draw: validation, then the slice or row-per-workgroup kernels.
+template <bool GUMBEL>
+int sample_entry(const char* op, const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                 int max_logit, uint32_t seed, int64_t* ids, void* stream)
 {
-    const char* op = "exl3r_argmax_sample";
+
     if (!is_float_dtype(dtype)) return set_error(EXL3R_EDTYPE, "%s: unsupported logits dtype %s", op, dtype_name(dtype));
     if (rows < 0 || vocab <= 0 || vocab > 0xffffffffLL || (rows > 1 && ld < vocab))
         return set_error(EXL3R_EINVAL, "%s: invalid shape rows=%lld vocab=%lld ld=%lld", op, (long long)rows,
@@ -195,15 +371,15 @@ extern "C" int exl3r_argmax_sample(const void* logits, int dtype, int64_t rows, 
     if (!logits || !ids) return set_error(EXL3R_EINVAL, "%s: logits and ids must be non-null", op);
     const int64_t n = (max_logit <= 0 || max_logit > vocab) ? vocab : max_logit;
     const int es = dtype_bytes(dtype);
-    ArgArgs a{ (const char*)logits, (rows > 1 ? ld : vocab) * es, n, rows, (uint64_t*)ids };
+    ArgArgs a{ (const char*)logits, (rows > 1 ? ld : vocab) * es, n, rows, (uint64_t*)ids, seed };
     hipStream_t s = (hipStream_t)stream;
     const bool vec = aligned16(logits) && a.ld % 16 == 0;
     if (rows >= 512)
     {
         const unsigned grid = (unsigned)(rows < kMaxGridX ? rows : kMaxGridX);
         with_float_type(dtype, [&](auto T) {
-            if (vec) k_argmax_rows<decltype(T), true><<<grid, 256, 0, s>>>(a);
-            else k_argmax_rows<decltype(T), false><<<grid, 256, 0, s>>>(a);
+            if (vec) k_argmax_rows<decltype(T), true, GUMBEL><<<grid, 256, 0, s>>>(a);
+            else k_argmax_rows<decltype(T), false, GUMBEL><<<grid, 256, 0, s>>>(a);
         });
         return launch_status(op);
     }
@@ -218,15 +394,56 @@ extern "C" int exl3r_argmax_sample(const void* logits, int dtype, int64_t rows, 
         using Ty = decltype(T);
         if (unroll == 4)
         {
-            if (vec) k_argmax<Ty, true, 4><<<grid, 256, 0, s>>>(a);
-            else k_argmax<Ty, false, 4><<<grid, 256, 0, s>>>(a);
+            if (vec) k_argmax<Ty, true, 4, GUMBEL><<<grid, 256, 0, s>>>(a);
+            else k_argmax<Ty, false, 4, GUMBEL><<<grid, 256, 0, s>>>(a);
         }
         else
         {
-            if (vec) k_argmax<Ty, true, 1><<<grid, 256, 0, s>>>(a);
-            else k_argmax<Ty, false, 1><<<grid, 256, 0, s>>>(a);
+            if (vec) k_argmax<Ty, true, 1, GUMBEL><<<grid, 256, 0, s>>>(a);
+            else k_argmax<Ty, false, 1, GUMBEL><<<grid, 256, 0, s>>>(a);
         }
     });
     k_argmax_convert<<<small, 256, 0, s>>>(a.ids, rows);
+    return launch_status(op);
+}
+
+}  // namespace
+
+extern "C" int exl3r_argmax_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                                   int max_logit, int64_t* ids, void* stream)
+{
+    return sample_entry<false>("exl3r_argmax_sample", logits, dtype, rows, vocab, ld, max_logit, 0u, ids, stream);
+}
+
+extern "C" int exl3r_gumbel_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                                   int max_logit, uint32_t random, int64_t* ids, void* stream)
+{
+    return sample_entry<true>("exl3r_gumbel_sample", logits, dtype, rows, vocab, ld, max_logit, random, ids, stream);
+}
+
+extern "C" int exl3r_gumbel_noise(const void* x, int x_dtype, int64_t ldx, void* out, int out_dtype, int64_t ldo,
+                                  int64_t rows, int64_t cols, uint32_t random, void* stream)
+{
+    const char* op = "exl3r_gumbel_noise";
+    if (!is_float_dtype(x_dtype) || !is_float_dtype(out_dtype))
+        return set_error(EXL3R_EDTYPE, "%s: unsupported dtypes x=%s out=%s", op, dtype_name(x_dtype),
+                         dtype_name(out_dtype));
+    if (rows < 0 || cols < 0 || cols > 0xffffffffLL * 4 || (rows > 1 && (ldx < cols || ldo < cols)))
+        return set_error(EXL3R_EINVAL, "%s: invalid shape rows=%lld cols=%lld ldx=%lld ldo=%lld", op, (long long)rows,
+                         (long long)cols, (long long)ldx, (long long)ldo);
+    if (rows == 0 || cols == 0) return EXL3R_OK;
+    if (!x || !out) return set_error(EXL3R_EINVAL, "%s: x and out must be non-null", op);
+    const int xs = dtype_bytes(x_dtype), os = dtype_bytes(out_dtype);
+    NoiseArgs a{ (const char*)x, (char*)out, (rows > 1 ? ldx : cols) * xs, (rows > 1 ? ldo : cols) * os, rows, cols,
+                 random };
+    const bool vec = aligned16(x) && aligned16(out) && a.ldx % 16 == 0 && a.ldo % 16 == 0;
+    const dim3 grid((unsigned)((cols + 2047) / 2048), (unsigned)(rows < 65535 ? rows : 65535));
+    hipStream_t s = (hipStream_t)stream;
+    with_float_type(x_dtype, [&](auto TI) {
+        with_float_type(out_dtype, [&](auto TO) {
+            if (vec) k_gumbel_noise<decltype(TI), decltype(TO), true><<<grid, 256, 0, s>>>(a);
+            else k_gumbel_noise<decltype(TI), decltype(TO), false><<<grid, 256, 0, s>>>(a);
+        });
+    });
     return launch_status(op);
 }

@@ -6,6 +6,8 @@ index_select (src/modules.rs:430-436).
 Tensors must live on the GPU; every wrapper launches on the current torch stream (the reference's
 kernels use the current torch stream too, kernels/norm.cu:328) unless `stream` is given, and raises
 Exl3rError on a non-zero status (the reference's TORCH_CHECK raises)."""
+import math
+
 import torch
 
 from ._lib import BF16, F16, F32, I32, I64, check, load
@@ -38,6 +40,8 @@ def _rows(t):
     dim = t.shape[-1]
     if t.dim() == 1:
         return 1, dim, dim
+    if dim == 0:
+        return math.prod(t.shape[:-1]), 0, 0
     if dim > 1 and t.stride(-1) != 1:
         raise ValueError("last dimension must be contiguous")
     try:
@@ -229,6 +233,26 @@ def argmax_sample(logits, ids, max_logit=0, stream=None):
         raise ValueError("ids must be int64 with one entry per row")
     check(load().exl3r_argmax_sample(_ptr(logits), dtype_code(logits), rows, vocab, ld, int(max_logit), _ptr(ids),
                                      _stream(logits, stream)))
+
+
+def gumbel_sample(logits, ids, max_logit=0, random=0, stream=None):
+    """ids[i] = argmax of logits[i, :max_logit] + Gumbel(0, 1) noise of (random, i, column): a draw from
+    softmax(logits[i, :max_logit]) (src/ffi.rs:526-530)."""
+    rows, vocab, ld = _rows(logits)
+    if ids.dtype != torch.int64 or ids.numel() != rows:
+        raise ValueError("ids must be int64 with one entry per row")
+    check(load().exl3r_gumbel_sample(_ptr(logits), dtype_code(logits), rows, vocab, ld, int(max_logit),
+                                     int(random) & 0xFFFFFFFF, _ptr(ids), _stream(logits, stream)))
+
+
+def gumbel_noise(x, out, random=0, stream=None):
+    """out = x + the Gumbel noise of gumbel_sample (src/ffi.rs:531-535); out may be x."""
+    rows, cols, ldx = _rows(x)
+    ro, co, ldo = _rows(out)
+    if (ro, co) != (rows, cols):
+        raise ValueError("x and out must have the same shape")
+    check(load().exl3r_gumbel_noise(_ptr(x), dtype_code(x), ldx, _ptr(out), dtype_code(out), ldo, rows, cols,
+                                    int(random) & 0xFFFFFFFF, _stream(x, stream)))
 
 
 def embedding(table, ids, out, err_flag=None, stream=None):

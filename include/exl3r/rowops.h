@@ -33,6 +33,8 @@
  *   exl3r_deinterleave_qg   <- exl3_shim_deinterleave_qg  csrc/exl3_shim.cpp:168-171 (ffi.rs:167, 622-624)
  *   exl3r_argmax_sample     <- exl3_shim_argmax_sample    csrc/exl3_shim.cpp:229-231 (ffi.rs:136, 521-525) and the
  *                              generator's batched tch argmax over [bsz, vocab] logits  src/generator.rs:1596
+ *   exl3r_gumbel_sample     <- exl3_shim_gumbel_sample    csrc/exl3_shim.cpp:232-234 (ffi.rs:137, 526-530)
+ *   exl3r_gumbel_noise      <- exl3_shim_gumbel_noise_f32 csrc/exl3_shim.cpp:235-237 (ffi.rs:138, 531-535)
  *   exl3r_embedding         <- Embedding::forward's tch index_select + to_kind   src/modules.rs:430-436
  *   exl3r_embedding_rms_norm<- embed followed by RmsNorm::forward (MTP head)    src/mtp.rs:189-190
  */
@@ -229,6 +231,29 @@ EXL3R_API int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_stri
  */
 EXL3R_API int exl3r_argmax_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
                         int max_logit, int64_t* ids, void* stream);
+
+/*
+ * Gumbel-max categorical draw: ids[r] = the exl3r_argmax_sample index (same rule and mask) of
+ * fl32(logits[r, c] + g(random, r, c)), so that index i is drawn with probability
+ * softmax(logits[r, :max_logit])_i.  Replaces exl3_shim_gumbel_sample (csrc/exl3_shim.cpp:232-234 ->
+ * kernels/generator/sampling_basic.cu:94-128, 174-197).  The noise is Gumbel(0, 1) from this
+ * library's own stream, a function of (random, r, c) only:
+ *   bits = Philox4x32-10(counter {c >> 2, r mod 2^32, r >> 32, 0}, key {random, 0}), word c & 3
+ *   u = ((bits >> 9) + 0.5) * 2^-23,  g = -log(-log(u))  (fp32, finite: -2.82 < g < 16.64)
+ * The reference draws from cuRAND's Philox stream instead; draws agree in distribution, not in bits.
+ */
+EXL3R_API int exl3r_gumbel_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                        int max_logit, uint32_t random, int64_t* ids, void* stream);
+
+/*
+ * out[r, c] = x[r, c] + g(random, r, c) over every column (the noise of exl3r_gumbel_sample), rounded
+ * once to out_dtype; out may be x.  x and out: [rows, cols], row strides ldx / ldo elements,
+ * F16/BF16/F32.  With an F32 out, exl3r_argmax_sample of out equals exl3r_gumbel_sample of x.
+ * Replaces exl3_shim_gumbel_noise_f32 (csrc/exl3_shim.cpp:235-237 -> kernels/generator/gumbel.cu:
+ * 44-62, 114-137), which adds noise over the flattened tensor.
+ */
+EXL3R_API int exl3r_gumbel_noise(const void* x, int x_dtype, int64_t ldx, void* out, int out_dtype, int64_t ldo,
+                       int64_t rows, int64_t cols, uint32_t random, void* stream);
 
 /*
  * Token-embedding gather: out[i, :] = table[ids[i], :], bit-exact (same dtype) or exactly upcast to

@@ -32,6 +32,11 @@ _PROTOS = {
                                    _i, _i]),
     "oracle_deinterleave_qg": (_i, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i, _i, _i]),
     "oracle_argmax": (_i, [_vp, _i, _i64, _i64, _i64, _i, _vp, _i]),
+    "oracle_philox4x32_10": (None, [_vp, _vp, _vp]),
+    "oracle_log_f32": (ctypes.c_float, [_f]),
+    "oracle_gumbel_of_bits": (None, [_vp, _vp, _i64]),
+    "oracle_gumbel_noise": (_i, [_vp, _i, _i64, _vp, _i, _i64, _i64, _i64, ctypes.c_uint32, _i]),
+    "oracle_gumbel_sample": (_i, [_vp, _i, _i64, _i64, _i64, _i, ctypes.c_uint32, _vp, _i]),
     "oracle_paged_kv_append": (_i, [_vp, _i64, _i64, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _vp, _i, _i64,
                                     _vp, _i64, _vp, _vp, _i]),
     "oracle_embedding_rms_norm": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _i64, _vp, _i,
@@ -146,6 +151,45 @@ def argmax(logits, dt, max_logit=0, nthreads=1):
     rows, vocab = logits.shape
     ids = np.zeros(rows, np.int64)
     _check(load().oracle_argmax(_p(logits), dt, rows, vocab, vocab, max_logit, _p(ids), nthreads), "oracle_argmax")
+    return ids
+
+
+def philox4x32_10(ctr, key):
+    """One Philox4x32-10 block: ctr 4 x uint32, key 2 x uint32 -> 4 x uint32."""
+    c = np.ascontiguousarray(ctr, np.uint32)
+    k = np.ascontiguousarray(key, np.uint32)
+    out = np.zeros(4, np.uint32)
+    load().oracle_philox4x32_10(_p(c), _p(k), _p(out))
+    return out
+
+
+def log_f32(x):
+    return np.float32(load().oracle_log_f32(float(x)))
+
+
+def gumbel_of_bits(bits):
+    """Gumbel noise -log(-log(u)) for raw uint32 Philox words (u = ((b >> 9) + 0.5) * 2^-23)."""
+    b = np.ascontiguousarray(bits, np.uint32)
+    g = np.zeros(b.shape, np.float32)
+    load().oracle_gumbel_of_bits(_p(b), _p(g), b.size)
+    return g
+
+
+def gumbel_noise(x, xt, seed, out_dt=F32, nthreads=1):
+    """x: [rows, cols] storage.  Returns x + Gumbel noise of (seed, row, column), rounded to out_dt."""
+    rows, cols = x.shape
+    out = np.zeros((rows, cols), np.float32 if out_dt == F32 else np.uint16)
+    _check(load().oracle_gumbel_noise(_p(x), xt, cols, _p(out), out_dt, cols, rows, cols, seed, nthreads),
+           "oracle_gumbel_noise")
+    return out
+
+
+def gumbel_sample(logits, dt, seed, max_logit=0, nthreads=1):
+    """Gumbel-max draw per row: argmax over the first max_logit columns of logits + noise."""
+    rows, vocab = logits.shape
+    ids = np.zeros(rows, np.int64)
+    _check(load().oracle_gumbel_sample(_p(logits), dt, rows, vocab, vocab, max_logit, seed, _p(ids), nthreads),
+           "oracle_gumbel_sample")
     return ids
 
 

@@ -461,6 +461,108 @@ int oracle_argmax(const void* logits, int dt, int64_t rows, int64_t vocab, int64
     return 0;
 }
 
+/* Philox4x32-10 (Salmon et al., SC 2011): ten rounds of two 32x32->64 multiplies with the published
+ * multipliers and Weyl key increments. */
+void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4])
+{
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3], k0 = key[0], k1 = key[1];
+    for (int round = 0; round < 10; ++round)
+    {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        c1 = (uint32_t)p1;
+        c3 = (uint32_t)p0;
+        c0 = n0;
+        c2 = n2;
+        if (oracle_mutation != ORM_PHILOX_NO_BUMP) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+float oracle_log_f32(float x)
+{
+    uint32_t ix;
+    memcpy(&ix, &x, 4);
+    /* x = 2^e * m with m in [sqrt(1/2), sqrt(2)): 0x3f3504f3 is the bit pattern of sqrt(1/2) */
+    const int32_t e = ((int32_t)(ix - 0x3f3504f3u)) >> 23;
+    const uint32_t im = ix - ((uint32_t)e << 23);
+    float m;
+    memcpy(&m, &im, 4);
+    const float f = m - 1.0f;                       /* exact */
+    /* s = f / (2 + f) through 1/d: the linear minimax seed of 1/d on [2 - 0.2929, 2 + 0.4143]
+     * (relative error 1.49e-2) and two Newton steps (5.0e-8); s only enters the correction term. */
+    const float d = 2.0f + f;
+    float y = fmaf(d, -0x1.e9813ap-3f, 0x1.f859fcp-1f);
+    y = fmaf(y, fmaf(-d, y, 1.0f), y);
+    y = fmaf(y, fmaf(-d, y, 1.0f), y);
+    const float s = f * y;
+    const float z = s * s;
+    /* R = sum_{k=1..5} 2 s^2k / (2k + 1); coefficients are the floats nearest 2/3, 2/5, 2/7, 2/9, 2/11 */
+    const float R = z * fmaf(z, fmaf(z, fmaf(z, fmaf(z, 0x1.745d18p-3f, 0x1.c71c72p-3f), 0x1.24924ap-2f),
+                                      0x1.99999ap-2f), 0x1.555556p-1f);
+    const float hfsq = 0.5f * f * f;
+    const float ef = (float)e;
+    const float lo = oracle_mutation == ORM_LOG_NO_LN2LO ? 0.0f : ef * 0x1.7f7d1cp-20f;
+    /* ln2 = ln2_hi + ln2_lo; e * ln2_hi is exact: ln2_hi = 0x1.62e4p-1 (0.693145751953125) has 15
+     * significant bits and |e| < 2^9, so the final fma rounds once, as a product and a difference would.
+     * ln2_lo is the float nearest to ln2 - ln2_hi. */
+    return fmaf(ef, 0x1.62e4p-1f, -((hfsq - fmaf(s, hfsq + R, lo)) - f));
+}
+
+static inline float gumbel_of_bits(uint32_t b)
+{
+    const float u = ((float)(b >> 9) + 0.5f) * 1.1920928955078125e-07f;    /* 2^-23 */
+    return -oracle_log_f32(-oracle_log_f32(u));
+}
+
+void oracle_gumbel_of_bits(const uint32_t* bits, float* g, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) g[i] = gumbel_of_bits(bits[i]);
+}
+
+static inline float gumbel_at(uint32_t seed, int64_t r, int64_t c)
+{
+    if (oracle_mutation == ORM_GUMBEL_NO_ROW) r = 0;
+    const uint32_t ctr[4] = { (uint32_t)(c >> 2), (uint32_t)r, (uint32_t)((uint64_t)r >> 32), 0 };
+    const uint32_t key[2] = { seed, 0 };
+    uint32_t out[4];
+    oracle_philox4x32_10(ctr, key, out);
+    return gumbel_of_bits(out[c & 3]);
+}
+
+int oracle_gumbel_noise(const void* x, int xt, int64_t ldx, void* out, int ot, int64_t ldo, int64_t rows,
+                        int64_t cols, uint32_t seed, int nthreads)
+{
+    if (!x || !out || rows < 0 || cols < 0 || ldx < cols || ldo < cols) return -1;
+    if (!fdtype(xt) || !fdtype(ot)) return -2;
+    #pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c)
+            st(out, ot, r * ldo + c, ld(x, xt, r * ldx + c) + gumbel_at(seed, r, c));
+    return 0;
+}
+
+int oracle_gumbel_sample(const void* logits, int dt, int64_t rows, int64_t vocab, int64_t ldl, int max_logit,
+                         uint32_t seed, int64_t* ids, int nthreads)
+{
+    if (!logits || !ids || rows < 0 || vocab <= 0 || ldl < vocab) return -1;
+    if (!fdtype(dt)) return -2;
+    const int64_t n = (max_logit <= 0 || max_logit > vocab) ? vocab : max_logit;
+    #pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t i = 0; i < rows; ++i)
+    {
+        int64_t best = 0;
+        float bv = ld(logits, dt, i * ldl) + gumbel_at(seed, i, 0);
+        for (int64_t j = 1; j < n && !isnan(bv); ++j)
+        {
+            const float v = ld(logits, dt, i * ldl + j) + gumbel_at(seed, i, j);
+            if (isnan(v) || v > bv) { bv = v; best = j; }
+        }
+        ids[i] = best;
+    }
+    return 0;
+}
+
 /* kernels/norm.cu:482-581 (kernel), 591-668 (host rules) */
 int oracle_gated_rms_norm(const void* x, int xt, int64_t ldx, const void* w, int wt, int w_groups,
                           void* y, int yt, int64_t ldy, const void* g, int gt, int64_t ldg,

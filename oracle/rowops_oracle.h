@@ -62,6 +62,9 @@ extern int oracle_mutation;
 #define ORM_QG_SWAP          20  /* deinterleave returns q and g exchanged */
 #define ORM_ARGMAX_LAST_TIE  21  /* argmax ties go to the last index */
 #define ORM_ARGMAX_NO_MASK   22  /* argmax ignores max_logit */
+#define ORM_PHILOX_NO_BUMP   23  /* Philox key not advanced between rounds */
+#define ORM_LOG_NO_LN2LO     24  /* log drops the low part of e * ln2 */
+#define ORM_GUMBEL_NO_ROW    25  /* Gumbel noise ignores the row (every row draws the same noise) */
 
 /* Conversions (round to nearest even; NaN -> canonical quiet NaN). */
 uint16_t oracle_f32_to_f16(float f);
@@ -123,6 +126,32 @@ int oracle_deinterleave_qg(const void* qg, int64_t ldqg, void* q, int64_t ldq, v
  */
 int oracle_argmax(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld, int max_logit,
                   int64_t* ids, int nthreads);
+
+/*
+ * Gumbel-max sampling (the role of exl3_shim_gumbel_sample / exl3_shim_gumbel_noise_f32,
+ * kernels/generator/sampling_basic.cu:94-128, 174-197 and gumbel.cu:45-62).  The reference draws
+ * its uniforms from cuRAND's Philox stream; this build defines its own stream over the published
+ * Philox4x32-10 generator (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as 1, 2,
+ * 3", SC 2011):
+ *   bits(r, c) = Philox4x32-10(counter = {c >> 2, r mod 2^32, r >> 32, 0}, key = {seed, 0})[c & 3]
+ *   u = ((bits >> 9) + 0.5) * 2^-23                  (exact; 2^-24 <= u <= 1 - 2^-24)
+ *   g = -log(-log(u))                                 (log_f32 below, fp32)
+ *   noisy(r, c) = fl32(x(r, c) + g)
+ * so the noise of an element depends only on (seed, row, column), never on the launch shape.
+ */
+void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+/* The fp32 natural log both sides evaluate (argument reduction to [sqrt(1/2), sqrt(2)), Cody-Waite
+ * split of e*ln2, log(1+f) = f - (f^2/2 - s (f^2/2 + R(s^2))) with s = f/(2+f) from a Newton
+ * reciprocal and R the atanh series through s^10), for positive normal x. */
+float oracle_log_f32(float x);
+/* g[i] = -log(-log(u(bits[i]))) for raw Philox words. */
+void oracle_gumbel_of_bits(const uint32_t* bits, float* g, int64_t n);
+/* out[r, c] = x[r, c] + g(seed, r, c), every column; in F16/BF16/F32, out F16/BF16/F32 (one rounding). */
+int oracle_gumbel_noise(const void* x, int xt, int64_t ldx, void* out, int ot, int64_t ldo, int64_t rows,
+                        int64_t cols, uint32_t seed, int nthreads);
+/* ids[r] = argmax over c < max_logit of fl32(x[r, c] + g(seed, r, c)) (oracle_argmax's rule). */
+int oracle_gumbel_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld, int max_logit,
+                         uint32_t seed, int64_t* ids, int nthreads);
 
 /*
  * Paged KV-cache append (paged_kv_update_vec8_kernel, reference kernels/generator/cache.cu:143-243):
