@@ -599,6 +599,17 @@ def main():
             f"decode graph {df:.2f} us vs {du:.2f} us (x{du / df:.2f})")
         c2 = rms_c2_latencies()
         log(f"C2 residual RMSNorm us (graph): {[c2[t]['us_graph'] for t in c2]}")
+        sampling = {
+            "argmax_64x151936_graph_us": {"exl3r": ops["argmax_dec"]["us_graph"],
+                                          "torch_argmax": ops["argmax_dec_torch"]["us_graph"]},
+            "argmax_1024x151936_us": {"exl3r": ops["argmax_prefill"]["us"],
+                                      "torch_argmax": ops["argmax_prefill_torch"]["us"]},
+            "gumbel_64x151936_us": {"exl3r_graph": ops["gumbel_dec"]["us_graph"],
+                                    "torch_softmax_multinomial_eager": ops["gumbel_dec_torch"]["us"]},
+            "gumbel_1024x151936_us": {"exl3r": ops["gumbel_prefill"]["us"]},
+            "desc": "f16 logits; argmax vs torch.argmax (the generator's greedy path); Gumbel-max draw vs "
+                    "softmax + multinomial (the reference sampler's tch path)"}
+        log(f"sampling: {json.dumps(sampling)}")
 
         # The timed step: config-3 prefill row ops back to back.
         step_works = [works["rms_c3"], works["silu_c3"], works["gelu_c3"]]
@@ -636,7 +647,7 @@ def main():
                    "io_dtype": "bf16", "tokens": 8192, "hidden": 5120, "intermediate": 17408,
                    "frac_peak": round(value / PEAK_GBS, 4)},
         "roofline": roof, "cpu_baseline": cpu, "ops": ops, "decode_step": decode, "c2_decode_rms_norm": c2,
-        "rope_paged_kv": rope_kv,
+        "rope_paged_kv": rope_kv, "sampling": sampling,
         "copy_reference": {"gbs": round(copy_gbs, 1), "frac_peak": round(copy_gbs / PEAK_GBS, 4),
                            "desc": "non-temporal 16 B/lane device copy of 1 GiB (read + write), the practical HBM ceiling reference"},
     }

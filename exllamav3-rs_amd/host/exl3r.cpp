@@ -267,6 +267,25 @@ void argmax_sample(const Tensor& logits, const Tensor& ids, int max_logit, const
                                   static_cast<int64_t*>(ids.data), s.get()));
 }
 
+void gumbel_sample(const Tensor& logits, const Tensor& ids, int max_logit, uint32_t random, const Stream& s)
+{
+    int64_t rows, vocab, ld;
+    logits.rows_view(rows, vocab, ld);
+    require(ids.dtype == DType::I64 && ids.numel() == rows && ids.is_contiguous(),
+            "gumbel_sample: ids must be contiguous int64 with one entry per logits row");
+    check_abi(exl3r_gumbel_sample(logits.data, code(logits.dtype), rows, vocab, ld, max_logit, random,
+                                  static_cast<int64_t*>(ids.data), s.get()));
+}
+
+void gumbel_noise(const Tensor& x, const Tensor& out, uint32_t random, const Stream& s)
+{
+    int64_t rows, cols, ldx, ro, co, ldo;
+    x.rows_view(rows, cols, ldx);
+    out.rows_view(ro, co, ldo);
+    require(ro == rows && co == cols, "gumbel_noise: x and out shapes differ");
+    check_abi(exl3r_gumbel_noise(x.data, code(x.dtype), ldx, out.data, code(out.dtype), ldo, rows, cols, random, s.get()));
+}
+
 void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
           int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
           float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s, const Tensor* position_ids)

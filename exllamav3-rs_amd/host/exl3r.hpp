@@ -8,7 +8,7 @@
 //   exl3r::ffi::rms_norm / rms_norm_res_in / silu_mul / gelu_mul / rope  <- src/ffi.rs:293-333, 464-503
 //   exl3r::ffi::gated_rms_norm / mul_sigmoid_ / deinterleave_qg          <- src/ffi.rs:479-483, 616-624
 //   exl3r::ffi::rope_paged_kv                                            <- rope + paged append, src/modules.rs:666-704
-//   exl3r::ffi::argmax_sample                                            <- src/ffi.rs:521-525, src/generator.rs:1596
+//   exl3r::ffi::argmax_sample / gumbel_sample / gumbel_noise             <- src/ffi.rs:521-535, src/generator.rs:1596
 //   exl3r::ffi::embedding                                                <- index_select, src/modules.rs:430-436
 //   exl3r::RmsNorm::forward / forward_res                                <- src/modules.rs:342-412
 //   exl3r::Embedding::forward                                            <- src/modules.rs:418-437
@@ -153,6 +153,11 @@ void rope_paged_kv(const Tensor& q, const Tensor& out_q, const Tensor& k, const 
 // src/ffi.rs:521-525 (and the generator's batched argmax, src/generator.rs:1596): ids[i] = first index of the
 // maximum of logits[i, :max_logit] (whole row when max_logit <= 0), NaN maximal; ids int64 [rows].
 void argmax_sample(const Tensor& logits, const Tensor& ids, int max_logit, const Stream& s);
+// src/ffi.rs:526-530: a draw from softmax(logits[i, :max_logit]) per row (Gumbel-max over this library's
+// Philox4x32-10 stream keyed by `random`); ids int64 [rows].
+void gumbel_sample(const Tensor& logits, const Tensor& ids, int max_logit, uint32_t random, const Stream& s);
+// src/ffi.rs:531-535: out = x + the Gumbel noise gumbel_sample adds (out may be x).
+void gumbel_noise(const Tensor& x, const Tensor& out, uint32_t random, const Stream& s);
 // Embedding gather: out[i] = table[ids[i]] (bit-exact, or exact upcast to f32); err_flag optional.
 void embedding(const Tensor& table, const Tensor& ids, const Tensor& out, int32_t* err_flag, const Stream& s);
 // Gather fused with the following RMSNorm; h optional.

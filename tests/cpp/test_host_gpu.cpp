@@ -281,6 +281,27 @@ int main()
         const bool ok = std::memcmp(got.data(), want.data(), rows * 8) == 0 && want[3] == 307;
         report("ffi::argmax_sample bf16 masked", ok, ok ? "exact" : "DIFFER");
     }
+    // gumbel_noise (f16 -> f32) and gumbel_sample on the same logits: bitwise noise, equal ids, and the
+    // sample equals the argmax of the noisy logits.
+    {
+        const int rows = 5, vocab = 3001;
+        const uint32_t seed = 0xC0FFEEu;
+        auto lh = host_normal(DType::F16, rows * vocab, 0.f, 3.f);
+        auto l = upload(lh, DType::F16, { rows, vocab }, s);
+        auto noisy = OwnedTensor::empty(DType::F32, { rows, vocab });
+        auto ids = OwnedTensor::empty(DType::I64, { rows });
+        auto ids2 = OwnedTensor::empty(DType::I64, { rows });
+        ffi::gumbel_noise(l.t, noisy.t, seed, s);
+        ffi::gumbel_sample(l.t, ids.t, 0, seed, s);
+        ffi::argmax_sample(noisy.t, ids2.t, 0, s);
+        auto gn = download(noisy, s), gi = download(ids, s), gi2 = download(ids2, s);
+        std::vector<uint8_t> en(gn.size());
+        std::vector<int64_t> ei(rows);
+        oracle_gumbel_noise(lh.data(), OR_F16, vocab, en.data(), OR_F32, vocab, rows, vocab, seed, 1);
+        oracle_gumbel_sample(lh.data(), OR_F16, rows, vocab, vocab, 0, seed, ei.data(), 1);
+        const bool ok = gn == en && std::memcmp(gi.data(), ei.data(), rows * 8) == 0 && gi == gi2;
+        report("ffi::gumbel_noise / gumbel_sample", ok, ok ? "noise bitwise, ids exact" : "DIFFER");
+    }
     std::printf(failures ? "test_host_gpu: %d failures\n" : "test_host_gpu: all passed\n", failures);
     return failures ? 1 : 0;
 }
