@@ -81,3 +81,75 @@ def test_ops_on_side_stream():
     torch.cuda.synchronize()
     for k in ("resid", "y", "q", "k", "act", "emb"):
         assert torch.equal(buf[k], ref[k]), k
+
+
+def tail(buf):
+    """The attention-output gate, the paged append and the sampling step of a decode iteration."""
+    ffi.deinterleave_qg(buf["qg"], buf["qd"], buf["gd"], 64)
+    ffi.rope_paged_kv(buf["qd"], buf["qd"], buf["kk"], buf["kk"], buf["vv"], buf["inv"], 0, buf["sl"], None, None,
+                      1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, buf["kc"], buf["vc"], buf["bt"], buf["sl"])
+    ffi.mul_sigmoid_(buf["att"], buf["gd"])
+    ffi.gated_rms_norm(buf["att"], buf["gw"], buf["gy"], buf["gd"], 1e-6, 0.0, 1, False, 1)
+    ffi.argmax_sample(buf["logits"], buf["ids_a"], 30001)
+    ffi.gumbel_sample(buf["logits"], buf["ids_g"], 0, 4242)
+    ffi.gumbel_noise(buf["logits"], buf["noisy"], 4243)
+
+
+def make_tail(seed):
+    T, heads, hd, hk, V = 16, 4, 64, 2, 32000
+    f16 = torch.float16
+    return {
+        "qg": dev_normal((T, heads * 2 * hd), 0, 1, 1, seed),
+        "qd": torch.empty((T, 1, heads, hd), device="cuda", dtype=f16),
+        "gd": torch.empty((T, heads * hd), device="cuda", dtype=f16),
+        "kk": dev_normal((T, 1, hk, hd), 0, 1, 1, seed + 1), "vv": dev_normal((T, 1, hk, hd), 0, 1, 1, seed + 2),
+        "inv": torch.from_numpy((1.0 / 1e6 ** (np.arange(0, hd, 2) / hd)).astype(np.float32)).cuda(),
+        "kc": torch.zeros((40, 16, hk, hd), device="cuda", dtype=f16),
+        "vc": torch.zeros((40, 16, hk, hd), device="cuda", dtype=f16),
+        "bt": torch.arange(T * 2, dtype=torch.int32, device="cuda").view(T, 2),
+        "sl": torch.zeros(T, dtype=torch.int32, device="cuda"),
+        "att": dev_normal((T, heads * hd), 0, 1, 1, seed + 3),
+        "gw": dev_normal((heads * hd,), 1, 0.1, 0, seed + 4),
+        "gy": torch.empty((T, heads * hd), device="cuda", dtype=f16),
+        "logits": dev_normal((T, V), 0, 3, 2, seed + 5),
+        "ids_a": torch.zeros(T, dtype=torch.int64, device="cuda"),
+        "ids_g": torch.zeros(T, dtype=torch.int64, device="cuda"),
+        "noisy": torch.empty((T, V), device="cuda", dtype=torch.float32),
+    }
+
+
+def test_tail_graph_replays_match_eager():
+    """Gated ops, the fused paged append and both samplers under capture: each replay, with new
+    logits, projections and cache lengths written between replays, equals the eager run bitwise (the
+    argmax's clear / convert launches are kernels, not memsets, so replays start from a clean slot)."""
+    g_buf = make_tail(20)
+    e_buf = {k: v.clone() for k, v in g_buf.items()}
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        tail(g_buf)
+    torch.cuda.synchronize()
+    for k in g_buf:
+        g_buf[k].copy_(e_buf[k])
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        tail(g_buf)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(5)
+    for rep in range(4):
+        sl = torch.from_numpy(rng.integers(0, 16, 16).astype(np.int32))
+        for b in (g_buf, e_buf):
+            b["sl"].copy_(sl)
+            b["logits"].copy_(dev_normal((16, 32000), 0, 3, 2, 200 + rep))
+            b["qg"].copy_(dev_normal((16, 512), 0, 1, 1, 300 + rep))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        tail(e_buf)
+        torch.cuda.synchronize()
+        for k in ("qd", "gd", "kk", "kc", "vc", "att", "gy", "ids_a", "ids_g", "noisy"):
+            a, b = g_buf[k], e_buf[k]
+            if a.dtype in (torch.float16, torch.bfloat16):
+                a, b = a.view(torch.int16), b.view(torch.int16)
+            assert torch.equal(a, b), (rep, k)
+        assert not torch.equal(g_buf["ids_a"], torch.zeros_like(g_buf["ids_a"]))
