@@ -447,8 +447,9 @@ __global__ __launch_bounds__(256) void k_rms_norm_generic(RmsArgs a, int xt, int
 
 // Launch shape: a workgroup per row, MAXV chunks per thread.  Latency-bound launches (few rows)
 // spread a row over up to 1024 lanes; bandwidth-bound launches use <= 384 lanes per row so several
-// rows share a CU (C3 on MI355X: 2 chunks x 320 threads 58 us, 4 x 192 66 us, 1 x 640 70 us; one
-// wave per row 74 us; persistent workgroups prefetching the next row 58 us).
+// rows share a CU (C3 on MI355X, chunks x threads: 2 x 320 57.3 us, 2 x 384 56.9, 3 x 320 57.0,
+// 4 x 192 58.5, 5 x 128 59.4, 8 x 128 83.7, 1 x 640 70; one wave per row 74 us; persistent
+// workgroups prefetching the next row 58 us).
 struct RmsShape
 {
     int maxv;

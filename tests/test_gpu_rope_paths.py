@@ -51,3 +51,14 @@ def test_both_kernels_no_norm_q_only_out_of_place(tune, use):
     tune(use)
     run(1, 65, 8, 0, 128, 128, exl3r.ROPE_NEOX, F16, norm=False, with_k=False, position=70000)
     run(3, 21, 8, 2, 128, 128, exl3r.ROPE_NEOX, F16, norm=True, position=11, out_of_place=True, attn=0.5, cb=1.0)
+
+
+@pytest.mark.parametrize("use", [1, 2])
+@pytest.mark.parametrize("hq,hk,hd", [(128, 8, 128), (6, 3, 128), (1, 1, 128), (40, 0, 128), (50, 10, 64),
+                                      (9, 3, 256)])
+def test_both_kernels_head_counts(tune, use, hq, hk, hd):
+    """Many heads (128 + 8), a lane group that mixes q and k heads (6 + 3), single heads, q only, and the
+    64 / 256 head dims."""
+    tune(use)
+    run(2, 50, hq, hk, hd, hd, exl3r.ROPE_NEOX, F16, position=321, with_k=hk > 0, seed=hq + hk)
+    run(1, 33, hq, hk, hd, hd // 2, exl3r.ROPE_GPTJ, BF16, nwt=F32, position=9, with_k=hk > 0, seed=hq * hk + 1)
