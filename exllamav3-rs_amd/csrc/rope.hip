@@ -36,6 +36,10 @@ struct RopeArgs
     int hq, hk, hd, R;
     int64_t seq_len, tokens;
     const float* inv_freq;
+    // Angle table (exl3r_rope_table): angle of frequency t for token (b, s) at position pos is
+    // table[b * table_bstride + pos * (R / 2) + t]; nullptr: angle = inv_freq[t] * pos.
+    const float* table;
+    int64_t table_rows, table_bstride;
     int32_t position;
     const int32_t* positions;
     const int32_t* position_ids;
@@ -132,20 +136,36 @@ __device__ __forceinline__ void sincos_angle(float a, double& sd, double& cd)
     cd = q == 0 ? c : q == 1 ? -s : q == 2 ? -c : s;
 }
 
-// {cos, sin} * attn_factor of rotary frequency t at position pos: fp64 evaluation of the fp32
-// angle, rounded once (correctly rounded fp32 values).
-__device__ __forceinline__ float2 rope_cs(const RopeArgs& a, int t, int pos)
+// {cos, sin} * attn_factor of rotary frequency t for token tok at position pos: fp64 evaluation of
+// the fp32 angle, rounded once (correctly rounded fp32 values).  TABLE: the angle is read from the
+// token's sequence row `pos` of the angle table; a position outside the table sets *err and rotates
+// by 0.  (A compile-time choice: even a never-taken runtime branch here costs the prefill kernel
+// ~5 us at C4 through its code generation.)
+template <bool TABLE>
+__device__ __forceinline__ float2 rope_cs(const RopeArgs& a, int t, int tok, int pos)
 {
-    const float ang = __fmul_rn(a.inv_freq[t], (float)pos);
+    float ang;
+    if constexpr (TABLE)
+    {
+        const int64_t b = tok / (int)a.seq_len;
+        if (pos >= 0 && pos < a.table_rows) ang = a.table[b * a.table_bstride + (int64_t)pos * (a.R >> 1) + t];
+        else
+        {
+            if (a.err) atomicOr(a.err, 1);
+            ang = 0.0f;
+        }
+    }
+    else ang = __fmul_rn(a.inv_freq[t], (float)pos);
     double sd, cd;
     sincos_angle(ang, sd, cd);
     return make_float2((float)cd * a.attn, (float)sd * a.attn);
 }
 
 // sin/cos of every rotary frequency of one token into LDS (generic kernel).
-__device__ __forceinline__ void fill_sincos(const RopeArgs& a, int pos, float2* cs)
+__device__ __forceinline__ void fill_sincos(const RopeArgs& a, int tok, int pos, float2* cs)
 {
-    for (int t = threadIdx.x; t < a.R / 2; t += blockDim.x) cs[t] = rope_cs(a, t, pos);
+    for (int t = threadIdx.x; t < a.R / 2; t += blockDim.x)
+        cs[t] = a.table ? rope_cs<true>(a, t, tok, pos) : rope_cs<false>(a, t, tok, pos);
 }
 
 // Norm weights of one lane's 8-element chunk with the constant bias folded in, loaded once per
@@ -321,7 +341,7 @@ __device__ __forceinline__ void lane_sincos(const float2* row, int e0, int R, fl
 // Decode / small launches.  Work item = one (token, head) pair; a workgroup takes a contiguous range
 // of slots * ITERS items, which spans at most a.tok_span tokens.  Every head chunk is loaded first;
 // the sin/cos of the spanned tokens are evaluated into LDS while those loads are in flight.
-template <class IO, int MODE, int LPH, int ITERS, int NORM, bool APPEND>
+template <class IO, int MODE, int LPH, int ITERS, int NORM, bool APPEND, bool TABLE>
 __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
 {
     extern __shared__ float2 cs[];            // [tok_span][R / 2]
@@ -400,7 +420,7 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
         {
             const int tr = i / R2;
             const int tok = tok0 + tr;
-            if (tok < a.tokens) cs[i] = rope_cs(a, i - tr * R2, token_position(a, tok));
+            if (tok < a.tokens) cs[i] = rope_cs<TABLE>(a, i - tr * R2, tok, token_position(a, tok));
         }
         __syncthreads();
 
@@ -495,7 +515,7 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
     auto fill = [&](int64_t tok) {
         const int pos = token_position(a, (int)tok);
         wave_lds_sync();
-        for (int t = l64; t < R2; t += 64) row[t] = rope_cs(a, t, pos);
+        for (int t = l64; t < R2; t += 64) row[t] = rope_cs<false>(a, t, (int)tok, pos);
         wave_lds_sync();
         lane_sincos<MODE>(row, e0, a.R, c, s);
     };
@@ -567,7 +587,7 @@ __global__ __launch_bounds__(256) void k_rope_generic(RopeArgs a, int dt, int mo
     const int half = a.R / 2;
     for (int64_t tok = blockIdx.x; tok < a.tokens; tok += gridDim.x)
     {
-    fill_sincos(a, token_position(a, (int)tok), cs);
+    fill_sincos(a, (int)tok, token_position(a, (int)tok), cs);
     const int64_t crow = a.kc ? cache_row(a, tok) : -1;
     __syncthreads();
     for (int head = 0; head < a.hq + a.hk + a.hv; ++head)
@@ -631,7 +651,7 @@ __global__ __launch_bounds__(256) void k_rope_generic(RopeArgs a, int dt, int mo
     }
 }
 
-template <class IO, int MODE, int LPH, int NORM>
+template <class IO, int MODE, int LPH, int NORM, bool TABLE>
 static void launch_rope_lph(RopeArgs a, int iters, hipStream_t s)
 {
     const int threads = 256;
@@ -642,10 +662,16 @@ static void launch_rope_lph(RopeArgs a, int iters, hipStream_t s)
     int64_t blocks = (items + per_wg - 1) / per_wg;
     if (blocks > kMaxGridX) blocks = kMaxGridX;
     const size_t lds = (size_t)a.tok_span * (a.R / 2) * sizeof(float2);
+    if constexpr (TABLE)
+    {
+        // Angle tables (never with a paged append): two heads per lane.
+        k_rope<IO, MODE, LPH, 2, NORM, false, true><<<(unsigned)blocks, threads, lds, s>>>(a);
+        return;
+    }
     auto go = [&](auto I) {
         constexpr int IT = decltype(I)::value;
-        if (a.kc) k_rope<IO, MODE, LPH, IT, NORM, true><<<(unsigned)blocks, threads, lds, s>>>(a);
-        else k_rope<IO, MODE, LPH, IT, NORM, false><<<(unsigned)blocks, threads, lds, s>>>(a);
+        if (a.kc) k_rope<IO, MODE, LPH, IT, NORM, true, false><<<(unsigned)blocks, threads, lds, s>>>(a);
+        else k_rope<IO, MODE, LPH, IT, NORM, false, false><<<(unsigned)blocks, threads, lds, s>>>(a);
     };
     switch (iters)
     {
@@ -690,6 +716,13 @@ template <class IO, int MODE, int NORM>
 static void launch_rope_vec(const RopeArgs& a, int lph, hipStream_t s)
 {
     const Tuning& tu = tuning();
+    if (a.table)
+    {
+        if (lph == 8) launch_rope_lph<IO, MODE, 8, NORM, true>(a, 2, s);
+        else if (lph == 16) launch_rope_lph<IO, MODE, 16, NORM, true>(a, 2, s);
+        else launch_rope_lph<IO, MODE, 32, NORM, true>(a, 2, s);
+        return;
+    }
     if constexpr (MODE == EXL3R_ROPE_NEOX)
     {
         if (tu.rope_tok == 2 || (tu.rope_tok == 0 && a.tokens >= 1024))
@@ -706,9 +739,9 @@ static void launch_rope_vec(const RopeArgs& a, int lph, hipStream_t s)
     if (tu.rope_iters == 1 || tu.rope_iters == 2 || tu.rope_iters == 4) iters = tu.rope_iters;
     else if (items >= slots * 4 * 2048) iters = 4;
     else if (items >= slots * 2 * 2048) iters = 2;
-    if (lph == 8) launch_rope_lph<IO, MODE, 8, NORM>(a, iters, s);
-    else if (lph == 16) launch_rope_lph<IO, MODE, 16, NORM>(a, iters, s);
-    else launch_rope_lph<IO, MODE, 32, NORM>(a, iters, s);
+    if (lph == 8) launch_rope_lph<IO, MODE, 8, NORM, false>(a, iters, s);
+    else if (lph == 16) launch_rope_lph<IO, MODE, 16, NORM, false>(a, iters, s);
+    else launch_rope_lph<IO, MODE, 32, NORM, false>(a, iters, s);
 }
 
 template <class IO>
@@ -733,7 +766,7 @@ static int rope_prepare(const char* op, RopeArgs& a, const void* q, void* out_q,
                         const int32_t* positions, const int32_t* position_ids, const void* q_norm, const void* k_norm,
                         int norm_dtype, float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor)
 {
-    if (!inv_freq) return set_error(EXL3R_EINVAL, "%s: inv_freq must be non-null", op);
+    if (!inv_freq) return set_error(EXL3R_EINVAL, "%s: inv_freq (angle table) must be non-null", op);
     if (dtype != EXL3R_F16 && dtype != EXL3R_BF16)
         return set_error(EXL3R_EDTYPE, "%s: q/k dtype must be f16 or bf16, got %s", op, dtype_name(dtype));
     if (rope_mode != EXL3R_ROPE_GPTJ && rope_mode != EXL3R_ROPE_NEOX)
@@ -858,5 +891,30 @@ extern "C" int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_str
     a.page_log2 = lg;
     a.pages = num_pages; a.max_blocks = max_blocks_per_seq;
     a.block_table = block_table; a.cache_seqlens = cache_seqlens; a.err = err_flag;
+    return rope_dispatch(op, a, dtype, rope_mode, stream);
+}
+
+extern "C" int exl3r_rope_table(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int num_heads_q,
+                                const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int num_heads_k,
+                                int dtype, int64_t bsz, int64_t seq_len, int head_dim,
+                                const float* angle_table, int64_t table_rows, int64_t table_batch_stride, int rotary_dim,
+                                int32_t position, const int32_t* positions, const int32_t* position_ids,
+                                const void* q_norm, const void* k_norm, int norm_dtype,
+                                float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
+                                int32_t* err_flag, void* stream)
+{
+    const char* op = "exl3r_rope_table";
+    if (table_rows <= 0 || table_batch_stride < 0)
+        return set_error(EXL3R_EINVAL, "%s: table_rows must be positive and table_batch_stride non-negative", op);
+    RopeArgs a;
+    const int rc = rope_prepare(op, a, q, out_q, q_tok_stride, q_head_stride, num_heads_q, k, out_k, false, k_tok_stride,
+                                k_head_stride, num_heads_k, dtype, bsz, seq_len, head_dim, angle_table, rotary_dim,
+                                position, positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps,
+                                norm_constant_bias, rope_mode, attn_factor);
+    if (rc || a.tokens == 0) return rc;
+    a.table = angle_table;
+    a.table_rows = table_rows;
+    a.table_bstride = table_batch_stride;
+    a.err = err_flag;
     return rope_dispatch(op, a, dtype, rope_mode, stream);
 }

@@ -151,9 +151,12 @@ def deinterleave_qg(qg, q, g, head_dim, stream=None):
 
 
 def rope(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias,
-         rope_mode, attn_factor, position_ids=None, stream=None):
+         rope_mode, attn_factor, position_ids=None, stream=None, err_flag=None):
     """Fused (optional) q/k head RMSNorm + RoPE.  q, k: (bsz, seq_len, heads, head_dim); `positions`
-    (int32 [bsz], device) or `position_ids` (int32 [bsz, seq_len], device) override `position`."""
+    (int32 [bsz], device) or `position_ids` (int32 [bsz, seq_len], device) override `position`.
+    As in the reference (rope.cu:340-347), a 2-D [max_pos, R/2] or 3-D [bsz, max_pos, R/2] inv_freq
+    is a table of precomputed angles (RoPE::apply's freq_table, src/rope.rs:225-260): the 2-D table
+    is shared by every sequence; a position outside it sets err_flag (int32, device) if given."""
     if q.dim() != 4:
         raise ValueError("q must be (bsz, seq_len, heads, head_dim)")
     bsz, seq, hq, hd = q.shape
@@ -174,6 +177,21 @@ def rope(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm
         if t is not None and t.dtype != torch.int32:
             raise TypeError("positions / position_ids must be int32")
     nw = q_norm if q_norm is not None else k_norm
+    if inv_freq.dim() > 1:
+        if inv_freq.dtype != torch.float32 or not inv_freq.is_contiguous() or inv_freq.dim() > 3:
+            raise ValueError("an angle table must be a contiguous float32 [max_pos, R/2] or [bsz, max_pos, R/2]")
+        if inv_freq.dim() == 3 and inv_freq.shape[0] < bsz:
+            raise ValueError("a per-sequence angle table needs bsz rows of tables")
+        rows, half = inv_freq.shape[-2], inv_freq.shape[-1]
+        bstride = rows * half if inv_freq.dim() == 3 else 0
+        check(load().exl3r_rope_table(_ptr(q), _ptr(out_q), q.stride(1), q.stride(2), hq,
+                                      _ptr(k), _ptr(out_k), k_ts, k_hs, hk,
+                                      dtype_code(q), bsz, seq, hd, _ptr(inv_freq), rows, bstride, half * 2,
+                                      int(position), _ptr(positions), _ptr(position_ids),
+                                      _ptr(q_norm), _ptr(k_norm), dtype_code(nw) if nw is not None else F16,
+                                      norm_eps, norm_constant_bias, rope_mode, attn_factor, _ptr(err_flag),
+                                      _stream(q, stream)))
+        return
     check(load().exl3r_rope(_ptr(q), _ptr(out_q), q.stride(1), q.stride(2), hq,
                             _ptr(k), _ptr(out_k), k_ts, k_hs, hk,
                             dtype_code(q), bsz, seq, hd, _ptr(inv_freq), inv_freq.shape[-1] * 2,

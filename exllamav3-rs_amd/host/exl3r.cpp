@@ -288,7 +288,8 @@ void gumbel_noise(const Tensor& x, const Tensor& out, uint32_t random, const Str
 
 void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
           int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
-          float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s, const Tensor* position_ids)
+          float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s, const Tensor* position_ids,
+          int32_t* err_flag)
 {
     require(q.dim() == 4, "rope: q must be (bsz, seq_len, heads, head_dim)");
     require(q.stride(3) == 1 && out_q.strides == q.strides && out_q.shape == q.shape,
@@ -309,6 +310,19 @@ void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* o
     require(!positions || positions->dtype == DType::I32, "rope: positions must be int32");
     require(!position_ids || position_ids->dtype == DType::I32, "rope: position_ids must be int32");
     const Tensor* nw = q_norm ? q_norm : k_norm;
+    if (inv_freq.dim() > 1)
+    {
+        require(inv_freq.dim() <= 3 && inv_freq.is_contiguous(), "rope: an angle table must be contiguous [max_pos, R/2] or [bsz, max_pos, R/2]");
+        require(inv_freq.dim() == 2 || inv_freq.size(0) >= bsz, "rope: a per-sequence angle table needs bsz tables");
+        const int64_t rows = inv_freq.size(-2), half = inv_freq.size(-1);
+        check_abi(exl3r_rope_table(q.data, out_q.data, q.stride(1), q.stride(2), (int)q.size(2), k ? k->data : nullptr,
+                                   out_k ? out_k->data : nullptr, kts, khs, (int)hk, code(q.dtype), bsz, seq, (int)hd,
+                                   (const float*)inv_freq.data, rows, inv_freq.dim() == 3 ? rows * half : 0, (int)(half * 2),
+                                   (int32_t)position, (const int32_t*)ptr(positions), (const int32_t*)ptr(position_ids),
+                                   ptr(q_norm), ptr(k_norm), code_or(nw, DType::F16), norm_eps, norm_constant_bias,
+                                   (int)rope_mode, attn_factor, err_flag, s.get()));
+        return;
+    }
     check_abi(exl3r_rope(q.data, out_q.data, q.stride(1), q.stride(2), (int)q.size(2), k ? k->data : nullptr,
                          out_k ? out_k->data : nullptr, kts, khs, (int)hk, code(q.dtype), bsz, seq, (int)hd,
                          (const float*)inv_freq.data, (int)(inv_freq.numel() * 2), (int32_t)position,
@@ -445,10 +459,11 @@ std::vector<float> RoPE::default_inv_freq(double theta, int rotary_dim, double l
 }
 
 void RoPE::apply(const Tensor& q, const Tensor& k, int64_t position, const Tensor* positions, const Tensor* q_norm,
-                 const Tensor* k_norm, float norm_eps, float norm_constant_bias, const Stream& s) const
+                 const Tensor* k_norm, float norm_eps, float norm_constant_bias, const Stream& s,
+                 const Tensor* freq_table) const
 {
-    ffi::rope(q, q, &k, &k, inv_freq_t_, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias, style_,
-              attn_factor_, s);
+    ffi::rope(q, q, &k, &k, freq_table ? *freq_table : inv_freq_t_, position, positions, q_norm, k_norm, norm_eps,
+              norm_constant_bias, style_, attn_factor_, s);
 }
 
 void RoPE::apply_paged(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& k_cache, const Tensor& v_cache,

@@ -137,11 +137,14 @@ void mul_sigmoid_(const Tensor& x, const Tensor& y, const Stream& s);
 // g [.., heads * head_dim].
 void deinterleave_qg(const Tensor& qg, const Tensor& q, const Tensor& g, int64_t head_dim, const Stream& s);
 // src/ffi.rs:298-333: fused (optional) q/k head RMSNorm + RoPE on (bsz, seq, heads, head_dim)
-// tensors; positions (int32 [bsz]) or position_ids (int32 [bsz, seq]) override position.
+// tensors; positions (int32 [bsz]) or position_ids (int32 [bsz, seq]) override position.  As in the
+// reference (rope.cu:340-347), a 2-D [max_pos, R/2] (shared by every sequence) or 3-D
+// [bsz, max_pos, R/2] inv_freq is a table of precomputed angles; a position outside it stores 1 to
+// err_flag (device int32) when given.
 void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
           int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
           float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s,
-          const Tensor* position_ids = nullptr);
+          const Tensor* position_ids = nullptr, int32_t* err_flag = nullptr);
 // rope() fused with the paged KV-cache append that follows it in paged attention (src/modules.rs:666-704,
 // ffi.rs:337-350): the roped k (also written to out_k when given) and v go to k_cache / v_cache
 // [pages, page_size, kv_heads, head_dim] at cache_seqlens[b] + s through block_table [bsz, max_blocks].
@@ -214,8 +217,11 @@ public:
     // divided by `linear_factor` for rope_type "linear" (rope.rs:55-59).
     RoPE(double theta, int rotary_dim, RopeStyle style, double attn_factor = 1.0, double linear_factor = 1.0);
     static std::vector<float> default_inv_freq(double theta, int rotary_dim, double linear_factor = 1.0);
+    // freq_table: optional [max_pos, rotary_dim/2] f32 precomputed angles used in place of inv_freq
+    // (rope.rs:225-260: MRoPE, the vision tower's 2-D RoPE).
     void apply(const Tensor& q, const Tensor& k, int64_t position, const Tensor* positions, const Tensor* q_norm,
-               const Tensor* k_norm, float norm_eps, float norm_constant_bias, const Stream& s) const;
+               const Tensor* k_norm, float norm_eps, float norm_constant_bias, const Stream& s,
+               const Tensor* freq_table = nullptr) const;
     void apply_one(const Tensor& x, int64_t position, const Tensor* positions, const Tensor* norm, float norm_eps,
                    float norm_constant_bias, const Stream& s) const;
     // apply() on q and k in place, then k and v appended to the paged caches (one launch); the rotary

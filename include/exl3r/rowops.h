@@ -26,6 +26,9 @@
  *   exl3r_silu_mul          <- exl3_shim_silu_mul         csrc/exl3_shim.cpp:151     (ffi.rs:125, 492-495)
  *   exl3r_gelu_mul          <- exl3_shim_gelu_mul         csrc/exl3_shim.cpp:152     (ffi.rs:126, 496-499)
  *   exl3r_rope              <- exl3_shim_rope             csrc/exl3_shim.cpp:87-98   (ffi.rs:51-65, 298-333)
+ *   exl3r_rope_table        <- exl3_shim_rope with a [max_pos, rotary_dim/2] (or per-sequence
+ *                              [bsz, max_pos, rotary_dim/2]) angle table as inv_freq, RoPE::apply's
+ *                              freq_table  src/rope.rs:225-260, kernels/rope.cu:69-83, 340-347
  *   exl3r_rope_paged_kv     <- exl3_shim_rope followed by exl3_shim_paged_kv_cache_update
  *                              csrc/exl3_shim.cpp:87-98, 109-112 (ffi.rs:298-350; call sites modules.rs:666-704)
  *   exl3r_gated_rms_norm    <- exl3_shim_gated_rms_norm   csrc/exl3_shim.cpp:143-147 (ffi.rs:118-124, 479-483)
@@ -187,6 +190,26 @@ EXL3R_API int exl3r_rope(const void* q, void* out_q, int64_t q_tok_stride, int64
                float norm_eps, float norm_constant_bias,
                int rope_mode, float attn_factor,
                void* stream);
+
+/*
+ * exl3r_rope with precomputed rotation angles (MRoPE, the vision tower's 2-D RoPE): the angle of
+ * frequency t for token s of sequence b at position pos (from position / positions / position_ids as
+ * in exl3r_rope) is angle_table[b*table_batch_stride + pos*(rotary_dim/2) + t]; sin and cos of it
+ * are evaluated as in exl3r_rope.  table_batch_stride 0 shares one [table_rows, rotary_dim/2] table
+ * between sequences; table_rows*rotary_dim/2 gives each sequence its own.  Replaces exl3_shim_rope
+ * called with a 2-D / 3-D inv_freq (kernels/rope.cu:69-83, 340-347, where the 2-D form is only
+ * valid for bsz 1).
+ *   err_flag: NULL or a device int32; a position outside [0, table_rows) is rotated by angle 0 and
+ *             1 is stored to *err_flag (the reference reads outside the table).
+ */
+EXL3R_API int exl3r_rope_table(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int num_heads_q,
+                     const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int num_heads_k,
+                     int dtype, int64_t bsz, int64_t seq_len, int head_dim,
+                     const float* angle_table, int64_t table_rows, int64_t table_batch_stride, int rotary_dim,
+                     int32_t position, const int32_t* positions, const int32_t* position_ids,
+                     const void* q_norm, const void* k_norm, int norm_dtype,
+                     float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
+                     int32_t* err_flag, void* stream);
 
 /*
  * exl3r_rope fused with the paged KV-cache append that follows it in paged attention

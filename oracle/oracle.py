@@ -27,6 +27,8 @@ _PROTOS = {
     "oracle_act_mul": (_i, [_i, _vp, _vp, _i, _vp, _i, _i64, _i64, _i64, _i64, _i64, _f, _i]),
     "oracle_rope": (_i, [_vp, _vp, _i64, _i64, _i, _vp, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _i,
                          _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _i]),
+    "oracle_rope_table": (_i, [_vp, _vp, _i64, _i64, _i, _vp, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _i64, _i64,
+                               _i, _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _vp, _i]),
     "oracle_embedding": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _i64, _vp, _i]),
     "oracle_gated_rms_norm": (_i, [_vp, _i, _i64, _vp, _i, _i, _vp, _i, _i64, _vp, _i, _i64, _i64, _i64, _f, _f, _i,
                                    _i, _i]),
@@ -217,6 +219,28 @@ def rope(q, k, dt, inv_freq, mode, position=0, positions=None, position_ids=None
                               _p(inv_freq), inv_freq.size * 2, int(position), _p(positions), _p(position_ids),
                               _p(q_norm), _p(k_norm), nwt, eps, cb, mode, attn, nthreads), "oracle_rope")
     return oq, ok
+
+
+def rope_table(q, k, dt, table, mode, table_bstride=None, position=0, positions=None, position_ids=None, q_norm=None,
+               k_norm=None, nwt=F16, eps=1e-6, cb=0.0, attn=1.0, nthreads=1):
+    """rope() with angles read from `table` ([rows, R/2], one table for every sequence, or
+    [bsz, rows, R/2], one per sequence).  Returns (out_q, out_k, err)."""
+    bsz, seq, hq, hd = q.shape
+    oq = np.empty_like(q)
+    ok, hk = None, 0
+    if k is not None:
+        hk = k.shape[2]
+        ok = np.empty_like(k)
+    table = np.ascontiguousarray(table, dtype=np.float32)
+    rows, half = table.shape[-2], table.shape[-1]
+    if table_bstride is None:
+        table_bstride = rows * half if table.ndim == 3 else 0
+    err = np.zeros(1, np.int32)
+    _check(load().oracle_rope_table(_p(q), _p(oq), hq * hd, hd, hq, _p(k), _p(ok), hk * hd, hd, hk, dt, bsz, seq, hd,
+                                    _p(table), rows, table_bstride, half * 2, int(position), _p(positions),
+                                    _p(position_ids), _p(q_norm), _p(k_norm), nwt, eps, cb, mode, attn, _p(err),
+                                    nthreads), "oracle_rope_table")
+    return oq, ok, int(err[0])
 
 
 def embedding(table, tt, ids, idt, ot, nthreads=1):

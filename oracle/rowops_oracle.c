@@ -341,15 +341,19 @@ static void rope_head(const void* in, void* out, int64_t off, int dt, int hd, in
     for (int d = 0; d < hd; ++d) st(out, dt, off + d, v[d]);
 }
 
-int oracle_rope(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int hq,
-                const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int hk,
-                int dt, int64_t bsz, int64_t seq_len, int hd,
-                const float* inv_freq, int R,
-                int32_t position, const int32_t* positions, const int32_t* position_ids,
-                const void* q_norm, const void* k_norm, int nwt,
-                float eps, float cb, int mode, float attn_factor, int nthreads)
+/* Shared by oracle_rope (angle = inv_freq[t] * pos) and oracle_rope_table (angle read from the
+ * table row of the token's sequence at pos; a position outside [0, table_rows) sets *err and
+ * rotates by angle 0). */
+static int rope_impl(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int hq,
+                     const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int hk,
+                     int dt, int64_t bsz, int64_t seq_len, int hd,
+                     const float* inv_freq, const float* table, int64_t table_rows, int64_t table_bstride,
+                     int32_t* err, int R,
+                     int32_t position, const int32_t* positions, const int32_t* position_ids,
+                     const void* q_norm, const void* k_norm, int nwt,
+                     float eps, float cb, int mode, float attn_factor, int nthreads)
 {
-    if (!q || !out_q || !inv_freq || hd <= 0 || (hd & 1) || R < 2 || (R & 1) || R > hd) return -1;
+    if (!q || !out_q || !(inv_freq || table) || hd <= 0 || (hd & 1) || R < 2 || (R & 1) || R > hd) return -1;
     if (dt != OR_F16 && dt != OR_BF16) return -2;
     if (mode != OR_ROPE_GPTJ && mode != OR_ROPE_NEOX) return -1;
     if (k && !out_k) return -1;
@@ -403,9 +407,20 @@ int oracle_rope(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head
             else if (position_ids) pos = position_ids[tok];
             if (oracle_mutation == ORM_ROPE_POS_OFF) pos += 1;
             float pf = (float)pos;
+            int64_t trow = -1;
+            if (table)
+            {
+                const int32_t tp = oracle_mutation == ORM_TABLE_ROW_OFF ? pos + 1 : pos;
+                if (tp >= 0 && tp < table_rows) trow = b * table_bstride + (int64_t)tp * (R / 2);
+                else if (err)
+                {
+                    #pragma omp atomic write
+                    *err = 1;
+                }
+            }
             for (int t = 0; t < R / 2; ++t)
             {
-                float a = inv_freq[t] * pf;
+                float a = table ? (trow >= 0 ? table[trow + t] : 0.0f) : inv_freq[t] * pf;
                 float c = (float)cos((double)a) * attn_factor;
                 float sn = (float)sin((double)a) * attn_factor;
                 if (oracle_mutation == ORM_ROPE_SWAP_SINCOS) { float tmp = c; c = sn; sn = tmp; }
@@ -423,6 +438,35 @@ int oracle_rope(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head
     }
     free(wfq); free(wfk); free(whq); free(whk);
     return 0;
+}
+
+int oracle_rope(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int hq,
+                const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int hk,
+                int dt, int64_t bsz, int64_t seq_len, int hd,
+                const float* inv_freq, int R,
+                int32_t position, const int32_t* positions, const int32_t* position_ids,
+                const void* q_norm, const void* k_norm, int nwt,
+                float eps, float cb, int mode, float attn_factor, int nthreads)
+{
+    if (!inv_freq) return -1;
+    return rope_impl(q, out_q, q_tok_stride, q_head_stride, hq, k, out_k, k_tok_stride, k_head_stride, hk, dt, bsz,
+                     seq_len, hd, inv_freq, NULL, 0, 0, NULL, R, position, positions, position_ids, q_norm, k_norm,
+                     nwt, eps, cb, mode, attn_factor, nthreads);
+}
+
+/* rope.cu:69-83 (inv_freq_table): the angle of frequency t is table[b * stride + pos * R/2 + t] */
+int oracle_rope_table(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int hq,
+                      const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int hk,
+                      int dt, int64_t bsz, int64_t seq_len, int hd,
+                      const float* table, int64_t table_rows, int64_t table_bstride, int R,
+                      int32_t position, const int32_t* positions, const int32_t* position_ids,
+                      const void* q_norm, const void* k_norm, int nwt,
+                      float eps, float cb, int mode, float attn_factor, int32_t* err, int nthreads)
+{
+    if (!table || table_rows <= 0 || table_bstride < 0) return -1;
+    return rope_impl(q, out_q, q_tok_stride, q_head_stride, hq, k, out_k, k_tok_stride, k_head_stride, hk, dt, bsz,
+                     seq_len, hd, NULL, table, table_rows, table_bstride, err, R, position, positions, position_ids,
+                     q_norm, k_norm, nwt, eps, cb, mode, attn_factor, nthreads);
 }
 
 /* ------------------------------------------------------------------------------------------ */

@@ -65,6 +65,7 @@ extern int oracle_mutation;
 #define ORM_PHILOX_NO_BUMP   23  /* Philox key not advanced between rounds */
 #define ORM_LOG_NO_LN2LO     24  /* log drops the low part of e * ln2 */
 #define ORM_GUMBEL_NO_ROW    25  /* Gumbel noise ignores the row (every row draws the same noise) */
+#define ORM_TABLE_ROW_OFF    26  /* angle table read one row past the position */
 
 /* Conversions (round to nearest even; NaN -> canonical quiet NaN). */
 uint16_t oracle_f32_to_f16(float f);
@@ -95,6 +96,20 @@ int oracle_rope(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head
                 const void* q_norm, const void* k_norm, int norm_dtype,
                 float norm_eps, float norm_constant_bias,
                 int rope_mode, float attn_factor, int nthreads);
+
+/*
+ * oracle_rope with an angle table in place of inv_freq (RoPE::apply's freq_table, src/rope.rs:225-260;
+ * rope.cu:69-83): the angle of frequency t for token s of sequence b at position pos is
+ * table[b * table_bstride + pos * R/2 + t] (table_bstride 0: one table for every sequence); a
+ * position outside [0, table_rows) stores 1 to *err (when given) and rotates by angle 0.
+ */
+int oracle_rope_table(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int hq,
+                      const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int hk,
+                      int dt, int64_t bsz, int64_t seq_len, int hd,
+                      const float* table, int64_t table_rows, int64_t table_bstride, int R,
+                      int32_t position, const int32_t* positions, const int32_t* position_ids,
+                      const void* q_norm, const void* k_norm, int nwt,
+                      float eps, float cb, int mode, float attn_factor, int32_t* err, int nthreads);
 
 /*
  * Gated RMSNorm (gated_rms_norm_kernel, reference kernels/norm.cu:482-581; host checks 591-668):

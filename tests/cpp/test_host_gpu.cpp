@@ -189,6 +189,25 @@ int main()
         const int64_t dx = max_ulp16(xo, ex);
         std::snprintf(msg, sizeof msg, "max ulp %lld", (long long)dx);
         report("RoPE::apply_one gptj partial rotary", dx <= 2, msg);
+
+        // RoPE::apply with a freq_table of arbitrary angles (MRoPE-style), [50, hd/2], shared by both sequences.
+        std::vector<float> table(50 * hd / 2);
+        for (size_t i = 0; i < table.size(); ++i) table[i] = normal(0.f, 300.f);
+        OwnedTensor tab = OwnedTensor::empty(DType::F32, { 50, hd / 2 });
+        tab.buf.upload(table.data(), table.size() * 4, s);
+        std::vector<int32_t> tpos = { 3, 40 };
+        pd.buf.upload(tpos.data(), tpos.size() * 4, s);
+        auto q2 = upload(qh, DType::F16, { bsz, seq, hq, hd }, s);
+        auto k2 = upload(kh, DType::F16, { bsz, seq, hk, hd }, s);
+        rope.apply(q2.t, k2.t, 0, &pd.t, &qn.t, &kn.t, 1e-6f, 0.f, s, &tab.t);
+        auto q2o = download(q2, s), k2o = download(k2, s);
+        int32_t terr = 0;
+        oracle_rope_table(qh.data(), eq.data(), hq * hd, hd, hq, kh.data(), ek.data(), hk * hd, hd, hk, OR_F16, bsz, seq,
+                          hd, table.data(), 50, 0, hd, 0, tpos.data(), nullptr, qnh.data(), knh.data(), OR_F16, 1e-6f,
+                          0.f, OR_ROPE_NEOX, 1.f, &terr, 1);
+        const int64_t tq = max_ulp16(q2o, eq), tk = max_ulp16(k2o, ek);
+        std::snprintf(msg, sizeof msg, "q max ulp %lld, k max ulp %lld", (long long)tq, (long long)tk);
+        report("RoPE::apply with freq_table", tq <= 2 && tk <= 2 && terr == 0, msg);
     }
     // RoPE::apply_paged: rope + paged KV append (16-token pages, positions = cache lengths).
     {
