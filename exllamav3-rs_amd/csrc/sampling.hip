@@ -16,9 +16,10 @@
 // Philox4x32-10 is the published generator of Salmon, Moraes, Dror and Shaw ("Parallel random
 // numbers: as easy as 1, 2, 3", SC 2011).
 //
-// Layout, fewer than 512 rows (decode): a row is cut into slices of 2048 or 8192 elements, a 256-lane
+// Layout, few rows (decode): a row is cut into slices of 2048 or 8192 elements, a 256-lane
 // workgroup per slice (grid (slices, rows)), so a single decode row of 152k logits still spreads over
-// ~75 CUs.  512 rows and more: a workgroup per row, the index written directly.  Each lane keeps its
+// ~75 CUs.  From 128 rows (argmax) or 384 rows (Gumbel draw): a workgroup of 512 or 1024 lanes per
+// row, the index written directly.  Each lane keeps its
 // best candidate as one 64-bit key -- an order-preserving image of the value in the high word, the
 // complement of the index in the low word -- so "larger key" is exactly "larger value, then lower
 // index".  With slices, the workgroup's maximum key (DPP butterfly, one LDS hop) goes to the row's
@@ -262,30 +263,33 @@ __global__ __launch_bounds__(256) void k_argmax(ArgArgs a)
     }
 }
 
-// Many rows: a workgroup owns a row, walks it 2048 elements per step with 4 chunks per lane in
-// flight, and writes the index itself (no atomics, no clear / convert launches).
-template <class IT, bool VEC, bool GUMBEL>
-__global__ __launch_bounds__(256) void k_argmax_rows(ArgArgs a)
+// Many rows: a workgroup of THREADS lanes owns a row, walks it THREADS * 8 elements per chunk round
+// with 4 chunks per lane in flight, and writes the index itself (no atomics, no clear / convert
+// launches).
+template <class IT, bool VEC, bool GUMBEL, int THREADS>
+__global__ __launch_bounds__(THREADS) void k_argmax_rows(ArgArgs a)
 {
-    __shared__ uint64_t part[4];
+    constexpr int WAVES = THREADS / 64;
+    constexpr int STEP = THREADS * 8;          // elements per chunk round
+    __shared__ uint64_t part[WAVES];
     const int tid = threadIdx.x;
     for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x)
     {
         const char* base = a.x + row * a.ld;
         LaneBest lb;
-        for (int64_t s0 = 0; s0 < a.n; s0 += 4 * 2048)
+        for (int64_t s0 = 0; s0 < a.n; s0 += 4 * STEP)
         {
             typename IT::Vec v[4];
             #pragma unroll
             for (int u = 0; u < 4; ++u)
             {
-                const int64_t c = s0 + u * 2048 + tid * 8;
+                const int64_t c = s0 + u * STEP + tid * 8;
                 if (VEC && c + 8 <= a.n) v[u] = load8s<IT>(base, c);
             }
             #pragma unroll
             for (int u = 0; u < 4; ++u)
             {
-                const int64_t c = s0 + u * 2048 + tid * 8;
+                const int64_t c = s0 + u * STEP + tid * 8;
                 if (VEC && c + 8 <= a.n)
                 {
                     float f[8];
@@ -306,7 +310,9 @@ __global__ __launch_bounds__(256) void k_argmax_rows(ArgArgs a)
         __syncthreads();
         if (tid == 0)
         {
-            best = max_u64(max_u64(part[0], part[1]), max_u64(part[2], part[3]));
+            best = part[0];
+            #pragma unroll
+            for (int w = 1; w < WAVES; ++w) best = max_u64(best, part[w]);
             a.ids[row] = best ? (uint64_t)(0xffffffffu - (uint32_t)best) : 0;
         }
         __syncthreads();
@@ -374,12 +380,35 @@ int sample_entry(const char* op, const void* logits, int dtype, int64_t rows, in
     ArgArgs a{ (const char*)logits, (rows > 1 ? ld : vocab) * es, n, rows, (uint64_t*)ids, seed };
     hipStream_t s = (hipStream_t)stream;
     const bool vec = aligned16(logits) && a.ld % 16 == 0;
-    if (rows >= 512)
+    // Measured on MI355X over f16 [rows, 151936] logits (us; sliced / a workgroup per row with 512 /
+    // 1024 lanes): argmax 64 rows 11.2 / 25.0 / 16.4, 128 rows 16.8 / 25.7 / 17.0, 192 rows 21.8 /
+    // 26.3 / 17.4, 512 rows - / 32.0 / 33.5 (256 lanes 57.0), 1024 rows - / 62.3 / 64.5; the Gumbel
+    // draw, compute-bound, keeps the sliced kernel longer: 256 rows 58.9 / 74.6 / 64.3, 512 rows
+    // 147.6 (256 lanes) / 125.9 / 125.6, 1024 rows - / 225.3 / 246.3.
+    const Tuning& tu = tuning();
+    const int64_t rows_min = tu.sample_rows_min > 0 ? tu.sample_rows_min : GUMBEL ? 384 : 128;
+    if (rows >= rows_min)
     {
         const unsigned grid = (unsigned)(rows < kMaxGridX ? rows : kMaxGridX);
+        int threads = GUMBEL || rows >= 512 ? 512 : 1024;
+        if (tu.sample_threads == 256 || tu.sample_threads == 512 || tu.sample_threads == 1024) threads = tu.sample_threads;
         with_float_type(dtype, [&](auto T) {
-            if (vec) k_argmax_rows<decltype(T), true, GUMBEL><<<grid, 256, 0, s>>>(a);
-            else k_argmax_rows<decltype(T), false, GUMBEL><<<grid, 256, 0, s>>>(a);
+            using Ty = decltype(T);
+            if (threads == 1024)
+            {
+                if (vec) k_argmax_rows<Ty, true, GUMBEL, 1024><<<grid, 1024, 0, s>>>(a);
+                else k_argmax_rows<Ty, false, GUMBEL, 1024><<<grid, 1024, 0, s>>>(a);
+            }
+            else if (threads == 512)
+            {
+                if (vec) k_argmax_rows<Ty, true, GUMBEL, 512><<<grid, 512, 0, s>>>(a);
+                else k_argmax_rows<Ty, false, GUMBEL, 512><<<grid, 512, 0, s>>>(a);
+            }
+            else
+            {
+                if (vec) k_argmax_rows<Ty, true, GUMBEL, 256><<<grid, 256, 0, s>>>(a);
+                else k_argmax_rows<Ty, false, GUMBEL, 256><<<grid, 256, 0, s>>>(a);
+            }
         });
         return launch_status(op);
     }

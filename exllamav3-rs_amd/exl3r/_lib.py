@@ -50,6 +50,7 @@ PROTOTYPES = {
     "exl3r_tune_rope": (None, [_i]),
     "exl3r_tune_rms_rows": (None, [_i]),
     "exl3r_tune_rope_tok": (None, [_i, _i, _i]),
+    "exl3r_tune_sample": (None, [_i, _i]),
     "exl3r_tune_embed": (None, [_i]),
 }
 

@@ -249,7 +249,7 @@ EXL3R_API int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_stri
  * 65-92, 151-172; for an odd max_logit its pairwise mask, 57-60, also drops index max_logit - 1;
  * here the mask is exact)
  * and the generator's batched tch argmax (src/generator.rs:1596).  ids must be 8-byte aligned.  Below
- * 512 rows ids is the reduction slot during the call (three launches on `stream`); from 512 rows a
+ * 128 rows ids is the reduction slot during the call (three launches on `stream`); from 128 rows a
  * single launch writes it directly.
  */
 EXL3R_API int exl3r_argmax_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,

@@ -70,7 +70,7 @@ def test_unaligned_and_unpadded():
     run(dev_normal((3, 13), 0, 3, F32, 9), F32, 12)
 
 
-@pytest.mark.parametrize("rows", [511, 512, 1500])
+@pytest.mark.parametrize("rows", [127, 128, 383, 384, 511, 512, 1500])
 def test_many_rows(rows):
     run(dev_normal((rows, 20000), 0, 3, F16, rows), F16)
     run(dev_normal((rows, 5003), 0, 3, BF16, rows + 1)[:, 1:], BF16, 4000)

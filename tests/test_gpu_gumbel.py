@@ -48,6 +48,11 @@ def test_sample_prefill_rows(dt):
     run_sample(dev_normal((600, 32000), 0, 3, dt, 41), dt, 77)          # row-per-workgroup kernel
 
 
+@pytest.mark.parametrize("rows", [383, 384])
+def test_sample_kernel_switch(rows):
+    run_sample(dev_normal((rows, 9001), 0, 3, F16, 49), F16, 78)
+
+
 @pytest.mark.parametrize("m", [1, 2, 151643, 151936, 200000])
 def test_sample_mask(m):
     ids = run_sample(dev_normal((4, 151936), 0, 1, F16, 42), F16, 5, m)
