@@ -442,6 +442,111 @@ RoPE::RoPE(double theta, int rotary_dim, RopeStyle style, double attn_factor, do
     inv_freq_t_ = Tensor(inv_freq_.data(), DType::F32, { (int64_t)inv_freq_host_.size() });
 }
 
+RoPE::RoPE(double theta, int rotary_dim, RopeStyle style, const RopeScaling& sc)
+    : style_(style)
+{
+    Params p = params(theta, rotary_dim, sc);
+    inv_freq_host_ = std::move(p.inv_freq);
+    rotary_dim_ = (int)inv_freq_host_.size() * 2;
+    attn_factor_ = (float)p.attn_factor;
+    inv_freq_ = DeviceBuffer(inv_freq_host_.size() * sizeof(float));
+    check_hip(hipMemcpy(inv_freq_.data(), inv_freq_host_.data(), inv_freq_.bytes(), hipMemcpyHostToDevice), "hipMemcpy inv_freq");
+    inv_freq_t_ = Tensor(inv_freq_.data(), DType::F32, { (int64_t)inv_freq_host_.size() });
+}
+
+RoPE::Params RoPE::params(double theta, int rotary_dim, const RopeScaling& sc)
+{
+    using T = RopeScaling::Type;
+    require(theta > 0.0, "RoPE: theta must be positive");
+    const double pi = 3.14159265358979323846;
+    const double factor_or_1 = sc.factor > 0.0 ? sc.factor : 1.0;
+    if (sc.type == T::Default) return { default_inv_freq(theta, rotary_dim), 1.0 };
+    if (sc.type == T::Linear) return { default_inv_freq(theta, rotary_dim, factor_or_1), 1.0 };
+    if (sc.type == T::Proportional)
+    {
+        // inv_freq over head_dim / 2 frequencies: theta^(-2i / head_dim) for the first
+        // partial_rotary_factor * head_dim / 2, zero after (those dims keep angle 0), all / factor.
+        require(sc.head_dim >= 2 && sc.head_dim % 2 == 0, "RoPE proportional: head_dim must be even");
+        const int angles = (int)(sc.partial_rotary_factor * sc.head_dim / 2.0);
+        require(angles >= 0 && angles <= sc.head_dim / 2, "RoPE proportional: partial_rotary_factor out of range");
+        std::vector<float> inv(sc.head_dim / 2, 0.0f);
+        for (int i = 0; i < angles; ++i)
+            inv[i] = (float)(std::exp(-(2.0 * i / sc.head_dim) * std::log(theta)) / factor_or_1);
+        return { inv, 1.0 };
+    }
+    require(rotary_dim >= 2 && rotary_dim % 2 == 0, "RoPE: rotary_dim must be even and >= 2");
+    const int half = rotary_dim / 2;
+    const std::vector<float> base = default_inv_freq(theta, rotary_dim);
+    std::vector<float> inv(half);
+    if (sc.type == T::Llama3)
+    {
+        // Wavelengths 2 pi / f above old_ctx / low_freq_factor are divided by factor, those below
+        // old_ctx / high_freq_factor kept, and the band between blended with
+        // smooth = (old_ctx / wavelen - low) / (high - low).
+        const double factor = sc.factor > 0.0 ? sc.factor : 8.0;
+        const double old_ctx = sc.original_max_position_embeddings > 0.0 ? sc.original_max_position_embeddings : 8192.0;
+        require(sc.high_freq_factor > sc.low_freq_factor, "RoPE llama3: high_freq_factor must exceed low_freq_factor");
+        const double low_wl = old_ctx / sc.low_freq_factor, high_wl = old_ctx / sc.high_freq_factor;
+        for (int i = 0; i < half; ++i)
+        {
+            const double f = base[i], wl = 2.0 * pi / f;
+            const double scaled = wl > low_wl ? f / factor : f;
+            if (wl >= high_wl && wl <= low_wl)
+            {
+                const double smooth = (old_ctx / wl - sc.low_freq_factor) / (sc.high_freq_factor - sc.low_freq_factor);
+                inv[i] = (float)((scaled / factor) * (1.0 - smooth) + scaled * smooth);
+            }
+            else
+                inv[i] = (float)scaled;
+        }
+        return { inv, 1.0 };
+    }
+    if (sc.type == T::Yarn)
+    {
+        require(sc.max_position_embeddings > 0, "RoPE yarn: max_position_embeddings is required");
+        double orig_max, factor;
+        if (sc.original_max_position_embeddings > 0.0)
+        {
+            orig_max = sc.original_max_position_embeddings;
+            factor = (double)sc.max_position_embeddings / orig_max;
+        }
+        else
+        {
+            orig_max = (double)sc.max_position_embeddings;
+            factor = factor_or_1;
+        }
+        require(factor > 0.0, "RoPE yarn: factor must be positive");
+        auto find = [&](double rot) { return rotary_dim * std::log(orig_max / (rot * 2.0 * pi)) / (2.0 * std::log(theta)); };
+        double low = find(sc.beta_fast), high = find(sc.beta_slow);
+        if (sc.truncate)
+        {
+            low = std::floor(low);
+            high = std::ceil(high);
+        }
+        low = std::max(low, 0.0);
+        high = std::min(high, rotary_dim - 1.0);
+        if (low == high) high += 0.001;
+        for (int i = 0; i < half; ++i)
+        {
+            const double pos_freq = std::exp((2.0 * i / rotary_dim) * std::log(theta));
+            const double ramp = std::min(std::max((i - low) / (high - low), 0.0), 1.0);
+            const double extrap = 1.0 - ramp;
+            inv[i] = (float)((1.0 / (factor * pos_freq)) * (1.0 - extrap) + (1.0 / pos_freq) * extrap);
+        }
+        const double attn = sc.has_attention_factor ? sc.attention_factor
+                                                    : (factor <= 1.0 ? 1.0 : 0.1 * std::log(factor) + 1.0);
+        return { inv, attn };
+    }
+    // LongRope / "su": per-frequency extension factors, long_factor when the context is extended.
+    const double a = (double)sc.max_position_embeddings, b = sc.original_max_position_embeddings;
+    require(a > 0.0 && b > 0.0, "RoPE longrope: max_position_embeddings and original_max_position_embeddings are required");
+    const std::vector<double>& ext = a > b ? sc.long_factor : sc.short_factor;
+    require((int)ext.size() == half, "RoPE longrope: one factor per frequency (rotary_dim / 2) is required");
+    for (int i = 0; i < half; ++i)
+        inv[i] = (float)(1.0 / (ext[i] * std::exp((2.0 * i / rotary_dim) * std::log(theta))));
+    return { inv, a > b ? std::sqrt(1.0 + std::log(a / b) / std::log(b)) : 1.0 };
+}
+
 std::vector<float> RoPE::default_inv_freq(double theta, int rotary_dim, double linear_factor)
 {
     require(rotary_dim >= 2 && rotary_dim % 2 == 0, "RoPE: rotary_dim must be even and >= 2");

@@ -210,9 +210,39 @@ struct GatedMlp
 
 // src/rope.rs:33-86, 233-292, 309-317: inv_freq producer (default and linear scaling) and the
 // in-place apply / apply_one.
+// config.json rope_scaling (src/rope.rs:15-26, 45-67): the rope_type and the fields its producer reads.
+struct RopeScaling
+{
+    enum class Type { Default, Linear, Llama3, Yarn, LongRope, Proportional };
+    Type type = Type::Default;
+    double factor = 0.0;                       // 0: absent (linear, yarn, proportional 1; llama3 8)
+    double low_freq_factor = 1.0;              // llama3
+    double high_freq_factor = 4.0;             // llama3
+    double original_max_position_embeddings = 0.0;  // llama3 (8192 when 0), yarn, longrope
+    int64_t max_position_embeddings = 0;       // yarn, longrope
+    double beta_fast = 32.0, beta_slow = 1.0;  // yarn
+    bool truncate = true;                      // yarn
+    bool has_attention_factor = false;         // yarn: attention_factor given
+    double attention_factor = 1.0;
+    std::vector<double> long_factor, short_factor;   // longrope: one factor per frequency
+    int head_dim = 0;                          // proportional
+    double partial_rotary_factor = 1.0;        // proportional
+};
+
 class RoPE
 {
 public:
+    struct Params
+    {
+        std::vector<float> inv_freq;
+        double attn_factor;
+    };
+    // inv_freq and attn_factor of every rope_type the reference knows (RoPE::new, src/rope.rs:45-67;
+    // default / mrope 82-86, linear 55-59, llama3 88-108, proportional 110-131, yarn 133-191,
+    // longrope 193-220).  rotary_dim is ignored by "proportional", which spans head_dim with zero
+    // frequencies past partial_rotary_factor.  Throws exl3r::Error on a missing or invalid field.
+    static Params params(double theta, int rotary_dim, const RopeScaling& sc);
+    RoPE(double theta, int rotary_dim, RopeStyle style, const RopeScaling& sc);
     // inv_freq[i] = 1 / exp((2i / rotary_dim) * ln(theta)) in fp32 (rope.rs:39-42, 82-86, 309-317),
     // divided by `linear_factor` for rope_type "linear" (rope.rs:55-59).
     RoPE(double theta, int rotary_dim, RopeStyle style, double attn_factor = 1.0, double linear_factor = 1.0);
