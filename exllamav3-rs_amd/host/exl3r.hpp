@@ -13,7 +13,7 @@
 //   exl3r::RmsNorm::forward / forward_res                                <- src/modules.rs:342-412
 //   exl3r::Embedding::forward                                            <- src/modules.rs:418-437
 //   exl3r::GatedMlp::activate                                            <- src/modules.rs:932-940 (silu_mul step)
-//   exl3r::RoPE (default / linear inv_freq, apply, apply_one)            <- src/rope.rs:33-86, 233-292, 309-317
+//   exl3r::RoPE (params of every rope_type, apply, apply_one, apply_paged) <- src/rope.rs:33-220, 225-292, 309-317
 //
 // Error behaviour: the reference panics / throws (TORCH_CHECK) on invalid input; here every failure
 // throws exl3r::Error carrying the C ABI status and message.  Kernels are enqueued on the given
@@ -178,7 +178,10 @@ public:
     // y = norm(x) in f16 (every call site in the Qwen3 tree), same shape as x.
     OwnedTensor forward(const Tensor& x, const Stream& s) const;
     // Pre-norm residual add fused with the norm: r += add (in place), returns norm(r) in f16.
-    // add == nullptr: plain forward(r).
+    // add == nullptr: plain forward(r).  r may have any row stride (the fused path then still
+    // updates it in place); a residual whose leading dims do not collapse to one row stride is
+    // rejected, where the reference falls back to norm(r + add) and leaves r unchanged
+    // (src/modules.rs:393-395).
     OwnedTensor forward_res(const Tensor& r, const Tensor* add, const Stream& s) const;
     const Tensor& weight() const { return weight_; }
 
