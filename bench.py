@@ -34,7 +34,7 @@ OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "
        "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "rope_kv_prefill",
        "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
        "deinterleave_q35", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
-       "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "calib_copy",
+       "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "calib_copy",
        "calib_copy_cached"]
 
 
@@ -312,6 +312,22 @@ def make_gumbel(name, rows, use_torch, vocab=151936, seed=720):
     return Work(name, nbytes, launch, f"categorical draw over f16 logits [{rows},{vocab}] ({what})", sets)
 
 
+def make_had(name, rows, cols, seed=740):
+    """EXL3 prefill input rotation: had_r_128 of f16 [rows, cols] with an f16 suh pre-scale (the
+    projection input transform, src/modules.rs:227), out of place."""
+    import torch
+    import exl3r.ffi as ffi
+    nbytes = 2 * rows * cols * 2 + cols * 2
+    sets = sets_for(nbytes)
+    xs = [gen((rows, cols), 0.0, 1.0, torch.float16, seed + k) for k in range(sets)]
+    outs = [torch.empty((rows, cols), device="cuda", dtype=torch.float16) for _ in range(sets)]
+    suh = torch.where(torch.rand(cols, device="cuda") < 0.5, -1.0, 1.0).to(torch.float16)
+
+    def launch(i):
+        ffi.had_r_128(xs[i % sets], outs[i % sets], suh)
+    return Work(name, nbytes, launch, f"random-Hadamard row transform f16 [{rows},{cols}] with suh", sets)
+
+
 def make_copy(name, cached=False):
     import torch
     import exl3r
@@ -421,6 +437,7 @@ def make_all(only=None):
         "gumbel_dec": lambda: make_gumbel("gumbel_dec", 64, False),
         "gumbel_dec_torch": lambda: make_gumbel("gumbel_dec_torch", 64, True),
         "gumbel_prefill": lambda: make_gumbel("gumbel_prefill", 1024, False),
+        "had_c3": lambda: make_had("had_c3", 8192, 5120),
         "calib_copy": lambda: make_copy("calib_copy"),
         "calib_copy_cached": lambda: make_copy("calib_copy_cached", cached=True),
     }

@@ -93,4 +93,6 @@ extern "C" void exl3r_tune_sample(int rows_min, int threads)
     exl3r::tuning().sample_threads = threads;
 }
 
+extern "C" void exl3r_tune_had(int blocks_per_group) { exl3r::tuning().had_unroll = blocks_per_group; }
+
 extern "C" void exl3r_tune_embed(int threads) { exl3r::tuning().embed_threads = threads; }

@@ -44,6 +44,7 @@ struct Tuning
     int rope_wgs_per_cu = 0; // wave-per-token kernel: persistent grid of this many workgroups per CU (0: one token per wave)
     int sample_rows_min = 0; // argmax / Gumbel: rows from which a workgroup owns a row (0: 512)
     int sample_threads = 0;  // ... and its lanes (256, 512, 1024; 0: 256)
+    int had_unroll = 0;      // Hadamard: 128-blocks per 16-lane group (1, 2, 4; 0: 1)
     int embed_threads = 0;
 };
 Tuning& tuning();

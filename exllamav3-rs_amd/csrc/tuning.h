@@ -16,6 +16,8 @@ EXL3R_API void exl3r_tune_rope(int iters);
 EXL3R_API void exl3r_tune_rope_tok(int use, int hpl, int wgs_per_cu);
 /* argmax / Gumbel sampling: rows from which a workgroup owns a whole row (0: 512), and its lanes (256, 512, 1024) */
 EXL3R_API void exl3r_tune_sample(int rows_min, int threads);
+/* Hadamard: 128-blocks per 16-lane group (1, 2, 4; 0 auto) */
+EXL3R_API void exl3r_tune_had(int blocks_per_group);
 EXL3R_API void exl3r_tune_embed(int threads);
 #ifdef __cplusplus
 }

@@ -38,6 +38,7 @@ PROTOTYPES = {
     "exl3r_deinterleave_qg": (_i, [_vp, _i64, _vp, _i64, _vp, _i64, _i, _i64, _i, _i, _vp]),
     "exl3r_argmax_sample": (_i, [_vp, _i, _i64, _i64, _i64, _i, _vp, _vp]),
     "exl3r_gumbel_sample": (_i, [_vp, _i, _i64, _i64, _i64, _i, ctypes.c_uint32, _vp, _vp]),
+    "exl3r_had_r_128": (_i, [_vp, _i, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _f, _vp]),
     "exl3r_gumbel_noise": (_i, [_vp, _i, _i64, _vp, _i, _i64, _i64, _i64, ctypes.c_uint32, _vp]),
     "exl3r_rope_paged_kv": (_i, [_vp, _vp, _i64, _i64, _i, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i, _i, _i64, _i64,
                                  _i, _vp, _i, _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _vp, _vp, _i, _i64,
@@ -51,6 +52,7 @@ PROTOTYPES = {
     "exl3r_tune_rms_rows": (None, [_i]),
     "exl3r_tune_rope_tok": (None, [_i, _i, _i]),
     "exl3r_tune_sample": (None, [_i, _i]),
+    "exl3r_tune_had": (None, [_i]),
     "exl3r_tune_embed": (None, [_i]),
 }
 

@@ -273,6 +273,20 @@ def gumbel_noise(x, out, random=0, stream=None):
                                     int(random) & 0xFFFFFFFF, _stream(x, stream)))
 
 
+def had_r_128(x, out, pre_scale=None, post_scale=None, scale=1.0, stream=None):
+    """Random-Hadamard transform of [rows, k] f16 / f32 x into out (k % 128 == 0), with an optional f16
+    per-column pre_scale (before) or post_scale (after) (src/ffi.rs:604-608)."""
+    rows, cols, ldx = _rows(x)
+    ro, co, ldo = _rows(out)
+    if (ro, co) != (rows, cols) or out.dtype != x.dtype:
+        raise ValueError("x and out must share shape and dtype")
+    for t in (pre_scale, post_scale):
+        if t is not None and (t.dtype != torch.float16 or t.numel() != cols or not t.is_contiguous()):
+            raise ValueError("scales must be contiguous f16 with one entry per column")
+    check(load().exl3r_had_r_128(_ptr(x), dtype_code(x), ldx, _ptr(out), ldo, rows, cols, _ptr(pre_scale),
+                                 _ptr(post_scale), float(scale), _stream(x, stream)))
+
+
 def embedding(table, ids, out, err_flag=None, stream=None):
     """out[i] = table[ids[i]] (bit-exact, or exact upcast to f32)."""
     vocab, hidden = table.shape

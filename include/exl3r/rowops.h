@@ -38,6 +38,8 @@
  *                              generator's batched tch argmax over [bsz, vocab] logits  src/generator.rs:1596
  *   exl3r_gumbel_sample     <- exl3_shim_gumbel_sample    csrc/exl3_shim.cpp:232-234 (ffi.rs:137, 526-530)
  *   exl3r_gumbel_noise      <- exl3_shim_gumbel_noise_f32 csrc/exl3_shim.cpp:235-237 (ffi.rs:138, 531-535)
+ *   exl3r_had_r_128         <- exl3_shim_had_r_128        csrc/exl3_shim.cpp:158-160 (ffi.rs:162-164, 604-608;
+ *                              call sites modules.rs:224-231)
  *   exl3r_embedding         <- Embedding::forward's tch index_select + to_kind   src/modules.rs:430-436
  *   exl3r_embedding_rms_norm<- embed followed by RmsNorm::forward (MTP head)    src/mtp.rs:189-190
  */
@@ -277,6 +279,20 @@ EXL3R_API int exl3r_gumbel_sample(const void* logits, int dtype, int64_t rows, i
  */
 EXL3R_API int exl3r_gumbel_noise(const void* x, int x_dtype, int64_t ldx, void* out, int out_dtype, int64_t ldo,
                        int64_t rows, int64_t cols, uint32_t random, void* stream);
+
+/*
+ * Random-Hadamard row transform: every 128-element block of each row of x [rows, cols]
+ * (cols % 128 == 0, row strides ldx / ldo elements) becomes r * H128 (x o pre_scale) o post_scale,
+ * H128 the Sylvester Hadamard matrix, r = scale / sqrt(128) in fp32; out may equal x.  dtype F16 or
+ * F32 (x and out alike); pre_scale / post_scale are f16 [cols] (EXL3's suh / svh) or NULL, and at most
+ * one of them is given (the reference silently drops post_scale when both are).  Rounding follows
+ * kernels/quant/hadamard_inner.cuh:96-200: an f16 pre-scale product is a half multiply, the transform
+ * is an fp32 butterfly over index bits 0..6 in order, the result times r is rounded once, an f16
+ * post-scale is a half multiply.  Replaces exl3_shim_had_r_128 (csrc/exl3_shim.cpp:158-160 ->
+ * had_r_128, kernels/quant/hadamard.cu:88-170).
+ */
+EXL3R_API int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out, int64_t ldo, int64_t rows,
+                    int64_t cols, const void* pre_scale, const void* post_scale, float scale, void* stream);
 
 /*
  * Token-embedding gather: out[i, :] = table[ids[i], :], bit-exact (same dtype) or exactly upcast to

@@ -35,6 +35,7 @@ _PROTOS = {
     "oracle_deinterleave_qg": (_i, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i, _i, _i]),
     "oracle_argmax": (_i, [_vp, _i, _i64, _i64, _i64, _i, _vp, _i]),
     "oracle_philox4x32_10": (None, [_vp, _vp, _vp]),
+    "oracle_had_r_128": (_i, [_vp, _i, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _f, _i]),
     "oracle_log_f32": (ctypes.c_float, [_f]),
     "oracle_gumbel_of_bits": (None, [_vp, _vp, _i64]),
     "oracle_gumbel_noise": (_i, [_vp, _i, _i64, _vp, _i, _i64, _i64, _i64, ctypes.c_uint32, _i]),
@@ -154,6 +155,17 @@ def argmax(logits, dt, max_logit=0, nthreads=1):
     ids = np.zeros(rows, np.int64)
     _check(load().oracle_argmax(_p(logits), dt, rows, vocab, vocab, max_logit, _p(ids), nthreads), "oracle_argmax")
     return ids
+
+
+def had_r_128(x, dt, pre=None, post=None, scale=1.0, nthreads=1):
+    """x: [rows, cols] storage (f16 bits or f32).  Returns the random-Hadamard transform (same dtype)."""
+    rows, cols = x.shape
+    out = np.zeros_like(x)
+    pre = None if pre is None else np.ascontiguousarray(pre, np.uint16)
+    post = None if post is None else np.ascontiguousarray(post, np.uint16)
+    _check(load().oracle_had_r_128(_p(np.ascontiguousarray(x)), dt, cols, _p(out), cols, rows, cols, _p(pre), _p(post),
+                                   scale, nthreads), "oracle_had_r_128")
+    return out
 
 
 def philox4x32_10(ctr, key):

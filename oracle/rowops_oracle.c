@@ -505,6 +505,56 @@ int oracle_argmax(const void* logits, int dt, int64_t rows, int64_t vocab, int64
     return 0;
 }
 
+/* kernels/quant/hadamard.cu:88-170, hadamard_inner.cuh:96-200 */
+int oracle_had_r_128(const void* x, int dt, int64_t ldx, void* out, int64_t ldo, int64_t rows, int64_t cols,
+                     const uint16_t* pre, const uint16_t* post, float scale, int nthreads)
+{
+    if (!x || !out || rows < 0 || cols < 0 || cols % 128 || ldx < cols || ldo < cols || (pre && post)) return -1;
+    if (dt != OR_F16 && dt != OR_F32) return -2;
+    const float r = scale * 0.0883883461356163f;        /* fl32(1/sqrt(128)) */
+    #pragma omp parallel for num_threads(nthr(nthreads)) schedule(static)
+    for (int64_t i = 0; i < rows; ++i)
+    {
+        float v[128];
+        for (int64_t b0 = 0; b0 < cols; b0 += 128)
+        {
+            for (int k = 0; k < 128; ++k)
+            {
+                float e = ld(x, dt, i * ldx + b0 + k);
+                if (pre)
+                {
+                    const float p = oracle_f16_to_f32(pre[b0 + k]);
+                    if (dt == OR_F16 && oracle_mutation != ORM_HAD_NO_PRE_ROUND)
+                        e = oracle_f16_to_f32(oracle_f32_to_f16(e * p));    /* __hmul2: one half rounding */
+                    else
+                        e = e * p;
+                }
+                v[k] = e;
+            }
+            for (int h = 1; h < 128; h <<= 1)
+                for (int k = 0; k < 128; ++k)
+                    if (!(k & h))
+                    {
+                        const float a = v[k], c = v[k | h];
+                        v[k] = a + c;
+                        v[k | h] = (oracle_mutation == ORM_HAD_SIGN && h == 64) ? c - a : a - c;
+                    }
+            for (int k = 0; k < 128; ++k)
+            {
+                float e = v[k] * r;
+                if (dt == OR_F16) e = oracle_f16_to_f32(oracle_f32_to_f16(e));
+                if (post)
+                {
+                    const float p = oracle_f16_to_f32(post[b0 + k]);
+                    e = dt == OR_F16 ? oracle_f16_to_f32(oracle_f32_to_f16(e * p)) : e * p;
+                }
+                st(out, dt, i * ldo + b0 + k, e);
+            }
+        }
+    }
+    return 0;
+}
+
 /* Philox4x32-10 (Salmon et al., SC 2011): ten rounds of two 32x32->64 multiplies with the published
  * multipliers and Weyl key increments. */
 void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4])

@@ -66,6 +66,8 @@ extern int oracle_mutation;
 #define ORM_LOG_NO_LN2LO     24  /* log drops the low part of e * ln2 */
 #define ORM_GUMBEL_NO_ROW    25  /* Gumbel noise ignores the row (every row draws the same noise) */
 #define ORM_TABLE_ROW_OFF    26  /* angle table read one row past the position */
+#define ORM_HAD_NO_PRE_ROUND 27  /* f16 pre-scale product kept in fp32 instead of rounded to half */
+#define ORM_HAD_SIGN         28  /* butterfly stage 6 computes b - a instead of a - b */
 
 /* Conversions (round to nearest even; NaN -> canonical quiet NaN). */
 uint16_t oracle_f32_to_f16(float f);
@@ -141,6 +143,19 @@ int oracle_deinterleave_qg(const void* qg, int64_t ldqg, void* q, int64_t ldq, v
  */
 int oracle_argmax(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld, int max_logit,
                   int64_t* ids, int nthreads);
+
+/*
+ * Random-Hadamard row transform had_r_128 (kernels/quant/hadamard.cu:88-170, inner
+ * hadamard_inner.cuh:96-200): every 128-element block of each row of x [rows, cols] (cols % 128 == 0)
+ * becomes y = r * H128 (x o pre) o post, H128 the Sylvester Hadamard matrix, r = fl32(scale *
+ * fl32(1/sqrt(128))).  F16: the pre-scale product is a half multiply (rounded to half), the transform
+ * runs in fp32 as the in-place butterfly with stages over index bits 0..6 in that order, each pair
+ * (a, b) -> (a + b, a - b); the result times r is rounded to half once, then the post-scale half
+ * multiply.  F32: the same with fp32 scale products.  pre and post are f16 [cols] or NULL; at most
+ * one is given.  out may be x.
+ */
+int oracle_had_r_128(const void* x, int dt, int64_t ldx, void* out, int64_t ldo, int64_t rows, int64_t cols,
+                     const uint16_t* pre, const uint16_t* post, float scale, int nthreads);
 
 /*
  * Gumbel-max sampling (the role of exl3_shim_gumbel_sample / exl3_shim_gumbel_noise_f32,
