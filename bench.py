@@ -34,7 +34,7 @@ OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "
        "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "rope_kv_prefill",
        "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
        "deinterleave_q35", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
-       "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "calib_copy",
+       "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "calib_copy",
        "calib_copy_cached"]
 
 
@@ -328,6 +328,35 @@ def make_had(name, rows, cols, seed=740):
     return Work(name, nbytes, launch, f"random-Hadamard row transform f16 [{rows},{cols}] with suh", sets)
 
 
+def make_norm_had(name, rows, cols, fused, seed=760):
+    """Qwen3-32B prefill attention input: r += x (f16 sublayer output into the f32 residual), the f16
+    RMSNorm, and the q / k / v projections' input rotations had_r_128(y, suh_i)
+    (src/modules.rs:224-227, 372-411): one fused launch, or the residual norm and three had_r_128
+    launches.  Both count the fused job's bytes (x, r read and written, three outputs, w, suh)."""
+    import torch
+    import exl3r.ffi as ffi
+    n = rows * cols
+    nbytes = n * (2 + 4 + 4 + 3 * 2) + 4 * cols * 2
+    sets = sets_for(nbytes)
+    bufs = [(gen((rows, cols), 0.0, 1.0, torch.float16, seed + 2 * k),
+             gen((rows, cols), 0.0, 4.0, torch.float32, seed + 2 * k + 1),
+             [torch.empty((rows, cols), device="cuda", dtype=torch.float16) for _ in range(3)]) for k in range(sets)]
+    w = gen((cols,), 1.0, 0.1, torch.float16, seed + 99)
+    suh = [torch.where(torch.rand(cols, device="cuda") < 0.5, -1.0, 1.0).to(torch.float16) for _ in range(3)]
+    y = torch.empty((rows, cols), device="cuda", dtype=torch.float16)
+
+    def launch(i):
+        x, r, outs = bufs[i % sets]
+        if fused:
+            ffi.rms_norm_had(x, w, outs, suh, 1e-6, r=r)
+        else:
+            ffi.rms_norm_res_in(x, w, y, r, 1e-6)
+            for o, p in zip(outs, suh):
+                ffi.had_r_128(y, o, p)
+    kind = "fused" if fused else "unfused (residual RMSNorm + 3 had_r_128)"
+    return Work(name, nbytes, launch, f"residual RMSNorm -> 3 Hadamard inputs [{rows},{cols}] f16/f32r, {kind}", sets)
+
+
 def make_copy(name, cached=False):
     import torch
     import exl3r
@@ -438,6 +467,8 @@ def make_all(only=None):
         "gumbel_dec_torch": lambda: make_gumbel("gumbel_dec_torch", 64, True),
         "gumbel_prefill": lambda: make_gumbel("gumbel_prefill", 1024, False),
         "had_c3": lambda: make_had("had_c3", 8192, 5120),
+        "norm_had_c3": lambda: make_norm_had("norm_had_c3", 8192, 5120, True),
+        "norm_had_c3_unfused": lambda: make_norm_had("norm_had_c3_unfused", 8192, 5120, False),
         "calib_copy": lambda: make_copy("calib_copy"),
         "calib_copy_cached": lambda: make_copy("calib_copy_cached", cached=True),
     }

@@ -1,0 +1,65 @@
+// 128-point Sylvester Hadamard butterfly over a 16-lane group (8 elements per lane), shared by the
+// Hadamard row transform (hadamard.hip) and the RMSNorm kernels that feed it (rms_norm_kernel.cuh).
+// Element 8 * l + j of a block sits in lane l, slot j: index bits 0..2 are in-lane stages, bits 3..6
+// lane exchanges at xor 1, 2, 4, 8, taken in that order, each pair (a, b) -> (a + b, a - b) with a the
+// lower index, in fp32 -- the order of the reference's warp butterfly (kernels/quant/
+// hadamard_inner.cuh:19-46, 127-141), so every caller rounds identically.
+#pragma once
+
+#include "common.cuh"
+
+namespace exl3r {
+
+// The value of lane (l ^ M) inside the 16-lane group.
+template <int M>
+__device__ __forceinline__ float lane_xor(float v)
+{
+    const int i = __builtin_bit_cast(int, v);
+    if constexpr (M == 1) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, i, DPP_QUAD_XOR1, 0xf, 0xf, false));
+    else if constexpr (M == 2) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, i, DPP_QUAD_XOR2, 0xf, 0xf, false));
+    else if constexpr (M == 4) return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(i, 0x101f));
+    else return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(i, 0x201f));
+}
+
+// One cross-lane butterfly stage: the lane whose bit M is clear holds a and keeps a + b, its partner
+// holds b and keeps a - b.
+template <int M>
+__device__ __forceinline__ void lane_stage(float (&f)[8], int l16)
+{
+    #pragma clang fp contract(off)
+    const bool upper = (l16 & M) != 0;
+    #pragma unroll
+    for (int j = 0; j < 8; ++j)
+    {
+        const float p = lane_xor<M>(f[j]);
+        f[j] = upper ? p - f[j] : f[j] + p;
+    }
+}
+
+__device__ __forceinline__ void butterfly128(float (&f)[8], int l16)
+{
+    #pragma clang fp contract(off)
+    #pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+    {
+        #pragma unroll
+        for (int j = 0; j < 8; ++j)
+        {
+            if (j & h) continue;
+            const float a = f[j], b = f[j | h];
+            f[j] = a + b;
+            f[j | h] = a - b;
+        }
+    }
+    lane_stage<1>(f, l16);
+    lane_stage<2>(f, l16);
+    lane_stage<4>(f, l16);
+    lane_stage<8>(f, l16);
+}
+
+__device__ __forceinline__ uint32_t hmul2(uint32_t a, uint32_t b)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, a) * __builtin_bit_cast(f16x2, b));
+}
+
+}  // namespace exl3r

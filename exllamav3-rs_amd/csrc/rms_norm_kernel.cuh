@@ -16,6 +16,7 @@
 
 #include "abi.hpp"
 #include "common.cuh"
+#include "hadamard.cuh"
 
 #include <type_traits>
 
@@ -44,6 +45,13 @@ struct RmsArgs
     int gact;           // RMS_GATED: 0 silu, 1 sigmoid
     int gfirst;         // RMS_GATED: gate applied before the norm
     int w_groups;       // RMS_GATED: the weight holds w_groups rows of dim, row r uses r % w_groups
+    // Hadamard outputs (HAD kernels, exl3r_rms_norm_had): output i = had_r_128 of the f16 norm
+    // output with pre-scale hpre[i] (f16 [dim] or nullptr), rows at stride ldh, hr = scale / sqrt(128).
+    int nh;
+    const void* hpre[4];
+    void* hout[4];
+    int64_t ldh;
+    float hr;
 };
 
 // RMS_GATED gate activation in fp32.
@@ -202,8 +210,8 @@ __device__ __forceinline__ typename RmsCache<XT, RT, MODE>::Vec rms_chunk1(const
 
 // Pass 2 of the chunk at element e: gate (GATED), weight (row offset wofs), scale, gate after the
 // norm (GATED), one rounding, store.
-template <class XT, class YT, class RT, int MODE>
-__device__ __forceinline__ void rms_chunk2(const RmsArgs& a, char* yrow, int64_t e, int64_t wofs,
+template <class XT, class YT, class RT, int MODE, bool HAD>
+__device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* yrow, int64_t e, int64_t wofs,
                                            const typename RmsCache<XT, RT, MODE>::Vec& cv,
                                            const typename RT::Vec& rv, u32x4 wv, float rmf)
 {
@@ -252,10 +260,37 @@ __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, char* yrow, int64_t
             for (int j = 0; j < 8; ++j) o[j] = o[j] * ga[j];
         }
     }
-    store8<YT>(yrow, e, pack8<YT>(o));
+    const typename YT::Vec yv = pack8<YT>(o);
+    if constexpr (!HAD) store8<YT>(yrow, e, yv);
+    else
+    {
+        #pragma clang fp contract(off)
+        // The f16 norm output, then each consumer's had_r_128 with its pre-scale.  The chunk's
+        // 16-lane group is the block's (lane counts are multiples of 16 and dim % 128 == 0), and
+        // l16 is both the lane's place in that group and the chunk's place in the block.
+        static_assert(YT::code == DT_F16, "the Hadamard prologue follows an f16 norm output");
+        if (a.y) store8<YT>(yrow, e, yv);
+        const int l16 = (int)((e >> 3) & 15);
+        for (int i = 0; i < a.nh; ++i)
+        {
+            TF16::Vec v = yv;
+            if (a.hpre[i])
+            {
+                const TF16::Vec p = load8<TF16>(a.hpre[i], e);
+                #pragma unroll
+                for (int q = 0; q < 4; ++q) v.a[q] = hmul2(v.a[q], p.a[q]);
+            }
+            float f[8];
+            unpack8<TF16>(v, f);
+            butterfly128(f, l16);
+            #pragma unroll
+            for (int j = 0; j < 8; ++j) f[j] = f[j] * a.hr;
+            store8<TF16>((char*)a.hout[i] + row * a.ldh * 2, e, pack8<TF16>(f));
+        }
+    }
 }
 
-template <class XT, class YT, class RT, int MAXV, int MODE>
+template <class XT, class YT, class RT, int MAXV, int MODE, bool HAD = false>
 __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int tid, int nt, RowRegs<XT, RT, MAXV>& L,
                                            double* red)
 {
@@ -284,24 +319,24 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
     for (int k = 0; k < MAXV; ++k)
     {
         const int c = tid + k * nt;
-        if (c < nc) rms_chunk2<XT, YT, RT, MODE>(a, yrow, (int64_t)c * 8, wofs, cache[k], L.rv[k], L.wv[k], rmf);
+        if (c < nc) rms_chunk2<XT, YT, RT, MODE, HAD>(a, row, yrow, (int64_t)c * 8, wofs, cache[k], L.rv[k], L.wv[k], rmf);
     }
 }
 
-template <class XT, class YT, class RT, int MAXV, int MODE>
+template <class XT, class YT, class RT, int MAXV, int MODE, bool HAD = false>
 __device__ __forceinline__ void rms_row(const RmsArgs& a, int64_t row, int tid, int nt, double* red)
 {
     RowRegs<XT, RT, MAXV> L;
     rms_load<XT, RT, MAXV, MODE>(a, row, tid, nt, true, L);
-    rms_finish<XT, YT, RT, MAXV, MODE>(a, row, tid, nt, L, red);
+    rms_finish<XT, YT, RT, MAXV, MODE, HAD>(a, row, tid, nt, L, red);
 }
 
-template <class XT, class YT, class RT, int MAXV, int MODE>
+template <class XT, class YT, class RT, int MAXV, int MODE, bool HAD = false>
 __global__ __launch_bounds__(1024) void k_rms_norm(RmsArgs a)
 {
     __shared__ double red[16];
     for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x)
-        rms_row<XT, YT, RT, MAXV, MODE>(a, row, threadIdx.x, blockDim.x, red);
+        rms_row<XT, YT, RT, MAXV, MODE, HAD>(a, row, threadIdx.x, blockDim.x, red);
 }
 
 // Short rows (at most 64 chunks of 8): LPR lanes per row (a power of two covering dim / 8), one
@@ -346,8 +381,8 @@ __global__ __launch_bounds__(256) void k_rms_rows(RmsArgs a)
             ss = group_sum64<LPR>(ss);
             const float rmf = rms_factor(ss, a.dim, a.eps) * a.cs;
             if (act[i])
-                rms_chunk2<XT, YT, RT, MODE>(a, (char*)a.y + row * a.ldy * YT::bytes, e, weight_row<MODE>(a, row), cv,
-                                             rv[i], wv[i], rmf);
+                rms_chunk2<XT, YT, RT, MODE, false>(a, row, (char*)a.y + row * a.ldy * YT::bytes, e,
+                                                    weight_row<MODE>(a, row), cv, rv[i], wv[i], rmf);
         }
     }
 }
@@ -472,7 +507,7 @@ inline RmsShape rms_shape(int nc, int64_t rows)
     return { 8, thr(8) };   // <= 1024 (rms_vec_ok bounds the row at 8192 chunks)
 }
 
-template <class XT, class YT, class RT, int MODE>
+template <class XT, class YT, class RT, int MODE, bool HAD = false>
 int launch_rms_vec(const RmsArgs& a, hipStream_t s)
 {
     const RmsShape sh = rms_shape(a.dim / 8, a.rows);
@@ -488,12 +523,12 @@ int launch_rms_vec(const RmsArgs& a, hipStream_t s)
     }
     switch (sh.maxv)
     {
-        case 1: k_rms_norm<XT, YT, RT, 1, MODE><<<grid, sh.threads, 0, s>>>(a); break;
-        case 2: k_rms_norm<XT, YT, RT, 2, MODE><<<grid, sh.threads, 0, s>>>(a); break;
-        case 3: k_rms_norm<XT, YT, RT, 3, MODE><<<grid, sh.threads, 0, s>>>(a); break;
-        case 4: k_rms_norm<XT, YT, RT, 4, MODE><<<grid, sh.threads, 0, s>>>(a); break;
-        case 5: k_rms_norm<XT, YT, RT, 5, MODE><<<grid, sh.threads, 0, s>>>(a); break;
-        default: k_rms_norm<XT, YT, RT, 8, MODE><<<grid, sh.threads, 0, s>>>(a); break;
+        case 1: k_rms_norm<XT, YT, RT, 1, MODE, HAD><<<grid, sh.threads, 0, s>>>(a); break;
+        case 2: k_rms_norm<XT, YT, RT, 2, MODE, HAD><<<grid, sh.threads, 0, s>>>(a); break;
+        case 3: k_rms_norm<XT, YT, RT, 3, MODE, HAD><<<grid, sh.threads, 0, s>>>(a); break;
+        case 4: k_rms_norm<XT, YT, RT, 4, MODE, HAD><<<grid, sh.threads, 0, s>>>(a); break;
+        case 5: k_rms_norm<XT, YT, RT, 5, MODE, HAD><<<grid, sh.threads, 0, s>>>(a); break;
+        default: k_rms_norm<XT, YT, RT, 8, MODE, HAD><<<grid, sh.threads, 0, s>>>(a); break;
     }
     return 0;
 }

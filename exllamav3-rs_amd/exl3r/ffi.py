@@ -6,6 +6,7 @@ index_select (src/modules.rs:430-436).
 Tensors must live on the GPU; every wrapper launches on the current torch stream (the reference's
 kernels use the current torch stream too, kernels/norm.cu:328) unless `stream` is given, and raises
 Exl3rError on a non-zero status (the reference's TORCH_CHECK raises)."""
+import ctypes
 import math
 
 import torch
@@ -285,6 +286,32 @@ def had_r_128(x, out, pre_scale=None, post_scale=None, scale=1.0, stream=None):
             raise ValueError("scales must be contiguous f16 with one entry per column")
     check(load().exl3r_had_r_128(_ptr(x), dtype_code(x), ldx, _ptr(out), ldo, rows, cols, _ptr(pre_scale),
                                  _ptr(post_scale), float(scale), _stream(x, stream)))
+
+
+def rms_norm_had(x, w, outs, pre_scales, eps, constant_bias=0.0, constant_scale=1.0, r=None, y=None, had_scale=1.0,
+                 stream=None):
+    """One pass: y = RMSNorm(x) (or r += x; y = RMSNorm(r)) in f16, then outs[i] = had_r_128(y, pre_scales[i])
+    for each projection (1..4 f16 outputs shaped like x; y is written only if given)."""
+    rows, dim, ldx = _rows(x)
+    if not 1 <= len(outs) <= 4 or len(pre_scales) != len(outs):
+        raise ValueError("1..4 outputs, one pre_scale (or None) each")
+    ldo = None
+    for o in outs:
+        ro, co, lo = _rows(o)
+        if (ro, co) != (rows, dim) or o.dtype != torch.float16 or (ldo is not None and lo != ldo):
+            raise ValueError("outputs must be f16 shaped like x with one row stride")
+        ldo = lo
+    ldr = _rows(r)[2] if r is not None else 0
+    ldy = _rows(y)[2] if y is not None else 0
+    if y is not None and y.dtype != torch.float16:
+        raise ValueError("y is the f16 norm output")
+    arr = ctypes.c_void_p * len(outs)
+    pre = arr(*[_ptr(p) for p in pre_scales])
+    out = arr(*[_ptr(o) for o in outs])
+    check(load().exl3r_rms_norm_had(_ptr(x), dtype_code(x), ldx, _ptr(w), dtype_code(w) if w is not None else F16,
+                                    _ptr(r), dtype_code(r) if r is not None else F16, ldr, _ptr(y), ldy, len(outs),
+                                    pre, out, ldo, rows, dim, eps, constant_bias, constant_scale, float(had_scale),
+                                    _stream(x, stream)))
 
 
 def embedding(table, ids, out, err_flag=None, stream=None):

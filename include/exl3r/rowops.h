@@ -40,6 +40,8 @@
  *   exl3r_gumbel_noise      <- exl3_shim_gumbel_noise_f32 csrc/exl3_shim.cpp:235-237 (ffi.rs:138, 531-535)
  *   exl3r_had_r_128         <- exl3_shim_had_r_128        csrc/exl3_shim.cpp:158-160 (ffi.rs:162-164, 604-608;
  *                              call sites modules.rs:224-231)
+ *   exl3r_rms_norm_had      <- RmsNorm::forward / forward_res followed by each projection's had_r_128
+ *                              input rotation  src/modules.rs:372-411, 224-227
  *   exl3r_embedding         <- Embedding::forward's tch index_select + to_kind   src/modules.rs:430-436
  *   exl3r_embedding_rms_norm<- embed followed by RmsNorm::forward (MTP head)    src/mtp.rs:189-190
  */
@@ -293,6 +295,23 @@ EXL3R_API int exl3r_gumbel_noise(const void* x, int x_dtype, int64_t ldx, void* 
  */
 EXL3R_API int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out, int64_t ldo, int64_t rows,
                     int64_t cols, const void* pre_scale, const void* post_scale, float scale, void* stream);
+
+/*
+ * RMSNorm whose f16 output feeds the random-Hadamard input rotation of 1..4 EXL3 projections, in one
+ * pass (the prefill path of RmsNorm::forward / forward_res, src/modules.rs:372-411, then
+ * had_r_128(y, suh) per projection, src/modules.rs:224-227):
+ *   r == NULL: y = RMSNorm(x) as exl3r_rms_norm; else r += x in place and y = RMSNorm(r) as
+ *              exl3r_rms_norm_res_in; y is f16 and written only when y != NULL (row stride ldy);
+ *   outs[i] = had_r_128(y, pre_scales[i]) with scale had_scale, f16 [rows, dim] at row stride ldo;
+ *              pre_scales[i] is f16 [dim] (the projection's suh) or NULL.
+ * dim % 128 == 0; n_out in 1..4; outputs alias nothing.  Results are bit-identical to the unfused
+ * calls.  Rows that are not 16-byte aligned run the unfused calls (the norm goes to y, or to outs[0]).
+ */
+EXL3R_API int exl3r_rms_norm_had(const void* x, int x_dtype, int64_t ldx, const void* w, int w_dtype,
+                       void* r, int r_dtype, int64_t ldr, void* y, int64_t ldy,
+                       int n_out, const void* const* pre_scales, void* const* outs, int64_t ldo,
+                       int64_t rows, int64_t dim, float eps, float constant_bias, float constant_scale,
+                       float had_scale, void* stream);
 
 /*
  * Token-embedding gather: out[i, :] = table[ids[i], :], bit-exact (same dtype) or exactly upcast to
