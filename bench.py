@@ -34,7 +34,8 @@ OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "
        "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "rope_kv_prefill",
        "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
        "deinterleave_q35", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
-       "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "calib_copy",
+       "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "silu_had_c3",
+       "silu_had_c3_unfused", "calib_copy",
        "calib_copy_cached"]
 
 
@@ -357,6 +358,30 @@ def make_norm_had(name, rows, cols, fused, seed=760):
     return Work(name, nbytes, launch, f"residual RMSNorm -> 3 Hadamard inputs [{rows},{cols}] f16/f32r, {kind}", sets)
 
 
+def make_act_had(name, rows, cols, fused, seed=780):
+    """MLP prefill tail: silu(gate) * up in f16 and the down projection's input rotation
+    had_r_128(a, suh) (src/modules.rs:932-940, 224-227): one fused launch, or exl3r_silu_mul and
+    exl3r_had_r_128.  Both count the fused job's bytes (gate, up, the rotated output, suh)."""
+    import torch
+    import exl3r.ffi as ffi
+    nbytes = rows * cols * 6 + cols * 2
+    sets = sets_for(nbytes)
+    bufs = [(gen((rows, cols), 0.0, 1.0, torch.float16, seed + 2 * k), gen((rows, cols), 0.0, 1.0, torch.float16, seed + 2 * k + 1),
+             torch.empty((rows, cols), device="cuda", dtype=torch.float16)) for k in range(sets)]
+    suh = torch.where(torch.rand(cols, device="cuda") < 0.5, -1.0, 1.0).to(torch.float16)
+    a = torch.empty((rows, cols), device="cuda", dtype=torch.float16)
+
+    def launch(i):
+        g, u, out = bufs[i % sets]
+        if fused:
+            ffi.act_mul_had("silu", g, u, out, suh)
+        else:
+            ffi.silu_mul(g, u, a)
+            ffi.had_r_128(a, out, suh)
+    kind = "fused" if fused else "unfused (silu_mul + had_r_128)"
+    return Work(name, nbytes, launch, f"SiLU(gate)*up -> Hadamard input [{rows},{cols}] f16, {kind}", sets)
+
+
 def make_copy(name, cached=False):
     import torch
     import exl3r
@@ -469,6 +494,8 @@ def make_all(only=None):
         "had_c3": lambda: make_had("had_c3", 8192, 5120),
         "norm_had_c3": lambda: make_norm_had("norm_had_c3", 8192, 5120, True),
         "norm_had_c3_unfused": lambda: make_norm_had("norm_had_c3_unfused", 8192, 5120, False),
+        "silu_had_c3": lambda: make_act_had("silu_had_c3", 8192, 17408, True),
+        "silu_had_c3_unfused": lambda: make_act_had("silu_had_c3_unfused", 8192, 17408, False),
         "calib_copy": lambda: make_copy("calib_copy"),
         "calib_copy_cached": lambda: make_copy("calib_copy_cached", cached=True),
     }

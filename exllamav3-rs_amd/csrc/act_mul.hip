@@ -12,8 +12,14 @@
 // Streaming layout: 8-element chunks (16 bytes per 16-bit tensor) per lane, UNROLL chunks in flight
 // per thread, strided by blockDim so each wave-wide access is 1 KiB contiguous.  Contiguous
 // operands are flattened to one row; strided rows use gridDim.y over rows.
+//
+// exl3r_act_mul_had feeds the f16 activation straight into the next EXL3 linear's input rotation
+// (GatedMlp::forward -> Linear::forward, src/modules.rs:932-940, 224-227): 16 consecutive lanes
+// hold the 16 chunks of one 128-element block, so the block's butterfly runs in registers
+// (hadamard.cuh) and the activation never returns to memory.
 #include "abi.hpp"
 #include "common.cuh"
+#include "hadamard.cuh"
 
 namespace exl3r {
 
@@ -26,6 +32,12 @@ struct ActArgs
     int64_t rows;
     int64_t cols;            // elements per row
     float limit;
+    // HAD kernels: out = had_r_128(z, hpre) at row stride ldh (f16), hr = scale / sqrt(128); z
+    // (the f16 activation) is stored only when non-null.
+    const void* hpre;
+    void* hout;
+    int64_t ldh;
+    float hr;
 };
 
 template <int ACT, bool LIMIT>
@@ -53,7 +65,7 @@ __device__ __forceinline__ void act_chunk(const float (&g)[8], const float (&u)[
     }
 }
 
-template <int ACT, class IT, class OT, int UNROLL, bool LIMIT>
+template <int ACT, class IT, class OT, int UNROLL, bool LIMIT, bool HAD = false>
 __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
 {
     const int64_t cpr = a.cols >> 3;   // chunks per row
@@ -87,7 +99,25 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
                     unpack8<IT>(xv[u], g);
                     unpack8<IT>(yv[u], v);
                     act_chunk<ACT, OT, LIMIT>(g, v, a.limit, o);
-                    store8<OT>(zr, c * 8, pack8<OT>(o));
+                    if constexpr (!HAD) store8<OT>(zr, c * 8, pack8<OT>(o));
+                    else
+                    {
+                        // The group of 16 lanes holding chunks c & ~15 .. c | 15 is the block's (the
+                        // row length is a multiple of 128 and nt * UNROLL of 16), all active together.
+                        static_assert(OT::code == DT_F16, "the Hadamard prologue follows an f16 activation");
+                        TF16::Vec hv = pack8<TF16>(o);
+                        if (a.z) store8<TF16>(zr, c * 8, hv);
+                        if (a.hpre)
+                        {
+                            const TF16::Vec p = load8<TF16>(a.hpre, c * 8);
+                            #pragma unroll
+                            for (int q = 0; q < 4; ++q) hv.a[q] = hmul2(hv.a[q], p.a[q]);
+                        }
+                        float f[8];
+                        unpack8<TF16>(hv, f);
+                        butterfly128(f, (int)(c & 15), a.hr);
+                        store8<TF16>((char*)a.hout + row * a.ldh * 2, c * 8, pack8<TF16>(f));
+                    }
                 }
             }
         }
@@ -110,7 +140,7 @@ __global__ __launch_bounds__(256) void k_act_mul_generic(ActArgs a, int it, int 
     }
 }
 
-template <int ACT, class IT, class OT>
+template <int ACT, class IT, class OT, bool HAD = false>
 static void launch_act_vec(const ActArgs& a, hipStream_t s)
 {
     const Tuning& tu = tuning();
@@ -128,17 +158,59 @@ static void launch_act_vec(const ActArgs& a, hipStream_t s)
     if (bx > kMaxGridX) bx = kMaxGridX;
     const dim3 grid((unsigned)bx, (unsigned)(a.rows < 65535 ? a.rows : 65535));
     if (a.limit != 0.0f)
-        k_act_mul<ACT, IT, OT, 2, true><<<grid, threads, 0, s>>>(a);
+        k_act_mul<ACT, IT, OT, 2, true, HAD><<<grid, threads, 0, s>>>(a);
     else
     {
         switch (unroll)
         {
-            case 1: k_act_mul<ACT, IT, OT, 1, false><<<grid, threads, 0, s>>>(a); break;
-            case 2: k_act_mul<ACT, IT, OT, 2, false><<<grid, threads, 0, s>>>(a); break;
-            case 8: k_act_mul<ACT, IT, OT, 8, false><<<grid, threads, 0, s>>>(a); break;
-            default: k_act_mul<ACT, IT, OT, 4, false><<<grid, threads, 0, s>>>(a); break;
+            case 1: k_act_mul<ACT, IT, OT, 1, false, HAD><<<grid, threads, 0, s>>>(a); break;
+            case 2: k_act_mul<ACT, IT, OT, 2, false, HAD><<<grid, threads, 0, s>>>(a); break;
+            case 8: k_act_mul<ACT, IT, OT, 8, false, HAD><<<grid, threads, 0, s>>>(a); break;
+            default: k_act_mul<ACT, IT, OT, 4, false, HAD><<<grid, threads, 0, s>>>(a); break;
         }
     }
+}
+
+extern "C" int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out, int64_t ldo, int64_t rows,
+                               int64_t cols, const void* pre_scale, const void* post_scale, float scale, void* stream);
+
+template <int ACT>
+static int act_mul_entry(const char* op, const void* x, const void* y, int it, void* z, int ot,
+                         int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz,
+                         float limit, void* stream);
+
+// Activation -> Hadamard: the vector kernel with HAD when every row is 16-byte aligned, else the
+// activation into z (or into out) and had_r_128 over it in place.
+template <int ACT>
+static int act_had_entry(const char* op, const void* x, const void* y, int it, int64_t ldx, int64_t ldy,
+                         void* z, int64_t ldz, const void* pre, void* out, int64_t ldo,
+                         int64_t rows, int64_t cols, float limit, float had_scale, void* stream)
+{
+    if (!is_float_dtype(it)) return set_error(EXL3R_EDTYPE, "%s: unsupported input dtype %s", op, dtype_name(it));
+    if (rows < 0 || cols <= 0 || cols % 128 || (rows > 1 && (ldx < cols || ldy < cols || ldo < cols || (z && ldz < cols))))
+        return set_error(EXL3R_EINVAL, "%s: invalid shape rows=%lld cols=%lld (a multiple of 128) or row strides", op,
+                         (long long)rows, (long long)cols);
+    if (rows == 0) return EXL3R_OK;
+    if (!x || !y || !out) return set_error(EXL3R_EINVAL, "%s: x, y and out must be non-null", op);
+    if (out == x || out == y || out == z || (z && (z == x || z == y)))
+        return set_error(EXL3R_EINVAL, "%s: out and z must not alias the inputs or each other", op);
+    const int64_t lx = rows > 1 ? ldx : cols, ly = rows > 1 ? ldy : cols, lo = rows > 1 ? ldo : cols;
+    const int64_t lz = z ? (rows > 1 ? ldz : cols) : cols;
+    hipStream_t s = (hipStream_t)stream;
+    const int eb = dtype_bytes(it);
+    const bool vec = aligned16(x) && aligned16(y) && aligned16(out) && (!z || aligned16(z)) && (!pre || aligned16(pre)) &&
+                     (lx * eb) % 16 == 0 && (ly * eb) % 16 == 0 && (lo * 2) % 16 == 0 && (lz * 2) % 16 == 0;
+    if (vec)
+    {
+        ActArgs a{ x, y, z, lx, ly, lz, rows, cols, limit, pre, out, lo, had_scale * 0.0883883461356163f };
+        with_float_type(it, [&](auto I) { launch_act_vec<ACT, decltype(I), TF16, true>(a, s); });
+        return launch_status(op);
+    }
+    void* dst = z ? z : out;
+    const int64_t ld = z ? lz : lo;
+    int rc = act_mul_entry<ACT>(op, x, y, it, dst, EXL3R_F16, rows, cols, lx, ly, ld, limit, stream);
+    if (rc == EXL3R_OK) rc = exl3r_had_r_128(dst, EXL3R_F16, ld, out, lo, rows, cols, pre, nullptr, had_scale, stream);
+    return rc;
 }
 
 template <int ACT>
@@ -213,6 +285,27 @@ extern "C" int exl3r_gelu_mul(const void* x, const void* y, int in_dtype, void* 
                               float act_limit, void* stream)
 {
     return act_mul_entry<ACT_GELU>("exl3r_gelu_mul", x, y, in_dtype, z, z_dtype, rows, cols, ldx, ldy, ldz, act_limit, stream);
+}
+
+extern "C" int exl3r_act_mul_had(int act, const void* x, const void* y, int in_dtype, int64_t ldx, int64_t ldy,
+                                 void* z, int64_t ldz, const void* pre_scale, void* out, int64_t ldo,
+                                 int64_t rows, int64_t cols, float act_limit, float had_scale, void* stream)
+{
+    const char* op = "exl3r_act_mul_had";
+    switch (act)
+    {
+        case EXL3R_ACT_SILU:
+            return act_had_entry<ACT_SILU>(op, x, y, in_dtype, ldx, ldy, z, ldz, pre_scale, out, ldo, rows, cols,
+                                           act_limit, had_scale, stream);
+        case EXL3R_ACT_GELU:
+            return act_had_entry<ACT_GELU>(op, x, y, in_dtype, ldx, ldy, z, ldz, pre_scale, out, ldo, rows, cols,
+                                           act_limit, had_scale, stream);
+        case EXL3R_ACT_MUL_SIGMOID:
+            if (act_limit != 0.0f) return set_error(EXL3R_EINVAL, "%s: act_limit applies to silu / gelu only", op);
+            return act_had_entry<ACT_SIGMOID>(op, y, x, in_dtype, ldy, ldx, z, ldz, pre_scale, out, ldo, rows, cols,
+                                              0.0f, had_scale, stream);
+        default: return set_error(EXL3R_EINVAL, "%s: unknown act %d", op, act);
+    }
 }
 
 // z = x * sigmoid(y): the act-mul kernels with the gate and value operands exchanged.

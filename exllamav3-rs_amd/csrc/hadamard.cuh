@@ -10,7 +10,8 @@
 
 namespace exl3r {
 
-// The value of lane (l ^ M) inside the 16-lane group.
+// The value of lane (l ^ M) inside the 16-lane group: quad_perm for xor 1 and 2, ds_swizzle (bit
+// mode) for xor 4, a row rotation by 8 for xor 8.
 template <int M>
 __device__ __forceinline__ float lane_xor(float v)
 {
@@ -18,11 +19,12 @@ __device__ __forceinline__ float lane_xor(float v)
     if constexpr (M == 1) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, i, DPP_QUAD_XOR1, 0xf, 0xf, false));
     else if constexpr (M == 2) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, i, DPP_QUAD_XOR2, 0xf, 0xf, false));
     else if constexpr (M == 4) return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(i, 0x101f));
-    else return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(i, 0x201f));
+    else return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, i, DPP_ROW_ROR8, 0xf, 0xf, false));
 }
 
 // One cross-lane butterfly stage: the lane whose bit M is clear holds a and keeps a + b, its partner
-// holds b and keeps a - b.
+// holds b and keeps a - b.  (Carrying a per-lane sign instead, to make this one fma, does not keep
+// the sign of exact zeros: -(x + y) and (-x) + (-y) differ when x + y == 0.)
 template <int M>
 __device__ __forceinline__ void lane_stage(float (&f)[8], int l16)
 {
@@ -36,7 +38,8 @@ __device__ __forceinline__ void lane_stage(float (&f)[8], int l16)
     }
 }
 
-__device__ __forceinline__ void butterfly128(float (&f)[8], int l16)
+// f = r * H128 (block) with r the transform's scale, rounded once after the fp32 butterfly.
+__device__ __forceinline__ void butterfly128(float (&f)[8], int l16, float r)
 {
     #pragma clang fp contract(off)
     #pragma unroll
@@ -55,6 +58,8 @@ __device__ __forceinline__ void butterfly128(float (&f)[8], int l16)
     lane_stage<2>(f, l16);
     lane_stage<4>(f, l16);
     lane_stage<8>(f, l16);
+    #pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = f[j] * r;
 }
 
 __device__ __forceinline__ uint32_t hmul2(uint32_t a, uint32_t b)

@@ -58,9 +58,7 @@ __device__ __forceinline__ void had_block(const HadArgs& a, int64_t blk, int l16
             for (int j = 0; j < 8; ++j) f[j] = f[j] * p[j];
         }
     }
-    butterfly128(f, l16);
-    #pragma unroll
-    for (int j = 0; j < 8; ++j) f[j] = f[j] * a.r;
+    butterfly128(f, l16, a.r);
     if constexpr (IO::code == DT_F16)
     {
         v = pack8<IO>(f);

@@ -282,9 +282,7 @@ __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* 
             }
             float f[8];
             unpack8<TF16>(v, f);
-            butterfly128(f, l16);
-            #pragma unroll
-            for (int j = 0; j < 8; ++j) f[j] = f[j] * a.hr;
+            butterfly128(f, l16, a.hr);
             store8<TF16>((char*)a.hout[i] + row * a.ldh * 2, e, pack8<TF16>(f));
         }
     }

@@ -314,6 +314,27 @@ def rms_norm_had(x, w, outs, pre_scales, eps, constant_bias=0.0, constant_scale=
                                     _stream(x, stream)))
 
 
+ACT_CODES = {"silu": 0, "gelu": 1, "mul_sigmoid": 2}
+
+
+def act_mul_had(act, x, y, out, pre_scale=None, z=None, act_limit=0.0, had_scale=1.0, stream=None):
+    """One pass: z = silu(x) * y, gelu(x) * y or x * sigmoid(y) in f16, then out = had_r_128(z, pre_scale)
+    (f16 [rows, cols], cols % 128 == 0); z is written only if given."""
+    rows, cols, ldx = _rows(x)
+    ry, cy, ldy = _rows(y)
+    ro, co, ldo = _rows(out)
+    if (ry, cy) != (rows, cols) or (ro, co) != (rows, cols) or y.dtype != x.dtype or out.dtype != torch.float16:
+        raise ValueError("y like x; out f16 shaped like x")
+    ldz = 0
+    if z is not None:
+        rz, cz, ldz = _rows(z)
+        if (rz, cz) != (rows, cols) or z.dtype != torch.float16:
+            raise ValueError("z is the f16 activation shaped like x")
+    check(load().exl3r_act_mul_had(ACT_CODES[act], _ptr(x), _ptr(y), dtype_code(x), ldx, ldy, _ptr(z), ldz,
+                                   _ptr(pre_scale), _ptr(out), ldo, rows, cols, act_limit, float(had_scale),
+                                   _stream(x, stream)))
+
+
 def embedding(table, ids, out, err_flag=None, stream=None):
     """out[i] = table[ids[i]] (bit-exact, or exact upcast to f32)."""
     vocab, hidden = table.shape

@@ -73,6 +73,11 @@ extern "C" {
 #define EXL3R_EDTYPE      (-2) /* unsupported dtype or dtype combination */
 
 /* rotary styles: same values as ROPESTYLE_* (kernels/rope.cuh:6-8) and ffi::ROPE_* (src/ffi.rs:217-219) */
+/* activations of exl3r_act_mul_had */
+#define EXL3R_ACT_SILU        0 /* silu(x) * y */
+#define EXL3R_ACT_GELU        1 /* gelu(x) * y */
+#define EXL3R_ACT_MUL_SIGMOID 2 /* x * sigmoid(y) */
+
 #define EXL3R_ROPE_NONE 0
 #define EXL3R_ROPE_GPTJ 1
 #define EXL3R_ROPE_NEOX 2
@@ -312,6 +317,22 @@ EXL3R_API int exl3r_rms_norm_had(const void* x, int x_dtype, int64_t ldx, const 
                        int n_out, const void* const* pre_scales, void* const* outs, int64_t ldo,
                        int64_t rows, int64_t dim, float eps, float constant_bias, float constant_scale,
                        float had_scale, void* stream);
+
+/*
+ * Gated activation whose f16 output feeds the random-Hadamard input rotation of the next EXL3
+ * projection, in one pass (GatedMlp::forward's silu_mul -> down_proj, src/modules.rs:932-940, and the
+ * Qwen3.5 attention gate -> o_proj; then had_r_128(z, suh), src/modules.rs:224-227):
+ *   z   = act(x, y) as exl3r_silu_mul / exl3r_gelu_mul / exl3r_mul_sigmoid with an f16 z
+ *         (act = EXL3R_ACT_*; act_limit as exl3r_silu_mul, 0 for EXL3R_ACT_MUL_SIGMOID), written
+ *         only when z != NULL (row stride ldz);
+ *   out = had_r_128(z, pre_scale) with scale had_scale: f16 [rows, cols], row stride ldo;
+ *         pre_scale is f16 [cols] (the projection's suh) or NULL.
+ * x, y: [rows, cols] of in_dtype (F16/BF16/F32), row strides ldx, ldy; cols % 128 == 0; out and z
+ * alias nothing.  Bit-identical to the unfused calls; rows that are not 16-byte aligned run them.
+ */
+EXL3R_API int exl3r_act_mul_had(int act, const void* x, const void* y, int in_dtype, int64_t ldx, int64_t ldy,
+                      void* z, int64_t ldz, const void* pre_scale, void* out, int64_t ldo,
+                      int64_t rows, int64_t cols, float act_limit, float had_scale, void* stream);
 
 /*
  * Token-embedding gather: out[i, :] = table[ids[i], :], bit-exact (same dtype) or exactly upcast to

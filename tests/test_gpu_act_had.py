@@ -1,0 +1,108 @@
+"""GPU parity of exl3r_act_mul_had (the gated activation feeding the next EXL3 projection's
+random-Hadamard input rotation in one pass: silu_mul -> down_proj, src/modules.rs:932-940, and the
+Qwen3.5 attention gate -> o_proj).  The activation z is checked against the oracle at the
+activation's own tolerance (<= 1 ulp of f16); the projection input is checked bit for bit against
+the oracle's had_r_128 of that z, and against the unfused GPU calls (exl3r_silu_mul / gelu_mul /
+mul_sigmoid into an f16 z, then exl3r_had_r_128).  Covers the MLP prefill shape of Qwen3-32B, every
+input dtype, act_limit, a missing pre-scale, a scalar transform scale, strided and unaligned rows
+(the unfused fallback), zero rows and the argument errors."""
+import numpy as np
+import pytest
+import torch
+
+import exl3r
+import exl3r.ffi as ffi
+from _gpu import NTHREADS, assert_bitwise, assert_close_ulp, dev_normal, from_dev
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+F32, F16, BF16 = orc.F32, orc.F16, orc.BF16
+UNFUSED = {"silu": ffi.silu_mul, "gelu": ffi.gelu_mul}
+
+
+def suh(cols, seed):
+    rng = np.random.default_rng(seed)
+    return torch.from_numpy((np.where(rng.random(cols) < 0.5, -1.0, 1.0) *
+                             (1 + 0.01 * rng.standard_normal(cols))).astype(np.float16)).cuda()
+
+
+def oracle_act(act, x, y, it, limit):
+    xh, yh = np.ascontiguousarray(from_dev(x)), np.ascontiguousarray(from_dev(y))
+    if act == "mul_sigmoid":
+        return orc.mul_sigmoid(xh, yh, it, F16, nthreads=NTHREADS)
+    code = orc.ACT_SILU if act == "silu" else orc.ACT_GELU
+    return orc.act_mul(code, xh, yh, it, F16, limit, nthreads=NTHREADS)
+
+
+def unfused(act, x, y, pre, limit, had_scale):
+    z = torch.empty(x.shape, device="cuda", dtype=torch.float16)
+    if act == "mul_sigmoid":
+        ffi.mul_sigmoid(x, y, z)
+    else:
+        UNFUSED[act](x, y, z, limit)
+    out = torch.empty_like(z)
+    ffi.had_r_128(z, out, pre, None, had_scale)
+    return z, out
+
+
+def run(act, rows, cols, it, limit=0.0, with_z=True, pre=True, had_scale=1.0, ld=None, off=0, seed=0):
+    ld = ld or cols
+    x = dev_normal((rows, ld + off), 0, 2, it, seed)[:, off:off + cols]
+    y = dev_normal((rows, ld + off), 0, 1, it, seed + 1)[:, off:off + cols]
+    p = suh(cols, seed + 2) if pre else None
+    z = torch.empty((rows, cols), device="cuda", dtype=torch.float16) if with_z else None
+    out = torch.empty((rows, cols), device="cuda", dtype=torch.float16)
+    ffi.act_mul_had(act, x, y, out, p, z, limit, had_scale)
+    ez, eout = unfused(act, x, y, p, limit, had_scale)
+    torch.cuda.synchronize()
+    tag = f"{act}_had {rows}x{cols} in{it} L{limit} z{int(with_z)} pre{int(pre)} ld{ld} off{off}"
+    assert_bitwise(from_dev(out), from_dev(eout), what=tag + " vs unfused")
+    if with_z:
+        gz = from_dev(z)
+        assert_bitwise(gz, from_dev(ez), what=tag + " z vs unfused")
+        assert_close_ulp(gz, oracle_act(act, x, y, it, limit), F16, 1, what=tag + " z vs oracle")
+        exp = orc.had_r_128(np.ascontiguousarray(gz), F16, pre=from_dev(p) if p is not None else None,
+                            scale=had_scale, nthreads=NTHREADS)
+        assert_bitwise(from_dev(out), exp, what=tag + " out vs oracle had_r_128(z)")
+
+
+def test_qwen3_down_proj_input_prefill():
+    """silu(gate) * up of Qwen3-32B prefill, 2048 x 25600 f16, into down_proj's input rotation."""
+    run("silu", 2048, 25600, F16, seed=1)
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu", "mul_sigmoid"])
+@pytest.mark.parametrize("it", [F16, BF16, F32])
+def test_acts_and_dtypes(act, it):
+    run(act, 37, 1024, it, seed=3)
+
+
+def test_limit_scale_missing_pre_and_no_z():
+    run("silu", 65, 2048, BF16, limit=2.5, had_scale=0.5, seed=4)
+    run("gelu", 65, 2048, F16, pre=False, with_z=False, seed=5)
+    run("silu", 1, 384, F16, with_z=False, seed=6)
+
+
+def test_strided_and_unaligned_rows():
+    run("silu", 19, 512, F16, ld=520, seed=7)                       # strided, vector kernel
+    run("gelu", 19, 512, F16, ld=515, seed=8)                       # unaligned stride: unfused fallback
+    run("mul_sigmoid", 7, 256, BF16, off=1, with_z=False, seed=9)    # unaligned base: fallback into out
+
+
+def test_zero_rows_and_errors():
+    z0 = torch.empty((0, 256), device="cuda", dtype=torch.float16)
+    ffi.act_mul_had("silu", z0, z0, torch.empty_like(z0))
+    x = dev_normal((4, 256), 0, 1, F16, 10)
+    y = dev_normal((4, 256), 0, 1, F16, 11)
+    with pytest.raises(exl3r.Exl3rError):
+        bad = dev_normal((4, 200), 0, 1, F16, 12)
+        ffi.act_mul_had("silu", bad, bad.clone(), torch.empty_like(bad))
+    with pytest.raises(exl3r.Exl3rError):
+        ffi.act_mul_had("silu", x, y, x)                                     # out aliases x
+    with pytest.raises(exl3r.Exl3rError):
+        ffi.act_mul_had("mul_sigmoid", x, y, torch.empty_like(x), act_limit=1.0)
+    rc = exl3r.load().exl3r_act_mul_had(7, x.data_ptr(), y.data_ptr(), F16, 256, 256, None, 0, None,
+                                        torch.empty_like(x).data_ptr(), 256, 4, 256, 0.0, 1.0, None)
+    assert rc == exl3r.EINVAL
+    torch.cuda.synchronize()
