@@ -257,6 +257,77 @@ void deinterleave_qg(const Tensor& qg, const Tensor& q, const Tensor& g, int64_t
                                     code(qg.dtype), rows, (int)heads, (int)head_dim, s.get()));
 }
 
+void had_r_128(const Tensor& x, const Tensor& out, const Tensor* pre_scale, const Tensor* post_scale, float scale,
+               const Stream& s)
+{
+    int64_t rows, cols, ldx, ro, co, ldo;
+    x.rows_view(rows, cols, ldx);
+    out.rows_view(ro, co, ldo);
+    require(ro == rows && co == cols && out.dtype == x.dtype, "had_r_128: x and out must share shape and dtype");
+    for (const Tensor* sc : { pre_scale, post_scale })
+        require(!sc || (sc->dtype == DType::F16 && sc->numel() == cols), "had_r_128: scales are f16 [cols]");
+    check_abi(exl3r_had_r_128(x.data, code(x.dtype), ldx, out.data, ldo, rows, cols, ptr(pre_scale), ptr(post_scale),
+                              scale, s.get()));
+}
+
+void rms_norm_had(const Tensor& x, const Tensor* w, const Tensor* r, const Tensor* y,
+                  const std::vector<const Tensor*>& outs, const std::vector<const Tensor*>& pre_scales, float eps,
+                  float constant_bias, float constant_scale, float had_scale, const Stream& s)
+{
+    int64_t rows, dim, ldx, ldr = 0, ldy = 0, ldo = -1;
+    x.rows_view(rows, dim, ldx);
+    require(!outs.empty() && outs.size() <= 4 && pre_scales.size() == outs.size(),
+            "rms_norm_had: 1..4 outputs, one pre_scale (or null) each");
+    std::vector<const void*> pre(outs.size());
+    std::vector<void*> out(outs.size());
+    for (size_t i = 0; i < outs.size(); ++i)
+    {
+        int64_t ro, co, lo;
+        require(outs[i] != nullptr, "rms_norm_had: outputs must be given");
+        outs[i]->rows_view(ro, co, lo);
+        require(ro == rows && co == dim && outs[i]->dtype == DType::F16 && (ldo < 0 || lo == ldo),
+                "rms_norm_had: outputs are f16 shaped like x with one row stride");
+        ldo = lo;
+        out[i] = outs[i]->data;
+        pre[i] = ptr(pre_scales[i]);
+    }
+    if (r)
+    {
+        int64_t rr, dr;
+        r->rows_view(rr, dr, ldr);
+        require(rr == rows && dr == dim, "rms_norm_had: r must be shaped like x");
+    }
+    if (y)
+    {
+        int64_t ry, dy;
+        y->rows_view(ry, dy, ldy);
+        require(ry == rows && dy == dim && y->dtype == DType::F16, "rms_norm_had: y is f16 shaped like x");
+    }
+    check_abi(exl3r_rms_norm_had(x.data, code(x.dtype), ldx, ptr(w), code_or(w, DType::F16), r ? r->data : nullptr,
+                                 r ? code(r->dtype) : EXL3R_F16, ldr, y ? y->data : nullptr, ldy, (int)outs.size(),
+                                 pre.data(), out.data(), ldo, rows, dim, eps, constant_bias, constant_scale, had_scale,
+                                 s.get()));
+}
+
+void act_mul_had(HadAct act, const Tensor& x, const Tensor& y, const Tensor& out, const Tensor* pre_scale,
+                 const Tensor* z, float act_limit, float had_scale, const Stream& s)
+{
+    int64_t rows, cols, ldx, ry, cy, ldy, ro, co, ldo, ldz = 0;
+    x.rows_view(rows, cols, ldx);
+    y.rows_view(ry, cy, ldy);
+    out.rows_view(ro, co, ldo);
+    require(ry == rows && cy == cols && y.dtype == x.dtype, "act_mul_had: x and y must share shape and dtype");
+    require(ro == rows && co == cols && out.dtype == DType::F16, "act_mul_had: out is f16 shaped like x");
+    if (z)
+    {
+        int64_t rz, cz;
+        z->rows_view(rz, cz, ldz);
+        require(rz == rows && cz == cols && z->dtype == DType::F16, "act_mul_had: z is f16 shaped like x");
+    }
+    check_abi(exl3r_act_mul_had((int)act, x.data, y.data, code(x.dtype), ldx, ldy, z ? z->data : nullptr, ldz,
+                                ptr(pre_scale), out.data, ldo, rows, cols, act_limit, had_scale, s.get()));
+}
+
 void argmax_sample(const Tensor& logits, const Tensor& ids, int max_logit, const Stream& s)
 {
     int64_t rows, vocab, ld;

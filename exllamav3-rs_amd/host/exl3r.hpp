@@ -9,6 +9,7 @@
 //   exl3r::ffi::gated_rms_norm / mul_sigmoid_ / deinterleave_qg          <- src/ffi.rs:479-483, 616-624
 //   exl3r::ffi::rope_paged_kv                                            <- rope + paged append, src/modules.rs:666-704
 //   exl3r::ffi::argmax_sample / gumbel_sample / gumbel_noise             <- src/ffi.rs:521-535, src/generator.rs:1596
+//   exl3r::ffi::had_r_128 / rms_norm_had / act_mul_had                   <- src/ffi.rs:606-607, src/modules.rs:224-231
 //   exl3r::ffi::embedding                                                <- index_select, src/modules.rs:430-436
 //   exl3r::RmsNorm::forward / forward_res                                <- src/modules.rs:342-412
 //   exl3r::Embedding::forward                                            <- src/modules.rs:418-437
@@ -161,6 +162,21 @@ void argmax_sample(const Tensor& logits, const Tensor& ids, int max_logit, const
 void gumbel_sample(const Tensor& logits, const Tensor& ids, int max_logit, uint32_t random, const Stream& s);
 // src/ffi.rs:531-535: out = x + the Gumbel noise gumbel_sample adds (out may be x).
 void gumbel_noise(const Tensor& x, const Tensor& out, uint32_t random, const Stream& s);
+// src/ffi.rs:606-607: the EXL3 linear's random-Hadamard rotation of [rows, cols] f16 / f32 x into out
+// (cols % 128 == 0; out may be x), with an optional f16 [cols] pre_scale (suh) or post_scale (svh).
+void had_r_128(const Tensor& x, const Tensor& out, const Tensor* pre_scale, const Tensor* post_scale, float scale,
+               const Stream& s);
+// RMSNorm (r == nullptr) or residual RMSNorm (r += x) whose f16 output feeds had_r_128(y, pre_scales[i]) of
+// 1..4 projections (src/modules.rs:372-411 then 224-227), in one pass; outs are f16 like x; y (f16) is
+// written only when given; pre_scales[i] may be null.
+void rms_norm_had(const Tensor& x, const Tensor* w, const Tensor* r, const Tensor* y,
+                  const std::vector<const Tensor*>& outs, const std::vector<const Tensor*>& pre_scales, float eps,
+                  float constant_bias, float constant_scale, float had_scale, const Stream& s);
+// Gated activation whose f16 output feeds the next projection's had_r_128(z, pre_scale)
+// (src/modules.rs:932-940 then 224-227): silu(x) * y, gelu(x) * y or x * sigmoid(y); z kept when given.
+enum class HadAct : int { Silu = EXL3R_ACT_SILU, Gelu = EXL3R_ACT_GELU, MulSigmoid = EXL3R_ACT_MUL_SIGMOID };
+void act_mul_had(HadAct act, const Tensor& x, const Tensor& y, const Tensor& out, const Tensor* pre_scale,
+                 const Tensor* z, float act_limit, float had_scale, const Stream& s);
 // Embedding gather: out[i] = table[ids[i]] (bit-exact, or exact upcast to f32); err_flag optional.
 void embedding(const Tensor& table, const Tensor& ids, const Tensor& out, int32_t* err_flag, const Stream& s);
 // Gather fused with the following RMSNorm; h optional.

@@ -321,6 +321,53 @@ int main()
         const bool ok = gn == en && std::memcmp(gi.data(), ei.data(), rows * 8) == 0 && gi == gi2;
         report("ffi::gumbel_noise / gumbel_sample", ok, ok ? "noise bitwise, ids exact" : "DIFFER");
     }
+    // had_r_128 with suh, then the fused residual norm -> q/k/v inputs and the fused SiLU -> down_proj
+    // input, each bitwise against the oracle composition.
+    {
+        const int rows = 12, dim = 512;
+        std::vector<uint8_t> sh(dim * 2);
+        for (int i = 0; i < dim; ++i)
+        {
+            const uint16_t v = (splitmix() & 1) ? 0xbc00 : 0x3c00;   // -1.0 / +1.0 in f16
+            std::memcpy(&sh[i * 2], &v, 2);
+        }
+        auto suh = upload(sh, DType::F16, { dim }, s);
+        auto xh = host_normal(DType::F16, rows * dim, 0.f, 1.f);
+        auto x = upload(xh, DType::F16, { rows, dim }, s);
+        auto hx = OwnedTensor::empty(DType::F16, { rows, dim });
+        ffi::had_r_128(x.t, hx.t, &suh.t, nullptr, 1.f, s);
+        std::vector<uint8_t> eh(xh.size());
+        oracle_had_r_128(xh.data(), OR_F16, dim, eh.data(), dim, rows, dim, (const uint16_t*)sh.data(), nullptr, 1.f, 1);
+        bool ok = download(hx, s) == eh;
+        report("ffi::had_r_128 f16 with suh", ok, ok ? "bitwise" : "DIFFER");
+
+        auto rh = host_normal(DType::F32, rows * dim, 0.f, 4.f);
+        auto wh = host_normal(DType::F16, dim, 1.f, 0.1f);
+        auto r = upload(rh, DType::F32, { rows, dim }, s);
+        auto w = upload(wh, DType::F16, { dim }, s);
+        auto o0 = OwnedTensor::empty(DType::F16, { rows, dim }), o1 = OwnedTensor::empty(DType::F16, { rows, dim });
+        ffi::rms_norm_had(x.t, &w.t, &r.t, nullptr, { &o0.t, &o1.t }, { &suh.t, nullptr }, 1e-6f, 0.f, 1.f, 1.f, s);
+        std::vector<uint8_t> ey(xh.size()), er = rh, e0(xh.size()), e1(xh.size());
+        oracle_rms_norm(xh.data(), OR_F16, dim, wh.data(), OR_F16, ey.data(), OR_F16, dim, er.data(), OR_F32, dim, rows, dim,
+                        1e-6f, 0.f, 1.f, 1);
+        oracle_had_r_128(ey.data(), OR_F16, dim, e0.data(), dim, rows, dim, (const uint16_t*)sh.data(), nullptr, 1.f, 1);
+        oracle_had_r_128(ey.data(), OR_F16, dim, e1.data(), dim, rows, dim, nullptr, nullptr, 1.f, 1);
+        ok = download(o0, s) == e0 && download(o1, s) == e1 && download(r, s) == er;
+        report("ffi::rms_norm_had residual, 2 outputs", ok, ok ? "bitwise" : "DIFFER");
+
+        auto gh = host_normal(DType::F16, rows * dim, 0.f, 2.f);
+        auto g = upload(gh, DType::F16, { rows, dim }, s);
+        auto z = OwnedTensor::empty(DType::F16, { rows, dim }), hz = OwnedTensor::empty(DType::F16, { rows, dim });
+        ffi::act_mul_had(ffi::HadAct::Silu, g.t, x.t, hz.t, &suh.t, &z.t, 0.f, 1.f, s);
+        auto zh = download(z, s);
+        std::vector<uint8_t> ez(zh.size()), ehz(zh.size());
+        oracle_act_mul(0, gh.data(), xh.data(), OR_F16, ez.data(), OR_F16, rows, dim, dim, dim, dim, 0.f, 1);
+        oracle_had_r_128(zh.data(), OR_F16, dim, ehz.data(), dim, rows, dim, (const uint16_t*)sh.data(), nullptr, 1.f, 1);
+        const int64_t u = max_ulp16(zh, ez);
+        ok = u <= 1 && download(hz, s) == ehz;
+        std::snprintf(msg, sizeof msg, "z max ulp %lld, rotation of z bitwise", (long long)u);
+        report("ffi::act_mul_had silu -> had", ok, ok ? msg : "DIFFER");
+    }
     std::printf(failures ? "test_host_gpu: %d failures\n" : "test_host_gpu: all passed\n", failures);
     return failures ? 1 : 0;
 }

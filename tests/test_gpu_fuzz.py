@@ -12,11 +12,14 @@ import exl3r.ffi as ffi
 from _gpu import NTHREADS, TORCH_DT, assert_bitwise, dev_normal, from_dev
 from oracle import oracle as orc
 from test_gpu_act import run as run_act
+from test_gpu_act_had import run as run_act_had
 from test_gpu_argmax import run as run_argmax
 from test_gpu_embedding import check_gather, run_fused
 from test_gpu_gated import check as check_gate, run_gated
 from test_gpu_gumbel import run_noise, run_sample
+from test_gpu_hadamard import run as run_had, scales
 from test_gpu_rms_norm import run_plain, run_res
+from test_gpu_rms_norm_had import run as run_norm_had
 from test_gpu_rope import run as run_rope
 from test_gpu_rope_paged import layout, run as run_paged
 from test_gpu_rope_table import run as run_rope_table
@@ -181,3 +184,24 @@ def test_fuzz_sampling(case):
     run_sample(logits, dt, int(rng.integers(0, 2 ** 32)), mask)
     cols = min(vocab, 5000)
     run_noise(logits[:, :cols], dt, int(rng.integers(0, 2 ** 32)), pick(rng, FLOATS))
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_fuzz_hadamard(case):
+    rng = np.random.default_rng(9000 + case)
+    rows, cols = int(rng.integers(1, 400)), 128 * int(rng.integers(1, 48))
+    dt = pick(rng, [F16, F32])
+    pad = int(pick(rng, [0, 0, 8, 3]))
+    x = dev_normal((rows, cols + pad), 0, float(pick(rng, [1.0, 30.0])), dt, case)[:, :cols]
+    mode = pick(rng, ["pre", "post", "none"])
+    s = scales(cols, case + 1)
+    run_had(x, dt, pre=s if mode == "pre" else None, post=s if mode == "post" else None,
+            scale=float(pick(rng, [1.0, 0.5, 1.7])), what=f"fuzz had {rows}x{cols}+{pad} dt{dt} {mode}")
+    n_out = int(rng.integers(1, 5))
+    run_norm_had(int(rng.integers(1, 300)), 128 * int(rng.integers(1, 40)), pick(rng, FLOATS),
+                 pick(rng, [None, F32, F16, BF16]), pick(rng, FLOATS), n_out=n_out, with_y=bool(rng.random() < 0.5),
+                 cb=float(pick(rng, [0.0, 1.0])), had_scale=float(pick(rng, [1.0, 0.25])),
+                 pre_none=tuple(i for i in range(n_out) if rng.random() < 0.3), seed=case + 3)
+    run_act_had(pick(rng, ["silu", "gelu", "mul_sigmoid"]), int(rng.integers(1, 300)), 128 * int(rng.integers(1, 80)),
+                pick(rng, FLOATS), with_z=bool(rng.random() < 0.6), pre=bool(rng.random() < 0.8),
+                ld=None if rng.random() < 0.7 else 128 * int(rng.integers(81, 90)) + int(pick(rng, [0, 8, 3])), seed=case + 5)
