@@ -34,7 +34,7 @@ OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "
        "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "rope_kv_prefill",
        "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
        "deinterleave_q35", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
-       "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "silu_had_c3",
+       "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_unfused", "silu_had_c3",
        "silu_had_c3_unfused", "calib_copy",
        "calib_copy_cached"]
 
@@ -329,15 +329,17 @@ def make_had(name, rows, cols, seed=740):
     return Work(name, nbytes, launch, f"random-Hadamard row transform f16 [{rows},{cols}] with suh", sets)
 
 
-def make_norm_had(name, rows, cols, fused, seed=760):
+def make_norm_had(name, rows, cols, fused, seed=760, rotate=False):
     """Qwen3-32B prefill attention input: r += x (f16 sublayer output into the f32 residual), the f16
     RMSNorm, and the q / k / v projections' input rotations had_r_128(y, suh_i)
     (src/modules.rs:224-227, 372-411): one fused launch, or the residual norm and three had_r_128
-    launches.  Both count the fused job's bytes (x, r read and written, three outputs, w, suh)."""
+    launches.  With rotate, x is the previous projection's raw output and its own output rotation
+    had_r_128(x, x, None, svh) (src/modules.rs:231) comes first (unfused: in place, one more launch).
+    Both count the fused job's bytes (x, r read and written, three outputs, w, suh, svh)."""
     import torch
     import exl3r.ffi as ffi
     n = rows * cols
-    nbytes = n * (2 + 4 + 4 + 3 * 2) + 4 * cols * 2
+    nbytes = n * (2 + 4 + 4 + 3 * 2) + (5 if rotate else 4) * cols * 2
     sets = sets_for(nbytes)
     bufs = [(gen((rows, cols), 0.0, 1.0, torch.float16, seed + 2 * k),
              gen((rows, cols), 0.0, 4.0, torch.float32, seed + 2 * k + 1),
@@ -345,17 +347,21 @@ def make_norm_had(name, rows, cols, fused, seed=760):
     w = gen((cols,), 1.0, 0.1, torch.float16, seed + 99)
     suh = [torch.where(torch.rand(cols, device="cuda") < 0.5, -1.0, 1.0).to(torch.float16) for _ in range(3)]
     y = torch.empty((rows, cols), device="cuda", dtype=torch.float16)
+    svh = torch.where(torch.rand(cols, device="cuda") < 0.5, -1.0, 1.0).to(torch.float16) if rotate else None
 
     def launch(i):
         x, r, outs = bufs[i % sets]
         if fused:
-            ffi.rms_norm_had(x, w, outs, suh, 1e-6, r=r)
+            ffi.rms_norm_had(x, w, outs, suh, 1e-6, r=r, rotate_x=rotate, x_post_scale=svh)
         else:
+            if rotate:
+                ffi.had_r_128(x, x, None, svh)
             ffi.rms_norm_res_in(x, w, y, r, 1e-6)
             for o, p in zip(outs, suh):
                 ffi.had_r_128(y, o, p)
-    kind = "fused" if fused else "unfused (residual RMSNorm + 3 had_r_128)"
-    return Work(name, nbytes, launch, f"residual RMSNorm -> 3 Hadamard inputs [{rows},{cols}] f16/f32r, {kind}", sets)
+    kind = "fused" if fused else f"unfused ({'had_r_128 in place + ' if rotate else ''}residual RMSNorm + 3 had_r_128)"
+    head = "had(svh) -> residual RMSNorm" if rotate else "residual RMSNorm"
+    return Work(name, nbytes, launch, f"{head} -> 3 Hadamard inputs [{rows},{cols}] f16/f32r, {kind}", sets)
 
 
 def make_act_had(name, rows, cols, fused, seed=780):
@@ -494,6 +500,8 @@ def make_all(only=None):
         "had_c3": lambda: make_had("had_c3", 8192, 5120),
         "norm_had_c3": lambda: make_norm_had("norm_had_c3", 8192, 5120, True),
         "norm_had_c3_unfused": lambda: make_norm_had("norm_had_c3_unfused", 8192, 5120, False),
+        "norm_had_rot_c3": lambda: make_norm_had("norm_had_rot_c3", 8192, 5120, True, rotate=True),
+        "norm_had_rot_c3_unfused": lambda: make_norm_had("norm_had_rot_c3_unfused", 8192, 5120, False, rotate=True),
         "silu_had_c3": lambda: make_act_had("silu_had_c3", 8192, 17408, True),
         "silu_had_c3_unfused": lambda: make_act_had("silu_had_c3_unfused", 8192, 17408, False),
         "calib_copy": lambda: make_copy("calib_copy"),

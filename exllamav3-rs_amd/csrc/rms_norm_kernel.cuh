@@ -45,14 +45,22 @@ struct RmsArgs
     int gact;           // RMS_GATED: 0 silu, 1 sigmoid
     int gfirst;         // RMS_GATED: gate applied before the norm
     int w_groups;       // RMS_GATED: the weight holds w_groups rows of dim, row r uses r % w_groups
-    // Hadamard outputs (HAD kernels, exl3r_rms_norm_had): output i = had_r_128 of the f16 norm
+    // Hadamard outputs (HAD_OUT kernels, exl3r_rms_norm_had): output i = had_r_128 of the f16 norm
     // output with pre-scale hpre[i] (f16 [dim] or nullptr), rows at stride ldh, hr = scale / sqrt(128).
     int nh;
     const void* hpre[4];
     void* hout[4];
     int64_t ldh;
     float hr;
+    // HAD_IN kernels: f16 x is first replaced by had_r_128(x) * hxpost (the EXL3 linear's output
+    // rotation with its f16 post-scale, or none when null), hxr = 1 / sqrt(128).
+    const void* hxpost;
+    float hxr;
 };
+
+// Hadamard flags of the norm kernels (exl3r_rms_norm_had).
+constexpr int HAD_OUT = 1;   // rotated f16 outputs, one per projection
+constexpr int HAD_IN = 2;    // x rotated on load
 
 // RMS_GATED gate activation in fp32.
 __device__ __forceinline__ float gate_act(int gact, float g) { return gact ? act_f<ACT_SIGMOID>(g) : act_f<ACT_SILU>(g); }
@@ -150,7 +158,7 @@ using RmsCache = std::conditional_t<MODE == RMS_RES_IN, RT, XT>;
 // Pass 1 of the 8-element chunk at element e of a row: clamp (f16 x), residual update (RES_IN),
 // gathered-row copy (GATHER), gate before the norm (GATED), and the chunk's squares added to ss
 // (fp64: squares and sums of 16-bit data are exact).  Returns the chunk's cached form.
-template <class XT, class RT, int MODE>
+template <class XT, class RT, int MODE, int HAD = 0>
 __device__ __forceinline__ typename RmsCache<XT, RT, MODE>::Vec rms_chunk1(const RmsArgs& a, char* rrow, int64_t e,
                                                                           bool valid, typename XT::Vec& xv,
                                                                           const typename RT::Vec& rv, double& ss)
@@ -158,6 +166,23 @@ __device__ __forceinline__ typename RmsCache<XT, RT, MODE>::Vec rms_chunk1(const
     using CT = RmsCache<XT, RT, MODE>;
     typename CT::Vec cv;
     float h[8];
+    if constexpr ((HAD & HAD_IN) != 0)
+    {
+        // x = had_r_128(x, post = hxpost) as the projection's own output rotation rounds it: the
+        // fp32 butterfly, one rounding to f16, then the half post-scale product.  The chunk's
+        // 16-lane group is the 128-element block, as for the outputs.
+        static_assert(XT::code == DT_F16 && MODE != RMS_GATHER && MODE != RMS_GATED, "x rotation takes f16 x");
+        float f[8];
+        unpack8<TF16>(xv, f);
+        butterfly128(f, (int)((e >> 3) & 15), a.hxr);
+        xv = pack8<TF16>(f);
+        if (a.hxpost)
+        {
+            const TF16::Vec p = load8<TF16>(a.hxpost, e);
+            #pragma unroll
+            for (int q = 0; q < 4; ++q) xv.a[q] = hmul2(xv.a[q], p.a[q]);
+        }
+    }
     if (valid)
         unpack8<XT>(xv, h);
     else
@@ -210,7 +235,7 @@ __device__ __forceinline__ typename RmsCache<XT, RT, MODE>::Vec rms_chunk1(const
 
 // Pass 2 of the chunk at element e: gate (GATED), weight (row offset wofs), scale, gate after the
 // norm (GATED), one rounding, store.
-template <class XT, class YT, class RT, int MODE, bool HAD>
+template <class XT, class YT, class RT, int MODE, int HAD>
 __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* yrow, int64_t e, int64_t wofs,
                                            const typename RmsCache<XT, RT, MODE>::Vec& cv,
                                            const typename RT::Vec& rv, u32x4 wv, float rmf)
@@ -261,7 +286,7 @@ __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* 
         }
     }
     const typename YT::Vec yv = pack8<YT>(o);
-    if constexpr (!HAD) store8<YT>(yrow, e, yv);
+    if constexpr (!(HAD & HAD_OUT)) store8<YT>(yrow, e, yv);
     else
     {
         #pragma clang fp contract(off)
@@ -288,7 +313,7 @@ __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* 
     }
 }
 
-template <class XT, class YT, class RT, int MAXV, int MODE, bool HAD = false>
+template <class XT, class YT, class RT, int MAXV, int MODE, int HAD = 0>
 __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int tid, int nt, RowRegs<XT, RT, MAXV>& L,
                                            double* red)
 {
@@ -304,7 +329,7 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
     for (int k = 0; k < MAXV; ++k)
     {
         const int c = tid + k * nt;
-        if (c < nc) cache[k] = rms_chunk1<XT, RT, MODE>(a, rrow, (int64_t)c * 8, L.valid, L.xv[k], L.rv[k], ss);
+        if (c < nc) cache[k] = rms_chunk1<XT, RT, MODE, HAD>(a, rrow, (int64_t)c * 8, L.valid, L.xv[k], L.rv[k], ss);
     }
 
     // fp64 row sum (exact for 16-bit data), one rounding, IEEE fp32 sqrt and divide.
@@ -321,7 +346,7 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
     }
 }
 
-template <class XT, class YT, class RT, int MAXV, int MODE, bool HAD = false>
+template <class XT, class YT, class RT, int MAXV, int MODE, int HAD = 0>
 __device__ __forceinline__ void rms_row(const RmsArgs& a, int64_t row, int tid, int nt, double* red)
 {
     RowRegs<XT, RT, MAXV> L;
@@ -329,7 +354,7 @@ __device__ __forceinline__ void rms_row(const RmsArgs& a, int64_t row, int tid, 
     rms_finish<XT, YT, RT, MAXV, MODE, HAD>(a, row, tid, nt, L, red);
 }
 
-template <class XT, class YT, class RT, int MAXV, int MODE, bool HAD = false>
+template <class XT, class YT, class RT, int MAXV, int MODE, int HAD = 0>
 __global__ __launch_bounds__(1024) void k_rms_norm(RmsArgs a)
 {
     __shared__ double red[16];
@@ -379,7 +404,7 @@ __global__ __launch_bounds__(256) void k_rms_rows(RmsArgs a)
             ss = group_sum64<LPR>(ss);
             const float rmf = rms_factor(ss, a.dim, a.eps) * a.cs;
             if (act[i])
-                rms_chunk2<XT, YT, RT, MODE, false>(a, row, (char*)a.y + row * a.ldy * YT::bytes, e,
+                rms_chunk2<XT, YT, RT, MODE, 0>(a, row, (char*)a.y + row * a.ldy * YT::bytes, e,
                                                     weight_row<MODE>(a, row), cv, rv[i], wv[i], rmf);
         }
     }
@@ -505,7 +530,7 @@ inline RmsShape rms_shape(int nc, int64_t rows)
     return { 8, thr(8) };   // <= 1024 (rms_vec_ok bounds the row at 8192 chunks)
 }
 
-template <class XT, class YT, class RT, int MODE, bool HAD = false>
+template <class XT, class YT, class RT, int MODE, int HAD = 0>
 int launch_rms_vec(const RmsArgs& a, hipStream_t s)
 {
     const RmsShape sh = rms_shape(a.dim / 8, a.rows);

@@ -39,7 +39,7 @@ PROTOTYPES = {
     "exl3r_argmax_sample": (_i, [_vp, _i, _i64, _i64, _i64, _i, _vp, _vp]),
     "exl3r_gumbel_sample": (_i, [_vp, _i, _i64, _i64, _i64, _i, ctypes.c_uint32, _vp, _vp]),
     "exl3r_rms_norm_had": (_i, [_vp, _i, _i64, _vp, _i, _vp, _i, _i64, _vp, _i64, _i, _vp, _vp, _i64, _i64, _i64,
-                                _f, _f, _f, _f, _vp]),
+                                _f, _f, _f, _f, _i, _vp, _vp]),
     "exl3r_had_r_128": (_i, [_vp, _i, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _f, _vp]),
     "exl3r_act_mul_had": (_i, [_i, _vp, _vp, _i, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _f, _f, _vp]),
     "exl3r_gumbel_noise": (_i, [_vp, _i, _i64, _vp, _i, _i64, _i64, _i64, ctypes.c_uint32, _vp]),

@@ -289,9 +289,10 @@ def had_r_128(x, out, pre_scale=None, post_scale=None, scale=1.0, stream=None):
 
 
 def rms_norm_had(x, w, outs, pre_scales, eps, constant_bias=0.0, constant_scale=1.0, r=None, y=None, had_scale=1.0,
-                 stream=None):
+                 rotate_x=False, x_post_scale=None, stream=None):
     """One pass: y = RMSNorm(x) (or r += x; y = RMSNorm(r)) in f16, then outs[i] = had_r_128(y, pre_scales[i])
-    for each projection (1..4 f16 outputs shaped like x; y is written only if given)."""
+    for each projection (1..4 f16 outputs shaped like x; y is written only if given).  rotate_x: x (f16) is
+    first taken through its producer's output rotation had_r_128(x, post_scale=x_post_scale)."""
     rows, dim, ldx = _rows(x)
     if not 1 <= len(outs) <= 4 or len(pre_scales) != len(outs):
         raise ValueError("1..4 outputs, one pre_scale (or None) each")
@@ -311,7 +312,7 @@ def rms_norm_had(x, w, outs, pre_scales, eps, constant_bias=0.0, constant_scale=
     check(load().exl3r_rms_norm_had(_ptr(x), dtype_code(x), ldx, _ptr(w), dtype_code(w) if w is not None else F16,
                                     _ptr(r), dtype_code(r) if r is not None else F16, ldr, _ptr(y), ldy, len(outs),
                                     pre, out, ldo, rows, dim, eps, constant_bias, constant_scale, float(had_scale),
-                                    _stream(x, stream)))
+                                    1 if rotate_x else 0, _ptr(x_post_scale), _stream(x, stream)))
 
 
 ACT_CODES = {"silu": 0, "gelu": 1, "mul_sigmoid": 2}

@@ -272,7 +272,8 @@ void had_r_128(const Tensor& x, const Tensor& out, const Tensor* pre_scale, cons
 
 void rms_norm_had(const Tensor& x, const Tensor* w, const Tensor* r, const Tensor* y,
                   const std::vector<const Tensor*>& outs, const std::vector<const Tensor*>& pre_scales, float eps,
-                  float constant_bias, float constant_scale, float had_scale, const Stream& s)
+                  float constant_bias, float constant_scale, float had_scale, const Stream& s, bool rotate_x,
+                  const Tensor* x_post_scale)
 {
     int64_t rows, dim, ldx, ldr = 0, ldy = 0, ldo = -1;
     x.rows_view(rows, dim, ldx);
@@ -306,7 +307,7 @@ void rms_norm_had(const Tensor& x, const Tensor* w, const Tensor* r, const Tenso
     check_abi(exl3r_rms_norm_had(x.data, code(x.dtype), ldx, ptr(w), code_or(w, DType::F16), r ? r->data : nullptr,
                                  r ? code(r->dtype) : EXL3R_F16, ldr, y ? y->data : nullptr, ldy, (int)outs.size(),
                                  pre.data(), out.data(), ldo, rows, dim, eps, constant_bias, constant_scale, had_scale,
-                                 s.get()));
+                                 rotate_x ? 1 : 0, ptr(x_post_scale), s.get()));
 }
 
 void act_mul_had(HadAct act, const Tensor& x, const Tensor& y, const Tensor& out, const Tensor* pre_scale,

@@ -168,10 +168,12 @@ void had_r_128(const Tensor& x, const Tensor& out, const Tensor* pre_scale, cons
                const Stream& s);
 // RMSNorm (r == nullptr) or residual RMSNorm (r += x) whose f16 output feeds had_r_128(y, pre_scales[i]) of
 // 1..4 projections (src/modules.rs:372-411 then 224-227), in one pass; outs are f16 like x; y (f16) is
-// written only when given; pre_scales[i] may be null.
+// written only when given; pre_scales[i] may be null.  rotate_x: f16 x is first taken through its
+// producer's output rotation had_r_128(x, post_scale = x_post_scale) (src/modules.rs:231).
 void rms_norm_had(const Tensor& x, const Tensor* w, const Tensor* r, const Tensor* y,
                   const std::vector<const Tensor*>& outs, const std::vector<const Tensor*>& pre_scales, float eps,
-                  float constant_bias, float constant_scale, float had_scale, const Stream& s);
+                  float constant_bias, float constant_scale, float had_scale, const Stream& s,
+                  bool rotate_x = false, const Tensor* x_post_scale = nullptr);
 // Gated activation whose f16 output feeds the next projection's had_r_128(z, pre_scale)
 // (src/modules.rs:932-940 then 224-227): silu(x) * y, gelu(x) * y or x * sigmoid(y); z kept when given.
 enum class HadAct : int { Silu = EXL3R_ACT_SILU, Gelu = EXL3R_ACT_GELU, MulSigmoid = EXL3R_ACT_MUL_SIGMOID };

@@ -309,14 +309,18 @@ EXL3R_API int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out, 
  *              exl3r_rms_norm_res_in; y is f16 and written only when y != NULL (row stride ldy);
  *   outs[i] = had_r_128(y, pre_scales[i]) with scale had_scale, f16 [rows, dim] at row stride ldo;
  *              pre_scales[i] is f16 [dim] (the projection's suh) or NULL.
+ *   rotate_x != 0: x (f16, the raw output of the previous EXL3 projection) is first replaced by that
+ *              projection's output rotation had_r_128(x, x, NULL, x_post_scale, 1.0)
+ *              (src/modules.rs:231; x_post_scale is its f16 [dim] svh, or NULL); x is not written.
  * dim % 128 == 0; n_out in 1..4; outputs alias nothing.  Results are bit-identical to the unfused
- * calls.  Rows that are not 16-byte aligned run the unfused calls (the norm goes to y, or to outs[0]).
+ * calls.  Rows that are not 16-byte aligned run the unfused calls (the rotated x and the norm go
+ * to y or to outs[0]).
  */
 EXL3R_API int exl3r_rms_norm_had(const void* x, int x_dtype, int64_t ldx, const void* w, int w_dtype,
                        void* r, int r_dtype, int64_t ldr, void* y, int64_t ldy,
                        int n_out, const void* const* pre_scales, void* const* outs, int64_t ldo,
                        int64_t rows, int64_t dim, float eps, float constant_bias, float constant_scale,
-                       float had_scale, void* stream);
+                       float had_scale, int rotate_x, const void* x_post_scale, void* stream);
 
 /*
  * Gated activation whose f16 output feeds the random-Hadamard input rotation of the next EXL3

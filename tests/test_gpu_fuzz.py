@@ -198,10 +198,12 @@ def test_fuzz_hadamard(case):
     run_had(x, dt, pre=s if mode == "pre" else None, post=s if mode == "post" else None,
             scale=float(pick(rng, [1.0, 0.5, 1.7])), what=f"fuzz had {rows}x{cols}+{pad} dt{dt} {mode}")
     n_out = int(rng.integers(1, 5))
-    run_norm_had(int(rng.integers(1, 300)), 128 * int(rng.integers(1, 40)), pick(rng, FLOATS),
+    rot = bool(rng.random() < 0.4)
+    run_norm_had(int(rng.integers(1, 300)), 128 * int(rng.integers(1, 40)), F16 if rot else pick(rng, FLOATS),
                  pick(rng, [None, F32, F16, BF16]), pick(rng, FLOATS), n_out=n_out, with_y=bool(rng.random() < 0.5),
                  cb=float(pick(rng, [0.0, 1.0])), had_scale=float(pick(rng, [1.0, 0.25])),
-                 pre_none=tuple(i for i in range(n_out) if rng.random() < 0.3), seed=case + 3)
+                 pre_none=tuple(i for i in range(n_out) if rng.random() < 0.3), seed=case + 3, rotate_x=rot,
+                 svh=bool(rng.random() < 0.8))
     run_act_had(pick(rng, ["silu", "gelu", "mul_sigmoid"]), int(rng.integers(1, 300)), 128 * int(rng.integers(1, 80)),
                 pick(rng, FLOATS), with_z=bool(rng.random() < 0.6), pre=bool(rng.random() < 0.8),
                 ld=None if rng.random() < 0.7 else 128 * int(rng.integers(81, 90)) + int(pick(rng, [0, 8, 3])), seed=case + 5)

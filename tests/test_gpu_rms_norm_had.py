@@ -1,7 +1,8 @@
 """GPU parity of exl3r_rms_norm_had (RMSNorm, optionally with the residual add, feeding the
 random-Hadamard input rotation of up to four EXL3 projections in one pass) against the oracle
-composition -- oracle_rms_norm to an f16 y, then oracle_had_r_128 per projection -- bit for bit,
-and against the unfused GPU calls: the Qwen3 attention-input case (f16 x, f32 residual, three
+composition -- oracle_rms_norm to an f16 y, then oracle_had_r_128 per projection, after
+oracle_had_r_128(x, post=svh) when x is rotated on load -- bit for bit, and against the unfused GPU
+calls: the Qwen3 attention-input case (f16 x, f32 residual, three
 projections), plain norms, Qwen3.5's constant bias, a scalar transform scale, the unaligned fallback
 with and without y, zero rows and the argument errors."""
 import numpy as np
@@ -23,7 +24,8 @@ def suh(dim, seed):
     return torch.from_numpy(np.where(rng.random(dim) < 0.5, -1.0, 1.0).astype(np.float16)).cuda()
 
 
-def run(rows, dim, xt, rt=None, wt=F16, n_out=3, with_y=True, cb=0.0, had_scale=1.0, ld=None, seed=0, pre_none=()):
+def run(rows, dim, xt, rt=None, wt=F16, n_out=3, with_y=True, cb=0.0, had_scale=1.0, ld=None, seed=0, pre_none=(),
+        rotate_x=False, svh=True):
     ld = ld or dim
     x = dev_normal((rows, ld), 0, 1, xt, seed)[:, :dim]
     r = dev_normal((rows, ld), 0, 4, rt, seed + 1)[:, :dim] if rt is not None else None
@@ -34,11 +36,15 @@ def run(rows, dim, xt, rt=None, wt=F16, n_out=3, with_y=True, cb=0.0, had_scale=
     xh = np.ascontiguousarray(from_dev(x))
     rh = np.ascontiguousarray(from_dev(r)).copy() if r is not None else None
     wh = from_dev(w)
-    ffi.rms_norm_had(x, w, outs, pres, 1e-6, cb, 1.0, r=r, y=y, had_scale=had_scale)
+    xsv = suh(dim, seed + 30) if rotate_x and svh else None
+    ffi.rms_norm_had(x, w, outs, pres, 1e-6, cb, 1.0, r=r, y=y, had_scale=had_scale, rotate_x=rotate_x,
+                     x_post_scale=xsv)
     torch.cuda.synchronize()
+    if rotate_x:      # the producer's output rotation, had_r_128(x, x, None, svh), before the norm
+        xh = orc.had_r_128(xh, F16, post=from_dev(xsv) if xsv is not None else None, nthreads=NTHREADS)
     ey = orc.rms_norm(xh, xt, wh, wt, F16, 1e-6, cb, 1.0, r=rh, rt=rt if rt is not None else F32, nthreads=NTHREADS) \
         if r is not None else orc.rms_norm(xh, xt, wh, wt, F16, 1e-6, cb, 1.0, nthreads=NTHREADS)
-    tag = f"norm_had {rows}x{dim} x{xt} r{rt} out{n_out} y{int(with_y)}"
+    tag = f"norm_had {rows}x{dim} x{xt} r{rt} out{n_out} y{int(with_y)} rot{int(rotate_x)}"
     if with_y:
         assert_bitwise(from_dev(y), ey, what=tag + " y")
     if r is not None:
@@ -62,6 +68,22 @@ def test_dtypes_plain_and_residual(xt, rt, wt):
 
 def test_four_outputs_bias_scale_and_missing_pre():
     run(33, 2048, F16, F32, n_out=4, cb=1.0, had_scale=0.5, pre_none=(1,), seed=3)
+
+
+def test_rotated_input_qwen3_layer_boundary():
+    """o_proj / down_proj output (raw f16, before its svh rotation) into the f32 residual, then the
+    next norm's three projection inputs: one pass for had(svh) -> residual add -> norm -> 3 x had(suh)."""
+    run(2048, 5120, F16, F32, n_out=3, with_y=False, rotate_x=True, seed=11)
+
+
+@pytest.mark.parametrize("rt", [None, F32, F16, BF16])
+def test_rotated_input_variants(rt):
+    run(45, 1024, F16, rt, F32, n_out=2, with_y=True, rotate_x=True, svh=rt != F16, cb=1.0, seed=12)
+
+
+def test_rotated_input_unaligned_fallback():
+    run(9, 256, F16, F32, n_out=2, with_y=False, ld=259, rotate_x=True, seed=13)
+    run(9, 256, F16, None, n_out=1, with_y=True, ld=259, rotate_x=True, seed=14)
 
 
 def test_unaligned_fallback():
@@ -103,4 +125,9 @@ def test_zero_rows_and_errors():
         ffi.rms_norm_had(x, None, [o] * 5, [None] * 5, 1e-6)
     with pytest.raises(exl3r.Exl3rError):
         ffi.rms_norm_had(x, None, [o, o], [None, None], 1e-6)          # outputs alias each other
+    with pytest.raises(exl3r.Exl3rError):
+        xb = x.to(torch.bfloat16)
+        ffi.rms_norm_had(xb, None, [o], [None], 1e-6, rotate_x=True)   # the rotation takes f16 x
+    with pytest.raises(exl3r.Exl3rError):
+        ffi.rms_norm_had(x, None, [o], [None], 1e-6, x_post_scale=suh(256, 1))   # post-scale without rotate_x
     torch.cuda.synchronize()
