@@ -35,7 +35,7 @@ OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "
        "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
        "deinterleave_q35", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
        "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_unfused", "silu_had_c3",
-       "silu_had_c3_unfused", "calib_copy",
+       "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_unfused", "calib_copy",
        "calib_copy_cached"]
 
 
@@ -133,6 +133,39 @@ def make_act(name, rows, cols, dt, act, seed):
         g, u, z = bufs[i % sets]
         fn(g, u, z)
     return Work(name, nbytes, launch, f"{act.upper()}(gate)*up [{rows},{cols}] {str(dt).split('.')[-1]}", sets)
+
+
+def make_rope_had(name, pos, hq, hk, hd, fused, seed=330):
+    """C4 prefill q/k on the raw f16 projection outputs: each projection's output rotation
+    had_r_128(y, y, None, svh) (src/modules.rs:231), then head-norm + NeoX RoPE, in place.  One fused
+    launch (exl3r_rope_had), or two had_r_128 launches and exl3r_rope.  Both count the fused job's bytes
+    (C4's RoPE bytes plus both svh vectors)."""
+    import numpy as np
+    import torch
+    import exl3r
+    import exl3r.ffi as ffi
+    T = pos.size
+    nbytes = 2 * T * (hq + hk) * hd * 2 + 4 * T + 2 * hd * 2 + (hd // 2) * 4 + (hq + hk) * hd * 2
+    sets = sets_for(nbytes)
+    inv = torch.from_numpy((1.0 / 1e6 ** (np.arange(0, hd, 2, dtype=np.float64) / hd)).astype(np.float32)).cuda()
+    qn, kn = gen((hd,), 1.0, 0.1, torch.float16, seed + 50), gen((hd,), 1.0, 0.1, torch.float16, seed + 51)
+    qs = torch.where(torch.rand(hq * hd, device="cuda") < 0.5, -1.0, 1.0).to(torch.float16)
+    ks = torch.where(torch.rand(hk * hd, device="cuda") < 0.5, -1.0, 1.0).to(torch.float16)
+    pid = torch.from_numpy(pos).cuda().view(1, -1)
+    bufs = [(gen((1, T, hq, hd), 0.0, 1.0, torch.float16, seed + 2 * k),
+             gen((1, T, hk, hd), 0.0, 1.0, torch.float16, seed + 2 * k + 1)) for k in range(sets)]
+
+    def launch(i):
+        q, k = bufs[i % sets]
+        if fused:
+            ffi.rope_had(q, q, k, k, inv, 0, None, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, q_post_scale=qs,
+                         k_post_scale=ks, position_ids=pid)
+        else:
+            ffi.had_r_128(q.view(T, hq * hd), q.view(T, hq * hd), None, qs)
+            ffi.had_r_128(k.view(T, hk * hd), k.view(T, hk * hd), None, ks)
+            ffi.rope(q, q, k, k, inv, 0, None, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, position_ids=pid)
+    kind = "fused" if fused else "unfused (2 had_r_128 + rope)"
+    return Work(name, nbytes, launch, f"q/k output rotation + head-norm + NeoX RoPE T={T} heads {hq}/{hk}, {kind}", sets)
 
 
 def make_rope(name, pos, hq, hk, hd, R, mode, dt, seed, bsz=1, per_seq=False):
@@ -502,6 +535,8 @@ def make_all(only=None):
         "norm_had_c3_unfused": lambda: make_norm_had("norm_had_c3_unfused", 8192, 5120, False),
         "norm_had_rot_c3": lambda: make_norm_had("norm_had_rot_c3", 8192, 5120, True, rotate=True),
         "norm_had_rot_c3_unfused": lambda: make_norm_had("norm_had_rot_c3_unfused", 8192, 5120, False, rotate=True),
+        "rope_had_c4": lambda: make_rope_had("rope_had_c4", ragged, 64, 8, 128, True),
+        "rope_had_c4_unfused": lambda: make_rope_had("rope_had_c4_unfused", ragged, 64, 8, 128, False),
         "silu_had_c3": lambda: make_act_had("silu_had_c3", 8192, 17408, True),
         "silu_had_c3_unfused": lambda: make_act_had("silu_had_c3_unfused", 8192, 17408, False),
         "calib_copy": lambda: make_copy("calib_copy"),

@@ -23,6 +23,7 @@
 // through LDS.
 #include "abi.hpp"
 #include "common.cuh"
+#include "hadamard.cuh"
 
 namespace exl3r {
 
@@ -61,6 +62,10 @@ struct RopeArgs
     const int32_t* block_table;
     const int32_t* cache_seqlens;
     int32_t* err;
+    // Output rotation of the q / k projections (exl3r_rope_had): each 128-element head is first
+    // replaced by had_r_128(head) times its f16 post-scale (svh; nullptr: none).
+    const void* q_post;
+    const void* k_post;
 };
 
 // Head kinds of the item space [0, hq) q, [hq, hq + hk) k, [hq + hk, hq + hk + hv) v.
@@ -472,7 +477,24 @@ struct RopeBatch
     int b;
 };
 
-template <class IO, int MODE, int LPH, int HPL, int NORM, bool APPEND>
+// The q / k projection's output rotation of one 128-element head held by 16 lanes (e0 = 8 * lane):
+// had_r_128(v) * post as hadamard.hip rounds it -- the fp32 butterfly, one rounding to f16, then the
+// half post-scale product.
+__device__ __forceinline__ void head_out_rotation(TF16::Vec& v, const void* post, int64_t col)
+{
+    float f[8];
+    unpack8<TF16>(v, f);
+    butterfly128(f, (int)((col >> 3) & 15), 0.0883883461356163f);
+    v = pack8<TF16>(f);
+    if (post)
+    {
+        const TF16::Vec p = load8<TF16>(post, col);
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) v.a[q] = hmul2(v.a[q], p.a[q]);
+    }
+}
+
+template <class IO, int MODE, int LPH, int HPL, int NORM, bool APPEND, bool HADR = false>
 __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
 {
     extern __shared__ float2 cs[];            // [4 waves][R / 2]
@@ -531,6 +553,13 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
                 for (int j = 0; j < 4; ++j) t.v[i].a[j] = 0;
             }
             const int kd = t.isq[i] ? KIND_Q : t.isv[i] ? KIND_V : KIND_K;
+            if constexpr (HADR)
+            {
+                // A head is one rotation block: head_dim 128, 16 lanes, all active or all not (a
+                // padding head past the last one has no post-scale entries and is left alone).
+                static_assert(IO::code == DT_F16 && LPH == 16 && !APPEND, "output rotation: f16 heads of 128");
+                if (t.act[i]) head_out_rotation(t.v[i], t.isq[i] ? a.q_post : a.k_post, (int64_t)t.hidx[i] * 128 + e0);
+            }
             rope_head<IO, MODE, LPH, NORM>(a, t.v[i], kd != KIND_V, select_w<NORM>(kd == KIND_Q, wq, wk), c, s, e0, l64);
             if (!t.act[i]) continue;
             if (!APPEND)
@@ -686,12 +715,14 @@ static void launch_rope_lph(RopeArgs a, int iters, hipStream_t s)
 // token per wave (38.5 us; 3 per lane 42 us); bf16 heads (fp32 norm) with 3 per lane on a
 // persistent grid of 4 workgroups per CU (37.0 us; 2 per lane 42 us).  With the paged append
 // (4096 tokens, + 8 v heads) 3 per lane: 40.0 us, 2 per lane 41-43 us.
-template <class IO, int MODE, int LPH, int NORM>
+template <class IO, int MODE, int LPH, int NORM, bool HADR = false>
 static void launch_rope_tok(RopeArgs a, hipStream_t s)
 {
     const Tuning& tu = tuning();
-    int hpl = IO::code == DT_F16 && !a.kc ? 2 : 3;
-    int wgs_per_cu = IO::code == DT_F16 ? 0 : 4;
+    // With the output rotation (HADR; C4 shape: 62.1 us against 66.6 us with the plain kernel's
+    // shape) the kernel takes the bf16 shape: 3 heads per lane, 4 workgroups per CU.
+    int hpl = IO::code == DT_F16 && !a.kc && !HADR ? 2 : 3;
+    int wgs_per_cu = IO::code == DT_F16 && !HADR ? 0 : 4;
     if (tu.rope_hpl > 0) hpl = tu.rope_hpl;
     if (tu.rope_wgs_per_cu > 0) wgs_per_cu = tu.rope_wgs_per_cu;
     hpl = hpl <= 2 ? 2 : 3;
@@ -701,12 +732,15 @@ static void launch_rope_tok(RopeArgs a, hipStream_t s)
     const size_t lds = 4 * (size_t)(a.R / 2) * sizeof(float2);
     auto go = [&](auto H) {
         constexpr int HP = decltype(H)::value;
-        if (a.kc) k_rope_tok<IO, MODE, LPH, HP, NORM, true><<<(unsigned)blocks, 256, lds, s>>>(a);
+        if constexpr (HADR) k_rope_tok<IO, MODE, LPH, HP, NORM, false, true><<<(unsigned)blocks, 256, lds, s>>>(a);
+        else if (a.kc) k_rope_tok<IO, MODE, LPH, HP, NORM, true><<<(unsigned)blocks, 256, lds, s>>>(a);
         else k_rope_tok<IO, MODE, LPH, HP, NORM, false><<<(unsigned)blocks, 256, lds, s>>>(a);
     };
     if (hpl == 2) go(std::integral_constant<int, 2>{});
     else go(std::integral_constant<int, 3>{});
 }
+
+static bool rope_tok_launch(const RopeArgs& a);
 
 // Prefill-sized NeoX launches (a wave per token still gives every CU several waves) take the
 // wave-per-token kernel.  GPT-J (C4 at rotary 64: 35.2 us flattened vs 37.5 us per token) and
@@ -725,7 +759,7 @@ static void launch_rope_vec(const RopeArgs& a, int lph, hipStream_t s)
     }
     if constexpr (MODE == EXL3R_ROPE_NEOX)
     {
-        if (tu.rope_tok == 2 || (tu.rope_tok == 0 && a.tokens >= 1024))
+        if (rope_tok_launch(a))
         {
             if (lph == 8) launch_rope_tok<IO, MODE, 8, NORM>(a, s);
             else if (lph == 16) launch_rope_tok<IO, MODE, 16, NORM>(a, s);
@@ -805,20 +839,45 @@ static int rope_prepare(const char* op, RopeArgs& a, const void* q, void* out_q,
     return EXL3R_OK;
 }
 
-static int rope_dispatch(const char* op, const RopeArgs& a, int dtype, int rope_mode, void* stream)
+static int rope_norm_kind(const RopeArgs& a, int dtype)
 {
-    const int norm = !a.qw ? NORM_NONE : (a.wt == EXL3R_F16 && dtype == EXL3R_F16) ? NORM_HALF : NORM_F32;
-    hipStream_t s = (hipStream_t)stream;
-    auto a16 = [](const void* p) { return p == nullptr || aligned16(p); };
+    return !a.qw ? NORM_NONE : (a.wt == EXL3R_F16 && dtype == EXL3R_F16) ? NORM_HALF : NORM_F32;
+}
+
+static int rope_lph(const RopeArgs& a)
+{
     int lph = 1;
     while (lph * 8 < a.hd) lph *= 2;
-    // Vector kernels: 8-element lane chunks, 8 to 32 lanes per head (head_dim 64 .. 256).
+    return lph;
+}
+
+// Vector kernels: 8-element lane chunks, 8 to 32 lanes per head (head_dim 64 .. 256), 16-byte
+// aligned rows and heads.
+static bool rope_vec_ok(const RopeArgs& a, int rope_mode)
+{
+    auto a16 = [](const void* p) { return p == nullptr || aligned16(p); };
+    const int lph = rope_lph(a);
     bool vec = a.hd % 8 == 0 && lph >= 8 && lph <= 32 && a.R % (rope_mode == EXL3R_ROPE_NEOX ? 16 : 2) == 0;
     vec = vec && aligned16(a.q) && aligned16(a.oq) && a.q_ts % 8 == 0 && a.q_hs % 8 == 0;
     vec = vec && (!a.k || (aligned16(a.k) && a16(a.ok) && a.k_ts % 8 == 0 && a.k_hs % 8 == 0));
     vec = vec && (!a.v || (aligned16(a.v) && a.v_ts % 8 == 0 && a.v_hs % 8 == 0 && a16(a.kc) && a16(a.vc)));
     vec = vec && (!a.qw || (aligned16(a.qw) && a16(a.kw)));
-    if (vec)
+    return vec;
+}
+
+// Prefill-sized NeoX launches take the wave-per-token kernel (launch_rope_vec).
+static bool rope_tok_launch(const RopeArgs& a)
+{
+    const Tuning& tu = tuning();
+    return tu.rope_tok == 2 || (tu.rope_tok == 0 && a.tokens >= 1024);
+}
+
+static int rope_dispatch(const char* op, const RopeArgs& a, int dtype, int rope_mode, void* stream)
+{
+    const int norm = rope_norm_kind(a, dtype);
+    hipStream_t s = (hipStream_t)stream;
+    const int lph = rope_lph(a);
+    if (rope_vec_ok(a, rope_mode))
     {
         if (dtype == EXL3R_F16) launch_rope_io<TF16>(a, rope_mode, norm, lph, s);
         else launch_rope_io<TBF16>(a, rope_mode, norm, lph, s);
@@ -917,4 +976,57 @@ extern "C" int exl3r_rope_table(const void* q, void* out_q, int64_t q_tok_stride
     a.table_bstride = table_batch_stride;
     a.err = err_flag;
     return rope_dispatch(op, a, dtype, rope_mode, stream);
+}
+
+extern "C" int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out, int64_t ldo, int64_t rows,
+                               int64_t cols, const void* pre_scale, const void* post_scale, float scale, void* stream);
+
+// exl3r_rope with the q / k projections' output rotation first (Linear::forward's
+// had_r_128(y, y, None, svh), src/modules.rs:231, then RoPE::apply on y).  Prefill-sized NeoX launches
+// of f16 heads of 128 run it inside the wave-per-token kernel; anything else runs the rotations into
+// out_q / out_k and exl3r_rope in place there.
+extern "C" int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, int num_heads_q,
+                              const void* k, void* out_k, int64_t k_tok_stride, int num_heads_k,
+                              int dtype, int64_t bsz, int64_t seq_len, int head_dim,
+                              const float* inv_freq, int rotary_dim,
+                              int32_t position, const int32_t* positions, const int32_t* position_ids,
+                              const void* q_norm, const void* k_norm, int norm_dtype,
+                              float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
+                              const void* q_post_scale, const void* k_post_scale, void* stream)
+{
+    const char* op = "exl3r_rope_had";
+    if (dtype != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: the rotated projection outputs are f16", op);
+    if (head_dim <= 0 || ((int64_t)num_heads_q * head_dim) % 128 || (k && ((int64_t)num_heads_k * head_dim) % 128))
+        return set_error(EXL3R_EINVAL, "%s: heads * head_dim must be a multiple of 128", op);
+    if (!k && (out_k || k_post_scale)) return set_error(EXL3R_EINVAL, "%s: out_k / k_post_scale without k", op);
+    RopeArgs a;
+    int rc = rope_prepare(op, a, q, out_q, q_tok_stride, head_dim, num_heads_q, k, out_k, false, k_tok_stride, head_dim,
+                          num_heads_k, dtype, bsz, seq_len, head_dim, inv_freq, rotary_dim, position, positions,
+                          position_ids, q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias, rope_mode, attn_factor);
+    if (rc || a.tokens == 0) return rc;
+    a.q_post = q_post_scale;
+    a.k_post = k_post_scale;
+    const bool fused = head_dim == 128 && rope_mode == EXL3R_ROPE_NEOX && rope_vec_ok(a, rope_mode) &&
+                       rope_tok_launch(a) && (!q_post_scale || aligned16(q_post_scale)) &&
+                       (!k_post_scale || aligned16(k_post_scale));
+    if (fused)
+    {
+        hipStream_t s = (hipStream_t)stream;
+        const int norm = rope_norm_kind(a, dtype);
+        if (norm == NORM_NONE) launch_rope_tok<TF16, EXL3R_ROPE_NEOX, 16, NORM_NONE, true>(a, s);
+        else if (norm == NORM_HALF) launch_rope_tok<TF16, EXL3R_ROPE_NEOX, 16, NORM_HALF, true>(a, s);
+        else launch_rope_tok<TF16, EXL3R_ROPE_NEOX, 16, NORM_F32, true>(a, s);
+        return launch_status(op);
+    }
+    const int64_t tokens = a.tokens;
+    rc = exl3r_had_r_128(q, EXL3R_F16, q_tok_stride, out_q, q_tok_stride, tokens, (int64_t)num_heads_q * head_dim,
+                         nullptr, q_post_scale, 1.0f, stream);
+    if (rc == EXL3R_OK && k)
+        rc = exl3r_had_r_128(k, EXL3R_F16, k_tok_stride, out_k, k_tok_stride, tokens, (int64_t)num_heads_k * head_dim,
+                             nullptr, k_post_scale, 1.0f, stream);
+    if (rc != EXL3R_OK) return rc;
+    return exl3r_rope(out_q, out_q, q_tok_stride, head_dim, num_heads_q, k ? out_k : nullptr, k ? out_k : nullptr,
+                      k_tok_stride, head_dim, num_heads_k, dtype, bsz, seq_len, head_dim, inv_freq, rotary_dim, position,
+                      positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias, rope_mode,
+                      attn_factor, stream);
 }

@@ -201,6 +201,36 @@ def rope(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm
                             norm_eps, norm_constant_bias, rope_mode, attn_factor, _stream(q, stream)))
 
 
+def rope_had(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias,
+             rope_mode, attn_factor, q_post_scale=None, k_post_scale=None, position_ids=None, stream=None):
+    """rope() on the raw f16 outputs of the q / k projections, each first given its projection's output
+    rotation had_r_128(y, y, None, svh) (src/modules.rs:231).  q, k: (bsz, seq_len, heads, head_dim) with
+    heads packed; q_post_scale / k_post_scale: f16 [heads * head_dim] or None."""
+    if q.dim() != 4:
+        raise ValueError("q must be (bsz, seq_len, heads, head_dim)")
+    bsz, seq, hq, hd = q.shape
+    if q.stride(3) != 1 or q.stride(2) != hd or out_q.stride() != q.stride() or out_q.shape != q.shape:
+        raise ValueError("q heads must be packed and out_q must share q's layout")
+    if seq > 1 and bsz > 1 and q.stride(0) != seq * q.stride(1):
+        raise ValueError("q batch stride must be seq_len * token stride")
+    hk, k_ts = 0, 0
+    if k is not None:
+        if k.dim() != 4 or k.shape[:2] != q.shape[:2] or k.shape[3] != hd or k.stride(3) != 1 or k.stride(2) != hd:
+            raise ValueError("k must be (bsz, seq_len, kv_heads, head_dim) with packed heads")
+        if out_k is None or out_k.stride() != k.stride() or out_k.shape != k.shape:
+            raise ValueError("out_k must share k's layout")
+        if seq > 1 and bsz > 1 and k.stride(0) != seq * k.stride(1):
+            raise ValueError("k batch stride must be seq_len * token stride")
+        hk, k_ts = k.shape[2], k.stride(1)
+    nw = q_norm if q_norm is not None else k_norm
+    check(load().exl3r_rope_had(_ptr(q), _ptr(out_q), q.stride(1), hq, _ptr(k), _ptr(out_k), k_ts, hk,
+                                dtype_code(q), bsz, seq, hd, _ptr(inv_freq), inv_freq.shape[-1] * 2,
+                                int(position), _ptr(positions), _ptr(position_ids),
+                                _ptr(q_norm), _ptr(k_norm), dtype_code(nw) if nw is not None else F16,
+                                norm_eps, norm_constant_bias, rope_mode, attn_factor, _ptr(q_post_scale),
+                                _ptr(k_post_scale), _stream(q, stream)))
+
+
 def rope_paged_kv(q, out_q, k, out_k, v, inv_freq, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias,
                   rope_mode, attn_factor, k_cache, v_cache, block_table, cache_seqlens, position_ids=None,
                   err_flag=None, stream=None):

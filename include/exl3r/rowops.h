@@ -221,6 +221,25 @@ EXL3R_API int exl3r_rope_table(const void* q, void* out_q, int64_t q_tok_stride,
                      int32_t* err_flag, void* stream);
 
 /*
+ * exl3r_rope preceded by the q / k projections' output rotation, in one pass at prefill: the EXL3
+ * linear's had_r_128(y, y, NULL, svh, 1.0) (src/modules.rs:231) on each projection output, then
+ * RoPE::apply on it (src/rope.rs:233-260).  q, k: f16 [tokens, heads * head_dim] rows with heads
+ * packed (head stride = head_dim), heads * head_dim a multiple of 128; q_post_scale / k_post_scale:
+ * f16 [heads * head_dim] (the projections' svh) or NULL.  Other arguments as exl3r_rope.  q and k are
+ * only read when out_q / out_k differ from them.  Bit-identical to exl3r_had_r_128 on q and k
+ * followed by exl3r_rope.  NeoX, head_dim 128, 16-byte aligned, 1024 or more tokens: one fused
+ * launch; otherwise the rotations run into out_q / out_k and exl3r_rope in place there.
+ */
+EXL3R_API int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, int num_heads_q,
+                   const void* k, void* out_k, int64_t k_tok_stride, int num_heads_k,
+                   int dtype, int64_t bsz, int64_t seq_len, int head_dim,
+                   const float* inv_freq, int rotary_dim,
+                   int32_t position, const int32_t* positions, const int32_t* position_ids,
+                   const void* q_norm, const void* k_norm, int norm_dtype,
+                   float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
+                   const void* q_post_scale, const void* k_post_scale, void* stream);
+
+/*
  * exl3r_rope fused with the paged KV-cache append that follows it in paged attention
  * (Attention::forward, src/modules.rs:666-704: rope in place, then paged_kv_cache_update,
  * kernels/generator/cache.cu:143-243):
