@@ -402,6 +402,37 @@ void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* o
                          code_or(nw, DType::F16), norm_eps, norm_constant_bias, (int)rope_mode, attn_factor, s.get()));
 }
 
+void rope_had(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
+              int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
+              float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Tensor* q_post_scale,
+              const Tensor* k_post_scale, const Stream& s, const Tensor* position_ids)
+{
+    require(q.dim() == 4 && q.dtype == DType::F16, "rope_had: q must be f16 (bsz, seq_len, heads, head_dim)");
+    const int64_t bsz = q.size(0), seq = q.size(1), hd = q.size(3);
+    require(q.stride(3) == 1 && q.stride(2) == hd && out_q.strides == q.strides && out_q.shape == q.shape,
+            "rope_had: q heads must be packed and out_q must share q's layout");
+    require(bsz <= 1 || seq <= 1 || q.stride(0) == seq * q.stride(1), "rope_had: q batch stride must be seq_len * token stride");
+    int64_t hk = 0, kts = 0;
+    if (k)
+    {
+        require(out_k && k->dim() == 4 && k->size(0) == bsz && k->size(1) == seq && k->size(3) == hd &&
+                    k->stride(3) == 1 && k->stride(2) == hd && out_k->strides == k->strides,
+                "rope_had: k must be packed like q, out_k sharing its layout");
+        hk = k->size(2);
+        kts = k->stride(1);
+    }
+    require(inv_freq.dtype == DType::F32 && inv_freq.dim() == 1, "rope_had: inv_freq must be float32 [R/2]");
+    require(!positions || positions->dtype == DType::I32, "rope_had: positions must be int32");
+    require(!position_ids || position_ids->dtype == DType::I32, "rope_had: position_ids must be int32");
+    const Tensor* nw = q_norm ? q_norm : k_norm;
+    check_abi(exl3r_rope_had(q.data, out_q.data, q.stride(1), (int)q.size(2), k ? k->data : nullptr,
+                             out_k ? out_k->data : nullptr, kts, (int)hk, code(q.dtype), bsz, seq, (int)hd,
+                             (const float*)inv_freq.data, (int)(inv_freq.numel() * 2), (int32_t)position,
+                             (const int32_t*)ptr(positions), (const int32_t*)ptr(position_ids), ptr(q_norm),
+                             ptr(k_norm), code_or(nw, DType::F16), norm_eps, norm_constant_bias, (int)rope_mode,
+                             attn_factor, ptr(q_post_scale), ptr(k_post_scale), s.get()));
+}
+
 void rope_paged_kv(const Tensor& q, const Tensor& out_q, const Tensor& k, const Tensor* out_k, const Tensor& v,
                    const Tensor& inv_freq, int64_t position, const Tensor* positions, const Tensor* q_norm,
                    const Tensor* k_norm, float norm_eps, float norm_constant_bias, RopeStyle rope_mode, float attn_factor,

@@ -9,7 +9,7 @@
 //   exl3r::ffi::gated_rms_norm / mul_sigmoid_ / deinterleave_qg          <- src/ffi.rs:479-483, 616-624
 //   exl3r::ffi::rope_paged_kv                                            <- rope + paged append, src/modules.rs:666-704
 //   exl3r::ffi::argmax_sample / gumbel_sample / gumbel_noise             <- src/ffi.rs:521-535, src/generator.rs:1596
-//   exl3r::ffi::had_r_128 / rms_norm_had / act_mul_had                   <- src/ffi.rs:606-607, src/modules.rs:224-231
+//   exl3r::ffi::had_r_128 / rms_norm_had / act_mul_had / rope_had        <- src/ffi.rs:606-607, src/modules.rs:224-231
 //   exl3r::ffi::embedding                                                <- index_select, src/modules.rs:430-436
 //   exl3r::RmsNorm::forward / forward_res                                <- src/modules.rs:342-412
 //   exl3r::Embedding::forward                                            <- src/modules.rs:418-437
@@ -146,6 +146,13 @@ void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* o
           int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
           float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s,
           const Tensor* position_ids = nullptr, int32_t* err_flag = nullptr);
+// rope() on the raw f16 outputs of the q / k projections (heads packed), each first given its projection's
+// output rotation had_r_128(y, y, None, svh) (src/modules.rs:231); q_post_scale / k_post_scale are the
+// projections' f16 svh or null.
+void rope_had(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
+              int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
+              float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Tensor* q_post_scale,
+              const Tensor* k_post_scale, const Stream& s, const Tensor* position_ids = nullptr);
 // rope() fused with the paged KV-cache append that follows it in paged attention (src/modules.rs:666-704,
 // ffi.rs:337-350): the roped k (also written to out_k when given) and v go to k_cache / v_cache
 // [pages, page_size, kv_heads, head_dim] at cache_seqlens[b] + s through block_table [bsz, max_blocks].

@@ -368,6 +368,34 @@ int main()
         std::snprintf(msg, sizeof msg, "z max ulp %lld, rotation of z bitwise", (long long)u);
         report("ffi::act_mul_had silu -> had", ok, ok ? msg : "DIFFER");
     }
+    // rope_had: the q / k output rotations then head-norm + NeoX RoPE, equal to had_r_128 then rope.
+    {
+        const int T = 1100, hq = 4, hk = 2, hd = 128;
+        auto qh = host_normal(DType::F16, T * hq * hd, 0.f, 2.f), kh = host_normal(DType::F16, T * hk * hd, 0.f, 2.f);
+        auto nh = host_normal(DType::F16, hd, 1.f, 0.1f);
+        std::vector<uint8_t> sq(hq * hd * 2);
+        for (int i = 0; i < hq * hd; ++i)
+        {
+            const uint16_t v = (splitmix() & 1) ? 0xbc00 : 0x3c00;
+            std::memcpy(&sq[i * 2], &v, 2);
+        }
+        std::vector<float> fh(hd / 2);
+        for (int i = 0; i < hd / 2; ++i) fh[i] = (float)(1.0 / std::pow(1e6, 2.0 * i / hd));
+        std::vector<uint8_t> fb(fh.size() * 4);
+        std::memcpy(fb.data(), fh.data(), fb.size());
+        auto q = upload(qh, DType::F16, { 1, T, hq, hd }, s), k = upload(kh, DType::F16, { 1, T, hk, hd }, s);
+        auto q2 = upload(qh, DType::F16, { 1, T, hq, hd }, s), k2 = upload(kh, DType::F16, { 1, T, hk, hd }, s);
+        auto qn = upload(nh, DType::F16, { hd }, s), svq = upload(sq, DType::F16, { hq * hd }, s);
+        auto f = upload(fb, DType::F32, { hd / 2 }, s);
+        ffi::rope_had(q.t, q.t, &k.t, &k.t, f.t, 5, nullptr, &qn.t, &qn.t, 1e-6f, 0.f, RopeStyle::NeoX, 1.f, &svq.t,
+                      nullptr, s);
+        Tensor q2v(q2.t.data, DType::F16, { T, hq * hd }), k2v(k2.t.data, DType::F16, { T, hk * hd });
+        ffi::had_r_128(q2v, q2v, nullptr, &svq.t, 1.f, s);
+        ffi::had_r_128(k2v, k2v, nullptr, nullptr, 1.f, s);
+        ffi::rope(q2.t, q2.t, &k2.t, &k2.t, f.t, 5, nullptr, &qn.t, &qn.t, 1e-6f, 0.f, RopeStyle::NeoX, 1.f, s);
+        const bool ok = download(q, s) == download(q2, s) && download(k, s) == download(k2, s);
+        report("ffi::rope_had == had_r_128 + rope", ok, ok ? "bitwise" : "DIFFER");
+    }
     std::printf(failures ? "test_host_gpu: %d failures\n" : "test_host_gpu: all passed\n", failures);
     return failures ? 1 : 0;
 }

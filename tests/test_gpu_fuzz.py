@@ -21,6 +21,7 @@ from test_gpu_hadamard import run as run_had, scales
 from test_gpu_rms_norm import run_plain, run_res
 from test_gpu_rms_norm_had import run as run_norm_had
 from test_gpu_rope import run as run_rope
+from test_gpu_rope_had import run as run_rope_had
 from test_gpu_rope_paged import layout, run as run_paged
 from test_gpu_rope_table import run as run_rope_table
 
@@ -207,3 +208,18 @@ def test_fuzz_hadamard(case):
     run_act_had(pick(rng, ["silu", "gelu", "mul_sigmoid"]), int(rng.integers(1, 300)), 128 * int(rng.integers(1, 80)),
                 pick(rng, FLOATS), with_z=bool(rng.random() < 0.6), pre=bool(rng.random() < 0.8),
                 ld=None if rng.random() < 0.7 else 128 * int(rng.integers(81, 90)) + int(pick(rng, [0, 8, 3])), seed=case + 5)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_fuzz_rope_had(case):
+    rng = np.random.default_rng(9500 + case)
+    hd = int(pick(rng, [128, 128, 128, 64, 256]))
+    hq, hk = 2 * int(rng.integers(1, 20)), 2 * int(rng.integers(1, 4))
+    bsz = int(rng.integers(1, 3))
+    seq = int(pick(rng, [int(rng.integers(1, 64)), int(rng.integers(520, 1500))]))
+    R = int(pick(rng, [hd, hd, hd // 2]))
+    with_k = bool(rng.random() < 0.85)
+    run_rope_had(bsz, seq, hq, hk if with_k else 0, hd, R, pick(rng, [exl3r.ROPE_NEOX, exl3r.ROPE_NEOX, exl3r.ROPE_GPTJ]),
+                 nwt=pick(rng, FLOATS), norm=bool(rng.random() < 0.7), with_k=with_k, q_post=bool(rng.random() < 0.8),
+                 k_post=bool(rng.random() < 0.8), position=int(rng.integers(0, 30000)),
+                 out_of_place=bool(rng.random() < 0.3), seed=case)
