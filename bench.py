@@ -728,6 +728,15 @@ def main():
             "desc": "f16 logits; argmax vs torch.argmax (the generator's greedy path); Gumbel-max draw vs "
                     "softmax + multinomial (the reference sampler's tch path)"}
         log(f"sampling: {json.dumps(sampling)}")
+        hadamard = {"had_r_128_8192x5120_us": ops["had_c3"]["us"]}
+        for fused, label in (("norm_had_c3", "res_norm_to_3_inputs_8192x5120"),
+                             ("norm_had_rot_c3", "rotate_res_norm_to_3_inputs_8192x5120"),
+                             ("silu_had_c3", "silu_mul_to_input_8192x17408"), ("rope_had_c4", "qk_rotate_rope_c4")):
+            f_us, u_us = ops[fused]["us"], ops[fused + "_unfused"]["us"]
+            hadamard[label] = {"fused_us": f_us, "unfused_us": u_us, "speedup": round(u_us / f_us, 3)}
+        hadamard["desc"] = ("the EXL3 linear's random-Hadamard rotation (had_r_128) alone, and fused into the op that "
+                            "produces its input or consumes its output, vs the same calls one after another")
+        log(f"hadamard: {json.dumps(hadamard)}")
 
         # The timed step: config-3 prefill row ops back to back.
         step_works = [works["rms_c3"], works["silu_c3"], works["gelu_c3"]]
@@ -765,7 +774,7 @@ def main():
                    "io_dtype": "bf16", "tokens": 8192, "hidden": 5120, "intermediate": 17408,
                    "frac_peak": round(value / PEAK_GBS, 4)},
         "roofline": roof, "cpu_baseline": cpu, "ops": ops, "decode_step": decode, "c2_decode_rms_norm": c2,
-        "rope_paged_kv": rope_kv, "sampling": sampling,
+        "rope_paged_kv": rope_kv, "sampling": sampling, "hadamard": hadamard,
         "copy_reference": {"gbs": round(copy_gbs, 1), "frac_peak": round(copy_gbs / PEAK_GBS, 4),
                            "desc": "non-temporal 16 B/lane device copy of 1 GiB (read + write), the practical HBM ceiling reference"},
     }
