@@ -35,7 +35,8 @@ OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "
        "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
        "deinterleave_q35", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
        "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_unfused", "silu_had_c3",
-       "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_unfused", "calib_copy",
+       "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_unfused",
+       "rope_kv_had_prefill", "rope_kv_had_prefill_unfused", "calib_copy",
        "calib_copy_cached"]
 
 
@@ -223,10 +224,12 @@ def make_gather(name, vocab, hidden, n, dt, out_dt, ids, seed, norm=False):
     return Work(name, nbytes, launch, desc, sets)
 
 
-def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64):
+def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64, had=False):
     """q/k head-norm + NeoX RoPE followed by the paged KV-cache append (64 q / 8 kv heads of 128, f16,
     256-token pages, positions = cache lengths): one fused exl3r_rope_paged_kv launch, or exl3r_rope
-    then a separate append kernel (the reference's two launches)."""
+    then a separate append kernel (the reference's two launches).  With had, q / k / v are the raw
+    projection outputs and their output rotations had_r_128(y, y, None, svh) (src/modules.rs:231) come
+    first: one exl3r_rope_paged_kv_had launch, or three in-place rotations and the two launches."""
     import numpy as np
     import torch
     import exl3r
@@ -235,6 +238,8 @@ def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64):
     T = bsz * seq
     # fused-op bytes: q, k read + written in place, v read, both cache rows written, positions
     nbytes = 2 * T * hq * hd * 2 + 2 * T * hk * hd * 2 + T * hk * hd * 2 + 2 * T * hk * hd * 2 + 4 * bsz + 2 * hd * 2
+    if had:
+        nbytes += (hq + 2 * hk) * hd * 2
     sets = sets_for(nbytes)
     rng = np.random.default_rng(seed)
     pages = bsz * max_blocks + 4
@@ -247,9 +252,17 @@ def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64):
     bufs = [tuple(gen((bsz, seq, h, hd), 0.0, 1.0, torch.float16, seed + 10 * j + i) for i, h in enumerate((hq, hk, hk)))
             for j in range(sets)]
     naive = exl3r.load_naive()
+    sv = [torch.where(torch.rand(h * hd, device="cuda") < 0.5, -1.0, 1.0).to(torch.float16) for h in (hq, hk, hk)]
 
     def launch(i):
         q, k, v = bufs[i % sets]
+        if had and fused:
+            ffi.rope_paged_kv_had(q, q, k, k, v, inv, 0, sl, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, kc, vc, bt, sl,
+                                  q_post_scale=sv[0], k_post_scale=sv[1], v_post_scale=sv[2])
+            return
+        if had:
+            for t, p in zip((q, k, v), sv):
+                ffi.had_r_128(t.view(T, -1), t.view(T, -1), None, p)
         if fused:
             ffi.rope_paged_kv(q, q, k, k, v, inv, 0, sl, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, kc, vc, bt, sl)
         else:
@@ -259,7 +272,10 @@ def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64):
                                                  torch.cuda.current_stream().cuda_stream)
             assert rc == 0
     kind = "fused (1 launch)" if fused else "rope + separate append (2 launches)"
-    return Work(name, nbytes, launch, f"q/k norm + RoPE + paged KV append bsz {bsz} x {seq} tokens, {kind}", sets)
+    if had:
+        kind = "fused (1 launch)" if fused else "3 in-place rotations + rope + separate append (5 launches)"
+    head = "q/k/v output rotation + " if had else ""
+    return Work(name, nbytes, launch, f"{head}q/k norm + RoPE + paged KV append bsz {bsz} x {seq} tokens, {kind}", sets)
 
 
 def make_gated(name, kind, tokens=4096, heads=32, hd=128, seed=600):
@@ -535,6 +551,8 @@ def make_all(only=None):
         "norm_had_c3_unfused": lambda: make_norm_had("norm_had_c3_unfused", 8192, 5120, False),
         "norm_had_rot_c3": lambda: make_norm_had("norm_had_rot_c3", 8192, 5120, True, rotate=True),
         "norm_had_rot_c3_unfused": lambda: make_norm_had("norm_had_rot_c3_unfused", 8192, 5120, False, rotate=True),
+        "rope_kv_had_prefill": lambda: make_rope_kv("rope_kv_had_prefill", 1, 4096, True, had=True),
+        "rope_kv_had_prefill_unfused": lambda: make_rope_kv("rope_kv_had_prefill_unfused", 1, 4096, False, had=True),
         "rope_had_c4": lambda: make_rope_had("rope_had_c4", ragged, 64, 8, 128, True),
         "rope_had_c4_unfused": lambda: make_rope_had("rope_had_c4_unfused", ragged, 64, 8, 128, False),
         "silu_had_c3": lambda: make_act_had("silu_had_c3", 8192, 17408, True),
@@ -731,7 +749,8 @@ def main():
         hadamard = {"had_r_128_8192x5120_us": ops["had_c3"]["us"]}
         for fused, label in (("norm_had_c3", "res_norm_to_3_inputs_8192x5120"),
                              ("norm_had_rot_c3", "rotate_res_norm_to_3_inputs_8192x5120"),
-                             ("silu_had_c3", "silu_mul_to_input_8192x17408"), ("rope_had_c4", "qk_rotate_rope_c4")):
+                             ("silu_had_c3", "silu_mul_to_input_8192x17408"), ("rope_had_c4", "qk_rotate_rope_c4"),
+                             ("rope_kv_had_prefill", "qkv_rotate_rope_paged_append_4096")):
             f_us, u_us = ops[fused]["us"], ops[fused + "_unfused"]["us"]
             hadamard[label] = {"fused_us": f_us, "unfused_us": u_us, "speedup": round(u_us / f_us, 3)}
         hadamard["desc"] = ("the EXL3 linear's random-Hadamard rotation (had_r_128) alone, and fused into the op that "

@@ -62,10 +62,12 @@ struct RopeArgs
     const int32_t* block_table;
     const int32_t* cache_seqlens;
     int32_t* err;
-    // Output rotation of the q / k projections (exl3r_rope_had): each 128-element head is first
-    // replaced by had_r_128(head) times its f16 post-scale (svh; nullptr: none).
+    // Output rotation of the q / k (and, with a paged append, v) projections (exl3r_rope_had,
+    // exl3r_rope_paged_kv_had): each 128-element head is first replaced by had_r_128(head) times its
+    // f16 post-scale (svh; nullptr: none).
     const void* q_post;
     const void* k_post;
+    const void* v_post;
 };
 
 // Head kinds of the item space [0, hq) q, [hq, hq + hk) k, [hq + hk, hq + hk + hv) v.
@@ -557,8 +559,9 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
             {
                 // A head is one rotation block: head_dim 128, 16 lanes, all active or all not (a
                 // padding head past the last one has no post-scale entries and is left alone).
-                static_assert(IO::code == DT_F16 && LPH == 16 && !APPEND, "output rotation: f16 heads of 128");
-                if (t.act[i]) head_out_rotation(t.v[i], t.isq[i] ? a.q_post : a.k_post, (int64_t)t.hidx[i] * 128 + e0);
+                static_assert(IO::code == DT_F16 && LPH == 16, "output rotation: f16 heads of 128");
+                const void* post = kd == KIND_Q ? a.q_post : kd == KIND_K ? a.k_post : a.v_post;
+                if (t.act[i]) head_out_rotation(t.v[i], post, (int64_t)t.hidx[i] * 128 + e0);
             }
             rope_head<IO, MODE, LPH, NORM>(a, t.v[i], kd != KIND_V, select_w<NORM>(kd == KIND_Q, wq, wk), c, s, e0, l64);
             if (!t.act[i]) continue;
@@ -732,7 +735,11 @@ static void launch_rope_tok(RopeArgs a, hipStream_t s)
     const size_t lds = 4 * (size_t)(a.R / 2) * sizeof(float2);
     auto go = [&](auto H) {
         constexpr int HP = decltype(H)::value;
-        if constexpr (HADR) k_rope_tok<IO, MODE, LPH, HP, NORM, false, true><<<(unsigned)blocks, 256, lds, s>>>(a);
+        if constexpr (HADR)
+        {
+            if (a.kc) k_rope_tok<IO, MODE, LPH, HP, NORM, true, true><<<(unsigned)blocks, 256, lds, s>>>(a);
+            else k_rope_tok<IO, MODE, LPH, HP, NORM, false, true><<<(unsigned)blocks, 256, lds, s>>>(a);
+        }
         else if (a.kc) k_rope_tok<IO, MODE, LPH, HP, NORM, true><<<(unsigned)blocks, 256, lds, s>>>(a);
         else k_rope_tok<IO, MODE, LPH, HP, NORM, false><<<(unsigned)blocks, 256, lds, s>>>(a);
     };
@@ -913,6 +920,45 @@ extern "C" int exl3r_rope(const void* q, void* out_q, int64_t q_tok_stride, int6
     return rope_dispatch(op, a, dtype, rope_mode, stream);
 }
 
+// Argument checks and RopeArgs of the fused append, shared by exl3r_rope_paged_kv and
+// exl3r_rope_paged_kv_had.  Returns EXL3R_OK with a.tokens == 0 when there is nothing to launch.
+static int paged_prepare(const char* op, RopeArgs& a, const void* q, void* out_q, int64_t q_tok_stride,
+                         int64_t q_head_stride, int num_heads_q, const void* k, void* out_k, int64_t k_tok_stride,
+                         int64_t k_head_stride, const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                         int num_heads_kv, int dtype, int64_t bsz, int64_t seq_len, int head_dim,
+                         const float* inv_freq, int rotary_dim, int32_t position, const int32_t* positions,
+                         const int32_t* position_ids, const void* q_norm, const void* k_norm, int norm_dtype,
+                         float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
+                         void* k_cache, void* v_cache, int page_size, int64_t num_pages,
+                         const int32_t* block_table, int64_t max_blocks_per_seq, const int32_t* cache_seqlens,
+                         int32_t* err_flag)
+{
+    if (num_heads_kv <= 0) return set_error(EXL3R_EINVAL, "%s: num_heads_kv must be positive", op);
+    if (page_size <= 0 || (page_size & (page_size - 1)) || num_pages <= 0 || max_blocks_per_seq <= 0)
+        return set_error(EXL3R_EINVAL, "%s: page_size %d must be a power of two, num_pages and max_blocks_per_seq positive",
+                         op, page_size);
+    if (v_head_stride < head_dim || v_tok_stride < (int64_t)num_heads_kv * v_head_stride)
+        return set_error(EXL3R_EINVAL, "%s: v strides (%lld, %lld) overlap heads", op, (long long)v_tok_stride,
+                         (long long)v_head_stride);
+    if (num_pages > ((int64_t)1 << 62) / ((int64_t)page_size * num_heads_kv * (head_dim > 0 ? head_dim : 1)))
+        return set_error(EXL3R_EINVAL, "%s: cache too large", op);
+    if (bsz > 0 && seq_len > 0 && (!k || !v || !k_cache || !v_cache || !block_table || !cache_seqlens))
+        return set_error(EXL3R_EINVAL, "%s: k, v, k_cache, v_cache, block_table and cache_seqlens must be non-null", op);
+    const int rc = rope_prepare(op, a, q, out_q, q_tok_stride, q_head_stride, num_heads_q, k, out_k, true, k_tok_stride,
+                                k_head_stride, num_heads_kv, dtype, bsz, seq_len, head_dim, inv_freq, rotary_dim, position,
+                                positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias,
+                                rope_mode, attn_factor);
+    if (rc || a.tokens == 0) return rc;
+    a.v = v; a.v_ts = v_tok_stride; a.v_hs = v_head_stride; a.hv = num_heads_kv;
+    a.kc = k_cache; a.vc = v_cache;
+    int lg = 0;
+    while ((1 << lg) < page_size) ++lg;
+    a.page_log2 = lg;
+    a.pages = num_pages; a.max_blocks = max_blocks_per_seq;
+    a.block_table = block_table; a.cache_seqlens = cache_seqlens; a.err = err_flag;
+    return EXL3R_OK;
+}
+
 extern "C" int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride,
                                    int num_heads_q, const void* k, void* out_k, int64_t k_tok_stride,
                                    int64_t k_head_stride, const void* v, int64_t v_tok_stride, int64_t v_head_stride,
@@ -926,30 +972,13 @@ extern "C" int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_str
                                    const int32_t* cache_seqlens, int32_t* err_flag, void* stream)
 {
     const char* op = "exl3r_rope_paged_kv";
-    if (num_heads_kv <= 0) return set_error(EXL3R_EINVAL, "%s: num_heads_kv must be positive", op);
-    if (page_size <= 0 || (page_size & (page_size - 1)) || num_pages <= 0 || max_blocks_per_seq <= 0)
-        return set_error(EXL3R_EINVAL, "%s: page_size %d must be a power of two, num_pages and max_blocks_per_seq positive",
-                         op, page_size);
-    if (v_head_stride < head_dim || v_tok_stride < (int64_t)num_heads_kv * v_head_stride)
-        return set_error(EXL3R_EINVAL, "%s: v strides (%lld, %lld) overlap heads", op, (long long)v_tok_stride,
-                         (long long)v_head_stride);
-    if (num_pages > ((int64_t)1 << 62) / ((int64_t)page_size * num_heads_kv * (head_dim > 0 ? head_dim : 1)))
-        return set_error(EXL3R_EINVAL, "%s: cache too large", op);
-    if (bsz > 0 && seq_len > 0 && (!k || !v || !k_cache || !v_cache || !block_table || !cache_seqlens))
-        return set_error(EXL3R_EINVAL, "%s: k, v, k_cache, v_cache, block_table and cache_seqlens must be non-null", op);
     RopeArgs a;
-    const int rc = rope_prepare(op, a, q, out_q, q_tok_stride, q_head_stride, num_heads_q, k, out_k, true, k_tok_stride,
-                                k_head_stride, num_heads_kv, dtype, bsz, seq_len, head_dim, inv_freq, rotary_dim, position,
-                                positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias,
-                                rope_mode, attn_factor);
+    const int rc = paged_prepare(op, a, q, out_q, q_tok_stride, q_head_stride, num_heads_q, k, out_k, k_tok_stride,
+                                 k_head_stride, v, v_tok_stride, v_head_stride, num_heads_kv, dtype, bsz, seq_len,
+                                 head_dim, inv_freq, rotary_dim, position, positions, position_ids, q_norm, k_norm,
+                                 norm_dtype, norm_eps, norm_constant_bias, rope_mode, attn_factor, k_cache, v_cache,
+                                 page_size, num_pages, block_table, max_blocks_per_seq, cache_seqlens, err_flag);
     if (rc || a.tokens == 0) return rc;
-    a.v = v; a.v_ts = v_tok_stride; a.v_hs = v_head_stride; a.hv = num_heads_kv;
-    a.kc = k_cache; a.vc = v_cache;
-    int lg = 0;
-    while ((1 << lg) < page_size) ++lg;
-    a.page_log2 = lg;
-    a.pages = num_pages; a.max_blocks = max_blocks_per_seq;
-    a.block_table = block_table; a.cache_seqlens = cache_seqlens; a.err = err_flag;
     return rope_dispatch(op, a, dtype, rope_mode, stream);
 }
 
@@ -1029,4 +1058,66 @@ extern "C" int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, 
                       k_tok_stride, head_dim, num_heads_k, dtype, bsz, seq_len, head_dim, inv_freq, rotary_dim, position,
                       positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias, rope_mode,
                       attn_factor, stream);
+}
+
+// exl3r_rope_paged_kv preceded by the q / k / v projections' output rotation (Linear::forward's
+// had_r_128(y, y, None, svh), src/modules.rs:231, then RoPE::apply and paged_kv_cache_update,
+// src/modules.rs:669-704).  Prefill-sized NeoX launches of f16 heads of 128 run it inside the
+// wave-per-token kernel; anything else rotates q into out_q, k into out_k (in place when out_k is
+// null) and v in place, then runs exl3r_rope_paged_kv there.
+extern "C" int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok_stride, int num_heads_q,
+                                       const void* k, void* out_k, int64_t k_tok_stride, const void* v,
+                                       int64_t v_tok_stride, int num_heads_kv, int dtype, int64_t bsz,
+                                       int64_t seq_len, int head_dim, const float* inv_freq, int rotary_dim,
+                                       int32_t position, const int32_t* positions, const int32_t* position_ids,
+                                       const void* q_norm, const void* k_norm, int norm_dtype,
+                                       float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
+                                       void* k_cache, void* v_cache, int page_size, int64_t num_pages,
+                                       const int32_t* block_table, int64_t max_blocks_per_seq,
+                                       const int32_t* cache_seqlens, int32_t* err_flag,
+                                       const void* q_post_scale, const void* k_post_scale, const void* v_post_scale,
+                                       void* stream)
+{
+    const char* op = "exl3r_rope_paged_kv_had";
+    if (dtype != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: the rotated projection outputs are f16", op);
+    if (head_dim <= 0 || ((int64_t)num_heads_q * head_dim) % 128 || ((int64_t)num_heads_kv * head_dim) % 128)
+        return set_error(EXL3R_EINVAL, "%s: heads * head_dim must be a multiple of 128", op);
+    RopeArgs a;
+    int rc = paged_prepare(op, a, q, out_q, q_tok_stride, head_dim, num_heads_q, k, out_k, k_tok_stride, head_dim, v,
+                           v_tok_stride, head_dim, num_heads_kv, dtype, bsz, seq_len, head_dim, inv_freq, rotary_dim,
+                           position, positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias,
+                           rope_mode, attn_factor, k_cache, v_cache, page_size, num_pages, block_table,
+                           max_blocks_per_seq, cache_seqlens, err_flag);
+    if (rc || a.tokens == 0) return rc;
+    a.q_post = q_post_scale;
+    a.k_post = k_post_scale;
+    a.v_post = v_post_scale;
+    auto a16 = [](const void* p) { return p == nullptr || aligned16(p); };
+    const bool fused = head_dim == 128 && rope_mode == EXL3R_ROPE_NEOX && rope_vec_ok(a, rope_mode) &&
+                       rope_tok_launch(a) && a16(q_post_scale) && a16(k_post_scale) && a16(v_post_scale);
+    if (fused)
+    {
+        hipStream_t s = (hipStream_t)stream;
+        const int norm = rope_norm_kind(a, dtype);
+        if (norm == NORM_NONE) launch_rope_tok<TF16, EXL3R_ROPE_NEOX, 16, NORM_NONE, true>(a, s);
+        else if (norm == NORM_HALF) launch_rope_tok<TF16, EXL3R_ROPE_NEOX, 16, NORM_HALF, true>(a, s);
+        else launch_rope_tok<TF16, EXL3R_ROPE_NEOX, 16, NORM_F32, true>(a, s);
+        return launch_status(op);
+    }
+    const int64_t tokens = a.tokens;
+    void* kr = out_k ? out_k : const_cast<void*>(k);
+    rc = exl3r_had_r_128(q, EXL3R_F16, q_tok_stride, out_q, q_tok_stride, tokens, (int64_t)num_heads_q * head_dim,
+                         nullptr, q_post_scale, 1.0f, stream);
+    if (rc == EXL3R_OK)
+        rc = exl3r_had_r_128(k, EXL3R_F16, k_tok_stride, kr, k_tok_stride, tokens, (int64_t)num_heads_kv * head_dim,
+                             nullptr, k_post_scale, 1.0f, stream);
+    if (rc == EXL3R_OK)
+        rc = exl3r_had_r_128(v, EXL3R_F16, v_tok_stride, const_cast<void*>(v), v_tok_stride, tokens,
+                             (int64_t)num_heads_kv * head_dim, nullptr, v_post_scale, 1.0f, stream);
+    if (rc != EXL3R_OK) return rc;
+    return exl3r_rope_paged_kv(out_q, out_q, q_tok_stride, head_dim, num_heads_q, kr, out_k, k_tok_stride, head_dim, v,
+                               v_tok_stride, head_dim, num_heads_kv, dtype, bsz, seq_len, head_dim, inv_freq,
+                               rotary_dim, position, positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps,
+                               norm_constant_bias, rope_mode, attn_factor, k_cache, v_cache, page_size, num_pages,
+                               block_table, max_blocks_per_seq, cache_seqlens, err_flag, stream);
 }

@@ -274,6 +274,41 @@ def rope_paged_kv(q, out_q, k, out_k, v, inv_freq, position, positions, q_norm, 
                                      _ptr(err_flag), _stream(q, stream)))
 
 
+def rope_paged_kv_had(q, out_q, k, out_k, v, inv_freq, position, positions, q_norm, k_norm, norm_eps,
+                      norm_constant_bias, rope_mode, attn_factor, k_cache, v_cache, block_table, cache_seqlens,
+                      q_post_scale=None, k_post_scale=None, v_post_scale=None, position_ids=None, err_flag=None,
+                      stream=None):
+    """rope_paged_kv() on the raw f16 outputs of the q / k / v projections (heads packed), each first given
+    its projection's output rotation had_r_128(y, y, None, svh) (src/modules.rs:231).  Outside the fused
+    launch (NeoX, head_dim 128, >= 1024 tokens) v, and k when out_k is None, are rotated in place."""
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be (bsz, seq_len, heads, head_dim)")
+    bsz, seq, hq, hd = q.shape
+    hk = k.shape[2]
+    if k.shape != v.shape or k.shape[:2] != q.shape[:2] or k.shape[3] != hd:
+        raise ValueError("k and v must be (bsz, seq_len, kv_heads, head_dim) like q")
+    for t in (q, k, v) + ((out_k,) if out_k is not None else ()):
+        if t.stride(3) != 1 or t.stride(2) != hd or (seq > 1 and bsz > 1 and t.stride(0) != seq * t.stride(1)):
+            raise ValueError("q / k / v / out_k: packed heads and batch stride seq_len * token stride")
+    if out_q.stride() != q.stride() or out_q.shape != q.shape or (out_k is not None and out_k.stride() != k.stride()):
+        raise ValueError("out_q / out_k must share q's / k's layout")
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or k_cache.shape[2:] != (hk, hd) or \
+            not k_cache.is_contiguous() or not v_cache.is_contiguous():
+        raise ValueError("caches must be contiguous (pages, page_size, kv_heads, head_dim)")
+    if block_table.dim() != 2 or block_table.dtype != torch.int32 or cache_seqlens.dtype != torch.int32:
+        raise TypeError("block_table (bsz, max_blocks) and cache_seqlens (bsz) must be int32")
+    nw = q_norm if q_norm is not None else k_norm
+    check(load().exl3r_rope_paged_kv_had(_ptr(q), _ptr(out_q), q.stride(1), hq, _ptr(k), _ptr(out_k), k.stride(1),
+                                         _ptr(v), v.stride(1), hk, dtype_code(q), bsz, seq, hd, _ptr(inv_freq),
+                                         inv_freq.shape[-1] * 2, int(position), _ptr(positions), _ptr(position_ids),
+                                         _ptr(q_norm), _ptr(k_norm), dtype_code(nw) if nw is not None else F16,
+                                         norm_eps, norm_constant_bias, rope_mode, attn_factor,
+                                         _ptr(k_cache), _ptr(v_cache), k_cache.shape[1], k_cache.shape[0],
+                                         _ptr(block_table), block_table.shape[1], _ptr(cache_seqlens), _ptr(err_flag),
+                                         _ptr(q_post_scale), _ptr(k_post_scale), _ptr(v_post_scale),
+                                         _stream(q, stream)))
+
+
 def argmax_sample(logits, ids, max_logit=0, stream=None):
     """ids[i] = first index of the maximum of logits[i, :max_logit] (NaN maximal), int64
     (src/ffi.rs:521-525; the generator's batched argmax)."""

@@ -468,6 +468,42 @@ void rope_paged_kv(const Tensor& q, const Tensor& out_q, const Tensor& k, const 
                                   (const int32_t*)cache_seqlens.data, err_flag, s.get()));
 }
 
+void rope_paged_kv_had(const Tensor& q, const Tensor& out_q, const Tensor& k, const Tensor* out_k, const Tensor& v,
+                       const Tensor& inv_freq, int64_t position, const Tensor* positions, const Tensor* q_norm,
+                       const Tensor* k_norm, float norm_eps, float norm_constant_bias, RopeStyle rope_mode,
+                       float attn_factor, const Tensor& k_cache, const Tensor& v_cache, const Tensor& block_table,
+                       const Tensor& cache_seqlens, int32_t* err_flag, const Tensor* q_post_scale,
+                       const Tensor* k_post_scale, const Tensor* v_post_scale, const Stream& s)
+{
+    require(q.dim() == 4 && k.dim() == 4 && v.dim() == 4 && q.dtype == DType::F16,
+            "rope_paged_kv_had: q, k, v must be f16 (bsz, seq_len, heads, head_dim)");
+    const int64_t bsz = q.size(0), seq = q.size(1), hd = q.size(3), hk = k.size(2);
+    require(out_q.strides == q.strides && out_q.shape == q.shape, "rope_paged_kv_had: out_q must share q's layout");
+    require(k.shape == v.shape && k.size(0) == bsz && k.size(1) == seq && k.size(3) == hd &&
+                (!out_k || out_k->strides == k.strides),
+            "rope_paged_kv_had: k and v must be (bsz, seq_len, kv_heads, head_dim); out_k shares k's layout");
+    for (const Tensor* t : { &q, &k, &v })
+        require(t->stride(3) == 1 && t->stride(2) == hd && (bsz <= 1 || seq <= 1 || t->stride(0) == seq * t->stride(1)),
+                "rope_paged_kv_had: packed heads and batch stride seq_len * token stride");
+    require(k_cache.dim() == 4 && k_cache.shape == v_cache.shape && k_cache.size(2) == hk && k_cache.size(3) == hd &&
+                k_cache.is_contiguous() && v_cache.is_contiguous(),
+            "rope_paged_kv_had: caches must be contiguous (pages, page_size, kv_heads, head_dim)");
+    require(block_table.dim() == 2 && block_table.dtype == DType::I32 && cache_seqlens.dtype == DType::I32,
+            "rope_paged_kv_had: block_table (bsz, max_blocks) and cache_seqlens (bsz) must be int32");
+    require(inv_freq.dtype == DType::F32 && (!positions || positions->dtype == DType::I32),
+            "rope_paged_kv_had: inv_freq float32, positions int32");
+    const Tensor* nw = q_norm ? q_norm : k_norm;
+    check_abi(exl3r_rope_paged_kv_had(q.data, out_q.data, q.stride(1), (int)q.size(2), k.data,
+                                      out_k ? out_k->data : nullptr, k.stride(1), v.data, v.stride(1), (int)hk,
+                                      code(q.dtype), bsz, seq, (int)hd, (const float*)inv_freq.data,
+                                      (int)(inv_freq.numel() * 2), (int32_t)position, (const int32_t*)ptr(positions),
+                                      nullptr, ptr(q_norm), ptr(k_norm), code_or(nw, DType::F16), norm_eps,
+                                      norm_constant_bias, (int)rope_mode, attn_factor, k_cache.data, v_cache.data,
+                                      (int)k_cache.size(1), k_cache.size(0), (const int32_t*)block_table.data,
+                                      block_table.size(1), (const int32_t*)cache_seqlens.data, err_flag,
+                                      ptr(q_post_scale), ptr(k_post_scale), ptr(v_post_scale), s.get()));
+}
+
 void embedding(const Tensor& table, const Tensor& ids, const Tensor& out, int32_t* err_flag, const Stream& s)
 {
     require(table.dim() == 2 && table.stride(1) == 1, "embedding: table must be [vocab, hidden] with dense rows");

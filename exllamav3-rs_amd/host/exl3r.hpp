@@ -153,6 +153,15 @@ void rope_had(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tenso
               int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
               float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Tensor* q_post_scale,
               const Tensor* k_post_scale, const Stream& s, const Tensor* position_ids = nullptr);
+// rope_paged_kv() on the raw f16 outputs of the q / k / v projections (heads packed), each first given its
+// projection's output rotation had_r_128(y, y, None, svh); outside the fused launch v (and k without out_k)
+// are rotated in place.
+void rope_paged_kv_had(const Tensor& q, const Tensor& out_q, const Tensor& k, const Tensor* out_k, const Tensor& v,
+                       const Tensor& inv_freq, int64_t position, const Tensor* positions, const Tensor* q_norm,
+                       const Tensor* k_norm, float norm_eps, float norm_constant_bias, RopeStyle rope_mode,
+                       float attn_factor, const Tensor& k_cache, const Tensor& v_cache, const Tensor& block_table,
+                       const Tensor& cache_seqlens, int32_t* err_flag, const Tensor* q_post_scale,
+                       const Tensor* k_post_scale, const Tensor* v_post_scale, const Stream& s);
 // rope() fused with the paged KV-cache append that follows it in paged attention (src/modules.rs:666-704,
 // ffi.rs:337-350): the roped k (also written to out_k when given) and v go to k_cache / v_cache
 // [pages, page_size, kv_heads, head_dim] at cache_seqlens[b] + s through block_table [bsz, max_blocks].

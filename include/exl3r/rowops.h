@@ -240,6 +240,29 @@ EXL3R_API int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, i
                    const void* q_post_scale, const void* k_post_scale, void* stream);
 
 /*
+ * exl3r_rope_paged_kv preceded by the q / k / v projections' output rotation at prefill: each
+ * projection output first becomes had_r_128(y, y, NULL, svh, 1.0) (src/modules.rs:231), then RoPE::apply
+ * and paged_kv_cache_update (src/modules.rs:669-704).  q, k, v: f16 with heads packed (head stride =
+ * head_dim), heads * head_dim a multiple of 128; *_post_scale: f16 [heads * head_dim] (svh) or NULL.
+ * Other arguments as exl3r_rope_paged_kv.  Bit-identical to exl3r_had_r_128 on q, k and v followed by
+ * exl3r_rope_paged_kv.  NeoX, head_dim 128, 16-byte aligned, 1024 or more tokens: one fused launch that
+ * writes only out_q, out_k (if given) and the caches.  Otherwise the rotations run first -- q into
+ * out_q, k into out_k (into k itself when out_k is NULL) and v in place -- then exl3r_rope_paged_kv.
+ */
+EXL3R_API int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok_stride, int num_heads_q,
+                            const void* k, void* out_k, int64_t k_tok_stride, const void* v,
+                            int64_t v_tok_stride, int num_heads_kv, int dtype, int64_t bsz,
+                            int64_t seq_len, int head_dim, const float* inv_freq, int rotary_dim,
+                            int32_t position, const int32_t* positions, const int32_t* position_ids,
+                            const void* q_norm, const void* k_norm, int norm_dtype,
+                            float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
+                            void* k_cache, void* v_cache, int page_size, int64_t num_pages,
+                            const int32_t* block_table, int64_t max_blocks_per_seq,
+                            const int32_t* cache_seqlens, int32_t* err_flag,
+                            const void* q_post_scale, const void* k_post_scale, const void* v_post_scale,
+                            void* stream);
+
+/*
  * exl3r_rope fused with the paged KV-cache append that follows it in paged attention
  * (Attention::forward, src/modules.rs:666-704: rope in place, then paged_kv_cache_update,
  * kernels/generator/cache.cu:143-243):
