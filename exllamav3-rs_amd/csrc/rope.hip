@@ -321,13 +321,16 @@ __device__ __forceinline__ void rope_head(const RopeArgs& a, typename IO::Vec& v
             unpack8<IO>(v, f);
             unpack8<IO>(po, g);
             #pragma unroll
-            for (int j = 0; j < 8; ++j) f[j] = lower ? f[j] * c[j] - g[j] * s[j] : f[j] * c[j] + g[j] * s[j];
+            for (int j = 0; j < 8; ++j) f[j] = f[j] * c[j] + g[j] * s[j];   // lower half: s holds -sin
             v = pack8<IO>(f);
         }
     }
 }
 
-// cos / sin of the lane's frequencies (rope_head's c, s) out of a row of R/2 {cos, sin} pairs.
+// cos / sin of the lane's frequencies (rope_head's c, s) out of a row of R/2 {cos, sin} pairs.  NeoX
+// lanes of the lower half take -sin, so every rotated lane computes v c + partner s: fl(v c) +
+// fl(partner (-sin)) is fl(v c) - fl(partner sin) bit for bit (negation is exact and x - y is
+// x + (-y)).
 template <int MODE>
 __device__ __forceinline__ void lane_sincos(const float2* row, int e0, int R, float (&c)[8], float (&s)[8])
 {
@@ -340,7 +343,7 @@ __device__ __forceinline__ void lane_sincos(const float2* row, int e0, int R, fl
         {
             const float2 x = row[t0 + j];
             c[j] = x.x;
-            s[j] = x.y;
+            s[j] = MODE == EXL3R_ROPE_NEOX && e0 < (R >> 1) ? -x.y : x.y;
         }
     }
 }
