@@ -36,7 +36,7 @@ OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "
        "deinterleave_q35", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
        "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_unfused", "silu_had_c3",
        "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_unfused",
-       "rope_kv_had_prefill", "rope_kv_had_prefill_unfused", "calib_copy",
+       "rope_kv_had_prefill", "rope_kv_had_prefill_unfused", "mlp_had_c3", "mlp_had_c3_unfused", "calib_copy",
        "calib_copy_cached"]
 
 
@@ -413,28 +413,38 @@ def make_norm_had(name, rows, cols, fused, seed=760, rotate=False):
     return Work(name, nbytes, launch, f"{head} -> 3 Hadamard inputs [{rows},{cols}] f16/f32r, {kind}", sets)
 
 
-def make_act_had(name, rows, cols, fused, seed=780):
+def make_act_had(name, rows, cols, fused, seed=780, rotate=False):
     """MLP prefill tail: silu(gate) * up in f16 and the down projection's input rotation
     had_r_128(a, suh) (src/modules.rs:932-940, 224-227): one fused launch, or exl3r_silu_mul and
-    exl3r_had_r_128.  Both count the fused job's bytes (gate, up, the rotated output, suh)."""
+    exl3r_had_r_128.  With rotate, gate and up are the raw gate_proj / up_proj outputs and their own
+    output rotations (src/modules.rs:231) come first (unfused: two in-place rotations).  Both count the
+    fused job's bytes (gate, up, the rotated output, suh, and svh of gate and up)."""
     import torch
     import exl3r.ffi as ffi
-    nbytes = rows * cols * 6 + cols * 2
+    nbytes = rows * cols * 6 + (3 if rotate else 1) * cols * 2
     sets = sets_for(nbytes)
     bufs = [(gen((rows, cols), 0.0, 1.0, torch.float16, seed + 2 * k), gen((rows, cols), 0.0, 1.0, torch.float16, seed + 2 * k + 1),
              torch.empty((rows, cols), device="cuda", dtype=torch.float16)) for k in range(sets)]
-    suh = torch.where(torch.rand(cols, device="cuda") < 0.5, -1.0, 1.0).to(torch.float16)
+    suh, sg, su = (torch.where(torch.rand(cols, device="cuda") < 0.5, -1.0, 1.0).to(torch.float16) for _ in range(3))
     a = torch.empty((rows, cols), device="cuda", dtype=torch.float16)
 
     def launch(i):
         g, u, out = bufs[i % sets]
         if fused:
-            ffi.act_mul_had("silu", g, u, out, suh)
+            if rotate:
+                ffi.act_mul_had("silu", g, u, out, suh, rotate_x=True, rotate_y=True, x_post_scale=sg, y_post_scale=su)
+            else:
+                ffi.act_mul_had("silu", g, u, out, suh)
         else:
+            if rotate:
+                ffi.had_r_128(g, g, None, sg)
+                ffi.had_r_128(u, u, None, su)
             ffi.silu_mul(g, u, a)
             ffi.had_r_128(a, out, suh)
-    kind = "fused" if fused else "unfused (silu_mul + had_r_128)"
-    return Work(name, nbytes, launch, f"SiLU(gate)*up -> Hadamard input [{rows},{cols}] f16, {kind}", sets)
+    kind = "fused" if fused else ("unfused (2 in-place rotations + silu_mul + had_r_128)" if rotate else
+                                  "unfused (silu_mul + had_r_128)")
+    head = "rotated gate, up -> " if rotate else ""
+    return Work(name, nbytes, launch, f"{head}SiLU(gate)*up -> Hadamard input [{rows},{cols}] f16, {kind}", sets)
 
 
 def make_copy(name, cached=False):
@@ -555,6 +565,8 @@ def make_all(only=None):
         "rope_kv_had_prefill_unfused": lambda: make_rope_kv("rope_kv_had_prefill_unfused", 1, 4096, False, had=True),
         "rope_had_c4": lambda: make_rope_had("rope_had_c4", ragged, 64, 8, 128, True),
         "rope_had_c4_unfused": lambda: make_rope_had("rope_had_c4_unfused", ragged, 64, 8, 128, False),
+        "mlp_had_c3": lambda: make_act_had("mlp_had_c3", 8192, 17408, True, rotate=True),
+        "mlp_had_c3_unfused": lambda: make_act_had("mlp_had_c3_unfused", 8192, 17408, False, rotate=True),
         "silu_had_c3": lambda: make_act_had("silu_had_c3", 8192, 17408, True),
         "silu_had_c3_unfused": lambda: make_act_had("silu_had_c3_unfused", 8192, 17408, False),
         "calib_copy": lambda: make_copy("calib_copy"),
@@ -750,7 +762,8 @@ def main():
         for fused, label in (("norm_had_c3", "res_norm_to_3_inputs_8192x5120"),
                              ("norm_had_rot_c3", "rotate_res_norm_to_3_inputs_8192x5120"),
                              ("silu_had_c3", "silu_mul_to_input_8192x17408"), ("rope_had_c4", "qk_rotate_rope_c4"),
-                             ("rope_kv_had_prefill", "qkv_rotate_rope_paged_append_4096")):
+                             ("rope_kv_had_prefill", "qkv_rotate_rope_paged_append_4096"),
+                             ("mlp_had_c3", "rotate_gate_up_silu_mul_to_input_8192x17408")):
             f_us, u_us = ops[fused]["us"], ops[fused + "_unfused"]["us"]
             hadamard[label] = {"fused_us": f_us, "unfused_us": u_us, "speedup": round(u_us / f_us, 3)}
         hadamard["desc"] = ("the EXL3 linear's random-Hadamard rotation (had_r_128) alone, and fused into the op that "

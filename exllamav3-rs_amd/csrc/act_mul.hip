@@ -38,7 +38,16 @@ struct ActArgs
     void* hout;
     int64_t ldh;
     float hr;
+    // AH_IN_X / AH_IN_Y kernels: f16 x / y are first given their projection's output rotation
+    // had_r_128(v) * post (xpost / ypost: f16 per column, or null).
+    const void* xpost;
+    const void* ypost;
 };
+
+// Hadamard flags of the act-mul kernels (exl3r_act_mul_had).
+constexpr int AH_OUT = 1;    // the f16 activation goes through the next projection's input rotation
+constexpr int AH_IN_X = 2;   // x rotated on load
+constexpr int AH_IN_Y = 4;   // y rotated on load
 
 template <int ACT, bool LIMIT>
 __device__ __forceinline__ float act_mul1(float g, float u, float limit)
@@ -65,7 +74,7 @@ __device__ __forceinline__ void act_chunk(const float (&g)[8], const float (&u)[
     }
 }
 
-template <int ACT, class IT, class OT, int UNROLL, bool LIMIT, bool HAD = false>
+template <int ACT, class IT, class OT, int UNROLL, bool LIMIT, int HAD = 0>
 __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
 {
     const int64_t cpr = a.cols >> 3;   // chunks per row
@@ -95,11 +104,18 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
                 const int64_t c = base + (int64_t)u * nt;
                 if (c < cpr)
                 {
+                    // Input rotations: the chunk's 16-lane group is its 128-column block (as below).
+                    if constexpr ((HAD & (AH_IN_X | AH_IN_Y)) != 0)
+                    {
+                        static_assert(IT::code == DT_F16, "input rotations take f16 x and y");
+                        if constexpr ((HAD & AH_IN_X) != 0) output_rotation8(xv[u], a.xpost, c * 8);
+                        if constexpr ((HAD & AH_IN_Y) != 0) output_rotation8(yv[u], a.ypost, c * 8);
+                    }
                     float g[8], v[8], o[8];
                     unpack8<IT>(xv[u], g);
                     unpack8<IT>(yv[u], v);
                     act_chunk<ACT, OT, LIMIT>(g, v, a.limit, o);
-                    if constexpr (!HAD) store8<OT>(zr, c * 8, pack8<OT>(o));
+                    if constexpr (!(HAD & AH_OUT)) store8<OT>(zr, c * 8, pack8<OT>(o));
                     else
                     {
                         // The group of 16 lanes holding chunks c & ~15 .. c | 15 is the block's (the
@@ -140,7 +156,7 @@ __global__ __launch_bounds__(256) void k_act_mul_generic(ActArgs a, int it, int 
     }
 }
 
-template <int ACT, class IT, class OT, bool HAD = false>
+template <int ACT, class IT, class OT, int HAD = 0>
 static void launch_act_vec(const ActArgs& a, hipStream_t s)
 {
     const Tuning& tu = tuning();
@@ -184,9 +200,14 @@ static int act_mul_entry(const char* op, const void* x, const void* y, int it, v
 template <int ACT>
 static int act_had_entry(const char* op, const void* x, const void* y, int it, int64_t ldx, int64_t ldy,
                          void* z, int64_t ldz, const void* pre, void* out, int64_t ldo,
-                         int64_t rows, int64_t cols, float limit, float had_scale, void* stream)
+                         int64_t rows, int64_t cols, float limit, float had_scale, int rotate_in,
+                         const void* x_post, const void* y_post, void* stream)
 {
     if (!is_float_dtype(it)) return set_error(EXL3R_EDTYPE, "%s: unsupported input dtype %s", op, dtype_name(it));
+    if (rotate_in & ~3) return set_error(EXL3R_EINVAL, "%s: rotate_in takes bits 0 (x) and 1 (y)", op);
+    if (rotate_in && it != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: rotated inputs are f16", op);
+    if ((x_post && !(rotate_in & 1)) || (y_post && !(rotate_in & 2)))
+        return set_error(EXL3R_EINVAL, "%s: a post-scale without its input rotation", op);
     if (rows < 0 || cols <= 0 || cols % 128 || (rows > 1 && (ldx < cols || ldy < cols || ldo < cols || (z && ldz < cols))))
         return set_error(EXL3R_EINVAL, "%s: invalid shape rows=%lld cols=%lld (a multiple of 128) or row strides", op,
                          (long long)rows, (long long)cols);
@@ -199,13 +220,19 @@ static int act_had_entry(const char* op, const void* x, const void* y, int it, i
     hipStream_t s = (hipStream_t)stream;
     const int eb = dtype_bytes(it);
     const bool vec = aligned16(x) && aligned16(y) && aligned16(out) && (!z || aligned16(z)) && (!pre || aligned16(pre)) &&
+                     (!x_post || aligned16(x_post)) && (!y_post || aligned16(y_post)) &&
                      (lx * eb) % 16 == 0 && (ly * eb) % 16 == 0 && (lo * 2) % 16 == 0 && (lz * 2) % 16 == 0;
     if (vec)
     {
-        ActArgs a{ x, y, z, lx, ly, lz, rows, cols, limit, pre, out, lo, had_scale * 0.0883883461356163f };
-        with_float_type(it, [&](auto I) { launch_act_vec<ACT, decltype(I), TF16, true>(a, s); });
+        ActArgs a{ x, y, z, lx, ly, lz, rows, cols, limit, pre, out, lo, had_scale * 0.0883883461356163f, x_post, y_post };
+        if (rotate_in == 3) launch_act_vec<ACT, TF16, TF16, AH_OUT | AH_IN_X | AH_IN_Y>(a, s);
+        else if (rotate_in == 1) launch_act_vec<ACT, TF16, TF16, AH_OUT | AH_IN_X>(a, s);
+        else if (rotate_in == 2) launch_act_vec<ACT, TF16, TF16, AH_OUT | AH_IN_Y>(a, s);
+        else with_float_type(it, [&](auto I) { launch_act_vec<ACT, decltype(I), TF16, AH_OUT>(a, s); });
         return launch_status(op);
     }
+    // The input rotations have no buffer of their own to go through outside the fused kernel.
+    if (rotate_in) return set_error(EXL3R_EINVAL, "%s: rotated inputs need 16-byte aligned rows", op);
     void* dst = z ? z : out;
     const int64_t ld = z ? lz : lo;
     int rc = act_mul_entry<ACT>(op, x, y, it, dst, EXL3R_F16, rows, cols, lx, ly, ld, limit, stream);
@@ -289,21 +316,26 @@ extern "C" int exl3r_gelu_mul(const void* x, const void* y, int in_dtype, void* 
 
 extern "C" int exl3r_act_mul_had(int act, const void* x, const void* y, int in_dtype, int64_t ldx, int64_t ldy,
                                  void* z, int64_t ldz, const void* pre_scale, void* out, int64_t ldo,
-                                 int64_t rows, int64_t cols, float act_limit, float had_scale, void* stream)
+                                 int64_t rows, int64_t cols, float act_limit, float had_scale, int rotate_in,
+                                 const void* x_post_scale, const void* y_post_scale, void* stream)
 {
     const char* op = "exl3r_act_mul_had";
     switch (act)
     {
         case EXL3R_ACT_SILU:
             return act_had_entry<ACT_SILU>(op, x, y, in_dtype, ldx, ldy, z, ldz, pre_scale, out, ldo, rows, cols,
-                                           act_limit, had_scale, stream);
+                                           act_limit, had_scale, rotate_in, x_post_scale, y_post_scale, stream);
         case EXL3R_ACT_GELU:
             return act_had_entry<ACT_GELU>(op, x, y, in_dtype, ldx, ldy, z, ldz, pre_scale, out, ldo, rows, cols,
-                                           act_limit, had_scale, stream);
+                                           act_limit, had_scale, rotate_in, x_post_scale, y_post_scale, stream);
         case EXL3R_ACT_MUL_SIGMOID:
+        {
             if (act_limit != 0.0f) return set_error(EXL3R_EINVAL, "%s: act_limit applies to silu / gelu only", op);
+            // The kernels take the gate first: x and y, their rotations and post-scales swap.
+            const int swapped = rotate_in & ~3 ? rotate_in : ((rotate_in & 1) << 1) | ((rotate_in >> 1) & 1);
             return act_had_entry<ACT_SIGMOID>(op, y, x, in_dtype, ldy, ldx, z, ldz, pre_scale, out, ldo, rows, cols,
-                                              0.0f, had_scale, stream);
+                                              0.0f, had_scale, swapped, y_post_scale, x_post_scale, stream);
+        }
         default: return set_error(EXL3R_EINVAL, "%s: unknown act %d", op, act);
     }
 }

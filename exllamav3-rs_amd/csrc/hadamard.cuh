@@ -67,4 +67,21 @@ __device__ __forceinline__ uint32_t hmul2(uint32_t a, uint32_t b)
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, a) * __builtin_bit_cast(f16x2, b));
 }
 
+// The EXL3 linear's output rotation had_r_128(y, y, None, post) (scale 1) of the 8-element f16 chunk
+// at column col of a row, held as lane (col / 8) % 16 of its block's 16-lane group: the fp32
+// butterfly, one rounding to f16, then the half post-scale product (post: f16 per column, or null).
+__device__ __forceinline__ void output_rotation8(TF16::Vec& v, const void* post, int64_t col)
+{
+    float f[8];
+    unpack8<TF16>(v, f);
+    butterfly128(f, (int)((col >> 3) & 15), 0.0883883461356163f);
+    v = pack8<TF16>(f);
+    if (post)
+    {
+        const TF16::Vec p = load8<TF16>(post, col);
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) v.a[q] = hmul2(v.a[q], p.a[q]);
+    }
+}
+
 }  // namespace exl3r

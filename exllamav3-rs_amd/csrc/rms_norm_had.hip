@@ -47,7 +47,7 @@ extern "C" int exl3r_rms_norm_had(const void* x, int xt, int64_t ldx, const void
     a.r = r; a.ldr = r ? (rows > 1 ? ldr : dim) : 0;
     a.rows = rows; a.dim = (int)dim; a.eps = eps; a.cb = constant_bias; a.cs = constant_scale;
     a.nh = n_out; a.ldh = rows > 1 ? ldo : dim; a.hr = had_scale * 0.0883883461356163f;
-    a.hxpost = x_post_scale; a.hxr = 0.0883883461356163f;
+    a.hxpost = x_post_scale;
     bool aligned = (a.ldh * 2) % 16 == 0;
     for (int i = 0; i < n_out; ++i)
     {

@@ -53,9 +53,8 @@ struct RmsArgs
     int64_t ldh;
     float hr;
     // HAD_IN kernels: f16 x is first replaced by had_r_128(x) * hxpost (the EXL3 linear's output
-    // rotation with its f16 post-scale, or none when null), hxr = 1 / sqrt(128).
+    // rotation with its f16 post-scale, or none when null).
     const void* hxpost;
-    float hxr;
 };
 
 // Hadamard flags of the norm kernels (exl3r_rms_norm_had).
@@ -172,16 +171,7 @@ __device__ __forceinline__ typename RmsCache<XT, RT, MODE>::Vec rms_chunk1(const
         // fp32 butterfly, one rounding to f16, then the half post-scale product.  The chunk's
         // 16-lane group is the 128-element block, as for the outputs.
         static_assert(XT::code == DT_F16 && MODE != RMS_GATHER && MODE != RMS_GATED, "x rotation takes f16 x");
-        float f[8];
-        unpack8<TF16>(xv, f);
-        butterfly128(f, (int)((e >> 3) & 15), a.hxr);
-        xv = pack8<TF16>(f);
-        if (a.hxpost)
-        {
-            const TF16::Vec p = load8<TF16>(a.hxpost, e);
-            #pragma unroll
-            for (int q = 0; q < 4; ++q) xv.a[q] = hmul2(xv.a[q], p.a[q]);
-        }
+        output_rotation8(xv, a.hxpost, e);
     }
     if (valid)
         unpack8<XT>(xv, h);

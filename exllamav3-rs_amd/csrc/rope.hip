@@ -482,23 +482,6 @@ struct RopeBatch
     int b;
 };
 
-// The q / k projection's output rotation of one 128-element head held by 16 lanes (e0 = 8 * lane):
-// had_r_128(v) * post as hadamard.hip rounds it -- the fp32 butterfly, one rounding to f16, then the
-// half post-scale product.
-__device__ __forceinline__ void head_out_rotation(TF16::Vec& v, const void* post, int64_t col)
-{
-    float f[8];
-    unpack8<TF16>(v, f);
-    butterfly128(f, (int)((col >> 3) & 15), 0.0883883461356163f);
-    v = pack8<TF16>(f);
-    if (post)
-    {
-        const TF16::Vec p = load8<TF16>(post, col);
-        #pragma unroll
-        for (int q = 0; q < 4; ++q) v.a[q] = hmul2(v.a[q], p.a[q]);
-    }
-}
-
 template <class IO, int MODE, int LPH, int HPL, int NORM, bool APPEND, bool HADR = false>
 __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
 {
@@ -564,7 +547,7 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
                 // padding head past the last one has no post-scale entries and is left alone).
                 static_assert(IO::code == DT_F16 && LPH == 16, "output rotation: f16 heads of 128");
                 const void* post = kd == KIND_Q ? a.q_post : kd == KIND_K ? a.k_post : a.v_post;
-                if (t.act[i]) head_out_rotation(t.v[i], post, (int64_t)t.hidx[i] * 128 + e0);
+                if (t.act[i]) output_rotation8(t.v[i], post, (int64_t)t.hidx[i] * 128 + e0);
             }
             rope_head<IO, MODE, LPH, NORM>(a, t.v[i], kd != KIND_V, select_w<NORM>(kd == KIND_Q, wq, wk), c, s, e0, l64);
             if (!t.act[i]) continue;

@@ -43,7 +43,8 @@ PROTOTYPES = {
     "exl3r_rms_norm_had": (_i, [_vp, _i, _i64, _vp, _i, _vp, _i, _i64, _vp, _i64, _i, _vp, _vp, _i64, _i64, _i64,
                                 _f, _f, _f, _f, _i, _vp, _vp]),
     "exl3r_had_r_128": (_i, [_vp, _i, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _f, _vp]),
-    "exl3r_act_mul_had": (_i, [_i, _vp, _vp, _i, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _f, _f, _vp]),
+    "exl3r_act_mul_had": (_i, [_i, _vp, _vp, _i, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _f, _f, _i, _vp,
+                               _vp, _vp]),
     "exl3r_gumbel_noise": (_i, [_vp, _i, _i64, _vp, _i, _i64, _i64, _i64, ctypes.c_uint32, _vp]),
     "exl3r_rope_paged_kv": (_i, [_vp, _vp, _i64, _i64, _i, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i, _i, _i64, _i64,
                                  _i, _vp, _i, _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _vp, _vp, _i, _i64,

@@ -383,9 +383,11 @@ def rms_norm_had(x, w, outs, pre_scales, eps, constant_bias=0.0, constant_scale=
 ACT_CODES = {"silu": 0, "gelu": 1, "mul_sigmoid": 2}
 
 
-def act_mul_had(act, x, y, out, pre_scale=None, z=None, act_limit=0.0, had_scale=1.0, stream=None):
+def act_mul_had(act, x, y, out, pre_scale=None, z=None, act_limit=0.0, had_scale=1.0, rotate_x=False, rotate_y=False,
+                x_post_scale=None, y_post_scale=None, stream=None):
     """One pass: z = silu(x) * y, gelu(x) * y or x * sigmoid(y) in f16, then out = had_r_128(z, pre_scale)
-    (f16 [rows, cols], cols % 128 == 0); z is written only if given."""
+    (f16 [rows, cols], cols % 128 == 0); z is written only if given.  rotate_x / rotate_y: the f16 input is
+    first given its projection's output rotation had_r_128(v, post_scale=x_post_scale / y_post_scale)."""
     rows, cols, ldx = _rows(x)
     ry, cy, ldy = _rows(y)
     ro, co, ldo = _rows(out)
@@ -398,7 +400,8 @@ def act_mul_had(act, x, y, out, pre_scale=None, z=None, act_limit=0.0, had_scale
             raise ValueError("z is the f16 activation shaped like x")
     check(load().exl3r_act_mul_had(ACT_CODES[act], _ptr(x), _ptr(y), dtype_code(x), ldx, ldy, _ptr(z), ldz,
                                    _ptr(pre_scale), _ptr(out), ldo, rows, cols, act_limit, float(had_scale),
-                                   _stream(x, stream)))
+                                   (1 if rotate_x else 0) | (2 if rotate_y else 0), _ptr(x_post_scale),
+                                   _ptr(y_post_scale), _stream(x, stream)))
 
 
 def embedding(table, ids, out, err_flag=None, stream=None):

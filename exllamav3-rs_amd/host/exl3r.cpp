@@ -311,7 +311,8 @@ void rms_norm_had(const Tensor& x, const Tensor* w, const Tensor* r, const Tenso
 }
 
 void act_mul_had(HadAct act, const Tensor& x, const Tensor& y, const Tensor& out, const Tensor* pre_scale,
-                 const Tensor* z, float act_limit, float had_scale, const Stream& s)
+                 const Tensor* z, float act_limit, float had_scale, const Stream& s, bool rotate_x, bool rotate_y,
+                 const Tensor* x_post, const Tensor* y_post)
 {
     int64_t rows, cols, ldx, ry, cy, ldy, ro, co, ldo, ldz = 0;
     x.rows_view(rows, cols, ldx);
@@ -326,7 +327,8 @@ void act_mul_had(HadAct act, const Tensor& x, const Tensor& y, const Tensor& out
         require(rz == rows && cz == cols && z->dtype == DType::F16, "act_mul_had: z is f16 shaped like x");
     }
     check_abi(exl3r_act_mul_had((int)act, x.data, y.data, code(x.dtype), ldx, ldy, z ? z->data : nullptr, ldz,
-                                ptr(pre_scale), out.data, ldo, rows, cols, act_limit, had_scale, s.get()));
+                                ptr(pre_scale), out.data, ldo, rows, cols, act_limit, had_scale,
+                                (rotate_x ? 1 : 0) | (rotate_y ? 2 : 0), ptr(x_post), ptr(y_post), s.get()));
 }
 
 void argmax_sample(const Tensor& logits, const Tensor& ids, int max_logit, const Stream& s)

@@ -193,8 +193,11 @@ void rms_norm_had(const Tensor& x, const Tensor* w, const Tensor* r, const Tenso
 // Gated activation whose f16 output feeds the next projection's had_r_128(z, pre_scale)
 // (src/modules.rs:932-940 then 224-227): silu(x) * y, gelu(x) * y or x * sigmoid(y); z kept when given.
 enum class HadAct : int { Silu = EXL3R_ACT_SILU, Gelu = EXL3R_ACT_GELU, MulSigmoid = EXL3R_ACT_MUL_SIGMOID };
+// rotate_x / rotate_y: the f16 input is first given its projection's output rotation (post-scale x_post /
+// y_post, or none).
 void act_mul_had(HadAct act, const Tensor& x, const Tensor& y, const Tensor& out, const Tensor* pre_scale,
-                 const Tensor* z, float act_limit, float had_scale, const Stream& s);
+                 const Tensor* z, float act_limit, float had_scale, const Stream& s, bool rotate_x = false,
+                 bool rotate_y = false, const Tensor* x_post = nullptr, const Tensor* y_post = nullptr);
 // Embedding gather: out[i] = table[ids[i]] (bit-exact, or exact upcast to f32); err_flag optional.
 void embedding(const Tensor& table, const Tensor& ids, const Tensor& out, int32_t* err_flag, const Stream& s);
 // Gather fused with the following RMSNorm; h optional.

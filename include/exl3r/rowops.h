@@ -373,12 +373,17 @@ EXL3R_API int exl3r_rms_norm_had(const void* x, int x_dtype, int64_t ldx, const 
  *         only when z != NULL (row stride ldz);
  *   out = had_r_128(z, pre_scale) with scale had_scale: f16 [rows, cols], row stride ldo;
  *         pre_scale is f16 [cols] (the projection's suh) or NULL.
+ *   rotate_in: bit 0 / bit 1 -- x / y (f16, the raw output of an EXL3 projection: gate_proj and up_proj
+ *         in the MLP) is first given that projection's output rotation had_r_128(v, v, NULL, post, 1.0)
+ *         (src/modules.rs:231) with post = x_post_scale / y_post_scale (f16 [cols] svh, or NULL); x and y
+ *         are not written.  Needs 16-byte aligned rows.
  * x, y: [rows, cols] of in_dtype (F16/BF16/F32), row strides ldx, ldy; cols % 128 == 0; out and z
  * alias nothing.  Bit-identical to the unfused calls; rows that are not 16-byte aligned run them.
  */
 EXL3R_API int exl3r_act_mul_had(int act, const void* x, const void* y, int in_dtype, int64_t ldx, int64_t ldy,
                       void* z, int64_t ldz, const void* pre_scale, void* out, int64_t ldo,
-                      int64_t rows, int64_t cols, float act_limit, float had_scale, void* stream);
+                      int64_t rows, int64_t cols, float act_limit, float had_scale, int rotate_in,
+                      const void* x_post_scale, const void* y_post_scale, void* stream);
 
 /*
  * Token-embedding gather: out[i, :] = table[ids[i], :], bit-exact (same dtype) or exactly upcast to

@@ -5,7 +5,9 @@ activation's own tolerance (<= 1 ulp of f16); the projection input is checked bi
 the oracle's had_r_128 of that z, and against the unfused GPU calls (exl3r_silu_mul / gelu_mul /
 mul_sigmoid into an f16 z, then exl3r_had_r_128).  Covers the MLP prefill shape of Qwen3-32B, every
 input dtype, act_limit, a missing pre-scale, a scalar transform scale, strided and unaligned rows
-(the unfused fallback), zero rows and the argument errors."""
+(the unfused fallback), zero rows and the argument errors; and with x and / or y given their producing
+projection's output rotation on load (the MLP from the raw gate_proj / up_proj outputs), checked
+bitwise against the rotations run first."""
 import numpy as np
 import pytest
 import torch
@@ -90,6 +92,52 @@ def test_strided_and_unaligned_rows():
     run("mul_sigmoid", 7, 256, BF16, off=1, with_z=False, seed=9)    # unaligned base: fallback into out
 
 
+def run_rotated(act, rows, cols, rot_x, rot_y, posts=True, with_z=True, seed=0):
+    """x / y are raw projection outputs: the fused call rotates them on load; the reference path rotates
+    them first (had_r_128 with post-scale), then runs the unfused activation and input rotation."""
+    x = dev_normal((rows, cols), 0, 2, F16, seed)
+    y = dev_normal((rows, cols), 0, 1, F16, seed + 1)
+    p = suh(cols, seed + 2)
+    xs = suh(cols, seed + 3) if rot_x and posts else None
+    ys = suh(cols, seed + 4) if rot_y and posts else None
+    z = torch.empty((rows, cols), device="cuda", dtype=torch.float16) if with_z else None
+    out = torch.empty((rows, cols), device="cuda", dtype=torch.float16)
+    ffi.act_mul_had(act, x, y, out, p, z, rotate_x=rot_x, rotate_y=rot_y, x_post_scale=xs, y_post_scale=ys)
+    rx, ry = x, y
+    if rot_x:
+        rx = torch.empty_like(x)
+        ffi.had_r_128(x, rx, None, xs)
+    if rot_y:
+        ry = torch.empty_like(y)
+        ffi.had_r_128(y, ry, None, ys)
+    ez, eout = unfused(act, rx, ry, p, 0.0, 1.0)
+    torch.cuda.synchronize()
+    tag = f"{act}_had rotated x{int(rot_x)} y{int(rot_y)} {rows}x{cols}"
+    assert_bitwise(from_dev(out), from_dev(eout), what=tag + " vs unfused")
+    if with_z:
+        assert_bitwise(from_dev(z), from_dev(ez), what=tag + " z vs unfused")
+        # the rotated inputs against the oracle's rotation, bit for bit
+        ox = orc.had_r_128(np.ascontiguousarray(from_dev(x)), F16, post=from_dev(xs) if xs is not None else None,
+                           nthreads=NTHREADS) if rot_x else from_dev(x)
+        oy = orc.had_r_128(np.ascontiguousarray(from_dev(y)), F16, post=from_dev(ys) if ys is not None else None,
+                           nthreads=NTHREADS) if rot_y else from_dev(y)
+        assert_bitwise(from_dev(rx), ox, what=tag + " rotated x")
+        assert_bitwise(from_dev(ry), oy, what=tag + " rotated y")
+        assert_close_ulp(from_dev(z), oracle_act(act, rx, ry, F16, 0.0), F16, 1, what=tag + " z vs oracle")
+
+
+def test_mlp_tail_rotated_gate_and_up():
+    """The Qwen3-32B MLP at prefill from the raw gate_proj / up_proj outputs: their svh rotations, silu(g) * u
+    and down_proj's input rotation in one pass."""
+    run_rotated("silu", 1024, 25600, True, True, with_z=False, seed=21)
+
+
+@pytest.mark.parametrize("act,rx,ry", [("silu", True, False), ("gelu", False, True), ("mul_sigmoid", False, True),
+                                       ("mul_sigmoid", True, True)])
+def test_rotated_inputs(act, rx, ry):
+    run_rotated(act, 33, 1024, rx, ry, posts=act != "gelu", seed=22)
+
+
 def test_zero_rows_and_errors():
     z0 = torch.empty((0, 256), device="cuda", dtype=torch.float16)
     ffi.act_mul_had("silu", z0, z0, torch.empty_like(z0))
@@ -103,6 +151,14 @@ def test_zero_rows_and_errors():
     with pytest.raises(exl3r.Exl3rError):
         ffi.act_mul_had("mul_sigmoid", x, y, torch.empty_like(x), act_limit=1.0)
     rc = exl3r.load().exl3r_act_mul_had(7, x.data_ptr(), y.data_ptr(), F16, 256, 256, None, 0, None,
-                                        torch.empty_like(x).data_ptr(), 256, 4, 256, 0.0, 1.0, None)
+                                        torch.empty_like(x).data_ptr(), 256, 4, 256, 0.0, 1.0, 0, None, None, None)
     assert rc == exl3r.EINVAL
+    with pytest.raises(exl3r.Exl3rError):                                   # rotated inputs are f16
+        xb = x.to(torch.bfloat16)
+        ffi.act_mul_had("silu", xb, xb.clone(), torch.empty_like(x), rotate_x=True)
+    with pytest.raises(exl3r.Exl3rError):                                   # post-scale without its rotation
+        ffi.act_mul_had("silu", x, y, torch.empty_like(x), y_post_scale=suh(256, 1))
+    with pytest.raises(exl3r.Exl3rError):                                   # unaligned rows cannot rotate inputs
+        xs = dev_normal((4, 259), 0, 1, F16, 13)[:, :256]
+        ffi.act_mul_had("silu", xs, xs, torch.empty_like(x), rotate_x=True)
     torch.cuda.synchronize()
