@@ -12,7 +12,7 @@ import exl3r.ffi as ffi
 from _gpu import NTHREADS, TORCH_DT, assert_bitwise, dev_normal, from_dev
 from oracle import oracle as orc
 from test_gpu_act import run as run_act
-from test_gpu_act_had import run as run_act_had
+from test_gpu_act_had import run as run_act_had, run_rotated as run_act_had_rotated
 from test_gpu_argmax import run as run_argmax
 from test_gpu_embedding import check_gather, run_fused
 from test_gpu_gated import check as check_gate, run_gated
@@ -208,6 +208,10 @@ def test_fuzz_hadamard(case):
     run_act_had(pick(rng, ["silu", "gelu", "mul_sigmoid"]), int(rng.integers(1, 300)), 128 * int(rng.integers(1, 80)),
                 pick(rng, FLOATS), with_z=bool(rng.random() < 0.6), pre=bool(rng.random() < 0.8),
                 ld=None if rng.random() < 0.7 else 128 * int(rng.integers(81, 90)) + int(pick(rng, [0, 8, 3])), seed=case + 5)
+    rx = bool(rng.random() < 0.7)
+    run_act_had_rotated(pick(rng, ["silu", "gelu", "mul_sigmoid"]), int(rng.integers(1, 200)),
+                        128 * int(rng.integers(1, 60)), rx, (not rx) or bool(rng.random() < 0.6),
+                        posts=bool(rng.random() < 0.8), with_z=bool(rng.random() < 0.6), seed=case + 6)
 
 
 @pytest.mark.parametrize("case", CASES)
