@@ -36,7 +36,8 @@ OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "
        "deinterleave_q35", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
        "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_unfused", "silu_had_c3",
        "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_unfused",
-       "rope_kv_had_prefill", "rope_kv_had_prefill_unfused", "mlp_had_c3", "mlp_had_c3_unfused", "calib_copy",
+       "rope_kv_had_prefill", "rope_kv_had_prefill_unfused", "mlp_had_c3", "mlp_had_c3_unfused",
+       "prefill_layer", "prefill_layer_unfused", "calib_copy",
        "calib_copy_cached"]
 
 
@@ -447,6 +448,92 @@ def make_act_had(name, rows, cols, fused, seed=780, rotate=False):
     return Work(name, nbytes, launch, f"{head}SiLU(gate)*up -> Hadamard input [{rows},{cols}] f16, {kind}", sets)
 
 
+def make_prefill_layer(name, fused, T=4096, seed=900):
+    """The row ops and Hadamard rotations of one Qwen3-32B prefill layer (hidden 5120, 64 / 8 heads of
+    128, intermediate 25600, f16 activations, f32 residual, 256-token pages), GEMMs and attention
+    excluded.  Unfused, in the reference's order (src/modules.rs:224-231, 372-411, 669-704, 932-940,
+    1020-1035): down_proj's output rotation, the residual norm, q / k / v input rotations, their output
+    rotations, RoPE, the paged append, o_proj's input and output rotations, the residual norm, gate /
+    up input rotations, their output rotations, silu_mul and down_proj's input rotation -- 20 launches.
+    Fused: exl3r_rms_norm_had (rotate_x, 3 outputs), exl3r_rope_paged_kv_had, had_r_128 (o_proj input,
+    after attention), exl3r_rms_norm_had (rotate_x, 2 outputs), exl3r_act_mul_had (both inputs
+    rotated) -- 5 launches.  Bytes are the fused launches' algorithmic bytes."""
+    import numpy as np
+    import torch
+    import exl3r
+    import exl3r.ffi as ffi
+    H, hq, hk, hd, I, page = 5120, 64, 8, 128, 25600, 256
+    f16 = torch.float16
+
+    def sgn(n):
+        return torch.where(torch.rand(n, device="cuda") < 0.5, -1.0, 1.0).to(f16)
+    r = gen((T, H), 0.0, 4.0, torch.float32, seed)
+    y_down, y_o = gen((T, H), 0.0, 1.0, f16, seed + 1), gen((T, H), 0.0, 1.0, f16, seed + 2)
+    q = gen((1, T, hq, hd), 0.0, 1.0, f16, seed + 3)
+    k, v = gen((1, T, hk, hd), 0.0, 1.0, f16, seed + 4), gen((1, T, hk, hd), 0.0, 1.0, f16, seed + 5)
+    o = gen((T, hq * hd), 0.0, 1.0, f16, seed + 6)
+    g, u = gen((T, I), 0.0, 1.0, f16, seed + 7), gen((T, I), 0.0, 1.0, f16, seed + 8)
+    w1, w2 = gen((H,), 1.0, 0.1, f16, seed + 9), gen((H,), 1.0, 0.1, f16, seed + 10)
+    qn, kn = gen((hd,), 1.0, 0.1, f16, seed + 11), gen((hd,), 1.0, 0.1, f16, seed + 12)
+    suh_q, suh_k, suh_v, suh_g, suh_u = sgn(H), sgn(H), sgn(H), sgn(H), sgn(H)
+    svh_q, svh_k, svh_v, svh_o, svh_g, svh_u, svh_d = (sgn(hq * hd), sgn(hk * hd), sgn(hk * hd), sgn(H), sgn(I),
+                                                       sgn(I), sgn(H))
+    suh_o, suh_d = sgn(hq * hd), sgn(I)
+    xq, xk, xv, xg, xu = (torch.empty((T, H), device="cuda", dtype=f16) for _ in range(5))
+    xo = torch.empty((T, hq * hd), device="cuda", dtype=f16)
+    xd, a = torch.empty((T, I), device="cuda", dtype=f16), torch.empty((T, I), device="cuda", dtype=f16)
+    y = torch.empty((T, H), device="cuda", dtype=f16)
+    max_blocks = T // page + 2
+    pages = max_blocks + 2
+    rng = np.random.default_rng(seed)
+    bt = torch.from_numpy(rng.permutation(pages)[:max_blocks].reshape(1, max_blocks).astype(np.int32)).cuda()
+    sl = torch.zeros(1, dtype=torch.int32, device="cuda")
+    kc = torch.empty((pages, page, hk, hd), device="cuda", dtype=f16)
+    vc = torch.empty_like(kc)
+    inv = torch.from_numpy((1.0 / 1e6 ** (np.arange(0, hd, 2, dtype=np.float64) / hd)).astype(np.float32)).cuda()
+    naive = exl3r.load_naive()
+    N = T * H
+    nbytes = (N * (2 + 4 + 4 + 3 * 2) + 5 * H * 2                                     # norm -> q / k / v inputs
+              + 2 * T * (hq + hk) * hd * 2 + T * hk * hd * 2 * 3 + 4 + 2 * hd * 2 + (hq + 2 * hk) * hd * 2   # rope + append
+              + 2 * T * hq * hd * 2 + hq * hd * 2                                   # o_proj input rotation
+              + N * (2 + 4 + 4 + 2 * 2) + 4 * H * 2                                 # norm -> gate / up inputs
+              + T * I * 6 + 3 * I * 2)                                              # MLP tail
+
+    def launch(i):
+        if fused:
+            ffi.rms_norm_had(y_down, w1, [xq, xk, xv], [suh_q, suh_k, suh_v], 1e-6, r=r, rotate_x=True,
+                             x_post_scale=svh_d)
+            ffi.rope_paged_kv_had(q, q, k, k, v, inv, 0, sl, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, kc, vc, bt, sl,
+                                  q_post_scale=svh_q, k_post_scale=svh_k, v_post_scale=svh_v)
+            ffi.had_r_128(o, xo, suh_o)
+            ffi.rms_norm_had(y_o, w2, [xg, xu], [suh_g, suh_u], 1e-6, r=r, rotate_x=True, x_post_scale=svh_o)
+            ffi.act_mul_had("silu", g, u, xd, suh_d, rotate_x=True, rotate_y=True, x_post_scale=svh_g,
+                            y_post_scale=svh_u)
+            return
+        ffi.had_r_128(y_down, y_down, None, svh_d)
+        ffi.rms_norm_res_in(y_down, w1, y, r, 1e-6)
+        for x_, s_ in ((xq, suh_q), (xk, suh_k), (xv, suh_v)):
+            ffi.had_r_128(y, x_, s_)
+        for t_, s_ in ((q, svh_q), (k, svh_k), (v, svh_v)):
+            ffi.had_r_128(t_.view(T, -1), t_.view(T, -1), None, s_)
+        ffi.rope(q, q, k, k, inv, 0, sl, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0)
+        rc = naive.naive_paged_kv_update_f16(k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(),
+                                             sl.data_ptr(), 1, T, hk, hd, max_blocks, page,
+                                             torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        ffi.had_r_128(o, xo, suh_o)
+        ffi.had_r_128(y_o, y_o, None, svh_o)
+        ffi.rms_norm_res_in(y_o, w2, y, r, 1e-6)
+        for x_, s_ in ((xg, suh_g), (xu, suh_u)):
+            ffi.had_r_128(y, x_, s_)
+        ffi.had_r_128(g, g, None, svh_g)
+        ffi.had_r_128(u, u, None, svh_u)
+        ffi.silu_mul(g, u, a)
+        ffi.had_r_128(a, xd, suh_d)
+    kind = "fused (5 launches)" if fused else "unfused, the reference's order (20 launches)"
+    return Work(name, nbytes, launch, f"Qwen3-32B prefill layer row ops + rotations T={T}, {kind}")
+
+
 def make_copy(name, cached=False):
     import torch
     import exl3r
@@ -565,6 +652,8 @@ def make_all(only=None):
         "rope_kv_had_prefill_unfused": lambda: make_rope_kv("rope_kv_had_prefill_unfused", 1, 4096, False, had=True),
         "rope_had_c4": lambda: make_rope_had("rope_had_c4", ragged, 64, 8, 128, True),
         "rope_had_c4_unfused": lambda: make_rope_had("rope_had_c4_unfused", ragged, 64, 8, 128, False),
+        "prefill_layer": lambda: make_prefill_layer("prefill_layer", True),
+        "prefill_layer_unfused": lambda: make_prefill_layer("prefill_layer_unfused", False),
         "mlp_had_c3": lambda: make_act_had("mlp_had_c3", 8192, 17408, True, rotate=True),
         "mlp_had_c3_unfused": lambda: make_act_had("mlp_had_c3_unfused", 8192, 17408, False, rotate=True),
         "silu_had_c3": lambda: make_act_had("silu_had_c3", 8192, 17408, True),
@@ -763,7 +852,8 @@ def main():
                              ("norm_had_rot_c3", "rotate_res_norm_to_3_inputs_8192x5120"),
                              ("silu_had_c3", "silu_mul_to_input_8192x17408"), ("rope_had_c4", "qk_rotate_rope_c4"),
                              ("rope_kv_had_prefill", "qkv_rotate_rope_paged_append_4096"),
-                             ("mlp_had_c3", "rotate_gate_up_silu_mul_to_input_8192x17408")):
+                             ("mlp_had_c3", "rotate_gate_up_silu_mul_to_input_8192x17408"),
+                             ("prefill_layer", "qwen3_32b_prefill_layer_T4096")):
             f_us, u_us = ops[fused]["us"], ops[fused + "_unfused"]["us"]
             hadamard[label] = {"fused_us": f_us, "unfused_us": u_us, "speedup": round(u_us / f_us, 3)}
         hadamard["desc"] = ("the EXL3 linear's random-Hadamard rotation (had_r_128) alone, and fused into the op that "
