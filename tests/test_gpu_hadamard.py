@@ -61,6 +61,40 @@ def test_in_place_strided_and_unaligned():
     run(dev_normal((5, 384 + 3), 0, 1, F16, 10)[:, :384], F16, what="odd stride (generic kernel)")
 
 
+def test_signed_zeros_and_special_values():
+    """Zero blocks of either sign (an exact zero's sign follows the butterfly's order: (-0) + (-0) = -0,
+    (+0) - (+0) = +0), infinities, overflow to infinity and NaN, with a sign-flipping pre-scale.  Finite
+    and infinite results are compared bit for bit; NaN positions must agree (a NaN's sign and payload
+    are the arithmetic unit's own)."""
+    cols = 256
+    x = np.zeros((7, cols), np.float16)
+    x[1] = -0.0
+    x[2, ::3] = -0.0
+    x[3, 5] = np.inf
+    x[4, 7] = np.nan
+    x[5] = 60000.0
+    x[6, 3], x[6, 9] = np.inf, -np.inf
+    pre = np.where(np.arange(cols) % 5 == 0, -1.0, 1.0).astype(np.float16)
+    xd = torch.from_numpy(x.view(np.int16)).view(torch.float16).cuda()
+    pd = torch.from_numpy(pre.view(np.int16)).view(torch.float16).cuda()
+    for p_ in (None, pd):
+        out = torch.empty_like(xd)
+        ffi.had_r_128(xd, out, p_)
+        torch.cuda.synchronize()
+        got = from_dev(out).view(np.float16)
+        exp = orc.had_r_128(x.view(np.uint16), F16, pre=pre.view(np.uint16) if p_ is not None else None).view(np.float16)
+        gn, en = np.isnan(got), np.isnan(exp)
+        assert np.array_equal(gn, en), "NaN positions differ"
+        assert np.array_equal(got.view(np.uint16)[~gn], exp.view(np.uint16)[~en]), "non-NaN results differ bitwise"
+        if p_ is None:
+            # an all -0 block: only the all-plus row of H sums -0 + -0 ...; every other output is +0
+            assert np.array_equal(np.nonzero(np.signbit(got[1]))[0], [0, 128])
+            # one infinity spreads over its whole block (the other block stays zero); a constant block
+            # of 60000 sums to 60000 * sqrt(128) at output 0 -- past the f16 range -- and to zero elsewhere
+            assert np.isinf(got[3, :128]).all() and not got[3, 128:].any()
+            assert np.isinf(got[5, [0, 128]]).all() and not np.delete(got[5], [0, 128]).any()
+
+
 def test_involution_on_device():
     x = dev_normal((64, 512), 0, 1, F32, 11)
     y = torch.empty_like(x)

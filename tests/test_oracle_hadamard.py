@@ -60,6 +60,18 @@ def test_unit_vectors_exact_and_blocks_independent():
     assert not got[:, 128:].any()
 
 
+def test_signed_zeros_follow_the_butterfly():
+    """IEEE rules fix the sign of an exact zero: (-0) + (-0) = -0 and every difference of equal zeros
+    is +0.  An all -0 block therefore gives -0 only at output 0 (the all-plus row of H, reached by
+    additions alone) and +0 elsewhere; an all +0 block gives +0 everywhere."""
+    x = np.zeros((2, 256), np.float16)
+    x[1] = -0.0
+    o = orc.had_r_128(x.view(np.uint16), F16).view(np.float16)
+    assert not np.signbit(o[0]).any()
+    assert np.array_equal(np.nonzero(np.signbit(o[1]))[0], [0, 128])
+    assert not o.any()
+
+
 def test_involution():
     x = np.random.default_rng(2).standard_normal((8, 384)).astype(np.float32)
     back = orc.had_r_128(orc.had_r_128(x, F32), F32)
