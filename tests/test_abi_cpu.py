@@ -162,3 +162,134 @@ def test_rope_paged_kv_validation():
     assert call(dt=F32) == exl3r.EDTYPE
     assert call(hkv=0) == exl3r.EINVAL
     assert call(q=None, oq=None, k=None, v=None, kc=None, vc=None, bt=None, sl=None, seq=0) == exl3r.OK
+
+
+def test_gated_and_gate_ops_validation():
+    lib = exl3r.load()
+    # exl3r_gated_rms_norm(x, xt, ldx, w, wt, w_groups, y, yt, ldy, g, gt, ldg, rows, dim, eps, cb, gate_first, gate_act)
+    base = [FAKE, BF16, 128, None, F32, 1, FAKE + 65536, F16, 128, FAKE + 131072, F32, 128, 4, 128, 1e-6, 0.0, 0, 0]
+    def gated(**kw):
+        a = list(base)
+        for i, v in kw.items():
+            a[int(i[1:])] = v
+        return lib.exl3r_gated_rms_norm(*a, None)
+    assert gated(a10=7) == exl3r.EDTYPE
+    assert gated(a11=64) == exl3r.EINVAL and "gate row stride" in _err()
+    assert gated(a5=0) == exl3r.EINVAL and "w_groups" in _err()
+    assert gated(a17=2) == exl3r.EINVAL and "gate_act" in _err()
+    assert gated(a9=None) == exl3r.EINVAL
+    assert gated(a9=FAKE + 65536) == exl3r.EINVAL and "alias" in _err()
+    assert gated(a12=0) == exl3r.OK
+    # exl3r_mul_sigmoid(x, y, in_dtype, z, z_dtype, rows, cols, ldx, ldy, ldz)
+    assert lib.exl3r_mul_sigmoid(FAKE, FAKE + 4096, 7, FAKE + 8192, F16, 2, 8, 8, 8, 8, None) == exl3r.EDTYPE
+    assert lib.exl3r_mul_sigmoid(FAKE, FAKE + 4096, F16, FAKE + 8192, F16, 2, 8, 4, 8, 8, None) == exl3r.EINVAL
+    assert lib.exl3r_mul_sigmoid(FAKE, FAKE + 4096, F16, FAKE + 8192, F16, 0, 8, 8, 8, 8, None) == exl3r.OK
+    # exl3r_deinterleave_qg(qg, ld_qg, q, ld_q, g, ld_g, dtype, rows, heads, head_dim)
+    assert lib.exl3r_deinterleave_qg(FAKE, 512, FAKE + 4096, 256, FAKE + 8192, 256, I32, 2, 2, 128, None) == exl3r.EDTYPE
+    assert lib.exl3r_deinterleave_qg(FAKE, 256, FAKE + 4096, 256, FAKE + 8192, 256, F16, 2, 2, 128, None) == exl3r.EINVAL
+    assert lib.exl3r_deinterleave_qg(FAKE, 512, FAKE, 256, FAKE + 8192, 256, F16, 2, 2, 128, None) == exl3r.EINVAL
+    assert "alias" in _err()
+    assert lib.exl3r_deinterleave_qg(None, 512, None, 256, None, 256, F16, 0, 2, 128, None) == exl3r.OK
+
+
+def test_sampling_validation():
+    lib = exl3r.load()
+    for fn, extra in ((lib.exl3r_argmax_sample, ()), (lib.exl3r_gumbel_sample, (7,))):
+        # (logits, dtype, rows, vocab, ld, max_logit[, random], ids)
+        assert fn(FAKE, I64, 2, 100, 100, 0, *extra, FAKE + 4096, None) == exl3r.EDTYPE
+        assert fn(FAKE, F16, 2, 0, 100, 0, *extra, FAKE + 4096, None) == exl3r.EINVAL
+        assert fn(FAKE, F16, 2, 100, 50, 0, *extra, FAKE + 4096, None) == exl3r.EINVAL and "ld" in _err()
+        assert fn(FAKE, F16, 2, 100, 100, 0, *extra, None, None) == exl3r.EINVAL and "non-null" in _err()
+        assert fn(None, F16, 0, 100, 100, 0, *extra, None, None) == exl3r.OK
+    # exl3r_gumbel_noise(x, x_dtype, ldx, out, out_dtype, ldo, rows, cols, random)
+    assert lib.exl3r_gumbel_noise(FAKE, F16, 64, FAKE + 8192, I32, 64, 2, 64, 1, None) == exl3r.EDTYPE
+    assert lib.exl3r_gumbel_noise(FAKE, F16, 32, FAKE + 8192, F32, 64, 2, 64, 1, None) == exl3r.EINVAL
+    assert lib.exl3r_gumbel_noise(None, F16, 64, None, F32, 64, 2, 0, 1, None) == exl3r.OK
+
+
+def test_rope_table_validation():
+    lib = exl3r.load()
+    def call(rows=16, bstride=0, table=FAKE + 65536):
+        return lib.exl3r_rope_table(FAKE, FAKE, 4 * 64, 64, 4, None, None, 0, 64, 0, F16, 1, 3, 64, table, rows,
+                                    bstride, 64, 0, None, None, None, None, F16, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0,
+                                    None, None)
+    assert call(rows=0) == exl3r.EINVAL and "table_rows" in _err()
+    assert call(bstride=-1) == exl3r.EINVAL
+    assert call(table=None) == exl3r.EINVAL and "angle table" in _err()
+
+
+def test_hadamard_validation():
+    lib = exl3r.load()
+    # exl3r_had_r_128(x, dtype, ldx, out, ldo, rows, cols, pre, post, scale)
+    assert lib.exl3r_had_r_128(FAKE, BF16, 256, FAKE + 8192, 256, 2, 256, None, None, 1.0, None) == exl3r.EDTYPE
+    assert lib.exl3r_had_r_128(FAKE, F16, 200, FAKE + 8192, 200, 2, 200, None, None, 1.0, None) == exl3r.EINVAL
+    assert "multiple of 128" in _err()
+    assert lib.exl3r_had_r_128(FAKE, F16, 256, FAKE + 8192, 256, 2, 256, FAKE, FAKE, 1.0, None) == exl3r.EINVAL
+    assert "at most one" in _err()
+    assert lib.exl3r_had_r_128(None, F16, 256, None, 256, 0, 256, None, None, 1.0, None) == exl3r.OK
+
+    arr = ctypes.c_void_p * 4
+    outs, pres = arr(FAKE + 65536, FAKE + 131072, 0, 0), arr(0, 0, 0, 0)
+    def norm_had(**kw):
+        # (x, xt, ldx, w, wt, r, rt, ldr, y, ldy, n_out, pres, outs, ldo, rows, dim, eps, cb, cs, had_scale,
+        #  rotate_x, x_post)
+        a = dict(x=FAKE, xt=F16, ldx=256, w=None, wt=F16, r=None, rt=F32, ldr=256, y=None, ldy=256, n=2, pres=pres,
+                 outs=outs, ldo=256, rows=4, dim=256, eps=1e-6, cb=0.0, cs=1.0, hs=1.0, rot=0, xpost=None)
+        a.update(kw)
+        return lib.exl3r_rms_norm_had(*a.values(), None)
+    assert norm_had(dim=200, ldx=200, ldo=200) == exl3r.EINVAL
+    assert norm_had(n=5) == exl3r.EINVAL and "n_out" in _err()
+    assert norm_had(xt=7) == exl3r.EDTYPE
+    assert norm_had(rot=1, xt=BF16) == exl3r.EDTYPE and "rotate_x" in _err()
+    assert norm_had(xpost=FAKE) == exl3r.EINVAL and "rotate_x" in _err()
+    assert norm_had(outs=arr(FAKE, FAKE + 131072, 0, 0)) == exl3r.EINVAL and "alias" in _err()
+    assert norm_had(outs=arr(FAKE + 65536, FAKE + 65536, 0, 0)) == exl3r.EINVAL and "alias" in _err()
+    assert norm_had(rows=0) == exl3r.OK
+
+    def act_had(**kw):
+        # (act, x, y, in_dtype, ldx, ldy, z, ldz, pre, out, ldo, rows, cols, act_limit, had_scale, rotate_in,
+        #  x_post, y_post)
+        a = dict(act=0, x=FAKE, y=FAKE + 8192, it=F16, ldx=256,
+                 ldy=256, z=None, ldz=256, pre=None, out=FAKE + 65536, ldo=256, rows=4, cols=256, lim=0.0, hs=1.0,
+                 rot=0, xp=None, yp=None)
+        a.update(kw)
+        return lib.exl3r_act_mul_had(*a.values(), None)
+    assert act_had(act=9) == exl3r.EINVAL and "unknown act" in _err()
+    assert act_had(cols=200, ldx=200, ldy=200, ldo=200) == exl3r.EINVAL
+    assert act_had(out=FAKE) == exl3r.EINVAL and "alias" in _err()
+    assert act_had(rot=4) == exl3r.EINVAL
+    assert act_had(rot=1, it=BF16) == exl3r.EDTYPE
+    assert act_had(yp=FAKE) == exl3r.EINVAL and "post-scale" in _err()
+    assert act_had(act=2, lim=1.0) == exl3r.EINVAL and "act_limit" in _err()
+    assert act_had(rows=0) == exl3r.OK
+
+
+def test_rope_had_validation():
+    lib = exl3r.load()
+    def rope_had(**kw):
+        # (q, oq, q_ts, hq, k, ok, k_ts, hk, dtype, bsz, seq, hd, inv, R, pos, positions, ids, qn, kn, nwt, eps, cb,
+        #  mode, attn, q_post, k_post)
+        a = dict(q=FAKE, oq=FAKE, qts=4 * 128, hq=4, k=None, ok=None, kts=0, hk=0, dt=F16, bsz=1, seq=3, hd=128,
+                 inv=FAKE + 65536, R=128, pos=0, positions=None, ids=None, qn=None, kn=None, nwt=F16, eps=1e-6, cb=0.0,
+                 mode=exl3r.ROPE_NEOX, attn=1.0, qp=None, kp=None)
+        a.update(kw)
+        return lib.exl3r_rope_had(*a.values(), None)
+    assert rope_had(dt=BF16) == exl3r.EDTYPE
+    assert rope_had(hq=3, hd=64, R=64, qts=3 * 64) == exl3r.EINVAL and "multiple of 128" in _err()
+    assert rope_had(kp=FAKE) == exl3r.EINVAL
+    assert rope_had(inv=None) == exl3r.EINVAL
+    assert rope_had(seq=0) == exl3r.OK
+
+    def paged_had(**kw):
+        a = dict(q=FAKE, oq=FAKE, qts=4 * 128, hq=4, k=FAKE + 65536, ok=None, kts=2 * 128, v=FAKE + 98304,
+                 vts=2 * 128, hkv=2, dt=F16, bsz=1, seq=3, hd=128, inv=FAKE + 131072, R=128, pos=0, positions=None,
+                 ids=None, qn=None, kn=None, nwt=F16, eps=1e-6, cb=0.0, mode=exl3r.ROPE_NEOX, attn=1.0,
+                 kc=FAKE + 262144, vc=FAKE + 393216, page=256, pages=4, bt=FAKE + 524288, mb=2, sl=FAKE + 528384,
+                 err=None, qp=None, kp=None, vp=None)
+        a.update(kw)
+        return lib.exl3r_rope_paged_kv_had(*a.values(), None)
+    assert paged_had(dt=BF16) == exl3r.EDTYPE
+    assert paged_had(page=100) == exl3r.EINVAL
+    assert paged_had(v=None) == exl3r.EINVAL
+    assert paged_had(hkv=0) == exl3r.EINVAL
+    assert paged_had(seq=0, q=None, oq=None, k=None, v=None, kc=None, vc=None, bt=None, sl=None) == exl3r.OK
