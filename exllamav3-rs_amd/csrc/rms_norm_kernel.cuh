@@ -503,17 +503,24 @@ __global__ __launch_bounds__(256) void k_rms_norm_generic(RmsArgs a, int xt, int
 // Host-side launch.
 
 // Launch shape: a workgroup per row, MAXV chunks per thread.  Latency-bound launches (few rows)
-// spread a row over up to 1024 lanes; bandwidth-bound launches use <= 384 lanes per row so several
-// rows share a CU (C3 on MI355X, chunks x threads: 2 x 320 57.3 us, 2 x 384 56.9, 3 x 320 57.0,
-// 4 x 192 58.5, 5 x 128 59.4, 8 x 128 83.7, 1 x 640 70; one wave per row 74 us; persistent
-// workgroups prefetching the next row 58 us).
+// spread a row over up to 1024 lanes.  Bandwidth-bound launches (bf16 residual norm, 42 M elements,
+// MI355X, us; default before -> after this rule, best shape measured):
+//   dim 2048: 1 x 256 55.2 (3 x 256 54.5)   3584: 2 x 256 56.0 -> 1 x 448 55.1 (1 x 512 54.9)
+//   4096: 2 x 256 56.3 -> 1 x 512 55.2      5120: 2 x 320 57.1 -> 2 x 384 56.1 (best)
+//   7168: 4 x 256 58.8 -> 2 x 448 57.6 (3 x 448 57.1)   8192: 4 x 256 59.1 -> 2 x 512 56.7 (best)
+// so one chunk per lane up to 512 lanes, else two chunks on at least 384 lanes (at 5120 the 64
+// lanes without a second chunk pay off).  Not for the Hadamard kernels, whose chunks carry up to
+// four butterflies: at 5120 2 x 320 runs 133.8 / 141.5 us (3 outputs / with the input rotation)
+// against 134.4 / 144.4 us at 2 x 384.  Other C3 shapes: 3 x 320 56.3, 4 x 192 58.2, 5 x 128
+// 59.4, 8 x 128 83.7, 1 x 640 61.4; one wave per row 74 us; persistent workgroups prefetching the
+// next row 58 us.
 struct RmsShape
 {
     int maxv;
     int threads;
 };
 
-inline RmsShape rms_shape(int nc, int64_t rows)
+inline RmsShape rms_shape(int nc, int64_t rows, bool had = false)
 {
     auto thr = [&](int m) { int t = (nc + m - 1) / m; return ((t + 63) / 64) * 64; };
     const Tuning& tu = tuning();
@@ -521,18 +528,21 @@ inline RmsShape rms_shape(int nc, int64_t rows)
         (tu.rms_threads == 0 || (tu.rms_threads % 64 == 0 && tu.rms_threads <= 1024)))
         return { tu.rms_maxv, tu.rms_threads > 0 ? tu.rms_threads : thr(tu.rms_maxv) };
     // MAXV = 8 does not fit the VGPR budget of a 1024-thread bound; it is the last resort.
+    if (rows > 1024)
+    {
+        if (thr(1) <= 512) return { 1, thr(1) };
+        if (thr(2) <= 1024) return { 2, thr(2) > 384 || had ? thr(2) : 384 };
+    }
     static const int opts[3] = { 1, 2, 4 };
-    const int target = rows <= 1024 ? 1024 : 384;
     for (int m : opts)
-        if (thr(m) <= target) return { m, thr(m) };
-    if (thr(4) <= 1024) return { 4, thr(4) };
+        if (thr(m) <= 1024) return { m, thr(m) };
     return { 8, thr(8) };   // <= 1024 (rms_vec_ok bounds the row at 8192 chunks)
 }
 
 template <class XT, class YT, class RT, int MODE, int HAD = 0>
 int launch_rms_vec(const RmsArgs& a, hipStream_t s)
 {
-    const RmsShape sh = rms_shape(a.dim / 8, a.rows);
+    const RmsShape sh = rms_shape(a.dim / 8, a.rows, HAD != 0);
     const dim3 grid((unsigned)(a.rows < kMaxGridX ? a.rows : kMaxGridX));
     if constexpr (MODE == RMS_GATED)
     {
