@@ -33,7 +33,7 @@ METRIC = "fused norm/act/RoPE/embed HBM GB/s + % of MI355X peak; decode-step us"
 OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "gather_norm_c5", "rms_c1",
        "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "rope_kv_prefill",
        "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
-       "deinterleave_q35", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
+       "deinterleave_q35", "gated_norm_had_q35", "gated_norm_had_q35_unfused", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
        "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_unfused", "silu_had_c3",
        "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_unfused",
        "rope_kv_had_prefill", "rope_kv_had_prefill_unfused", "mlp_had_c3", "mlp_had_c3_unfused",
@@ -298,6 +298,27 @@ def make_gated(name, kind, tokens=4096, heads=32, hd=128, seed=600):
             x, g, y = bufs[i % sets]
             ffi.gated_rms_norm(x, w, y, g, 1e-6, 0.0, 1, False, 0)
         desc = f"gated RMSNorm (silu gate) [{tokens * heads},{hd}] bf16 x, f32 g, f16 y"
+    elif kind in ("norm_had", "norm_had_unfused"):
+        # ... feeding o_proj's input rotation (src/qwen3_5.rs:208-214): one fused launch, or the gated
+        # norm into y and exl3r_had_r_128; both count the fused job's bytes
+        nbytes = n * (2 + 4 + 2) + hd * 4 + heads * hd * 2
+        sets = sets_for(nbytes)
+        bufs = [(gen((tokens * heads, hd), 0.0, 1.0, torch.bfloat16, seed + 3 * k),
+                 gen((tokens * heads, hd), 0.0, 2.0, torch.float32, seed + 3 * k + 1),
+                 torch.empty((tokens, heads * hd), device="cuda", dtype=torch.float16)) for k in range(sets)]
+        w = gen((hd,), 1.0, 0.1, torch.float32, seed + 99)
+        suh = torch.where(torch.rand(heads * hd, device="cuda") < 0.5, -1.0, 1.0).to(torch.float16)
+        y = torch.empty((tokens * heads, hd), device="cuda", dtype=torch.float16)
+
+        def launch(i):
+            x, g, out = bufs[i % sets]
+            if kind == "norm_had":
+                ffi.gated_rms_norm_had(x, w, g, out.view(tokens * heads, hd), 1e-6, suh, pre_rows=heads)
+            else:
+                ffi.gated_rms_norm(x, w, y, g, 1e-6, 0.0, 1, False, 0)
+                ffi.had_r_128(y.view(tokens, heads * hd), out, suh)
+        desc = (f"gated RMSNorm [{tokens * heads},{hd}] -> o_proj input rotation [{tokens},{heads * hd}], "
+                f"{'fused' if kind == 'norm_had' else 'unfused (gated norm + had_r_128)'}")
     elif kind == "sigmoid":
         nbytes = 3 * n * 2
         sets = sets_for(nbytes)
@@ -636,6 +657,8 @@ def make_all(only=None):
         "gated_norm_q35": lambda: make_gated("gated_norm_q35", "norm"),
         "mul_sigmoid_q35": lambda: make_gated("mul_sigmoid_q35", "sigmoid"),
         "deinterleave_q35": lambda: make_gated("deinterleave_q35", "deinterleave"),
+        "gated_norm_had_q35": lambda: make_gated("gated_norm_had_q35", "norm_had"),
+        "gated_norm_had_q35_unfused": lambda: make_gated("gated_norm_had_q35_unfused", "norm_had_unfused"),
         "argmax_dec": lambda: make_argmax("argmax_dec", 64, False),
         "argmax_dec_torch": lambda: make_argmax("argmax_dec_torch", 64, True),
         "argmax_prefill": lambda: make_argmax("argmax_prefill", 1024, False),
@@ -853,7 +876,8 @@ def main():
                              ("silu_had_c3", "silu_mul_to_input_8192x17408"), ("rope_had_c4", "qk_rotate_rope_c4"),
                              ("rope_kv_had_prefill", "qkv_rotate_rope_paged_append_4096"),
                              ("mlp_had_c3", "rotate_gate_up_silu_mul_to_input_8192x17408"),
-                             ("prefill_layer", "qwen3_32b_prefill_layer_T4096")):
+                             ("prefill_layer", "qwen3_32b_prefill_layer_T4096"),
+                             ("gated_norm_had_q35", "qwen35_gdn_norm_to_o_proj_input_4096x32x128")):
             f_us, u_us = ops[fused]["us"], ops[fused + "_unfused"]["us"]
             hadamard[label] = {"fused_us": f_us, "unfused_us": u_us, "speedup": round(u_us / f_us, 3)}
         hadamard["desc"] = ("the EXL3 linear's random-Hadamard rotation (had_r_128) alone, and fused into the op that "

@@ -59,3 +59,70 @@ extern "C" int exl3r_gated_rms_norm(const void* x, int xt, int64_t ldx, const vo
     }
     return launch_status(op);
 }
+
+extern "C" int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out, int64_t ldo, int64_t rows,
+                               int64_t cols, const void* pre_scale, const void* post_scale, float scale, void* stream);
+
+// exl3r_gated_rms_norm with an f16 output feeding the next EXL3 projection's input rotation, in one
+// pass: the gated-delta-net output norm, then o_proj's had_r_128(y, suh) (src/qwen3_5.rs:208-214,
+// src/modules.rs:224-227).  A 128-column block of the rotation is 16 lanes of one row's lane group.
+extern "C" int exl3r_gated_rms_norm_had(const void* x, int xt, int64_t ldx, const void* w, int wt, int w_groups,
+                                        const void* g, int gt, int64_t ldg, void* y, int64_t ldy,
+                                        const void* pre_scale, int pre_rows, void* out, int64_t ldo, int64_t rows,
+                                        int64_t dim, float eps, float constant_bias, int gate_first, int gate_act,
+                                        float had_scale, void* stream)
+{
+    const char* op = "exl3r_gated_rms_norm_had";
+    if (dim <= 0 || dim % 128) return set_error(EXL3R_EINVAL, "%s: dim %lld must be a multiple of 128", op, (long long)dim);
+    int rc = check_rms_common(op, x, xt, ldx, w, wt, out, EXL3R_F16, ldo, rows, dim);
+    if (rc) return rc;
+    if (!is_float_dtype(gt)) return set_error(EXL3R_EDTYPE, "%s: unsupported gate dtype %s", op, dtype_name(gt));
+    if (ldg < dim || (y && rows > 1 && ldy < dim))
+        return set_error(EXL3R_EINVAL, "%s: gate / y row stride below dim %lld", op, (long long)dim);
+    if (w_groups < 1) return set_error(EXL3R_EINVAL, "%s: w_groups must be >= 1", op);
+    if (pre_rows < 1) return set_error(EXL3R_EINVAL, "%s: pre_rows must be >= 1", op);
+    if (gate_act != 0 && gate_act != 1) return set_error(EXL3R_EINVAL, "%s: gate_act must be 0 (silu) or 1 (sigmoid)", op);
+    if (rows == 0) return EXL3R_OK;
+    if (!g) return set_error(EXL3R_EINVAL, "%s: gate g must be non-null", op);
+    if (pre_rows > 1 && (rows % pre_rows || ldo != dim || (y && ldy != dim)))
+        return set_error(EXL3R_EINVAL, "%s: pre_rows > 1 needs whole projection rows of dense norm rows", op);
+    if (out == x || out == g || out == y || (y && (y == x || y == g)))
+        return set_error(EXL3R_EINVAL, "%s: out and y must not alias the inputs or each other", op);
+
+    RmsArgs a{};
+    a.x = x; a.ldx = ldx; a.w = w; a.wt = wt; a.y = y; a.ldy = y ? ldy : dim; a.r = const_cast<void*>(g); a.ldr = ldg;
+    a.rows = rows; a.dim = (int)dim; a.eps = eps; a.cb = constant_bias; a.cs = 1.0f;
+    a.gact = gate_act; a.gfirst = gate_first != 0; a.w_groups = w_groups;
+    a.nh = 1; a.hpre[0] = pre_scale; a.hpre_rows = pre_rows; a.hout[0] = out; a.ldh = rows > 1 ? ldo : dim;
+    a.hr = had_scale * 0.0883883461356163f;
+    hipStream_t s = (hipStream_t)stream;
+    const bool short_rows = dim <= 512 && (gt == EXL3R_F32 || gt == EXL3R_BF16);
+    const bool aligned = aligned16(out) && (a.ldh * 2) % 16 == 0 && (!pre_scale || aligned16(pre_scale));
+    if (xt != EXL3R_F32 && aligned && rms_vec_ok(a, xt, EXL3R_F16, gt, true))
+    {
+        auto go_x = [&](auto X) {
+            using XTy = decltype(X);
+            if (short_rows)
+            {
+                if (gt == EXL3R_F32) launch_rms_rows<XTy, TF16, TF32, RMS_GATED, HAD_OUT>(a, s);
+                else launch_rms_rows<XTy, TF16, TBF16, RMS_GATED, HAD_OUT>(a, s);
+                return;
+            }
+            with_float_type(gt, [&](auto G) { launch_rms_vec<XTy, TF16, decltype(G), RMS_GATED, HAD_OUT>(a, s); });
+        };
+        if (xt == EXL3R_F16) go_x(TF16{});
+        else go_x(TBF16{});
+        return launch_status(op);
+    }
+    // Otherwise the calls one after another: the norm into y (or into out), then the rotation.
+    void* dst = y ? y : out;
+    const int64_t ldd = y ? a.ldy : a.ldh;
+    rc = exl3r_gated_rms_norm(x, xt, ldx, w, wt, w_groups, dst, EXL3R_F16, ldd, g, gt, ldg, rows, dim, eps, constant_bias,
+                              gate_first, gate_act, stream);
+    // With pre_rows > 1 the norm rows are dense, so pre_rows of them form one projection row.
+    const int64_t prow = rows / pre_rows, pcols = dim * pre_rows;
+    if (rc == EXL3R_OK)
+        rc = exl3r_had_r_128(dst, EXL3R_F16, pre_rows > 1 ? pcols : ldd, out, pre_rows > 1 ? pcols : a.ldh,
+                             pre_rows > 1 ? prow : rows, pre_rows > 1 ? pcols : dim, pre_scale, nullptr, had_scale, stream);
+    return rc;
+}

@@ -52,6 +52,10 @@ struct RmsArgs
     void* hout[4];
     int64_t ldh;
     float hr;
+    // Row r of the norm takes pre-scale row r % hpre_rows ([hpre_rows, dim], 0 or 1: one row): a
+    // projection input made of several norm rows (the head-dim rows of a gated norm) has one scale
+    // per column of the whole input row.
+    int hpre_rows;
     // HAD_IN kernels: f16 x is first replaced by had_r_128(x) * hxpost (the EXL3 linear's output
     // rotation with its f16 post-scale, or none when null).
     const void* hxpost;
@@ -296,7 +300,7 @@ __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* 
             TF16::Vec v = yv;
             if (a.hpre[i])
             {
-                const TF16::Vec p = load8<TF16>(a.hpre[i], e);
+                const TF16::Vec p = load8<TF16>(a.hpre[i], (a.hpre_rows > 1 ? (row % a.hpre_rows) * a.dim : 0) + e);
                 #pragma unroll
                 for (int q = 0; q < 4; ++q) v.a[q] = hmul2(v.a[q], p.a[q]);
             }
@@ -365,7 +369,7 @@ __global__ __launch_bounds__(1024) void k_rms_norm(RmsArgs a)
 // chunk per lane, 256 / LPR rows per workgroup and RPL rows per lane in flight.  The row sum is a
 // DPP butterfly inside the LPR-lane group -- no LDS, no barrier -- so a 128-element head row costs
 // 16 lanes instead of a workgroup.
-template <class XT, class YT, class RT, int LPR, int RPL, int MODE>
+template <class XT, class YT, class RT, int LPR, int RPL, int MODE, int HAD = 0>
 __global__ __launch_bounds__(256) void k_rms_rows(RmsArgs a)
 {
     static_assert(MODE != RMS_GATHER, "gathered rows take the workgroup kernel");
@@ -403,13 +407,13 @@ __global__ __launch_bounds__(256) void k_rms_rows(RmsArgs a)
             ss = group_sum64<LPR>(ss);
             const float rmf = rms_factor(ss, a.dim, a.eps) * a.cs;
             if (act[i])
-                rms_chunk2<XT, YT, RT, MODE, 0>(a, row, (char*)a.y + row * a.ldy * YT::bytes, e,
-                                                    weight_row<MODE>(a, row), cv, rv[i], wv[i], rmf);
+                rms_chunk2<XT, YT, RT, MODE, HAD>(a, row, (char*)a.y + row * a.ldy * YT::bytes, e,
+                                                      weight_row<MODE>(a, row), cv, rv[i], wv[i], rmf);
         }
     }
 }
 
-template <class XT, class YT, class RT, int MODE>
+template <class XT, class YT, class RT, int MODE, int HAD = 0>
 void launch_rms_rows(const RmsArgs& a, hipStream_t s)
 {
     const int nc = a.dim >> 3;
@@ -423,9 +427,9 @@ void launch_rms_rows(const RmsArgs& a, hipStream_t s)
         const int rpl = (tuned == 1 || tuned == 2 || tuned == 4) ? tuned : 1;
         int64_t blocks = (a.rows + (int64_t)SLOTS * rpl - 1) / ((int64_t)SLOTS * rpl);
         if (blocks > kMaxGridX) blocks = kMaxGridX;
-        if (rpl == 4) k_rms_rows<XT, YT, RT, LPR, 4, MODE><<<(unsigned)blocks, 256, 0, s>>>(a);
-        else if (rpl == 2) k_rms_rows<XT, YT, RT, LPR, 2, MODE><<<(unsigned)blocks, 256, 0, s>>>(a);
-        else k_rms_rows<XT, YT, RT, LPR, 1, MODE><<<(unsigned)blocks, 256, 0, s>>>(a);
+        if (rpl == 4) k_rms_rows<XT, YT, RT, LPR, 4, MODE, HAD><<<(unsigned)blocks, 256, 0, s>>>(a);
+        else if (rpl == 2) k_rms_rows<XT, YT, RT, LPR, 2, MODE, HAD><<<(unsigned)blocks, 256, 0, s>>>(a);
+        else k_rms_rows<XT, YT, RT, LPR, 1, MODE, HAD><<<(unsigned)blocks, 256, 0, s>>>(a);
     };
     if (nc <= 8) go(std::integral_constant<int, 8>{});
     else if (nc <= 16) go(std::integral_constant<int, 16>{});
@@ -547,10 +551,10 @@ int launch_rms_vec(const RmsArgs& a, hipStream_t s)
     if constexpr (MODE == RMS_GATED)
     {
         // Chunks per lane 1, 2, 4 or 8 (a tuned 3 or 5 rounds up; the grid still covers the row).
-        if (sh.maxv == 1) k_rms_norm<XT, YT, RT, 1, MODE><<<grid, sh.threads, 0, s>>>(a);
-        else if (sh.maxv == 2) k_rms_norm<XT, YT, RT, 2, MODE><<<grid, sh.threads, 0, s>>>(a);
-        else if (sh.maxv <= 4) k_rms_norm<XT, YT, RT, 4, MODE><<<grid, sh.threads, 0, s>>>(a);
-        else k_rms_norm<XT, YT, RT, 8, MODE><<<grid, sh.threads, 0, s>>>(a);
+        if (sh.maxv == 1) k_rms_norm<XT, YT, RT, 1, MODE, HAD><<<grid, sh.threads, 0, s>>>(a);
+        else if (sh.maxv == 2) k_rms_norm<XT, YT, RT, 2, MODE, HAD><<<grid, sh.threads, 0, s>>>(a);
+        else if (sh.maxv <= 4) k_rms_norm<XT, YT, RT, 4, MODE, HAD><<<grid, sh.threads, 0, s>>>(a);
+        else k_rms_norm<XT, YT, RT, 8, MODE, HAD><<<grid, sh.threads, 0, s>>>(a);
         return 0;
     }
     switch (sh.maxv)

@@ -36,6 +36,8 @@ PROTOTYPES = {
                               _i, _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _vp, _vp]),
     "exl3r_gated_rms_norm": (_i, [_vp, _i, _i64, _vp, _i, _i, _vp, _i, _i64, _vp, _i, _i64, _i64, _i64, _f, _f, _i, _i,
                                   _vp]),
+    "exl3r_gated_rms_norm_had": (_i, [_vp, _i, _i64, _vp, _i, _i, _vp, _i, _i64, _vp, _i64, _vp, _i, _vp, _i64, _i64,
+                                      _i64, _f, _f, _i, _i, _f, _vp]),
     "exl3r_mul_sigmoid": (_i, [_vp, _vp, _i, _vp, _i, _i64, _i64, _i64, _i64, _i64, _vp]),
     "exl3r_deinterleave_qg": (_i, [_vp, _i64, _vp, _i64, _vp, _i64, _i, _i64, _i, _i, _vp]),
     "exl3r_argmax_sample": (_i, [_vp, _i, _i64, _i64, _i64, _i, _vp, _vp]),

@@ -114,6 +114,30 @@ def gated_rms_norm(x, w, y, g, eps, constant_bias=0.0, w_groups=1, gate_first=Fa
                                       constant_bias, int(bool(gate_first)), int(gate_act), _stream(x, stream)))
 
 
+
+def gated_rms_norm_had(x, w, g, out, eps, pre_scale=None, y=None, constant_bias=0.0, w_groups=1, gate_first=False,
+                       gate_act=0, had_scale=1.0, pre_rows=1, stream=None):
+    """One pass: the gated norm of gated_rms_norm into an f16 y (written only if given), then
+    out = had_r_128(y, pre_scale) (f16, dim % 128 == 0): o_proj's input rotation.  Norm row r uses
+    pre_scale[(r % pre_rows) * dim:]: with rows = tokens * heads of head_dim, pre_rows = heads."""
+    rows, dim, ldx = _rows(x)
+    rg, dg, ldg = _rows(g)
+    ro, do, ldo = _rows(out)
+    if (rg, dg) != (rows, dim) or (ro, do) != (rows, dim) or out.dtype != torch.float16:
+        raise ValueError("g like x; out f16 shaped like x")
+    ldy = 0
+    if y is not None:
+        ry, dy, ldy = _rows(y)
+        if (ry, dy) != (rows, dim) or y.dtype != torch.float16:
+            raise ValueError("y is the f16 norm output shaped like x")
+    if w is not None and w.numel() != w_groups * dim:
+        raise ValueError("w must hold w_groups * dim values")
+    check(load().exl3r_gated_rms_norm_had(_ptr(x), dtype_code(x), ldx, _ptr(w), dtype_code(w) if w is not None else F32,
+                                          w_groups, _ptr(g), dtype_code(g), ldg, _ptr(y), ldy, _ptr(pre_scale),
+                                          int(pre_rows), _ptr(out), ldo, rows, dim, eps, constant_bias,
+                                          int(bool(gate_first)),
+                                          int(gate_act), float(had_scale), _stream(x, stream)))
+
 def mul_sigmoid(x, y, z, stream=None):
     """z = x * sigmoid(y) (fp32, one rounding); z may be x."""
     rows, cols, ldx = _rows(x)

@@ -237,6 +237,29 @@ void gated_rms_norm(const Tensor& x, const Tensor* w, const Tensor& y, const Ten
                                    gate_act, s.get()));
 }
 
+void gated_rms_norm_had(const Tensor& x, const Tensor* w, const Tensor& g, const Tensor& out, const Tensor* y,
+                        const Tensor* pre_scale, float eps, float bias, int w_groups, bool gate_first, int gate_act,
+                        float had_scale, const Stream& s, int pre_rows)
+{
+    int64_t rows, dim, ldx, rg, dg, ldg, ro, dout, ldo, ldy = 0;
+    x.rows_view(rows, dim, ldx);
+    g.rows_view(rg, dg, ldg);
+    out.rows_view(ro, dout, ldo);
+    require(rg == rows && dg == dim && ro == rows && dout == dim && out.dtype == DType::F16,
+            "gated_rms_norm_had: g like x, out f16 like x");
+    if (y)
+    {
+        int64_t ry, dy;
+        y->rows_view(ry, dy, ldy);
+        require(ry == rows && dy == dim && y->dtype == DType::F16, "gated_rms_norm_had: y is f16 like x");
+    }
+    require(!w || w->numel() == (int64_t)w_groups * dim, "gated_rms_norm_had: w must hold w_groups * dim values");
+    check_abi(exl3r_gated_rms_norm_had(x.data, code(x.dtype), ldx, ptr(w), code_or(w, DType::F32), w_groups, g.data,
+                                       code(g.dtype), ldg, y ? y->data : nullptr, ldy, ptr(pre_scale), pre_rows,
+                                       out.data, ldo,
+                                       rows, dim, eps, bias, gate_first ? 1 : 0, gate_act, had_scale, s.get()));
+}
+
 void mul_sigmoid_(const Tensor& x, const Tensor& y, const Stream& s)
 {
     int64_t rows, cols, ldx, ry, cy, ldy;

@@ -132,6 +132,12 @@ void gelu_mul(const Tensor& x, const Tensor& y, const Tensor& z, float act_limit
 // gate_first; act = silu (gate_act 0) or sigmoid (1); w may be null or hold w_groups rows of dim.
 void gated_rms_norm(const Tensor& x, const Tensor* w, const Tensor& y, const Tensor& g, float eps, float bias,
                     int w_groups, bool gate_first, int gate_act, const Stream& s);
+// gated_rms_norm into an f16 y (optional) that feeds o_proj's input rotation: out = had_r_128(y, pre_scale)
+// (src/qwen3_5.rs:208-214 -> src/modules.rs:224-227), one pass.
+// Norm row r uses pre_scale[(r % pre_rows) * dim ..] (rows = tokens * heads of head_dim: pre_rows = heads).
+void gated_rms_norm_had(const Tensor& x, const Tensor* w, const Tensor& g, const Tensor& out, const Tensor* y,
+                        const Tensor* pre_scale, float eps, float bias, int w_groups, bool gate_first, int gate_act,
+                        float had_scale, const Stream& s, int pre_rows = 1);
 // src/ffi.rs:616-618: x *= sigmoid(y), in place.
 void mul_sigmoid_(const Tensor& x, const Tensor& y, const Stream& s);
 // src/ffi.rs:622-624: split [.., heads * 2 * head_dim] interleaved (q | g) rows into q [.., heads, head_dim] and

@@ -154,6 +154,26 @@ EXL3R_API int exl3r_gated_rms_norm(const void* x, int x_dtype, int64_t ldx, cons
                          int gate_first, int gate_act, void* stream);
 
 /*
+ * exl3r_gated_rms_norm with an f16 output that feeds the next EXL3 projection's input rotation, in one
+ * pass: the Qwen3.5 gated-delta-net output norm, then o_proj's had_r_128(y, pre_scale)
+ * (src/qwen3_5.rs:208-214 -> src/modules.rs:224-227).
+ *   out = had_r_128(y, pre_scale) with scale had_scale: f16 [rows, dim] at row stride ldo (y, out
+ *         and the rows of the projection input share one layout); y (f16, the norm output) is written
+ *         only when y != NULL.
+ *   pre_scale: the projection's f16 suh or NULL; norm row r uses pre_scale[(r % pre_rows) * dim ..] --
+ *         with the usual layout (rows = tokens * heads of dim = head_dim, dense) pre_rows = heads and
+ *         pre_scale is [heads * head_dim]; pre_rows > 1 needs rows % pre_rows == 0 and ldo == ldy == dim.
+ * dim % 128 == 0; out and y alias nothing.  Bit-identical to exl3r_gated_rms_norm with an f16 y
+ * followed by exl3r_had_r_128 over the [rows / pre_rows, pre_rows * dim] projection rows; unaligned or
+ * f32-x rows run those calls.
+ */
+EXL3R_API int exl3r_gated_rms_norm_had(const void* x, int x_dtype, int64_t ldx, const void* w, int w_dtype,
+                             int w_groups, const void* g, int g_dtype, int64_t ldg, void* y, int64_t ldy,
+                             const void* pre_scale, int pre_rows, void* out, int64_t ldo, int64_t rows,
+                             int64_t dim, float eps, float constant_bias, int gate_first, int gate_act,
+                             float had_scale, void* stream);
+
+/*
  * Sigmoid gate: z = x * sigmoid(y), in fp32, rounded once to z's dtype (the gated-attention
  * output gate, src/modules.rs:785-787).  Replaces exl3_shim_mul_sigmoid_ (csrc/exl3_shim.cpp:167 ->
  * mul_sigmoid_, kernels/activation.cu:532-568, in place on f16 with half arithmetic).
