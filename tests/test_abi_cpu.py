@@ -293,3 +293,23 @@ def test_rope_had_validation():
     assert paged_had(v=None) == exl3r.EINVAL
     assert paged_had(hkv=0) == exl3r.EINVAL
     assert paged_had(seq=0, q=None, oq=None, k=None, v=None, kc=None, vc=None, bt=None, sl=None) == exl3r.OK
+
+
+def test_gated_rms_norm_had_validation():
+    lib = exl3r.load()
+    def call(**kw):
+        # (x, xt, ldx, w, wt, w_groups, g, gt, ldg, y, ldy, pre, pre_rows, out, ldo, rows, dim, eps, cb, first, act, hs)
+        a = dict(x=FAKE, xt=BF16, ldx=128, w=None, wt=F32, wg=1, g=FAKE + 65536, gt=F32, ldg=128, y=None, ldy=128,
+                 pre=None, pre_rows=1, out=FAKE + 131072, ldo=128, rows=4, dim=128, eps=1e-6, cb=0.0, first=0, act=0,
+                 hs=1.0)
+        a.update(kw)
+        return lib.exl3r_gated_rms_norm_had(*a.values(), None)
+    assert call(dim=100, ldx=100, ldg=100, ldo=100) == exl3r.EINVAL and "multiple of 128" in _err()
+    assert call(gt=7) == exl3r.EDTYPE
+    assert call(pre_rows=0) == exl3r.EINVAL
+    assert call(pre_rows=3) == exl3r.EINVAL and "pre_rows" in _err()
+    assert call(act=2) == exl3r.EINVAL
+    assert call(out=FAKE, xt=F16) == exl3r.EINVAL and "alias" in _err()
+    assert call(out=FAKE + 65536) == exl3r.EINVAL and "alias" in _err()
+    assert call(g=None) == exl3r.EINVAL
+    assert call(rows=0) == exl3r.OK

@@ -16,6 +16,7 @@ from test_gpu_act_had import run as run_act_had, run_rotated as run_act_had_rota
 from test_gpu_argmax import run as run_argmax
 from test_gpu_embedding import check_gather, run_fused
 from test_gpu_gated import check as check_gate, run_gated
+from test_gpu_gated_had import run as run_gated_had
 from test_gpu_gumbel import run_noise, run_sample
 from test_gpu_hadamard import run as run_had, scales
 from test_gpu_rms_norm import run_plain, run_res
@@ -73,6 +74,12 @@ def test_fuzz_gated_rms_norm(case):
               w_groups=int(pick(rng, [1, 1, 2, 4])), gate_first=bool(rng.random() < 0.5), gate_act=int(rng.integers(2)),
               cb=float(pick(rng, [0.0, 1.0])), with_w=bool(rng.random() < 0.85), seed=case,
               ld=dim + int(rng.integers(0, 2)) * 8)
+    hdim = 128 * int(pick(rng, [1, 1, 2, 3, 8]))
+    heads = int(pick(rng, [1, 2, 8, 32]))
+    run_gated_had(heads * int(rng.integers(1, 40)), hdim, pick(rng, [F16, BF16]), pick(rng, FLOATS), pick(rng, FLOATS),
+                  w_groups=int(pick(rng, [1, 1, 2])), gate_first=bool(rng.random() < 0.5), gate_act=int(rng.integers(2)),
+                  cb=float(pick(rng, [0.0, 1.0])), with_w=bool(rng.random() < 0.85), with_y=bool(rng.random() < 0.5),
+                  pre=bool(rng.random() < 0.85), heads=heads, seed=case + 1)
 
 
 @pytest.mark.parametrize("case", CASES)
