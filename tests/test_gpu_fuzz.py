@@ -3,6 +3,8 @@ arguments drawn at random inside each op's documented domain (rows and dims that
 of the vector width, padded rows, every dtype combination, every position source, odd masks),
 each case checked against the CPU oracle at the same tolerance as the op's own tests.  The cases
 are fixed by their seeds, so a failure names a reproducible configuration."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -30,7 +32,8 @@ pytestmark = pytest.mark.gpu
 
 F32, F16, BF16, I32, I64 = orc.F32, orc.F16, orc.BF16, orc.I32, orc.I64
 FLOATS = [F32, F16, BF16]
-CASES = range(24)
+# EXL3R_FUZZ_CASES widens the sweep for a longer run (the default keeps the suite at seconds).
+CASES = range(int(os.environ.get("EXL3R_FUZZ_CASES", "24")))
 
 
 def pick(rng, seq):
