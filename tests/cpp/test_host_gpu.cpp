@@ -396,6 +396,29 @@ int main()
         const bool ok = download(q, s) == download(q2, s) && download(k, s) == download(k2, s);
         report("ffi::rope_had == had_r_128 + rope", ok, ok ? "bitwise" : "DIFFER");
     }
+    // gated_rms_norm_had: the GDN output norm (8 tokens x 4 heads of 128, one o_proj row per token)
+    // into o_proj's input rotation, bitwise equal to the gated norm followed by had_r_128.
+    {
+        const int heads = 4, rows = 8 * heads, dim = 128;
+        auto xh = host_normal(DType::BF16, rows * dim, 0.f, 1.f), gh = host_normal(DType::F32, rows * dim, 0.f, 2.f);
+        auto wh = host_normal(DType::F32, dim, 1.f, 0.1f);
+        std::vector<uint8_t> sh(heads * dim * 2);
+        for (int i = 0; i < heads * dim; ++i)
+        {
+            const uint16_t v = (splitmix() & 1) ? 0xbc00 : 0x3c00;
+            std::memcpy(&sh[i * 2], &v, 2);
+        }
+        auto x = upload(xh, DType::BF16, { rows, dim }, s), g = upload(gh, DType::F32, { rows, dim }, s);
+        auto w = upload(wh, DType::F32, { dim }, s), sv = upload(sh, DType::F16, { heads * dim }, s);
+        auto out = OwnedTensor::empty(DType::F16, { rows, dim }), y = OwnedTensor::empty(DType::F16, { rows, dim });
+        auto ref = OwnedTensor::empty(DType::F16, { rows / heads, heads * dim });
+        ffi::gated_rms_norm_had(x.t, &w.t, g.t, out.t, nullptr, &sv.t, 1e-6f, 0.f, 1, false, 1, 1.f, s, heads);
+        ffi::gated_rms_norm(x.t, &w.t, y.t, g.t, 1e-6f, 0.f, 1, false, 1, s);
+        Tensor yv(y.t.data, DType::F16, { rows / heads, heads * dim });
+        ffi::had_r_128(yv, ref.t, &sv.t, nullptr, 1.f, s);
+        const bool ok = download(out, s) == download(ref, s);
+        report("ffi::gated_rms_norm_had == gated norm + had_r_128", ok, ok ? "bitwise" : "DIFFER");
+    }
     std::printf(failures ? "test_host_gpu: %d failures\n" : "test_host_gpu: all passed\n", failures);
     return failures ? 1 : 0;
 }
