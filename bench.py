@@ -35,7 +35,7 @@ OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "
        "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
        "deinterleave_q35", "gated_norm_had_q35", "gated_norm_had_q35_unfused", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
        "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_unfused", "silu_had_c3",
-       "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_unfused",
+       "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_unfused", "rope_cs_c4", "rope_cs_table_c4",
        "rope_kv_had_prefill", "rope_kv_had_prefill_unfused", "mlp_had_c3", "mlp_had_c3_unfused",
        "prefill_layer", "prefill_layer_unfused", "calib_copy",
        "calib_copy_cached"]
@@ -168,6 +168,36 @@ def make_rope_had(name, pos, hq, hk, hd, fused, seed=330):
             ffi.rope(q, q, k, k, inv, 0, None, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, position_ids=pid)
     kind = "fused" if fused else "unfused (2 had_r_128 + rope)"
     return Work(name, nbytes, launch, f"q/k output rotation + head-norm + NeoX RoPE T={T} heads {hq}/{hk}, {kind}", sets)
+
+
+def make_rope_cs(name, pos, hq, hk, hd, R, dt, seed, table_only):
+    """C4 with the sin / cos of the forward pass precomputed: the per-layer RoPE reading the {cos, sin}
+    table (exl3r_rope_cs: C4's q/k bytes, the norm weights and the token's table row), or the table build
+    that serves every layer of the forward (exl3r_rope_cs_table: the positions and inv_freq read, the
+    table written)."""
+    import numpy as np
+    import torch
+    import exl3r
+    import exl3r.ffi as ffi
+    T = pos.size
+    inv = torch.from_numpy((1.0 / 1e6 ** (np.arange(0, R, 2, dtype=np.float64) / R)).astype(np.float32)).cuda()
+    pid = torch.from_numpy(pos).cuda().view(1, -1)
+    table = ffi.rope_cs_table(1, T, inv, 0, position_ids=pid)
+    if table_only:
+        nbytes = 4 * T + (R // 2) * 4 + T * (R // 2) * 8
+        return Work(name, nbytes, lambda i: ffi.rope_cs_table(1, T, inv, 0, position_ids=pid, out=table),
+                    f"{{cos, sin}} table of T={T} ragged positions, rotary {R}")
+    nbytes = 2 * T * (hq + hk) * hd * 2 + T * (R // 2) * 8 + 2 * hd * 2
+    sets = sets_for(nbytes)
+    qn, kn = gen((hd,), 1.0, 0.1, dt, seed + 50), gen((hd,), 1.0, 0.1, dt, seed + 51)
+    bufs = [(gen((1, T, hq, hd), 0.0, 1.0, dt, seed + 2 * k), gen((1, T, hk, hd), 0.0, 1.0, dt, seed + 2 * k + 1))
+            for k in range(sets)]
+
+    def launch(i):
+        q, k = bufs[i % sets]
+        ffi.rope_cs(q, q, k, k, table, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX)
+    return Work(name, nbytes, launch, f"q/k head-norm + neox RoPE from a {{cos, sin}} table T={T} heads {hq}/{hk}",
+                sets)
 
 
 def make_rope(name, pos, hq, hk, hd, R, mode, dt, seed, bsz=1, per_seq=False):
@@ -639,6 +669,8 @@ def make_all(only=None):
         "gelu_c3": lambda: make_act("gelu_c3", 8192, 17408, bf16, "gelu", 200),
         "rope_c4": lambda: make_rope("rope_c4", ragged, 64, 8, 128, 128, "neox", f16, 300),
         "rope_c4_gptj": lambda: make_rope("rope_c4_gptj", ragged, 64, 8, 128, 64, "gptj", f16, 310),
+        "rope_cs_c4": lambda: make_rope_cs("rope_cs_c4", ragged, 64, 8, 128, 128, f16, 300, False),
+        "rope_cs_table_c4": lambda: make_rope_cs("rope_cs_table_c4", ragged, 64, 8, 128, 128, f16, 300, True),
         "gather_c5": lambda: make_gather("gather_c5", 151936, 5120, 16384, bf16, bf16, zipf_ids(16384, 151936, 1), 400),
         "gather_norm_c5": lambda: make_gather("gather_norm_c5", 151936, 5120, 16384, bf16, bf16,
                                               zipf_ids(16384, 151936, 1), 400, norm=True),
@@ -886,6 +918,12 @@ def main():
         hadamard["desc"] = ("the EXL3 linear's random-Hadamard rotation (had_r_128) alone, and fused into the op that "
                             "produces its input or consumes its output, vs the same calls one after another")
         log(f"hadamard: {json.dumps(hadamard)}")
+        r_us, c_us, t_us = ops["rope_c4"]["us"], ops["rope_cs_c4"]["us"], ops["rope_cs_table_c4"]["us"]
+        rope_cs = {"rope_c4_us": r_us, "rope_cs_c4_us": c_us, "table_per_forward_us": t_us,
+                   "per_layer_saving_us": round(r_us - c_us, 2),
+                   "desc": "C4 RoPE evaluating sin / cos in every layer vs reading a {cos, sin} table built once "
+                           "per forward pass (bit-identical results); the table costs table_per_forward_us once"}
+        log(f"rope_cs: {json.dumps(rope_cs)}")
 
         # The timed step: config-3 prefill row ops back to back.
         step_works = [works["rms_c3"], works["silu_c3"], works["gelu_c3"]]
@@ -923,7 +961,7 @@ def main():
                    "io_dtype": "bf16", "tokens": 8192, "hidden": 5120, "intermediate": 17408,
                    "frac_peak": round(value / PEAK_GBS, 4)},
         "roofline": roof, "cpu_baseline": cpu, "ops": ops, "decode_step": decode, "c2_decode_rms_norm": c2,
-        "rope_paged_kv": rope_kv, "sampling": sampling, "hadamard": hadamard,
+        "rope_paged_kv": rope_kv, "sampling": sampling, "hadamard": hadamard, "rope_cs_table": rope_cs,
         "copy_reference": {"gbs": round(copy_gbs, 1), "frac_peak": round(copy_gbs / PEAK_GBS, 4),
                            "desc": "non-temporal 16 B/lane device copy of 1 GiB (read + write), the practical HBM ceiling reference"},
     }

@@ -20,7 +20,8 @@
 // kernels: k_rope_tok (prefill NeoX) gives each wave whole tokens -- the token's sin/cos evaluated
 // once, one per lane, and its heads walked in software-pipelined batches; k_rope (decode, GPT-J)
 // flattens (token, head) items over workgroups that share the sin/cos of the tokens they span
-// through LDS.
+// through LDS.  exl3r_rope_cs_table evaluates the sin/cos of a forward pass once into a table
+// that exl3r_rope_cs's kernels (the same two) copy rows of, instead of evaluating them per layer.
 #include "abi.hpp"
 #include "common.cuh"
 #include "hadamard.cuh"
@@ -68,7 +69,14 @@ struct RopeArgs
     const void* q_post;
     const void* k_post;
     const void* v_post;
+    // Precomputed rotary pairs (exl3r_rope_cs): {cos, sin} * attn_factor of frequency t for token
+    // tok is cst[tok * (R / 2) + t]; nullptr: evaluated from inv_freq or the angle table.
+    const float2* cst;
 };
+
+// Where a kernel takes its rotary pairs: evaluated from inv_freq[t] * pos, evaluated from the angle
+// table, or read from the precomputed {cos, sin} table.
+enum { SRC_FREQ = 0, SRC_ANGLE = 1, SRC_CS = 2 };
 
 // Head kinds of the item space [0, hq) q, [hq, hq + hk) k, [hq + hk, hq + hk + hv) v.
 enum { KIND_Q = 0, KIND_K = 1, KIND_V = 2 };
@@ -144,15 +152,17 @@ __device__ __forceinline__ void sincos_angle(float a, double& sd, double& cd)
 }
 
 // {cos, sin} * attn_factor of rotary frequency t for token tok at position pos: fp64 evaluation of
-// the fp32 angle, rounded once (correctly rounded fp32 values).  TABLE: the angle is read from the
-// token's sequence row `pos` of the angle table; a position outside the table sets *err and rotates
-// by 0.  (A compile-time choice: even a never-taken runtime branch here costs the prefill kernel
-// ~5 us at C4 through its code generation.)
-template <bool TABLE>
+// the fp32 angle, rounded once (correctly rounded fp32 values).  SRC_ANGLE: the angle is read from
+// the token's sequence row `pos` of the angle table; a position outside the table sets *err and
+// rotates by 0.  SRC_CS: the pair is read from the precomputed table, which exl3r_rope_cs_table fills
+// with this function's SRC_FREQ values.  (A compile-time choice: even a never-taken runtime branch
+// here costs the prefill kernel ~5 us at C4 through its code generation.)
+template <int SRC>
 __device__ __forceinline__ float2 rope_cs(const RopeArgs& a, int t, int tok, int pos)
 {
+    if constexpr (SRC == SRC_CS) return a.cst[(int64_t)tok * (a.R >> 1) + t];
     float ang;
-    if constexpr (TABLE)
+    if constexpr (SRC == SRC_ANGLE)
     {
         const int64_t b = tok / (int)a.seq_len;
         if (pos >= 0 && pos < a.table_rows) ang = a.table[b * a.table_bstride + (int64_t)pos * (a.R >> 1) + t];
@@ -172,7 +182,8 @@ __device__ __forceinline__ float2 rope_cs(const RopeArgs& a, int t, int tok, int
 __device__ __forceinline__ void fill_sincos(const RopeArgs& a, int tok, int pos, float2* cs)
 {
     for (int t = threadIdx.x; t < a.R / 2; t += blockDim.x)
-        cs[t] = a.table ? rope_cs<true>(a, t, tok, pos) : rope_cs<false>(a, t, tok, pos);
+        cs[t] = a.cst ? rope_cs<SRC_CS>(a, t, tok, pos) : a.table ? rope_cs<SRC_ANGLE>(a, t, tok, pos)
+                                                                 : rope_cs<SRC_FREQ>(a, t, tok, pos);
 }
 
 // Norm weights of one lane's 8-element chunk with the constant bias folded in, loaded once per
@@ -351,7 +362,7 @@ __device__ __forceinline__ void lane_sincos(const float2* row, int e0, int R, fl
 // Decode / small launches.  Work item = one (token, head) pair; a workgroup takes a contiguous range
 // of slots * ITERS items, which spans at most a.tok_span tokens.  Every head chunk is loaded first;
 // the sin/cos of the spanned tokens are evaluated into LDS while those loads are in flight.
-template <class IO, int MODE, int LPH, int ITERS, int NORM, bool APPEND, bool TABLE>
+template <class IO, int MODE, int LPH, int ITERS, int NORM, bool APPEND, int SRC>
 __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
 {
     extern __shared__ float2 cs[];            // [tok_span][R / 2]
@@ -430,7 +441,7 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
         {
             const int tr = i / R2;
             const int tok = tok0 + tr;
-            if (tok < a.tokens) cs[i] = rope_cs<TABLE>(a, i - tr * R2, tok, token_position(a, tok));
+            if (tok < a.tokens) cs[i] = rope_cs<SRC>(a, i - tr * R2, tok, token_position(a, tok));
         }
         __syncthreads();
 
@@ -482,7 +493,7 @@ struct RopeBatch
     int b;
 };
 
-template <class IO, int MODE, int LPH, int HPL, int NORM, bool APPEND, bool HADR = false>
+template <class IO, int MODE, int LPH, int HPL, int NORM, bool APPEND, bool HADR = false, int SRC = SRC_FREQ>
 __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
 {
     extern __shared__ float2 cs[];            // [4 waves][R / 2]
@@ -525,7 +536,7 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
     auto fill = [&](int64_t tok) {
         const int pos = token_position(a, (int)tok);
         wave_lds_sync();
-        for (int t = l64; t < R2; t += 64) row[t] = rope_cs<false>(a, t, (int)tok, pos);
+        for (int t = l64; t < R2; t += 64) row[t] = rope_cs<SRC>(a, t, (int)tok, pos);
         wave_lds_sync();
         lane_sincos<MODE>(row, e0, a.R, c, s);
     };
@@ -669,7 +680,7 @@ __global__ __launch_bounds__(256) void k_rope_generic(RopeArgs a, int dt, int mo
     }
 }
 
-template <class IO, int MODE, int LPH, int NORM, bool TABLE>
+template <class IO, int MODE, int LPH, int NORM, int SRC>
 static void launch_rope_lph(RopeArgs a, int iters, hipStream_t s)
 {
     const int threads = 256;
@@ -680,16 +691,16 @@ static void launch_rope_lph(RopeArgs a, int iters, hipStream_t s)
     int64_t blocks = (items + per_wg - 1) / per_wg;
     if (blocks > kMaxGridX) blocks = kMaxGridX;
     const size_t lds = (size_t)a.tok_span * (a.R / 2) * sizeof(float2);
-    if constexpr (TABLE)
+    if constexpr (SRC != SRC_FREQ)
     {
-        // Angle tables (never with a paged append): two heads per lane.
-        k_rope<IO, MODE, LPH, 2, NORM, false, true><<<(unsigned)blocks, threads, lds, s>>>(a);
+        // Angle and {cos, sin} tables (never with a paged append): two heads per lane.
+        k_rope<IO, MODE, LPH, 2, NORM, false, SRC><<<(unsigned)blocks, threads, lds, s>>>(a);
         return;
     }
     auto go = [&](auto I) {
         constexpr int IT = decltype(I)::value;
-        if (a.kc) k_rope<IO, MODE, LPH, IT, NORM, true, false><<<(unsigned)blocks, threads, lds, s>>>(a);
-        else k_rope<IO, MODE, LPH, IT, NORM, false, false><<<(unsigned)blocks, threads, lds, s>>>(a);
+        if (a.kc) k_rope<IO, MODE, LPH, IT, NORM, true, SRC_FREQ><<<(unsigned)blocks, threads, lds, s>>>(a);
+        else k_rope<IO, MODE, LPH, IT, NORM, false, SRC_FREQ><<<(unsigned)blocks, threads, lds, s>>>(a);
     };
     switch (iters)
     {
@@ -704,7 +715,7 @@ static void launch_rope_lph(RopeArgs a, int iters, hipStream_t s)
 // token per wave (38.5 us; 3 per lane 42 us); bf16 heads (fp32 norm) with 3 per lane on a
 // persistent grid of 4 workgroups per CU (37.0 us; 2 per lane 42 us).  With the paged append
 // (4096 tokens, + 8 v heads) 3 per lane: 40.0 us, 2 per lane 41-43 us.
-template <class IO, int MODE, int LPH, int NORM, bool HADR = false>
+template <class IO, int MODE, int LPH, int NORM, bool HADR = false, int SRC = SRC_FREQ>
 static void launch_rope_tok(RopeArgs a, hipStream_t s)
 {
     const Tuning& tu = tuning();
@@ -721,7 +732,9 @@ static void launch_rope_tok(RopeArgs a, hipStream_t s)
     const size_t lds = 4 * (size_t)(a.R / 2) * sizeof(float2);
     auto go = [&](auto H) {
         constexpr int HP = decltype(H)::value;
-        if constexpr (HADR)
+        if constexpr (SRC == SRC_CS)
+            k_rope_tok<IO, MODE, LPH, HP, NORM, false, false, SRC_CS><<<(unsigned)blocks, 256, lds, s>>>(a);
+        else if constexpr (HADR)
         {
             if (a.kc) k_rope_tok<IO, MODE, LPH, HP, NORM, true, true><<<(unsigned)blocks, 256, lds, s>>>(a);
             else k_rope_tok<IO, MODE, LPH, HP, NORM, false, true><<<(unsigned)blocks, 256, lds, s>>>(a);
@@ -743,11 +756,26 @@ template <class IO, int MODE, int NORM>
 static void launch_rope_vec(const RopeArgs& a, int lph, hipStream_t s)
 {
     const Tuning& tu = tuning();
+    if (a.cst)
+    {
+        // exl3r_rope_cs (no append, no output rotation): the kernels of exl3r_rope, which copy the
+        // token's table row to LDS in place of evaluating it.
+        if (MODE == EXL3R_ROPE_NEOX && rope_tok_launch(a))
+        {
+            if (lph == 8) launch_rope_tok<IO, MODE, 8, NORM, false, SRC_CS>(a, s);
+            else if (lph == 16) launch_rope_tok<IO, MODE, 16, NORM, false, SRC_CS>(a, s);
+            else launch_rope_tok<IO, MODE, 32, NORM, false, SRC_CS>(a, s);
+        }
+        else if (lph == 8) launch_rope_lph<IO, MODE, 8, NORM, SRC_CS>(a, 2, s);
+        else if (lph == 16) launch_rope_lph<IO, MODE, 16, NORM, SRC_CS>(a, 2, s);
+        else launch_rope_lph<IO, MODE, 32, NORM, SRC_CS>(a, 2, s);
+        return;
+    }
     if (a.table)
     {
-        if (lph == 8) launch_rope_lph<IO, MODE, 8, NORM, true>(a, 2, s);
-        else if (lph == 16) launch_rope_lph<IO, MODE, 16, NORM, true>(a, 2, s);
-        else launch_rope_lph<IO, MODE, 32, NORM, true>(a, 2, s);
+        if (lph == 8) launch_rope_lph<IO, MODE, 8, NORM, SRC_ANGLE>(a, 2, s);
+        else if (lph == 16) launch_rope_lph<IO, MODE, 16, NORM, SRC_ANGLE>(a, 2, s);
+        else launch_rope_lph<IO, MODE, 32, NORM, SRC_ANGLE>(a, 2, s);
         return;
     }
     if constexpr (MODE == EXL3R_ROPE_NEOX)
@@ -766,9 +794,9 @@ static void launch_rope_vec(const RopeArgs& a, int lph, hipStream_t s)
     if (tu.rope_iters == 1 || tu.rope_iters == 2 || tu.rope_iters == 4) iters = tu.rope_iters;
     else if (items >= slots * 4 * 2048) iters = 4;
     else if (items >= slots * 2 * 2048) iters = 2;
-    if (lph == 8) launch_rope_lph<IO, MODE, 8, NORM, false>(a, iters, s);
-    else if (lph == 16) launch_rope_lph<IO, MODE, 16, NORM, false>(a, iters, s);
-    else launch_rope_lph<IO, MODE, 32, NORM, false>(a, iters, s);
+    if (lph == 8) launch_rope_lph<IO, MODE, 8, NORM, SRC_FREQ>(a, iters, s);
+    else if (lph == 16) launch_rope_lph<IO, MODE, 16, NORM, SRC_FREQ>(a, iters, s);
+    else launch_rope_lph<IO, MODE, 32, NORM, SRC_FREQ>(a, iters, s);
 }
 
 template <class IO>
@@ -830,6 +858,21 @@ static int rope_prepare(const char* op, RopeArgs& a, const void* q, void* out_q,
     a.eps = norm_eps; a.cb = norm_constant_bias; a.attn = attn_factor;
     a.inv_hd = (head_dim & (head_dim - 1)) == 0 ? 1.0f / (float)head_dim : 0.0f;
     return EXL3R_OK;
+}
+
+// Precomputed {cos, sin} * attn_factor (exl3r_rope_cs_table): row tok of [tokens, R / 2] holds the
+// rotary pairs of token tok's position, evaluated as rope_cs does, so RoPE from the table is
+// bit-identical to RoPE that evaluates them itself.
+__global__ __launch_bounds__(256) void k_rope_cs_table(RopeArgs a, float2* cst)
+{
+    const int R2 = a.R >> 1;
+    const int64_t n = a.tokens * R2;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    {
+        const int64_t tok = i / R2;
+        const int t = (int)(i - tok * R2);
+        cst[i] = rope_cs<SRC_FREQ>(a, t, (int)tok, token_position(a, (int)tok));
+    }
 }
 
 static int rope_norm_kind(const RopeArgs& a, int dtype)
@@ -1106,4 +1149,56 @@ extern "C" int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok
                                rotary_dim, position, positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps,
                                norm_constant_bias, rope_mode, attn_factor, k_cache, v_cache, page_size, num_pages,
                                block_table, max_blocks_per_seq, cache_seqlens, err_flag, stream);
+}
+
+// {cos, sin} * attn_factor of every token's rotary frequencies into cs_table [bsz * seq_len, R / 2]
+// (float2), for exl3r_rope_cs: the positions of a forward pass are the same in every layer, so the
+// table is built once and every layer's RoPE reads it.  Positions as exl3r_rope.
+extern "C" int exl3r_rope_cs_table(int64_t bsz, int64_t seq_len, const float* inv_freq, int rotary_dim,
+                                   int32_t position, const int32_t* positions, const int32_t* position_ids,
+                                   float attn_factor, void* cs_table, void* stream)
+{
+    const char* op = "exl3r_rope_cs_table";
+    if (bsz < 0 || seq_len < 0 || rotary_dim < 2 || rotary_dim % 2)
+        return set_error(EXL3R_EINVAL, "%s: invalid shape bsz=%lld seq_len=%lld rotary_dim=%d", op, (long long)bsz,
+                         (long long)seq_len, rotary_dim);
+    if (positions && position_ids) return set_error(EXL3R_EINVAL, "%s: at most one of positions / position_ids", op);
+    const int64_t tokens = bsz * seq_len;
+    if (tokens == 0) return EXL3R_OK;
+    if (!inv_freq || !cs_table) return set_error(EXL3R_EINVAL, "%s: inv_freq and cs_table must be non-null", op);
+    if ((uintptr_t)cs_table % 8) return set_error(EXL3R_EINVAL, "%s: cs_table must be 8-byte aligned", op);
+    if (tokens > 0x7fffffff) return set_error(EXL3R_EINVAL, "%s: too many tokens", op);
+    RopeArgs a{};
+    a.R = rotary_dim; a.seq_len = seq_len; a.tokens = tokens; a.inv_freq = inv_freq; a.position = position;
+    a.positions = positions; a.position_ids = position_ids; a.attn = attn_factor;
+    const int64_t n = tokens * (rotary_dim / 2);
+    const unsigned blocks = (unsigned)((n + 255) / 256 < kMaxGridX ? (n + 255) / 256 : kMaxGridX);
+    k_rope_cs_table<<<blocks, 256, 0, (hipStream_t)stream>>>(a, (float2*)cs_table);
+    return launch_status(op);
+}
+
+// exl3r_rope with the rotary pairs read from a table built by exl3r_rope_cs_table (same positions,
+// inv_freq, rotary_dim and attn_factor): bit-identical to exl3r_rope, on the same kernels and shapes.
+extern "C" int exl3r_rope_cs(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride,
+                             int num_heads_q, const void* k, void* out_k, int64_t k_tok_stride,
+                             int64_t k_head_stride, int num_heads_k, int dtype, int64_t bsz, int64_t seq_len,
+                             int head_dim, const void* cs_table, int rotary_dim, const void* q_norm,
+                             const void* k_norm, int norm_dtype, float norm_eps, float norm_constant_bias,
+                             int rope_mode, void* stream)
+{
+    const char* op = "exl3r_rope_cs";
+    if (!cs_table && bsz > 0 && seq_len > 0) return set_error(EXL3R_EINVAL, "%s: cs_table must be non-null", op);
+    // rope_prepare checks the rotation source of exl3r_rope; the table of an empty call may be NULL.
+    static const float kEmpty = 0.0f;
+    RopeArgs a;
+    int rc = rope_prepare(op, a, q, out_q, q_tok_stride, q_head_stride, num_heads_q, k, out_k, false, k_tok_stride,
+                          k_head_stride, num_heads_k, dtype, bsz, seq_len, head_dim,
+                          cs_table ? (const float*)cs_table : &kEmpty, rotary_dim,
+                          0, nullptr, nullptr, q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias, rope_mode, 1.0f);
+    if (rc || a.tokens == 0) return rc;
+    if ((uintptr_t)cs_table % 8) return set_error(EXL3R_EINVAL, "%s: cs_table must be 8-byte aligned", op);
+    a.inv_freq = nullptr;
+    a.cst = (const float2*)cs_table;
+    rc = rope_dispatch(op, a, dtype, rope_mode, stream);
+    return rc;
 }

@@ -225,6 +225,55 @@ def rope(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm
                             norm_eps, norm_constant_bias, rope_mode, attn_factor, _stream(q, stream)))
 
 
+def rope_cs_table(bsz, seq_len, inv_freq, position, positions=None, position_ids=None, attn_factor=1.0, out=None,
+                  stream=None):
+    """{cos, sin} * attn_factor of every token's rotary frequencies (float32 [bsz * seq_len, R/2, 2]), as
+    rope() evaluates them for the same positions: built once per forward pass, read by every layer's
+    rope_cs().  `out`, if given, is filled in place."""
+    if inv_freq.dim() != 1 or inv_freq.dtype != torch.float32:
+        raise ValueError("inv_freq must be float32 [R/2]")
+    for t in (positions, position_ids):
+        if t is not None and t.dtype != torch.int32:
+            raise TypeError("positions / position_ids must be int32")
+    half = inv_freq.shape[0]
+    if out is None:
+        out = torch.empty((bsz * seq_len, half, 2), device=inv_freq.device, dtype=torch.float32)
+    elif out.dtype != torch.float32 or not out.is_contiguous() or out.shape != (bsz * seq_len, half, 2):
+        raise ValueError("out must be a contiguous float32 [bsz * seq_len, R/2, 2]")
+    check(load().exl3r_rope_cs_table(bsz, seq_len, _ptr(inv_freq), half * 2, int(position), _ptr(positions),
+                                     _ptr(position_ids), attn_factor, _ptr(out), _stream(inv_freq, stream)))
+    return out
+
+
+def rope_cs(q, out_q, k, out_k, cs_table, q_norm, k_norm, norm_eps, norm_constant_bias, rope_mode, stream=None):
+    """rope() with the rotary pairs read from a rope_cs_table() of the same positions: bit-identical to
+    rope(), the per-layer sin / cos evaluation replaced by a table row copy.  q, k: as rope()."""
+    if q.dim() != 4:
+        raise ValueError("q must be (bsz, seq_len, heads, head_dim)")
+    bsz, seq, hq, hd = q.shape
+    if q.stride(3) != 1 or out_q.stride() != q.stride() or out_q.shape != q.shape:
+        raise ValueError("q innermost dim must be dense and out_q must share q's layout")
+    if seq > 1 and q.stride(0) != seq * q.stride(1) and bsz > 1:
+        raise ValueError("q batch stride must be seq_len * token stride")
+    hk, k_ts, k_hs = 0, 0, 0
+    if k is not None:
+        if k.dim() != 4 or k.shape[0] != bsz or k.shape[1] != seq or k.shape[3] != hd:
+            raise ValueError("k is incorrect shape")
+        if k.stride(3) != 1 or out_k is None or out_k.stride() != k.stride():
+            raise ValueError("k innermost dim must be dense and out_k must share k's layout")
+        if seq > 1 and k.stride(0) != seq * k.stride(1) and bsz > 1:
+            raise ValueError("k batch stride must be seq_len * token stride")
+        hk, k_ts, k_hs = k.shape[2], k.stride(1), k.stride(2)
+    if (cs_table.dtype != torch.float32 or not cs_table.is_contiguous() or cs_table.dim() != 3
+            or cs_table.shape[0] != bsz * seq or cs_table.shape[2] != 2):
+        raise ValueError("cs_table must be a contiguous float32 [bsz * seq_len, R/2, 2]")
+    nw = q_norm if q_norm is not None else k_norm
+    check(load().exl3r_rope_cs(_ptr(q), _ptr(out_q), q.stride(1), q.stride(2), hq, _ptr(k), _ptr(out_k), k_ts, k_hs,
+                               hk, dtype_code(q), bsz, seq, hd, _ptr(cs_table), cs_table.shape[1] * 2,
+                               _ptr(q_norm), _ptr(k_norm), dtype_code(nw) if nw is not None else F16,
+                               norm_eps, norm_constant_bias, rope_mode, _stream(q, stream)))
+
+
 def rope_had(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias,
              rope_mode, attn_factor, q_post_scale=None, k_post_scale=None, position_ids=None, stream=None):
     """rope() on the raw f16 outputs of the q / k projections, each first given its projection's output

@@ -383,6 +383,49 @@ void gumbel_noise(const Tensor& x, const Tensor& out, uint32_t random, const Str
     check_abi(exl3r_gumbel_noise(x.data, code(x.dtype), ldx, out.data, code(out.dtype), ldo, rows, cols, random, s.get()));
 }
 
+void rope_cs_table(int64_t bsz, int64_t seq_len, const Tensor& inv_freq, int64_t position, const Tensor* positions,
+                   const Tensor* position_ids, float attn_factor, const Tensor& cs_table, const Stream& s)
+{
+    require(inv_freq.dtype == DType::F32 && inv_freq.dim() == 1, "rope_cs_table: inv_freq must be float32 [R/2]");
+    require(!positions || positions->dtype == DType::I32, "rope_cs_table: positions must be int32");
+    require(!position_ids || position_ids->dtype == DType::I32, "rope_cs_table: position_ids must be int32");
+    require(cs_table.dtype == DType::F32 && cs_table.is_contiguous() && cs_table.dim() == 3 &&
+                cs_table.size(0) == bsz * seq_len && cs_table.size(1) == inv_freq.size(0) && cs_table.size(2) == 2,
+            "rope_cs_table: cs_table must be contiguous float32 [bsz * seq_len, R/2, 2]");
+    check_abi(exl3r_rope_cs_table(bsz, seq_len, (const float*)inv_freq.data, (int)(inv_freq.size(0) * 2),
+                                  (int32_t)position, (const int32_t*)ptr(positions), (const int32_t*)ptr(position_ids),
+                                  attn_factor, cs_table.data, s.get()));
+}
+
+void rope_cs(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& cs_table,
+             const Tensor* q_norm, const Tensor* k_norm, float norm_eps, float norm_constant_bias, RopeStyle rope_mode,
+             const Stream& s)
+{
+    require(q.dim() == 4, "rope_cs: q must be (bsz, seq_len, heads, head_dim)");
+    require(q.stride(3) == 1 && out_q.strides == q.strides && out_q.shape == q.shape,
+            "rope_cs: q innermost dim must be dense and out_q must share q's layout");
+    const int64_t bsz = q.size(0), seq = q.size(1), hd = q.size(3);
+    require(bsz <= 1 || seq <= 1 || q.stride(0) == seq * q.stride(1), "rope_cs: q batch stride must be seq_len * token stride");
+    int64_t hk = 0, kts = 0, khs = 0;
+    if (k)
+    {
+        require(out_k && k->dim() == 4 && k->size(0) == bsz && k->size(1) == seq && k->size(3) == hd,
+                "rope_cs: k is incorrect shape");
+        require(k->stride(3) == 1 && out_k->strides == k->strides, "rope_cs: out_k must share k's layout");
+        hk = k->size(2);
+        kts = k->stride(1);
+        khs = k->stride(2);
+    }
+    require(cs_table.dtype == DType::F32 && cs_table.is_contiguous() && cs_table.dim() == 3 &&
+                cs_table.size(0) == bsz * seq && cs_table.size(2) == 2,
+            "rope_cs: cs_table must be contiguous float32 [bsz * seq_len, R/2, 2]");
+    const Tensor* nw = q_norm ? q_norm : k_norm;
+    check_abi(exl3r_rope_cs(q.data, out_q.data, q.stride(1), q.stride(2), (int)q.size(2), k ? k->data : nullptr,
+                            out_k ? out_k->data : nullptr, kts, khs, (int)hk, code(q.dtype), bsz, seq, (int)hd,
+                            cs_table.data, (int)(cs_table.size(1) * 2), ptr(q_norm), ptr(k_norm),
+                            code_or(nw, DType::F16), norm_eps, norm_constant_bias, (int)rope_mode, s.get()));
+}
+
 void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
           int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
           float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s, const Tensor* position_ids,

@@ -10,6 +10,7 @@
 //   exl3r::ffi::rope_paged_kv                                            <- rope + paged append, src/modules.rs:666-704
 //   exl3r::ffi::argmax_sample / gumbel_sample / gumbel_noise             <- src/ffi.rs:521-535, src/generator.rs:1596
 //   exl3r::ffi::had_r_128 / rms_norm_had / act_mul_had / rope_had        <- src/ffi.rs:606-607, src/modules.rs:224-231
+//   exl3r::ffi::rope_cs_table / rope_cs                                  <- rope() with the sin / cos hoisted per forward
 //   exl3r::ffi::embedding                                                <- index_select, src/modules.rs:430-436
 //   exl3r::RmsNorm::forward / forward_res                                <- src/modules.rs:342-412
 //   exl3r::Embedding::forward                                            <- src/modules.rs:418-437
@@ -152,6 +153,15 @@ void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* o
           int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
           float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s,
           const Tensor* position_ids = nullptr, int32_t* err_flag = nullptr);
+// {cos, sin} * attn_factor of every token's rotary frequencies into cs_table (float32 [bsz * seq, R/2, 2]),
+// as rope() evaluates them for the same positions: built once per forward pass for every layer's rope_cs()
+// (the reference evaluates them in each layer's kernel, kernels/rope.cu:69-85).
+void rope_cs_table(int64_t bsz, int64_t seq_len, const Tensor& inv_freq, int64_t position, const Tensor* positions,
+                   const Tensor* position_ids, float attn_factor, const Tensor& cs_table, const Stream& s);
+// rope() with the rotary pairs read from a rope_cs_table() of the same positions: bit-identical to rope().
+void rope_cs(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& cs_table,
+             const Tensor* q_norm, const Tensor* k_norm, float norm_eps, float norm_constant_bias, RopeStyle rope_mode,
+             const Stream& s);
 // rope() on the raw f16 outputs of the q / k projections (heads packed), each first given its projection's
 // output rotation had_r_128(y, y, None, svh) (src/modules.rs:231); q_post_scale / k_post_scale are the
 // projections' f16 svh or null.

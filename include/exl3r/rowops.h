@@ -29,6 +29,9 @@
  *   exl3r_rope_table        <- exl3_shim_rope with a [max_pos, rotary_dim/2] (or per-sequence
  *                              [bsz, max_pos, rotary_dim/2]) angle table as inv_freq, RoPE::apply's
  *                              freq_table  src/rope.rs:225-260, kernels/rope.cu:69-83, 340-347
+ *   exl3r_rope_cs_table,    <- exl3_shim_rope with its per-layer sin / cos evaluation (kernels/rope.cu:69-85)
+ *   exl3r_rope_cs              hoisted into one table per forward pass, as RoPE::angle_table hoists the
+ *                              angles (src/rope.rs:225-260, 294-301)
  *   exl3r_rope_paged_kv     <- exl3_shim_rope followed by exl3_shim_paged_kv_cache_update
  *                              csrc/exl3_shim.cpp:87-98, 109-112 (ffi.rs:298-350; call sites modules.rs:666-704)
  *   exl3r_gated_rms_norm    <- exl3_shim_gated_rms_norm   csrc/exl3_shim.cpp:143-147 (ffi.rs:118-124, 479-483)
@@ -239,6 +242,31 @@ EXL3R_API int exl3r_rope_table(const void* q, void* out_q, int64_t q_tok_stride,
                      const void* q_norm, const void* k_norm, int norm_dtype,
                      float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
                      int32_t* err_flag, void* stream);
+
+/*
+ * {cos, sin} * attn_factor of every token's rotary frequencies, for exl3r_rope_cs: the positions of a
+ * forward pass are the same in every layer, so one table serves all of its RoPE calls (the reference
+ * evaluates sin / cos in every layer's kernel, kernels/rope.cu:69-85; RoPE::angle_table hoists only the
+ * angles, src/rope.rs:294-301).
+ *   cs_table: [bsz*seq_len, rotary_dim/2] pairs of float32 {cos, sin} (8 * bsz*seq_len * rotary_dim/2
+ *             bytes, 8-byte aligned); row b*seq_len + s holds token s of sequence b.
+ *   inv_freq, rotary_dim, position / positions / position_ids, attn_factor: as exl3r_rope; each pair
+ *             is the value exl3r_rope evaluates for that token and frequency.
+ */
+EXL3R_API int exl3r_rope_cs_table(int64_t bsz, int64_t seq_len, const float* inv_freq, int rotary_dim,
+                                  int32_t position, const int32_t* positions, const int32_t* position_ids,
+                                  float attn_factor, void* cs_table, void* stream);
+
+/*
+ * exl3r_rope with the rotary pairs read from a table that exl3r_rope_cs_table filled for the same
+ * bsz, seq_len, inv_freq, rotary_dim, positions and attn_factor: bit-identical to exl3r_rope, and every
+ * other argument as there.  The kernels copy a token's table row where exl3r_rope evaluates it.
+ */
+EXL3R_API int exl3r_rope_cs(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int num_heads_q,
+                            const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int num_heads_k,
+                            int dtype, int64_t bsz, int64_t seq_len, int head_dim, const void* cs_table,
+                            int rotary_dim, const void* q_norm, const void* k_norm, int norm_dtype, float norm_eps,
+                            float norm_constant_bias, int rope_mode, void* stream);
 
 /*
  * exl3r_rope preceded by the q / k projections' output rotation, in one pass at prefill: the EXL3

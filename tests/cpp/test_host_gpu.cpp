@@ -396,6 +396,25 @@ int main()
         const bool ok = download(q, s) == download(q2, s) && download(k, s) == download(k2, s);
         report("ffi::rope_had == had_r_128 + rope", ok, ok ? "bitwise" : "DIFFER");
     }
+    // rope_cs: RoPE from a {cos, sin} table built once, bitwise equal to rope() evaluating sin / cos.
+    {
+        const int T = 1200, hq = 8, hk = 2, hd = 128;
+        auto qh = host_normal(DType::BF16, T * hq * hd, 0.f, 1.f), kh = host_normal(DType::BF16, T * hk * hd, 0.f, 1.f);
+        auto nh = host_normal(DType::F32, hd, 1.f, 0.1f);
+        std::vector<float> fh(hd / 2);
+        for (int i = 0; i < hd / 2; ++i) fh[i] = (float)(1.0 / std::pow(1e6, 2.0 * i / hd));
+        std::vector<uint8_t> fb(fh.size() * 4);
+        std::memcpy(fb.data(), fh.data(), fb.size());
+        auto q = upload(qh, DType::BF16, { 1, T, hq, hd }, s), k = upload(kh, DType::BF16, { 1, T, hk, hd }, s);
+        auto q2 = upload(qh, DType::BF16, { 1, T, hq, hd }, s), k2 = upload(kh, DType::BF16, { 1, T, hk, hd }, s);
+        auto qn = upload(nh, DType::F32, { hd }, s), f = upload(fb, DType::F32, { hd / 2 }, s);
+        auto cs = OwnedTensor::empty(DType::F32, { T, hd / 2, 2 });
+        ffi::rope_cs_table(1, T, f.t, 3000, nullptr, nullptr, 1.f, cs.t, s);
+        ffi::rope_cs(q.t, q.t, &k.t, &k.t, cs.t, &qn.t, &qn.t, 1e-6f, 0.f, RopeStyle::NeoX, s);
+        ffi::rope(q2.t, q2.t, &k2.t, &k2.t, f.t, 3000, nullptr, &qn.t, &qn.t, 1e-6f, 0.f, RopeStyle::NeoX, 1.f, s);
+        const bool ok = download(q, s) == download(q2, s) && download(k, s) == download(k2, s);
+        report("ffi::rope_cs_table + rope_cs == rope", ok, ok ? "bitwise" : "DIFFER");
+    }
     // gated_rms_norm_had: the GDN output norm (8 tokens x 4 heads of 128, one o_proj row per token)
     // into o_proj's input rotation, bitwise equal to the gated norm followed by had_r_128.
     {

@@ -218,6 +218,32 @@ def test_rope_table_validation():
     assert call(table=None) == exl3r.EINVAL and "angle table" in _err()
 
 
+def test_rope_cs_validation():
+    lib = exl3r.load()
+    # exl3r_rope_cs_table(bsz, seq, inv_freq, R, position, positions, position_ids, attn, cs_table)
+    assert lib.exl3r_rope_cs_table(1, 3, FAKE, 63, 0, None, None, 1.0, FAKE + 65536, None) == exl3r.EINVAL
+    assert lib.exl3r_rope_cs_table(1, 3, FAKE, 64, 0, FAKE, FAKE, 1.0, FAKE + 65536, None) == exl3r.EINVAL
+    assert "at most one" in _err()
+    assert lib.exl3r_rope_cs_table(1, 3, FAKE, 64, 0, None, None, 1.0, FAKE + 65540, None) == exl3r.EINVAL
+    assert "aligned" in _err()
+    assert lib.exl3r_rope_cs_table(1, 3, None, 64, 0, None, None, 1.0, FAKE + 65536, None) == exl3r.EINVAL
+    assert lib.exl3r_rope_cs_table(0, 3, None, 64, 0, None, None, 1.0, None, None) == exl3r.OK
+
+    def rope_cs(**kw):
+        # (q, oq, q_ts, q_hs, hq, k, ok, k_ts, k_hs, hk, dtype, bsz, seq, hd, cs, R, qn, kn, nwt, eps, cb, mode)
+        a = dict(q=FAKE, oq=FAKE, qts=4 * 64, qhs=64, hq=4, k=None, ok=None, kts=0, khs=64, hk=0, dt=F16, bsz=1,
+                 seq=3, hd=64, cs=FAKE + 65536, R=64, qn=None, kn=None, nwt=F16, eps=1e-6, cb=0.0,
+                 mode=exl3r.ROPE_NEOX)
+        a.update(kw)
+        return lib.exl3r_rope_cs(*a.values(), None)
+    assert rope_cs(dt=F32) == exl3r.EDTYPE
+    assert rope_cs(cs=None) == exl3r.EINVAL
+    assert rope_cs(cs=FAKE + 65540) == exl3r.EINVAL and "aligned" in _err()
+    assert rope_cs(R=128) == exl3r.EINVAL
+    assert rope_cs(mode=3) == exl3r.EINVAL
+    assert rope_cs(seq=0) == exl3r.OK
+
+
 def test_hadamard_validation():
     lib = exl3r.load()
     # exl3r_had_r_128(x, dtype, ldx, out, ldo, rows, cols, pre, post, scale)

@@ -1,0 +1,123 @@
+"""GPU parity of exl3r_rope_cs_table + exl3r_rope_cs: RoPE (with the optional head RMSNorm) whose
+per-layer sin / cos evaluation (kernels/rope.cu:69-85) is hoisted into one {cos, sin} table per forward
+pass.  exl3r_rope_cs is checked bit for bit against exl3r_rope on the same inputs (which the rope tests
+pin against the oracle) on every kernel it shares with it: the wave-per-token prefill kernel (NeoX,
+f16 and bf16), the flattened kernel (decode, GPT-J, head_dim 64 / 256) and the generic one (head_dim
+not a multiple of 8), with each position source, attn_factor, q without k, out of place and batches.
+The table itself is checked against the closed form: fl32(cos / sin of the fp32 angle
+fl32(inv_freq[t] * pos)) * attn_factor, to <= 1 ulp of fp32, and bitwise on exactly representable
+angles (pos 0)."""
+import numpy as np
+import pytest
+import torch
+
+import exl3r
+import exl3r.ffi as ffi
+from _gpu import dev_normal, from_dev
+from oracle import oracle as orc
+from test_gpu_rope import inv_freq, ragged_position_ids
+
+pytestmark = pytest.mark.gpu
+
+F16, BF16, F32 = orc.F16, orc.BF16, orc.F32
+
+
+def same(a, b):
+    return torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def run(bsz, seq, hq, hk, hd, R, mode, dt, nwt=None, position=0, positions=None, position_ids=None, attn=1.0,
+        with_k=True, out_of_place=False, seed=0):
+    q = dev_normal((bsz, seq, hq, hd), 0.0, 1.0, dt, seed)
+    k = dev_normal((bsz, seq, hk, hd), 0.0, 1.0, dt, seed + 1) if with_k else None
+    qn = dev_normal((hd,), 1.0, 0.1, nwt, seed + 2) if nwt is not None else None
+    kn = dev_normal((hd,), 1.0, 0.1, nwt, seed + 3) if nwt is not None and with_k else None
+    f = torch.from_numpy(inv_freq(R)).cuda()
+    pos_d = torch.from_numpy(positions).cuda() if positions is not None else None
+    pid_d = torch.from_numpy(position_ids).cuda() if position_ids is not None else None
+    eq, ek = q.clone(), (k.clone() if with_k else None)
+    ffi.rope(eq, eq, ek, ek, f, position, pos_d, qn, kn, 1e-6, 0.0, mode, attn, position_ids=pid_d)
+    cs = ffi.rope_cs_table(bsz, seq, f, position, pos_d, pid_d, attn)
+    oq = torch.empty_like(q) if out_of_place else q
+    ok = (torch.empty_like(k) if out_of_place else k) if with_k else None
+    qh = from_dev(q)
+    ffi.rope_cs(q, oq, k, ok, cs, qn, kn, 1e-6, 0.0, mode)
+    torch.cuda.synchronize()
+    tag = f"rope_cs b{bsz} s{seq} h{hq}/{hk} d{hd} R{R} mode{mode} {dt} w{nwt}"
+    assert same(oq, eq), tag + " q vs exl3r_rope"
+    if with_k:
+        assert same(ok, ek), tag + " k vs exl3r_rope"
+    if out_of_place:
+        assert np.array_equal(from_dev(q), qh), tag + " q must not be written"
+    return cs
+
+
+def token_positions(bsz, seq, position, positions, position_ids):
+    if position_ids is not None:
+        return position_ids.reshape(-1).astype(np.int64)
+    base = positions.astype(np.int64) if positions is not None else np.full(bsz, position, np.int64)
+    return (base[:, None] + np.arange(seq)[None, :]).reshape(-1)
+
+
+def test_c4_prefill_wave_per_token():
+    """Config 4's ragged prefill (~4.6k tokens, positions up to ~33k), 64 q / 8 kv heads of 128, NeoX."""
+    pid = ragged_position_ids(0)[None, :]
+    run(1, pid.size, 64, 8, 128, 128, exl3r.ROPE_NEOX, F16, nwt=F16, position_ids=pid, seed=1)
+    run(1, pid.size, 64, 8, 128, 128, exl3r.ROPE_NEOX, BF16, nwt=BF16, position_ids=pid, seed=2)
+
+
+def test_table_closed_form():
+    """cos / sin of the fp32 angle evaluated in fp64 and rounded once, times attn_factor: within 1 ulp of
+    numpy's double-precision cos / sin of the same fp32 angle rounded to fp32 (the kernel's own fp64
+    evaluation may sit on the other side of a rounding boundary), bitwise at position 0."""
+    bsz, seq, R, attn = 3, 700, 128, 0.75
+    positions = np.array([0, 5000, 31000], np.int32)
+    cs = from_dev(run(bsz, seq, 8, 2, 128, R, exl3r.ROPE_NEOX, F16, nwt=F32, positions=positions, attn=attn,
+                      seed=3))
+    pos = token_positions(bsz, seq, 0, positions, None)
+    f = inv_freq(R)
+    ang = (f[None, :] * pos[:, None].astype(np.float32)).astype(np.float32)
+    ec = (np.cos(ang.astype(np.float64)).astype(np.float32) * np.float32(attn)).astype(np.float32)
+    es = (np.sin(ang.astype(np.float64)).astype(np.float32) * np.float32(attn)).astype(np.float32)
+    for got, exp, what in ((cs[..., 0], ec, "cos"), (cs[..., 1], es, "sin")):
+        ulp = np.abs(got.view(np.int32).astype(np.int64) - exp.view(np.int32).astype(np.int64))
+        sign_ok = (np.sign(got) == np.sign(exp)) | (got == 0) | (exp == 0)
+        assert sign_ok.all() and ulp[got != 0].max() <= 1, what
+        assert np.array_equal(got[0], exp[0]), what + " at position 0"
+    assert np.array_equal(cs[0, :, 0], np.full(R // 2, attn, np.float32))
+
+
+@pytest.mark.parametrize("case", ["decode", "gptj", "hd64", "hd256", "generic", "q_only", "position"])
+def test_flattened_and_generic_kernels(case):
+    if case == "decode":          # 64 sequences x 1 token at per-sequence positions: the flattened kernel
+        pos = np.random.default_rng(4).integers(0, 40000, 64).astype(np.int32)
+        run(64, 1, 64, 8, 128, 128, exl3r.ROPE_NEOX, F16, nwt=F16, positions=pos, seed=4)
+    elif case == "gptj":
+        pid = ragged_position_ids(5)[None, :]
+        run(1, pid.size, 16, 4, 128, 64, exl3r.ROPE_GPTJ, BF16, nwt=F32, position_ids=pid, seed=5)
+    elif case == "hd64":
+        run(2, 600, 8, 2, 64, 64, exl3r.ROPE_NEOX, F16, nwt=F16, position=123, out_of_place=True, seed=6)
+    elif case == "hd256":
+        run(2, 300, 4, 1, 256, 128, exl3r.ROPE_NEOX, BF16, position=7, seed=7)
+    elif case == "generic":       # head_dim 100: not 8-element lane chunks
+        run(2, 50, 4, 2, 100, 100, exl3r.ROPE_NEOX, F16, nwt=F16, position=9, seed=8)
+    elif case == "q_only":
+        run(1, 1500, 12, 0, 128, 128, exl3r.ROPE_NEOX, F16, with_k=False, position=3, attn=1.25, seed=9)
+    else:
+        run(4, 1100, 8, 8, 128, 128, exl3r.ROPE_NEOX, F16, nwt=BF16, position=20000, seed=10)
+
+
+def test_zero_tokens_and_errors():
+    f = torch.from_numpy(inv_freq(128)).cuda()
+    z = torch.empty((1, 0, 4, 128), device="cuda", dtype=torch.float16)
+    cs0 = ffi.rope_cs_table(1, 0, f, 0)
+    assert cs0.shape == (0, 64, 2)
+    ffi.rope_cs(z, z, None, None, cs0, None, None, 1e-6, 0.0, exl3r.ROPE_NEOX)
+    q = dev_normal((1, 4, 4, 128), 0, 1, F16, 11)
+    cs = ffi.rope_cs_table(1, 4, f, 0)
+    with pytest.raises(ValueError):                                 # table of another token count
+        ffi.rope_cs(q, q, None, None, cs[:3], None, None, 1e-6, 0.0, exl3r.ROPE_NEOX)
+    with pytest.raises(exl3r.Exl3rError):                           # rotary_dim beyond head_dim
+        q64 = dev_normal((1, 4, 4, 64), 0, 1, F16, 12)
+        ffi.rope_cs(q64, q64, None, None, cs, None, None, 1e-6, 0.0, exl3r.ROPE_NEOX)
+    torch.cuda.synchronize()
