@@ -36,6 +36,7 @@ OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "
        "deinterleave_q35", "gated_norm_had_q35", "gated_norm_had_q35_unfused", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
        "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_unfused", "silu_had_c3",
        "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_unfused", "rope_cs_c4", "rope_cs_table_c4",
+       "qg_rope_q35", "qg_rope_q35_unfused",
        "rope_kv_had_prefill", "rope_kv_had_prefill_unfused", "mlp_had_c3", "mlp_had_c3_unfused",
        "prefill_layer", "prefill_layer_unfused", "calib_copy",
        "calib_copy_cached"]
@@ -198,6 +199,41 @@ def make_rope_cs(name, pos, hq, hk, hd, R, dt, seed, table_only):
         ffi.rope_cs(q, q, k, k, table, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX)
     return Work(name, nbytes, launch, f"q/k head-norm + neox RoPE from a {{cos, sin}} table T={T} heads {hq}/{hk}",
                 sets)
+
+
+def make_qg_rope(name, fused, tokens=4096, hq=32, hk=4, hd=128, seed=640):
+    """Qwen3.5 gated attention around the attention kernel: the q projection's interleaved [q | g] heads
+    split (src/modules.rs:637-646), q / k head-norm (bias 1) + NeoX RoPE (669-681), and the output gate
+    o *= sigmoid(g) (786).  Fused: exl3r_rope_qg reads q from qg and writes it dense, mul_sigmoid reads g
+    in place from qg; unfused: deinterleave_qg, rope in place, mul_sigmoid on the dense g.  Both count the
+    fused job's bytes: q read and written, k read and written, o and g read, o written, norm weights."""
+    import numpy as np
+    import torch
+    import exl3r
+    import exl3r.ffi as ffi
+    f16 = torch.float16
+    nbytes = 2 * tokens * hq * hd * 2 + 2 * tokens * hk * hd * 2 + 3 * tokens * hq * hd * 2 + 2 * hd * 2
+    sets = sets_for(nbytes)
+    inv = torch.from_numpy((1.0 / 1e6 ** (np.arange(0, hd, 2, dtype=np.float64) / hd)).astype(np.float32)).cuda()
+    qn, kn = gen((hd,), 0.0, 0.1, f16, seed + 50), gen((hd,), 0.0, 0.1, f16, seed + 51)
+    n = tokens * hq
+    bufs = [(gen((1, tokens, hq, 2 * hd), 0.0, 1.0, f16, seed + 3 * k), gen((1, tokens, hk, hd), 0.0, 1.0, f16, seed + 3 * k + 1),
+             gen((n, hd), 0.0, 1.0, f16, seed + 3 * k + 2)) for k in range(sets)]
+    q = torch.empty((1, tokens, hq, hd), device="cuda", dtype=f16)
+    g = torch.empty((1, tokens, hq * hd), device="cuda", dtype=f16)
+
+    def launch(i):
+        qg, k, o = bufs[i % sets]
+        if fused:
+            ffi.rope_qg(qg, q, k, k, inv, 0, None, qn, kn, 1e-6, 1.0, exl3r.ROPE_NEOX, 1.0)
+            ffi.mul_sigmoid(o, qg.view(n, 2 * hd)[:, hd:], o)
+        else:
+            ffi.deinterleave_qg(qg.view(1, tokens, hq * 2 * hd), q, g, hd)
+            ffi.rope(q, q, k, k, inv, 0, None, qn, kn, 1e-6, 1.0, exl3r.ROPE_NEOX, 1.0)
+            ffi.mul_sigmoid(o, g.view(n, hd), o)
+    kind = "fused (rope_qg + gate read from qg)" if fused else "unfused (deinterleave + rope + gate)"
+    return Work(name, nbytes, launch, f"gated attention q | g split + head-norm RoPE + output gate T={tokens} "
+                                      f"heads {hq}/{hk} of {hd}, {kind}", sets)
 
 
 def make_rope(name, pos, hq, hk, hd, R, mode, dt, seed, bsz=1, per_seq=False):
@@ -671,6 +707,8 @@ def make_all(only=None):
         "rope_c4_gptj": lambda: make_rope("rope_c4_gptj", ragged, 64, 8, 128, 64, "gptj", f16, 310),
         "rope_cs_c4": lambda: make_rope_cs("rope_cs_c4", ragged, 64, 8, 128, 128, f16, 300, False),
         "rope_cs_table_c4": lambda: make_rope_cs("rope_cs_table_c4", ragged, 64, 8, 128, 128, f16, 300, True),
+        "qg_rope_q35": lambda: make_qg_rope("qg_rope_q35", True),
+        "qg_rope_q35_unfused": lambda: make_qg_rope("qg_rope_q35_unfused", False),
         "gather_c5": lambda: make_gather("gather_c5", 151936, 5120, 16384, bf16, bf16, zipf_ids(16384, 151936, 1), 400),
         "gather_norm_c5": lambda: make_gather("gather_norm_c5", 151936, 5120, 16384, bf16, bf16,
                                               zipf_ids(16384, 151936, 1), 400, norm=True),
@@ -924,6 +962,11 @@ def main():
                    "desc": "C4 RoPE evaluating sin / cos in every layer vs reading a {cos, sin} table built once "
                            "per forward pass (bit-identical results); the table costs table_per_forward_us once"}
         log(f"rope_cs: {json.dumps(rope_cs)}")
+        qf, qu = ops["qg_rope_q35"]["us"], ops["qg_rope_q35_unfused"]["us"]
+        gated_attn = {"fused_us": qf, "unfused_us": qu, "speedup": round(qu / qf, 3),
+                      "desc": "Qwen3.5 gated attention's q | g split + q/k head-norm RoPE + output gate, 4096 tokens, "
+                              "32/4 heads of 128: rope_qg with the gate read in place vs deinterleave + rope + gate"}
+        log(f"gated_attention: {json.dumps(gated_attn)}")
 
         # The timed step: config-3 prefill row ops back to back.
         step_works = [works["rms_c3"], works["silu_c3"], works["gelu_c3"]]
@@ -962,6 +1005,7 @@ def main():
                    "frac_peak": round(value / PEAK_GBS, 4)},
         "roofline": roof, "cpu_baseline": cpu, "ops": ops, "decode_step": decode, "c2_decode_rms_norm": c2,
         "rope_paged_kv": rope_kv, "sampling": sampling, "hadamard": hadamard, "rope_cs_table": rope_cs,
+        "gated_attention_qg": gated_attn,
         "copy_reference": {"gbs": round(copy_gbs, 1), "frac_peak": round(copy_gbs / PEAK_GBS, 4),
                            "desc": "non-temporal 16 B/lane device copy of 1 GiB (read + write), the practical HBM ceiling reference"},
     }

@@ -140,6 +140,44 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
     }
 }
 
+// Short strided rows (at most 64 chunks, e.g. the gate of one 128-wide head read in place from an
+// interleaved q | g projection): (row, chunk) items flattened over the whole grid, so a workgroup
+// covers several rows instead of idling most of its lanes on one.  UNROLL items per thread in flight.
+template <int ACT, class IT, class OT, int UNROLL, bool LIMIT>
+__global__ __launch_bounds__(256) void k_act_mul_short(ActArgs a)
+{
+    const uint32_t cpr = (uint32_t)(a.cols >> 3);
+    const uint32_t n = (uint32_t)a.rows * cpr;
+    const uint32_t nt = blockDim.x;
+    for (uint32_t base = blockIdx.x * nt * UNROLL + threadIdx.x; base < n; base += gridDim.x * nt * UNROLL)
+    {
+        typename IT::Vec xv[UNROLL], yv[UNROLL];
+        uint32_t r[UNROLL], c[UNROLL];
+        #pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+        {
+            const uint32_t i = base + u * nt;
+            r[u] = i / cpr;
+            c[u] = i - r[u] * cpr;
+            if (i < n)
+            {
+                xv[u] = load8s<IT>((const char*)a.x + (int64_t)r[u] * a.ldx * IT::bytes, (int64_t)c[u] * 8);
+                yv[u] = load8s<IT>((const char*)a.y + (int64_t)r[u] * a.ldy * IT::bytes, (int64_t)c[u] * 8);
+            }
+        }
+        #pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+        {
+            if (base + u * nt >= n) continue;
+            float g[8], v[8], o[8];
+            unpack8<IT>(xv[u], g);
+            unpack8<IT>(yv[u], v);
+            act_chunk<ACT, OT, LIMIT>(g, v, a.limit, o);
+            store8<OT>((char*)a.z + (int64_t)r[u] * a.ldz * OT::bytes, (int64_t)c[u] * 8, pack8<OT>(o));
+        }
+    }
+}
+
 // Generic fallback: any shape, stride and alignment, one element per thread.
 template <int ACT>
 __global__ __launch_bounds__(256) void k_act_mul_generic(ActArgs a, int it, int ot)
@@ -164,6 +202,20 @@ static void launch_act_vec(const ActArgs& a, hipStream_t s)
     const int unroll = (tu.act_unroll == 1 || tu.act_unroll == 2 || tu.act_unroll == 4 || tu.act_unroll == 8) ? tu.act_unroll : 2;
     const int threads = (tu.act_threads > 0 && tu.act_threads % 64 == 0 && tu.act_threads <= 256) ? tu.act_threads : 128;
     const int64_t cpr = a.cols >> 3;
+    if constexpr (HAD == 0)
+    {
+        // Rows of at most 64 chunks: one workgroup per row would idle most of its lanes (a 128-wide
+        // strided gate: 52 us against 17 us for the same bytes as one flat row).
+        if (a.rows > 1 && cpr <= 64 && a.rows * cpr < ((int64_t)1 << 31))
+        {
+            const int64_t n = a.rows * cpr;
+            int64_t blocks = (n + 256 * 2 - 1) / (256 * 2);
+            if (blocks > kMaxGridX) blocks = kMaxGridX;
+            if (a.limit != 0.0f) k_act_mul_short<ACT, IT, OT, 2, true><<<(unsigned)blocks, 256, 0, s>>>(a);
+            else k_act_mul_short<ACT, IT, OT, 2, false><<<(unsigned)blocks, 256, 0, s>>>(a);
+            return;
+        }
+    }
     const int per = a.limit != 0.0f ? 2 : unroll;
     int64_t bx = (cpr + (int64_t)threads * per - 1) / ((int64_t)threads * per);
     if (tu.act_blocks_per_cu > 0)

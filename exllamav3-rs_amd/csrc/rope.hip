@@ -35,6 +35,7 @@ struct RopeArgs
     const void* k;
     void* ok;
     int64_t q_ts, q_hs, k_ts, k_hs;   // token / head strides (elements)
+    int64_t oq_ts, oq_hs;             // out_q's token / head strides (q's, except exl3r_rope_qg)
     int hq, hk, hd, R;
     int64_t seq_len, tokens;
     const float* inv_freq;
@@ -405,9 +406,8 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a)
                 const char* ip;
                 if (kind[it] == KIND_Q)
                 {
-                    const int64_t off = ((int64_t)tok * a.q_ts + (int64_t)rel * a.q_hs) * IO::bytes;
-                    ip = (const char*)a.q + off;
-                    optr[it] = (char*)a.oq + off;
+                    ip = (const char*)a.q + ((int64_t)tok * a.q_ts + (int64_t)rel * a.q_hs) * IO::bytes;
+                    optr[it] = (char*)a.oq + ((int64_t)tok * a.oq_ts + (int64_t)rel * a.oq_hs) * IO::bytes;
                 }
                 else if constexpr (!APPEND)
                 {
@@ -493,7 +493,8 @@ struct RopeBatch
     int b;
 };
 
-template <class IO, int MODE, int LPH, int HPL, int NORM, bool APPEND, bool HADR = false, int SRC = SRC_FREQ>
+template <class IO, int MODE, int LPH, int HPL, int NORM, bool APPEND, bool HADR = false, int SRC = SRC_FREQ,
+          bool QOUT = false>
 __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
 {
     extern __shared__ float2 cs[];            // [4 waves][R / 2]
@@ -512,7 +513,7 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
     const LaneW<NORM> wk = lane_weights<NORM>(a, a.kw, e0, lane_ok);
     // Per-lane choices between argument fields select values, not addresses: a selected field
     // address is read with a vector load from the argument segment on every use.
-    const int64_t q_hs = a.q_hs, k_hs = a.k_hs, v_hs = APPEND ? a.v_hs : 0;
+    const int64_t q_hs = a.q_hs, k_hs = a.k_hs, v_hs = APPEND ? a.v_hs : 0, oq_hs = a.oq_hs;
     auto head_stride = [&](int kind) { return kind == KIND_Q ? q_hs : kind == KIND_K ? k_hs : v_hs; };
 
     auto issue = [&](RopeBatch<IO, HPL>& t) {
@@ -541,7 +542,7 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
         lane_sincos<MODE>(row, e0, a.R, c, s);
     };
     auto compute = [&](RopeBatch<IO, HPL>& t, const float (&c)[8], const float (&s)[8]) {
-        char* qo = (char*)a.oq + t.tok * a.q_ts * IO::bytes;
+        char* qo = (char*)a.oq + t.tok * (QOUT ? a.oq_ts : a.q_ts) * IO::bytes;
         char* ko = (char*)a.ok + t.tok * a.k_ts * IO::bytes;
         #pragma unroll
         for (int i = 0; i < HPL; ++i)
@@ -562,12 +563,16 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
             }
             rope_head<IO, MODE, LPH, NORM>(a, t.v[i], kd != KIND_V, select_w<NORM>(kd == KIND_Q, wq, wk), c, s, e0, l64);
             if (!t.act[i]) continue;
+            // QOUT: out_q has its own layout (exl3r_rope_qg).  A compile-time choice: the separate
+            // offset costs the plain prefill kernel 7 us at C4 (45.6 vs 38.5 us).
+            const int32_t qoff = QOUT ? (int32_t)((int64_t)t.hidx[i] * oq_hs) + e0 : t.off[i];
             if (!APPEND)
             {
-                store8<IO>(kd == KIND_Q ? qo : ko, t.off[i], t.v[i]);
+                if (kd == KIND_Q) store8<IO>(qo, qoff, t.v[i]);
+                else store8<IO>(ko, t.off[i], t.v[i]);
                 continue;
             }
-            if (kd == KIND_Q) store8<IO>(qo, t.off[i], t.v[i]);
+            if (kd == KIND_Q) store8<IO>(qo, qoff, t.v[i]);
             else
             {
                 if (kd == KIND_K && a.ok) store8<IO>(ko, t.off[i], t.v[i]);
@@ -628,6 +633,7 @@ __global__ __launch_bounds__(256) void k_rope_generic(RopeArgs a, int dt, int mo
         void* op = isq ? a.oq : kind == KIND_K ? a.ok : nullptr;
         const int64_t off = isq ? tok * a.q_ts + (int64_t)head * a.q_hs
                                 : kind == KIND_K ? tok * a.k_ts + (int64_t)hkv * a.k_hs : tok * a.v_ts + (int64_t)hkv * a.v_hs;
+        const int64_t ooff = isq ? tok * a.oq_ts + (int64_t)head * a.oq_hs : off;
         void* cp = crow >= 0 && kind != KIND_Q ? (kind == KIND_K ? a.kc : a.vc) : nullptr;
         const int64_t coff = crow + (int64_t)hkv * a.hd;
         if (kind == KIND_V)
@@ -672,7 +678,7 @@ __global__ __launch_bounds__(256) void k_rope_generic(RopeArgs a, int dt, int mo
         __syncthreads();
         for (int d = tid; d < a.hd; d += blockDim.x)
         {
-            if (op) store1(op, dt, off + d, hv[d]);
+            if (op) store1(op, dt, ooff + d, hv[d]);
             if (cp) store1(cp, dt, coff + d, hv[d]);
         }
         __syncthreads();
@@ -715,7 +721,7 @@ static void launch_rope_lph(RopeArgs a, int iters, hipStream_t s)
 // token per wave (38.5 us; 3 per lane 42 us); bf16 heads (fp32 norm) with 3 per lane on a
 // persistent grid of 4 workgroups per CU (37.0 us; 2 per lane 42 us).  With the paged append
 // (4096 tokens, + 8 v heads) 3 per lane: 40.0 us, 2 per lane 41-43 us.
-template <class IO, int MODE, int LPH, int NORM, bool HADR = false, int SRC = SRC_FREQ>
+template <class IO, int MODE, int LPH, int NORM, bool HADR = false, int SRC = SRC_FREQ, bool QOUT = false>
 static void launch_rope_tok(RopeArgs a, hipStream_t s)
 {
     const Tuning& tu = tuning();
@@ -732,7 +738,9 @@ static void launch_rope_tok(RopeArgs a, hipStream_t s)
     const size_t lds = 4 * (size_t)(a.R / 2) * sizeof(float2);
     auto go = [&](auto H) {
         constexpr int HP = decltype(H)::value;
-        if constexpr (SRC == SRC_CS)
+        if constexpr (QOUT)
+            k_rope_tok<IO, MODE, LPH, HP, NORM, false, false, SRC_FREQ, true><<<(unsigned)blocks, 256, lds, s>>>(a);
+        else if constexpr (SRC == SRC_CS)
             k_rope_tok<IO, MODE, LPH, HP, NORM, false, false, SRC_CS><<<(unsigned)blocks, 256, lds, s>>>(a);
         else if constexpr (HADR)
         {
@@ -780,6 +788,14 @@ static void launch_rope_vec(const RopeArgs& a, int lph, hipStream_t s)
     }
     if constexpr (MODE == EXL3R_ROPE_NEOX)
     {
+        if (rope_tok_launch(a) && (a.oq_ts != a.q_ts || a.oq_hs != a.q_hs))
+        {
+            // exl3r_rope_qg (no append): out_q in its own layout.
+            if (lph == 8) launch_rope_tok<IO, MODE, 8, NORM, false, SRC_FREQ, true>(a, s);
+            else if (lph == 16) launch_rope_tok<IO, MODE, 16, NORM, false, SRC_FREQ, true>(a, s);
+            else launch_rope_tok<IO, MODE, 32, NORM, false, SRC_FREQ, true>(a, s);
+            return;
+        }
         if (rope_tok_launch(a))
         {
             if (lph == 8) launch_rope_tok<IO, MODE, 8, NORM>(a, s);
@@ -851,6 +867,7 @@ static int rope_prepare(const char* op, RopeArgs& a, const void* q, void* out_q,
 
     a.q = q; a.oq = out_q; a.k = k; a.ok = out_k;
     a.q_ts = q_tok_stride; a.q_hs = q_head_stride; a.k_ts = k_tok_stride; a.k_hs = k_head_stride;
+    a.oq_ts = q_tok_stride; a.oq_hs = q_head_stride;
     a.hq = num_heads_q; a.hk = k ? num_heads_k : 0; a.hd = head_dim; a.R = rotary_dim;
     a.seq_len = seq_len; a.tokens = tokens; a.inv_freq = inv_freq;
     a.position = position; a.positions = positions; a.position_ids = position_ids;
@@ -895,6 +912,7 @@ static bool rope_vec_ok(const RopeArgs& a, int rope_mode)
     const int lph = rope_lph(a);
     bool vec = a.hd % 8 == 0 && lph >= 8 && lph <= 32 && a.R % (rope_mode == EXL3R_ROPE_NEOX ? 16 : 2) == 0;
     vec = vec && aligned16(a.q) && aligned16(a.oq) && a.q_ts % 8 == 0 && a.q_hs % 8 == 0;
+    vec = vec && a.oq_ts % 8 == 0 && a.oq_hs % 8 == 0;
     vec = vec && (!a.k || (aligned16(a.k) && a16(a.ok) && a.k_ts % 8 == 0 && a.k_hs % 8 == 0));
     vec = vec && (!a.v || (aligned16(a.v) && a.v_ts % 8 == 0 && a.v_hs % 8 == 0 && a16(a.kc) && a16(a.vc)));
     vec = vec && (!a.qw || (aligned16(a.qw) && a16(a.kw)));
@@ -1201,4 +1219,35 @@ extern "C" int exl3r_rope_cs(const void* q, void* out_q, int64_t q_tok_stride, i
     a.cst = (const float2*)cs_table;
     rc = rope_dispatch(op, a, dtype, rope_mode, stream);
     return rc;
+}
+
+// exl3r_deinterleave_qg followed by exl3r_rope on q (and k), in one pass: the q half of each head's
+// interleaved [q | g] pair is read straight from qg and written roped (and normed) to a dense out_q;
+// g stays in qg for exl3r_mul_sigmoid with a row stride of 2 * head_dim.
+extern "C" int exl3r_rope_qg(const void* qg, int64_t qg_tok_stride, void* out_q, int num_heads_q, const void* k,
+                             void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int num_heads_k, int dtype,
+                             int64_t bsz, int64_t seq_len, int head_dim, const float* inv_freq, int rotary_dim,
+                             int32_t position, const int32_t* positions, const int32_t* position_ids,
+                             const void* q_norm, const void* k_norm, int norm_dtype, float norm_eps,
+                             float norm_constant_bias, int rope_mode, float attn_factor, void* stream)
+{
+    const char* op = "exl3r_rope_qg";
+    if (head_dim <= 0 || head_dim > 4096)
+        return set_error(EXL3R_EINVAL, "%s: head_dim %d must be in [2, 4096]", op, head_dim);
+    RopeArgs a;
+    int rc = rope_prepare(op, a, qg, out_q, qg_tok_stride, 2 * (int64_t)head_dim, num_heads_q, k, out_k, false,
+                          k_tok_stride, k_head_stride, num_heads_k, dtype, bsz, seq_len, head_dim, inv_freq, rotary_dim,
+                          position, positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias,
+                          rope_mode, attn_factor);
+    if (rc || a.tokens == 0) return rc;
+    a.oq_hs = head_dim;
+    a.oq_ts = (int64_t)num_heads_q * head_dim;
+    // out_q is written while qg is read by other workgroups: the two must not overlap.
+    const int es = dtype_bytes(dtype);
+    const char* q0 = (const char*)qg;
+    const char* q1 = q0 + ((a.tokens - 1) * qg_tok_stride + 2 * (int64_t)num_heads_q * head_dim) * es;
+    const char* o0 = (const char*)out_q;
+    const char* o1 = o0 + a.tokens * a.oq_ts * es;
+    if (o0 < q1 && q0 < o1) return set_error(EXL3R_EINVAL, "%s: out_q overlaps qg", op);
+    return rope_dispatch(op, a, dtype, rope_mode, stream);
 }

@@ -34,6 +34,8 @@ PROTOTYPES = {
                             _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _vp, _vp, _vp]),
     "exl3r_rope_table": (_i, [_vp, _vp, _i64, _i64, _i, _vp, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _i64, _i64,
                               _i, _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _vp, _vp]),
+    "exl3r_rope_qg": (_i, [_vp, _i64, _vp, _i, _vp, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _i, _i32, _vp, _vp, _vp,
+                           _vp, _i, _f, _f, _i, _f, _vp]),
     "exl3r_rope_cs_table": (_i, [_i64, _i64, _vp, _i, _i32, _vp, _vp, _f, _vp, _vp]),
     "exl3r_rope_cs": (_i, [_vp, _vp, _i64, _i64, _i, _vp, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _i, _vp, _vp, _i,
                            _f, _f, _i, _vp]),

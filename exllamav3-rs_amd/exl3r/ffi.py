@@ -225,6 +225,40 @@ def rope(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm
                             norm_eps, norm_constant_bias, rope_mode, attn_factor, _stream(q, stream)))
 
 
+def rope_qg(qg, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias,
+            rope_mode, attn_factor, position_ids=None, stream=None):
+    """deinterleave_qg() then rope() on its q, in one pass (gated attention, src/modules.rs:637-646 then
+    669-681): qg (bsz, seq_len, heads, 2 * head_dim) holds each head's [q | g]; out_q (bsz, seq_len, heads,
+    head_dim) dense receives the roped q.  The gate stays in qg: qg[..., head_dim:] as rows of head_dim with
+    row stride 2 * head_dim (mul_sigmoid's y)."""
+    if qg.dim() != 4 or out_q.dim() != 4:
+        raise ValueError("qg must be (bsz, seq_len, heads, 2 * head_dim) and out_q (bsz, seq_len, heads, head_dim)")
+    bsz, seq, hq, hd2 = qg.shape
+    hd = hd2 // 2
+    if hd2 % 2 or tuple(out_q.shape) != (bsz, seq, hq, hd) or not out_q.is_contiguous():
+        raise ValueError("out_q must be a dense (bsz, seq_len, heads, head_dim)")
+    if qg.stride(3) != 1 or qg.stride(2) != hd2 or (bsz > 1 and seq > 1 and qg.stride(0) != seq * qg.stride(1)):
+        raise ValueError("qg must hold dense [q | g] heads with batch stride seq_len * token stride")
+    hk, k_ts, k_hs = 0, 0, 0
+    if k is not None:
+        if k.dim() != 4 or k.shape[0] != bsz or k.shape[1] != seq or k.shape[3] != hd:
+            raise ValueError("k is incorrect shape")
+        if k.stride(3) != 1 or out_k is None or out_k.stride() != k.stride():
+            raise ValueError("k innermost dim must be dense and out_k must share k's layout")
+        if seq > 1 and k.stride(0) != seq * k.stride(1) and bsz > 1:
+            raise ValueError("k batch stride must be seq_len * token stride")
+        hk, k_ts, k_hs = k.shape[2], k.stride(1), k.stride(2)
+    for t in (positions, position_ids):
+        if t is not None and t.dtype != torch.int32:
+            raise TypeError("positions / position_ids must be int32")
+    nw = q_norm if q_norm is not None else k_norm
+    check(load().exl3r_rope_qg(_ptr(qg), qg.stride(1), _ptr(out_q), hq, _ptr(k), _ptr(out_k), k_ts, k_hs, hk,
+                               dtype_code(qg), bsz, seq, hd, _ptr(inv_freq), inv_freq.shape[-1] * 2, int(position),
+                               _ptr(positions), _ptr(position_ids), _ptr(q_norm), _ptr(k_norm),
+                               dtype_code(nw) if nw is not None else F16, norm_eps, norm_constant_bias, rope_mode,
+                               attn_factor, _stream(qg, stream)))
+
+
 def rope_cs_table(bsz, seq_len, inv_freq, position, positions=None, position_ids=None, attn_factor=1.0, out=None,
                   stream=None):
     """{cos, sin} * attn_factor of every token's rotary frequencies (float32 [bsz * seq_len, R/2, 2]), as

@@ -383,6 +383,37 @@ void gumbel_noise(const Tensor& x, const Tensor& out, uint32_t random, const Str
     check_abi(exl3r_gumbel_noise(x.data, code(x.dtype), ldx, out.data, code(out.dtype), ldo, rows, cols, random, s.get()));
 }
 
+void rope_qg(const Tensor& qg, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
+             int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
+             float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s, const Tensor* position_ids)
+{
+    require(qg.dim() == 4 && out_q.dim() == 4, "rope_qg: qg and out_q must be (bsz, seq_len, heads, 2 * head_dim / head_dim)");
+    const int64_t bsz = qg.size(0), seq = qg.size(1), hq = qg.size(2), hd = qg.size(3) / 2;
+    require(qg.size(3) % 2 == 0 && qg.stride(3) == 1 && qg.stride(2) == 2 * hd, "rope_qg: qg must hold dense [q | g] heads");
+    require(bsz <= 1 || seq <= 1 || qg.stride(0) == seq * qg.stride(1), "rope_qg: qg batch stride must be seq_len * token stride");
+    require(out_q.is_contiguous() && out_q.size(0) == bsz && out_q.size(1) == seq && out_q.size(2) == hq && out_q.size(3) == hd,
+            "rope_qg: out_q must be a dense (bsz, seq_len, heads, head_dim)");
+    int64_t hk = 0, kts = 0, khs = 0;
+    if (k)
+    {
+        require(out_k && k->dim() == 4 && k->size(0) == bsz && k->size(1) == seq && k->size(3) == hd,
+                "rope_qg: k is incorrect shape");
+        require(k->stride(3) == 1 && out_k->strides == k->strides, "rope_qg: out_k must share k's layout");
+        hk = k->size(2);
+        kts = k->stride(1);
+        khs = k->stride(2);
+    }
+    require(inv_freq.dtype == DType::F32 && inv_freq.dim() == 1, "rope_qg: inv_freq must be float32 [R/2]");
+    require(!positions || positions->dtype == DType::I32, "rope_qg: positions must be int32");
+    require(!position_ids || position_ids->dtype == DType::I32, "rope_qg: position_ids must be int32");
+    const Tensor* nw = q_norm ? q_norm : k_norm;
+    check_abi(exl3r_rope_qg(qg.data, qg.stride(1), out_q.data, (int)hq, k ? k->data : nullptr, out_k ? out_k->data : nullptr,
+                            kts, khs, (int)hk, code(qg.dtype), bsz, seq, (int)hd, (const float*)inv_freq.data,
+                            (int)(inv_freq.size(0) * 2), (int32_t)position, (const int32_t*)ptr(positions),
+                            (const int32_t*)ptr(position_ids), ptr(q_norm), ptr(k_norm), code_or(nw, DType::F16), norm_eps,
+                            norm_constant_bias, (int)rope_mode, attn_factor, s.get()));
+}
+
 void rope_cs_table(int64_t bsz, int64_t seq_len, const Tensor& inv_freq, int64_t position, const Tensor* positions,
                    const Tensor* position_ids, float attn_factor, const Tensor& cs_table, const Stream& s)
 {

@@ -11,6 +11,7 @@
 //   exl3r::ffi::argmax_sample / gumbel_sample / gumbel_noise             <- src/ffi.rs:521-535, src/generator.rs:1596
 //   exl3r::ffi::had_r_128 / rms_norm_had / act_mul_had / rope_had        <- src/ffi.rs:606-607, src/modules.rs:224-231
 //   exl3r::ffi::rope_cs_table / rope_cs                                  <- rope() with the sin / cos hoisted per forward
+//   exl3r::ffi::rope_qg                                                  <- deinterleave_qg + rope, src/modules.rs:637-681
 //   exl3r::ffi::embedding                                                <- index_select, src/modules.rs:430-436
 //   exl3r::RmsNorm::forward / forward_res                                <- src/modules.rs:342-412
 //   exl3r::Embedding::forward                                            <- src/modules.rs:418-437
@@ -153,6 +154,13 @@ void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* o
           int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
           float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s,
           const Tensor* position_ids = nullptr, int32_t* err_flag = nullptr);
+// deinterleave_qg() then rope() on its q in one pass (gated attention, src/modules.rs:637-646 then 669-681):
+// qg (bsz, seq, heads, 2 * head_dim) holds each head's [q | g]; out_q (bsz, seq, heads, head_dim) dense gets
+// the roped q.  The gate stays in qg for mul_sigmoid_ with a row stride of 2 * head_dim.
+void rope_qg(const Tensor& qg, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
+             int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
+             float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Stream& s,
+             const Tensor* position_ids = nullptr);
 // {cos, sin} * attn_factor of every token's rotary frequencies into cs_table (float32 [bsz * seq, R/2, 2]),
 // as rope() evaluates them for the same positions: built once per forward pass for every layer's rope_cs()
 // (the reference evaluates them in each layer's kernel, kernels/rope.cu:69-85).

@@ -34,6 +34,8 @@
  *                              angles (src/rope.rs:225-260, 294-301)
  *   exl3r_rope_paged_kv     <- exl3_shim_rope followed by exl3_shim_paged_kv_cache_update
  *                              csrc/exl3_shim.cpp:87-98, 109-112 (ffi.rs:298-350; call sites modules.rs:666-704)
+ *   exl3r_rope_qg           <- exl3_shim_deinterleave_qg then exl3_shim_rope on q (gated attention,
+ *                              src/modules.rs:637-646 then 669-681)
  *   exl3r_gated_rms_norm    <- exl3_shim_gated_rms_norm   csrc/exl3_shim.cpp:143-147 (ffi.rs:118-124, 479-483)
  *   exl3r_mul_sigmoid       <- exl3_shim_mul_sigmoid_     csrc/exl3_shim.cpp:167     (ffi.rs:166, 616-618)
  *   exl3r_deinterleave_qg   <- exl3_shim_deinterleave_qg  csrc/exl3_shim.cpp:168-171 (ffi.rs:167, 622-624)
@@ -242,6 +244,23 @@ EXL3R_API int exl3r_rope_table(const void* q, void* out_q, int64_t q_tok_stride,
                      const void* q_norm, const void* k_norm, int norm_dtype,
                      float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
                      int32_t* err_flag, void* stream);
+
+/*
+ * exl3r_deinterleave_qg followed by exl3r_rope on its q, in one pass (gated attention's q projection,
+ * src/modules.rs:637-646, then RoPE::apply, src/modules.rs:669-681): head h of token (b, s) is read
+ * from the q half of the interleaved pair at qg + (b*seq_len + s)*qg_tok_stride + h*2*head_dim and
+ * written roped (and normed) to a dense out_q [bsz, seq_len, num_heads_q, head_dim].  Bit-identical to
+ * the two calls.  The gate is left in qg (g of head h at + h*2*head_dim + head_dim): with a dense qg
+ * (qg_tok_stride = num_heads_q*2*head_dim), exl3r_mul_sigmoid over rows = tokens*num_heads_q and
+ * cols = head_dim reads it with ldy = 2*head_dim, so the deinterleave copy disappears.  out_q must not
+ * overlap qg; every other argument as exl3r_rope.
+ */
+EXL3R_API int exl3r_rope_qg(const void* qg, int64_t qg_tok_stride, void* out_q, int num_heads_q, const void* k,
+                            void* out_k, int64_t k_tok_stride, int64_t k_head_stride, int num_heads_k, int dtype,
+                            int64_t bsz, int64_t seq_len, int head_dim, const float* inv_freq, int rotary_dim,
+                            int32_t position, const int32_t* positions, const int32_t* position_ids,
+                            const void* q_norm, const void* k_norm, int norm_dtype, float norm_eps,
+                            float norm_constant_bias, int rope_mode, float attn_factor, void* stream);
 
 /*
  * {cos, sin} * attn_factor of every token's rotary frequencies, for exl3r_rope_cs: the positions of a

@@ -415,6 +415,27 @@ int main()
         const bool ok = download(q, s) == download(q2, s) && download(k, s) == download(k2, s);
         report("ffi::rope_cs_table + rope_cs == rope", ok, ok ? "bitwise" : "DIFFER");
     }
+    // rope_qg: q read from the interleaved q | g projection, bitwise equal to deinterleave_qg + rope.
+    {
+        const int T = 1100, hq = 4, hk = 2, hd = 128;
+        auto qgh = host_normal(DType::F16, T * hq * 2 * hd, 0.f, 1.f), kh = host_normal(DType::F16, T * hk * hd, 0.f, 1.f);
+        auto nh = host_normal(DType::F16, hd, 0.f, 0.1f);
+        std::vector<float> fh(hd / 2);
+        for (int i = 0; i < hd / 2; ++i) fh[i] = (float)(1.0 / std::pow(1e6, 2.0 * i / hd));
+        std::vector<uint8_t> fb(fh.size() * 4);
+        std::memcpy(fb.data(), fh.data(), fb.size());
+        auto qg = upload(qgh, DType::F16, { 1, T, hq, 2 * hd }, s);
+        auto k = upload(kh, DType::F16, { 1, T, hk, hd }, s), k2 = upload(kh, DType::F16, { 1, T, hk, hd }, s);
+        auto qn = upload(nh, DType::F16, { hd }, s), f = upload(fb, DType::F32, { hd / 2 }, s);
+        auto oq = OwnedTensor::empty(DType::F16, { 1, T, hq, hd }), q = OwnedTensor::empty(DType::F16, { 1, T, hq, hd });
+        auto g = OwnedTensor::empty(DType::F16, { 1, T, hq * hd });
+        ffi::rope_qg(qg.t, oq.t, &k.t, &k.t, f.t, 9, nullptr, &qn.t, &qn.t, 1e-6f, 1.f, RopeStyle::NeoX, 1.f, s);
+        Tensor qgv(qg.t.data, DType::F16, { 1, T, hq * 2 * hd });
+        ffi::deinterleave_qg(qgv, q.t, g.t, hd, s);
+        ffi::rope(q.t, q.t, &k2.t, &k2.t, f.t, 9, nullptr, &qn.t, &qn.t, 1e-6f, 1.f, RopeStyle::NeoX, 1.f, s);
+        const bool ok = download(oq, s) == download(q, s) && download(k, s) == download(k2, s);
+        report("ffi::rope_qg == deinterleave_qg + rope", ok, ok ? "bitwise" : "DIFFER");
+    }
     // gated_rms_norm_had: the GDN output norm (8 tokens x 4 heads of 128, one o_proj row per token)
     // into o_proj's input rotation, bitwise equal to the gated norm followed by had_r_128.
     {

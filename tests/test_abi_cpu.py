@@ -218,6 +218,23 @@ def test_rope_table_validation():
     assert call(table=None) == exl3r.EINVAL and "angle table" in _err()
 
 
+def test_rope_qg_validation():
+    lib = exl3r.load()
+    def rope_qg(**kw):
+        # (qg, qg_ts, oq, hq, k, ok, k_ts, k_hs, hk, dtype, bsz, seq, hd, inv, R, pos, positions, ids, qn, kn, nwt, eps,
+        #  cb, mode, attn)
+        a = dict(qg=FAKE, qts=4 * 256, oq=FAKE + 65536, hq=4, k=None, ok=None, kts=0, khs=128, hk=0, dt=F16, bsz=1,
+                 seq=3, hd=128, inv=FAKE + 131072, R=128, pos=0, positions=None, ids=None, qn=None, kn=None, nwt=F16,
+                 eps=1e-6, cb=0.0, mode=exl3r.ROPE_NEOX, attn=1.0)
+        a.update(kw)
+        return lib.exl3r_rope_qg(*a.values(), None)
+    assert rope_qg(oq=FAKE + 1024) == exl3r.EINVAL and "overlaps" in _err()
+    assert rope_qg(dt=F32) == exl3r.EDTYPE
+    assert rope_qg(qts=4 * 256 - 8) == exl3r.EINVAL                  # token stride below heads * 2 * head_dim
+    assert rope_qg(hd=0) == exl3r.EINVAL
+    assert rope_qg(seq=0) == exl3r.OK
+
+
 def test_rope_cs_validation():
     lib = exl3r.load()
     # exl3r_rope_cs_table(bsz, seq, inv_freq, R, position, positions, position_ids, attn, cs_table)

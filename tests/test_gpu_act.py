@@ -68,6 +68,8 @@ def test_strided_odd_and_tail(act):
     run(act, 7, 1001, F16, F16, seed=22)                  # flat, 7007 % 8 != 0 -> vector body + tail
     run(act, 7, 1001, F16, F16, ld=1003, seed=23)         # strided odd rows -> generic kernel
     run(act, 1, 5, F16, F16, seed=24)                     # smaller than one chunk
+    run(act, 4099, 128, F16, F16, ld=256, seed=25)        # short strided rows: the flattened short-row kernel
+    run(act, 33, 512, BF16, F32, ld=520, limit=3.0, seed=26)   # 64 chunks per row, act_limit
 
 
 def test_in_place_and_specials():

@@ -74,6 +74,17 @@ def test_mul_sigmoid(it, zt):
     check(from_dev(z), exp, zt, f"mul_sigmoid in{it} z{zt}")
 
 
+def test_mul_sigmoid_gate_read_in_place_from_qg():
+    """The attention output gate read in place from an interleaved q | g projection (32 heads of 128 per
+    token: rows of 128 with a 256-element stride, the short-row kernel), o updated in place."""
+    qg = dev_normal((3000 * 32, 256), 0, 2, F16, 40)
+    o = dev_normal((3000 * 32, 128), 0, 1, F16, 41)
+    oh, gh = from_dev(o).copy(), np.ascontiguousarray(from_dev(qg)[:, 128:])
+    ffi.mul_sigmoid_(o, qg[:, 128:])
+    torch.cuda.synchronize()
+    check(from_dev(o), orc.mul_sigmoid(oh, gh, F16, F16, nthreads=NTHREADS), F16, "mul_sigmoid_ gate from qg")
+
+
 def test_mul_sigmoid_in_place_and_tail():
     x = dev_normal((3, 1001), 0, 2, F16, 33)
     y = dev_normal((3, 1001), 0, 3, F16, 34)
