@@ -37,6 +37,7 @@ OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "
        "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_unfused", "silu_had_c3",
        "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_unfused", "rope_cs_c4", "rope_cs_table_c4",
        "qg_rope_q35", "qg_rope_q35_unfused",
+       "rope_kv_prefill_cs", "rope_kv_had_prefill_cs", "prefill_layer_cs",
        "rope_kv_had_prefill", "rope_kv_had_prefill_unfused", "mlp_had_c3", "mlp_had_c3_unfused",
        "prefill_layer", "prefill_layer_unfused", "calib_copy",
        "calib_copy_cached"]
@@ -291,12 +292,14 @@ def make_gather(name, vocab, hidden, n, dt, out_dt, ids, seed, norm=False):
     return Work(name, nbytes, launch, desc, sets)
 
 
-def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64, had=False):
+def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64, had=False, cs=False):
     """q/k head-norm + NeoX RoPE followed by the paged KV-cache append (64 q / 8 kv heads of 128, f16,
     256-token pages, positions = cache lengths): one fused exl3r_rope_paged_kv launch, or exl3r_rope
     then a separate append kernel (the reference's two launches).  With had, q / k / v are the raw
     projection outputs and their output rotations had_r_128(y, y, None, svh) (src/modules.rs:231) come
-    first: one exl3r_rope_paged_kv_had launch, or three in-place rotations and the two launches."""
+    first: one exl3r_rope_paged_kv_had launch, or three in-place rotations and the two launches.  With cs,
+    the fused launch reads the forward pass's {cos, sin} table (exl3r_rope_cs_table, built once outside
+    the timed launches) in place of evaluating sin / cos; its bytes count the table rows."""
     import numpy as np
     import torch
     import exl3r
@@ -307,6 +310,8 @@ def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64, had=False):
     nbytes = 2 * T * hq * hd * 2 + 2 * T * hk * hd * 2 + T * hk * hd * 2 + 2 * T * hk * hd * 2 + 4 * bsz + 2 * hd * 2
     if had:
         nbytes += (hq + 2 * hk) * hd * 2
+    if cs:
+        nbytes += T * (hd // 2) * 8 - 4 * bsz
     sets = sets_for(nbytes)
     rng = np.random.default_rng(seed)
     pages = bsz * max_blocks + 4
@@ -320,18 +325,20 @@ def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64, had=False):
             for j in range(sets)]
     naive = exl3r.load_naive()
     sv = [torch.where(torch.rand(h * hd, device="cuda") < 0.5, -1.0, 1.0).to(torch.float16) for h in (hq, hk, hk)]
+    table = ffi.rope_cs_table(bsz, seq, inv, 0, sl) if cs else None
 
     def launch(i):
         q, k, v = bufs[i % sets]
         if had and fused:
             ffi.rope_paged_kv_had(q, q, k, k, v, inv, 0, sl, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, kc, vc, bt, sl,
-                                  q_post_scale=sv[0], k_post_scale=sv[1], v_post_scale=sv[2])
+                                  q_post_scale=sv[0], k_post_scale=sv[1], v_post_scale=sv[2], cs_table=table)
             return
         if had:
             for t, p in zip((q, k, v), sv):
                 ffi.had_r_128(t.view(T, -1), t.view(T, -1), None, p)
         if fused:
-            ffi.rope_paged_kv(q, q, k, k, v, inv, 0, sl, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, kc, vc, bt, sl)
+            ffi.rope_paged_kv(q, q, k, k, v, inv, 0, sl, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, kc, vc, bt, sl,
+                              cs_table=table)
         else:
             ffi.rope(q, q, k, k, inv, 0, sl, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0)
             rc = naive.naive_paged_kv_update_f16(k.data_ptr(), v.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(),
@@ -342,6 +349,8 @@ def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64, had=False):
     if had:
         kind = "fused (1 launch)" if fused else "3 in-place rotations + rope + separate append (5 launches)"
     head = "q/k/v output rotation + " if had else ""
+    if cs:
+        kind += ", {cos, sin} table"
     return Work(name, nbytes, launch, f"{head}q/k norm + RoPE + paged KV append bsz {bsz} x {seq} tokens, {kind}", sets)
 
 
@@ -535,7 +544,7 @@ def make_act_had(name, rows, cols, fused, seed=780, rotate=False):
     return Work(name, nbytes, launch, f"{head}SiLU(gate)*up -> Hadamard input [{rows},{cols}] f16, {kind}", sets)
 
 
-def make_prefill_layer(name, fused, T=4096, seed=900):
+def make_prefill_layer(name, fused, T=4096, seed=900, cs=False):
     """The row ops and Hadamard rotations of one Qwen3-32B prefill layer (hidden 5120, 64 / 8 heads of
     128, intermediate 25600, f16 activations, f32 residual, 256-token pages), GEMMs and attention
     excluded.  Unfused, in the reference's order (src/modules.rs:224-231, 372-411, 669-704, 932-940,
@@ -586,12 +595,14 @@ def make_prefill_layer(name, fused, T=4096, seed=900):
               + N * (2 + 4 + 4 + 2 * 2) + 4 * H * 2                                 # norm -> gate / up inputs
               + T * I * 6 + 3 * I * 2)                                              # MLP tail
 
+    table = ffi.rope_cs_table(1, T, inv, 0, sl) if cs else None
+
     def launch(i):
         if fused:
             ffi.rms_norm_had(y_down, w1, [xq, xk, xv], [suh_q, suh_k, suh_v], 1e-6, r=r, rotate_x=True,
                              x_post_scale=svh_d)
             ffi.rope_paged_kv_had(q, q, k, k, v, inv, 0, sl, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, kc, vc, bt, sl,
-                                  q_post_scale=svh_q, k_post_scale=svh_k, v_post_scale=svh_v)
+                                  q_post_scale=svh_q, k_post_scale=svh_k, v_post_scale=svh_v, cs_table=table)
             ffi.had_r_128(o, xo, suh_o)
             ffi.rms_norm_had(y_o, w2, [xg, xu], [suh_g, suh_u], 1e-6, r=r, rotate_x=True, x_post_scale=svh_o)
             ffi.act_mul_had("silu", g, u, xd, suh_d, rotate_x=True, rotate_y=True, x_post_scale=svh_g,
@@ -708,6 +719,9 @@ def make_all(only=None):
         "rope_cs_c4": lambda: make_rope_cs("rope_cs_c4", ragged, 64, 8, 128, 128, f16, 300, False),
         "rope_cs_table_c4": lambda: make_rope_cs("rope_cs_table_c4", ragged, 64, 8, 128, 128, f16, 300, True),
         "qg_rope_q35": lambda: make_qg_rope("qg_rope_q35", True),
+        "rope_kv_prefill_cs": lambda: make_rope_kv("rope_kv_prefill_cs", 1, 4096, True, cs=True),
+        "rope_kv_had_prefill_cs": lambda: make_rope_kv("rope_kv_had_prefill_cs", 1, 4096, True, had=True, cs=True),
+        "prefill_layer_cs": lambda: make_prefill_layer("prefill_layer_cs", True, cs=True),
         "qg_rope_q35_unfused": lambda: make_qg_rope("qg_rope_q35_unfused", False),
         "gather_c5": lambda: make_gather("gather_c5", 151936, 5120, 16384, bf16, bf16, zipf_ids(16384, 151936, 1), 400),
         "gather_norm_c5": lambda: make_gather("gather_norm_c5", 151936, 5120, 16384, bf16, bf16,
@@ -959,6 +973,12 @@ def main():
         r_us, c_us, t_us = ops["rope_c4"]["us"], ops["rope_cs_c4"]["us"], ops["rope_cs_table_c4"]["us"]
         rope_cs = {"rope_c4_us": r_us, "rope_cs_c4_us": c_us, "table_per_forward_us": t_us,
                    "per_layer_saving_us": round(r_us - c_us, 2),
+                   "paged_append_4096_us": {"evaluated": ops["rope_kv_prefill"]["us"],
+                                            "table": ops["rope_kv_prefill_cs"]["us"]},
+                   "qkv_rotate_paged_append_4096_us": {"evaluated": ops["rope_kv_had_prefill"]["us"],
+                                                       "table": ops["rope_kv_had_prefill_cs"]["us"]},
+                   "qwen3_32b_prefill_layer_T4096_us": {"evaluated": ops["prefill_layer"]["us"],
+                                                        "table": ops["prefill_layer_cs"]["us"]},
                    "desc": "C4 RoPE evaluating sin / cos in every layer vs reading a {cos, sin} table built once "
                            "per forward pass (bit-identical results); the table costs table_per_forward_us once"}
         log(f"rope_cs: {json.dumps(rope_cs)}")

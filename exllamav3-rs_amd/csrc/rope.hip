@@ -699,7 +699,15 @@ static void launch_rope_lph(RopeArgs a, int iters, hipStream_t s)
     const size_t lds = (size_t)a.tok_span * (a.R / 2) * sizeof(float2);
     if constexpr (SRC != SRC_FREQ)
     {
-        // Angle and {cos, sin} tables (never with a paged append): two heads per lane.
+        // Angle tables (never with a paged append) and {cos, sin} tables: two heads per lane.
+        if constexpr (SRC == SRC_CS)
+        {
+            if (a.kc)
+            {
+                k_rope<IO, MODE, LPH, 2, NORM, true, SRC><<<(unsigned)blocks, threads, lds, s>>>(a);
+                return;
+            }
+        }
         k_rope<IO, MODE, LPH, 2, NORM, false, SRC><<<(unsigned)blocks, threads, lds, s>>>(a);
         return;
     }
@@ -740,15 +748,8 @@ static void launch_rope_tok(RopeArgs a, hipStream_t s)
         constexpr int HP = decltype(H)::value;
         if constexpr (QOUT)
             k_rope_tok<IO, MODE, LPH, HP, NORM, false, false, SRC_FREQ, true><<<(unsigned)blocks, 256, lds, s>>>(a);
-        else if constexpr (SRC == SRC_CS)
-            k_rope_tok<IO, MODE, LPH, HP, NORM, false, false, SRC_CS><<<(unsigned)blocks, 256, lds, s>>>(a);
-        else if constexpr (HADR)
-        {
-            if (a.kc) k_rope_tok<IO, MODE, LPH, HP, NORM, true, true><<<(unsigned)blocks, 256, lds, s>>>(a);
-            else k_rope_tok<IO, MODE, LPH, HP, NORM, false, true><<<(unsigned)blocks, 256, lds, s>>>(a);
-        }
-        else if (a.kc) k_rope_tok<IO, MODE, LPH, HP, NORM, true><<<(unsigned)blocks, 256, lds, s>>>(a);
-        else k_rope_tok<IO, MODE, LPH, HP, NORM, false><<<(unsigned)blocks, 256, lds, s>>>(a);
+        else if (a.kc) k_rope_tok<IO, MODE, LPH, HP, NORM, true, HADR, SRC><<<(unsigned)blocks, 256, lds, s>>>(a);
+        else k_rope_tok<IO, MODE, LPH, HP, NORM, false, HADR, SRC><<<(unsigned)blocks, 256, lds, s>>>(a);
     };
     if (hpl == 2) go(std::integral_constant<int, 2>{});
     else go(std::integral_constant<int, 3>{});
@@ -766,8 +767,8 @@ static void launch_rope_vec(const RopeArgs& a, int lph, hipStream_t s)
     const Tuning& tu = tuning();
     if (a.cst)
     {
-        // exl3r_rope_cs (no append, no output rotation): the kernels of exl3r_rope, which copy the
-        // token's table row to LDS in place of evaluating it.
+        // A {cos, sin} table (exl3r_rope_cs, or the cs_table of the paged / rotating entries): the
+        // kernels of exl3r_rope, which copy the token's table row to LDS in place of evaluating it.
         if (MODE == EXL3R_ROPE_NEOX && rope_tok_launch(a))
         {
             if (lph == 8) launch_rope_tok<IO, MODE, 8, NORM, false, SRC_CS>(a, s);
@@ -967,6 +968,32 @@ extern "C" int exl3r_rope(const void* q, void* out_q, int64_t q_tok_stride, int6
     return rope_dispatch(op, a, dtype, rope_mode, stream);
 }
 
+// The optional {cos, sin} table of the paged and rotating entry points (built by exl3r_rope_cs_table for
+// the same positions): the kernels read it in place of evaluating sin / cos from inv_freq.
+static int use_cs_table(const char* op, RopeArgs& a, const void* cs_table)
+{
+    if (!cs_table) return EXL3R_OK;
+    if ((uintptr_t)cs_table % 8) return set_error(EXL3R_EINVAL, "%s: cs_table must be 8-byte aligned", op);
+    a.cst = (const float2*)cs_table;
+    a.inv_freq = nullptr;
+    return EXL3R_OK;
+}
+
+// The rotation source rope_prepare checks: inv_freq, or the cs_table standing in for it.
+static const float* rotation_source(const float* inv_freq, const void* cs_table)
+{
+    return inv_freq ? inv_freq : (const float*)cs_table;
+}
+
+// Launches the wave-per-token kernel with the output rotation, the rotary pairs evaluated or read
+// from the {cos, sin} table.
+template <int NORM>
+static void launch_had_tok(const RopeArgs& a, hipStream_t s)
+{
+    if (a.cst) launch_rope_tok<TF16, EXL3R_ROPE_NEOX, 16, NORM, true, SRC_CS>(a, s);
+    else launch_rope_tok<TF16, EXL3R_ROPE_NEOX, 16, NORM, true>(a, s);
+}
+
 // Argument checks and RopeArgs of the fused append, shared by exl3r_rope_paged_kv and
 // exl3r_rope_paged_kv_had.  Returns EXL3R_OK with a.tokens == 0 when there is nothing to launch.
 static int paged_prepare(const char* op, RopeArgs& a, const void* q, void* out_q, int64_t q_tok_stride,
@@ -1016,16 +1043,18 @@ extern "C" int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_str
                                    float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
                                    void* k_cache, void* v_cache, int page_size, int64_t num_pages,
                                    const int32_t* block_table, int64_t max_blocks_per_seq,
-                                   const int32_t* cache_seqlens, int32_t* err_flag, void* stream)
+                                   const int32_t* cache_seqlens, int32_t* err_flag, const void* cs_table,
+                                   void* stream)
 {
     const char* op = "exl3r_rope_paged_kv";
     RopeArgs a;
-    const int rc = paged_prepare(op, a, q, out_q, q_tok_stride, q_head_stride, num_heads_q, k, out_k, k_tok_stride,
-                                 k_head_stride, v, v_tok_stride, v_head_stride, num_heads_kv, dtype, bsz, seq_len,
-                                 head_dim, inv_freq, rotary_dim, position, positions, position_ids, q_norm, k_norm,
-                                 norm_dtype, norm_eps, norm_constant_bias, rope_mode, attn_factor, k_cache, v_cache,
-                                 page_size, num_pages, block_table, max_blocks_per_seq, cache_seqlens, err_flag);
+    int rc = paged_prepare(op, a, q, out_q, q_tok_stride, q_head_stride, num_heads_q, k, out_k, k_tok_stride,
+                           k_head_stride, v, v_tok_stride, v_head_stride, num_heads_kv, dtype, bsz, seq_len, head_dim,
+                           rotation_source(inv_freq, cs_table), rotary_dim, position, positions, position_ids, q_norm,
+                           k_norm, norm_dtype, norm_eps, norm_constant_bias, rope_mode, attn_factor, k_cache, v_cache,
+                           page_size, num_pages, block_table, max_blocks_per_seq, cache_seqlens, err_flag);
     if (rc || a.tokens == 0) return rc;
+    if ((rc = use_cs_table(op, a, cs_table))) return rc;
     return rope_dispatch(op, a, dtype, rope_mode, stream);
 }
 
@@ -1068,7 +1097,7 @@ extern "C" int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, 
                               int32_t position, const int32_t* positions, const int32_t* position_ids,
                               const void* q_norm, const void* k_norm, int norm_dtype,
                               float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
-                              const void* q_post_scale, const void* k_post_scale, void* stream)
+                              const void* q_post_scale, const void* k_post_scale, const void* cs_table, void* stream)
 {
     const char* op = "exl3r_rope_had";
     if (dtype != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: the rotated projection outputs are f16", op);
@@ -1077,9 +1106,11 @@ extern "C" int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, 
     if (!k && (out_k || k_post_scale)) return set_error(EXL3R_EINVAL, "%s: out_k / k_post_scale without k", op);
     RopeArgs a;
     int rc = rope_prepare(op, a, q, out_q, q_tok_stride, head_dim, num_heads_q, k, out_k, false, k_tok_stride, head_dim,
-                          num_heads_k, dtype, bsz, seq_len, head_dim, inv_freq, rotary_dim, position, positions,
-                          position_ids, q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias, rope_mode, attn_factor);
+                          num_heads_k, dtype, bsz, seq_len, head_dim, rotation_source(inv_freq, cs_table), rotary_dim,
+                          position, positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias,
+                          rope_mode, attn_factor);
     if (rc || a.tokens == 0) return rc;
+    if ((rc = use_cs_table(op, a, cs_table))) return rc;
     a.q_post = q_post_scale;
     a.k_post = k_post_scale;
     const bool fused = head_dim == 128 && rope_mode == EXL3R_ROPE_NEOX && rope_vec_ok(a, rope_mode) &&
@@ -1089,9 +1120,9 @@ extern "C" int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, 
     {
         hipStream_t s = (hipStream_t)stream;
         const int norm = rope_norm_kind(a, dtype);
-        if (norm == NORM_NONE) launch_rope_tok<TF16, EXL3R_ROPE_NEOX, 16, NORM_NONE, true>(a, s);
-        else if (norm == NORM_HALF) launch_rope_tok<TF16, EXL3R_ROPE_NEOX, 16, NORM_HALF, true>(a, s);
-        else launch_rope_tok<TF16, EXL3R_ROPE_NEOX, 16, NORM_F32, true>(a, s);
+        if (norm == NORM_NONE) launch_had_tok<NORM_NONE>(a, s);
+        else if (norm == NORM_HALF) launch_had_tok<NORM_HALF>(a, s);
+        else launch_had_tok<NORM_F32>(a, s);
         return launch_status(op);
     }
     const int64_t tokens = a.tokens;
@@ -1101,6 +1132,10 @@ extern "C" int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, 
         rc = exl3r_had_r_128(k, EXL3R_F16, k_tok_stride, out_k, k_tok_stride, tokens, (int64_t)num_heads_k * head_dim,
                              nullptr, k_post_scale, 1.0f, stream);
     if (rc != EXL3R_OK) return rc;
+    if (cs_table)
+        return exl3r_rope_cs(out_q, out_q, q_tok_stride, head_dim, num_heads_q, k ? out_k : nullptr, k ? out_k : nullptr,
+                             k_tok_stride, head_dim, num_heads_k, dtype, bsz, seq_len, head_dim, cs_table, rotary_dim,
+                             q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias, rope_mode, stream);
     return exl3r_rope(out_q, out_q, q_tok_stride, head_dim, num_heads_q, k ? out_k : nullptr, k ? out_k : nullptr,
                       k_tok_stride, head_dim, num_heads_k, dtype, bsz, seq_len, head_dim, inv_freq, rotary_dim, position,
                       positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias, rope_mode,
@@ -1123,7 +1158,7 @@ extern "C" int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok
                                        const int32_t* block_table, int64_t max_blocks_per_seq,
                                        const int32_t* cache_seqlens, int32_t* err_flag,
                                        const void* q_post_scale, const void* k_post_scale, const void* v_post_scale,
-                                       void* stream)
+                                       const void* cs_table, void* stream)
 {
     const char* op = "exl3r_rope_paged_kv_had";
     if (dtype != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: the rotated projection outputs are f16", op);
@@ -1131,11 +1166,12 @@ extern "C" int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok
         return set_error(EXL3R_EINVAL, "%s: heads * head_dim must be a multiple of 128", op);
     RopeArgs a;
     int rc = paged_prepare(op, a, q, out_q, q_tok_stride, head_dim, num_heads_q, k, out_k, k_tok_stride, head_dim, v,
-                           v_tok_stride, head_dim, num_heads_kv, dtype, bsz, seq_len, head_dim, inv_freq, rotary_dim,
-                           position, positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps, norm_constant_bias,
-                           rope_mode, attn_factor, k_cache, v_cache, page_size, num_pages, block_table,
-                           max_blocks_per_seq, cache_seqlens, err_flag);
+                           v_tok_stride, head_dim, num_heads_kv, dtype, bsz, seq_len, head_dim,
+                           rotation_source(inv_freq, cs_table), rotary_dim, position, positions, position_ids, q_norm,
+                           k_norm, norm_dtype, norm_eps, norm_constant_bias, rope_mode, attn_factor, k_cache, v_cache,
+                           page_size, num_pages, block_table, max_blocks_per_seq, cache_seqlens, err_flag);
     if (rc || a.tokens == 0) return rc;
+    if ((rc = use_cs_table(op, a, cs_table))) return rc;
     a.q_post = q_post_scale;
     a.k_post = k_post_scale;
     a.v_post = v_post_scale;
@@ -1146,9 +1182,9 @@ extern "C" int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok
     {
         hipStream_t s = (hipStream_t)stream;
         const int norm = rope_norm_kind(a, dtype);
-        if (norm == NORM_NONE) launch_rope_tok<TF16, EXL3R_ROPE_NEOX, 16, NORM_NONE, true>(a, s);
-        else if (norm == NORM_HALF) launch_rope_tok<TF16, EXL3R_ROPE_NEOX, 16, NORM_HALF, true>(a, s);
-        else launch_rope_tok<TF16, EXL3R_ROPE_NEOX, 16, NORM_F32, true>(a, s);
+        if (norm == NORM_NONE) launch_had_tok<NORM_NONE>(a, s);
+        else if (norm == NORM_HALF) launch_had_tok<NORM_HALF>(a, s);
+        else launch_had_tok<NORM_F32>(a, s);
         return launch_status(op);
     }
     const int64_t tokens = a.tokens;
@@ -1166,7 +1202,7 @@ extern "C" int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok
                                v_tok_stride, head_dim, num_heads_kv, dtype, bsz, seq_len, head_dim, inv_freq,
                                rotary_dim, position, positions, position_ids, q_norm, k_norm, norm_dtype, norm_eps,
                                norm_constant_bias, rope_mode, attn_factor, k_cache, v_cache, page_size, num_pages,
-                               block_table, max_blocks_per_seq, cache_seqlens, err_flag, stream);
+                               block_table, max_blocks_per_seq, cache_seqlens, err_flag, cs_table, stream);
 }
 
 // {cos, sin} * attn_factor of every token's rotary frequencies into cs_table [bsz * seq_len, R / 2]

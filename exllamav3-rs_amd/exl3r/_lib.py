@@ -31,7 +31,7 @@ PROTOTYPES = {
     "exl3r_rope": (_i, [_vp, _vp, _i64, _i64, _i, _vp, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _i,
                         _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _vp]),
     "exl3r_rope_had": (_i, [_vp, _vp, _i64, _i, _vp, _vp, _i64, _i, _i, _i64, _i64, _i, _vp, _i,
-                            _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _vp, _vp, _vp]),
+                            _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _vp, _vp, _vp, _vp]),
     "exl3r_rope_table": (_i, [_vp, _vp, _i64, _i64, _i, _vp, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _i64, _i64,
                               _i, _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _vp, _vp]),
     "exl3r_rope_qg": (_i, [_vp, _i64, _vp, _i, _vp, _vp, _i64, _i64, _i, _i, _i64, _i64, _i, _vp, _i, _i32, _vp, _vp, _vp,
@@ -55,10 +55,10 @@ PROTOTYPES = {
     "exl3r_gumbel_noise": (_i, [_vp, _i, _i64, _vp, _i, _i64, _i64, _i64, ctypes.c_uint32, _vp]),
     "exl3r_rope_paged_kv": (_i, [_vp, _vp, _i64, _i64, _i, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i, _i, _i64, _i64,
                                  _i, _vp, _i, _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _vp, _vp, _i, _i64,
-                                 _vp, _i64, _vp, _vp, _vp]),
+                                 _vp, _i64, _vp, _vp, _vp, _vp]),
     "exl3r_rope_paged_kv_had": (_i, [_vp, _vp, _i64, _i, _vp, _vp, _i64, _vp, _i64, _i, _i, _i64, _i64, _i, _vp, _i,
                                      _i32, _vp, _vp, _vp, _vp, _i, _f, _f, _i, _f, _vp, _vp, _i, _i64,
-                                     _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
+                                     _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "exl3r_embedding": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _i64, _vp, _vp]),
     "exl3r_embedding_rms_norm": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _i64, _vp, _i,
                                       _vp, _i, _i64, _f, _f, _f, _vp, _vp]),

@@ -225,6 +225,17 @@ def rope(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm
                             norm_eps, norm_constant_bias, rope_mode, attn_factor, _stream(q, stream)))
 
 
+def _rotary_dim(inv_freq, cs_table):
+    """rotary_dim from inv_freq [R/2], or from a {cos, sin} table [tokens, R/2, 2] when inv_freq is None."""
+    if cs_table is not None:
+        if cs_table.dtype != torch.float32 or not cs_table.is_contiguous() or cs_table.dim() != 3 or cs_table.shape[2] != 2:
+            raise ValueError("cs_table must be a contiguous float32 [bsz * seq_len, R/2, 2]")
+        if inv_freq is not None and inv_freq.shape[-1] != cs_table.shape[1]:
+            raise ValueError("cs_table and inv_freq disagree on rotary_dim")
+        return cs_table.shape[1] * 2
+    return inv_freq.shape[-1] * 2
+
+
 def rope_qg(qg, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias,
             rope_mode, attn_factor, position_ids=None, stream=None):
     """deinterleave_qg() then rope() on its q, in one pass (gated attention, src/modules.rs:637-646 then
@@ -309,7 +320,8 @@ def rope_cs(q, out_q, k, out_k, cs_table, q_norm, k_norm, norm_eps, norm_constan
 
 
 def rope_had(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias,
-             rope_mode, attn_factor, q_post_scale=None, k_post_scale=None, position_ids=None, stream=None):
+             rope_mode, attn_factor, q_post_scale=None, k_post_scale=None, position_ids=None, stream=None,
+             cs_table=None):
     """rope() on the raw f16 outputs of the q / k projections, each first given its projection's output
     rotation had_r_128(y, y, None, svh) (src/modules.rs:231).  q, k: (bsz, seq_len, heads, head_dim) with
     heads packed; q_post_scale / k_post_scale: f16 [heads * head_dim] or None."""
@@ -331,20 +343,21 @@ def rope_had(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, 
         hk, k_ts = k.shape[2], k.stride(1)
     nw = q_norm if q_norm is not None else k_norm
     check(load().exl3r_rope_had(_ptr(q), _ptr(out_q), q.stride(1), hq, _ptr(k), _ptr(out_k), k_ts, hk,
-                                dtype_code(q), bsz, seq, hd, _ptr(inv_freq), inv_freq.shape[-1] * 2,
+                                dtype_code(q), bsz, seq, hd, _ptr(inv_freq), _rotary_dim(inv_freq, cs_table),
                                 int(position), _ptr(positions), _ptr(position_ids),
                                 _ptr(q_norm), _ptr(k_norm), dtype_code(nw) if nw is not None else F16,
                                 norm_eps, norm_constant_bias, rope_mode, attn_factor, _ptr(q_post_scale),
-                                _ptr(k_post_scale), _stream(q, stream)))
+                                _ptr(k_post_scale), _ptr(cs_table), _stream(q, stream)))
 
 
 def rope_paged_kv(q, out_q, k, out_k, v, inv_freq, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias,
                   rope_mode, attn_factor, k_cache, v_cache, block_table, cache_seqlens, position_ids=None,
-                  err_flag=None, stream=None):
+                  err_flag=None, stream=None, cs_table=None):
     """rope() on q and k fused with the paged KV-cache append that follows it (paged_kv_cache_update):
     the roped k (also written to out_k unless it is None) and v go to k_cache / v_cache
     [pages, page_size, kv_heads, head_dim] at cache_seqlens[b] + s through block_table
-    (int32 [bsz, max_blocks])."""
+    (int32 [bsz, max_blocks]).  cs_table: a rope_cs_table() of the same positions, read in place of
+    evaluating sin / cos (inv_freq may then be None)."""
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q, k, v must be (bsz, seq_len, heads, head_dim)")
     bsz, seq, hq, hd = q.shape
@@ -372,19 +385,19 @@ def rope_paged_kv(q, out_q, k, out_k, v, inv_freq, position, positions, q_norm, 
     check(load().exl3r_rope_paged_kv(_ptr(q), _ptr(out_q), q.stride(1), q.stride(2), hq,
                                      _ptr(k), _ptr(out_k), k.stride(1), k.stride(2),
                                      _ptr(v), v.stride(1), v.stride(2), hk,
-                                     dtype_code(q), bsz, seq, hd, _ptr(inv_freq), inv_freq.shape[-1] * 2,
+                                     dtype_code(q), bsz, seq, hd, _ptr(inv_freq), _rotary_dim(inv_freq, cs_table),
                                      int(position), _ptr(positions), _ptr(position_ids),
                                      _ptr(q_norm), _ptr(k_norm), dtype_code(nw) if nw is not None else F16,
                                      norm_eps, norm_constant_bias, rope_mode, attn_factor,
                                      _ptr(k_cache), _ptr(v_cache), k_cache.shape[1], k_cache.shape[0],
                                      _ptr(block_table), block_table.shape[1], _ptr(cache_seqlens),
-                                     _ptr(err_flag), _stream(q, stream)))
+                                     _ptr(err_flag), _ptr(cs_table), _stream(q, stream)))
 
 
 def rope_paged_kv_had(q, out_q, k, out_k, v, inv_freq, position, positions, q_norm, k_norm, norm_eps,
                       norm_constant_bias, rope_mode, attn_factor, k_cache, v_cache, block_table, cache_seqlens,
                       q_post_scale=None, k_post_scale=None, v_post_scale=None, position_ids=None, err_flag=None,
-                      stream=None):
+                      stream=None, cs_table=None):
     """rope_paged_kv() on the raw f16 outputs of the q / k / v projections (heads packed), each first given
     its projection's output rotation had_r_128(y, y, None, svh) (src/modules.rs:231).  Outside the fused
     launch (NeoX, head_dim 128, >= 1024 tokens) v, and k when out_k is None, are rotated in place."""
@@ -407,13 +420,14 @@ def rope_paged_kv_had(q, out_q, k, out_k, v, inv_freq, position, positions, q_no
     nw = q_norm if q_norm is not None else k_norm
     check(load().exl3r_rope_paged_kv_had(_ptr(q), _ptr(out_q), q.stride(1), hq, _ptr(k), _ptr(out_k), k.stride(1),
                                          _ptr(v), v.stride(1), hk, dtype_code(q), bsz, seq, hd, _ptr(inv_freq),
-                                         inv_freq.shape[-1] * 2, int(position), _ptr(positions), _ptr(position_ids),
+                                         _rotary_dim(inv_freq, cs_table), int(position), _ptr(positions),
+                                         _ptr(position_ids),
                                          _ptr(q_norm), _ptr(k_norm), dtype_code(nw) if nw is not None else F16,
                                          norm_eps, norm_constant_bias, rope_mode, attn_factor,
                                          _ptr(k_cache), _ptr(v_cache), k_cache.shape[1], k_cache.shape[0],
                                          _ptr(block_table), block_table.shape[1], _ptr(cache_seqlens), _ptr(err_flag),
                                          _ptr(q_post_scale), _ptr(k_post_scale), _ptr(v_post_scale),
-                                         _stream(q, stream)))
+                                         _ptr(cs_table), _stream(q, stream)))
 
 
 def argmax_sample(logits, ids, max_logit=0, stream=None):

@@ -504,7 +504,7 @@ void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* o
 void rope_had(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
               int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
               float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Tensor* q_post_scale,
-              const Tensor* k_post_scale, const Stream& s, const Tensor* position_ids)
+              const Tensor* k_post_scale, const Stream& s, const Tensor* position_ids, const Tensor* cs_table)
 {
     require(q.dim() == 4 && q.dtype == DType::F16, "rope_had: q must be f16 (bsz, seq_len, heads, head_dim)");
     const int64_t bsz = q.size(0), seq = q.size(1), hd = q.size(3);
@@ -529,14 +529,14 @@ void rope_had(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tenso
                              (const float*)inv_freq.data, (int)(inv_freq.numel() * 2), (int32_t)position,
                              (const int32_t*)ptr(positions), (const int32_t*)ptr(position_ids), ptr(q_norm),
                              ptr(k_norm), code_or(nw, DType::F16), norm_eps, norm_constant_bias, (int)rope_mode,
-                             attn_factor, ptr(q_post_scale), ptr(k_post_scale), s.get()));
+                             attn_factor, ptr(q_post_scale), ptr(k_post_scale), ptr(cs_table), s.get()));
 }
 
 void rope_paged_kv(const Tensor& q, const Tensor& out_q, const Tensor& k, const Tensor* out_k, const Tensor& v,
                    const Tensor& inv_freq, int64_t position, const Tensor* positions, const Tensor* q_norm,
                    const Tensor* k_norm, float norm_eps, float norm_constant_bias, RopeStyle rope_mode, float attn_factor,
                    const Tensor& k_cache, const Tensor& v_cache, const Tensor& block_table, const Tensor& cache_seqlens,
-                   int32_t* err_flag, const Stream& s)
+                   int32_t* err_flag, const Stream& s, const Tensor* cs_table)
 {
     require(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "rope_paged_kv: q, k, v must be (bsz, seq_len, heads, head_dim)");
     require(q.stride(3) == 1 && out_q.strides == q.strides && out_q.shape == q.shape,
@@ -564,7 +564,7 @@ void rope_paged_kv(const Tensor& q, const Tensor& out_q, const Tensor& k, const 
                                   ptr(q_norm), ptr(k_norm), code_or(nw, DType::F16), norm_eps, norm_constant_bias,
                                   (int)rope_mode, attn_factor, k_cache.data, v_cache.data, (int)k_cache.size(1),
                                   k_cache.size(0), (const int32_t*)block_table.data, block_table.size(1),
-                                  (const int32_t*)cache_seqlens.data, err_flag, s.get()));
+                                  (const int32_t*)cache_seqlens.data, err_flag, ptr(cs_table), s.get()));
 }
 
 void rope_paged_kv_had(const Tensor& q, const Tensor& out_q, const Tensor& k, const Tensor* out_k, const Tensor& v,
@@ -572,7 +572,8 @@ void rope_paged_kv_had(const Tensor& q, const Tensor& out_q, const Tensor& k, co
                        const Tensor* k_norm, float norm_eps, float norm_constant_bias, RopeStyle rope_mode,
                        float attn_factor, const Tensor& k_cache, const Tensor& v_cache, const Tensor& block_table,
                        const Tensor& cache_seqlens, int32_t* err_flag, const Tensor* q_post_scale,
-                       const Tensor* k_post_scale, const Tensor* v_post_scale, const Stream& s)
+                       const Tensor* k_post_scale, const Tensor* v_post_scale, const Stream& s,
+                       const Tensor* cs_table)
 {
     require(q.dim() == 4 && k.dim() == 4 && v.dim() == 4 && q.dtype == DType::F16,
             "rope_paged_kv_had: q, k, v must be f16 (bsz, seq_len, heads, head_dim)");
@@ -600,7 +601,7 @@ void rope_paged_kv_had(const Tensor& q, const Tensor& out_q, const Tensor& k, co
                                       norm_constant_bias, (int)rope_mode, attn_factor, k_cache.data, v_cache.data,
                                       (int)k_cache.size(1), k_cache.size(0), (const int32_t*)block_table.data,
                                       block_table.size(1), (const int32_t*)cache_seqlens.data, err_flag,
-                                      ptr(q_post_scale), ptr(k_post_scale), ptr(v_post_scale), s.get()));
+                                      ptr(q_post_scale), ptr(k_post_scale), ptr(v_post_scale), ptr(cs_table), s.get()));
 }
 
 void embedding(const Tensor& table, const Tensor& ids, const Tensor& out, int32_t* err_flag, const Stream& s)

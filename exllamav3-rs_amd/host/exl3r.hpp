@@ -170,13 +170,16 @@ void rope_cs_table(int64_t bsz, int64_t seq_len, const Tensor& inv_freq, int64_t
 void rope_cs(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& cs_table,
              const Tensor* q_norm, const Tensor* k_norm, float norm_eps, float norm_constant_bias, RopeStyle rope_mode,
              const Stream& s);
+// rope_had, rope_paged_kv and rope_paged_kv_had take an optional cs_table (a rope_cs_table() of the same
+// positions) that the kernels read in place of evaluating sin / cos; the results are the same bits.
 // rope() on the raw f16 outputs of the q / k projections (heads packed), each first given its projection's
 // output rotation had_r_128(y, y, None, svh) (src/modules.rs:231); q_post_scale / k_post_scale are the
 // projections' f16 svh or null.
 void rope_had(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
               int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
               float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Tensor* q_post_scale,
-              const Tensor* k_post_scale, const Stream& s, const Tensor* position_ids = nullptr);
+              const Tensor* k_post_scale, const Stream& s, const Tensor* position_ids = nullptr,
+              const Tensor* cs_table = nullptr);
 // rope_paged_kv() on the raw f16 outputs of the q / k / v projections (heads packed), each first given its
 // projection's output rotation had_r_128(y, y, None, svh); outside the fused launch v (and k without out_k)
 // are rotated in place.
@@ -185,7 +188,8 @@ void rope_paged_kv_had(const Tensor& q, const Tensor& out_q, const Tensor& k, co
                        const Tensor* k_norm, float norm_eps, float norm_constant_bias, RopeStyle rope_mode,
                        float attn_factor, const Tensor& k_cache, const Tensor& v_cache, const Tensor& block_table,
                        const Tensor& cache_seqlens, int32_t* err_flag, const Tensor* q_post_scale,
-                       const Tensor* k_post_scale, const Tensor* v_post_scale, const Stream& s);
+                       const Tensor* k_post_scale, const Tensor* v_post_scale, const Stream& s,
+                       const Tensor* cs_table = nullptr);
 // rope() fused with the paged KV-cache append that follows it in paged attention (src/modules.rs:666-704,
 // ffi.rs:337-350): the roped k (also written to out_k when given) and v go to k_cache / v_cache
 // [pages, page_size, kv_heads, head_dim] at cache_seqlens[b] + s through block_table [bsz, max_blocks].
@@ -193,7 +197,7 @@ void rope_paged_kv(const Tensor& q, const Tensor& out_q, const Tensor& k, const 
                    const Tensor& inv_freq, int64_t position, const Tensor* positions, const Tensor* q_norm,
                    const Tensor* k_norm, float norm_eps, float norm_constant_bias, RopeStyle rope_mode, float attn_factor,
                    const Tensor& k_cache, const Tensor& v_cache, const Tensor& block_table, const Tensor& cache_seqlens,
-                   int32_t* err_flag, const Stream& s);
+                   int32_t* err_flag, const Stream& s, const Tensor* cs_table = nullptr);
 // src/ffi.rs:521-525 (and the generator's batched argmax, src/generator.rs:1596): ids[i] = first index of the
 // maximum of logits[i, :max_logit] (whole row when max_logit <= 0), NaN maximal; ids int64 [rows].
 void argmax_sample(const Tensor& logits, const Tensor& ids, int max_logit, const Stream& s);

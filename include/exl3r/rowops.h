@@ -296,6 +296,9 @@ EXL3R_API int exl3r_rope_cs(const void* q, void* out_q, int64_t q_tok_stride, in
  * only read when out_q / out_k differ from them.  Bit-identical to exl3r_had_r_128 on q and k
  * followed by exl3r_rope.  NeoX, head_dim 128, 16-byte aligned, 1024 or more tokens: one fused
  * launch; otherwise the rotations run into out_q / out_k and exl3r_rope in place there.
+ *   cs_table: NULL, or a {cos, sin} table that exl3r_rope_cs_table filled for the same positions,
+ *             inv_freq, rotary_dim and attn_factor; the rotary pairs are then read from it (inv_freq
+ *             may be NULL; the results are the same bits).
  */
 EXL3R_API int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, int num_heads_q,
                    const void* k, void* out_k, int64_t k_tok_stride, int num_heads_k,
@@ -304,7 +307,7 @@ EXL3R_API int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, i
                    int32_t position, const int32_t* positions, const int32_t* position_ids,
                    const void* q_norm, const void* k_norm, int norm_dtype,
                    float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
-                   const void* q_post_scale, const void* k_post_scale, void* stream);
+                   const void* q_post_scale, const void* k_post_scale, const void* cs_table, void* stream);
 
 /*
  * exl3r_rope_paged_kv preceded by the q / k / v projections' output rotation at prefill: each
@@ -315,6 +318,7 @@ EXL3R_API int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, i
  * exl3r_rope_paged_kv.  NeoX, head_dim 128, 16-byte aligned, 1024 or more tokens: one fused launch that
  * writes only out_q, out_k (if given) and the caches.  Otherwise the rotations run first -- q into
  * out_q, k into out_k (into k itself when out_k is NULL) and v in place -- then exl3r_rope_paged_kv.
+ * cs_table: as exl3r_rope_had.
  */
 EXL3R_API int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok_stride, int num_heads_q,
                             const void* k, void* out_k, int64_t k_tok_stride, const void* v,
@@ -327,7 +331,7 @@ EXL3R_API int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok_
                             const int32_t* block_table, int64_t max_blocks_per_seq,
                             const int32_t* cache_seqlens, int32_t* err_flag,
                             const void* q_post_scale, const void* k_post_scale, const void* v_post_scale,
-                            void* stream);
+                            const void* cs_table, void* stream);
 
 /*
  * exl3r_rope fused with the paged KV-cache append that follows it in paged attention
@@ -346,6 +350,9 @@ EXL3R_API int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok_
  *         reference does not check).  k heads are still written to out_k.
  * The rotary position arguments are independent of cache_seqlens (the paged path passes the same
  * per-sequence lengths to both: positions = cache_seqlens).
+ *   cs_table: NULL, or a {cos, sin} table that exl3r_rope_cs_table filled for the same positions,
+ *         inv_freq, rotary_dim and attn_factor: the rotary pairs are read from it (inv_freq may be
+ *         NULL), bit-identical to evaluating them.  One table serves every layer of a forward pass.
  */
 EXL3R_API int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_stride, int64_t q_head_stride, int num_heads_q,
                         const void* k, void* out_k, int64_t k_tok_stride, int64_t k_head_stride,
@@ -357,7 +364,7 @@ EXL3R_API int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_stri
                         float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
                         void* k_cache, void* v_cache, int page_size, int64_t num_pages,
                         const int32_t* block_table, int64_t max_blocks_per_seq, const int32_t* cache_seqlens,
-                        int32_t* err_flag, void* stream);
+                        int32_t* err_flag, const void* cs_table, void* stream);
 
 /*
  * Row argmax of logits [rows, vocab] (row stride ld elements; F16/BF16/F32) into int64 ids[rows]:

@@ -152,7 +152,7 @@ def test_rope_paged_kv_validation():
                  positions=None, ids=None, qn=None, kn=None, nwt=F16, eps=1e-6, cb=0.0, mode=exl3r.ROPE_NEOX, attn=1.0,
                  kc=kc, vc=vc, page=256, pages=4, bt=bt, mb=2, sl=sl, err=None)
         a.update(kw)
-        return lib.exl3r_rope_paged_kv(*a.values(), None)
+        return lib.exl3r_rope_paged_kv(*a.values(), None, None)
     assert call(page=100) == exl3r.EINVAL
     assert call(pages=0) == exl3r.EINVAL
     assert call(v=None) == exl3r.EINVAL
@@ -316,7 +316,7 @@ def test_rope_had_validation():
                  inv=FAKE + 65536, R=128, pos=0, positions=None, ids=None, qn=None, kn=None, nwt=F16, eps=1e-6, cb=0.0,
                  mode=exl3r.ROPE_NEOX, attn=1.0, qp=None, kp=None)
         a.update(kw)
-        return lib.exl3r_rope_had(*a.values(), None)
+        return lib.exl3r_rope_had(*a.values(), None, None)
     assert rope_had(dt=BF16) == exl3r.EDTYPE
     assert rope_had(hq=3, hd=64, R=64, qts=3 * 64) == exl3r.EINVAL and "multiple of 128" in _err()
     assert rope_had(kp=FAKE) == exl3r.EINVAL
@@ -330,7 +330,7 @@ def test_rope_had_validation():
                  kc=FAKE + 262144, vc=FAKE + 393216, page=256, pages=4, bt=FAKE + 524288, mb=2, sl=FAKE + 528384,
                  err=None, qp=None, kp=None, vp=None)
         a.update(kw)
-        return lib.exl3r_rope_paged_kv_had(*a.values(), None)
+        return lib.exl3r_rope_paged_kv_had(*a.values(), None, None)
     assert paged_had(dt=BF16) == exl3r.EDTYPE
     assert paged_had(page=100) == exl3r.EINVAL
     assert paged_had(v=None) == exl3r.EINVAL

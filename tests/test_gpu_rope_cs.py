@@ -121,3 +121,79 @@ def test_zero_tokens_and_errors():
         q64 = dev_normal((1, 4, 4, 64), 0, 1, F16, 12)
         ffi.rope_cs(q64, q64, None, None, cs, None, None, 1e-6, 0.0, exl3r.ROPE_NEOX)
     torch.cuda.synchronize()
+
+
+def paged_case(bsz, seq, hq, hk, page, max_blocks, had, tune_use=0, seed=0):
+    """exl3r_rope_paged_kv / exl3r_rope_paged_kv_had with a {cos, sin} table against the same call evaluating
+    sin / cos: q, out_k, both whole caches and the error flag bitwise."""
+    import exl3r._lib as L
+    from test_gpu_rope_paged import layout
+    from test_gpu_rope_had import svh
+    hd = 128
+    pages, bt, sl = layout(bsz, seq, page, max_blocks, seed)
+    q = dev_normal((bsz, seq, hq, hd), 0, 2, F16, seed)
+    k = dev_normal((bsz, seq, hk, hd), 0, 2, F16, seed + 1)
+    v = dev_normal((bsz, seq, hk, hd), 0, 2, F16, seed + 2)
+    kc = dev_normal((pages, page, hk, hd), 0, 1, F16, seed + 3)
+    vc = dev_normal((pages, page, hk, hd), 0, 1, F16, seed + 4)
+    qn = dev_normal((hd,), 1, 0.1, F16, seed + 5)
+    kn = dev_normal((hd,), 1, 0.1, F16, seed + 6)
+    f = torch.from_numpy(inv_freq(hd)).cuda()
+    sld = torch.from_numpy(sl.astype(np.int32)).cuda()
+    btd = torch.from_numpy(bt.astype(np.int32)).cuda()
+    cs = ffi.rope_cs_table(bsz, seq, f, 0, sld)
+    posts = dict(q_post_scale=svh(hq * hd, seed + 7), k_post_scale=svh(hk * hd, seed + 8),
+                 v_post_scale=svh(hk * hd, seed + 9)) if had else {}
+    outs = []
+    lib = L.load()
+    lib.exl3r_tune_rope_tok(tune_use, 0, 0)
+    try:
+        for table in (None, cs):
+            oq, ok, vv, kcc, vcc = torch.empty_like(q), torch.empty_like(k), v.clone(), kc.clone(), vc.clone()
+            err = torch.zeros(1, dtype=torch.int32, device="cuda")
+            fn = ffi.rope_paged_kv_had if had else ffi.rope_paged_kv
+            fn(q, oq, k.clone(), ok, vv, f if table is None else None, 0, sld, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0,
+               kcc, vcc, btd, sld, err_flag=err, cs_table=table, **posts)
+            outs.append((oq, ok, kcc, vcc, err))
+        torch.cuda.synchronize()
+    finally:
+        lib.exl3r_tune_rope_tok(0, 0, 0)
+    tag = f"paged{'_had' if had else ''} cs b{bsz} s{seq} h{hq}/{hk} use{tune_use}"
+    for a, b, what in zip(outs[0], outs[1], ("q", "out_k", "k_cache", "v_cache", "err")):
+        assert same(a, b) if a.dtype == torch.float16 else torch.equal(a, b), tag + " " + what
+
+
+@pytest.mark.parametrize("had", [False, True])
+@pytest.mark.parametrize("use", [0, 1])
+def test_paged_append_with_table(had, use):
+    """The wave-per-token kernel (prefill, 2 x 1100 tokens crossing 256-token pages; with the output rotation
+    of q / k / v when `had`), and with use=1 the flattened kernel / the rotations followed by the paged RoPE."""
+    paged_case(2, 1100, 16, 4, 256, 6, had, tune_use=use, seed=21 + had + 2 * use)
+
+
+def test_paged_append_with_table_decode():
+    paged_case(16, 1, 32, 8, 16, 64, False, seed=25)
+
+
+@pytest.mark.parametrize("tok", [True, False])
+def test_rope_had_with_table(tok):
+    """exl3r_rope_had with a {cos, sin} table against the same call evaluating sin / cos: the fused launch
+    (1100 tokens) and the fallback (the rotations, then exl3r_rope_cs)."""
+    from test_gpu_rope_had import svh
+    bsz, seq, hq, hk, hd = (1, 1100, 16, 4, 128) if tok else (8, 1, 16, 4, 128)
+    q = dev_normal((bsz, seq, hq, hd), 0, 2, F16, 30)
+    k = dev_normal((bsz, seq, hk, hd), 0, 2, F16, 31)
+    qn = dev_normal((hd,), 1, 0.1, BF16, 32)
+    kn = dev_normal((hd,), 1, 0.1, BF16, 33)
+    qs, ks = svh(hq * hd, 34), svh(hk * hd, 35)
+    f = torch.from_numpy(inv_freq(hd)).cuda()
+    pos = torch.from_numpy(np.arange(bsz, dtype=np.int32) * 977 + 5).cuda()
+    cs = ffi.rope_cs_table(bsz, seq, f, 0, pos)
+    res = []
+    for table in (None, cs):
+        oq, ok = torch.empty_like(q), torch.empty_like(k)
+        ffi.rope_had(q, oq, k, ok, f, 0, pos, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, q_post_scale=qs, k_post_scale=ks,
+                     cs_table=table)
+        res.append((oq, ok))
+    torch.cuda.synchronize()
+    assert same(res[0][0], res[1][0]) and same(res[0][1], res[1][1]), f"rope_had cs tok={tok}"
