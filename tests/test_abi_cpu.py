@@ -151,8 +151,9 @@ def test_rope_paged_kv_validation():
                  v=FAKE + 98304, vts=2 * 64, vhs=64, hkv=2, dt=F16, bsz=1, seq=3, hd=64, inv=inv, R=64, pos=0,
                  positions=None, ids=None, qn=None, kn=None, nwt=F16, eps=1e-6, cb=0.0, mode=exl3r.ROPE_NEOX, attn=1.0,
                  kc=kc, vc=vc, page=256, pages=4, bt=bt, mb=2, sl=sl, err=None)
+        cs = kw.pop("cs", None)
         a.update(kw)
-        return lib.exl3r_rope_paged_kv(*a.values(), None, None)
+        return lib.exl3r_rope_paged_kv(*a.values(), cs, None)
     assert call(page=100) == exl3r.EINVAL
     assert call(pages=0) == exl3r.EINVAL
     assert call(v=None) == exl3r.EINVAL
@@ -161,6 +162,8 @@ def test_rope_paged_kv_validation():
     assert call(vhs=32) == exl3r.EINVAL
     assert call(dt=F32) == exl3r.EDTYPE
     assert call(hkv=0) == exl3r.EINVAL
+    assert call(cs=FAKE + 65540) == exl3r.EINVAL and "cs_table" in _err()    # misaligned {cos, sin} table
+    assert call(inv=None) == exl3r.EINVAL                                      # no rotation source
     assert call(q=None, oq=None, k=None, v=None, kc=None, vc=None, bt=None, sl=None, seq=0) == exl3r.OK
 
 
@@ -315,11 +318,13 @@ def test_rope_had_validation():
         a = dict(q=FAKE, oq=FAKE, qts=4 * 128, hq=4, k=None, ok=None, kts=0, hk=0, dt=F16, bsz=1, seq=3, hd=128,
                  inv=FAKE + 65536, R=128, pos=0, positions=None, ids=None, qn=None, kn=None, nwt=F16, eps=1e-6, cb=0.0,
                  mode=exl3r.ROPE_NEOX, attn=1.0, qp=None, kp=None)
+        cs = kw.pop("cs", None)
         a.update(kw)
-        return lib.exl3r_rope_had(*a.values(), None, None)
+        return lib.exl3r_rope_had(*a.values(), cs, None)
     assert rope_had(dt=BF16) == exl3r.EDTYPE
     assert rope_had(hq=3, hd=64, R=64, qts=3 * 64) == exl3r.EINVAL and "multiple of 128" in _err()
     assert rope_had(kp=FAKE) == exl3r.EINVAL
+    assert rope_had(inv=None, cs=FAKE + 65540) == exl3r.EINVAL and "cs_table" in _err()
     assert rope_had(inv=None) == exl3r.EINVAL
     assert rope_had(seq=0) == exl3r.OK
 
@@ -329,10 +334,12 @@ def test_rope_had_validation():
                  ids=None, qn=None, kn=None, nwt=F16, eps=1e-6, cb=0.0, mode=exl3r.ROPE_NEOX, attn=1.0,
                  kc=FAKE + 262144, vc=FAKE + 393216, page=256, pages=4, bt=FAKE + 524288, mb=2, sl=FAKE + 528384,
                  err=None, qp=None, kp=None, vp=None)
+        cs = kw.pop("cs", None)
         a.update(kw)
-        return lib.exl3r_rope_paged_kv_had(*a.values(), None, None)
+        return lib.exl3r_rope_paged_kv_had(*a.values(), cs, None)
     assert paged_had(dt=BF16) == exl3r.EDTYPE
     assert paged_had(page=100) == exl3r.EINVAL
+    assert paged_had(cs=FAKE + 65540) == exl3r.EINVAL and "cs_table" in _err()
     assert paged_had(v=None) == exl3r.EINVAL
     assert paged_had(hkv=0) == exl3r.EINVAL
     assert paged_had(seq=0, q=None, oq=None, k=None, v=None, kc=None, vc=None, bt=None, sl=None) == exl3r.OK
