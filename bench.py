@@ -30,7 +30,7 @@ sys.path.insert(0, os.path.join(ROOT, "exllamav3-rs_amd"))
 
 PEAK_GBS = 8000.0            # MI355X HBM3E
 METRIC = "fused norm/act/RoPE/embed HBM GB/s + % of MI355X peak; decode-step us"
-OPS = ["rms_c3", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "gather_norm_c5", "rms_c1",
+OPS = ["rms_c3", "rms_q3mix", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "gather_norm_c5", "rms_c1",
        "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "rope_kv_prefill",
        "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
        "deinterleave_q35", "gated_norm_had_q35", "gated_norm_had_q35_unfused", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
@@ -101,16 +101,21 @@ def ragged_positions(seed):
     return np.concatenate([s + np.arange(n) for s, n in zip(starts, lens)]).astype(np.int32)
 
 
-def make_rms(name, rows, dim, dt, res, seed):
+def make_rms(name, rows, dim, dt, res, seed, rdt=None):
+    """RMSNorm, or with `res` the residual norm (r += x in place, y = norm(r)); x, y and the weight are
+    `dt`, the residual `rdt` (default `dt`; float32 is the reference's Qwen3 residual stream,
+    kernels/norm.cu:403)."""
     import torch
     import exl3r.ffi as ffi
     es = 2
-    nbytes = (4 if res else 2) * rows * dim * es + dim * es
+    rdt = rdt or dt
+    res_es = torch.empty((), dtype=rdt).element_size()
+    nbytes = (rows * dim * (2 * es + 2 * res_es) if res else 2 * rows * dim * es) + dim * es
     sets = sets_for(nbytes)
     bufs = []
     for k in range(sets):
         x = gen((rows, dim), 0.0, 1.0, dt, seed + 3 * k)
-        r = gen((rows, dim), 0.0, 4.0, dt, seed + 3 * k + 1) if res else None
+        r = gen((rows, dim), 0.0, 4.0, rdt, seed + 3 * k + 1) if res else None
         bufs.append((x, r, torch.empty_like(x)))
     w = gen((dim,), 1.0, 0.1, dt, seed + 99)
 
@@ -121,7 +126,8 @@ def make_rms(name, rows, dim, dt, res, seed):
         else:
             ffi.rms_norm(x, w, y, 1e-6)
     kind = "residual RMSNorm" if res else "RMSNorm"
-    return Work(name, nbytes, launch, f"{kind} [{rows},{dim}] {str(dt).split('.')[-1]}", sets)
+    dts = str(dt).split('.')[-1] + (f" x / {str(rdt).split('.')[-1]} residual" if res and rdt != dt else "")
+    return Work(name, nbytes, launch, f"{kind} [{rows},{dim}] {dts}", sets)
 
 
 def make_act(name, rows, cols, dt, act, seed):
@@ -712,6 +718,7 @@ def make_all(only=None):
     ragged = ragged_positions(0)
     builders = {
         "rms_c3": lambda: make_rms("rms_c3", 8192, 5120, bf16, True, 100),
+        "rms_q3mix": lambda: make_rms("rms_q3mix", 8192, 5120, f16, True, 110, rdt=torch.float32),
         "silu_c3": lambda: make_act("silu_c3", 8192, 17408, bf16, "silu", 200),
         "gelu_c3": lambda: make_act("gelu_c3", 8192, 17408, bf16, "gelu", 200),
         "rope_c4": lambda: make_rope("rope_c4", ragged, 64, 8, 128, 128, "neox", f16, 300),

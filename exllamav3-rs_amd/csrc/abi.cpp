@@ -1,6 +1,9 @@
-// Thread-local error reporting and the version/tuning entry points of the C ABI.
+// Thread-local error reporting and the version entry point of the C ABI; with EXL3R_TUNING (the
+// sweep/test build only) also the launch-shape overrides of csrc/tuning.h.
 #include "abi.hpp"
+#ifdef EXL3R_TUNING
 #include "tuning.h"
+#endif
 
 #include <cstdarg>
 #include <cstdio>
@@ -38,11 +41,13 @@ const char* dtype_name(int dt)
     }
 }
 
+#ifdef EXL3R_TUNING
 Tuning& tuning()
 {
     static Tuning t;
     return t;
 }
+#endif
 
 int device_cus()
 {
@@ -64,6 +69,7 @@ extern "C" int exl3r_version(void) { return 10000; }
 
 extern "C" const char* exl3r_last_error(void) { return exl3r::g_last_error; }
 
+#ifdef EXL3R_TUNING
 extern "C" void exl3r_tune_rms(int maxv, int threads)
 {
     exl3r::tuning().rms_maxv = maxv;
@@ -96,3 +102,4 @@ extern "C" void exl3r_tune_sample(int rows_min, int threads)
 extern "C" void exl3r_tune_had(int blocks_per_group) { exl3r::tuning().had_unroll = blocks_per_group; }
 
 extern "C" void exl3r_tune_embed(int threads) { exl3r::tuning().embed_threads = threads; }
+#endif  // EXL3R_TUNING

@@ -15,6 +15,12 @@ int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3
 // Status of the kernel launch just issued (hipGetLastError); sets the message on failure.
 int launch_status(const char* op);
 
+// Discards an error left on this thread by an earlier, unrelated HIP call (hipGetLastError keeps the
+// last failure until it is read), so that launch_status reports this entry point's own launches only.
+// Every entry point calls it before validating its arguments; device faults, which are sticky, are
+// still reported by the launch itself.
+inline void clear_stale_error() { (void)hipGetLastError(); }
+
 inline bool is_float_dtype(int dt) { return dt == EXL3R_F32 || dt == EXL3R_F16 || dt == EXL3R_BF16; }
 inline int dtype_bytes(int dt)
 {
@@ -32,7 +38,10 @@ const char* dtype_name(int dt);
 // Grid rows are walked with a stride loop beyond this many workgroups.
 constexpr int64_t kMaxGridX = 1 << 20;
 
-// Tuning overrides (0 = automatic); set only by exl3r_tune_* for sweeps.
+// Launch-shape overrides (0 = automatic).  The product library is built without EXL3R_TUNING: every
+// field is then a compile-time zero and the shape rules below are fixed.  The sweep/test build
+// (lib/libexl3rowops_tune.so, EXL3R_TUNING defined) exports exl3r_tune_* (csrc/tuning.h), which set
+// them process-wide.
 struct Tuning
 {
     int rms_maxv = 0, rms_threads = 0;
@@ -47,7 +56,15 @@ struct Tuning
     int had_unroll = 0;      // Hadamard: 128-blocks per 16-lane group (1, 2, 4; 0: 1)
     int embed_threads = 0;
 };
+#ifdef EXL3R_TUNING
 Tuning& tuning();
+#else
+inline const Tuning& tuning()
+{
+    static constexpr Tuning t{};
+    return t;
+}
+#endif
 
 // Compute units of the current device (cached after the first call).
 int device_cus();

@@ -255,6 +255,7 @@ static int act_had_entry(const char* op, const void* x, const void* y, int it, i
                          int64_t rows, int64_t cols, float limit, float had_scale, int rotate_in,
                          const void* x_post, const void* y_post, void* stream)
 {
+    clear_stale_error();
     if (!is_float_dtype(it)) return set_error(EXL3R_EDTYPE, "%s: unsupported input dtype %s", op, dtype_name(it));
     if (rotate_in & ~3) return set_error(EXL3R_EINVAL, "%s: rotate_in takes bits 0 (x) and 1 (y)", op);
     if (rotate_in && it != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: rotated inputs are f16", op);
@@ -356,6 +357,7 @@ extern "C" int exl3r_silu_mul(const void* x, const void* y, int in_dtype, void* 
                               int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz,
                               float act_limit, void* stream)
 {
+    clear_stale_error();
     return act_mul_entry<ACT_SILU>("exl3r_silu_mul", x, y, in_dtype, z, z_dtype, rows, cols, ldx, ldy, ldz, act_limit, stream);
 }
 
@@ -363,6 +365,7 @@ extern "C" int exl3r_gelu_mul(const void* x, const void* y, int in_dtype, void* 
                               int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz,
                               float act_limit, void* stream)
 {
+    clear_stale_error();
     return act_mul_entry<ACT_GELU>("exl3r_gelu_mul", x, y, in_dtype, z, z_dtype, rows, cols, ldx, ldy, ldz, act_limit, stream);
 }
 
@@ -371,6 +374,7 @@ extern "C" int exl3r_act_mul_had(int act, const void* x, const void* y, int in_d
                                  int64_t rows, int64_t cols, float act_limit, float had_scale, int rotate_in,
                                  const void* x_post_scale, const void* y_post_scale, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_act_mul_had";
     switch (act)
     {
@@ -396,6 +400,7 @@ extern "C" int exl3r_act_mul_had(int act, const void* x, const void* y, int in_d
 extern "C" int exl3r_mul_sigmoid(const void* x, const void* y, int in_dtype, void* z, int z_dtype,
                                  int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz, void* stream)
 {
+    clear_stale_error();
     return act_mul_entry<ACT_SIGMOID>("exl3r_mul_sigmoid", y, x, in_dtype, z, z_dtype, rows, cols, ldy, ldx, ldz, 0.0f,
                                       stream);
 }

@@ -353,6 +353,20 @@ __device__ __forceinline__ double block_sum64(double v, double* lds16)
     return t;
 }
 
+// fp64 workgroup sum with a single barrier, for a workgroup that reduces once: its LDS slots are
+// never written again, so no second barrier is needed before the kernel ends.
+__device__ __forceinline__ double block_sum64_once(double v, double* lds16)
+{
+    v = group_sum64<64>(v);
+    const int nw = blockDim.x >> 6;
+    if (nw == 1) return v;
+    if ((threadIdx.x & 63) == 0) lds16[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int i = 0; i < nw; ++i) t += lds16[i];
+    return t;
+}
+
 // ---------------------------------------------------------------------------------------------
 // Host-side runtime dtype -> tag dispatch.
 

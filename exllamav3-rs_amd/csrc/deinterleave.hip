@@ -72,6 +72,7 @@ using namespace exl3r;
 extern "C" int exl3r_deinterleave_qg(const void* qg, int64_t ld_qg, void* q, int64_t ld_q, void* g, int64_t ld_g,
                                      int dtype, int64_t rows, int heads, int head_dim, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_deinterleave_qg";
     if (!is_float_dtype(dtype)) return set_error(EXL3R_EDTYPE, "%s: unsupported dtype %s", op, dtype_name(dtype));
     if (rows < 0 || heads <= 0 || head_dim <= 0 || (int64_t)heads * head_dim > ((int64_t)1 << 28))

@@ -117,6 +117,7 @@ extern "C" int exl3r_embedding(const void* table, int tt, int64_t vocab, int64_t
                                const void* ids, int idt, int64_t n, void* out, int ot, int64_t ldo,
                                int32_t* err_flag, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_embedding";
     int rc = check_gather(op, table, tt, vocab, hidden, ldt, ids, idt, n);
     if (rc) return rc;
@@ -159,6 +160,7 @@ extern "C" int exl3r_embedding_rms_norm(const void* table, int tt, int64_t vocab
                                         float eps, float constant_bias, float constant_scale,
                                         int32_t* err_flag, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_embedding_rms_norm";
     int rc = check_gather(op, table, tt, vocab, hidden, ldt, ids, idt, n);
     if (rc) return rc;
@@ -175,7 +177,7 @@ extern "C" int exl3r_embedding_rms_norm(const void* table, int tt, int64_t vocab
     a.rows = n; a.dim = (int)hidden; a.eps = eps; a.cb = constant_bias; a.cs = constant_scale;
     hipStream_t s = (hipStream_t)stream;
 
-    if (rms_vec_ok(a, tt, yt, h ? ht : tt, h != nullptr))
+    if (rms_vec_ok(a, tt, yt, h ? ht : tt, h != nullptr, RMS_GATHER, 0))
     {
         with_float_type(tt, [&](auto T) {
             with_float_type(yt, [&](auto Y) {

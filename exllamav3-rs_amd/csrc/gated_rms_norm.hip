@@ -14,6 +14,7 @@ extern "C" int exl3r_gated_rms_norm(const void* x, int xt, int64_t ldx, const vo
                                     int64_t rows, int64_t dim, float eps, float constant_bias,
                                     int gate_first, int gate_act, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_gated_rms_norm";
     int rc = check_rms_common(op, x, xt, ldx, w, wt, y, yt, ldy, rows, dim);
     if (rc) return rc;
@@ -34,7 +35,7 @@ extern "C" int exl3r_gated_rms_norm(const void* x, int xt, int64_t ldx, const vo
     // Short rows (head-dim rows of the gated-delta-net output) take the lanes-per-row kernel for the
     // reference's gate types (bf16 / f32); everything else the workgroup-per-row kernel.
     const bool short_rows = dim <= 512 && (gt == EXL3R_F32 || gt == EXL3R_BF16);
-    if (xt != EXL3R_F32 && rms_vec_ok(a, xt, yt, gt, true))
+    if (xt != EXL3R_F32 && rms_vec_ok(a, xt, yt, gt, true, RMS_GATED, 0))
     {
         auto go_x = [&](auto X) {
             with_float_type(yt, [&](auto Y) {
@@ -72,6 +73,7 @@ extern "C" int exl3r_gated_rms_norm_had(const void* x, int xt, int64_t ldx, cons
                                         int64_t dim, float eps, float constant_bias, int gate_first, int gate_act,
                                         float had_scale, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_gated_rms_norm_had";
     if (dim <= 0 || dim % 128) return set_error(EXL3R_EINVAL, "%s: dim %lld must be a multiple of 128", op, (long long)dim);
     int rc = check_rms_common(op, x, xt, ldx, w, wt, out, EXL3R_F16, ldo, rows, dim);
@@ -98,7 +100,7 @@ extern "C" int exl3r_gated_rms_norm_had(const void* x, int xt, int64_t ldx, cons
     hipStream_t s = (hipStream_t)stream;
     const bool short_rows = dim <= 512 && (gt == EXL3R_F32 || gt == EXL3R_BF16);
     const bool aligned = aligned16(out) && (a.ldh * 2) % 16 == 0 && (!pre_scale || aligned16(pre_scale));
-    if (xt != EXL3R_F32 && aligned && rms_vec_ok(a, xt, EXL3R_F16, gt, true))
+    if (xt != EXL3R_F32 && aligned && rms_vec_ok(a, xt, EXL3R_F16, gt, true, RMS_GATED, HAD_OUT))
     {
         auto go_x = [&](auto X) {
             using XTy = decltype(X);

@@ -151,6 +151,7 @@ using namespace exl3r;
 extern "C" int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out, int64_t ldo, int64_t rows,
                                int64_t cols, const void* pre_scale, const void* post_scale, float scale, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_had_r_128";
     if (dtype != EXL3R_F16 && dtype != EXL3R_F32)
         return set_error(EXL3R_EDTYPE, "%s: x / out must be f16 or f32, got %s", op, dtype_name(dtype));

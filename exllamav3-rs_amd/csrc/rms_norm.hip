@@ -30,6 +30,7 @@ extern "C" int exl3r_rms_norm(const void* x, int xt, int64_t ldx, const void* w,
                               void* y, int yt, int64_t ldy, int64_t rows, int64_t dim,
                               float eps, float constant_bias, float constant_scale, void* stream)
 {
+    clear_stale_error();
     int rc = check_rms_common("exl3r_rms_norm", x, xt, ldx, w, wt, y, yt, ldy, rows, dim);
     if (rc) return rc;
     if (rows == 0) return EXL3R_OK;
@@ -39,7 +40,7 @@ extern "C" int exl3r_rms_norm(const void* x, int xt, int64_t ldx, const void* w,
     a.rows = rows; a.dim = (int)dim; a.eps = eps; a.cb = constant_bias; a.cs = constant_scale;
     hipStream_t s = (hipStream_t)stream;
 
-    if (rms_vec_ok(a, xt, yt, 0, false))
+    if (rms_vec_ok(a, xt, yt, 0, false, RMS_PLAIN, 0))
     {
         with_float_type(xt, [&](auto X) {
             with_float_type(yt, [&](auto Y) {

@@ -7,8 +7,9 @@
 //   (norm.cu:273; IEEE fp32 sqrt and divide here);
 //   y = (x * (w + constant_bias)) * rmf in fp32, rounded once (norm.cu:110-124, 232-239, 75-83).
 //
-// Layout: one row per workgroup.  A row is split into chunks of 8 elements; thread t owns chunks
-// t, t + nt, ... (at most MAXV), so every wave-wide access is 64 lanes x 16 bytes contiguous.
+// Layout: one row per workgroup (row = row0 + blockIdx.x; the host splits launches beyond the grid
+// limit).  A row is split into chunks of 8 elements; thread t owns chunks t, t + nt, ... (at most
+// MAXV), so every wave-wide access is 64 lanes x 16 bytes contiguous.
 // The whole row stays in VGPRs between the reduction and the output pass: one HBM read of x (and r),
 // one write of y (and r) per row -- the 4-pass minimum for RES_IN, where the reference re-reads r
 // at dim > 4096.  The row reduction is a DPP butterfly inside each wave and one LDS hop across waves.
@@ -40,6 +41,7 @@ struct RmsArgs
     int64_t vocab;
     int32_t* err;       // RMS_GATHER: device error flag or nullptr
     int64_t rows;
+    int64_t row0;       // first row of this launch (launches of more than kMaxGridX rows are split)
     int dim;
     float eps, cb, cs;
     int gact;           // RMS_GATED: 0 silu, 1 sigmoid
@@ -65,6 +67,15 @@ struct RmsArgs
 constexpr int HAD_OUT = 1;   // rotated f16 outputs, one per projection
 constexpr int HAD_IN = 2;    // x rotated on load
 
+// When a row's weight chunks are fetched (a launch-shape choice: the results are the same bits).
+//   W_EARLY: with the row's HBM loads, so the L2 fetch overlaps them (latency-bound launches);
+//   W_MID:   after pass 1, so the fetch overlaps the row reduction;
+//   W_LATE:  chunk by chunk in pass 2, after the reduction.
+// Streaming launches fetch it late: the row then holds no weight registers while its HBM loads are in
+// flight (MI355X, [8192, 5120]: bf16 residual norm 56.3 us early -> 54.9 late; f16 x / f32 r / f16 y
+// 93.6 -> 88.6; plain bf16 norm 31.5 -> 30.7 mid).
+enum { W_EARLY = 0, W_MID = 1, W_LATE = 2 };
+
 // RMS_GATED gate activation in fp32.
 __device__ __forceinline__ float gate_act(int gact, float g) { return gact ? act_f<ACT_SIGMOID>(g) : act_f<ACT_SILU>(g); }
 
@@ -81,9 +92,9 @@ __device__ __forceinline__ int64_t load_id(const void* ids, int idt, int64_t i)
     return idt == DT_I64 ? ((const int64_t*)ids)[i] : (int64_t)((const int32_t*)ids)[i];
 }
 
-// Weight chunks are prefetched as one 16-byte access before the row reduction (the whole chunk
-// for F16/BF16 weights, the first four floats for F32 weights, whose second half is fetched after
-// the reduction), so the L2 fetch overlaps the reduction at 4 VGPRs per chunk.
+// A weight chunk is fetched as one 16-byte access at the point the launch's weight mode picks (the
+// whole chunk for F16/BF16 weights; for F32 weights the first four floats, the second half being read
+// in pass 2), 4 VGPRs per chunk.
 __device__ __forceinline__ u32x4 prefetch_w8(const void* w, int wt, int64_t e)
 {
     return *(const u32x4*)((const char*)w + e * (wt == DT_F32 ? 4 : 2));
@@ -312,7 +323,7 @@ __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* 
     }
 }
 
-template <class XT, class YT, class RT, int MAXV, int MODE, int HAD = 0>
+template <class XT, class YT, class RT, int MAXV, int MODE, int HAD, int WM>
 __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int tid, int nt, RowRegs<XT, RT, MAXV>& L,
                                            double* red)
 {
@@ -331,38 +342,49 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
         if (c < nc) cache[k] = rms_chunk1<XT, RT, MODE, HAD>(a, rrow, (int64_t)c * 8, L.valid, L.xv[k], L.rv[k], ss);
     }
 
-    // fp64 row sum (exact for 16-bit data), one rounding, IEEE fp32 sqrt and divide.
-    ss = block_sum64(ss, red);
+    const int64_t wofs = weight_row<MODE>(a, row);
+    if constexpr (WM == W_MID)
+    {
+        #pragma unroll
+        for (int k = 0; k < MAXV; ++k)
+        {
+            const int c = tid + k * nt;
+            if (c < nc && a.w) L.wv[k] = prefetch_w8(a.w, a.wt, wofs + (int64_t)c * 8);
+        }
+    }
+
+    // fp64 row sum (exact for 16-bit data), one rounding, IEEE fp32 sqrt and divide.  The workgroup
+    // reduces once, so one barrier suffices.
+    ss = block_sum64_once(ss, red);
     const float rmf = rms_factor(ss, a.dim, a.eps) * a.cs;
 
     // Pass 2: scale, weight, round once, store.
-    const int64_t wofs = weight_row<MODE>(a, row);
     #pragma unroll
     for (int k = 0; k < MAXV; ++k)
     {
         const int c = tid + k * nt;
         if (c < nc)
         {
+            if constexpr (WM == W_LATE)
+            {
+                if (a.w) L.wv[k] = prefetch_w8(a.w, a.wt, wofs + (int64_t)c * 8);
+            }
             if constexpr (kDeferResidual<MODE, RT>) store8<RT>(rrow, (int64_t)c * 8, cache[k]);
             rms_chunk2<XT, YT, RT, MODE, HAD>(a, row, yrow, (int64_t)c * 8, wofs, cache[k], L.rv[k], L.wv[k], rmf);
         }
     }
 }
 
-template <class XT, class YT, class RT, int MAXV, int MODE, int HAD = 0>
-__device__ __forceinline__ void rms_row(const RmsArgs& a, int64_t row, int tid, int nt, double* red)
-{
-    RowRegs<XT, RT, MAXV> L;
-    rms_load<XT, RT, MAXV, MODE>(a, row, tid, nt, true, L);
-    rms_finish<XT, YT, RT, MAXV, MODE, HAD>(a, row, tid, nt, L, red);
-}
-
-template <class XT, class YT, class RT, int MAXV, int MODE, int HAD = 0>
+// One row per workgroup: its loads, pass 1, one reduction, pass 2.  (A grid-stride loop over rows, with
+// the second barrier it needs before LDS reuse, measured ~1 us slower at [8192, 5120].)
+template <class XT, class YT, class RT, int MAXV, int MODE, int HAD = 0, int WM = W_EARLY>
 __global__ __launch_bounds__(1024) void k_rms_norm(RmsArgs a)
 {
     __shared__ double red[16];
-    for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x)
-        rms_row<XT, YT, RT, MAXV, MODE, HAD>(a, row, threadIdx.x, blockDim.x, red);
+    const int64_t row = a.row0 + blockIdx.x;
+    RowRegs<XT, RT, MAXV> L;
+    rms_load<XT, RT, MAXV, MODE>(a, row, threadIdx.x, blockDim.x, WM == W_EARLY, L);
+    rms_finish<XT, YT, RT, MAXV, MODE, HAD, WM>(a, row, threadIdx.x, blockDim.x, L, red);
 }
 
 // Short rows (at most 64 chunks of 8): LPR lanes per row (a power of two covering dim / 8), one
@@ -506,71 +528,98 @@ __global__ __launch_bounds__(256) void k_rms_norm_generic(RmsArgs a, int xt, int
 // ---------------------------------------------------------------------------------------------
 // Host-side launch.
 
-// Launch shape: a workgroup per row, MAXV chunks per thread.  Latency-bound launches (few rows)
-// spread a row over up to 1024 lanes.  Bandwidth-bound launches (bf16 residual norm, 42 M elements,
-// MI355X, us; default before -> after this rule, best shape measured):
-//   dim 2048: 1 x 256 55.2 (3 x 256 54.5)   3584: 2 x 256 56.0 -> 1 x 448 55.1 (1 x 512 54.9)
-//   4096: 2 x 256 56.3 -> 1 x 512 55.2      5120: 2 x 320 57.1 -> 2 x 384 56.1 (best)
-//   7168: 4 x 256 58.8 -> 2 x 448 57.6 (3 x 448 57.1)   8192: 4 x 256 59.1 -> 2 x 512 56.7 (best)
-// so one chunk per lane up to 512 lanes, else two chunks on at least 384 lanes (at 5120 the 64
-// lanes without a second chunk pay off).  Not for the Hadamard kernels, whose chunks carry up to
-// four butterflies: at 5120 2 x 320 runs 133.8 / 141.5 us (3 outputs / with the input rotation)
-// against 134.4 / 144.4 us at 2 x 384.  Other C3 shapes: 3 x 320 56.3, 4 x 192 58.2, 5 x 128
-// 59.4, 8 x 128 83.7, 1 x 640 61.4; one wave per row 74 us; persistent workgroups prefetching the
-// next row 58 us.
+// Launch shape: a workgroup per row, MAXV chunks per lane, and when the weight is fetched.
+//   Latency-bound launches (<= 1024 rows) spread a row over up to 1024 lanes, weight fetched early.
+//   Streaming residual norms (RES_IN, no Hadamard outputs): up to 512 chunks one per lane; longer rows
+//   two chunks per lane on a power-of-two wave count (512 lanes up to 1024 chunks), so that 32 / waves
+//   workgroups fill a CU's 32 wave slots with no idle wave; weight fetched late.  MI355X, [8192, 5120]
+//   bf16 (us): 2 x 320 57.2, 2 x 384 56.3, 2 x 512 54.9, 1 x 640 57.3, 3 x 256 58.3, 1 x 1024 62.1; the
+//   f16 x / f32 r / f16 y mix 2 x 384 92.4, 2 x 512 88.6, 1 x 640 89.2.
+//   Other streaming norms keep the rule fitted to a sweep of the residual norm over hidden sizes 2048 to
+//   8192 before the weight moved (one chunk per lane up to 512 lanes, else two chunks on at least 384
+//   lanes; 320 for the Hadamard kernels, whose chunks carry up to four butterflies), with the weight
+//   fetched mid-row (plain; gather and Hadamard kernels: early, where fetching it later measured no gain).
 struct RmsShape
 {
     int maxv;
     int threads;
+    int wmode;
 };
 
-inline RmsShape rms_shape(int nc, int64_t rows, bool had = false)
+inline RmsShape rms_shape(int nc, int64_t rows, int mode, int had)
 {
     auto thr = [&](int m) { int t = (nc + m - 1) / m; return ((t + 63) / 64) * 64; };
+    auto pick = [&](int m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8; };
+    RmsShape sh{ 0, 0, W_EARLY };
+#ifdef EXL3R_TUNING
     const Tuning& tu = tuning();
-    if (((tu.rms_maxv >= 1 && tu.rms_maxv <= 5) || tu.rms_maxv == 8) &&
+    if ((tu.rms_maxv == 1 || tu.rms_maxv == 2 || tu.rms_maxv == 4 || tu.rms_maxv == 8) &&
         (tu.rms_threads == 0 || (tu.rms_threads % 64 == 0 && tu.rms_threads <= 1024)))
-        return { tu.rms_maxv, tu.rms_threads > 0 ? tu.rms_threads : thr(tu.rms_maxv) };
-    // MAXV = 8 does not fit the VGPR budget of a 1024-thread bound; it is the last resort.
+    {
+        sh.maxv = tu.rms_maxv;
+        sh.threads = tu.rms_threads > 0 ? tu.rms_threads : thr(tu.rms_maxv);
+        sh.wmode = rows > 1024 && !had ? (mode == RMS_RES_IN ? W_LATE : mode == RMS_PLAIN ? W_MID : W_EARLY) : W_EARLY;
+        return sh;
+    }
+#endif
+    if (rows > 1024 && mode == RMS_RES_IN && !had)
+    {
+        if (nc <= 512) return { 1, thr(1), W_LATE };
+        int waves = 1;
+        while (waves < 16 && waves * 128 < nc) waves *= 2;
+        while (waves > 1 && (waves - 1) * 64 >= nc) waves /= 2;
+        const int m = (nc + waves * 64 - 1) / (waves * 64);
+        return { pick(m), waves * 64, W_LATE };
+    }
     if (rows > 1024)
     {
-        if (thr(1) <= 512) return { 1, thr(1) };
-        if (thr(2) <= 1024) return { 2, thr(2) > 384 || had ? thr(2) : 384 };
+        const int wm = !had && mode == RMS_PLAIN ? W_MID : W_EARLY;
+        if (thr(1) <= 512) return { 1, thr(1), wm };
+        if (thr(2) <= 1024) return { 2, thr(2) > 384 || had ? thr(2) : 384, wm };
     }
     static const int opts[3] = { 1, 2, 4 };
     for (int m : opts)
-        if (thr(m) <= 1024) return { m, thr(m) };
-    return { 8, thr(8) };   // <= 1024 (rms_vec_ok bounds the row at 8192 chunks)
+        if (thr(m) <= 1024) return { m, thr(m), W_EARLY };
+    return { 8, thr(8), W_EARLY };   // <= 1024 (rms_vec_ok bounds the row at 8192 chunks)
+}
+
+template <class XT, class YT, class RT, int MODE, int HAD, int WM>
+void launch_rms_wm(const RmsArgs& a0, const RmsShape& sh, hipStream_t s)
+{
+    // Launches of more than kMaxGridX rows go out in blocks of kMaxGridX rows (row0 offsets the block).
+    for (int64_t r0 = 0; r0 < a0.rows; r0 += kMaxGridX)
+    {
+        RmsArgs a = a0;
+        a.row0 = r0;
+        const dim3 grid((unsigned)(a0.rows - r0 < kMaxGridX ? a0.rows - r0 : kMaxGridX));
+        switch (sh.maxv)
+        {
+            case 1: k_rms_norm<XT, YT, RT, 1, MODE, HAD, WM><<<grid, sh.threads, 0, s>>>(a); break;
+            case 2: k_rms_norm<XT, YT, RT, 2, MODE, HAD, WM><<<grid, sh.threads, 0, s>>>(a); break;
+            case 4: k_rms_norm<XT, YT, RT, 4, MODE, HAD, WM><<<grid, sh.threads, 0, s>>>(a); break;
+            default: k_rms_norm<XT, YT, RT, 8, MODE, HAD, WM><<<grid, sh.threads, 0, s>>>(a); break;
+        }
+    }
 }
 
 template <class XT, class YT, class RT, int MODE, int HAD = 0>
-int launch_rms_vec(const RmsArgs& a, hipStream_t s)
+void launch_rms_vec(const RmsArgs& a, hipStream_t s)
 {
-    const RmsShape sh = rms_shape(a.dim / 8, a.rows, HAD != 0);
-    const dim3 grid((unsigned)(a.rows < kMaxGridX ? a.rows : kMaxGridX));
-    if constexpr (MODE == RMS_GATED)
+    const RmsShape sh = rms_shape(a.dim / 8, a.rows, MODE, HAD);
+    if constexpr (HAD == 0 && MODE == RMS_RES_IN)
     {
-        // Chunks per lane 1, 2, 4 or 8 (a tuned 3 or 5 rounds up; the grid still covers the row).
-        if (sh.maxv == 1) k_rms_norm<XT, YT, RT, 1, MODE, HAD><<<grid, sh.threads, 0, s>>>(a);
-        else if (sh.maxv == 2) k_rms_norm<XT, YT, RT, 2, MODE, HAD><<<grid, sh.threads, 0, s>>>(a);
-        else if (sh.maxv <= 4) k_rms_norm<XT, YT, RT, 4, MODE, HAD><<<grid, sh.threads, 0, s>>>(a);
-        else k_rms_norm<XT, YT, RT, 8, MODE, HAD><<<grid, sh.threads, 0, s>>>(a);
-        return 0;
+        if (sh.wmode == W_LATE) return launch_rms_wm<XT, YT, RT, MODE, HAD, W_LATE>(a, sh, s);
     }
-    switch (sh.maxv)
+    if constexpr (HAD == 0 && MODE == RMS_PLAIN)
     {
-        case 1: k_rms_norm<XT, YT, RT, 1, MODE, HAD><<<grid, sh.threads, 0, s>>>(a); break;
-        case 2: k_rms_norm<XT, YT, RT, 2, MODE, HAD><<<grid, sh.threads, 0, s>>>(a); break;
-        case 3: k_rms_norm<XT, YT, RT, 3, MODE, HAD><<<grid, sh.threads, 0, s>>>(a); break;
-        case 4: k_rms_norm<XT, YT, RT, 4, MODE, HAD><<<grid, sh.threads, 0, s>>>(a); break;
-        case 5: k_rms_norm<XT, YT, RT, 5, MODE, HAD><<<grid, sh.threads, 0, s>>>(a); break;
-        default: k_rms_norm<XT, YT, RT, 8, MODE, HAD><<<grid, sh.threads, 0, s>>>(a); break;
+        if (sh.wmode == W_MID) return launch_rms_wm<XT, YT, RT, MODE, HAD, W_MID>(a, sh, s);
     }
-    return 0;
+    launch_rms_wm<XT, YT, RT, MODE, HAD, W_EARLY>(a, sh, s);
 }
 
-// The vector kernel needs 16-byte aligned rows of whole chunks and a row that fits 1024 x 8 chunks.
-inline bool rms_vec_ok(const RmsArgs& a, int xt, int yt, int rt, bool has_r)
+// The vector kernel needs 16-byte aligned rows of whole chunks and a launch shape that covers the row
+// (at most 1024 lanes x 8 chunks).
+inline bool rms_vec_ok(const RmsArgs& a, int xt, int yt, int rt, bool has_r, int mode, int had)
 {
     if (a.dim % 8 != 0 || a.dim / 8 > 8 * 1024) return false;
     auto ok = [](const void* p, int64_t ld, int dt) {
@@ -579,8 +628,8 @@ inline bool rms_vec_ok(const RmsArgs& a, int xt, int yt, int rt, bool has_r)
     if (!ok(a.x, a.ldx, xt) || !ok(a.y, a.ldy, yt)) return false;
     if (has_r && !ok(a.r, a.ldr, rt)) return false;
     if (a.w && !aligned16(a.w)) return false;
-    const RmsShape sh = rms_shape(a.dim / 8, a.rows);
-    return (int64_t)sh.maxv * sh.threads >= a.dim / 8 && sh.threads <= 1024;
+    const RmsShape sh = rms_shape(a.dim / 8, a.rows, mode, had);
+    return (int64_t)sh.maxv * sh.threads >= a.dim / 8 && sh.threads <= 1024 && sh.threads % 64 == 0;
 }
 
 }  // namespace exl3r

@@ -10,6 +10,7 @@ extern "C" int exl3r_rms_norm_res_in(const void* x, int xt, int64_t ldx, const v
                                      int64_t rows, int64_t dim,
                                      float eps, float constant_bias, float constant_scale, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_rms_norm_res_in";
     int rc = check_rms_common(op, x, xt, ldx, w, wt, y, yt, ldy, rows, dim);
     if (rc) return rc;
@@ -25,7 +26,7 @@ extern "C" int exl3r_rms_norm_res_in(const void* x, int xt, int64_t ldx, const v
     a.rows = rows; a.dim = (int)dim; a.eps = eps; a.cb = constant_bias; a.cs = constant_scale;
     hipStream_t s = (hipStream_t)stream;
 
-    if (rms_vec_ok(a, xt, yt, rt, true))
+    if (rms_vec_ok(a, xt, yt, rt, true, RMS_RES_IN, 0))
     {
         with_float_type(xt, [&](auto X) {
             with_float_type(rt, [&](auto R) {

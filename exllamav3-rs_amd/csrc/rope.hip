@@ -958,6 +958,7 @@ extern "C" int exl3r_rope(const void* q, void* out_q, int64_t q_tok_stride, int6
                           float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
                           void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_rope";
     RopeArgs a;
     const int rc = rope_prepare(op, a, q, out_q, q_tok_stride, q_head_stride, num_heads_q, k, out_k, false, k_tok_stride,
@@ -1046,6 +1047,7 @@ extern "C" int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_str
                                    const int32_t* cache_seqlens, int32_t* err_flag, const void* cs_table,
                                    void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_rope_paged_kv";
     RopeArgs a;
     int rc = paged_prepare(op, a, q, out_q, q_tok_stride, q_head_stride, num_heads_q, k, out_k, k_tok_stride,
@@ -1067,6 +1069,7 @@ extern "C" int exl3r_rope_table(const void* q, void* out_q, int64_t q_tok_stride
                                 float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
                                 int32_t* err_flag, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_rope_table";
     if (table_rows <= 0 || table_batch_stride < 0)
         return set_error(EXL3R_EINVAL, "%s: table_rows must be positive and table_batch_stride non-negative", op);
@@ -1099,6 +1102,7 @@ extern "C" int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, 
                               float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
                               const void* q_post_scale, const void* k_post_scale, const void* cs_table, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_rope_had";
     if (dtype != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: the rotated projection outputs are f16", op);
     if (head_dim <= 0 || ((int64_t)num_heads_q * head_dim) % 128 || (k && ((int64_t)num_heads_k * head_dim) % 128))
@@ -1160,6 +1164,7 @@ extern "C" int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok
                                        const void* q_post_scale, const void* k_post_scale, const void* v_post_scale,
                                        const void* cs_table, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_rope_paged_kv_had";
     if (dtype != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: the rotated projection outputs are f16", op);
     if (head_dim <= 0 || ((int64_t)num_heads_q * head_dim) % 128 || ((int64_t)num_heads_kv * head_dim) % 128)
@@ -1212,6 +1217,7 @@ extern "C" int exl3r_rope_cs_table(int64_t bsz, int64_t seq_len, const float* in
                                    int32_t position, const int32_t* positions, const int32_t* position_ids,
                                    float attn_factor, void* cs_table, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_rope_cs_table";
     if (bsz < 0 || seq_len < 0 || rotary_dim < 2 || rotary_dim % 2)
         return set_error(EXL3R_EINVAL, "%s: invalid shape bsz=%lld seq_len=%lld rotary_dim=%d", op, (long long)bsz,
@@ -1240,6 +1246,7 @@ extern "C" int exl3r_rope_cs(const void* q, void* out_q, int64_t q_tok_stride, i
                              const void* k_norm, int norm_dtype, float norm_eps, float norm_constant_bias,
                              int rope_mode, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_rope_cs";
     if (!cs_table && bsz > 0 && seq_len > 0) return set_error(EXL3R_EINVAL, "%s: cs_table must be non-null", op);
     // rope_prepare checks the rotation source of exl3r_rope; the table of an empty call may be NULL.
@@ -1267,6 +1274,7 @@ extern "C" int exl3r_rope_qg(const void* qg, int64_t qg_tok_stride, void* out_q,
                              const void* q_norm, const void* k_norm, int norm_dtype, float norm_eps,
                              float norm_constant_bias, int rope_mode, float attn_factor, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_rope_qg";
     if (head_dim <= 0 || head_dim > 4096)
         return set_error(EXL3R_EINVAL, "%s: head_dim %d must be in [2, 4096]", op, head_dim);

@@ -441,18 +441,21 @@ int sample_entry(const char* op, const void* logits, int dtype, int64_t rows, in
 extern "C" int exl3r_argmax_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
                                    int max_logit, int64_t* ids, void* stream)
 {
+    clear_stale_error();
     return sample_entry<false>("exl3r_argmax_sample", logits, dtype, rows, vocab, ld, max_logit, 0u, ids, stream);
 }
 
 extern "C" int exl3r_gumbel_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
                                    int max_logit, uint32_t random, int64_t* ids, void* stream)
 {
+    clear_stale_error();
     return sample_entry<true>("exl3r_gumbel_sample", logits, dtype, rows, vocab, ld, max_logit, random, ids, stream);
 }
 
 extern "C" int exl3r_gumbel_noise(const void* x, int x_dtype, int64_t ldx, void* out, int out_dtype, int64_t ldo,
                                   int64_t rows, int64_t cols, uint32_t random, void* stream)
 {
+    clear_stale_error();
     const char* op = "exl3r_gumbel_noise";
     if (!is_float_dtype(x_dtype) || !is_float_dtype(out_dtype))
         return set_error(EXL3R_EDTYPE, "%s: unsupported dtypes x=%s out=%s", op, dtype_name(x_dtype),

@@ -1,5 +1,8 @@
-/* Launch-shape overrides for benchmarking sweeps (not part of the drop-in ABI).  0 restores the
- * automatic choice.  Process-global, not thread-safe: set them before launching. */
+/* Launch-shape overrides for tests and benchmarking sweeps -- not part of the drop-in ABI and not
+ * exported by the product library (lib/libexl3rowops.so).  They exist only in the sweep/test build
+ * lib/libexl3rowops_tune.so (the same sources compiled with EXL3R_TUNING), where the tests use them
+ * to force each RoPE kernel on the same inputs.  0 restores the automatic choice.
+ * Process-global, not thread-safe: set them before launching. */
 #ifndef EXL3R_TUNING_H
 #define EXL3R_TUNING_H
 #include "../../include/exl3r/rowops.h"

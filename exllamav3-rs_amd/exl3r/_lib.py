@@ -2,6 +2,7 @@
 
 The library is the product; this module is plumbing.  `load()` raises when the shared object is
 missing -- there is no fallback implementation of any op."""
+import contextlib
 import ctypes
 import os
 
@@ -9,6 +10,7 @@ _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_DIR = os.path.join(_PKG_ROOT, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libexl3rowops.so")
 NAIVE_PATH = os.path.join(LIB_DIR, "libexl3r_naive.so")
+TUNE_PATH = os.path.join(LIB_DIR, "libexl3rowops_tune.so")
 HEADER_PATH = os.path.join(os.path.dirname(_PKG_ROOT), "include", "exl3r", "rowops.h")
 
 F32, F16, BF16, I32, I64 = 0, 1, 2, 3, 4
@@ -62,10 +64,14 @@ PROTOTYPES = {
     "exl3r_embedding": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _i64, _vp, _vp]),
     "exl3r_embedding_rms_norm": (_i, [_vp, _i, _i64, _i64, _i64, _vp, _i, _i64, _vp, _i, _i64, _vp, _i,
                                       _vp, _i, _i64, _f, _f, _f, _vp, _vp]),
+}
+
+# Launch-shape overrides of the sweep/test build only (csrc/tuning.h); the product library has none.
+TUNE_PROTOTYPES = {
     "exl3r_tune_rms": (None, [_i, _i]),
+    "exl3r_tune_rms_rows": (None, [_i]),
     "exl3r_tune_act": (None, [_i, _i, _i]),
     "exl3r_tune_rope": (None, [_i]),
-    "exl3r_tune_rms_rows": (None, [_i]),
     "exl3r_tune_rope_tok": (None, [_i, _i, _i]),
     "exl3r_tune_sample": (None, [_i, _i]),
     "exl3r_tune_had": (None, [_i]),
@@ -86,6 +92,7 @@ NAIVE_PROTOTYPES = {
 
 _lib = None
 _naive = None
+_tune = None
 
 
 def _bind(path, protos):
@@ -113,6 +120,37 @@ def load_naive():
     if _naive is None:
         _naive = _bind(NAIVE_PATH, NAIVE_PROTOTYPES)
     return _naive
+
+
+def load_tune():
+    """The sweep/test build of the library (lib/libexl3rowops_tune.so): the same sources compiled with
+    EXL3R_TUNING, which adds the process-global exl3r_tune_* launch-shape overrides.  Tests only."""
+    global _tune
+    if _tune is None:
+        _tune = _bind(TUNE_PATH, {**PROTOTYPES, **TUNE_PROTOTYPES})
+    return _tune
+
+
+@contextlib.contextmanager
+def tuned():
+    """Within the block, the ffi wrappers call the sweep/test build (load_tune()), whose handle is
+    yielded to set its overrides; on exit every override is reset and the product library restored."""
+    global _lib
+    saved = load()
+    lib = load_tune()
+    _lib = lib
+    try:
+        yield lib
+    finally:
+        lib.exl3r_tune_rms(0, 0)
+        lib.exl3r_tune_rms_rows(0)
+        lib.exl3r_tune_act(0, 0, 0)
+        lib.exl3r_tune_rope(0)
+        lib.exl3r_tune_rope_tok(0, 0, 0)
+        lib.exl3r_tune_sample(0, 0)
+        lib.exl3r_tune_had(0)
+        lib.exl3r_tune_embed(0)
+        _lib = saved
 
 
 class Exl3rError(RuntimeError):

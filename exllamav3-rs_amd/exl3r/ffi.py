@@ -225,15 +225,26 @@ def rope(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm
                             norm_eps, norm_constant_bias, rope_mode, attn_factor, _stream(q, stream)))
 
 
-def _rotary_dim(inv_freq, cs_table):
-    """rotary_dim from inv_freq [R/2], or from a {cos, sin} table [tokens, R/2, 2] when inv_freq is None."""
+def _rotary_dim(inv_freq, cs_table, tokens, device):
+    """rotary_dim of the entry points that take inv_freq [R/2] and / or a rope_cs_table() {cos, sin} table
+    [tokens, R/2, 2] (tokens = bsz * seq_len).  These kernels index the table by token, so a table built for
+    fewer tokens (one reused across forward passes of different lengths) is rejected here; an angle table
+    (2-D / 3-D inv_freq) is rope()'s input only."""
+    if inv_freq is not None and (inv_freq.dim() != 1 or inv_freq.dtype != torch.float32):
+        raise ValueError("inv_freq must be float32 [R/2]; an angle table (RoPE::apply's freq_table) takes rope()")
     if cs_table is not None:
-        if cs_table.dtype != torch.float32 or not cs_table.is_contiguous() or cs_table.dim() != 3 or cs_table.shape[2] != 2:
-            raise ValueError("cs_table must be a contiguous float32 [bsz * seq_len, R/2, 2]")
-        if inv_freq is not None and inv_freq.shape[-1] != cs_table.shape[1]:
+        if (cs_table.dtype != torch.float32 or not cs_table.is_contiguous() or cs_table.dim() != 3
+                or cs_table.shape[0] != tokens or cs_table.shape[2] != 2):
+            raise ValueError(f"cs_table must be a contiguous float32 [bsz * seq_len = {tokens}, R/2, 2], "
+                             f"got {tuple(cs_table.shape)} {cs_table.dtype}")
+        if cs_table.device != device:
+            raise ValueError("cs_table must be on the device of q")
+        if inv_freq is not None and inv_freq.shape[0] != cs_table.shape[1]:
             raise ValueError("cs_table and inv_freq disagree on rotary_dim")
         return cs_table.shape[1] * 2
-    return inv_freq.shape[-1] * 2
+    if inv_freq is None:
+        raise ValueError("inv_freq or cs_table is required")
+    return inv_freq.shape[0] * 2
 
 
 def rope_qg(qg, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias,
@@ -264,7 +275,8 @@ def rope_qg(qg, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, 
             raise TypeError("positions / position_ids must be int32")
     nw = q_norm if q_norm is not None else k_norm
     check(load().exl3r_rope_qg(_ptr(qg), qg.stride(1), _ptr(out_q), hq, _ptr(k), _ptr(out_k), k_ts, k_hs, hk,
-                               dtype_code(qg), bsz, seq, hd, _ptr(inv_freq), inv_freq.shape[-1] * 2, int(position),
+                               dtype_code(qg), bsz, seq, hd, _ptr(inv_freq), _rotary_dim(inv_freq, None, 0, qg.device),
+                               int(position),
                                _ptr(positions), _ptr(position_ids), _ptr(q_norm), _ptr(k_norm),
                                dtype_code(nw) if nw is not None else F16, norm_eps, norm_constant_bias, rope_mode,
                                attn_factor, _stream(qg, stream)))
@@ -343,7 +355,7 @@ def rope_had(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, 
         hk, k_ts = k.shape[2], k.stride(1)
     nw = q_norm if q_norm is not None else k_norm
     check(load().exl3r_rope_had(_ptr(q), _ptr(out_q), q.stride(1), hq, _ptr(k), _ptr(out_k), k_ts, hk,
-                                dtype_code(q), bsz, seq, hd, _ptr(inv_freq), _rotary_dim(inv_freq, cs_table),
+                                dtype_code(q), bsz, seq, hd, _ptr(inv_freq), _rotary_dim(inv_freq, cs_table, bsz * seq, q.device),
                                 int(position), _ptr(positions), _ptr(position_ids),
                                 _ptr(q_norm), _ptr(k_norm), dtype_code(nw) if nw is not None else F16,
                                 norm_eps, norm_constant_bias, rope_mode, attn_factor, _ptr(q_post_scale),
@@ -385,7 +397,7 @@ def rope_paged_kv(q, out_q, k, out_k, v, inv_freq, position, positions, q_norm, 
     check(load().exl3r_rope_paged_kv(_ptr(q), _ptr(out_q), q.stride(1), q.stride(2), hq,
                                      _ptr(k), _ptr(out_k), k.stride(1), k.stride(2),
                                      _ptr(v), v.stride(1), v.stride(2), hk,
-                                     dtype_code(q), bsz, seq, hd, _ptr(inv_freq), _rotary_dim(inv_freq, cs_table),
+                                     dtype_code(q), bsz, seq, hd, _ptr(inv_freq), _rotary_dim(inv_freq, cs_table, bsz * seq, q.device),
                                      int(position), _ptr(positions), _ptr(position_ids),
                                      _ptr(q_norm), _ptr(k_norm), dtype_code(nw) if nw is not None else F16,
                                      norm_eps, norm_constant_bias, rope_mode, attn_factor,
@@ -420,7 +432,7 @@ def rope_paged_kv_had(q, out_q, k, out_k, v, inv_freq, position, positions, q_no
     nw = q_norm if q_norm is not None else k_norm
     check(load().exl3r_rope_paged_kv_had(_ptr(q), _ptr(out_q), q.stride(1), hq, _ptr(k), _ptr(out_k), k.stride(1),
                                          _ptr(v), v.stride(1), hk, dtype_code(q), bsz, seq, hd, _ptr(inv_freq),
-                                         _rotary_dim(inv_freq, cs_table), int(position), _ptr(positions),
+                                         _rotary_dim(inv_freq, cs_table, bsz * seq, q.device), int(position), _ptr(positions),
                                          _ptr(position_ids),
                                          _ptr(q_norm), _ptr(k_norm), dtype_code(nw) if nw is not None else F16,
                                          norm_eps, norm_constant_bias, rope_mode, attn_factor,

@@ -501,6 +501,19 @@ void rope(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* o
                          code_or(nw, DType::F16), norm_eps, norm_constant_bias, (int)rope_mode, attn_factor, s.get()));
 }
 
+// rotary_dim of the entry points that take inv_freq [R/2] and optionally a rope_cs_table() {cos, sin} table
+// [tokens, R/2, 2] (tokens = bsz * seq_len).  Their kernels index the table by token, so a table built for
+// fewer tokens (one kept across forward passes of different lengths) is rejected before the launch.
+static int rotary_dim_of(const char* op, const Tensor& inv_freq, const Tensor* cs_table, int64_t tokens)
+{
+    require(inv_freq.dtype == DType::F32 && inv_freq.dim() == 1, std::string(op) + ": inv_freq must be float32 [R/2]");
+    if (cs_table)
+        require(cs_table->dtype == DType::F32 && cs_table->is_contiguous() && cs_table->dim() == 3 &&
+                    cs_table->size(0) == tokens && cs_table->size(1) == inv_freq.size(0) && cs_table->size(2) == 2,
+                std::string(op) + ": cs_table must be contiguous float32 [bsz * seq_len, R/2, 2] with R/2 = inv_freq's length");
+    return (int)(inv_freq.size(0) * 2);
+}
+
 void rope_had(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
               int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
               float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Tensor* q_post_scale,
@@ -520,13 +533,13 @@ void rope_had(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tenso
         hk = k->size(2);
         kts = k->stride(1);
     }
-    require(inv_freq.dtype == DType::F32 && inv_freq.dim() == 1, "rope_had: inv_freq must be float32 [R/2]");
+    const int rdim = rotary_dim_of("rope_had", inv_freq, cs_table, bsz * seq);
     require(!positions || positions->dtype == DType::I32, "rope_had: positions must be int32");
     require(!position_ids || position_ids->dtype == DType::I32, "rope_had: position_ids must be int32");
     const Tensor* nw = q_norm ? q_norm : k_norm;
     check_abi(exl3r_rope_had(q.data, out_q.data, q.stride(1), (int)q.size(2), k ? k->data : nullptr,
                              out_k ? out_k->data : nullptr, kts, (int)hk, code(q.dtype), bsz, seq, (int)hd,
-                             (const float*)inv_freq.data, (int)(inv_freq.numel() * 2), (int32_t)position,
+                             (const float*)inv_freq.data, rdim, (int32_t)position,
                              (const int32_t*)ptr(positions), (const int32_t*)ptr(position_ids), ptr(q_norm),
                              ptr(k_norm), code_or(nw, DType::F16), norm_eps, norm_constant_bias, (int)rope_mode,
                              attn_factor, ptr(q_post_scale), ptr(k_post_scale), ptr(cs_table), s.get()));
@@ -554,13 +567,13 @@ void rope_paged_kv(const Tensor& q, const Tensor& out_q, const Tensor& k, const 
             "rope_paged_kv: caches must be contiguous (pages, page_size, kv_heads, head_dim)");
     require(block_table.dim() == 2 && block_table.dtype == DType::I32 && cache_seqlens.dtype == DType::I32,
             "rope_paged_kv: block_table (bsz, max_blocks) and cache_seqlens (bsz) must be int32");
-    require(inv_freq.dtype == DType::F32, "rope_paged_kv: inv_freq must be float32");
+    const int rdim = rotary_dim_of("rope_paged_kv", inv_freq, cs_table, bsz * seq);
     require(!positions || positions->dtype == DType::I32, "rope_paged_kv: positions must be int32");
     const Tensor* nw = q_norm ? q_norm : k_norm;
     check_abi(exl3r_rope_paged_kv(q.data, out_q.data, q.stride(1), q.stride(2), (int)q.size(2), k.data,
                                   out_k ? out_k->data : nullptr, k.stride(1), k.stride(2), v.data, v.stride(1), v.stride(2),
                                   (int)hk, code(q.dtype), bsz, seq, (int)hd, (const float*)inv_freq.data,
-                                  (int)(inv_freq.numel() * 2), (int32_t)position, (const int32_t*)ptr(positions), nullptr,
+                                  rdim, (int32_t)position, (const int32_t*)ptr(positions), nullptr,
                                   ptr(q_norm), ptr(k_norm), code_or(nw, DType::F16), norm_eps, norm_constant_bias,
                                   (int)rope_mode, attn_factor, k_cache.data, v_cache.data, (int)k_cache.size(1),
                                   k_cache.size(0), (const int32_t*)block_table.data, block_table.size(1),
@@ -590,13 +603,13 @@ void rope_paged_kv_had(const Tensor& q, const Tensor& out_q, const Tensor& k, co
             "rope_paged_kv_had: caches must be contiguous (pages, page_size, kv_heads, head_dim)");
     require(block_table.dim() == 2 && block_table.dtype == DType::I32 && cache_seqlens.dtype == DType::I32,
             "rope_paged_kv_had: block_table (bsz, max_blocks) and cache_seqlens (bsz) must be int32");
-    require(inv_freq.dtype == DType::F32 && (!positions || positions->dtype == DType::I32),
-            "rope_paged_kv_had: inv_freq float32, positions int32");
+    const int rdim = rotary_dim_of("rope_paged_kv_had", inv_freq, cs_table, bsz * seq);
+    require(!positions || positions->dtype == DType::I32, "rope_paged_kv_had: positions must be int32");
     const Tensor* nw = q_norm ? q_norm : k_norm;
     check_abi(exl3r_rope_paged_kv_had(q.data, out_q.data, q.stride(1), (int)q.size(2), k.data,
                                       out_k ? out_k->data : nullptr, k.stride(1), v.data, v.stride(1), (int)hk,
                                       code(q.dtype), bsz, seq, (int)hd, (const float*)inv_freq.data,
-                                      (int)(inv_freq.numel() * 2), (int32_t)position, (const int32_t*)ptr(positions),
+                                      rdim, (int32_t)position, (const int32_t*)ptr(positions),
                                       nullptr, ptr(q_norm), ptr(k_norm), code_or(nw, DType::F16), norm_eps,
                                       norm_constant_bias, (int)rope_mode, attn_factor, k_cache.data, v_cache.data,
                                       (int)k_cache.size(1), k_cache.size(0), (const int32_t*)block_table.data,

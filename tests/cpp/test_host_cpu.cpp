@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdio>
 #include <functional>
+#include <string>
 
 using namespace exl3r;
 
@@ -55,6 +56,37 @@ int main()
     Tensor g(fake, DType::BF16, { 8, 128 }), u(fake, DType::F16, { 8, 128 }), z(fake, DType::BF16, { 8, 128 });
     expect_error("act dtype mismatch", EXL3R_EINVAL, [&] { ffi::silu_mul(g, u, z, 0.f, s); });
     expect_error("RoPE odd rotary_dim", EXL3R_EINVAL, [&] { RoPE::default_inv_freq(1e6, 63); });
+
+    // {cos, sin} tables must cover the call's bsz * seq_len tokens (the kernels index them by token) and
+    // match inv_freq's R/2; an angle table is rope()'s input only.
+    {
+        Tensor q4(fake, DType::F16, { 1, 3, 4, 128 }), k4(fake, DType::F16, { 1, 3, 2, 128 }), v4(fake, DType::F16, { 1, 3, 2, 128 });
+        Tensor inv64(fake, DType::F32, { 64 }), angles(fake, DType::F32, { 16, 64 });
+        Tensor cs_short(fake, DType::F32, { 2, 64, 2 }), cs_rdim(fake, DType::F32, { 3, 32, 2 }), cs_f16(fake, DType::F16, { 3, 64, 2 });
+        Tensor kc(fake, DType::F16, { 4, 256, 2, 128 }), bt(fake, DType::I32, { 1, 2 }), sl(fake, DType::I32, { 1 });
+        auto had = [&](const Tensor& inv, const Tensor* cs) {
+            ffi::rope_had(q4, q4, &k4, &k4, inv, 0, nullptr, nullptr, nullptr, 1e-6f, 0.f, RopeStyle::NeoX, 1.f, nullptr,
+                          nullptr, s, nullptr, cs);
+        };
+        auto paged = [&](const Tensor& inv, const Tensor* cs) {
+            ffi::rope_paged_kv(q4, q4, k4, nullptr, v4, inv, 0, nullptr, nullptr, nullptr, 1e-6f, 0.f, RopeStyle::NeoX, 1.f,
+                               kc, kc, bt, sl, nullptr, s, cs);
+        };
+        auto paged_had = [&](const Tensor& inv, const Tensor* cs) {
+            ffi::rope_paged_kv_had(q4, q4, k4, nullptr, v4, inv, 0, nullptr, nullptr, nullptr, 1e-6f, 0.f, RopeStyle::NeoX,
+                                   1.f, kc, kc, bt, sl, nullptr, nullptr, nullptr, nullptr, s, cs);
+        };
+        const std::function<void(const Tensor&, const Tensor*)> ops[3] = { had, paged, paged_had };
+        const char* names[3] = { "rope_had", "rope_paged_kv", "rope_paged_kv_had" };
+        for (int i = 0; i < 3; ++i)
+        {
+            const std::string n = names[i];
+            expect_error((n + " short cs_table").c_str(), EXL3R_EINVAL, [&] { ops[i](inv64, &cs_short); });
+            expect_error((n + " cs_table R/2 != inv_freq").c_str(), EXL3R_EINVAL, [&] { ops[i](inv64, &cs_rdim); });
+            expect_error((n + " f16 cs_table").c_str(), EXL3R_EINVAL, [&] { ops[i](inv64, &cs_f16); });
+            expect_error((n + " angle table as inv_freq").c_str(), EXL3R_EINVAL, [&] { ops[i](angles, nullptr); });
+        }
+    }
 
     // inv_freq: 1 / exp((2i/d) ln theta) in fp32 equals theta^(-2i/d) to a few fp32 ulps.
     const std::vector<float> inv_freq = RoPE::default_inv_freq(1e6, 128);

@@ -145,9 +145,8 @@ def paged_case(bsz, seq, hq, hk, page, max_blocks, had, tune_use=0, seed=0):
     posts = dict(q_post_scale=svh(hq * hd, seed + 7), k_post_scale=svh(hk * hd, seed + 8),
                  v_post_scale=svh(hk * hd, seed + 9)) if had else {}
     outs = []
-    lib = L.load()
-    lib.exl3r_tune_rope_tok(tune_use, 0, 0)
-    try:
+    with L.tuned() as lib:
+        lib.exl3r_tune_rope_tok(tune_use, 0, 0)
         for table in (None, cs):
             oq, ok, vv, kcc, vcc = torch.empty_like(q), torch.empty_like(k), v.clone(), kc.clone(), vc.clone()
             err = torch.zeros(1, dtype=torch.int32, device="cuda")
@@ -156,8 +155,6 @@ def paged_case(bsz, seq, hq, hk, page, max_blocks, had, tune_use=0, seed=0):
                kcc, vcc, btd, sld, err_flag=err, cs_table=table, **posts)
             outs.append((oq, ok, kcc, vcc, err))
         torch.cuda.synchronize()
-    finally:
-        lib.exl3r_tune_rope_tok(0, 0, 0)
     tag = f"paged{'_had' if had else ''} cs b{bsz} s{seq} h{hq}/{hk} use{tune_use}"
     for a, b, what in zip(outs[0], outs[1], ("q", "out_k", "k_cache", "v_cache", "err")):
         assert same(a, b) if a.dtype == torch.float16 else torch.equal(a, b), tag + " " + what

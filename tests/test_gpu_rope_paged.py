@@ -61,9 +61,10 @@ def layout(bsz, seq, page, max_blocks, seed, pages=None):
 
 @pytest.fixture
 def tune():
-    lib = L.load()
-    yield lambda use: lib.exl3r_tune_rope_tok(use, 0, 0)
-    lib.exl3r_tune_rope_tok(0, 0, 0)
+    """Forces the RoPE kernel (0 auto, 1 never the wave-per-token kernel, 2 always) through the sweep/test
+    build of the library, which the wrappers call inside the fixture."""
+    with L.tuned() as lib:
+        yield lambda use: lib.exl3r_tune_rope_tok(use, 0, 0)
 
 
 @pytest.mark.parametrize("use", [0, 1, 2])

@@ -1,5 +1,6 @@
 """Both vector RoPE kernels (the wave-per-token NeoX prefill kernel and the flattened kernel)
-forced through the launch-shape hook on the same cases, each checked against the CPU oracle: every
+forced through the launch-shape hook of the sweep/test build (libexl3rowops_tune.so, the same
+sources with the overrides compiled in) on the same cases, each checked against the CPU oracle: every
 batch width and grid shape of the prefill kernel, head dims 64 / 128 / 256, partial rotary, q only,
 strided rows and every position source, so parity does not depend on which kernel the size
 heuristic picks (GPT-J always takes the flattened kernel)."""
@@ -20,12 +21,12 @@ F16, BF16, F32 = exl3r.F16, exl3r.BF16, exl3r.F32
 
 @pytest.fixture
 def tune():
-    lib = L.load()
-
-    def set_(use, hpl=0, wpc=0):
-        lib.exl3r_tune_rope_tok(use, hpl, wpc)
-    yield set_
-    lib.exl3r_tune_rope_tok(0, 0, 0)
+    """Kernel choice, heads per lane and grid of the sweep/test build, which the wrappers call inside the
+    fixture."""
+    with L.tuned() as lib:
+        def set_(use, hpl=0, wpc=0):
+            lib.exl3r_tune_rope_tok(use, hpl, wpc)
+        yield set_
 
 
 @pytest.mark.parametrize("hpl,wpc", [(2, 0), (3, 0), (2, 1), (3, 1), (2, 4), (3, 4)])

@@ -20,9 +20,10 @@ F16, BF16, F32 = exl3r.F16, exl3r.BF16, exl3r.F32
 
 @pytest.fixture
 def tune():
-    lib = L.load()
-    yield lambda use: lib.exl3r_tune_rope_tok(use, 0, 0)
-    lib.exl3r_tune_rope_tok(0, 0, 0)
+    """Forces the RoPE kernel (0 auto, 1 never the wave-per-token kernel, 2 always) through the sweep/test
+    build of the library, which the wrappers call inside the fixture."""
+    with L.tuned() as lib:
+        yield lambda use: lib.exl3r_tune_rope_tok(use, 0, 0)
 
 
 def inv_freq(R, theta=1e6):
