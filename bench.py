@@ -54,7 +54,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--op", choices=OPS, default=None, help="time one kernel only")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
     return p.parse_args()
 
 
@@ -833,38 +833,168 @@ def rms_c2_latencies():
 # ------------------------------------------------------------------------------------------------
 # CPU baseline (the oracle, timed on this host)
 
+def cpu_threads():
+    """Threads of the CPU baseline: every core of the process affinity mask, capped by OMP_NUM_THREADS
+    when the environment sets it (the GPU boxes set it to the process's CPU share, 16 per GPU)."""
+    aff = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    return (min(aff, int(omp)) if omp.isdigit() and int(omp) > 0 else aff), aff
+
+
 def cpu_baseline(seconds):
+    """The CPU oracle (C, OpenMP; the reference has no CPU path for these ops) timed on this host over
+    every BASELINE config and the decode composite, each config on the sample named in its entry, with
+    outputs preallocated (the oracle's C entry points are called directly).  Per config: one warm-up,
+    then repetitions until its share of `seconds` is spent (at least 5); the median is reported.  The
+    headline `value` is the C3 step sample (the bench's own workload)."""
+    import ctypes
     import numpy as np
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
-    cores = min(16, len(os.sched_getaffinity(0)))
+    lib = orc.load()
+    nthreads, aff = cpu_threads()
     rng = np.random.default_rng(0)
-    rows_n, rows_a = 256, 64
-    x = orc.to_bits(rng.standard_normal((rows_n, 5120), dtype=np.float32), orc.BF16)
-    r0 = orc.to_bits(rng.standard_normal((rows_n, 5120), dtype=np.float32) * 4, orc.BF16)
-    w = orc.to_bits(rng.standard_normal(5120, dtype=np.float32) * 0.1 + 1, orc.BF16)
-    g = orc.to_bits(rng.standard_normal((rows_a, 17408), dtype=np.float32), orc.BF16)
-    u = orc.to_bits(rng.standard_normal((rows_a, 17408), dtype=np.float32), orc.BF16)
-    nbytes = (4 * rows_n * 5120 + 5120) * 2 + 2 * 3 * rows_a * 17408 * 2
+    P = orc._p
+    F16, BF16, F32 = orc.F16, orc.BF16, orc.F32
 
-    def step():
-        r = r0.copy()
-        orc.rms_norm(x, orc.BF16, w, orc.BF16, orc.BF16, 1e-6, r=r, rt=orc.BF16, nthreads=cores)
-        orc.act_mul(orc.ACT_SILU, g, u, orc.BF16, orc.BF16, nthreads=cores)
-        orc.act_mul(orc.ACT_GELU, g, u, orc.BF16, orc.BF16, nthreads=cores)
+    def normal(shape, mean, std, code):
+        return orc.to_bits(rng.standard_normal(shape, dtype=np.float32) * std + mean, code)
 
-    step()
+    def empty(shape, code):
+        return np.empty(shape, orc.storage_dtype(code))
+
+    def res_norm(T, H, dt):
+        x, r0, w = normal((T, H), 0, 1, dt), normal((T, H), 0, 4, dt), normal((H,), 1, 0.1, dt)
+        r, y = r0.copy(), empty((T, H), dt)
+
+        def run():   # r accumulates x over the reps (values stay finite: the timing does not depend on them)
+            lib.oracle_rms_norm(P(x), dt, H, P(w), dt, P(y), dt, H, P(r), dt, H, T, H, 1e-6, 0.0, 1.0, nthreads)
+        return run, 4 * T * H * 2 + H * 2
+
+    def norm(T, H, dt):
+        x, w, y = normal((T, H), 0, 1, dt), normal((H,), 1, 0.1, dt), empty((T, H), dt)
+
+        def run():
+            lib.oracle_rms_norm(P(x), dt, H, P(w), dt, P(y), dt, H, None, F32, H, T, H, 1e-6, 0.0, 1.0, nthreads)
+        return run, 2 * T * H * 2 + H * 2
+
+    def act(T, I, dt, a):
+        g, u, z = normal((T, I), 0, 1, dt), normal((T, I), 0, 1, dt), empty((T, I), dt)
+
+        def run():
+            lib.oracle_act_mul(a, P(g), P(u), dt, P(z), dt, T, I, I, I, I, 0.0, nthreads)
+        return run, 3 * T * I * 2
+
+    def rope(pos, hq, hk, hd, R, mode):
+        T = pos.size
+        q, k = normal((1, T, hq, hd), 0, 1, F16), normal((1, T, hk, hd), 0, 1, F16)
+        qn, kn = normal((hd,), 1, 0.1, F16), normal((hd,), 1, 0.1, F16)
+        oq, ok = empty(q.shape, F16), empty(k.shape, F16)
+        inv = (1.0 / 1e6 ** (np.arange(0, R, 2, dtype=np.float64) / R)).astype(np.float32)
+        pid = np.ascontiguousarray(pos.reshape(1, T), np.int32)
+
+        def run():
+            lib.oracle_rope(P(q), P(oq), hq * hd, hd, hq, P(k), P(ok), hk * hd, hd, hk, F16, 1, T, hd, P(inv), R, 0,
+                            None, P(pid), P(qn), P(kn), F16, 1e-6, 0.0, mode, 1.0, nthreads)
+        return run, 2 * T * (hq + hk) * hd * 2 + 4 * T + 2 * hd * 2 + (R // 2) * 4
+
+    def gather(vocab, H, ids, dt, with_norm):
+        table = np.zeros((vocab, H), orc.storage_dtype(dt))    # values do not change the work; rows touched once
+        table[np.unique(ids)] = normal((np.unique(ids).size, H), 0, 0.02, dt)
+        ids = np.ascontiguousarray(ids, np.int64)
+        n = ids.size
+        w, h, y = normal((H,), 1, 0.1, dt), empty((n, H), dt), empty((n, H), dt)
+        err = np.zeros(1, np.int32)
+        if with_norm:
+            def run():
+                lib.oracle_embedding_rms_norm(P(table), dt, vocab, H, H, P(ids), orc.I64, n, P(h), dt, H, P(w), dt,
+                                              P(y), dt, H, 1e-6, 0.0, 1.0, P(err), nthreads)
+            return run, n * H * 2 * 3 + n * 8 + H * 2
+        def run():
+            lib.oracle_embedding(P(table), dt, vocab, H, H, P(ids), orc.I64, n, P(h), dt, H, P(err), nthreads)
+        return run, n * H * 2 * 2 + n * 8
+
+    ragged = ragged_positions(0)
+    cases = {
+        "c1_rms_norm": ("full C1: RMSNorm [512,1024] f16", lambda: norm(512, 1024, F16)),
+        "c1_silu_mul": ("full C1: SiLU-mul [512,3072] f16", lambda: act(512, 3072, F16, orc.ACT_SILU)),
+        "c1_rope": ("full C1: q/k head-norm + NeoX RoPE, 512 tokens, 16/8 heads of 128, f16",
+                    lambda: rope(np.arange(512, dtype=np.int32), 16, 8, 128, 128, orc.ROPE_NEOX)),
+        "c1_gather": ("full C1: gather of 512 uniform ids from [151936,1024] f16",
+                      lambda: gather(151936, 1024, np.random.default_rng(0).integers(0, 151936, 512), F16, False)),
+        "c2_res_norm_t64": ("full C2 at T=64: residual RMSNorm [64,5120] f16", lambda: res_norm(64, 5120, F16)),
+        "c3_res_norm": ("C3 row sample: residual RMSNorm [256,5120] bf16", lambda: res_norm(256, 5120, BF16)),
+        "c3_silu_mul": ("C3 row sample: SiLU-mul [64,17408] bf16", lambda: act(64, 17408, BF16, orc.ACT_SILU)),
+        "c3_gelu_mul": ("C3 row sample: GELU-mul [64,17408] bf16", lambda: act(64, 17408, BF16, orc.ACT_GELU)),
+        "c4_rope_neox": ("C4 token sample: the first 512 of the ragged tokens, 64/8 heads of 128, NeoX, f16",
+                         lambda: rope(ragged[:512], 64, 8, 128, 128, orc.ROPE_NEOX)),
+        "c4_rope_gptj": ("C4 token sample: 512 tokens, GPT-J at rotary_dim 64",
+                         lambda: rope(ragged[:512], 64, 8, 128, 64, orc.ROPE_GPTJ)),
+        "c5_gather_norm": ("C5 id sample: gather + RMSNorm of 1024 Zipf ids from [151936,5120] bf16 (h and y)",
+                           lambda: gather(151936, 5120, zipf_ids(1024, 151936, 1), BF16, True)),
+    }
+    out = {}
+    share = seconds / (len(cases) + 1)
+    for name, (sample, build) in cases.items():
+        run, nbytes = build()
+        run()
+        times = []
+        t_end = time.perf_counter() + share
+        while time.perf_counter() < t_end or len(times) < 5:
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        out[name] = {"us": round(med * 1e6, 2), "gbs": round(nbytes / med / 1e9, 3), "bytes": nbytes,
+                     "reps": len(times), "sample": sample}
+    # the 64-row decode layer: the sum of its four ops (2 residual norms, RoPE, SiLU-mul), f16
+    runs = [res_norm(64, 5120, F16), res_norm(64, 5120, F16),
+            rope(np.random.default_rng(7).integers(0, 32768, 64).astype(np.int32), 64, 8, 128, 128, orc.ROPE_NEOX),
+            act(64, 17408, F16, orc.ACT_SILU)]
+    for r, _ in runs:
+        r()
     times = []
-    t_end = time.perf_counter() + seconds
+    t_end = time.perf_counter() + share
     while time.perf_counter() < t_end or len(times) < 5:
         t0 = time.perf_counter()
-        step()
+        for r, _ in runs:
+            r()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": (f"C3 step on a row sample: residual RMSNorm [{rows_n},5120] + SiLU-mul and GELU-mul "
-                       f"[{rows_a},17408] bf16, CPU oracle (C, OpenMP, {cores} threads), median of {len(times)} "
-                       f"reps over ~{seconds:.0f} s")}
+    nb = sum(b for _, b in runs)
+    out["decode_layer_t64"] = {"us": round(med * 1e6, 2), "gbs": round(nb / med / 1e9, 3), "bytes": nb,
+                               "reps": len(times), "sample": "full: 64-row decode layer, 2 residual norms + RoPE + SiLU-mul, f16"}
+    c3 = [out[k] for k in ("c3_res_norm", "c3_silu_mul", "c3_gelu_mul")]
+    c3_gbs = sum(c["bytes"] for c in c3) / (sum(c["us"] for c in c3) * 1e-6) / 1e9
+    return {"value": round(c3_gbs, 3), "unit": "GB/s", "cores": nthreads, "affinity_cores": aff, "kind": "port",
+            "sample": (f"value: the C3 step on a row sample (residual RMSNorm [256,5120] + SiLU-mul and GELU-mul "
+                       f"[64,17408] bf16); the CPU oracle (C, OpenMP, {nthreads} threads of {aff} in the affinity "
+                       f"mask), median per config over ~{share:.1f} s each; every config in `configs`"),
+            "configs": out}
+
+
+def decode_eager_compiled(timeout=120):
+    """Runs the compiled eager decode-layer timing (exllamav3-rs_amd/bin/exl3r_bench_decode) as a child
+    process and returns its JSON, or None (with the reason logged) when it is not built or fails."""
+    import subprocess
+    exe = os.path.join(ROOT, "exllamav3-rs_amd", "bin", "exl3r_bench_decode")
+    if not os.path.exists(exe):
+        log(f"decode eager (compiled): {exe} is not built")
+        return None
+    try:
+        p = subprocess.run([exe, "2000", "7"], capture_output=True, text=True, timeout=timeout)
+    except subprocess.TimeoutExpired:
+        log("decode eager (compiled): timed out")
+        return None
+    if p.returncode != 0:
+        log(f"decode eager (compiled): exit {p.returncode}: {p.stderr.strip()[-300:]}")
+        return None
+    res = json.loads(p.stdout.strip().splitlines()[-1])
+    res["timing"] = ("median of 7 windows of 2000 layers enqueued back to back from C++ (host layer ffi wrappers "
+                     "with their argument checks / the naive C entry points), HIP events on the stream")
+    log(f"decode eager (compiled): fused {res['fused_us']:.2f} us vs naive {res['naive_us']:.2f} us "
+        f"(x{res['speedup']:.2f}); host enqueue {res['fused_host_enqueue_us']:.2f} / {res['naive_host_enqueue_us']:.2f} us")
+    return res
 
 
 def traffic_from_profiles(op):
@@ -890,6 +1020,9 @@ def main():
               "token-independent and would shard over tokens with no exchange -- run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+    # The eager decode layer timed from compiled code (a child process, started before this process
+    # touches the GPU): the reference's batched decode is not graph-captured.
+    dec_compiled = None if args.op else decode_eager_compiled()
     import torch
     import exl3r
     exl3r.load()
@@ -936,13 +1069,22 @@ def main():
         dec = {}
         for name in ("decode_fused", "decode_naive"):
             dec[name] = {"us_eager": ops[name]["us"], "us_graph": round(time_graph(works[name], 20, 10) * 1000, 3)}
-        decode = {"fused_us": dec["decode_fused"]["us_graph"], "naive_us": dec["decode_naive"]["us_graph"],
-                  "speedup": round(dec["decode_naive"]["us_graph"] / dec["decode_fused"]["us_graph"], 3),
-                  "eager": {"fused_us": dec["decode_fused"]["us_eager"], "naive_us": dec["decode_naive"]["us_eager"],
-                            "speedup": round(dec["decode_naive"]["us_eager"] / dec["decode_fused"]["us_eager"], 3)},
-                  "timing": "HIP graph replay of 20 layers x 10 replays (eager: back-to-back launches)"}
-        log(f"decode layer T=64: fused {decode['fused_us']:.2f} us vs naive {decode['naive_us']:.2f} us "
-            f"(x{decode['speedup']:.2f}, graph); eager x{decode['eager']['speedup']:.2f}")
+        graph = {"fused_us": dec["decode_fused"]["us_graph"], "naive_us": dec["decode_naive"]["us_graph"],
+                 "speedup": round(dec["decode_naive"]["us_graph"] / dec["decode_fused"]["us_graph"], 3),
+                 "timing": "HIP graph replay of 20 layers x 10 replays"}
+        eager_py = {"fused_us": dec["decode_fused"]["us_eager"], "naive_us": dec["decode_naive"]["us_eager"],
+                    "speedup": round(dec["decode_naive"]["us_eager"] / dec["decode_fused"]["us_eager"], 3),
+                    "timing": "back-to-back launches from Python ctypes"}
+        decode = {"graph": graph, "eager_python": eager_py, "eager_compiled": dec_compiled,
+                  "desc": "one 64-row decode layer's row ops, f16: 2 residual norms + q/k norm RoPE + SiLU-mul; "
+                          "fused (4 launches) vs the naive unfused HIP baseline (10 launches).  The headline "
+                          "figures are eager_compiled: back-to-back launches from C++ through the host layer, "
+                          "the regime of the reference's batched decode (not graph-captured)"}
+        if dec_compiled:
+            decode.update({k: dec_compiled[k] for k in ("fused_us", "naive_us", "speedup")})
+        log(f"decode layer T=64: eager from C++ x{(dec_compiled or {}).get('speedup')}; graph fused "
+            f"{graph['fused_us']:.2f} us vs naive {graph['naive_us']:.2f} us (x{graph['speedup']:.2f}); "
+            f"eager from Python x{eager_py['speedup']:.2f}")
         pf, pu = ops["rope_kv_prefill"]["us"], ops["rope_kv_prefill_unfused"]["us"]
         df, du = ops["rope_kv_dec"]["us_graph"], ops["rope_kv_dec_unfused"]["us_graph"]
         rope_kv = {"prefill_4096": {"fused_us": pf, "unfused_us": pu, "speedup": round(pu / pf, 3)},
@@ -1019,7 +1161,8 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(args.cpu_seconds)
-        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
+        log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['affinity_cores']} in the mask); "
+            + ", ".join(f"{k} {v['us']:.0f} us" for k, v in cpu["configs"].items()))
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",

@@ -1,7 +1,8 @@
 """GPU parity of exl3r_rope_cs_table + exl3r_rope_cs: RoPE (with the optional head RMSNorm) whose
 per-layer sin / cos evaluation (kernels/rope.cu:69-85) is hoisted into one {cos, sin} table per forward
-pass.  exl3r_rope_cs is checked bit for bit against exl3r_rope on the same inputs (which the rope tests
-pin against the oracle) on every kernel it shares with it: the wave-per-token prefill kernel (NeoX,
+pass.  exl3r_rope_cs is checked against the CPU oracle's rope (<= 2 ulp, the RoPE bound; the oracle
+evaluates cos / sin itself, in double, of the same fp32 angles) and bit for bit against exl3r_rope on the
+same inputs, on every kernel it shares with it: the wave-per-token prefill kernel (NeoX,
 f16 and bf16), the flattened kernel (decode, GPT-J, head_dim 64 / 256) and the generic one (head_dim
 not a multiple of 8), with each position source, attn_factor, q without k, out of place and batches.
 The table itself is checked against the closed form: fl32(cos / sin of the fp32 angle
@@ -13,7 +14,7 @@ import torch
 
 import exl3r
 import exl3r.ffi as ffi
-from _gpu import dev_normal, from_dev
+from _gpu import NTHREADS, assert_close_ulp, dev_normal, from_dev
 from oracle import oracle as orc
 from test_gpu_rope import inv_freq, ragged_position_ids
 
@@ -41,9 +42,17 @@ def run(bsz, seq, hq, hk, hd, R, mode, dt, nwt=None, position=0, positions=None,
     oq = torch.empty_like(q) if out_of_place else q
     ok = (torch.empty_like(k) if out_of_place else k) if with_k else None
     qh = from_dev(q)
+    kh = from_dev(k) if with_k else None
     ffi.rope_cs(q, oq, k, ok, cs, qn, kn, 1e-6, 0.0, mode)
     torch.cuda.synchronize()
     tag = f"rope_cs b{bsz} s{seq} h{hq}/{hk} d{hd} R{R} mode{mode} {dt} w{nwt}"
+    eq_o, ek_o = orc.rope(qh, kh, dt, inv_freq(R), mode, position=position, positions=positions,
+                          position_ids=position_ids.reshape(-1) if position_ids is not None else None,
+                          q_norm=from_dev(qn) if qn is not None else None, k_norm=from_dev(kn) if kn is not None else None,
+                          nwt=nwt if nwt is not None else F16, eps=1e-6, attn=attn, nthreads=NTHREADS)
+    assert_close_ulp(from_dev(oq), eq_o, dt, 2, what=tag + " q vs oracle")
+    if with_k:
+        assert_close_ulp(from_dev(ok), ek_o, dt, 2, what=tag + " k vs oracle")
     assert same(oq, eq), tag + " q vs exl3r_rope"
     if with_k:
         assert same(ok, ek), tag + " k vs exl3r_rope"

@@ -1,8 +1,9 @@
 """GPU parity of exl3r_rope_paged_kv_had: RoPE and the paged KV-cache append on the raw f16 outputs of
 the q / k / v projections, each first given its projection's output rotation had_r_128(y, y, None, svh)
-(src/modules.rs:231, then src/modules.rs:669-704).  Checked bitwise against the unfused GPU calls
-(exl3r_had_r_128 on q, k and v, then exl3r_rope_paged_kv): q, the optional out_k, the whole k / v
-caches and the error flag, on the fused wave-per-token launch and on the fallback, with and without
+(src/modules.rs:231, then src/modules.rs:669-704).  Checked against the CPU oracle's composition
+(oracle had_r_128 of q, k and v with their post-scales, oracle rope, oracle paged_kv_append) and bitwise
+against the unfused GPU calls (exl3r_had_r_128 on q, k and v, then exl3r_rope_paged_kv): q, the optional
+out_k, the whole k / v caches and the error flag, on the fused wave-per-token launch and on the fallback, with and without
 post-scales and head norms, pages crossed, a bad block-table entry, and the errors."""
 import numpy as np
 import pytest
@@ -11,7 +12,7 @@ import torch
 import exl3r
 import exl3r._lib as L
 import exl3r.ffi as ffi
-from _gpu import dev_normal
+from _gpu import NTHREADS, assert_bitwise, assert_close_ulp, dev_normal, from_dev
 from oracle import oracle as orc
 from test_gpu_rope import inv_freq
 from test_gpu_rope_had import svh
@@ -47,6 +48,7 @@ def run(bsz, seq, hq, hk, page, max_blocks, norm=True, with_out_k=True, posts=(T
     btd = torch.from_numpy(bt.astype(np.int32)).cuda()
     # unfused: rotations into copies, then the paged RoPE on them
     n = bsz * seq
+    ukc_in, uvc_in = kc.clone(), vc.clone()
     uq, uk, uv, ukc, uvc = q.clone(), k.clone(), v.clone(), kc.clone(), vc.clone()
     ffi.had_r_128(uq.view(n, hq * hd), uq.view(n, hq * hd), None, sq)
     ffi.had_r_128(uk.view(n, hk * hd), uk.view(n, hk * hd), None, sk)
@@ -63,6 +65,21 @@ def run(bsz, seq, hq, hk, page, max_blocks, norm=True, with_out_k=True, posts=(T
                           sld, q_post_scale=sq, k_post_scale=sk, v_post_scale=sv, err_flag=err)
     torch.cuda.synchronize()
     tag = f"paged_had b{bsz} s{seq} h{hq}/{hk} page{page} norm{int(norm)} outk{int(with_out_k)} posts{posts}"
+    # the oracle: each projection's output rotation, RoPE at the cache positions, the paged append
+    def rot(t, heads, post):
+        return orc.had_r_128(from_dev(t).reshape(n, heads * hd), F16, post=from_dev(post) if post is not None else None,
+                             nthreads=NTHREADS).reshape(bsz, seq, heads, hd)
+    eq, ek = orc.rope(rot(q, hq, sq), rot(k, hk, sk), F16, inv_freq(hd), exl3r.ROPE_NEOX, positions=sl.astype(np.int32),
+                      q_norm=from_dev(qn) if norm else None, k_norm=from_dev(kn) if norm else None, nwt=F16, eps=1e-6,
+                      nthreads=NTHREADS)
+    ekc, evc = from_dev(ukc_in), from_dev(uvc_in)
+    e_err = orc.paged_kv_append(ek, rot(v, hk, sv), F16, ekc, evc, bt, sl, nthreads=NTHREADS)
+    assert_close_ulp(from_dev(oq), eq, F16, 0, what=tag + " q vs oracle")
+    if with_out_k:
+        assert_close_ulp(from_dev(ok), ek, F16, 0, what=tag + " out_k vs oracle")
+    assert_bitwise(from_dev(kc), ekc, what=tag + " k_cache vs oracle")
+    assert_bitwise(from_dev(vc), evc, what=tag + " v_cache vs oracle")
+    assert int(err.item()) == e_err, tag + " err flag vs oracle"
     assert same(oq, uq), tag + " q"
     if with_out_k:
         assert same(ok, uk), tag + " out_k"

@@ -1,7 +1,8 @@
 """GPU parity of exl3r_rope_qg: gated attention's q | g split (exl3r_deinterleave_qg, src/modules.rs:637-646)
 and the q / k head-norm + RoPE that follows (src/modules.rs:669-681) in one pass, q read straight from the
-interleaved projection output and written dense.  Checked bit for bit against exl3r_deinterleave_qg then
-exl3r_rope (both pinned against the oracle by their own tests), with qg left unread-only, and the output
+interleaved projection output and written dense.  Checked against the CPU oracle's composition
+(oracle deinterleave_qg, then oracle rope on its q: <= 2 ulp, the RoPE bound), and bit for bit against
+exl3r_deinterleave_qg then exl3r_rope, with qg left unwritten, and the output
 gate read in place from qg (exl3r_mul_sigmoid with a 2 * head_dim row stride) against the gate from the
 deinterleave.  Covers the wave-per-token prefill kernel (f16 and bf16, head_dim 128 and 256 with partial
 rotary), decode-sized launches, GPT-J, a strided qg, the generic kernel, and the errors."""
@@ -11,7 +12,7 @@ import torch
 
 import exl3r
 import exl3r.ffi as ffi
-from _gpu import dev_normal, from_dev
+from _gpu import NTHREADS, assert_close_ulp, dev_normal, from_dev
 from oracle import oracle as orc
 from test_gpu_rope import inv_freq, ragged_position_ids
 
@@ -35,6 +36,7 @@ def run(bsz, seq, hq, hk, hd, R, mode, dt, nwt=None, cb=0.0, position=0, positio
     pos_d = torch.from_numpy(positions).cuda() if positions is not None else None
     pid_d = torch.from_numpy(position_ids).cuda() if position_ids is not None else None
     before = from_dev(qg_full).copy()
+    kh = from_dev(k)
     # reference: the split, then RoPE in place on the dense q
     q = torch.empty((bsz, seq, hq, hd), device="cuda", dtype=qg.dtype)
     g = torch.empty((bsz, seq, hq * hd), device="cuda", dtype=qg.dtype)
@@ -47,6 +49,17 @@ def run(bsz, seq, hq, hk, hd, R, mode, dt, nwt=None, cb=0.0, position=0, positio
     ffi.rope_qg(qg, oq, ok, ok, f, position, pos_d, qn, kn, 1e-6, cb, mode, 1.0, position_ids=pid_d)
     torch.cuda.synchronize()
     tag = f"rope_qg b{bsz} s{seq} h{hq}/{hk} d{hd} R{R} mode{mode} {dt} w{nwt} pad{pad}"
+    # the oracle: split the interleaved rows, then rope the q half (and k)
+    oq_h, _ = orc.deinterleave_qg(np.ascontiguousarray(before.reshape(bsz * seq, -1)[:, :hq * 2 * hd]), hq, hd,
+                                  nthreads=NTHREADS)
+    eq_o, ek_o = orc.rope(oq_h.reshape(bsz, seq, hq, hd), kh, dt, inv_freq(R), mode, position=position,
+                          positions=positions,
+                          position_ids=position_ids.reshape(-1) if position_ids is not None else None,
+                          q_norm=from_dev(qn) if qn is not None else None,
+                          k_norm=from_dev(kn) if kn is not None else None,
+                          nwt=nwt if nwt is not None else F16, eps=1e-6, cb=cb, nthreads=NTHREADS)
+    assert_close_ulp(from_dev(oq), eq_o, dt, 2, what=tag + " q vs oracle")
+    assert_close_ulp(from_dev(ok), ek_o, dt, 2, what=tag + " k vs oracle")
     assert same(oq, q), tag + " q vs deinterleave + rope"
     assert same(ok, ek), tag + " k vs rope"
     assert np.array_equal(from_dev(qg_full), before), tag + " qg must not be written"
