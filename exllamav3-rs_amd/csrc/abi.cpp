@@ -93,6 +93,8 @@ extern "C" void exl3r_tune_rope_tok(int use, int hpl, int wgs_per_cu)
     exl3r::tuning().rope_wgs_per_cu = wgs_per_cu;
 }
 
+extern "C" void exl3r_tune_rope_nx(int passes) { exl3r::tuning().rope_nx = passes; }
+
 extern "C" void exl3r_tune_sample(int rows_min, int threads)
 {
     exl3r::tuning().sample_rows_min = rows_min;

@@ -610,6 +610,306 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
     while (step(A, B) && step(B, A)) {}
 }
 
+// head_dim 128 at prefill sizes, NeoX with rotary_dim 128 (Qwen3, Llama) or GPT-J with any rotary_dim:
+// 8 lanes per head, lane j of a head's group holding elements [8j, 8j + 8) and [64 + 8j, 64 + 8j + 8),
+// so every rotary pair sits in one lane -- NeoX (t, t + 64) across the two chunks, GPT-J (2t, 2t + 1)
+// inside a chunk -- with no partner exchange; the head sum is a 3-step DPP butterfly, and each 16-byte
+// load or store instruction covers whole 128-byte lines of 8 heads.  An item is one pass
+// of 8 heads of one token (items in token order, a token's q passes then its k pass).  Each wave
+// walks items i, i + W, i + 2W, ... (W waves in the grid), so the waves in flight sweep the rows in
+// order; the next item's loads (and its {cos, sin} table row) are issued before the current item is
+// computed.  Evaluated rotary pairs: one sin / cos per lane into the wave's LDS row, per item.
+template <class IO, int NORM, int SRC, int P>
+struct NxItem
+{
+    typename IO::Vec lo[P], hi[P];
+    float4 cs[4];                // SRC_CS: the lane's 8 {cos, sin} pairs as loaded
+    int64_t tok;
+    int slice;
+    int pos;                     // SRC_FREQ: the token's position
+};
+
+template <class IO, int MODE, int NORM, int SRC, bool QOUT, int P>
+__global__ __launch_bounds__(256) void k_rope_nx(RopeArgs a, int nslice)
+{
+    extern __shared__ float2 cs[];            // [4 waves][64] (SRC_FREQ)
+    // Norm weights with the constant bias folded in, q then k: h(w + h(cb)) (NORM_HALF) or w + cb (NORM_F32).
+    __shared__ __align__(16) float wsh[256];
+    static_assert(SRC == SRC_FREQ || SRC == SRC_CS, "angle tables take the flattened kernel");
+    const int l64 = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t W = (int64_t)gridDim.x * 4;
+    const int64_t items = a.tokens * nslice;
+    const int grp = l64 >> 3;                 // head of a pass held by this lane's group of 8
+    const int e0 = (l64 & 7) * 8;             // the lane's chunks: [e0, e0 + 8) and [e0 + 64, e0 + 72)
+    const int64_t q_hs = a.q_hs, k_hs = a.k_hs, q_ts = a.q_ts, k_ts = a.k_ts;
+    const int hq = a.hq, H = a.hq + a.hk;
+    const int R = a.R, R2 = a.R >> 1;
+    using Item = NxItem<IO, NORM, SRC, P>;
+
+    // Loads of one item: the lane's two chunks of head (slice * P + p) * 8 + grp for each of the P passes,
+    // and its rotary pairs (SRC_CS) or the token's position (SRC_FREQ).
+    auto issue = [&](Item& t, int64_t item) {
+        t.tok = item / nslice;
+        t.slice = (int)(item - t.tok * nslice);
+        #pragma unroll
+        for (int p = 0; p < P; ++p)
+        {
+            const int h = (t.slice * P + p) * 8 + grp;
+            if (h < H)
+            {
+                const char* base = h < hq ? (const char*)a.q + (t.tok * q_ts + (int64_t)h * q_hs) * IO::bytes
+                                          : (const char*)a.k + (t.tok * k_ts + (int64_t)(h - hq) * k_hs) * IO::bytes;
+                t.lo[p] = load8s<IO>(base, e0);
+                t.hi[p] = load8s<IO>(base, e0 + 64);
+            }
+        }
+        if constexpr (SRC == SRC_CS)
+        {
+            // NeoX: pairs e0 .. e0 + 7; GPT-J: pairs e0/2 .. e0/2 + 3 (lo chunk) and 32 + e0/2 .. (hi chunk)
+            const float2* row = a.cst + t.tok * R2;
+            if constexpr (MODE == EXL3R_ROPE_NEOX)
+            {
+                #pragma unroll
+                for (int i = 0; i < 4; ++i) t.cs[i] = ((const float4*)(row + e0))[i];
+            }
+            else
+            {
+                #pragma unroll
+                for (int i = 0; i < 2; ++i)
+                {
+                    t.cs[i] = e0 / 2 + 2 * i < R2 ? ((const float4*)(row + e0 / 2))[i] : make_float4(0, 0, 0, 0);
+                    t.cs[2 + i] = 32 + e0 / 2 + 2 * i < R2 ? ((const float4*)(row + 32 + e0 / 2))[i] : make_float4(0, 0, 0, 0);
+                }
+            }
+        }
+        else
+            t.pos = token_position(a, (int)t.tok);
+    };
+
+    if constexpr (NORM != NORM_NONE)
+    {
+        const int i = threadIdx.x, e = i & 127;
+        const void* w = i < 128 ? a.qw : a.kw;
+        if constexpr (NORM == NORM_HALF)
+        {
+            _Float16* wh = (_Float16*)wsh;
+            wh[i] = w ? ((const _Float16*)w)[e] + to_f16(a.cb) : (_Float16)0.0f;
+        }
+        else
+            wsh[i] = w ? load1(w, a.wt, e) + a.cb : 0.0f;
+        __syncthreads();
+    }
+
+    // Head norm, rotation and stores of one pass (lo / hi: the lane's chunks of head h).
+    auto pass = [&](int64_t tok, int h, typename IO::Vec& lo, typename IO::Vec& hi, const float (&c)[8],
+                    const float (&s)[8]) {
+        const bool act = h < H;
+        const bool isq = h < hq;
+        if (!act)
+        {
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) lo.a[i] = hi.a[i] = 0;
+        }
+        if constexpr (NORM != NORM_NONE)
+        {
+            float fl[8], fh[8];
+            unpack8<IO>(lo, fl);
+            unpack8<IO>(hi, fh);
+            // fp64 sum of squares (as rope_head: exact for 16-bit data, one rounding to fp32)
+            double ss = 0.0;
+            #pragma unroll
+            for (int j = 0; j < 8; ++j) ss = fma((double)fl[j], (double)fl[j], ss);
+            #pragma unroll
+            for (int j = 0; j < 8; ++j) ss = fma((double)fh[j], (double)fh[j], ss);
+            ss = group_sum64<8>(ss);
+            const float mean = (float)ss * a.inv_hd;     // head_dim 128: an exact multiply
+            const float rmf = 1.0f / sqrtf(mean + a.eps);
+            const int wo = (isq ? 0 : 128) + e0;
+            if constexpr (NORM == NORM_HALF)
+            {
+                const u32x4 wl = *(const u32x4*)((const _Float16*)wsh + wo);
+                const u32x4 wh = *(const u32x4*)((const _Float16*)wsh + wo + 64);
+                #pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    const f16x2 nl = { to_f16(fl[2 * i] * rmf), to_f16(fl[2 * i + 1] * rmf) };
+                    const f16x2 nh = { to_f16(fh[2 * i] * rmf), to_f16(fh[2 * i + 1] * rmf) };
+                    // (uint32_t) first: a bit_cast of a single u32x4 element is lowered as a broadcast of
+                    // element 0 by hipcc (ROCm 7.2) with the packed-fp32 forms disabled.
+                    lo.a[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, (uint32_t)wl[i]) * nl);
+                    hi.a[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, (uint32_t)wh[i]) * nh);
+                }
+            }
+            else
+            {
+                // The product stays an fp32 value before the io rounding (opaque: no single-rounding
+                // mixed multiply-convert).
+                #pragma unroll
+                for (int j = 0; j < 8; ++j)
+                {
+                    fl[j] = opaque((fl[j] * rmf) * wsh[wo + j]);
+                    fh[j] = opaque((fh[j] * rmf) * wsh[wo + 64 + j]);
+                }
+                lo = pack8<IO>(fl);
+                hi = pack8<IO>(fh);
+            }
+        }
+        {
+            // r1 = fl(fl(v1 c) - fl(v2 s)), r2 = fl(fl(v2 c) + fl(v1 s)), each rounded once to io.
+            #pragma clang fp contract(off)
+            float fl[8], fh[8];
+            unpack8<IO>(lo, fl);
+            unpack8<IO>(hi, fh);
+            if constexpr (MODE == EXL3R_ROPE_NEOX)
+            {
+                #pragma unroll
+                for (int j = 0; j < 8; ++j)
+                {
+                    const float x = fl[j], y = fh[j];
+                    fl[j] = opaque(x * c[j] - y * s[j]);
+                    fh[j] = opaque(y * c[j] + x * s[j]);
+                }
+            }
+            else
+            {
+                // c / s [0, 4): the lo chunk's pairs, [4, 8): the hi chunk's; dims >= rotary_dim pass through
+                #pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    if (e0 + 2 * i < R)
+                    {
+                        const float x = fl[2 * i], y = fl[2 * i + 1];
+                        fl[2 * i] = opaque(x * c[i] - y * s[i]);
+                        fl[2 * i + 1] = opaque(y * c[i] + x * s[i]);
+                    }
+                    if (64 + e0 + 2 * i < R)
+                    {
+                        const float x = fh[2 * i], y = fh[2 * i + 1];
+                        fh[2 * i] = opaque(x * c[4 + i] - y * s[4 + i]);
+                        fh[2 * i + 1] = opaque(y * c[4 + i] + x * s[4 + i]);
+                    }
+                }
+            }
+            lo = pack8<IO>(fl);
+            hi = pack8<IO>(fh);
+        }
+        if (!act) return;
+        char* ob;
+        int32_t oo;
+        if (isq)
+        {
+            ob = (char*)a.oq + tok * (QOUT ? a.oq_ts : q_ts) * IO::bytes;
+            oo = (int32_t)((int64_t)h * (QOUT ? a.oq_hs : q_hs)) + e0;
+        }
+        else
+        {
+            ob = (char*)a.ok + tok * k_ts * IO::bytes;
+            oo = (int32_t)((int64_t)(h - hq) * k_hs) + e0;
+        }
+        store8<IO>(ob, oo, lo);
+        store8<IO>(ob, oo + 64, hi);
+    };
+
+    auto compute = [&](Item& t) {
+        float c[8], s[8];
+        if constexpr (SRC == SRC_CS)
+        {
+            #pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                c[2 * i] = t.cs[i].x;
+                s[2 * i] = t.cs[i].y;
+                c[2 * i + 1] = t.cs[i].z;
+                s[2 * i + 1] = t.cs[i].w;
+            }
+        }
+        else
+        {
+            float2* row = cs + wave * 64;
+            wave_lds_sync();
+            if (l64 < R2) row[l64] = rope_cs<SRC_FREQ>(a, l64, (int)t.tok, t.pos);
+            wave_lds_sync();
+            #pragma unroll
+            for (int j = 0; j < 8; ++j)
+            {
+                // NeoX: pair e0 + j; GPT-J: pair e0/2 + j (lo chunk, j < 4) or 32 + e0/2 + j - 4 (hi chunk)
+                const int tp = MODE == EXL3R_ROPE_NEOX ? e0 + j : j < 4 ? e0 / 2 + j : 32 + e0 / 2 + (j - 4);
+                const float2 x = tp < R2 ? row[tp] : make_float2(0.0f, 0.0f);
+                c[j] = x.x;
+                s[j] = x.y;
+            }
+        }
+        #pragma unroll
+        for (int p = 0; p < P; ++p) pass(t.tok, (t.slice * P + p) * 8 + grp, t.lo[p], t.hi[p], c, s);
+    };
+
+    int64_t item = (int64_t)blockIdx.x * 4 + wave;
+    if (item >= items) return;
+    Item A, B;
+    issue(A, item);
+    for (;;)
+    {
+        // Issue the next item's loads, then finish this one (the loop alternates the two buffers).
+        const int64_t nb = item + W;
+        if (nb < items) issue(B, nb);
+        compute(A);
+        if (nb >= items) break;
+        const int64_t na = nb + W;
+        if (na < items) issue(A, na);
+        compute(B);
+        if (na >= items) break;
+        item = na;
+    }
+}
+
+// The k_rope_nx launch: head_dim 128 at prefill sizes (NeoX with rotary_dim 128, GPT-J with rotary_dim a
+// multiple of 4), plain RoPE (no paged append, no output rotation, no angle table), with a 16-byte aligned
+// {cos, sin} table when one is given.  A grid of
+// `wgs` four-wave workgroups per CU walks the items (one item per wave when 0).
+static bool rope_nx_ok(const RopeArgs& a, int rope_mode)
+{
+    const Tuning& tu = tuning();
+    // GPT-J: rotary_dim % 4 == 0 keeps each 16-byte table read (two pairs) inside the token's row.
+    if (tu.rope_nx < 0 || a.hd != 128 || (rope_mode == EXL3R_ROPE_NEOX ? a.R != 128 : a.R % 4 != 0) || a.kc || a.table)
+        return false;
+    if (a.q_post || a.k_post || a.v_post) return false;
+    if (a.cst && ((uintptr_t)a.cst & 15)) return false;
+    return tu.rope_nx > 0 || a.tokens >= 1024;
+}
+
+template <class IO, int MODE, int NORM, int SRC, bool QOUT, int P>
+static void launch_rope_nx_p(const RopeArgs& a, hipStream_t s)
+{
+    const int nslice = ((a.hq + a.hk + 7) / 8 + P - 1) / P;
+    const int64_t items = a.tokens * nslice;
+    const size_t lds = SRC == SRC_FREQ ? 4 * 64 * sizeof(float2) : 0;
+    // Grid: the workgroups resident at once (per CU, from the occupancy of this instance), each wave
+    // walking its items i, i + W, ...
+    static const int resident = [lds] {   // workgroups per CU (per template instance; thread-safe init)
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_rope_nx<IO, MODE, NORM, SRC, QOUT, P>, 256, lds) != hipSuccess || nb < 1)
+            nb = 4;
+        return nb;
+    }();
+    const int wpc = tuning().rope_wgs_per_cu;
+    int64_t blocks = (int64_t)(wpc > 0 ? wpc : resident) * device_cus();
+    if (blocks > (items + 3) / 4) blocks = (items + 3) / 4;
+    if (blocks > kMaxGridX) blocks = kMaxGridX;
+    k_rope_nx<IO, MODE, NORM, SRC, QOUT, P><<<(unsigned)blocks, 256, lds, s>>>(a, nslice);
+}
+
+// Passes per item: two (the token's sin / cos or table row shared by two passes), one when out_q has
+// its own layout (exl3r_rope_qg).  MI355X, C4 NeoX f16 (us, two / one / wave-per-token kernel): evaluated
+// 32.9 / 33.4 / 38.4, from the table 32.6 / 33.6 / 36.5; Qwen3.5 q | g split 37.5 / 36.2 / 37.7.
+template <class IO, int MODE, int NORM, int SRC, bool QOUT>
+static void launch_rope_nx(const RopeArgs& a, hipStream_t s)
+{
+    const int tp = tuning().rope_nx;
+    if (tp == 2 || (tp == 0 && !QOUT)) launch_rope_nx_p<IO, MODE, NORM, SRC, QOUT, 2>(a, s);
+    else launch_rope_nx_p<IO, MODE, NORM, SRC, QOUT, 1>(a, s);
+}
+
 // Generic fallback (any even head_dim / rotary_dim, any alignment): one workgroup per token, heads
 // walked serially through an LDS copy.
 __global__ __launch_bounds__(256) void k_rope_generic(RopeArgs a, int dt, int mode, int norm)
@@ -765,6 +1065,14 @@ template <class IO, int MODE, int NORM>
 static void launch_rope_vec(const RopeArgs& a, int lph, hipStream_t s)
 {
     const Tuning& tu = tuning();
+    if (rope_nx_ok(a, MODE))
+    {
+        const bool qout = a.oq_ts != a.q_ts || a.oq_hs != a.q_hs;
+        if (a.cst) launch_rope_nx<IO, MODE, NORM, SRC_CS, false>(a, s);
+        else if (qout) launch_rope_nx<IO, MODE, NORM, SRC_FREQ, true>(a, s);
+        else launch_rope_nx<IO, MODE, NORM, SRC_FREQ, false>(a, s);
+        return;
+    }
     if (a.cst)
     {
         // A {cos, sin} table (exl3r_rope_cs, or the cs_table of the paged / rotating entries): the

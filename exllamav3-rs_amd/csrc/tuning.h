@@ -17,6 +17,9 @@ EXL3R_API void exl3r_tune_act(int unroll, int threads, int blocks_per_cu);
 EXL3R_API void exl3r_tune_rope(int iters);
 /* wave-per-token RoPE kernel: use 0 auto / 1 never / 2 always; heads per lane in flight 2, 4, 6, 8 (0 auto) */
 EXL3R_API void exl3r_tune_rope_tok(int use, int hpl, int wgs_per_cu);
+/* NeoX RoPE at head_dim = rotary_dim = 128, 8 lanes per head: 0 auto, -1 never, 1..3 always with that many
+ * 8-head passes per wave */
+EXL3R_API void exl3r_tune_rope_nx(int passes);
 /* argmax / Gumbel sampling: rows from which a workgroup owns a whole row (0: 512), and its lanes (256, 512, 1024) */
 EXL3R_API void exl3r_tune_sample(int rows_min, int threads);
 /* Hadamard: 128-blocks per 16-lane group (1, 2, 4; 0 auto) */

@@ -73,6 +73,7 @@ TUNE_PROTOTYPES = {
     "exl3r_tune_act": (None, [_i, _i, _i]),
     "exl3r_tune_rope": (None, [_i]),
     "exl3r_tune_rope_tok": (None, [_i, _i, _i]),
+    "exl3r_tune_rope_nx": (None, [_i]),
     "exl3r_tune_sample": (None, [_i, _i]),
     "exl3r_tune_had": (None, [_i]),
     "exl3r_tune_embed": (None, [_i]),
@@ -147,6 +148,7 @@ def tuned():
         lib.exl3r_tune_act(0, 0, 0)
         lib.exl3r_tune_rope(0)
         lib.exl3r_tune_rope_tok(0, 0, 0)
+        lib.exl3r_tune_rope_nx(0)
         lib.exl3r_tune_sample(0, 0)
         lib.exl3r_tune_had(0)
         lib.exl3r_tune_embed(0)

@@ -1,0 +1,133 @@
+"""GPU parity of the head_dim-128 RoPE kernel with 8 lanes per head (k_rope_nx: every rotary pair in one
+lane, items of one or two 8-head passes walked by a resident grid), forced through the launch-shape hook
+of the sweep/test build on shapes the size rule would not give it: few tokens, head counts that mix q and
+k heads inside a pass or leave a pass part-empty, q only, GPT-J at several rotary dims, every weight
+dtype, no norm, out of place, packed q/k/v views, each position source, grids of 1 and 2 workgroups per
+CU (so each wave walks many items), the {cos, sin} table, and out_q in its own layout (exl3r_rope_qg).
+Each case is checked against the CPU oracle (<= 2 ulp, the RoPE bound)."""
+import numpy as np
+import pytest
+import torch
+
+import exl3r
+import exl3r._lib as L
+import exl3r.ffi as ffi
+from _gpu import NTHREADS, assert_close_ulp, dev_normal, from_dev
+from oracle import oracle as orc
+from test_gpu_rope import inv_freq, ragged_position_ids, run
+
+pytestmark = pytest.mark.gpu
+
+F16, BF16, F32 = orc.F16, orc.BF16, orc.F32
+
+
+@pytest.fixture
+def nx():
+    """Forces the 8-lane kernel with `passes` (1, 2) passes per item on a grid of `wpc` workgroups per CU
+    (0: the resident grid)."""
+    with L.tuned() as lib:
+        def set_(passes, wpc=0):
+            lib.exl3r_tune_rope_nx(passes)
+            lib.exl3r_tune_rope_tok(0, 0, wpc)
+        yield set_
+
+
+@pytest.mark.parametrize("passes", [1, 2])
+@pytest.mark.parametrize("hq,hk", [(64, 8), (6, 3), (1, 1), (12, 0), (20, 7), (9, 8)])
+def test_head_counts(nx, passes, hq, hk):
+    """(6, 3), (20, 7): q and k heads inside one pass; (1, 1), (9, 8): mostly empty passes; (12, 0): q only."""
+    nx(passes)
+    run(2, 61, hq, hk, 128, 128, exl3r.ROPE_NEOX, F16, position=300, with_k=hk > 0, seed=hq * 10 + hk)
+    run(1, 45, hq, hk, 128, 64, exl3r.ROPE_GPTJ, BF16, nwt=F32, position=7, with_k=hk > 0, seed=hq + hk + 1)
+
+
+@pytest.mark.parametrize("passes", [1, 2])
+@pytest.mark.parametrize("R,mode", [(128, exl3r.ROPE_NEOX), (128, exl3r.ROPE_GPTJ), (64, exl3r.ROPE_GPTJ),
+                                    (96, exl3r.ROPE_GPTJ), (4, exl3r.ROPE_GPTJ)])
+@pytest.mark.parametrize("dt,nwt", [(F16, F16), (F16, F32), (F16, BF16), (BF16, BF16), (BF16, F16)])
+def test_modes_and_dtypes(nx, passes, R, mode, dt, nwt):
+    nx(passes)
+    run(1, 130, 10, 2, 128, R, mode, dt, nwt=nwt, position=1234, cb=1.0 if nwt != F32 else 0.5, seed=R + dt + nwt)
+
+
+@pytest.mark.parametrize("passes", [1, 2])
+def test_no_norm_out_of_place_attn(nx, passes):
+    nx(passes)
+    run(1, 70, 8, 2, 128, 128, exl3r.ROPE_NEOX, F16, norm=False, position=5000, out_of_place=True, attn=0.75)
+    run(3, 20, 8, 0, 128, 64, exl3r.ROPE_GPTJ, BF16, norm=False, with_k=False, positions=np.array([0, 1, 40000], np.int32))
+
+
+@pytest.mark.parametrize("passes,wpc", [(1, 1), (2, 1), (2, 2), (1, 0)])
+def test_c4_grids(nx, passes, wpc):
+    """Config 4's ragged prefill (~4.6k tokens, 64 / 8 heads) on small persistent grids: every wave walks
+    dozens of items through both buffers."""
+    nx(passes, wpc)
+    pid = ragged_position_ids(3)[None, :]
+    run(1, pid.size, 64, 8, 128, 128, exl3r.ROPE_NEOX, F16, position_ids=pid, seed=31 + passes)
+    run(1, pid.size, 64, 8, 128, 64, exl3r.ROPE_GPTJ, F16, position_ids=pid, seed=33 + passes)
+
+
+@pytest.mark.parametrize("passes", [1, 2])
+def test_packed_qkv_views(nx, passes):
+    """q and k as views into one [bsz, seq, hq + 2 hk, hd] projection output; the v heads stay unwritten."""
+    nx(passes)
+    bsz, seq, hq, hk, hd = 2, 37, 16, 4, 128
+    qkv = dev_normal((bsz, seq, hq + 2 * hk, hd), 0.0, 1.0, F16, 21)
+    qn, kn = dev_normal((hd,), 1.0, 0.1, F16, 22), dev_normal((hd,), 1.0, 0.1, F16, 23)
+    before = from_dev(qkv)
+    q, k = qkv[:, :, :hq], qkv[:, :, hq:hq + hk]
+    f = inv_freq(128)
+    pos = np.array([3, 20000], np.int32)
+    ffi.rope(q, q, k, k, torch.from_numpy(f).cuda(), 0, torch.from_numpy(pos).cuda(), qn, kn, 1e-6, 0.0,
+             exl3r.ROPE_NEOX, 1.0)
+    torch.cuda.synchronize()
+    eq, ek = orc.rope(np.ascontiguousarray(before[:, :, :hq]), np.ascontiguousarray(before[:, :, hq:hq + hk]), F16, f,
+                      exl3r.ROPE_NEOX, positions=pos, q_norm=from_dev(qn), k_norm=from_dev(kn), nwt=F16, eps=1e-6,
+                      nthreads=NTHREADS)
+    after = from_dev(qkv)
+    assert_close_ulp(after[:, :, :hq], eq, F16, 2, what="packed q")
+    assert_close_ulp(after[:, :, hq:hq + hk], ek, F16, 2, what="packed k")
+    assert np.array_equal(after[:, :, hq + hk:], before[:, :, hq + hk:]), "v heads modified"
+
+
+@pytest.mark.parametrize("passes", [1, 2])
+@pytest.mark.parametrize("mode,R", [(exl3r.ROPE_NEOX, 128), (exl3r.ROPE_GPTJ, 64)])
+def test_cs_table(nx, passes, mode, R):
+    """exl3r_rope_cs on the forced kernel against the oracle (the table row read per item)."""
+    nx(passes)
+    bsz, seq, hq, hk, hd = 3, 90, 10, 3, 128
+    q = dev_normal((bsz, seq, hq, hd), 0, 1, F16, 40)
+    k = dev_normal((bsz, seq, hk, hd), 0, 1, F16, 41)
+    qn, kn = dev_normal((hd,), 1, 0.1, F16, 42), dev_normal((hd,), 1, 0.1, F16, 43)
+    f = inv_freq(R)
+    pos = np.array([7, 900, 31000], np.int32)
+    qh, kh = from_dev(q), from_dev(k)
+    cs = ffi.rope_cs_table(bsz, seq, torch.from_numpy(f).cuda(), 0, torch.from_numpy(pos).cuda(), None, 0.8)
+    ffi.rope_cs(q, q, k, k, cs, qn, kn, 1e-6, 0.0, mode)
+    torch.cuda.synchronize()
+    eq, ek = orc.rope(qh, kh, F16, f, mode, positions=pos, q_norm=from_dev(qn), k_norm=from_dev(kn), nwt=F16,
+                      eps=1e-6, attn=0.8, nthreads=NTHREADS)
+    assert_close_ulp(from_dev(q), eq, F16, 2, what=f"rope_cs nx{passes} mode{mode} q")
+    assert_close_ulp(from_dev(k), ek, F16, 2, what=f"rope_cs nx{passes} mode{mode} k")
+
+
+@pytest.mark.parametrize("passes", [1, 2])
+def test_qg_out_layout(nx, passes):
+    """exl3r_rope_qg (q read from the q halves of [q | g] heads, written to a dense out_q) on the forced
+    kernel against the oracle's deinterleave then rope."""
+    nx(passes)
+    bsz, seq, hq, hk, hd = 1, 200, 12, 2, 128
+    qg = dev_normal((bsz, seq, hq, 2 * hd), 0, 1, F16, 50)
+    k = dev_normal((bsz, seq, hk, hd), 0, 1, F16, 51)
+    qn, kn = dev_normal((hd,), 1, 0.1, F16, 52), dev_normal((hd,), 1, 0.1, F16, 53)
+    f = inv_freq(128)
+    qgh, kh = from_dev(qg), from_dev(k)
+    oq = torch.empty((bsz, seq, hq, hd), device="cuda", dtype=torch.float16)
+    ffi.rope_qg(qg, oq, k, k, torch.from_numpy(f).cuda(), 9, None, qn, kn, 1e-6, 1.0, exl3r.ROPE_NEOX, 1.0)
+    torch.cuda.synchronize()
+    qh, _ = orc.deinterleave_qg(qgh.reshape(bsz * seq, -1), hq, hd, nthreads=NTHREADS)
+    eq, ek = orc.rope(qh.reshape(bsz, seq, hq, hd), kh, F16, f, exl3r.ROPE_NEOX, position=9, q_norm=from_dev(qn),
+                      k_norm=from_dev(kn), nwt=F16, eps=1e-6, cb=1.0, nthreads=NTHREADS)
+    assert_close_ulp(from_dev(oq), eq, F16, 2, what=f"rope_qg nx{passes} q")
+    assert_close_ulp(from_dev(k), ek, F16, 2, what=f"rope_qg nx{passes} k")
+    assert np.array_equal(from_dev(qg), qgh), "qg modified"
