@@ -841,7 +841,9 @@ __global__ __launch_bounds__(256) void k_rope_nx(RopeArgs a, int nslice)
             }
         }
         #pragma unroll
-        for (int p = 0; p < P; ++p) pass(t.tok, (t.slice * P + p) * 8 + grp, t.lo[p], t.hi[p], c, s);
+        for (int p = 0; p < P; ++p)
+            if ((t.slice * P + p) * 8 < H)    // wave-uniform: a pass past the last head is skipped whole
+                pass(t.tok, (t.slice * P + p) * 8 + grp, t.lo[p], t.hi[p], c, s);
     };
 
     int64_t item = (int64_t)blockIdx.x * 4 + wave;
@@ -899,14 +901,15 @@ static void launch_rope_nx_p(const RopeArgs& a, hipStream_t s)
     k_rope_nx<IO, MODE, NORM, SRC, QOUT, P><<<(unsigned)blocks, 256, lds, s>>>(a, nslice);
 }
 
-// Passes per item: two (the token's sin / cos or table row shared by two passes), one when out_q has
-// its own layout (exl3r_rope_qg).  MI355X, C4 NeoX f16 (us, two / one / wave-per-token kernel): evaluated
-// 32.9 / 33.4 / 38.4, from the table 32.6 / 33.6 / 36.5; Qwen3.5 q | g split 37.5 / 36.2 / 37.7.
+// Passes per item: one for NeoX, two for GPT-J (its token's sin / cos or table row shared by two passes).
+// MI355X, C4 f16, 10 interleaved windows on one box (us, one / two passes / the wave-per-token or flattened
+// kernel): NeoX evaluated 32.9 / 33.9 / 38.1, from the table 31.7 / 32.9 / 36.4, GPT-J 35.4 / 34.9 / 35.3;
+// Qwen3.5 q | g split 36.4 / 36.6 / 37.4.
 template <class IO, int MODE, int NORM, int SRC, bool QOUT>
 static void launch_rope_nx(const RopeArgs& a, hipStream_t s)
 {
     const int tp = tuning().rope_nx;
-    if (tp == 2 || (tp == 0 && !QOUT)) launch_rope_nx_p<IO, MODE, NORM, SRC, QOUT, 2>(a, s);
+    if (tp == 2 || (tp == 0 && MODE == EXL3R_ROPE_GPTJ && !QOUT)) launch_rope_nx_p<IO, MODE, NORM, SRC, QOUT, 2>(a, s);
     else launch_rope_nx_p<IO, MODE, NORM, SRC, QOUT, 1>(a, s);
 }
 

@@ -179,6 +179,24 @@ OwnedTensor OwnedTensor::empty(DType dt, std::vector<int64_t> shape)
     return o;
 }
 
+Arena::Arena(size_t bytes) : buf_(bytes) {}
+
+Tensor Arena::empty(DType dt, std::vector<int64_t> shape)
+{
+    int64_t n = 1;
+    for (int64_t d : shape)
+    {
+        require(d >= 0, "Arena::empty: negative dimension");
+        n *= d;
+    }
+    const size_t bytes = (size_t)n * dtype_size(dt);
+    const size_t off = (off_ + 255) & ~(size_t)255;
+    require(off + bytes <= buf_.bytes(), "Arena::empty: " + std::to_string(bytes) + " bytes do not fit (" +
+                                             std::to_string(buf_.bytes() - off_) + " free)");
+    off_ = off + bytes;
+    return Tensor((char*)buf_.data() + off, dt, std::move(shape));
+}
+
 // ------------------------------------------------------------------------------------------------
 // ffi
 
@@ -652,37 +670,58 @@ void embedding_rms_norm(const Tensor& table, const Tensor& ids, const Tensor* h,
 // ------------------------------------------------------------------------------------------------
 // Modules
 
-OwnedTensor RmsNorm::forward(const Tensor& x, const Stream& s) const
+Tensor RmsNorm::forward(const Tensor& x, Arena& arena, const Stream& s) const
 {
-    OwnedTensor y = OwnedTensor::empty(DType::F16, x.shape);
-    ffi::rms_norm(x, &weight_, y.t, eps_, constant_bias_, constant_scale_, s);
+    Tensor y = arena.empty(DType::F16, x.shape);
+    forward_into(x, y, s);
     return y;
 }
 
-OwnedTensor RmsNorm::forward_res(const Tensor& r, const Tensor* add, const Stream& s) const
+void RmsNorm::forward_into(const Tensor& x, const Tensor& y, const Stream& s) const
 {
-    if (!add) return forward(r, s);
+    ffi::rms_norm(x, &weight_, y, eps_, constant_bias_, constant_scale_, s);
+}
+
+Tensor RmsNorm::forward_res(const Tensor& r, const Tensor* add, Arena& arena, const Stream& s) const
+{
+    Tensor y = arena.empty(DType::F16, r.shape);
+    forward_res_into(r, add, y, s);
+    return y;
+}
+
+void RmsNorm::forward_res_into(const Tensor& r, const Tensor* add, const Tensor& y, const Stream& s) const
+{
+    if (!add) return forward_into(r, y, s);
     require(add->shape == r.shape, "RmsNorm::forward_res: add and residual shapes differ");
-    OwnedTensor y = OwnedTensor::empty(DType::F16, r.shape);
-    ffi::rms_norm_res_in(*add, &weight_, y.t, r, eps_, constant_bias_, constant_scale_, s);
-    return y;
+    ffi::rms_norm_res_in(*add, &weight_, y, r, eps_, constant_bias_, constant_scale_, s);
 }
 
-OwnedTensor Embedding::forward(const Tensor& ids, const Stream& s) const
+Tensor Embedding::forward(const Tensor& ids, Arena& arena, const Stream& s) const
 {
     std::vector<int64_t> shape = ids.shape;
     shape.push_back(weight_.size(1));
-    OwnedTensor out = OwnedTensor::empty(out_kind_, shape);
-    ffi::embedding(weight_, ids, out.t, nullptr, s);
+    Tensor out = arena.empty(out_kind_, shape);
+    forward_into(ids, out, s);
     return out;
 }
 
-OwnedTensor GatedMlp::activate(const Tensor& g, const Tensor& u, Act act, float act_limit, const Stream& s)
+void Embedding::forward_into(const Tensor& ids, const Tensor& out, const Stream& s) const
 {
-    OwnedTensor a = OwnedTensor::empty(g.dtype, g.shape);
-    if (act == Act::Silu) ffi::silu_mul(g, u, a.t, act_limit, s);
-    else ffi::gelu_mul(g, u, a.t, act_limit, s);
+    ffi::embedding(weight_, ids, out, nullptr, s);
+}
+
+Tensor GatedMlp::activate(const Tensor& g, const Tensor& u, Act act, float act_limit, Arena& arena, const Stream& s)
+{
+    Tensor a = arena.empty(g.dtype, g.shape);
+    activate_into(g, u, a, act, act_limit, s);
     return a;
+}
+
+void GatedMlp::activate_into(const Tensor& g, const Tensor& u, const Tensor& a, Act act, float act_limit,
+                             const Stream& s)
+{
+    if (act == Act::Silu) ffi::silu_mul(g, u, a, act_limit, s);
+    else ffi::gelu_mul(g, u, a, act_limit, s);
 }
 
 RoPE::RoPE(double theta, int rotary_dim, RopeStyle style, double attn_factor, double linear_factor)

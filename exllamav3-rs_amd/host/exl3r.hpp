@@ -111,12 +111,34 @@ struct Tensor
     void rows_view(int64_t& rows, int64_t& cols, int64_t& ld) const;
 };
 
-// Tensor with its own storage.
+// Tensor with its own storage (one hipMalloc; for weights and long-lived buffers, not per-call outputs).
 struct OwnedTensor
 {
     DeviceBuffer buf;
     Tensor t;
     static OwnedTensor empty(DType dt, std::vector<int64_t> shape);
+};
+
+// Device memory for module outputs, reserved once (one hipMalloc at construction) and handed out by
+// bumping an offset (256-byte aligned): a module call then allocates, frees and synchronises nothing, so
+// it can run inside a captured HIP graph or a tight decode loop.  This is the role tch's caching
+// allocator plays for the reference's modules (src/modules.rs:376, 400, 937 take `empty_like` outputs).
+// reset() hands the whole arena out again: the caller resets once no earlier output is read any more
+// (after each decode step, say).  An arena is not thread-safe.
+class Arena
+{
+public:
+    explicit Arena(size_t bytes);
+    // A contiguous tensor of `shape` carved from the arena; throws exl3r::Error (EXL3R_EINVAL) when it
+    // does not fit.
+    Tensor empty(DType dt, std::vector<int64_t> shape);
+    void reset() { off_ = 0; }
+    size_t used() const { return off_; }
+    size_t capacity() const { return buf_.bytes(); }
+
+private:
+    DeviceBuffer buf_;
+    size_t off_ = 0;
 };
 
 namespace ffi {
@@ -234,20 +256,22 @@ void embedding_rms_norm(const Tensor& table, const Tensor& ids, const Tensor* h,
 
 }  // namespace ffi
 
-// src/modules.rs:342-412.
+// src/modules.rs:342-412.  No call allocates: the output comes from an Arena or from the caller.
 class RmsNorm
 {
 public:
     RmsNorm(Tensor weight, float eps, float constant_bias = 0.0f, float constant_scale = 1.0f)
         : weight_(std::move(weight)), eps_(eps), constant_bias_(constant_bias), constant_scale_(constant_scale) {}
     // y = norm(x) in f16 (every call site in the Qwen3 tree), same shape as x.
-    OwnedTensor forward(const Tensor& x, const Stream& s) const;
+    Tensor forward(const Tensor& x, Arena& arena, const Stream& s) const;
+    void forward_into(const Tensor& x, const Tensor& y, const Stream& s) const;
     // Pre-norm residual add fused with the norm: r += add (in place), returns norm(r) in f16.
     // add == nullptr: plain forward(r).  r may have any row stride (the fused path then still
     // updates it in place); a residual whose leading dims do not collapse to one row stride is
     // rejected, where the reference falls back to norm(r + add) and leaves r unchanged
     // (src/modules.rs:393-395).
-    OwnedTensor forward_res(const Tensor& r, const Tensor* add, const Stream& s) const;
+    Tensor forward_res(const Tensor& r, const Tensor* add, Arena& arena, const Stream& s) const;
+    void forward_res_into(const Tensor& r, const Tensor* add, const Tensor& y, const Stream& s) const;
     const Tensor& weight() const { return weight_; }
 
 private:
@@ -260,8 +284,9 @@ class Embedding
 {
 public:
     explicit Embedding(Tensor weight, DType out_kind = DType::F32) : weight_(std::move(weight)), out_kind_(out_kind) {}
-    // ids: [b, s] int64 -> [b, s, hidden] of out_kind.
-    OwnedTensor forward(const Tensor& ids, const Stream& s) const;
+    // ids: [b, s] int64 -> [b, s, hidden] of out_kind (from the arena, or into the caller's out).
+    Tensor forward(const Tensor& ids, Arena& arena, const Stream& s) const;
+    void forward_into(const Tensor& ids, const Tensor& out, const Stream& s) const;
 
 private:
     Tensor weight_;
@@ -272,8 +297,10 @@ private:
 struct GatedMlp
 {
     enum class Act { Silu, Gelu };
-    // a = act(g) * u, same shape and dtype as g.
-    static OwnedTensor activate(const Tensor& g, const Tensor& u, Act act, float act_limit, const Stream& s);
+    // a = act(g) * u, same shape and dtype as g (from the arena, or into the caller's a).
+    static Tensor activate(const Tensor& g, const Tensor& u, Act act, float act_limit, Arena& arena, const Stream& s);
+    static void activate_into(const Tensor& g, const Tensor& u, const Tensor& a, Act act, float act_limit,
+                              const Stream& s);
 };
 
 // src/rope.rs:33-86, 233-292, 309-317: inv_freq producer (default and linear scaling) and the

@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -59,6 +60,24 @@ static std::vector<uint8_t> download(const OwnedTensor& t, const Stream& s)
     return h;
 }
 
+static void hip_ok(hipError_t e, const char* what)
+{
+    if (e != hipSuccess)
+    {
+        std::printf("FAIL %s: %s\n", what, hipGetErrorString(e));
+        std::exit(1);
+    }
+}
+
+// A contiguous view's bytes (arena outputs).
+static std::vector<uint8_t> download(const Tensor& t, const Stream& s)
+{
+    std::vector<uint8_t> h((size_t)t.numel() * dtype_size(t.dtype));
+    hip_ok(hipMemcpyAsync(h.data(), t.data, h.size(), hipMemcpyDeviceToHost, s.get()), "hipMemcpyAsync D2H");
+    s.synchronize();
+    return h;
+}
+
 static int64_t ordered16(uint16_t b) { return (b & 0x8000) ? -(int64_t)(b & 0x7fff) : (int64_t)b; }
 
 // Max ulp distance of two 16-bit storage arrays.
@@ -86,6 +105,7 @@ int main()
 {
     Stream s = Stream::create();
     char msg[256];
+    Arena arena(64 << 20);   // module outputs (no allocation inside a module call)
 
     // RmsNorm::forward on a 3-D f16 tensor (rows collapse to 21 x 512), f16 weight.
     {
@@ -94,7 +114,7 @@ int main()
         auto x = upload(xh, DType::F16, { 3, 7, 512 }, s);
         auto w = upload(wh, DType::F16, { 512 }, s);
         RmsNorm norm(w.t, 1e-6f);
-        auto y = norm.forward(x.t, s);
+        auto y = norm.forward(x.t, arena, s);
         auto yh = download(y, s);
         std::vector<uint8_t> ey(yh.size());
         oracle_rms_norm(xh.data(), OR_F16, 512, wh.data(), OR_F16, ey.data(), OR_F16, 512, nullptr, OR_F32, 512, 21, 512,
@@ -112,7 +132,7 @@ int main()
         auto add = upload(ah, DType::F16, { 1, 8, 1024 }, s);
         auto w = upload(wh, DType::F16, { 1024 }, s);
         RmsNorm norm(w.t, 1e-6f, 1.0f);
-        auto y = norm.forward_res(r.t, &add.t, s);
+        auto y = norm.forward_res(r.t, &add.t, arena, s);
         auto yh = download(y, s), rh2 = download(r, s);
         std::vector<uint8_t> ey(yh.size()), er = rh;
         oracle_rms_norm(ah.data(), OR_F16, 1024, wh.data(), OR_F16, ey.data(), OR_F16, 1024, er.data(), OR_F32, 1024, 8,
@@ -130,12 +150,12 @@ int main()
         OwnedTensor idt = OwnedTensor::empty(DType::I64, { 2, 5 });
         idt.buf.upload(ids.data(), ids.size() * 8, s);
         Embedding emb(table.t);
-        auto out = emb.forward(idt.t, s);
+        auto out = emb.forward(idt.t, arena, s);
         auto oh = download(out, s);
         std::vector<uint8_t> eo(oh.size());
         int32_t err = 0;
         oracle_embedding(th.data(), OR_BF16, 100, 64, 64, ids.data(), OR_I64, 10, eo.data(), OR_F32, 64, &err, 1);
-        const bool ok = out.t.shape == std::vector<int64_t>({ 2, 5, 64 }) && std::memcmp(oh.data(), eo.data(), eo.size()) == 0;
+        const bool ok = out.shape == std::vector<int64_t>({ 2, 5, 64 }) && std::memcmp(oh.data(), eo.data(), eo.size()) == 0;
         report("Embedding::forward bf16 -> f32", ok, ok ? "bit-exact" : "mismatch");
     }
     // GatedMlp::activate (SiLU and GELU), bf16 [16, 256].
@@ -145,7 +165,7 @@ int main()
         auto uh = host_normal(DType::BF16, 16 * 256, 0.f, 1.f);
         auto g = upload(gh, DType::BF16, { 16, 256 }, s);
         auto u = upload(uh, DType::BF16, { 16, 256 }, s);
-        auto a = GatedMlp::activate(g.t, u.t, act ? GatedMlp::Act::Gelu : GatedMlp::Act::Silu, 0.f, s);
+        auto a = GatedMlp::activate(g.t, u.t, act ? GatedMlp::Act::Gelu : GatedMlp::Act::Silu, 0.f, arena, s);
         auto ah = download(a, s);
         std::vector<uint8_t> ea(ah.size());
         oracle_act_mul(act ? OR_ACT_GELU : OR_ACT_SILU, gh.data(), uh.data(), OR_BF16, ea.data(), OR_BF16, 16, 256, 256,
@@ -459,6 +479,65 @@ int main()
         const bool ok = download(out, s) == download(ref, s);
         report("ffi::gated_rms_norm_had == gated norm + had_r_128", ok, ok ? "bitwise" : "DIFFER");
     }
+    // Graph capture: RmsNorm::forward_res (output from an arena) and RoPE::apply (positions read from device
+    // memory) recorded into a HIP graph in the strict (global) capture mode, which fails any allocation or
+    // synchronisation inside the calls; replayed three times with new inputs and positions uploaded eagerly
+    // between the replays, every replay checked against the oracle.
+    {
+        const int T = 8, H = 512, hq = 4, hk = 2, hd = 128;
+        Stream cs = Stream::create();
+        OwnedTensor r = OwnedTensor::empty(DType::F32, { T, H }), add = OwnedTensor::empty(DType::F16, { T, H });
+        OwnedTensor q = OwnedTensor::empty(DType::F16, { T, 1, hq, hd }), k = OwnedTensor::empty(DType::F16, { T, 1, hk, hd });
+        OwnedTensor pos = OwnedTensor::empty(DType::I32, { T });
+        auto wh = host_normal(DType::F16, H, 1.f, 0.1f);
+        auto qnh = host_normal(DType::F16, hd, 1.f, 0.1f), knh = host_normal(DType::F16, hd, 1.f, 0.1f);
+        auto w = upload(wh, DType::F16, { H }, cs);
+        auto qn = upload(qnh, DType::F16, { hd }, cs), kn = upload(knh, DType::F16, { hd }, cs);
+        RmsNorm norm(w.t, 1e-6f, 1.0f);
+        RoPE rope(1e6, hd, RopeStyle::NeoX);
+        Arena garena(1 << 20);
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        hip_ok(hipStreamBeginCapture(cs.get(), hipStreamCaptureModeGlobal), "hipStreamBeginCapture");
+        Tensor y = norm.forward_res(r.t, &add.t, garena, cs);
+        rope.apply(q.t, k.t, 0, &pos.t, &qn.t, &kn.t, 1e-6f, 0.f, cs);
+        hip_ok(hipStreamEndCapture(cs.get(), &graph), "hipStreamEndCapture");
+        hip_ok(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+        bool all_ok = true;
+        for (int rep = 0; rep < 3; ++rep)
+        {
+            auto rh = host_normal(DType::F32, T * H, 0.f, 4.f), ah = host_normal(DType::F16, T * H, 0.f, 1.f);
+            auto qh = host_normal(DType::F16, T * hq * hd, 0.f, 1.f), kh = host_normal(DType::F16, T * hk * hd, 0.f, 1.f);
+            std::vector<int32_t> ph(T);
+            for (int i = 0; i < T; ++i) ph[i] = (int32_t)((splitmix() >> 40) % 40000);
+            r.buf.upload(rh.data(), rh.size(), cs);
+            add.buf.upload(ah.data(), ah.size(), cs);
+            q.buf.upload(qh.data(), qh.size(), cs);
+            k.buf.upload(kh.data(), kh.size(), cs);
+            pos.buf.upload(ph.data(), ph.size() * 4, cs);
+            hip_ok(hipGraphLaunch(exec, cs.get()), "hipGraphLaunch");
+            cs.synchronize();
+            auto yo = download(y, cs), ro = download(r, cs), qo = download(q, cs), ko = download(k, cs);
+            std::vector<uint8_t> ey(yo.size()), er = rh, eq(qh.size()), ek(kh.size());
+            oracle_rms_norm(ah.data(), OR_F16, H, wh.data(), OR_F16, ey.data(), OR_F16, H, er.data(), OR_F32, H, T, H,
+                            1e-6f, 1.0f, 1.f, 1);
+            oracle_rope(qh.data(), eq.data(), hq * hd, hd, hq, kh.data(), ek.data(), hk * hd, hd, hk, OR_F16, T, 1, hd,
+                        rope.inv_freq_host().data(), hd, 0, ph.data(), nullptr, qnh.data(), knh.data(), OR_F16, 1e-6f,
+                        0.f, OR_ROPE_NEOX, 1.f, 1);
+            const int64_t dy = max_ulp16(yo, ey), dq = max_ulp16(qo, eq), dk = max_ulp16(ko, ek);
+            const bool r_ok = std::memcmp(ro.data(), er.data(), er.size()) == 0;
+            std::snprintf(msg, sizeof msg, "replay %d: y max ulp %lld, residual bit-exact %s, q/k max ulp %lld/%lld", rep,
+                          (long long)dy, r_ok ? "yes" : "no", (long long)dq, (long long)dk);
+            const bool ok = dy <= 1 && r_ok && dq <= 2 && dk <= 2;
+            report("captured forward_res + RoPE::apply", ok, msg);
+            all_ok = all_ok && ok;
+        }
+        hip_ok(hipGraphExecDestroy(exec), "hipGraphExecDestroy");
+        hip_ok(hipGraphDestroy(graph), "hipGraphDestroy");
+        report("graph capture of the module layer (no allocation inside the calls)", all_ok && garena.used() > 0,
+               all_ok ? "3 replays" : "mismatch");
+    }
+
     std::printf(failures ? "test_host_gpu: %d failures\n" : "test_host_gpu: all passed\n", failures);
     return failures ? 1 : 0;
 }
