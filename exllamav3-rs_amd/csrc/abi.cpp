@@ -78,6 +78,12 @@ extern "C" void exl3r_tune_rms(int maxv, int threads)
 
 extern "C" void exl3r_tune_rms_rows(int rows_per_lane) { exl3r::tuning().rms_rows_rpl = rows_per_lane; }
 
+extern "C" void exl3r_tune_rms_split(int split, int wmode)
+{
+    exl3r::tuning().rms_split = split;
+    exl3r::tuning().rms_split_wm = wmode;
+}
+
 extern "C" void exl3r_tune_act(int unroll, int threads, int blocks_per_cu)
 {
     exl3r::tuning().act_unroll = unroll;

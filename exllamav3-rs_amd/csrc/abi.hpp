@@ -45,7 +45,8 @@ constexpr int64_t kMaxGridX = 1 << 20;
 struct Tuning
 {
     int rms_maxv = 0, rms_threads = 0;
-    int rms_rows_rpl = 0;    // short-row RMSNorm kernel: rows per lane in flight (1, 2, 4; 0 auto)
+    int rms_rows_rpl = 0;
+    int rms_split = 0, rms_split_wm = 1;   // split chunks: -1 never, 0 auto, 1 always; weight mode (1 mid, 2 late)    // short-row RMSNorm kernel: rows per lane in flight (1, 2, 4; 0 auto)
     int act_unroll = 0, act_threads = 0, act_blocks_per_cu = 0;
     int rope_iters = 0;
     int rope_tok = 0;       // 0 auto, 1 never the wave-per-token kernel, 2 always (where it applies)

@@ -74,9 +74,12 @@ __device__ __forceinline__ void act_chunk(const float (&g)[8], const float (&u)[
     }
 }
 
-template <int ACT, class IT, class OT, int UNROLL, bool LIMIT, int HAD = 0>
+// SPLIT: split chunks (two quads 256 apart) for rows of whole 512-element spans with an f32 side, so
+// that each wave-wide f32 access is one contiguous 1 KB.
+template <int ACT, class IT, class OT, int UNROLL, bool LIMIT, int HAD = 0, bool SPLIT = false>
 __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
 {
+    static_assert(!SPLIT || HAD == 0, "split chunks: no Hadamard blocks");
     const int64_t cpr = a.cols >> 3;   // chunks per row
     const int nt = blockDim.x;
     for (int64_t row = blockIdx.y; row < a.rows; row += gridDim.y)
@@ -94,8 +97,16 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
                 const int64_t c = base + (int64_t)u * nt;
                 if (c < cpr)
                 {
-                    xv[u] = load8s<IT>(xr, c * 8);
-                    yv[u] = load8s<IT>(yr, c * 8);
+                    if constexpr (SPLIT)
+                    {
+                        xv[u] = load8s_split<IT>(xr, chunk_elem<true>(c));
+                        yv[u] = load8s_split<IT>(yr, chunk_elem<true>(c));
+                    }
+                    else
+                    {
+                        xv[u] = load8s<IT>(xr, c * 8);
+                        yv[u] = load8s<IT>(yr, c * 8);
+                    }
                 }
             }
             #pragma unroll
@@ -115,7 +126,8 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
                     unpack8<IT>(xv[u], g);
                     unpack8<IT>(yv[u], v);
                     act_chunk<ACT, OT, LIMIT>(g, v, a.limit, o);
-                    if constexpr (!(HAD & AH_OUT)) store8<OT>(zr, c * 8, pack8<OT>(o));
+                    if constexpr (SPLIT) store8_split<OT>(zr, chunk_elem<true>(c), pack8<OT>(o));
+                    else if constexpr (!(HAD & AH_OUT)) store8<OT>(zr, c * 8, pack8<OT>(o));
                     else
                     {
                         // The group of 16 lanes holding chunks c & ~15 .. c | 15 is the block's (the
@@ -225,6 +237,16 @@ static void launch_act_vec(const ActArgs& a, hipStream_t s)
     }
     if (bx > kMaxGridX) bx = kMaxGridX;
     const dim3 grid((unsigned)bx, (unsigned)(a.rows < 65535 ? a.rows : 65535));
+    if constexpr (HAD == 0 && (IT::code == DT_F32 || OT::code == DT_F32))
+    {
+        if (a.cols % 512 == 0 && tu.rms_split != -1)
+        {
+            // two chunks per thread (the grid-stride loop covers the row whatever the grid)
+            if (a.limit != 0.0f) k_act_mul<ACT, IT, OT, 2, true, 0, true><<<grid, threads, 0, s>>>(a);
+            else k_act_mul<ACT, IT, OT, 2, false, 0, true><<<grid, threads, 0, s>>>(a);
+            return;
+        }
+    }
     if (a.limit != 0.0f)
         k_act_mul<ACT, IT, OT, 2, true, HAD><<<grid, threads, 0, s>>>(a);
     else

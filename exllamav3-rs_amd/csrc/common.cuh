@@ -14,6 +14,7 @@ namespace exl3r {
 enum : int { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2, DT_I32 = 3, DT_I64 = 4 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -139,6 +140,90 @@ template <> __device__ __forceinline__ void store8<TF32>(void* base, int64_t e, 
     u32x4* p = (u32x4*)((float*)base + e);
     __builtin_nontemporal_store(v.a, p);
     __builtin_nontemporal_store(v.b, p + 1);
+}
+
+// Split chunks: the 8 elements of a chunk are the quads at e and e + kSplitGap, each one 8-byte (16-bit
+// data) or 16-byte (f32) access.  With lane l of a wave taking the quads at 4 l and 256 + 4 l of a
+// 512-element span, each wave-wide access of an operand covers one contiguous range: 512 B, or 1 KB for
+// f32, where an f32 chunk of 8 contiguous elements is two accesses that each touch every other 16 bytes
+// of 2 KB (MI355X, RES_IN f16 x / f32 r / f16 y at [8192, 5120]: 89.3 -> 82 us).
+constexpr int kSplitGap = 256;
+// First element of chunk c: 8 c, or for split chunks (rows of whole 512-element spans, 64 consecutive
+// chunks per wave) the quad at 4 (c % 64) of span c / 64, whose second half is kSplitGap further on.
+template <bool SPLIT>
+__device__ __forceinline__ int64_t chunk_elem(int64_t c)
+{
+    if constexpr (SPLIT) return ((c >> 6) << 9) + ((c & 63) << 2);
+    else return c * 8;
+}
+
+template <class T> __device__ __forceinline__ typename T::Vec load8s_split(const void* base, int64_t e);
+template <class T> __device__ __forceinline__ void store8_split(void* base, int64_t e, const typename T::Vec& v);
+
+__device__ __forceinline__ u32x4 load16x2_split(const uint16_t* p)
+{
+    const u32x2 lo = __builtin_nontemporal_load((const u32x2*)p);
+    const u32x2 hi = __builtin_nontemporal_load((const u32x2*)(p + kSplitGap));
+    return u32x4{ lo.x, lo.y, hi.x, hi.y };
+}
+__device__ __forceinline__ void store16x2_split(uint16_t* p, u32x4 v)
+{
+    __builtin_nontemporal_store(u32x2{ v.x, v.y }, (u32x2*)p);
+    __builtin_nontemporal_store(u32x2{ v.z, v.w }, (u32x2*)(p + kSplitGap));
+}
+template <> __device__ __forceinline__ TF16::Vec load8s_split<TF16>(const void* base, int64_t e)
+{
+    return { load16x2_split((const uint16_t*)base + e) };
+}
+template <> __device__ __forceinline__ TBF16::Vec load8s_split<TBF16>(const void* base, int64_t e)
+{
+    return { load16x2_split((const uint16_t*)base + e) };
+}
+template <> __device__ __forceinline__ TF32::Vec load8s_split<TF32>(const void* base, int64_t e)
+{
+    const float* p = (const float*)base + e;
+    TF32::Vec v;
+    v.a = __builtin_nontemporal_load((const u32x4*)p);
+    v.b = __builtin_nontemporal_load((const u32x4*)(p + kSplitGap));
+    return v;
+}
+// Cached form (hot embedding-table rows).
+template <class T> __device__ __forceinline__ typename T::Vec load8_split(const void* base, int64_t e);
+__device__ __forceinline__ u32x4 load16x2_split_cached(const uint16_t* p)
+{
+    const u32x2 lo = *(const u32x2*)p, hi = *(const u32x2*)(p + kSplitGap);
+    return u32x4{ lo.x, lo.y, hi.x, hi.y };
+}
+template <> __device__ __forceinline__ TF16::Vec load8_split<TF16>(const void* base, int64_t e)
+{
+    return { load16x2_split_cached((const uint16_t*)base + e) };
+}
+template <> __device__ __forceinline__ TBF16::Vec load8_split<TBF16>(const void* base, int64_t e)
+{
+    return { load16x2_split_cached((const uint16_t*)base + e) };
+}
+template <> __device__ __forceinline__ TF32::Vec load8_split<TF32>(const void* base, int64_t e)
+{
+    const float* p = (const float*)base + e;
+    TF32::Vec v;
+    v.a = *(const u32x4*)p;
+    v.b = *(const u32x4*)(p + kSplitGap);
+    return v;
+}
+
+template <> __device__ __forceinline__ void store8_split<TF16>(void* base, int64_t e, const TF16::Vec& v)
+{
+    store16x2_split((uint16_t*)base + e, v.a);
+}
+template <> __device__ __forceinline__ void store8_split<TBF16>(void* base, int64_t e, const TBF16::Vec& v)
+{
+    store16x2_split((uint16_t*)base + e, v.a);
+}
+template <> __device__ __forceinline__ void store8_split<TF32>(void* base, int64_t e, const TF32::Vec& v)
+{
+    float* p = (float*)base + e;
+    __builtin_nontemporal_store(v.a, (u32x4*)p);
+    __builtin_nontemporal_store(v.b, (u32x4*)(p + kSplitGap));
 }
 
 template <> __device__ __forceinline__ void unpack8<TF16>(const TF16::Vec& v, float (&f)[8])

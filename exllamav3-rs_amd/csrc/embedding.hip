@@ -3,9 +3,11 @@
 // (the gather fused with the RMSNorm that follows it, as the MTP head applies
 // pre_fc_norm_embedding to embed(t), reference src/mtp.rs:189-190).
 //
-// The gather is a pure copy: 16-byte chunks per lane, one workgroup per token row, copied
-// bit-for-bit when out has the table's dtype and upcast exactly to F32 otherwise.  Ids outside
-// [0, vocab) produce a zero row and set the caller's device error flag.
+// The gather is a pure copy: 8-element chunks per lane, one workgroup per token row, copied
+// bit-for-bit when out has the table's dtype and upcast exactly to F32 otherwise.  With an f32 side
+// and rows of whole 512-element spans the chunks are split (two quads 256 apart), so that every
+// wave-wide f32 access is one contiguous 1 KB (MI355X: bf16 table -> f32 rows at [16384, 5120] Zipf,
+// see the launch).  Ids outside [0, vocab) produce a zero row and set the caller's device error flag.
 #include "rms_norm_kernel.cuh"
 #include "rms_norm_launch.hpp"
 
@@ -24,7 +26,7 @@ struct EmbArgs
     int32_t* err;
 };
 
-template <class TT, class OT, int UNROLL>
+template <class TT, class OT, int UNROLL, bool SPLIT = false>
 __global__ __launch_bounds__(1024) void k_embedding(EmbArgs a)
 {
     const int nc = a.hidden >> 3;
@@ -43,7 +45,11 @@ __global__ __launch_bounds__(1024) void k_embedding(EmbArgs a)
             for (int u = 0; u < UNROLL; ++u)
             {
                 const int c = base + u * nt;
-                if (c < nc && valid) v[u] = load8<TT>(src, (int64_t)c * 8);
+                if (c < nc && valid)
+                {
+                    if constexpr (SPLIT) v[u] = load8_split<TT>(src, chunk_elem<true>(c));
+                    else v[u] = load8<TT>(src, (int64_t)c * 8);
+                }
             }
             #pragma unroll
             for (int u = 0; u < UNROLL; ++u)
@@ -51,6 +57,11 @@ __global__ __launch_bounds__(1024) void k_embedding(EmbArgs a)
                 const int c = base + u * nt;
                 if (c < nc)
                 {
+                    const int64_t e = chunk_elem<SPLIT>(c);
+                    auto put = [&](const typename OT::Vec& o) {
+                        if constexpr (SPLIT) store8_split<OT>(dst, e, o);
+                        else store8<OT>(dst, e, o);
+                    };
                     if constexpr (TT::code == OT::code)
                     {
                         if (!valid)
@@ -58,7 +69,7 @@ __global__ __launch_bounds__(1024) void k_embedding(EmbArgs a)
                             const float z[8] = {};
                             v[u] = pack8<TT>(z);
                         }
-                        store8<OT>(dst, (int64_t)c * 8, v[u]);
+                        put(v[u]);
                     }
                     else
                     {
@@ -69,7 +80,7 @@ __global__ __launch_bounds__(1024) void k_embedding(EmbArgs a)
                             #pragma unroll
                             for (int j = 0; j < 8; ++j) f[j] = 0.0f;
                         }
-                        store8<OT>(dst, (int64_t)c * 8, pack8<OT>(f));
+                        put(pack8<OT>(f));
                     }
                 }
             }
@@ -139,12 +150,16 @@ extern "C" int exl3r_embedding(const void* table, int tt, int64_t vocab, int64_t
         int threads = (tu.embed_threads > 0 && tu.embed_threads % 64 == 0 && tu.embed_threads <= 1024) ? tu.embed_threads
                       : nc >= 1024 ? 256 : ((nc / 4 + 63) / 64) * 64;
         if (threads < 64) threads = 64;
+        const bool split = nc % 64 == 0 && (tt == EXL3R_F32 || ot == EXL3R_F32) && tu.rms_split != -1;
         with_float_type(tt, [&](auto T) {
             with_float_type(ot, [&](auto O) {
                 using TTy = decltype(T);
                 using OTy = decltype(O);
                 if constexpr (TTy::code == OTy::code || OTy::code == DT_F32)
-                    k_embedding<TTy, OTy, 4><<<grid, threads, 0, s>>>(a);
+                {
+                    if (split) k_embedding<TTy, OTy, 4, true><<<grid, threads, 0, s>>>(a);
+                    else k_embedding<TTy, OTy, 4><<<grid, threads, 0, s>>>(a);
+                }
             });
         });
     }

@@ -95,11 +95,21 @@ __device__ __forceinline__ int64_t load_id(const void* ids, int idt, int64_t i)
 // A weight chunk is fetched as one 16-byte access at the point the launch's weight mode picks (the
 // whole chunk for F16/BF16 weights; for F32 weights the first four floats, the second half being read
 // in pass 2), 4 VGPRs per chunk.
+// A split chunk (SPLIT) takes its two halves from the quads at e and e + kSplitGap.
+template <bool SPLIT = false>
 __device__ __forceinline__ u32x4 prefetch_w8(const void* w, int wt, int64_t e)
 {
+    if constexpr (SPLIT)
+    {
+        if (wt == DT_F32) return *(const u32x4*)((const float*)w + e);
+        const uint16_t* p = (const uint16_t*)w + e;
+        const u32x2 lo = *(const u32x2*)p, hi = *(const u32x2*)(p + kSplitGap);
+        return u32x4{ lo.x, lo.y, hi.x, hi.y };
+    }
     return *(const u32x4*)((const char*)w + e * (wt == DT_F32 ? 4 : 2));
 }
 
+template <bool SPLIT = false>
 __device__ __forceinline__ void unpack_w8(u32x4 pre, const void* w, int wt, int64_t e, float (&f)[8])
 {
     if (wt == DT_F16) { TF16::Vec v; v.a = pre; unpack8<TF16>(v, f); }
@@ -108,7 +118,7 @@ __device__ __forceinline__ void unpack_w8(u32x4 pre, const void* w, int wt, int6
     {
         TF32::Vec v;
         v.a = pre;
-        v.b = *(const u32x4*)((const float*)w + e + 4);
+        v.b = *(const u32x4*)((const float*)w + e + (SPLIT ? kSplitGap : 4));
         unpack8<TF32>(v, f);
     }
 }
@@ -125,7 +135,7 @@ struct RowRegs
 
 // Issues every HBM load of one row -- x (and r) in chunks c = tid, tid + nt, ... (at most MAXV per
 // lane), plus the weight chunks when load_w -- before any arithmetic.
-template <class XT, class RT, int MAXV, int MODE>
+template <class XT, class RT, int MAXV, int MODE, bool SPLIT = false>
 __device__ __forceinline__ void rms_load(const RmsArgs& a, int64_t row, int tid, int nt, bool load_w,
                                          RowRegs<XT, RT, MAXV>& L)
 {
@@ -150,15 +160,21 @@ __device__ __forceinline__ void rms_load(const RmsArgs& a, int64_t row, int tid,
     for (int k = 0; k < MAXV; ++k)
     {
         const int c = tid + k * nt;
+        const int64_t e = chunk_elem<SPLIT>(c);
         if (c < nc)
         {
             if (L.valid)
             {
-                if constexpr (MODE == RMS_GATHER) L.xv[k] = load8<XT>(xrow, (int64_t)c * 8);   // hot table rows
-                else L.xv[k] = load8s<XT>(xrow, (int64_t)c * 8);
+                if constexpr (SPLIT) L.xv[k] = load8s_split<XT>(xrow, e);
+                else if constexpr (MODE == RMS_GATHER) L.xv[k] = load8<XT>(xrow, e);   // hot table rows
+                else L.xv[k] = load8s<XT>(xrow, e);
             }
-            if constexpr (MODE == RMS_RES_IN || MODE == RMS_GATED) L.rv[k] = load8s<RT>(rrow, (int64_t)c * 8);
-            if (load_w && a.w) L.wv[k] = prefetch_w8(a.w, a.wt, weight_row<MODE>(a, row) + (int64_t)c * 8);
+            if constexpr (MODE == RMS_RES_IN || MODE == RMS_GATED)
+            {
+                if constexpr (SPLIT) L.rv[k] = load8s_split<RT>(rrow, e);
+                else L.rv[k] = load8s<RT>(rrow, e);
+            }
+            if (load_w && a.w) L.wv[k] = prefetch_w8<SPLIT>(a.w, a.wt, weight_row<MODE>(a, row) + e);
         }
     }
 }
@@ -245,7 +261,7 @@ __device__ __forceinline__ typename RmsCache<XT, RT, MODE>::Vec rms_chunk1(const
 
 // Pass 2 of the chunk at element e: gate (GATED), weight (row offset wofs), scale, gate after the
 // norm (GATED), one rounding, store.
-template <class XT, class YT, class RT, int MODE, int HAD>
+template <class XT, class YT, class RT, int MODE, int HAD, bool SPLIT = false>
 __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* yrow, int64_t e, int64_t wofs,
                                            const typename RmsCache<XT, RT, MODE>::Vec& cv,
                                            const typename RT::Vec& rv, u32x4 wv, float rmf)
@@ -273,7 +289,7 @@ __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* 
     if (a.w)
     {
         float wf[8];
-        unpack_w8(wv, a.w, a.wt, wofs + e, wf);
+        unpack_w8<SPLIT>(wv, a.w, a.wt, wofs + e, wf);
         if (a.cb != 0.0f)
         {
             #pragma unroll
@@ -296,7 +312,8 @@ __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* 
         }
     }
     const typename YT::Vec yv = pack8<YT>(o);
-    if constexpr (!(HAD & HAD_OUT)) store8<YT>(yrow, e, yv);
+    if constexpr (SPLIT) store8_split<YT>(yrow, e, yv);
+    else if constexpr (!(HAD & HAD_OUT)) store8<YT>(yrow, e, yv);
     else
     {
         #pragma clang fp contract(off)
@@ -323,7 +340,7 @@ __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* 
     }
 }
 
-template <class XT, class YT, class RT, int MAXV, int MODE, int HAD, int WM>
+template <class XT, class YT, class RT, int MAXV, int MODE, int HAD, int WM, bool SPLIT = false>
 __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int tid, int nt, RowRegs<XT, RT, MAXV>& L,
                                            double* red)
 {
@@ -339,7 +356,7 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
     for (int k = 0; k < MAXV; ++k)
     {
         const int c = tid + k * nt;
-        if (c < nc) cache[k] = rms_chunk1<XT, RT, MODE, HAD>(a, rrow, (int64_t)c * 8, L.valid, L.xv[k], L.rv[k], ss);
+        if (c < nc) cache[k] = rms_chunk1<XT, RT, MODE, HAD>(a, rrow, chunk_elem<SPLIT>(c), L.valid, L.xv[k], L.rv[k], ss);
     }
 
     const int64_t wofs = weight_row<MODE>(a, row);
@@ -349,7 +366,7 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
         for (int k = 0; k < MAXV; ++k)
         {
             const int c = tid + k * nt;
-            if (c < nc && a.w) L.wv[k] = prefetch_w8(a.w, a.wt, wofs + (int64_t)c * 8);
+            if (c < nc && a.w) L.wv[k] = prefetch_w8<SPLIT>(a.w, a.wt, wofs + chunk_elem<SPLIT>(c));
         }
     }
 
@@ -365,26 +382,32 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
         const int c = tid + k * nt;
         if (c < nc)
         {
+            const int64_t e = chunk_elem<SPLIT>(c);
             if constexpr (WM == W_LATE)
             {
-                if (a.w) L.wv[k] = prefetch_w8(a.w, a.wt, wofs + (int64_t)c * 8);
+                if (a.w) L.wv[k] = prefetch_w8<SPLIT>(a.w, a.wt, wofs + e);
             }
-            if constexpr (kDeferResidual<MODE, RT>) store8<RT>(rrow, (int64_t)c * 8, cache[k]);
-            rms_chunk2<XT, YT, RT, MODE, HAD>(a, row, yrow, (int64_t)c * 8, wofs, cache[k], L.rv[k], L.wv[k], rmf);
+            if constexpr (kDeferResidual<MODE, RT>)
+            {
+                if constexpr (SPLIT) store8_split<RT>(rrow, e, cache[k]);
+                else store8<RT>(rrow, e, cache[k]);
+            }
+            rms_chunk2<XT, YT, RT, MODE, HAD, SPLIT>(a, row, yrow, e, wofs, cache[k], L.rv[k], L.wv[k], rmf);
         }
     }
 }
 
 // One row per workgroup: its loads, pass 1, one reduction, pass 2.  (A grid-stride loop over rows, with
 // the second barrier it needs before LDS reuse, measured ~1 us slower at [8192, 5120].)
-template <class XT, class YT, class RT, int MAXV, int MODE, int HAD = 0, int WM = W_EARLY>
+template <class XT, class YT, class RT, int MAXV, int MODE, int HAD = 0, int WM = W_EARLY, bool SPLIT = false>
 __global__ __launch_bounds__(1024) void k_rms_norm(RmsArgs a)
 {
+    static_assert(!SPLIT || (HAD == 0 && (MODE == RMS_PLAIN || MODE == RMS_RES_IN)), "split chunks: plain and residual norms");
     __shared__ double red[16];
     const int64_t row = a.row0 + blockIdx.x;
     RowRegs<XT, RT, MAXV> L;
-    rms_load<XT, RT, MAXV, MODE>(a, row, threadIdx.x, blockDim.x, WM == W_EARLY, L);
-    rms_finish<XT, YT, RT, MAXV, MODE, HAD, WM>(a, row, threadIdx.x, blockDim.x, L, red);
+    rms_load<XT, RT, MAXV, MODE, SPLIT>(a, row, threadIdx.x, blockDim.x, WM == W_EARLY, L);
+    rms_finish<XT, YT, RT, MAXV, MODE, HAD, WM, SPLIT>(a, row, threadIdx.x, blockDim.x, L, red);
 }
 
 // Short rows (at most 64 chunks of 8): LPR lanes per row (a power of two covering dim / 8), one
@@ -539,17 +562,33 @@ __global__ __launch_bounds__(256) void k_rms_norm_generic(RmsArgs a, int xt, int
 //   8192 before the weight moved (one chunk per lane up to 512 lanes, else two chunks on at least 384
 //   lanes; 320 for the Hadamard kernels, whose chunks carry up to four butterflies), with the weight
 //   fetched mid-row (plain; gather and Hadamard kernels: early, where fetching it later measured no gain).
+//   Split chunks (rows of whole 512-element spans, plain and residual norms without Hadamard outputs,
+//   streaming launches with an f32 operand): one chunk per lane up to 1024 chunks, else two, weight
+//   fetched mid-row.  MI355X, f16 x / f32 r / f16 y at [8192, 5120] (us), 4-element quads per lane
+//   standing in for split chunks: 640 lanes x 2 quads 82.0 mid / 82.5 late, 320 x 4 85.1 / 83.8,
+//   256 x 5 83.7 / 85.8; contiguous chunks 2 x 512 late 89.3.
 struct RmsShape
 {
     int maxv;
     int threads;
     int wmode;
+    bool split = false;
 };
 
-inline RmsShape rms_shape(int nc, int64_t rows, int mode, int had)
+// wide: an f32 operand (x, r or y).
+inline RmsShape rms_shape(int nc, int64_t rows, int mode, int had, bool wide = false)
 {
     auto thr = [&](int m) { int t = (nc + m - 1) / m; return ((t + 63) / 64) * 64; };
     auto pick = [&](int m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8; };
+    const bool split_ok = !had && (mode == RMS_PLAIN || mode == RMS_RES_IN) && nc % 64 == 0 && nc <= 2048;
+    auto split_shape = [&](int wm) { return RmsShape{ nc <= 1024 ? 1 : 2, nc <= 1024 ? nc : thr(2), wm, true }; };
+#ifdef EXL3R_TUNING
+    const int split_mode = tuning().rms_split;
+    const int split_wm = tuning().rms_split_wm == W_LATE ? W_LATE : W_MID;
+#else
+    constexpr int split_mode = 0, split_wm = W_MID;
+#endif
+    if (split_ok && (split_mode == 1 || (split_mode == 0 && wide && rows > 1024))) return split_shape(split_wm);
     RmsShape sh{ 0, 0, W_EARLY };
 #ifdef EXL3R_TUNING
     const Tuning& tu = tuning();
@@ -583,7 +622,7 @@ inline RmsShape rms_shape(int nc, int64_t rows, int mode, int had)
     return { 8, thr(8), W_EARLY };   // <= 1024 (rms_vec_ok bounds the row at 8192 chunks)
 }
 
-template <class XT, class YT, class RT, int MODE, int HAD, int WM>
+template <class XT, class YT, class RT, int MODE, int HAD, int WM, bool SPLIT = false>
 void launch_rms_wm(const RmsArgs& a0, const RmsShape& sh, hipStream_t s)
 {
     // Launches of more than kMaxGridX rows go out in blocks of kMaxGridX rows (row0 offsets the block).
@@ -594,18 +633,33 @@ void launch_rms_wm(const RmsArgs& a0, const RmsShape& sh, hipStream_t s)
         const dim3 grid((unsigned)(a0.rows - r0 < kMaxGridX ? a0.rows - r0 : kMaxGridX));
         switch (sh.maxv)
         {
-            case 1: k_rms_norm<XT, YT, RT, 1, MODE, HAD, WM><<<grid, sh.threads, 0, s>>>(a); break;
-            case 2: k_rms_norm<XT, YT, RT, 2, MODE, HAD, WM><<<grid, sh.threads, 0, s>>>(a); break;
-            case 4: k_rms_norm<XT, YT, RT, 4, MODE, HAD, WM><<<grid, sh.threads, 0, s>>>(a); break;
-            default: k_rms_norm<XT, YT, RT, 8, MODE, HAD, WM><<<grid, sh.threads, 0, s>>>(a); break;
+            case 1: k_rms_norm<XT, YT, RT, 1, MODE, HAD, WM, SPLIT><<<grid, sh.threads, 0, s>>>(a); break;
+            case 2: k_rms_norm<XT, YT, RT, 2, MODE, HAD, WM, SPLIT><<<grid, sh.threads, 0, s>>>(a); break;
+            case 4:
+                if constexpr (!SPLIT) k_rms_norm<XT, YT, RT, 4, MODE, HAD, WM><<<grid, sh.threads, 0, s>>>(a);
+                break;
+            default:
+                if constexpr (!SPLIT) k_rms_norm<XT, YT, RT, 8, MODE, HAD, WM><<<grid, sh.threads, 0, s>>>(a);
+                break;
         }
     }
 }
 
+template <class XT, class YT, class RT>
+constexpr bool rms_wide = XT::code == DT_F32 || YT::code == DT_F32 || RT::code == DT_F32;
+
 template <class XT, class YT, class RT, int MODE, int HAD = 0>
 void launch_rms_vec(const RmsArgs& a, hipStream_t s)
 {
-    const RmsShape sh = rms_shape(a.dim / 8, a.rows, MODE, HAD);
+    const RmsShape sh = rms_shape(a.dim / 8, a.rows, MODE, HAD, rms_wide<XT, YT, RT>);
+    if constexpr (HAD == 0 && (MODE == RMS_RES_IN || MODE == RMS_PLAIN))
+    {
+        if (sh.split)
+        {
+            if (sh.wmode == W_LATE) return launch_rms_wm<XT, YT, RT, MODE, HAD, W_LATE, true>(a, sh, s);
+            return launch_rms_wm<XT, YT, RT, MODE, HAD, W_MID, true>(a, sh, s);
+        }
+    }
     if constexpr (HAD == 0 && MODE == RMS_RES_IN)
     {
         if (sh.wmode == W_LATE) return launch_rms_wm<XT, YT, RT, MODE, HAD, W_LATE>(a, sh, s);
@@ -628,7 +682,8 @@ inline bool rms_vec_ok(const RmsArgs& a, int xt, int yt, int rt, bool has_r, int
     if (!ok(a.x, a.ldx, xt) || !ok(a.y, a.ldy, yt)) return false;
     if (has_r && !ok(a.r, a.ldr, rt)) return false;
     if (a.w && !aligned16(a.w)) return false;
-    const RmsShape sh = rms_shape(a.dim / 8, a.rows, mode, had);
+    const bool wide = xt == DT_F32 || yt == DT_F32 || (has_r && rt == DT_F32);
+    const RmsShape sh = rms_shape(a.dim / 8, a.rows, mode, had, wide);
     return (int64_t)sh.maxv * sh.threads >= a.dim / 8 && sh.threads <= 1024 && sh.threads % 64 == 0;
 }
 

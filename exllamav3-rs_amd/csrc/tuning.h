@@ -12,6 +12,9 @@ extern "C" {
 EXL3R_API void exl3r_tune_rms(int maxv, int threads);
 /* short-row RMSNorm kernel: rows per lane in flight (1, 2, 4; 0 auto) */
 EXL3R_API void exl3r_tune_rms_rows(int rows_per_lane);
+/* plain / residual RMSNorm with split chunks (rows of whole 512-element spans): -1 never, 0 auto,
+ * 1 always; the weight fetched mid-row (1) or late (2) in split launches */
+EXL3R_API void exl3r_tune_rms_split(int split, int wmode);
 EXL3R_API void exl3r_tune_act(int unroll, int threads, int blocks_per_cu);
 /* heads per lane: 1, 2 or 4 */
 EXL3R_API void exl3r_tune_rope(int iters);

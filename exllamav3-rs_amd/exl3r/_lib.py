@@ -70,6 +70,7 @@ PROTOTYPES = {
 TUNE_PROTOTYPES = {
     "exl3r_tune_rms": (None, [_i, _i]),
     "exl3r_tune_rms_rows": (None, [_i]),
+    "exl3r_tune_rms_split": (None, [_i, _i]),
     "exl3r_tune_act": (None, [_i, _i, _i]),
     "exl3r_tune_rope": (None, [_i]),
     "exl3r_tune_rope_tok": (None, [_i, _i, _i]),
@@ -145,6 +146,7 @@ def tuned():
     finally:
         lib.exl3r_tune_rms(0, 0)
         lib.exl3r_tune_rms_rows(0)
+        lib.exl3r_tune_rms_split(0, 1)
         lib.exl3r_tune_act(0, 0, 0)
         lib.exl3r_tune_rope(0)
         lib.exl3r_tune_rope_tok(0, 0, 0)

@@ -72,6 +72,16 @@ def test_strided_odd_and_tail(act):
     run(act, 33, 512, BF16, F32, ld=520, limit=3.0, seed=26)   # 64 chunks per row, act_limit
 
 
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+@pytest.mark.parametrize("it,zt", [(F32, F16), (F16, F32), (F32, F32), (BF16, F32)])
+def test_split_chunks_f32(act, it, zt):
+    """An f32 side with rows of whole 512-element spans: split chunks (two quads 256 apart per lane),
+    contiguous, strided (gate / up as column slices) and with act_limit."""
+    run(act, 40, 2048, it, zt, seed=31 + it + zt, std=4.0)
+    run(act, 24, 1024, it, zt, ld=2048, seed=32 + it + zt)
+    run(act, 9, 4608, it, zt, limit=5.0, std=6.0, seed=33 + it + zt)
+
+
 def test_in_place_and_specials():
     x = torch.tensor([[0.0, -0.0, 60.0, -60.0, float("inf"), float("-inf"), float("nan"), 300.0]], device="cuda")
     y = torch.tensor([[5.0, 5.0, 3.0, 3.0, 1.0, 1.0, 1.0, 300.0]], device="cuda")

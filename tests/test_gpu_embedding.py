@@ -64,6 +64,16 @@ def test_small_tables(tt, ot):
     check_gather(table2, tt, np.arange(50)[::-1].copy(), I64, ot)
 
 
+@pytest.mark.parametrize("tt,ot,hidden", [(BF16, F32, 5120), (F32, F32, 2048), (F16, F32, 512)])
+def test_split_chunks_f32(tt, ot, hidden):
+    """An f32 side with rows of whole 512-element spans: split chunks (two quads 256 apart per lane),
+    with out-of-range ids zeroing their rows."""
+    table = dev_normal((3000, hidden), 0.0, 0.02, tt, 6)
+    ids = np.random.default_rng(7).integers(0, 3000, 700)
+    ids[[5, 300]] = [-2, 3000]
+    check_gather(table, tt, ids, I64, ot)
+
+
 def test_out_of_range_ids():
     table = dev_normal((100, 256), 0.0, 0.02, BF16, 5)
     check_gather(table, BF16, np.array([3, -1, 100, 99, 1 << 40, 0]), I64, BF16)

@@ -1,10 +1,13 @@
 """GPU parity of exl3r_rms_norm / exl3r_rms_norm_res_in against the CPU oracle on the same bits:
 <= 1 ulp for 16-bit outputs (<= 3 for f32), max abs err <= 2e-3 of the output scale, and the
-residual written back by RES_IN bit-exact."""
+residual written back by RES_IN bit-exact.  Covers the contiguous and the split chunk placements
+(each lane's 8 elements as two quads 256 apart), the latter automatic for streaming launches with an
+f32 operand and forced through the sweep/test build's hook on other shapes and dtypes."""
 import numpy as np
 import pytest
 import torch
 
+import exl3r._lib as L
 import exl3r.ffi as ffi
 from _gpu import NTHREADS, assert_bitwise, assert_close_ulp, code_of, dev_normal, from_dev
 from oracle import oracle as orc
@@ -132,3 +135,35 @@ def test_zero_rows():
     ffi.rms_norm(x, w, torch.empty_like(x), 1e-6)
     ffi.rms_norm_res_in(x, w, torch.empty_like(x), torch.empty_like(x), 1e-6)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("rows,dim,xt,rt,yt,wt", [(1100, 5120, F16, F32, F16, F16), (1030, 2048, F32, None, BF16, F32),
+                                                  (1025, 4096, BF16, None, F32, BF16), (1200, 2560, F32, F32, F32, F32)])
+def test_split_chunks_streaming(rows, dim, xt, rt, yt, wt):
+    """Streaming launches (> 1024 rows) with an f32 operand: the automatic split placement."""
+    if rt is None:
+        run_plain(rows, dim, xt, wt, yt, seed=dim + xt)
+    else:
+        run_res(rows, dim, xt, rt, yt, wt, seed=dim + rt)
+
+
+@pytest.mark.parametrize("wm", [1, 2])
+@pytest.mark.parametrize("dim", [512, 1024, 2560, 16384])
+@pytest.mark.parametrize("xt,rt,yt,wt", [(F16, F32, F16, F16), (BF16, BF16, BF16, BF16), (F32, F16, BF16, F32),
+                                         (F16, None, F16, F16), (BF16, None, F32, BF16), (F32, None, F16, F32)])
+def test_split_chunks_forced(wm, dim, xt, rt, yt, wt):
+    """Split chunks forced on short launches: one chunk per lane up to 1024 chunks, two at dim 16384;
+    the weight fetched mid-row (1) or late (2); f32 weights read their second half 256 on."""
+    with L.tuned() as lib:
+        lib.exl3r_tune_rms_split(1, wm)
+        if rt is None:
+            run_plain(23, dim, xt, wt, yt, seed=dim + xt + wm)
+        else:
+            run_res(23, dim, xt, rt, yt, wt, seed=dim + rt + wm, cb=1.0 if wm == 2 else 0.0)
+
+
+def test_split_chunks_strided():
+    """Split chunks over row strides beyond dim (16-byte aligned), padding left untouched."""
+    with L.tuned() as lib:
+        lib.exl3r_tune_rms_split(1, 1)
+        run_plain(9, 1024, F32, F16, F16, ldx=1024 + 64, ldy=1024 + 128, seed=77)
