@@ -30,7 +30,8 @@ sys.path.insert(0, os.path.join(ROOT, "exllamav3-rs_amd"))
 
 PEAK_GBS = 8000.0            # MI355X HBM3E
 METRIC = "fused norm/act/RoPE/embed HBM GB/s + % of MI355X peak; decode-step us"
-OPS = ["rms_c3", "rms_q3mix", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "gather_norm_c5", "rms_c1",
+OPS = ["rms_c3", "rms_q3mix", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "gather_f32_c5",
+       "gather_norm_c5", "rms_c1",
        "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "rope_kv_prefill",
        "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
        "deinterleave_q35", "gated_norm_had_q35", "gated_norm_had_q35_unfused", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
@@ -739,6 +740,8 @@ def make_all(only=None):
         "prefill_layer_cs": lambda: make_prefill_layer("prefill_layer_cs", True, cs=True),
         "qg_rope_q35_unfused": lambda: make_qg_rope("qg_rope_q35_unfused", False),
         "gather_c5": lambda: make_gather("gather_c5", 151936, 5120, 16384, bf16, bf16, zipf_ids(16384, 151936, 1), 400),
+        "gather_f32_c5": lambda: make_gather("gather_f32_c5", 151936, 5120, 16384, bf16, torch.float32,
+                                             zipf_ids(16384, 151936, 1), 400),
         "gather_norm_c5": lambda: make_gather("gather_norm_c5", 151936, 5120, 16384, bf16, bf16,
                                               zipf_ids(16384, 151936, 1), 400, norm=True),
         "rms_c1": lambda: make_rms("rms_c1", 512, 1024, f16, False, 500),
