@@ -625,13 +625,99 @@ struct NxItem
     typename IO::Vec lo[P], hi[P];
     float4 cs[4];                // SRC_CS: the lane's 8 {cos, sin} pairs as loaded
     int64_t tok;
+    int64_t crow;                // APPEND: the token's cache row (cache_row), -1: none or not needed
     int slice;
     int pos;                     // SRC_FREQ: the token's position
 };
 
-template <class IO, int MODE, int NORM, int SRC, bool QOUT, int P>
-__global__ __launch_bounds__(256) void k_rope_nx(RopeArgs a, int nslice)
+// Wave-uniform values read from memory (an item's cache row and position) moved to scalar registers, so
+// that the two items in flight do not hold them in VGPRs.
+__device__ __forceinline__ int uniform32(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int64_t uniform64(int64_t v)
 {
+    const uint64_t u = (uint64_t)v;
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)u);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+    return (int64_t)((hi << 32) | lo);
+}
+
+// One of three values by a per-lane choice (q / k / v heads), as mask arithmetic: hipcc turns a chain
+// of selects between three values into a lookup table in scratch memory indexed per lane (~600 bytes
+// per lane and twice the kernel time in the paged instances).
+__device__ __forceinline__ uint64_t pick_qkv_bits(bool isq, bool isv, uint64_t q, uint64_t k, uint64_t v)
+{
+    const uint64_t mq = (uint64_t)0 - (uint64_t)isq, mv = (uint64_t)0 - (uint64_t)(!isq && isv);
+    const uint64_t mk = ~(mq | mv);
+    return (q & mq) | (k & mk) | (v & mv);
+}
+template <class T>
+__device__ __forceinline__ T* pick_qkv(bool isq, bool isv, T* q, T* k, T* v)
+{
+    return (T*)pick_qkv_bits(isq, isv, (uint64_t)q, (uint64_t)k, (uint64_t)v);
+}
+__device__ __forceinline__ int64_t pick_qkv(bool isq, bool isv, int64_t q, int64_t k, int64_t v)
+{
+    return (int64_t)pick_qkv_bits(isq, isv, (uint64_t)q, (uint64_t)k, (uint64_t)v);
+}
+
+// The EXL3 linear's output rotation had_r_128(head) of one f16 head of 128 on the 8-lane layout (lane
+// l8 of the head's group holds elements [8 l8, 8 l8 + 8) in lo and [64 + 8 l8, 64 + 8 l8 + 8) in hi):
+// index bits 0-2 in-lane in both chunks, bits 3-5 lane exchanges at xor 1, 2, 4 inside the group, bit
+// 6 the lo / hi pair -- the reference's order of stages (bits 0..6) and pairs (a, b) -> (a + b, a - b)
+// in fp32, then the scale 1/sqrt(128) and one rounding to f16 (the post-scale product follows).
+__device__ __forceinline__ void rotate_head_nx(TF16::Vec& lo, TF16::Vec& hi, int l8)
+{
+    #pragma clang fp contract(off)
+    float fl[8], fh[8];
+    unpack8<TF16>(lo, fl);
+    unpack8<TF16>(hi, fh);
+    #pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+    {
+        #pragma unroll
+        for (int j = 0; j < 8; ++j)
+        {
+            if (j & h) continue;
+            float a = fl[j], b = fl[j | h];
+            fl[j] = a + b;
+            fl[j | h] = a - b;
+            a = fh[j];
+            b = fh[j | h];
+            fh[j] = a + b;
+            fh[j | h] = a - b;
+        }
+    }
+    lane_stage<1>(fl, l8);
+    lane_stage<1>(fh, l8);
+    lane_stage<2>(fl, l8);
+    lane_stage<2>(fh, l8);
+    lane_stage<4>(fl, l8);
+    lane_stage<4>(fh, l8);
+    #pragma unroll
+    for (int j = 0; j < 8; ++j)
+    {
+        const float a = fl[j], b = fh[j];
+        fl[j] = opaque((a + b) * 0.0883883461356163f);
+        fh[j] = opaque((a - b) * 0.0883883461356163f);
+    }
+    lo = pack8<TF16>(fl);
+    hi = pack8<TF16>(fh);
+}
+
+// APPEND: v heads follow the k heads in the item space; k and v rows are written to the paged caches
+// (exl3r_rope_paged_kv).  HADR: every head is first replaced by its projection's output rotation
+// (exl3r_rope_had, exl3r_rope_paged_kv_had).  Both take one pass per item.
+// The paged + rotating instance evaluating sin / cos lands one VGPR above the five-wave budget (97 of
+// 96); it is held to five waves per SIMD.
+template <bool APPEND, bool HADR, int SRC>
+constexpr int kNxMinWaves = APPEND && HADR && SRC == SRC_FREQ ? 5 : 1;
+
+template <class IO, int MODE, int NORM, int SRC, bool QOUT, int P, bool APPEND = false, bool HADR = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kNxMinWaves<APPEND, HADR, SRC>)))
+void k_rope_nx(RopeArgs a, int nslice)
+{
+    static_assert(!(APPEND || HADR) || (P == 1 && !QOUT), "paged / rotating items are single passes");
+    static_assert(!HADR || IO::code == DT_F16, "output rotation: f16 heads");
     extern __shared__ float2 cs[];            // [4 waves][64] (SRC_FREQ)
     // Norm weights with the constant bias folded in, q then k: h(w + h(cb)) (NORM_HALF) or w + cb (NORM_F32).
     __shared__ __align__(16) float wsh[256];
@@ -643,13 +729,26 @@ __global__ __launch_bounds__(256) void k_rope_nx(RopeArgs a, int nslice)
     const int grp = l64 >> 3;                 // head of a pass held by this lane's group of 8
     const int e0 = (l64 & 7) * 8;             // the lane's chunks: [e0, e0 + 8) and [e0 + 64, e0 + 72)
     const int64_t q_hs = a.q_hs, k_hs = a.k_hs, q_ts = a.q_ts, k_ts = a.k_ts;
-    const int hq = a.hq, H = a.hq + a.hk;
+    const int64_t v_hs = APPEND ? a.v_hs : 0, v_ts = APPEND ? a.v_ts : 0;
+    const int hq = a.hq, hk = a.hk, H = a.hq + a.hk + (APPEND ? a.hv : 0);
+    // Per-lane choices between argument fields select values, not addresses.
+    const void* const qpost = HADR ? a.q_post : nullptr;
+    const void* const kpost = HADR ? a.k_post : nullptr;
+    const void* const vpost = HADR ? a.v_post : nullptr;
+    char* const kcache = APPEND ? (char*)a.kc : nullptr;
+    char* const vcache = APPEND ? (char*)a.vc : nullptr;
+    const char* const qin = (const char*)a.q;
+    const char* const kin = (const char*)a.k;
+    const char* const vin = APPEND ? (const char*)a.v : nullptr;
+    char* const qout = (char*)a.oq;
+    char* const kout = (char*)a.ok;
+    const int64_t oq_ts = QOUT ? a.oq_ts : q_ts, oq_hs = QOUT ? a.oq_hs : q_hs;
     const int R = a.R, R2 = a.R >> 1;
     using Item = NxItem<IO, NORM, SRC, P>;
 
     // Loads of one item: the lane's two chunks of head (slice * P + p) * 8 + grp for each of the P passes,
     // and its rotary pairs (SRC_CS) or the token's position (SRC_FREQ).
-    auto issue = [&](Item& t, int64_t item) {
+    auto issue = [&](Item& t, int64_t item) __attribute__((always_inline)) {
         t.tok = item / nslice;
         t.slice = (int)(item - t.tok * nslice);
         #pragma unroll
@@ -658,12 +757,16 @@ __global__ __launch_bounds__(256) void k_rope_nx(RopeArgs a, int nslice)
             const int h = (t.slice * P + p) * 8 + grp;
             if (h < H)
             {
-                const char* base = h < hq ? (const char*)a.q + (t.tok * q_ts + (int64_t)h * q_hs) * IO::bytes
-                                          : (const char*)a.k + (t.tok * k_ts + (int64_t)(h - hq) * k_hs) * IO::bytes;
+                const bool iq = h < hq, iv = APPEND && h >= hq + hk;
+                const int hi = h - (iq ? 0 : hq) - (iv ? hk : 0);
+                const int64_t ts = pick_qkv(iq, iv, q_ts, k_ts, v_ts), hs = pick_qkv(iq, iv, q_hs, k_hs, v_hs);
+                const char* base = pick_qkv(iq, iv, qin, kin, vin) + (t.tok * ts + (int64_t)hi * hs) * IO::bytes;
                 t.lo[p] = load8s<IO>(base, e0);
                 t.hi[p] = load8s<IO>(base, e0 + 64);
             }
         }
+        // The cache row, once per item that holds k or v heads (wave-uniform).
+        if constexpr (APPEND) t.crow = (t.slice + 1) * 8 > hq ? uniform64(cache_row(a, t.tok)) : -1;
         if constexpr (SRC == SRC_CS)
         {
             // NeoX: pairs e0 .. e0 + 7; GPT-J: pairs e0/2 .. e0/2 + 3 (lo chunk) and 32 + e0/2 .. (hi chunk)
@@ -684,7 +787,7 @@ __global__ __launch_bounds__(256) void k_rope_nx(RopeArgs a, int nslice)
             }
         }
         else
-            t.pos = token_position(a, (int)t.tok);
+            t.pos = uniform32(token_position(a, (int)t.tok));
     };
 
     if constexpr (NORM != NORM_NONE)
@@ -703,14 +806,46 @@ __global__ __launch_bounds__(256) void k_rope_nx(RopeArgs a, int nslice)
 
     // Head norm, rotation and stores of one pass (lo / hi: the lane's chunks of head h).
     auto pass = [&](int64_t tok, int h, typename IO::Vec& lo, typename IO::Vec& hi, const float (&c)[8],
-                    const float (&s)[8]) {
+                    const float (&s)[8], int64_t crow) __attribute__((always_inline)) {
         const bool act = h < H;
         const bool isq = h < hq;
+        const bool isv = APPEND && h >= hq + hk;
+        const int hidx = h - (isq ? 0 : hq) - (isv ? hk : 0);
         if (!act)
         {
             #pragma unroll
             for (int i = 0; i < 4; ++i) lo.a[i] = hi.a[i] = 0;
         }
+        if constexpr (HADR)
+        {
+            // The head's post-scale (f16 per column of the projection output), loaded before the
+            // butterfly so that its latency hides under it (after it: 0.87x instead of 0.83x of the
+            // wave-per-token kernel's time at C4), applied after its rounding; a padding head past the
+            // last one has none.
+            const void* post = pick_qkv(isq, isv, qpost, kpost, vpost);
+            const bool hp = act && post != nullptr;
+            u32x4 pl = {}, ph = {};
+            if (hp)
+            {
+                const _Float16* pp = (const _Float16*)post + (int64_t)hidx * 128 + e0;
+                pl = *(const u32x4*)pp;
+                ph = *(const u32x4*)(pp + 64);
+            }
+            rotate_head_nx(lo, hi, l64 & 7);
+            if (hp)
+            {
+                #pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    lo.a[i] = hmul2(lo.a[i], (uint32_t)pl[i]);
+                    hi.a[i] = hmul2(hi.a[i], (uint32_t)ph[i]);
+                }
+            }
+        }
+        // v heads (APPEND) are only copied to the cache; a group of 8 lanes is one head, so the
+        // head norm's exchanges stay inside lanes that take the same branch.
+        if (!isv)
+        {
         if constexpr (NORM != NORM_NONE)
         {
             float fl[8], fh[8];
@@ -794,24 +929,38 @@ __global__ __launch_bounds__(256) void k_rope_nx(RopeArgs a, int nslice)
             lo = pack8<IO>(fl);
             hi = pack8<IO>(fh);
         }
+        }
         if (!act) return;
-        char* ob;
-        int32_t oo;
-        if (isq)
+        if (isq || (!isv && (!APPEND || kout)))
         {
-            ob = (char*)a.oq + tok * (QOUT ? a.oq_ts : q_ts) * IO::bytes;
-            oo = (int32_t)((int64_t)h * (QOUT ? a.oq_hs : q_hs)) + e0;
+            char* ob;
+            int32_t oo;
+            if (isq)
+            {
+                ob = qout + tok * oq_ts * IO::bytes;
+                oo = (int32_t)((int64_t)h * oq_hs) + e0;
+            }
+            else
+            {
+                ob = kout + tok * k_ts * IO::bytes;
+                oo = (int32_t)((int64_t)hidx * k_hs) + e0;
+            }
+            store8<IO>(ob, oo, lo);
+            store8<IO>(ob, oo + 64, hi);
         }
-        else
+        if constexpr (APPEND)
         {
-            ob = (char*)a.ok + tok * k_ts * IO::bytes;
-            oo = (int32_t)((int64_t)(h - hq) * k_hs) + e0;
+            if (!isq && crow >= 0)
+            {
+                char* cb = isv ? vcache : kcache;
+                const int64_t co = crow + (int64_t)hidx * 128 + e0;
+                store8<IO>(cb, co, lo);
+                store8<IO>(cb, co + 64, hi);
+            }
         }
-        store8<IO>(ob, oo, lo);
-        store8<IO>(ob, oo + 64, hi);
     };
 
-    auto compute = [&](Item& t) {
+    auto compute = [&](Item& t) __attribute__((always_inline)) {
         float c[8], s[8];
         if constexpr (SRC == SRC_CS)
         {
@@ -843,7 +992,7 @@ __global__ __launch_bounds__(256) void k_rope_nx(RopeArgs a, int nslice)
         #pragma unroll
         for (int p = 0; p < P; ++p)
             if ((t.slice * P + p) * 8 < H)    // wave-uniform: a pass past the last head is skipped whole
-                pass(t.tok, (t.slice * P + p) * 8 + grp, t.lo[p], t.hi[p], c, s);
+                pass(t.tok, (t.slice * P + p) * 8 + grp, t.lo[p], t.hi[p], c, s, APPEND ? t.crow : -1);
     };
 
     int64_t item = (int64_t)blockIdx.x * 4 + wave;
@@ -866,31 +1015,39 @@ __global__ __launch_bounds__(256) void k_rope_nx(RopeArgs a, int nslice)
 }
 
 // The k_rope_nx launch: head_dim 128 at prefill sizes (NeoX with rotary_dim 128, GPT-J with rotary_dim a
-// multiple of 4), plain RoPE (no paged append, no output rotation, no angle table), with a 16-byte aligned
-// {cos, sin} table when one is given.  A grid of
-// `wgs` four-wave workgroups per CU walks the items (one item per wave when 0).
-static bool rope_nx_ok(const RopeArgs& a, int rope_mode)
+// multiple of 4), from inv_freq or a 16-byte aligned {cos, sin} table (no angle table), plain, with the
+// paged append, and / or with the output rotations (16-byte aligned post-scales).  The grid walks the
+// items with the workgroups resident at once.
+// had: the launch carries the output rotations (exl3r_rope_had, exl3r_rope_paged_kv_had).
+static bool rope_nx_ok(const RopeArgs& a, int rope_mode, bool had = false)
 {
     const Tuning& tu = tuning();
+    auto a16 = [](const void* p) { return p == nullptr || aligned16(p); };
     // GPT-J: rotary_dim % 4 == 0 keeps each 16-byte table read (two pairs) inside the token's row.
-    if (tu.rope_nx < 0 || a.hd != 128 || (rope_mode == EXL3R_ROPE_NEOX ? a.R != 128 : a.R % 4 != 0) || a.kc || a.table)
+    if (tu.rope_nx < 0 || a.hd != 128 || (rope_mode == EXL3R_ROPE_NEOX ? a.R != 128 : a.R % 4 != 0) || a.table)
         return false;
-    if (a.q_post || a.k_post || a.v_post) return false;
+    if (tu.rope_tok != 0 && tu.rope_nx == 0) return false;   // a test forcing one of the other kernels
+    if (a.kc && a.hv != a.hk) return false;
+    // The paged append without the rotations stays with the wave-per-token kernel unless forced
+    // (MI355X, 4096-token prefill, same process: 39.7 us there against 43.0 us here).
+    if (a.kc && !had && tu.rope_nx <= 0) return false;
+    if (!a16(a.q_post) || !a16(a.k_post) || !a16(a.v_post)) return false;
     if (a.cst && ((uintptr_t)a.cst & 15)) return false;
     return tu.rope_nx > 0 || a.tokens >= 1024;
 }
 
-template <class IO, int MODE, int NORM, int SRC, bool QOUT, int P>
+template <class IO, int MODE, int NORM, int SRC, bool QOUT, int P, bool APPEND = false, bool HADR = false>
 static void launch_rope_nx_p(const RopeArgs& a, hipStream_t s)
 {
-    const int nslice = ((a.hq + a.hk + 7) / 8 + P - 1) / P;
+    const int nslice = ((a.hq + a.hk + (APPEND ? a.hv : 0) + 7) / 8 + P - 1) / P;
     const int64_t items = a.tokens * nslice;
     const size_t lds = SRC == SRC_FREQ ? 4 * 64 * sizeof(float2) : 0;
     // Grid: the workgroups resident at once (per CU, from the occupancy of this instance), each wave
     // walking its items i, i + W, ...
-    static const int resident = [lds] {   // workgroups per CU (per template instance; thread-safe init)
+    static const int resident = [&] {   // workgroups per CU (per template instance; thread-safe init)
         int nb = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_rope_nx<IO, MODE, NORM, SRC, QOUT, P>, 256, lds) != hipSuccess || nb < 1)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_rope_nx<IO, MODE, NORM, SRC, QOUT, P, APPEND, HADR>, 256,
+                                                         lds) != hipSuccess || nb < 1)
             nb = 4;
         return nb;
     }();
@@ -898,7 +1055,7 @@ static void launch_rope_nx_p(const RopeArgs& a, hipStream_t s)
     int64_t blocks = (int64_t)(wpc > 0 ? wpc : resident) * device_cus();
     if (blocks > (items + 3) / 4) blocks = (items + 3) / 4;
     if (blocks > kMaxGridX) blocks = kMaxGridX;
-    k_rope_nx<IO, MODE, NORM, SRC, QOUT, P><<<(unsigned)blocks, 256, lds, s>>>(a, nslice);
+    k_rope_nx<IO, MODE, NORM, SRC, QOUT, P, APPEND, HADR><<<(unsigned)blocks, 256, lds, s>>>(a, nslice);
 }
 
 // Passes per item: one for NeoX, two for GPT-J (its token's sin / cos or table row shared by two passes).
@@ -908,9 +1065,35 @@ static void launch_rope_nx_p(const RopeArgs& a, hipStream_t s)
 template <class IO, int MODE, int NORM, int SRC, bool QOUT>
 static void launch_rope_nx(const RopeArgs& a, hipStream_t s)
 {
+    if constexpr (!QOUT)
+    {
+        if (a.kc)
+        {
+            launch_rope_nx_p<IO, MODE, NORM, SRC, false, 1, true>(a, s);
+            return;
+        }
+    }
     const int tp = tuning().rope_nx;
     if (tp == 2 || (tp == 0 && MODE == EXL3R_ROPE_GPTJ && !QOUT)) launch_rope_nx_p<IO, MODE, NORM, SRC, QOUT, 2>(a, s);
     else launch_rope_nx_p<IO, MODE, NORM, SRC, QOUT, 1>(a, s);
+}
+
+// The output rotations (exl3r_rope_had, exl3r_rope_paged_kv_had) in the 8-lane kernel, f16 heads.
+template <int NORM>
+static void launch_had_nx(const RopeArgs& a, int rope_mode, hipStream_t s)
+{
+    auto go = [&](auto M) {
+        constexpr int MODE = decltype(M)::value;
+        if (a.kc)
+        {
+            if (a.cst) launch_rope_nx_p<TF16, MODE, NORM, SRC_CS, false, 1, true, true>(a, s);
+            else launch_rope_nx_p<TF16, MODE, NORM, SRC_FREQ, false, 1, true, true>(a, s);
+        }
+        else if (a.cst) launch_rope_nx_p<TF16, MODE, NORM, SRC_CS, false, 1, false, true>(a, s);
+        else launch_rope_nx_p<TF16, MODE, NORM, SRC_FREQ, false, 1, false, true>(a, s);
+    };
+    if (rope_mode == EXL3R_ROPE_GPTJ) go(std::integral_constant<int, EXL3R_ROPE_GPTJ>{});
+    else go(std::integral_constant<int, EXL3R_ROPE_NEOX>{});
 }
 
 // Generic fallback (any even head_dim / rotary_dim, any alignment): one workgroup per token, heads
@@ -1428,6 +1611,15 @@ extern "C" int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, 
     if ((rc = use_cs_table(op, a, cs_table))) return rc;
     a.q_post = q_post_scale;
     a.k_post = k_post_scale;
+    if (rope_vec_ok(a, rope_mode) && rope_nx_ok(a, rope_mode, true))
+    {
+        hipStream_t s = (hipStream_t)stream;
+        const int norm = rope_norm_kind(a, dtype);
+        if (norm == NORM_NONE) launch_had_nx<NORM_NONE>(a, rope_mode, s);
+        else if (norm == NORM_HALF) launch_had_nx<NORM_HALF>(a, rope_mode, s);
+        else launch_had_nx<NORM_F32>(a, rope_mode, s);
+        return launch_status(op);
+    }
     const bool fused = head_dim == 128 && rope_mode == EXL3R_ROPE_NEOX && rope_vec_ok(a, rope_mode) &&
                        rope_tok_launch(a) && (!q_post_scale || aligned16(q_post_scale)) &&
                        (!k_post_scale || aligned16(k_post_scale));
@@ -1491,6 +1683,15 @@ extern "C" int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok
     a.q_post = q_post_scale;
     a.k_post = k_post_scale;
     a.v_post = v_post_scale;
+    if (rope_vec_ok(a, rope_mode) && rope_nx_ok(a, rope_mode, true))
+    {
+        hipStream_t s = (hipStream_t)stream;
+        const int norm = rope_norm_kind(a, dtype);
+        if (norm == NORM_NONE) launch_had_nx<NORM_NONE>(a, rope_mode, s);
+        else if (norm == NORM_HALF) launch_had_nx<NORM_HALF>(a, rope_mode, s);
+        else launch_had_nx<NORM_F32>(a, rope_mode, s);
+        return launch_status(op);
+    }
     auto a16 = [](const void* p) { return p == nullptr || aligned16(p); };
     const bool fused = head_dim == 128 && rope_mode == EXL3R_ROPE_NEOX && rope_vec_ok(a, rope_mode) &&
                        rope_tok_launch(a) && a16(q_post_scale) && a16(k_post_scale) && a16(v_post_scale);

@@ -3,8 +3,10 @@ lane, items of one or two 8-head passes walked by a resident grid), forced throu
 of the sweep/test build on shapes the size rule would not give it: few tokens, head counts that mix q and
 k heads inside a pass or leave a pass part-empty, q only, GPT-J at several rotary dims, every weight
 dtype, no norm, out of place, packed q/k/v views, each position source, grids of 1 and 2 workgroups per
-CU (so each wave walks many items), the {cos, sin} table, and out_q in its own layout (exl3r_rope_qg).
-Each case is checked against the CPU oracle (<= 2 ulp, the RoPE bound)."""
+CU (so each wave walks many items), the {cos, sin} table, out_q in its own layout (exl3r_rope_qg), the
+paged append (exl3r_rope_paged_kv) and the projections' output rotations (exl3r_rope_had,
+exl3r_rope_paged_kv_had).  Each case is checked against the CPU oracle (<= 2 ulp, the RoPE bound; the
+caches bit for bit)."""
 import numpy as np
 import pytest
 import torch
@@ -131,3 +133,62 @@ def test_qg_out_layout(nx, passes):
     assert_close_ulp(from_dev(oq), eq, F16, 2, what=f"rope_qg nx{passes} q")
     assert_close_ulp(from_dev(k), ek, F16, 2, what=f"rope_qg nx{passes} k")
     assert np.array_equal(from_dev(qg), qgh), "qg modified"
+
+
+@pytest.mark.parametrize("case", ["neox_f16", "gptj_bf16", "mixed_passes", "no_norm_no_out_k", "bad_entries"])
+def test_paged_append(nx, case):
+    """exl3r_rope_paged_kv on the forced kernel (v heads after the k heads in the item space, k and v
+    rows written to the paged caches) against the oracle's rope then paged_kv_append."""
+    import test_gpu_rope_paged as P
+    nx(1)
+    if case == "neox_f16":
+        pages, bt, sl = P.layout(2, 45, 16, 8, 61)
+        P.run(2, 45, 16, 4, 128, 128, exl3r.ROPE_NEOX, F16, 16, pages, 8, sl, bt, seed=61)
+    elif case == "gptj_bf16":
+        pages, bt, sl = P.layout(3, 30, 32, 4, 62)
+        P.run(3, 30, 8, 2, 128, 64, exl3r.ROPE_GPTJ, BF16, 32, pages, 4, sl, bt, seed=62)
+    elif case == "mixed_passes":     # 12 q / 3 kv heads: passes holding q and k, and k and v heads
+        pages, bt, sl = P.layout(2, 37, 16, 8, 63)
+        P.run(2, 37, 12, 3, 128, 128, exl3r.ROPE_NEOX, F16, 16, pages, 8, sl, bt, seed=63)
+    elif case == "no_norm_no_out_k":
+        pages, bt, sl = P.layout(1, 90, 64, 4, 64)
+        P.run(1, 90, 16, 8, 128, 128, exl3r.ROPE_NEOX, F16, 64, pages, 4, sl, bt, norm=False, with_out_k=False,
+              seed=64)
+    else:
+        pages, bt, sl = P.layout(4, 20, 16, 4, 65)
+        bt[1, :] = pages + 7
+        sl[2] = 4 * 16 - 10
+        sl[3] = -3
+        P.run(4, 20, 8, 2, 128, 128, exl3r.ROPE_NEOX, F16, 16, pages, 4, sl, bt, seed=65)
+
+
+@pytest.mark.parametrize("case", ["neox", "gptj", "no_norm_missing_posts", "q_only", "out_of_place_bf16w"])
+def test_output_rotation(nx, case):
+    """exl3r_rope_had on the forced kernel: each head's output rotation on the 8-lane layout (bits 0-2 and 6
+    in-lane, bits 3-5 across the group), against the unfused calls and the oracle's had_r_128 then rope."""
+    import test_gpu_rope_had as RH
+    nx(1)
+    if case == "neox":
+        RH.run(1, 70, 12, 3, 128, 128, exl3r.ROPE_NEOX, position=21, seed=71)
+    elif case == "gptj":
+        RH.run(2, 30, 8, 2, 128, 64, exl3r.ROPE_GPTJ, nwt=F32, position=5, seed=72)
+    elif case == "no_norm_missing_posts":
+        RH.run(1, 40, 16, 4, 128, 128, exl3r.ROPE_NEOX, norm=False, q_post=False, seed=73)
+    elif case == "q_only":
+        RH.run(1, 33, 10, 0, 128, 128, exl3r.ROPE_NEOX, with_k=False, position=300, seed=74)
+    else:
+        RH.run(2, 25, 8, 8, 128, 128, exl3r.ROPE_NEOX, nwt=BF16, k_post=False, out_of_place=True, seed=75)
+
+
+@pytest.mark.parametrize("case", ["qwen3_shape", "mixed_passes_no_out_k", "bad_entry_posts"])
+def test_paged_output_rotation(nx, case):
+    """exl3r_rope_paged_kv_had on the forced kernel: q / k / v rotated, q / k normed and roped, k / v
+    appended; against the oracle composition and the unfused calls."""
+    import test_gpu_rope_paged_had as PH
+    nx(1)
+    if case == "qwen3_shape":
+        PH.run(1, 80, 64, 8, 16, 8, seed=81)
+    elif case == "mixed_passes_no_out_k":
+        PH.run(2, 30, 12, 3, 16, 4, with_out_k=False, posts=(True, False, True), seed=82)
+    else:
+        PH.run(3, 25, 8, 2, 16, 4, norm=False, posts=(False, True, False), bad_entry=True, seed=83)
