@@ -65,7 +65,8 @@ def parse():
 class Work:
     """One timed launch.  nbytes is the algorithmic byte count of a launch; hbm_bytes, when given, is
     the least HBM traffic that can serve it (a gather whose ids repeat reads each distinct table row
-    once and serves the repeats from L2 / MALL), and its frac_peak is taken over that."""
+    once and serves the repeats from L2 / MALL).  Such a launch's frac_peak is taken over the traffic
+    the rocprofv3 counters measured for it (the committed summary), or over hbm_bytes without one."""
     def __init__(self, name, nbytes, launch, desc, sets=1, hbm_bytes=None):
         self.name, self.nbytes, self.launch, self.desc, self.sets = name, nbytes, launch, desc, sets
         self.hbm_bytes = hbm_bytes
@@ -1064,11 +1065,15 @@ def main():
             ops[name] = {"desc": w.desc, "us": round(ms * 1000, 3), "us_min": round(windows[0] * 1000, 3),
                          "bytes": w.nbytes, "gbs": round(gbs, 1), "frac_peak": round(gbs / PEAK_GBS, 4)}
             if w.hbm_bytes is not None:
-                # repeats are cache hits: the HBM fraction is over the distinct rows' bytes, and the
-                # all-rows rate stays beside it as gbs
-                hbm_gbs = w.hbm_bytes / (ms * 1e-3) / 1e9
-                ops[name].update({"hbm_bytes": w.hbm_bytes, "hbm_gbs": round(hbm_gbs, 1),
-                                  "frac_peak": round(hbm_gbs / PEAK_GBS, 4)})
+                # repeats are cache hits: the HBM fraction is over the counted traffic (a row read by
+                # workgroups on several XCDs is fetched into each XCD's L2), else over the distinct rows'
+                # bytes; the all-rows rate stays beside it as gbs
+                counted = traffic_from_profiles(name)
+                hb = counted if counted else w.hbm_bytes
+                hbm_gbs = hb / (ms * 1e-3) / 1e9
+                ops[name].update({"hbm_bytes": hb, "hbm_bytes_source": "rocprofv3 FETCH/WRITE" if counted else
+                                  "distinct rows (lower bound)", "hbm_bytes_min": w.hbm_bytes,
+                                  "hbm_gbs": round(hbm_gbs, 1), "frac_peak": round(hbm_gbs / PEAK_GBS, 4)})
                 gbs = hbm_gbs
             extra = ""
             if name.endswith("_c1") or name.startswith("rope_kv_dec") or name.startswith("argmax_dec") or \
