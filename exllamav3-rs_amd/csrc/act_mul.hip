@@ -210,9 +210,15 @@ template <int ACT, class IT, class OT, int HAD = 0>
 static void launch_act_vec(const ActArgs& a, hipStream_t s)
 {
     const Tuning& tu = tuning();
-    // Two chunks per thread in 128-thread workgroups measured best on MI355X (C3: 136 us, 6.3 TB/s).
-    const int unroll = (tu.act_unroll == 1 || tu.act_unroll == 2 || tu.act_unroll == 4 || tu.act_unroll == 8) ? tu.act_unroll : 2;
-    const int threads = (tu.act_threads > 0 && tu.act_threads % 64 == 0 && tu.act_threads <= 256) ? tu.act_threads : 128;
+    // Two chunks per thread in 128-thread workgroups measured best on MI355X for streaming launches
+    // (C3: 136 us, 6.3 TB/s); up to 8M elements one chunk per thread in 256-thread workgroups (HIP graph,
+    // us, [rows, 17408] f16: 64 rows 3.15 vs 3.46, 256 rows 5.03 vs 5.41; [512, 3072] 3.24 vs 3.54; from
+    // 1024 rows the streaming shape wins, 16.9 vs 18.8).
+    const bool small = a.rows * a.cols <= ((int64_t)8 << 20);
+    const int unroll = (tu.act_unroll == 1 || tu.act_unroll == 2 || tu.act_unroll == 4 || tu.act_unroll == 8) ? tu.act_unroll
+                       : small ? 1 : 2;
+    const int threads = (tu.act_threads > 0 && tu.act_threads % 64 == 0 && tu.act_threads <= 256) ? tu.act_threads
+                        : small ? 256 : 128;
     const int64_t cpr = a.cols >> 3;
     if constexpr (HAD == 0)
     {

@@ -23,6 +23,13 @@ void require(bool ok, const std::string& msg)
     if (!ok) throw Error(EXL3R_EINVAL, msg);
 }
 
+// Literal messages (every check on the launch path): the string is built only when the check fails,
+// not on each call.
+void require(bool ok, const char* msg)
+{
+    if (!ok) throw Error(EXL3R_EINVAL, std::string(msg));
+}
+
 int code(DType t) { return (int)t; }
 int code_or(const Tensor* t, DType dflt) { return t ? (int)t->dtype : (int)dflt; }
 const void* ptr(const Tensor* t) { return t ? t->data : nullptr; }
