@@ -631,7 +631,7 @@ struct NxItem
 };
 
 // Wave-uniform values read from memory (an item's cache row and position) moved to scalar registers, so
-// that the two items in flight do not hold them in VGPRs.
+// that the two items in flight do not hold them in VGPRs (see UNIFORM_ITEM in k_rope_nx).
 __device__ __forceinline__ int uniform32(int v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ int64_t uniform64(int64_t v)
 {
@@ -707,10 +707,10 @@ __device__ __forceinline__ void rotate_head_nx(TF16::Vec& lo, TF16::Vec& hi, int
 // APPEND: v heads follow the k heads in the item space; k and v rows are written to the paged caches
 // (exl3r_rope_paged_kv).  HADR: every head is first replaced by its projection's output rotation
 // (exl3r_rope_had, exl3r_rope_paged_kv_had).  Both take one pass per item.
-// The paged + rotating instance evaluating sin / cos lands one VGPR above the five-wave budget (97 of
-// 96); it is held to five waves per SIMD.
+// The rotating instances evaluating sin / cos land just above the five-wave budget (97 VGPRs of 96); they
+// are held to five waves per SIMD (no spill: see UNIFORM_ITEM).
 template <bool APPEND, bool HADR, int SRC>
-constexpr int kNxMinWaves = APPEND && HADR && SRC == SRC_FREQ ? 5 : 1;
+constexpr int kNxMinWaves = HADR && SRC == SRC_FREQ ? 5 : 1;
 
 template <class IO, int MODE, int NORM, int SRC, bool QOUT, int P, bool APPEND = false, bool HADR = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kNxMinWaves<APPEND, HADR, SRC>)))
@@ -718,6 +718,12 @@ void k_rope_nx(RopeArgs a, int nslice)
 {
     static_assert(!(APPEND || HADR) || (P == 1 && !QOUT), "paged / rotating items are single passes");
     static_assert(!HADR || IO::code == DT_F16, "output rotation: f16 heads");
+    // An item's position and cache row moved to scalar registers when they are loaded: the wait for
+    // them then falls in issue(), before the current item's work, which costs 0.9-1.4 us at C4 (36.5
+    // vs 35.1 us NeoX, 34.2 vs 33.3 GPT-J, same process); only the paged + rotating instance evaluating
+    // sin / cos takes it, since without the VGPRs it frees that instance spills under its five-wave
+    // hold (58.9 vs 64.0 us).
+    constexpr bool UNIFORM_ITEM = APPEND && HADR && SRC == SRC_FREQ;
     extern __shared__ float2 cs[];            // [4 waves][64] (SRC_FREQ)
     // Norm weights with the constant bias folded in, q then k: h(w + h(cb)) (NORM_HALF) or w + cb (NORM_F32).
     __shared__ __align__(16) float wsh[256];
@@ -757,16 +763,23 @@ void k_rope_nx(RopeArgs a, int nslice)
             const int h = (t.slice * P + p) * 8 + grp;
             if (h < H)
             {
-                const bool iq = h < hq, iv = APPEND && h >= hq + hk;
-                const int hi = h - (iq ? 0 : hq) - (iv ? hk : 0);
-                const int64_t ts = pick_qkv(iq, iv, q_ts, k_ts, v_ts), hs = pick_qkv(iq, iv, q_hs, k_hs, v_hs);
-                const char* base = pick_qkv(iq, iv, qin, kin, vin) + (t.tok * ts + (int64_t)hi * hs) * IO::bytes;
+                const char* base;
+                if constexpr (APPEND)
+                {
+                    const bool iq = h < hq, iv = h >= hq + hk;
+                    const int hi = h - (iq ? 0 : hq) - (iv ? hk : 0);
+                    const int64_t ts = pick_qkv(iq, iv, q_ts, k_ts, v_ts), hs = pick_qkv(iq, iv, q_hs, k_hs, v_hs);
+                    base = pick_qkv(iq, iv, qin, kin, vin) + (t.tok * ts + (int64_t)hi * hs) * IO::bytes;
+                }
+                else   // two choices: plain selects (the mask form costs this kernel ~0.5 us at C4)
+                    base = h < hq ? qin + (t.tok * q_ts + (int64_t)h * q_hs) * IO::bytes
+                                  : kin + (t.tok * k_ts + (int64_t)(h - hq) * k_hs) * IO::bytes;
                 t.lo[p] = load8s<IO>(base, e0);
                 t.hi[p] = load8s<IO>(base, e0 + 64);
             }
         }
         // The cache row, once per item that holds k or v heads (wave-uniform).
-        if constexpr (APPEND) t.crow = (t.slice + 1) * 8 > hq ? uniform64(cache_row(a, t.tok)) : -1;
+        if constexpr (APPEND) t.crow = (t.slice + 1) * 8 > hq ? (UNIFORM_ITEM ? uniform64(cache_row(a, t.tok)) : cache_row(a, t.tok)) : -1;
         if constexpr (SRC == SRC_CS)
         {
             // NeoX: pairs e0 .. e0 + 7; GPT-J: pairs e0/2 .. e0/2 + 3 (lo chunk) and 32 + e0/2 .. (hi chunk)
@@ -787,7 +800,7 @@ void k_rope_nx(RopeArgs a, int nslice)
             }
         }
         else
-            t.pos = uniform32(token_position(a, (int)t.tok));
+            t.pos = UNIFORM_ITEM ? uniform32(token_position(a, (int)t.tok)) : token_position(a, (int)t.tok);
     };
 
     if constexpr (NORM != NORM_NONE)
