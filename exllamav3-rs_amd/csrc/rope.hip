@@ -1824,3 +1824,85 @@ extern "C" int exl3r_rope_qg(const void* qg, int64_t qg_tok_stride, void* out_q,
     if (o0 < q1 && q0 < o1) return set_error(EXL3R_EINVAL, "%s: out_q overlaps qg", op);
     return rope_dispatch(op, a, dtype, rope_mode, stream);
 }
+
+// The descriptor form of every RoPE entry point above: checks that one variant is named, then calls
+// its entry point, whose checks, results and errors it has.
+extern "C" int exl3r_rope_run(const exl3r_rope_desc* d, void* stream)
+{
+    clear_stale_error();
+    const char* op = "exl3r_rope_run";
+    if (!d) return set_error(EXL3R_EINVAL, "%s: descriptor must be non-null", op);
+    if (d->struct_size < (int32_t)sizeof(exl3r_rope_desc))
+        return set_error(EXL3R_EINVAL, "%s: struct_size %d < sizeof(exl3r_rope_desc) %d", op, d->struct_size,
+                         (int)sizeof(exl3r_rope_desc));
+    const int sources = (d->inv_freq != nullptr) + (d->angle_table != nullptr) + (d->cs_table != nullptr);
+    const bool cs_with_freq = d->cs_table && d->inv_freq && !d->angle_table;   // rotate / k_cache forms
+    if (sources == 0) return set_error(EXL3R_EINVAL, "%s: no rotation source (inv_freq, angle_table or cs_table)", op);
+    if (sources > 1 && !(cs_with_freq && (d->rotate || d->k_cache)))
+        return set_error(EXL3R_EINVAL, "%s: more than one rotation source", op);
+    const int64_t oq_ts = d->out_q_tok_stride ? d->out_q_tok_stride : d->q_tok_stride;
+    const int64_t oq_hs = d->out_q_head_stride ? d->out_q_head_stride : d->q_head_stride;
+    const bool own_layout = oq_ts != d->q_tok_stride || oq_hs != d->q_head_stride;
+    const bool post = d->q_post_scale || d->k_post_scale || d->v_post_scale;
+    if (!d->rotate && post) return set_error(EXL3R_EINVAL, "%s: post-scales given without rotate", op);
+    if (!d->k_cache && (d->v || d->v_cache || d->block_table || d->cache_seqlens))
+        return set_error(EXL3R_EINVAL, "%s: v / v_cache / block_table / cache_seqlens given without k_cache", op);
+    if ((d->rotate || d->k_cache) && d->angle_table)
+        return set_error(EXL3R_EINVAL, "%s: the rotating and paged forms take inv_freq or cs_table, not an angle table", op);
+    if (own_layout && (d->rotate || d->k_cache || d->angle_table || d->cs_table))
+        return set_error(EXL3R_EINVAL, "%s: an out_q layout of its own is the q | g split only (inv_freq, no cache, no rotation)", op);
+    const int64_t hd = d->head_dim;
+    if (d->rotate)
+    {
+        // The rotating forms take packed heads (head stride = head_dim).
+        if (d->q_head_stride != hd || (d->k && d->k_head_stride != hd) || (d->v && d->v_head_stride != hd))
+            return set_error(EXL3R_EINVAL, "%s: rotate takes packed heads (head strides equal to head_dim)", op);
+        if (d->k_cache)
+            return exl3r_rope_paged_kv_had(d->q, d->out_q, d->q_tok_stride, d->num_heads_q, d->k, d->out_k, d->k_tok_stride,
+                                           d->v, d->v_tok_stride, d->num_heads_k, d->dtype, d->bsz, d->seq_len,
+                                           d->head_dim, d->inv_freq, d->rotary_dim, d->position, d->positions,
+                                           d->position_ids, d->q_norm, d->k_norm, d->norm_dtype, d->norm_eps,
+                                           d->norm_constant_bias, d->rope_mode, d->attn_factor, d->k_cache, d->v_cache,
+                                           d->page_size, d->num_pages, d->block_table, d->max_blocks_per_seq,
+                                           d->cache_seqlens, d->err_flag, d->q_post_scale, d->k_post_scale,
+                                           d->v_post_scale, d->cs_table, stream);
+        return exl3r_rope_had(d->q, d->out_q, d->q_tok_stride, d->num_heads_q, d->k, d->out_k, d->k_tok_stride,
+                              d->num_heads_k, d->dtype, d->bsz, d->seq_len, d->head_dim, d->inv_freq, d->rotary_dim,
+                              d->position, d->positions, d->position_ids, d->q_norm, d->k_norm, d->norm_dtype,
+                              d->norm_eps, d->norm_constant_bias, d->rope_mode, d->attn_factor, d->q_post_scale,
+                              d->k_post_scale, d->cs_table, stream);
+    }
+    if (d->k_cache)
+        return exl3r_rope_paged_kv(d->q, d->out_q, d->q_tok_stride, d->q_head_stride, d->num_heads_q, d->k, d->out_k,
+                                   d->k_tok_stride, d->k_head_stride, d->v, d->v_tok_stride, d->v_head_stride,
+                                   d->num_heads_k, d->dtype, d->bsz, d->seq_len, d->head_dim, d->inv_freq,
+                                   d->rotary_dim, d->position, d->positions, d->position_ids, d->q_norm, d->k_norm,
+                                   d->norm_dtype, d->norm_eps, d->norm_constant_bias, d->rope_mode, d->attn_factor,
+                                   d->k_cache, d->v_cache, d->page_size, d->num_pages, d->block_table,
+                                   d->max_blocks_per_seq, d->cache_seqlens, d->err_flag, d->cs_table, stream);
+    if (d->angle_table)
+        return exl3r_rope_table(d->q, d->out_q, d->q_tok_stride, d->q_head_stride, d->num_heads_q, d->k, d->out_k,
+                                d->k_tok_stride, d->k_head_stride, d->num_heads_k, d->dtype, d->bsz, d->seq_len,
+                                d->head_dim, d->angle_table, d->table_rows, d->table_batch_stride, d->rotary_dim,
+                                d->position, d->positions, d->position_ids, d->q_norm, d->k_norm, d->norm_dtype,
+                                d->norm_eps, d->norm_constant_bias, d->rope_mode, d->attn_factor, d->err_flag, stream);
+    if (own_layout)
+    {
+        if (d->q_head_stride != 2 * hd || oq_hs != hd || oq_ts != (int64_t)d->num_heads_q * hd)
+            return set_error(EXL3R_EINVAL, "%s: an out_q layout of its own is the q | g split: q head stride 2 * head_dim "
+                             "and a dense out_q", op);
+        return exl3r_rope_qg(d->q, d->q_tok_stride, d->out_q, d->num_heads_q, d->k, d->out_k, d->k_tok_stride,
+                             d->k_head_stride, d->num_heads_k, d->dtype, d->bsz, d->seq_len, d->head_dim, d->inv_freq,
+                             d->rotary_dim, d->position, d->positions, d->position_ids, d->q_norm, d->k_norm,
+                             d->norm_dtype, d->norm_eps, d->norm_constant_bias, d->rope_mode, d->attn_factor, stream);
+    }
+    if (d->cs_table)
+        return exl3r_rope_cs(d->q, d->out_q, d->q_tok_stride, d->q_head_stride, d->num_heads_q, d->k, d->out_k,
+                             d->k_tok_stride, d->k_head_stride, d->num_heads_k, d->dtype, d->bsz, d->seq_len, d->head_dim,
+                             d->cs_table, d->rotary_dim, d->q_norm, d->k_norm, d->norm_dtype, d->norm_eps,
+                             d->norm_constant_bias, d->rope_mode, stream);
+    return exl3r_rope(d->q, d->out_q, d->q_tok_stride, d->q_head_stride, d->num_heads_q, d->k, d->out_k, d->k_tok_stride,
+                      d->k_head_stride, d->num_heads_k, d->dtype, d->bsz, d->seq_len, d->head_dim, d->inv_freq,
+                      d->rotary_dim, d->position, d->positions, d->position_ids, d->q_norm, d->k_norm, d->norm_dtype,
+                      d->norm_eps, d->norm_constant_bias, d->rope_mode, d->attn_factor, stream);
+}

@@ -23,7 +23,25 @@ _i64 = ctypes.c_int64
 _f = ctypes.c_float
 _i32 = ctypes.c_int32
 
+
+class RopeDesc(ctypes.Structure):
+    """exl3r_rope_desc of include/exl3r/rowops.h, field for field (exl3r_rope_run)."""
+    _fields_ = [("struct_size", _i32), ("dtype", _i32), ("bsz", _i64), ("seq_len", _i64), ("head_dim", _i32),
+                ("rotary_dim", _i32), ("rope_mode", _i32), ("attn_factor", _f), ("q", _vp), ("out_q", _vp),
+                ("q_tok_stride", _i64), ("q_head_stride", _i64), ("out_q_tok_stride", _i64),
+                ("out_q_head_stride", _i64), ("num_heads_q", _i32), ("num_heads_k", _i32), ("k", _vp),
+                ("out_k", _vp), ("k_tok_stride", _i64), ("k_head_stride", _i64), ("inv_freq", _vp),
+                ("angle_table", _vp), ("table_rows", _i64), ("table_batch_stride", _i64), ("cs_table", _vp),
+                ("positions", _vp), ("position_ids", _vp), ("position", _i32), ("norm_dtype", _i32),
+                ("q_norm", _vp), ("k_norm", _vp), ("norm_eps", _f), ("norm_constant_bias", _f),
+                ("rotate", _i32), ("page_size", _i32), ("q_post_scale", _vp), ("k_post_scale", _vp),
+                ("v_post_scale", _vp), ("v", _vp), ("v_tok_stride", _i64), ("v_head_stride", _i64),
+                ("k_cache", _vp), ("v_cache", _vp), ("num_pages", _i64), ("max_blocks_per_seq", _i64),
+                ("block_table", _vp), ("cache_seqlens", _vp), ("err_flag", _vp)]
+
+
 PROTOTYPES = {
+    "exl3r_rope_run": (_i, [ctypes.POINTER(RopeDesc), _vp]),
     "exl3r_version": (_i, []),
     "exl3r_last_error": (ctypes.c_char_p, []),
     "exl3r_rms_norm": (_i, [_vp, _i, _i64, _vp, _i, _vp, _i, _i64, _i64, _i64, _f, _f, _f, _vp]),

@@ -11,7 +11,7 @@ import math
 
 import torch
 
-from ._lib import BF16, F16, F32, I32, I64, check, load
+from ._lib import BF16, F16, F32, I32, I64, RopeDesc, check, load
 
 _DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.int32: I32, torch.int64: I64}
 
@@ -412,7 +412,7 @@ def rope_paged_kv_had(q, out_q, k, out_k, v, inv_freq, position, positions, q_no
                       stream=None, cs_table=None):
     """rope_paged_kv() on the raw f16 outputs of the q / k / v projections (heads packed), each first given
     its projection's output rotation had_r_128(y, y, None, svh) (src/modules.rs:231).  Outside the fused
-    launch (NeoX, head_dim 128, >= 1024 tokens) v, and k when out_k is None, are rotated in place."""
+    launch (head_dim 128, 16-byte aligned) v, and k when out_k is None, are rotated in place."""
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q, k, v must be (bsz, seq_len, heads, head_dim)")
     bsz, seq, hq, hd = q.shape
@@ -440,6 +440,27 @@ def rope_paged_kv_had(q, out_q, k, out_k, v, inv_freq, position, positions, q_no
                                          _ptr(block_table), block_table.shape[1], _ptr(cache_seqlens), _ptr(err_flag),
                                          _ptr(q_post_scale), _ptr(k_post_scale), _ptr(v_post_scale),
                                          _ptr(cs_table), _stream(q, stream)))
+
+
+def rope_run(stream=None, **fields):
+    """exl3r_rope_run: every RoPE variant through one descriptor (exl3r_rope_desc).  Fields by name;
+    tensors pass their device pointers, None a null pointer, the rest their values; struct_size is set
+    here.  The variant and its checks follow from the fields that are set (see the header)."""
+    d = RopeDesc()
+    d.struct_size = ctypes.sizeof(RopeDesc)
+    names = {f[0] for f in RopeDesc._fields_}
+    first = None
+    for key, val in fields.items():
+        if key not in names or key == "struct_size":
+            raise TypeError(f"rope_run: unknown field {key}")
+        if isinstance(val, torch.Tensor):
+            first = first if first is not None else val
+            val = val.data_ptr()
+        elif val is None:
+            val = 0
+        setattr(d, key, val)
+    s = _stream(first, stream) if first is not None else (stream or 0)
+    check(load().exl3r_rope_run(ctypes.byref(d), s))
 
 
 def argmax_sample(logits, ids, max_logit=0, stream=None):

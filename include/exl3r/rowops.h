@@ -294,7 +294,7 @@ EXL3R_API int exl3r_rope_cs(const void* q, void* out_q, int64_t q_tok_stride, in
  * packed (head stride = head_dim), heads * head_dim a multiple of 128; q_post_scale / k_post_scale:
  * f16 [heads * head_dim] (the projections' svh) or NULL.  Other arguments as exl3r_rope.  q and k are
  * only read when out_q / out_k differ from them.  Bit-identical to exl3r_had_r_128 on q and k
- * followed by exl3r_rope.  NeoX, head_dim 128, 16-byte aligned, 1024 or more tokens: one fused
+ * followed by exl3r_rope.  head_dim 128 (NeoX at rotary_dim 128, or GPT-J at a rotary_dim multiple of 4), 16-byte aligned: one fused
  * launch; otherwise the rotations run into out_q / out_k and exl3r_rope in place there.
  *   cs_table: NULL, or a {cos, sin} table that exl3r_rope_cs_table filled for the same positions,
  *             inv_freq, rotary_dim and attn_factor; the rotary pairs are then read from it (inv_freq
@@ -315,8 +315,8 @@ EXL3R_API int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, i
  * and paged_kv_cache_update (src/modules.rs:669-704).  q, k, v: f16 with heads packed (head stride =
  * head_dim), heads * head_dim a multiple of 128; *_post_scale: f16 [heads * head_dim] (svh) or NULL.
  * Other arguments as exl3r_rope_paged_kv.  Bit-identical to exl3r_had_r_128 on q, k and v followed by
- * exl3r_rope_paged_kv.  NeoX, head_dim 128, 16-byte aligned, 1024 or more tokens: one fused launch that
- * writes only out_q, out_k (if given) and the caches.  Otherwise the rotations run first -- q into
+ * exl3r_rope_paged_kv.  head_dim 128 (NeoX at rotary_dim 128, or GPT-J at a rotary_dim multiple of 4), 16-byte aligned: one fused
+ * launch that writes only out_q, out_k (if given) and the caches.  Otherwise the rotations run first -- q into
  * out_q, k into out_k (into k itself when out_k is NULL) and v in place -- then exl3r_rope_paged_kv.
  * cs_table: as exl3r_rope_had.
  */
@@ -365,6 +365,66 @@ EXL3R_API int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_stri
                         void* k_cache, void* v_cache, int page_size, int64_t num_pages,
                         const int32_t* block_table, int64_t max_blocks_per_seq, const int32_t* cache_seqlens,
                         int32_t* err_flag, const void* cs_table, void* stream);
+
+/*
+ * Every RoPE variant above through one descriptor: the variant follows from the fields that are set,
+ * so a further fusion adds fields here instead of another entry point.  No counterpart in the
+ * reference (its RoPE is one shim, exl3_shim_rope); for callers that build their arguments once per
+ * layer and for bindings that would otherwise mirror eight signatures.  Semantics, results and errors
+ * are those of the entry point it selects:
+ *   rotate != 0 (the projections' output rotations; q_post_scale / k_post_scale / v_post_scale)
+ *                      -> exl3r_rope_paged_kv_had with k_cache, else exl3r_rope_had (heads packed);
+ *   k_cache != NULL    -> exl3r_rope_paged_kv (v, caches, block table, cache_seqlens, err_flag);
+ *   angle_table        -> exl3r_rope_table (table_rows, table_batch_stride, err_flag);
+ *   out_q in its own layout (q_head_stride = 2 * head_dim, out_q dense: the gated q | g split)
+ *                      -> exl3r_rope_qg;
+ *   cs_table           -> exl3r_rope_cs;
+ *   otherwise          -> exl3r_rope.
+ * One rotation source: inv_freq, angle_table or cs_table (rotate and k_cache accept cs_table with
+ * inv_freq too, as their entry points do).  out_q_tok_stride and out_q_head_stride of 0 mean q's.
+ * struct_size must be at least sizeof(exl3r_rope_desc) as this header declares it.
+ */
+typedef struct exl3r_rope_desc
+{
+    int32_t struct_size;
+    int32_t dtype;
+    int64_t bsz, seq_len;
+    int32_t head_dim, rotary_dim;
+    int32_t rope_mode;
+    float attn_factor;
+    const void* q;
+    void* out_q;
+    int64_t q_tok_stride, q_head_stride, out_q_tok_stride, out_q_head_stride;
+    int32_t num_heads_q, num_heads_k;
+    const void* k;
+    void* out_k;
+    int64_t k_tok_stride, k_head_stride;
+    const float* inv_freq;
+    const float* angle_table;
+    int64_t table_rows, table_batch_stride;
+    const void* cs_table;
+    const int32_t* positions;
+    const int32_t* position_ids;
+    int32_t position;
+    int32_t norm_dtype;
+    const void* q_norm;
+    const void* k_norm;
+    float norm_eps, norm_constant_bias;
+    int32_t rotate, page_size;
+    const void* q_post_scale;
+    const void* k_post_scale;
+    const void* v_post_scale;
+    const void* v;
+    int64_t v_tok_stride, v_head_stride;
+    void* k_cache;
+    void* v_cache;
+    int64_t num_pages, max_blocks_per_seq;
+    const int32_t* block_table;
+    const int32_t* cache_seqlens;
+    int32_t* err_flag;
+} exl3r_rope_desc;
+
+EXL3R_API int exl3r_rope_run(const exl3r_rope_desc* d, void* stream);
 
 /*
  * Row argmax of logits [rows, vocab] (row stride ld elements; F16/BF16/F32) into int64 ids[rows]:
