@@ -46,13 +46,14 @@ struct Tuning
 {
     int rms_maxv = 0, rms_threads = 0;
     int rms_rows_rpl = 0;
-    int rms_split = 0, rms_split_wm = 1;   // split chunks: -1 never, 0 auto, 1 always; weight mode (1 mid, 2 late)    // short-row RMSNorm kernel: rows per lane in flight (1, 2, 4; 0 auto)
+    int rms_split = 0, rms_split_wm = 1;   // split chunks: -1 never, 0 auto, 1 always; weight mode (1 mid, 2 late)
     int act_unroll = 0, act_threads = 0, act_blocks_per_cu = 0;
     int rope_iters = 0;
     int rope_tok = 0;       // 0 auto, 1 never the wave-per-token kernel, 2 always (where it applies)
     int rope_hpl = 0;       // heads per lane in flight of the wave-per-token kernel (2, 4, 6, 8)
     int rope_wgs_per_cu = 0; // wave-per-token kernel: persistent grid of this many workgroups per CU (0: one token per wave)
     int rope_nx = 0;         // NeoX 128 kernel of 8 lanes per head: 0 auto, -1 never, 1..3 always with that many passes per wave
+    int rope_nx_run = 0;     // ... consecutive items of one wave (a token's angles evaluated once per run; 0 auto)
     int sample_rows_min = 0; // argmax / Gumbel: rows from which a workgroup owns a row (0: 512)
     int sample_threads = 0;  // ... and its lanes (256, 512, 1024; 0: 256)
     int had_unroll = 0;      // Hadamard: 128-blocks per 16-lane group (1, 2, 4; 0: 1)

@@ -589,9 +589,9 @@ inline RmsShape rms_shape(int nc, int64_t rows, int mode, int had, bool wide = f
     constexpr int split_mode = 0, split_wm = W_MID;
 #endif
     if (split_ok && (split_mode == 1 || (split_mode == 0 && wide && rows > 1024))) return split_shape(split_wm);
-    RmsShape sh{ 0, 0, W_EARLY };
 #ifdef EXL3R_TUNING
     const Tuning& tu = tuning();
+    RmsShape sh{ 0, 0, W_EARLY };
     if ((tu.rms_maxv == 1 || tu.rms_maxv == 2 || tu.rms_maxv == 4 || tu.rms_maxv == 8) &&
         (tu.rms_threads == 0 || (tu.rms_threads % 64 == 0 && tu.rms_threads <= 1024)))
     {

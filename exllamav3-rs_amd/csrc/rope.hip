@@ -616,9 +616,10 @@ __global__ __launch_bounds__(256) void k_rope_tok(RopeArgs a)
 // inside a chunk -- with no partner exchange; the head sum is a 3-step DPP butterfly, and each 16-byte
 // load or store instruction covers whole 128-byte lines of 8 heads.  An item is one pass
 // of 8 heads of one token (items in token order, a token's q passes then its k pass).  Each wave
-// walks items i, i + W, i + 2W, ... (W waves in the grid), so the waves in flight sweep the rows in
-// order; the next item's loads (and its {cos, sin} table row) are issued before the current item is
-// computed.  Evaluated rotary pairs: one sin / cos per lane into the wave's LDS row, per item.
+// walks runs of `run` consecutive items, run r of wave g being items [(g + r W) run, (g + r W + 1) run)
+// (W waves in the grid), so the waves in flight sweep the rows in order; the next item's loads (and
+// its {cos, sin} table row) are issued before the current item is computed.  Evaluated rotary pairs:
+// one sin / cos per lane into the wave's LDS row, once per token within a run.
 template <class IO, int NORM, int SRC, int P>
 struct NxItem
 {
@@ -714,7 +715,7 @@ constexpr int kNxMinWaves = HADR && SRC == SRC_FREQ ? 5 : 1;
 
 template <class IO, int MODE, int NORM, int SRC, bool QOUT, int P, bool APPEND = false, bool HADR = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kNxMinWaves<APPEND, HADR, SRC>)))
-void k_rope_nx(RopeArgs a, int nslice)
+void k_rope_nx(RopeArgs a, int nslice, int run)
 {
     static_assert(!(APPEND || HADR) || (P == 1 && !QOUT), "paged / rotating items are single passes");
     static_assert(!HADR || IO::code == DT_F16, "output rotation: f16 heads");
@@ -751,6 +752,7 @@ void k_rope_nx(RopeArgs a, int nslice)
     const int64_t oq_ts = QOUT ? a.oq_ts : q_ts, oq_hs = QOUT ? a.oq_hs : q_hs;
     const int R = a.R, R2 = a.R >> 1;
     using Item = NxItem<IO, NORM, SRC, P>;
+    int64_t evaluated = -1;                   // SRC_FREQ: the token whose pairs the wave's LDS row holds
 
     // Loads of one item: the lane's two chunks of head (slice * P + p) * 8 + grp for each of the P passes,
     // and its rotary pairs (SRC_CS) or the token's position (SRC_FREQ).
@@ -989,9 +991,13 @@ void k_rope_nx(RopeArgs a, int nslice)
         else
         {
             float2* row = cs + wave * 64;
-            wave_lds_sync();
-            if (l64 < R2) row[l64] = rope_cs<SRC_FREQ>(a, l64, (int)t.tok, t.pos);
-            wave_lds_sync();
+            if (t.tok != evaluated)           // wave-uniform: once per token within a run
+            {
+                wave_lds_sync();
+                if (l64 < R2) row[l64] = rope_cs<SRC_FREQ>(a, l64, (int)t.tok, t.pos);
+                wave_lds_sync();
+                evaluated = t.tok;
+            }
             #pragma unroll
             for (int j = 0; j < 8; ++j)
             {
@@ -1008,18 +1014,24 @@ void k_rope_nx(RopeArgs a, int nslice)
                 pass(t.tok, (t.slice * P + p) * 8 + grp, t.lo[p], t.hi[p], c, s, APPEND ? t.crow : -1);
     };
 
-    int64_t item = (int64_t)blockIdx.x * 4 + wave;
+    int64_t item = ((int64_t)blockIdx.x * 4 + wave) * run;
     if (item >= items) return;
+    int j = 0;                                // item's place in its run
+    auto next = [&](int64_t it) __attribute__((always_inline)) -> int64_t {
+        if (++j < run) return it + 1;
+        j = 0;
+        return it + 1 + (W - 1) * run;
+    };
     Item A, B;
     issue(A, item);
     for (;;)
     {
         // Issue the next item's loads, then finish this one (the loop alternates the two buffers).
-        const int64_t nb = item + W;
+        const int64_t nb = next(item);
         if (nb < items) issue(B, nb);
         compute(A);
         if (nb >= items) break;
-        const int64_t na = nb + W;
+        const int64_t na = next(nb);
         if (na < items) issue(A, na);
         compute(B);
         if (na >= items) break;
@@ -1069,9 +1081,19 @@ static void launch_rope_nx_p(const RopeArgs& a, hipStream_t s)
     }();
     const int wpc = tuning().rope_wgs_per_cu;
     int64_t blocks = (int64_t)(wpc > 0 ? wpc : resident) * device_cus();
-    if (blocks > (items + 3) / 4) blocks = (items + 3) / 4;
+    // Items a wave takes in a row, its token's angles evaluated once within them, where every wave gets
+    // whole runs (prefill sizes).  MI355X, same process, us at runs of 1 / 2 / 3: C4 NeoX 33.2 / 32.1 /
+    // 33.3; q / k rotations + RoPE at C4 46.8 / 45.5 / 42.7; q / k / v rotations + RoPE + paged append at
+    // 4096 tokens 57.5 / 53.4 / 51.3, from the {cos, sin} table 48.4 / 47.1 / 46.1 (the post-scales and
+    // cache rows of one token reused too).  Two passes per item (GPT-J) and the plain kernel reading the
+    // table are fastest at 1.
+    constexpr int kRun = HADR ? 3 : SRC == SRC_FREQ && P == 1 && !QOUT ? 2 : 1;
+    const int tr = tuning().rope_nx_run;
+    const int run = tr > 0 ? tr : items >= (int64_t)kRun * blocks * 4 ? kRun : 1;
+    const int64_t runs = (items + run - 1) / run;
+    if (blocks > (runs + 3) / 4) blocks = (runs + 3) / 4;
     if (blocks > kMaxGridX) blocks = kMaxGridX;
-    k_rope_nx<IO, MODE, NORM, SRC, QOUT, P, APPEND, HADR><<<(unsigned)blocks, 256, lds, s>>>(a, nslice);
+    k_rope_nx<IO, MODE, NORM, SRC, QOUT, P, APPEND, HADR><<<(unsigned)blocks, 256, lds, s>>>(a, nslice, run);
 }
 
 // Passes per item: one for NeoX, two for GPT-J (its token's sin / cos or table row shared by two passes).

@@ -3,7 +3,8 @@ lane, items of one or two 8-head passes walked by a resident grid), forced throu
 of the sweep/test build on shapes the size rule would not give it: few tokens, head counts that mix q and
 k heads inside a pass or leave a pass part-empty, q only, GPT-J at several rotary dims, every weight
 dtype, no norm, out of place, packed q/k/v views, each position source, grids of 1 and 2 workgroups per
-CU (so each wave walks many items), the {cos, sin} table, out_q in its own layout (exl3r_rope_qg), the
+CU (so each wave walks many items), runs of consecutive items per wave (a token's angles evaluated
+once per run, runs crossing tokens), the {cos, sin} table, out_q in its own layout (exl3r_rope_qg), the
 paged append (exl3r_rope_paged_kv) and the projections' output rotations (exl3r_rope_had,
 exl3r_rope_paged_kv_had).  Each case is checked against the CPU oracle (<= 2 ulp, the RoPE bound; the
 caches bit for bit)."""
@@ -26,11 +27,12 @@ F16, BF16, F32 = orc.F16, orc.BF16, orc.F32
 @pytest.fixture
 def nx():
     """Forces the 8-lane kernel with `passes` (1, 2) passes per item on a grid of `wpc` workgroups per CU
-    (0: the resident grid)."""
+    (0: the resident grid), each wave taking `run` consecutive items at a time (0: the automatic choice)."""
     with L.tuned() as lib:
-        def set_(passes, wpc=0):
+        def set_(passes, wpc=0, run=0):
             lib.exl3r_tune_rope_nx(passes)
             lib.exl3r_tune_rope_tok(0, 0, wpc)
+            lib.exl3r_tune_rope_nx_run(run)
         yield set_
 
 
@@ -97,6 +99,10 @@ def test_packed_qkv_views(nx, passes):
 def test_cs_table(nx, passes, mode, R):
     """exl3r_rope_cs on the forced kernel against the oracle (the table row read per item)."""
     nx(passes)
+    cs_case(mode, R, f"nx{passes}")
+
+
+def cs_case(mode, R, tag):
     bsz, seq, hq, hk, hd = 3, 90, 10, 3, 128
     q = dev_normal((bsz, seq, hq, hd), 0, 1, F16, 40)
     k = dev_normal((bsz, seq, hk, hd), 0, 1, F16, 41)
@@ -109,8 +115,8 @@ def test_cs_table(nx, passes, mode, R):
     torch.cuda.synchronize()
     eq, ek = orc.rope(qh, kh, F16, f, mode, positions=pos, q_norm=from_dev(qn), k_norm=from_dev(kn), nwt=F16,
                       eps=1e-6, attn=0.8, nthreads=NTHREADS)
-    assert_close_ulp(from_dev(q), eq, F16, 2, what=f"rope_cs nx{passes} mode{mode} q")
-    assert_close_ulp(from_dev(k), ek, F16, 2, what=f"rope_cs nx{passes} mode{mode} k")
+    assert_close_ulp(from_dev(q), eq, F16, 2, what=f"rope_cs {tag} mode{mode} q")
+    assert_close_ulp(from_dev(k), ek, F16, 2, what=f"rope_cs {tag} mode{mode} k")
 
 
 @pytest.mark.parametrize("passes", [1, 2])
@@ -192,3 +198,26 @@ def test_paged_output_rotation(nx, case):
         PH.run(2, 30, 12, 3, 16, 4, with_out_k=False, posts=(True, False, True), seed=82)
     else:
         PH.run(3, 25, 8, 2, 16, 4, norm=False, posts=(False, True, False), bad_entry=True, seed=83)
+
+
+@pytest.mark.parametrize("passes,length,wpc", [(1, 2, 0), (1, 3, 1), (1, 5, 0), (2, 3, 0), (1, 9, 2), (2, 16, 1)])
+def test_runs(nx, passes, length, wpc):
+    """Each wave taking `length` consecutive items: the token's angles are evaluated once per token within
+    a run, runs that cross token boundaries re-evaluate them, and small grids make every wave walk many
+    runs.  Ragged position ids (consecutive tokens of different sequences rotate by unrelated angles),
+    mixed q / k passes, GPT-J, per-sequence positions, and with one pass per item the {cos, sin} table,
+    the paged append and the output rotations, each against the oracle."""
+    import test_gpu_rope_had as RH
+    import test_gpu_rope_paged as P
+    import test_gpu_rope_paged_had as PH
+    nx(passes, wpc, length)
+    pid = ragged_position_ids(5)[None, :700]
+    run(1, pid.size, 20, 7, 128, 128, exl3r.ROPE_NEOX, F16, position_ids=pid, seed=90 + length)
+    run(1, pid.size, 64, 8, 128, 64, exl3r.ROPE_GPTJ, BF16, position_ids=pid, seed=91 + length)
+    run(3, 41, 9, 8, 128, 128, exl3r.ROPE_NEOX, F16, positions=np.array([3, 20000, 77], np.int32), seed=92 + length)
+    if passes == 1:
+        cs_case(exl3r.ROPE_NEOX, 128, f"run{length}")
+        pages, bt, sl = P.layout(2, 45, 16, 8, 93)
+        P.run(2, 45, 12, 3, 128, 128, exl3r.ROPE_NEOX, F16, 16, pages, 8, sl, bt, seed=93)
+        RH.run(1, 70, 12, 3, 128, 128, exl3r.ROPE_NEOX, position=21, seed=94)
+        PH.run(2, 40, 16, 4, 16, 8, seed=95)
