@@ -109,30 +109,39 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
                     }
                 }
             }
-            #pragma unroll
-            for (int u = 0; u < UNROLL; ++u)
+            if constexpr (HAD == 0)
             {
-                const int64_t c = base + (int64_t)u * nt;
-                if (c < cpr)
+                #pragma unroll
+                for (int u = 0; u < UNROLL; ++u)
                 {
-                    // Input rotations: the chunk's 16-lane group is its 128-column block (as below).
-                    if constexpr ((HAD & (AH_IN_X | AH_IN_Y)) != 0)
+                    const int64_t c = base + (int64_t)u * nt;
+                    if (c < cpr)
                     {
-                        static_assert(IT::code == DT_F16, "input rotations take f16 x and y");
-                        if constexpr ((HAD & AH_IN_X) != 0) output_rotation8(xv[u], a.xpost, c * 8);
-                        if constexpr ((HAD & AH_IN_Y) != 0) output_rotation8(yv[u], a.ypost, c * 8);
+                        float g[8], v[8], o[8];
+                        unpack8<IT>(xv[u], g);
+                        unpack8<IT>(yv[u], v);
+                        act_chunk<ACT, OT, LIMIT>(g, v, a.limit, o);
+                        if constexpr (SPLIT) store8_split<OT>(zr, chunk_elem<true>(c), pack8<OT>(o));
+                        else store8<OT>(zr, c * 8, pack8<OT>(o));
                     }
-                    float g[8], v[8], o[8];
-                    unpack8<IT>(xv[u], g);
-                    unpack8<IT>(yv[u], v);
-                    act_chunk<ACT, OT, LIMIT>(g, v, a.limit, o);
-                    if constexpr (SPLIT) store8_split<OT>(zr, chunk_elem<true>(c), pack8<OT>(o));
-                    else if constexpr (!(HAD & AH_OUT)) store8<OT>(zr, c * 8, pack8<OT>(o));
-                    else
+                }
+            }
+            else if constexpr ((HAD & (AH_IN_X | AH_IN_Y)) == 0)
+            {
+                // The output rotation alone: the exact stages, block by block (with the carried-sign
+                // stages, and with the blocks of a step rotated together, [8192, 17408] f16 ran 161-164
+                // against 148-153 us: this kernel's time is not the butterfly's).
+                #pragma unroll
+                for (int u = 0; u < UNROLL; ++u)
+                {
+                    const int64_t c = base + (int64_t)u * nt;
+                    if (c < cpr)
                     {
-                        // The group of 16 lanes holding chunks c & ~15 .. c | 15 is the block's (the
-                        // row length is a multiple of 128 and nt * UNROLL of 16), all active together.
                         static_assert(OT::code == DT_F16, "the Hadamard prologue follows an f16 activation");
+                        float g[8], v[8], o[8];
+                        unpack8<IT>(xv[u], g);
+                        unpack8<IT>(yv[u], v);
+                        act_chunk<ACT, OT, LIMIT>(g, v, a.limit, o);
                         TF16::Vec hv = pack8<TF16>(o);
                         if (a.z) store8<TF16>(zr, c * 8, hv);
                         if (a.hpre)
@@ -147,6 +156,75 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
                         store8<TF16>((char*)a.hout + row * a.ldh * 2, c * 8, pack8<TF16>(f));
                     }
                 }
+            }
+            else
+            {
+                // The group of 16 lanes holding chunks c & ~15 .. c | 15 is one 128-column block (the
+                // row length is a multiple of 128 and nt * UNROLL of 16), all active together.  One
+                // wave-uniform choice of butterfly stages (hadamard.cuh) covers every block of a step.
+                static_assert(OT::code == DT_F16, "the Hadamard prologue follows an f16 activation");
+                // With the input rotations the three butterflies per element set the time: the
+                // carried-sign stages where valid (MI355X, [8192, 17408] f16: 248-252 vs 270-272 us).
+                bool live[UNROLL];
+                #pragma unroll
+                for (int u = 0; u < UNROLL; ++u) live[u] = base + (int64_t)u * nt < cpr;
+                if constexpr ((HAD & (AH_IN_X | AH_IN_Y)) != 0)
+                {
+                    // Input rotations: x / y get their projections' output rotations first.
+                    static_assert(IT::code == DT_F16, "input rotations take f16 x and y");
+                    bool zero = false;
+                    #pragma unroll
+                    for (int u = 0; u < UNROLL; ++u)
+                        if (live[u])
+                        {
+                            if constexpr ((HAD & AH_IN_X) != 0) zero |= zero_lane16(xv[u]);
+                            if constexpr ((HAD & AH_IN_Y) != 0) zero |= zero_lane16(yv[u]);
+                        }
+                    with_carried<true>(zero, 0.0883883461356163f, [&](auto C) {
+                        #pragma unroll
+                        for (int u = 0; u < UNROLL; ++u)
+                            if (live[u])
+                            {
+                                const int64_t c = base + (int64_t)u * nt;
+                                if constexpr ((HAD & AH_IN_X) != 0) output_rotation8<decltype(C)::value>(xv[u], a.xpost, c * 8);
+                                if constexpr ((HAD & AH_IN_Y) != 0) output_rotation8<decltype(C)::value>(yv[u], a.ypost, c * 8);
+                            }
+                    });
+                }
+                float f[UNROLL][8];
+                bool zero = false;
+                #pragma unroll
+                for (int u = 0; u < UNROLL; ++u)
+                {
+                    const int64_t c = base + (int64_t)u * nt;
+                    if (live[u])
+                    {
+                        float g[8], v[8], o[8];
+                        unpack8<IT>(xv[u], g);
+                        unpack8<IT>(yv[u], v);
+                        act_chunk<ACT, OT, LIMIT>(g, v, a.limit, o);
+                        TF16::Vec hv = pack8<TF16>(o);
+                        if (a.z) store8<TF16>(zr, c * 8, hv);
+                        if (a.hpre)
+                        {
+                            const TF16::Vec p = load8<TF16>(a.hpre, c * 8);
+                            #pragma unroll
+                            for (int q = 0; q < 4; ++q) hv.a[q] = hmul2(hv.a[q], p.a[q]);
+                        }
+                        unpack8<TF16>(hv, f[u]);
+                        zero |= zero_lane(f[u]);
+                    }
+                }
+                with_carried<true>(zero, a.hr, [&](auto C) {
+                    #pragma unroll
+                    for (int u = 0; u < UNROLL; ++u)
+                        if (live[u])
+                        {
+                            const int64_t c = base + (int64_t)u * nt;
+                            butterfly128_t<decltype(C)::value>(f[u], (int)(c & 15), a.hr);
+                            store8<TF16>((char*)a.hout + row * a.ldh * 2, c * 8, pack8<TF16>(f[u]));
+                        }
+                });
             }
         }
     }

@@ -334,8 +334,10 @@ __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* 
             }
             float f[8];
             unpack8<TF16>(v, f);
-            butterfly128(f, l16, a.hr);
-            store8<TF16>((char*)a.hout[i] + row * a.ldh * 2, e, pack8<TF16>(f));
+            with_carried<true>(zero_lane16(v), a.hr, [&](auto C) {
+                butterfly128_t<decltype(C)::value>(f, l16, a.hr);
+                store8<TF16>((char*)a.hout[i] + row * a.ldh * 2, e, pack8<TF16>(f));
+            });
         }
     }
 }

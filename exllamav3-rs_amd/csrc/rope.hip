@@ -113,6 +113,46 @@ __device__ __forceinline__ int token_position(const RopeArgs& a, int tok)
     return a.position + s;
 }
 
+// Wave-uniform forms of token_position and cache_row for kernels whose wave works on one token at a
+// time: the index is moved to scalar registers and the int32 reads go through the scalar cache
+// (constant address space), so their waits count only scalar loads and never the item data the wave
+// has in flight (a vector read of the position or the block table would make its dependent use wait
+// for every load issued before it).
+__device__ __forceinline__ int64_t uniform64(int64_t v)
+{
+    const uint64_t u = (uint64_t)v;
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)u);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+    return (int64_t)((hi << 32) | lo);
+}
+__device__ __forceinline__ int32_t scalar_i32(const int32_t* p, int64_t i)
+{
+    return ((const __attribute__((address_space(4))) int32_t*)p)[uniform64(i)];
+}
+__device__ __forceinline__ int token_position_u(const RopeArgs& a, int64_t tok)
+{
+    tok = uniform64(tok);
+    const int64_t b = uniform64(tok / a.seq_len);
+    const int s = (int)(tok - b * a.seq_len);
+    if (a.positions) return scalar_i32(a.positions, b) + s;
+    if (a.position_ids) return scalar_i32(a.position_ids, tok);
+    return a.position + s;
+}
+__device__ __forceinline__ int64_t cache_row_u(const RopeArgs& a, int64_t tok)
+{
+    tok = uniform64(tok);
+    const int64_t b = uniform64(tok / a.seq_len);
+    const int64_t pos = (int64_t)scalar_i32(a.cache_seqlens, b) + (tok - b * a.seq_len);
+    const int64_t lb = pos >> a.page_log2;
+    const int64_t page = (pos >= 0 && lb < a.max_blocks) ? (int64_t)scalar_i32(a.block_table, b * a.max_blocks + lb) : -1;
+    if (page < 0 || page >= a.pages)
+    {
+        if (a.err) atomicOr(a.err, 1);
+        return -1;
+    }
+    return uniform64(((page << a.page_log2) + (pos & (((int64_t)1 << a.page_log2) - 1))) * a.hk * a.hd);
+}
+
 // sin and cos of an fp32 angle |a| < 2^52 in double precision (an int32 position times any
 // inv_freq below 2^21), without the large-argument machinery of a general double sincos, which
 // would cost ~30 VGPRs here.  Cody-Waite reduction a = k pi/2 + r with pi/2 split into three
@@ -631,17 +671,6 @@ struct NxItem
     int pos;                     // SRC_FREQ: the token's position
 };
 
-// Wave-uniform values read from memory (an item's cache row and position) moved to scalar registers, so
-// that the two items in flight do not hold them in VGPRs (see UNIFORM_ITEM in k_rope_nx).
-__device__ __forceinline__ int uniform32(int v) { return __builtin_amdgcn_readfirstlane(v); }
-__device__ __forceinline__ int64_t uniform64(int64_t v)
-{
-    const uint64_t u = (uint64_t)v;
-    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)u);
-    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
-    return (int64_t)((hi << 32) | lo);
-}
-
 // One of three values by a per-lane choice (q / k / v heads), as mask arithmetic: hipcc turns a chain
 // of selects between three values into a lookup table in scratch memory indexed per lane (~600 bytes
 // per lane and twice the kernel time in the paged instances).
@@ -709,7 +738,7 @@ __device__ __forceinline__ void rotate_head_nx(TF16::Vec& lo, TF16::Vec& hi, int
 // (exl3r_rope_paged_kv).  HADR: every head is first replaced by its projection's output rotation
 // (exl3r_rope_had, exl3r_rope_paged_kv_had).  Both take one pass per item.
 // The rotating instances evaluating sin / cos land just above the five-wave budget (97 VGPRs of 96); they
-// are held to five waves per SIMD (no spill: see UNIFORM_ITEM).
+// are held to five waves per SIMD.
 template <bool APPEND, bool HADR, int SRC>
 constexpr int kNxMinWaves = HADR && SRC == SRC_FREQ ? 5 : 1;
 
@@ -719,12 +748,6 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
 {
     static_assert(!(APPEND || HADR) || (P == 1 && !QOUT), "paged / rotating items are single passes");
     static_assert(!HADR || IO::code == DT_F16, "output rotation: f16 heads");
-    // An item's position and cache row moved to scalar registers when they are loaded: the wait for
-    // them then falls in issue(), before the current item's work, which costs 0.9-1.4 us at C4 (36.5
-    // vs 35.1 us NeoX, 34.2 vs 33.3 GPT-J, same process); only the paged + rotating instance evaluating
-    // sin / cos takes it, since without the VGPRs it frees that instance spills under its five-wave
-    // hold (58.9 vs 64.0 us).
-    constexpr bool UNIFORM_ITEM = APPEND && HADR && SRC == SRC_FREQ;
     extern __shared__ float2 cs[];            // [4 waves][64] (SRC_FREQ)
     // Norm weights with the constant bias folded in, q then k: h(w + h(cb)) (NORM_HALF) or w + cb (NORM_F32).
     __shared__ __align__(16) float wsh[256];
@@ -781,7 +804,7 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
             }
         }
         // The cache row, once per item that holds k or v heads (wave-uniform).
-        if constexpr (APPEND) t.crow = (t.slice + 1) * 8 > hq ? (UNIFORM_ITEM ? uniform64(cache_row(a, t.tok)) : cache_row(a, t.tok)) : -1;
+        if constexpr (APPEND) t.crow = (t.slice + 1) * 8 > hq ? cache_row_u(a, t.tok) : -1;
         if constexpr (SRC == SRC_CS)
         {
             // NeoX: pairs e0 .. e0 + 7; GPT-J: pairs e0/2 .. e0/2 + 3 (lo chunk) and 32 + e0/2 .. (hi chunk)
@@ -802,7 +825,7 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
             }
         }
         else
-            t.pos = UNIFORM_ITEM ? uniform32(token_position(a, (int)t.tok)) : token_position(a, (int)t.tok);
+            t.pos = token_position_u(a, t.tok);
     };
 
     if constexpr (NORM != NORM_NONE)

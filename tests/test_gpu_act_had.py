@@ -14,7 +14,7 @@ import torch
 
 import exl3r
 import exl3r.ffi as ffi
-from _gpu import NTHREADS, assert_bitwise, assert_close_ulp, dev_normal, from_dev
+from _gpu import NTHREADS, assert_bitwise, assert_close_ulp, dev_normal, from_dev, to_dev
 from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -162,3 +162,44 @@ def test_zero_rows_and_errors():
         xs = dev_normal((4, 259), 0, 1, F16, 13)[:, :256]
         ffi.act_mul_had("silu", xs, xs, torch.empty_like(x), rotate_x=True)
     torch.cuda.synchronize()
+
+
+def zero_sign_rows(rows, cols, seed):
+    """f16 rows built to exercise the signs of exact zeros in the rotations: small integers (exact
+    cancellations inside the butterflies), rows of +0, rows of -0, rows whose first 128-block has one
+    16-lane chunk (8 values) of -0 among non-zero values, and blocks half +0, half non-zero."""
+    rng = np.random.default_rng(seed)
+    x = rng.integers(-2, 3, (rows, cols)).astype(np.float16)
+    x[1] = 0.0
+    x[2] = -0.0
+    x[3, :8] = -0.0
+    x[4].reshape(-1, 128)[:, :64] = 0.0
+    x[5].reshape(-1, 128)[:, 64:] = -0.0
+    x[6, 128:256] = -0.0
+    return to_dev(x.view(np.uint16), F16)
+
+
+@pytest.mark.parametrize("act", ["silu", "mul_sigmoid"])
+def test_rotated_inputs_zero_signs(act):
+    """x / y rotated on load where the rotations produce exact zeros: the fused kernel's butterflies
+    (the carried-sign lane stages, or the exact ones for a wave holding 8 zeros with a -0 in one lane)
+    against the unfused exact calls, bit for bit, signs of zeros included; and the rotations themselves
+    against the oracle."""
+    rows, cols = 40, 1024
+    x, y = zero_sign_rows(rows, cols, 31), zero_sign_rows(rows, cols, 32)
+    y[2:4] = y[2:4].neg()
+    p = torch.from_numpy(np.where(np.random.default_rng(33).random(cols) < 0.5, -1.0, 1.0).astype(np.float16)).cuda()
+    z = torch.empty((rows, cols), device="cuda", dtype=torch.float16)
+    out = torch.empty((rows, cols), device="cuda", dtype=torch.float16)
+    ffi.act_mul_had(act, x, y, out, p, z, rotate_x=True, rotate_y=True)
+    rx, ry = torch.empty_like(x), torch.empty_like(y)
+    ffi.had_r_128(x, rx, None, None)
+    ffi.had_r_128(y, ry, None, None)
+    ez, eout = unfused(act, rx, ry, p, 0.0, 1.0)
+    torch.cuda.synchronize()
+    assert_bitwise(from_dev(rx), orc.had_r_128(np.ascontiguousarray(from_dev(x)), F16, nthreads=NTHREADS), what="rotated x")
+    assert_bitwise(from_dev(ry), orc.had_r_128(np.ascontiguousarray(from_dev(y)), F16, nthreads=NTHREADS), what="rotated y")
+    zeros = (from_dev(rx) & 0x7fff) == 0
+    assert zeros.sum() > 1000 and (from_dev(rx)[zeros] == 0x8000).any()    # the cases are there
+    assert_bitwise(from_dev(z), from_dev(ez), what=f"{act} zero signs: z")
+    assert_bitwise(from_dev(out), from_dev(eout), what=f"{act} zero signs: out")

@@ -11,7 +11,7 @@ import torch
 
 import exl3r
 import exl3r.ffi as ffi
-from _gpu import NTHREADS, TORCH_DT, assert_bitwise, dev_normal, from_dev
+from _gpu import NTHREADS, TORCH_DT, assert_bitwise, dev_normal, from_dev, to_dev
 from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -131,3 +131,34 @@ def test_zero_rows_and_errors():
     with pytest.raises(exl3r.Exl3rError):
         ffi.rms_norm_had(x, None, [o], [None], 1e-6, x_post_scale=suh(256, 1))   # post-scale without rotate_x
     torch.cuda.synchronize()
+
+
+def test_zero_signs_of_the_rotations():
+    """Norm outputs whose rotations produce exact zeros (x in {-1, 0, 1}, unit weights, +-1 pre-scales:
+    whole blocks cancel), rows of +0 and of -0, a lane of -0 among non-zero values: the fused
+    butterflies (carried-sign lane stages where valid, else exact) against the oracle, bit for bit,
+    signs of zeros included."""
+    rows, dim = 24, 1024
+    rng = np.random.default_rng(41)
+    xh = rng.integers(-1, 2, (rows, dim)).astype(np.float16)
+    xh[1] = 0.0
+    xh[2] = -0.0
+    xh[3, :8] = -0.0
+    xh[4].reshape(-1, 128)[:, :64] = 0.0
+    xh[5, 128:256] = -0.0
+    xh[6] = 1.0
+    x = to_dev(xh.view(np.uint16), F16)
+    w = torch.ones(dim, device="cuda", dtype=torch.float16)
+    y = torch.empty((rows, dim), device="cuda", dtype=torch.float16)
+    outs = [torch.empty((rows, dim), device="cuda", dtype=torch.float16) for _ in range(3)]
+    pres = [suh(dim, 50 + i) for i in range(3)]
+    ffi.rms_norm_had(x, w, outs, pres, 1e-6, 0.0, 1.0, y=y)
+    torch.cuda.synchronize()
+    ey = orc.rms_norm(xh.view(np.uint16), F16, from_dev(w), F16, F16, 1e-6, 0.0, 1.0, nthreads=NTHREADS)
+    assert_bitwise(from_dev(y), ey, what="zero signs: y")
+    nzero = 0
+    for i, o in enumerate(outs):
+        exp = orc.had_r_128(ey, F16, pre=from_dev(pres[i]), nthreads=NTHREADS)
+        nzero += int(((exp & 0x7fff) == 0).sum())
+        assert_bitwise(from_dev(o), exp, what=f"zero signs: out{i}")
+    assert nzero > 1000    # the cancellations are there
