@@ -129,10 +129,15 @@ __device__ __forceinline__ int32_t scalar_i32(const int32_t* p, int64_t i)
 {
     return ((const __attribute__((address_space(4))) int32_t*)p)[uniform64(i)];
 }
+// Sequence of token tok (< 2^31): a 32-bit division, none for a single sequence.
+__device__ __forceinline__ int64_t token_seq_u(const RopeArgs& a, int64_t tok)
+{
+    return a.seq_len == a.tokens ? 0 : (int64_t)uniform64((uint32_t)tok / (uint32_t)a.seq_len);
+}
 __device__ __forceinline__ int token_position_u(const RopeArgs& a, int64_t tok)
 {
     tok = uniform64(tok);
-    const int64_t b = uniform64(tok / a.seq_len);
+    const int64_t b = token_seq_u(a, tok);
     const int s = (int)(tok - b * a.seq_len);
     if (a.positions) return scalar_i32(a.positions, b) + s;
     if (a.position_ids) return scalar_i32(a.position_ids, tok);
@@ -141,7 +146,7 @@ __device__ __forceinline__ int token_position_u(const RopeArgs& a, int64_t tok)
 __device__ __forceinline__ int64_t cache_row_u(const RopeArgs& a, int64_t tok)
 {
     tok = uniform64(tok);
-    const int64_t b = uniform64(tok / a.seq_len);
+    const int64_t b = token_seq_u(a, tok);
     const int64_t pos = (int64_t)scalar_i32(a.cache_seqlens, b) + (tok - b * a.seq_len);
     const int64_t lb = pos >> a.page_log2;
     const int64_t page = (pos >= 0 && lb < a.max_blocks) ? (int64_t)scalar_i32(a.block_table, b * a.max_blocks + lb) : -1;
@@ -1076,9 +1081,7 @@ static bool rope_nx_ok(const RopeArgs& a, int rope_mode, bool had = false)
         return false;
     if (tu.rope_tok != 0 && tu.rope_nx == 0) return false;   // a test forcing one of the other kernels
     if (a.kc && a.hv != a.hk) return false;
-    // The paged append without the rotations stays with the wave-per-token kernel unless forced
-    // (MI355X, 4096-token prefill, same process: 39.7 us there against 43.0 us here).
-    if (a.kc && !had && tu.rope_nx <= 0) return false;
+    if (a.tokens >= ((int64_t)1 << 31)) return false;    // 32-bit token arithmetic
     if (!a16(a.q_post) || !a16(a.k_post) || !a16(a.v_post)) return false;
     if (a.cst && ((uintptr_t)a.cst & 15)) return false;
     // Every size: at decode and small prefills too it beats the flattened kernel (MI355X, HIP graph,
@@ -1109,8 +1112,10 @@ static void launch_rope_nx_p(const RopeArgs& a, hipStream_t s)
     // 33.3; q / k rotations + RoPE at C4 46.8 / 45.5 / 42.7; q / k / v rotations + RoPE + paged append at
     // 4096 tokens 57.5 / 53.4 / 51.3, from the {cos, sin} table 48.4 / 47.1 / 46.1 (the post-scales and
     // cache rows of one token reused too).  Two passes per item (GPT-J) and the plain kernel reading the
-    // table are fastest at 1.
-    constexpr int kRun = HADR ? 3 : SRC == SRC_FREQ && P == 1 && !QOUT ? 2 : 1;
+    // table are fastest at 1.  q / k norm + RoPE + paged append at 4096 tokens, runs of 1 / 2 / 3 / 4 / 6:
+    // 42.5 / 38.8 / 39.7 / 38.5 / 39.6, from the table 38.2 / 36.5 / 38.3 / 35.8 / 41.3 (the wave-per-token
+    // kernel: 41.7 / 38.8).
+    constexpr int kRun = HADR ? 3 : APPEND ? 4 : SRC == SRC_FREQ && P == 1 && !QOUT ? 2 : 1;
     const int tr = tuning().rope_nx_run;
     const int run = tr > 0 ? tr : items >= (int64_t)kRun * blocks * 4 ? kRun : 1;
     const int64_t runs = (items + run - 1) / run;
