@@ -1119,6 +1119,11 @@ static void launch_rope_nx_p(const RopeArgs& a, hipStream_t s)
     const int tr = tuning().rope_nx_run;
     const int run = tr > 0 ? tr : items >= (int64_t)kRun * blocks * 4 ? kRun : 1;
     const int64_t runs = (items + run - 1) / run;
+    // Plain passes reading the {cos, sin} table carry nothing from one item to the next: a wave per
+    // run over the whole grid, dispatched as workgroups retire, beats the resident grid (C4, same
+    // process: 30.8 vs 32.1 us; the evaluated and the GPT-J passes lose with it, 37.5 / 35.7 us).
+    constexpr bool kFlat = SRC == SRC_CS && P == 1 && !APPEND && !HADR;
+    if (kFlat && wpc == 0) blocks = (runs + 3) / 4;
     if (blocks > (runs + 3) / 4) blocks = (runs + 3) / 4;
     if (blocks > kMaxGridX) blocks = kMaxGridX;
     k_rope_nx<IO, MODE, NORM, SRC, QOUT, P, APPEND, HADR><<<(unsigned)blocks, 256, lds, s>>>(a, nslice, run);
