@@ -1010,17 +1010,20 @@ def decode_eager_compiled(timeout=120):
 
 
 def traffic_from_profiles(op):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary, or None."""
+    """HBM bytes per launch of the op's main kernel from the committed rocprofv3 --pmc summary, or None
+    (an op with a second, small kernel -- the {cos, sin} table -- has a line for each: the larger is kept)."""
     path = os.path.join(ROOT, "profiles", "pmc_traffic.txt")
     if not os.path.exists(path):
         return None
+    best = None
     for line in open(path):
         parts = line.split()
         if len(parts) >= 2 and parts[0] == op + ":":
             kv = dict(p.split("=", 1) for p in parts[1:] if "=" in p)
             if "traffic_bytes" in kv:
-                return int(float(kv["traffic_bytes"]))
-    return None
+                t = int(float(kv["traffic_bytes"]))
+                best = t if best is None else max(best, t)
+    return best
 
 
 # ------------------------------------------------------------------------------------------------
