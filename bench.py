@@ -34,8 +34,8 @@ OPS = ["rms_c3", "rms_q3mix", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "
        "gather_norm_c5", "rms_c1",
        "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "rope_kv_prefill",
        "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
-       "deinterleave_q35", "gated_norm_had_q35", "gated_norm_had_q35_unfused", "argmax_dec", "argmax_dec_torch", "argmax_prefill", "argmax_prefill_torch",
-       "gumbel_dec", "gumbel_dec_torch", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_unfused", "silu_had_c3",
+       "deinterleave_q35", "gated_norm_had_q35", "gated_norm_had_q35_unfused", "argmax_dec", "argmax_dec_torch", "argmax_dec_ws", "argmax_prefill", "argmax_prefill_torch",
+       "gumbel_dec", "gumbel_dec_torch", "gumbel_dec_ws", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_unfused", "silu_had_c3",
        "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_unfused", "rope_cs_c4", "rope_cs_table_c4",
        "qg_rope_q35", "qg_rope_q35_unfused",
        "rope_kv_prefill_cs", "rope_kv_had_prefill_cs", "prefill_layer_cs",
@@ -434,27 +434,31 @@ def make_gated(name, kind, tokens=4096, heads=32, hd=128, seed=600):
     return Work(name, nbytes, launch, desc, sets)
 
 
-def make_argmax(name, rows, use_torch, vocab=151936, seed=700):
-    """Greedy token choice over f16 logits [rows, vocab]: exl3r_argmax_sample, or torch.argmax on the
-    same tensor (the generator's batched tch argmax, the reference's call path)."""
+def make_argmax(name, rows, use_torch, vocab=151936, seed=700, ws=False):
+    """Greedy token choice over f16 logits [rows, vocab]: exl3r_argmax_sample (ws: its one-launch form
+    exl3r_argmax_sample_ws), or torch.argmax on the same tensor (the generator's batched tch argmax, the
+    reference's call path)."""
     import torch
     import exl3r.ffi as ffi
     nbytes = rows * vocab * 2 + rows * 8
     sets = sets_for(nbytes)
     bufs = [gen((rows, vocab), 0.0, 3.0, torch.float16, seed + k) for k in range(sets)]
     ids = torch.empty(rows, dtype=torch.int64, device="cuda")
+    wsb = torch.zeros(ffi.sample_workspace_bytes(), dtype=torch.uint8, device="cuda") if ws else None
 
     def launch(i):
         x = bufs[i % sets]
         if use_torch:
             torch.argmax(x, dim=1, out=ids)
+        elif ws:
+            ffi.argmax_sample_ws(x, ids, wsb)
         else:
             ffi.argmax_sample(x, ids)
-    return Work(name, nbytes, launch, f"argmax over f16 logits [{rows},{vocab}] ({'torch.argmax' if use_torch else 'exl3r'})",
-                sets)
+    what = "torch.argmax" if use_torch else "exl3r, one launch with a workspace" if ws else "exl3r"
+    return Work(name, nbytes, launch, f"argmax over f16 logits [{rows},{vocab}] ({what})", sets)
 
 
-def make_gumbel(name, rows, use_torch, vocab=151936, seed=720):
+def make_gumbel(name, rows, use_torch, vocab=151936, seed=720, ws=False):
     """Categorical draw from softmax(f16 logits [rows, vocab]): exl3r_gumbel_sample (Gumbel-max, one
     launch chain), or the reference sampler's tch path (src/sampler.rs:114: softmax, then
     multinomial(1, replacement)) on the same tensor."""
@@ -464,14 +468,18 @@ def make_gumbel(name, rows, use_torch, vocab=151936, seed=720):
     sets = sets_for(nbytes)
     bufs = [gen((rows, vocab), 0.0, 3.0, torch.float16, seed + k) for k in range(sets)]
     ids = torch.empty(rows, dtype=torch.int64, device="cuda")
+    wsb = torch.zeros(ffi.sample_workspace_bytes(), dtype=torch.uint8, device="cuda") if ws else None
 
     def launch(i):
         x = bufs[i % sets]
         if use_torch:
             torch.multinomial(torch.softmax(x.float(), dim=-1), 1, True)
+        elif ws:
+            ffi.gumbel_sample_ws(x, ids, wsb, 0, i)
         else:
             ffi.gumbel_sample(x, ids, 0, i)
-    what = "torch softmax + multinomial" if use_torch else "exl3r Gumbel-max"
+    what = "torch softmax + multinomial" if use_torch else \
+        "exl3r Gumbel-max, one launch with a workspace" if ws else "exl3r Gumbel-max"
     return Work(name, nbytes, launch, f"categorical draw over f16 logits [{rows},{vocab}] ({what})", sets)
 
 
@@ -764,9 +772,11 @@ def make_all(only=None):
         "gated_norm_had_q35_unfused": lambda: make_gated("gated_norm_had_q35_unfused", "norm_had_unfused"),
         "argmax_dec": lambda: make_argmax("argmax_dec", 64, False),
         "argmax_dec_torch": lambda: make_argmax("argmax_dec_torch", 64, True),
+        "argmax_dec_ws": lambda: make_argmax("argmax_dec_ws", 64, False, ws=True),
         "argmax_prefill": lambda: make_argmax("argmax_prefill", 1024, False),
         "argmax_prefill_torch": lambda: make_argmax("argmax_prefill_torch", 1024, True),
         "gumbel_dec": lambda: make_gumbel("gumbel_dec", 64, False),
+        "gumbel_dec_ws": lambda: make_gumbel("gumbel_dec_ws", 64, False, ws=True),
         "gumbel_dec_torch": lambda: make_gumbel("gumbel_dec_torch", 64, True),
         "gumbel_prefill": lambda: make_gumbel("gumbel_prefill", 1024, False),
         "had_c3": lambda: make_had("had_c3", 8192, 5120),
@@ -1080,7 +1090,7 @@ def main():
                 gbs = hbm_gbs
             extra = ""
             if name.endswith("_c1") or name.startswith("rope_kv_dec") or name.startswith("argmax_dec") or \
-                    name == "gumbel_dec":
+                    name in ("gumbel_dec", "gumbel_dec_ws"):
                 # Launch-latency-bound: eager timing is the host's launch rate; the graph replay is
                 # the device time per launch.
                 us_g = time_graph(w, 20, 10) * 1000
@@ -1123,10 +1133,12 @@ def main():
         log(f"C2 residual RMSNorm us (graph): {[c2[t]['us_graph'] for t in c2]}")
         sampling = {
             "argmax_64x151936_graph_us": {"exl3r": ops["argmax_dec"]["us_graph"],
+                                          "exl3r_one_launch_workspace": ops["argmax_dec_ws"]["us_graph"],
                                           "torch_argmax": ops["argmax_dec_torch"]["us_graph"]},
             "argmax_1024x151936_us": {"exl3r": ops["argmax_prefill"]["us"],
                                       "torch_argmax": ops["argmax_prefill_torch"]["us"]},
             "gumbel_64x151936_us": {"exl3r_graph": ops["gumbel_dec"]["us_graph"],
+                                    "exl3r_one_launch_workspace_graph": ops["gumbel_dec_ws"]["us_graph"],
                                     "torch_softmax_multinomial_eager": ops["gumbel_dec_torch"]["us"]},
             "gumbel_1024x151936_us": {"exl3r": ops["gumbel_prefill"]["us"]},
             "desc": "f16 logits; argmax vs torch.argmax (the generator's greedy path); Gumbel-max draw vs "

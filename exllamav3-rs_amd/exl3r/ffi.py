@@ -483,6 +483,39 @@ def gumbel_sample(logits, ids, max_logit=0, random=0, stream=None):
                                      int(random) & 0xFFFFFFFF, _ptr(ids), _stream(logits, stream)))
 
 
+def sample_workspace_bytes():
+    """Bytes of the workspace argmax_sample_ws / gumbel_sample_ws take (any shape up to 384 rows)."""
+    return int(load().exl3r_sample_workspace_bytes())
+
+
+def _workspace(ws, logits):
+    if ws is None or ws.device != logits.device or not ws.is_contiguous() or ws.data_ptr() % 256:
+        raise ValueError("workspace must be a contiguous 256-byte aligned tensor on the logits' device")
+    return _ptr(ws), ws.numel() * ws.element_size()
+
+
+def argmax_sample_ws(logits, ids, workspace, max_logit=0, stream=None):
+    """argmax_sample in one launch below 128 rows, the row counters and slots in `workspace` (at least
+    sample_workspace_bytes() bytes, zero before the first use; every call leaves it zero).  The ids are
+    identical to argmax_sample's."""
+    rows, vocab, ld = _rows(logits)
+    if ids.dtype != torch.int64 or ids.numel() != rows:
+        raise ValueError("ids must be int64 with one entry per row")
+    wp, wb = _workspace(workspace, logits)
+    check(load().exl3r_argmax_sample_ws(_ptr(logits), dtype_code(logits), rows, vocab, ld, int(max_logit), _ptr(ids),
+                                        wp, wb, _stream(logits, stream)))
+
+
+def gumbel_sample_ws(logits, ids, workspace, max_logit=0, random=0, stream=None):
+    """gumbel_sample in one launch below 384 rows, with the workspace of argmax_sample_ws; the same draws."""
+    rows, vocab, ld = _rows(logits)
+    if ids.dtype != torch.int64 or ids.numel() != rows:
+        raise ValueError("ids must be int64 with one entry per row")
+    wp, wb = _workspace(workspace, logits)
+    check(load().exl3r_gumbel_sample_ws(_ptr(logits), dtype_code(logits), rows, vocab, ld, int(max_logit),
+                                        int(random) & 0xFFFFFFFF, _ptr(ids), wp, wb, _stream(logits, stream)))
+
+
 def gumbel_noise(x, out, random=0, stream=None):
     """out = x + the Gumbel noise of gumbel_sample (src/ffi.rs:531-535); out may be x."""
     rows, cols, ldx = _rows(x)

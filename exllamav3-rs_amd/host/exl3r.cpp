@@ -399,6 +399,28 @@ void gumbel_sample(const Tensor& logits, const Tensor& ids, int max_logit, uint3
                                   static_cast<int64_t*>(ids.data), s.get()));
 }
 
+void argmax_sample_ws(const Tensor& logits, const Tensor& ids, int max_logit, const DeviceBuffer& workspace,
+                      const Stream& s)
+{
+    int64_t rows, vocab, ld;
+    logits.rows_view(rows, vocab, ld);
+    require(ids.dtype == DType::I64 && ids.numel() == rows && ids.is_contiguous(),
+            "argmax_sample_ws: ids must be contiguous int64 with one entry per logits row");
+    check_abi(exl3r_argmax_sample_ws(logits.data, code(logits.dtype), rows, vocab, ld, max_logit,
+                                     static_cast<int64_t*>(ids.data), workspace.data(), workspace.bytes(), s.get()));
+}
+
+void gumbel_sample_ws(const Tensor& logits, const Tensor& ids, int max_logit, uint32_t random,
+                      const DeviceBuffer& workspace, const Stream& s)
+{
+    int64_t rows, vocab, ld;
+    logits.rows_view(rows, vocab, ld);
+    require(ids.dtype == DType::I64 && ids.numel() == rows && ids.is_contiguous(),
+            "gumbel_sample_ws: ids must be contiguous int64 with one entry per logits row");
+    check_abi(exl3r_gumbel_sample_ws(logits.data, code(logits.dtype), rows, vocab, ld, max_logit, random,
+                                     static_cast<int64_t*>(ids.data), workspace.data(), workspace.bytes(), s.get()));
+}
+
 void gumbel_noise(const Tensor& x, const Tensor& out, uint32_t random, const Stream& s)
 {
     int64_t rows, cols, ldx, ro, co, ldo;

@@ -226,6 +226,13 @@ void argmax_sample(const Tensor& logits, const Tensor& ids, int max_logit, const
 // src/ffi.rs:526-530: a draw from softmax(logits[i, :max_logit]) per row (Gumbel-max over this library's
 // Philox4x32-10 stream keyed by `random`); ids int64 [rows].
 void gumbel_sample(const Tensor& logits, const Tensor& ids, int max_logit, uint32_t random, const Stream& s);
+// argmax_sample / gumbel_sample in one launch below 128 / 384 rows, with a workspace of
+// exl3r_sample_workspace_bytes() bytes (zero before its first use, left zero by every call; one per
+// stream): the same ids.
+void argmax_sample_ws(const Tensor& logits, const Tensor& ids, int max_logit, const DeviceBuffer& workspace,
+                      const Stream& s);
+void gumbel_sample_ws(const Tensor& logits, const Tensor& ids, int max_logit, uint32_t random,
+                      const DeviceBuffer& workspace, const Stream& s);
 // src/ffi.rs:531-535: out = x + the Gumbel noise gumbel_sample adds (out may be x).
 void gumbel_noise(const Tensor& x, const Tensor& out, uint32_t random, const Stream& s);
 // src/ffi.rs:606-607: the EXL3 linear's random-Hadamard rotation of [rows, cols] f16 / f32 x into out

@@ -53,6 +53,7 @@
 #ifndef EXL3R_ROWOPS_H
 #define EXL3R_ROWOPS_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #if defined(__GNUC__) || defined(__clang__)
@@ -452,6 +453,25 @@ EXL3R_API int exl3r_argmax_sample(const void* logits, int dtype, int64_t rows, i
  */
 EXL3R_API int exl3r_gumbel_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
                         int max_logit, uint32_t random, int64_t* ids, void* stream);
+
+/*
+ * exl3r_argmax_sample / exl3r_gumbel_sample in one launch below 128 / 384 rows (decode batches): each
+ * slice's workgroup folds its key into the row's slot in the workspace and the last one to finish a
+ * row writes the index, instead of three launches through the ids slot.  Same rule, mask and noise;
+ * the ids are identical.  workspace: exl3r_sample_workspace_bytes() bytes of device memory (row
+ * counters and row slots for up to 384 rows), 256-byte aligned and zero before its first use; every
+ * completed call leaves it zero again, so a workspace is cleared once, when it is allocated.  Calls
+ * that share a workspace must not overlap (one stream, or ordered by events).  From 128 / 384 rows
+ * the workgroup-per-row kernel runs and the workspace is not touched.  Same call sites as
+ * exl3r_argmax_sample (src/generator.rs:1596) and exl3r_gumbel_sample (ffi.rs:526-530), for callers
+ * that keep a workspace per stream.
+ */
+EXL3R_API size_t exl3r_sample_workspace_bytes(void);
+EXL3R_API int exl3r_argmax_sample_ws(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                        int max_logit, int64_t* ids, void* workspace, size_t workspace_bytes, void* stream);
+EXL3R_API int exl3r_gumbel_sample_ws(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                        int max_logit, uint32_t random, int64_t* ids, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 /*
  * out[r, c] = x[r, c] + g(random, r, c) over every column (the noise of exl3r_gumbel_sample), rounded

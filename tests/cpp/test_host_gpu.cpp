@@ -319,6 +319,17 @@ int main()
         oracle_argmax(lh.data(), OR_BF16, rows, vocab, vocab, mask, want.data(), 1);
         const bool ok = std::memcmp(got.data(), want.data(), rows * 8) == 0 && want[3] == 307;
         report("ffi::argmax_sample bf16 masked", ok, ok ? "exact" : "DIFFER");
+        // The one-launch form with a workspace (zeroed once), twice in a row on one workspace.
+        DeviceBuffer ws(exl3r_sample_workspace_bytes());
+        hip_ok(hipMemsetAsync(ws.data(), 0, ws.bytes(), s.get()), "hipMemsetAsync");
+        auto ids_ws = OwnedTensor::empty(DType::I64, { rows });
+        bool ok_ws = true;
+        for (int rep = 0; rep < 2; ++rep)
+        {
+            ffi::argmax_sample_ws(l.t, ids_ws.t, mask, ws, s);
+            ok_ws = ok_ws && std::memcmp(download(ids_ws, s).data(), want.data(), rows * 8) == 0;
+        }
+        report("ffi::argmax_sample_ws bf16 masked, workspace reused", ok_ws, ok_ws ? "exact" : "DIFFER");
     }
     // gumbel_noise (f16 -> f32) and gumbel_sample on the same logits: bitwise noise, equal ids, and the
     // sample equals the argmax of the noisy logits.

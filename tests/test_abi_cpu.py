@@ -204,6 +204,19 @@ def test_sampling_validation():
         assert fn(FAKE, F16, 2, 100, 50, 0, *extra, FAKE + 4096, None) == exl3r.EINVAL and "ld" in _err()
         assert fn(FAKE, F16, 2, 100, 100, 0, *extra, None, None) == exl3r.EINVAL and "non-null" in _err()
         assert fn(None, F16, 0, 100, 100, 0, *extra, None, None) == exl3r.OK
+    # the one-launch forms: (..., ids, workspace, workspace_bytes)
+    need = lib.exl3r_sample_workspace_bytes()
+    assert need == 384 * (4 + 8)                            # a counter and a slot per row, up to 384 rows
+    for fn, extra in ((lib.exl3r_argmax_sample_ws, ()), (lib.exl3r_gumbel_sample_ws, (7,))):
+        ws = FAKE + (1 << 20)
+        assert fn(FAKE, F16, 2, 151936, 151936, 0, *extra, FAKE + 4096, None, need, None) == exl3r.EINVAL
+        assert "workspace" in _err()
+        assert fn(FAKE, F16, 2, 151936, 151936, 0, *extra, FAKE + 4096, ws, need - 8, None) == exl3r.EINVAL
+        assert "workspace" in _err() and str(need) in _err()
+        assert fn(FAKE, F16, 2, 151936, 151936, 0, *extra, FAKE + 4096, ws + 128, need, None) == exl3r.EINVAL
+        assert "aligned" in _err()
+        assert fn(FAKE, I64, 2, 100, 100, 0, *extra, FAKE + 4096, ws, need, None) == exl3r.EDTYPE
+        assert fn(None, F16, 0, 100, 100, 0, *extra, None, ws, need, None) == exl3r.OK
     # exl3r_gumbel_noise(x, x_dtype, ldx, out, out_dtype, ldo, rows, cols, random)
     assert lib.exl3r_gumbel_noise(FAKE, F16, 64, FAKE + 8192, I32, 64, 2, 64, 1, None) == exl3r.EDTYPE
     assert lib.exl3r_gumbel_noise(FAKE, F16, 32, FAKE + 8192, F32, 64, 2, 64, 1, None) == exl3r.EINVAL
