@@ -25,6 +25,8 @@
 // index".  With slices, the workgroup's maximum key (DPP butterfly, one LDS hop) goes to the row's
 // int64 output with one atomicMax; a clear kernel before and a convert kernel after turn that slot
 // into the index.  Capture-safe: no memset.
+#include <mutex>
+
 #include "abi.hpp"
 #include "common.cuh"
 
@@ -409,9 +411,16 @@ __global__ __launch_bounds__(256) void k_gumbel_noise(NoiseArgs a)
 
 using namespace exl3r;
 
+// exl3r_argmax_sample_noalloc's scratch: the one-launch kernel's row counters and slots for 384 rows
+// (4608 bytes: the workspace of exl3r_argmax_sample_ws), one copy per GPU the library runs on, held
+// until the process ends.  It is zero when the code object is loaded, and every completed call leaves
+// it zero (the last workgroup of a row resets the row's counter and slot), so no call clears it.  Host
+// code never uses the name as an address: scratch_of_current_device() asks the runtime for the
+// current device's copy, once per device.
+static __device__ __align__(256) unsigned char scratch[384 * 12];
+
 namespace {
 
-// Shared by the argmax and the Gumbel draw: validation, then the slice or row-per-workgroup kernels.
 // Workspace of the single-launch sliced path: kWsMaxRows row counters (u32), then as many row slots
 // (u64), all zero between calls.
 constexpr int64_t kWsMaxRows = 384;
@@ -422,16 +431,48 @@ constexpr size_t kWsBytes = kCountBytes + kWsMaxRows * 8;
 // few rows take 2048-element slices so the row still spreads over enough CUs.
 inline int slice_unroll(int64_t rows) { return rows >= 16 ? 4 : 1; }
 
-
 struct Workspace
 {
     void* base;      // nullptr: the three-launch path (ids as the reduction slot)
     size_t bytes;
+    bool scratch;    // the library's scratch (looked up when the sliced kernel needs it); a call it cannot
+                     // serve is an error, not the three-launch path
 };
 
+static_assert(sizeof(scratch) == kWsBytes, "the scratch is one workspace");
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address: hipGetSymbolAddress on the first call with that device
+// current, kept per device.
+int scratch_of_current_device(const char* op, void** out)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error((int)e, "%s: hipGetDevice: %s", op, hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_error(EXL3R_EINVAL, "%s: device %d is beyond the %d devices this entry point serves", op, dev,
+                         kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev])
+    {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_error(e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol, "%s: hipGetSymbolAddress(scratch): %s",
+                             op, hipGetErrorString(e != hipSuccess ? e : hipErrorInvalidSymbol));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return EXL3R_OK;
+}
+
+// Shared by the argmax and the Gumbel draw: validation, then the slice or row-per-workgroup kernels.
 template <bool GUMBEL>
 int sample_entry(const char* op, const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
-                 int max_logit, uint32_t seed, int64_t* ids, void* stream, Workspace ws = { nullptr, 0 })
+                 int max_logit, uint32_t seed, int64_t* ids, void* stream, Workspace ws = { nullptr, 0, false })
 {
 
     if (!is_float_dtype(dtype)) return set_error(EXL3R_EDTYPE, "%s: unsupported logits dtype %s", op, dtype_name(dtype));
@@ -480,6 +521,14 @@ int sample_entry(const char* op, const void* logits, int dtype, int64_t rows, in
     const int unroll = slice_unroll(rows);
     const int64_t slice = (int64_t)unroll * 2048;
     const dim3 grid((unsigned)((n + slice - 1) / slice), (unsigned)rows);
+    if (ws.scratch)
+    {
+        if (rows > kWsMaxRows)
+            return set_error(EXL3R_EINVAL, "%s: %lld rows take the sliced kernel, whose scratch holds %lld rows", op,
+                             (long long)rows, (long long)kWsMaxRows);
+        const int rc = scratch_of_current_device(op, &ws.base);
+        if (rc) return rc;
+    }
     if (ws.base && rows <= kWsMaxRows)
     {
         // One launch: the slice keys and row counters in the workspace.
@@ -524,6 +573,14 @@ int sample_entry(const char* op, const void* logits, int dtype, int64_t rows, in
 
 }  // namespace
 
+extern "C" int exl3r_argmax_sample_noalloc(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                                           int max_logit, int64_t* ids, void* stream)
+{
+    clear_stale_error();
+    const char* op = "exl3r_argmax_sample_noalloc";
+    return sample_entry<false>(op, logits, dtype, rows, vocab, ld, max_logit, 0u, ids, stream, { nullptr, kWsBytes, true });
+}
+
 extern "C" int exl3r_argmax_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
                                    int max_logit, int64_t* ids, void* stream)
 {
@@ -540,7 +597,7 @@ extern "C" int exl3r_argmax_sample_ws(const void* logits, int dtype, int64_t row
     clear_stale_error();
     if (!workspace) return set_error(EXL3R_EINVAL, "exl3r_argmax_sample_ws: workspace must be non-null");
     return sample_entry<false>("exl3r_argmax_sample_ws", logits, dtype, rows, vocab, ld, max_logit, 0u, ids, stream,
-                               { workspace, workspace_bytes });
+                               { workspace, workspace_bytes, false });
 }
 
 extern "C" int exl3r_gumbel_sample_ws(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
@@ -550,7 +607,7 @@ extern "C" int exl3r_gumbel_sample_ws(const void* logits, int dtype, int64_t row
     clear_stale_error();
     if (!workspace) return set_error(EXL3R_EINVAL, "exl3r_gumbel_sample_ws: workspace must be non-null");
     return sample_entry<true>("exl3r_gumbel_sample_ws", logits, dtype, rows, vocab, ld, max_logit, random, ids,
-                              stream, { workspace, workspace_bytes });
+                              stream, { workspace, workspace_bytes, false });
 }
 
 extern "C" int exl3r_gumbel_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,

@@ -70,6 +70,7 @@ PROTOTYPES = {
     "exl3r_sample_workspace_bytes": (ctypes.c_size_t, []),
     "exl3r_argmax_sample_ws": (_i, [_vp, _i, _i64, _i64, _i64, _i, _vp, _vp, ctypes.c_size_t, _vp]),
     "exl3r_gumbel_sample_ws": (_i, [_vp, _i, _i64, _i64, _i64, _i, ctypes.c_uint32, _vp, _vp, ctypes.c_size_t, _vp]),
+    "exl3r_argmax_sample_noalloc": (_i, [_vp, _i, _i64, _i64, _i64, _i, _vp, _vp]),
     "exl3r_rms_norm_had": (_i, [_vp, _i, _i64, _vp, _i, _vp, _i, _i64, _vp, _i64, _i, _vp, _vp, _i64, _i64, _i64,
                                 _f, _f, _f, _f, _i, _vp, _vp]),
     "exl3r_had_r_128": (_i, [_vp, _i, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _f, _vp]),

@@ -474,6 +474,21 @@ EXL3R_API int exl3r_gumbel_sample_ws(const void* logits, int dtype, int64_t rows
                         size_t workspace_bytes, void* stream);
 
 /*
+ * exl3r_argmax_sample_ws without a workspace argument: the library's own scratch, a fixed
+ * exl3r_sample_workspace_bytes()-byte array per GPU (384 rows) held until the process ends, serves as
+ * the workspace, so the call allocates nothing, ever: no hipMalloc, hipFree or allocating library
+ * routine (the device address is looked up once per device, on the first call with it current).
+ * No counterpart in the reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  The ids equal
+ * exl3r_argmax_sample's.  Calls that overlap on one GPU (several streams, or several graph replays in
+ * flight) share the scratch and race; a call that would need more rows of it than it holds is
+ * refused with EXL3R_EINVAL (below 128 rows the sliced kernel runs; from 128 the workgroup-per-row
+ * kernel, which needs no scratch).
+ */
+EXL3R_API int exl3r_argmax_sample_noalloc(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                        int max_logit, int64_t* ids, void* stream);
+
+/*
  * out[r, c] = x[r, c] + g(random, r, c) over every column (the noise of exl3r_gumbel_sample), rounded
  * once to out_dtype; out may be x.  x and out: [rows, cols], row strides ldx / ldo elements,
  * F16/BF16/F32.  With an F32 out, exl3r_argmax_sample of out equals exl3r_gumbel_sample of x.

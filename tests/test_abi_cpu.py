@@ -217,6 +217,11 @@ def test_sampling_validation():
         assert "aligned" in _err()
         assert fn(FAKE, I64, 2, 100, 100, 0, *extra, FAKE + 4096, ws, need, None) == exl3r.EDTYPE
         assert fn(None, F16, 0, 100, 100, 0, *extra, None, ws, need, None) == exl3r.OK
+    # the allocation-free argmax validates before it looks up its scratch
+    assert lib.exl3r_argmax_sample_noalloc(FAKE, I64, 2, 100, 100, 0, FAKE + 4096, None) == exl3r.EDTYPE
+    assert lib.exl3r_argmax_sample_noalloc(FAKE, F16, 2, 100, 50, 0, FAKE + 4096, None) == exl3r.EINVAL
+    assert lib.exl3r_argmax_sample_noalloc(FAKE, F16, 2, 100, 100, 0, None, None) == exl3r.EINVAL
+    assert lib.exl3r_argmax_sample_noalloc(None, F16, 0, 100, 100, 0, None, None) == exl3r.OK
     # exl3r_gumbel_noise(x, x_dtype, ldx, out, out_dtype, ldo, rows, cols, random)
     assert lib.exl3r_gumbel_noise(FAKE, F16, 64, FAKE + 8192, I32, 64, 2, 64, 1, None) == exl3r.EDTYPE
     assert lib.exl3r_gumbel_noise(FAKE, F16, 32, FAKE + 8192, F32, 64, 2, 64, 1, None) == exl3r.EINVAL
