@@ -114,3 +114,34 @@ def test_small_workspace_is_an_error():
     ids = torch.empty(4, dtype=torch.int64, device="cuda")
     with pytest.raises(Exception, match="workspace"):
         ffi.argmax_sample_ws(x, ids, ws)
+
+
+def test_graph_replays_reuse_the_workspace():
+    """argmax_sample_ws and gumbel_sample_ws captured in one HIP graph on one workspace, replayed with new
+    logits written between replays: every replay's ids equal the oracle's (the workspace must be back at
+    zero after each replay, since nothing in the graph clears it)."""
+    rows, vocab = 64, 151936
+    x = dev_normal((rows, vocab), 0, 3, F16, 980)
+    ws = workspace()
+    ids_a = torch.empty(rows, dtype=torch.int64, device="cuda")
+    ids_g = torch.empty(rows, dtype=torch.int64, device="cuda")
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        ffi.argmax_sample_ws(x, ids_a, ws)                  # warm-up outside capture
+        ffi.gumbel_sample_ws(x, ids_g, ws, 0, 11)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ffi.argmax_sample_ws(x, ids_a, ws)
+        ffi.gumbel_sample_ws(x, ids_g, ws, 0, 11)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        x.copy_(dev_normal((rows, vocab), 0, 3, F16, 981 + rep))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        xh = np.ascontiguousarray(from_dev(x))
+        assert np.array_equal(ids_a.cpu().numpy(), orc.argmax(xh, F16, 0, nthreads=NTHREADS)), f"replay {rep} argmax"
+        assert np.array_equal(ids_g.cpu().numpy(), orc.gumbel_sample(xh, F16, 11, 0, nthreads=NTHREADS)), \
+            f"replay {rep} gumbel"
+    assert int(ws.count_nonzero()) == 0

@@ -49,3 +49,30 @@ def test_noalloc_matches_workspace_entry_point():
         print(f"noalloc call {k}: rows={rows} vocab={vocab}", flush=True)
         assert np.array_equal(got.cpu().numpy(), ref.cpu().numpy()), f"call {k}: differs from exl3r_argmax_sample_ws"
         assert np.array_equal(got.cpu().numpy(), exp), f"call {k}: differs from the oracle"
+
+
+def test_noalloc_in_graph_replays():
+    """The allocation-free argmax captured in a HIP graph (after one eager call on the device, which looks
+    up the scratch), replayed with new logits written between replays, each replay against the
+    workspace entry point's ids."""
+    rows, vocab = 32, 151936
+    x = dev_normal((rows, vocab), 0, 3, F16, 990)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        ids = ids_noalloc(x)
+    torch.cuda.synchronize()
+    lib = L.load()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = torch.cuda.current_stream().cuda_stream
+        rc = lib.exl3r_argmax_sample_noalloc(x.data_ptr(), L.F16, rows, vocab, vocab, 0, ids.data_ptr(), st)
+    assert rc == 0
+    torch.cuda.synchronize()
+    for rep in range(3):
+        x.copy_(dev_normal((rows, vocab), 0, 3, F16, 991 + rep))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = ids_ws(x)
+        torch.cuda.synchronize()
+        assert np.array_equal(ids.cpu().numpy(), ref.cpu().numpy()), f"replay {rep}"
