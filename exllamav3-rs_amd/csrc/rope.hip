@@ -197,6 +197,14 @@ __device__ __forceinline__ void sincos_angle(float a, double& sd, double& cd)
     cd = q == 0 ? c : q == 1 ? -s : q == 2 ? -c : s;
 }
 
+// {cos, sin} * attn_factor of an fp32 angle.
+__device__ __forceinline__ float2 rope_cs_of_angle(float ang, float attn)
+{
+    double sd, cd;
+    sincos_angle(ang, sd, cd);
+    return make_float2((float)cd * attn, (float)sd * attn);
+}
+
 // {cos, sin} * attn_factor of rotary frequency t for token tok at position pos: fp64 evaluation of
 // the fp32 angle, rounded once (correctly rounded fp32 values).  SRC_ANGLE: the angle is read from
 // the token's sequence row `pos` of the angle table; a position outside the table sets *err and
@@ -219,9 +227,7 @@ __device__ __forceinline__ float2 rope_cs(const RopeArgs& a, int t, int tok, int
         }
     }
     else ang = __fmul_rn(a.inv_freq[t], (float)pos);
-    double sd, cd;
-    sincos_angle(ang, sd, cd);
-    return make_float2((float)cd * a.attn, (float)sd * a.attn);
+    return rope_cs_of_angle(ang, a.attn);
 }
 
 // sin/cos of every rotary frequency of one token into LDS (generic kernel).
@@ -781,6 +787,11 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
     const int R = a.R, R2 = a.R >> 1;
     using Item = NxItem<IO, NORM, SRC, P>;
     int64_t evaluated = -1;                   // SRC_FREQ: the token whose pairs the wave's LDS row holds
+    // SRC_FREQ: the lane's rotary frequency inv_freq[l64], staged through LDS with the norm weights, so
+    // that the item loop's only vector loads are the items' own (a wait for an evaluation's read of
+    // inv_freq would also wait for the next item's loads).
+    __shared__ float fsh[SRC == SRC_FREQ ? 64 : 1];
+    float freq = 0.0f;
 
     // Loads of one item: the lane's two chunks of head (slice * P + p) * 8 + grp for each of the P passes,
     // and its rotary pairs (SRC_CS) or the token's position (SRC_FREQ).
@@ -790,8 +801,11 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
         #pragma unroll
         for (int p = 0; p < P; ++p)
         {
-            const int h = (t.slice * P + p) * 8 + grp;
-            if (h < H)
+            // Lanes past the last head take head H - 1: they load, compute and store exactly what that
+            // head's lanes do (identical bytes to the same addresses), so every lane loads and stores
+            // and no branch around a load or store makes the compiler's waits for the item's data cover
+            // later loads too.
+            const int h = min((t.slice * P + p) * 8 + grp, H - 1);
             {
                 const char* base;
                 if constexpr (APPEND)
@@ -844,21 +858,21 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
         }
         else
             wsh[i] = w ? load1(w, a.wt, e) + a.cb : 0.0f;
+    }
+    if constexpr (SRC == SRC_FREQ)
+        if (threadIdx.x < 64) fsh[threadIdx.x] = (int)threadIdx.x < R2 ? a.inv_freq[threadIdx.x] : 0.0f;
+    if constexpr (NORM != NORM_NONE || SRC == SRC_FREQ)
+    {
         __syncthreads();
+        if constexpr (SRC == SRC_FREQ) freq = fsh[l64];
     }
 
-    // Head norm, rotation and stores of one pass (lo / hi: the lane's chunks of head h).
+    // Head norm, rotation and stores of one pass (lo / hi: the lane's chunks of head h < H).
     auto pass = [&](int64_t tok, int h, typename IO::Vec& lo, typename IO::Vec& hi, const float (&c)[8],
                     const float (&s)[8], int64_t crow) __attribute__((always_inline)) {
-        const bool act = h < H;
         const bool isq = h < hq;
         const bool isv = APPEND && h >= hq + hk;
         const int hidx = h - (isq ? 0 : hq) - (isv ? hk : 0);
-        if (!act)
-        {
-            #pragma unroll
-            for (int i = 0; i < 4; ++i) lo.a[i] = hi.a[i] = 0;
-        }
         if constexpr (HADR)
         {
             // The head's post-scale (f16 per column of the projection output), loaded before the
@@ -866,7 +880,7 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
             // wave-per-token kernel's time at C4), applied after its rounding; a padding head past the
             // last one has none.
             const void* post = pick_qkv(isq, isv, qpost, kpost, vpost);
-            const bool hp = act && post != nullptr;
+            const bool hp = post != nullptr;
             u32x4 pl = {}, ph = {};
             if (hp)
             {
@@ -973,7 +987,6 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
             hi = pack8<IO>(fh);
         }
         }
-        if (!act) return;
         if (isq || (!isv && (!APPEND || kout)))
         {
             char* ob;
@@ -1022,7 +1035,7 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
             if (t.tok != evaluated)           // wave-uniform: once per token within a run
             {
                 wave_lds_sync();
-                if (l64 < R2) row[l64] = rope_cs<SRC_FREQ>(a, l64, (int)t.tok, t.pos);
+                if (MODE == EXL3R_ROPE_NEOX || l64 < R2) row[l64] = rope_cs_of_angle(__fmul_rn(freq, (float)t.pos), a.attn);
                 wave_lds_sync();
                 evaluated = t.tok;
             }
@@ -1031,15 +1044,15 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
             {
                 // NeoX: pair e0 + j; GPT-J: pair e0/2 + j (lo chunk, j < 4) or 32 + e0/2 + j - 4 (hi chunk)
                 const int tp = MODE == EXL3R_ROPE_NEOX ? e0 + j : j < 4 ? e0 / 2 + j : 32 + e0 / 2 + (j - 4);
-                const float2 x = tp < R2 ? row[tp] : make_float2(0.0f, 0.0f);
+                const float2 x = MODE == EXL3R_ROPE_NEOX || tp < R2 ? row[tp] : make_float2(0.0f, 0.0f);   // NeoX: R2 = 64
                 c[j] = x.x;
                 s[j] = x.y;
             }
         }
         #pragma unroll
         for (int p = 0; p < P; ++p)
-            if ((t.slice * P + p) * 8 < H)    // wave-uniform: a pass past the last head is skipped whole
-                pass(t.tok, (t.slice * P + p) * 8 + grp, t.lo[p], t.hi[p], c, s, APPEND ? t.crow : -1);
+            if (p == 0 || (t.slice * P + p) * 8 < H)   // wave-uniform: a pass past the last head is skipped whole
+                pass(t.tok, min((t.slice * P + p) * 8 + grp, H - 1), t.lo[p], t.hi[p], c, s, APPEND ? t.crow : -1);
     };
 
     int64_t item = ((int64_t)blockIdx.x * 4 + wave) * run;
@@ -1050,11 +1063,15 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
         j = 0;
         return it + 1 + (W - 1) * run;
     };
+    // Issue the next item's loads, then finish this one (the loop alternates the two buffers).  (The
+    // compiler's wait for an item's data also covers the next item's loads, the issue being conditional;
+    // finishing each wave's last item on a path of its own makes that wait exact, but the second copy of
+    // the item code costs registers and measured no faster: C4 32.6 us either way, from the table 33.2
+    // against 31.2 us.)
     Item A, B;
     issue(A, item);
     for (;;)
     {
-        // Issue the next item's loads, then finish this one (the loop alternates the two buffers).
         const int64_t nb = next(item);
         if (nb < items) issue(B, nb);
         compute(A);
