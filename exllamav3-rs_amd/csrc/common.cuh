@@ -77,6 +77,20 @@ __device__ __forceinline__ float opaque(float v)
     return v;
 }
 __device__ __forceinline__ _Float16 to_f16(float v) { return (_Float16)opaque(v); }
+
+// fl32(h * c) for the f16 element h in the low (HI = false) or high half of a packed pair and an fp32 c,
+// in one instruction: the mixed-precision fma converts h exactly and adds -0, which leaves every
+// product as the fp32 multiply rounds it (x * c + -0 = x * c, signed zeros included).
+template <bool HI>
+__device__ __forceinline__ float mul_f16_f32(uint32_t pair, float c)
+{
+    float r;
+    if constexpr (HI)
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(c), "s"(-0.0f));
+    else
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(c), "s"(-0.0f));
+    return r;
+}
 __device__ __forceinline__ float round_f16(float v) { return (float)to_f16(v); }
 __device__ __forceinline__ float round_bf16(float v) { return bf16lo(pack_bf16(v, 0.0f)); }
 

@@ -953,7 +953,20 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
             float fl[8], fh[8];
             unpack8<IO>(lo, fl);
             unpack8<IO>(hi, fh);
-            if constexpr (MODE == EXL3R_ROPE_NEOX)
+            if constexpr (MODE == EXL3R_ROPE_NEOX && IO::code == DT_F16)
+            {
+                // The products straight from the packed f16 pairs (no unpacking; the same roundings).
+                #pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    const uint32_t x = lo.a[i], y = hi.a[i];
+                    fl[2 * i] = opaque(mul_f16_f32<false>(x, c[2 * i]) - mul_f16_f32<false>(y, s[2 * i]));
+                    fh[2 * i] = opaque(mul_f16_f32<false>(y, c[2 * i]) + mul_f16_f32<false>(x, s[2 * i]));
+                    fl[2 * i + 1] = opaque(mul_f16_f32<true>(x, c[2 * i + 1]) - mul_f16_f32<true>(y, s[2 * i + 1]));
+                    fh[2 * i + 1] = opaque(mul_f16_f32<true>(y, c[2 * i + 1]) + mul_f16_f32<true>(x, s[2 * i + 1]));
+                }
+            }
+            else if constexpr (MODE == EXL3R_ROPE_NEOX)
             {
                 #pragma unroll
                 for (int j = 0; j < 8; ++j)
