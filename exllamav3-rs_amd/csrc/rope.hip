@@ -1144,8 +1144,9 @@ static void launch_rope_nx_p(const RopeArgs& a, hipStream_t s)
     // cache rows of one token reused too).  Two passes per item (GPT-J) and the plain kernel reading the
     // table are fastest at 1.  q / k norm + RoPE + paged append at 4096 tokens, runs of 1 / 2 / 3 / 4 / 6:
     // 42.5 / 38.8 / 39.7 / 38.5 / 39.6, from the table 38.2 / 36.5 / 38.3 / 35.8 / 41.3 (the wave-per-token
-    // kernel: 41.7 / 38.8).
-    constexpr int kRun = HADR ? 3 : APPEND ? 4 : SRC == SRC_FREQ && P == 1 && !QOUT ? 2 : 1;
+    // kernel: 41.7 / 38.8).  The q | g split (rope_qg, Qwen3.5 4096 tokens) at runs of 1 / 2 / 4: 35.4 /
+    // 34.7 / 34.5.
+    constexpr int kRun = HADR ? 3 : APPEND ? 4 : SRC == SRC_FREQ && P == 1 ? 2 : 1;
     const int tr = tuning().rope_nx_run;
     const int run = tr > 0 ? tr : items >= (int64_t)kRun * blocks * 4 ? kRun : 1;
     const int64_t runs = (items + run - 1) / run;
