@@ -151,8 +151,7 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
                             for (int q = 0; q < 4; ++q) hv.a[q] = hmul2(hv.a[q], p.a[q]);
                         }
                         float f[8];
-                        unpack8<TF16>(hv, f);
-                        butterfly128(f, (int)(c & 15), a.hr);
+                        butterfly128_f16<false>(hv, f, (int)(c & 15), a.hr);
                         store8<TF16>((char*)a.hout + row * a.ldh * 2, c * 8, pack8<TF16>(f));
                     }
                 }
@@ -191,7 +190,7 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
                             }
                     });
                 }
-                float f[UNROLL][8];
+                TF16::Vec hvs[UNROLL];
                 bool zero = false;
                 #pragma unroll
                 for (int u = 0; u < UNROLL; ++u)
@@ -211,8 +210,8 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
                             #pragma unroll
                             for (int q = 0; q < 4; ++q) hv.a[q] = hmul2(hv.a[q], p.a[q]);
                         }
-                        unpack8<TF16>(hv, f[u]);
-                        zero |= zero_lane(f[u]);
+                        hvs[u] = hv;
+                        zero |= zero_lane16(hv);
                     }
                 }
                 with_carried<true>(zero, a.hr, [&](auto C) {
@@ -221,8 +220,9 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
                         if (live[u])
                         {
                             const int64_t c = base + (int64_t)u * nt;
-                            butterfly128_t<decltype(C)::value>(f[u], (int)(c & 15), a.hr);
-                            store8<TF16>((char*)a.hout + row * a.ldh * 2, c * 8, pack8<TF16>(f[u]));
+                            float f[8];
+                            butterfly128_f16<decltype(C)::value>(hvs[u], f, (int)(c & 15), a.hr);
+                            store8<TF16>((char*)a.hout + row * a.ldh * 2, c * 8, pack8<TF16>(f));
                         }
                 });
             }

@@ -81,36 +81,30 @@ __device__ __forceinline__ void lane_stage_carried(float (&f)[8], int l16)
 // is -0 only if every input it depends on is a zero and one of them is -0 (a cancellation of non-zero
 // values gives +0, and -0 comes only from (-0) + (-0) or (-0) - (+0)); each of the 128-point
 // transform's results depends on all 128 inputs.  So unless some lane holds 8 zero inputs with a -0
-// among them (zero_lane), every zero result is +0, and fma(v, +-r, +0) turns the carried value's zero,
-// of either sign, into +0 while it rounds every other product as r * value does (r > 0).  Otherwise
-// (zero blocks with -0 in them, r <= 0 or NaN) the wave takes the exact stages.
-__device__ __forceinline__ bool zero_lane(const float (&f)[8])
-{
-    uint32_t o = 0;
-    #pragma unroll
-    for (int j = 0; j < 8; ++j) o |= __builtin_bit_cast(uint32_t, f[j]);
-    return o == 0x80000000u;
-}
-// zero_lane of a lane's 8 f16 values as loaded (an f16 zero widens to the fp32 zero of its sign).
+// among them (zero_lane16), every zero result is +0, and fma(v, +-r, +0) turns the carried value's
+// zero, of either sign, into +0 while it rounds every other product as r * value does (r > 0).
+// Otherwise (zero blocks with -0 in them, r <= 0 or NaN) the wave takes the exact stages.
+// The test on a lane's 8 f16 inputs as loaded (an f16 zero widens to the fp32 zero of its sign).
 __device__ __forceinline__ bool zero_lane16(const TF16::Vec& v)
 {
     const uint32_t o = v.a[0] | v.a[1] | v.a[2] | v.a[3];
     return ((o | (o >> 16)) & 0xffffu) == 0x8000u;
 }
-// Wave-uniform: no lane of the wave raised `zero` (zero_lane of any of its blocks) and r > 0.
+// Wave-uniform: no lane of the wave raised `zero` (zero_lane16 of any of its blocks) and r > 0.
 __device__ __forceinline__ bool carried_ok(bool zero, float r)
 {
     return r > 0.0f && __builtin_amdgcn_ballot_w64(zero) == 0;
 }
 
 // f = r * H128 (block) with r the transform's scale, rounded once after the fp32 butterfly; CARRIED:
-// the carried-sign lane stages (only where carried_ok holds for the wave).
-template <bool CARRIED>
+// the carried-sign lane stages (only where carried_ok holds for the wave).  H0 = 2: f already holds the
+// first in-lane stage (unpack8_stage1).
+template <bool CARRIED, int H0 = 1>
 __device__ __forceinline__ void butterfly128_t(float (&f)[8], int l16, float r)
 {
     #pragma clang fp contract(off)
     #pragma unroll
-    for (int h = 1; h < 8; h <<= 1)
+    for (int h = H0; h < 8; h <<= 1)
     {
         #pragma unroll
         for (int j = 0; j < 8; ++j)
@@ -147,6 +141,29 @@ __device__ __forceinline__ void butterfly128_t(float (&f)[8], int l16, float r)
 // One block per call, exact stages (the callers that rotate one block at a time).
 __device__ __forceinline__ void butterfly128(float (&f)[8], int l16, float r) { butterfly128_t<false>(f, l16, r); }
 
+// The butterfly's first in-lane stage (pairs 2i, 2i + 1: the two halves of packed word i) straight from
+// an f16 chunk: fl32(a + b) and fl32(a - b) as mixed-precision fmas a * 1 + (+-b), which convert both
+// halves exactly and round once, as the fp32 add and subtract of the converted halves do (signed zeros
+// included).  One instruction per element instead of a conversion and an add.
+__device__ __forceinline__ void unpack8_stage1(const TF16::Vec& v, float (&f)[8])
+{
+    #pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const uint32_t w = v.a[i];
+        asm("v_fma_mix_f32 %0, %1, 1.0, %1 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(f[2 * i]) : "v"(w));
+        asm("v_fma_mix_f32 %0, %1, 1.0, -%1 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(f[2 * i + 1]) : "v"(w));
+    }
+}
+
+// f = r * H128 of the f16 chunk v (its lane's share of the block).
+template <bool CARRIED>
+__device__ __forceinline__ void butterfly128_f16(const TF16::Vec& v, float (&f)[8], int l16, float r)
+{
+    unpack8_stage1(v, f);
+    butterfly128_t<CARRIED, 2>(f, l16, r);
+}
+
 // Runs body(std::true_type) where the carried-sign stages are valid for the wave, else
 // body(std::false_type): one wave-uniform branch around every butterfly of the body.  ENABLE false
 // keeps the exact stages without the test (kernels whose time the butterfly does not set).
@@ -174,8 +191,7 @@ template <bool CARRIED = false>
 __device__ __forceinline__ void output_rotation8(TF16::Vec& v, const void* post, int64_t col)
 {
     float f[8];
-    unpack8<TF16>(v, f);
-    butterfly128_t<CARRIED>(f, (int)((col >> 3) & 15), 0.0883883461356163f);
+    butterfly128_f16<CARRIED>(v, f, (int)((col >> 3) & 15), 0.0883883461356163f);
     v = pack8<TF16>(f);
     if (post)
     {

@@ -45,7 +45,7 @@ __device__ __forceinline__ void had_block(const HadArgs& a, int64_t blk, int l16
             #pragma unroll
             for (int i = 0; i < 4; ++i) v.a[i] = hmul2(v.a[i], p.a[i]);
         }
-        unpack8<IO>(v, f);
+        butterfly128_f16<false>(v, f, l16, a.r);
     }
     else
     {
@@ -57,8 +57,8 @@ __device__ __forceinline__ void had_block(const HadArgs& a, int64_t blk, int l16
             #pragma unroll
             for (int j = 0; j < 8; ++j) f[j] = f[j] * p[j];
         }
+        butterfly128(f, l16, a.r);
     }
-    butterfly128(f, l16, a.r);
     if constexpr (IO::code == DT_F16)
     {
         v = pack8<IO>(f);

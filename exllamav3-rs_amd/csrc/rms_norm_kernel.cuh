@@ -332,10 +332,9 @@ __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* 
                 #pragma unroll
                 for (int q = 0; q < 4; ++q) v.a[q] = hmul2(v.a[q], p.a[q]);
             }
-            float f[8];
-            unpack8<TF16>(v, f);
             with_carried<true>(zero_lane16(v), a.hr, [&](auto C) {
-                butterfly128_t<decltype(C)::value>(f, l16, a.hr);
+                float f[8];
+                butterfly128_f16<decltype(C)::value>(v, f, l16, a.hr);
                 store8<TF16>((char*)a.hout[i] + row * a.ldh * 2, e, pack8<TF16>(f));
             });
         }

@@ -710,10 +710,10 @@ __device__ __forceinline__ void rotate_head_nx(TF16::Vec& lo, TF16::Vec& hi, int
 {
     #pragma clang fp contract(off)
     float fl[8], fh[8];
-    unpack8<TF16>(lo, fl);
-    unpack8<TF16>(hi, fh);
+    unpack8_stage1(lo, fl);     // index bit 0 from the packed pairs
+    unpack8_stage1(hi, fh);
     #pragma unroll
-    for (int h = 1; h < 8; h <<= 1)
+    for (int h = 2; h < 8; h <<= 1)
     {
         #pragma unroll
         for (int j = 0; j < 8; ++j)
