@@ -877,8 +877,7 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
         {
             // The head's post-scale (f16 per column of the projection output), loaded before the
             // butterfly so that its latency hides under it (after it: 0.87x instead of 0.83x of the
-            // wave-per-token kernel's time at C4), applied after its rounding; a padding head past the
-            // last one has none.
+            // wave-per-token kernel's time at C4), applied after its rounding.
             const void* post = pick_qkv(isq, isv, qpost, kpost, vpost);
             const bool hp = post != nullptr;
             u32x4 pl = {}, ph = {};
