@@ -63,17 +63,20 @@ def test_in_place_strided_and_unaligned():
 
 def test_signed_zeros_and_special_values():
     """Zero blocks of either sign (an exact zero's sign follows the butterfly's order: (-0) + (-0) = -0,
-    (+0) - (+0) = +0), infinities, overflow to infinity and NaN, with a sign-flipping pre-scale.  Finite
+    (+0) - (+0) = +0), infinities, overflow to infinity, NaN and f16 subnormals, with a sign-flipping
+    pre-scale.  Finite
     and infinite results are compared bit for bit; NaN positions must agree (a NaN's sign and payload
     are the arithmetic unit's own)."""
     cols = 256
-    x = np.zeros((7, cols), np.float16)
+    x = np.zeros((8, cols), np.float16)
     x[1] = -0.0
     x[2, ::3] = -0.0
     x[3, 5] = np.inf
     x[4, 7] = np.nan
     x[5] = 60000.0
     x[6, 3], x[6, 9] = np.inf, -np.inf
+    # f16 subnormals of both signs next to zeros (the first butterfly stage converts the packed halves itself)
+    x[7] = (np.random.default_rng(3).integers(-1023, 1024, cols) * 2.0 ** -24).astype(np.float16)
     pre = np.where(np.arange(cols) % 5 == 0, -1.0, 1.0).astype(np.float16)
     xd = torch.from_numpy(x.view(np.int16)).view(torch.float16).cuda()
     pd = torch.from_numpy(pre.view(np.int16)).view(torch.float16).cuda()

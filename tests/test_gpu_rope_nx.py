@@ -15,7 +15,7 @@ import torch
 import exl3r
 import exl3r._lib as L
 import exl3r.ffi as ffi
-from _gpu import NTHREADS, assert_close_ulp, dev_normal, from_dev
+from _gpu import NTHREADS, assert_close_ulp, dev_normal, from_dev, to_dev
 from oracle import oracle as orc
 from test_gpu_rope import inv_freq, ragged_position_ids, run
 
@@ -221,3 +221,32 @@ def test_runs(nx, passes, length, wpc):
         P.run(2, 45, 12, 3, 128, 128, exl3r.ROPE_NEOX, F16, 16, pages, 8, sl, bt, seed=93)
         RH.run(1, 70, 12, 3, 128, 128, exl3r.ROPE_NEOX, position=21, seed=94)
         PH.run(2, 40, 16, 4, 16, 8, seed=95)
+
+
+@pytest.mark.parametrize("passes", [1, 2])
+def test_rotation_f16_special_values(nx, passes):
+    """The f16 NeoX rotation forms its fp32 products straight from the packed f16 pairs (a mixed-precision
+    fma with a -0 addend): f16 subnormals, signed zeros, the f16 maximum (products past it round to
+    infinity) and position 0 (sin = 0: every second product is a zero of either sign), without the head
+    norm so that the raw inputs reach the products.  Against the oracle (<= 2 ulp), and every result the
+    oracle gives as a zero carries the oracle's sign."""
+    nx(passes)
+    seq, hq, hk = 48, 12, 5
+    rng = np.random.default_rng(123)
+    vals = np.array([0.0, -0.0, 6e-8, -6e-8, 3.0e-5, -2.4e-5, 65504.0, -65504.0, 1.0, -1.0, 0.5, 1e-3],
+                    np.float16)
+    qh = rng.choice(vals, (1, seq, hq, 128)).astype(np.float16).view(np.uint16)
+    kh = rng.choice(vals, (1, seq, hk, 128)).astype(np.float16).view(np.uint16)
+    pid = np.concatenate([np.zeros(16, np.int32), rng.integers(1, 40000, seq - 16).astype(np.int32)])[None, :]
+    f = inv_freq(128)
+    q, k = to_dev(qh, F16), to_dev(kh, F16)
+    ffi.rope(q, q, k, k, torch.from_numpy(f).cuda(), 0, None, None, None, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0,
+             position_ids=torch.from_numpy(pid).cuda())
+    torch.cuda.synchronize()
+    eq, ek = orc.rope(qh, kh, F16, f, exl3r.ROPE_NEOX, position_ids=pid.reshape(-1), q_norm=None, k_norm=None,
+                      nwt=F16, eps=1e-6, cb=0.0, attn=1.0, nthreads=NTHREADS)
+    for got, exp, what in ((from_dev(q), eq, "q"), (from_dev(k), ek, "k")):
+        assert_close_ulp(got, exp, F16, 2, what=f"f16 specials {what} passes={passes}")
+        zero = (exp & 0x7FFF) == 0
+        assert zero.sum() > 100, "the case must hold zero results"
+        assert np.array_equal(got[zero], exp[zero]), f"zero signs differ ({what})"
