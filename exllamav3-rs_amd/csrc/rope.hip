@@ -949,12 +949,10 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
         {
             // r1 = fl(fl(v1 c) - fl(v2 s)), r2 = fl(fl(v2 c) + fl(v1 s)), each rounded once to io.
             #pragma clang fp contract(off)
-            float fl[8], fh[8];
-            unpack8<IO>(lo, fl);
-            unpack8<IO>(hi, fh);
             if constexpr (MODE == EXL3R_ROPE_NEOX && IO::code == DT_F16)
             {
                 // The products straight from the packed f16 pairs (no unpacking; the same roundings).
+                float fl[8], fh[8];
                 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                 {
@@ -964,39 +962,63 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
                     fl[2 * i + 1] = opaque(mul_f16_f32<true>(x, c[2 * i + 1]) - mul_f16_f32<true>(y, s[2 * i + 1]));
                     fh[2 * i + 1] = opaque(mul_f16_f32<true>(y, c[2 * i + 1]) + mul_f16_f32<true>(x, s[2 * i + 1]));
                 }
+                lo = pack8<IO>(fl);
+                hi = pack8<IO>(fh);
             }
-            else if constexpr (MODE == EXL3R_ROPE_NEOX)
+            else if constexpr (IO::code == DT_F16)
             {
+                // GPT-J f16: a pair is the two halves of one packed word, its products taken from the word;
+                // dims >= rotary_dim keep their bits.  c / s [0, 4): the lo chunk's pairs, [4, 8): the hi chunk's.
+                auto pair = [](uint32_t w, float cc, float ss) __attribute__((always_inline)) {
+                    const float r1 = opaque(mul_f16_f32<false>(w, cc) - mul_f16_f32<true>(w, ss));
+                    const float r2 = opaque(mul_f16_f32<true>(w, cc) + mul_f16_f32<false>(w, ss));
+                    return pack_f16(r1, r2);
+                };
                 #pragma unroll
-                for (int j = 0; j < 8; ++j)
+                for (int i = 0; i < 4; ++i)
                 {
-                    const float x = fl[j], y = fh[j];
-                    fl[j] = opaque(x * c[j] - y * s[j]);
-                    fh[j] = opaque(y * c[j] + x * s[j]);
+                    if (e0 + 2 * i < R) lo.a[i] = pair(lo.a[i], c[i], s[i]);
+                    if (64 + e0 + 2 * i < R) hi.a[i] = pair(hi.a[i], c[4 + i], s[4 + i]);
                 }
             }
             else
             {
-                // c / s [0, 4): the lo chunk's pairs, [4, 8): the hi chunk's; dims >= rotary_dim pass through
-                #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                float fl[8], fh[8];
+                unpack8<IO>(lo, fl);
+                unpack8<IO>(hi, fh);
+                if constexpr (MODE == EXL3R_ROPE_NEOX)
                 {
-                    if (e0 + 2 * i < R)
+                    #pragma unroll
+                    for (int j = 0; j < 8; ++j)
                     {
-                        const float x = fl[2 * i], y = fl[2 * i + 1];
-                        fl[2 * i] = opaque(x * c[i] - y * s[i]);
-                        fl[2 * i + 1] = opaque(y * c[i] + x * s[i]);
-                    }
-                    if (64 + e0 + 2 * i < R)
-                    {
-                        const float x = fh[2 * i], y = fh[2 * i + 1];
-                        fh[2 * i] = opaque(x * c[4 + i] - y * s[4 + i]);
-                        fh[2 * i + 1] = opaque(y * c[4 + i] + x * s[4 + i]);
+                        const float x = fl[j], y = fh[j];
+                        fl[j] = opaque(x * c[j] - y * s[j]);
+                        fh[j] = opaque(y * c[j] + x * s[j]);
                     }
                 }
+                else
+                {
+                    // c / s [0, 4): the lo chunk's pairs, [4, 8): the hi chunk's; dims >= rotary_dim pass through
+                    #pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                    {
+                        if (e0 + 2 * i < R)
+                        {
+                            const float x = fl[2 * i], y = fl[2 * i + 1];
+                            fl[2 * i] = opaque(x * c[i] - y * s[i]);
+                            fl[2 * i + 1] = opaque(y * c[i] + x * s[i]);
+                        }
+                        if (64 + e0 + 2 * i < R)
+                        {
+                            const float x = fh[2 * i], y = fh[2 * i + 1];
+                            fh[2 * i] = opaque(x * c[4 + i] - y * s[4 + i]);
+                            fh[2 * i + 1] = opaque(y * c[4 + i] + x * s[4 + i]);
+                        }
+                    }
+                }
+                lo = pack8<IO>(fl);
+                hi = pack8<IO>(fh);
             }
-            lo = pack8<IO>(fl);
-            hi = pack8<IO>(fh);
         }
         }
         if (isq || (!isv && (!APPEND || kout)))
