@@ -23,7 +23,7 @@ int set_error(int code, const char* fmt, ...)
 
 int launch_status(const char* op)
 {
-    hipError_t e = hipGetLastError();
+    const hipError_t e = t_launch_error;
     if (e != hipSuccess) return set_error((int)e, "%s: kernel launch failed: %s", op, hipGetErrorString(e));
     return EXL3R_OK;
 }

@@ -1,9 +1,13 @@
 // Host-side helpers shared by the C ABI entry points: thread-local error message, argument
-// validation, launch-status check.  Nothing here allocates or synchronises.
+// validation, kernel launches that report their own status.  Nothing here allocates or synchronises.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <tuple>
+#include <type_traits>
+#include <utility>
 
 #include "../../include/exl3r/rowops.h"
 
@@ -12,14 +16,35 @@ namespace exl3r {
 // Records a printf-style message for exl3r_last_error() and returns `code`.
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
-// Status of the kernel launch just issued (hipGetLastError); sets the message on failure.
+// Launch status of the current entry point call, kept in this library's own thread-local slot.
+// Launches go through hipLaunchKernel, whose return value is that launch's own status, so the
+// thread's HIP last-error state is never read or cleared: an error that another caller (torch, the
+// application) left pending stays where it was.
+inline thread_local hipError_t t_launch_error = hipSuccess;
+
+// Every entry point starts with begin_call(), before validating its arguments.
+inline void begin_call() { t_launch_error = hipSuccess; }
+
+// The first failed launch of this call, or EXL3R_OK; sets the message on failure.
 int launch_status(const char* op);
 
-// Discards an error left on this thread by an earlier, unrelated HIP call (hipGetLastError keeps the
-// last failure until it is read), so that launch_status reports this entry point's own launches only.
-// Every entry point calls it before validating its arguments; device faults, which are sticky, are
-// still reported by the launch itself.
-inline void clear_stale_error() { (void)hipGetLastError(); }
+// k<<<grid, block, shmem, stream>>>(args...) with the launch's own status: recorded for
+// launch_status and returned (as an int hipError_t).  Each argument is converted to its kernel
+// parameter's type.
+template <class... P, class... A>
+inline int launch(void (*k)(P...), dim3 grid, dim3 block, size_t shmem, hipStream_t stream, A&&... args)
+{
+    static_assert(sizeof...(P) == sizeof...(A), "one argument per kernel parameter");
+    std::tuple<std::remove_cv_t<P>...> vals(std::forward<A>(args)...);
+    void* argv[sizeof...(P) > 0 ? sizeof...(P) : 1] = {};
+    std::apply([&](auto&... v) {
+        int i = 0;
+        ((argv[i++] = (void*)&v), ...);
+    }, vals);
+    const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(k), grid, block, argv, shmem, stream);
+    if (e != hipSuccess && t_launch_error == hipSuccess) t_launch_error = e;
+    return (int)e;
+}
 
 inline bool is_float_dtype(int dt) { return dt == EXL3R_F32 || dt == EXL3R_F16 || dt == EXL3R_BF16; }
 inline int dtype_bytes(int dt)

@@ -307,8 +307,8 @@ static void launch_act_vec(const ActArgs& a, hipStream_t s)
             const int64_t n = a.rows * cpr;
             int64_t blocks = (n + 256 * 2 - 1) / (256 * 2);
             if (blocks > kMaxGridX) blocks = kMaxGridX;
-            if (a.limit != 0.0f) k_act_mul_short<ACT, IT, OT, 2, true><<<(unsigned)blocks, 256, 0, s>>>(a);
-            else k_act_mul_short<ACT, IT, OT, 2, false><<<(unsigned)blocks, 256, 0, s>>>(a);
+            if (a.limit != 0.0f) launch(k_act_mul_short<ACT, IT, OT, 2, true>, (unsigned)blocks, 256, 0, s, a);
+            else launch(k_act_mul_short<ACT, IT, OT, 2, false>, (unsigned)blocks, 256, 0, s, a);
             return;
         }
     }
@@ -326,21 +326,21 @@ static void launch_act_vec(const ActArgs& a, hipStream_t s)
         if (a.cols % 512 == 0 && tu.rms_split != -1)
         {
             // two chunks per thread (the grid-stride loop covers the row whatever the grid)
-            if (a.limit != 0.0f) k_act_mul<ACT, IT, OT, 2, true, 0, true><<<grid, threads, 0, s>>>(a);
-            else k_act_mul<ACT, IT, OT, 2, false, 0, true><<<grid, threads, 0, s>>>(a);
+            if (a.limit != 0.0f) launch(k_act_mul<ACT, IT, OT, 2, true, 0, true>, grid, threads, 0, s, a);
+            else launch(k_act_mul<ACT, IT, OT, 2, false, 0, true>, grid, threads, 0, s, a);
             return;
         }
     }
     if (a.limit != 0.0f)
-        k_act_mul<ACT, IT, OT, 2, true, HAD><<<grid, threads, 0, s>>>(a);
+        launch(k_act_mul<ACT, IT, OT, 2, true, HAD>, grid, threads, 0, s, a);
     else
     {
         switch (unroll)
         {
-            case 1: k_act_mul<ACT, IT, OT, 1, false, HAD><<<grid, threads, 0, s>>>(a); break;
-            case 2: k_act_mul<ACT, IT, OT, 2, false, HAD><<<grid, threads, 0, s>>>(a); break;
-            case 8: k_act_mul<ACT, IT, OT, 8, false, HAD><<<grid, threads, 0, s>>>(a); break;
-            default: k_act_mul<ACT, IT, OT, 4, false, HAD><<<grid, threads, 0, s>>>(a); break;
+            case 1: launch(k_act_mul<ACT, IT, OT, 1, false, HAD>, grid, threads, 0, s, a); break;
+            case 2: launch(k_act_mul<ACT, IT, OT, 2, false, HAD>, grid, threads, 0, s, a); break;
+            case 8: launch(k_act_mul<ACT, IT, OT, 8, false, HAD>, grid, threads, 0, s, a); break;
+            default: launch(k_act_mul<ACT, IT, OT, 4, false, HAD>, grid, threads, 0, s, a); break;
         }
     }
 }
@@ -361,7 +361,7 @@ static int act_had_entry(const char* op, const void* x, const void* y, int it, i
                          int64_t rows, int64_t cols, float limit, float had_scale, int rotate_in,
                          const void* x_post, const void* y_post, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     if (!is_float_dtype(it)) return set_error(EXL3R_EDTYPE, "%s: unsupported input dtype %s", op, dtype_name(it));
     if (rotate_in & ~3) return set_error(EXL3R_EINVAL, "%s: rotate_in takes bits 0 (x) and 1 (y)", op);
     if (rotate_in && it != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: rotated inputs are f16", op);
@@ -442,7 +442,7 @@ static int act_mul_entry(const char* op, const void* x, const void* y, int it, v
             t.z = (char*)a.z + body * dtype_bytes(ot);
             t.cols = a.cols - body;
             t.ldx = t.ldy = t.ldz = t.cols;
-            k_act_mul_generic<ACT><<<1, 64, 0, s>>>(t, it, ot);
+            launch(k_act_mul_generic<ACT>, 1, 64, 0, s, t, it, ot);
         }
     }
     else
@@ -450,7 +450,7 @@ static int act_mul_entry(const char* op, const void* x, const void* y, int it, v
         const int64_t n = a.rows * a.cols;
         int64_t blocks = (n + 255) / 256;
         if (blocks > kMaxGridX) blocks = kMaxGridX;
-        k_act_mul_generic<ACT><<<(unsigned)blocks, 256, 0, s>>>(a, it, ot);
+        launch(k_act_mul_generic<ACT>, (unsigned)blocks, 256, 0, s, a, it, ot);
     }
     return launch_status(op);
 }
@@ -463,7 +463,7 @@ extern "C" int exl3r_silu_mul(const void* x, const void* y, int in_dtype, void* 
                               int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz,
                               float act_limit, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     return act_mul_entry<ACT_SILU>("exl3r_silu_mul", x, y, in_dtype, z, z_dtype, rows, cols, ldx, ldy, ldz, act_limit, stream);
 }
 
@@ -471,7 +471,7 @@ extern "C" int exl3r_gelu_mul(const void* x, const void* y, int in_dtype, void* 
                               int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz,
                               float act_limit, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     return act_mul_entry<ACT_GELU>("exl3r_gelu_mul", x, y, in_dtype, z, z_dtype, rows, cols, ldx, ldy, ldz, act_limit, stream);
 }
 
@@ -480,7 +480,7 @@ extern "C" int exl3r_act_mul_had(int act, const void* x, const void* y, int in_d
                                  int64_t rows, int64_t cols, float act_limit, float had_scale, int rotate_in,
                                  const void* x_post_scale, const void* y_post_scale, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_act_mul_had";
     switch (act)
     {
@@ -506,7 +506,7 @@ extern "C" int exl3r_act_mul_had(int act, const void* x, const void* y, int in_d
 extern "C" int exl3r_mul_sigmoid(const void* x, const void* y, int in_dtype, void* z, int z_dtype,
                                  int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, int64_t ldz, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     return act_mul_entry<ACT_SIGMOID>("exl3r_mul_sigmoid", y, x, in_dtype, z, z_dtype, rows, cols, ldy, ldx, ldz, 0.0f,
                                       stream);
 }

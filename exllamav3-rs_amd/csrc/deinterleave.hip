@@ -72,7 +72,7 @@ using namespace exl3r;
 extern "C" int exl3r_deinterleave_qg(const void* qg, int64_t ld_qg, void* q, int64_t ld_q, void* g, int64_t ld_g,
                                      int dtype, int64_t rows, int heads, int head_dim, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_deinterleave_qg";
     if (!is_float_dtype(dtype)) return set_error(EXL3R_EDTYPE, "%s: unsupported dtype %s", op, dtype_name(dtype));
     if (rows < 0 || heads <= 0 || head_dim <= 0 || (int64_t)heads * head_dim > ((int64_t)1 << 28))
@@ -93,12 +93,12 @@ extern "C" int exl3r_deinterleave_qg(const void* qg, int64_t ld_qg, void* q, int
     {
         const int chunks = heads * (a.hb >> 4);
         const dim3 grid((unsigned)((chunks + 255) / 256), (unsigned)(rows < 65535 ? rows : 65535));
-        k_deinterleave_qg<<<grid, 256, 0, s>>>(a);
+        launch(k_deinterleave_qg, grid, 256, 0, s, a);
     }
     else
     {
         const int64_t n = rows * width;
-        k_deinterleave_qg_generic<<<(unsigned)((n + 255) / 256 < kMaxGridX ? (n + 255) / 256 : kMaxGridX), 256, 0, s>>>(a, es);
+        launch(k_deinterleave_qg_generic, (unsigned)((n + 255) / 256 < kMaxGridX ? (n + 255) / 256 : kMaxGridX), 256, 0, s, a, es);
     }
     return launch_status(op);
 }

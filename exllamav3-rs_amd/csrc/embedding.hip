@@ -128,7 +128,7 @@ extern "C" int exl3r_embedding(const void* table, int tt, int64_t vocab, int64_t
                                const void* ids, int idt, int64_t n, void* out, int ot, int64_t ldo,
                                int32_t* err_flag, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_embedding";
     int rc = check_gather(op, table, tt, vocab, hidden, ldt, ids, idt, n);
     if (rc) return rc;
@@ -157,14 +157,14 @@ extern "C" int exl3r_embedding(const void* table, int tt, int64_t vocab, int64_t
                 using OTy = decltype(O);
                 if constexpr (TTy::code == OTy::code || OTy::code == DT_F32)
                 {
-                    if (split) k_embedding<TTy, OTy, 4, true><<<grid, threads, 0, s>>>(a);
-                    else k_embedding<TTy, OTy, 4><<<grid, threads, 0, s>>>(a);
+                    if (split) launch(k_embedding<TTy, OTy, 4, true>, grid, threads, 0, s, a);
+                    else launch(k_embedding<TTy, OTy, 4>, grid, threads, 0, s, a);
                 }
             });
         });
     }
     else
-        k_embedding_generic<<<grid, 256, 0, s>>>(a, tt, ot);
+        launch(k_embedding_generic, grid, 256, 0, s, a, tt, ot);
     return launch_status(op);
 }
 
@@ -175,7 +175,7 @@ extern "C" int exl3r_embedding_rms_norm(const void* table, int tt, int64_t vocab
                                         float eps, float constant_bias, float constant_scale,
                                         int32_t* err_flag, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_embedding_rms_norm";
     int rc = check_gather(op, table, tt, vocab, hidden, ldt, ids, idt, n);
     if (rc) return rc;
@@ -207,7 +207,7 @@ extern "C" int exl3r_embedding_rms_norm(const void* table, int tt, int64_t vocab
     else
     {
         const unsigned grid = (unsigned)(n < kMaxGridX ? n : kMaxGridX);
-        k_rms_norm_generic<RMS_GATHER><<<grid, 256, 0, s>>>(a, tt, yt, h ? ht : tt);
+        launch(k_rms_norm_generic<RMS_GATHER>, grid, 256, 0, s, a, tt, yt, h ? ht : tt);
     }
     return launch_status(op);
 }

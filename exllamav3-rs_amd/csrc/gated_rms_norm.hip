@@ -14,7 +14,7 @@ extern "C" int exl3r_gated_rms_norm(const void* x, int xt, int64_t ldx, const vo
                                     int64_t rows, int64_t dim, float eps, float constant_bias,
                                     int gate_first, int gate_act, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_gated_rms_norm";
     int rc = check_rms_common(op, x, xt, ldx, w, wt, y, yt, ldy, rows, dim);
     if (rc) return rc;
@@ -56,7 +56,7 @@ extern "C" int exl3r_gated_rms_norm(const void* x, int xt, int64_t ldx, const vo
     else
     {
         const unsigned grid = (unsigned)(rows < kMaxGridX ? rows : kMaxGridX);
-        k_rms_norm_generic<RMS_GATED><<<grid, 256, 0, s>>>(a, xt, yt, gt);
+        launch(k_rms_norm_generic<RMS_GATED>, grid, 256, 0, s, a, xt, yt, gt);
     }
     return launch_status(op);
 }
@@ -73,7 +73,7 @@ extern "C" int exl3r_gated_rms_norm_had(const void* x, int xt, int64_t ldx, cons
                                         int64_t dim, float eps, float constant_bias, int gate_first, int gate_act,
                                         float had_scale, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_gated_rms_norm_had";
     if (dim <= 0 || dim % 128) return set_error(EXL3R_EINVAL, "%s: dim %lld must be a multiple of 128", op, (long long)dim);
     int rc = check_rms_common(op, x, xt, ldx, w, wt, out, EXL3R_F16, ldo, rows, dim);

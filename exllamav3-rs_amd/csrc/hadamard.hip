@@ -151,7 +151,7 @@ using namespace exl3r;
 extern "C" int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out, int64_t ldo, int64_t rows,
                                int64_t cols, const void* pre_scale, const void* post_scale, float scale, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_had_r_128";
     if (dtype != EXL3R_F16 && dtype != EXL3R_F32)
         return set_error(EXL3R_EDTYPE, "%s: x / out must be f16 or f32, got %s", op, dtype_name(dtype));
@@ -177,9 +177,9 @@ extern "C" int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out,
         auto go = [&](auto T, auto U) {
             using IO = decltype(T);
             constexpr int UN = decltype(U)::value;
-            if (pre_scale) k_had<IO, true, false, UN><<<(unsigned)grid, 256, 0, s>>>(a);
-            else if (post_scale) k_had<IO, false, true, UN><<<(unsigned)grid, 256, 0, s>>>(a);
-            else k_had<IO, false, false, UN><<<(unsigned)grid, 256, 0, s>>>(a);
+            if (pre_scale) launch(k_had<IO, true, false, UN>, (unsigned)grid, 256, 0, s, a);
+            else if (post_scale) launch(k_had<IO, false, true, UN>, (unsigned)grid, 256, 0, s, a);
+            else launch(k_had<IO, false, false, UN>, (unsigned)grid, 256, 0, s, a);
         };
         auto go_u = [&](auto T) {
             if (u == 4) go(T, std::integral_constant<int, 4>{});
@@ -190,6 +190,6 @@ extern "C" int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out,
         else go_u(TF32{});
     }
     else
-        k_had_generic<<<(unsigned)(blocks < kMaxGridX ? blocks : kMaxGridX), 128, 0, s>>>(a, dtype);
+        launch(k_had_generic, (unsigned)(blocks < kMaxGridX ? blocks : kMaxGridX), 128, 0, s, a, dtype);
     return launch_status(op);
 }

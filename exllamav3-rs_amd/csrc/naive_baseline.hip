@@ -3,7 +3,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "abi.hpp"
 #include "naive_baseline.h"
+
+using exl3r::launch;
 
 typedef _Float16 half_t;
 
@@ -123,42 +126,36 @@ static unsigned blocks_for(int64_t n, int threads)
 
 extern "C" int naive_add_f16(const void* x, const void* r, void* h, int64_t n, void* stream)
 {
-    k_naive_add<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const half_t*)x, (const half_t*)r, (half_t*)h, n);
-    return (int)hipGetLastError();
+    return launch(k_naive_add, blocks_for(n, 256), 256, 0, (hipStream_t)stream, (const half_t*)x, (const half_t*)r, (half_t*)h, n);
 }
 
 extern "C" int naive_rms_norm_f16(const void* x, const void* w, void* y, int64_t rows, int dim, float eps, void* stream)
 {
-    k_naive_rms<<<(unsigned)rows, 1024, 0, (hipStream_t)stream>>>((const half_t*)x, (const half_t*)w, (half_t*)y, dim, eps);
-    return (int)hipGetLastError();
+    return launch(k_naive_rms, (unsigned)rows, 1024, 0, (hipStream_t)stream, (const half_t*)x, (const half_t*)w, (half_t*)y, dim, eps);
 }
 
 extern "C" int naive_head_norm_f16(void* x, const void* w, int64_t tokens, int heads, int hd, float eps, void* stream)
 {
     int threads = 64;
     while (threads < hd) threads *= 2;
-    k_naive_head_norm<<<(unsigned)(tokens * heads), threads, 0, (hipStream_t)stream>>>((half_t*)x, (const half_t*)w, hd, eps);
-    return (int)hipGetLastError();
+    return launch(k_naive_head_norm, (unsigned)(tokens * heads), threads, 0, (hipStream_t)stream, (half_t*)x, (const half_t*)w, hd, eps);
 }
 
 extern "C" int naive_rope_neox_f16(void* x, const float* inv_freq, const int32_t* positions, int64_t tokens,
                                    int64_t seq_len, int heads, int hd, void* stream)
 {
     const int64_t n = tokens * heads * (hd / 2);
-    k_naive_rope<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((half_t*)x, inv_freq, positions, tokens, seq_len, heads, hd);
-    return (int)hipGetLastError();
+    return launch(k_naive_rope, blocks_for(n, 256), 256, 0, (hipStream_t)stream, (half_t*)x, inv_freq, positions, tokens, seq_len, heads, hd);
 }
 
 extern "C" int naive_silu_f16(const void* g, void* z, int64_t n, void* stream)
 {
-    k_naive_silu<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const half_t*)g, (half_t*)z, n);
-    return (int)hipGetLastError();
+    return launch(k_naive_silu, blocks_for(n, 256), 256, 0, (hipStream_t)stream, (const half_t*)g, (half_t*)z, n);
 }
 
 extern "C" int naive_mul_f16(const void* a, const void* b, void* z, int64_t n, void* stream)
 {
-    k_naive_mul<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>((const half_t*)a, (const half_t*)b, (half_t*)z, n);
-    return (int)hipGetLastError();
+    return launch(k_naive_mul, blocks_for(n, 256), 256, 0, (hipStream_t)stream, (const half_t*)a, (const half_t*)b, (half_t*)z, n);
 }
 
 extern "C" int calib_copy(const void* src, void* dst, int64_t nbytes, void* stream)
@@ -166,8 +163,7 @@ extern "C" int calib_copy(const void* src, void* dst, int64_t nbytes, void* stre
     if (nbytes % 16) return -1;
     const int64_t n16 = nbytes / 16;
     if (n16 > ((int64_t)1 << 37)) return -1;
-    k_calib_copy<<<(unsigned)((n16 + 127) / 128), 128, 0, (hipStream_t)stream>>>((const u32x4*)src, (u32x4*)dst, n16);
-    return (int)hipGetLastError();
+    return launch(k_calib_copy, (unsigned)((n16 + 127) / 128), 128, 0, (hipStream_t)stream, (const u32x4*)src, (u32x4*)dst, n16);
 }
 
 extern "C" int calib_copy_cached(const void* src, void* dst, int64_t nbytes, void* stream)
@@ -175,8 +171,7 @@ extern "C" int calib_copy_cached(const void* src, void* dst, int64_t nbytes, voi
     if (nbytes % 16) return -1;
     const int64_t n16 = nbytes / 16;
     if (n16 > ((int64_t)1 << 37)) return -1;
-    k_calib_copy_cached<<<(unsigned)((n16 + 127) / 128), 128, 0, (hipStream_t)stream>>>((const u32x4*)src, (u32x4*)dst, n16);
-    return (int)hipGetLastError();
+    return launch(k_calib_copy_cached, (unsigned)((n16 + 127) / 128), 128, 0, (hipStream_t)stream, (const u32x4*)src, (u32x4*)dst, n16);
 }
 
 extern "C" int naive_paged_kv_update_f16(const void* k, const void* v, void* k_cache, void* v_cache,
@@ -187,8 +182,7 @@ extern "C" int naive_paged_kv_update_f16(const void* k, const void* v, void* k_c
     if (hd % 8 || bsz <= 0 || seq_len <= 0) return -1;
     const int64_t total = bsz * seq_len * heads * (hd / 8);
     const unsigned grid = (unsigned)((total + 255) / 256 < 65535 ? (total + 255) / 256 : 65535);
-    k_naive_paged_kv<<<grid, 256, 0, (hipStream_t)stream>>>((const u32x4*)k, (const u32x4*)v, (u32x4*)k_cache,
+    return launch(k_naive_paged_kv, grid, 256, 0, (hipStream_t)stream, (const u32x4*)k, (const u32x4*)v, (u32x4*)k_cache,
                                                            (u32x4*)v_cache, block_table, cache_seqlens, seq_len, heads,
                                                            hd / 8, max_blocks, page_size, total);
-    return (int)hipGetLastError();
 }

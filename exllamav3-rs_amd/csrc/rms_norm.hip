@@ -30,7 +30,7 @@ extern "C" int exl3r_rms_norm(const void* x, int xt, int64_t ldx, const void* w,
                               void* y, int yt, int64_t ldy, int64_t rows, int64_t dim,
                               float eps, float constant_bias, float constant_scale, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     int rc = check_rms_common("exl3r_rms_norm", x, xt, ldx, w, wt, y, yt, ldy, rows, dim);
     if (rc) return rc;
     if (rows == 0) return EXL3R_OK;
@@ -51,7 +51,7 @@ extern "C" int exl3r_rms_norm(const void* x, int xt, int64_t ldx, const void* w,
     else
     {
         const unsigned grid = (unsigned)(rows < kMaxGridX ? rows : kMaxGridX);
-        k_rms_norm_generic<RMS_PLAIN><<<grid, 256, 0, s>>>(a, xt, yt, 0);
+        launch(k_rms_norm_generic<RMS_PLAIN>, grid, 256, 0, s, a, xt, yt, 0);
     }
     return launch_status("exl3r_rms_norm");
 }

@@ -18,7 +18,7 @@ extern "C" int exl3r_rms_norm_had(const void* x, int xt, int64_t ldx, const void
                                   int64_t rows, int64_t dim, float eps, float constant_bias, float constant_scale,
                                   float had_scale, int rotate_x, const void* x_post_scale, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_rms_norm_had";
     if (rotate_x && xt != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: rotate_x takes f16 x", op);
     if (!rotate_x && x_post_scale) return set_error(EXL3R_EINVAL, "%s: x_post_scale without rotate_x", op);

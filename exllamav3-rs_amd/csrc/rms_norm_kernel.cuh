@@ -473,9 +473,9 @@ void launch_rms_rows(const RmsArgs& a, hipStream_t s)
         const int rpl = (tuned == 1 || tuned == 2 || tuned == 4) ? tuned : 1;
         int64_t blocks = (a.rows + (int64_t)SLOTS * rpl - 1) / ((int64_t)SLOTS * rpl);
         if (blocks > kMaxGridX) blocks = kMaxGridX;
-        if (rpl == 4) k_rms_rows<XT, YT, RT, LPR, 4, MODE, HAD><<<(unsigned)blocks, 256, 0, s>>>(a);
-        else if (rpl == 2) k_rms_rows<XT, YT, RT, LPR, 2, MODE, HAD><<<(unsigned)blocks, 256, 0, s>>>(a);
-        else k_rms_rows<XT, YT, RT, LPR, 1, MODE, HAD><<<(unsigned)blocks, 256, 0, s>>>(a);
+        if (rpl == 4) launch(k_rms_rows<XT, YT, RT, LPR, 4, MODE, HAD>, (unsigned)blocks, 256, 0, s, a);
+        else if (rpl == 2) launch(k_rms_rows<XT, YT, RT, LPR, 2, MODE, HAD>, (unsigned)blocks, 256, 0, s, a);
+        else launch(k_rms_rows<XT, YT, RT, LPR, 1, MODE, HAD>, (unsigned)blocks, 256, 0, s, a);
     };
     if (nc <= 8) go(std::integral_constant<int, 8>{});
     else if (nc <= 16) go(std::integral_constant<int, 16>{});
@@ -634,13 +634,13 @@ void launch_rms_wm(const RmsArgs& a0, const RmsShape& sh, hipStream_t s)
         const dim3 grid((unsigned)(a0.rows - r0 < kMaxGridX ? a0.rows - r0 : kMaxGridX));
         switch (sh.maxv)
         {
-            case 1: k_rms_norm<XT, YT, RT, 1, MODE, HAD, WM, SPLIT><<<grid, sh.threads, 0, s>>>(a); break;
-            case 2: k_rms_norm<XT, YT, RT, 2, MODE, HAD, WM, SPLIT><<<grid, sh.threads, 0, s>>>(a); break;
+            case 1: launch(k_rms_norm<XT, YT, RT, 1, MODE, HAD, WM, SPLIT>, grid, sh.threads, 0, s, a); break;
+            case 2: launch(k_rms_norm<XT, YT, RT, 2, MODE, HAD, WM, SPLIT>, grid, sh.threads, 0, s, a); break;
             case 4:
-                if constexpr (!SPLIT) k_rms_norm<XT, YT, RT, 4, MODE, HAD, WM><<<grid, sh.threads, 0, s>>>(a);
+                if constexpr (!SPLIT) launch(k_rms_norm<XT, YT, RT, 4, MODE, HAD, WM>, grid, sh.threads, 0, s, a);
                 break;
             default:
-                if constexpr (!SPLIT) k_rms_norm<XT, YT, RT, 8, MODE, HAD, WM><<<grid, sh.threads, 0, s>>>(a);
+                if constexpr (!SPLIT) launch(k_rms_norm<XT, YT, RT, 8, MODE, HAD, WM>, grid, sh.threads, 0, s, a);
                 break;
         }
     }

@@ -10,7 +10,7 @@ extern "C" int exl3r_rms_norm_res_in(const void* x, int xt, int64_t ldx, const v
                                      int64_t rows, int64_t dim,
                                      float eps, float constant_bias, float constant_scale, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_rms_norm_res_in";
     int rc = check_rms_common(op, x, xt, ldx, w, wt, y, yt, ldy, rows, dim);
     if (rc) return rc;
@@ -39,7 +39,7 @@ extern "C" int exl3r_rms_norm_res_in(const void* x, int xt, int64_t ldx, const v
     else
     {
         const unsigned grid = (unsigned)(rows < kMaxGridX ? rows : kMaxGridX);
-        k_rms_norm_generic<RMS_RES_IN><<<grid, 256, 0, s>>>(a, xt, yt, rt);
+        launch(k_rms_norm_generic<RMS_RES_IN>, grid, 256, 0, s, a, xt, yt, rt);
     }
     return launch_status(op);
 }

@@ -1178,7 +1178,7 @@ static void launch_rope_nx_p(const RopeArgs& a, hipStream_t s)
     if (kFlat && wpc == 0) blocks = (runs + 3) / 4;
     if (blocks > (runs + 3) / 4) blocks = (runs + 3) / 4;
     if (blocks > kMaxGridX) blocks = kMaxGridX;
-    k_rope_nx<IO, MODE, NORM, SRC, QOUT, P, APPEND, HADR><<<(unsigned)blocks, 256, lds, s>>>(a, nslice, run);
+    launch(k_rope_nx<IO, MODE, NORM, SRC, QOUT, P, APPEND, HADR>, (unsigned)blocks, 256, lds, s, a, nslice, run);
 }
 
 // Passes per item: one for NeoX, two for GPT-J (its token's sin / cos or table row shared by two passes).
@@ -1314,17 +1314,17 @@ static void launch_rope_lph(RopeArgs a, int iters, hipStream_t s)
         {
             if (a.kc)
             {
-                k_rope<IO, MODE, LPH, 2, NORM, true, SRC><<<(unsigned)blocks, threads, lds, s>>>(a);
+                launch(k_rope<IO, MODE, LPH, 2, NORM, true, SRC>, (unsigned)blocks, threads, lds, s, a);
                 return;
             }
         }
-        k_rope<IO, MODE, LPH, 2, NORM, false, SRC><<<(unsigned)blocks, threads, lds, s>>>(a);
+        launch(k_rope<IO, MODE, LPH, 2, NORM, false, SRC>, (unsigned)blocks, threads, lds, s, a);
         return;
     }
     auto go = [&](auto I) {
         constexpr int IT = decltype(I)::value;
-        if (a.kc) k_rope<IO, MODE, LPH, IT, NORM, true, SRC_FREQ><<<(unsigned)blocks, threads, lds, s>>>(a);
-        else k_rope<IO, MODE, LPH, IT, NORM, false, SRC_FREQ><<<(unsigned)blocks, threads, lds, s>>>(a);
+        if (a.kc) launch(k_rope<IO, MODE, LPH, IT, NORM, true, SRC_FREQ>, (unsigned)blocks, threads, lds, s, a);
+        else launch(k_rope<IO, MODE, LPH, IT, NORM, false, SRC_FREQ>, (unsigned)blocks, threads, lds, s, a);
     };
     switch (iters)
     {
@@ -1357,9 +1357,9 @@ static void launch_rope_tok(RopeArgs a, hipStream_t s)
     auto go = [&](auto H) {
         constexpr int HP = decltype(H)::value;
         if constexpr (QOUT)
-            k_rope_tok<IO, MODE, LPH, HP, NORM, false, false, SRC_FREQ, true><<<(unsigned)blocks, 256, lds, s>>>(a);
-        else if (a.kc) k_rope_tok<IO, MODE, LPH, HP, NORM, true, HADR, SRC><<<(unsigned)blocks, 256, lds, s>>>(a);
-        else k_rope_tok<IO, MODE, LPH, HP, NORM, false, HADR, SRC><<<(unsigned)blocks, 256, lds, s>>>(a);
+            launch(k_rope_tok<IO, MODE, LPH, HP, NORM, false, false, SRC_FREQ, true>, (unsigned)blocks, 256, lds, s, a);
+        else if (a.kc) launch(k_rope_tok<IO, MODE, LPH, HP, NORM, true, HADR, SRC>, (unsigned)blocks, 256, lds, s, a);
+        else launch(k_rope_tok<IO, MODE, LPH, HP, NORM, false, HADR, SRC>, (unsigned)blocks, 256, lds, s, a);
     };
     if (hpl == 2) go(std::integral_constant<int, 2>{});
     else go(std::integral_constant<int, 3>{});
@@ -1558,7 +1558,7 @@ static int rope_dispatch(const char* op, const RopeArgs& a, int dtype, int rope_
     else
     {
         const size_t lds = (size_t)(a.R / 2) * sizeof(float2) + (size_t)a.hd * sizeof(float);
-        k_rope_generic<<<(unsigned)(a.tokens < kMaxGridX ? a.tokens : kMaxGridX), 256, lds, s>>>(a, dtype, rope_mode, norm);
+        launch(k_rope_generic, (unsigned)(a.tokens < kMaxGridX ? a.tokens : kMaxGridX), 256, lds, s, a, dtype, rope_mode, norm);
     }
     return launch_status(op);
 }
@@ -1576,7 +1576,7 @@ extern "C" int exl3r_rope(const void* q, void* out_q, int64_t q_tok_stride, int6
                           float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
                           void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_rope";
     RopeArgs a;
     const int rc = rope_prepare(op, a, q, out_q, q_tok_stride, q_head_stride, num_heads_q, k, out_k, false, k_tok_stride,
@@ -1665,7 +1665,7 @@ extern "C" int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_str
                                    const int32_t* cache_seqlens, int32_t* err_flag, const void* cs_table,
                                    void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_rope_paged_kv";
     RopeArgs a;
     int rc = paged_prepare(op, a, q, out_q, q_tok_stride, q_head_stride, num_heads_q, k, out_k, k_tok_stride,
@@ -1687,7 +1687,7 @@ extern "C" int exl3r_rope_table(const void* q, void* out_q, int64_t q_tok_stride
                                 float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
                                 int32_t* err_flag, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_rope_table";
     if (table_rows <= 0 || table_batch_stride < 0)
         return set_error(EXL3R_EINVAL, "%s: table_rows must be positive and table_batch_stride non-negative", op);
@@ -1720,7 +1720,7 @@ extern "C" int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, 
                               float norm_eps, float norm_constant_bias, int rope_mode, float attn_factor,
                               const void* q_post_scale, const void* k_post_scale, const void* cs_table, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_rope_had";
     if (dtype != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: the rotated projection outputs are f16", op);
     if (head_dim <= 0 || ((int64_t)num_heads_q * head_dim) % 128 || (k && ((int64_t)num_heads_k * head_dim) % 128))
@@ -1791,7 +1791,7 @@ extern "C" int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok
                                        const void* q_post_scale, const void* k_post_scale, const void* v_post_scale,
                                        const void* cs_table, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_rope_paged_kv_had";
     if (dtype != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: the rotated projection outputs are f16", op);
     if (head_dim <= 0 || ((int64_t)num_heads_q * head_dim) % 128 || ((int64_t)num_heads_kv * head_dim) % 128)
@@ -1853,7 +1853,7 @@ extern "C" int exl3r_rope_cs_table(int64_t bsz, int64_t seq_len, const float* in
                                    int32_t position, const int32_t* positions, const int32_t* position_ids,
                                    float attn_factor, void* cs_table, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_rope_cs_table";
     if (bsz < 0 || seq_len < 0 || rotary_dim < 2 || rotary_dim % 2)
         return set_error(EXL3R_EINVAL, "%s: invalid shape bsz=%lld seq_len=%lld rotary_dim=%d", op, (long long)bsz,
@@ -1869,7 +1869,7 @@ extern "C" int exl3r_rope_cs_table(int64_t bsz, int64_t seq_len, const float* in
     a.positions = positions; a.position_ids = position_ids; a.attn = attn_factor;
     const int64_t n = tokens * (rotary_dim / 2);
     const unsigned blocks = (unsigned)((n + 255) / 256 < kMaxGridX ? (n + 255) / 256 : kMaxGridX);
-    k_rope_cs_table<<<blocks, 256, 0, (hipStream_t)stream>>>(a, (float2*)cs_table);
+    launch(k_rope_cs_table, blocks, 256, 0, (hipStream_t)stream, a, (float2*)cs_table);
     return launch_status(op);
 }
 
@@ -1882,7 +1882,7 @@ extern "C" int exl3r_rope_cs(const void* q, void* out_q, int64_t q_tok_stride, i
                              const void* k_norm, int norm_dtype, float norm_eps, float norm_constant_bias,
                              int rope_mode, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_rope_cs";
     if (!cs_table && bsz > 0 && seq_len > 0) return set_error(EXL3R_EINVAL, "%s: cs_table must be non-null", op);
     // rope_prepare checks the rotation source of exl3r_rope; the table of an empty call may be NULL.
@@ -1910,7 +1910,7 @@ extern "C" int exl3r_rope_qg(const void* qg, int64_t qg_tok_stride, void* out_q,
                              const void* q_norm, const void* k_norm, int norm_dtype, float norm_eps,
                              float norm_constant_bias, int rope_mode, float attn_factor, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_rope_qg";
     if (head_dim <= 0 || head_dim > 4096)
         return set_error(EXL3R_EINVAL, "%s: head_dim %d must be in [2, 4096]", op, head_dim);
@@ -1936,12 +1936,17 @@ extern "C" int exl3r_rope_qg(const void* qg, int64_t qg_tok_stride, void* out_q,
 // its entry point, whose checks, results and errors it has.
 extern "C" int exl3r_rope_run(const exl3r_rope_desc* d, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_rope_run";
     if (!d) return set_error(EXL3R_EINVAL, "%s: descriptor must be non-null", op);
     if (d->struct_size < (int32_t)sizeof(exl3r_rope_desc))
         return set_error(EXL3R_EINVAL, "%s: struct_size %d < sizeof(exl3r_rope_desc) %d", op, d->struct_size,
                          (int)sizeof(exl3r_rope_desc));
+    // A zero-initialised descriptor leaves attn_factor 0, which would scale every {cos, sin} pair to
+    // zero and return zeroed q / k as a success: refused, 1.0 being the unscaled rotation.
+    if (d->attn_factor == 0.0f || d->attn_factor != d->attn_factor)
+        return set_error(EXL3R_EINVAL, "%s: attn_factor %g (1.0 for no scaling; a zero-initialised descriptor must set it)",
+                         op, (double)d->attn_factor);
     const int sources = (d->inv_freq != nullptr) + (d->angle_table != nullptr) + (d->cs_table != nullptr);
     const bool cs_with_freq = d->cs_table && d->inv_freq && !d->angle_table;   // rotate / k_cache forms
     if (sources == 0) return set_error(EXL3R_EINVAL, "%s: no rotation source (inv_freq, angle_table or cs_table)", op);

@@ -502,18 +502,18 @@ int sample_entry(const char* op, const void* logits, int dtype, int64_t rows, in
             using Ty = decltype(T);
             if (threads == 1024)
             {
-                if (vec) k_argmax_rows<Ty, true, GUMBEL, 1024><<<grid, 1024, 0, s>>>(a);
-                else k_argmax_rows<Ty, false, GUMBEL, 1024><<<grid, 1024, 0, s>>>(a);
+                if (vec) launch(k_argmax_rows<Ty, true, GUMBEL, 1024>, grid, 1024, 0, s, a);
+                else launch(k_argmax_rows<Ty, false, GUMBEL, 1024>, grid, 1024, 0, s, a);
             }
             else if (threads == 512)
             {
-                if (vec) k_argmax_rows<Ty, true, GUMBEL, 512><<<grid, 512, 0, s>>>(a);
-                else k_argmax_rows<Ty, false, GUMBEL, 512><<<grid, 512, 0, s>>>(a);
+                if (vec) launch(k_argmax_rows<Ty, true, GUMBEL, 512>, grid, 512, 0, s, a);
+                else launch(k_argmax_rows<Ty, false, GUMBEL, 512>, grid, 512, 0, s, a);
             }
             else
             {
-                if (vec) k_argmax_rows<Ty, true, GUMBEL, 256><<<grid, 256, 0, s>>>(a);
-                else k_argmax_rows<Ty, false, GUMBEL, 256><<<grid, 256, 0, s>>>(a);
+                if (vec) launch(k_argmax_rows<Ty, true, GUMBEL, 256>, grid, 256, 0, s, a);
+                else launch(k_argmax_rows<Ty, false, GUMBEL, 256>, grid, 256, 0, s, a);
             }
         });
         return launch_status(op);
@@ -541,33 +541,33 @@ int sample_entry(const char* op, const void* logits, int dtype, int64_t rows, in
             using Ty = decltype(T);
             if (unroll == 4)
             {
-                if (vec) k_argmax_ws<Ty, true, 4, GUMBEL><<<grid, 256, 0, s>>>(a, count, part);
-                else k_argmax_ws<Ty, false, 4, GUMBEL><<<grid, 256, 0, s>>>(a, count, part);
+                if (vec) launch(k_argmax_ws<Ty, true, 4, GUMBEL>, grid, 256, 0, s, a, count, part);
+                else launch(k_argmax_ws<Ty, false, 4, GUMBEL>, grid, 256, 0, s, a, count, part);
             }
             else
             {
-                if (vec) k_argmax_ws<Ty, true, 1, GUMBEL><<<grid, 256, 0, s>>>(a, count, part);
-                else k_argmax_ws<Ty, false, 1, GUMBEL><<<grid, 256, 0, s>>>(a, count, part);
+                if (vec) launch(k_argmax_ws<Ty, true, 1, GUMBEL>, grid, 256, 0, s, a, count, part);
+                else launch(k_argmax_ws<Ty, false, 1, GUMBEL>, grid, 256, 0, s, a, count, part);
             }
         });
         return launch_status(op);
     }
     const unsigned small = (unsigned)((rows + 255) / 256);
-    k_argmax_clear<<<small, 256, 0, s>>>(a.ids, rows);
+    launch(k_argmax_clear, small, 256, 0, s, a.ids, rows);
     with_float_type(dtype, [&](auto T) {
         using Ty = decltype(T);
         if (unroll == 4)
         {
-            if (vec) k_argmax<Ty, true, 4, GUMBEL><<<grid, 256, 0, s>>>(a);
-            else k_argmax<Ty, false, 4, GUMBEL><<<grid, 256, 0, s>>>(a);
+            if (vec) launch(k_argmax<Ty, true, 4, GUMBEL>, grid, 256, 0, s, a);
+            else launch(k_argmax<Ty, false, 4, GUMBEL>, grid, 256, 0, s, a);
         }
         else
         {
-            if (vec) k_argmax<Ty, true, 1, GUMBEL><<<grid, 256, 0, s>>>(a);
-            else k_argmax<Ty, false, 1, GUMBEL><<<grid, 256, 0, s>>>(a);
+            if (vec) launch(k_argmax<Ty, true, 1, GUMBEL>, grid, 256, 0, s, a);
+            else launch(k_argmax<Ty, false, 1, GUMBEL>, grid, 256, 0, s, a);
         }
     });
-    k_argmax_convert<<<small, 256, 0, s>>>(a.ids, rows);
+    launch(k_argmax_convert, small, 256, 0, s, a.ids, rows);
     return launch_status(op);
 }
 
@@ -576,7 +576,7 @@ int sample_entry(const char* op, const void* logits, int dtype, int64_t rows, in
 extern "C" int exl3r_argmax_sample_noalloc(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
                                            int max_logit, int64_t* ids, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_argmax_sample_noalloc";
     return sample_entry<false>(op, logits, dtype, rows, vocab, ld, max_logit, 0u, ids, stream, { nullptr, kWsBytes, true });
 }
@@ -584,7 +584,7 @@ extern "C" int exl3r_argmax_sample_noalloc(const void* logits, int dtype, int64_
 extern "C" int exl3r_argmax_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
                                    int max_logit, int64_t* ids, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     return sample_entry<false>("exl3r_argmax_sample", logits, dtype, rows, vocab, ld, max_logit, 0u, ids, stream);
 }
 
@@ -594,7 +594,7 @@ extern "C" int exl3r_argmax_sample_ws(const void* logits, int dtype, int64_t row
                                       int max_logit, int64_t* ids, void* workspace, size_t workspace_bytes,
                                       void* stream)
 {
-    clear_stale_error();
+    begin_call();
     if (!workspace) return set_error(EXL3R_EINVAL, "exl3r_argmax_sample_ws: workspace must be non-null");
     return sample_entry<false>("exl3r_argmax_sample_ws", logits, dtype, rows, vocab, ld, max_logit, 0u, ids, stream,
                                { workspace, workspace_bytes, false });
@@ -604,7 +604,7 @@ extern "C" int exl3r_gumbel_sample_ws(const void* logits, int dtype, int64_t row
                                       int max_logit, uint32_t random, int64_t* ids, void* workspace,
                                       size_t workspace_bytes, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     if (!workspace) return set_error(EXL3R_EINVAL, "exl3r_gumbel_sample_ws: workspace must be non-null");
     return sample_entry<true>("exl3r_gumbel_sample_ws", logits, dtype, rows, vocab, ld, max_logit, random, ids,
                               stream, { workspace, workspace_bytes, false });
@@ -613,14 +613,14 @@ extern "C" int exl3r_gumbel_sample_ws(const void* logits, int dtype, int64_t row
 extern "C" int exl3r_gumbel_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
                                    int max_logit, uint32_t random, int64_t* ids, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     return sample_entry<true>("exl3r_gumbel_sample", logits, dtype, rows, vocab, ld, max_logit, random, ids, stream);
 }
 
 extern "C" int exl3r_gumbel_noise(const void* x, int x_dtype, int64_t ldx, void* out, int out_dtype, int64_t ldo,
                                   int64_t rows, int64_t cols, uint32_t random, void* stream)
 {
-    clear_stale_error();
+    begin_call();
     const char* op = "exl3r_gumbel_noise";
     if (!is_float_dtype(x_dtype) || !is_float_dtype(out_dtype))
         return set_error(EXL3R_EDTYPE, "%s: unsupported dtypes x=%s out=%s", op, dtype_name(x_dtype),
@@ -638,8 +638,8 @@ extern "C" int exl3r_gumbel_noise(const void* x, int x_dtype, int64_t ldx, void*
     hipStream_t s = (hipStream_t)stream;
     with_float_type(x_dtype, [&](auto TI) {
         with_float_type(out_dtype, [&](auto TO) {
-            if (vec) k_gumbel_noise<decltype(TI), decltype(TO), true><<<grid, 256, 0, s>>>(a);
-            else k_gumbel_noise<decltype(TI), decltype(TO), false><<<grid, 256, 0, s>>>(a);
+            if (vec) launch(k_gumbel_noise<decltype(TI), decltype(TO), true>, grid, 256, 0, s, a);
+            else launch(k_gumbel_noise<decltype(TI), decltype(TO), false>, grid, 256, 0, s, a);
         });
     });
     return launch_status(op);

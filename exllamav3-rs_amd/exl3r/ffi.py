@@ -445,9 +445,11 @@ def rope_paged_kv_had(q, out_q, k, out_k, v, inv_freq, position, positions, q_no
 def rope_run(stream=None, **fields):
     """exl3r_rope_run: every RoPE variant through one descriptor (exl3r_rope_desc).  Fields by name;
     tensors pass their device pointers, None a null pointer, the rest their values; struct_size is set
-    here.  The variant and its checks follow from the fields that are set (see the header)."""
+    here.  The variant and its checks follow from the fields that are set (see the header).
+    attn_factor defaults to 1.0 (the unscaled rotation), as the Rust binding's Default does."""
     d = RopeDesc()
     d.struct_size = ctypes.sizeof(RopeDesc)
+    d.attn_factor = 1.0
     names = {f[0] for f in RopeDesc._fields_}
     first = None
     for key, val in fields.items():

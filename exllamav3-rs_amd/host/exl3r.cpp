@@ -714,15 +714,58 @@ void RmsNorm::forward_into(const Tensor& x, const Tensor& y, const Stream& s) co
 Tensor RmsNorm::forward_res(const Tensor& r, const Tensor* add, Arena& arena, const Stream& s) const
 {
     Tensor y = arena.empty(DType::F16, r.shape);
-    forward_res_into(r, add, y, s);
+    if (add && !r.is_contiguous())
+    {
+        const Tensor scratch = arena.empty(r.dtype, r.shape);
+        forward_res_into(r, add, y, s, &scratch);
+    }
+    else
+        forward_res_into(r, add, y, s);
     return y;
 }
 
-void RmsNorm::forward_res_into(const Tensor& r, const Tensor* add, const Tensor& y, const Stream& s) const
+// dst (contiguous, src's dtype and shape) = src, whose last dim is dense: one 2-D copy per index of the
+// dims before the last two.
+static void copy_to_contiguous(const Tensor& src, const Tensor& dst, const Stream& s)
+{
+    require(dst.dtype == src.dtype && dst.shape == src.shape && dst.is_contiguous(),
+            "RmsNorm::forward_res: scratch must be contiguous with the residual's dtype and shape");
+    const int nd = src.dim();
+    require(nd >= 1 && src.stride(-1) == 1, "RmsNorm::forward_res: a non-contiguous residual needs a dense last dim");
+    if (src.numel() == 0) return;
+    const size_t es = dtype_size(src.dtype);
+    const int64_t cols = src.size(-1);
+    const int64_t inner = nd >= 2 ? src.size(-2) : 1;
+    const int64_t pitch = inner > 1 ? src.stride(-2) : cols;
+    require(pitch >= cols, "RmsNorm::forward_res: residual rows overlap");
+    int64_t outer = 1;
+    for (int i = 0; i + 2 < nd; ++i) outer *= src.shape[i];
+    for (int64_t o = 0; o < outer; ++o)
+    {
+        int64_t rem = o, off = 0;
+        for (int i = nd - 3; i >= 0; --i)
+        {
+            off += (rem % src.shape[i]) * src.strides[i];
+            rem /= src.shape[i];
+        }
+        check_hip(hipMemcpy2DAsync((char*)dst.data + (size_t)(o * inner * cols) * es, (size_t)cols * es,
+                                   (const char*)src.data + (size_t)off * es, (size_t)pitch * es, (size_t)cols * es,
+                                   (size_t)inner, hipMemcpyDeviceToDevice, s.get()),
+                  "hipMemcpy2DAsync residual");
+    }
+}
+
+void RmsNorm::forward_res_into(const Tensor& r, const Tensor* add, const Tensor& y, const Stream& s,
+                               const Tensor* scratch) const
 {
     if (!add) return forward_into(r, y, s);
     require(add->shape == r.shape, "RmsNorm::forward_res: add and residual shapes differ");
-    ffi::rms_norm_res_in(*add, &weight_, y, r, eps_, constant_bias_, constant_scale_, s);
+    if (r.is_contiguous())
+        return ffi::rms_norm_res_in(*add, &weight_, y, r, eps_, constant_bias_, constant_scale_, s);
+    // src/modules.rs:393-395: forward(r + add), r unchanged.
+    require(scratch != nullptr, "RmsNorm::forward_res: a non-contiguous residual needs a scratch tensor");
+    copy_to_contiguous(r, *scratch, s);
+    ffi::rms_norm_res_in(*add, &weight_, y, *scratch, eps_, constant_bias_, constant_scale_, s);
 }
 
 Tensor Embedding::forward(const Tensor& ids, Arena& arena, const Stream& s) const

@@ -273,12 +273,14 @@ public:
     Tensor forward(const Tensor& x, Arena& arena, const Stream& s) const;
     void forward_into(const Tensor& x, const Tensor& y, const Stream& s) const;
     // Pre-norm residual add fused with the norm: r += add (in place), returns norm(r) in f16.
-    // add == nullptr: plain forward(r).  r may have any row stride (the fused path then still
-    // updates it in place); a residual whose leading dims do not collapse to one row stride is
-    // rejected, where the reference falls back to norm(r + add) and leaves r unchanged
-    // (src/modules.rs:393-395).
+    // add == nullptr: plain forward(r).  A residual that is not contiguous takes the reference's
+    // unfused path (src/modules.rs:393-395): y = norm(r + add) and r is left unchanged.  r + add is
+    // then formed in `scratch` (contiguous, r's dtype and shape; from the arena in forward_res): r is
+    // copied into it (2-D copies, no allocation) and the fused kernel updates the copy instead of r.
+    // Such a residual needs a dense last dim.
     Tensor forward_res(const Tensor& r, const Tensor* add, Arena& arena, const Stream& s) const;
-    void forward_res_into(const Tensor& r, const Tensor* add, const Tensor& y, const Stream& s) const;
+    void forward_res_into(const Tensor& r, const Tensor* add, const Tensor& y, const Stream& s,
+                          const Tensor* scratch = nullptr) const;
     const Tensor& weight() const { return weight_; }
 
 private:

@@ -11,6 +11,9 @@
  *   - returns EXL3R_OK (0) on success, a negative EXL3R_E* code for an invalid argument (nothing is
  *     launched), or a positive hipError_t when the launch itself failed;
  *   - on failure exl3r_last_error() returns a message for the calling thread;
+ *   - the status covers this call's own launches only: the thread's HIP last-error state
+ *     (hipGetLastError / hipPeekAtLastError) is neither read nor cleared, so an error another
+ *     caller left pending stays pending (a launch that fails sets it, as any failing HIP call does);
  *   - never allocates, never synchronises the host, never throws or exits;
  *   - is stateless and thread-safe; work is enqueued on `stream` only (capture-safe: the
  *     device-resident position/id buffers are read by the kernels, so a captured graph can be
@@ -383,7 +386,9 @@ EXL3R_API int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_stri
  *   otherwise          -> exl3r_rope.
  * One rotation source: inv_freq, angle_table or cs_table (rotate and k_cache accept cs_table with
  * inv_freq too, as their entry points do).  out_q_tok_stride and out_q_head_stride of 0 mean q's.
- * struct_size must be at least sizeof(exl3r_rope_desc) as this header declares it.
+ * struct_size must be at least sizeof(exl3r_rope_desc) as this header declares it.  attn_factor must be
+ * set (1.0 for the unscaled rotation): 0 or NaN, which a zero-initialised descriptor would pass, is
+ * refused with EXL3R_EINVAL.
  */
 typedef struct exl3r_rope_desc
 {

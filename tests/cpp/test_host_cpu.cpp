@@ -56,6 +56,20 @@ int main()
     Tensor g(fake, DType::BF16, { 8, 128 }), u(fake, DType::F16, { 8, 128 }), z(fake, DType::BF16, { 8, 128 });
     expect_error("act dtype mismatch", EXL3R_EINVAL, [&] { ffi::silu_mul(g, u, z, 0.f, s); });
     expect_error("RoPE odd rotary_dim", EXL3R_EINVAL, [&] { RoPE::default_inv_freq(1e6, 63); });
+    // RmsNorm::forward_res_into with a residual that is not contiguous takes the reference's unfused path
+    // through a caller's scratch: refused without one, with a scratch of another dtype, or for a residual
+    // whose last dim is not dense.
+    {
+        RmsNorm norm(w, 1e-6f);
+        Tensor rs(fake, DType::F32, { 2, 3, 64 }, { 1000, 64, 1 }), add(fake, DType::F16, { 2, 3, 64 });
+        Tensor yy(fake, DType::F16, { 2, 3, 64 }), sc16(fake, DType::F16, { 2, 3, 64 }), sc(fake, DType::F32, { 2, 3, 64 });
+        Tensor rt(fake, DType::F32, { 2, 3, 64 }, { 1000, 1, 3 });
+        expect_error("forward_res non-contiguous residual without scratch", EXL3R_EINVAL,
+                     [&] { norm.forward_res_into(rs, &add, yy, s); });
+        expect_error("forward_res scratch dtype", EXL3R_EINVAL, [&] { norm.forward_res_into(rs, &add, yy, s, &sc16); });
+        expect_error("forward_res residual last dim not dense", EXL3R_EINVAL,
+                     [&] { norm.forward_res_into(rt, &add, yy, s, &sc); });
+    }
 
     // {cos, sin} tables must cover the call's bsz * seq_len tokens (the kernels index them by token) and
     // match inv_freq's R/2; an angle table is rope()'s input only.

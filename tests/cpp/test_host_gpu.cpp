@@ -142,6 +142,31 @@ int main()
         std::snprintf(msg, sizeof msg, "y max ulp %lld, residual bit-exact %s", (long long)u, r_ok ? "yes" : "no");
         report("RmsNorm::forward_res f32 residual", u <= 1 && r_ok, msg);
     }
+    // RmsNorm::forward_res with a residual that is not contiguous (tokens 1..3 of each sequence of a
+    // [2, 5, 256] f32 buffer): the reference's unfused path, y = norm(r + add) with r unchanged
+    // (src/modules.rs:393-395), formed in a scratch tensor from the arena.
+    {
+        const int64_t B = 2, S = 5, T = 3, D = 256;
+        auto bh = host_normal(DType::F32, B * S * D, 0.f, 4.f);
+        auto ah = host_normal(DType::F16, B * T * D, 0.f, 1.f);
+        auto wh = host_normal(DType::F16, D, 1.f, 0.1f);
+        auto big = upload(bh, DType::F32, { B, S, D }, s);
+        auto add = upload(ah, DType::F16, { B, T, D }, s);
+        auto w = upload(wh, DType::F16, { D }, s);
+        const Tensor r((char*)big.t.data + D * 4, DType::F32, { B, T, D }, { S * D, D, 1 });
+        RmsNorm norm(w.t, 1e-6f);
+        auto y = norm.forward_res(r, &add.t, arena, s);
+        auto yh = download(y, s), bh2 = download(big, s);
+        std::vector<uint8_t> rc((size_t)(B * T * D) * 4), ey(yh.size());
+        for (int64_t b = 0; b < B; ++b)
+            std::memcpy(&rc[(size_t)(b * T * D) * 4], &bh[(size_t)((b * S + 1) * D) * 4], (size_t)(T * D) * 4);
+        oracle_rms_norm(ah.data(), OR_F16, D, wh.data(), OR_F16, ey.data(), OR_F16, D, rc.data(), OR_F32, D, B * T, D,
+                        1e-6f, 0.f, 1.f, 1);
+        const int64_t u = max_ulp16(yh, ey);
+        const bool r_ok = std::memcmp(bh2.data(), bh.data(), bh.size()) == 0;
+        std::snprintf(msg, sizeof msg, "y max ulp %lld, residual buffer unchanged %s", (long long)u, r_ok ? "yes" : "no");
+        report("RmsNorm::forward_res non-contiguous residual (unfused path)", u <= 1 && r_ok && y.shape == r.shape, msg);
+    }
     // Embedding::forward: bf16 table -> f32 rows (exact upcast), ids [2, 5] int64.
     {
         auto th = host_normal(DType::BF16, 100 * 64, 0.f, 0.02f);

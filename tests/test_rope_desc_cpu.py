@@ -85,6 +85,25 @@ def test_struct_size_and_null():
     assert lib.exl3r_rope_run(None, None) == _lib.EINVAL
 
 
+def test_attn_factor_default_and_zero():
+    """rope_run sets attn_factor = 1.0 unless given (the Rust binding's Default): a descriptor without it
+    reaches the selected entry point's own checks.  A raw zero-initialised descriptor (attn_factor 0)
+    or a NaN attn_factor is refused before any launch."""
+    kw = base(dtype=exl3r.F32)
+    del kw["attn_factor"]
+    with pytest.raises(exl3r.Exl3rError) as e:
+        ffi.rope_run(stream=0, **kw)
+    assert "exl3r_rope:" in str(e.value)
+    lib = exl3r.load()
+    for bad in (0.0, -0.0, float("nan")):
+        d = _lib.RopeDesc()
+        for k, v in base(attn_factor=bad).items():
+            setattr(d, k, v)
+        d.struct_size = ctypes.sizeof(d)
+        assert lib.exl3r_rope_run(ctypes.byref(d), None) == _lib.EINVAL, bad
+        assert "attn_factor" in lib.exl3r_last_error().decode(), bad
+
+
 def test_unknown_field():
     with pytest.raises(TypeError):
         ffi.rope_run(stream=0, no_such_field=1)
