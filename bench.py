@@ -8,7 +8,9 @@ A step is one pass of the config-3 prefill row ops (residual RMSNorm [8192, 5120
 the step's algorithmic bytes / step time.  The line also carries every other config's per-op
 figures (C1 Qwen3-0.6B ops, C2 decode residual norm, C4 paged q/k-norm + RoPE, C5 embedding gather
 and gather + norm), the 64-row decode-step composite fused vs the naive unfused HIP baseline, the
-roofline of the dominant kernel (SiLU-mul), and the CPU oracle timed on this host as a baseline.
+roofline of the step's dominant kernel (the slowest of the three, with each kernel's own time inside the
+step and its HBM traffic counted by rocprofv3 in the same run), and the CPU oracle timed on this host
+as a baseline.
 
   python bench.py [--steps K] [--warmup W]            full run (N = 1)
   python bench.py --op silu_c3 [--steps K]            one kernel only (for rocprofv3 --pmc runs)
@@ -19,29 +21,41 @@ timed loop rotates over enough buffer sets that a launch never finds its operand
 Infinity Cache from the previous launch.
 """
 import argparse
+import csv
+import glob
 import json
 import os
+import shutil
+import signal
 import statistics
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "exllamav3-rs_amd"))
 
 PEAK_GBS = 8000.0            # MI355X HBM3E
+# The C3 step (BASELINE configs[2]) and the kernel each of its ops launches (bf16 I/O, the shapes'
+# automatic launch choice).
+STEP_OPS = ["rms_c3", "silu_c3", "gelu_c3"]
+STEP_KERNELS = {"rms_c3": "k_rms_norm<bf16 x, bf16 y, bf16 r, RES_IN>", "silu_c3": "k_act_mul<SILU, bf16, bf16>",
+                "gelu_c3": "k_act_mul<GELU, bf16, bf16>"}
 METRIC = "fused norm/act/RoPE/embed HBM GB/s + % of MI355X peak; decode-step us"
 OPS = ["rms_c3", "rms_q3mix", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "gather_c5", "gather_f32_c5",
        "gather_norm_c5", "rms_c1",
        "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "rope_kv_prefill",
        "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
        "deinterleave_q35", "gated_norm_had_q35", "gated_norm_had_q35_unfused", "argmax_dec", "argmax_dec_torch", "argmax_dec_ws", "argmax_prefill", "argmax_prefill_torch",
-       "gumbel_dec", "gumbel_dec_torch", "gumbel_dec_ws", "gumbel_prefill", "had_c3", "norm_had_c3", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_unfused", "silu_had_c3",
-       "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_unfused", "rope_cs_c4", "rope_cs_table_c4",
+       "gumbel_dec", "gumbel_dec_torch", "gumbel_dec_ws", "gumbel_prefill", "had_c3", "had_c3_mfma", "norm_had_c3",
+       "norm_had_c3_exact", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_exact", "norm_had_rot_c3_unfused",
+       "silu_had_c3", "silu_had_c3_exact", "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_unfused", "rope_cs_c4", "rope_cs_table_c4",
        "qg_rope_q35", "qg_rope_q35_unfused",
        "rope_kv_prefill_cs", "rope_kv_had_prefill_cs", "prefill_layer_cs",
-       "rope_kv_had_prefill", "rope_kv_had_prefill_unfused", "mlp_had_c3", "mlp_had_c3_unfused",
+       "rope_kv_had_prefill", "rope_kv_had_prefill_unfused", "mlp_had_c3", "mlp_had_c3_exact", "mlp_had_c3_unfused",
        "prefill_layer", "prefill_layer_unfused", "calib_copy",
-       "calib_copy_cached"]
+       "calib_copy_cached", "c3_step"]
 
 
 def log(*a):
@@ -53,8 +67,10 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--op", choices=OPS, default=None, help="time one kernel only")
+    p.add_argument("--op", choices=OPS, default=None,
+                   help="time one kernel only (c3_step: launch the C3 step sequence, for kernel-trace runs)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter runs of the dominant kernel")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     return p.parse_args()
 
@@ -483,9 +499,10 @@ def make_gumbel(name, rows, use_torch, vocab=151936, seed=720, ws=False):
     return Work(name, nbytes, launch, f"categorical draw over f16 logits [{rows},{vocab}] ({what})", sets)
 
 
-def make_had(name, rows, cols, seed=740):
+def make_had(name, rows, cols, seed=740, mfma=False):
     """EXL3 prefill input rotation: had_r_128 of f16 [rows, cols] with an f16 suh pre-scale (the
-    projection input transform, src/modules.rs:227), out of place."""
+    projection input transform, src/modules.rs:227), out of place: the reference's butterfly
+    (exl3r_had_r_128), or with mfma the matrix-core form (exl3r_had_r_128_mfma)."""
     import torch
     import exl3r.ffi as ffi
     nbytes = 2 * rows * cols * 2 + cols * 2
@@ -495,17 +512,20 @@ def make_had(name, rows, cols, seed=740):
     suh = torch.where(torch.rand(cols, device="cuda") < 0.5, -1.0, 1.0).to(torch.float16)
 
     def launch(i):
-        ffi.had_r_128(xs[i % sets], outs[i % sets], suh)
-    return Work(name, nbytes, launch, f"random-Hadamard row transform f16 [{rows},{cols}] with suh", sets)
+        ffi.had_r_128(xs[i % sets], outs[i % sets], suh, mfma=mfma)
+    return Work(name, nbytes, launch, f"random-Hadamard row transform f16 [{rows},{cols}] with suh"
+                + (", matrix cores" if mfma else ""), sets)
 
 
-def make_norm_had(name, rows, cols, fused, seed=760, rotate=False):
+def make_norm_had(name, rows, cols, fused, seed=760, rotate=False, exact=False):
     """Qwen3-32B prefill attention input: r += x (f16 sublayer output into the f32 residual), the f16
     RMSNorm, and the q / k / v projections' input rotations had_r_128(y, suh_i)
     (src/modules.rs:224-227, 372-411): one fused launch, or the residual norm and three had_r_128
     launches.  With rotate, x is the previous projection's raw output and its own output rotation
     had_r_128(x, x, None, svh) (src/modules.rs:231) comes first (unfused: in place, one more launch).
-    Both count the fused job's bytes (x, r read and written, three outputs, w, suh, svh)."""
+    Both count the fused job's bytes (x, r read and written, three outputs, w, suh, svh).  The fused
+    launch runs its transforms on the matrix cores, or with exact as the reference's butterfly; the
+    unfused calls are the reference's (exl3r_had_r_128)."""
     import torch
     import exl3r.ffi as ffi
     n = rows * cols
@@ -522,24 +542,26 @@ def make_norm_had(name, rows, cols, fused, seed=760, rotate=False):
     def launch(i):
         x, r, outs = bufs[i % sets]
         if fused:
-            ffi.rms_norm_had(x, w, outs, suh, 1e-6, r=r, rotate_x=rotate, x_post_scale=svh)
+            ffi.rms_norm_had(x, w, outs, suh, 1e-6, r=r, rotate_x=rotate, x_post_scale=svh, exact=exact)
         else:
             if rotate:
                 ffi.had_r_128(x, x, None, svh)
             ffi.rms_norm_res_in(x, w, y, r, 1e-6)
             for o, p in zip(outs, suh):
                 ffi.had_r_128(y, o, p)
-    kind = "fused" if fused else f"unfused ({'had_r_128 in place + ' if rotate else ''}residual RMSNorm + 3 had_r_128)"
+    kind = ("fused, butterfly" if exact else "fused") if fused else \
+        f"unfused ({'had_r_128 in place + ' if rotate else ''}residual RMSNorm + 3 had_r_128)"
     head = "had(svh) -> residual RMSNorm" if rotate else "residual RMSNorm"
     return Work(name, nbytes, launch, f"{head} -> 3 Hadamard inputs [{rows},{cols}] f16/f32r, {kind}", sets)
 
 
-def make_act_had(name, rows, cols, fused, seed=780, rotate=False):
+def make_act_had(name, rows, cols, fused, seed=780, rotate=False, exact=False):
     """MLP prefill tail: silu(gate) * up in f16 and the down projection's input rotation
     had_r_128(a, suh) (src/modules.rs:932-940, 224-227): one fused launch, or exl3r_silu_mul and
     exl3r_had_r_128.  With rotate, gate and up are the raw gate_proj / up_proj outputs and their own
     output rotations (src/modules.rs:231) come first (unfused: two in-place rotations).  Both count the
-    fused job's bytes (gate, up, the rotated output, suh, and svh of gate and up)."""
+    fused job's bytes (gate, up, the rotated output, suh, and svh of gate and up).  The fused launch runs
+    its transforms on the matrix cores, or with exact as the reference's butterfly."""
     import torch
     import exl3r.ffi as ffi
     nbytes = rows * cols * 6 + (3 if rotate else 1) * cols * 2
@@ -553,16 +575,18 @@ def make_act_had(name, rows, cols, fused, seed=780, rotate=False):
         g, u, out = bufs[i % sets]
         if fused:
             if rotate:
-                ffi.act_mul_had("silu", g, u, out, suh, rotate_x=True, rotate_y=True, x_post_scale=sg, y_post_scale=su)
+                ffi.act_mul_had("silu", g, u, out, suh, rotate_x=True, rotate_y=True, x_post_scale=sg, y_post_scale=su,
+                                exact=exact)
             else:
-                ffi.act_mul_had("silu", g, u, out, suh)
+                ffi.act_mul_had("silu", g, u, out, suh, exact=exact)
         else:
             if rotate:
                 ffi.had_r_128(g, g, None, sg)
                 ffi.had_r_128(u, u, None, su)
             ffi.silu_mul(g, u, a)
             ffi.had_r_128(a, out, suh)
-    kind = "fused" if fused else ("unfused (2 in-place rotations + silu_mul + had_r_128)" if rotate else
+    kind = ("fused, butterfly" if exact else "fused") if fused else \
+        ("unfused (2 in-place rotations + silu_mul + had_r_128)" if rotate else
                                   "unfused (silu_mul + had_r_128)")
     head = "rotated gate, up -> " if rotate else ""
     return Work(name, nbytes, launch, f"{head}SiLU(gate)*up -> Hadamard input [{rows},{cols}] f16, {kind}", sets)
@@ -780,9 +804,13 @@ def make_all(only=None):
         "gumbel_dec_torch": lambda: make_gumbel("gumbel_dec_torch", 64, True),
         "gumbel_prefill": lambda: make_gumbel("gumbel_prefill", 1024, False),
         "had_c3": lambda: make_had("had_c3", 8192, 5120),
+        "had_c3_mfma": lambda: make_had("had_c3_mfma", 8192, 5120, mfma=True),
         "norm_had_c3": lambda: make_norm_had("norm_had_c3", 8192, 5120, True),
+        "norm_had_c3_exact": lambda: make_norm_had("norm_had_c3_exact", 8192, 5120, True, exact=True),
         "norm_had_c3_unfused": lambda: make_norm_had("norm_had_c3_unfused", 8192, 5120, False),
         "norm_had_rot_c3": lambda: make_norm_had("norm_had_rot_c3", 8192, 5120, True, rotate=True),
+        "norm_had_rot_c3_exact": lambda: make_norm_had("norm_had_rot_c3_exact", 8192, 5120, True, rotate=True,
+                                                       exact=True),
         "norm_had_rot_c3_unfused": lambda: make_norm_had("norm_had_rot_c3_unfused", 8192, 5120, False, rotate=True),
         "rope_kv_had_prefill": lambda: make_rope_kv("rope_kv_had_prefill", 1, 4096, True, had=True),
         "rope_kv_had_prefill_unfused": lambda: make_rope_kv("rope_kv_had_prefill_unfused", 1, 4096, False, had=True),
@@ -791,13 +819,16 @@ def make_all(only=None):
         "prefill_layer": lambda: make_prefill_layer("prefill_layer", True),
         "prefill_layer_unfused": lambda: make_prefill_layer("prefill_layer_unfused", False),
         "mlp_had_c3": lambda: make_act_had("mlp_had_c3", 8192, 17408, True, rotate=True),
+        "mlp_had_c3_exact": lambda: make_act_had("mlp_had_c3_exact", 8192, 17408, True, rotate=True, exact=True),
         "mlp_had_c3_unfused": lambda: make_act_had("mlp_had_c3_unfused", 8192, 17408, False, rotate=True),
         "silu_had_c3": lambda: make_act_had("silu_had_c3", 8192, 17408, True),
+        "silu_had_c3_exact": lambda: make_act_had("silu_had_c3_exact", 8192, 17408, True, exact=True),
         "silu_had_c3_unfused": lambda: make_act_had("silu_had_c3_unfused", 8192, 17408, False),
         "calib_copy": lambda: make_copy("calib_copy"),
         "calib_copy_cached": lambda: make_copy("calib_copy_cached", cached=True),
     }
-    names = [only] if only else [n for n in OPS if n not in ("rms_c2", "calib_copy_cached")]
+    names = ([only] if isinstance(only, str) else list(only)) if only else \
+        [n for n in OPS if n not in ("rms_c2", "calib_copy_cached", "c3_step")]
     return {n: builders[n]() for n in names}
 
 
@@ -1019,6 +1050,84 @@ def decode_eager_compiled(timeout=120):
     return res
 
 
+def pmc_kib(op, counter, timeout=120):
+    """Median KiB per dispatch of a rocprofv3 counter for each of this library's kernels in
+    `bench.py --op OP` (a child process under rocprofv3 --pmc, one counter per run), or None when the
+    profiler is missing or the run fails."""
+    exe = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(exe):
+        return None
+    with tempfile.TemporaryDirectory(dir="/tmp") as d:
+        cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "run", "--", sys.executable,
+               os.path.abspath(__file__), "--op", op, "--steps", "5", "--warmup", "1"]
+        p = subprocess.Popen(cmd, cwd="/tmp", stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                             env={**os.environ, "TMPDIR": "/tmp"}, start_new_session=True)
+        try:
+            rc = p.wait(timeout=timeout)
+        except subprocess.TimeoutExpired:
+            os.killpg(p.pid, signal.SIGKILL)
+            p.wait()
+            return None
+        files = glob.glob(os.path.join(d, "**", "run_counter_collection.csv"), recursive=True)
+        if rc != 0 and not files:
+            return None
+        vals = {}
+        for f in files:
+            for r in csv.DictReader(open(f)):
+                k = r.get("Kernel_Name", "")
+                if "exl3r::" in k or "k_calib" in k:
+                    vals.setdefault(k, []).append(float(r["Counter_Value"]))
+        return {k: statistics.median(v) for k, v in vals.items()} or None
+
+
+def trace_step(steps, warmup, timeout=150):
+    """Each C3 step kernel's mean duration (us) inside the step sequence: a rocprofv3 --kernel-trace run of
+    `bench.py --op c3_step` (the three launches back to back, as in the timed step), the warmup launches
+    dropped.  None when the profiler is missing or the run fails."""
+    exe = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(exe):
+        return None
+    with tempfile.TemporaryDirectory(dir="/tmp") as d:
+        cmd = [exe, "--kernel-trace", "--output-format", "csv", "-d", d, "-o", "run", "--", sys.executable,
+               os.path.abspath(__file__), "--op", "c3_step", "--steps", str(steps), "--warmup", str(warmup)]
+        p = subprocess.Popen(cmd, cwd="/tmp", stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                             env={**os.environ, "TMPDIR": "/tmp"}, start_new_session=True)
+        try:
+            p.wait(timeout=timeout)
+        except subprocess.TimeoutExpired:
+            os.killpg(p.pid, signal.SIGKILL)
+            p.wait()
+            return None
+        files = glob.glob(os.path.join(d, "**", "run_kernel_trace.csv"), recursive=True)
+        durs = {n: [] for n in STEP_OPS}
+        for f in files:
+            rows = sorted(csv.DictReader(open(f)), key=lambda r: int(r["Start_Timestamp"]))
+            for r in rows:
+                k = r.get("Kernel_Name", "")
+                n = "rms_c3" if "k_rms_norm" in k else "silu_c3" if "k_act_mul<0," in k else \
+                    "gelu_c3" if "k_act_mul<1," in k else None
+                if n:
+                    durs[n].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        out = {n: statistics.mean(v[warmup:]) for n, v in durs.items() if len(v) > warmup}
+        return out or None
+
+
+def live_traffic(op):
+    """HBM bytes per launch of op's main kernel counted in this run: FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch, one rocprofv3 --pmc run each), scaled by what the same counters read for a plain copy of
+    1 GiB read + 1 GiB write (calib_copy).  Returns (bytes, kernel name, detail) or None."""
+    cf, cw = pmc_kib("calib_copy", "FETCH_SIZE"), pmc_kib("calib_copy", "WRITE_SIZE")
+    f, w = pmc_kib(op, "FETCH_SIZE"), pmc_kib(op, "WRITE_SIZE")
+    if not (cf and cw and f and w):
+        return None
+    fs = (1 << 30) / (max(cf.values()) * 1024)
+    ws = (1 << 30) / (max(cw.values()) * 1024)
+    per = {k: f[k] * 1024 * fs + w.get(k, 0.0) * 1024 * ws for k in f}
+    k = max(per, key=per.get)
+    return int(per[k]), k, {"fetch_kib": round(f[k], 1), "write_kib": round(w.get(k, 0.0), 1),
+                            "fetch_scale": round(fs, 4), "write_scale": round(ws, 4)}
+
+
 def traffic_from_profiles(op):
     """HBM bytes per launch of the op's main kernel from the committed rocprofv3 --pmc summary, or None
     (an op with a second, small kernel -- the {cos, sin} table -- has a line for each: the larger is kept)."""
@@ -1054,6 +1163,15 @@ def main():
     torch.cuda.set_device(0)
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
+        if args.op == "c3_step":
+            # the timed step's launch sequence on its own (rocprofv3 kernel-trace runs)
+            ws = make_all(STEP_OPS)
+            for i in range(args.warmup + args.steps):
+                for n in STEP_OPS:
+                    ws[n].launch(i)
+            torch.cuda.synchronize()
+            log(f"c3_step: {args.warmup + args.steps} steps launched")
+            return
         if args.op:
             work = make_all(args.op)[args.op] if args.op != "rms_c2" else None
             if work is None:
@@ -1078,15 +1196,17 @@ def main():
             ops[name] = {"desc": w.desc, "us": round(ms * 1000, 3), "us_min": round(windows[0] * 1000, 3),
                          "bytes": w.nbytes, "gbs": round(gbs, 1), "frac_peak": round(gbs / PEAK_GBS, 4)}
             if w.hbm_bytes is not None:
-                # repeats are cache hits: the HBM fraction is over the counted traffic (a row read by
-                # workgroups on several XCDs is fetched into each XCD's L2), else over the distinct rows'
-                # bytes; the all-rows rate stays beside it as gbs
-                counted = traffic_from_profiles(name)
-                hb = counted if counted else w.hbm_bytes
-                hbm_gbs = hb / (ms * 1e-3) / 1e9
-                ops[name].update({"hbm_bytes": hb, "hbm_bytes_source": "rocprofv3 FETCH/WRITE" if counted else
-                                  "distinct rows (lower bound)", "hbm_bytes_min": w.hbm_bytes,
+                # repeats are cache hits: the HBM fraction is over the least traffic that serves the launch
+                # (each distinct row read once, computed from this run's ids); the all-rows rate stays beside
+                # it as gbs, and the committed rocprofv3 FETCH/WRITE count (a row read by workgroups on
+                # several XCDs is fetched into each XCD's L2) beside that, with its source
+                hbm_gbs = w.hbm_bytes / (ms * 1e-3) / 1e9
+                ops[name].update({"hbm_bytes": w.hbm_bytes, "hbm_bytes_source": "distinct rows (lower bound)",
                                   "hbm_gbs": round(hbm_gbs, 1), "frac_peak": round(hbm_gbs / PEAK_GBS, 4)})
+                counted = traffic_from_profiles(name)
+                if counted:
+                    ops[name].update({"hbm_bytes_profiled": counted,
+                                      "hbm_bytes_profiled_source": "profiles/pmc_traffic.txt (committed counters)"})
                 gbs = hbm_gbs
             extra = ""
             if name.endswith("_c1") or name.startswith("rope_kv_dec") or name.startswith("argmax_dec") or \
@@ -1175,8 +1295,9 @@ def main():
                               "32/4 heads of 128: rope_qg with the gate read in place vs deinterleave + rope + gate"}
         log(f"gated_attention: {json.dumps(gated_attn)}")
 
-        # The timed step: config-3 prefill row ops back to back.
-        step_works = [works["rms_c3"], works["silu_c3"], works["gelu_c3"]]
+        # The timed step: config-3 prefill row ops back to back (no event between the kernels: an event
+        # record between two launches costs the next one a cache flush).
+        step_works = [works[n] for n in STEP_OPS]
         step_bytes = sum(w.nbytes for w in step_works)
         for i in range(args.warmup):
             for w in step_works:
@@ -1192,10 +1313,42 @@ def main():
         ms_step = s.elapsed_time(e) / args.steps
 
     value = step_bytes / (ms_step * 1e-3) / 1e9
-    dom = ops["silu_c3"]
-    roof = {"bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_GBS, "unit": "GB/s",
-            "frac": round(dom["gbs"] / PEAK_GBS, 4), "traffic": traffic_from_profiles("silu_c3"),
-            "kernel": "k_act_mul<SILU, bf16, bf16> (silu_c3)", "bytes_per_launch": dom["bytes"]}
+    # Each step kernel: its HIP-event time over back-to-back launches of it alone (ops above), and its
+    # duration inside the step sequence from a rocprofv3 kernel trace of that sequence in this run.  The
+    # roofline is quoted on the step's dominant kernel, the one that takes the most time in the step.
+    in_step = None if args.no_traffic else trace_step(args.steps, args.warmup)
+    kernels = {}
+    for n in STEP_OPS:
+        v = ops[n]
+        kernels[n] = {"kernel": STEP_KERNELS[n], "bytes": v["bytes"], "us": v["us"], "gbs": v["gbs"],
+                      "frac": v["frac_peak"]}
+        if in_step and n in in_step:
+            us = in_step[n]
+            kernels[n].update({"us_in_step": round(us, 3), "frac_in_step": round(v["bytes"] / (us * 1e-6) / 1e9 / PEAK_GBS, 4)})
+    by = "us_in_step" if in_step and all(n in in_step for n in STEP_OPS) else "us"
+    dom_name = max(kernels, key=lambda n: kernels[n][by])
+    dom = kernels[dom_name]
+    log("C3 step kernels: " + ", ".join(
+        f"{n} {v['us']:.2f} us alone" + (f", {v['us_in_step']:.2f} us in the step" if "us_in_step" in v else "")
+        for n, v in kernels.items()))
+    roof = {"bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_GBS, "unit": "GB/s", "frac": dom["frac"],
+            "traffic": None, "kernel": f"{dom['kernel']} ({dom_name})", "bytes_per_launch": dom["bytes"],
+            "timing": "HIP events on the launch stream over back-to-back launches of the kernel (us); its "
+                      "duration inside the step sequence from a rocprofv3 kernel trace in this run (us_in_step); "
+                      "the dominant kernel is the slowest " + ("in the step" if by == "us_in_step" else "alone"),
+            "kernels": kernels}
+    if not args.no_traffic:
+        t0 = time.time()
+        lt = live_traffic(dom_name)
+        if lt:
+            roof["traffic"] = lt[0]
+            roof["traffic_source"] = ("rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on bench.py --op " + dom_name +
+                                      " in this run, scaled by the same counters on a 1 GiB copy")
+            roof["traffic_detail"] = {"kernel": lt[1], **lt[2],
+                                      "traffic_over_algorithmic": round(lt[0] / dom["bytes"], 4)}
+        else:
+            roof["traffic_source"] = "counter runs unavailable in this run"
+        log(f"traffic of {dom_name}: {roof['traffic']} bytes ({time.time() - t0:.0f} s of counter runs)")
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(args.cpu_seconds)

@@ -84,6 +84,14 @@ extern "C" void exl3r_tune_rms_split(int split, int wmode)
     exl3r::tuning().rms_split_wm = wmode;
 }
 
+extern "C" void exl3r_tune_rms_mode(int sum32, int wmode, int r_cached, int pipe)
+{
+    exl3r::tuning().rms_sum32 = sum32;
+    exl3r::tuning().rms_wmode = wmode;
+    exl3r::tuning().rms_r_cached = r_cached;
+    exl3r::tuning().rms_pipe = pipe;
+}
+
 extern "C" void exl3r_tune_act(int unroll, int threads, int blocks_per_cu)
 {
     exl3r::tuning().act_unroll = unroll;
@@ -109,6 +117,13 @@ extern "C" void exl3r_tune_sample(int rows_min, int threads)
 }
 
 extern "C" void exl3r_tune_had(int blocks_per_group) { exl3r::tuning().had_unroll = blocks_per_group; }
+
+extern "C" void exl3r_tune_had_mfma(int unroll, int blocks_per_cu, int cached)
+{
+    exl3r::tuning().had_mfma_unroll = unroll;
+    exl3r::tuning().had_mfma_per_cu = blocks_per_cu;
+    exl3r::tuning().had_mfma_cached = cached;
+}
 
 extern "C" void exl3r_tune_embed(int threads) { exl3r::tuning().embed_threads = threads; }
 #endif  // EXL3R_TUNING

@@ -72,6 +72,11 @@ struct Tuning
     int rms_maxv = 0, rms_threads = 0;
     int rms_rows_rpl = 0;
     int rms_split = 0, rms_split_wm = 1;   // split chunks: -1 never, 0 auto, 1 always; weight mode (1 mid, 2 late)
+    int rms_sum32 = 0;                     // plain / residual norms: 1 = fp32 row sum (0: fp64)
+    int rms_wmode = 0;                     // streaming plain / residual norms: weight fetched 1 early, 2 mid, 3 late (0 auto)
+    int rms_r_cached = 0;                  // Hadamard norms: 1 = cached residual stores
+    int rms_pipe = 0;                      // streaming plain / residual norms: 1 = resident grid, as many
+                                           // workgroups per CU as fit; n > 1: n - 1 per CU
     int act_unroll = 0, act_threads = 0, act_blocks_per_cu = 0;
     int rope_iters = 0;
     int rope_tok = 0;       // 0 auto, 1 never the wave-per-token kernel, 2 always (where it applies)
@@ -82,6 +87,9 @@ struct Tuning
     int sample_rows_min = 0; // argmax / Gumbel: rows from which a workgroup owns a row (0: 512)
     int sample_threads = 0;  // ... and its lanes (256, 512, 1024; 0: 256)
     int had_unroll = 0;      // Hadamard: 128-blocks per 16-lane group (1, 2, 4; 0: 1)
+    int had_mfma_unroll = 0; // matrix-core Hadamard kernels: spans per wave in flight (1, 2, 4; 0: 2)
+    int had_mfma_per_cu = 0; // ... workgroups per CU of the looping grid (0: 8; < 0: one span group per wave, no cap)
+    int had_mfma_cached = 0; // ... 1: cached input loads instead of non-temporal ones
     int embed_threads = 0;
 };
 #ifdef EXL3R_TUNING

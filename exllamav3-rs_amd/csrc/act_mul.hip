@@ -62,6 +62,51 @@ __device__ __forceinline__ float act_mul1(float g, float u, float limit)
     return a * u;
 }
 
+// act_chunk with one wave-uniform test: when no lane's chunk has an element in act_f's tail (|t| > 64,
+// |x| > 44 for SiLU), every element takes act_f_short -- the operations act_f performs there, without
+// the tail's selects -- else act_f.  The results are act_chunk's in both cases.  The whole wave must
+// reach it.
+template <int ACT, class OT, bool LIMIT>
+__device__ __forceinline__ void act_chunk_wave(const float (&g)[8], const float (&u)[8], float limit, float (&o)[8])
+{
+    float t[8];
+    bool tail = false;
+    #pragma unroll
+    for (int j = 0; j < 8; ++j)
+    {
+        t[j] = act_t<ACT>(g[j]);
+        tail |= !(fabsf(t[j]) <= 64.0f);
+    }
+    if (__builtin_amdgcn_ballot_w64(tail) == 0)
+    {
+        #pragma unroll
+        for (int j = 0; j < 8; ++j)
+        {
+            float a = act_f_short<ACT>(g[j], t[j]);
+            float v = u[j];
+            if constexpr (LIMIT)
+            {
+                if (v < -limit) v = -limit;
+                if (v > limit) v = limit;
+                if (a > limit) a = limit;
+            }
+            float p = a * v;
+            if constexpr (OT::code == DT_F16) p = clamp_f16(p);
+            o[j] = p;
+        }
+    }
+    else
+    {
+        #pragma unroll
+        for (int j = 0; j < 8; ++j)
+        {
+            float p = act_mul1<ACT, LIMIT>(g[j], u[j], limit);
+            if constexpr (OT::code == DT_F16) p = clamp_f16(p);
+            o[j] = p;
+        }
+    }
+}
+
 template <int ACT, class OT, bool LIMIT>
 __device__ __forceinline__ void act_chunk(const float (&g)[8], const float (&u)[8], float limit, float (&o)[8])
 {
@@ -230,6 +275,112 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
     }
 }
 
+// The activation -> Hadamard kernels with the transforms on the matrix cores (had128_mfma, hadamard.cuh).
+// A wave takes spans of 64 chunks (4 blocks) of a row, lane l holding chunk mfma_chunk(l) of its span;
+// the spans of the whole tensor (rows * spans_per_row, counted in 32 bits) are dealt to the waves of
+// the grid in turn, UNROLL spans per wave in flight.  Loop bounds are wave-uniform, so every MFMA runs
+// with the whole wave; lanes past a row's last block carry zeros and store nothing.  Same rounding
+// points as the butterfly kernel (hadamard.cuh documents how the transform's sums may differ).
+template <int ACT, class IT, int HAD, bool LIMIT, int UNROLL, bool CACHED = false>
+__global__ __launch_bounds__(256) void k_act_mul_had_mfma(ActArgs a)
+{
+    static_assert((HAD & AH_OUT) != 0, "the input rotations come with the output rotation");
+    const int lane = threadIdx.x & 63;
+    const uint32_t cpr = (uint32_t)(a.cols >> 3);
+    const uint32_t spr = (cpr + 63) >> 6;
+    const uint32_t nspans = (uint32_t)a.rows * spr;
+    // wave-uniform span and row indices (scalar registers: the row bases are scalar, the lane offsets
+    // 32-bit)
+    const uint32_t wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const uint32_t nwaves = (gridDim.x * blockDim.x) >> 6;
+    const HadMfma H = had_mfma_operands(lane);
+    const uint32_t lc = (uint32_t)mfma_chunk(lane);
+    for (uint32_t s0 = wave * UNROLL; s0 < nspans; s0 += nwaves * UNROLL)
+    {
+        typename IT::Vec xv[UNROLL], yv[UNROLL];
+        uint32_t row[UNROLL], c[UNROLL];
+        bool live[UNROLL];
+        #pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+        {
+            const uint32_t sp = s0 + u;
+            row[u] = sp / spr;
+            c[u] = (sp - row[u] * spr) * 64 + lc;
+            live[u] = sp < nspans && c[u] < cpr;
+            if (live[u])
+            {
+                if constexpr (CACHED)
+                {
+                    xv[u] = load8<IT>((const char*)a.x + (int64_t)row[u] * a.ldx * IT::bytes, (int64_t)c[u] * 8);
+                    yv[u] = load8<IT>((const char*)a.y + (int64_t)row[u] * a.ldy * IT::bytes, (int64_t)c[u] * 8);
+                }
+                else
+                {
+                    xv[u] = load8s<IT>((const char*)a.x + (int64_t)row[u] * a.ldx * IT::bytes, (int64_t)c[u] * 8);
+                    yv[u] = load8s<IT>((const char*)a.y + (int64_t)row[u] * a.ldy * IT::bytes, (int64_t)c[u] * 8);
+                }
+            }
+            else
+            {
+                const float zf[8] = {};
+                xv[u] = pack8<IT>(zf);
+                yv[u] = pack8<IT>(zf);
+            }
+        }
+        if constexpr ((HAD & (AH_IN_X | AH_IN_Y)) != 0)
+        {
+            // the input rotations of every span in flight, their MFMAs issued together
+            static_assert(IT::code == DT_F16, "input rotations take f16 x and y");
+            constexpr int NX = (HAD & AH_IN_X) != 0 ? UNROLL : 0, NY = (HAD & AH_IN_Y) != 0 ? UNROLL : 0;
+            TF16::Vec v[NX + NY];
+            const void* post[NX + NY];
+            int64_t col[NX + NY];
+            #pragma unroll
+            for (int u = 0; u < UNROLL; ++u)
+            {
+                if constexpr (NX) { v[u] = xv[u]; post[u] = live[u] ? a.xpost : nullptr; col[u] = (int64_t)c[u] * 8; }
+                if constexpr (NY) { v[NX + u] = yv[u]; post[NX + u] = live[u] ? a.ypost : nullptr; col[NX + u] = (int64_t)c[u] * 8; }
+            }
+            output_rotations_mfma<NX + NY>(H, v, post, col, lane);
+            #pragma unroll
+            for (int u = 0; u < UNROLL; ++u)
+            {
+                if constexpr (NX) xv[u] = v[u];
+                if constexpr (NY) yv[u] = v[NX + u];
+            }
+        }
+        MfmaOut m[UNROLL];
+        #pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+        {
+            float g[8], v[8], o[8];
+            unpack8<IT>(xv[u], g);
+            unpack8<IT>(yv[u], v);
+            act_chunk_wave<ACT, TF16, LIMIT>(g, v, a.limit, o);
+            TF16::Vec hv = pack8<TF16>(o);
+            if (live[u])
+            {
+                if (a.z) store8<TF16>((char*)a.z + (int64_t)row[u] * a.ldz * 2, (int64_t)c[u] * 8, hv);
+                if (a.hpre)
+                {
+                    const TF16::Vec p = load8<TF16>(a.hpre, (int64_t)c[u] * 8);
+                    #pragma unroll
+                    for (int q = 0; q < 4; ++q) hv.a[q] = hmul2(hv.a[q], p.a[q]);
+                }
+            }
+            m[u] = had128_mfma_issue(H, hv);
+        }
+        mfma_wait_all(m);
+        #pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+        {
+            float f[8];
+            had128_mfma_finish(m[u], f, lane, a.hr);
+            if (live[u]) store8<TF16>((char*)a.hout + (int64_t)row[u] * a.ldh * 2, (int64_t)c[u] * 8, pack8<TF16>(f));
+        }
+    }
+}
+
 // Short strided rows (at most 64 chunks, e.g. the gate of one 128-wide head read in place from an
 // interleaved q | g projection): (row, chunk) items flattened over the whole grid, so a workgroup
 // covers several rows instead of idling most of its lanes on one.  UNROLL items per thread in flight.
@@ -345,6 +496,43 @@ static void launch_act_vec(const ActArgs& a, hipStream_t s)
     }
 }
 
+// Grid of the matrix-core kernel: one wave per UNROLL spans, no cap (kHadMfmaBlocksPerCu <= 0).  MI355X,
+// [8192, 17408] f16, median of interleaved runs (us): SiLU -> input rotation 140.1 with UNROLL 2 and no
+// cap, 153.7 UNROLL 1; a looping grid of 8 workgroups per CU 160.1, 16 per CU 153.3, 4 per CU 178.4;
+// cached instead of non-temporal input loads 146.9.  With both input rotations: 187.1 / 205.5 / 207.8 /
+// 194.4 / 246.6 / 198.8.
+constexpr int kHadMfmaBlocksPerCu = -1;
+
+template <int ACT, class IT, int HAD, int UNROLL, bool CACHED>
+static void launch_act_had_mfma_u(const ActArgs& a, int per_cu, hipStream_t s)
+{
+    const int64_t spans = a.rows * ((a.cols / 8 + 63) / 64);
+    int64_t blocks = (spans + 4 * UNROLL - 1) / (4 * UNROLL);
+    if (per_cu > 0 && blocks > (int64_t)per_cu * device_cus()) blocks = (int64_t)per_cu * device_cus();
+    if (blocks > kMaxGridX) blocks = kMaxGridX;
+    if (a.limit != 0.0f) launch(k_act_mul_had_mfma<ACT, IT, HAD, true, UNROLL, CACHED>, (unsigned)blocks, 256, 0, s, a);
+    else launch(k_act_mul_had_mfma<ACT, IT, HAD, false, UNROLL, CACHED>, (unsigned)blocks, 256, 0, s, a);
+}
+
+template <int ACT, class IT, int HAD>
+static void launch_act_had_mfma(const ActArgs& a, hipStream_t s)
+{
+#ifdef EXL3R_TUNING
+    const Tuning& tu = tuning();
+    const int per_cu = tu.had_mfma_per_cu != 0 ? tu.had_mfma_per_cu : kHadMfmaBlocksPerCu;   // <= 0: no cap
+    const bool cached = tu.had_mfma_cached != 0;
+    auto go = [&](auto C) {
+        if (tu.had_mfma_unroll == 1) launch_act_had_mfma_u<ACT, IT, HAD, 1, decltype(C)::value>(a, per_cu, s);
+        else if (tu.had_mfma_unroll == 4) launch_act_had_mfma_u<ACT, IT, HAD, 4, decltype(C)::value>(a, per_cu, s);
+        else launch_act_had_mfma_u<ACT, IT, HAD, 2, decltype(C)::value>(a, per_cu, s);
+    };
+    if (cached) go(std::true_type{});
+    else go(std::false_type{});
+#else
+    launch_act_had_mfma_u<ACT, IT, HAD, 2, false>(a, kHadMfmaBlocksPerCu, s);
+#endif
+}
+
 extern "C" int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out, int64_t ldo, int64_t rows,
                                int64_t cols, const void* pre_scale, const void* post_scale, float scale, void* stream);
 
@@ -363,7 +551,9 @@ static int act_had_entry(const char* op, const void* x, const void* y, int it, i
 {
     begin_call();
     if (!is_float_dtype(it)) return set_error(EXL3R_EDTYPE, "%s: unsupported input dtype %s", op, dtype_name(it));
-    if (rotate_in & ~3) return set_error(EXL3R_EINVAL, "%s: rotate_in takes bits 0 (x) and 1 (y)", op);
+    const bool exact = (rotate_in & EXL3R_HAD_EXACT) != 0;
+    rotate_in &= ~EXL3R_HAD_EXACT;
+    if (rotate_in & ~3) return set_error(EXL3R_EINVAL, "%s: rotate_in takes bits 0 (x) and 1 (y) and EXL3R_HAD_EXACT", op);
     if (rotate_in && it != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: rotated inputs are f16", op);
     if ((x_post && !(rotate_in & 1)) || (y_post && !(rotate_in & 2)))
         return set_error(EXL3R_EINVAL, "%s: a post-scale without its input rotation", op);
@@ -381,6 +571,18 @@ static int act_had_entry(const char* op, const void* x, const void* y, int it, i
     const bool vec = aligned16(x) && aligned16(y) && aligned16(out) && (!z || aligned16(z)) && (!pre || aligned16(pre)) &&
                      (!x_post || aligned16(x_post)) && (!y_post || aligned16(y_post)) &&
                      (lx * eb) % 16 == 0 && (ly * eb) % 16 == 0 && (lo * 2) % 16 == 0 && (lz * 2) % 16 == 0;
+    // The matrix-core transforms unless the caller asks for the reference's butterfly; spans are counted
+    // in 32 bits.
+    const bool mfma = !exact && rows * ((cols / 8 + 63) / 64) < ((int64_t)1 << 31);
+    if (vec && mfma)
+    {
+        ActArgs a{ x, y, z, lx, ly, lz, rows, cols, limit, pre, out, lo, had_scale * 0.0883883461356163f, x_post, y_post };
+        if (rotate_in == 3) launch_act_had_mfma<ACT, TF16, AH_OUT | AH_IN_X | AH_IN_Y>(a, s);
+        else if (rotate_in == 1) launch_act_had_mfma<ACT, TF16, AH_OUT | AH_IN_X>(a, s);
+        else if (rotate_in == 2) launch_act_had_mfma<ACT, TF16, AH_OUT | AH_IN_Y>(a, s);
+        else with_float_type(it, [&](auto I) { launch_act_had_mfma<ACT, decltype(I), AH_OUT>(a, s); });
+        return launch_status(op);
+    }
     if (vec)
     {
         ActArgs a{ x, y, z, lx, ly, lz, rows, cols, limit, pre, out, lo, had_scale * 0.0883883461356163f, x_post, y_post };
@@ -494,7 +696,9 @@ extern "C" int exl3r_act_mul_had(int act, const void* x, const void* y, int in_d
         {
             if (act_limit != 0.0f) return set_error(EXL3R_EINVAL, "%s: act_limit applies to silu / gelu only", op);
             // The kernels take the gate first: x and y, their rotations and post-scales swap.
-            const int swapped = rotate_in & ~3 ? rotate_in : ((rotate_in & 1) << 1) | ((rotate_in >> 1) & 1);
+            const int bits = rotate_in & ~EXL3R_HAD_EXACT;
+            const int swapped = bits & ~3 ? rotate_in
+                                          : (((bits & 1) << 1) | ((bits >> 1) & 1) | (rotate_in & EXL3R_HAD_EXACT));
             return act_had_entry<ACT_SIGMOID>(op, y, x, in_dtype, ldy, ldx, z, ldz, pre_scale, out, ldo, rows, cols,
                                               0.0f, had_scale, swapped, y_post_scale, x_post_scale, stream);
         }

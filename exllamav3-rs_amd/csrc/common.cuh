@@ -156,6 +156,24 @@ template <> __device__ __forceinline__ void store8<TF32>(void* base, int64_t e, 
     __builtin_nontemporal_store(v.b, p + 1);
 }
 
+// Cached stores (no non-temporal hint): the L2 keeps the line, so the halves of a 128-byte line that two
+// store instructions write are merged there before the line goes to HBM.
+template <class T> __device__ __forceinline__ void store8c(void* base, int64_t elem, const typename T::Vec& v);
+template <> __device__ __forceinline__ void store8c<TF16>(void* base, int64_t e, const TF16::Vec& v)
+{
+    *(u32x4*)((uint16_t*)base + e) = v.a;
+}
+template <> __device__ __forceinline__ void store8c<TBF16>(void* base, int64_t e, const TBF16::Vec& v)
+{
+    *(u32x4*)((uint16_t*)base + e) = v.a;
+}
+template <> __device__ __forceinline__ void store8c<TF32>(void* base, int64_t e, const TF32::Vec& v)
+{
+    u32x4* p = (u32x4*)((float*)base + e);
+    p[0] = v.a;
+    p[1] = v.b;
+}
+
 // Split chunks: the 8 elements of a chunk are the quads at e and e + kSplitGap, each one 8-byte (16-bit
 // data) or 16-byte (f32) access.  With lane l of a wave taking the quads at 4 l and 256 + 4 l of a
 // 512-element span, each wave-wide access of an operand covers one contiguous range: 512 B, or 1 KB for
@@ -320,10 +338,15 @@ __device__ __forceinline__ void load8_dyn(const void* base, int dt, int64_t e, f
 
 // Reciprocal RMS factor from an fp64 sum of squares: the sum is rounded once to fp32, then
 // mean = sum / n, and 1 / sqrt(mean + eps) with IEEE-correct fp32 sqrt and division (hipcc's
-// default), so the CPU oracle reproduces it bit-for-bit.
+// default), so the CPU oracle reproduces it bit-for-bit.  (An fp32 sum enters the same way.)
 __device__ __forceinline__ float rms_factor(double sum, int n, float eps)
 {
     const float mean = (float)sum / (float)n;
+    return 1.0f / sqrtf(mean + eps);
+}
+__device__ __forceinline__ float rms_factor(float sum, int n, float eps)
+{
+    const float mean = sum / (float)n;
     return 1.0f / sqrtf(mean + eps);
 }
 
@@ -340,12 +363,28 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kGeluK1 = (float)(-2.0 * 0.79788456080286535588 * 1.4426950408889634074);
 constexpr float kGeluK2 = (float)(-2.0 * 0.79788456080286535588 * 0.044715 * 1.4426950408889634074);
 
+// t with e^-z = 2^t.
+template <int ACT>
+__device__ __forceinline__ float act_t(float x)
+{
+    if constexpr (ACT == ACT_GELU) return x * fmaf(kGeluK2, x * x, kGeluK1);
+    else return x * -kLog2e;
+}
+
+// act_f for a t with |t| <= 64 (no tail scaling): the same operations and results as act_f there.
+template <int ACT>
+__device__ __forceinline__ float act_f_short(float x, float t)
+{
+    const float p = __builtin_amdgcn_exp2f(-fabsf(t));
+    const float q = __builtin_amdgcn_rcpf(1.0f + p);
+    const float s = t <= 0.0f ? q : p * q;
+    return ACT == ACT_SIGMOID ? s : x * s;
+}
+
 template <int ACT>
 __device__ __forceinline__ float act_f(float x)
 {
-    float t;   // e^-z = 2^t
-    if constexpr (ACT == ACT_GELU) t = x * fmaf(kGeluK2, x * x, kGeluK1);
-    else t = x * -kLog2e;
+    const float t = act_t<ACT>(x);   // e^-z = 2^t
     const float n = -fabsf(t);
     const bool tail = n < -64.0f;
     const float p = __builtin_amdgcn_exp2f(tail ? n + 64.0f : n);   // normal for n >= -190
@@ -462,6 +501,20 @@ __device__ __forceinline__ double block_sum64_once(double v, double* lds16)
     if ((threadIdx.x & 63) == 0) lds16[threadIdx.x >> 6] = v;
     __syncthreads();
     double t = 0.0;
+    for (int i = 0; i < nw; ++i) t += lds16[i];
+    return t;
+}
+
+// Workgroup sum with a single barrier (see block_sum64_once), for an fp64 or fp32 partial.
+__device__ __forceinline__ double block_sum_once(double v, double* lds16) { return block_sum64_once(v, lds16); }
+__device__ __forceinline__ float block_sum_once(float v, float* lds16)
+{
+    v = group_sum<64>(v);
+    const int nw = blockDim.x >> 6;
+    if (nw == 1) return v;
+    if ((threadIdx.x & 63) == 0) lds16[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.0f;
     for (int i = 0; i < nw; ++i) t += lds16[i];
     return t;
 }

@@ -201,4 +201,159 @@ __device__ __forceinline__ void output_rotation8(TF16::Vec& v, const void* post,
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// The 128-point transform on the matrix cores.  H128 is the tensor product of the 2-point transforms
+// over the 7 index bits, which can be applied in any grouping: bits {0, 1, 2, 5, 6} are contracted by
+// v_mfma_f32_16x16x32_f16 against +-1 f16 operands (the f16 products are exact; the 32-term sums are
+// fp32), bits {3, 4} by two carried-sign DPP stages inside each lane quad.  Per 4 blocks (512
+// elements) that is 2 MFMAs and 16 DPP fmas per lane, against 24 in-lane and 32 cross-lane
+// operations per lane for the butterfly.  The sums are grouped differently from the reference's
+// butterfly (kernels/quant/hadamard_inner.cuh:19-46, 127-141), so the fp32 results can differ from it
+// by rounding: each is within about 2^-20 * sum|x| of the exact transform, and after the rounding to
+// f16 a result equals the butterfly's or is its f16 neighbour, except where the transform cancels to
+// below ~2^-17 * r * sum|x| (there both are that close to the exact value).  Zero results are +0.
+//
+// Lane placement: a wave holds 4 consecutive blocks of one row (64 chunks of 8 elements).  Lane
+// l = 16 g + j (j = l & 15, g = l >> 4) holds chunk mfma_chunk(l) = (l & 3) + 4 g + 16 (j >> 2) of the
+// span: elements 8 (l & 3) + 32 g + 0..7 of block j >> 2.  Each lane quad reads 64 contiguous bytes of
+// 16-bit data and a wave-wide access covers the span's 1 KB.  As MFMA operands, B[k][j] is the data of
+// segment j (block j >> 2, index bits 3-4 = j & 3) at k = (index bits 5-6 = g, bits 0-2 = slot), and
+// the result rows come back to the lanes that loaded them: D lane l, slot v of MFMA h is index bits
+// 0-2 = 4 h + v and bits 5-6 = g, so after the two MFMAs every lane holds its own 8 positions.
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// Chunk of a 64-chunk span held by lane l (swaps lane bits 2-3 with bits 4-5; its own inverse).
+__device__ __forceinline__ int mfma_chunk(int lane) { return (lane & 3) | ((lane >> 2) & 12) | ((lane << 2) & 48); }
+
+// The lane's A operands of the two MFMAs: A_h[i][k] = (-1)^(popcount(go & gk) + popcount((4h + v) & e))
+// for row i = 4 go + v (i = lane & 15) and k = 8 gk + e (gk = lane >> 4, slot e).
+struct HadMfma
+{
+    f16x8 a[2];
+};
+
+__device__ __forceinline__ HadMfma had_mfma_operands(int lane)
+{
+    const int go = (lane & 15) >> 2, v = lane & 3, gk = lane >> 4;
+    const int pg = __builtin_popcount(go & gk);
+    HadMfma H;
+    #pragma unroll
+    for (int h = 0; h < 2; ++h)
+    {
+        #pragma unroll
+        for (int e = 0; e < 8; ++e)
+            H.a[h][e] = ((pg + __builtin_popcount((4 * h + v) & e)) & 1) ? (_Float16)-1.0f : (_Float16)1.0f;
+    }
+    return H;
+}
+
+// The transform in three steps, so that a caller can issue the MFMAs of several blocks before reading
+// any result:
+//   had128_mfma_issue: the two MFMAs of the lane's f16 chunk v (must be reached by the whole wave: the
+//     MFMA reads every lane; lanes past the data pass zeros and drop the result);
+//   mfma_wait: the wait states a VALU read of an MFMA result needs (a 16x16x32 f16 MFMA is 4 passes,
+//     under 12 wait states; 16 here), taking the results of the batch as operands so that none of their
+//     MFMAs is issued after it; the DPP stages below are inline asm, which the compiler's hazard
+//     handling does not see into;
+//   had128_mfma_finish: the two carried-sign stages and the scale: f = r * H128 of the block, fp32,
+//     before the rounding to the output type.
+struct MfmaOut
+{
+    f32x4 d0, d1;
+};
+
+__device__ __forceinline__ MfmaOut had128_mfma_issue(const HadMfma& H, const TF16::Vec& v)
+{
+    const f16x8 b = __builtin_bit_cast(f16x8, v.a);
+    const f32x4 zero = { 0.0f, 0.0f, 0.0f, 0.0f };
+    return { __builtin_amdgcn_mfma_f32_16x16x32_f16(H.a[0], b, zero, 0, 0, 0),
+             __builtin_amdgcn_mfma_f32_16x16x32_f16(H.a[1], b, zero, 0, 0, 0) };
+}
+
+__device__ __forceinline__ void mfma_wait(MfmaOut& a)
+{
+    asm volatile("s_nop 7\ns_nop 7" : "+v"(a.d0), "+v"(a.d1));
+}
+__device__ __forceinline__ void mfma_wait(MfmaOut& a, MfmaOut& b)
+{
+    asm volatile("s_nop 7\ns_nop 7" : "+v"(a.d0), "+v"(a.d1), "+v"(b.d0), "+v"(b.d1));
+}
+__device__ __forceinline__ void mfma_wait(MfmaOut& a, MfmaOut& b, MfmaOut& c, MfmaOut& d)
+{
+    asm volatile("s_nop 7\ns_nop 7" : "+v"(a.d0), "+v"(a.d1), "+v"(b.d0), "+v"(b.d1), "+v"(c.d0), "+v"(c.d1), "+v"(d.d0),
+                 "+v"(d.d1));
+}
+
+__device__ __forceinline__ void had128_mfma_finish(const MfmaOut& m, float (&f)[8], int lane, float r)
+{
+    #pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        f[i] = m.d0[i];
+        f[4 + i] = m.d1[i];
+    }
+    lane_stage_carried<1>(f, lane);
+    lane_stage_carried<2>(f, lane);
+    // The two carried stages leave (-1)^popcount(lane & 3) times the transform; the scale undoes it.
+    const float sr = (__builtin_popcount(lane & 3) & 1) ? -r : r;
+    #pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = opaque(__builtin_fmaf(f[j], sr, 0.0f));
+}
+
+// f = r * H128 of the lane's f16 chunk v, one block on its own (issue, wait, finish).
+__device__ __forceinline__ void had128_mfma(const HadMfma& H, const TF16::Vec& v, float (&f)[8], int lane, float r)
+{
+    MfmaOut m = had128_mfma_issue(H, v);
+    mfma_wait(m);
+    had128_mfma_finish(m, f, lane, r);
+}
+
+// The f16 post-scale product of an output rotation's chunk (none when post is null).
+__device__ __forceinline__ void post_scale8(TF16::Vec& v, const void* post, int64_t col)
+{
+    if (post)
+    {
+        const TF16::Vec p = load8<TF16>(post, col);
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) v.a[q] = hmul2(v.a[q], p.a[q]);
+    }
+}
+
+// A batch of N (1, 2, 4, 8) transforms' results through one wait.
+template <int N>
+__device__ __forceinline__ void mfma_wait_all(MfmaOut (&m)[N])
+{
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8, "batches of 1, 2, 4 or 8");
+    if constexpr (N == 1) mfma_wait(m[0]);
+    else if constexpr (N == 2) mfma_wait(m[0], m[1]);
+    else if constexpr (N == 4) mfma_wait(m[0], m[1], m[2], m[3]);
+    else
+    {
+        mfma_wait(m[0], m[1], m[2], m[3]);
+        mfma_wait(m[4], m[5], m[6], m[7]);
+    }
+}
+
+// The EXL3 linear's output rotation had_r_128(y, y, None, post) (scale 1) of N f16 chunks at columns
+// col[n] (mfma_chunk placement), their MFMAs issued together: each transform, one rounding to f16, then
+// the half post-scale (post[n] null: none).
+template <int N>
+__device__ __forceinline__ void output_rotations_mfma(const HadMfma& H, TF16::Vec* v, const void* const* post,
+                                                      const int64_t* col, int lane)
+{
+    MfmaOut m[N];
+    #pragma unroll
+    for (int n = 0; n < N; ++n) m[n] = had128_mfma_issue(H, v[n]);
+    mfma_wait_all(m);
+    #pragma unroll
+    for (int n = 0; n < N; ++n)
+    {
+        float f[8];
+        had128_mfma_finish(m[n], f, lane, 0.0883883461356163f);
+        v[n] = pack8<TF16>(f);
+        post_scale8(v[n], post[n], col[n]);
+    }
+}
+
 }  // namespace exl3r

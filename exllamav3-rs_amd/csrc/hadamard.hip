@@ -107,6 +107,73 @@ __global__ __launch_bounds__(256) void k_had(HadArgs a)
         if (blk0 + u < nblk) had_block<IO, PRE, POST>(a, blk0 + u, l16, v[u]);
 }
 
+// The same transform on the matrix cores (had128_mfma, hadamard.cuh), f16 only.  A wave takes spans of
+// 4 blocks of a row, lane l holding chunk mfma_chunk(l) of its span; the spans of the tensor (rows *
+// spans_per_row, counted in 32 bits) are dealt to the waves in turn, UN per wave in flight.  Loop
+// bounds are wave-uniform (every MFMA runs with the whole wave); lanes past a row's last block carry
+// zeros and store nothing.  A span's loads all complete before its MFMAs, so out may equal x.
+template <bool PRE, bool POST, int UN>
+__global__ __launch_bounds__(256) void k_had_mfma(HadArgs a)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t cpr = (uint32_t)(a.nb * 16);
+    const uint32_t spr = (uint32_t)((a.nb + 3) / 4);
+    const uint32_t nspans = (uint32_t)a.rows * spr;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    const uint32_t nwaves = (gridDim.x * blockDim.x) >> 6;
+    const HadMfma H = had_mfma_operands(lane);
+    const uint32_t lc = (uint32_t)mfma_chunk(lane);
+    for (uint32_t s0 = wave * UN; s0 < nspans; s0 += nwaves * UN)
+    {
+        TF16::Vec v[UN];
+        uint32_t row[UN], c[UN];
+        bool live[UN];
+        #pragma unroll
+        for (int u = 0; u < UN; ++u)
+        {
+            const uint32_t sp = s0 + u;
+            row[u] = sp / spr;
+            c[u] = (sp - row[u] * spr) * 64 + lc;
+            live[u] = sp < nspans && c[u] < cpr;
+            if (live[u]) v[u] = load8s<TF16>(a.x + (int64_t)row[u] * a.ldx, (int64_t)c[u] * 8);
+            else v[u].a = u32x4{ 0u, 0u, 0u, 0u };
+        }
+        MfmaOut m[UN];
+        #pragma unroll
+        for (int u = 0; u < UN; ++u)
+        {
+            if constexpr (PRE)
+            {
+                if (live[u])
+                {
+                    const TF16::Vec p = load8<TF16>(a.pre, (int64_t)c[u] * 8);
+                    #pragma unroll
+                    for (int i = 0; i < 4; ++i) v[u].a[i] = hmul2(v[u].a[i], p.a[i]);
+                }
+            }
+            m[u] = had128_mfma_issue(H, v[u]);
+        }
+        mfma_wait_all(m);
+        #pragma unroll
+        for (int u = 0; u < UN; ++u)
+        {
+            float f[8];
+            had128_mfma_finish(m[u], f, lane, a.r);
+            TF16::Vec o = pack8<TF16>(f);
+            if (live[u])
+            {
+                if constexpr (POST)
+                {
+                    const TF16::Vec p = load8<TF16>(a.post, (int64_t)c[u] * 8);
+                    #pragma unroll
+                    for (int i = 0; i < 4; ++i) o.a[i] = hmul2(o.a[i], p.a[i]);
+                }
+                store8<TF16>(a.out + (int64_t)row[u] * a.ldo, (int64_t)c[u] * 8, o);
+            }
+        }
+    }
+}
+
 // Any alignment: a 128-lane workgroup per block, the same butterfly through LDS.
 __global__ __launch_bounds__(128) void k_had_generic(HadArgs a, int dt)
 {
@@ -191,5 +258,43 @@ extern "C" int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out,
     }
     else
         launch(k_had_generic, (unsigned)(blocks < kMaxGridX ? blocks : kMaxGridX), 128, 0, s, a, dtype);
+    return launch_status(op);
+}
+
+// exl3r_had_r_128 with the transform on the matrix cores (f16; the kernel the fused Hadamard entry
+// points use unless EXL3R_HAD_EXACT).  Rows that are not 16-byte aligned take exl3r_had_r_128's
+// butterfly, which is within the same tolerance.
+extern "C" int exl3r_had_r_128_mfma(const void* x, int dtype, int64_t ldx, void* out, int64_t ldo, int64_t rows,
+                                    int64_t cols, const void* pre_scale, const void* post_scale, float scale,
+                                    void* stream)
+{
+    begin_call();
+    const char* op = "exl3r_had_r_128_mfma";
+    if (dtype != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: x / out must be f16, got %s", op, dtype_name(dtype));
+    if (rows < 0 || cols < 0 || cols % 128 || (rows > 1 && (ldx < cols || ldo < cols)))
+        return set_error(EXL3R_EINVAL, "%s: invalid shape rows=%lld cols=%lld (a multiple of 128) ldx=%lld ldo=%lld", op,
+                         (long long)rows, (long long)cols, (long long)ldx, (long long)ldo);
+    if (pre_scale && post_scale)
+        return set_error(EXL3R_EINVAL, "%s: give at most one of pre_scale / post_scale", op);
+    if (rows == 0 || cols == 0) return EXL3R_OK;
+    if (!x || !out) return set_error(EXL3R_EINVAL, "%s: x and out must be non-null", op);
+    const int64_t lx = (rows > 1 ? ldx : cols) * 2, lo = (rows > 1 ? ldo : cols) * 2;
+    const void* sc = pre_scale ? pre_scale : post_scale;
+    const int64_t spans = rows * ((cols / 128 + 3) / 4);
+    const bool vec = aligned16(x) && aligned16(out) && lx % 16 == 0 && lo % 16 == 0 && (!sc || aligned16(sc));
+    if (!vec || spans >= ((int64_t)1 << 31))
+        return exl3r_had_r_128(x, dtype, ldx, out, ldo, rows, cols, pre_scale, post_scale, scale, stream);
+    HadArgs a{ (const char*)x, (char*)out, lx, lo, rows, cols / 128, (const uint16_t*)pre_scale,
+               (const uint16_t*)post_scale, scale * 0.0883883461356163f };
+    hipStream_t s = (hipStream_t)stream;
+    constexpr int UN = 2;
+    // one wave per UN spans (the grid does not loop; see the act -> Hadamard kernels' launch shape)
+    const int per_cu = tuning().had_mfma_per_cu;
+    int64_t blocks = (spans + 4 * UN - 1) / (4 * UN);
+    if (per_cu > 0 && blocks > (int64_t)per_cu * device_cus()) blocks = (int64_t)per_cu * device_cus();
+    if (blocks > kMaxGridX) blocks = kMaxGridX;
+    if (pre_scale) launch(k_had_mfma<true, false, UN>, (unsigned)blocks, 256, 0, s, a);
+    else if (post_scale) launch(k_had_mfma<false, true, UN>, (unsigned)blocks, 256, 0, s, a);
+    else launch(k_had_mfma<false, false, UN>, (unsigned)blocks, 256, 0, s, a);
     return launch_status(op);
 }

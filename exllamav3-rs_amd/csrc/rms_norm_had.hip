@@ -3,7 +3,8 @@
 // RmsNorm::forward / forward_res (src/modules.rs:372-411) followed by each consumer's
 // had_r_128(y, suh) (src/modules.rs:224-227; kernels/quant/hadamard.cu:88-170).  With rotate_x, x
 // is first given the producing projection's own output rotation had_r_128(x, x, None, svh)
-// (src/modules.rs:231).  Bit-identical to those calls made one after another.
+// (src/modules.rs:231).  The transforms run on the matrix cores (had128_mfma), or with EXL3R_HAD_EXACT in
+// rotate_x as the reference's butterfly, bit-identical to those calls made one after another.
 #include "rms_norm_kernel.cuh"
 #include "rms_norm_launch.hpp"
 
@@ -20,6 +21,9 @@ extern "C" int exl3r_rms_norm_had(const void* x, int xt, int64_t ldx, const void
 {
     begin_call();
     const char* op = "exl3r_rms_norm_had";
+    const bool exact = (rotate_x & EXL3R_HAD_EXACT) != 0;
+    rotate_x &= ~EXL3R_HAD_EXACT;
+    if (rotate_x & ~1) return set_error(EXL3R_EINVAL, "%s: rotate_x takes 0 or 1 (and EXL3R_HAD_EXACT)", op);
     if (rotate_x && xt != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: rotate_x takes f16 x", op);
     if (!rotate_x && x_post_scale) return set_error(EXL3R_EINVAL, "%s: x_post_scale without rotate_x", op);
     if (!is_float_dtype(xt) || (w && !is_float_dtype(wt)) || (r && !is_float_dtype(rt)))
@@ -49,6 +53,9 @@ extern "C" int exl3r_rms_norm_had(const void* x, int xt, int64_t ldx, const void
     a.rows = rows; a.dim = (int)dim; a.eps = eps; a.cb = constant_bias; a.cs = constant_scale;
     a.nh = n_out; a.ldh = rows > 1 ? ldo : dim; a.hr = had_scale * 0.0883883461356163f;
     a.hxpost = x_post_scale;
+#ifdef EXL3R_TUNING
+    a.r_cached = tuning().rms_r_cached;
+#endif
     bool aligned = (a.ldh * 2) % 16 == 0;
     for (int i = 0; i < n_out; ++i)
     {
@@ -60,16 +67,21 @@ extern "C" int exl3r_rms_norm_had(const void* x, int xt, int64_t ldx, const void
     hipStream_t s = (hipStream_t)stream;
     if (aligned && rms_vec_ok(a, xt, EXL3R_F16, r ? rt : EXL3R_F16, r != nullptr, r ? RMS_RES_IN : RMS_PLAIN, HAD_OUT))
     {
-        if (rotate_x)
-        {
-            if (!r) launch_rms_vec<TF16, TF16, TNone, RMS_PLAIN, HAD_IN | HAD_OUT>(a, s);
-            else with_float_type(rt, [&](auto R) { launch_rms_vec<TF16, TF16, decltype(R), RMS_RES_IN, HAD_IN | HAD_OUT>(a, s); });
-        }
-        else
-            with_float_type(xt, [&](auto X) {
-                if (!r) launch_rms_vec<decltype(X), TF16, TNone, RMS_PLAIN, HAD_OUT>(a, s);
-                else with_float_type(rt, [&](auto R) { launch_rms_vec<decltype(X), TF16, decltype(R), RMS_RES_IN, HAD_OUT>(a, s); });
-            });
+        auto go = [&](auto M) {
+            constexpr int F = decltype(M)::value;   // HAD_MFMA or 0 (the butterfly)
+            if (rotate_x)
+            {
+                if (!r) launch_rms_vec<TF16, TF16, TNone, RMS_PLAIN, HAD_IN | HAD_OUT | F>(a, s);
+                else with_float_type(rt, [&](auto R) { launch_rms_vec<TF16, TF16, decltype(R), RMS_RES_IN, HAD_IN | HAD_OUT | F>(a, s); });
+            }
+            else
+                with_float_type(xt, [&](auto X) {
+                    if (!r) launch_rms_vec<decltype(X), TF16, TNone, RMS_PLAIN, HAD_OUT | F>(a, s);
+                    else with_float_type(rt, [&](auto R) { launch_rms_vec<decltype(X), TF16, decltype(R), RMS_RES_IN, HAD_OUT | F>(a, s); });
+                });
+        };
+        if (exact) go(std::integral_constant<int, 0>{});
+        else go(std::integral_constant<int, HAD_MFMA>{});
         return launch_status(op);
     }
     // Unaligned rows: the calls one after another.  A rotated x goes to the first output, the norm

@@ -61,11 +61,30 @@ struct RmsArgs
     // HAD_IN kernels: f16 x is first replaced by had_r_128(x) * hxpost (the EXL3 linear's output
     // rotation with its f16 post-scale, or none when null).
     const void* hxpost;
+    // Hadamard kernels: the updated residual is written with cached stores (1) instead of non-temporal ones.
+    int r_cached;
 };
 
 // Hadamard flags of the norm kernels (exl3r_rms_norm_had).
 constexpr int HAD_OUT = 1;   // rotated f16 outputs, one per projection
 constexpr int HAD_IN = 2;    // x rotated on load
+constexpr int HAD_MFMA = 4;  // the transforms on the matrix cores (had128_mfma)
+
+// The matrix-core transforms need chunk mfma_chunk(l) of a wave's 64-chunk span in lane l, while the
+// row's loads and stores keep chunk l in lane l (with the permuted placement the norm kernels' f32
+// residual and three outputs fetched 1.15x and wrote 1.20x their bytes, against 1.01x and 1.00x with
+// the lane-ordered one: a line's halves come from different rows of a store).  A chunk moves between
+// the two placements through the lane crossbar (ds_bpermute, no LDS storage; the permutation is its own
+// inverse).  Thread counts are multiples of 64, so a wave's chunks c = tid + k * nt are one span of 4
+// blocks for every k.
+__device__ __forceinline__ TF16::Vec mfma_permute(const TF16::Vec& v, int lane)
+{
+    const int src = mfma_chunk(lane) << 2;
+    TF16::Vec o;
+    #pragma unroll
+    for (int q = 0; q < 4; ++q) o.a[q] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)v.a[q]);
+    return o;
+}
 
 // When a row's weight chunks are fetched (a launch-shape choice: the results are the same bits).
 //   W_EARLY: with the row's HBM loads, so the L2 fetch overlaps them (latency-bound launches);
@@ -135,7 +154,7 @@ struct RowRegs
 
 // Issues every HBM load of one row -- x (and r) in chunks c = tid, tid + nt, ... (at most MAXV per
 // lane), plus the weight chunks when load_w -- before any arithmetic.
-template <class XT, class RT, int MAXV, int MODE, bool SPLIT = false>
+template <class XT, class RT, int MAXV, int MODE, bool SPLIT = false, int HAD = 0>
 __device__ __forceinline__ void rms_load(const RmsArgs& a, int64_t row, int tid, int nt, bool load_w,
                                          RowRegs<XT, RT, MAXV>& L)
 {
@@ -161,9 +180,23 @@ __device__ __forceinline__ void rms_load(const RmsArgs& a, int64_t row, int tid,
     {
         const int c = tid + k * nt;
         const int64_t e = chunk_elem<SPLIT>(c);
+        if constexpr ((HAD & HAD_MFMA) != 0)
+        {
+            // the transforms read every lane: zeros past the row (one select per word, so that the
+            // chunk stays in registers)
+            static_assert(MODE != RMS_GATHER, "gathered rows take the butterfly");
+            const typename XT::Vec z = load8s<XT>(xrow, c < nc ? e : 0);
+            #pragma unroll
+            for (int q = 0; q < 4; ++q) L.xv[k].a[q] = c < nc ? z.a[q] : 0u;
+            if constexpr (XT::code == DT_F32)
+            {
+                #pragma unroll
+                for (int q = 0; q < 4; ++q) L.xv[k].b[q] = c < nc ? z.b[q] : 0u;
+            }
+        }
         if (c < nc)
         {
-            if (L.valid)
+            if ((HAD & HAD_MFMA) == 0 && L.valid)
             {
                 if constexpr (SPLIT) L.xv[k] = load8s_split<XT>(xrow, e);
                 else if constexpr (MODE == RMS_GATHER) L.xv[k] = load8<XT>(xrow, e);   // hot table rows
@@ -193,11 +226,14 @@ constexpr bool kDeferResidual = MODE == RMS_RES_IN;
 // Pass 1 of the 8-element chunk at element e of a row: clamp (f16 x), residual update (RES_IN),
 // gathered-row copy (GATHER), gate before the norm (GATED), and the chunk's squares added to ss
 // (fp64: squares and sums of 16-bit data are exact).  Returns the chunk's cached form.
-template <class XT, class RT, int MODE, int HAD = 0>
+template <class XT, class RT, int MODE, int HAD = 0, bool SPLIT = false, class ACC = double>
 __device__ __forceinline__ typename RmsCache<XT, RT, MODE>::Vec rms_chunk1(const RmsArgs& a, char* rrow, int64_t e,
                                                                           bool valid, typename XT::Vec& xv,
-                                                                          const typename RT::Vec& rv, double& ss)
+                                                                          const typename RT::Vec& rv, ACC& ss)
 {
+    // A pass-1 residual store is contiguous: split chunks (two quads 256 apart) must defer it to pass 2,
+    // where the split store is used.
+    static_assert(!SPLIT || kDeferResidual<MODE, RT> || MODE != RMS_RES_IN, "split chunks store the residual in pass 2");
     using CT = RmsCache<XT, RT, MODE>;
     typename CT::Vec cv;
     float h[8];
@@ -255,16 +291,16 @@ __device__ __forceinline__ typename RmsCache<XT, RT, MODE>::Vec rms_chunk1(const
         }
     }
     #pragma unroll
-    for (int j = 0; j < 8; ++j) ss = fma((double)h[j], (double)h[j], ss);
+    for (int j = 0; j < 8; ++j) ss = fma((ACC)h[j], (ACC)h[j], ss);
     return cv;
 }
 
 // Pass 2 of the chunk at element e: gate (GATED), weight (row offset wofs), scale, gate after the
-// norm (GATED), one rounding, store.
-template <class XT, class YT, class RT, int MODE, int HAD, bool SPLIT = false>
-__device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* yrow, int64_t e, int64_t wofs,
-                                           const typename RmsCache<XT, RT, MODE>::Vec& cv,
-                                           const typename RT::Vec& rv, u32x4 wv, float rmf)
+// norm (GATED), one rounding: the chunk of y.
+template <class XT, class YT, class RT, int MODE, bool SPLIT = false>
+__device__ __forceinline__ typename YT::Vec rms_out8(const RmsArgs& a, int64_t e, int64_t wofs,
+                                                     const typename RmsCache<XT, RT, MODE>::Vec& cv,
+                                                     const typename RT::Vec& rv, u32x4 wv, float rmf)
 {
     float h[8];
     unpack8<RmsCache<XT, RT, MODE>>(cv, h);
@@ -311,7 +347,17 @@ __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* 
             for (int j = 0; j < 8; ++j) o[j] = o[j] * ga[j];
         }
     }
-    const typename YT::Vec yv = pack8<YT>(o);
+    return pack8<YT>(o);
+}
+
+// Pass 2 of the chunk at element e: rms_out8, then the stores (y, or the Hadamard outputs by the
+// butterfly).
+template <class XT, class YT, class RT, int MODE, int HAD, bool SPLIT = false>
+__device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* yrow, int64_t e, int64_t wofs,
+                                           const typename RmsCache<XT, RT, MODE>::Vec& cv,
+                                           const typename RT::Vec& rv, u32x4 wv, float rmf)
+{
+    const typename YT::Vec yv = rms_out8<XT, YT, RT, MODE, SPLIT>(a, e, wofs, cv, rv, wv, rmf);
     if constexpr (SPLIT) store8_split<YT>(yrow, e, yv);
     else if constexpr (!(HAD & HAD_OUT)) store8<YT>(yrow, e, yv);
     else
@@ -341,23 +387,56 @@ __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* 
     }
 }
 
-template <class XT, class YT, class RT, int MAXV, int MODE, int HAD, int WM, bool SPLIT = false>
+// ACC: the type of the row's sum of squares -- double (exact for 16-bit data, rounded once to fp32) or
+// float (one fp32 FMA chain per lane in chunk order, then the wave butterfly and the cross-wave sum in
+// a fixed order: the reference's own precision, norm.cu:101-108, 140-151).
+template <class XT, class YT, class RT, int MAXV, int MODE, int HAD, int WM, bool SPLIT = false, class ACC = double>
 __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int tid, int nt, RowRegs<XT, RT, MAXV>& L,
-                                           double* red)
+                                           ACC* red)
 {
     const int nc = a.dim >> 3;
     char* rrow = (char*)a.r + row * a.ldr * RT::bytes;
     char* yrow = (char*)a.y + row * a.ldy * YT::bytes;
+    constexpr bool MF = (HAD & HAD_MFMA) != 0;
+    const int c0 = tid;
+    const int lane = tid & 63;
+    // chunk held in the matrix-core placement: chunk k of the lane's wave, mfma_chunk(lane) within it
+    [[maybe_unused]] const int cp0 = (tid & ~63) | mfma_chunk(lane);
+    [[maybe_unused]] HadMfma H;
+    if constexpr (MF)
+    {
+        H = had_mfma_operands(lane);
+        if constexpr ((HAD & HAD_IN) != 0)
+        {
+            // x = the producing projection's output rotation, every lane of the wave taking part
+            static_assert(XT::code == DT_F16 && MODE != RMS_GATHER && MODE != RMS_GATED, "x rotation takes f16 x");
+            const void* post[MAXV];
+            int64_t col[MAXV];
+            #pragma unroll
+            for (int k = 0; k < MAXV; ++k)
+            {
+                const int cp = cp0 + k * nt;
+                post[k] = cp < nc ? a.hxpost : nullptr;
+                col[k] = (int64_t)cp * 8;
+                L.xv[k] = mfma_permute(L.xv[k], lane);
+            }
+            output_rotations_mfma<MAXV>(H, L.xv, post, col, lane);
+            #pragma unroll
+            for (int k = 0; k < MAXV; ++k) L.xv[k] = mfma_permute(L.xv[k], lane);
+        }
+    }
     // Pass 1: residual update and sum of squares.  The row is then cached in its narrowest exact
     // form (x as loaded, or the rounded residual), 4 VGPRs per chunk for 16-bit data, and
     // re-expanded in pass 2.
     typename RmsCache<XT, RT, MODE>::Vec cache[MAXV];
-    double ss = 0.0;
+    ACC ss = 0;
     #pragma unroll
     for (int k = 0; k < MAXV; ++k)
     {
-        const int c = tid + k * nt;
-        if (c < nc) cache[k] = rms_chunk1<XT, RT, MODE, HAD>(a, rrow, chunk_elem<SPLIT>(c), L.valid, L.xv[k], L.rv[k], ss);
+        const int c = c0 + k * nt;
+        if (c < nc)
+            cache[k] = rms_chunk1<XT, RT, MODE, MF ? 0 : HAD, SPLIT, ACC>(a, rrow, chunk_elem<SPLIT>(c), L.valid, L.xv[k],
+                                                                    L.rv[k], ss);
     }
 
     const int64_t wofs = weight_row<MODE>(a, row);
@@ -366,16 +445,90 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
         #pragma unroll
         for (int k = 0; k < MAXV; ++k)
         {
-            const int c = tid + k * nt;
+            const int c = c0 + k * nt;
             if (c < nc && a.w) L.wv[k] = prefetch_w8<SPLIT>(a.w, a.wt, wofs + chunk_elem<SPLIT>(c));
         }
     }
 
-    // fp64 row sum (exact for 16-bit data), one rounding, IEEE fp32 sqrt and divide.  The workgroup
-    // reduces once, so one barrier suffices.
-    ss = block_sum64_once(ss, red);
+    // Row sum (fp64: exact for 16-bit data, then one rounding), IEEE fp32 sqrt and divide.  The
+    // workgroup reduces once, so one barrier suffices.
+    ss = block_sum_once(ss, red);
     const float rmf = rms_factor(ss, a.dim, a.eps) * a.cs;
 
+    if constexpr (MF)
+    {
+        // Pass 2 with the matrix-core transforms: the f16 norm output of every live chunk (zeros past the
+        // row), then each consumer's had_r_128 with its pre-scale, every lane of the wave taking part.
+        static_assert((HAD & HAD_OUT) != 0 && YT::code == DT_F16 && !SPLIT, "the Hadamard outputs follow an f16 norm");
+        #pragma unroll
+        for (int k = 0; k < MAXV; ++k)
+        {
+            const int c = c0 + k * nt;
+            const int64_t e = (int64_t)c * 8;
+            const bool live = c < nc;
+            TF16::Vec yv;
+            yv.a = u32x4{ 0u, 0u, 0u, 0u };
+            if (live)
+            {
+                if constexpr (WM == W_LATE)
+                {
+                    if (a.w) L.wv[k] = prefetch_w8(a.w, a.wt, wofs + e);
+                }
+                if constexpr (kDeferResidual<MODE, RT>)
+                {
+                    if (a.r_cached) store8c<RT>(rrow, e, cache[k]);
+                    else store8<RT>(rrow, e, cache[k]);
+                }
+                yv = rms_out8<XT, YT, RT, MODE>(a, e, wofs, cache[k], L.rv[k], L.wv[k], rmf);
+                if (a.y) store8<YT>(yrow, e, yv);
+            }
+            // the consumers' transforms of this chunk (at most 4) in the matrix-core placement, their
+            // MFMAs issued together, each result moved back to its lane for the store
+            const TF16::Vec yp = mfma_permute(yv, lane);
+            const int cp = cp0 + k * nt;
+            const bool plive = cp < nc;
+            const int64_t ep = (int64_t)cp * 8;
+            // (in pairs: four results at once would hold 32 more VGPRs and cost a wave per SIMD)
+            #pragma unroll
+            for (int i0 = 0; i0 < 4; i0 += 2)
+            {
+                if (i0 >= a.nh) break;
+                MfmaOut m[2];
+                #pragma unroll
+                for (int d = 0; d < 2; ++d)
+                {
+                    const int i = i0 + d;
+                    if (i < a.nh)
+                    {
+                        TF16::Vec v = yp;
+                        if (plive && a.hpre[i])
+                        {
+                            const TF16::Vec p = load8<TF16>(a.hpre[i], (a.hpre_rows > 1 ? (row % a.hpre_rows) * a.dim : 0) + ep);
+                            #pragma unroll
+                            for (int q = 0; q < 4; ++q) v.a[q] = hmul2(v.a[q], p.a[q]);
+                        }
+                        m[d] = had128_mfma_issue(H, v);
+                    }
+                    else
+                        m[d] = MfmaOut{};
+                }
+                mfma_wait_all(m);
+                #pragma unroll
+                for (int d = 0; d < 2; ++d)
+                {
+                    const int i = i0 + d;
+                    if (i < a.nh)
+                    {
+                        float f[8];
+                        had128_mfma_finish(m[d], f, lane, a.hr);
+                        const TF16::Vec o = mfma_permute(pack8<TF16>(f), lane);
+                        if (live) store8<TF16>((char*)a.hout[i] + row * a.ldh * 2, e, o);
+                    }
+                }
+            }
+        }
+        return;
+    }
     // Pass 2: scale, weight, round once, store.
     #pragma unroll
     for (int k = 0; k < MAXV; ++k)
@@ -391,6 +544,11 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
             if constexpr (kDeferResidual<MODE, RT>)
             {
                 if constexpr (SPLIT) store8_split<RT>(rrow, e, cache[k]);
+                else if constexpr (HAD != 0)
+                {
+                    if (a.r_cached) store8c<RT>(rrow, e, cache[k]);
+                    else store8<RT>(rrow, e, cache[k]);
+                }
                 else store8<RT>(rrow, e, cache[k]);
             }
             rms_chunk2<XT, YT, RT, MODE, HAD, SPLIT>(a, row, yrow, e, wofs, cache[k], L.rv[k], L.wv[k], rmf);
@@ -400,15 +558,53 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
 
 // One row per workgroup: its loads, pass 1, one reduction, pass 2.  (A grid-stride loop over rows, with
 // the second barrier it needs before LDS reuse, measured ~1 us slower at [8192, 5120].)
-template <class XT, class YT, class RT, int MAXV, int MODE, int HAD = 0, int WM = W_EARLY, bool SPLIT = false>
+template <class XT, class YT, class RT, int MAXV, int MODE, int HAD = 0, int WM = W_EARLY, bool SPLIT = false,
+          class ACC = double>
 __global__ __launch_bounds__(1024) void k_rms_norm(RmsArgs a)
 {
     static_assert(!SPLIT || (HAD == 0 && (MODE == RMS_PLAIN || MODE == RMS_RES_IN)), "split chunks: plain and residual norms");
-    __shared__ double red[16];
+    __shared__ ACC red[16];
     const int64_t row = a.row0 + blockIdx.x;
     RowRegs<XT, RT, MAXV> L;
-    rms_load<XT, RT, MAXV, MODE, SPLIT>(a, row, threadIdx.x, blockDim.x, WM == W_EARLY, L);
-    rms_finish<XT, YT, RT, MAXV, MODE, HAD, WM, SPLIT>(a, row, threadIdx.x, blockDim.x, L, red);
+    rms_load<XT, RT, MAXV, MODE, SPLIT, HAD>(a, row, threadIdx.x, blockDim.x, WM == W_EARLY, L);
+    rms_finish<XT, YT, RT, MAXV, MODE, HAD, WM, SPLIT, ACC>(a, row, threadIdx.x, blockDim.x, L, red);
+}
+
+// Streaming plain / residual norms as a resident grid: workgroup b takes rows b, b + G, b + 2G, ... (G
+// workgroups, all resident at once) and issues the loads of its next row before the reduction and
+// stores of the current one, so a workgroup's HBM reads stay in flight across its barrier.  The weight
+// chunks are fetched once per workgroup.  The two rows in flight alternate between two register sets
+// and two LDS reduction slots (a slot is rewritten two rows later, after every wave has passed the
+// barrier in between, so one barrier per row suffices).
+template <class XT, class YT, class RT, int MAXV, int MODE, class ACC = double>
+__global__ __launch_bounds__(1024) void k_rms_norm_pipe(RmsArgs a)
+{
+    static_assert(MODE == RMS_PLAIN || MODE == RMS_RES_IN, "plain and residual norms");
+    __shared__ ACC red[2][16];
+    const int tid = threadIdx.x, nt = blockDim.x, nc = a.dim >> 3;
+    u32x4 wv[MAXV];
+    #pragma unroll
+    for (int k = 0; k < MAXV; ++k)
+    {
+        const int c = tid + k * nt;
+        if (c < nc && a.w) wv[k] = prefetch_w8(a.w, a.wt, (int64_t)c * 8);
+    }
+    const int64_t G = gridDim.x;
+    RowRegs<XT, RT, MAXV> A, B;
+    int64_t row = blockIdx.x;
+    if (row < a.rows) rms_load<XT, RT, MAXV, MODE>(a, row, tid, nt, false, A);
+    for (; row < a.rows; row += 2 * G)
+    {
+        if (row + G < a.rows) rms_load<XT, RT, MAXV, MODE>(a, row + G, tid, nt, false, B);
+        #pragma unroll
+        for (int k = 0; k < MAXV; ++k) A.wv[k] = wv[k];
+        rms_finish<XT, YT, RT, MAXV, MODE, 0, W_EARLY, false, ACC>(a, row, tid, nt, A, red[0]);
+        if (row + G >= a.rows) break;
+        if (row + 2 * G < a.rows) rms_load<XT, RT, MAXV, MODE>(a, row + 2 * G, tid, nt, false, A);
+        #pragma unroll
+        for (int k = 0; k < MAXV; ++k) B.wv[k] = wv[k];
+        rms_finish<XT, YT, RT, MAXV, MODE, 0, W_EARLY, false, ACC>(a, row + G, tid, nt, B, red[1]);
+    }
 }
 
 // Short rows (at most 64 chunks of 8): LPR lanes per row (a power of two covering dim / 8), one
@@ -602,6 +798,20 @@ inline RmsShape rms_shape(int nc, int64_t rows, int mode, int had, bool wide = f
         return sh;
     }
 #endif
+#ifdef EXL3R_TUNING
+    if (rows > 1024 && !had && (mode == RMS_RES_IN || mode == RMS_PLAIN) && tuning().rms_wmode > 0)
+    {
+        // the automatic lane shape with the weight fetched early (1), mid-row (2) or late (3)
+        Tuning t = tuning();
+        t.rms_wmode = 0;
+        const Tuning saved = tuning();
+        tuning() = t;
+        RmsShape sh = rms_shape(nc, rows, mode, had, wide);
+        tuning() = saved;
+        sh.wmode = saved.rms_wmode - 1;
+        return sh;
+    }
+#endif
     if (rows > 1024 && mode == RMS_RES_IN && !had)
     {
         if (nc <= 512) return { 1, thr(1), W_LATE };
@@ -623,8 +833,8 @@ inline RmsShape rms_shape(int nc, int64_t rows, int mode, int had, bool wide = f
     return { 8, thr(8), W_EARLY };   // <= 1024 (rms_vec_ok bounds the row at 8192 chunks)
 }
 
-template <class XT, class YT, class RT, int MODE, int HAD, int WM, bool SPLIT = false>
-void launch_rms_wm(const RmsArgs& a0, const RmsShape& sh, hipStream_t s)
+template <class XT, class YT, class RT, int MODE, int HAD, int WM, bool SPLIT = false, class ACC = double>
+void launch_rms_acc(const RmsArgs& a0, const RmsShape& sh, hipStream_t s)
 {
     // Launches of more than kMaxGridX rows go out in blocks of kMaxGridX rows (row0 offsets the block).
     for (int64_t r0 = 0; r0 < a0.rows; r0 += kMaxGridX)
@@ -634,25 +844,68 @@ void launch_rms_wm(const RmsArgs& a0, const RmsShape& sh, hipStream_t s)
         const dim3 grid((unsigned)(a0.rows - r0 < kMaxGridX ? a0.rows - r0 : kMaxGridX));
         switch (sh.maxv)
         {
-            case 1: launch(k_rms_norm<XT, YT, RT, 1, MODE, HAD, WM, SPLIT>, grid, sh.threads, 0, s, a); break;
-            case 2: launch(k_rms_norm<XT, YT, RT, 2, MODE, HAD, WM, SPLIT>, grid, sh.threads, 0, s, a); break;
+            case 1: launch(k_rms_norm<XT, YT, RT, 1, MODE, HAD, WM, SPLIT, ACC>, grid, sh.threads, 0, s, a); break;
+            case 2: launch(k_rms_norm<XT, YT, RT, 2, MODE, HAD, WM, SPLIT, ACC>, grid, sh.threads, 0, s, a); break;
             case 4:
-                if constexpr (!SPLIT) launch(k_rms_norm<XT, YT, RT, 4, MODE, HAD, WM>, grid, sh.threads, 0, s, a);
+                if constexpr (!SPLIT) launch(k_rms_norm<XT, YT, RT, 4, MODE, HAD, WM, false, ACC>, grid, sh.threads, 0, s, a);
                 break;
             default:
-                if constexpr (!SPLIT) launch(k_rms_norm<XT, YT, RT, 8, MODE, HAD, WM>, grid, sh.threads, 0, s, a);
+                if constexpr (!SPLIT) launch(k_rms_norm<XT, YT, RT, 8, MODE, HAD, WM, false, ACC>, grid, sh.threads, 0, s, a);
                 break;
         }
     }
 }
 
+template <class XT, class YT, class RT, int MODE, int HAD, int WM, bool SPLIT = false>
+void launch_rms_wm(const RmsArgs& a0, const RmsShape& sh, hipStream_t s)
+{
+#ifdef EXL3R_TUNING
+    if (HAD == 0 && (MODE == RMS_PLAIN || MODE == RMS_RES_IN) && tuning().rms_sum32 == 1)
+        return launch_rms_acc<XT, YT, RT, MODE, HAD, WM, SPLIT, float>(a0, sh, s);
+#endif
+    launch_rms_acc<XT, YT, RT, MODE, HAD, WM, SPLIT, double>(a0, sh, s);
+}
+
 template <class XT, class YT, class RT>
 constexpr bool rms_wide = XT::code == DT_F32 || YT::code == DT_F32 || RT::code == DT_F32;
+
+// The resident-grid form: workgroups per CU from the occupancy of the instance (once per instance).
+template <class XT, class YT, class RT, int MAXV, int MODE, class ACC>
+void launch_rms_pipe(const RmsArgs& a, int threads, int per_cu, hipStream_t s)
+{
+    static const int resident = [&] {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_rms_norm_pipe<XT, YT, RT, MAXV, MODE, ACC>, threads, 0) !=
+                hipSuccess || nb < 1)
+            nb = 1;
+        return nb;
+    }();
+    int64_t blocks = (int64_t)(per_cu > 0 && per_cu < resident ? per_cu : resident) * device_cus();
+    if (blocks > a.rows) blocks = a.rows;
+    launch(k_rms_norm_pipe<XT, YT, RT, MAXV, MODE, ACC>, (unsigned)blocks, threads, 0, s, a);
+}
 
 template <class XT, class YT, class RT, int MODE, int HAD = 0>
 void launch_rms_vec(const RmsArgs& a, hipStream_t s)
 {
     const RmsShape sh = rms_shape(a.dim / 8, a.rows, MODE, HAD, rms_wide<XT, YT, RT>);
+#ifdef EXL3R_TUNING
+    if constexpr (HAD == 0 && (MODE == RMS_RES_IN || MODE == RMS_PLAIN))
+    {
+        if (tuning().rms_pipe > 0 && !sh.split && a.rows <= kMaxGridX && (sh.maxv == 1 || sh.maxv == 2))
+        {
+            const int pc = tuning().rms_pipe;   // 1: as many as fit, else that many per CU
+            auto go = [&](auto M) {
+                constexpr int MV = decltype(M)::value;
+                if (tuning().rms_sum32 == 1) launch_rms_pipe<XT, YT, RT, MV, MODE, float>(a, sh.threads, pc - 1, s);
+                else launch_rms_pipe<XT, YT, RT, MV, MODE, double>(a, sh.threads, pc - 1, s);
+            };
+            if (sh.maxv == 1) go(std::integral_constant<int, 1>{});
+            else go(std::integral_constant<int, 2>{});
+            return;
+        }
+    }
+#endif
     if constexpr (HAD == 0 && (MODE == RMS_RES_IN || MODE == RMS_PLAIN))
     {
         if (sh.split)
@@ -661,12 +914,9 @@ void launch_rms_vec(const RmsArgs& a, hipStream_t s)
             return launch_rms_wm<XT, YT, RT, MODE, HAD, W_MID, true>(a, sh, s);
         }
     }
-    if constexpr (HAD == 0 && MODE == RMS_RES_IN)
+    if constexpr (HAD == 0 && (MODE == RMS_RES_IN || MODE == RMS_PLAIN))
     {
         if (sh.wmode == W_LATE) return launch_rms_wm<XT, YT, RT, MODE, HAD, W_LATE>(a, sh, s);
-    }
-    if constexpr (HAD == 0 && MODE == RMS_PLAIN)
-    {
         if (sh.wmode == W_MID) return launch_rms_wm<XT, YT, RT, MODE, HAD, W_MID>(a, sh, s);
     }
     launch_rms_wm<XT, YT, RT, MODE, HAD, W_EARLY>(a, sh, s);

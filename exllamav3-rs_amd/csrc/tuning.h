@@ -15,6 +15,10 @@ EXL3R_API void exl3r_tune_rms_rows(int rows_per_lane);
 /* plain / residual RMSNorm with split chunks (rows of whole 512-element spans): -1 never, 0 auto,
  * 1 always; the weight fetched mid-row (1) or late (2) in split launches */
 EXL3R_API void exl3r_tune_rms_split(int split, int wmode);
+/* streaming plain / residual RMSNorm: fp32 row sum (sum32 = 1; 0 fp64), weight fetched early / mid / late
+ * (wmode 1 / 2 / 3; 0 auto), resident grid (pipe 1: as many workgroups per CU as fit, n > 1: n - 1);
+ * Hadamard norms: cached residual stores (r_cached = 1) */
+EXL3R_API void exl3r_tune_rms_mode(int sum32, int wmode, int r_cached, int pipe);
 EXL3R_API void exl3r_tune_act(int unroll, int threads, int blocks_per_cu);
 /* heads per lane: 1, 2 or 4 */
 EXL3R_API void exl3r_tune_rope(int iters);
@@ -30,6 +34,9 @@ EXL3R_API void exl3r_tune_rope_nx_run(int run);
 EXL3R_API void exl3r_tune_sample(int rows_min, int threads);
 /* Hadamard: 128-blocks per 16-lane group (1, 2, 4; 0 auto) */
 EXL3R_API void exl3r_tune_had(int blocks_per_group);
+/* matrix-core Hadamard kernels: spans per wave in flight (1, 2, 4; 0 auto), workgroups per CU of the looping
+ * grid (0 auto, < 0 one span group per wave), cached input loads (1) */
+EXL3R_API void exl3r_tune_had_mfma(int unroll, int blocks_per_cu, int cached);
 EXL3R_API void exl3r_tune_embed(int threads);
 #ifdef __cplusplus
 }

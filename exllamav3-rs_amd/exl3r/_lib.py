@@ -16,6 +16,7 @@ HEADER_PATH = os.path.join(os.path.dirname(_PKG_ROOT), "include", "exl3r", "rowo
 F32, F16, BF16, I32, I64 = 0, 1, 2, 3, 4
 OK, EINVAL, EDTYPE = 0, -1, -2
 ROPE_NONE, ROPE_GPTJ, ROPE_NEOX = 0, 1, 2
+HAD_EXACT = 16   # EXL3R_HAD_EXACT: the fused Hadamard entry points' reference butterfly
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -74,6 +75,7 @@ PROTOTYPES = {
     "exl3r_rms_norm_had": (_i, [_vp, _i, _i64, _vp, _i, _vp, _i, _i64, _vp, _i64, _i, _vp, _vp, _i64, _i64, _i64,
                                 _f, _f, _f, _f, _i, _vp, _vp]),
     "exl3r_had_r_128": (_i, [_vp, _i, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _f, _vp]),
+    "exl3r_had_r_128_mfma": (_i, [_vp, _i, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _f, _vp]),
     "exl3r_act_mul_had": (_i, [_i, _vp, _vp, _i, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _f, _f, _i, _vp,
                                _vp, _vp]),
     "exl3r_gumbel_noise": (_i, [_vp, _i, _i64, _vp, _i, _i64, _i64, _i64, ctypes.c_uint32, _vp]),
@@ -93,6 +95,7 @@ TUNE_PROTOTYPES = {
     "exl3r_tune_rms": (None, [_i, _i]),
     "exl3r_tune_rms_rows": (None, [_i]),
     "exl3r_tune_rms_split": (None, [_i, _i]),
+    "exl3r_tune_rms_mode": (None, [_i, _i, _i, _i]),
     "exl3r_tune_act": (None, [_i, _i, _i]),
     "exl3r_tune_rope": (None, [_i]),
     "exl3r_tune_rope_tok": (None, [_i, _i, _i]),
@@ -100,6 +103,7 @@ TUNE_PROTOTYPES = {
     "exl3r_tune_rope_nx_run": (None, [_i]),
     "exl3r_tune_sample": (None, [_i, _i]),
     "exl3r_tune_had": (None, [_i]),
+    "exl3r_tune_had_mfma": (None, [_i, _i, _i]),
     "exl3r_tune_embed": (None, [_i]),
 }
 
@@ -170,6 +174,7 @@ def tuned():
         lib.exl3r_tune_rms(0, 0)
         lib.exl3r_tune_rms_rows(0)
         lib.exl3r_tune_rms_split(0, 1)
+        lib.exl3r_tune_rms_mode(0, 0, 0, 0)
         lib.exl3r_tune_act(0, 0, 0)
         lib.exl3r_tune_rope(0)
         lib.exl3r_tune_rope_tok(0, 0, 0)
@@ -177,6 +182,7 @@ def tuned():
         lib.exl3r_tune_rope_nx_run(0)
         lib.exl3r_tune_sample(0, 0)
         lib.exl3r_tune_had(0)
+        lib.exl3r_tune_had_mfma(0, 0, 0)
         lib.exl3r_tune_embed(0)
         _lib = saved
 

@@ -11,7 +11,7 @@ import math
 
 import torch
 
-from ._lib import BF16, F16, F32, I32, I64, RopeDesc, check, load
+from ._lib import BF16, F16, F32, HAD_EXACT, I32, I64, RopeDesc, check, load
 
 _DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.int32: I32, torch.int64: I64}
 
@@ -528,9 +528,10 @@ def gumbel_noise(x, out, random=0, stream=None):
                                     int(random) & 0xFFFFFFFF, _stream(x, stream)))
 
 
-def had_r_128(x, out, pre_scale=None, post_scale=None, scale=1.0, stream=None):
+def had_r_128(x, out, pre_scale=None, post_scale=None, scale=1.0, stream=None, mfma=False):
     """Random-Hadamard transform of [rows, k] f16 / f32 x into out (k % 128 == 0), with an optional f16
-    per-column pre_scale (before) or post_scale (after) (src/ffi.rs:604-608)."""
+    per-column pre_scale (before) or post_scale (after) (src/ffi.rs:604-608).  mfma=True: the transform on
+    the matrix cores (exl3r_had_r_128_mfma, f16 only; within the stated rounding tolerance)."""
     rows, cols, ldx = _rows(x)
     ro, co, ldo = _rows(out)
     if (ro, co) != (rows, cols) or out.dtype != x.dtype:
@@ -538,15 +539,17 @@ def had_r_128(x, out, pre_scale=None, post_scale=None, scale=1.0, stream=None):
     for t in (pre_scale, post_scale):
         if t is not None and (t.dtype != torch.float16 or t.numel() != cols or not t.is_contiguous()):
             raise ValueError("scales must be contiguous f16 with one entry per column")
-    check(load().exl3r_had_r_128(_ptr(x), dtype_code(x), ldx, _ptr(out), ldo, rows, cols, _ptr(pre_scale),
-                                 _ptr(post_scale), float(scale), _stream(x, stream)))
+    fn = load().exl3r_had_r_128_mfma if mfma else load().exl3r_had_r_128
+    check(fn(_ptr(x), dtype_code(x), ldx, _ptr(out), ldo, rows, cols, _ptr(pre_scale), _ptr(post_scale), float(scale),
+             _stream(x, stream)))
 
 
 def rms_norm_had(x, w, outs, pre_scales, eps, constant_bias=0.0, constant_scale=1.0, r=None, y=None, had_scale=1.0,
-                 rotate_x=False, x_post_scale=None, stream=None):
+                 rotate_x=False, x_post_scale=None, stream=None, exact=False):
     """One pass: y = RMSNorm(x) (or r += x; y = RMSNorm(r)) in f16, then outs[i] = had_r_128(y, pre_scales[i])
     for each projection (1..4 f16 outputs shaped like x; y is written only if given).  rotate_x: x (f16) is
-    first taken through its producer's output rotation had_r_128(x, post_scale=x_post_scale)."""
+    first taken through its producer's output rotation had_r_128(x, post_scale=x_post_scale).  The
+    transforms run on the matrix cores; exact=True: the reference's butterfly (EXL3R_HAD_EXACT)."""
     rows, dim, ldx = _rows(x)
     if not 1 <= len(outs) <= 4 or len(pre_scales) != len(outs):
         raise ValueError("1..4 outputs, one pre_scale (or None) each")
@@ -566,17 +569,20 @@ def rms_norm_had(x, w, outs, pre_scales, eps, constant_bias=0.0, constant_scale=
     check(load().exl3r_rms_norm_had(_ptr(x), dtype_code(x), ldx, _ptr(w), dtype_code(w) if w is not None else F16,
                                     _ptr(r), dtype_code(r) if r is not None else F16, ldr, _ptr(y), ldy, len(outs),
                                     pre, out, ldo, rows, dim, eps, constant_bias, constant_scale, float(had_scale),
-                                    1 if rotate_x else 0, _ptr(x_post_scale), _stream(x, stream)))
+                                    (1 if rotate_x else 0) | (HAD_EXACT if exact else 0), _ptr(x_post_scale),
+                                    _stream(x, stream)))
 
 
 ACT_CODES = {"silu": 0, "gelu": 1, "mul_sigmoid": 2}
 
 
 def act_mul_had(act, x, y, out, pre_scale=None, z=None, act_limit=0.0, had_scale=1.0, rotate_x=False, rotate_y=False,
-                x_post_scale=None, y_post_scale=None, stream=None):
+                x_post_scale=None, y_post_scale=None, stream=None, exact=False):
     """One pass: z = silu(x) * y, gelu(x) * y or x * sigmoid(y) in f16, then out = had_r_128(z, pre_scale)
     (f16 [rows, cols], cols % 128 == 0); z is written only if given.  rotate_x / rotate_y: the f16 input is
-    first given its projection's output rotation had_r_128(v, post_scale=x_post_scale / y_post_scale)."""
+    first given its projection's output rotation had_r_128(v, post_scale=x_post_scale / y_post_scale).
+    The transforms run on the matrix cores; exact=True: the reference's butterfly (EXL3R_HAD_EXACT),
+    bit-identical to the unfused calls."""
     rows, cols, ldx = _rows(x)
     ry, cy, ldy = _rows(y)
     ro, co, ldo = _rows(out)
@@ -589,7 +595,8 @@ def act_mul_had(act, x, y, out, pre_scale=None, z=None, act_limit=0.0, had_scale
             raise ValueError("z is the f16 activation shaped like x")
     check(load().exl3r_act_mul_had(ACT_CODES[act], _ptr(x), _ptr(y), dtype_code(x), ldx, ldy, _ptr(z), ldz,
                                    _ptr(pre_scale), _ptr(out), ldo, rows, cols, act_limit, float(had_scale),
-                                   (1 if rotate_x else 0) | (2 if rotate_y else 0), _ptr(x_post_scale),
+                                   (1 if rotate_x else 0) | (2 if rotate_y else 0) | (HAD_EXACT if exact else 0),
+                                   _ptr(x_post_scale),
                                    _ptr(y_post_scale), _stream(x, stream)))
 
 

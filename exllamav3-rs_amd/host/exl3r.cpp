@@ -321,7 +321,7 @@ void had_r_128(const Tensor& x, const Tensor& out, const Tensor* pre_scale, cons
 void rms_norm_had(const Tensor& x, const Tensor* w, const Tensor* r, const Tensor* y,
                   const std::vector<const Tensor*>& outs, const std::vector<const Tensor*>& pre_scales, float eps,
                   float constant_bias, float constant_scale, float had_scale, const Stream& s, bool rotate_x,
-                  const Tensor* x_post_scale)
+                  const Tensor* x_post_scale, bool exact)
 {
     int64_t rows, dim, ldx, ldr = 0, ldy = 0, ldo = -1;
     x.rows_view(rows, dim, ldx);
@@ -355,12 +355,12 @@ void rms_norm_had(const Tensor& x, const Tensor* w, const Tensor* r, const Tenso
     check_abi(exl3r_rms_norm_had(x.data, code(x.dtype), ldx, ptr(w), code_or(w, DType::F16), r ? r->data : nullptr,
                                  r ? code(r->dtype) : EXL3R_F16, ldr, y ? y->data : nullptr, ldy, (int)outs.size(),
                                  pre.data(), out.data(), ldo, rows, dim, eps, constant_bias, constant_scale, had_scale,
-                                 rotate_x ? 1 : 0, ptr(x_post_scale), s.get()));
+                                 (rotate_x ? 1 : 0) | (exact ? EXL3R_HAD_EXACT : 0), ptr(x_post_scale), s.get()));
 }
 
 void act_mul_had(HadAct act, const Tensor& x, const Tensor& y, const Tensor& out, const Tensor* pre_scale,
                  const Tensor* z, float act_limit, float had_scale, const Stream& s, bool rotate_x, bool rotate_y,
-                 const Tensor* x_post, const Tensor* y_post)
+                 const Tensor* x_post, const Tensor* y_post, bool exact)
 {
     int64_t rows, cols, ldx, ry, cy, ldy, ro, co, ldo, ldz = 0;
     x.rows_view(rows, cols, ldx);
@@ -376,7 +376,8 @@ void act_mul_had(HadAct act, const Tensor& x, const Tensor& y, const Tensor& out
     }
     check_abi(exl3r_act_mul_had((int)act, x.data, y.data, code(x.dtype), ldx, ldy, z ? z->data : nullptr, ldz,
                                 ptr(pre_scale), out.data, ldo, rows, cols, act_limit, had_scale,
-                                (rotate_x ? 1 : 0) | (rotate_y ? 2 : 0), ptr(x_post), ptr(y_post), s.get()));
+                                (rotate_x ? 1 : 0) | (rotate_y ? 2 : 0) | (exact ? EXL3R_HAD_EXACT : 0), ptr(x_post),
+                                ptr(y_post), s.get()));
 }
 
 void argmax_sample(const Tensor& logits, const Tensor& ids, int max_logit, const Stream& s)

@@ -243,18 +243,21 @@ void had_r_128(const Tensor& x, const Tensor& out, const Tensor* pre_scale, cons
 // 1..4 projections (src/modules.rs:372-411 then 224-227), in one pass; outs are f16 like x; y (f16) is
 // written only when given; pre_scales[i] may be null.  rotate_x: f16 x is first taken through its
 // producer's output rotation had_r_128(x, post_scale = x_post_scale) (src/modules.rs:231).
+// The transforms run on the matrix cores; exact: the reference's butterfly (EXL3R_HAD_EXACT).
 void rms_norm_had(const Tensor& x, const Tensor* w, const Tensor* r, const Tensor* y,
                   const std::vector<const Tensor*>& outs, const std::vector<const Tensor*>& pre_scales, float eps,
                   float constant_bias, float constant_scale, float had_scale, const Stream& s,
-                  bool rotate_x = false, const Tensor* x_post_scale = nullptr);
+                  bool rotate_x = false, const Tensor* x_post_scale = nullptr, bool exact = false);
 // Gated activation whose f16 output feeds the next projection's had_r_128(z, pre_scale)
 // (src/modules.rs:932-940 then 224-227): silu(x) * y, gelu(x) * y or x * sigmoid(y); z kept when given.
 enum class HadAct : int { Silu = EXL3R_ACT_SILU, Gelu = EXL3R_ACT_GELU, MulSigmoid = EXL3R_ACT_MUL_SIGMOID };
 // rotate_x / rotate_y: the f16 input is first given its projection's output rotation (post-scale x_post /
 // y_post, or none).
+// The transforms run on the matrix cores; exact: the reference's butterfly (EXL3R_HAD_EXACT).
 void act_mul_had(HadAct act, const Tensor& x, const Tensor& y, const Tensor& out, const Tensor* pre_scale,
                  const Tensor* z, float act_limit, float had_scale, const Stream& s, bool rotate_x = false,
-                 bool rotate_y = false, const Tensor* x_post = nullptr, const Tensor* y_post = nullptr);
+                 bool rotate_y = false, const Tensor* x_post = nullptr, const Tensor* y_post = nullptr,
+                 bool exact = false);
 // Embedding gather: out[i] = table[ids[i]] (bit-exact, or exact upcast to f32); err_flag optional.
 void embedding(const Tensor& table, const Tensor& ids, const Tensor& out, int32_t* err_flag, const Stream& s);
 // Gather fused with the following RMSNorm; h optional.

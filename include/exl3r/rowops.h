@@ -87,6 +87,12 @@ extern "C" {
 #define EXL3R_ACT_GELU        1 /* gelu(x) * y */
 #define EXL3R_ACT_MUL_SIGMOID 2 /* x * sigmoid(y) */
 
+/* Flag of the fused Hadamard entry points (exl3r_act_mul_had's rotate_in, exl3r_rms_norm_had's rotate_x):
+ * the 128-point transforms
+ * as the reference's fp32 butterfly (bit-identical to the unfused calls) instead of the matrix-core
+ * form (within the stated rounding tolerance of it). */
+#define EXL3R_HAD_EXACT 16
+
 #define EXL3R_ROPE_NONE 0
 #define EXL3R_ROPE_GPTJ 1
 #define EXL3R_ROPE_NEOX 2
@@ -518,6 +524,19 @@ EXL3R_API int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out, 
                     int64_t cols, const void* pre_scale, const void* post_scale, float scale, void* stream);
 
 /*
+ * exl3r_had_r_128 with the 128-point transform on the matrix cores (v_mfma_f32_16x16x32_f16 against
+ * +-1 f16 operands, fp32 sums): the transform the fused Hadamard entry points use unless
+ * EXL3R_HAD_EXACT.  Same arguments, dtype F16 only, same pre / post-scale roundings.  The sums are
+ * grouped differently from the reference's butterfly, so each f16 result is exl3r_had_r_128's or its
+ * f16 neighbour, or within 2^-17 * r * sum|input| of it where the transform cancels (r = scale /
+ * sqrt(128), the sum over the 128 pre-scaled inputs of the block); zero results are +0.  Rows that
+ * are not 16-byte aligned run exl3r_had_r_128.  No counterpart in the reference (same call site,
+ * src/modules.rs:224-231, for callers that take the tolerance for the speed).
+ */
+EXL3R_API int exl3r_had_r_128_mfma(const void* x, int dtype, int64_t ldx, void* out, int64_t ldo, int64_t rows,
+                    int64_t cols, const void* pre_scale, const void* post_scale, float scale, void* stream);
+
+/*
  * RMSNorm whose f16 output feeds the random-Hadamard input rotation of 1..4 EXL3 projections, in one
  * pass (the prefill path of RmsNorm::forward / forward_res, src/modules.rs:372-411, then
  * had_r_128(y, suh) per projection, src/modules.rs:224-227):
@@ -525,12 +544,16 @@ EXL3R_API int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out, 
  *              exl3r_rms_norm_res_in; y is f16 and written only when y != NULL (row stride ldy);
  *   outs[i] = had_r_128(y, pre_scales[i]) with scale had_scale, f16 [rows, dim] at row stride ldo;
  *              pre_scales[i] is f16 [dim] (the projection's suh) or NULL.
- *   rotate_x != 0: x (f16, the raw output of the previous EXL3 projection) is first replaced by that
+ *   rotate_x = 1: x (f16, the raw output of the previous EXL3 projection) is first replaced by that
  *              projection's output rotation had_r_128(x, x, NULL, x_post_scale, 1.0)
  *              (src/modules.rs:231; x_post_scale is its f16 [dim] svh, or NULL); x is not written.
- * dim % 128 == 0; n_out in 1..4; outputs alias nothing.  Results are bit-identical to the unfused
- * calls.  Rows that are not 16-byte aligned run the unfused calls (the rotated x and the norm go
- * to y or to outs[0]).
+ *              | EXL3R_HAD_EXACT: see below.
+ * dim % 128 == 0; n_out in 1..4; outputs alias nothing.  The transforms run on the matrix cores, as
+ * exl3r_had_r_128_mfma: each result is the unfused calls' (exl3r_had_r_128) or its f16 neighbour, or
+ * within 2^-17 * r * sum|input| of it where the transform cancels.  With EXL3R_HAD_EXACT in rotate_x
+ * the transforms are the reference's butterfly and the results are bit-identical to the unfused
+ * calls.  Rows that are not 16-byte aligned run the unfused calls (the rotated x and the norm go to y
+ * or to outs[0]).
  */
 EXL3R_API int exl3r_rms_norm_had(const void* x, int x_dtype, int64_t ldx, const void* w, int w_dtype,
                        void* r, int r_dtype, int64_t ldr, void* y, int64_t ldy,
@@ -550,9 +573,15 @@ EXL3R_API int exl3r_rms_norm_had(const void* x, int x_dtype, int64_t ldx, const 
  *   rotate_in: bit 0 / bit 1 -- x / y (f16, the raw output of an EXL3 projection: gate_proj and up_proj
  *         in the MLP) is first given that projection's output rotation had_r_128(v, v, NULL, post, 1.0)
  *         (src/modules.rs:231) with post = x_post_scale / y_post_scale (f16 [cols] svh, or NULL); x and y
- *         are not written.  Needs 16-byte aligned rows.
+ *         are not written.  Needs 16-byte aligned rows.  | EXL3R_HAD_EXACT: see below.
  * x, y: [rows, cols] of in_dtype (F16/BF16/F32), row strides ldx, ldy; cols % 128 == 0; out and z
- * alias nothing.  Bit-identical to the unfused calls; rows that are not 16-byte aligned run them.
+ * alias nothing.  Rows that are not 16-byte aligned run the unfused calls.
+ * The 128-point transforms run on the matrix cores (v_mfma_f32_16x16x32_f16: f16 operands, fp32
+ * sums grouped differently from the reference's butterfly).  Each f16 result of a transform is then
+ * the unfused call's result or its f16 neighbour, or within 2^-17 * r * sum|input| of it where the
+ * transform cancels (r = had_scale / sqrt(128), the sum over the 128 inputs of the block); zero
+ * results are +0.  With EXL3R_HAD_EXACT in rotate_in the transforms are the reference's fp32 butterfly
+ * and the results are bit-identical to the unfused calls.
  */
 EXL3R_API int exl3r_act_mul_had(int act, const void* x, const void* y, int in_dtype, int64_t ldx, int64_t ldy,
                       void* z, int64_t ldz, const void* pre_scale, void* out, int64_t ldo,

@@ -76,3 +76,37 @@ def assert_bitwise(got, exp, what=""):
     same = np.array_equal(np.ascontiguousarray(got).view(np.uint8), np.ascontiguousarray(exp).view(np.uint8))
     print(f"{what}: bitwise={'yes' if same else 'NO'}")
     assert same, what
+
+
+def had_abs_tol(xin, r):
+    """Per element: 2^-17 * |r| * (sum of |input| over the element's 128-block), xin [rows, cols] floats.
+    The matrix-core and butterfly fp32 transforms are each within a few 2^-24 * sum|input| of the exact
+    one (32-term MFMA sums plus 2 stages, against 7 butterfly stages), so their difference before the f16
+    rounding is well inside this."""
+    a = np.abs(np.asarray(xin, np.float64))
+    rows, cols = a.shape
+    s = a.reshape(rows, cols // 128, 128).sum(-1)
+    return np.repeat(2.0 ** -17 * abs(r) * s, 128, axis=1)
+
+
+def assert_had_close(got, exp, xin, r, what="", min_exact=0.98, max_ulp=1):
+    """Matrix-core Hadamard results against the butterfly's (f16 storage [rows, cols]): each element is
+    the same value (+0 and -0 equal), within max_ulp f16 steps (1: the neighbour; 2 after an f16
+    post-scale product, which rounds a second time), or within had_abs_tol (where the transform
+    cancels); NaN only where the other is NaN; and at least min_exact of the elements are identical."""
+    got = np.ascontiguousarray(got)
+    exp = np.ascontiguousarray(exp)
+    g = orc.to_f32(got, orc.F16).astype(np.float64)
+    e = orc.to_f32(exp, orc.F16).astype(np.float64)
+    d = ulp_dist(got, exp, orc.F16)
+    with np.errstate(invalid="ignore"):
+        diff = np.abs(g - e)
+        ok = (d <= max_ulp) | (diff <= had_abs_tol(xin, r))
+    same = d == 0
+    bad = int((~ok).sum())
+    stats = (f"{what}: identical={same.mean():.6f} neighbour={np.mean(d == 1):.6f} "
+             f"beyond_neighbour={np.mean(d > 1):.6f} outside_tolerance={bad}")
+    print(stats)
+    assert bad == 0, stats
+    assert same.mean() >= min_exact, stats
+

@@ -402,7 +402,8 @@ int main()
         auto r = upload(rh, DType::F32, { rows, dim }, s);
         auto w = upload(wh, DType::F16, { dim }, s);
         auto o0 = OwnedTensor::empty(DType::F16, { rows, dim }), o1 = OwnedTensor::empty(DType::F16, { rows, dim });
-        ffi::rms_norm_had(x.t, &w.t, &r.t, nullptr, { &o0.t, &o1.t }, { &suh.t, nullptr }, 1e-6f, 0.f, 1.f, 1.f, s);
+        ffi::rms_norm_had(x.t, &w.t, &r.t, nullptr, { &o0.t, &o1.t }, { &suh.t, nullptr }, 1e-6f, 0.f, 1.f, 1.f, s,
+                          false, nullptr, true);
         std::vector<uint8_t> ey(xh.size()), er = rh, e0(xh.size()), e1(xh.size());
         oracle_rms_norm(xh.data(), OR_F16, dim, wh.data(), OR_F16, ey.data(), OR_F16, dim, er.data(), OR_F32, dim, rows, dim,
                         1e-6f, 0.f, 1.f, 1);
@@ -414,7 +415,8 @@ int main()
         auto gh = host_normal(DType::F16, rows * dim, 0.f, 2.f);
         auto g = upload(gh, DType::F16, { rows, dim }, s);
         auto z = OwnedTensor::empty(DType::F16, { rows, dim }), hz = OwnedTensor::empty(DType::F16, { rows, dim });
-        ffi::act_mul_had(ffi::HadAct::Silu, g.t, x.t, hz.t, &suh.t, &z.t, 0.f, 1.f, s);
+        ffi::act_mul_had(ffi::HadAct::Silu, g.t, x.t, hz.t, &suh.t, &z.t, 0.f, 1.f, s, false, false, nullptr, nullptr,
+                         true);
         auto zh = download(z, s);
         std::vector<uint8_t> ez(zh.size()), ehz(zh.size());
         oracle_act_mul(0, gh.data(), xh.data(), OR_F16, ez.data(), OR_F16, rows, dim, dim, dim, dim, 0.f, 1);

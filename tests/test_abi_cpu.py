@@ -291,6 +291,12 @@ def test_hadamard_validation():
     assert lib.exl3r_had_r_128(FAKE, F16, 256, FAKE + 8192, 256, 2, 256, FAKE, FAKE, 1.0, None) == exl3r.EINVAL
     assert "at most one" in _err()
     assert lib.exl3r_had_r_128(None, F16, 256, None, 256, 0, 256, None, None, 1.0, None) == exl3r.OK
+    # the matrix-core form: f16 only, same shape and scale checks
+    assert lib.exl3r_had_r_128_mfma(FAKE, F32, 256, FAKE + 8192, 256, 2, 256, None, None, 1.0, None) == exl3r.EDTYPE
+    assert lib.exl3r_had_r_128_mfma(FAKE, F16, 200, FAKE + 8192, 200, 2, 200, None, None, 1.0, None) == exl3r.EINVAL
+    assert lib.exl3r_had_r_128_mfma(FAKE, F16, 256, FAKE + 8192, 256, 2, 256, FAKE, FAKE, 1.0, None) == exl3r.EINVAL
+    assert "exl3r_had_r_128_mfma" in _err()
+    assert lib.exl3r_had_r_128_mfma(None, F16, 256, None, 256, 0, 256, None, None, 1.0, None) == exl3r.OK
 
     arr = ctypes.c_void_p * 4
     outs, pres = arr(FAKE + 65536, FAKE + 131072, 0, 0), arr(0, 0, 0, 0)
@@ -306,6 +312,7 @@ def test_hadamard_validation():
     assert norm_had(xt=7) == exl3r.EDTYPE
     assert norm_had(rot=1, xt=BF16) == exl3r.EDTYPE and "rotate_x" in _err()
     assert norm_had(xpost=FAKE) == exl3r.EINVAL and "rotate_x" in _err()
+    assert norm_had(rot=2) == exl3r.EINVAL and "rotate_x" in _err()
     assert norm_had(outs=arr(FAKE, FAKE + 131072, 0, 0)) == exl3r.EINVAL and "alias" in _err()
     assert norm_had(outs=arr(FAKE + 65536, FAKE + 65536, 0, 0)) == exl3r.EINVAL and "alias" in _err()
     assert norm_had(rows=0) == exl3r.OK

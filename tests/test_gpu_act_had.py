@@ -1,6 +1,7 @@
 """GPU parity of exl3r_act_mul_had (the gated activation feeding the next EXL3 projection's
 random-Hadamard input rotation in one pass: silu_mul -> down_proj, src/modules.rs:932-940, and the
-Qwen3.5 attention gate -> o_proj).  The activation z is checked against the oracle at the
+Qwen3.5 attention gate -> o_proj), with EXL3R_HAD_EXACT (the reference's butterfly; the matrix-core
+default is covered by test_gpu_had_mfma.py).  The activation z is checked against the oracle at the
 activation's own tolerance (<= 1 ulp of f16); the projection input is checked bit for bit against
 the oracle's had_r_128 of that z, and against the unfused GPU calls (exl3r_silu_mul / gelu_mul /
 mul_sigmoid into an f16 z, then exl3r_had_r_128).  Covers the MLP prefill shape of Qwen3-32B, every
@@ -55,7 +56,7 @@ def run(act, rows, cols, it, limit=0.0, with_z=True, pre=True, had_scale=1.0, ld
     p = suh(cols, seed + 2) if pre else None
     z = torch.empty((rows, cols), device="cuda", dtype=torch.float16) if with_z else None
     out = torch.empty((rows, cols), device="cuda", dtype=torch.float16)
-    ffi.act_mul_had(act, x, y, out, p, z, limit, had_scale)
+    ffi.act_mul_had(act, x, y, out, p, z, limit, had_scale, exact=True)
     ez, eout = unfused(act, x, y, p, limit, had_scale)
     torch.cuda.synchronize()
     tag = f"{act}_had {rows}x{cols} in{it} L{limit} z{int(with_z)} pre{int(pre)} ld{ld} off{off}"
@@ -102,7 +103,7 @@ def run_rotated(act, rows, cols, rot_x, rot_y, posts=True, with_z=True, seed=0):
     ys = suh(cols, seed + 4) if rot_y and posts else None
     z = torch.empty((rows, cols), device="cuda", dtype=torch.float16) if with_z else None
     out = torch.empty((rows, cols), device="cuda", dtype=torch.float16)
-    ffi.act_mul_had(act, x, y, out, p, z, rotate_x=rot_x, rotate_y=rot_y, x_post_scale=xs, y_post_scale=ys)
+    ffi.act_mul_had(act, x, y, out, p, z, rotate_x=rot_x, rotate_y=rot_y, x_post_scale=xs, y_post_scale=ys, exact=True)
     rx, ry = x, y
     if rot_x:
         rx = torch.empty_like(x)
@@ -191,7 +192,7 @@ def test_rotated_inputs_zero_signs(act):
     p = torch.from_numpy(np.where(np.random.default_rng(33).random(cols) < 0.5, -1.0, 1.0).astype(np.float16)).cuda()
     z = torch.empty((rows, cols), device="cuda", dtype=torch.float16)
     out = torch.empty((rows, cols), device="cuda", dtype=torch.float16)
-    ffi.act_mul_had(act, x, y, out, p, z, rotate_x=True, rotate_y=True)
+    ffi.act_mul_had(act, x, y, out, p, z, rotate_x=True, rotate_y=True, exact=True)
     rx, ry = torch.empty_like(x), torch.empty_like(y)
     ffi.had_r_128(x, rx, None, None)
     ffi.had_r_128(y, ry, None, None)

@@ -1,5 +1,6 @@
-"""GPU parity of exl3r_rms_norm_had (RMSNorm, optionally with the residual add, feeding the
-random-Hadamard input rotation of up to four EXL3 projections in one pass) against the oracle
+"""GPU parity of exl3r_rms_norm_had with EXL3R_HAD_EXACT (RMSNorm, optionally with the residual add,
+feeding the random-Hadamard input rotation of up to four EXL3 projections in one pass; the matrix-core
+default is covered by test_gpu_had_mfma.py) against the oracle
 composition -- oracle_rms_norm to an f16 y, then oracle_had_r_128 per projection, after
 oracle_had_r_128(x, post=svh) when x is rotated on load -- bit for bit, and against the unfused GPU
 calls: the Qwen3 attention-input case (f16 x, f32 residual, three
@@ -38,7 +39,7 @@ def run(rows, dim, xt, rt=None, wt=F16, n_out=3, with_y=True, cb=0.0, had_scale=
     wh = from_dev(w)
     xsv = suh(dim, seed + 30) if rotate_x and svh else None
     ffi.rms_norm_had(x, w, outs, pres, 1e-6, cb, 1.0, r=r, y=y, had_scale=had_scale, rotate_x=rotate_x,
-                     x_post_scale=xsv)
+                     x_post_scale=xsv, exact=True)
     torch.cuda.synchronize()
     if rotate_x:      # the producer's output rotation, had_r_128(x, x, None, svh), before the norm
         xh = orc.had_r_128(xh, F16, post=from_dev(xsv) if xsv is not None else None, nthreads=NTHREADS)
@@ -99,7 +100,7 @@ def test_fused_equals_unfused_gpu_calls():
     w = dev_normal((dim,), 1, 0.1, F16, 8)
     pres = [suh(dim, 20 + i) for i in range(3)]
     fused = [torch.empty((rows, dim), device="cuda", dtype=torch.float16) for _ in range(3)]
-    ffi.rms_norm_had(x, w, fused, pres, 1e-6, r=r1)
+    ffi.rms_norm_had(x, w, fused, pres, 1e-6, r=r1, exact=True)
     y = torch.empty((rows, dim), device="cuda", dtype=torch.float16)
     ffi.rms_norm_res_in(x, w, y, r2, 1e-6)
     sep = [torch.empty_like(y) for _ in range(3)]
@@ -152,7 +153,7 @@ def test_zero_signs_of_the_rotations():
     y = torch.empty((rows, dim), device="cuda", dtype=torch.float16)
     outs = [torch.empty((rows, dim), device="cuda", dtype=torch.float16) for _ in range(3)]
     pres = [suh(dim, 50 + i) for i in range(3)]
-    ffi.rms_norm_had(x, w, outs, pres, 1e-6, 0.0, 1.0, y=y)
+    ffi.rms_norm_had(x, w, outs, pres, 1e-6, 0.0, 1.0, y=y, exact=True)
     torch.cuda.synchronize()
     ey = orc.rms_norm(xh.view(np.uint16), F16, from_dev(w), F16, F16, 1e-6, 0.0, 1.0, nthreads=NTHREADS)
     assert_bitwise(from_dev(y), ey, what="zero signs: y")
