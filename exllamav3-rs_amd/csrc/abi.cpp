@@ -109,6 +109,7 @@ extern "C" void exl3r_tune_rope_tok(int use, int hpl, int wgs_per_cu)
 
 extern "C" void exl3r_tune_rope_nx(int passes) { exl3r::tuning().rope_nx = passes; }
 extern "C" void exl3r_tune_rope_nx_run(int run) { exl3r::tuning().rope_nx_run = run; }
+extern "C" void exl3r_tune_rope_ss32(int on) { exl3r::tuning().rope_ss32 = on; }
 
 extern "C" void exl3r_tune_sample(int rows_min, int threads)
 {

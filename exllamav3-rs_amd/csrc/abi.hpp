@@ -84,6 +84,7 @@ struct Tuning
     int rope_wgs_per_cu = 0; // wave-per-token kernel: persistent grid of this many workgroups per CU (0: one token per wave)
     int rope_nx = 0;         // NeoX 128 kernel of 8 lanes per head: 0 auto, -1 never, 1..3 always with that many passes per wave
     int rope_nx_run = 0;     // ... consecutive items of one wave (a token's angles evaluated once per run; 0 auto)
+    int rope_ss32 = 0;       // ... head norm's sum of squares in fp32 (1) instead of fp64
     int sample_rows_min = 0; // argmax / Gumbel: rows from which a workgroup owns a row (0: 512)
     int sample_threads = 0;  // ... and its lanes (256, 512, 1024; 0: 256)
     int had_unroll = 0;      // Hadamard: 128-blocks per 16-lane group (1, 2, 4; 0: 1)

@@ -73,6 +73,8 @@ struct RopeArgs
     // Precomputed rotary pairs (exl3r_rope_cs): {cos, sin} * attn_factor of frequency t for token
     // tok is cst[tok * (R / 2) + t]; nullptr: evaluated from inv_freq or the angle table.
     const float2* cst;
+    // 8-lane kernel: the head norm's sum of squares in fp32 (1) instead of fp64 (sweep/test build only).
+    int ss32;
 };
 
 // Where a kernel takes its rotary pairs: evaluated from inv_freq[t] * pos, evaluated from the angle
@@ -908,13 +910,26 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
             unpack8<IO>(lo, fl);
             unpack8<IO>(hi, fh);
             // fp64 sum of squares (as rope_head: exact for 16-bit data, one rounding to fp32)
-            double ss = 0.0;
-            #pragma unroll
-            for (int j = 0; j < 8; ++j) ss = fma((double)fl[j], (double)fl[j], ss);
-            #pragma unroll
-            for (int j = 0; j < 8; ++j) ss = fma((double)fh[j], (double)fh[j], ss);
-            ss = group_sum64<8>(ss);
-            const float mean = (float)ss * a.inv_hd;     // head_dim 128: an exact multiply
+            float mean;
+            if (a.ss32)
+            {
+                float s32 = 0.0f;
+                #pragma unroll
+                for (int j = 0; j < 8; ++j) s32 = fmaf(fl[j], fl[j], s32);
+                #pragma unroll
+                for (int j = 0; j < 8; ++j) s32 = fmaf(fh[j], fh[j], s32);
+                mean = group_sum<8>(s32) * a.inv_hd;
+            }
+            else
+            {
+                double ss = 0.0;
+                #pragma unroll
+                for (int j = 0; j < 8; ++j) ss = fma((double)fl[j], (double)fl[j], ss);
+                #pragma unroll
+                for (int j = 0; j < 8; ++j) ss = fma((double)fh[j], (double)fh[j], ss);
+                ss = group_sum64<8>(ss);
+                mean = (float)ss * a.inv_hd;     // head_dim 128: an exact multiply
+            }
             const float rmf = 1.0f / sqrtf(mean + a.eps);
             const int wo = (isq ? 0 : 128) + e0;
             if constexpr (NORM == NORM_HALF)
@@ -1493,6 +1508,9 @@ static int rope_prepare(const char* op, RopeArgs& a, const void* q, void* out_q,
     a.qw = q_norm; a.kw = k_norm; a.wt = norm_dtype;
     a.eps = norm_eps; a.cb = norm_constant_bias; a.attn = attn_factor;
     a.inv_hd = (head_dim & (head_dim - 1)) == 0 ? 1.0f / (float)head_dim : 0.0f;
+#ifdef EXL3R_TUNING
+    a.ss32 = tuning().rope_ss32;
+#endif
     return EXL3R_OK;
 }
 

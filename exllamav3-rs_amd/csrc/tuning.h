@@ -30,6 +30,8 @@ EXL3R_API void exl3r_tune_rope_nx(int passes);
 /* the same kernel: items (8-head passes) a wave takes in a row, its token's angles evaluated once per
  * token within them (1..16; 0 auto) */
 EXL3R_API void exl3r_tune_rope_nx_run(int run);
+/* the same kernel: the head norm's sum of squares in fp32 (1) instead of fp64 (0) */
+EXL3R_API void exl3r_tune_rope_ss32(int on);
 /* argmax / Gumbel sampling: rows from which a workgroup owns a whole row (0: 512), and its lanes (256, 512, 1024) */
 EXL3R_API void exl3r_tune_sample(int rows_min, int threads);
 /* Hadamard: 128-blocks per 16-lane group (1, 2, 4; 0 auto) */
