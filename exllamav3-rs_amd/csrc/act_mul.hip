@@ -62,22 +62,18 @@ __device__ __forceinline__ float act_mul1(float g, float u, float limit)
     return a * u;
 }
 
-// act_chunk with one wave-uniform test: when no lane's chunk has an element in act_f's tail (|t| > 64,
-// |x| > 44 for SiLU), every element takes act_f_short -- the operations act_f performs there, without
-// the tail's selects -- else act_f.  The results are act_chunk's in both cases.  The whole wave must
-// reach it.
+// act_chunk with one wave-uniform test: when no lane's chunk has an element in act_f's tail (t > 64,
+// x < -44.4 for SiLU), every element takes act_f_short -- the operations act_f performs there, without
+// the tail's selects -- else act_f.  The results are act_chunk's in both cases (a NaN t takes the same
+// operations on either path; fmaxf drops it from the chunk's maximum).  The whole wave must reach it.
 template <int ACT, class OT, bool LIMIT>
 __device__ __forceinline__ void act_chunk_wave(const float (&g)[8], const float (&u)[8], float limit, float (&o)[8])
 {
     float t[8];
-    bool tail = false;
     #pragma unroll
-    for (int j = 0; j < 8; ++j)
-    {
-        t[j] = act_t<ACT>(g[j]);
-        tail |= !(fabsf(t[j]) <= 64.0f);
-    }
-    if (__builtin_amdgcn_ballot_w64(tail) == 0)
+    for (int j = 0; j < 8; ++j) t[j] = act_t<ACT>(g[j]);
+    const float tmax = fmaxf(fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3])), fmaxf(fmaxf(t[4], t[5]), fmaxf(t[6], t[7])));
+    if (__builtin_amdgcn_ballot_w64(tmax > 64.0f) == 0)
     {
         #pragma unroll
         for (int j = 0; j < 8; ++j)

@@ -353,10 +353,12 @@ __device__ __forceinline__ float rms_factor(float sum, int n, float eps)
 // ---------------------------------------------------------------------------------------------
 // Activations in fp32, each a product m * sigmoid(z): SiLU m = x, z = x; GELU(tanh) m = x,
 // z = 2 sqrt(2/pi) (x + 0.044715 x^3) (0.5 (1 + tanh(u)) = sigmoid(2u), no 1 + tanh cancellation for
-// x << 0); SIGMOID m = 1, z = x.  With e^-z = 2^t, sigmoid = q for t <= 0 and p * q for t > 0, where
-// p = 2^-|t| in (0, 1] and q = 1 / (1 + p).  For |t| > 64 (where 1 + p == 1) p is evaluated as
-// 2^(64 - |t|) and the 2^-64 is applied to the final product, so tail results keep full precision
-// down into the fp32 denormals instead of flushing inside v_exp_f32.
+// x << 0); SIGMOID m = 1, z = x.  With e^-z = 2^t, sigmoid = 1 / (1 + 2^t): one v_exp_f32 and one
+// v_rcp_f32, both within 1 ulp, for any t <= 64 (2^t normal or below 2^-64, where 1 + 2^t == 1; the
+// reciprocal's argument in [1, 2^64 + 1], its result normal).  For t > 64 (sigmoid < 2^-64, where
+// 1 / (1 + 2^t) == 2^-t to fp32 precision) 2^-t is evaluated as 2^(64 - t) and the 2^-64 is applied
+// to the final product, so tail results keep full precision down into the fp32 denormals instead of
+// flushing inside v_exp_f32.
 enum { ACT_SILU = 0, ACT_GELU = 1, ACT_SIGMOID = 2 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -371,13 +373,11 @@ __device__ __forceinline__ float act_t(float x)
     else return x * -kLog2e;
 }
 
-// act_f for a t with |t| <= 64 (no tail scaling): the same operations and results as act_f there.
+// act_f for a t <= 64 or NaN (no tail scaling): the same operations and results as act_f there.
 template <int ACT>
 __device__ __forceinline__ float act_f_short(float x, float t)
 {
-    const float p = __builtin_amdgcn_exp2f(-fabsf(t));
-    const float q = __builtin_amdgcn_rcpf(1.0f + p);
-    const float s = t <= 0.0f ? q : p * q;
+    const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
     return ACT == ACT_SIGMOID ? s : x * s;
 }
 
@@ -385,13 +385,11 @@ template <int ACT>
 __device__ __forceinline__ float act_f(float x)
 {
     const float t = act_t<ACT>(x);   // e^-z = 2^t
-    const float n = -fabsf(t);
-    const bool tail = n < -64.0f;
-    const float p = __builtin_amdgcn_exp2f(tail ? n + 64.0f : n);   // normal for n >= -190
-    const float q = __builtin_amdgcn_rcpf(1.0f + (tail ? 0.0f : p)); // argument in [1, 2]
-    const float s = t <= 0.0f ? q : p * q;
+    const bool tail = t > 64.0f;
+    const float e = __builtin_amdgcn_exp2f(tail ? 64.0f - t : t);   // tail: normal for t <= 190
+    const float s = tail ? e : __builtin_amdgcn_rcpf(1.0f + e);
     const float r = ACT == ACT_SIGMOID ? s : x * s;
-    return (tail && t > 0.0f) ? r * 0x1p-64f : r;
+    return tail ? r * 0x1p-64f : r;
 }
 
 // CLAMP_FP16: +-inf -> +-65504, NaN -> 65504 (v_min/v_max return the non-NaN operand).
