@@ -119,11 +119,10 @@ extern "C" void exl3r_tune_sample(int rows_min, int threads)
 
 extern "C" void exl3r_tune_had(int blocks_per_group) { exl3r::tuning().had_unroll = blocks_per_group; }
 
-extern "C" void exl3r_tune_had_mfma(int unroll, int blocks_per_cu, int cached)
+extern "C" void exl3r_tune_had_mfma(int unroll, int blocks_per_cu)
 {
     exl3r::tuning().had_mfma_unroll = unroll;
     exl3r::tuning().had_mfma_per_cu = blocks_per_cu;
-    exl3r::tuning().had_mfma_cached = cached;
 }
 
 extern "C" void exl3r_tune_embed(int threads) { exl3r::tuning().embed_threads = threads; }

@@ -88,9 +88,8 @@ struct Tuning
     int sample_rows_min = 0; // argmax / Gumbel: rows from which a workgroup owns a row (0: 512)
     int sample_threads = 0;  // ... and its lanes (256, 512, 1024; 0: 256)
     int had_unroll = 0;      // Hadamard: 128-blocks per 16-lane group (1, 2, 4; 0: 1)
-    int had_mfma_unroll = 0; // matrix-core Hadamard kernels: spans per wave in flight (1, 2, 4; 0: 2)
-    int had_mfma_per_cu = 0; // ... workgroups per CU of the looping grid (0: 8; < 0: one span group per wave, no cap)
-    int had_mfma_cached = 0; // ... 1: cached input loads instead of non-temporal ones
+    int had_mfma_unroll = 0; // matrix-core Hadamard kernels: spans (act-mul: rows of a span) per wave in flight (1, 2, 4; 0: 2)
+    int had_mfma_per_cu = 0; // ... workgroups per CU of a looping grid (0: the kernel's default; < 0: one item per wave, no cap)
     int embed_threads = 0;
 };
 #ifdef EXL3R_TUNING

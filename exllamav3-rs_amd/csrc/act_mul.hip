@@ -62,14 +62,16 @@ __device__ __forceinline__ float act_mul1(float g, float u, float limit)
     return a * u;
 }
 
-// act_chunk with one wave-uniform test: when no lane's chunk has an element in act_f's tail (t > 64,
-// x < -44.4 for SiLU), every element takes act_f_short -- the operations act_f performs there, without
-// the tail's selects -- else act_f.  The results are act_chunk's in both cases (a NaN t takes the same
-// operations on either path; fmaxf drops it from the chunk's maximum).  The whole wave must reach it.
-template <int ACT, class OT, bool LIMIT>
-__device__ __forceinline__ void act_chunk_wave(const float (&g)[8], const float (&u)[8], float limit, float (&o)[8])
+// act_chunk to f16, packed, with one wave-uniform test: when no lane's chunk has an element in act_f's
+// tail (t > 64, x < -44.4 for SiLU), every element takes act_f_short -- the operations act_f performs
+// there, without the tail's selects -- else act_f.  The results are act_chunk's in both cases (a NaN t
+// takes the same operations on either path; fmaxf drops it from the chunk's maximum).  Each path packs
+// its own results, so that the clamp's negation folds into the conversion.  The whole wave must reach
+// it.
+template <int ACT, bool LIMIT>
+__device__ __forceinline__ TF16::Vec act_chunk_wave_f16(const float (&g)[8], const float (&u)[8], float limit)
 {
-    float t[8];
+    float t[8], n[8];
     #pragma unroll
     for (int j = 0; j < 8; ++j) t[j] = act_t<ACT>(g[j]);
     const float tmax = fmaxf(fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3])), fmaxf(fmaxf(t[4], t[5]), fmaxf(t[6], t[7])));
@@ -86,21 +88,13 @@ __device__ __forceinline__ void act_chunk_wave(const float (&g)[8], const float 
                 if (v > limit) v = limit;
                 if (a > limit) a = limit;
             }
-            float p = a * v;
-            if constexpr (OT::code == DT_F16) p = clamp_f16(p);
-            o[j] = p;
+            n[j] = -nclamp_f16(a * v);
         }
+        return pack8<TF16>(n);
     }
-    else
-    {
-        #pragma unroll
-        for (int j = 0; j < 8; ++j)
-        {
-            float p = act_mul1<ACT, LIMIT>(g[j], u[j], limit);
-            if constexpr (OT::code == DT_F16) p = clamp_f16(p);
-            o[j] = p;
-        }
-    }
+    #pragma unroll
+    for (int j = 0; j < 8; ++j) n[j] = -nclamp_f16(act_mul1<ACT, LIMIT>(g[j], u[j], limit));
+    return pack8<TF16>(n);
 }
 
 template <int ACT, class OT, bool LIMIT>
@@ -272,97 +266,99 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
 }
 
 // The activation -> Hadamard kernels with the transforms on the matrix cores (had128_mfma, hadamard.cuh).
-// A wave takes spans of 64 chunks (4 blocks) of a row, lane l holding chunk mfma_chunk(l) of its span;
-// the spans of the whole tensor (rows * spans_per_row, counted in 32 bits) are dealt to the waves of
-// the grid in turn, UNROLL spans per wave in flight.  Loop bounds are wave-uniform, so every MFMA runs
-// with the whole wave; lanes past a row's last block carry zeros and store nothing.  Same rounding
-// points as the butterfly kernel (hadamard.cuh documents how the transform's sums may differ).
-template <int ACT, class IT, int HAD, bool LIMIT, int UNROLL, bool CACHED = false>
+// A wave takes a span of 64 chunks (4 blocks) in UNROLL consecutive rows, lane l holding chunk
+// mfma_chunk(l) of the span in each row; the (row group, span) items of the tensor (counted in 32 bits)
+// are dealt to the waves of the grid in turn.  The span's scale chunks are loaded once for its rows.
+// Every access goes through a row's bounded buffer descriptor, so the chunks past a row's last block
+// (whole blocks: cols is a multiple of 128) and the rows past the last one load zeros and store
+// nothing, with no per-lane branch; loop bounds are wave-uniform, so every MFMA runs with the whole
+// wave.  Same rounding points as the butterfly kernel (hadamard.cuh documents how the transform's sums
+// may differ).
+template <int ACT, class IT, int HAD, bool LIMIT, int UNROLL>
 __global__ __launch_bounds__(256) void k_act_mul_had_mfma(ActArgs a)
 {
     static_assert((HAD & AH_OUT) != 0, "the input rotations come with the output rotation");
+    constexpr bool IN_X = (HAD & AH_IN_X) != 0, IN_Y = (HAD & AH_IN_Y) != 0;
+    static_assert(!(IN_X || IN_Y) || IT::code == DT_F16, "input rotations take f16 x and y");
     const int lane = threadIdx.x & 63;
     const uint32_t cpr = (uint32_t)(a.cols >> 3);
     const uint32_t spr = (cpr + 63) >> 6;
-    const uint32_t nspans = (uint32_t)a.rows * spr;
-    // wave-uniform span and row indices (scalar registers: the row bases are scalar, the lane offsets
-    // 32-bit)
+    const uint32_t rows = (uint32_t)a.rows;
+    const uint32_t items = ((rows + UNROLL - 1) / UNROLL) * spr;
+    const uint32_t in_bytes = (uint32_t)a.cols * IT::bytes, out_bytes = (uint32_t)a.cols * 2;
+    // wave-uniform item, row and span indices (scalar registers: the descriptors are scalar)
     const uint32_t wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const uint32_t nwaves = (gridDim.x * blockDim.x) >> 6;
     const HadMfma H = had_mfma_operands(lane);
     const uint32_t lc = (uint32_t)mfma_chunk(lane);
-    for (uint32_t s0 = wave * UNROLL; s0 < nspans; s0 += nwaves * UNROLL)
+    const brsrc xpost = row_rsrc(a.xpost, a.xpost ? out_bytes : 0), ypost = row_rsrc(a.ypost, a.ypost ? out_bytes : 0);
+    const brsrc hpre = row_rsrc(a.hpre, a.hpre ? out_bytes : 0);
+    for (uint32_t it = wave; it < items; it += nwaves)
     {
+        const uint32_t rg = it / spr, sp = it - rg * spr;
+        const uint32_t c = sp * 64 + lc;                                  // the lane's chunk in each row
+        const uint32_t off_in = c * (8 * IT::bytes), off16 = c * 16;     // its byte offsets
         typename IT::Vec xv[UNROLL], yv[UNROLL];
-        uint32_t row[UNROLL], c[UNROLL];
-        bool live[UNROLL];
+        brsrc zr[UNROLL], hr[UNROLL];
         #pragma unroll
         for (int u = 0; u < UNROLL; ++u)
         {
-            const uint32_t sp = s0 + u;
-            row[u] = sp / spr;
-            c[u] = (sp - row[u] * spr) * 64 + lc;
-            live[u] = sp < nspans && c[u] < cpr;
-            if (live[u])
-            {
-                if constexpr (CACHED)
-                {
-                    xv[u] = load8<IT>((const char*)a.x + (int64_t)row[u] * a.ldx * IT::bytes, (int64_t)c[u] * 8);
-                    yv[u] = load8<IT>((const char*)a.y + (int64_t)row[u] * a.ldy * IT::bytes, (int64_t)c[u] * 8);
-                }
-                else
-                {
-                    xv[u] = load8s<IT>((const char*)a.x + (int64_t)row[u] * a.ldx * IT::bytes, (int64_t)c[u] * 8);
-                    yv[u] = load8s<IT>((const char*)a.y + (int64_t)row[u] * a.ldy * IT::bytes, (int64_t)c[u] * 8);
-                }
-            }
-            else
-            {
-                const float zf[8] = {};
-                xv[u] = pack8<IT>(zf);
-                yv[u] = pack8<IT>(zf);
-            }
+            const uint32_t row = rg * UNROLL + u;
+            const bool in = row < rows;
+            const int64_t r = in ? row : 0;
+            xv[u] = bload8s<IT>(row_rsrc((const char*)a.x + r * a.ldx * IT::bytes, in ? in_bytes : 0), off_in);
+            yv[u] = bload8s<IT>(row_rsrc((const char*)a.y + r * a.ldy * IT::bytes, in ? in_bytes : 0), off_in);
+            zr[u] = row_rsrc((char*)a.z + r * a.ldz * 2, in && a.z ? out_bytes : 0);
+            hr[u] = row_rsrc((char*)a.hout + r * a.ldh * 2, in ? out_bytes : 0);
         }
-        if constexpr ((HAD & (AH_IN_X | AH_IN_Y)) != 0)
+        TF16::Vec px, py, pp;
+        if constexpr (IN_X) px.a = bload16(xpost, off16);
+        if constexpr (IN_Y) py.a = bload16(ypost, off16);
+        if (a.hpre) pp.a = bload16(hpre, off16);
+        if constexpr (IN_X || IN_Y)
         {
-            // the input rotations of every span in flight, their MFMAs issued together
-            static_assert(IT::code == DT_F16, "input rotations take f16 x and y");
-            constexpr int NX = (HAD & AH_IN_X) != 0 ? UNROLL : 0, NY = (HAD & AH_IN_Y) != 0 ? UNROLL : 0;
-            TF16::Vec v[NX + NY];
-            const void* post[NX + NY];
-            int64_t col[NX + NY];
+            // the input rotations of every row in flight, their MFMAs issued together; each transform,
+            // one rounding to f16, then the half post-scale
+            constexpr int NX = IN_X ? UNROLL : 0, NY = IN_Y ? UNROLL : 0;
+            MfmaOut m[NX + NY];
             #pragma unroll
             for (int u = 0; u < UNROLL; ++u)
             {
-                if constexpr (NX) { v[u] = xv[u]; post[u] = live[u] ? a.xpost : nullptr; col[u] = (int64_t)c[u] * 8; }
-                if constexpr (NY) { v[NX + u] = yv[u]; post[NX + u] = live[u] ? a.ypost : nullptr; col[NX + u] = (int64_t)c[u] * 8; }
+                if constexpr (IN_X) m[u] = had128_mfma_issue(H, xv[u]);
+                if constexpr (IN_Y) m[NX + u] = had128_mfma_issue(H, yv[u]);
             }
-            output_rotations_mfma<NX + NY>(H, v, post, col, lane);
+            mfma_wait_all(m);
+            auto finish = [&](const MfmaOut& mo, const TF16::Vec& p, bool on) {
+                float f[8];
+                had128_mfma_finish(mo, f, lane, 0.0883883461356163f);
+                TF16::Vec v = pack8<TF16>(f);
+                if (on)
+                {
+                    #pragma unroll
+                    for (int q = 0; q < 4; ++q) v.a[q] = hmul2(v.a[q], p.a[q]);
+                }
+                return v;
+            };
             #pragma unroll
             for (int u = 0; u < UNROLL; ++u)
             {
-                if constexpr (NX) xv[u] = v[u];
-                if constexpr (NY) yv[u] = v[NX + u];
+                if constexpr (IN_X) xv[u] = finish(m[u], px, a.xpost != nullptr);
+                if constexpr (IN_Y) yv[u] = finish(m[NX + u], py, a.ypost != nullptr);
             }
         }
         MfmaOut m[UNROLL];
         #pragma unroll
         for (int u = 0; u < UNROLL; ++u)
         {
-            float g[8], v[8], o[8];
+            float g[8], v[8];
             unpack8<IT>(xv[u], g);
             unpack8<IT>(yv[u], v);
-            act_chunk_wave<ACT, TF16, LIMIT>(g, v, a.limit, o);
-            TF16::Vec hv = pack8<TF16>(o);
-            if (live[u])
+            TF16::Vec hv = act_chunk_wave_f16<ACT, LIMIT>(g, v, a.limit);
+            if (a.z) bstore16(zr[u], off16, hv.a);
+            if (a.hpre)
             {
-                if (a.z) store8<TF16>((char*)a.z + (int64_t)row[u] * a.ldz * 2, (int64_t)c[u] * 8, hv);
-                if (a.hpre)
-                {
-                    const TF16::Vec p = load8<TF16>(a.hpre, (int64_t)c[u] * 8);
-                    #pragma unroll
-                    for (int q = 0; q < 4; ++q) hv.a[q] = hmul2(hv.a[q], p.a[q]);
-                }
+                #pragma unroll
+                for (int q = 0; q < 4; ++q) hv.a[q] = hmul2(hv.a[q], pp.a[q]);
             }
             m[u] = had128_mfma_issue(H, hv);
         }
@@ -372,7 +368,7 @@ __global__ __launch_bounds__(256) void k_act_mul_had_mfma(ActArgs a)
         {
             float f[8];
             had128_mfma_finish(m[u], f, lane, a.hr);
-            if (live[u]) store8<TF16>((char*)a.hout + (int64_t)row[u] * a.ldh * 2, (int64_t)c[u] * 8, pack8<TF16>(f));
+            bstore16(hr[u], off16, pack8<TF16>(f).a);
         }
     }
 }
@@ -492,22 +488,20 @@ static void launch_act_vec(const ActArgs& a, hipStream_t s)
     }
 }
 
-// Grid of the matrix-core kernel: one wave per UNROLL spans, no cap (kHadMfmaBlocksPerCu <= 0).  MI355X,
-// [8192, 17408] f16, median of interleaved runs (us): SiLU -> input rotation 140.1 with UNROLL 2 and no
-// cap, 153.7 UNROLL 1; a looping grid of 8 workgroups per CU 160.1, 16 per CU 153.3, 4 per CU 178.4;
-// cached instead of non-temporal input loads 146.9.  With both input rotations: 187.1 / 205.5 / 207.8 /
-// 194.4 / 246.6 / 198.8.
+// Grid of the matrix-core kernel: one wave per item (a span in UNROLL rows), no cap
+// (kHadMfmaBlocksPerCu <= 0); the tuning build sweeps UNROLL and a looping grid of that many workgroups
+// per CU.
 constexpr int kHadMfmaBlocksPerCu = -1;
 
-template <int ACT, class IT, int HAD, int UNROLL, bool CACHED>
+template <int ACT, class IT, int HAD, int UNROLL>
 static void launch_act_had_mfma_u(const ActArgs& a, int per_cu, hipStream_t s)
 {
-    const int64_t spans = a.rows * ((a.cols / 8 + 63) / 64);
-    int64_t blocks = (spans + 4 * UNROLL - 1) / (4 * UNROLL);
+    const int64_t items = (a.rows + UNROLL - 1) / UNROLL * ((a.cols / 8 + 63) / 64);
+    int64_t blocks = (items + 3) / 4;
     if (per_cu > 0 && blocks > (int64_t)per_cu * device_cus()) blocks = (int64_t)per_cu * device_cus();
     if (blocks > kMaxGridX) blocks = kMaxGridX;
-    if (a.limit != 0.0f) launch(k_act_mul_had_mfma<ACT, IT, HAD, true, UNROLL, CACHED>, (unsigned)blocks, 256, 0, s, a);
-    else launch(k_act_mul_had_mfma<ACT, IT, HAD, false, UNROLL, CACHED>, (unsigned)blocks, 256, 0, s, a);
+    if (a.limit != 0.0f) launch(k_act_mul_had_mfma<ACT, IT, HAD, true, UNROLL>, (unsigned)blocks, 256, 0, s, a);
+    else launch(k_act_mul_had_mfma<ACT, IT, HAD, false, UNROLL>, (unsigned)blocks, 256, 0, s, a);
 }
 
 template <int ACT, class IT, int HAD>
@@ -516,16 +510,11 @@ static void launch_act_had_mfma(const ActArgs& a, hipStream_t s)
 #ifdef EXL3R_TUNING
     const Tuning& tu = tuning();
     const int per_cu = tu.had_mfma_per_cu != 0 ? tu.had_mfma_per_cu : kHadMfmaBlocksPerCu;   // <= 0: no cap
-    const bool cached = tu.had_mfma_cached != 0;
-    auto go = [&](auto C) {
-        if (tu.had_mfma_unroll == 1) launch_act_had_mfma_u<ACT, IT, HAD, 1, decltype(C)::value>(a, per_cu, s);
-        else if (tu.had_mfma_unroll == 4) launch_act_had_mfma_u<ACT, IT, HAD, 4, decltype(C)::value>(a, per_cu, s);
-        else launch_act_had_mfma_u<ACT, IT, HAD, 2, decltype(C)::value>(a, per_cu, s);
-    };
-    if (cached) go(std::true_type{});
-    else go(std::false_type{});
+    if (tu.had_mfma_unroll == 1) launch_act_had_mfma_u<ACT, IT, HAD, 1>(a, per_cu, s);
+    else if (tu.had_mfma_unroll == 4) launch_act_had_mfma_u<ACT, IT, HAD, 4>(a, per_cu, s);
+    else launch_act_had_mfma_u<ACT, IT, HAD, 2>(a, per_cu, s);
 #else
-    launch_act_had_mfma_u<ACT, IT, HAD, 2, false>(a, kHadMfmaBlocksPerCu, s);
+    launch_act_had_mfma_u<ACT, IT, HAD, 2>(a, kHadMfmaBlocksPerCu, s);
 #endif
 }
 
@@ -567,9 +556,9 @@ static int act_had_entry(const char* op, const void* x, const void* y, int it, i
     const bool vec = aligned16(x) && aligned16(y) && aligned16(out) && (!z || aligned16(z)) && (!pre || aligned16(pre)) &&
                      (!x_post || aligned16(x_post)) && (!y_post || aligned16(y_post)) &&
                      (lx * eb) % 16 == 0 && (ly * eb) % 16 == 0 && (lo * 2) % 16 == 0 && (lz * 2) % 16 == 0;
-    // The matrix-core transforms unless the caller asks for the reference's butterfly; spans are counted
-    // in 32 bits.
-    const bool mfma = !exact && rows * ((cols / 8 + 63) / 64) < ((int64_t)1 << 31);
+    // The matrix-core transforms unless the caller asks for the reference's butterfly; items are counted
+    // in 32 bits, and a row's bytes in a buffer descriptor's 32-bit length.
+    const bool mfma = !exact && rows * ((cols / 8 + 63) / 64) < ((int64_t)1 << 31) && cols * eb < ((int64_t)1 << 31);
     if (vec && mfma)
     {
         ActArgs a{ x, y, z, lx, ly, lz, rows, cols, limit, pre, out, lo, had_scale * 0.0883883461356163f, x_post, y_post };

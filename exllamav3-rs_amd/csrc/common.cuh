@@ -174,6 +174,34 @@ template <> __device__ __forceinline__ void store8c<TF32>(void* base, int64_t e,
     p[1] = v.b;
 }
 
+// Buffer accesses through a bounded descriptor: a row's base and its length in bytes.  A 16-byte load
+// whose offset is at or past the length returns zeros and such a store writes nothing, so lanes and
+// rows past the data need neither a branch nor a clamped address.  dword 3 = 0x00020000 (32-bit data
+// format, raw addressing) for gfx9 (CDNA) buffer descriptors.  Offsets are 32-bit: rows under 4 GB.
+typedef __amdgpu_buffer_rsrc_t brsrc;
+constexpr int kBufNT = 2;   // cache policy bits of a non-temporal access (the nt bit)
+__device__ __forceinline__ brsrc row_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload16(brsrc r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
+__device__ __forceinline__ u32x4 bload16s(brsrc r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufNT);
+}
+__device__ __forceinline__ void bstore16(brsrc r, uint32_t off, u32x4 v)
+{
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kBufNT);
+}
+// A chunk of 8 elements at byte offset off (8 * es bytes: one access, or two for f32).
+template <class T> __device__ __forceinline__ typename T::Vec bload8s(brsrc r, uint32_t off)
+{
+    typename T::Vec v;
+    v.a = bload16s(r, off);
+    if constexpr (T::bytes == 4) v.b = bload16s(r, off + 16);
+    return v;
+}
+
 // Split chunks: the 8 elements of a chunk are the quads at e and e + kSplitGap, each one 8-byte (16-bit
 // data) or 16-byte (f32) access.  With lane l of a wave taking the quads at 4 l and 256 + 4 l of a
 // 512-element span, each wave-wide access of an operand covers one contiguous range: 512 B, or 1 KB for
@@ -392,8 +420,18 @@ __device__ __forceinline__ float act_f(float x)
     return tail ? r * 0x1p-64f : r;
 }
 
-// CLAMP_FP16: +-inf -> +-65504, NaN -> 65504 (v_min/v_max return the non-NaN operand).
-__device__ __forceinline__ float clamp_f16(float v) { return fmaxf(-65504.0f, fminf(v, 65504.0f)); }
+// CLAMP_FP16: +-inf -> +-65504, NaN -> 65504, the results of max(-65504, min(v, 65504)) with IEEE
+// min / max (which return the non-NaN operand), in one instruction: -med3(-v, -65504, 65504).
+// v_med3_f32 returns the min3 of its operands when one is NaN (-65504 here), so NaN maps to +65504;
+// -0 and +0 pass through with their signs.  Inline assembly, because the compiler folds the two
+// negations away (med3(v, 65504, -65504)), which would map NaN to -65504.
+__device__ __forceinline__ float nclamp_f16(float v)   // -CLAMP_FP16(v)
+{
+    float c;
+    asm("v_med3_f32 %0, -%1, -%2, %2" : "=v"(c) : "v"(v), "s"(65504.0f));
+    return c;
+}
+__device__ __forceinline__ float clamp_f16(float v) { return -nclamp_f16(v); }
 
 // ---------------------------------------------------------------------------------------------
 // Reductions.

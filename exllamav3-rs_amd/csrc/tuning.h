@@ -36,9 +36,9 @@ EXL3R_API void exl3r_tune_rope_ss32(int on);
 EXL3R_API void exl3r_tune_sample(int rows_min, int threads);
 /* Hadamard: 128-blocks per 16-lane group (1, 2, 4; 0 auto) */
 EXL3R_API void exl3r_tune_had(int blocks_per_group);
-/* matrix-core Hadamard kernels: spans per wave in flight (1, 2, 4; 0 auto), workgroups per CU of the looping
- * grid (0 auto, < 0 one span group per wave), cached input loads (1) */
-EXL3R_API void exl3r_tune_had_mfma(int unroll, int blocks_per_cu, int cached);
+/* matrix-core Hadamard kernels: spans (act-mul: rows of a span) per wave in flight (1, 2, 4; 0 auto),
+ * workgroups per CU of a looping grid (0 auto, < 0 one item per wave) */
+EXL3R_API void exl3r_tune_had_mfma(int unroll, int blocks_per_cu);
 EXL3R_API void exl3r_tune_embed(int threads);
 #ifdef __cplusplus
 }

@@ -104,7 +104,7 @@ TUNE_PROTOTYPES = {
     "exl3r_tune_rope_ss32": (None, [_i]),
     "exl3r_tune_sample": (None, [_i, _i]),
     "exl3r_tune_had": (None, [_i]),
-    "exl3r_tune_had_mfma": (None, [_i, _i, _i]),
+    "exl3r_tune_had_mfma": (None, [_i, _i]),
     "exl3r_tune_embed": (None, [_i]),
 }
 
@@ -184,7 +184,7 @@ def tuned():
         lib.exl3r_tune_rope_ss32(0)
         lib.exl3r_tune_sample(0, 0)
         lib.exl3r_tune_had(0)
-        lib.exl3r_tune_had_mfma(0, 0, 0)
+        lib.exl3r_tune_had_mfma(0, 0)
         lib.exl3r_tune_embed(0)
         _lib = saved
 
