@@ -97,6 +97,52 @@ __device__ __forceinline__ TF16::Vec act_chunk_wave_f16(const float (&g)[8], con
     return pack8<TF16>(n);
 }
 
+// The same from the input chunks as loaded.  SiLU of f16 x and u without act_limit takes its three
+// products by x and u straight from the packed pairs (mul_f16_f32: the exact conversion and one fp32
+// rounding, as the product of the unpacked values), so the short path converts nothing; the results are
+// act_chunk_wave_f16's.
+template <int ACT, bool LIMIT, class IT>
+__device__ __forceinline__ TF16::Vec act_chunk_wave_in(const typename IT::Vec& xv, const typename IT::Vec& yv, float limit)
+{
+    if constexpr (ACT == ACT_SILU && !LIMIT && IT::code == DT_F16)
+    {
+        float t[8], n[8];
+        #pragma unroll
+        for (int j = 0; j < 8; j += 2)
+        {
+            t[j] = mul_f16_f32<false>(xv.a[j / 2], -kLog2e);
+            t[j + 1] = mul_f16_f32<true>(xv.a[j / 2], -kLog2e);
+        }
+        const float tmax = fmaxf(fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3])), fmaxf(fmaxf(t[4], t[5]), fmaxf(t[6], t[7])));
+        if (__builtin_amdgcn_ballot_w64(tmax > 64.0f) == 0)
+        {
+            #pragma unroll
+            for (int j = 0; j < 8; j += 2)
+            {
+                const float s0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t[j]));
+                const float s1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t[j + 1]));
+                // s0, s1 come straight from v_rcp_f32 (a transcendental): the first reads wait a state
+                n[j] = -nclamp_f16(mul_f16_f32<false>(yv.a[j / 2], mul_f16_f32<false, true>(xv.a[j / 2], s0)));
+                n[j + 1] = -nclamp_f16(mul_f16_f32<true>(yv.a[j / 2], mul_f16_f32<true, true>(xv.a[j / 2], s1)));
+            }
+            return pack8<TF16>(n);
+        }
+        float g[8], u[8];
+        unpack8<IT>(xv, g);
+        unpack8<IT>(yv, u);
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) n[j] = -nclamp_f16(act_mul1<ACT, LIMIT>(g[j], u[j], limit));
+        return pack8<TF16>(n);
+    }
+    else
+    {
+        float g[8], u[8];
+        unpack8<IT>(xv, g);
+        unpack8<IT>(yv, u);
+        return act_chunk_wave_f16<ACT, LIMIT>(g, u, limit);
+    }
+}
+
 template <int ACT, class OT, bool LIMIT>
 __device__ __forceinline__ void act_chunk(const float (&g)[8], const float (&u)[8], float limit, float (&o)[8])
 {
@@ -350,10 +396,7 @@ __global__ __launch_bounds__(256) void k_act_mul_had_mfma(ActArgs a)
         #pragma unroll
         for (int u = 0; u < UNROLL; ++u)
         {
-            float g[8], v[8];
-            unpack8<IT>(xv[u], g);
-            unpack8<IT>(yv[u], v);
-            TF16::Vec hv = act_chunk_wave_f16<ACT, LIMIT>(g, v, a.limit);
+            TF16::Vec hv = act_chunk_wave_in<ACT, LIMIT, IT>(xv[u], yv[u], a.limit);
             if (a.z) bstore16(zr[u], off16, hv.a);
             if (a.hpre)
             {

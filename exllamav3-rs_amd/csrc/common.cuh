@@ -81,11 +81,18 @@ __device__ __forceinline__ _Float16 to_f16(float v) { return (_Float16)opaque(v)
 // fl32(h * c) for the f16 element h in the low (HI = false) or high half of a packed pair and an fp32 c,
 // in one instruction: the mixed-precision fma converts h exactly and adds -0, which leaves every
 // product as the fp32 multiply rounds it (x * c + -0 = x * c, signed zeros included).
-template <bool HI>
+// The compiler's hazard handling does not see the operands of inline assembly: a c just written by a
+// transcendental instruction (v_exp, v_rcp, v_sqrt, ...) needs one wait state before it is read (without
+// it the previous value of the register is read), which AFTER_TRANS = true puts in front.
+template <bool HI, bool AFTER_TRANS = false>
 __device__ __forceinline__ float mul_f16_f32(uint32_t pair, float c)
 {
     float r;
-    if constexpr (HI)
+    if constexpr (AFTER_TRANS && HI)
+        asm("s_nop 0\nv_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(c), "s"(-0.0f));
+    else if constexpr (AFTER_TRANS)
+        asm("s_nop 0\nv_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(c), "s"(-0.0f));
+    else if constexpr (HI)
         asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(c), "s"(-0.0f));
     else
         asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(c), "s"(-0.0f));
@@ -425,6 +432,8 @@ __device__ __forceinline__ float act_f(float x)
 // v_med3_f32 returns the min3 of its operands when one is NaN (-65504 here), so NaN maps to +65504;
 // -0 and +0 pass through with their signs.  Inline assembly, because the compiler folds the two
 // negations away (med3(v, 65504, -65504)), which would map NaN to -65504.
+// v must not come straight from a transcendental instruction (see mul_f16_f32: the wait state the
+// compiler would put in front of a read of it is not put in front of inline assembly).
 __device__ __forceinline__ float nclamp_f16(float v)   // -CLAMP_FP16(v)
 {
     float c;
