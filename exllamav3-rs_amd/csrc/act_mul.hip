@@ -62,14 +62,14 @@ __device__ __forceinline__ float act_mul1(float g, float u, float limit)
     return a * u;
 }
 
-// act_chunk to f16, packed, with one wave-uniform test: when no lane's chunk has an element in act_f's
-// tail (t > 64, x < -44.4 for SiLU), every element takes act_f_short -- the operations act_f performs
-// there, without the tail's selects -- else act_f.  The results are act_chunk's in both cases (a NaN t
-// takes the same operations on either path; fmaxf drops it from the chunk's maximum).  Each path packs
-// its own results, so that the clamp's negation folds into the conversion.  The whole wave must reach
-// it.
-template <int ACT, bool LIMIT>
-__device__ __forceinline__ TF16::Vec act_chunk_wave_f16(const float (&g)[8], const float (&u)[8], float limit)
+// act_chunk packed to OT, with one wave-uniform test: when no active lane's chunk has an element in
+// act_f's tail (t > 64, x < -44.4 for SiLU), every element takes act_f_short -- the operations act_f
+// performs there, without the tail's selects -- else act_f.  The results are act_chunk's in both
+// cases (a NaN t takes the same operations on either path; fmaxf drops it from the chunk's maximum).
+// Each path packs its own results, so that the f16 clamp's negation folds into the conversion.
+// Lanes outside the exec mask take no part in the test.
+template <int ACT, class OT, bool LIMIT>
+__device__ __forceinline__ typename OT::Vec act_pack_wave(const float (&g)[8], const float (&u)[8], float limit)
 {
     float t[8], n[8];
     #pragma unroll
@@ -88,13 +88,23 @@ __device__ __forceinline__ TF16::Vec act_chunk_wave_f16(const float (&g)[8], con
                 if (v > limit) v = limit;
                 if (a > limit) a = limit;
             }
-            n[j] = -nclamp_f16(a * v);
+            n[j] = OT::code == DT_F16 ? -nclamp_f16(a * v) : a * v;
         }
-        return pack8<TF16>(n);
+        return pack8<OT>(n);
     }
     #pragma unroll
-    for (int j = 0; j < 8; ++j) n[j] = -nclamp_f16(act_mul1<ACT, LIMIT>(g[j], u[j], limit));
-    return pack8<TF16>(n);
+    for (int j = 0; j < 8; ++j)
+    {
+        const float p = act_mul1<ACT, LIMIT>(g[j], u[j], limit);
+        n[j] = OT::code == DT_F16 ? -nclamp_f16(p) : p;
+    }
+    return pack8<OT>(n);
+}
+
+template <int ACT, bool LIMIT>
+__device__ __forceinline__ TF16::Vec act_chunk_wave_f16(const float (&g)[8], const float (&u)[8], float limit)
+{
+    return act_pack_wave<ACT, TF16, LIMIT>(g, u, limit);
 }
 
 // The same from the input chunks as loaded.  SiLU of f16 x and u without act_limit takes its three
@@ -198,12 +208,12 @@ __global__ __launch_bounds__(256) void k_act_mul(ActArgs a)
                     const int64_t c = base + (int64_t)u * nt;
                     if (c < cpr)
                     {
-                        float g[8], v[8], o[8];
+                        float g[8], v[8];
                         unpack8<IT>(xv[u], g);
                         unpack8<IT>(yv[u], v);
-                        act_chunk<ACT, OT, LIMIT>(g, v, a.limit, o);
-                        if constexpr (SPLIT) store8_split<OT>(zr, chunk_elem<true>(c), pack8<OT>(o));
-                        else store8<OT>(zr, c * 8, pack8<OT>(o));
+                        const typename OT::Vec o = act_pack_wave<ACT, OT, LIMIT>(g, v, a.limit);
+                        if constexpr (SPLIT) store8_split<OT>(zr, chunk_elem<true>(c), o);
+                        else store8<OT>(zr, c * 8, o);
                     }
                 }
             }
@@ -445,11 +455,11 @@ __global__ __launch_bounds__(256) void k_act_mul_short(ActArgs a)
         for (int u = 0; u < UNROLL; ++u)
         {
             if (base + u * nt >= n) continue;
-            float g[8], v[8], o[8];
+            float g[8], v[8];
             unpack8<IT>(xv[u], g);
             unpack8<IT>(yv[u], v);
-            act_chunk<ACT, OT, LIMIT>(g, v, a.limit, o);
-            store8<OT>((char*)a.z + (int64_t)r[u] * a.ldz * OT::bytes, (int64_t)c[u] * 8, pack8<OT>(o));
+            store8<OT>((char*)a.z + (int64_t)r[u] * a.ldz * OT::bytes, (int64_t)c[u] * 8,
+                       act_pack_wave<ACT, OT, LIMIT>(g, v, a.limit));
         }
     }
 }
