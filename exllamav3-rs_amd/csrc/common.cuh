@@ -19,6 +19,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// __builtin_bit_cast(T, vec[i]) of an element of one of these vectors reads element 0 with this
+// compiler (the element lvalue is lowered as the vector's own address): every bit_cast here takes a
+// value, e.g. (uint32_t)vec[i].
 
 // ---------------------------------------------------------------------------------------------
 // dtype tags.  Each tag loads/stores chunks of 8 consecutive elements; F16/BF16 chunks are one

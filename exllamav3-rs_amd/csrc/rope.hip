@@ -324,7 +324,7 @@ __device__ __forceinline__ void rope_head(const RopeArgs& a, typename IO::Vec& v
             for (int i = 0; i < 4; ++i)
             {
                 const f16x2 n2 = { to_f16(f[2 * i] * rmf), to_f16(f[2 * i + 1] * rmf) };
-                v.a[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, w.a[i]) * n2);
+                v.a[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, (uint32_t)w.a[i]) * n2);
             }
         }
         else

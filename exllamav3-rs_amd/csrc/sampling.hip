@@ -178,6 +178,58 @@ struct LaneBest
     __device__ __forceinline__ uint64_t key() const { return has ? cand_key(v, i) : 0; }
 };
 
+// f16 logits without noise: a lane keeps its best chunk of 8 instead of its best element.  The chunk's
+// maximum cm comes from NaN-propagating packed maxima (v_pk_maximum3_f16: a NaN anywhere in the chunk
+// makes cm NaN); the chunk replaces the held one when it is the lane's first chunk, when cm is larger
+// (-0 and +0 compare equal, so the earlier chunk stays), or when cm is the first NaN (a NaN best is
+// final).  The held chunk's data is kept and its element found once at the end: the first one equal
+// to the maximum, or the first NaN when the maximum is NaN, which is the element LaneBest keeps over
+// the same elements in the same order.  Per 8 elements: 3 maxima, 3 compares and 6 selects instead of
+// 8 x LaneBest::consider.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+struct LaneBestF16
+{
+    _Float16 m = 0;
+    uint32_t c = 0;     // first element of the held chunk
+    u32x4 d = {};       // its data
+    bool has = false;
+
+    // FIRST: the lane's first chunk (taken unconditionally).
+    template <bool FIRST>
+    __device__ __forceinline__ void consider8(const u32x4& w, uint32_t c0)
+    {
+        // (uint32_t) casts: the operand of a bit_cast must be a value, not a vector element -- this
+        // compiler lowers __builtin_bit_cast of an ext_vector element lvalue as a read of element 0.
+        const f16x2 p = __builtin_elementwise_maximum(
+            __builtin_elementwise_maximum(__builtin_bit_cast(f16x2, (uint32_t)w[0]), __builtin_bit_cast(f16x2, (uint32_t)w[1])),
+            __builtin_elementwise_maximum(__builtin_bit_cast(f16x2, (uint32_t)w[2]), __builtin_bit_cast(f16x2, (uint32_t)w[3])));
+        const _Float16 cm = __builtin_elementwise_maximum(p[0], p[1]);
+        const bool take = FIRST || (cm > m) || ((cm != cm) & (m == m));
+        m = take ? cm : m;
+        c = take ? c0 : c;
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) d[q] = take ? w[q] : d[q];
+        has = FIRST || has;
+    }
+
+    __device__ __forceinline__ LaneBest lane_best() const
+    {
+        LaneBest lb;
+        int j = 7;
+        #pragma unroll
+        for (int q = 7; q >= 0; --q)
+        {
+            const _Float16 x = __builtin_bit_cast(f16x2, (uint32_t)d[q >> 1])[q & 1];
+            j = ((x == m) | ((x != x) & (m != m))) ? q : j;
+        }
+        lb.v = (float)m;
+        lb.i = c + (uint32_t)j;
+        lb.has = has;
+        return lb;
+    }
+};
+
 template <int CTRL>
 __device__ __forceinline__ uint64_t dpp_u64(uint64_t v)
 {
@@ -229,12 +281,29 @@ __device__ __forceinline__ uint64_t slice_lane_key(const ArgArgs& a, int64_t row
         const int64_t c = start + u * 2048 + tid * 8;
         if (VEC && c + 8 <= a.n) v[u] = load8s<IT>(base, c);
     }
+    if constexpr (VEC && IT::code == DT_F16 && !GUMBEL)
+    {
+        // whole chunks by LaneBestF16 (a chunk is whole only when every earlier one of the lane is)
+        LaneBestF16 hb;
+        #pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+        {
+            const int64_t c = start + u * 2048 + tid * 8;
+            if (c + 8 <= a.n)
+            {
+                if (u == 0) hb.consider8<true>(v[u].a, (uint32_t)c);
+                else hb.consider8<false>(v[u].a, (uint32_t)c);
+            }
+        }
+        lb = hb.lane_best();
+    }
     #pragma unroll
     for (int u = 0; u < UNROLL; ++u)
     {
         const int64_t c = start + u * 2048 + tid * 8;
         if (VEC && c + 8 <= a.n)
         {
+            if constexpr (IT::code == DT_F16 && !GUMBEL) continue;   // taken above
             float f[8];
             unpack8<IT>(v[u], f);
             candidates8<GUMBEL>(f, a, row, c);
@@ -327,7 +396,38 @@ __global__ __launch_bounds__(THREADS) void k_argmax_rows(ArgArgs a)
     {
         const char* base = a.x + row * a.ld;
         LaneBest lb;
-        for (int64_t s0 = 0; s0 < a.n; s0 += 4 * STEP)
+        if constexpr (VEC && IT::code == DT_F16 && !GUMBEL)
+        {
+            // whole chunks by LaneBestF16, then the elements of a partial last chunk (after every whole
+            // one) by the lane that holds it
+            const int64_t nw = a.n & ~(int64_t)7;
+            LaneBestF16 hb;
+            auto round = [&](int64_t s0, auto FIRST) __attribute__((always_inline)) {
+                u32x4 v[4];
+                #pragma unroll
+                for (int u = 0; u < 4; ++u)
+                {
+                    const int64_t c = s0 + u * STEP + tid * 8;
+                    if (c < nw) v[u] = load8s<TF16>(base, c).a;
+                }
+                #pragma unroll
+                for (int u = 0; u < 4; ++u)
+                {
+                    const int64_t c = s0 + u * STEP + tid * 8;
+                    if (c < nw)
+                    {
+                        if (decltype(FIRST)::value && u == 0) hb.consider8<true>(v[u], (uint32_t)c);
+                        else hb.consider8<false>(v[u], (uint32_t)c);
+                    }
+                }
+            };
+            if (nw > 0) round((int64_t)0, std::true_type{});
+            for (int64_t s0 = 4 * STEP; s0 < nw; s0 += 4 * STEP) round(s0, std::false_type{});
+            lb = hb.lane_best();
+            if (nw < a.n && tid * 8 == nw % STEP)
+                for (int64_t c = nw; c < a.n; ++c) lb.consider(load1(base, DT_F16, c), c);
+        }
+        else for (int64_t s0 = 0; s0 < a.n; s0 += 4 * STEP)
         {
             typename IT::Vec v[4];
             #pragma unroll
