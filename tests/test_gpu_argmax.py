@@ -80,3 +80,29 @@ def test_zero_rows():
     ids = torch.empty(0, dtype=torch.int64, device="cuda")
     ffi.argmax_sample(torch.empty((0, 100), device="cuda", dtype=torch.float16), ids)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("rows", [6, 130])
+def test_f16_chunk_path_special_values(rows):
+    """f16 logits take the chunk-wise path (packed NaN-propagating maxima per 8 logits, the held chunk
+    searched once): the element rule must still hold inside a chunk, across chunks and in a partial
+    last chunk, on both kernels (6 rows: sliced; 130: a workgroup per row)."""
+    n = 4104                                   # 513 whole chunks; masks below cut partial ones
+    x = np.full((rows, n), -3.0, np.float32)
+    x[0, [16, 17]] = [-0.0, 0.0]               # -0 then +0 in one chunk, both maximal -> 16
+    x[0, :16] = -1.0
+    x[1, [9, 40]] = [0.0, -0.0]                # +0 in an earlier chunk than -0 -> 9
+    x[2, [2, 11]] = [np.inf, np.nan]           # a NaN after an inf -> the NaN
+    x[3, [13, 4000, 4001]] = [np.nan, np.nan, np.nan]   # the first NaN
+    x[4, [7, 8]] = [5.0, 5.0]                  # equal maxima across a chunk boundary -> 7
+    x[5, [6, 5]] = [9.0, 9.0]                  # within one chunk -> 5
+    x[:, n - 1] = np.where(np.arange(rows) >= 6, 100.0, x[:, n - 1])  # rows >= 6: the last logit
+    bits = orc.to_bits(x, F16)
+    bits[3, 13] = 0xFE00                       # a negative-signed NaN is a NaN (still the first)
+    dev = to_dev(bits, F16)
+    run(dev, F16)
+    run(dev, F16, n - 3)                       # a partial last chunk, row maxima cut off
+    y = np.full((rows, n), -np.inf, np.float32)   # all -inf -> 0; one finite value in a partial chunk
+    y[1, 4100] = -70000.0                      # -inf in f16 after rounding: still all -inf -> 0
+    y[2, 4101] = 1.0
+    run(to_dev(orc.to_bits(y, F16), F16), F16, 4102)
