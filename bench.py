@@ -1081,9 +1081,10 @@ def pmc_kib(op, counter, timeout=120):
 
 
 def trace_step(steps, warmup, timeout=150):
-    """Each C3 step kernel's mean duration (us) inside the step sequence: a rocprofv3 --kernel-trace run of
+    """Each C3 step kernel's median duration (us) inside the step sequence: a rocprofv3 --kernel-trace run of
     `bench.py --op c3_step` (the three launches back to back, as in the timed step), the warmup launches
-    dropped.  None when the profiler is missing or the run fails."""
+    dropped (the median: one dispatch delayed by the profiler does not move it).  None when the profiler
+    is missing or the run fails."""
     exe = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
     if not os.path.exists(exe):
         return None
@@ -1108,7 +1109,7 @@ def trace_step(steps, warmup, timeout=150):
                     "gelu_c3" if "k_act_mul<1," in k else None
                 if n:
                     durs[n].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-        out = {n: statistics.mean(v[warmup:]) for n, v in durs.items() if len(v) > warmup}
+        out = {n: statistics.median(v[warmup:]) for n, v in durs.items() if len(v) > warmup}
         return out or None
 
 
@@ -1334,7 +1335,7 @@ def main():
     roof = {"bound": "hbm", "achieved": dom["gbs"], "peak": PEAK_GBS, "unit": "GB/s", "frac": dom["frac"],
             "traffic": None, "kernel": f"{dom['kernel']} ({dom_name})", "bytes_per_launch": dom["bytes"],
             "timing": "HIP events on the launch stream over back-to-back launches of the kernel (us); its "
-                      "duration inside the step sequence from a rocprofv3 kernel trace in this run (us_in_step); "
+                      "median duration inside the step sequence from a rocprofv3 kernel trace in this run (us_in_step); "
                       "the dominant kernel is the slowest " + ("in the step" if by == "us_in_step" else "alone"),
             "kernels": kernels}
     if not args.no_traffic:
