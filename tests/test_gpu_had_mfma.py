@@ -249,3 +249,34 @@ def test_norm_had_partial_spans():
     """dim 384: 3 blocks, so the last wave span of a row is part empty (those lanes carry zeros)."""
     run_norm(33, 384, F16, F32, n_out=4, seed=64)
     run_norm(5, 128, F16, None, n_out=1, rotate_x=True, seed=65)
+
+
+@pytest.mark.parametrize("act,rot", [("silu", (True, True)), ("gelu", (False, False))])
+def test_strided_rows_padding_untouched(act, rot):
+    """Strided x, y, z and out (row strides past cols): the matrix-core kernel reaches every row through a
+    descriptor bounded at the row's bytes, so the padding columns keep their sentinel and every result
+    equals the contiguous call's, bit for bit -- also for an odd row count (a row group with a missing
+    row) and cols not a multiple of 512 (a span with missing blocks)."""
+    rows, cols, ld = 67, 1152, 1152 + 72
+    sentinel = 0x7E5A                                  # an f16 NaN pattern no result takes
+
+    def padded(v):
+        t = torch.full((rows, ld), 0.0, device="cuda", dtype=torch.float16)
+        t[:, :cols] = v
+        return t
+    x = dev_normal((rows, cols), 0, 2, F16, 91)
+    y = dev_normal((rows, cols), 0, 1, F16, 92)
+    p = suh(cols, 93)
+    ps = tuple(suh(cols, 94 + i) if rot[i] else None for i in range(2))
+    zc, oc = torch.empty_like(x), torch.empty_like(x)
+    ffi.act_mul_had(act, x, y, oc, p, zc, rotate_x=rot[0], rotate_y=rot[1], x_post_scale=ps[0], y_post_scale=ps[1])
+    xs, ys = padded(x), padded(y)
+    zs = torch.full((rows, ld), 0.0, device="cuda", dtype=torch.float16).view(torch.int16).fill_(sentinel).view(torch.float16)
+    os_ = torch.full((rows, ld), 0.0, device="cuda", dtype=torch.float16).view(torch.int16).fill_(sentinel).view(torch.float16)
+    ffi.act_mul_had(act, xs[:, :cols], ys[:, :cols], os_[:, :cols], p, zs[:, :cols], rotate_x=rot[0], rotate_y=rot[1],
+                    x_post_scale=ps[0], y_post_scale=ps[1])
+    torch.cuda.synchronize()
+    for name, got, exp in (("out", os_, oc), ("z", zs, zc)):
+        g = got.view(torch.int16).cpu().numpy()
+        assert (g[:, cols:] == sentinel).all(), f"{act} {name}: padding written"
+        assert_bitwise(np.ascontiguousarray(g[:, :cols]), from_dev(exp).view(np.int16), what=f"{act} {name} strided")
