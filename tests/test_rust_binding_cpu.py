@@ -261,3 +261,16 @@ def test_hip_externs_match_the_runtime_header():
             if rust_class(pt) != hip_class(ct):
                 bad.append(f"{name} arg {i} ({pn}): {pt} vs HIP's {ct}")
     assert not bad, "\n".join(bad)
+
+
+def test_every_header_constant_has_a_rust_const():
+    """Each integer #define EXL3R_<NAME> of the header has `pub const EXL3R_<NAME>: i32 = <same value>;` in the
+    binding (status codes, dtype codes, activations, rotary styles, the exact-Hadamard flag)."""
+    text = strip_c_comments(open(_lib.HEADER_PATH).read())
+    hdr = {n: int(v) for n, v in re.findall(r"#define\s+(EXL3R_[A-Z0-9_]+)\s+\(?(-?\d+)\)?\s*$", text, re.M)}
+    assert {"EXL3R_F16", "EXL3R_EINVAL", "EXL3R_ACT_GELU", "EXL3R_HAD_EXACT", "EXL3R_ROPE_NEOX"} <= set(hdr)
+    rs = {}
+    for block in rust_blocks():
+        rs.update({n: int(v) for n, v in re.findall(r"pub const (EXL3R_[A-Z0-9_]+):\s*i32\s*=\s*(-?\d+)\s*;", block)})
+    bad = [f"{n}: header {v}, binding {rs.get(n)}" for n, v in sorted(hdr.items()) if rs.get(n) != v]
+    assert not bad, "\n".join(bad)
