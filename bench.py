@@ -50,10 +50,10 @@ OPS = ["rms_c3", "rms_q3mix", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "
        "deinterleave_q35", "gated_norm_had_q35", "gated_norm_had_q35_unfused", "argmax_dec", "argmax_dec_torch", "argmax_dec_ws", "argmax_prefill", "argmax_prefill_torch",
        "gumbel_dec", "gumbel_dec_torch", "gumbel_dec_ws", "gumbel_prefill", "had_c3", "had_c3_mfma", "norm_had_c3",
        "norm_had_c3_exact", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_exact", "norm_had_rot_c3_unfused",
-       "silu_had_c3", "silu_had_c3_exact", "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_unfused", "rope_cs_c4", "rope_cs_table_c4",
+       "silu_had_c3", "silu_had_c3_exact", "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_exact", "rope_had_c4_unfused", "rope_cs_c4", "rope_cs_table_c4",
        "qg_rope_q35", "qg_rope_q35_unfused",
        "rope_kv_prefill_cs", "rope_kv_had_prefill_cs", "prefill_layer_cs",
-       "rope_kv_had_prefill", "rope_kv_had_prefill_unfused", "mlp_had_c3", "mlp_had_c3_exact", "mlp_had_c3_unfused",
+       "rope_kv_had_prefill", "rope_kv_had_prefill_exact", "rope_kv_had_prefill_unfused", "mlp_had_c3", "mlp_had_c3_exact", "mlp_had_c3_unfused",
        "prefill_layer", "prefill_layer_unfused", "calib_copy",
        "calib_copy_cached", "c3_step"]
 
@@ -167,11 +167,12 @@ def make_act(name, rows, cols, dt, act, seed):
     return Work(name, nbytes, launch, f"{act.upper()}(gate)*up [{rows},{cols}] {str(dt).split('.')[-1]}", sets)
 
 
-def make_rope_had(name, pos, hq, hk, hd, fused, seed=330):
+def make_rope_had(name, pos, hq, hk, hd, fused, seed=330, exact=False):
     """C4 prefill q/k on the raw f16 projection outputs: each projection's output rotation
     had_r_128(y, y, None, svh) (src/modules.rs:231), then head-norm + NeoX RoPE, in place.  One fused
-    launch (exl3r_rope_had), or two had_r_128 launches and exl3r_rope.  Both count the fused job's bytes
-    (C4's RoPE bytes plus both svh vectors)."""
+    launch (exl3r_rope_had; transforms on the matrix cores, or with exact the reference's butterfly), or
+    two had_r_128 launches and exl3r_rope.  Both count the fused job's bytes (C4's RoPE bytes plus both
+    svh vectors)."""
     import numpy as np
     import torch
     import exl3r
@@ -191,12 +192,12 @@ def make_rope_had(name, pos, hq, hk, hd, fused, seed=330):
         q, k = bufs[i % sets]
         if fused:
             ffi.rope_had(q, q, k, k, inv, 0, None, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, q_post_scale=qs,
-                         k_post_scale=ks, position_ids=pid)
+                         k_post_scale=ks, position_ids=pid, exact=exact)
         else:
             ffi.had_r_128(q.view(T, hq * hd), q.view(T, hq * hd), None, qs)
             ffi.had_r_128(k.view(T, hk * hd), k.view(T, hk * hd), None, ks)
             ffi.rope(q, q, k, k, inv, 0, None, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, position_ids=pid)
-    kind = "fused" if fused else "unfused (2 had_r_128 + rope)"
+    kind = ("fused, butterfly" if exact else "fused") if fused else "unfused (2 had_r_128 + rope)"
     return Work(name, nbytes, launch, f"q/k output rotation + head-norm + NeoX RoPE T={T} heads {hq}/{hk}, {kind}", sets)
 
 
@@ -324,12 +325,13 @@ def make_gather(name, vocab, hidden, n, dt, out_dt, ids, seed, norm=False):
     return Work(name, nbytes, launch, f"{desc}, {distinct} distinct ids", sets, hbm_bytes=hbm)
 
 
-def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64, had=False, cs=False):
+def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64, had=False, cs=False, exact=False):
     """q/k head-norm + NeoX RoPE followed by the paged KV-cache append (64 q / 8 kv heads of 128, f16,
     256-token pages, positions = cache lengths): one fused exl3r_rope_paged_kv launch, or exl3r_rope
     then a separate append kernel (the reference's two launches).  With had, q / k / v are the raw
     projection outputs and their output rotations had_r_128(y, y, None, svh) (src/modules.rs:231) come
-    first: one exl3r_rope_paged_kv_had launch, or three in-place rotations and the two launches.  With cs,
+    first: one exl3r_rope_paged_kv_had launch (transforms on the matrix cores, or with exact the
+    reference's butterfly), or three in-place rotations and the two launches.  With cs,
     the fused launch reads the forward pass's {cos, sin} table (exl3r_rope_cs_table, built once outside
     the timed launches) in place of evaluating sin / cos; its bytes count the table rows."""
     import numpy as np
@@ -363,7 +365,8 @@ def make_rope_kv(name, bsz, seq, fused, seed=400, max_blocks=64, had=False, cs=F
         q, k, v = bufs[i % sets]
         if had and fused:
             ffi.rope_paged_kv_had(q, q, k, k, v, inv, 0, sl, qn, kn, 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, kc, vc, bt, sl,
-                                  q_post_scale=sv[0], k_post_scale=sv[1], v_post_scale=sv[2], cs_table=table)
+                                  q_post_scale=sv[0], k_post_scale=sv[1], v_post_scale=sv[2], cs_table=table,
+                                  exact=exact)
             return
         if had:
             for t, p in zip((q, k, v), sv):
@@ -814,7 +817,10 @@ def make_all(only=None):
         "norm_had_rot_c3_unfused": lambda: make_norm_had("norm_had_rot_c3_unfused", 8192, 5120, False, rotate=True),
         "rope_kv_had_prefill": lambda: make_rope_kv("rope_kv_had_prefill", 1, 4096, True, had=True),
         "rope_kv_had_prefill_unfused": lambda: make_rope_kv("rope_kv_had_prefill_unfused", 1, 4096, False, had=True),
+        "rope_kv_had_prefill_exact": lambda: make_rope_kv("rope_kv_had_prefill_exact", 1, 4096, True, had=True,
+                                                          exact=True),
         "rope_had_c4": lambda: make_rope_had("rope_had_c4", ragged, 64, 8, 128, True),
+        "rope_had_c4_exact": lambda: make_rope_had("rope_had_c4_exact", ragged, 64, 8, 128, True, exact=True),
         "rope_had_c4_unfused": lambda: make_rope_had("rope_had_c4_unfused", ragged, 64, 8, 128, False),
         "prefill_layer": lambda: make_prefill_layer("prefill_layer", True),
         "prefill_layer_unfused": lambda: make_prefill_layer("prefill_layer_unfused", False),

@@ -499,6 +499,26 @@ __device__ __forceinline__ double group_sum64(double v)
     return v;
 }
 
+// v(l) + v(l ^ 16) in every lane l: v_permlane16_swap_b32 of v with itself hands both lanes of a pair
+// the pair's two values in the same order (the even row's first), so both get the same bits.  Both
+// lanes of a pair must be active.
+__device__ __forceinline__ float sum_xor16(float v)
+{
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (uint32_t)p[0]) + __builtin_bit_cast(float, (uint32_t)p[1]);
+}
+__device__ __forceinline__ double sum_xor16(double v)
+{
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)u, hi = (uint32_t)(u >> 32);
+    const auto pl = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto ph = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    const double a = __builtin_bit_cast(double, ((uint64_t)(uint32_t)ph[0] << 32) | (uint32_t)pl[0]);
+    const double b = __builtin_bit_cast(double, ((uint64_t)(uint32_t)ph[1] << 32) | (uint32_t)pl[1]);
+    return a + b;
+}
+
 // Full-wave sum, uniform result: row sums by DPP, then the four rows combined through readlane.
 __device__ __forceinline__ float wave_sum(float v)
 {

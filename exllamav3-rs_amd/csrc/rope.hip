@@ -749,13 +749,61 @@ __device__ __forceinline__ void rotate_head_nx(TF16::Vec& lo, TF16::Vec& hi, int
 
 // APPEND: v heads follow the k heads in the item space; k and v rows are written to the paged caches
 // (exl3r_rope_paged_kv).  HADR: every head is first replaced by its projection's output rotation
-// (exl3r_rope_had, exl3r_rope_paged_kv_had).  Both take one pass per item.
-// The rotating instances evaluating sin / cos land just above the five-wave budget (97 VGPRs of 96); they
-// are held to five waves per SIMD.
-template <bool APPEND, bool HADR, int SRC>
-constexpr int kNxMinWaves = HADR && SRC == SRC_FREQ ? 5 : 1;
+// (exl3r_rope_had, exl3r_rope_paged_kv_had), as the reference's butterfly (HADR_EXACT,
+// rotate_head_nx) or on the matrix cores (HADR_MFMA).  Both take one pass per item.
+// The rotating instances evaluating sin / cos, and the matrix-core ones reading the table, land just above
+// the five-wave budget (97-100 VGPRs of 96); they are held to five waves per SIMD.
+enum { HADR_NONE = 0, HADR_EXACT = 1, HADR_MFMA = 2 };
+template <bool APPEND, int HADR, int SRC>
+constexpr int kNxMinWaves = HADR && (SRC == SRC_FREQ || HADR == HADR_MFMA) ? 5 : 1;
 
-template <class IO, int MODE, int NORM, int SRC, bool QOUT, int P, bool APPEND = false, bool HADR = false>
+// Lane layouts of a pass (8 heads of 128, 16 elements per lane: the chunks [e0, e0 + 8) and
+// [e0 + 64, e0 + 72) of head grp, the NeoX pairs of the full rotary width side by side):
+//  - the 8-lane layout: head grp = lane bits 3-5, e0 = 8 * (lane bits 0-2);
+//  - the matrix-core layout (HADR_MFMA): head grp = lane bits 2, 3, 5, e0 = 8 * (lane bits 0, 1, 4).
+//    The items are loaded as two 4-head spans in had128_mfma's placement (slot s: head 4 s + lane bits
+//    2-3, chunk lane bits 0, 1, 4, 5 = index bits 3-6), transformed there, and moved to this layout by
+//    one v_permlane32_swap per word pair: the swap exchanges lane bit 5 (index bit 6) with the slot
+//    (head bit 2).  A head's 8 lanes are then lanes {0, 1, 4} of its group, so the head norm sums over
+//    lanes xor 1, 2 and 16.
+template <int HADR>
+__device__ __forceinline__ int nx_head_of_lane(int l64)
+{
+    return HADR == HADR_MFMA ? ((l64 >> 2) & 3) | ((l64 >> 3) & 4) : l64 >> 3;
+}
+template <int HADR>
+__device__ __forceinline__ int nx_e0_of_lane(int l64)
+{
+    return HADR == HADR_MFMA ? 8 * ((l64 & 3) | ((l64 >> 2) & 4)) : (l64 & 7) * 8;
+}
+
+// Sum over the 8 lanes of a head of a pass (every lane of the head gets the same bits).
+template <int HADR>
+__device__ __forceinline__ float nx_head_sum(float v)
+{
+    if constexpr (HADR == HADR_MFMA)
+    {
+        v += dpp<DPP_QUAD_XOR1>(v);
+        v += dpp<DPP_QUAD_XOR2>(v);
+        return sum_xor16(v);
+    }
+    else
+        return group_sum<8>(v);
+}
+template <int HADR>
+__device__ __forceinline__ double nx_head_sum(double v)
+{
+    if constexpr (HADR == HADR_MFMA)
+    {
+        v += dpp64<DPP_QUAD_XOR1>(v);
+        v += dpp64<DPP_QUAD_XOR2>(v);
+        return sum_xor16(v);
+    }
+    else
+        return group_sum64<8>(v);
+}
+
+template <class IO, int MODE, int NORM, int SRC, bool QOUT, int P, bool APPEND = false, int HADR = HADR_NONE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kNxMinWaves<APPEND, HADR, SRC>)))
 void k_rope_nx(RopeArgs a, int nslice, int run)
 {
@@ -769,8 +817,15 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t W = (int64_t)gridDim.x * 4;
     const int64_t items = a.tokens * nslice;
-    const int grp = l64 >> 3;                 // head of a pass held by this lane's group of 8
-    const int e0 = (l64 & 7) * 8;             // the lane's chunks: [e0, e0 + 8) and [e0 + 64, e0 + 72)
+    const int grp = nx_head_of_lane<HADR>(l64);   // head of a pass held by this lane
+    const int e0 = nx_e0_of_lane<HADR>(l64);      // the lane's chunks: [e0, e0 + 8) and [e0 + 64, e0 + 72)
+    constexpr bool MF = HADR == HADR_MFMA;
+    // had128_mfma's placement: the lane's chunk of each span (index bits 3-6 = lane bits 0, 1, 4, 5) and
+    // its head inside the span (lane bits 2-3).
+    const int mf_e = 8 * ((l64 & 3) | ((l64 >> 2) & 12));
+    const int mf_h = (l64 >> 2) & 3;
+    HadMfmaWords hw{};
+    if constexpr (MF) hw = had_mfma_words(l64);
     const int64_t q_hs = a.q_hs, k_hs = a.k_hs, q_ts = a.q_ts, k_ts = a.k_ts;
     const int64_t v_hs = APPEND ? a.v_hs : 0, v_ts = APPEND ? a.v_ts : 0;
     const int hq = a.hq, hk = a.hk, H = a.hq + a.hk + (APPEND ? a.hv : 0);
@@ -800,6 +855,19 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
     auto issue = [&](Item& t, int64_t item) __attribute__((always_inline)) {
         t.tok = item / nslice;
         t.slice = (int)(item - t.tok * nslice);
+        // The row of head h of token tok.
+        auto head_base = [&](int h) __attribute__((always_inline)) -> const char* {
+            if constexpr (APPEND)
+            {
+                const bool iq = h < hq, iv = h >= hq + hk;
+                const int hi = h - (iq ? 0 : hq) - (iv ? hk : 0);
+                const int64_t ts = pick_qkv(iq, iv, q_ts, k_ts, v_ts), hs = pick_qkv(iq, iv, q_hs, k_hs, v_hs);
+                return pick_qkv(iq, iv, qin, kin, vin) + (t.tok * ts + (int64_t)hi * hs) * IO::bytes;
+            }
+            else   // two choices: plain selects (the mask form costs this kernel ~0.5 us at C4)
+                return h < hq ? qin + (t.tok * q_ts + (int64_t)h * q_hs) * IO::bytes
+                              : kin + (t.tok * k_ts + (int64_t)(h - hq) * k_hs) * IO::bytes;
+        };
         #pragma unroll
         for (int p = 0; p < P; ++p)
         {
@@ -807,19 +875,16 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
             // head's lanes do (identical bytes to the same addresses), so every lane loads and stores
             // and no branch around a load or store makes the compiler's waits for the item's data cover
             // later loads too.
-            const int h = min((t.slice * P + p) * 8 + grp, H - 1);
+            if constexpr (MF)
             {
-                const char* base;
-                if constexpr (APPEND)
-                {
-                    const bool iq = h < hq, iv = h >= hq + hk;
-                    const int hi = h - (iq ? 0 : hq) - (iv ? hk : 0);
-                    const int64_t ts = pick_qkv(iq, iv, q_ts, k_ts, v_ts), hs = pick_qkv(iq, iv, q_hs, k_hs, v_hs);
-                    base = pick_qkv(iq, iv, qin, kin, vin) + (t.tok * ts + (int64_t)hi * hs) * IO::bytes;
-                }
-                else   // two choices: plain selects (the mask form costs this kernel ~0.5 us at C4)
-                    base = h < hq ? qin + (t.tok * q_ts + (int64_t)h * q_hs) * IO::bytes
-                                  : kin + (t.tok * k_ts + (int64_t)(h - hq) * k_hs) * IO::bytes;
+                // the two spans in had128_mfma's placement (lo: heads 0-3 of the pass, hi: heads 4-7)
+                const int h0 = t.slice * 8 + mf_h;
+                t.lo[p] = load8s<IO>(head_base(min(h0, H - 1)), mf_e);
+                t.hi[p] = load8s<IO>(head_base(min(h0 + 4, H - 1)), mf_e);
+            }
+            else
+            {
+                const char* base = head_base(min((t.slice * P + p) * 8 + grp, H - 1));
                 t.lo[p] = load8s<IO>(base, e0);
                 t.hi[p] = load8s<IO>(base, e0 + 64);
             }
@@ -883,13 +948,38 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
             const void* post = pick_qkv(isq, isv, qpost, kpost, vpost);
             const bool hp = post != nullptr;
             u32x4 pl = {}, ph = {};
-            if (hp)
+            auto load_post = [&]() __attribute__((always_inline)) {
+                if (hp)
+                {
+                    const _Float16* pp = (const _Float16*)post + (int64_t)hidx * 128 + e0;
+                    pl = *(const u32x4*)pp;
+                    ph = *(const u32x4*)(pp + 64);
+                }
+            };
+            if constexpr (!MF) load_post();
+            if constexpr (MF)
             {
-                const _Float16* pp = (const _Float16*)post + (int64_t)hidx * 128 + e0;
-                pl = *(const u32x4*)pp;
-                ph = *(const u32x4*)(pp + 64);
+                // Both spans' MFMAs, one wait, the two lane stages and the rounding to f16 (exl3r_had_r_128_mfma's
+                // operations on the same placement), then to the pass layout.
+                const HadMfma hm = had_mfma_rebuild(hw);
+                MfmaOut m0 = had128_mfma_issue(hm, lo), m1 = had128_mfma_issue(hm, hi);
+                mfma_wait(m0, m1);
+                float f[8];
+                had128_mfma_finish(m0, f, l64, 0.0883883461356163f);
+                lo = pack8<TF16>(f);
+                had128_mfma_finish(m1, f, l64, 0.0883883461356163f);
+                hi = pack8<TF16>(f);
+                #pragma unroll
+                for (int i = 0; i < 4; ++i)
+                {
+                    const auto w = __builtin_amdgcn_permlane32_swap((uint32_t)lo.a[i], (uint32_t)hi.a[i], false, false);
+                    lo.a[i] = w[0];
+                    hi.a[i] = w[1];
+                }
+                load_post();
             }
-            rotate_head_nx(lo, hi, l64 & 7);
+            else
+                rotate_head_nx(lo, hi, l64 & 7);
             if (hp)
             {
                 #pragma unroll
@@ -918,7 +1008,7 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
                 for (int j = 0; j < 8; ++j) s32 = fmaf(fl[j], fl[j], s32);
                 #pragma unroll
                 for (int j = 0; j < 8; ++j) s32 = fmaf(fh[j], fh[j], s32);
-                mean = group_sum<8>(s32) * a.inv_hd;
+                mean = nx_head_sum<HADR>(s32) * a.inv_hd;
             }
             else
             {
@@ -927,7 +1017,7 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
                 for (int j = 0; j < 8; ++j) ss = fma((double)fl[j], (double)fl[j], ss);
                 #pragma unroll
                 for (int j = 0; j < 8; ++j) ss = fma((double)fh[j], (double)fh[j], ss);
-                ss = group_sum64<8>(ss);
+                ss = nx_head_sum<HADR>(ss);
                 mean = (float)ss * a.inv_hd;     // head_dim 128: an exact multiply
             }
             const float rmf = 1.0f / sqrtf(mean + a.eps);
@@ -1156,7 +1246,7 @@ static bool rope_nx_ok(const RopeArgs& a, int rope_mode, bool had = false)
     return true;
 }
 
-template <class IO, int MODE, int NORM, int SRC, bool QOUT, int P, bool APPEND = false, bool HADR = false>
+template <class IO, int MODE, int NORM, int SRC, bool QOUT, int P, bool APPEND = false, int HADR = HADR_NONE>
 static void launch_rope_nx_p(const RopeArgs& a, hipStream_t s)
 {
     const int nslice = ((a.hq + a.hk + (APPEND ? a.hv : 0) + 7) / 8 + P - 1) / P;
@@ -1217,22 +1307,27 @@ static void launch_rope_nx(const RopeArgs& a, hipStream_t s)
     else launch_rope_nx_p<IO, MODE, NORM, SRC, QOUT, 1>(a, s);
 }
 
-// The output rotations (exl3r_rope_had, exl3r_rope_paged_kv_had) in the 8-lane kernel, f16 heads.
+// The output rotations (exl3r_rope_had, exl3r_rope_paged_kv_had) in the 8-lane kernel, f16 heads: on the
+// matrix cores, or (exact) as the reference's butterfly.
 template <int NORM>
-static void launch_had_nx(const RopeArgs& a, int rope_mode, hipStream_t s)
+static void launch_had_nx(const RopeArgs& a, int rope_mode, bool exact, hipStream_t s)
 {
-    auto go = [&](auto M) {
-        constexpr int MODE = decltype(M)::value;
+    auto go = [&](auto M, auto X) {
+        constexpr int MODE = decltype(M)::value, HADR = decltype(X)::value;
         if (a.kc)
         {
-            if (a.cst) launch_rope_nx_p<TF16, MODE, NORM, SRC_CS, false, 1, true, true>(a, s);
-            else launch_rope_nx_p<TF16, MODE, NORM, SRC_FREQ, false, 1, true, true>(a, s);
+            if (a.cst) launch_rope_nx_p<TF16, MODE, NORM, SRC_CS, false, 1, true, HADR>(a, s);
+            else launch_rope_nx_p<TF16, MODE, NORM, SRC_FREQ, false, 1, true, HADR>(a, s);
         }
-        else if (a.cst) launch_rope_nx_p<TF16, MODE, NORM, SRC_CS, false, 1, false, true>(a, s);
-        else launch_rope_nx_p<TF16, MODE, NORM, SRC_FREQ, false, 1, false, true>(a, s);
+        else if (a.cst) launch_rope_nx_p<TF16, MODE, NORM, SRC_CS, false, 1, false, HADR>(a, s);
+        else launch_rope_nx_p<TF16, MODE, NORM, SRC_FREQ, false, 1, false, HADR>(a, s);
     };
-    if (rope_mode == EXL3R_ROPE_GPTJ) go(std::integral_constant<int, EXL3R_ROPE_GPTJ>{});
-    else go(std::integral_constant<int, EXL3R_ROPE_NEOX>{});
+    auto with_mode = [&](auto X) {
+        if (rope_mode == EXL3R_ROPE_GPTJ) go(std::integral_constant<int, EXL3R_ROPE_GPTJ>{}, X);
+        else go(std::integral_constant<int, EXL3R_ROPE_NEOX>{}, X);
+    };
+    if (exact) with_mode(std::integral_constant<int, HADR_EXACT>{});
+    else with_mode(std::integral_constant<int, HADR_MFMA>{});
 }
 
 // Generic fallback (any even head_dim / rotary_dim, any alignment): one workgroup per token, heads
@@ -1740,6 +1835,8 @@ extern "C" int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, 
 {
     begin_call();
     const char* op = "exl3r_rope_had";
+    const bool exact = (rope_mode & EXL3R_HAD_EXACT) != 0;
+    rope_mode &= ~EXL3R_HAD_EXACT;
     if (dtype != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: the rotated projection outputs are f16", op);
     if (head_dim <= 0 || ((int64_t)num_heads_q * head_dim) % 128 || (k && ((int64_t)num_heads_k * head_dim) % 128))
         return set_error(EXL3R_EINVAL, "%s: heads * head_dim must be a multiple of 128", op);
@@ -1757,9 +1854,9 @@ extern "C" int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, 
     {
         hipStream_t s = (hipStream_t)stream;
         const int norm = rope_norm_kind(a, dtype);
-        if (norm == NORM_NONE) launch_had_nx<NORM_NONE>(a, rope_mode, s);
-        else if (norm == NORM_HALF) launch_had_nx<NORM_HALF>(a, rope_mode, s);
-        else launch_had_nx<NORM_F32>(a, rope_mode, s);
+        if (norm == NORM_NONE) launch_had_nx<NORM_NONE>(a, rope_mode, exact, s);
+        else if (norm == NORM_HALF) launch_had_nx<NORM_HALF>(a, rope_mode, exact, s);
+        else launch_had_nx<NORM_F32>(a, rope_mode, exact, s);
         return launch_status(op);
     }
     const bool fused = head_dim == 128 && rope_mode == EXL3R_ROPE_NEOX && rope_vec_ok(a, rope_mode) &&
@@ -1811,6 +1908,8 @@ extern "C" int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok
 {
     begin_call();
     const char* op = "exl3r_rope_paged_kv_had";
+    const bool exact = (rope_mode & EXL3R_HAD_EXACT) != 0;
+    rope_mode &= ~EXL3R_HAD_EXACT;
     if (dtype != EXL3R_F16) return set_error(EXL3R_EDTYPE, "%s: the rotated projection outputs are f16", op);
     if (head_dim <= 0 || ((int64_t)num_heads_q * head_dim) % 128 || ((int64_t)num_heads_kv * head_dim) % 128)
         return set_error(EXL3R_EINVAL, "%s: heads * head_dim must be a multiple of 128", op);
@@ -1829,9 +1928,9 @@ extern "C" int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok
     {
         hipStream_t s = (hipStream_t)stream;
         const int norm = rope_norm_kind(a, dtype);
-        if (norm == NORM_NONE) launch_had_nx<NORM_NONE>(a, rope_mode, s);
-        else if (norm == NORM_HALF) launch_had_nx<NORM_HALF>(a, rope_mode, s);
-        else launch_had_nx<NORM_F32>(a, rope_mode, s);
+        if (norm == NORM_NONE) launch_had_nx<NORM_NONE>(a, rope_mode, exact, s);
+        else if (norm == NORM_HALF) launch_had_nx<NORM_HALF>(a, rope_mode, exact, s);
+        else launch_had_nx<NORM_F32>(a, rope_mode, exact, s);
         return launch_status(op);
     }
     auto a16 = [](const void* p) { return p == nullptr || aligned16(p); };
@@ -1982,9 +2081,13 @@ extern "C" int exl3r_rope_run(const exl3r_rope_desc* d, void* stream)
     if (own_layout && (d->rotate || d->k_cache || d->angle_table || d->cs_table))
         return set_error(EXL3R_EINVAL, "%s: an out_q layout of its own is the q | g split only (inv_freq, no cache, no rotation)", op);
     const int64_t hd = d->head_dim;
+    if (d->rotate != 0 && d->rotate != 1 && d->rotate != (1 | EXL3R_HAD_EXACT))
+        return set_error(EXL3R_EINVAL, "%s: rotate takes 0, 1 or 1 | EXL3R_HAD_EXACT", op);
     if (d->rotate)
     {
-        // The rotating forms take packed heads (head stride = head_dim).
+        // The rotating forms take packed heads (head stride = head_dim); EXL3R_HAD_EXACT goes to their
+        // rope_mode.
+        const int mode = d->rope_mode | (d->rotate & EXL3R_HAD_EXACT);
         if (d->q_head_stride != hd || (d->k && d->k_head_stride != hd) || (d->v && d->v_head_stride != hd))
             return set_error(EXL3R_EINVAL, "%s: rotate takes packed heads (head strides equal to head_dim)", op);
         if (d->k_cache)
@@ -1992,14 +2095,14 @@ extern "C" int exl3r_rope_run(const exl3r_rope_desc* d, void* stream)
                                            d->v, d->v_tok_stride, d->num_heads_k, d->dtype, d->bsz, d->seq_len,
                                            d->head_dim, d->inv_freq, d->rotary_dim, d->position, d->positions,
                                            d->position_ids, d->q_norm, d->k_norm, d->norm_dtype, d->norm_eps,
-                                           d->norm_constant_bias, d->rope_mode, d->attn_factor, d->k_cache, d->v_cache,
+                                           d->norm_constant_bias, mode, d->attn_factor, d->k_cache, d->v_cache,
                                            d->page_size, d->num_pages, d->block_table, d->max_blocks_per_seq,
                                            d->cache_seqlens, d->err_flag, d->q_post_scale, d->k_post_scale,
                                            d->v_post_scale, d->cs_table, stream);
         return exl3r_rope_had(d->q, d->out_q, d->q_tok_stride, d->num_heads_q, d->k, d->out_k, d->k_tok_stride,
                               d->num_heads_k, d->dtype, d->bsz, d->seq_len, d->head_dim, d->inv_freq, d->rotary_dim,
                               d->position, d->positions, d->position_ids, d->q_norm, d->k_norm, d->norm_dtype,
-                              d->norm_eps, d->norm_constant_bias, d->rope_mode, d->attn_factor, d->q_post_scale,
+                              d->norm_eps, d->norm_constant_bias, mode, d->attn_factor, d->q_post_scale,
                               d->k_post_scale, d->cs_table, stream);
     }
     if (d->k_cache)

@@ -333,10 +333,11 @@ def rope_cs(q, out_q, k, out_k, cs_table, q_norm, k_norm, norm_eps, norm_constan
 
 def rope_had(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias,
              rope_mode, attn_factor, q_post_scale=None, k_post_scale=None, position_ids=None, stream=None,
-             cs_table=None):
+             cs_table=None, exact=False):
     """rope() on the raw f16 outputs of the q / k projections, each first given its projection's output
     rotation had_r_128(y, y, None, svh) (src/modules.rs:231).  q, k: (bsz, seq_len, heads, head_dim) with
-    heads packed; q_post_scale / k_post_scale: f16 [heads * head_dim] or None."""
+    heads packed; q_post_scale / k_post_scale: f16 [heads * head_dim] or None.  The fused launch runs the
+    rotations on the matrix cores; exact=True: the reference's butterfly (EXL3R_HAD_EXACT in rope_mode)."""
     if q.dim() != 4:
         raise ValueError("q must be (bsz, seq_len, heads, head_dim)")
     bsz, seq, hq, hd = q.shape
@@ -358,8 +359,8 @@ def rope_had(q, out_q, k, out_k, inv_freq, position, positions, q_norm, k_norm, 
                                 dtype_code(q), bsz, seq, hd, _ptr(inv_freq), _rotary_dim(inv_freq, cs_table, bsz * seq, q.device),
                                 int(position), _ptr(positions), _ptr(position_ids),
                                 _ptr(q_norm), _ptr(k_norm), dtype_code(nw) if nw is not None else F16,
-                                norm_eps, norm_constant_bias, rope_mode, attn_factor, _ptr(q_post_scale),
-                                _ptr(k_post_scale), _ptr(cs_table), _stream(q, stream)))
+                                norm_eps, norm_constant_bias, rope_mode | (HAD_EXACT if exact else 0), attn_factor,
+                                _ptr(q_post_scale), _ptr(k_post_scale), _ptr(cs_table), _stream(q, stream)))
 
 
 def rope_paged_kv(q, out_q, k, out_k, v, inv_freq, position, positions, q_norm, k_norm, norm_eps, norm_constant_bias,
@@ -409,10 +410,11 @@ def rope_paged_kv(q, out_q, k, out_k, v, inv_freq, position, positions, q_norm, 
 def rope_paged_kv_had(q, out_q, k, out_k, v, inv_freq, position, positions, q_norm, k_norm, norm_eps,
                       norm_constant_bias, rope_mode, attn_factor, k_cache, v_cache, block_table, cache_seqlens,
                       q_post_scale=None, k_post_scale=None, v_post_scale=None, position_ids=None, err_flag=None,
-                      stream=None, cs_table=None):
+                      stream=None, cs_table=None, exact=False):
     """rope_paged_kv() on the raw f16 outputs of the q / k / v projections (heads packed), each first given
     its projection's output rotation had_r_128(y, y, None, svh) (src/modules.rs:231).  Outside the fused
-    launch (head_dim 128, 16-byte aligned) v, and k when out_k is None, are rotated in place."""
+    launch (head_dim 128, 16-byte aligned) v, and k when out_k is None, are rotated in place.  The fused
+    launch runs the rotations on the matrix cores; exact=True: the reference's butterfly."""
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q, k, v must be (bsz, seq_len, heads, head_dim)")
     bsz, seq, hq, hd = q.shape
@@ -435,8 +437,8 @@ def rope_paged_kv_had(q, out_q, k, out_k, v, inv_freq, position, positions, q_no
                                          _rotary_dim(inv_freq, cs_table, bsz * seq, q.device), int(position), _ptr(positions),
                                          _ptr(position_ids),
                                          _ptr(q_norm), _ptr(k_norm), dtype_code(nw) if nw is not None else F16,
-                                         norm_eps, norm_constant_bias, rope_mode, attn_factor,
-                                         _ptr(k_cache), _ptr(v_cache), k_cache.shape[1], k_cache.shape[0],
+                                         norm_eps, norm_constant_bias, rope_mode | (HAD_EXACT if exact else 0),
+                                         attn_factor, _ptr(k_cache), _ptr(v_cache), k_cache.shape[1], k_cache.shape[0],
                                          _ptr(block_table), block_table.shape[1], _ptr(cache_seqlens), _ptr(err_flag),
                                          _ptr(q_post_scale), _ptr(k_post_scale), _ptr(v_post_scale),
                                          _ptr(cs_table), _stream(q, stream)))

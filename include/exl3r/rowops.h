@@ -87,10 +87,10 @@ extern "C" {
 #define EXL3R_ACT_GELU        1 /* gelu(x) * y */
 #define EXL3R_ACT_MUL_SIGMOID 2 /* x * sigmoid(y) */
 
-/* Flag of the fused Hadamard entry points (exl3r_act_mul_had's rotate_in, exl3r_rms_norm_had's rotate_x):
- * the 128-point transforms
- * as the reference's fp32 butterfly (bit-identical to the unfused calls) instead of the matrix-core
- * form (within the stated rounding tolerance of it). */
+/* Flag of the fused Hadamard entry points (exl3r_act_mul_had's rotate_in, exl3r_rms_norm_had's rotate_x,
+ * the rope_mode of exl3r_rope_had / exl3r_rope_paged_kv_had, exl3r_rope_desc's rotate): the 128-point
+ * transforms as the reference's fp32 butterfly (bit-identical to the unfused calls) instead of the
+ * matrix-core form (within the stated rounding tolerance of it). */
 #define EXL3R_HAD_EXACT 16
 
 #define EXL3R_ROPE_NONE 0
@@ -303,9 +303,12 @@ EXL3R_API int exl3r_rope_cs(const void* q, void* out_q, int64_t q_tok_stride, in
  * RoPE::apply on it (src/rope.rs:233-260).  q, k: f16 [tokens, heads * head_dim] rows with heads
  * packed (head stride = head_dim), heads * head_dim a multiple of 128; q_post_scale / k_post_scale:
  * f16 [heads * head_dim] (the projections' svh) or NULL.  Other arguments as exl3r_rope.  q and k are
- * only read when out_q / out_k differ from them.  Bit-identical to exl3r_had_r_128 on q and k
- * followed by exl3r_rope.  head_dim 128 (NeoX at rotary_dim 128, or GPT-J at a rotary_dim multiple of 4), 16-byte aligned: one fused
- * launch; otherwise the rotations run into out_q / out_k and exl3r_rope in place there.
+ * only read when out_q / out_k differ from them.  head_dim 128 (NeoX at rotary_dim 128, or GPT-J at a
+ * rotary_dim multiple of 4), 16-byte aligned: one fused launch, whose transforms run on the matrix cores:
+ * bit-identical to exl3r_had_r_128_mfma on q and k followed by exl3r_rope (each rotated value the
+ * butterfly's or its f16 neighbour, as exl3r_had_r_128_mfma states); with EXL3R_HAD_EXACT in rope_mode,
+ * the reference's butterfly, bit-identical to exl3r_had_r_128 followed by exl3r_rope.  Otherwise the
+ * rotations run (as exl3r_had_r_128) into out_q / out_k and exl3r_rope in place there.
  *   cs_table: NULL, or a {cos, sin} table that exl3r_rope_cs_table filled for the same positions,
  *             inv_freq, rotary_dim and attn_factor; the rotary pairs are then read from it (inv_freq
  *             may be NULL; the results are the same bits).
@@ -324,11 +327,13 @@ EXL3R_API int exl3r_rope_had(const void* q, void* out_q, int64_t q_tok_stride, i
  * projection output first becomes had_r_128(y, y, NULL, svh, 1.0) (src/modules.rs:231), then RoPE::apply
  * and paged_kv_cache_update (src/modules.rs:669-704).  q, k, v: f16 with heads packed (head stride =
  * head_dim), heads * head_dim a multiple of 128; *_post_scale: f16 [heads * head_dim] (svh) or NULL.
- * Other arguments as exl3r_rope_paged_kv.  Bit-identical to exl3r_had_r_128 on q, k and v followed by
- * exl3r_rope_paged_kv.  head_dim 128 (NeoX at rotary_dim 128, or GPT-J at a rotary_dim multiple of 4), 16-byte aligned: one fused
- * launch that writes only out_q, out_k (if given) and the caches.  Otherwise the rotations run first -- q into
- * out_q, k into out_k (into k itself when out_k is NULL) and v in place -- then exl3r_rope_paged_kv.
- * cs_table: as exl3r_rope_had.
+ * Other arguments as exl3r_rope_paged_kv.  head_dim 128 (NeoX at rotary_dim 128, or GPT-J at a
+ * rotary_dim multiple of 4), 16-byte aligned: one fused launch that writes only out_q, out_k (if given)
+ * and the caches, its transforms on the matrix cores (bit-identical to exl3r_had_r_128_mfma on q, k and
+ * v followed by exl3r_rope_paged_kv) or, with EXL3R_HAD_EXACT in rope_mode, as the reference's butterfly
+ * (bit-identical to exl3r_had_r_128 followed by exl3r_rope_paged_kv).  Otherwise the rotations run first
+ * (as exl3r_had_r_128) -- q into out_q, k into out_k (into k itself when out_k is NULL) and v in place --
+ * then exl3r_rope_paged_kv.  cs_table: as exl3r_rope_had.
  */
 EXL3R_API int exl3r_rope_paged_kv_had(const void* q, void* out_q, int64_t q_tok_stride, int num_heads_q,
                             const void* k, void* out_k, int64_t k_tok_stride, const void* v,
@@ -382,7 +387,8 @@ EXL3R_API int exl3r_rope_paged_kv(const void* q, void* out_q, int64_t q_tok_stri
  * reference (its RoPE is one shim, exl3_shim_rope); for callers that build their arguments once per
  * layer and for bindings that would otherwise mirror eight signatures.  Semantics, results and errors
  * are those of the entry point it selects:
- *   rotate != 0 (the projections' output rotations; q_post_scale / k_post_scale / v_post_scale)
+ *   rotate = 1 or 1 | EXL3R_HAD_EXACT (the projections' output rotations; q_post_scale / k_post_scale /
+ *                      v_post_scale; the flag goes to rope_mode)
  *                      -> exl3r_rope_paged_kv_had with k_cache, else exl3r_rope_had (heads packed);
  *   k_cache != NULL    -> exl3r_rope_paged_kv (v, caches, block table, cache_seqlens, err_flag);
  *   angle_table        -> exl3r_rope_table (table_rows, table_batch_stride, err_flag);

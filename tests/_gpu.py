@@ -110,3 +110,27 @@ def assert_had_close(got, exp, xin, r, what="", min_exact=0.98, max_ulp=1):
     assert bad == 0, stats
     assert same.mean() >= min_exact, stats
 
+
+
+def assert_head_close(got, exp, hd, what="", rel=2.0 ** -8, max_ulp=2, min_exact=0.97):
+    """f16 heads of hd elements computed from the matrix-core output rotation against the oracle's
+    composition with the butterfly: each element within max_ulp f16 steps of the oracle, or within rel
+    times its head's largest |oracle value| (a last-place difference of the transform moves through the
+    head norm's statistic and RoPE's differences, which can cancel to a small result); NaN only where
+    the oracle has NaN; at least min_exact of the elements identical.  A wrong index, sign or operand
+    moves results by the order of the head's scale, far outside this."""
+    got = np.ascontiguousarray(got).reshape(-1, hd)
+    exp = np.ascontiguousarray(exp).reshape(-1, hd)
+    g = orc.to_f32(got, orc.F16).astype(np.float64)
+    e = orc.to_f32(exp, orc.F16).astype(np.float64)
+    d = ulp_dist(got, exp, orc.F16)
+    with np.errstate(invalid="ignore"):
+        scale = np.nanmax(np.where(np.isfinite(e), np.abs(e), 0.0), axis=1, keepdims=True)
+        ok = (d <= max_ulp) | (np.abs(g - e) <= rel * scale)
+    same = d == 0
+    bad = int((~ok).sum())
+    stats = (f"{what}: identical={same.mean():.6f} within_2ulp={np.mean(d <= 2):.6f} "
+             f"outside_tolerance={bad} of {d.size}")
+    print(stats)
+    assert bad == 0, stats
+    assert same.mean() >= min_exact, stats

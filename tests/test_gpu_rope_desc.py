@@ -96,6 +96,12 @@ def test_rotations_and_paged(tokens):
     ffi.rope_run(q=q, out_q=o2, k=k, out_k=ok2, inv_freq=f, positions=sld, rotate=1, q_post_scale=sq, k_post_scale=sk, **c)
     torch.cuda.synchronize()
     assert same(o1, o2) and same(ok1, ok2)
+    # the reference's butterfly: EXL3R_HAD_EXACT in rotate
+    ffi.rope_had(q, o1, k, ok1, f, 0, sld, qn, kn, 1e-6, 0.0, NEOX, 1.0, q_post_scale=sq, k_post_scale=sk, exact=True)
+    ffi.rope_run(q=q, out_q=o2, k=k, out_k=ok2, inv_freq=f, positions=sld, rotate=1 | ffi.HAD_EXACT, q_post_scale=sq,
+                 k_post_scale=sk, **c)
+    torch.cuda.synchronize()
+    assert same(o1, o2) and same(ok1, ok2), "rotate | EXL3R_HAD_EXACT"
     # the paged append, then with the rotations
     for rotate in (0, 1):
         kc1, vc1 = dev_normal((pages, page, hk, hd), 0, 1, F16, 30), dev_normal((pages, page, hk, hd), 0, 1, F16, 31)

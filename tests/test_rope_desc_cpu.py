@@ -56,6 +56,8 @@ def base(**kw):
     ("own out_q layout with cs", dict(inv_freq=None, cs_table=FAKE, out_q_head_stride=64)),
     ("own out_q layout that is not the q|g split", dict(out_q_head_stride=64)),
     ("rotate with padded heads", dict(rotate=1, q_head_stride=192, q_tok_stride=384)),
+    ("rotate 2", dict(rotate=2)),
+    ("EXL3R_HAD_EXACT without rotate", dict(rotate=16)),
 ])
 def test_router_rejects(case, kw):
     with pytest.raises(exl3r.Exl3rError) as e:
