@@ -928,7 +928,27 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
     }
     if constexpr (SRC == SRC_FREQ)
         if (threadIdx.x < 64) fsh[threadIdx.x] = (int)threadIdx.x < R2 ? a.inv_freq[threadIdx.x] : 0.0f;
-    if constexpr (NORM != NORM_NONE || SRC == SRC_FREQ)
+    // HADR: the post-scales of all H heads (item-space order, 128 halfs each; zeros for a projection
+    // without one, never read) into LDS after the {cos, sin} rows, 16 bytes per thread and step, so that
+    // an item's read of them is an LDS read, whose wait does not also wait for the next item's loads.
+    // (Indexed as an LDS array: a generic pointer into it trips an instruction-selection error in hipcc,
+    // ROCm 7.2, for the comparisons of the flat address.)
+    extern __shared__ u32x4 dyn16[];          // the dynamic LDS in 16-byte units
+    constexpr int kPost16 = SRC == SRC_FREQ ? 4 * 64 * 8 / 16 : 0;
+    if constexpr (HADR != HADR_NONE)
+    {
+        for (int i = threadIdx.x; i < H * 16; i += 256)
+        {
+            const int h = i >> 4;
+            const bool iq = h < hq, iv = APPEND && h >= hq + hk;
+            const int hi = h - (iq ? 0 : hq) - (iv ? hk : 0);
+            const void* p = pick_qkv(iq, iv, qpost, kpost, vpost);
+            u32x4 v = {};
+            if (p) v = *(const u32x4*)((const _Float16*)p + (int64_t)hi * 128 + (i & 15) * 8);
+            dyn16[kPost16 + i] = v;
+        }
+    }
+    if constexpr (NORM != NORM_NONE || SRC == SRC_FREQ || HADR != HADR_NONE)
     {
         __syncthreads();
         if constexpr (SRC == SRC_FREQ) freq = fsh[l64];
@@ -951,9 +971,8 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
             auto load_post = [&]() __attribute__((always_inline)) {
                 if (hp)
                 {
-                    const _Float16* pp = (const _Float16*)post + (int64_t)hidx * 128 + e0;
-                    pl = *(const u32x4*)pp;
-                    ph = *(const u32x4*)(pp + 64);
+                    pl = dyn16[kPost16 + h * 16 + (e0 >> 3)];
+                    ph = dyn16[kPost16 + h * 16 + (e0 >> 3) + 8];
                 }
             };
             if constexpr (!MF) load_post();
@@ -1206,7 +1225,10 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
     // compiler's wait for an item's data also covers the next item's loads, the issue being conditional;
     // finishing each wave's last item on a path of its own makes that wait exact, but the second copy of
     // the item code costs registers and measured no faster: C4 32.6 us either way, from the table 33.2
-    // against 31.2 us.)
+    // against 31.2 us.  An unconditional issue -- past its last item a wave reloading the grid's last
+    // item -- makes it exact too (vmcnt(2) instead of vmcnt(0) before an item's math) and ran slower in
+    // every instance, same process: C4 33.1 -> 33.9 us, from the table 31.4 -> 39.3, the rotating paged
+    // form 38.4 -> 58.4 (13-20 VGPRs spilled: the next item's registers live across the math).)
     Item A, B;
     issue(A, item);
     for (;;)
@@ -1237,6 +1259,8 @@ static bool rope_nx_ok(const RopeArgs& a, int rope_mode, bool had = false)
         return false;
     if (tu.rope_tok != 0 && tu.rope_nx == 0) return false;   // a test forcing one of the other kernels
     if (a.kc && a.hv != a.hk) return false;
+    // the output rotations' post-scales of all heads in LDS: up to 192 heads (48 KB)
+    if (had && (int64_t)(a.hq + a.hk + (a.kc ? a.hv : 0)) * 256 > (48 << 10)) return false;
     if (a.tokens >= ((int64_t)1 << 31)) return false;    // 32-bit token arithmetic
     if (!a16(a.q_post) || !a16(a.k_post) || !a16(a.v_post)) return false;
     if (a.cst && ((uintptr_t)a.cst & 15)) return false;
@@ -1249,18 +1273,27 @@ static bool rope_nx_ok(const RopeArgs& a, int rope_mode, bool had = false)
 template <class IO, int MODE, int NORM, int SRC, bool QOUT, int P, bool APPEND = false, int HADR = HADR_NONE>
 static void launch_rope_nx_p(const RopeArgs& a, hipStream_t s)
 {
-    const int nslice = ((a.hq + a.hk + (APPEND ? a.hv : 0) + 7) / 8 + P - 1) / P;
+    const int H = a.hq + a.hk + (APPEND ? a.hv : 0);
+    const int nslice = ((H + 7) / 8 + P - 1) / P;
     const int64_t items = a.tokens * nslice;
-    const size_t lds = SRC == SRC_FREQ ? 4 * 64 * sizeof(float2) : 0;
+    // The output rotations' post-scales sit in LDS (H * 256 bytes; rope_nx_ok bounds H).  Up to 96 heads
+    // five workgroups of 20 resident waves per CU take at most 130 KB of its 160 KB with the {cos, sin}
+    // rows; more heads can lower the occupancy, which is then asked for at the launch.
+    const size_t cs_lds = SRC == SRC_FREQ ? 4 * 64 * sizeof(float2) : 0;
+    const size_t lds = cs_lds + (HADR != HADR_NONE ? (size_t)H * 256 : 0);
+    constexpr size_t kLdsCommon = SRC == SRC_FREQ ? 4 * 64 * sizeof(float2) + (HADR != HADR_NONE ? 24 << 10 : 0)
+                                                  : (HADR != HADR_NONE ? 24 << 10 : 0);
     // Grid: the workgroups resident at once (per CU, from the occupancy of this instance), each wave
     // walking its items i, i + W, ...
-    static const int resident = [&] {   // workgroups per CU (per template instance; thread-safe init)
+    auto occupancy = [](size_t bytes) {
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_rope_nx<IO, MODE, NORM, SRC, QOUT, P, APPEND, HADR>, 256,
-                                                         lds) != hipSuccess || nb < 1)
+                                                         bytes) != hipSuccess || nb < 1)
             nb = 4;
         return nb;
-    }();
+    };
+    static const int resident_common = occupancy(kLdsCommon);   // per template instance; thread-safe init
+    const int resident = lds <= kLdsCommon ? resident_common : occupancy(lds);
     const int wpc = tuning().rope_wgs_per_cu;
     int64_t blocks = (int64_t)(wpc > 0 ? wpc : resident) * device_cus();
     // Items a wave takes in a row, its token's angles evaluated once within them, where every wave gets

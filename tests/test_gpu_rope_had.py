@@ -29,11 +29,12 @@ def svh(n, seed):
                              (1 + 0.02 * rng.standard_normal(n))).astype(np.float16)).cuda()
 
 
-def nx_rotation(hd, R, mode):
+def nx_rotation(hd, R, mode, heads=0):
     """Whether exl3r_rope_had / exl3r_rope_paged_kv_had take the 8-lane kernel, whose default transform
-    runs on the matrix cores: heads of 128, NeoX over the full width or GPT-J over a multiple of 4 (16-byte
-    aligned post-scales, evaluated or {cos, sin} rotations; the tests' tensors are aligned)."""
-    return hd == 128 and (R == 128 if mode == exl3r.ROPE_NEOX else R % 4 == 0)
+    runs on the matrix cores: heads of 128, NeoX over the full width or GPT-J over a multiple of 4, at
+    most 192 heads (q + k, + v with the cache) for the post-scales in LDS (16-byte aligned post-scales,
+    evaluated or {cos, sin} rotations; the tests' tensors are aligned)."""
+    return hd == 128 and (R == 128 if mode == exl3r.ROPE_NEOX else R % 4 == 0) and heads <= 192
 
 
 def run(bsz, seq, hq, hk, hd, R, mode, nwt=F16, norm=True, with_k=True, q_post=True, k_post=True, position=0,
@@ -48,7 +49,7 @@ def run(bsz, seq, hq, hk, hd, R, mode, nwt=F16, norm=True, with_k=True, q_post=T
     fd = torch.from_numpy(f).cuda()
     pid_d = torch.from_numpy(position_ids).cuda() if position_ids is not None else None
     qh, kh = from_dev(q), (from_dev(k) if with_k else None)
-    mf = not exact and nx_rotation(hd, R, mode)
+    mf = not exact and nx_rotation(hd, R, mode, hq + (hk if with_k else 0))
     # unfused GPU reference: the output rotations (in the fused launch's form), then exl3r_rope in place
     uq = torch.empty_like(q)
     ffi.had_r_128(q.view(bsz * seq, hq * hd), uq.view(bsz * seq, hq * hd), None, qs, mfma=mf)
@@ -117,6 +118,13 @@ def test_odd_head_counts():
     head 5), and q heads ending inside a 4-head span of the matrix-core placement."""
     run(3, 333, 5, 1, 128, 128, exl3r.ROPE_NEOX, position=3, seed=11)
     run(1, 700, 6, 0, 128, 128, exl3r.ROPE_NEOX, with_k=False, nwt=F32, seed=12)
+
+
+def test_head_counts_at_the_post_scale_bound():
+    """192 heads: the 8-lane kernel with every post-scale in LDS (48 KB, lower occupancy); 200 heads: the
+    wave-per-token kernel and its butterfly."""
+    run(1, 96, 184, 8, 128, 128, exl3r.ROPE_NEOX, position=9, seed=13)
+    run(1, 96, 192, 8, 128, 128, exl3r.ROPE_NEOX, position=9, seed=14)
 
 
 @pytest.mark.parametrize("case", ["decode", "gptj", "gptj_exact", "hd64", "hd256"])
