@@ -47,7 +47,7 @@ OPS = ["rms_c3", "rms_q3mix", "silu_c3", "gelu_c3", "rope_c4", "rope_c4_gptj", "
        "gather_norm_c5", "rms_c1",
        "silu_c1", "rope_c1", "gather_c1", "rms_c2", "decode_fused", "decode_naive", "rope_kv_prefill",
        "rope_kv_prefill_unfused", "rope_kv_dec", "rope_kv_dec_unfused", "gated_norm_q35", "mul_sigmoid_q35",
-       "deinterleave_q35", "gated_norm_had_q35", "gated_norm_had_q35_unfused", "argmax_dec", "argmax_dec_torch", "argmax_dec_ws", "argmax_prefill", "argmax_prefill_torch",
+       "deinterleave_q35", "gated_norm_had_q35", "gated_norm_had_q35_exact", "gated_norm_had_q35_unfused", "argmax_dec", "argmax_dec_torch", "argmax_dec_ws", "argmax_prefill", "argmax_prefill_torch",
        "gumbel_dec", "gumbel_dec_torch", "gumbel_dec_ws", "gumbel_prefill", "had_c3", "had_c3_mfma", "norm_had_c3",
        "norm_had_c3_exact", "norm_had_c3_unfused", "norm_had_rot_c3", "norm_had_rot_c3_exact", "norm_had_rot_c3_unfused",
        "silu_had_c3", "silu_had_c3_exact", "silu_had_c3_unfused", "rope_had_c4", "rope_had_c4_exact", "rope_had_c4_unfused", "rope_cs_c4", "rope_cs_table_c4",
@@ -408,9 +408,10 @@ def make_gated(name, kind, tokens=4096, heads=32, hd=128, seed=600):
             x, g, y = bufs[i % sets]
             ffi.gated_rms_norm(x, w, y, g, 1e-6, 0.0, 1, False, 0)
         desc = f"gated RMSNorm (silu gate) [{tokens * heads},{hd}] bf16 x, f32 g, f16 y"
-    elif kind in ("norm_had", "norm_had_unfused"):
-        # ... feeding o_proj's input rotation (src/qwen3_5.rs:208-214): one fused launch, or the gated
-        # norm into y and exl3r_had_r_128; both count the fused job's bytes
+    elif kind in ("norm_had", "norm_had_exact", "norm_had_unfused"):
+        # ... feeding o_proj's input rotation (src/qwen3_5.rs:208-214): one fused launch (the transform on
+        # the matrix cores, or the reference's butterfly), or the gated norm into y and exl3r_had_r_128;
+        # all count the fused job's bytes
         nbytes = n * (2 + 4 + 2) + hd * 4 + heads * hd * 2
         sets = sets_for(nbytes)
         bufs = [(gen((tokens * heads, hd), 0.0, 1.0, torch.bfloat16, seed + 3 * k),
@@ -422,13 +423,15 @@ def make_gated(name, kind, tokens=4096, heads=32, hd=128, seed=600):
 
         def launch(i):
             x, g, out = bufs[i % sets]
-            if kind == "norm_had":
-                ffi.gated_rms_norm_had(x, w, g, out.view(tokens * heads, hd), 1e-6, suh, pre_rows=heads)
+            if kind != "norm_had_unfused":
+                ffi.gated_rms_norm_had(x, w, g, out.view(tokens * heads, hd), 1e-6, suh, pre_rows=heads,
+                                       exact=kind == "norm_had_exact")
             else:
                 ffi.gated_rms_norm(x, w, y, g, 1e-6, 0.0, 1, False, 0)
                 ffi.had_r_128(y.view(tokens, heads * hd), out, suh)
         desc = (f"gated RMSNorm [{tokens * heads},{hd}] -> o_proj input rotation [{tokens},{heads * hd}], "
-                f"{'fused' if kind == 'norm_had' else 'unfused (gated norm + had_r_128)'}")
+                f"{'unfused (gated norm + had_r_128)' if kind == 'norm_had_unfused' else 'fused'}"
+                f"{', butterfly' if kind == 'norm_had_exact' else ''}")
     elif kind == "sigmoid":
         nbytes = 3 * n * 2
         sets = sets_for(nbytes)
@@ -797,6 +800,7 @@ def make_all(only=None):
         "deinterleave_q35": lambda: make_gated("deinterleave_q35", "deinterleave"),
         "gated_norm_had_q35": lambda: make_gated("gated_norm_had_q35", "norm_had"),
         "gated_norm_had_q35_unfused": lambda: make_gated("gated_norm_had_q35_unfused", "norm_had_unfused"),
+        "gated_norm_had_q35_exact": lambda: make_gated("gated_norm_had_q35_exact", "norm_had_exact"),
         "argmax_dec": lambda: make_argmax("argmax_dec", 64, False),
         "argmax_dec_torch": lambda: make_argmax("argmax_dec_torch", 64, True),
         "argmax_dec_ws": lambda: make_argmax("argmax_dec_ws", 64, False, ws=True),

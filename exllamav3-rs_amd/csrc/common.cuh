@@ -519,6 +519,19 @@ __device__ __forceinline__ double sum_xor16(double v)
     return a + b;
 }
 
+// v(l) + v(l ^ 32) in every lane l, the same bits in both (v_permlane32_swap_b32 of v with itself: the
+// lower half's value first).  Both lanes of a pair must be active.
+__device__ __forceinline__ double sum_xor32(double v)
+{
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)u, hi = (uint32_t)(u >> 32);
+    const auto pl = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto ph = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    const double a = __builtin_bit_cast(double, ((uint64_t)(uint32_t)ph[0] << 32) | (uint32_t)pl[0]);
+    const double b = __builtin_bit_cast(double, ((uint64_t)(uint32_t)ph[1] << 32) | (uint32_t)pl[1]);
+    return a + b;
+}
+
 // Full-wave sum, uniform result: row sums by DPP, then the four rows combined through readlane.
 __device__ __forceinline__ float wave_sum(float v)
 {

@@ -66,7 +66,9 @@ extern "C" int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out,
 
 // exl3r_gated_rms_norm with an f16 output feeding the next EXL3 projection's input rotation, in one
 // pass: the gated-delta-net output norm, then o_proj's had_r_128(y, suh) (src/qwen3_5.rs:208-214,
-// src/modules.rs:224-227).  A 128-column block of the rotation is 16 lanes of one row's lane group.
+// src/modules.rs:224-227).  A 128-column block of the rotation is 16 lanes of one row's lane group; rows
+// of one block (head_dim 128) run the transform on the matrix cores unless EXL3R_HAD_EXACT is in
+// gate_act (then, and at other row lengths, the reference's butterfly).
 extern "C" int exl3r_gated_rms_norm_had(const void* x, int xt, int64_t ldx, const void* w, int wt, int w_groups,
                                         const void* g, int gt, int64_t ldg, void* y, int64_t ldy,
                                         const void* pre_scale, int pre_rows, void* out, int64_t ldo, int64_t rows,
@@ -75,6 +77,8 @@ extern "C" int exl3r_gated_rms_norm_had(const void* x, int xt, int64_t ldx, cons
 {
     begin_call();
     const char* op = "exl3r_gated_rms_norm_had";
+    const bool exact = (gate_act & EXL3R_HAD_EXACT) != 0;
+    gate_act &= ~EXL3R_HAD_EXACT;
     if (dim <= 0 || dim % 128) return set_error(EXL3R_EINVAL, "%s: dim %lld must be a multiple of 128", op, (long long)dim);
     int rc = check_rms_common(op, x, xt, ldx, w, wt, out, EXL3R_F16, ldo, rows, dim);
     if (rc) return rc;
@@ -106,7 +110,13 @@ extern "C" int exl3r_gated_rms_norm_had(const void* x, int xt, int64_t ldx, cons
             using XTy = decltype(X);
             if (short_rows)
             {
-                if (gt == EXL3R_F32) launch_rms_rows<XTy, TF16, TF32, RMS_GATED, HAD_OUT>(a, s);
+                // rows of one block: the transform on the matrix cores unless exact
+                if (dim == 128 && !exact)
+                {
+                    if (gt == EXL3R_F32) launch_rms_rows<XTy, TF16, TF32, RMS_GATED, HAD_OUT | HAD_MFMA>(a, s);
+                    else launch_rms_rows<XTy, TF16, TBF16, RMS_GATED, HAD_OUT | HAD_MFMA>(a, s);
+                }
+                else if (gt == EXL3R_F32) launch_rms_rows<XTy, TF16, TF32, RMS_GATED, HAD_OUT>(a, s);
                 else launch_rms_rows<XTy, TF16, TBF16, RMS_GATED, HAD_OUT>(a, s);
                 return;
             }

@@ -299,6 +299,36 @@ __device__ __forceinline__ MfmaOut had128_mfma_issue(const HadMfma& H, const TF1
              __builtin_amdgcn_mfma_f32_16x16x32_f16(H.a[1], b, zero, 0, 0, 0) };
 }
 
+// had128_mfma_issue of one or two chunks from the two words, with one 4-VGPR operand: the MFMAs of A_0
+// first, then its upper words negated in place (A_1) for the others.
+__device__ __forceinline__ void had128_mfma_issue_w(HadMfmaWords w, const TF16::Vec& v0, MfmaOut& m0)
+{
+    asm volatile("" : "+v"(w.w0), "+v"(w.w1));
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    u32x4v a = { w.w0, w.w1, w.w0, w.w1 };
+    const f32x4 zero = { 0.0f, 0.0f, 0.0f, 0.0f };
+    const f16x8 b0 = __builtin_bit_cast(f16x8, v0.a);
+    m0.d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), b0, zero, 0, 0, 0);
+    a.z ^= 0x80008000u;
+    a.w ^= 0x80008000u;
+    m0.d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), b0, zero, 0, 0, 0);
+}
+__device__ __forceinline__ void had128_mfma_issue_w(HadMfmaWords w, const TF16::Vec& v0, const TF16::Vec& v1,
+                                                    MfmaOut& m0, MfmaOut& m1)
+{
+    asm volatile("" : "+v"(w.w0), "+v"(w.w1));
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    u32x4v a = { w.w0, w.w1, w.w0, w.w1 };
+    const f32x4 zero = { 0.0f, 0.0f, 0.0f, 0.0f };
+    const f16x8 b0 = __builtin_bit_cast(f16x8, v0.a), b1 = __builtin_bit_cast(f16x8, v1.a);
+    m0.d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), b0, zero, 0, 0, 0);
+    m1.d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), b1, zero, 0, 0, 0);
+    a.z ^= 0x80008000u;
+    a.w ^= 0x80008000u;
+    m0.d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), b0, zero, 0, 0, 0);
+    m1.d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), b1, zero, 0, 0, 0);
+}
+
 __device__ __forceinline__ void mfma_wait(MfmaOut& a)
 {
     asm volatile("s_nop 7\ns_nop 7" : "+v"(a.d0), "+v"(a.d1));

@@ -611,20 +611,30 @@ __global__ __launch_bounds__(1024) void k_rms_norm_pipe(RmsArgs a)
 // chunk per lane, 256 / LPR rows per workgroup and RPL rows per lane in flight.  The row sum is a
 // DPP butterfly inside the LPR-lane group -- no LDS, no barrier -- so a 128-element head row costs
 // 16 lanes instead of a workgroup.
+// HAD_MFMA (rows of one 128-element block, one f16 output): a wave's 4 rows are one span of
+// had128_mfma's placement -- row = lane bits 2-3, chunk = lane bits 0, 1, 4, 5 -- so the row sum runs
+// over lanes xor 1, 2, 16 and 32, which groups it as the 16-lane butterfly does (quads, pairs of quads,
+// then the two pairs), the same bits.
 template <class XT, class YT, class RT, int LPR, int RPL, int MODE, int HAD = 0>
 __global__ __launch_bounds__(256) void k_rms_rows(RmsArgs a)
 {
     static_assert(MODE != RMS_GATHER, "gathered rows take the workgroup kernel");
+    constexpr bool MF = (HAD & HAD_MFMA) != 0;
+    static_assert(!MF || (LPR == 16 && (HAD & HAD_OUT) != 0), "matrix-core rows: one block each, an output");
     constexpr int SLOTS = 256 / LPR;
-    const int lane = threadIdx.x % LPR;
-    const int slot = threadIdx.x / LPR;
+    const int l64 = threadIdx.x & 63;
+    const int lane = MF ? (l64 & 3) | ((l64 >> 2) & 12) : (int)threadIdx.x % LPR;
+    const int slot = MF ? (int)(threadIdx.x >> 6) * 4 + ((l64 >> 2) & 3) : (int)threadIdx.x / LPR;
     const bool lane_ok = lane < (a.dim >> 3);
     const int64_t e = (int64_t)lane * 8;
+    [[maybe_unused]] HadMfmaWords hw{};
+    if constexpr (MF) hw = had_mfma_words(l64);
     for (int64_t r0 = (int64_t)blockIdx.x * SLOTS * RPL; r0 < a.rows; r0 += (int64_t)gridDim.x * SLOTS * RPL)
     {
         typename XT::Vec xv[RPL];
         typename RT::Vec rv[RPL];
         u32x4 wv[RPL];
+        [[maybe_unused]] TF16::Vec pv[RPL];     // HAD_OUT: the row's pre-scale chunk, fetched with its loads
         bool act[RPL];
         #pragma unroll
         for (int i = 0; i < RPL; ++i)
@@ -637,6 +647,8 @@ __global__ __launch_bounds__(256) void k_rms_rows(RmsArgs a)
                 if constexpr (MODE == RMS_RES_IN || MODE == RMS_GATED)
                     rv[i] = load8s<RT>((const char*)a.r + row * a.ldr * RT::bytes, e);
                 if (a.w) wv[i] = prefetch_w8(a.w, a.wt, weight_row<MODE>(a, row) + e);
+                if constexpr ((HAD & HAD_OUT) != 0)
+                    if (a.hpre[0]) pv[i] = load8<TF16>(a.hpre[0], (a.hpre_rows > 1 ? (row % a.hpre_rows) * a.dim : 0) + e);
             }
         }
         #pragma unroll
@@ -646,9 +658,58 @@ __global__ __launch_bounds__(256) void k_rms_rows(RmsArgs a)
             double ss = 0.0;
             typename RmsCache<XT, RT, MODE>::Vec cv;
             if (act[i]) cv = rms_chunk1<XT, RT, MODE>(a, (char*)a.r + row * a.ldr * RT::bytes, e, true, xv[i], rv[i], ss);
-            ss = group_sum64<LPR>(ss);
+            if constexpr (MF)
+            {
+                ss += dpp64<DPP_QUAD_XOR1>(ss);
+                ss += dpp64<DPP_QUAD_XOR2>(ss);
+                ss = sum_xor32(sum_xor16(ss));
+            }
+            else
+                ss = group_sum64<LPR>(ss);
             const float rmf = rms_factor(ss, a.dim, a.eps) * a.cs;
-            if (act[i])
+            if constexpr (MF)
+            {
+                // The f16 norm output and its pre-scale product (zeros in the rows past the end, whose
+                // lanes still take part in the MFMAs), the transform, then the stores of live rows.
+                TF16::Vec v = {};
+                if (act[i])
+                {
+                    v = rms_out8<XT, YT, RT, MODE, false>(a, e, weight_row<MODE>(a, row), cv, rv[i], wv[i], rmf);
+                    if (a.y) store8<YT>((char*)a.y + row * a.ldy * YT::bytes, e, v);
+                    if (a.hpre[0])
+                    {
+                        #pragma unroll
+                        for (int q = 0; q < 4; ++q) v.a[q] = hmul2(v.a[q], pv[i].a[q]);
+                    }
+                }
+                MfmaOut m;
+                had128_mfma_issue_w(hw, v, m);
+                mfma_wait(m);
+                float f[8];
+                had128_mfma_finish(m, f, l64, a.hr);
+                if (act[i]) store8<TF16>((char*)a.hout[0] + row * a.ldh * 2, e, pack8<TF16>(f));
+            }
+            else if constexpr ((HAD & HAD_OUT) != 0)
+            {
+                // the butterfly on the row's 16-lane block groups (one output), as rms_chunk2 does it
+                static_assert(YT::code == DT_F16, "the Hadamard prologue follows an f16 norm output");
+                if (act[i])
+                {
+                    TF16::Vec v = rms_out8<XT, YT, RT, MODE, false>(a, e, weight_row<MODE>(a, row), cv, rv[i], wv[i], rmf);
+                    if (a.y) store8<YT>((char*)a.y + row * a.ldy * YT::bytes, e, v);
+                    if (a.hpre[0])
+                    {
+                        #pragma unroll
+                        for (int q = 0; q < 4; ++q) v.a[q] = hmul2(v.a[q], pv[i].a[q]);
+                    }
+                    with_carried<true>(zero_lane16(v), a.hr, [&](auto C) {
+                        float f[8];
+                        butterfly128_f16<decltype(C)::value>(v, f, lane & 15, a.hr);
+                        store8<TF16>((char*)a.hout[0] + row * a.ldh * 2, e, pack8<TF16>(f));
+                    });
+                }
+            }
+            else if (act[i])
                 rms_chunk2<XT, YT, RT, MODE, HAD>(a, row, (char*)a.y + row * a.ldy * YT::bytes, e,
                                                       weight_row<MODE>(a, row), cv, rv[i], wv[i], rmf);
         }
@@ -673,7 +734,9 @@ void launch_rms_rows(const RmsArgs& a, hipStream_t s)
         else if (rpl == 2) launch(k_rms_rows<XT, YT, RT, LPR, 2, MODE, HAD>, (unsigned)blocks, 256, 0, s, a);
         else launch(k_rms_rows<XT, YT, RT, LPR, 1, MODE, HAD>, (unsigned)blocks, 256, 0, s, a);
     };
-    if (nc <= 8) go(std::integral_constant<int, 8>{});
+    if constexpr ((HAD & HAD_MFMA) != 0)
+        go(std::integral_constant<int, 16>{});   // rows of one block (the caller checks dim == 128)
+    else if (nc <= 8) go(std::integral_constant<int, 8>{});
     else if (nc <= 16) go(std::integral_constant<int, 16>{});
     else if (nc <= 32) go(std::integral_constant<int, 32>{});
     else go(std::integral_constant<int, 64>{});

@@ -116,10 +116,12 @@ def gated_rms_norm(x, w, y, g, eps, constant_bias=0.0, w_groups=1, gate_first=Fa
 
 
 def gated_rms_norm_had(x, w, g, out, eps, pre_scale=None, y=None, constant_bias=0.0, w_groups=1, gate_first=False,
-                       gate_act=0, had_scale=1.0, pre_rows=1, stream=None):
+                       gate_act=0, had_scale=1.0, pre_rows=1, stream=None, exact=False):
     """One pass: the gated norm of gated_rms_norm into an f16 y (written only if given), then
     out = had_r_128(y, pre_scale) (f16, dim % 128 == 0): o_proj's input rotation.  Norm row r uses
-    pre_scale[(r % pre_rows) * dim:]: with rows = tokens * heads of head_dim, pre_rows = heads."""
+    pre_scale[(r % pre_rows) * dim:]: with rows = tokens * heads of head_dim, pre_rows = heads.  Rows of
+    128 run the transform on the matrix cores; exact=True: the reference's butterfly (EXL3R_HAD_EXACT in
+    gate_act)."""
     rows, dim, ldx = _rows(x)
     rg, dg, ldg = _rows(g)
     ro, do, ldo = _rows(out)
@@ -136,7 +138,8 @@ def gated_rms_norm_had(x, w, g, out, eps, pre_scale=None, y=None, constant_bias=
                                           w_groups, _ptr(g), dtype_code(g), ldg, _ptr(y), ldy, _ptr(pre_scale),
                                           int(pre_rows), _ptr(out), ldo, rows, dim, eps, constant_bias,
                                           int(bool(gate_first)),
-                                          int(gate_act), float(had_scale), _stream(x, stream)))
+                                          int(gate_act) | (HAD_EXACT if exact else 0), float(had_scale),
+                                          _stream(x, stream)))
 
 def mul_sigmoid(x, y, z, stream=None):
     """z = x * sigmoid(y) (fp32, one rounding); z may be x."""

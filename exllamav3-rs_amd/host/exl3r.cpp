@@ -264,7 +264,7 @@ void gated_rms_norm(const Tensor& x, const Tensor* w, const Tensor& y, const Ten
 
 void gated_rms_norm_had(const Tensor& x, const Tensor* w, const Tensor& g, const Tensor& out, const Tensor* y,
                         const Tensor* pre_scale, float eps, float bias, int w_groups, bool gate_first, int gate_act,
-                        float had_scale, const Stream& s, int pre_rows)
+                        float had_scale, const Stream& s, int pre_rows, bool exact)
 {
     int64_t rows, dim, ldx, rg, dg, ldg, ro, dout, ldo, ldy = 0;
     x.rows_view(rows, dim, ldx);
@@ -282,7 +282,8 @@ void gated_rms_norm_had(const Tensor& x, const Tensor* w, const Tensor& g, const
     check_abi(exl3r_gated_rms_norm_had(x.data, code(x.dtype), ldx, ptr(w), code_or(w, DType::F32), w_groups, g.data,
                                        code(g.dtype), ldg, y ? y->data : nullptr, ldy, ptr(pre_scale), pre_rows,
                                        out.data, ldo,
-                                       rows, dim, eps, bias, gate_first ? 1 : 0, gate_act, had_scale, s.get()));
+                                       rows, dim, eps, bias, gate_first ? 1 : 0, gate_act | (exact ? EXL3R_HAD_EXACT : 0),
+                                       had_scale, s.get()));
 }
 
 void mul_sigmoid_(const Tensor& x, const Tensor& y, const Stream& s)
@@ -565,7 +566,8 @@ static int rotary_dim_of(const char* op, const Tensor& inv_freq, const Tensor* c
 void rope_had(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tensor* out_k, const Tensor& inv_freq,
               int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
               float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Tensor* q_post_scale,
-              const Tensor* k_post_scale, const Stream& s, const Tensor* position_ids, const Tensor* cs_table)
+              const Tensor* k_post_scale, const Stream& s, const Tensor* position_ids, const Tensor* cs_table,
+              bool exact)
 {
     require(q.dim() == 4 && q.dtype == DType::F16, "rope_had: q must be f16 (bsz, seq_len, heads, head_dim)");
     const int64_t bsz = q.size(0), seq = q.size(1), hd = q.size(3);
@@ -589,8 +591,9 @@ void rope_had(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tenso
                              out_k ? out_k->data : nullptr, kts, (int)hk, code(q.dtype), bsz, seq, (int)hd,
                              (const float*)inv_freq.data, rdim, (int32_t)position,
                              (const int32_t*)ptr(positions), (const int32_t*)ptr(position_ids), ptr(q_norm),
-                             ptr(k_norm), code_or(nw, DType::F16), norm_eps, norm_constant_bias, (int)rope_mode,
-                             attn_factor, ptr(q_post_scale), ptr(k_post_scale), ptr(cs_table), s.get()));
+                             ptr(k_norm), code_or(nw, DType::F16), norm_eps, norm_constant_bias,
+                             (int)rope_mode | (exact ? EXL3R_HAD_EXACT : 0), attn_factor, ptr(q_post_scale),
+                             ptr(k_post_scale), ptr(cs_table), s.get()));
 }
 
 void rope_paged_kv(const Tensor& q, const Tensor& out_q, const Tensor& k, const Tensor* out_k, const Tensor& v,
@@ -634,7 +637,7 @@ void rope_paged_kv_had(const Tensor& q, const Tensor& out_q, const Tensor& k, co
                        float attn_factor, const Tensor& k_cache, const Tensor& v_cache, const Tensor& block_table,
                        const Tensor& cache_seqlens, int32_t* err_flag, const Tensor* q_post_scale,
                        const Tensor* k_post_scale, const Tensor* v_post_scale, const Stream& s,
-                       const Tensor* cs_table)
+                       const Tensor* cs_table, bool exact)
 {
     require(q.dim() == 4 && k.dim() == 4 && v.dim() == 4 && q.dtype == DType::F16,
             "rope_paged_kv_had: q, k, v must be f16 (bsz, seq_len, heads, head_dim)");
@@ -659,10 +662,11 @@ void rope_paged_kv_had(const Tensor& q, const Tensor& out_q, const Tensor& k, co
                                       code(q.dtype), bsz, seq, (int)hd, (const float*)inv_freq.data,
                                       rdim, (int32_t)position, (const int32_t*)ptr(positions),
                                       nullptr, ptr(q_norm), ptr(k_norm), code_or(nw, DType::F16), norm_eps,
-                                      norm_constant_bias, (int)rope_mode, attn_factor, k_cache.data, v_cache.data,
-                                      (int)k_cache.size(1), k_cache.size(0), (const int32_t*)block_table.data,
-                                      block_table.size(1), (const int32_t*)cache_seqlens.data, err_flag,
-                                      ptr(q_post_scale), ptr(k_post_scale), ptr(v_post_scale), ptr(cs_table), s.get()));
+                                      norm_constant_bias, (int)rope_mode | (exact ? EXL3R_HAD_EXACT : 0), attn_factor,
+                                      k_cache.data, v_cache.data, (int)k_cache.size(1), k_cache.size(0),
+                                      (const int32_t*)block_table.data, block_table.size(1),
+                                      (const int32_t*)cache_seqlens.data, err_flag, ptr(q_post_scale),
+                                      ptr(k_post_scale), ptr(v_post_scale), ptr(cs_table), s.get()));
 }
 
 void embedding(const Tensor& table, const Tensor& ids, const Tensor& out, int32_t* err_flag, const Stream& s)

@@ -159,9 +159,10 @@ void gated_rms_norm(const Tensor& x, const Tensor* w, const Tensor& y, const Ten
 // gated_rms_norm into an f16 y (optional) that feeds o_proj's input rotation: out = had_r_128(y, pre_scale)
 // (src/qwen3_5.rs:208-214 -> src/modules.rs:224-227), one pass.
 // Norm row r uses pre_scale[(r % pre_rows) * dim ..] (rows = tokens * heads of head_dim: pre_rows = heads).
+// Rows of 128 run the transform on the matrix cores; exact: the reference's butterfly (EXL3R_HAD_EXACT).
 void gated_rms_norm_had(const Tensor& x, const Tensor* w, const Tensor& g, const Tensor& out, const Tensor* y,
                         const Tensor* pre_scale, float eps, float bias, int w_groups, bool gate_first, int gate_act,
-                        float had_scale, const Stream& s, int pre_rows = 1);
+                        float had_scale, const Stream& s, int pre_rows = 1, bool exact = false);
 // src/ffi.rs:616-618: x *= sigmoid(y), in place.
 void mul_sigmoid_(const Tensor& x, const Tensor& y, const Stream& s);
 // src/ffi.rs:622-624: split [.., heads * 2 * head_dim] interleaved (q | g) rows into q [.., heads, head_dim] and
@@ -201,17 +202,18 @@ void rope_had(const Tensor& q, const Tensor& out_q, const Tensor* k, const Tenso
               int64_t position, const Tensor* positions, const Tensor* q_norm, const Tensor* k_norm, float norm_eps,
               float norm_constant_bias, RopeStyle rope_mode, float attn_factor, const Tensor* q_post_scale,
               const Tensor* k_post_scale, const Stream& s, const Tensor* position_ids = nullptr,
-              const Tensor* cs_table = nullptr);
+              const Tensor* cs_table = nullptr, bool exact = false);
 // rope_paged_kv() on the raw f16 outputs of the q / k / v projections (heads packed), each first given its
 // projection's output rotation had_r_128(y, y, None, svh); outside the fused launch v (and k without out_k)
-// are rotated in place.
+// are rotated in place.  (rope_had and rope_paged_kv_had: the fused launch runs the transforms on the
+// matrix cores; exact: the reference's butterfly, EXL3R_HAD_EXACT.)
 void rope_paged_kv_had(const Tensor& q, const Tensor& out_q, const Tensor& k, const Tensor* out_k, const Tensor& v,
                        const Tensor& inv_freq, int64_t position, const Tensor* positions, const Tensor* q_norm,
                        const Tensor* k_norm, float norm_eps, float norm_constant_bias, RopeStyle rope_mode,
                        float attn_factor, const Tensor& k_cache, const Tensor& v_cache, const Tensor& block_table,
                        const Tensor& cache_seqlens, int32_t* err_flag, const Tensor* q_post_scale,
                        const Tensor* k_post_scale, const Tensor* v_post_scale, const Stream& s,
-                       const Tensor* cs_table = nullptr);
+                       const Tensor* cs_table = nullptr, bool exact = false);
 // rope() fused with the paged KV-cache append that follows it in paged attention (src/modules.rs:666-704,
 // ffi.rs:337-350): the roped k (also written to out_k when given) and v go to k_cache / v_cache
 // [pages, page_size, kv_heads, head_dim] at cache_seqlens[b] + s through block_table [bsz, max_blocks].

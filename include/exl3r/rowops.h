@@ -88,7 +88,8 @@ extern "C" {
 #define EXL3R_ACT_MUL_SIGMOID 2 /* x * sigmoid(y) */
 
 /* Flag of the fused Hadamard entry points (exl3r_act_mul_had's rotate_in, exl3r_rms_norm_had's rotate_x,
- * the rope_mode of exl3r_rope_had / exl3r_rope_paged_kv_had, exl3r_rope_desc's rotate): the 128-point
+ * the rope_mode of exl3r_rope_had / exl3r_rope_paged_kv_had, exl3r_rope_desc's rotate,
+ * exl3r_gated_rms_norm_had's gate_act): the 128-point
  * transforms as the reference's fp32 butterfly (bit-identical to the unfused calls) instead of the
  * matrix-core form (within the stated rounding tolerance of it). */
 #define EXL3R_HAD_EXACT 16
@@ -178,9 +179,12 @@ EXL3R_API int exl3r_gated_rms_norm(const void* x, int x_dtype, int64_t ldx, cons
  *   pre_scale: the projection's f16 suh or NULL; norm row r uses pre_scale[(r % pre_rows) * dim ..] --
  *         with the usual layout (rows = tokens * heads of dim = head_dim, dense) pre_rows = heads and
  *         pre_scale is [heads * head_dim]; pre_rows > 1 needs rows % pre_rows == 0 and ldo == ldy == dim.
- * dim % 128 == 0; out and y alias nothing.  Bit-identical to exl3r_gated_rms_norm with an f16 y
- * followed by exl3r_had_r_128 over the [rows / pre_rows, pre_rows * dim] projection rows; unaligned or
- * f32-x rows run those calls.
+ *   gate_act: as exl3r_gated_rms_norm, | EXL3R_HAD_EXACT for the reference's butterfly.
+ * dim % 128 == 0; out and y alias nothing.  Rows of dim 128 (16-bit x, f32 or bf16 gate, 16-byte
+ * aligned) run the transform on the matrix cores: bit-identical to exl3r_gated_rms_norm with an f16 y
+ * followed by exl3r_had_r_128_mfma over the [rows / pre_rows, pre_rows * dim] projection rows.  With
+ * EXL3R_HAD_EXACT, and at other row lengths, bit-identical to it followed by exl3r_had_r_128;
+ * unaligned or f32-x rows run those calls.
  */
 EXL3R_API int exl3r_gated_rms_norm_had(const void* x, int x_dtype, int64_t ldx, const void* w, int w_dtype,
                              int w_groups, const void* g, int g_dtype, int64_t ldg, void* y, int64_t ldy,

@@ -426,7 +426,8 @@ int main()
         std::snprintf(msg, sizeof msg, "z max ulp %lld, rotation of z bitwise", (long long)u);
         report("ffi::act_mul_had silu -> had", ok, ok ? msg : "DIFFER");
     }
-    // rope_had: the q / k output rotations then head-norm + NeoX RoPE, equal to had_r_128 then rope.
+    // rope_had (exact: the butterfly): the q / k output rotations then head-norm + NeoX RoPE, equal to
+    // had_r_128 then rope.
     {
         const int T = 1100, hq = 4, hk = 2, hd = 128;
         auto qh = host_normal(DType::F16, T * hq * hd, 0.f, 2.f), kh = host_normal(DType::F16, T * hk * hd, 0.f, 2.f);
@@ -446,13 +447,13 @@ int main()
         auto qn = upload(nh, DType::F16, { hd }, s), svq = upload(sq, DType::F16, { hq * hd }, s);
         auto f = upload(fb, DType::F32, { hd / 2 }, s);
         ffi::rope_had(q.t, q.t, &k.t, &k.t, f.t, 5, nullptr, &qn.t, &qn.t, 1e-6f, 0.f, RopeStyle::NeoX, 1.f, &svq.t,
-                      nullptr, s);
+                      nullptr, s, nullptr, nullptr, true);
         Tensor q2v(q2.t.data, DType::F16, { T, hq * hd }), k2v(k2.t.data, DType::F16, { T, hk * hd });
         ffi::had_r_128(q2v, q2v, nullptr, &svq.t, 1.f, s);
         ffi::had_r_128(k2v, k2v, nullptr, nullptr, 1.f, s);
         ffi::rope(q2.t, q2.t, &k2.t, &k2.t, f.t, 5, nullptr, &qn.t, &qn.t, 1e-6f, 0.f, RopeStyle::NeoX, 1.f, s);
         const bool ok = download(q, s) == download(q2, s) && download(k, s) == download(k2, s);
-        report("ffi::rope_had == had_r_128 + rope", ok, ok ? "bitwise" : "DIFFER");
+        report("ffi::rope_had exact == had_r_128 + rope", ok, ok ? "bitwise" : "DIFFER");
     }
     // rope_cs: RoPE from a {cos, sin} table built once, bitwise equal to rope() evaluating sin / cos.
     {
@@ -495,7 +496,7 @@ int main()
         report("ffi::rope_qg == deinterleave_qg + rope", ok, ok ? "bitwise" : "DIFFER");
     }
     // gated_rms_norm_had: the GDN output norm (8 tokens x 4 heads of 128, one o_proj row per token)
-    // into o_proj's input rotation, bitwise equal to the gated norm followed by had_r_128.
+    // into o_proj's input rotation (exact: the butterfly), bitwise equal to the gated norm followed by had_r_128.
     {
         const int heads = 4, rows = 8 * heads, dim = 128;
         auto xh = host_normal(DType::BF16, rows * dim, 0.f, 1.f), gh = host_normal(DType::F32, rows * dim, 0.f, 2.f);
@@ -510,12 +511,12 @@ int main()
         auto w = upload(wh, DType::F32, { dim }, s), sv = upload(sh, DType::F16, { heads * dim }, s);
         auto out = OwnedTensor::empty(DType::F16, { rows, dim }), y = OwnedTensor::empty(DType::F16, { rows, dim });
         auto ref = OwnedTensor::empty(DType::F16, { rows / heads, heads * dim });
-        ffi::gated_rms_norm_had(x.t, &w.t, g.t, out.t, nullptr, &sv.t, 1e-6f, 0.f, 1, false, 1, 1.f, s, heads);
+        ffi::gated_rms_norm_had(x.t, &w.t, g.t, out.t, nullptr, &sv.t, 1e-6f, 0.f, 1, false, 1, 1.f, s, heads, true);
         ffi::gated_rms_norm(x.t, &w.t, y.t, g.t, 1e-6f, 0.f, 1, false, 1, s);
         Tensor yv(y.t.data, DType::F16, { rows / heads, heads * dim });
         ffi::had_r_128(yv, ref.t, &sv.t, nullptr, 1.f, s);
         const bool ok = download(out, s) == download(ref, s);
-        report("ffi::gated_rms_norm_had == gated norm + had_r_128", ok, ok ? "bitwise" : "DIFFER");
+        report("ffi::gated_rms_norm_had exact == gated norm + had_r_128", ok, ok ? "bitwise" : "DIFFER");
     }
     // Graph capture: RmsNorm::forward_res (output from an arena) and RoPE::apply (positions read from device
     // memory) recorded into a HIP graph in the strict (global) capture mode, which fails any allocation or

@@ -1,17 +1,20 @@
 """GPU parity of exl3r_gated_rms_norm_had: the Qwen3.5 gated-delta-net output norm whose f16 output feeds
 o_proj's random-Hadamard input rotation in one pass (src/qwen3_5.rs:208-214 -> src/modules.rs:224-227).
-The rotated output is checked bit for bit against the unfused GPU calls (exl3r_gated_rms_norm into an
-f16 y, then exl3r_had_r_128) and against the oracle's rotation of that y; y itself against the oracle
-at the gated norm's tolerance (<= 1 ulp of f16).  Covers the Qwen3.5 prefill shape (head_dim-128 rows
-on the short-row kernel), longer rows (the workgroup kernel), both gates before and after the norm,
-weight groups, a bias, a missing pre-scale, the unaligned fallback, zero rows and the errors."""
+The rotated output is checked bit for bit against the unfused GPU calls with the same form of the
+transform (exl3r_gated_rms_norm into an f16 y, then exl3r_had_r_128_mfma for rows of 128 on the
+short-row kernel, exl3r_had_r_128 with EXL3R_HAD_EXACT and elsewhere) and against the oracle's rotation
+of that y (bitwise with the butterfly, within the matrix-core transform's tolerance otherwise); y itself
+against the oracle at the gated norm's tolerance (<= 1 ulp of f16).  Covers the Qwen3.5 prefill shape
+(head_dim-128 rows on the short-row kernel) in both forms, row counts that end inside a wave's 4 rows,
+longer rows (the workgroup kernel), both gates before and after the norm, weight groups, a bias, a
+missing pre-scale, the unaligned fallback, zero rows and the errors."""
 import numpy as np
 import pytest
 import torch
 
 import exl3r
 import exl3r.ffi as ffi
-from _gpu import NTHREADS, assert_bitwise, assert_close_ulp, dev_normal, from_dev
+from _gpu import NTHREADS, assert_bitwise, assert_close_ulp, assert_had_close, dev_normal, from_dev
 from oracle import oracle as orc
 from test_gpu_act_had import suh
 
@@ -21,9 +24,11 @@ F32, F16, BF16 = orc.F32, orc.F16, orc.BF16
 
 
 def run(rows, dim, xt=BF16, gt=F32, wt=F32, w_groups=1, gate_first=False, gate_act=0, cb=0.0, with_w=True,
-        with_y=True, pre=True, had_scale=1.0, ld=None, heads=1, seed=0):
+        with_y=True, pre=True, had_scale=1.0, ld=None, heads=1, seed=0, exact=False):
     """`heads` norm rows of dim form one projection input row (pre_rows): the projection's suh has
-    heads * dim entries and the reference rotates the [rows / heads, heads * dim] projection rows."""
+    heads * dim entries and the reference rotates the [rows / heads, heads * dim] projection rows.  The
+    matrix-core transform runs where the short-row kernel takes rows of 128 (16-bit x, f32 or bf16 gate,
+    aligned rows) unless exact."""
     ld = ld or dim
     x = dev_normal((rows, ld), 0, 1, xt, seed)[:, :dim]
     g = dev_normal((rows, ld), 0, 2, gt, seed + 1)[:, :dim]
@@ -31,13 +36,17 @@ def run(rows, dim, xt=BF16, gt=F32, wt=F32, w_groups=1, gate_first=False, gate_a
     p = suh(heads * dim, seed + 3) if pre else None
     y = torch.empty((rows, dim), device="cuda", dtype=torch.float16) if with_y else None
     out = torch.empty((rows, dim), device="cuda", dtype=torch.float16)
-    ffi.gated_rms_norm_had(x, w, g, out, 1e-6, p, y, cb, w_groups, gate_first, gate_act, had_scale, pre_rows=heads)
+    mf = not exact and dim == 128 and xt != F32 and gt in (F32, BF16) and ld % 8 == 0
+    ffi.gated_rms_norm_had(x, w, g, out, 1e-6, p, y, cb, w_groups, gate_first, gate_act, had_scale, pre_rows=heads,
+                           exact=exact)
     uy = torch.empty((rows, dim), device="cuda", dtype=torch.float16)
     ffi.gated_rms_norm(x, w, uy, g, 1e-6, cb, w_groups, gate_first, gate_act)
     uout = torch.empty_like(out)
-    ffi.had_r_128(uy.view(rows // heads, heads * dim), uout.view(rows // heads, heads * dim), p, None, had_scale)
+    ffi.had_r_128(uy.view(rows // heads, heads * dim), uout.view(rows // heads, heads * dim), p, None, had_scale,
+                  mfma=mf)
     torch.cuda.synchronize()
-    tag = f"gated_had {rows}x{dim} x{xt} g{gt} G{w_groups} first{int(gate_first)} act{gate_act} y{int(with_y)}"
+    tag = (f"gated_had {rows}x{dim} x{xt} g{gt} G{w_groups} first{int(gate_first)} act{gate_act} y{int(with_y)} "
+           f"{'mfma' if mf else 'exact'}")
     assert_bitwise(from_dev(out), from_dev(uout), what=tag + " vs unfused")
     if with_y:
         assert_bitwise(from_dev(y), from_dev(uy), what=tag + " y vs unfused")
@@ -45,17 +54,34 @@ def run(rows, dim, xt=BF16, gt=F32, wt=F32, w_groups=1, gate_first=False, gate_a
                             w=from_dev(w) if with_w else None, wt=wt, w_groups=w_groups, eps=1e-6, cb=cb,
                             gate_first=gate_first, gate_act=gate_act, nthreads=NTHREADS)
     assert_close_ulp(from_dev(uy), ey, F16, 1, what=tag + " y vs oracle")
-    eo = orc.had_r_128(np.ascontiguousarray(from_dev(uy)).reshape(rows // heads, heads * dim), F16,
-                       pre=from_dev(p) if p is not None else None, scale=had_scale, nthreads=NTHREADS)
-    assert_bitwise(from_dev(out).reshape(rows // heads, heads * dim), eo, what=tag + " out vs oracle had_r_128(y)")
+    yin = np.ascontiguousarray(from_dev(uy)).reshape(rows // heads, heads * dim)
+    eo = orc.had_r_128(yin, F16, pre=from_dev(p) if p is not None else None, scale=had_scale, nthreads=NTHREADS)
+    got = from_dev(out).reshape(rows // heads, heads * dim)
+    if mf:
+        xin = orc.to_f32(yin, F16).astype(np.float64) * (orc.to_f32(from_dev(p), F16).astype(np.float64)[None, :]
+                                                         if p is not None else 1.0)
+        assert_had_close(got, eo, xin, 0.0883883461356163 * had_scale, what=tag + " out vs oracle had_r_128(y)")
+    else:
+        assert_bitwise(got, eo, what=tag + " out vs oracle had_r_128(y)")
 
 
 @pytest.mark.parametrize("gate_act", [0, 1])
 @pytest.mark.parametrize("gate_first", [False, True])
 def test_qwen35_gdn_output_into_o_proj(gate_act, gate_first):
-    """2048 tokens x 32 value heads of 128: bf16 core, f32 gate, f32 weight, the short-row kernel."""
+    """2048 tokens x 32 value heads of 128: bf16 core, f32 gate, f32 weight, the short-row kernel (its
+    matrix-core form; the butterfly with EXL3R_HAD_EXACT for one of the gates)."""
     run(2048 * 32, 128, gate_first=gate_first, gate_act=gate_act, with_y=False, heads=32,
         seed=gate_act + 2 * gate_first)
+    if gate_act == 0:
+        run(512 * 32, 128, gate_first=gate_first, gate_act=gate_act, with_y=False, heads=32, seed=20 + gate_first,
+            exact=True)
+
+
+@pytest.mark.parametrize("rows", [1, 3, 5, 4 * 16 + 2, 4097])
+def test_row_counts_inside_a_span(rows):
+    """Row counts that end inside a wave's 4 rows (the rows past the end take part in the MFMAs with
+    zeros and store nothing), with y written, bf16 gate and weight, f16 x."""
+    run(rows, 128, xt=F16, gt=BF16, wt=BF16, had_scale=-0.75, seed=30 + rows)
 
 
 @pytest.mark.parametrize("xt,gt,wt", [(F16, BF16, F16), (BF16, BF16, BF16), (F16, F32, F32)])
