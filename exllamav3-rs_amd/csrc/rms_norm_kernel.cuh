@@ -102,7 +102,9 @@ __device__ __forceinline__ float gate_act(int gact, float g) { return gact ? act
 template <int MODE>
 __device__ __forceinline__ int64_t weight_row(const RmsArgs& a, int64_t row)
 {
-    if constexpr (MODE == RMS_GATED) return (row % a.w_groups) * a.dim;
+    // (one weight group, the usual case, skips the per-row 64-bit remainder: a kernel-uniform branch,
+    // gated norm [131072, 128] 26.9 -> 25.2 us)
+    if constexpr (MODE == RMS_GATED) return a.w_groups == 1 ? 0 : (row % a.w_groups) * a.dim;
     else return 0;
 }
 
