@@ -108,6 +108,17 @@ __device__ __forceinline__ int64_t weight_row(const RmsArgs& a, int64_t row)
     else return 0;
 }
 
+// Element offset of the pre-scale row a norm row uses (hpre_rows norm rows form one projection row):
+// kernel-uniform branches, a mask for a power-of-two count (heads per projection row), the 64-bit
+// remainder otherwise.
+__device__ __forceinline__ int64_t pre_row(const RmsArgs& a, int64_t row)
+{
+    const int pr = a.hpre_rows;
+    if (pr <= 1) return 0;
+    if ((pr & (pr - 1)) == 0) return (row & (pr - 1)) * a.dim;
+    return (row % pr) * a.dim;
+}
+
 __device__ __forceinline__ int64_t load_id(const void* ids, int idt, int64_t i)
 {
     return idt == DT_I64 ? ((const int64_t*)ids)[i] : (int64_t)((const int32_t*)ids)[i];
@@ -376,7 +387,7 @@ __device__ __forceinline__ void rms_chunk2(const RmsArgs& a, int64_t row, char* 
             TF16::Vec v = yv;
             if (a.hpre[i])
             {
-                const TF16::Vec p = load8<TF16>(a.hpre[i], (a.hpre_rows > 1 ? (row % a.hpre_rows) * a.dim : 0) + e);
+                const TF16::Vec p = load8<TF16>(a.hpre[i], pre_row(a, row) + e);
                 #pragma unroll
                 for (int q = 0; q < 4; ++q) v.a[q] = hmul2(v.a[q], p.a[q]);
             }
@@ -505,7 +516,7 @@ __device__ __forceinline__ void rms_finish(const RmsArgs& a, int64_t row, int ti
                         TF16::Vec v = yp;
                         if (plive && a.hpre[i])
                         {
-                            const TF16::Vec p = load8<TF16>(a.hpre[i], (a.hpre_rows > 1 ? (row % a.hpre_rows) * a.dim : 0) + ep);
+                            const TF16::Vec p = load8<TF16>(a.hpre[i], pre_row(a, row) + ep);
                             #pragma unroll
                             for (int q = 0; q < 4; ++q) v.a[q] = hmul2(v.a[q], p.a[q]);
                         }
@@ -650,7 +661,7 @@ __global__ __launch_bounds__(256) void k_rms_rows(RmsArgs a)
                     rv[i] = load8s<RT>((const char*)a.r + row * a.ldr * RT::bytes, e);
                 if (a.w) wv[i] = prefetch_w8(a.w, a.wt, weight_row<MODE>(a, row) + e);
                 if constexpr ((HAD & HAD_OUT) != 0)
-                    if (a.hpre[0]) pv[i] = load8<TF16>(a.hpre[0], (a.hpre_rows > 1 ? (row % a.hpre_rows) * a.dim : 0) + e);
+                    if (a.hpre[0]) pv[i] = load8<TF16>(a.hpre[0], pre_row(a, row) + e);
             }
         }
         #pragma unroll
