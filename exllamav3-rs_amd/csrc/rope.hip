@@ -75,7 +75,27 @@ struct RopeArgs
     const float2* cst;
     // 8-lane kernel: the head norm's sum of squares in fp32 (1) instead of fp64 (sweep/test build only).
     int ss32;
+    // 8-lane kernel: item / nslice as a multiply by ns_m and shifts by ns_l (udiv_magic), set at its launch.
+    uint64_t ns_m;
+    int ns_l;
 };
+
+// Unsigned division by an invariant d >= 1 as a multiply-high and two shifts (Granlund and Montgomery,
+// "Division by invariant integers using multiplication", PLDI 1994, the round-up method): with
+// l = ceil(log2 d) and m = floor(2^64 (2^l - d) / d) + 1 (below 2^64), n / d = (t + ((n - t) >> min(l, 1)))
+// >> max(l - 1, 0) for t = mulhi(m, n), every n < 2^64.  For wave-uniform n it runs on the scalar unit and
+// holds no vector register (the compiler's division keeps the divisor's float reciprocal in one).
+static inline void udiv_magic_init(uint64_t d, uint64_t& m, int& l)
+{
+    l = 0;
+    while (((uint64_t)1 << l) < d) ++l;
+    m = (uint64_t)((((unsigned __int128)1 << 64) * (((uint64_t)1 << l) - d)) / d) + 1;
+}
+__device__ __forceinline__ uint64_t udiv_magic(uint64_t n, uint64_t m, int l)
+{
+    const uint64_t t = __umul64hi(m, n);
+    return (t + ((n - t) >> (l < 1 ? l : 1))) >> (l > 1 ? l - 1 : 0);
+}
 
 // Where a kernel takes its rotary pairs: evaluated from inv_freq[t] * pos, evaluated from the angle
 // table, or read from the precomputed {cos, sin} table.
@@ -853,7 +873,7 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
     // Loads of one item: the lane's two chunks of head (slice * P + p) * 8 + grp for each of the P passes,
     // and its rotary pairs (SRC_CS) or the token's position (SRC_FREQ).
     auto issue = [&](Item& t, int64_t item) __attribute__((always_inline)) {
-        t.tok = item / nslice;
+        t.tok = (int64_t)udiv_magic((uint64_t)item, a.ns_m, a.ns_l);   // item / nslice
         t.slice = (int)(item - t.tok * nslice);
         // The row of head h of token tok.
         auto head_base = [&](int h) __attribute__((always_inline)) -> const char* {
@@ -1316,7 +1336,9 @@ static void launch_rope_nx_p(const RopeArgs& a, hipStream_t s)
     if (kFlat && wpc == 0) blocks = (runs + 3) / 4;
     if (blocks > (runs + 3) / 4) blocks = (runs + 3) / 4;
     if (blocks > kMaxGridX) blocks = kMaxGridX;
-    launch(k_rope_nx<IO, MODE, NORM, SRC, QOUT, P, APPEND, HADR>, (unsigned)blocks, 256, lds, s, a, nslice, run);
+    RopeArgs b = a;
+    udiv_magic_init((uint64_t)nslice, b.ns_m, b.ns_l);
+    launch(k_rope_nx<IO, MODE, NORM, SRC, QOUT, P, APPEND, HADR>, (unsigned)blocks, 256, lds, s, b, nslice, run);
 }
 
 // Passes per item: one for NeoX, two for GPT-J (its token's sin / cos or table row shared by two passes).
