@@ -1,7 +1,8 @@
-"""Capture safety: a decode-layer sequence of the fused ops captured in a HIP graph (through
-torch.cuda.CUDAGraph on its capture stream) is replayed several times with new device-side
-positions and residual contents between replays, and every replay must equal the eager run on the
-same inputs bit for bit.  The ops allocate nothing, synchronise nothing and record no memset."""
+"""Capture safety: a decode-layer sequence of the fused ops, a decode tail (gates, paged append,
+samplers) and a prefill layer's fused rotations (matrix-core transforms, per-launch dynamic LDS) are
+each captured in a HIP graph (through torch.cuda.CUDAGraph on its capture stream) and replayed several
+times with new device-side inputs between replays; every replay must equal the eager run on the same
+inputs bit for bit.  The ops allocate nothing, synchronise nothing and record no memset."""
 import numpy as np
 import pytest
 import torch
@@ -153,3 +154,90 @@ def test_tail_graph_replays_match_eager():
                 a, b = a.view(torch.int16), b.view(torch.int16)
             assert torch.equal(a, b), (rep, k)
         assert not torch.equal(g_buf["ids_a"], torch.zeros_like(g_buf["ids_a"]))
+
+
+def prefill(buf):
+    """The fused rotations of a prefill layer (their matrix-core defaults): the previous projection's output
+    rotation into the residual norm and three projection inputs, the q / k / v output rotations into RoPE and
+    the paged append (post-scales staged in LDS), the gated norm into o_proj's input rotation, and the MLP
+    tail from the raw gate / up outputs."""
+    ffi.rms_norm_had(buf["x"], buf["w"], [buf["xq"], buf["xk"], buf["xv"]], [buf["sq"], buf["sk"], buf["sv"]], 1e-6,
+                     r=buf["r"], rotate_x=True, x_post_scale=buf["svx"])
+    ffi.rope_paged_kv_had(buf["q"], buf["oq"], buf["k"], buf["ok"], buf["v"], buf["inv"], 0, buf["sl"], buf["qn"],
+                          buf["kn"], 1e-6, 0.0, exl3r.ROPE_NEOX, 1.0, buf["kc"], buf["vc"], buf["bt"], buf["sl"],
+                          q_post_scale=buf["pq"], k_post_scale=buf["pk"], v_post_scale=buf["pv"])
+    ffi.gated_rms_norm_had(buf["ga"], buf["gw"], buf["gg"], buf["go"], 1e-6, buf["gs"], pre_rows=4)
+    ffi.act_mul_had("silu", buf["mg"], buf["mu"], buf["mo"], buf["ms"], rotate_x=True, rotate_y=True,
+                    x_post_scale=buf["mpg"], y_post_scale=buf["mpu"])
+
+
+def make_prefill(seed):
+    T, H, hq, hk, hd, I = 384, 1024, 8, 2, 128, 2048
+    f16 = torch.float16
+
+    def sign(n, s):
+        g = torch.Generator(device="cuda").manual_seed(s)
+        return torch.where(torch.rand(n, generator=g, device="cuda") < 0.5, -1.0, 1.0).to(f16)
+
+    b = {"x": dev_normal((T, H), 0, 1, 1, seed), "r": dev_normal((T, H), 0, 4, 0, seed + 1),
+         "w": dev_normal((H,), 1, 0.1, 1, seed + 2), "svx": sign(H, seed + 3)}
+    for i, n in enumerate(("xq", "xk", "xv")):
+        b[n] = torch.empty((T, H), device="cuda", dtype=f16)
+        b["s" + n[1]] = sign(H, seed + 4 + i)
+    b.update({"q": dev_normal((1, T, hq, hd), 0, 2, 1, seed + 10), "k": dev_normal((1, T, hk, hd), 0, 2, 1, seed + 11),
+              "v": dev_normal((1, T, hk, hd), 0, 2, 1, seed + 12),
+              "oq": torch.empty((1, T, hq, hd), device="cuda", dtype=f16),
+              "ok": torch.empty((1, T, hk, hd), device="cuda", dtype=f16),
+              "qn": dev_normal((hd,), 1, 0.1, 1, seed + 13), "kn": dev_normal((hd,), 1, 0.1, 1, seed + 14),
+              "inv": torch.from_numpy((1.0 / 1e6 ** (np.arange(0, hd, 2) / hd)).astype(np.float32)).cuda(),
+              "kc": torch.zeros((8, 64, hk, hd), device="cuda", dtype=f16),
+              "vc": torch.zeros((8, 64, hk, hd), device="cuda", dtype=f16),
+              "bt": torch.arange(8, dtype=torch.int32, device="cuda").view(1, 8),
+              "sl": torch.zeros(1, dtype=torch.int32, device="cuda"),
+              "pq": sign(hq * hd, seed + 15), "pk": sign(hk * hd, seed + 16), "pv": sign(hk * hd, seed + 17),
+              "ga": dev_normal((T * 4, hd), 0, 1, 2, seed + 20), "gg": dev_normal((T * 4, hd), 0, 2, 0, seed + 21),
+              "gw": dev_normal((hd,), 1, 0.1, 0, seed + 22), "go": torch.empty((T * 4, hd), device="cuda", dtype=f16),
+              "gs": sign(4 * hd, seed + 23),
+              "mg": dev_normal((T, I), 0, 1, 1, seed + 30), "mu": dev_normal((T, I), 0, 1, 1, seed + 31),
+              "mo": torch.empty((T, I), device="cuda", dtype=f16), "ms": sign(I, seed + 32),
+              "mpg": sign(I, seed + 33), "mpu": sign(I, seed + 34)})
+    return b
+
+
+def test_prefill_rotations_graph_replays_match_eager():
+    """The matrix-core fused rotations under capture (MFMAs, dynamic LDS sized by the head count): each
+    replay, with new projection outputs, residual and cache lengths written between replays, equals the
+    eager run bit for bit."""
+    g_buf = make_prefill(40)
+    e_buf = {k: v.clone() for k, v in g_buf.items()}
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        prefill(g_buf)
+    torch.cuda.synchronize()
+    for k in g_buf:
+        g_buf[k].copy_(e_buf[k])
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        prefill(g_buf)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(7)
+    for rep in range(4):
+        sl = torch.tensor([int(rng.integers(0, 64))], dtype=torch.int32)
+        new = {"x": dev_normal((384, 1024), 0, 1, 1, 400 + rep), "r": dev_normal((384, 1024), 0, 4, 0, 410 + rep),
+               "q": dev_normal((1, 384, 8, 128), 0, 2, 1, 420 + rep), "mg": dev_normal((384, 2048), 0, 1, 1, 430 + rep),
+               "ga": dev_normal((1536, 128), 0, 1, 2, 440 + rep)}
+        for b in (g_buf, e_buf):
+            b["sl"].copy_(sl)
+            for k, v in new.items():
+                b[k].copy_(v)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        prefill(e_buf)
+        torch.cuda.synchronize()
+        for k in ("r", "xq", "xk", "xv", "oq", "ok", "kc", "vc", "go", "mo"):
+            a, b = g_buf[k], e_buf[k]
+            if a.dtype in (torch.float16, torch.bfloat16):
+                a, b = a.view(torch.int16), b.view(torch.int16)
+            assert torch.equal(a, b), (rep, k)
