@@ -1248,7 +1248,10 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
     // against 31.2 us.  An unconditional issue -- past its last item a wave reloading the grid's last
     // item -- makes it exact too (vmcnt(2) instead of vmcnt(0) before an item's math) and ran slower in
     // every instance, same process: C4 33.1 -> 33.9 us, from the table 31.4 -> 39.3, the rotating paged
-    // form 38.4 -> 58.4 (13-20 VGPRs spilled: the next item's registers live across the math).)
+    // form 38.4 -> 58.4 (13-20 VGPRs spilled: the next item's registers live across the math).  Issuing
+    // the first item before the setup barrier ran the same or slower (the rotating C4 form 38.7 -> 41.4
+    // us: 3 VGPRs spilled), and so did carrying the item's token / slice along the walk instead of
+    // dividing (plain C4 at 93 VGPRs instead of 85).)
     Item A, B;
     issue(A, item);
     for (;;)
