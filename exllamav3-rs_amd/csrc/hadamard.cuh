@@ -250,8 +250,7 @@ __device__ __forceinline__ HadMfma had_mfma_operands(int lane)
 
 // The same operands from two words per lane, for kernels short of registers: A_0[e] depends on e only
 // through e & 3 (v < 4), so A_0 = {w0, w1, w0, w1} as f16 pairs, and A_1[e] = A_0[e] * (-1)^(e >> 2),
-// A_1 = {w0, w1, -w0, -w1}.  had_mfma_rebuild forms the two operands from the words where they are used:
-// the empty asm makes the words look new at each use, so the operands are not kept live in between.
+// A_1 = {w0, w1, -w0, -w1}.  had128_mfma_issue_w (below) forms them where the MFMAs are issued.
 struct HadMfmaWords
 {
     uint32_t w0, w1;
@@ -262,18 +261,6 @@ __device__ __forceinline__ HadMfmaWords had_mfma_words(int lane)
     const HadMfma H = had_mfma_operands(lane);
     return { __builtin_bit_cast(uint32_t, __builtin_shufflevector(H.a[0], H.a[0], 0, 1)),
              __builtin_bit_cast(uint32_t, __builtin_shufflevector(H.a[0], H.a[0], 2, 3)) };
-}
-
-__device__ __forceinline__ HadMfma had_mfma_rebuild(HadMfmaWords w)
-{
-    asm volatile("" : "+v"(w.w0), "+v"(w.w1));
-    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-    const u32x4v a0 = { w.w0, w.w1, w.w0, w.w1 };
-    const u32x4v a1 = { w.w0, w.w1, w.w0 ^ 0x80008000u, w.w1 ^ 0x80008000u };
-    HadMfma H;
-    H.a[0] = __builtin_bit_cast(f16x8, a0);
-    H.a[1] = __builtin_bit_cast(f16x8, a1);
-    return H;
 }
 
 // The transform in three steps, so that a caller can issue the MFMAs of several blocks before reading
@@ -300,7 +287,8 @@ __device__ __forceinline__ MfmaOut had128_mfma_issue(const HadMfma& H, const TF1
 }
 
 // had128_mfma_issue of one or two chunks from the two words, with one 4-VGPR operand: the MFMAs of A_0
-// first, then its upper words negated in place (A_1) for the others.
+// first, then its upper words negated in place (A_1) for the others.  The empty asm makes the words look
+// new at each use, so that the operand is formed here and not kept live between uses.
 __device__ __forceinline__ void had128_mfma_issue_w(HadMfmaWords w, const TF16::Vec& v0, MfmaOut& m0)
 {
     asm volatile("" : "+v"(w.w0), "+v"(w.w1));

@@ -1000,8 +1000,8 @@ void k_rope_nx(RopeArgs a, int nslice, int run)
             {
                 // Both spans' MFMAs, one wait, the two lane stages and the rounding to f16 (exl3r_had_r_128_mfma's
                 // operations on the same placement), then to the pass layout.
-                const HadMfma hm = had_mfma_rebuild(hw);
-                MfmaOut m0 = had128_mfma_issue(hm, lo), m1 = had128_mfma_issue(hm, hi);
+                MfmaOut m0, m1;
+                had128_mfma_issue_w(hw, lo, hi, m0, m1);
                 mfma_wait(m0, m1);
                 float f[8];
                 had128_mfma_finish(m0, f, l64, 0.0883883461356163f);
