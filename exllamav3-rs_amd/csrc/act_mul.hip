@@ -345,7 +345,7 @@ __global__ __launch_bounds__(256) void k_act_mul_had_mfma(ActArgs a)
     // wave-uniform item, row and span indices (scalar registers: the descriptors are scalar)
     const uint32_t wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const uint32_t nwaves = (gridDim.x * blockDim.x) >> 6;
-    const HadMfma H = had_mfma_operands(lane);
+    const HadMfmaWords hw = had_mfma_words(lane);
     const uint32_t lc = (uint32_t)mfma_chunk(lane);
     const brsrc xpost = row_rsrc(a.xpost, a.xpost ? out_bytes : 0), ypost = row_rsrc(a.ypost, a.ypost ? out_bytes : 0);
     const brsrc hpre = row_rsrc(a.hpre, a.hpre ? out_bytes : 0);
@@ -376,13 +376,15 @@ __global__ __launch_bounds__(256) void k_act_mul_had_mfma(ActArgs a)
             // the input rotations of every row in flight, their MFMAs issued together; each transform,
             // one rounding to f16, then the half post-scale
             constexpr int NX = IN_X ? UNROLL : 0, NY = IN_Y ? UNROLL : 0;
-            MfmaOut m[NX + NY];
+            TF16::Vec in[NX + NY];
             #pragma unroll
             for (int u = 0; u < UNROLL; ++u)
             {
-                if constexpr (IN_X) m[u] = had128_mfma_issue(H, xv[u]);
-                if constexpr (IN_Y) m[NX + u] = had128_mfma_issue(H, yv[u]);
+                if constexpr (IN_X) in[u] = xv[u];
+                if constexpr (IN_Y) in[NX + u] = yv[u];
             }
+            MfmaOut m[NX + NY];
+            had128_mfma_issue_w(hw, in, m);
             mfma_wait_all(m);
             auto finish = [&](const MfmaOut& mo, const TF16::Vec& p, bool on) {
                 float f[8];
@@ -402,19 +404,20 @@ __global__ __launch_bounds__(256) void k_act_mul_had_mfma(ActArgs a)
                 if constexpr (IN_Y) yv[u] = finish(m[NX + u], py, a.ypost != nullptr);
             }
         }
-        MfmaOut m[UNROLL];
+        TF16::Vec hv[UNROLL];
         #pragma unroll
         for (int u = 0; u < UNROLL; ++u)
         {
-            TF16::Vec hv = act_chunk_wave_in<ACT, LIMIT, IT>(xv[u], yv[u], a.limit);
-            if (a.z) bstore16(zr[u], off16, hv.a);
+            hv[u] = act_chunk_wave_in<ACT, LIMIT, IT>(xv[u], yv[u], a.limit);
+            if (a.z) bstore16(zr[u], off16, hv[u].a);
             if (a.hpre)
             {
                 #pragma unroll
-                for (int q = 0; q < 4; ++q) hv.a[q] = hmul2(hv.a[q], pp.a[q]);
+                for (int q = 0; q < 4; ++q) hv[u].a[q] = hmul2(hv[u].a[q], pp.a[q]);
             }
-            m[u] = had128_mfma_issue(H, hv);
         }
+        MfmaOut m[UNROLL];
+        had128_mfma_issue_w(hw, hv, m);
         mfma_wait_all(m);
         #pragma unroll
         for (int u = 0; u < UNROLL; ++u)

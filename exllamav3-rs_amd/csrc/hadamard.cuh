@@ -316,6 +316,24 @@ __device__ __forceinline__ void had128_mfma_issue_w(HadMfmaWords w, const TF16::
     m0.d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), b0, zero, 0, 0, 0);
     m1.d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), b1, zero, 0, 0, 0);
 }
+template <int N>
+__device__ __forceinline__ void had128_mfma_issue_w(HadMfmaWords w, const TF16::Vec (&v)[N], MfmaOut (&m)[N])
+{
+    asm volatile("" : "+v"(w.w0), "+v"(w.w1));
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    u32x4v a = { w.w0, w.w1, w.w0, w.w1 };
+    const f32x4 zero = { 0.0f, 0.0f, 0.0f, 0.0f };
+    #pragma unroll
+    for (int n = 0; n < N; ++n)
+        m[n].d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, v[n].a),
+                                                        zero, 0, 0, 0);
+    a.z ^= 0x80008000u;
+    a.w ^= 0x80008000u;
+    #pragma unroll
+    for (int n = 0; n < N; ++n)
+        m[n].d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, v[n].a),
+                                                        zero, 0, 0, 0);
+}
 
 __device__ __forceinline__ void mfma_wait(MfmaOut& a)
 {
