@@ -58,6 +58,13 @@ def test_shapes_groups_bias(rows, dim):
     run_gated(rows, dim, with_w=False, seed=rows)
 
 
+@pytest.mark.parametrize("xt,gt,wt,yt", [(F16, F32, F32, F32), (F16, F16, F16, F16), (BF16, BF16, F32, F16)])
+def test_wide_rows(xt, gt, wt, yt):
+    """Rows over 32768 columns: 8 chunks on each of 1024 lanes (the instances that spill to scratch)."""
+    run_gated(2, 65536, xt, gt, wt, yt, gate_act=1, seed=80)
+    run_gated(3, 40960, xt, gt, wt, yt, gate_first=True, cb=1.0, seed=81)
+
+
 def test_strided_rows_generic_path():
     run_gated(11, 128, ld=136, seed=21)                      # 16-byte-aligned rows: vector kernel
     run_gated(11, 128, xt=BF16, gt=BF16, ld=131, seed=22)    # unaligned rows: generic kernel

@@ -91,6 +91,12 @@ def test_dtypes_and_row_lengths(xt, gt, wt):
     run(7, 384, xt, F16, wt, heads=7, seed=7)         # f16 gate: workgroup kernel
 
 
+def test_wide_rows():
+    """Rows over 32768 columns: 8 chunks on each of 1024 lanes (the instances that spill to scratch)."""
+    run(2, 65536, F16, F32, F32, gate_act=1, seed=11)
+    run(3, 40960, BF16, BF16, BF16, gate_first=True, seed=12)
+
+
 def test_bias_scale_missing_pre_and_fallback():
     run(33, 128, cb=1.0, had_scale=0.5, pre=False, seed=8)
     run(9, 256, ld=259, seed=9)                       # unaligned rows: the unfused calls

@@ -245,6 +245,12 @@ def test_norm_had_dtypes(xt, rt, wt):
     run_norm(67, 1152, xt, rt, wt, n_out=2, cb=1.0, had_scale=0.5, seed=63)
 
 
+def test_norm_had_wide_rows():
+    """Rows over 32768 columns: 8 chunks on each of 1024 lanes (the instances that spill to scratch)."""
+    run_norm(3, 40960, F16, F32, n_out=3, with_y=True, rotate_x=True, seed=66)
+    run_norm(2, 65536, BF16, None, BF16, n_out=2, seed=67)
+
+
 def test_norm_had_partial_spans():
     """dim 384: 3 blocks, so the last wave span of a row is part empty (those lanes carry zeros)."""
     run_norm(33, 384, F16, F32, n_out=4, seed=64)

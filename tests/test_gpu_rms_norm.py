@@ -116,6 +116,18 @@ def test_res_in_dtype_mixes(xt, rt, yt, wt):
     run_res(50, 2560, xt, rt, yt, wt, seed=xt + 4 * rt + 16 * yt)
 
 
+@pytest.mark.parametrize("dim,xt,rt,yt,wt", [(40960, F16, F32, F16, F16), (65536, F32, F32, F32, F32),
+                                            (65536, BF16, BF16, BF16, BF16), (49152, F16, F16, F32, F16)])
+def test_res_in_wide_rows(dim, xt, rt, yt, wt):
+    """Rows over 32768 columns: 8 chunks on each of 1024 lanes, the instances that spill to scratch."""
+    run_res(3, dim, xt, rt, yt, wt, seed=dim // 1024 + xt)
+
+
+def test_plain_wide_rows_f32_input():
+    run_plain(3, 65536, F32, F16, F16, seed=71)
+    run_plain(2, 40960, F32, BF16, BF16, seed=72)
+
+
 def test_res_in_generic_and_bias():
     run_res(5, 1001, F16, F32, F16, F16, seed=5, cb=1.0, cs=2.0)
 

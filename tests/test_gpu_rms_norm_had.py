@@ -82,6 +82,12 @@ def test_rotated_input_variants(rt):
     run(45, 1024, F16, rt, F32, n_out=2, with_y=True, rotate_x=True, svh=rt != F16, cb=1.0, seed=12)
 
 
+def test_wide_rows():
+    """Rows over 32768 columns (8 chunks on each of 1024 lanes, the instances that spill), the butterfly."""
+    run(3, 40960, F16, F32, n_out=3, with_y=True, rotate_x=True, seed=15)
+    run(2, 65536, F32, F32, F32, n_out=1, with_y=True, seed=16)
+
+
 def test_rotated_input_unaligned_fallback():
     run(9, 256, F16, F32, n_out=2, with_y=False, ld=259, rotate_x=True, seed=13)
     run(9, 256, F16, None, n_out=1, with_y=True, ld=259, rotate_x=True, seed=14)
