@@ -487,15 +487,21 @@ template <int ACT, class IT, class OT, int HAD = 0>
 static void launch_act_vec(const ActArgs& a, hipStream_t s)
 {
     const Tuning& tu = tuning();
-    // Two chunks per thread in 128-thread workgroups measured best on MI355X for streaming launches
-    // (C3: 136 us, 6.3 TB/s); up to 8M elements one chunk per thread in 256-thread workgroups (HIP graph,
-    // us, [rows, 17408] f16: 64 rows 3.15 vs 3.46, 256 rows 5.03 vs 5.41; [512, 3072] 3.24 vs 3.54; from
-    // 1024 rows the streaming shape wins, 16.9 vs 18.8).
+    // Streaming launches take two chunks per thread: in one-wave workgroups from 32M elements (C3 bf16,
+    // same process, us: 2 x 64 lanes 130.8 GELU / 131.0 SiLU against 134.0 / 134.9 with 2 x 128 and
+    // 131.7 / 132.0 with 2 x 192; 1 x 64 133.8 / 134.5, 4 x 64 134.6 / 135.0; SiLU bf16 at [8192, 13824 ..
+    // 25600] and [16384, 4096] 1-4% faster), in 128-thread workgroups below that (16.8M elements: SiLU
+    // 18.38 against 18.60, the in-place sigmoid gate 18.19 against 18.65; 33.6M: the same); the
+    // butterfly Hadamard forms at [8192, 17408] alike (145.1 against 147.0, with the input rotations
+    // 222.0 against 222.9; each pair timed alternately).  Up to 8M elements one chunk per thread in 256-thread
+    // workgroups (HIP graph, us, [rows, 17408] f16: 64 rows 3.15 vs 3.46, 256 rows 5.03 vs 5.41;
+    // [512, 3072] 3.24 vs 3.54; from 1024 rows the streaming shape wins, 16.9 vs 18.8).
     const bool small = a.rows * a.cols <= ((int64_t)8 << 20);
     const int unroll = (tu.act_unroll == 1 || tu.act_unroll == 2 || tu.act_unroll == 4 || tu.act_unroll == 8) ? tu.act_unroll
                        : small ? 1 : 2;
+    const bool one_wave = a.rows * a.cols >= ((int64_t)1 << 25);
     const int threads = (tu.act_threads > 0 && tu.act_threads % 64 == 0 && tu.act_threads <= 256) ? tu.act_threads
-                        : small ? 256 : 128;
+                        : small ? 256 : one_wave ? 64 : 128;
     const int64_t cpr = a.cols >> 3;
     if constexpr (HAD == 0)
     {
