@@ -125,5 +125,7 @@ extern "C" void exl3r_tune_had_mfma(int unroll, int blocks_per_cu)
     exl3r::tuning().had_mfma_per_cu = blocks_per_cu;
 }
 
+extern "C" void exl3r_tune_had_threads(int threads) { exl3r::tuning().had_threads = threads; }
+
 extern "C" void exl3r_tune_embed(int threads) { exl3r::tuning().embed_threads = threads; }
 #endif  // EXL3R_TUNING

@@ -90,6 +90,7 @@ struct Tuning
     int had_unroll = 0;      // Hadamard: 128-blocks per 16-lane group (1, 2, 4; 0: 1)
     int had_mfma_unroll = 0; // matrix-core Hadamard kernels: spans (act-mul: rows of a span) per wave in flight (1, 2, 4; 0: 2)
     int had_mfma_per_cu = 0; // ... workgroups per CU of a looping grid (0: the kernel's default; < 0: one item per wave, no cap)
+    int had_threads = 0;     // lanes per workgroup of k_had, k_had_mfma and k_act_mul_had_mfma (64, 128, 256; 0: the default)
     int embed_threads = 0;
 };
 #ifdef EXL3R_TUNING
@@ -101,6 +102,17 @@ inline const Tuning& tuning()
     return t;
 }
 #endif
+
+// Lanes per workgroup of the Hadamard kernels (k_had, k_had_mfma, k_act_mul_had_mfma): one wave.  Same
+// process, orders rotated, us for 64 / 128 / 256 lanes: had_r_128 [8192, 5120] butterfly 29.95 / 31.72 /
+// 31.79, matrix cores 29.85 / 30.14 / 30.15; SiLU -> rotation [8192, 17408] 130.7 / 131.6 / 130.4; the
+// MLP tail from raw gate / up 142.1 / 144.8 / 146.2; 64 against 256 lanes, alternating: the MLP tail at
+// [4096, 25600] 104.6 against 107.1, the Qwen3-32B prefill layer's row ops 308.2 against 310.5.
+inline int had_threads()
+{
+    const int t = tuning().had_threads;
+    return t == 64 || t == 128 || t == 256 ? t : 64;
+}
 
 // Compute units of the current device (cached after the first call).
 int device_cus();

@@ -559,11 +559,13 @@ template <int ACT, class IT, int HAD, int UNROLL>
 static void launch_act_had_mfma_u(const ActArgs& a, int per_cu, hipStream_t s)
 {
     const int64_t items = (a.rows + UNROLL - 1) / UNROLL * ((a.cols / 8 + 63) / 64);
-    int64_t blocks = (items + 3) / 4;
+    const int threads = had_threads();
+    const int wpb = threads / 64;
+    int64_t blocks = (items + wpb - 1) / wpb;
     if (per_cu > 0 && blocks > (int64_t)per_cu * device_cus()) blocks = (int64_t)per_cu * device_cus();
     if (blocks > kMaxGridX) blocks = kMaxGridX;
-    if (a.limit != 0.0f) launch(k_act_mul_had_mfma<ACT, IT, HAD, true, UNROLL>, (unsigned)blocks, 256, 0, s, a);
-    else launch(k_act_mul_had_mfma<ACT, IT, HAD, false, UNROLL>, (unsigned)blocks, 256, 0, s, a);
+    if (a.limit != 0.0f) launch(k_act_mul_had_mfma<ACT, IT, HAD, true, UNROLL>, (unsigned)blocks, threads, 0, s, a);
+    else launch(k_act_mul_had_mfma<ACT, IT, HAD, false, UNROLL>, (unsigned)blocks, threads, 0, s, a);
 }
 
 template <int ACT, class IT, int HAD>

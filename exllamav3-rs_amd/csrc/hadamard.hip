@@ -89,7 +89,7 @@ template <class IO, bool PRE, bool POST, int U>
 __global__ __launch_bounds__(256) void k_had(HadArgs a)
 {
     const int l16 = threadIdx.x & 15;
-    const int64_t blk0 = ((int64_t)blockIdx.x * 16 + (threadIdx.x >> 4)) * U;
+    const int64_t blk0 = ((int64_t)blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4)) * U;
     const int64_t nblk = a.rows * a.nb;
     typename IO::Vec v[U];
     #pragma unroll
@@ -239,14 +239,15 @@ extern "C" int exl3r_had_r_128(const void* x, int dtype, int64_t ldx, void* out,
     if (vec)
     {
         const int u = tuning().had_unroll == 2 || tuning().had_unroll == 4 ? tuning().had_unroll : 1;
-        const int64_t grid = (blocks + 16 * u - 1) / (16 * u);
+        const int threads = had_threads(), gpb = threads / 16 * u;   // 16-lane groups (x blocks each) per workgroup
+        const int64_t grid = (blocks + gpb - 1) / gpb;
         if (grid > 0x7fffffffLL) return set_error(EXL3R_EINVAL, "%s: too many blocks", op);
         auto go = [&](auto T, auto U) {
             using IO = decltype(T);
             constexpr int UN = decltype(U)::value;
-            if (pre_scale) launch(k_had<IO, true, false, UN>, (unsigned)grid, 256, 0, s, a);
-            else if (post_scale) launch(k_had<IO, false, true, UN>, (unsigned)grid, 256, 0, s, a);
-            else launch(k_had<IO, false, false, UN>, (unsigned)grid, 256, 0, s, a);
+            if (pre_scale) launch(k_had<IO, true, false, UN>, (unsigned)grid, threads, 0, s, a);
+            else if (post_scale) launch(k_had<IO, false, true, UN>, (unsigned)grid, threads, 0, s, a);
+            else launch(k_had<IO, false, false, UN>, (unsigned)grid, threads, 0, s, a);
         };
         auto go_u = [&](auto T) {
             if (u == 4) go(T, std::integral_constant<int, 4>{});
@@ -290,11 +291,12 @@ extern "C" int exl3r_had_r_128_mfma(const void* x, int dtype, int64_t ldx, void*
     constexpr int UN = 2;
     // one wave per UN spans (the grid does not loop; see the act -> Hadamard kernels' launch shape)
     const int per_cu = tuning().had_mfma_per_cu;
-    int64_t blocks = (spans + 4 * UN - 1) / (4 * UN);
+    const int threads = had_threads(), spb = threads / 64 * UN;   // spans per workgroup
+    int64_t blocks = (spans + spb - 1) / spb;
     if (per_cu > 0 && blocks > (int64_t)per_cu * device_cus()) blocks = (int64_t)per_cu * device_cus();
     if (blocks > kMaxGridX) blocks = kMaxGridX;
-    if (pre_scale) launch(k_had_mfma<true, false, UN>, (unsigned)blocks, 256, 0, s, a);
-    else if (post_scale) launch(k_had_mfma<false, true, UN>, (unsigned)blocks, 256, 0, s, a);
-    else launch(k_had_mfma<false, false, UN>, (unsigned)blocks, 256, 0, s, a);
+    if (pre_scale) launch(k_had_mfma<true, false, UN>, (unsigned)blocks, threads, 0, s, a);
+    else if (post_scale) launch(k_had_mfma<false, true, UN>, (unsigned)blocks, threads, 0, s, a);
+    else launch(k_had_mfma<false, false, UN>, (unsigned)blocks, threads, 0, s, a);
     return launch_status(op);
 }

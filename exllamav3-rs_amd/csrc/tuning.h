@@ -39,6 +39,8 @@ EXL3R_API void exl3r_tune_had(int blocks_per_group);
 /* matrix-core Hadamard kernels: spans (act-mul: rows of a span) per wave in flight (1, 2, 4; 0 auto),
  * workgroups per CU of a looping grid (0 auto, < 0 one item per wave) */
 EXL3R_API void exl3r_tune_had_mfma(int unroll, int blocks_per_cu);
+/* lanes per workgroup of the Hadamard kernels k_had, k_had_mfma and k_act_mul_had_mfma (64, 128, 256; 0 auto) */
+EXL3R_API void exl3r_tune_had_threads(int threads);
 EXL3R_API void exl3r_tune_embed(int threads);
 #ifdef __cplusplus
 }

@@ -105,6 +105,7 @@ TUNE_PROTOTYPES = {
     "exl3r_tune_sample": (None, [_i, _i]),
     "exl3r_tune_had": (None, [_i]),
     "exl3r_tune_had_mfma": (None, [_i, _i]),
+    "exl3r_tune_had_threads": (None, [_i]),
     "exl3r_tune_embed": (None, [_i]),
 }
 
@@ -185,6 +186,7 @@ def tuned():
         lib.exl3r_tune_sample(0, 0)
         lib.exl3r_tune_had(0)
         lib.exl3r_tune_had_mfma(0, 0)
+        lib.exl3r_tune_had_threads(0)
         lib.exl3r_tune_embed(0)
         _lib = saved
 
