@@ -634,7 +634,7 @@ __global__ __launch_bounds__(256) void k_rms_rows(RmsArgs a)
     static_assert(MODE != RMS_GATHER, "gathered rows take the workgroup kernel");
     constexpr bool MF = (HAD & HAD_MFMA) != 0;
     static_assert(!MF || (LPR == 16 && (HAD & HAD_OUT) != 0), "matrix-core rows: one block each, an output");
-    constexpr int SLOTS = 256 / LPR;
+    const int SLOTS = (int)blockDim.x / LPR;   // row slots of the workgroup
     const int l64 = threadIdx.x & 63;
     const int lane = MF ? (l64 & 3) | ((l64 >> 2) & 12) : (int)threadIdx.x % LPR;
     const int slot = MF ? (int)(threadIdx.x >> 6) * 4 + ((l64 >> 2) & 3) : (int)threadIdx.x / LPR;
@@ -735,7 +735,10 @@ void launch_rms_rows(const RmsArgs& a, hipStream_t s)
     const int nc = a.dim >> 3;
     auto go = [&](auto L) {
         constexpr int LPR = decltype(L)::value;
-        constexpr int SLOTS = 256 / LPR;
+        // One-wave workgroups (same process, both orders, us for 64 / 256 lanes at [131072, 128]: gated
+        // norm 24.8 / 25.2, with the o_proj rotation on the matrix cores 28.6 / 29.5, butterfly 28.9 / 29.1).
+        constexpr int kThreads = 64;
+        constexpr int SLOTS = kThreads / LPR;
         const int tuned = tuning().rms_rows_rpl;
         // One row per lane: at 62 VGPRs (f32 gate) 8 waves per SIMD keep the loads in flight.  Measured
         // on MI355X, gated norm [131072, 128] bf16 x / f32 g / f16 y: 1 row per lane 25.2 us, 2 rows
@@ -743,9 +746,9 @@ void launch_rms_rows(const RmsArgs& a, hipStream_t s)
         const int rpl = (tuned == 1 || tuned == 2 || tuned == 4) ? tuned : 1;
         int64_t blocks = (a.rows + (int64_t)SLOTS * rpl - 1) / ((int64_t)SLOTS * rpl);
         if (blocks > kMaxGridX) blocks = kMaxGridX;
-        if (rpl == 4) launch(k_rms_rows<XT, YT, RT, LPR, 4, MODE, HAD>, (unsigned)blocks, 256, 0, s, a);
-        else if (rpl == 2) launch(k_rms_rows<XT, YT, RT, LPR, 2, MODE, HAD>, (unsigned)blocks, 256, 0, s, a);
-        else launch(k_rms_rows<XT, YT, RT, LPR, 1, MODE, HAD>, (unsigned)blocks, 256, 0, s, a);
+        if (rpl == 4) launch(k_rms_rows<XT, YT, RT, LPR, 4, MODE, HAD>, (unsigned)blocks, kThreads, 0, s, a);
+        else if (rpl == 2) launch(k_rms_rows<XT, YT, RT, LPR, 2, MODE, HAD>, (unsigned)blocks, kThreads, 0, s, a);
+        else launch(k_rms_rows<XT, YT, RT, LPR, 1, MODE, HAD>, (unsigned)blocks, kThreads, 0, s, a);
     };
     if constexpr ((HAD & HAD_MFMA) != 0)
         go(std::integral_constant<int, 16>{});   // rows of one block (the caller checks dim == 128)
